@@ -1,0 +1,73 @@
+// device.hpp -- small device-side building blocks shared by the kernels.
+//
+// Numerics contract (all kernels are built with -ffp-contract=off and the
+// default correctly rounded fp32 division and square root):
+//   * every fp32 expression below is evaluated in the same operation order as
+//     the reference CPU code it replaces, one rounding per operation;
+//   * exp / log1p are computed in fp64 and rounded once to fp32, i.e. they are
+//     correctly rounded. The reference calls glibc's expf / log1pf, which agree
+//     with the correctly rounded value on all but a few inputs in 10^4
+//     (expf) or 10^3 (log1pf), so those two can differ in the last bit.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "hero/fp16.hpp"
+
+namespace hero {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float exp_f32(float x) { return float(::exp(double(x))); }
+__device__ __forceinline__ float log1p_f32(float x) { return float(::log1p(double(x))); }
+
+// nm/src/core.hpp:579
+__device__ __forceinline__ float sigmoid_f32(float x) { return 1.f / (1.f + exp_f32(-x)); }
+// nm/src/components.hpp:105 -- x/(1+e^-x), not x*sigmoid(x)
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.f + exp_f32(-x)); }
+// nm/src/recurrent.hpp:35
+__device__ __forceinline__ float softplus_f32(float x) { return x > 20.f ? x : log1p_f32(exp_f32(x)); }
+
+__device__ __forceinline__ float half_bits_to_f32(uint16_t h) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return float(v);
+}
+
+// 4-way int8 dot product into an int32 accumulator (v_dot4_i32_i8), exact.
+__device__ __forceinline__ int dot4_i8(int a, int b, int acc) { return __builtin_amdgcn_sdot4(a, b, acc, false); }
+
+__device__ __forceinline__ int dot16_i8(const int4& w, const int4& x, int acc) {
+    acc = dot4_i8(w.x, x.x, acc);
+    acc = dot4_i8(w.y, x.y, acc);
+    acc = dot4_i8(w.z, x.z, acc);
+    acc = dot4_i8(w.w, x.w, acc);
+    return acc;
+}
+
+// Quantize one 32-value block held 8 per lane by 4 consecutive lanes
+// (nm/src/quant_i8.hpp:70-80): amax over the block, d = amax/127,
+// id = 1/d (0 if d == 0), q = roundf(x*id), d stored through the reference
+// fp16 encoder. Returns the 8 int8 values packed in two ints; *dh receives
+// the fp16 bits of d (identical on all four lanes).
+__device__ __forceinline__ int2 quantize8_in_quad(const float (&x)[8], uint16_t* dh) {
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(x[j]));
+    // max over the 4 lanes of the quad (exact: max is order independent)
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    const float d = amax / 127.f;
+    const float id = d != 0.f ? 1.f / d : 0.f;
+    *dh = fp32_to_fp16_ref(d);
+    int packed[2] = {0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int q = int(roundf(x[j] * id));
+        packed[j / 4] |= (q & 0xFF) << (8 * (j % 4));
+    }
+    return make_int2(packed[0], packed[1]);
+}
+
+}  // namespace hero

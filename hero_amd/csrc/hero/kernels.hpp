@@ -1,0 +1,74 @@
+// kernels.hpp -- host-side launchers of the gfx950 kernels (internal API).
+// Pointers are device pointers; every launcher enqueues on `s` and returns
+// immediately. Shape validation happens in the C ABI layer (capi.cpp).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstddef>
+#include <cstdint>
+
+namespace hero {
+
+enum : int { kEpiStore = 0, kEpiResidual = 1 };
+
+// bytes of a packed Q8_0 weight / a quantized activation block set
+inline int64_t packed_q8_bytes(int64_t N, int64_t K) { return N * K + N * (K / 32) * 2; }
+inline int64_t act_q8_bytes(int64_t M, int64_t K) { return M * K + M * (K / 32) * 4; }
+
+// q8.hip
+void launch_quantize_act(const float* x, void* act, int64_t M, int64_t K, hipStream_t s);
+void launch_pack_q8(const void* gguf_blocks, void* packed, int64_t N_total, int64_t K, int64_t row0, int64_t rows, hipStream_t s);
+void launch_gemv_q8(const void* packed, const void* act, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s);
+void launch_block_sums(const void* packed, const void* act, int32_t* out, int64_t N, int64_t K, hipStream_t s);
+int gemv_rows_per_group(int64_t N, int64_t K);
+
+// norm.hip: rows x [M][D] -> RMSNorm (gamma, eps) -> quantized act; y (fp32) optional
+void launch_rmsnorm_quant(const float* x, const float* gamma, float eps, float* y, void* act, int64_t M, int64_t D, hipStream_t s);
+
+// ew.hip
+void launch_swiglu_quant(const float* gate_up, void* act, int64_t M, int64_t FF, hipStream_t s);
+void launch_embed_q8(const void* packed_embedding, int64_t V, int64_t D, const int32_t* ids, int64_t n, float* out, hipStream_t s);
+// argmax over n logits per row (ties -> lowest index); out_index[M]
+void launch_argmax(const float* logits, int64_t M, int64_t n, int32_t* out_index, uint64_t* scratch_keys, hipStream_t s);
+
+// gdn.hip: gated delta-net decode for B sequences x Hv heads (one token each)
+struct GdnDecodeArgs {
+    const float* proj;      // [B][proj_stride]: qkv at 0, z at z_off, beta at beta_off, alpha at alpha_off
+    int64_t proj_stride, z_off, beta_off, alpha_off;
+    const float* conv_taps; // [CC][W]
+    float* conv_hist;       // [B][W-1][CC], ring: slot p % (W-1) holds position p
+    float* state;           // [B][Hv][Dk][Dv]
+    const float* dt_bias;   // [Hv]
+    const float* decay;     // [Hv], -exp(A_log)
+    const float* norm_gamma;// [Dv]
+    float eps;
+    const int32_t* positions; // [B] position of this token
+    void* act_out;          // quantized WO input [B][Hv*Dv]
+    float* out_f32;         // optional [B][Hv*Dv], the gated output before quantization
+    int B, Hk, Hv, Dk, Dv, W;
+};
+void launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t s);
+
+// attn.hip: gated GQA decode over an fp32 K/V cache (one token per sequence)
+struct AttnDecodeArgs {
+    const float* proj;       // [B][proj_stride]: q|gate pairs at 0, k at k_off, v at v_off
+    int64_t proj_stride, k_off, v_off;
+    const float* q_gamma;    // [Dh]
+    const float* k_gamma;    // [Dh]
+    float eps;
+    const float* rope_cs;    // [max_pos][Dh/2][2] (cos, sin) per position and plane
+    float* k_cache;          // [B][max_ctx][Hkv*Dh]
+    float* v_cache;
+    int64_t max_ctx;
+    const int32_t* positions;// [B]
+    float* scores;           // scratch [B][Hq][max_ctx]
+    float score_scale;
+    int window;              // 0 = full causal
+    void* act_out;           // quantized WO input [B][Hq*Dh]
+    float* out_f32;          // optional [B][Hq*Dh]
+    int B, Hq, Hkv, Dh;
+};
+void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s);
+
+}  // namespace hero

@@ -1,0 +1,143 @@
+// model.hpp -- the GPU Qwen 3.5 hybrid model: the C++ side of the drop-in.
+//
+// Mirrors the reference's model contract (nm/src/transformer.hpp:70-78):
+//   Qwen35Model::open(gguf)        <- qwen35_loader::load<C> (qwen35_loader.hpp:141-155)
+//   model.new_state(max_tokens)    <- Qwen35State<C> (qwen35.hpp:206-241)
+//   state.tokens()                 <- PrefixState::tokens()
+//   model.embed(ids, n, rows)      <- Qwen35Model::embed (qwen35.hpp:285)
+//   model.forward(state, rows|ids) <- Qwen35Model::forward (qwen35.hpp:288-303)
+// Dimensions are read from the GGUF metadata at run time (the reference fixes
+// them at compile time) and validated the way validate_metadata does.
+// The model is immutable after load and non-copyable; a State belongs to one
+// sequence and one caller thread.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace hero {
+
+class GgufFile;
+
+struct ModelConfig {
+    int64_t V = 0, D = 0, L = 0, CTX = 0;
+    int64_t Hq = 0, Hkv = 0, Dh = 0, rotary_dims = 0;
+    int64_t Dk = 0, Dv = 0, Hk = 0, Hv = 0, W = 0;
+    int64_t FF = 0;
+    double rope_base = 0;
+    float eps = 0;
+    bool tied = true;
+    bool is_recurrent(int64_t layer) const { return (layer + 1) % 4 != 0; }
+    int64_t conv_channels() const { return 2 * Hk * Dk + Hv * Dv; }
+    int64_t q_width() const { return Hq * Dh; }
+    int64_t kv_width() const { return Hkv * Dh; }
+    int64_t v_width() const { return Hv * Dv; }
+};
+
+// Owning device allocation.
+class DeviceBuffer {
+public:
+    DeviceBuffer() = default;
+    explicit DeviceBuffer(size_t bytes);
+    ~DeviceBuffer();
+    DeviceBuffer(DeviceBuffer&& o) noexcept : p_(o.p_), bytes_(o.bytes_) {
+        o.p_ = nullptr;
+        o.bytes_ = 0;
+    }
+    DeviceBuffer& operator=(DeviceBuffer&& o) noexcept;
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    template <class T = void>
+    T* get() const {
+        return static_cast<T*>(p_);
+    }
+    size_t bytes() const { return bytes_; }
+
+private:
+    void* p_ = nullptr;
+    size_t bytes_ = 0;
+};
+
+struct LayerWeights {
+    bool recurrent = true;
+    DeviceBuffer mixer_norm, channel_norm;  // [D] fp32
+    DeviceBuffer w_in;                      // packed Q8_0, K = D
+    int64_t n_in = 0;
+    DeviceBuffer w_out;                     // packed Q8_0 [D][Hv*Dv or Hq*Dh]
+    DeviceBuffer w_gate_up;                 // packed Q8_0 [2FF][D]: gate rows then up rows
+    DeviceBuffer w_down;                    // packed Q8_0 [D][FF]
+    // recurrent: w_in rows = [qkv CC | z Hv*Dv | beta Hv | alpha Hv]
+    DeviceBuffer conv, dt_bias, decay, ssm_norm;
+    int64_t z_off = 0, beta_off = 0, alpha_off = 0;
+    // attention: w_in rows = [q|gate pairs 2*Hq*Dh | k Hkv*Dh | v Hkv*Dh]
+    DeviceBuffer q_norm, k_norm;
+    int64_t k_off = 0, v_off = 0;
+};
+
+class Qwen35Model {
+public:
+    class State;
+
+    static std::unique_ptr<Qwen35Model> open(const std::string& gguf_path);
+    static std::unique_ptr<Qwen35Model> open_image(const uint8_t* image, uint64_t size);
+    ~Qwen35Model();
+    Qwen35Model(const Qwen35Model&) = delete;
+    Qwen35Model& operator=(const Qwen35Model&) = delete;
+
+    const ModelConfig& config() const { return c_; }
+    int64_t device_bytes() const { return device_bytes_; }
+    hipStream_t stream() const { return stream_; }
+
+    std::unique_ptr<State> new_state(int64_t max_tokens) const;
+    // host rows out[n][D]
+    void embed(const int32_t* ids, int64_t n, float* out) const;
+    // T rows from host `rows` or from `ids`; logits / greedy id of the last row
+    void forward(State& s, const float* rows, const int32_t* ids, int64_t T, float* logits, int32_t* next_id) const;
+    // greedy loop from `first_id`; out_ids[steps] on the host
+    void decode_greedy(State& s, int32_t first_id, int64_t steps, int32_t* out_ids, float* logits) const;
+    double last_decode_seconds() const { return last_decode_seconds_; }
+
+private:
+    Qwen35Model() = default;
+    void load(const GgufFile& g);
+    void build_rope_table(int64_t positions);
+    // one token at the state's device position; `with_head` adds the final
+    // norm, LM head and argmax (the reference computes logits for the last row only)
+    void enqueue_step(State& s, bool from_ids, bool with_head) const;
+
+    ModelConfig c_;
+    std::vector<LayerWeights> layers_;
+    DeviceBuffer embedding_, output_, final_norm_, rope_cs_;
+    int64_t rope_positions_ = 0;
+    int64_t device_bytes_ = 0;
+    hipStream_t stream_ = nullptr;
+    hipEvent_t ev_start_ = nullptr, ev_stop_ = nullptr;
+    mutable double last_decode_seconds_ = 0;
+};
+
+class Qwen35Model::State {
+public:
+    ~State();
+    int64_t tokens() const { return tokens_; }
+    int64_t max_tokens() const { return max_tokens_; }
+    void reset();
+
+private:
+    friend class Qwen35Model;
+    explicit State(const Qwen35Model& m, int64_t max_tokens);
+
+    const Qwen35Model& m_;
+    int64_t tokens_ = 0, max_tokens_ = 0;
+    // per-step device scalars: [0] position, [1] token id, [2] step counter
+    DeviceBuffer step_;
+    DeviceBuffer x_, h_, rows_, proj_, act_d_, act_mix_, act_ff_, gate_up_, logits_, argmax_scratch_, out_ids_;
+    int64_t rows_capacity_ = 0, out_ids_capacity_ = 0;
+    std::vector<DeviceBuffer> k_cache_, v_cache_, scores_, conv_hist_, delta_;
+    hipGraphExec_t graph_ = nullptr;  // one greedy decode step, replayed
+};
+
+}  // namespace hero

@@ -1,0 +1,22 @@
+// synth.hpp -- seeded random-init Qwen 3.5-style hybrid models as GGUF images.
+#pragma once
+#include <cstdint>
+#include <string>
+
+namespace hero {
+
+struct SynthConfig {
+    uint64_t V = 32000, D = 1024, L = 4, FF = 2816;
+    uint64_t Hq = 8, Hkv = 2, head_dim = 128;
+    uint64_t Dk = 128, Dv = 128, Hk = 8, Hv = 8, conv_width = 4;
+    uint64_t ctx = 4096;
+    double rope_base = 1e6;
+    bool tied = true;
+    uint64_t seed = 1;
+};
+
+uint64_t synth_qwen35_size(const SynthConfig& c);
+void synth_qwen35_image(const SynthConfig& c, uint8_t* image, uint64_t capacity);
+void synth_qwen35_file(const SynthConfig& c, const std::string& path);
+
+}  // namespace hero

@@ -1,0 +1,152 @@
+// capi_kernels.cpp -- the extern "C" kernel entry points of include/hero_kernels.h:
+// argument validation, then the launcher. No allocation happens here.
+#include "hero_kernels.h"
+
+#include <string>
+
+#include "hero/errors.hpp"
+#include "hero/kernels.hpp"
+
+using namespace hero;
+
+namespace {
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+void require(bool ok, const std::string& what) {
+    if (!ok) throw Error(HERO_EINVAL, what);
+}
+
+void check_q8_shape(int64_t n, int64_t k) {
+    require(n > 0 && k > 0, "shape must be positive");
+    require(k % 32 == 0, "K must be a multiple of 32 (Q8_0 block)");
+    require(n <= (int64_t(1) << 31) && k <= (int64_t(1) << 20), "shape too large");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* hero_last_error(void) { return last_error_message(); }
+const char* hero_version(void) { return "hero_amd 0.1 (gfx950)"; }
+
+int64_t hero_q8_0_packed_bytes(int64_t n, int64_t k) { return packed_q8_bytes(n, k); }
+int64_t hero_q8_0_act_bytes(int64_t m, int64_t k) { return act_q8_bytes(m, k); }
+
+int hero_q8_0_pack(const void* src, void* packed, int64_t n_total, int64_t k, int64_t row0, int64_t rows, void* stream) {
+    return guard([&] {
+        check_q8_shape(n_total, k);
+        require(src && packed, "null pointer");
+        require(aligned(packed, 16), "packed buffer must be 16-byte aligned");
+        require(row0 >= 0 && rows > 0 && row0 + rows <= n_total, "row range outside the packed matrix");
+        launch_pack_q8(src, packed, n_total, k, row0, rows, as_stream(stream));
+        check_launch("hero_q8_0_pack");
+    });
+}
+
+int hero_q8_0_quantize(const float* x, void* act, int64_t m, int64_t k, void* stream) {
+    return guard([&] {
+        check_q8_shape(m, k);
+        require(x && act, "null pointer");
+        require(aligned(x, 16) && aligned(act, 16), "x and act must be 16-byte aligned");
+        launch_quantize_act(x, act, m, k, as_stream(stream));
+        check_launch("hero_q8_0_quantize");
+    });
+}
+
+int hero_q8_0_gemv(const void* packed, const void* act, float* y, const float* residual, int64_t n, int64_t k, void* stream) {
+    return guard([&] {
+        check_q8_shape(n, k);
+        require(packed && act && y, "null pointer");
+        require(aligned(packed, 16) && aligned(act, 16), "packed and act must be 16-byte aligned");
+        launch_gemv_q8(packed, act, y, residual, n, k, residual ? kEpiResidual : kEpiStore, as_stream(stream));
+        check_launch("hero_q8_0_gemv");
+    });
+}
+
+int hero_q8_0_block_sums(const void* packed, const void* act, int32_t* out, int64_t n, int64_t k, void* stream) {
+    return guard([&] {
+        check_q8_shape(n, k);
+        require(packed && act && out, "null pointer");
+        require(aligned(packed, 16) && aligned(act, 16), "packed and act must be 16-byte aligned");
+        launch_block_sums(packed, act, out, n, k, as_stream(stream));
+        check_launch("hero_q8_0_block_sums");
+    });
+}
+
+int hero_rmsnorm_quant(const float* x, const float* gamma, float eps, float* y, void* act, int64_t m, int64_t d, void* stream) {
+    return guard([&] {
+        check_q8_shape(m, d);
+        require(x && gamma, "null pointer");
+        require(d <= 16384, "row width above 16384 is not supported");
+        require(aligned(x, 16) && aligned(gamma, 16) && aligned(y, 16) && aligned(act, 16), "buffers must be 16-byte aligned");
+        launch_rmsnorm_quant(x, gamma, eps, y, act, m, d, as_stream(stream));
+        check_launch("hero_rmsnorm_quant");
+    });
+}
+
+int hero_swiglu_quant(const float* gate_up, void* act, int64_t m, int64_t ff, void* stream) {
+    return guard([&] {
+        check_q8_shape(m, ff);
+        require(gate_up && act, "null pointer");
+        require(aligned(gate_up, 16) && aligned(act, 16), "buffers must be 16-byte aligned");
+        launch_swiglu_quant(gate_up, act, m, ff, as_stream(stream));
+        check_launch("hero_swiglu_quant");
+    });
+}
+
+int hero_q8_0_embed(const void* packed, int64_t v, int64_t d, const int32_t* ids, int64_t n, float* out, void* stream) {
+    return guard([&] {
+        check_q8_shape(v, d);
+        require(n > 0 && packed && ids && out, "bad arguments");
+        launch_embed_q8(packed, v, d, ids, n, out, as_stream(stream));
+        check_launch("hero_q8_0_embed");
+    });
+}
+
+int hero_argmax(const float* logits, int64_t m, int64_t n, int32_t* out, uint64_t* scratch, void* stream) {
+    return guard([&] {
+        require(m > 0 && n > 0 && n < (int64_t(1) << 31), "bad shape");
+        require(logits && out && scratch, "null pointer");
+        launch_argmax(logits, m, n, out, scratch, as_stream(stream));
+        check_launch("hero_argmax");
+    });
+}
+
+int hero_gdn_decode(const hero_gdn_decode_args* p, void* stream) {
+    return guard([&] {
+        require(p != nullptr, "null args");
+        const hero_gdn_decode_args& a = *p;
+        require(a.dk == 128 && a.dv == 128, "delta-net heads must be 128x128");
+        require(a.b > 0 && a.hk > 0 && a.hv > 0 && a.hv % a.hk == 0, "bad head counts");
+        require(a.conv_width >= 1 && a.conv_width <= 8, "conv width must be 1..8");
+        require(a.proj && a.conv_taps && a.conv_hist && a.state && a.dt_bias && a.decay && a.norm_gamma && a.positions && a.act_out, "null pointer");
+        const int64_t cc = 2 * int64_t(a.hk) * 128 + int64_t(a.hv) * 128;
+        require(a.proj_stride >= cc && a.z_off >= cc && a.z_off + int64_t(a.hv) * 128 <= a.proj_stride, "z slice outside the projection row");
+        require(a.beta_off >= 0 && a.beta_off + a.hv <= a.proj_stride && a.alpha_off >= 0 && a.alpha_off + a.hv <= a.proj_stride, "gate slices outside the projection row");
+        GdnDecodeArgs g{a.proj, a.proj_stride, a.z_off, a.beta_off, a.alpha_off, a.conv_taps, a.conv_hist, a.state, a.dt_bias, a.decay, a.norm_gamma, a.eps, a.positions, a.act_out, a.out_f32, a.b, a.hk, a.hv, a.dk, a.dv, a.conv_width};
+        launch_gdn_decode(g, as_stream(stream));
+        check_launch("hero_gdn_decode");
+    });
+}
+
+int hero_attn_decode(const hero_attn_decode_args* p, void* stream) {
+    return guard([&] {
+        require(p != nullptr, "null args");
+        const hero_attn_decode_args& a = *p;
+        require(a.dh == 128, "attention head dim must be 128");
+        require(a.b > 0 && a.hkv > 0 && a.hq > 0 && a.hq % a.hkv == 0, "bad head counts");
+        require(a.window >= 0 && a.max_ctx > 0, "bad window or cache size");
+        require(a.proj && a.q_gamma && a.k_gamma && a.rope_cs && a.k_cache && a.v_cache && a.positions && a.scores && a.act_out, "null pointer");
+        const int64_t kw = int64_t(a.hkv) * 128;
+        require(a.proj_stride >= 2 * int64_t(a.hq) * 128 && a.k_off + kw <= a.proj_stride && a.v_off + kw <= a.proj_stride, "k/v slices outside the projection row");
+        require(aligned(a.k_cache, 16), "k_cache must be 16-byte aligned");
+        AttnDecodeArgs g{a.proj, a.proj_stride, a.k_off, a.v_off, a.q_gamma, a.k_gamma, a.eps, a.rope_cs, a.k_cache, a.v_cache, a.max_ctx, a.positions, a.scores, a.score_scale, a.window, a.act_out, a.out_f32, a.b, a.hq, a.hkv, a.dh};
+        launch_attn_decode(g, as_stream(stream));
+        check_launch("hero_attn_decode");
+    });
+}
+
+}  // extern "C"

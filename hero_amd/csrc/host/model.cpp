@@ -1,0 +1,492 @@
+// model.cpp -- load, state and the per-token schedule of the GPU model.
+//
+// Per token and layer the device runs (all on the model's stream):
+//   rmsnorm_quant(x)                       mixer norm + Q8_0 quantize
+//   gemv(w_in)                             all input projections of the layer in one matvec
+//   gdn_decode | attn_decode               token mixer, emits the quantized W_o input
+//   gemv(w_out, residual x)   -> h         h = x + mix(norm(x))      (qwen35.hpp:319-321)
+//   rmsnorm_quant(h)                       channel norm
+//   gemv(w_gate_up)                        gate and up in one matvec
+//   swiglu_quant                           silu(gate)*up, quantized
+//   gemv(w_down, residual h)  -> x         out = h + mlp(norm(h))    (qwen35.hpp:324-326)
+// then, for the last row only, the final norm, the LM head matvec and the
+// argmax (qwen35.hpp:296-302, logits.hpp:61-66). The position and the token
+// id of a step live in device memory and are advanced by the device, so a
+// greedy decode step has no host input and is replayed as one hipGraph.
+#include "hero/model.hpp"
+
+#include <cmath>
+#include <cstring>
+
+#include "hero/errors.hpp"
+#include "hero/fp16.hpp"
+#include "hero/gguf.hpp"
+#include "hero/kernels.hpp"
+#include "hero_kernels.h"
+
+namespace hero {
+
+// ---- small device helpers for the step scalars --------------------------------
+// step[0] = position, step[1] = token id, step[2] = greedy step counter
+__global__ void set_step_kernel(int32_t* step, int32_t position, int32_t token, int32_t counter) {
+    if (position >= 0) step[0] = position;
+    if (token >= 0) step[1] = token;
+    if (counter >= 0) step[2] = counter;
+}
+__global__ void advance_step_kernel(int32_t* step, int32_t* out_ids, int32_t record) {
+    step[0] += 1;
+    if (record) {
+        out_ids[step[2]] = step[1];
+        step[2] += 1;
+    }
+}
+
+// ---- DeviceBuffer -----------------------------------------------------------------
+DeviceBuffer::DeviceBuffer(size_t bytes) : bytes_(bytes) {
+    if (bytes == 0) return;
+    hip_check(hipMalloc(&p_, bytes), "hipMalloc");
+}
+DeviceBuffer::~DeviceBuffer() {
+    if (p_) (void)hipFree(p_);
+}
+DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& o) noexcept {
+    if (this != &o) {
+        if (p_) (void)hipFree(p_);
+        p_ = o.p_;
+        bytes_ = o.bytes_;
+        o.p_ = nullptr;
+        o.bytes_ = 0;
+    }
+    return *this;
+}
+
+namespace {
+
+void expect(bool ok, const std::string& what) {
+    if (!ok) throw Error(HERO_EIO, "qwen35 loader: " + what);
+}
+std::string blk(int64_t l, const char* s) { return "blk." + std::to_string(l) + "." + s; }
+int64_t meta_int(const GgufFile& g, const std::string& k) { return int64_t(g.num(k)); }
+
+std::vector<float> host_vector(const GgufFile& g, const std::string& name, int64_t n) {
+    const GgufFile::Tensor& t = g.require(name);
+    expect(int64_t(t.nelem) == n, name + " has length " + std::to_string(t.nelem) + ", expected " + std::to_string(n));
+    std::vector<float> v(static_cast<size_t>(n));
+    if (t.type == 0) {
+        std::memcpy(v.data(), t.data, size_t(n) * 4);
+    } else if (t.type == 1) {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(t.data);
+        for (int64_t i = 0; i < n; ++i) v[size_t(i)] = fp16_to_fp32_ref(h[i]);
+    } else {
+        expect(false, name + " must be F32 or F16");
+    }
+    return v;
+}
+
+DeviceBuffer upload(const std::vector<float>& v) {
+    DeviceBuffer b(v.size() * sizeof(float));
+    hip_check(hipMemcpy(b.get(), v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice), "upload");
+    return b;
+}
+
+struct Packer {
+    DeviceBuffer staging;
+    hipStream_t stream;
+    int64_t* counter;
+    // copy one Q8_0 GGUF tensor [K, rows] into rows [row0, row0+rows) of a packed matrix
+    void put(const GgufFile& g, const std::string& name, DeviceBuffer& dst, int64_t n_total, int64_t K, int64_t row0, int64_t rows) {
+        const GgufFile::Tensor& t = g.require(name);
+        expect(t.dims.size() == 2 && int64_t(t.dims[0]) == K && int64_t(t.dims[1]) == rows, name + " has the wrong shape");
+        expect(t.type == 8, name + " must be Q8_0");
+        if (staging.bytes() < t.nbytes) {
+            hip_check(hipStreamSynchronize(stream), "pack sync");
+            staging = DeviceBuffer(t.nbytes);
+        }
+        hip_check(hipStreamSynchronize(stream), "pack sync");
+        hip_check(hipMemcpy(staging.get(), t.data, t.nbytes, hipMemcpyHostToDevice), "weight upload");
+        launch_pack_q8(staging.get(), dst.get(), n_total, K, row0, rows, stream);
+        check_launch("pack");
+    }
+    DeviceBuffer alloc(int64_t n, int64_t K) {
+        *counter += packed_q8_bytes(n, K);
+        return DeviceBuffer(size_t(packed_q8_bytes(n, K)));
+    }
+};
+
+}  // namespace
+
+// ---- load ---------------------------------------------------------------------------
+std::unique_ptr<Qwen35Model> Qwen35Model::open(const std::string& path) {
+    GgufFile g;
+    g.open(path);
+    std::unique_ptr<Qwen35Model> m(new Qwen35Model());
+    m->load(g);
+    return m;
+}
+
+std::unique_ptr<Qwen35Model> Qwen35Model::open_image(const uint8_t* image, uint64_t size) {
+    GgufFile g;
+    g.parse(image, size);
+    std::unique_ptr<Qwen35Model> m(new Qwen35Model());
+    m->load(g);
+    return m;
+}
+
+Qwen35Model::~Qwen35Model() {
+    if (ev_start_) (void)hipEventDestroy(ev_start_);
+    if (ev_stop_) (void)hipEventDestroy(ev_stop_);
+    if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+// Schema validation restates nm/src/qwen35_loader.hpp:30-75 with the
+// dimensions read from the file instead of compared to a compiled config.
+void Qwen35Model::load(const GgufFile& g) {
+    expect(g.str("general.architecture") == "qwen35", "general.architecture is not 'qwen35'");
+    ModelConfig& c = c_;
+    c.L = meta_int(g, "qwen35.block_count");
+    c.D = meta_int(g, "qwen35.embedding_length");
+    c.FF = meta_int(g, "qwen35.feed_forward_length");
+    c.Hq = meta_int(g, "qwen35.attention.head_count");
+    c.Hkv = meta_int(g, "qwen35.attention.head_count_kv");
+    c.Dh = meta_int(g, "qwen35.attention.key_length");
+    expect(meta_int(g, "qwen35.attention.value_length") == c.Dh, "attention value_length != key_length");
+    c.eps = float(g.num("qwen35.attention.layer_norm_rms_epsilon"));
+    c.rope_base = double(float(g.num("qwen35.rope.freq_base")));
+    c.rotary_dims = meta_int(g, "qwen35.rope.dimension_count");
+    c.W = meta_int(g, "qwen35.ssm.conv_kernel");
+    c.Dk = meta_int(g, "qwen35.ssm.state_size");
+    c.Hk = meta_int(g, "qwen35.ssm.group_count");
+    c.Hv = meta_int(g, "qwen35.ssm.time_step_rank");
+    const int64_t inner = meta_int(g, "qwen35.ssm.inner_size");
+    expect(c.Hv > 0 && inner % c.Hv == 0, "ssm.inner_size is not a whole number of value heads");
+    c.Dv = inner / c.Hv;
+    c.CTX = g.has("qwen35.context_length") ? meta_int(g, "qwen35.context_length") : 262144;
+    if (g.has("qwen35.full_attention_interval")) expect(meta_int(g, "qwen35.full_attention_interval") == 4, "full_attention_interval must be 4");
+    if (g.has("qwen35.attention.recurrent_layers")) {
+        const auto& a = g.get("qwen35.attention.recurrent_layers").arr_num;
+        expect(int64_t(a.size()) >= c.L, "qwen35.attention.recurrent_layers is shorter than block_count");
+        for (int64_t l = 0; l < c.L; ++l) expect((a[size_t(l)] != 0) == c.is_recurrent(l), "layer " + std::to_string(l) + " disagrees with the hybrid schedule");
+    }
+    expect(c.L > 0 && c.L % 4 == 0, "block_count must be a positive multiple of 4 (3 delta-net : 1 attention)");
+    expect(c.Hkv > 0 && c.Hq % c.Hkv == 0, "query heads must be a multiple of K/V heads");
+    expect(c.Hk > 0 && c.Hv % c.Hk == 0, "value heads must be a multiple of key heads");
+    expect(c.Dk == 128 && c.Dv == 128, "this build runs 128x128 delta-net heads");
+    expect(c.Dh == 128, "this build runs 128-wide attention heads");
+    expect(c.rotary_dims % 2 == 0 && c.rotary_dims <= c.Dh, "rope.dimension_count out of range");
+    expect(c.W >= 1 && c.W <= 8, "ssm.conv_kernel must be 1..8");
+    expect(c.D % 256 == 0 && c.FF % 32 == 0, "embedding_length must be a multiple of 256 and feed_forward_length of 32");
+    const GgufFile::Tensor& emb = g.require("token_embd.weight");
+    expect(emb.dims.size() == 2 && int64_t(emb.dims[0]) == c.D, "token_embd.weight has the wrong shape");
+    c.V = int64_t(emb.dims[1]);
+    c.tied = g.find("output.weight") == nullptr;
+
+    hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "stream");
+    hip_check(hipEventCreate(&ev_start_), "event");
+    hip_check(hipEventCreate(&ev_stop_), "event");
+
+    Packer pk{DeviceBuffer(), stream_, &device_bytes_};
+    embedding_ = pk.alloc(c.V, c.D);
+    pk.put(g, "token_embd.weight", embedding_, c.V, c.D, 0, c.V);
+    if (!c.tied) {
+        output_ = pk.alloc(c.V, c.D);
+        pk.put(g, "output.weight", output_, c.V, c.D, 0, c.V);
+    }
+    final_norm_ = upload(host_vector(g, "output_norm.weight", c.D));
+
+    const int64_t CC = c.conv_channels(), VW = c.v_width(), QW = c.q_width(), KW = c.kv_width();
+    for (int64_t l = 0; l < c.L; ++l) {
+        LayerWeights L;
+        L.recurrent = c.is_recurrent(l);
+        L.mixer_norm = upload(host_vector(g, blk(l, "attn_norm.weight"), c.D));
+        L.channel_norm = upload(host_vector(g, blk(l, "post_attention_norm.weight"), c.D));
+        L.w_gate_up = pk.alloc(2 * c.FF, c.D);
+        pk.put(g, blk(l, "ffn_gate.weight"), L.w_gate_up, 2 * c.FF, c.D, 0, c.FF);
+        pk.put(g, blk(l, "ffn_up.weight"), L.w_gate_up, 2 * c.FF, c.D, c.FF, c.FF);
+        L.w_down = pk.alloc(c.D, c.FF);
+        pk.put(g, blk(l, "ffn_down.weight"), L.w_down, c.D, c.FF, 0, c.D);
+        if (L.recurrent) {
+            L.n_in = CC + VW + 2 * c.Hv;
+            L.z_off = CC;
+            L.beta_off = CC + VW;
+            L.alpha_off = CC + VW + c.Hv;
+            L.w_in = pk.alloc(L.n_in, c.D);
+            pk.put(g, blk(l, "attn_qkv.weight"), L.w_in, L.n_in, c.D, 0, CC);
+            pk.put(g, blk(l, "attn_gate.weight"), L.w_in, L.n_in, c.D, L.z_off, VW);
+            pk.put(g, blk(l, "ssm_beta.weight"), L.w_in, L.n_in, c.D, L.beta_off, c.Hv);
+            pk.put(g, blk(l, "ssm_alpha.weight"), L.w_in, L.n_in, c.D, L.alpha_off, c.Hv);
+            L.w_out = pk.alloc(c.D, VW);
+            pk.put(g, blk(l, "ssm_out.weight"), L.w_out, c.D, VW, 0, c.D);
+            const GgufFile::Tensor& conv = g.require(blk(l, "ssm_conv1d.weight"));
+            expect(conv.dims.size() == 2 && int64_t(conv.dims[0]) == c.W && int64_t(conv.dims[1]) == CC, blk(l, "ssm_conv1d.weight") + " has the wrong shape");
+            L.conv = upload(host_vector(g, blk(l, "ssm_conv1d.weight"), CC * c.W));
+            L.dt_bias = upload(host_vector(g, blk(l, "ssm_dt.bias"), c.Hv));
+            std::vector<float> a = host_vector(g, blk(l, "ssm_a"), c.Hv);
+            for (float& x : a) {  // nm/src/qwen35_loader.hpp:108-119
+                if (x > 0.f) x = -std::exp(x);
+                expect(x <= 0.f, blk(l, "ssm_a") + ": decay scale must be <= 0 (-exp(A_log))");
+            }
+            L.decay = upload(a);
+            L.ssm_norm = upload(host_vector(g, blk(l, "ssm_norm.weight"), c.Dv));
+        } else {
+            L.n_in = 2 * QW + 2 * KW;
+            L.k_off = 2 * QW;
+            L.v_off = 2 * QW + KW;
+            L.w_in = pk.alloc(L.n_in, c.D);
+            pk.put(g, blk(l, "attn_q.weight"), L.w_in, L.n_in, c.D, 0, 2 * QW);
+            pk.put(g, blk(l, "attn_k.weight"), L.w_in, L.n_in, c.D, L.k_off, KW);
+            pk.put(g, blk(l, "attn_v.weight"), L.w_in, L.n_in, c.D, L.v_off, KW);
+            L.w_out = pk.alloc(c.D, QW);
+            pk.put(g, blk(l, "attn_output.weight"), L.w_out, c.D, QW, 0, c.D);
+            L.q_norm = upload(host_vector(g, blk(l, "attn_q_norm.weight"), c.Dh));
+            L.k_norm = upload(host_vector(g, blk(l, "attn_k_norm.weight"), c.Dh));
+        }
+        layers_.push_back(std::move(L));
+    }
+    hip_check(hipStreamSynchronize(stream_), "load sync");
+    build_rope_table(std::min<int64_t>(c.CTX, 65536));
+}
+
+// cos/sin per (position, plane) with the reference's float expressions
+// (nm/src/attention.hpp:76-91): inv_freq = float(pow(double base, -2i/Dh)) for
+// the rotary planes and 0 otherwise; angle = float(pos) * inv_freq.
+void Qwen35Model::build_rope_table(int64_t positions) {
+    const int64_t planes = c_.Dh / 2, rotary = c_.rotary_dims / 2;
+    std::vector<float> inv(size_t(planes), 0.f);
+    for (int64_t i = 0; i < planes; ++i) inv[size_t(i)] = i < rotary ? float(std::pow(c_.rope_base, -double(2 * i) / double(c_.Dh))) : 0.f;
+    std::vector<float> cs(size_t(positions * planes * 2));
+    for (int64_t p = 0; p < positions; ++p)
+        for (int64_t i = 0; i < planes; ++i) {
+            const float angle = float(p) * inv[size_t(i)];
+            cs[size_t((p * planes + i) * 2)] = std::cos(angle);
+            cs[size_t((p * planes + i) * 2 + 1)] = std::sin(angle);
+        }
+    rope_cs_ = upload(cs);
+    rope_positions_ = positions;
+}
+
+// ---- state --------------------------------------------------------------------------
+std::unique_ptr<Qwen35Model::State> Qwen35Model::new_state(int64_t max_tokens) const {
+    if (max_tokens <= 0 || max_tokens > c_.CTX || max_tokens > rope_positions_) throw Error(HERO_ERANGE, "state: max_tokens must be in 1.." + std::to_string(std::min(c_.CTX, rope_positions_)));
+    return std::unique_ptr<State>(new State(*this, max_tokens));
+}
+
+Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens) : m_(m), max_tokens_(max_tokens) {
+    const ModelConfig& c = m.c_;
+    int64_t n_in_max = 0;
+    for (const LayerWeights& L : m.layers_) n_in_max = std::max(n_in_max, L.n_in);
+    step_ = DeviceBuffer(16);
+    x_ = DeviceBuffer(size_t(c.D) * 4);
+    h_ = DeviceBuffer(size_t(c.D) * 4);
+    proj_ = DeviceBuffer(size_t(n_in_max) * 4);
+    act_d_ = DeviceBuffer(size_t(act_q8_bytes(1, c.D)));
+    act_mix_ = DeviceBuffer(size_t(act_q8_bytes(1, std::max(c.q_width(), c.v_width()))));
+    act_ff_ = DeviceBuffer(size_t(act_q8_bytes(1, c.FF)));
+    gate_up_ = DeviceBuffer(size_t(2 * c.FF) * 4);
+    logits_ = DeviceBuffer(size_t(c.V) * 4);
+    argmax_scratch_ = DeviceBuffer(128 * 8);
+    out_ids_ = DeviceBuffer(size_t(max_tokens) * 4);
+    out_ids_capacity_ = max_tokens;
+    for (int64_t l = 0; l < c.L; ++l) {
+        if (c.is_recurrent(l)) {
+            k_cache_.emplace_back();
+            v_cache_.emplace_back();
+            scores_.emplace_back();
+            conv_hist_.emplace_back(size_t(c.W * c.conv_channels()) * 4);
+            delta_.emplace_back(size_t(c.Hv * c.Dk * c.Dv) * 4);
+        } else {
+            k_cache_.emplace_back(size_t(max_tokens * c.kv_width()) * 4);
+            v_cache_.emplace_back(size_t(max_tokens * c.kv_width()) * 4);
+            scores_.emplace_back(size_t(max_tokens * c.Hq) * 4);
+            conv_hist_.emplace_back();
+            delta_.emplace_back();
+        }
+    }
+    reset();
+}
+
+Qwen35Model::State::~State() {
+    if (graph_) (void)hipGraphExecDestroy(graph_);
+}
+
+void Qwen35Model::State::reset() {
+    hipStream_t s = m_.stream_;
+    auto zero = [&](DeviceBuffer& b) {
+        if (b.bytes()) hip_check(hipMemsetAsync(b.get(), 0, b.bytes(), s), "state reset");
+    };
+    for (auto& b : k_cache_) zero(b);
+    for (auto& b : v_cache_) zero(b);
+    for (auto& b : conv_hist_) zero(b);
+    for (auto& b : delta_) zero(b);
+    zero(step_);
+    hip_check(hipStreamSynchronize(s), "state reset");
+    tokens_ = 0;
+}
+
+// ---- the step -------------------------------------------------------------------------
+void Qwen35Model::enqueue_step(State& st, bool from_ids, bool with_head) const {
+    const ModelConfig& c = c_;
+    hipStream_t s = stream_;
+    int32_t* step = st.step_.get<int32_t>();
+    float* x = st.x_.get<float>();
+    float* h = st.h_.get<float>();
+    float* proj = st.proj_.get<float>();
+    if (from_ids) launch_embed_q8(embedding_.get(), c.V, c.D, step + 1, 1, x, s);
+    for (int64_t l = 0; l < c.L; ++l) {
+        const LayerWeights& L = layers_[size_t(l)];
+        launch_rmsnorm_quant(x, L.mixer_norm.get<float>(), c.eps, nullptr, st.act_d_.get(), 1, c.D, s);
+        launch_gemv_q8(L.w_in.get(), st.act_d_.get(), proj, nullptr, L.n_in, c.D, kEpiStore, s);
+        int64_t k_mix;
+        if (L.recurrent) {
+            GdnDecodeArgs a{};
+            a.proj = proj;
+            a.proj_stride = L.n_in;
+            a.z_off = L.z_off;
+            a.beta_off = L.beta_off;
+            a.alpha_off = L.alpha_off;
+            a.conv_taps = L.conv.get<float>();
+            a.conv_hist = st.conv_hist_[size_t(l)].get<float>();
+            a.state = st.delta_[size_t(l)].get<float>();
+            a.dt_bias = L.dt_bias.get<float>();
+            a.decay = L.decay.get<float>();
+            a.norm_gamma = L.ssm_norm.get<float>();
+            a.eps = c.eps;
+            a.positions = step;
+            a.act_out = st.act_mix_.get();
+            a.out_f32 = nullptr;
+            a.B = 1;
+            a.Hk = int(c.Hk);
+            a.Hv = int(c.Hv);
+            a.Dk = int(c.Dk);
+            a.Dv = int(c.Dv);
+            a.W = int(c.W);
+            launch_gdn_decode(a, s);
+            k_mix = c.v_width();
+        } else {
+            AttnDecodeArgs a{};
+            a.proj = proj;
+            a.proj_stride = L.n_in;
+            a.k_off = L.k_off;
+            a.v_off = L.v_off;
+            a.q_gamma = L.q_norm.get<float>();
+            a.k_gamma = L.k_norm.get<float>();
+            a.eps = c.eps;
+            a.rope_cs = rope_cs_.get<float>();
+            a.k_cache = st.k_cache_[size_t(l)].get<float>();
+            a.v_cache = st.v_cache_[size_t(l)].get<float>();
+            a.max_ctx = st.max_tokens_;
+            a.positions = step;
+            a.scores = st.scores_[size_t(l)].get<float>();
+            a.score_scale = 1.f / std::sqrt(float(c.Dh));  // qwen35.hpp:359
+            a.window = 0;
+            a.act_out = st.act_mix_.get();
+            a.out_f32 = nullptr;
+            a.B = 1;
+            a.Hq = int(c.Hq);
+            a.Hkv = int(c.Hkv);
+            a.Dh = int(c.Dh);
+            launch_attn_decode(a, s);
+            k_mix = c.q_width();
+        }
+        launch_gemv_q8(L.w_out.get(), st.act_mix_.get(), h, x, c.D, k_mix, kEpiResidual, s);
+        launch_rmsnorm_quant(h, L.channel_norm.get<float>(), c.eps, nullptr, st.act_d_.get(), 1, c.D, s);
+        launch_gemv_q8(L.w_gate_up.get(), st.act_d_.get(), st.gate_up_.get<float>(), nullptr, 2 * c.FF, c.D, kEpiStore, s);
+        launch_swiglu_quant(st.gate_up_.get<float>(), st.act_ff_.get(), 1, c.FF, s);
+        launch_gemv_q8(L.w_down.get(), st.act_ff_.get(), x, h, c.D, c.FF, kEpiResidual, s);
+    }
+    if (with_head) {
+        launch_rmsnorm_quant(x, final_norm_.get<float>(), c.eps, nullptr, st.act_d_.get(), 1, c.D, s);
+        launch_gemv_q8(c.tied ? embedding_.get() : output_.get(), st.act_d_.get(), st.logits_.get<float>(), nullptr, c.V, c.D, kEpiStore, s);
+        launch_argmax(st.logits_.get<float>(), 1, c.V, step + 1, st.argmax_scratch_.get<uint64_t>(), s);
+    }
+    hipLaunchKernelGGL(advance_step_kernel, dim3(1), dim3(1), 0, s, step, st.out_ids_.get<int32_t>(), int32_t(with_head && from_ids));
+    check_launch("decode step");
+}
+
+void Qwen35Model::forward(State& st, const float* rows, const int32_t* ids, int64_t T, float* logits, int32_t* next_id) const {
+    const ModelConfig& c = c_;
+    if (&st.m_ != this) throw Error(HERO_EINVAL, "forward: state belongs to another model");
+    if (T <= 0) throw Error(HERO_EINVAL, "forward: empty input");
+    if (!rows && !ids) throw Error(HERO_EINVAL, "forward: need rows or ids");
+    if (T > st.max_tokens_ - st.tokens_) throw Error(HERO_ERANGE, "Qwen35Model: context exhausted");
+    if (ids)
+        for (int64_t t = 0; t < T; ++t)
+            if (ids[t] < 0 || ids[t] >= c.V) throw Error(HERO_EINVAL, "forward: token id out of range");
+    hipStream_t s = stream_;
+    try {
+        if (rows) {
+            if (st.rows_capacity_ < T) {
+                hip_check(hipStreamSynchronize(s), "sync");
+                st.rows_ = DeviceBuffer(size_t(T * c.D) * 4);
+                st.rows_capacity_ = T;
+            }
+            hip_check(hipMemcpyAsync(st.rows_.get(), rows, size_t(T * c.D) * 4, hipMemcpyHostToDevice, s), "rows upload");
+        }
+        hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, s, st.step_.get<int32_t>(), int32_t(st.tokens_), -1, 0);
+        for (int64_t t = 0; t < T; ++t) {
+            if (rows)
+                hip_check(hipMemcpyAsync(st.x_.get(), st.rows_.get<float>() + t * c.D, size_t(c.D) * 4, hipMemcpyDeviceToDevice, s), "row copy");
+            else
+                hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, s, st.step_.get<int32_t>(), -1, ids[t], -1);
+            enqueue_step(st, rows == nullptr, t == T - 1);
+        }
+        if (logits) hip_check(hipMemcpyAsync(logits, st.logits_.get(), size_t(c.V) * 4, hipMemcpyDeviceToHost, s), "logits download");
+        int32_t scalars[4] = {0, 0, 0, 0};
+        hip_check(hipMemcpyAsync(scalars, st.step_.get(), 16, hipMemcpyDeviceToHost, s), "step download");
+        hip_check(hipStreamSynchronize(s), "forward");
+        if (next_id) *next_id = scalars[1];
+        st.tokens_ += T;
+    } catch (...) {
+        // the carried state is now unknown: forget it (transformer.hpp:139-142)
+        (void)hipStreamSynchronize(s);
+        st.reset();
+        throw;
+    }
+}
+
+void Qwen35Model::decode_greedy(State& st, int32_t first_id, int64_t steps, int32_t* out_ids, float* logits) const {
+    const ModelConfig& c = c_;
+    if (&st.m_ != this) throw Error(HERO_EINVAL, "decode: state belongs to another model");
+    if (steps <= 0) throw Error(HERO_EINVAL, "decode: steps must be positive");
+    if (first_id < 0 || first_id >= c.V) throw Error(HERO_EINVAL, "decode: token id out of range");
+    if (steps > st.max_tokens_ - st.tokens_) throw Error(HERO_ERANGE, "Qwen35Model: context exhausted");
+    hipStream_t s = stream_;
+    try {
+        if (!st.graph_) {
+            hipGraph_t graph = nullptr;
+            hip_check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "capture begin");
+            enqueue_step(st, true, true);
+            hip_check(hipStreamEndCapture(s, &graph), "capture end");
+            hip_check(hipGraphInstantiate(&st.graph_, graph, nullptr, nullptr, 0), "graph instantiate");
+            (void)hipGraphDestroy(graph);
+        }
+        hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, s, st.step_.get<int32_t>(), int32_t(st.tokens_), first_id, 0);
+        hip_check(hipEventRecord(ev_start_, s), "event");
+        for (int64_t i = 0; i < steps; ++i) hip_check(hipGraphLaunch(st.graph_, s), "graph launch");
+        hip_check(hipEventRecord(ev_stop_, s), "event");
+        hip_check(hipMemcpyAsync(out_ids, st.out_ids_.get(), size_t(steps) * 4, hipMemcpyDeviceToHost, s), "ids download");
+        if (logits) hip_check(hipMemcpyAsync(logits, st.logits_.get(), size_t(c.V) * 4, hipMemcpyDeviceToHost, s), "logits download");
+        hip_check(hipStreamSynchronize(s), "decode");
+        float ms = 0.f;
+        hip_check(hipEventElapsedTime(&ms, ev_start_, ev_stop_), "event time");
+        last_decode_seconds_ = double(ms) * 1e-3;
+        st.tokens_ += steps;
+    } catch (...) {
+        (void)hipStreamSynchronize(s);
+        st.reset();
+        throw;
+    }
+}
+
+void Qwen35Model::embed(const int32_t* ids, int64_t n, float* out) const {
+    if (n <= 0) throw Error(HERO_EINVAL, "embed: empty input");
+    for (int64_t i = 0; i < n; ++i)
+        if (ids[i] < 0 || ids[i] >= c_.V) throw Error(HERO_EINVAL, "embed: token id out of range");
+    DeviceBuffer d_ids(size_t(n) * 4), d_out(size_t(n * c_.D) * 4);
+    hip_check(hipMemcpyAsync(d_ids.get(), ids, size_t(n) * 4, hipMemcpyHostToDevice, stream_), "ids upload");
+    launch_embed_q8(embedding_.get(), c_.V, c_.D, d_ids.get<int32_t>(), n, d_out.get<float>(), stream_);
+    check_launch("embed");
+    hip_check(hipMemcpyAsync(out, d_out.get(), size_t(n * c_.D) * 4, hipMemcpyDeviceToHost, stream_), "rows download");
+    hip_check(hipStreamSynchronize(stream_), "embed");
+}
+
+}  // namespace hero

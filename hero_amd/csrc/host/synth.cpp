@@ -1,0 +1,303 @@
+// synth.cpp -- seeded random-init Qwen 3.5-style hybrid models written as
+// GGUF v3 images with Q8_0 weights, in the `qwen35` schema that
+// nm/src/qwen35_loader.hpp:30-155 reads.
+//
+// Every element is a pure function of (seed, tensor index, element index):
+// a splitmix64 counter hash gives two uniforms, Box-Muller (in double) gives
+// a standard normal, and the value is scale*normal rounded to fp32. 2-D
+// tensors are then quantized to Q8_0 with the reference weight quantizer
+// (nm/src/quant.hpp:404-413: d = amax/127, q = lround(x/d), d stored through
+// the reference fp16 encoder). Rows are generated in parallel; the bytes do
+// not depend on the thread count.
+//
+// Fixed choices the workload description leaves open:
+//   2-D weights N(0, 0.02); RMSNorm / q_norm / k_norm / ssm_norm gamma = 1;
+//   conv taps N(0, 0.5); ssm_a = -exp(N(0, 0.5)); ssm_dt.bias = 0;
+//   rope.dimension_count = head_dim/4 (Qwen 3.5's partial rotary factor).
+#include "hero/synth.hpp"
+
+#include "hero/fp16.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+namespace hero {
+
+namespace {
+
+inline uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+// Standard normal for element i of a stream.
+inline double normal_at(uint64_t stream, uint64_t i) {
+    const uint64_t a = splitmix64(stream ^ splitmix64(2 * i));
+    const uint64_t b = splitmix64(stream ^ splitmix64(2 * i + 1));
+    const double u1 = (double(a >> 11) + 0.5) * (1.0 / 9007199254740992.0);  // (0,1)
+    const double u2 = double(b >> 11) * (1.0 / 9007199254740992.0);          // [0,1)
+    return std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
+}
+
+inline uint64_t stream_of(uint64_t seed, uint64_t tensor_index) { return splitmix64(seed * 0x632BE59BD9B4E019ull + tensor_index + 1); }
+
+// Reference weight quantizer for one 32-block.
+void quantize_block_lround(const float* x, uint8_t* out34) {
+    float amax = 0.f;
+    for (int j = 0; j < 32; ++j) amax = std::max(amax, std::fabs(x[j]));
+    const float d = amax / 127.f;
+    const float id = d != 0.f ? 1.f / d : 0.f;
+    const uint16_t dh = fp32_to_fp16_ref(d);
+    std::memcpy(out34, &dh, 2);
+    for (int j = 0; j < 32; ++j) out34[2 + j] = uint8_t(int8_t(std::lround(x[j] * id)));
+}
+
+template <class F>
+void parallel_rows(size_t rows, F&& f) {
+    size_t threads = std::max<size_t>(1, std::min<size_t>(std::thread::hardware_concurrency(), 32));
+    threads = std::min(threads, std::max<size_t>(1, rows / 64));
+    if (threads <= 1) {
+        for (size_t r = 0; r < rows; ++r) f(r);
+        return;
+    }
+    std::vector<std::thread> pool;
+    for (size_t t = 0; t < threads; ++t)
+        pool.emplace_back([&, t] {
+            for (size_t r = t; r < rows; r += threads) f(r);
+        });
+    for (auto& th : pool) th.join();
+}
+
+// ---- GGUF image builder ------------------------------------------------------
+enum : uint32_t { GGUF_U32 = 4, GGUF_F32 = 6, GGUF_STRING = 8, GGUF_ARRAY = 9 };
+enum : uint32_t { T_F32 = 0, T_Q8_0 = 8 };
+
+struct TensorSpec {
+    std::string name;
+    uint64_t in = 0, out = 1;  // ggml dims [in, out]; a vector has out == 1 and one dim
+    bool matrix = false;
+    uint32_t type = T_F32;
+    enum Kind { Normal, Ones, Zeros, NegExpNormal } kind = Normal;
+    double scale = 0.02;
+    uint64_t offset = 0, bytes = 0;
+};
+
+struct Writer {
+    std::vector<uint8_t> buf;
+    void raw(const void* p, size_t n) {
+        const uint8_t* b = static_cast<const uint8_t*>(p);
+        buf.insert(buf.end(), b, b + n);
+    }
+    void u32(uint32_t v) { raw(&v, 4); }
+    void u64(uint64_t v) { raw(&v, 8); }
+    void f32(float v) { raw(&v, 4); }
+    void str(const std::string& s) {
+        u64(s.size());
+        raw(s.data(), s.size());
+    }
+    void kv_u32(const std::string& k, uint32_t v) {
+        str(k);
+        u32(GGUF_U32);
+        u32(v);
+    }
+    void kv_f32(const std::string& k, float v) {
+        str(k);
+        u32(GGUF_F32);
+        f32(v);
+    }
+    void kv_str(const std::string& k, const std::string& v) {
+        str(k);
+        u32(GGUF_STRING);
+        str(v);
+    }
+    void kv_u32_array(const std::string& k, const std::vector<uint32_t>& v) {
+        str(k);
+        u32(GGUF_ARRAY);
+        u32(GGUF_U32);
+        u64(v.size());
+        for (uint32_t x : v) u32(x);
+    }
+};
+
+std::vector<TensorSpec> tensor_specs(const SynthConfig& c) {
+    std::vector<TensorSpec> t;
+    auto mat = [&](const std::string& name, uint64_t in, uint64_t out) {
+        TensorSpec s;
+        s.name = name;
+        s.in = in;
+        s.out = out;
+        s.matrix = true;
+        s.type = T_Q8_0;
+        t.push_back(s);
+    };
+    auto vec = [&](const std::string& name, uint64_t n, TensorSpec::Kind kind, double scale = 0.0) {
+        TensorSpec s;
+        s.name = name;
+        s.in = n;
+        s.kind = kind;
+        s.scale = scale;
+        t.push_back(s);
+    };
+    const uint64_t D = c.D, CC = 2 * c.Hk * c.Dk + c.Hv * c.Dv;
+    mat("token_embd.weight", D, c.V);
+    vec("output_norm.weight", D, TensorSpec::Ones);
+    if (!c.tied) mat("output.weight", D, c.V);
+    for (uint64_t l = 0; l < c.L; ++l) {
+        const std::string b = "blk." + std::to_string(l) + ".";
+        vec(b + "attn_norm.weight", D, TensorSpec::Ones);
+        vec(b + "post_attention_norm.weight", D, TensorSpec::Ones);
+        mat(b + "ffn_gate.weight", D, c.FF);
+        mat(b + "ffn_up.weight", D, c.FF);
+        mat(b + "ffn_down.weight", c.FF, D);
+        if ((l + 1) % 4 != 0) {
+            mat(b + "attn_qkv.weight", D, CC);
+            mat(b + "attn_gate.weight", D, c.Hv * c.Dv);
+            TensorSpec conv;
+            conv.name = b + "ssm_conv1d.weight";
+            conv.in = c.conv_width;
+            conv.out = CC;
+            conv.matrix = true;  // 2-D F32 [conv_width, CC]
+            conv.type = T_F32;
+            conv.scale = 0.5;
+            t.push_back(conv);
+            vec(b + "ssm_a", c.Hv, TensorSpec::NegExpNormal, 0.5);
+            mat(b + "ssm_beta.weight", D, c.Hv);
+            mat(b + "ssm_alpha.weight", D, c.Hv);
+            vec(b + "ssm_dt.bias", c.Hv, TensorSpec::Zeros);
+            vec(b + "ssm_norm.weight", c.Dv, TensorSpec::Ones);
+            mat(b + "ssm_out.weight", c.Hv * c.Dv, D);
+        } else {
+            mat(b + "attn_q.weight", D, 2 * c.Hq * c.head_dim);
+            vec(b + "attn_q_norm.weight", c.head_dim, TensorSpec::Ones);
+            mat(b + "attn_k.weight", D, c.Hkv * c.head_dim);
+            vec(b + "attn_k_norm.weight", c.head_dim, TensorSpec::Ones);
+            mat(b + "attn_v.weight", D, c.Hkv * c.head_dim);
+            mat(b + "attn_output.weight", c.Hq * c.head_dim, D);
+        }
+    }
+    return t;
+}
+
+std::vector<uint8_t> header_bytes(const SynthConfig& c, std::vector<TensorSpec>& specs, uint64_t& data_start, uint64_t& total) {
+    Writer w;
+    w.u32(0x46554747u);
+    w.u32(3);
+    w.u64(specs.size());
+    const uint64_t kv_count = 20;
+    w.u64(kv_count);
+    w.kv_str("general.architecture", "qwen35");
+    w.kv_u32("general.alignment", 32);
+    w.kv_u32("qwen35.block_count", uint32_t(c.L));
+    w.kv_u32("qwen35.context_length", uint32_t(c.ctx));
+    w.kv_u32("qwen35.embedding_length", uint32_t(c.D));
+    w.kv_u32("qwen35.feed_forward_length", uint32_t(c.FF));
+    w.kv_u32("qwen35.attention.head_count", uint32_t(c.Hq));
+    w.kv_u32("qwen35.attention.head_count_kv", uint32_t(c.Hkv));
+    w.kv_u32("qwen35.attention.key_length", uint32_t(c.head_dim));
+    w.kv_u32("qwen35.attention.value_length", uint32_t(c.head_dim));
+    w.kv_f32("qwen35.attention.layer_norm_rms_epsilon", 1e-6f);
+    w.kv_f32("qwen35.rope.freq_base", float(c.rope_base));
+    w.kv_u32("qwen35.rope.dimension_count", uint32_t(c.head_dim / 4));
+    w.kv_u32("qwen35.ssm.conv_kernel", uint32_t(c.conv_width));
+    w.kv_u32("qwen35.ssm.state_size", uint32_t(c.Dk));
+    w.kv_u32("qwen35.ssm.group_count", uint32_t(c.Hk));
+    w.kv_u32("qwen35.ssm.time_step_rank", uint32_t(c.Hv));
+    w.kv_u32("qwen35.ssm.inner_size", uint32_t(c.Hv * c.Dv));
+    w.kv_u32("qwen35.full_attention_interval", 4);
+    std::vector<uint32_t> recurrent(c.L);
+    for (uint64_t l = 0; l < c.L; ++l) recurrent[l] = (l + 1) % 4 != 0;
+    w.kv_u32_array("qwen35.attention.recurrent_layers", recurrent);
+    uint64_t offset = 0;
+    for (TensorSpec& s : specs) {
+        const uint64_t n = s.in * s.out;
+        s.bytes = s.type == T_Q8_0 ? n / 32 * 34 : n * 4;
+        s.offset = offset;
+        offset = (offset + s.bytes + 31) & ~uint64_t(31);
+        w.str(s.name);
+        if (s.matrix) {
+            w.u32(2);
+            w.u64(s.in);
+            w.u64(s.out);
+        } else {
+            w.u32(1);
+            w.u64(s.in);
+        }
+        w.u32(s.type);
+        w.u64(s.offset);
+    }
+    data_start = (w.buf.size() + 31) & ~uint64_t(31);
+    total = data_start + offset;
+    w.buf.resize(data_start, 0);
+    return std::move(w.buf);
+}
+
+void fill_tensor(const SynthConfig& c, const TensorSpec& s, uint64_t tensor_index, uint8_t* dst) {
+    const uint64_t stream = stream_of(c.seed, tensor_index);
+    if (s.type == T_Q8_0) {
+        const uint64_t in = s.in, blocks = in / 32;
+        parallel_rows(s.out, [&](size_t r) {
+            std::vector<float> row(in);
+            for (uint64_t i = 0; i < in; ++i) row[i] = float(0.02 * normal_at(stream, uint64_t(r) * in + i));
+            for (uint64_t b = 0; b < blocks; ++b) quantize_block_lround(row.data() + b * 32, dst + (uint64_t(r) * blocks + b) * 34);
+        });
+        return;
+    }
+    const uint64_t n = s.in * s.out;
+    float* f = reinterpret_cast<float*>(dst);
+    for (uint64_t i = 0; i < n; ++i) {
+        switch (s.kind) {
+            case TensorSpec::Ones: f[i] = 1.f; break;
+            case TensorSpec::Zeros: f[i] = 0.f; break;
+            case TensorSpec::Normal: f[i] = float(s.scale * normal_at(stream, i)); break;
+            case TensorSpec::NegExpNormal: f[i] = -float(std::exp(s.scale * normal_at(stream, i))); break;
+        }
+    }
+}
+
+void check_config(const SynthConfig& c) {
+    if (c.L == 0 || c.L % 4 != 0) throw std::invalid_argument("synth: L must be a positive multiple of 4");
+    if (c.D % 32 || c.FF % 32 || (c.Hv * c.Dv) % 32 || (c.Hq * c.head_dim) % 32) throw std::invalid_argument("synth: every Q8_0 input width must be a multiple of 32");
+    if (c.Hkv == 0 || c.Hq % c.Hkv || c.Hk == 0 || c.Hv % c.Hk || c.Dk != c.Dv || c.head_dim % 8) throw std::invalid_argument("synth: inconsistent head shapes");
+}
+
+}  // namespace
+
+uint64_t synth_qwen35_size(const SynthConfig& c) {
+    check_config(c);
+    std::vector<TensorSpec> specs = tensor_specs(c);
+    uint64_t data_start = 0, total = 0;
+    header_bytes(c, specs, data_start, total);
+    return total;
+}
+
+void synth_qwen35_image(const SynthConfig& c, uint8_t* image, uint64_t capacity) {
+    check_config(c);
+    std::vector<TensorSpec> specs = tensor_specs(c);
+    uint64_t data_start = 0, total = 0;
+    const std::vector<uint8_t> header = header_bytes(c, specs, data_start, total);
+    if (capacity < total) throw std::invalid_argument("synth: image buffer too small");
+    std::memcpy(image, header.data(), header.size());
+    std::memset(image + header.size(), 0, size_t(total - header.size()));
+    for (size_t i = 0; i < specs.size(); ++i) fill_tensor(c, specs[i], i, image + data_start + specs[i].offset);
+}
+
+void synth_qwen35_file(const SynthConfig& c, const std::string& path) {
+    const uint64_t total = synth_qwen35_size(c);
+    std::vector<uint8_t> image(total);
+    synth_qwen35_image(c, image.data(), total);
+    FILE* f = std::fopen(path.c_str(), "wb");
+    if (!f) throw std::runtime_error("synth: cannot write " + path);
+    const size_t wrote = std::fwrite(image.data(), 1, image.size(), f);
+    std::fclose(f);
+    if (wrote != image.size()) throw std::runtime_error("synth: short write to " + path);
+}
+
+}  // namespace hero

@@ -1,0 +1,100 @@
+// ew.hip -- small elementwise kernels around the GEMVs: SwiGLU + quantize,
+// the Q8_0 embedding gather, and the greedy argmax.
+#include "hero/device.hpp"
+#include "hero/kernels.hpp"
+
+namespace hero {
+
+// nm/src/components.hpp:300-304 (GatedMLP): g = silu(gate(x)) * up(x), then
+// the down projection quantizes g. gate_up row = [gate FF | up FF].
+__global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restrict__ gu, int8_t* __restrict__ qs, float* __restrict__ qd, int64_t FF, int64_t total8) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= total8) return;
+    const int64_t per_row = FF >> 3;
+    const int64_t row = i / per_row, g = i - row * per_row;
+    const float* gate = gu + row * 2 * FF + g * 8;
+    const float* up = gate + FF;
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = silu_f32(gate[j]) * up[j];
+    uint16_t dh;
+    const int2 q = quantize8_in_quad(v, &dh);
+    reinterpret_cast<int2*>(qs)[i] = q;
+    if ((i & 3) == 0) qd[i >> 2] = half_bits_to_f32(dh);
+}
+
+void launch_swiglu_quant(const float* gate_up, void* act, int64_t M, int64_t FF, hipStream_t s) {
+    int8_t* qs = static_cast<int8_t*>(act);
+    float* qd = reinterpret_cast<float*>(qs + M * FF);
+    const int64_t total8 = M * FF / 8;
+    hipLaunchKernelGGL(swiglu_quant_kernel, dim3(unsigned((total8 + 255) / 256)), dim3(256), 0, s, gate_up, qs, qd, FF, total8);
+}
+
+// nm/src/quant.hpp:306-313: row = d * q
+__global__ __launch_bounds__(256) void embed_kernel(const int8_t* __restrict__ qs, const uint16_t* __restrict__ d, int64_t D, const int32_t* __restrict__ ids, float* __restrict__ out) {
+    const int64_t t = blockIdx.y;
+    const int64_t id = ids[t];
+    for (int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; c < D; c += int64_t(gridDim.x) * blockDim.x) {
+        const float scale = half_bits_to_f32(d[id * (D >> 5) + (c >> 5)]);
+        out[t * D + c] = scale * float(qs[id * D + c]);
+    }
+}
+
+void launch_embed_q8(const void* packed, int64_t V, int64_t D, const int32_t* ids, int64_t n, float* out, hipStream_t s) {
+    const int8_t* qs = static_cast<const int8_t*>(packed);
+    const uint16_t* d = reinterpret_cast<const uint16_t*>(qs + V * D);
+    hipLaunchKernelGGL(embed_kernel, dim3(unsigned((D + 255) / 256), unsigned(n)), dim3(256), 0, s, qs, d, D, ids, out);
+}
+
+// Greedy argmax (nm/src/logits.hpp:61-66): largest value, ties to the lowest
+// index. A key orders (value, -index): the value's bits mapped to an
+// order-preserving unsigned, -0 folded onto +0 so they tie as in `>`.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t index) {
+    uint32_t u = f32_bits(v == 0.f ? 0.f : v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (uint64_t(u) << 32) | uint64_t(0xFFFFFFFFu - index);
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint64_t o = __shfl_xor(k, off);
+        k = o > k ? o : k;
+    }
+    return k;
+}
+
+constexpr int kArgmaxGroups = 128;
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ logits, int64_t n, uint64_t* __restrict__ partial) {
+    const int64_t row = blockIdx.y;
+    const float* l = logits + row * n;
+    uint64_t best = 0;
+    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) {
+        const uint64_t k = argmax_key(l[i], uint32_t(i));
+        best = k > best ? k : best;
+    }
+    best = wave_max_u64(best);
+    __shared__ uint64_t waves[4];
+    if ((threadIdx.x & 63) == 0) waves[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = waves[0];
+        for (int w = 1; w < 4; ++w) b = waves[w] > b ? waves[w] : b;
+        partial[row * gridDim.x + blockIdx.x] = b;
+    }
+}
+
+__global__ __launch_bounds__(64) void argmax_final_kernel(const uint64_t* __restrict__ partial, int parts, int32_t* __restrict__ out) {
+    const int64_t row = blockIdx.x;
+    uint64_t best = 0;
+    for (int i = threadIdx.x; i < parts; i += 64) best = partial[row * parts + i] > best ? partial[row * parts + i] : best;
+    best = wave_max_u64(best);
+    if (threadIdx.x == 0) out[row] = int32_t(0xFFFFFFFFu - uint32_t(best & 0xFFFFFFFFu));
+}
+
+void launch_argmax(const float* logits, int64_t M, int64_t n, int32_t* out_index, uint64_t* scratch, hipStream_t s) {
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxGroups, unsigned(M)), dim3(256), 0, s, logits, n, scratch);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(unsigned(M)), dim3(64), 0, s, scratch, kArgmaxGroups, out_index);
+}
+
+}  // namespace hero

@@ -1,0 +1,133 @@
+/* hero_kernels.h -- C ABI of the gfx950 kernels under the Q8_0 Qwen 3.5 hybrid
+ * forward pass. Plain pointers and sizes only: every buffer argument is a
+ * DEVICE pointer (hipMalloc'd or a view into one), every `stream` is a
+ * hipStream_t passed as void* (NULL = the default stream). Calls enqueue work
+ * and return; they do not synchronize.
+ *
+ * Return value: 0 on success, otherwise a HERO_E* code; hero_last_error()
+ * then describes the failure (thread-local). Shapes are validated before
+ * anything is enqueued.
+ *
+ * Layouts
+ *   Q8_0 GGUF blocks   [N][K/32] x 34 bytes {fp16 d; int8 q[32]}, row-major by
+ *                      output row (the GGUF / ggml tensor layout).
+ *   packed weight      [N*K int8 q][N*(K/32) fp16 d]        hero_q8_0_packed_bytes()
+ *   quantized act      [M*K int8 q][M*(K/32) fp32 d]        hero_q8_0_act_bytes()
+ *                      (d is the fp16-rounded scale, decoded exactly)
+ */
+#ifndef HERO_KERNELS_H
+#define HERO_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    HERO_OK = 0,
+    HERO_EINVAL = 1,  /* bad shape, null or misaligned pointer */
+    HERO_EHIP = 2,    /* a HIP runtime call failed */
+    HERO_ERANGE = 3,  /* context or position out of range */
+    HERO_ENOMEM = 4,  /* device allocation failed */
+    HERO_EIO = 5      /* file / GGUF format error */
+};
+
+const char* hero_last_error(void);
+const char* hero_version(void);
+
+int64_t hero_q8_0_packed_bytes(int64_t n, int64_t k);
+int64_t hero_q8_0_act_bytes(int64_t m, int64_t k);
+
+/* GGUF Q8_0 blocks -> packed layout. Replaces the zero-copy Weight view of
+ * nm/src/quant.hpp:448-451 (weights are uploaded once, then repacked).
+ * `row0` places the rows at an offset inside a packed buffer of `n_total`
+ * rows, so several GGUF tensors with the same K can share one packed matrix. */
+int hero_q8_0_pack(const void* gguf_blocks, void* packed, int64_t n_total, int64_t k, int64_t row0, int64_t rows, void* stream);
+
+/* quantize_row_q8_0 on M rows (nm/src/quant_i8.hpp:70-80; ActQ::from,
+ * :329-341). x: [M][K] fp32. Bit-exact. K % 32 == 0. */
+int hero_q8_0_quantize(const float* x, void* act, int64_t m, int64_t k, void* stream);
+
+/* y[N] = W[N,K] x for one quantized activation row: Weight::matvec
+ * (nm/src/quant_i8.hpp:352-383), per-row block order preserved (bit-exact).
+ * If `residual` is non-NULL, y = residual + W x (the residual add of
+ * nm/src/qwen35.hpp:321,326). */
+int hero_q8_0_gemv(const void* packed, const void* act, float* y, const float* residual, int64_t n, int64_t k, void* stream);
+
+/* Exact int32 block dot products out[N][K/32] of one activation row: the
+ * `sumi` of nm/src/quant_i8.hpp:94-95, exported for parity checks. */
+int hero_q8_0_block_sums(const void* packed, const void* act, int32_t* out, int64_t n, int64_t k, void* stream);
+
+/* RMSNorm over each of M rows of D, then Q8_0 quantization
+ * (nm/src/components.hpp:176-181 followed by quant_i8.hpp:70-80).
+ * y (fp32 normalized rows) and act may each be NULL. D % 32 == 0. */
+int hero_rmsnorm_quant(const float* x, const float* gamma, float eps, float* y, void* act, int64_t m, int64_t d, void* stream);
+
+/* SwiGLU + quantize: g = silu(gate) * up over rows [gate FF | up FF]
+ * (nm/src/components.hpp:300-304), quantized for the down projection. */
+int hero_swiglu_quant(const float* gate_up, void* act, int64_t m, int64_t ff, void* stream);
+
+/* Embedding gather from a packed Q8_0 table [V][D]: out[i] = d*q
+ * (Weight::gather_rows, nm/src/quant.hpp:464-480). */
+int hero_q8_0_embed(const void* packed, int64_t v, int64_t d, const int32_t* ids, int64_t n, float* out, void* stream);
+
+/* Greedy argmax of M rows of n logits, ties to the lowest index
+ * (Logits::argmax, nm/src/logits.hpp:61-66). scratch: M*128 uint64. */
+int hero_argmax(const float* logits, int64_t m, int64_t n, int32_t* out, uint64_t* scratch, void* stream);
+
+/* Gated delta-net decode, one token for each of B sequences, all Hv heads:
+ * conv step + SiLU, q/k L2 norm, beta/decay gates, the gated delta rule,
+ * per-head RMSNorm, SiLU(z) gate, Q8_0 quantization of the output
+ * projection's input. Replaces the per-token body of
+ * QwenGatedDeltaNet mix_tokens (nm/src/qwen35.hpp:420-462) together with
+ * gated_delta_step (nm/src/recurrent.hpp:146-177). Dk = Dv = 128. */
+typedef struct hero_gdn_decode_args {
+    const float* proj;       /* [B][proj_stride] input projections, fp32 */
+    int64_t proj_stride;     /* floats per sequence */
+    int64_t z_off, beta_off, alpha_off; /* offsets of z [Hv*Dv], beta [Hv], alpha [Hv]; qkv at 0 */
+    const float* conv_taps;  /* [CC][W], CC = 2*Hk*Dk + Hv*Dv */
+    float* conv_hist;        /* [B][W][CC] ring, zero-initialized for a new sequence */
+    float* state;            /* [B][Hv][Dk][Dv] fp32, zero for a new sequence */
+    const float* dt_bias;    /* [Hv] */
+    const float* decay;      /* [Hv] = -exp(A_log) <= 0 */
+    const float* norm_gamma; /* [Dv] */
+    float eps;
+    const int32_t* positions;/* [B] position of the token being decoded */
+    void* act_out;           /* quantized act [B][Hv*Dv] */
+    float* out_f32;          /* optional [B][Hv*Dv] */
+    int32_t b, hk, hv, dk, dv, conv_width;
+} hero_gdn_decode_args;
+int hero_gdn_decode(const hero_gdn_decode_args* args, void* stream);
+
+/* Gated GQA attention decode over an fp32 K/V cache, one token for each of
+ * B sequences: head-pair split, q/k RMSNorm + RoPE (host table), cache
+ * append, softmax(scale*q.k) over the visible rows, sum alpha*v,
+ * sigmoid(gate), Q8_0 quantization for the output projection. Replaces the
+ * attention body of nm/src/qwen35.hpp:343-395 (window == 0) and the
+ * sliding-window visibility of nm/src/attention.hpp:159-176 (window > 0). */
+typedef struct hero_attn_decode_args {
+    const float* proj;       /* [B][proj_stride]: [q|gate] head pairs at 0, k, v */
+    int64_t proj_stride, k_off, v_off;
+    const float* q_gamma;    /* [Dh] */
+    const float* k_gamma;    /* [Dh] */
+    float eps;
+    const float* rope_cs;    /* [max_pos][Dh/2][2] cos, sin */
+    float* k_cache;          /* [B][max_ctx][Hkv*Dh] */
+    float* v_cache;
+    int64_t max_ctx;
+    const int32_t* positions;/* [B] */
+    float* scores;           /* scratch [B][Hq][max_ctx] */
+    float score_scale;       /* 1/sqrt(Dh) for Qwen, 1 for Gemma-style */
+    int32_t window;          /* 0 = full causal */
+    void* act_out;           /* quantized act [B][Hq*Dh] */
+    float* out_f32;          /* optional [B][Hq*Dh] */
+    int32_t b, hq, hkv, dh;
+} hero_attn_decode_args;
+int hero_attn_decode(const hero_attn_decode_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HERO_KERNELS_H */

@@ -1,0 +1,287 @@
+"""The oracle: a CPU restatement of the reference engine's Q8_0 Qwen 3.5 hybrid
+path (oracle.cpp, built into liboracle.so by oracle/Makefile).
+
+TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py may use it, and only as the checker or the
+timed CPU baseline -- never as part of the product path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_size_t, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_HARNESS = os.path.join(HERE, "_ref", "ref_harness")
+
+_sigs = {
+    "oracle_last_error": (c_char_p, []),
+    "oracle_set_threads": (None, [c_size_t]),
+    "oracle_threads": (c_size_t, []),
+    "oracle_fp16_to_fp32": (None, [c_void_p, c_void_p, c_size_t]),
+    "oracle_fp32_to_fp16": (None, [c_void_p, c_void_p, c_size_t]),
+    "oracle_quantize_row_q8_0": (None, [c_void_p, c_void_p, c_size_t]),
+    "oracle_quantize_q8_0": (None, [c_void_p, c_void_p, c_size_t]),
+    "oracle_vec_dot_q8_0": (c_float, [c_size_t, c_void_p, c_void_p]),
+    "oracle_block_sums_q8_0": (None, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+    "oracle_matvec_q8_0": (None, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+    "oracle_matmul_q8_0": (None, [c_void_p, c_size_t, c_size_t, c_void_p, c_size_t, c_void_p]),
+    "oracle_rmsnorm_rows": (None, [c_void_p, c_void_p, c_size_t, c_size_t, c_float]),
+    "oracle_l2_normalize": (None, [c_void_p, c_void_p, c_size_t, c_float]),
+    "oracle_silu": (None, [c_void_p, c_void_p, c_size_t]),
+    "oracle_sigmoid": (None, [c_void_p, c_void_p, c_size_t]),
+    "oracle_softplus": (None, [c_void_p, c_void_p, c_size_t]),
+    "oracle_softmax": (None, [c_void_p, c_size_t]),
+    "oracle_conv_step": (None, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_size_t]),
+    "oracle_gated_delta_step": (None, [c_void_p] * 7 + [c_size_t] * 4),
+    "oracle_rope_inv_freq": (None, [c_size_t, c_double, c_size_t, c_void_p]),
+    "oracle_rope_apply": (None, [c_void_p, c_size_t, c_void_p, c_size_t, c_size_t]),
+    "oracle_attend_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_size_t, c_size_t, c_float, c_void_p]),
+    "oracle_model_open": (c_void_p, [c_char_p]),
+    "oracle_model_open_image": (c_void_p, [c_void_p, c_size_t]),
+    "oracle_model_close": (None, [c_void_p]),
+    "oracle_model_dims": (None, [c_void_p, c_void_p]),
+    "oracle_model_reset": (None, [c_void_p]),
+    "oracle_model_tokens": (c_size_t, [c_void_p]),
+    "oracle_model_embed": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "oracle_model_forward": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "oracle_model_forward_ids": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "oracle_argmax": (c_int32, [c_void_p, c_size_t]),
+    "oracle_model_greedy": (c_int, [c_void_p, c_void_p, c_size_t, c_size_t, c_void_p, c_void_p, POINTER(c_double), POINTER(c_double)]),
+}
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built; run make -C oracle")
+    lib = ctypes.CDLL(LIB_PATH)
+    for n, (r, a) in _sigs.items():
+        f = getattr(lib, n)
+        f.restype = r
+        f.argtypes = a
+    return lib
+
+
+lib = _load()
+BLOCK = np.dtype([("d", "<u2"), ("qs", "i1", 32)])  # Q8_0 block, 34 bytes
+
+
+def _p(a):
+    return a.ctypes.data if a is not None else None
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def set_threads(n: int) -> None:
+    lib.oracle_set_threads(n)
+
+
+def threads() -> int:
+    return int(lib.oracle_threads())
+
+
+def fp16_to_fp32(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib.oracle_fp16_to_fp32(_p(h), _p(out), h.size)
+    return out
+
+
+def fp32_to_fp16(f):
+    f = _f32(f)
+    out = np.empty(f.shape, np.uint16)
+    lib.oracle_fp32_to_fp16(_p(f), _p(out), f.size)
+    return out
+
+
+def quantize_row_q8_0(x):
+    """activation quantizer (roundf) -> Q8_0 blocks [K/32]"""
+    x = _f32(x).ravel()
+    out = np.zeros(x.size // 32, BLOCK)
+    lib.oracle_quantize_row_q8_0(_p(x), _p(out), x.size)
+    return out
+
+
+def quantize_q8_0(x):
+    """weight quantizer (lround) -> Q8_0 blocks, row-major"""
+    x = _f32(x)
+    out = np.zeros(x.size // 32, BLOCK)
+    lib.oracle_quantize_q8_0(_p(x), _p(out), x.size)
+    return out
+
+
+def vec_dot_q8_0(w_blocks, x_blocks) -> np.float32:
+    return np.float32(lib.oracle_vec_dot_q8_0(w_blocks.size * 32, _p(w_blocks), _p(x_blocks)))
+
+
+def block_sums(w_blocks, n, k, x_blocks):
+    out = np.empty((n, k // 32), np.int32)
+    lib.oracle_block_sums_q8_0(_p(w_blocks), n, k, _p(x_blocks), _p(out))
+    return out
+
+
+def matvec(w_blocks, n, k, x):
+    x = _f32(x)
+    y = np.empty(n, np.float32)
+    lib.oracle_matvec_q8_0(_p(w_blocks), n, k, _p(x), _p(y))
+    return y
+
+
+def matmul(w_blocks, n, k, X):
+    X = _f32(X)
+    t = X.shape[0]
+    Y = np.empty((t, n), np.float32)
+    lib.oracle_matmul_q8_0(_p(w_blocks), n, k, _p(X), t, _p(Y))
+    return Y
+
+
+def rmsnorm(x, gamma, eps=1e-6):
+    x = _f32(x).copy()
+    g = _f32(gamma)
+    rows = x.size // g.size
+    lib.oracle_rmsnorm_rows(_p(x), _p(g), rows, g.size, eps)
+    return x
+
+
+def l2_normalize(x, eps=1e-6):
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib.oracle_l2_normalize(_p(x), _p(out), x.size, eps)
+    return out
+
+
+def _map(fn, x):
+    x = _f32(x)
+    out = np.empty_like(x)
+    fn(_p(x), _p(out), x.size)
+    return out
+
+
+def silu(x):
+    return _map(lib.oracle_silu, x)
+
+
+def sigmoid(x):
+    return _map(lib.oracle_sigmoid, x)
+
+
+def softplus(x):
+    return _map(lib.oracle_softplus, x)
+
+
+def softmax(v):
+    v = _f32(v).copy()
+    lib.oracle_softmax(_p(v), v.size)
+    return v
+
+
+def conv_step(x, taps, history):
+    """one causal conv step; history [(W-1)][C] oldest first is updated in place"""
+    x = _f32(x)
+    taps = _f32(taps)
+    c, w = taps.shape
+    out = np.empty(c, np.float32)
+    lib.oracle_conv_step(_p(x), _p(taps), _p(history), _p(out), c, w)
+    return out
+
+
+def gated_delta_step(state, q, k, v, gate, beta, key_heads):
+    """all heads of one token; state [H][Dk][Dv] updated in place"""
+    h, dk, dv = state.shape
+    out = np.empty((h, dv), np.float32)
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    gate, beta = _f32(gate), _f32(beta)
+    lib.oracle_gated_delta_step(_p(state), _p(q), _p(k), _p(v), _p(gate), _p(beta), _p(out), h, key_heads, dk, dv)
+    return out
+
+
+def rope_inv_freq(head_dim, base, rotary_dims):
+    out = np.empty(head_dim // 2, np.float32)
+    lib.oracle_rope_inv_freq(head_dim, base, rotary_dims, _p(out))
+    return out
+
+
+def rope_apply(heads, inv_freq, position):
+    heads = _f32(heads).copy()
+    hd = inv_freq.size * 2
+    lib.oracle_rope_apply(_p(heads), heads.size // hd, _p(_f32(inv_freq)), hd, position)
+    return heads
+
+
+def attend_decode(q, keys, values, hq, hkv, head_dim, window, scale):
+    q, keys, values = _f32(q), _f32(keys), _f32(values)
+    ctx = keys.shape[0]
+    out = np.empty((hq, head_dim), np.float32)
+    if lib.oracle_attend_decode(_p(q), _p(keys), _p(values), ctx, hq, hkv, head_dim, window, scale, _p(out)) != 0:
+        raise RuntimeError(lib.oracle_last_error().decode())
+    return out
+
+
+class Model:
+    """The oracle's Qwen 3.5 model over a GGUF file or an in-memory image."""
+
+    def __init__(self, path: str | None = None, image: np.ndarray | None = None):
+        if path is not None:
+            self._h = lib.oracle_model_open(path.encode())
+        else:
+            self._image = image
+            self._h = lib.oracle_model_open_image(_p(image), image.nbytes)
+        if not self._h:
+            raise RuntimeError(lib.oracle_last_error().decode())
+        dims = np.zeros(15, np.uint64)
+        lib.oracle_model_dims(self._h, _p(dims))
+        (self.V, self.D, self.L, self.CTX, self.Hq, self.Hkv, self.head_dim, self.rotary_dims,
+         self.Dk, self.Dv, self.Hk, self.Hv, self.conv_width, self.FF, self.tied) = (int(v) for v in dims)
+
+    def close(self):
+        if self._h:
+            lib.oracle_model_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self):
+        lib.oracle_model_reset(self._h)
+
+    def tokens(self) -> int:
+        return int(lib.oracle_model_tokens(self._h))
+
+    def embed(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.empty((len(ids), self.D), np.float32)
+        if lib.oracle_model_embed(self._h, _p(ids), len(ids), _p(out)) != 0:
+            raise RuntimeError(lib.oracle_last_error().decode())
+        return out
+
+    def forward(self, rows):
+        rows = _f32(rows).reshape(-1, self.D)
+        logits = np.empty(self.V, np.float32)
+        if lib.oracle_model_forward(self._h, _p(rows), rows.shape[0], _p(logits)) != 0:
+            raise RuntimeError(lib.oracle_last_error().decode())
+        return logits
+
+    def forward_ids(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        logits = np.empty(self.V, np.float32)
+        if lib.oracle_model_forward_ids(self._h, _p(ids), len(ids), _p(logits)) != 0:
+            raise RuntimeError(lib.oracle_last_error().decode())
+        return logits
+
+    def greedy(self, prompt, steps):
+        """prefill + `steps` decode passes; returns (ids[steps+1], last logits, prefill s, decode s)"""
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        ids = np.empty(steps + 1, np.int32)
+        logits = np.empty(self.V, np.float32)
+        pf, dc = c_double(), c_double()
+        if lib.oracle_model_greedy(self._h, _p(prompt), len(prompt), steps, _p(ids), _p(logits), ctypes.byref(pf), ctypes.byref(dc)) != 0:
+            raise RuntimeError(lib.oracle_last_error().decode())
+        return ids, logits, pf.value, dc.value

@@ -1,0 +1,153 @@
+// oracle.hpp -- CPU restatement of the reference engine's Q8_0 Qwen 3.5 hybrid
+// forward pass (flywithfang/hero, engine `nm/`), with runtime dimensions.
+//
+// TEST INFRASTRUCTURE ONLY. This library is the parity checker and the timed
+// CPU baseline. It is never linked into, loaded by, or called from the product
+// path (hero_amd/): only tests/, __graft_entry__.smoke() and bench.py's
+// cpu_baseline leg may use it, and only as the checker.
+//
+// Every function restates one reference function with the SAME fp32 operation
+// order (no FMA contraction: build with -ffp-contract=off), so that a pinned
+// result from the reference compiled with the same flags matches bit for bit.
+// Citations are file:line into nm/src of the reference.
+//
+// Parity status per function (what pins it; see tests/test_oracle_*.py):
+//   fp16 codec            exhaustive 2^16 decode check + closed-form encode cases + golden vectors
+//   quantize_row_q8_0     golden vectors from the compiled reference + invariants
+//   quantize_q8_0         golden vectors + round-trip bound
+//   vec_dot_q8_0_q8_0     golden vectors; int32 block sums by brute force
+//   rmsnorm / l2 / silu   golden vectors + closed forms
+//   conv_step             closed form 100/210/321
+//   gated_delta_step      associative-memory identities + golden vectors + fp64 brute force
+//   rope                  golden vectors (tables) + offset identity
+//   attention             hand-worked causal/window cases + golden vectors
+//   Qwen35 forward        full-model golden logits and greedy ids of the tiny Q8_0 model
+#pragma once
+#include <cstddef>
+#include <cstdint>
+#include <vector>
+
+namespace oracle {
+
+// ---- fp16 codec (nm/src/core.hpp:34-79) ------------------------------------
+float fp16_to_fp32(uint16_t h);
+uint16_t fp32_to_fp16(float f);
+
+// ---- Q8_0 block (nm/src/quant.hpp:59-62): fp16 d + 32 int8, 34 bytes ------
+#pragma pack(push, 1)
+struct BlockQ8 {
+    uint16_t d;
+    int8_t qs[32];
+};
+#pragma pack(pop)
+static_assert(sizeof(BlockQ8) == 34, "Q8_0 block is 34 bytes");
+
+// activation quantizer, roundf (nm/src/quant_i8.hpp:70-80)
+void quantize_row_q8_0(const float* x, BlockQ8* y, size_t k);
+// weight quantizer, lround (nm/src/quant.hpp:404-413)
+void quantize_q8_0(const float* x, BlockQ8* y, size_t n);
+// integer dot, sequential fp32 block combination (nm/src/quant_i8.hpp:85-100)
+float vec_dot_q8_0_q8_0(size_t n, const BlockQ8* w, const BlockQ8* x);
+// d*q row dequant (nm/src/quant.hpp:306-313)
+void dequant_row_q8_0(const BlockQ8* row, float* out, size_t k);
+
+// ---- the row-parallel pool (nm/src/core.cpp:22-117) -----------------------
+// Persistent pool of N-1 workers plus the caller; chunk = n/(threads*16);
+// nested calls run serially. Threads default to hardware_concurrency and can
+// be set with set_threads() (the reference reads NM_THREADS).
+void par_for(size_t n, void (*fn)(size_t, void*), void* ctx);
+size_t num_threads();
+void set_threads(size_t n);
+
+// y[N] = W[N,K] x (nm/src/quant_i8.hpp:352-383): x quantized once, serially.
+void matvec_q8_0(const BlockQ8* W, size_t N, size_t K, const float* x, float* y);
+// Y[T,N] = X[T,K] W^T (nm/src/quant_i8.hpp:430-474)
+void matmul_q8_0(const BlockQ8* W, size_t N, size_t K, const float* X, size_t T, float* Y);
+
+// ---- elementwise / small reductions ----------------------------------------
+float dot(const float* a, const float* b, size_t n);          // core.hpp:496-500
+float sigmoid(float x);                                         // core.hpp:579
+float silu(float x);                                            // components.hpp:105
+float softplus(float x);                                        // recurrent.hpp:35
+void rmsnorm(float* x, const float* gamma, size_t n, float eps);  // components.hpp:176-181
+void l2_normalize(const float* x, float* out, size_t n, float eps);  // recurrent.hpp:40-48
+void softmax(float* v, size_t n);                               // components.hpp:132-141
+
+// depthwise causal conv step (recurrent.hpp:75-106). history holds the last
+// (width-1) inputs, oldest first, [width-1][channels]; taps are [channels][width].
+void conv_step(const float* input, const float* taps, float* history, float* out, size_t channels, size_t width);
+
+// one head, one token, in place (recurrent.hpp:146-177)
+void gated_delta_step(float* state, const float* q, const float* k, const float* v, float gate, float beta, float* out, size_t dk, size_t dv);
+
+// RoPE inv_freq table (attention.hpp:76-80) and one head rotation (:82-91)
+std::vector<float> rope_inv_freq(size_t head_dim, double base, size_t rotary_dims);
+void rope_apply(float* head, const float* inv_freq, size_t head_dim, size_t position);
+
+// GQA decode/prefill reduction for one (query row, head):
+// softmax(scale * q.k_j) over rows [first, end), then sum alpha_j v_j
+// (qwen35.hpp:366-380 with scale 1/sqrt(Dh); gemma4.hpp:597-610 with scale 1).
+// keys/values are [rows][kv_width] with the head at offset kv_head*head_dim.
+void attend_one(const float* q, const float* keys, const float* values, size_t kv_width, size_t kv_head, size_t head_dim, size_t first, size_t end, float scale, float* out);
+
+// ---- the Qwen 3.5 hybrid model (qwen35.hpp:26-463) --------------------------
+struct Config {
+    size_t V = 0, D = 0, L = 0, CTX = 0;
+    size_t Hq = 0, Hkv = 0, head_dim = 0, rotary_dims = 0;
+    double rope_base = 0;
+    size_t Dk = 0, Dv = 0, Hk = 0, Hv = 0, conv_width = 0;
+    size_t FF = 0;
+    float eps = 0;
+    size_t full_attention_interval = 4;
+    bool tied = true;
+    bool is_recurrent(size_t layer) const { return (layer + 1) % full_attention_interval != 0; }
+    size_t conv_channels() const { return 2 * Hk * Dk + Hv * Dv; }
+};
+
+// A linear weight: Q8_0 blocks, row-major by output (N rows of K/32 blocks).
+struct Linear {
+    const BlockQ8* w = nullptr;
+    size_t N = 0, K = 0;
+};
+
+struct Layer {
+    std::vector<float> mixer_norm, channel_norm;  // [D]
+    Linear gate, up, down;
+    // attention mixer
+    Linear wqg, wk, wv, wo;
+    std::vector<float> q_norm, k_norm;  // [head_dim]
+    // delta-net mixer
+    Linear wqkv, wz, wbeta, walpha, wout;
+    std::vector<float> conv;         // [conv_channels][conv_width]
+    std::vector<float> dt_bias;      // [Hv]
+    std::vector<float> decay_scale;  // [Hv], -exp(A_log)
+    std::vector<float> ssm_norm;     // [Dv]
+};
+
+struct Model {
+    Config c;
+    Linear embedding;  // [V rows of D]
+    Linear output;     // untied head, or embedding when tied
+    std::vector<Layer> layers;
+    std::vector<float> final_norm;
+    std::vector<float> inv_freq;
+};
+
+struct State {
+    size_t tokens = 0;
+    // attention layers: fp32 K/V rows [tokens][Hkv*head_dim]
+    std::vector<std::vector<float>> keys, values;
+    // recurrent layers: conv history [(W-1)][CC] oldest first, delta state [Hv][Dk][Dv]
+    std::vector<std::vector<float>> conv_hist, delta;
+    void reset(const Config& c);
+};
+
+// gather_rows / dequant_row (quant.hpp:464-480)
+void embed(const Model& m, const int32_t* ids, size_t n, float* out);
+// Qwen35Model::forward (qwen35.hpp:288-303): rows [T][D] at state.tokens(),
+// writes logits [V] of the last row. Throws on context exhaustion.
+void forward(const Model& m, State& s, const float* rows, size_t T, float* logits);
+// Logits::argmax: ties go to the lowest id (logits.hpp:61-66)
+int32_t argmax(const float* logits, size_t n);
+
+}  // namespace oracle

@@ -1,0 +1,268 @@
+// ref_harness.cpp -- drives the REFERENCE engine (flywithfang/hero, nm/src),
+// compiled from its own sources where they lie, to write golden vectors.
+// TEST INFRASTRUCTURE ONLY: built by oracle/Makefile into oracle/_ref/ (not
+// committed); it needs the reference tree at build time only.
+//
+//   ref_harness kernels DIR          read DIR/*.in.bin, write DIR/*.out.bin
+//   ref_harness model CFG GGUF PROMPT STEPS OUTDIR
+//        CFG = tiny | 8b. Prefill the int32 ids in PROMPT through
+//        PrefixCache::evaluate, then STEPS greedy decode passes, exactly as
+//        tools/qwen35_check.cpp:43-70 does (minus the tokenizer).
+//
+// Each kernel case instantiates the reference template at a fixed size and
+// applies it to the inputs the golden script wrote.
+#include "src/qwen35_loader.hpp"
+
+#include <chrono>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace {
+
+template <class T>
+std::vector<T> read_bin(const std::string& path) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) throw std::runtime_error("cannot read " + path);
+    f.seekg(0, std::ios::end);
+    const size_t bytes = size_t(f.tellg());
+    f.seekg(0);
+    std::vector<T> v(bytes / sizeof(T));
+    f.read(reinterpret_cast<char*>(v.data()), std::streamsize(bytes));
+    return v;
+}
+template <class T>
+void write_bin(const std::string& path, const T* data, size_t n) {
+    std::ofstream f(path, std::ios::binary);
+    if (!f) throw std::runtime_error("cannot write " + path);
+    f.write(reinterpret_cast<const char*>(data), std::streamsize(n * sizeof(T)));
+}
+template <size_t N>
+Vec<N> vec_from(const float* p) {
+    Vec<N> v;
+    for (size_t i = 0; i < N; ++i) v[i] = p[i];
+    return v;
+}
+
+// ---- model configurations (runtime GGUF dims must equal these) --------------
+struct TinyConfig {
+    static constexpr size_t V = 32000, D = 1024, L = 4, CTX = 4096;
+    static constexpr size_t Hq = 8, Hkv = 2, HEAD_DIM = 128;
+    static constexpr size_t ROPE_BASE = 1000000, ROTARY_NUM = 1, ROTARY_DEN = 4;
+    static constexpr size_t KEY_HEAD_DIM = 128, VALUE_HEAD_DIM = 128, KEY_HEADS = 8, VALUE_HEADS = 8, CONV_WIDTH = 4;
+    static constexpr size_t FF = 2816;
+    static constexpr Scalar RMS_EPS = 1e-6f;
+    static constexpr size_t FULL_ATTENTION_INTERVAL = 4;
+    using OutputWeight = std::monostate;
+    static constexpr bool is_recurrent(size_t layer) { return (layer + 1) % FULL_ATTENTION_INTERVAL != 0; }
+};
+struct Hybrid8BConfig {
+    static constexpr size_t V = 151936, D = 4096, L = 32, CTX = 65536;
+    static constexpr size_t Hq = 32, Hkv = 8, HEAD_DIM = 128;
+    static constexpr size_t ROPE_BASE = 1000000, ROTARY_NUM = 1, ROTARY_DEN = 4;
+    static constexpr size_t KEY_HEAD_DIM = 128, VALUE_HEAD_DIM = 128, KEY_HEADS = 32, VALUE_HEADS = 32, CONV_WIDTH = 4;
+    static constexpr size_t FF = 12288;
+    static constexpr Scalar RMS_EPS = 1e-6f;
+    static constexpr size_t FULL_ATTENTION_INTERVAL = 4;
+    using OutputWeight = std::monostate;
+    static constexpr bool is_recurrent(size_t layer) { return (layer + 1) % FULL_ATTENTION_INTERVAL != 0; }
+};
+
+template <class C>
+int run_model(const char* gguf_path, const char* prompt_path, size_t steps, const std::string& out) {
+    const GGUF gguf(gguf_path);
+    auto model = qwen35_loader::load<C>(gguf);
+    const std::vector<int32_t> prompt_ids = read_bin<int32_t>(prompt_path);
+    std::vector<TokenId> tokens;
+    for (int32_t id : prompt_ids) tokens.push_back(TokenId{id});
+
+    EmbeddedSequence<C::D> sequence;
+    sequence.append(model.embed(tokens), tokens);
+    PrefixCache<Qwen35Model<C>> memo(model);
+    const auto t0 = std::chrono::steady_clock::now();
+    Logits<C::V> logits = memo.evaluate(sequence);
+    const auto t1 = std::chrono::steady_clock::now();
+    write_bin(out + "/logits_prefill.f32", &logits[0], C::V);
+
+    // per step: the greedy id, and the top-5 (ids, logits)
+    std::vector<int32_t> ids, top_ids;
+    std::vector<float> top_logits;
+    for (size_t i = 0;; ++i) {
+        const TokenId token = logits.argmax();
+        ids.push_back(int32_t(token));
+        for (const ScoredToken& s : logits.top(5)) {
+            top_ids.push_back(int32_t(s.id));
+            top_logits.push_back(s.logit);
+        }
+        if (i == steps) break;
+        const std::span<const TokenId> next(&token, 1);
+        sequence.append(model.embed(next), next);
+        logits = memo.evaluate(sequence);
+        if (i + 1 == steps / 2) write_bin(out + "/logits_mid.f32", &logits[0], C::V);
+    }
+    const auto t2 = std::chrono::steady_clock::now();
+    write_bin(out + "/logits_last.f32", &logits[0], C::V);
+    write_bin(out + "/ids.i32", ids.data(), ids.size());
+    write_bin(out + "/top5_ids.i32", top_ids.data(), top_ids.size());
+    write_bin(out + "/top5_logits.f32", top_logits.data(), top_logits.size());
+    const double prefill = std::chrono::duration<double>(t1 - t0).count();
+    const double decode = std::chrono::duration<double>(t2 - t1).count();
+    std::FILE* f = std::fopen((out + "/times.txt").c_str(), "w");
+    std::fprintf(f, "threads %zu\nprefill_seconds %.6f\nprompt_tokens %zu\ndecode_seconds %.6f\ndecode_passes %zu\n", nm_num_threads(), prefill, prompt_ids.size(), decode, steps);
+    std::fclose(f);
+    std::printf("reference %s: prefill %zu tokens %.3fs, %zu decode passes %.3fs (%.3f passes/s, %zu threads)\n", out.c_str(), prompt_ids.size(), prefill, steps, decode, steps / decode, nm_num_threads());
+    return 0;
+}
+
+// ---- kernel-level golden vectors ------------------------------------------------
+int run_kernels(const std::string& dir) {
+    auto in = [&](const char* name) { return read_bin<float>(dir + "/" + name + ".in.bin"); };
+    auto out = [&](const char* name, const std::vector<float>& v) { write_bin(dir + "/" + name + ".out.bin", v.data(), v.size()); };
+
+    {  // fp16 encoder over arbitrary fp32 bit patterns
+        const std::vector<float> x = in("fp16_encode");
+        std::vector<uint16_t> h(x.size());
+        for (size_t i = 0; i < x.size(); ++i) h[i] = fp32_to_fp16(x[i]);
+        write_bin(dir + "/fp16_encode.out.bin", h.data(), h.size());
+    }
+    {  // activation quantizer (roundf) and weight quantizer (lround), K = 4096
+        const std::vector<float> x = in("quant");
+        std::vector<block_q8_0> a(x.size() / 32), w(x.size() / 32);
+        quantize_row_q8_0(x.data(), a.data(), x.size());
+        quantize_q8_0(x.data(), w.data(), x.size());
+        write_bin(dir + "/quant_act.out.bin", a.data(), a.size());
+        write_bin(dir + "/quant_weight.out.bin", w.data(), w.size());
+    }
+    {  // Weight<4096,64>::matvec and ::matmul over 8 rows (int8-activation path)
+        const std::vector<float> wf = in("gemv_w");  // [64][4096] fp32, quantized here
+        const std::vector<float> x = in("gemv_x");   // [8][4096]
+        constexpr size_t K = 4096, N = 64;
+        auto blocks = std::make_shared<std::vector<block_q8_0>>(N * K / 32);
+        quantize_q8_0(wf.data(), blocks->data(), N * K);
+        write_bin(dir + "/gemv_wq.out.bin", blocks->data(), blocks->size());
+        const Weight<K, N> weight(GT::Q8_0, blocks->data(), blocks);
+        const Vec<N> y = weight.matvec(vec_from<K>(x.data()));
+        out("gemv_y", std::vector<float>(y.p.get(), y.p.get() + N));
+        Matrix<K> X;
+        for (size_t r = 0; r < 8; ++r) X.append(vec_from<K>(x.data() + r * K));
+        const Matrix<N> Y = weight.matmul(X.view());
+        std::vector<float> yy;
+        for (size_t r = 0; r < 8; ++r)
+            for (size_t n = 0; n < N; ++n) yy.push_back(Y.row(r)[n]);
+        out("gemm_y", yy);
+    }
+    {  // RMSNorm at the three widths the path uses; gamma is [width] after x
+        auto norm = [&]<size_t N>(const char* name, std::integral_constant<size_t, N>) {
+            const std::vector<float> v = in(name);  // [x | gamma]
+            const RMSNorm<N> rn(vec_from<N>(v.data() + N), 1e-6f);
+            const Vec<N> y = rn(vec_from<N>(v.data()));
+            out(name, std::vector<float>(y.p.get(), y.p.get() + N));
+        };
+        norm("rms128", std::integral_constant<size_t, 128>{});
+        norm("rms1024", std::integral_constant<size_t, 1024>{});
+        norm("rms4096", std::integral_constant<size_t, 4096>{});
+    }
+    {  // l2 normalize over 16 heads of 128
+        const std::vector<float> x = in("l2");
+        std::vector<float> y;
+        for (size_t h = 0; h < x.size() / 128; ++h) {
+            const Vec<128> r = l2_normalize<128>(vec_from<128>(x.data() + h * 128));
+            y.insert(y.end(), r.p.get(), r.p.get() + 128);
+        }
+        out("l2", y);
+    }
+    {  // scalar activations
+        const std::vector<float> x = in("act");
+        std::vector<float> s(x.size()), g(x.size()), p(x.size());
+        for (size_t i = 0; i < x.size(); ++i) {
+            Vec<1> v;
+            v[0] = x[i];
+            v = Silu{}(std::move(v));
+            s[i] = v[0];
+            g[i] = sigmoid(x[i]);
+            p[i] = softplus(x[i]);
+        }
+        out("silu", s);
+        out("sigmoid", g);
+        out("softplus", p);
+    }
+    {  // causal conv, 256 channels, width 4, 6 steps
+        const std::vector<float> taps = in("conv_taps");  // [256][4]
+        const std::vector<float> xs = in("conv_x");       // [6][256]
+        Matrix<4> w;
+        for (size_t c = 0; c < 256; ++c) w.append(vec_from<4>(taps.data() + c * 4));
+        CausalConv1dState<256, 4> conv;
+        std::vector<float> y;
+        for (size_t t = 0; t < 6; ++t) {
+            const Vec<256> r = conv.step(vec_from<256>(xs.data() + t * 256), w);
+            y.insert(y.end(), r.p.get(), r.p.get() + 256);
+        }
+        out("conv", y);
+    }
+    {  // gated delta rule, one head 128x128, 4 consecutive tokens
+        std::vector<float> state = in("delta_state");  // [128*128]
+        const std::vector<float> tok = in("delta_tok");  // 4 x [q 128 | k 128 | v 128 | gate | beta]
+        std::vector<float> y;
+        const size_t stride = 3 * 128 + 2;
+        for (size_t t = 0; t < 4; ++t) {
+            const float* p = tok.data() + t * stride;
+            const Vec<128> o = gated_delta_step<128, 128>(state.data(), vec_from<128>(p), vec_from<128>(p + 128), vec_from<128>(p + 256), p[384], p[385]);
+            y.insert(y.end(), o.p.get(), o.p.get() + 128);
+        }
+        out("delta_out", y);
+        out("delta_state", state);
+    }
+    {  // RoPE, head 128, base 1e6, rotary 1/4, at several positions
+        const std::vector<float> x = in("rope");  // [P][128]
+        static const size_t positions[] = {0, 1, 2, 7, 100, 1023, 4095, 65535};
+        const RotaryEmbedding<128, 1000000, 1, 4> rope;
+        std::vector<float> y;
+        for (size_t i = 0; i < 8; ++i) {
+            Vec<128> v = vec_from<128>(x.data() + i * 128);
+            rope(slice_mut<128>(v, 0), Position{positions[i]});
+            y.insert(y.end(), v.p.get(), v.p.get() + 128);
+        }
+        out("rope", y);
+    }
+    {  // attention reduction: one query over ctx keys (the decode case), at
+       // scale 1/sqrt(128) and at scale 1; scaled_dot_product_attention is
+       // the same dot / Softmax / scaled_add reduction as qwen35.hpp:366-380
+        const std::vector<float> q = in("attn_q");  // [128]
+        const std::vector<float> k = in("attn_k");  // [ctx][128]
+        const std::vector<float> v = in("attn_v");  // [ctx][128]
+        const size_t ctx = k.size() / 128;
+        Matrix<128> Q, K, V;
+        Q.append(vec_from<128>(q.data()));
+        for (size_t j = 0; j < ctx; ++j) {
+            K.append(vec_from<128>(k.data() + j * 128));
+            V.append(vec_from<128>(v.data() + j * 128));
+        }
+        for (const float scale : {1.f / std::sqrt(128.f), 1.f}) {
+            const Matrix<128> A = scaled_dot_product_attention<1, 128, 128>(Q.view(), K.view(), V.view(), scale);
+            out(scale == 1.f ? "attn_unit" : "attn_scaled", std::vector<float>(A.row(0).begin(), A.row(0).end()));
+        }
+    }
+    std::printf("kernel golden vectors written to %s\n", dir.c_str());
+    return 0;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    try {
+        if (argc == 3 && std::strcmp(argv[1], "kernels") == 0) return run_kernels(argv[2]);
+        if (argc == 7 && std::strcmp(argv[1], "model") == 0) {
+            const size_t steps = std::strtoull(argv[5], nullptr, 10);
+            if (std::strcmp(argv[2], "tiny") == 0) return run_model<TinyConfig>(argv[3], argv[4], steps, argv[6]);
+            if (std::strcmp(argv[2], "8b") == 0) return run_model<Hybrid8BConfig>(argv[3], argv[4], steps, argv[6]);
+        }
+        std::fprintf(stderr, "usage: %s kernels DIR | model {tiny|8b} GGUF PROMPT STEPS OUTDIR\n", argv[0]);
+        return 2;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_harness: %s\n", e.what());
+        return 1;
+    }
+}

@@ -1,0 +1,59 @@
+"""Shared fixtures. Tests marked `gpu` need an MI355X; everything else runs on
+the CPU (oracle vs the reference's golden vectors, host logic, the C ABI)."""
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+
+
+@pytest.fixture(scope="session")
+def manifest():
+    with open(os.path.join(GOLDEN, "manifest.json")) as f:
+        return json.load(f)
+
+
+@pytest.fixture(scope="session")
+def kernels_golden():
+    return dict(np.load(os.path.join(GOLDEN, "kernels.npz")))
+
+
+@pytest.fixture(scope="session")
+def tiny_golden():
+    return dict(np.load(os.path.join(GOLDEN, "tiny_model.npz")))
+
+
+@pytest.fixture(scope="session")
+def tiny_gguf(tmp_path_factory, manifest):
+    """The tiny Q8_0 hybrid GGUF, regenerated from its seed; its bytes must be
+    the ones the reference produced the golden vectors from."""
+    import hero_amd
+
+    t = manifest["tiny_model"]
+    path = str(tmp_path_factory.mktemp("tiny") / "tiny.gguf")
+    hero_amd.write_synthetic_gguf(path, hero_amd.TINY_CONFIG, seed=t["seed"], ctx=t["ctx"])
+    with open(path, "rb") as f:
+        assert hashlib.sha256(f.read()).hexdigest() == t["gguf_sha256"], "synthetic tiny model bytes changed"
+    return path
+
+
+def gpu_available() -> bool:
+    try:
+        import torch
+
+        return torch.cuda.is_available()
+    except Exception:
+        return False

@@ -1,0 +1,161 @@
+"""Write the golden vectors of tests/golden/ by running the REFERENCE engine.
+
+The reference (flywithfang/hero, nm/src) is compiled from its own sources by
+oracle/Makefile into oracle/_ref/ref_harness (this needs the reference tree,
+so it runs in the build container only). This script:
+
+  1. writes seeded inputs for every kernel case, runs `ref_harness kernels`,
+     and stores inputs + outputs in kernels.npz;
+  2. writes the tiny Q8_0 hybrid model as GGUF with the package's seeded
+     synthetic writer, runs `ref_harness model tiny` (16-token random prompt,
+     128 greedy decode passes through PrefixCache::evaluate) and stores the
+     greedy ids, per-step top-5 and three full logit vectors in tiny_model.npz.
+
+manifest.json records seeds, shapes, the GGUF's sha256 and the compiler
+flags (-O3 -march=x86-64-v3 -ffp-contract=off: no FMA contraction).
+
+Run:  python tests/golden/make_golden.py
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import subprocess
+import sys
+import tempfile
+
+import numpy as np
+
+ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), "..", ".."))
+sys.path.insert(0, ROOT)
+HERE = os.path.dirname(os.path.abspath(__file__))
+HARNESS = os.path.join(ROOT, "oracle", "_ref", "ref_harness")
+
+TINY_SEED = 1234
+PROMPT_SEED = 7
+PROMPT_LEN = 16
+DECODE_STEPS = 128
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def kernel_inputs(rng: np.random.Generator) -> dict[str, np.ndarray]:
+    inp = {}
+    # fp16 encoder: special values, exact ties, subnormals, random bit patterns
+    special = np.array([0.0, -0.0, 1.0, -1.0, 65504.0, 65519.0, 65520.0, 1e9, -1e9, np.inf, -np.inf, np.nan,
+                        5.960464477539063e-08, 2.9802322387695312e-08, 2.98023224e-08 * 1.5, 6.103515625e-05,
+                        6.097555160522461e-05, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 1.0 + 2.0 ** -11 + 2.0 ** -20,
+                        2049.0, 2051.0, 1e-8, 1e-12, 3.14159265], dtype=np.float32)
+    bits = rng.integers(0, 2 ** 32, 50000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    mags = (rng.standard_normal(20000) * np.exp(rng.uniform(-20, 12, 20000))).astype(np.float32)
+    inp["fp16_encode"] = f32(np.concatenate([special, bits, mags]))
+    # quantizer input: 128 blocks of varied magnitude + crafted blocks
+    x = rng.standard_normal(4096).astype(np.float32) * np.repeat(np.exp(rng.uniform(-8, 4, 128)), 32).astype(np.float32)
+    x[0:32] = 0.0                                          # zero block: d = 0, q = 0
+    x[32:64] = np.arange(-15.5, 16.5, 1.0)                 # amax 16.5 -> exercise .5 ties
+    x[64:96] = np.float32(127.0) * rng.uniform(-1, 1, 32)  # d near 1
+    x[64] = 127.0
+    x[65:73] = [0.5, -0.5, 1.5, -1.5, 2.5, -2.5, 126.5, -126.5]  # exact ties at id = 1
+    x[96:128] = rng.standard_normal(32) * 1e-6            # tiny d (fp16 subnormal scale)
+    inp["quant"] = f32(x)
+    inp["gemv_w"] = f32(rng.standard_normal((64, 4096)) * 0.02)
+    inp["gemv_x"] = f32(rng.standard_normal((8, 4096)))
+    for n in (128, 1024, 4096):
+        inp[f"rms{n}"] = f32(np.concatenate([rng.standard_normal(n) * 3, 1 + 0.1 * rng.standard_normal(n)]))
+    inp["l2"] = f32(rng.standard_normal((16, 128)))
+    act = np.concatenate([np.linspace(-30, 30, 4001), [0.0, 20.0, -20.0, 20.000002, 19.999998, 88.0, -88.0, 1e-20]])
+    inp["act"] = f32(np.concatenate([act, rng.standard_normal(87) * 5]))
+    inp["conv_taps"] = f32(rng.standard_normal((256, 4)) * 0.5)
+    inp["conv_x"] = f32(rng.standard_normal((6, 256)))
+    inp["delta_state"] = f32(rng.standard_normal(128 * 128) * 0.1)
+    tok = []
+    for _ in range(4):
+        q = rng.standard_normal(128)
+        k = rng.standard_normal(128)
+        q = q / np.linalg.norm(q) / np.sqrt(128)
+        k = k / np.linalg.norm(k)
+        v = rng.standard_normal(128)
+        gate = -np.log1p(np.exp(rng.standard_normal()))
+        beta = 1 / (1 + np.exp(-rng.standard_normal()))
+        tok.append(np.concatenate([q, k, v, [gate, beta]]))
+    inp["delta_tok"] = f32(np.concatenate(tok))
+    inp["rope"] = f32(rng.standard_normal((8, 128)))
+    ctx = 300
+    inp["attn_q"] = f32(rng.standard_normal(128) / np.sqrt(128))
+    inp["attn_k"] = f32(rng.standard_normal((ctx, 128)) / np.sqrt(128))
+    inp["attn_v"] = f32(rng.standard_normal((ctx, 128)) / np.sqrt(128))
+    return inp
+
+
+OUTPUTS = {  # name -> dtype of the .out.bin
+    "fp16_encode": np.uint16, "quant_act": np.uint8, "quant_weight": np.uint8, "gemv_wq": np.uint8,
+    "gemv_y": np.float32, "gemm_y": np.float32, "rms128": np.float32, "rms1024": np.float32, "rms4096": np.float32,
+    "l2": np.float32, "silu": np.float32, "sigmoid": np.float32, "softplus": np.float32, "conv": np.float32,
+    "delta_out": np.float32, "delta_state": np.float32, "rope": np.float32, "attn_scaled": np.float32, "attn_unit": np.float32,
+}
+
+
+def make_kernels(tmp: str) -> dict:
+    rng = np.random.default_rng(20260101)
+    inp = kernel_inputs(rng)
+    for k, v in inp.items():
+        v.tofile(os.path.join(tmp, f"{k}.in.bin"))
+    subprocess.run([HARNESS, "kernels", tmp], check=True)
+    # the fp32 GEMV weights are only the quantizer's input; the reference's
+    # quantized blocks (out_gemv_wq) are what the GEMV cases consume
+    out = {f"in_{k}": v for k, v in inp.items() if k != "gemv_w"}
+    for k, dt in OUTPUTS.items():
+        out[f"out_{k}"] = np.fromfile(os.path.join(tmp, f"{k}.out.bin"), dtype=dt)
+    np.savez_compressed(os.path.join(HERE, "kernels.npz"), **out)
+    return {"seed": 20260101, "cases": sorted(OUTPUTS)}
+
+
+def make_tiny(tmp: str) -> dict:
+    import hero_amd
+
+    gguf = os.path.join(tmp, "tiny.gguf")
+    hero_amd.write_synthetic_gguf(gguf, hero_amd.TINY_CONFIG, seed=TINY_SEED, ctx=4096)
+    sha = hashlib.sha256(open(gguf, "rb").read()).hexdigest()
+    prompt = np.random.default_rng(PROMPT_SEED).integers(0, hero_amd.TINY_CONFIG.vocab, PROMPT_LEN).astype(np.int32)
+    prompt.tofile(os.path.join(tmp, "prompt.i32"))
+    outdir = os.path.join(tmp, "tiny_out")
+    os.makedirs(outdir, exist_ok=True)
+    subprocess.run([HARNESS, "model", "tiny", gguf, os.path.join(tmp, "prompt.i32"), str(DECODE_STEPS), outdir], check=True)
+    rd = lambda n, dt: np.fromfile(os.path.join(outdir, n), dtype=dt)  # noqa: E731
+    np.savez_compressed(
+        os.path.join(HERE, "tiny_model.npz"),
+        prompt=prompt,
+        ids=rd("ids.i32", np.int32),
+        top5_ids=rd("top5_ids.i32", np.int32).reshape(-1, 5),
+        top5_logits=rd("top5_logits.f32", np.float32).reshape(-1, 5),
+        logits_prefill=rd("logits_prefill.f32", np.float32),
+        logits_mid=rd("logits_mid.f32", np.float32),
+        logits_last=rd("logits_last.f32", np.float32),
+    )
+    times = open(os.path.join(outdir, "times.txt")).read()
+    return {"seed": TINY_SEED, "prompt_seed": PROMPT_SEED, "prompt_len": PROMPT_LEN, "decode_steps": DECODE_STEPS,
+            "ctx": 4096, "gguf_sha256": sha, "gguf_bytes": os.path.getsize(gguf), "reference_times": times,
+            "logits_mid_after_pass": DECODE_STEPS // 2}
+
+
+def main():
+    if not os.path.exists(HARNESS):
+        sys.exit(f"{HARNESS} missing: build it with `make -C oracle` (needs the reference tree)")
+    with tempfile.TemporaryDirectory() as tmp:
+        manifest = {
+            "generator": "tests/golden/make_golden.py",
+            "reference": "flywithfang/hero nm/src compiled by oracle/Makefile",
+            "flags": "g++ -std=c++20 -O3 -march=x86-64-v3 -ffp-contract=off",
+            "kernels": make_kernels(tmp),
+            "tiny_model": make_tiny(tmp),
+        }
+    with open(os.path.join(HERE, "manifest.json"), "w") as f:
+        json.dump(manifest, f, indent=1, sort_keys=True)
+    print(json.dumps(manifest, indent=1))
+
+
+if __name__ == "__main__":
+    main()

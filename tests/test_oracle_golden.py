@@ -1,0 +1,117 @@
+"""Pin the oracle to the REFERENCE: every kernel case and the whole tiny Q8_0
+model must match the golden vectors that the compiled reference engine wrote
+(tests/golden/make_golden.py), bit for bit."""
+import numpy as np
+import pytest
+
+import oracle
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def test_fp16_encoder_matches_reference(kernels_golden):
+    x = kernels_golden["in_fp16_encode"]
+    assert np.array_equal(oracle.fp32_to_fp16(x), kernels_golden["out_fp16_encode"])
+
+
+def test_activation_and_weight_quantizers_match_reference(kernels_golden):
+    x = kernels_golden["in_quant"]
+    assert oracle.quantize_row_q8_0(x).tobytes() == kernels_golden["out_quant_act"].tobytes()
+    assert oracle.quantize_q8_0(x).tobytes() == kernels_golden["out_quant_weight"].tobytes()
+
+
+def test_matvec_and_matmul_match_reference(kernels_golden):
+    wq = kernels_golden["out_gemv_wq"].view(oracle.BLOCK)
+    x = kernels_golden["in_gemv_x"].reshape(8, 4096)
+    y = oracle.matvec(wq, 64, 4096, x[0])
+    assert np.array_equal(bits(y), bits(kernels_golden["out_gemv_y"]))
+    Y = oracle.matmul(wq, 64, 4096, x)
+    assert np.array_equal(bits(Y).ravel(), bits(kernels_golden["out_gemm_y"]))
+
+
+@pytest.mark.parametrize("n", [128, 1024, 4096])
+def test_rmsnorm_matches_reference(kernels_golden, n):
+    v = kernels_golden[f"in_rms{n}"]
+    y = oracle.rmsnorm(v[:n], v[n:])
+    assert np.array_equal(bits(y), bits(kernels_golden[f"out_rms{n}"]))
+
+
+def test_l2_normalize_matches_reference(kernels_golden):
+    x = kernels_golden["in_l2"].reshape(16, 128)
+    y = np.concatenate([oracle.l2_normalize(r) for r in x])
+    assert np.array_equal(bits(y), bits(kernels_golden["out_l2"]))
+
+
+@pytest.mark.parametrize("name", ["silu", "sigmoid", "softplus"])
+def test_scalar_activations_match_reference(kernels_golden, name):
+    x = kernels_golden["in_act"]
+    y = getattr(oracle, name)(x)
+    assert np.array_equal(bits(y), bits(kernels_golden[f"out_{name}"]))
+
+
+def test_conv_steps_match_reference(kernels_golden):
+    taps = kernels_golden["in_conv_taps"].reshape(256, 4)
+    xs = kernels_golden["in_conv_x"].reshape(6, 256)
+    hist = np.zeros((3, 256), np.float32)
+    y = np.concatenate([oracle.conv_step(x, taps, hist) for x in xs])
+    assert np.array_equal(bits(y), bits(kernels_golden["out_conv"]))
+
+
+def test_gated_delta_steps_match_reference(kernels_golden):
+    state = kernels_golden["in_delta_state"].reshape(1, 128, 128).copy()
+    tok = kernels_golden["in_delta_tok"].reshape(4, 386)
+    outs = [oracle.gated_delta_step(state, t[:128], t[128:256], t[256:384], t[384:385], t[385:386], 1) for t in tok]
+    assert np.array_equal(bits(np.concatenate(outs).ravel()), bits(kernels_golden["out_delta_out"]))
+    assert np.array_equal(bits(state.ravel()), bits(kernels_golden["out_delta_state"]))
+
+
+def test_rope_matches_reference(kernels_golden):
+    x = kernels_golden["in_rope"].reshape(8, 128)
+    inv = oracle.rope_inv_freq(128, 1e6, 32)
+    positions = [0, 1, 2, 7, 100, 1023, 4095, 65535]
+    y = np.concatenate([oracle.rope_apply(r, inv, p) for r, p in zip(x, positions)])
+    assert np.array_equal(bits(y), bits(kernels_golden["out_rope"]))
+
+
+@pytest.mark.parametrize("name,scale", [("attn_scaled", np.float32(1.0) / np.sqrt(np.float32(128.0))), ("attn_unit", 1.0)])
+def test_attention_reduction_matches_reference(kernels_golden, name, scale):
+    q = kernels_golden["in_attn_q"]
+    k = kernels_golden["in_attn_k"].reshape(-1, 128)
+    v = kernels_golden["in_attn_v"].reshape(-1, 128)
+    out = oracle.attend_decode(q, k, v, 1, 1, 128, 0, np.float32(scale))
+    assert np.array_equal(bits(out.ravel()), bits(kernels_golden[f"out_{name}"]))
+
+
+@pytest.fixture(scope="module")
+def tiny_run(tiny_gguf, tiny_golden):
+    m = oracle.Model(path=tiny_gguf)
+    oracle.set_threads(4)
+    prompt = tiny_golden["prompt"]
+    steps = len(tiny_golden["ids"]) - 1
+    logits_prefill = m.forward_ids(prompt)
+    ids = [oracle.argmax(logits_prefill)]
+    mid = None
+    for i in range(steps):
+        logits = m.forward_ids([ids[-1]])
+        ids.append(oracle.argmax(logits))
+        if i + 1 == steps // 2:
+            mid = logits.copy()
+    return dict(ids=np.array(ids, np.int32), prefill=logits_prefill, mid=mid, last=logits)
+
+
+def oracle_argmax(logits):
+    return int(oracle.lib.oracle_argmax(logits.ctypes.data, logits.size))
+
+
+oracle.argmax = oracle_argmax
+
+
+def test_tiny_model_greedy_ids_match_reference(tiny_run, tiny_golden):
+    assert np.array_equal(tiny_run["ids"], tiny_golden["ids"])
+
+
+@pytest.mark.parametrize("which", ["prefill", "mid", "last"])
+def test_tiny_model_logits_match_reference_bitwise(tiny_run, tiny_golden, which):
+    assert np.array_equal(bits(tiny_run[which]), bits(tiny_golden[f"logits_{which}"]))

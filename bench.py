@@ -1,0 +1,163 @@
+#!/usr/bin/env python3
+"""bench.py -- greedy decode throughput at batch 1 of the ~8B Q8_0 hybrid
+(32 layers: 24 gated delta-net + 8 GQA; d_model 4096, 32 q / 8 kv heads of
+128, delta-net 32 heads of 128, SwiGLU 12288, vocab 151936) on one MI355X.
+
+One step = one forward pass of one token through the whole model, fed the
+previous greedy id (the decode loop of the reference's qwen35_check tool). The
+model is random-init from a seed (synthetic data), written as a Q8_0 GGUF
+image in host memory and loaded through the normal loader; a uniform-random
+prompt of --prompt tokens is prefilled first, then --warmup untimed steps, then
+exactly --steps timed steps (all on the device: each step is one hipGraph
+replay, no host input).
+
+The JSON line also carries
+  roofline      the Q8_0 GEMV (the dominant kernel): algorithmic bytes per
+                launch / average launch duration, from HIP events around every
+                matvec of a decode step replayed back to back on the model's
+                stream (weights rotate through all 32 layers and the LM head,
+                8.4 GB per step, far beyond the 256 MB last-level cache);
+  cpu_baseline  the oracle (this repo's restatement of the reference CPU path,
+                int8-activation Q8_0 dot products, row-parallel over threads)
+                on the same model bytes, on the host cores, over a bounded
+                sample of decode steps.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+SEED = 20260101
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(image, prompt, seconds: float) -> dict:
+    import oracle
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    oracle.set_threads(threads)
+    m = oracle.Model(image=image)
+    short = prompt[:4]
+    logits = m.forward_ids(short)
+    nxt = int(np.argmax(logits))
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        logits = m.forward_ids([nxt])
+        nxt = int(np.argmax(logits))
+        passes += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    m.close()
+    return {
+        "value": passes / elapsed,
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle on the same 8B model bytes: prefill 4 tokens, then {passes} greedy decode passes "
+                  f"(context 4..{4 + passes}) in {elapsed:.1f} s, {threads} threads, g++ -O3 -ffp-contract=off",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--prompt", type=int, default=2048)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--gemv-reps", type=int, default=5)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the decode path would shard by heads and rows across GPUs, which is not built)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import hero_amd
+
+    assert torch.cuda.is_available(), "bench.py needs the GPU"
+    shape = hero_amd.HYBRID_8B_CONFIG
+    ctx = ((args.prompt + args.warmup + args.steps + 64 + 255) // 256) * 256
+    t = time.perf_counter()
+    image = hero_amd.synthetic_gguf_image(shape, seed=SEED, ctx=ctx)
+    log(f"synthetic 8B hybrid GGUF image: {image.nbytes / 1e9:.2f} GB in {time.perf_counter() - t:.1f} s")
+    t = time.perf_counter()
+    model = hero_amd.Qwen35Model.open_image(image)
+    log(f"loaded and packed: {model.dims.device_bytes / 1e9:.2f} GB of weights on the device in {time.perf_counter() - t:.1f} s")
+    state = model.new_state(ctx)
+    rng = np.random.default_rng(SEED)
+    prompt = rng.integers(0, shape.vocab, args.prompt).astype(np.int32)
+
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    first = model.forward(state, ids=prompt, want_logits=False)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t
+    log(f"prefill {args.prompt} tokens: {prefill_s:.2f} s ({args.prompt / prefill_s:.1f} tok/s)")
+
+    warm_ids, _ = model.decode_greedy(state, first, args.warmup)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    ids, _ = model.decode_greedy(state, int(warm_ids[-1]), args.steps)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t
+    device_s = model.last_decode_seconds()
+    log(f"decode {args.steps} steps: {wall * 1e3:.1f} ms wall, {device_s * 1e3:.1f} ms device ({args.steps / wall:.1f} tok/s)")
+
+    sec, launches, nbytes = model.time_gemvs(state, args.gemv_reps)
+    avg_launch = sec / (args.gemv_reps * launches)
+    achieved = (nbytes / launches) / avg_launch / 1e9
+    log(f"GEMV: {launches} launches/step, {nbytes / 1e9:.3f} GB/step, avg {avg_launch * 1e6:.2f} us/launch, {achieved:.0f} GB/s")
+
+    out = {
+        "metric": "decode tok/s @bs1, Q8_0 ~8B hybrid",
+        "value": args.steps / wall,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall * 1e3 / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 x int8 -> int32, fp32 accumulate (Q8_0)",
+        "data": "synthetic: seeded random-init N(0,0.02) weights quantized to Q8_0, uniform-random prompt ids",
+        "config": {
+            "workload": f"Q8_0 ~8B hybrid (32 layers: 24 gated delta-net + 8 GQA, d_model 4096, FFN 12288, vocab 151936), "
+                        f"{args.prompt}-token prefill then greedy decode at batch 1",
+            "batch": 1, "prompt_tokens": args.prompt, "context_at_timed_start": args.prompt + args.warmup + 1,
+            "prefill_seconds": prefill_s, "device_decode_seconds": device_s,
+            "gemv_gbs_per_step": nbytes / (device_s / args.steps) / 1e9,
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None, "kernel": "gemv_q8_kernel (all Q8_0 matvecs of a decode step)",
+            "bytes_per_launch": nbytes / launches, "avg_launch_us": avg_launch * 1e6,
+        },
+    }
+    if not args.no_cpu:
+        log(f"CPU baseline: about {args.cpu_seconds:.0f} s of decode on the host")
+        out["cpu_baseline"] = cpu_baseline(image, prompt, args.cpu_seconds)
+        log(f"CPU baseline: {out['cpu_baseline']['value']:.3f} tok/s on {out['cpu_baseline']['cores']} threads")
+    print(json.dumps(out), flush=True)
+    model.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -148,6 +148,13 @@ class Qwen35Model:
     def last_decode_seconds(self) -> float:
         return float(lib.hero_model_last_decode_seconds(self._h))
 
+    def time_gemvs(self, state: PrefixState, reps: int = 5):
+        """(seconds, launches per step, algorithmic bytes per step) of the
+        step's Q8_0 matvecs launched reps times back to back"""
+        sec, n, b = ctypes.c_double(), ctypes.c_int64(), ctypes.c_int64()
+        check(lib.hero_model_time_gemvs(self._h, state._h, reps, byref(sec), byref(n), byref(b)))
+        return sec.value, n.value, b.value
+
 
 _sequence_ids = itertools.count(1)
 

@@ -94,6 +94,7 @@ SIGNATURES = {
     "hero_model_forward": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
     "hero_model_decode_greedy": (c_int, [c_void_p, c_void_p, c_int32, c_int64, c_void_p, c_void_p]),
     "hero_model_last_decode_seconds": (c_double, [c_void_p]),
+    "hero_model_time_gemvs": (c_int, [c_void_p, c_void_p, c_int32, POINTER(c_double), POINTER(c_int64), POINTER(c_int64)]),
     "hero_synth_qwen35_size": (c_int64, [POINTER(SynthConfig)]),
     "hero_synth_qwen35_image": (c_int, [POINTER(SynthConfig), c_void_p, c_size_t]),
     "hero_synth_qwen35_file": (c_int, [POINTER(SynthConfig), c_char_p]),

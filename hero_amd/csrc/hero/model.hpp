@@ -100,6 +100,11 @@ public:
     // greedy loop from `first_id`; out_ids[steps] on the host
     void decode_greedy(State& s, int32_t first_id, int64_t steps, int32_t* out_ids, float* logits) const;
     double last_decode_seconds() const { return last_decode_seconds_; }
+    // Every Q8_0 matvec of one decode step (all layers + LM head), `reps`
+    // times back to back, between two events on the model's stream.
+    // Returns seconds; *launches and *bytes are per repetition (algorithmic
+    // bytes: weights + scales, activation, outputs, residual reads).
+    double time_gemvs(State& s, int reps, int64_t* launches, int64_t* bytes) const;
 
 private:
     Qwen35Model() = default;

@@ -134,6 +134,13 @@ int hero_model_decode_greedy(const hero_model* model, hero_state* state, int32_t
 
 double hero_model_last_decode_seconds(const hero_model* model) { return model ? model->impl->last_decode_seconds() : 0.0; }
 
+int hero_model_time_gemvs(const hero_model* model, hero_state* state, int32_t reps, double* seconds, int64_t* launches, int64_t* bytes) {
+    return guard([&] {
+        need(model && state && seconds && launches && bytes && reps > 0, "bad argument");
+        *seconds = model->impl->time_gemvs(*state->impl, reps, launches, bytes);
+    });
+}
+
 int64_t hero_synth_qwen35_size(const hero_synth_config* config) {
     int64_t size = -1;
     const int rc = guard([&] { size = int64_t(synth_qwen35_size(to_synth(config))); });

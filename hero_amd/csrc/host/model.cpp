@@ -477,6 +477,40 @@ void Qwen35Model::decode_greedy(State& st, int32_t first_id, int64_t steps, int3
     }
 }
 
+double Qwen35Model::time_gemvs(State& st, int reps, int64_t* launches, int64_t* bytes) const {
+    const ModelConfig& c = c_;
+    hipStream_t s = stream_;
+    int64_t n_launch = 0, n_bytes = 0;
+    auto gemv = [&](const DeviceBuffer& w, const DeviceBuffer& act, float* y, const float* resid, int64_t N, int64_t K) {
+        launch_gemv_q8(w.get(), act.get(), y, resid, N, K, resid ? kEpiResidual : kEpiStore, s);
+        ++n_launch;
+        n_bytes += packed_q8_bytes(N, K) + act_q8_bytes(1, K) + N * 4 + (resid ? N * 4 : 0);
+    };
+    auto one_step = [&] {
+        for (const LayerWeights& L : layers_) {
+            const int64_t k_mix = L.recurrent ? c.v_width() : c.q_width();
+            gemv(L.w_in, st.act_d_, st.proj_.get<float>(), nullptr, L.n_in, c.D);
+            gemv(L.w_out, st.act_mix_, st.h_.get<float>(), st.x_.get<float>(), c.D, k_mix);
+            gemv(L.w_gate_up, st.act_d_, st.gate_up_.get<float>(), nullptr, 2 * c.FF, c.D);
+            gemv(L.w_down, st.act_ff_, st.x_.get<float>(), st.h_.get<float>(), c.D, c.FF);
+        }
+        gemv(c.tied ? embedding_ : output_, st.act_d_, st.logits_.get<float>(), nullptr, c.V, c.D);
+    };
+    one_step();  // warm the instruction cache and the launch path
+    hip_check(hipStreamSynchronize(s), "gemv warmup");
+    n_launch = n_bytes = 0;
+    hip_check(hipEventRecord(ev_start_, s), "event");
+    for (int r = 0; r < reps; ++r) one_step();
+    hip_check(hipEventRecord(ev_stop_, s), "event");
+    hip_check(hipStreamSynchronize(s), "gemv timing");
+    check_launch("gemv timing");
+    float ms = 0.f;
+    hip_check(hipEventElapsedTime(&ms, ev_start_, ev_stop_), "event time");
+    *launches = n_launch / std::max(reps, 1);
+    *bytes = n_bytes / std::max(reps, 1);
+    return double(ms) * 1e-3;
+}
+
 void Qwen35Model::embed(const int32_t* ids, int64_t n, float* out) const {
     if (n <= 0) throw Error(HERO_EINVAL, "embed: empty input");
     for (int64_t i = 0; i < n; ++i)

@@ -3,9 +3,9 @@
 // nm/src/qwen35_loader.hpp:30-155 reads.
 //
 // Every element is a pure function of (seed, tensor index, element index):
-// a splitmix64 counter hash gives two uniforms, Box-Muller (in double) gives
-// a standard normal, and the value is scale*normal rounded to fp32. 2-D
-// tensors are then quantized to Q8_0 with the reference weight quantizer
+// a splitmix64 counter hash of the element pair gives two 24-bit uniforms,
+// Box-Muller (in fp32) gives the pair of standard normals, and the value is
+// scale*normal in fp32. 2-D tensors are then quantized to Q8_0 with the reference weight quantizer
 // (nm/src/quant.hpp:404-413: d = amax/127, q = lround(x/d), d stored through
 // the reference fp16 encoder). Rows are generated in parallel; the bytes do
 // not depend on the thread count.
@@ -21,6 +21,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <stdexcept>
 #include <string>
@@ -38,13 +39,21 @@ inline uint64_t splitmix64(uint64_t x) {
     return x ^ (x >> 31);
 }
 
-// Standard normal for element i of a stream.
-inline double normal_at(uint64_t stream, uint64_t i) {
-    const uint64_t a = splitmix64(stream ^ splitmix64(2 * i));
-    const uint64_t b = splitmix64(stream ^ splitmix64(2 * i + 1));
-    const double u1 = (double(a >> 11) + 0.5) * (1.0 / 9007199254740992.0);  // (0,1)
-    const double u2 = double(b >> 11) * (1.0 / 9007199254740992.0);          // [0,1)
-    return std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
+// Standard normals for elements 2p and 2p+1 of a stream: one counter hash
+// gives two 24-bit uniforms, Box-Muller (in fp32) gives the pair.
+inline void normal_pair(uint64_t stream, uint64_t p, float* z0, float* z1) {
+    const uint64_t h = splitmix64(stream ^ splitmix64(p));
+    const float u1 = (float(uint32_t(h >> 40)) + 0.5f) * (1.f / 16777216.f);            // (0,1)
+    const float u2 = float(uint32_t(h >> 8) & 0xFFFFFFu) * (1.f / 16777216.f);          // [0,1)
+    const float r = std::sqrt(-2.f * std::log(u1));
+    const float a = 6.2831853f * u2;
+    *z0 = r * std::cos(a);
+    *z1 = r * std::sin(a);
+}
+inline float normal_at(uint64_t stream, uint64_t i) {
+    float z0, z1;
+    normal_pair(stream, i >> 1, &z0, &z1);
+    return (i & 1) ? z1 : z0;
 }
 
 inline uint64_t stream_of(uint64_t seed, uint64_t tensor_index) { return splitmix64(seed * 0x632BE59BD9B4E019ull + tensor_index + 1); }
@@ -62,7 +71,8 @@ void quantize_block_lround(const float* x, uint8_t* out34) {
 
 template <class F>
 void parallel_rows(size_t rows, F&& f) {
-    size_t threads = std::max<size_t>(1, std::min<size_t>(std::thread::hardware_concurrency(), 32));
+    size_t threads = std::max<size_t>(1, std::min<size_t>(std::thread::hardware_concurrency(), 16));
+    if (const char* env = std::getenv("HERO_SYNTH_THREADS")) threads = std::max<long>(1, std::atol(env));
     threads = std::min(threads, std::max<size_t>(1, rows / 64));
     if (threads <= 1) {
         for (size_t r = 0; r < rows; ++r) f(r);
@@ -245,7 +255,13 @@ void fill_tensor(const SynthConfig& c, const TensorSpec& s, uint64_t tensor_inde
         const uint64_t in = s.in, blocks = in / 32;
         parallel_rows(s.out, [&](size_t r) {
             std::vector<float> row(in);
-            for (uint64_t i = 0; i < in; ++i) row[i] = float(0.02 * normal_at(stream, uint64_t(r) * in + i));
+            const uint64_t base = uint64_t(r) * in;  // in is even: pairs never straddle rows
+            for (uint64_t i = 0; i < in; i += 2) {
+                float z0, z1;
+                normal_pair(stream, (base + i) >> 1, &z0, &z1);
+                row[i] = 0.02f * z0;
+                row[i + 1] = 0.02f * z1;
+            }
             for (uint64_t b = 0; b < blocks; ++b) quantize_block_lround(row.data() + b * 32, dst + (uint64_t(r) * blocks + b) * 34);
         });
         return;
@@ -256,8 +272,8 @@ void fill_tensor(const SynthConfig& c, const TensorSpec& s, uint64_t tensor_inde
         switch (s.kind) {
             case TensorSpec::Ones: f[i] = 1.f; break;
             case TensorSpec::Zeros: f[i] = 0.f; break;
-            case TensorSpec::Normal: f[i] = float(s.scale * normal_at(stream, i)); break;
-            case TensorSpec::NegExpNormal: f[i] = -float(std::exp(s.scale * normal_at(stream, i))); break;
+            case TensorSpec::Normal: f[i] = float(s.scale) * normal_at(stream, i); break;
+            case TensorSpec::NegExpNormal: f[i] = -std::exp(float(s.scale) * normal_at(stream, i)); break;
         }
     }
 }

@@ -76,6 +76,14 @@ int hero_model_decode_greedy(const hero_model* model, hero_state* state, int32_t
  * events around the decode passes on the model's stream). */
 double hero_model_last_decode_seconds(const hero_model* model);
 
+/* Measurement: every Q8_0 matvec of one decode step (all layers and the LM
+ * head, the real weights, in step order) launched `reps` times back to back
+ * between HIP events on the model's stream. Returns the elapsed seconds in
+ * *seconds; *launches and *bytes are per repetition, bytes being algorithmic
+ * (weights + fp16 scales, quantized activation, outputs, residual reads).
+ * Touches only the state's scratch buffers; the carried state is unchanged. */
+int hero_model_time_gemvs(const hero_model* model, hero_state* state, int32_t reps, double* seconds, int64_t* launches, int64_t* bytes);
+
 /* ---- synthetic models (host) -------------------------------------------- */
 typedef struct hero_synth_config {
     int64_t vocab, d_model, layers, ffn;

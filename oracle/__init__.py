@@ -38,6 +38,7 @@ _sigs = {
     "oracle_conv_step": (None, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_size_t]),
     "oracle_gated_delta_step": (None, [c_void_p] * 7 + [c_size_t] * 4),
     "oracle_rope_inv_freq": (None, [c_size_t, c_double, c_size_t, c_void_p]),
+    "oracle_rope_table": (None, [c_size_t, c_double, c_size_t, c_size_t, c_void_p]),
     "oracle_rope_apply": (None, [c_void_p, c_size_t, c_void_p, c_size_t, c_size_t]),
     "oracle_attend_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_size_t, c_size_t, c_float, c_void_p]),
     "oracle_model_open": (c_void_p, [c_char_p]),
@@ -203,6 +204,12 @@ def gated_delta_step(state, q, k, v, gate, beta, key_heads):
 def rope_inv_freq(head_dim, base, rotary_dims):
     out = np.empty(head_dim // 2, np.float32)
     lib.oracle_rope_inv_freq(head_dim, base, rotary_dims, _p(out))
+    return out
+
+
+def rope_table(head_dim, base, rotary_dims, positions):
+    out = np.empty((positions, head_dim // 2, 2), np.float32)
+    lib.oracle_rope_table(head_dim, base, rotary_dims, positions, _p(out))
     return out
 
 

@@ -5,6 +5,7 @@
 #include "oracle_gguf.hpp"
 
 #include <chrono>
+#include <cmath>
 #include <cstring>
 #include <memory>
 #include <stdexcept>
@@ -95,6 +96,19 @@ void oracle_rope_inv_freq(size_t head_dim, double base, size_t rotary_dims, floa
 }
 void oracle_rope_apply(float* heads, size_t n_heads, const float* inv_freq, size_t head_dim, size_t position) {
     for (size_t h = 0; h < n_heads; ++h) rope_apply(heads + h * head_dim, inv_freq, head_dim, position);
+}
+
+// cos/sin per (position, plane) with the reference's float expressions
+// (attention.hpp:84-85): angle = float(pos) * inv_freq[i]. out [positions][planes][2]
+void oracle_rope_table(size_t head_dim, double base, size_t rotary_dims, size_t positions, float* out) {
+    const std::vector<float> inv = rope_inv_freq(head_dim, base, rotary_dims);
+    const size_t planes = head_dim / 2;
+    for (size_t p = 0; p < positions; ++p)
+        for (size_t i = 0; i < planes; ++i) {
+            const float angle = float(p) * inv[i];
+            out[(p * planes + i) * 2] = std::cos(angle);
+            out[(p * planes + i) * 2 + 1] = std::sin(angle);
+        }
 }
 
 // GQA decode over a [ctx][Hkv*Dh] fp32 cache: q [Hq][Dh] -> out [Hq][Dh].

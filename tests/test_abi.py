@@ -1,0 +1,90 @@
+"""The C ABI on the CPU: the library loads, exports every entry point the
+headers declare, and reports argument and file errors without touching a GPU."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import hero_amd
+from hero_amd import _lib
+from conftest import ROOT
+
+
+def declared_symbols():
+    names = set()
+    for h in ("hero_kernels.h", "hero_model.h"):
+        text = open(os.path.join(ROOT, "include", h)).read()
+        names |= set(re.findall(r"\b(hero_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    declared = declared_symbols()
+    assert len(declared) >= 30
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+
+
+def test_size_helpers():
+    assert _lib.lib.hero_q8_0_packed_bytes(4096, 4096) == 4096 * 4096 * 34 // 32
+    assert _lib.lib.hero_q8_0_act_bytes(2, 1024) == 2 * 1024 + 2 * 32 * 4
+
+
+def test_argument_errors_are_reported_before_any_launch():
+    lib = _lib.lib
+    assert lib.hero_q8_0_gemv(None, None, None, None, 64, 4096, None) == _lib.HERO_EINVAL
+    assert b"null" in lib.hero_last_error()
+    assert lib.hero_q8_0_gemv(16, 16, 16, None, 64, 100, None) == _lib.HERO_EINVAL  # K % 32
+    assert b"multiple of 32" in lib.hero_last_error()
+    assert lib.hero_q8_0_quantize(16, 16, 0, 4096, None) == _lib.HERO_EINVAL
+    assert lib.hero_rmsnorm_quant(16, 16, 1e-6, None, None, 1, 32768, None) == _lib.HERO_EINVAL
+    assert lib.hero_gdn_decode(None, None) == _lib.HERO_EINVAL
+    args = _lib.GdnDecodeArgs()
+    args.dk = args.dv = 64
+    assert lib.hero_gdn_decode(ctypes.byref(args), None) == _lib.HERO_EINVAL
+    assert b"128" in lib.hero_last_error()
+
+
+def write(path, data: bytes):
+    with open(path, "wb") as f:
+        f.write(data)
+
+
+@pytest.mark.parametrize("mutate,needle", [
+    (lambda b: b"XXXX" + b[4:], b"bad magic"),
+    (lambda b: b[:4] + (2).to_bytes(4, "little") + b[8:], b"unsupported version"),
+    (lambda b: b[: len(b) // 3], b"out of range"),
+    (lambda b: b[:40], b"truncated"),
+])
+def test_malformed_gguf_is_rejected(tmp_path, tiny_gguf, mutate, needle):
+    data = open(tiny_gguf, "rb").read()
+    bad = str(tmp_path / "bad.gguf")
+    write(bad, mutate(data))
+    with pytest.raises(hero_amd.HeroError) as e:
+        hero_amd.Qwen35Model.open(bad)
+    assert e.value.code == _lib.HERO_EIO
+    assert needle.decode() in str(e.value)
+
+
+def test_missing_file_is_an_io_error(tmp_path):
+    with pytest.raises(hero_amd.HeroError) as e:
+        hero_amd.Qwen35Model.open(str(tmp_path / "none.gguf"))
+    assert e.value.code == _lib.HERO_EIO
+
+
+def test_synthetic_model_is_deterministic(tiny_gguf):
+    img = hero_amd.synthetic_gguf_image(hero_amd.TINY_CONFIG, seed=1234, ctx=4096)
+    assert img.tobytes() == open(tiny_gguf, "rb").read()
+    other = hero_amd.synthetic_gguf_image(hero_amd.TINY_CONFIG, seed=1235, ctx=4096)
+    assert other.tobytes() != img.tobytes() and other.nbytes == img.nbytes
+
+
+def test_synth_rejects_bad_shapes():
+    cfg = hero_amd.synth_config(hero_amd.TINY_CONFIG, 1)
+    cfg.layers = 3
+    assert _lib.lib.hero_synth_qwen35_size(ctypes.byref(cfg)) == -1
+    assert b"multiple of 4" in _lib.lib.hero_last_error()

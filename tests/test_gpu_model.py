@@ -1,0 +1,128 @@
+"""The whole tiny Q8_0 hybrid model on the GPU against the REFERENCE's own
+outputs (tests/golden/tiny_model.npz, written by the compiled reference
+engine): greedy ids over a 16-token prefill plus 128 decode passes must be
+identical, and logits must agree within 1e-2 abs / 1e-3 rel (fp32
+accumulation throughout). The kernels replay the reference's fp32 operation
+order, so in practice nearly every logit is bit-identical; the test reports
+the exact-match fraction."""
+import numpy as np
+import pytest
+
+import hero_amd
+from gpu_util import bits
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-2, 1e-3
+
+
+@pytest.fixture(scope="module")
+def model(tiny_gguf):
+    import torch
+
+    assert torch.cuda.is_available()
+    m = hero_amd.Qwen35Model.open(tiny_gguf)
+    yield m
+    m.close()
+
+
+def close(a, b):
+    return np.abs(a - b) <= ATOL + RTOL * np.abs(b)
+
+
+def report(name, got, ref):
+    exact = float(np.mean(bits(got) == bits(ref)))
+    print(f"{name}: max|d|={np.max(np.abs(got - ref)):.3g} exact={exact:.4f}")
+    return exact
+
+
+def test_tiny_prefill_and_greedy_decode_match_reference(model, tiny_golden):
+    prompt = tiny_golden["prompt"]
+    ids_ref = tiny_golden["ids"]
+    steps = len(ids_ref) - 1
+    state = model.new_state(1024)
+    logits = model.forward(state, ids=prompt)
+    report("prefill", logits.values, tiny_golden["logits_prefill"])
+    assert np.all(close(logits.values, tiny_golden["logits_prefill"]))
+    assert logits.argmax() == ids_ref[0]
+    assert state.tokens() == len(prompt)
+    # decode loop, one forward per token, each fed the previous greedy id
+    ids = [logits.argmax()]
+    for i in range(steps):
+        lg = model.forward(state, ids=[ids[-1]])
+        ids.append(lg.argmax())
+        if i + 1 == steps // 2:
+            report("mid", lg.values, tiny_golden["logits_mid"])
+            assert np.all(close(lg.values, tiny_golden["logits_mid"]))
+    report("last", lg.values, tiny_golden["logits_last"])
+    assert np.all(close(lg.values, tiny_golden["logits_last"]))
+    assert np.array_equal(np.array(ids, np.int32), ids_ref), f"first divergence at step {int(np.argmax(np.array(ids) != ids_ref))}"
+    assert state.tokens() == len(prompt) + steps
+
+
+def test_graph_decode_equals_stepwise_forward(model, tiny_golden):
+    """the hipGraph greedy loop gives the same ids and logits as forward()"""
+    prompt = tiny_golden["prompt"]
+    ids_ref = tiny_golden["ids"]
+    steps = len(ids_ref) - 1
+    state = model.new_state(1024)
+    first = model.forward(state, ids=prompt).argmax()
+    ids, logits = model.decode_greedy(state, first, steps, want_logits=True)
+    assert np.array_equal(ids, ids_ref[1:])
+    assert np.all(close(logits.values, tiny_golden["logits_last"]))
+    assert state.tokens() == len(prompt) + steps
+    # replay again from a reset state: identical (graph replays are deterministic)
+    state.reset()
+    first2 = model.forward(state, ids=prompt).argmax()
+    ids2, logits2 = model.decode_greedy(state, first2, steps, want_logits=True)
+    assert np.array_equal(ids2, ids)
+    assert np.array_equal(bits(logits2.values), bits(logits.values))
+
+
+def test_rows_input_equals_ids_input(model, tiny_golden):
+    prompt = tiny_golden["prompt"]
+    s1, s2 = model.new_state(64), model.new_state(64)
+    a = model.forward(s1, ids=prompt).values
+    b = model.forward(s2, rows=model.embed(prompt)).values
+    assert np.array_equal(bits(a), bits(b))
+
+
+def test_decode_equals_prefill_exactly(model, tiny_golden):
+    """token-by-token decode equals one-shot prefill (qwen35_tests.cpp:224-255);
+    on this path the two are the same arithmetic, so the logits are equal"""
+    prompt = tiny_golden["prompt"][:6]
+    s1, s2 = model.new_state(64), model.new_state(64)
+    whole = model.forward(s1, ids=prompt).values
+    for t in prompt:
+        step = model.forward(s2, ids=[t]).values
+    assert np.array_equal(bits(whole), bits(step))
+
+
+def test_prefix_cache_reuse_and_divergence(model, tiny_golden):
+    prompt = tiny_golden["prompt"][:5]
+    cache = hero_amd.PrefixCache(model, 64)
+    seq = hero_amd.EmbeddedSequence(model.D)
+    seq.append(model.embed(prompt[:3]), prompt[:3])
+    cache.evaluate(seq)
+    seq.append(model.embed(prompt[3:]), prompt[3:])
+    grown = cache.evaluate(seq)
+    assert cache.reused_tokens == 3 and cache.computed_tokens == 2
+    fresh = hero_amd.EmbeddedSequence(model.D)
+    fresh.append(model.embed(prompt), prompt)
+    again = cache.evaluate(fresh)  # a different sequence: the state is rebuilt
+    assert cache.reused_tokens == 0 and cache.computed_tokens == 5
+    assert np.array_equal(bits(grown.values), bits(again.values))
+    same = cache.evaluate(fresh)  # nothing new: the cached logits come back
+    assert cache.computed_tokens == 0 and np.array_equal(bits(same.values), bits(again.values))
+
+
+def test_context_exhaustion_is_reported_and_clears_state(model):
+    state = model.new_state(4)
+    model.forward(state, ids=[1, 2, 3])
+    with pytest.raises(hero_amd.ContextExhausted):
+        model.forward(state, ids=[4, 5])
+    assert state.tokens() == 3  # rejected before any work
+    with pytest.raises(hero_amd.HeroError):
+        model.forward(state, ids=[model.V])  # bad id
+    with pytest.raises(hero_amd.ContextExhausted):
+        model.decode_greedy(state, 1, 2)

@@ -104,6 +104,15 @@ SIGNATURES = {
 def _load():
     if not os.path.exists(LIB_PATH):
         raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() or make -C hero_amd")
+    # One HIP runtime per process. PyTorch-ROCm ships its own libamdhip64 and
+    # loads it by file name, so a runtime loaded earlier by this library would
+    # not be shared: two runtimes would each own the device, and pointers from
+    # one are invalid in the other. Loading torch first makes this library's
+    # libamdhip64.so.7 / libhsa-runtime64.so.1 resolve to torch's copies.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(LIB_PATH)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)

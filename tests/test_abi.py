@@ -88,3 +88,15 @@ def test_synth_rejects_bad_shapes():
     cfg.layers = 3
     assert _lib.lib.hero_synth_qwen35_size(ctypes.byref(cfg)) == -1
     assert b"multiple of 4" in _lib.lib.hero_last_error()
+
+
+def test_one_hip_runtime_per_process():
+    """torch-ROCm bundles its own libamdhip64; the package must bind to the
+    same copy rather than load a second runtime (pointers would not be shared)."""
+    import hero_amd  # noqa: F401
+
+    maps = open(f"/proc/{os.getpid()}/maps").read()
+    hip = {l.split()[-1] for l in maps.splitlines() if "libamdhip64" in l}
+    hsa = {l.split()[-1] for l in maps.splitlines() if "libhsa-runtime64" in l}
+    assert len(hip) == 1, hip
+    assert len(hsa) == 1, hsa

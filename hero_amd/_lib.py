@@ -80,6 +80,7 @@ SIGNATURES = {
     "hero_swiglu_quant": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "hero_q8_0_embed": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
     "hero_argmax": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
+    "hero_math_eval": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
     "hero_gdn_decode": (c_int, [POINTER(GdnDecodeArgs), c_void_p]),
     "hero_attn_decode": (c_int, [POINTER(AttnDecodeArgs), c_void_p]),
     "hero_model_open": (c_int, [c_char_p, POINTER(c_void_p)]),

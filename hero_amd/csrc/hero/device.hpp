@@ -4,23 +4,23 @@
 // default correctly rounded fp32 division and square root):
 //   * every fp32 expression below is evaluated in the same operation order as
 //     the reference CPU code it replaces, one rounding per operation;
-//   * exp / log1p are computed in fp64 and rounded once to fp32, i.e. they are
-//     correctly rounded. The reference calls glibc's expf / log1pf, which agree
-//     with the correctly rounded value on all but a few inputs in 10^4
-//     (expf) or 10^3 (log1pf), so those two can differ in the last bit.
+//   * exp and log1p return exactly what the reference's glibc expf / log1pf
+//     return (hero/libm.hpp), so results that depend on them are bit-identical
+//     too.
 #pragma once
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 
 #include "hero/fp16.hpp"
+#include "hero/libm.hpp"
 
 namespace hero {
 
 constexpr int kWave = 64;
 
-__device__ __forceinline__ float exp_f32(float x) { return float(::exp(double(x))); }
-__device__ __forceinline__ float log1p_f32(float x) { return float(::log1p(double(x))); }
+__device__ __forceinline__ float exp_f32(float x) { return expf_glibc(x); }
+__device__ __forceinline__ float log1p_f32(float x) { return log1pf_glibc(x); }
 
 // nm/src/core.hpp:579
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.f / (1.f + exp_f32(-x)); }

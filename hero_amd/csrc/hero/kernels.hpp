@@ -32,6 +32,9 @@ void launch_embed_q8(const void* packed_embedding, int64_t V, int64_t D, const i
 // argmax over n logits per row (ties -> lowest index); out_index[M]
 void launch_argmax(const float* logits, int64_t M, int64_t n, int32_t* out_index, uint64_t* scratch_keys, hipStream_t s);
 
+// exp, log1p, silu, sigmoid, softplus of x[n] -> out[5][n] (parity export)
+void launch_math_eval(const float* x, float* out, int64_t n, hipStream_t s);
+
 // gdn.hip: gated delta-net decode for B sequences x Hv heads (one token each)
 struct GdnDecodeArgs {
     const float* proj;      // [B][proj_stride]: qkv at 0, z at z_off, beta at beta_off, alpha at alpha_off

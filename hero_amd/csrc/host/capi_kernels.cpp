@@ -115,6 +115,14 @@ int hero_argmax(const float* logits, int64_t m, int64_t n, int32_t* out, uint64_
     });
 }
 
+int hero_math_eval(const float* x, float* out, int64_t n, void* stream) {
+    return guard([&] {
+        require(x && out && n > 0 && n < (int64_t(1) << 40), "bad arguments");
+        launch_math_eval(x, out, n, as_stream(stream));
+        check_launch("hero_math_eval");
+    });
+}
+
 int hero_gdn_decode(const hero_gdn_decode_args* p, void* stream) {
     return guard([&] {
         require(p != nullptr, "null args");

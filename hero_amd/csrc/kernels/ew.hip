@@ -97,4 +97,21 @@ void launch_argmax(const float* logits, int64_t M, int64_t n, int32_t* out_index
     hipLaunchKernelGGL(argmax_final_kernel, dim3(unsigned(M)), dim3(64), 0, s, scratch, kArgmaxGroups, out_index);
 }
 
+// Elementwise evaluation of the scalar functions the path uses, for parity
+// checks: out = [exp | log1p | silu | sigmoid | softplus], each [n].
+__global__ __launch_bounds__(256) void math_eval_kernel(const float* __restrict__ x, float* __restrict__ out, int64_t n) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i];
+    out[i] = exp_f32(v);
+    out[n + i] = log1p_f32(v);
+    out[2 * n + i] = silu_f32(v);
+    out[3 * n + i] = sigmoid_f32(v);
+    out[4 * n + i] = softplus_f32(v);
+}
+
+void launch_math_eval(const float* x, float* out, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(math_eval_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, s, x, out, n);
+}
+
 }  // namespace hero

@@ -77,6 +77,12 @@ int hero_q8_0_embed(const void* packed, int64_t v, int64_t d, const int32_t* ids
  * (Logits::argmax, nm/src/logits.hpp:61-66). scratch: M*128 uint64. */
 int hero_argmax(const float* logits, int64_t m, int64_t n, int32_t* out, uint64_t* scratch, void* stream);
 
+/* The scalar functions of the path evaluated on the device, for parity
+ * checks: out[0..n) = expf, [n..2n) = log1pf, then silu
+ * (nm/src/components.hpp:105), sigmoid (nm/src/core.hpp:579), softplus
+ * (nm/src/recurrent.hpp:35). expf and log1pf return exactly glibc's values. */
+int hero_math_eval(const float* x, float* out, int64_t n, void* stream);
+
 /* Gated delta-net decode, one token for each of B sequences, all Hv heads:
  * conv step + SiLU, q/k L2 norm, beta/decay gates, the gated delta rule,
  * per-head RMSNorm, SiLU(z) gate, Q8_0 quantization of the output

@@ -35,6 +35,8 @@ _sigs = {
     "oracle_sigmoid": (None, [c_void_p, c_void_p, c_size_t]),
     "oracle_softplus": (None, [c_void_p, c_void_p, c_size_t]),
     "oracle_softmax": (None, [c_void_p, c_size_t]),
+    "oracle_expf": (None, [c_void_p, c_void_p, c_size_t]),
+    "oracle_log1pf": (None, [c_void_p, c_void_p, c_size_t]),
     "oracle_conv_step": (None, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_size_t]),
     "oracle_gated_delta_step": (None, [c_void_p] * 7 + [c_size_t] * 4),
     "oracle_rope_inv_freq": (None, [c_size_t, c_double, c_size_t, c_void_p]),
@@ -173,6 +175,14 @@ def sigmoid(x):
 
 def softplus(x):
     return _map(lib.oracle_softplus, x)
+
+
+def expf(x):
+    return _map(lib.oracle_expf, x)
+
+
+def log1pf(x):
+    return _map(lib.oracle_log1pf, x)
 
 
 def softmax(v):

@@ -80,6 +80,13 @@ void oracle_softplus(const float* x, float* y, size_t n) {
     for (size_t i = 0; i < n; ++i) y[i] = softplus(x[i]);
 }
 void oracle_softmax(float* v, size_t n) { softmax(v, n); }
+// glibc's expf and log1pf as the reference calls them (std::exp / std::log1p on float)
+void oracle_expf(const float* x, float* y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = std::exp(x[i]);
+}
+void oracle_log1pf(const float* x, float* y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = std::log1p(x[i]);
+}
 void oracle_conv_step(const float* input, const float* taps, float* history, float* out, size_t channels, size_t width) { conv_step(input, taps, history, out, channels, width); }
 
 // H heads of one token; head h reads key head h % Hk (qwen35.hpp:172)

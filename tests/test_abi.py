@@ -100,3 +100,18 @@ def test_one_hip_runtime_per_process():
     hsa = {l.split()[-1] for l in maps.splitlines() if "libhsa-runtime64" in l}
     assert len(hip) == 1, hip
     assert len(hsa) == 1, hsa
+
+
+def test_libm_header_equals_glibc_on_the_host(tmp_path):
+    """hero/libm.hpp's expf / log1pf (the device's exp and log1p) against
+    glibc on a dense stride of all float bit patterns; pass 1 as the stride
+    to sweep all 2^32 (a minute)."""
+    import subprocess
+
+    exe = str(tmp_path / "libm_check")
+    subprocess.run(["/opt/rocm/bin/hipcc", "-x", "hip", "-std=c++20", "-O2", "-ffp-contract=off", "-fno-builtin",
+                    "--offload-arch=gfx950", "-I", os.path.join(ROOT, "hero_amd", "csrc"),
+                    os.path.join(ROOT, "tests", "libm_check.cpp"), "-o", exe], check=True, capture_output=True)
+    out = subprocess.run([exe, "257"], capture_output=True, text=True)
+    n, be, bl = (int(v) for v in out.stdout.split())
+    assert n > 16_000_000 and be == 0 and bl == 0, out.stdout

@@ -40,8 +40,9 @@ def quantize_dev(lib, x: np.ndarray):
 def math_inputs():
     rng = np.random.default_rng(42)
     stride = np.arange(0, 2 ** 32, 4099, dtype=np.uint64).astype(np.uint32).view(np.float32)
-    hard = np.array([0x1.04845ep+5, -0x1.f8cbb2p+5, 0x1.a827aep-2, 0x1.a827b4p-2, 0x1.6a09e6p+125, 88.0, 88.72283, 88.7229,
-                     -103.97, -103.98, -87.3, -1.0, -0.99999994, 20.0, 20.000002, 1e-30, -1e-30, np.inf, -np.inf], np.float32)
+    hexes = ["0x1.04845ep+5", "-0x1.f8cbb2p+5", "0x1.a827aep-2", "0x1.a827b4p-2", "0x1.6a09e6p+125"]  # glibc != correctly rounded
+    hard = np.array([float.fromhex(h) for h in hexes] + [88.0, 88.72283, 88.7229, -103.97, -103.98, -87.3, -1.0, -0.99999994,
+                                                        20.0, 20.000002, 1e-30, -1e-30, np.inf, -np.inf], np.float32)
     dense = np.concatenate([rng.uniform(-30, 30, 1 << 20), rng.standard_normal(1 << 18) * 3]).astype(np.float32)
     x = np.concatenate([stride, hard, dense])
     return x[~np.isnan(x)]

@@ -42,7 +42,7 @@ class AttnDecodeArgs(ctypes.Structure):
         ("proj", c_void_p), ("proj_stride", c_int64), ("k_off", c_int64), ("v_off", c_int64),
         ("q_gamma", c_void_p), ("k_gamma", c_void_p), ("eps", c_float), ("rope_cs", c_void_p),
         ("k_cache", c_void_p), ("v_cache", c_void_p), ("max_ctx", c_int64), ("positions", c_void_p),
-        ("scores", c_void_p), ("score_scale", c_float), ("window", c_int32), ("act_out", c_void_p), ("out_f32", c_void_p),
+        ("scores", c_void_p), ("q_rot", c_void_p), ("score_scale", c_float), ("window", c_int32), ("act_out", c_void_p), ("out_f32", c_void_p),
         ("b", c_int32), ("hq", c_int32), ("hkv", c_int32), ("dh", c_int32),
     ]
 

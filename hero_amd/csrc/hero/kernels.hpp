@@ -61,11 +61,12 @@ struct AttnDecodeArgs {
     const float* k_gamma;    // [Dh]
     float eps;
     const float* rope_cs;    // [max_pos][Dh/2][2] (cos, sin) per position and plane
-    float* k_cache;          // [B][max_ctx][Hkv*Dh]
-    float* v_cache;
+    float* k_cache;          // [B][Hkv][Dh][max_ctx] (channel-major)
+    float* v_cache;          // [B][max_ctx][Hkv*Dh]
     int64_t max_ctx;
     const int32_t* positions;// [B]
     float* scores;           // scratch [B][Hq][max_ctx]
+    float* q_rot;            // scratch [B][Hq][Dh]
     float score_scale;
     int window;              // 0 = full causal
     void* act_out;           // quantized WO input [B][Hq*Dh]

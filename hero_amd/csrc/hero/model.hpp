@@ -139,7 +139,7 @@ private:
     int64_t tokens_ = 0, max_tokens_ = 0;
     // per-step device scalars: [0] position, [1] token id, [2] step counter
     DeviceBuffer step_;
-    DeviceBuffer x_, h_, rows_, proj_, act_d_, act_mix_, act_ff_, gate_up_, logits_, argmax_scratch_, out_ids_;
+    DeviceBuffer x_, h_, rows_, proj_, act_d_, act_mix_, act_ff_, gate_up_, logits_, argmax_scratch_, out_ids_, q_rot_;
     int64_t rows_capacity_ = 0, out_ids_capacity_ = 0;
     std::vector<DeviceBuffer> k_cache_, v_cache_, scores_, conv_hist_, delta_;
     hipGraphExec_t graph_ = nullptr;  // one greedy decode step, replayed

@@ -147,11 +147,11 @@ int hero_attn_decode(const hero_attn_decode_args* p, void* stream) {
         require(a.dh == 128, "attention head dim must be 128");
         require(a.b > 0 && a.hkv > 0 && a.hq > 0 && a.hq % a.hkv == 0, "bad head counts");
         require(a.window >= 0 && a.max_ctx > 0, "bad window or cache size");
-        require(a.proj && a.q_gamma && a.k_gamma && a.rope_cs && a.k_cache && a.v_cache && a.positions && a.scores && a.act_out, "null pointer");
+        require(a.proj && a.q_gamma && a.k_gamma && a.rope_cs && a.k_cache && a.v_cache && a.positions && a.scores && a.q_rot && a.act_out, "null pointer");
         const int64_t kw = int64_t(a.hkv) * 128;
         require(a.proj_stride >= 2 * int64_t(a.hq) * 128 && a.k_off + kw <= a.proj_stride && a.v_off + kw <= a.proj_stride, "k/v slices outside the projection row");
-        require(aligned(a.k_cache, 16), "k_cache must be 16-byte aligned");
-        AttnDecodeArgs g{a.proj, a.proj_stride, a.k_off, a.v_off, a.q_gamma, a.k_gamma, a.eps, a.rope_cs, a.k_cache, a.v_cache, a.max_ctx, a.positions, a.scores, a.score_scale, a.window, a.act_out, a.out_f32, a.b, a.hq, a.hkv, a.dh};
+        require(a.max_ctx <= (int64_t(1) << 24), "max_ctx too large");
+        AttnDecodeArgs g{a.proj, a.proj_stride, a.k_off, a.v_off, a.q_gamma, a.k_gamma, a.eps, a.rope_cs, a.k_cache, a.v_cache, a.max_ctx, a.positions, a.scores, a.q_rot, a.score_scale, a.window, a.act_out, a.out_f32, a.b, a.hq, a.hkv, a.dh};
         launch_attn_decode(g, as_stream(stream));
         check_launch("hero_attn_decode");
     });

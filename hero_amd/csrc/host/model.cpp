@@ -285,6 +285,7 @@ Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens) : m_(m), max
     logits_ = DeviceBuffer(size_t(c.V) * 4);
     argmax_scratch_ = DeviceBuffer(128 * 8);
     out_ids_ = DeviceBuffer(size_t(max_tokens) * 4);
+    q_rot_ = DeviceBuffer(size_t(c.q_width()) * 4);
     out_ids_capacity_ = max_tokens;
     for (int64_t l = 0; l < c.L; ++l) {
         if (c.is_recurrent(l)) {
@@ -376,6 +377,7 @@ void Qwen35Model::enqueue_step(State& st, bool from_ids, bool with_head) const {
             a.max_ctx = st.max_tokens_;
             a.positions = step;
             a.scores = st.scores_[size_t(l)].get<float>();
+            a.q_rot = st.q_rot_.get<float>();
             a.score_scale = 1.f / std::sqrt(float(c.Dh));  // qwen35.hpp:359
             a.window = 0;
             a.act_out = st.act_mix_.get();

@@ -1,39 +1,55 @@
 // attn.hip -- gated GQA attention decode over an fp32 K/V cache, one token
-// per sequence (nm/src/qwen35.hpp:343-395; the sliding-window mask of
-// nm/src/attention.hpp:159-176 when window > 0).
+// per sequence (nm/src/qwen35.hpp:343-395; with window > 0 the sliding-window
+// visibility of nm/src/attention.hpp:159-176).
 //
-// One workgroup per (sequence, query head), one lane per head channel
-// (Dh = 128). The workgroup fuses: the split of the packed [q | gate] head
-// pair, q RMSNorm + RoPE, the K/V head's RMSNorm + RoPE and the cache append
-// (done by the first query head of each group; the others use their own,
-// identical copy of the new row), the softmax reduction over the visible rows,
-// the sigmoid(gate) product, and Q8_0 quantization of the head's output.
-//
-// The reduction keeps the reference's order: each score is a sequential
-// 128-term dot (core.hpp:496-500), the softmax total is a sequential sum over
-// rows (components.hpp:132-141), and each output channel accumulates
-// alpha_j * v_j in row order (core.hpp:206-208). RoPE uses a host-built
-// cos/sin table computed with the same float expressions as
-// attention.hpp:76-91, so it is bit-identical.
+// Three kernels, each keeping the reference's fp32 operation order:
+//  1. prep    one workgroup per (sequence, query head), a lane per channel:
+//             split of the packed [q | gate] pair, q RMSNorm + RoPE; the first
+//             query head of each K/V group also normalises and rotates k and
+//             appends k and v to the cache.
+//  2. scores  a lane per visible key: s_j = scale * dot(q, k_j), the dot a
+//             sequential 128-term sum (nm/src/core.hpp:496-500). K is cached
+//             channel-major per head, [Dh][max_ctx], so lanes reading
+//             consecutive keys read consecutive addresses.
+//  3. reduce  one workgroup per (sequence, query head): max, e_j = exp(s_j -
+//             max), the softmax total as the sequential sum over j
+//             (components.hpp:132-141) computed exactly in parallel
+//             (hero/seqsum.hpp), alpha_j = e_j / total, then a lane per
+//             channel accumulates alpha_j * v_j[c] in row order
+//             (core.hpp:206-208), multiplies by sigmoid(gate)
+//             (qwen35.hpp:390-393) and quantizes the head's output (Q8_0).
+// RoPE reads a host-built cos/sin table made with the reference's float
+// expressions (attention.hpp:76-91).
 #include "hero/device.hpp"
 #include "hero/kernels.hpp"
+#include "hero/seqsum.hpp"
 
 namespace hero {
 
 constexpr int kAttnDim = 128;
+constexpr int kScoreTiles = 8;
 
-// RMSNorm over one head held one value per lane, then RoPE (NEOX pairs).
+// ---- 1. prep ----------------------------------------------------------------------
+// RMSNorm over one head held one value per lane (sequential 128-term sum of
+// squares by lane 0), then RoPE on the NEOX planes (i, i + 64).
 __device__ __forceinline__ float norm_rope_head(float x, const float* gamma, float eps, const float* cs, float* buf, float* scal, int j) {
-    buf[j] = x;
+    buf[j] = x * x;
     __syncthreads();
     if (j == 0) {
         float ss = 0.f;
-        for (int i = 0; i < kAttnDim; ++i) ss += buf[i] * buf[i];
+        const float4* b4 = reinterpret_cast<const float4*>(buf);
+#pragma unroll
+        for (int i = 0; i < kAttnDim / 4; ++i) {
+            const float4 v = b4[i];
+            ss += v.x;
+            ss += v.y;
+            ss += v.z;
+            ss += v.w;
+        }
         scal[0] = 1.f / sqrtf(ss / float(kAttnDim) + eps);
     }
     __syncthreads();
     const float n = gamma[j] * x * scal[0];
-    __syncthreads();
     buf[j] = n;
     __syncthreads();
     const int half = kAttnDim / 2;
@@ -45,104 +61,127 @@ __device__ __forceinline__ float norm_rope_head(float x, const float* gamma, flo
     return r;
 }
 
-__global__ __launch_bounds__(kAttnDim) void attn_decode_kernel(AttnDecodeArgs a) {
-    const int j = threadIdx.x;
-    const int h = blockIdx.x, b = blockIdx.y;
+__global__ __launch_bounds__(kAttnDim) void attn_prep_kernel(AttnDecodeArgs a) {
+    const int j = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
     const int group = a.Hq / a.Hkv;
     const int g = h / group;  // grouped K/V heads (nm/src/qwen35.hpp:369)
     const int pos = a.positions[b];
-    if (pos < 0 || pos >= a.max_ctx) return;  // the host keeps positions in range; never index past the cache
+    if (pos < 0 || pos >= a.max_ctx) return;  // the host keeps positions in range
     const float* P = a.proj + int64_t(b) * a.proj_stride;
-    const int64_t KW = int64_t(a.Hkv) * kAttnDim;
     const float* cs = a.rope_cs + int64_t(pos) * kAttnDim;  // [Dh/2][2]
-
-    __shared__ float buf[kAttnDim], qs_[kAttnDim], ks_[kAttnDim], vs_[kAttnDim];
-    __shared__ float scal[4];
-
-    const float q_raw = P[int64_t(h) * 2 * kAttnDim + j];
-    const float gate = P[int64_t(h) * 2 * kAttnDim + kAttnDim + j];
-    const float q = norm_rope_head(q_raw, a.q_gamma, a.eps, cs, buf, scal, j);
-    const float k = norm_rope_head(P[a.k_off + int64_t(g) * kAttnDim + j], a.k_gamma, a.eps, cs, buf, scal, j);
-    const float v = P[a.v_off + int64_t(g) * kAttnDim + j];
-    qs_[j] = q;
-    ks_[j] = k;
-    vs_[j] = v;
-    float* kc = a.k_cache + int64_t(b) * a.max_ctx * KW;
-    float* vc = a.v_cache + int64_t(b) * a.max_ctx * KW;
+    __shared__ __align__(16) float buf[kAttnDim];
+    __shared__ float scal[2];
+    const float q = norm_rope_head(P[int64_t(h) * 2 * kAttnDim + j], a.q_gamma, a.eps, cs, buf, scal, j);
+    a.q_rot[(int64_t(b) * a.Hq + h) * kAttnDim + j] = q;
     if (h % group == 0) {
-        kc[int64_t(pos) * KW + int64_t(g) * kAttnDim + j] = k;
-        vc[int64_t(pos) * KW + int64_t(g) * kAttnDim + j] = v;
+        const float k = norm_rope_head(P[a.k_off + int64_t(g) * kAttnDim + j], a.k_gamma, a.eps, cs, buf, scal, j);
+        const float v = P[a.v_off + int64_t(g) * kAttnDim + j];
+        const int64_t kv = int64_t(b) * a.Hkv + g;
+        a.k_cache[(kv * kAttnDim + j) * a.max_ctx + pos] = k;  // [B][Hkv][Dh][max_ctx]
+        a.v_cache[(int64_t(b) * a.max_ctx + pos) * (int64_t(a.Hkv) * kAttnDim) + int64_t(g) * kAttnDim + j] = v;  // [B][max_ctx][Hkv*Dh]
     }
-    __syncthreads();
+}
 
-    // visible rows [first, pos]
-    const int first = (a.window > 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
+__device__ __forceinline__ int visible_first(int pos, int window) { return (window > 0 && pos + 1 > window) ? pos + 1 - window : 0; }
+
+// ---- 2. scores -------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void attn_scores_kernel(AttnDecodeArgs a) {
+    const int h = blockIdx.x, tile0 = blockIdx.y, b = blockIdx.z;
+    const int pos = a.positions[b];
+    if (pos < 0 || pos >= a.max_ctx) return;
+    const int g = h / (a.Hq / a.Hkv);
+    const int first = visible_first(pos, a.window);
+    const int n = pos + 1 - first;
+    __shared__ float q[kAttnDim];
+    if (threadIdx.x < kAttnDim) q[threadIdx.x] = a.q_rot[(int64_t(b) * a.Hq + h) * kAttnDim + threadIdx.x];
+    __syncthreads();
+    const float* kh = a.k_cache + (int64_t(b) * a.Hkv + g) * kAttnDim * a.max_ctx;
+    float* sc = a.scores + (int64_t(b) * a.Hq + h) * a.max_ctx;
+    for (int t = tile0 * 256 + int(threadIdx.x); t < n; t += kScoreTiles * 256) {
+        const float* kj = kh + first + t;
+        float dot = 0.f;
+#pragma unroll 16
+        for (int c = 0; c < kAttnDim; ++c) dot += q[c] * kj[int64_t(c) * a.max_ctx];
+        sc[t] = a.score_scale * dot;
+    }
+}
+
+// ---- 3. softmax, weighted sum of values, gate, quantize ------------------------------------
+__global__ __launch_bounds__(256) void attn_reduce_kernel(AttnDecodeArgs a) {
+    const int tid = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
+    const int pos = a.positions[b];
+    if (pos < 0 || pos >= a.max_ctx) return;
+    const int g = h / (a.Hq / a.Hkv);
+    const int first = visible_first(pos, a.window);
     const int n = pos + 1 - first;
     float* sc = a.scores + (int64_t(b) * a.Hq + h) * a.max_ctx;
+    __shared__ seqsum::Shared sm;
+    __shared__ __align__(16) float chunk[seqsum::kMaxN];
+    __shared__ float red[4];
 
-    // ---- scores: scale * dot(q, k_j), one key per lane, sequential over channels
-    for (int t = j; t < n; t += kAttnDim) {
-        const int row = first + t;
-        float dotv = 0.f;
-        if (row == pos) {
-            for (int c = 0; c < kAttnDim; ++c) dotv += qs_[c] * ks_[c];
-        } else {
-            const float4* kr = reinterpret_cast<const float4*>(kc + int64_t(row) * KW + int64_t(g) * kAttnDim);
-            for (int c4 = 0; c4 < kAttnDim / 4; ++c4) {
-                const float4 kk = kr[c4];
-                dotv += qs_[4 * c4] * kk.x;
-                dotv += qs_[4 * c4 + 1] * kk.y;
-                dotv += qs_[4 * c4 + 2] * kk.z;
-                dotv += qs_[4 * c4 + 3] * kk.w;
-            }
-        }
-        sc[t] = a.score_scale * dotv;
-    }
-    __syncthreads();
-
-    // ---- softmax: max (order free), exp, sequential total, divide ----
+    // max over the visible scores (order free)
     float mx = -INFINITY;
-    for (int t = j; t < n; t += kAttnDim) mx = fmaxf(mx, sc[t]);
+    for (int t = tid; t < n; t += 256) mx = fmaxf(mx, sc[t]);
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if ((j & 63) == 0) buf[j >> 6] = mx;
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
-    mx = fmaxf(buf[0], buf[1]);
-    for (int t = j; t < n; t += kAttnDim) sc[t] = exp_f32(sc[t] - mx);
-    __syncthreads();
-    if (j == 0) {
-        float total = 0.f;
-        for (int t = 0; t < n; ++t) total += sc[t];
-        scal[1] = total;
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+
+    // e_j = exp(s_j - max); total = sequential sum, chunk by chunk: each chunk
+    // starts with the running total as its first term (fl(0 + s) == s)
+    float total = 0.f;
+    for (int base = 0; base < n; base += seqsum::kMaxN - 1) {
+        const int len = min(n - base, seqsum::kMaxN - 1);
+        for (int t = tid; t < len; t += 256) {
+            const float e = exp_f32(sc[base + t] - mx);
+            sc[base + t] = e;
+            chunk[t + 1] = e;
+        }
+        if (tid == 0) chunk[0] = total;
+        __syncthreads();
+        total = seqsum::sum_nonneg(chunk, len + 1, sm);
     }
-    __syncthreads();
-    const float total = scal[1];
-    for (int t = j; t < n; t += kAttnDim) sc[t] = sc[t] / total;
+    for (int t = tid; t < n; t += 256) sc[t] = sc[t] / total;
     __syncthreads();
 
-    // ---- out[c] = sum_j alpha_j * v_j[c], rows in order ----
-    float acc = 0.f;
-    for (int t = 0; t < n; ++t) {
-        const int row = first + t;
-        const float vv = row == pos ? vs_[j] : vc[int64_t(row) * KW + int64_t(g) * kAttnDim + j];
-        acc += sc[t] * vv;
-    }
-    const float out = acc * sigmoid_f32(gate);  // nm/src/qwen35.hpp:390-393
+    // out[c] = sum_j alpha_j * v_j[c], rows in order, a lane per channel
+    if (tid < kAttnDim) {
+        const int64_t kw = int64_t(a.Hkv) * kAttnDim;
+        const float* v = a.v_cache + (int64_t(b) * a.max_ctx + first) * kw + int64_t(g) * kAttnDim + tid;
+        float acc = 0.f;
+        int t = 0;
+        for (; t + 8 <= n; t += 8) {
+            float vv[8], al[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                vv[u] = v[int64_t(t + u) * kw];
+                al[u] = sc[t + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += al[u] * vv[u];
+        }
+        for (; t < n; ++t) acc += sc[t] * v[int64_t(t) * kw];
+        const float gate = a.proj[int64_t(b) * a.proj_stride + int64_t(h) * 2 * kAttnDim + kAttnDim + tid];
+        const float out = acc * sigmoid_f32(gate);
 
-    const int64_t width = int64_t(a.Hq) * kAttnDim;
-    const int64_t idx = int64_t(h) * kAttnDim + j;
-    if (a.out_f32) a.out_f32[int64_t(b) * width + idx] = out;
-    float amax = fabsf(out);
-    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
-    const float d = amax / 127.f;
-    const float id = d != 0.f ? 1.f / d : 0.f;
-    int8_t* qs = static_cast<int8_t*>(a.act_out);
-    float* qd = reinterpret_cast<float*>(qs + int64_t(a.B) * width);
-    qs[int64_t(b) * width + idx] = int8_t(int(roundf(out * id)));
-    if ((j & 31) == 0) qd[(int64_t(b) * width + idx) >> 5] = half_bits_to_f32(fp32_to_fp16_ref(d));
+        const int64_t width = int64_t(a.Hq) * kAttnDim;
+        const int64_t idx = int64_t(h) * kAttnDim + tid;
+        if (a.out_f32) a.out_f32[int64_t(b) * width + idx] = out;
+        float amax = fabsf(out);
+        for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+        const float d = amax / 127.f;
+        const float id = d != 0.f ? 1.f / d : 0.f;
+        int8_t* qs = static_cast<int8_t*>(a.act_out);
+        float* qd = reinterpret_cast<float*>(qs + int64_t(a.B) * width);
+        qs[int64_t(b) * width + idx] = int8_t(int(roundf(out * id)));
+        if ((tid & 31) == 0) qd[(int64_t(b) * width + idx) >> 5] = half_bits_to_f32(fp32_to_fp16_ref(d));
+    }
 }
 
 void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(attn_decode_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, a);
+    hipLaunchKernelGGL(attn_prep_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, a);
+    hipLaunchKernelGGL(attn_scores_kernel, dim3(unsigned(a.Hq), kScoreTiles, unsigned(a.B)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(attn_reduce_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(256), 0, s, a);
 }
 
 }  // namespace hero

@@ -23,6 +23,22 @@ namespace hero {
 
 constexpr int kGdnDim = 128;
 
+// sequential sum of squares of v[0..128) (nm/src/core.hpp:496-500 order),
+// reading shared memory four values at a time
+__device__ __forceinline__ float sum_squares_128(const float* v) {
+    const float4* v4 = reinterpret_cast<const float4*>(v);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kGdnDim / 4; ++i) {
+        const float4 x = v4[i];
+        ss += x.x * x.x;
+        ss += x.y * x.y;
+        ss += x.z * x.z;
+        ss += x.w * x.w;
+    }
+    return ss;
+}
+
 __device__ __forceinline__ float conv_channel(const GdnDecodeArgs& a, const float* hist, int64_t CC, int64_t c, int pos, float x) {
     const float* taps = a.conv_taps + c * a.W;
     float sum = taps[a.W - 1] * x;
@@ -45,7 +61,7 @@ __global__ __launch_bounds__(kGdnDim) void gdn_decode_kernel(GdnDecodeArgs a) {
     const float* P = a.proj + int64_t(b) * a.proj_stride;
     float* hist = a.conv_hist + int64_t(b) * a.W * CC;
 
-    __shared__ float qv[kGdnDim], kv[kGdnDim], ov[kGdnDim];
+    __shared__ __align__(16) float qv[kGdnDim], kv[kGdnDim], ov[kGdnDim];
     __shared__ float scal[4];
 
     // ---- conv + SiLU on this head's channels ----
@@ -66,9 +82,7 @@ __global__ __launch_bounds__(kGdnDim) void gdn_decode_kernel(GdnDecodeArgs a) {
 
     // ---- L2 norms (nm/src/recurrent.hpp:40-48), sequential sums ----
     if (j == 0 || j == 64) {
-        const float* src = j == 0 ? qv : kv;
-        float ss = 0.f;
-        for (int i = 0; i < kGdnDim; ++i) ss += src[i] * src[i];
+        const float ss = sum_squares_128(j == 0 ? qv : kv);
         scal[j == 0 ? 0 : 1] = 1.f / fmaxf(sqrtf(ss), 1e-6f);
     }
     __syncthreads();
@@ -109,11 +123,7 @@ __global__ __launch_bounds__(kGdnDim) void gdn_decode_kernel(GdnDecodeArgs a) {
     // ---- per-head RMSNorm (components.hpp:176-181) and the SiLU(z) gate ----
     ov[j] = o;
     __syncthreads();
-    if (j == 0) {
-        float ss = 0.f;
-        for (int i = 0; i < kGdnDim; ++i) ss += ov[i] * ov[i];
-        scal[2] = 1.f / sqrtf(ss / float(kGdnDim) + a.eps);
-    }
+    if (j == 0) scal[2] = 1.f / sqrtf(sum_squares_128(ov) / float(kGdnDim) + a.eps);
     __syncthreads();
     const float normed = a.norm_gamma[j] * o * scal[2];
     const float z = P[a.z_off + int64_t(h) * kGdnDim + j];

@@ -2,16 +2,18 @@
 //
 // nm/src/components.hpp:176-181: inv = 1/sqrt(dot(x,x)/N + eps), then
 // x[c] = (gamma[c]*x[c])*inv. dot() is a sequential fp32 sum
-// (nm/src/core.hpp:496-500), so the sum of squares here is the same
-// sequential chain: squares are formed in parallel (one rounding each, like
-// the reference's a[i]*b[i]) and added in index order by one lane.
+// (nm/src/core.hpp:496-500): the squares are formed in parallel (one rounding
+// each, like the reference's a[i]*b[i]) and summed in index order, bit for
+// bit, by the workgroup's exact parallel form of that loop (hero/seqsum.hpp).
 #include "hero/device.hpp"
 #include "hero/kernels.hpp"
+#include "hero/seqsum.hpp"
 
 namespace hero {
 
 __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restrict__ x, const float* __restrict__ gamma, float eps, float* __restrict__ y, int8_t* __restrict__ qs, float* __restrict__ qd, int D) {
-    extern __shared__ __align__(16) float sq[];  // [D] squares, then [1] inv
+    extern __shared__ __align__(16) float sq[];  // [D] squares
+    __shared__ seqsum::Shared sm;
     const int64_t row = blockIdx.x;
     const float* xr = x + row * D;
     const int tid = threadIdx.x;
@@ -20,13 +22,15 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restr
         sq[i] = v * v;
     }
     __syncthreads();
-    if (tid == 0) {
-        float s = 0.f;
-        for (int i = 0; i < D; ++i) s += sq[i];
-        sq[D] = 1.f / sqrtf(s / float(D) + eps);
+    float s;
+    if (D <= seqsum::kMaxN) {
+        s = seqsum::sum_nonneg(sq, D, sm);
+    } else {
+        if (tid == 0) sm.result = seqsum::serial_loop(sq, D);
+        __syncthreads();
+        s = sm.result;
     }
-    __syncthreads();
-    const float inv = sq[D];
+    const float inv = 1.f / sqrtf(s / float(D) + eps);
     const int groups = D >> 3;
     for (int g = tid; g < groups; g += 256) {
         const float4 a = reinterpret_cast<const float4*>(xr)[2 * g];
@@ -50,7 +54,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restr
 void launch_rmsnorm_quant(const float* x, const float* gamma, float eps, float* y, void* act, int64_t M, int64_t D, hipStream_t s) {
     int8_t* qs = static_cast<int8_t*>(act);
     float* qd = act ? reinterpret_cast<float*>(qs + M * D) : nullptr;
-    hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(unsigned(M)), dim3(256), size_t(D + 4) * 4, s, x, gamma, eps, y, qs, qd, int(D));
+    hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(unsigned(M)), dim3(256), size_t(D) * 4, s, x, gamma, eps, y, qs, qd, int(D));
 }
 
 }  // namespace hero

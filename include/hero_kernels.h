@@ -120,11 +120,12 @@ typedef struct hero_attn_decode_args {
     const float* k_gamma;    /* [Dh] */
     float eps;
     const float* rope_cs;    /* [max_pos][Dh/2][2] cos, sin */
-    float* k_cache;          /* [B][max_ctx][Hkv*Dh] */
-    float* v_cache;
+    float* k_cache;          /* [B][Hkv][Dh][max_ctx], channel-major per K/V head */
+    float* v_cache;          /* [B][max_ctx][Hkv*Dh] */
     int64_t max_ctx;
     const int32_t* positions;/* [B] */
     float* scores;           /* scratch [B][Hq][max_ctx] */
+    float* q_rot;            /* scratch [B][Hq][Dh] */
     float score_scale;       /* 1/sqrt(Dh) for Qwen, 1 for Gemma-style */
     int32_t window;          /* 0 = full causal */
     void* act_out;           /* quantized act [B][Hq*Dh] */

@@ -115,3 +115,18 @@ def test_libm_header_equals_glibc_on_the_host(tmp_path):
     out = subprocess.run([exe, "257"], capture_output=True, text=True)
     n, be, bl = (int(v) for v in out.stdout.split())
     assert n > 16_000_000 and be == 0 and bl == 0, out.stdout
+
+
+def test_seqsum_equals_the_sequential_loop_on_the_host(tmp_path):
+    """hero/seqsum.hpp's parallel sum of non-negative floats, run phase by
+    phase on the host, equals the left-to-right fp32 loop bit for bit on random
+    sums of squares, exponentials, mixed magnitudes, zeros and overflow."""
+    import subprocess
+
+    exe = str(tmp_path / "seqsum_check")
+    subprocess.run(["/opt/rocm/bin/hipcc", "-x", "hip", "-std=c++20", "-O2", "-ffp-contract=off",
+                    "--offload-arch=gfx950", "-I", os.path.join(ROOT, "hero_amd", "csrc"),
+                    os.path.join(ROOT, "tests", "seqsum_check.cpp"), "-o", exe], check=True, capture_output=True)
+    out = subprocess.run([exe, "3000"], capture_output=True, text=True, timeout=300)
+    trials, bad, _fallbacks = (int(v) for v in out.stdout.split()[-3:])
+    assert trials == 3000 and bad == 0, out.stdout

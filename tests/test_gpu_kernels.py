@@ -281,6 +281,7 @@ def test_attn_decode_matches_oracle(lib, window):
     d_cs = dev(oracle.rope_table(dh, 1e6, 32, max_ctx))  # the reference's own cos/sin values
     d_kc, d_vc = empty(B * max_ctx * kw * 4), empty(B * max_ctx * kw * 4)
     d_sc = empty(B * hq * max_ctx * 4)
+    d_qr = empty(B * hq * dh * 4)
     act = empty(lib.hero_q8_0_act_bytes(B, qw))
     out = empty(B * qw * 4)
     keys = [np.zeros((0, kw), np.float32) for _ in range(B)]
@@ -290,7 +291,7 @@ def test_attn_decode_matches_oracle(lib, window):
         proj = (rng.standard_normal((B, stride))).astype(np.float32)
         d_proj, d_pos = dev(proj), dev(np.array([step, step], np.int32))
         a = AttnDecodeArgs(ptr(d_proj), stride, 2 * qw, 2 * qw + kw, ptr(d_qg), ptr(d_kg), eps, ptr(d_cs), ptr(d_kc), ptr(d_vc),
-                           max_ctx, ptr(d_pos), ptr(d_sc), scale, window, ptr(act), ptr(out), B, hq, hkv, dh)
+                           max_ctx, ptr(d_pos), ptr(d_sc), ptr(d_qr), scale, window, ptr(act), ptr(out), B, hq, hkv, dh)
         check(lib.hero_attn_decode(a, stream()))
         got = host(out, np.float32, (B, qw))
         for b in range(B):

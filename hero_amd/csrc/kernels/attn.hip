@@ -2,7 +2,7 @@
 // per sequence (nm/src/qwen35.hpp:343-395; with window > 0 the sliding-window
 // visibility of nm/src/attention.hpp:159-176).
 //
-// Three kernels, each keeping the reference's fp32 operation order:
+// Four kernels, each keeping the reference's fp32 operation order:
 //  1. prep    one workgroup per (sequence, query head), a lane per channel:
 //             split of the packed [q | gate] pair, q RMSNorm + RoPE; the first
 //             query head of each K/V group also normalises and rotates k and
@@ -11,13 +11,14 @@
 //             sequential 128-term sum (nm/src/core.hpp:496-500). K is cached
 //             channel-major per head, [Dh][max_ctx], so lanes reading
 //             consecutive keys read consecutive addresses.
-//  3. reduce  one workgroup per (sequence, query head): max, e_j = exp(s_j -
+//  3. softmax one workgroup per (sequence, query head): max, e_j = exp(s_j -
 //             max), the softmax total as the sequential sum over j
 //             (components.hpp:132-141) computed exactly in parallel
-//             (hero/seqsum.hpp), alpha_j = e_j / total, then a lane per
-//             channel accumulates alpha_j * v_j[c] in row order
+//             (hero/seqsum.hpp), alpha_j = e_j / total.
+//  4. pv      four workgroups per (sequence, query head), 32 channels each:
+//             a lane per channel accumulates alpha_j * v_j[c] in row order
 //             (core.hpp:206-208), multiplies by sigmoid(gate)
-//             (qwen35.hpp:390-393) and quantizes the head's output (Q8_0).
+//             (qwen35.hpp:390-393) and quantizes the output (one Q8_0 block).
 // RoPE reads a host-built cos/sin table made with the reference's float
 // expressions (attention.hpp:76-91).
 #include "hero/device.hpp"
@@ -106,66 +107,117 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnDecodeArgs a) {
     }
 }
 
-// ---- 3. softmax, weighted sum of values, gate, quantize ------------------------------------
-__global__ __launch_bounds__(256) void attn_reduce_kernel(AttnDecodeArgs a) {
+// ---- 3. softmax ------------------------------------------------------------------------------
+// max over the visible scores (order free), e_j = exp(s_j - max), the total as
+// the sequential sum over j computed exactly in parallel, alpha_j = e_j / total
+// written back over the scores.
+__global__ __launch_bounds__(seqsum::kThreads) void attn_softmax_kernel(AttnDecodeArgs a) {
     const int tid = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
     const int pos = a.positions[b];
     if (pos < 0 || pos >= a.max_ctx) return;
-    const int g = h / (a.Hq / a.Hkv);
     const int first = visible_first(pos, a.window);
     const int n = pos + 1 - first;
     float* sc = a.scores + (int64_t(b) * a.Hq + h) * a.max_ctx;
     __shared__ seqsum::Shared sm;
     __shared__ __align__(16) float chunk[seqsum::kMaxN];
-    __shared__ float red[4];
+    __shared__ float red[seqsum::kWaves];
 
-    // max over the visible scores (order free)
     float mx = -INFINITY;
-    for (int t = tid; t < n; t += 256) mx = fmaxf(mx, sc[t]);
+    for (int t = tid; t < n; t += seqsum::kThreads) mx = fmaxf(mx, sc[t]);
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    mx = red[0];
+    for (int w = 1; w < seqsum::kWaves; ++w) mx = fmaxf(mx, red[w]);
 
-    // e_j = exp(s_j - max); total = sequential sum, chunk by chunk: each chunk
-    // starts with the running total as its first term (fl(0 + s) == s)
+    // chunk by chunk, each chunk starting with the running total as its first
+    // term (fl(0 + e) == e, so the first chunk matches the loop from s = 0)
     float total = 0.f;
     for (int base = 0; base < n; base += seqsum::kMaxN - 1) {
         const int len = min(n - base, seqsum::kMaxN - 1);
-        for (int t = tid; t < len; t += 256) {
+        for (int t = tid; t < len; t += seqsum::kThreads) {
             const float e = exp_f32(sc[base + t] - mx);
             sc[base + t] = e;
             chunk[t + 1] = e;
         }
         if (tid == 0) chunk[0] = total;
         __syncthreads();
-        total = seqsum::sum_nonneg(chunk, len + 1, sm);
+        total = seqsum::sum_nonneg(chunk, len + 1, sm);  // ends with a barrier
     }
-    for (int t = tid; t < n; t += 256) sc[t] = sc[t] / total;
-    __syncthreads();
+    for (int t = tid; t < n; t += seqsum::kThreads) sc[t] = sc[t] / total;
+}
 
-    // out[c] = sum_j alpha_j * v_j[c], rows in order, a lane per channel
-    if (tid < kAttnDim) {
-        const int64_t kw = int64_t(a.Hkv) * kAttnDim;
-        const float* v = a.v_cache + (int64_t(b) * a.max_ctx + first) * kw + int64_t(g) * kAttnDim + tid;
-        float acc = 0.f;
-        int t = 0;
-        for (; t + 8 <= n; t += 8) {
-            float vv[8], al[8];
+// ---- 4. weighted sum of values, gate, quantize -----------------------------------------------
+// out[c] = sum_j alpha_j * v_j[c] with the rows in order (core.hpp:206-208),
+// one lane per channel. Each workgroup owns 32 channels (one Q8_0 block) of a
+// head; its 256 lanes stream the V rows through a ring of register tiles into
+// two shared-memory tiles so the 32 chain lanes read V from shared memory.
+constexpr int kPvSplit = 4;
+constexpr int kPvCh = kAttnDim / kPvSplit;                  // 32
+constexpr int kPvThreads = 256;
+constexpr int kPvTile = 128;                                // rows per tile
+constexpr int kPvVec = kPvTile * kPvCh / 4 / kPvThreads;    // float4 per lane per tile
+constexpr int kPvRing = 4;                                  // tiles in flight
+
+__global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(AttnDecodeArgs a) {
+    const int tid = threadIdx.x, h = blockIdx.x / kPvSplit, part = blockIdx.x % kPvSplit, b = blockIdx.y;
+    const int pos = a.positions[b];
+    if (pos < 0 || pos >= a.max_ctx) return;
+    const int g = h / (a.Hq / a.Hkv);
+    const int first = visible_first(pos, a.window);
+    const int n = pos + 1 - first;
+    const float* alpha = a.scores + (int64_t(b) * a.Hq + h) * a.max_ctx;
+    const int64_t kw = int64_t(a.Hkv) * kAttnDim;
+    const float* vb = a.v_cache + (int64_t(b) * a.max_ctx + first) * kw + int64_t(g) * kAttnDim + part * kPvCh;
+    __shared__ __align__(16) float vt[2][kPvTile * kPvCh];
+    __shared__ float at[2][kPvTile];
+    const int ntiles = (n + kPvTile - 1) / kPvTile;
+
+    float4 ring[kPvRing][kPvVec];
+    float aring[kPvRing];
+    // lane slot k of a tile: float4 q = tid + k*256 -> row q/8, channels 4*(q%8)..+3
+    auto load = [&](int tile, float4* dst, float& adst) {
+        const int r0 = tile * kPvTile;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                vv[u] = v[int64_t(t + u) * kw];
-                al[u] = sc[t + u];
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) acc += al[u] * vv[u];
+        for (int k = 0; k < kPvVec; ++k) {
+            const int q = tid + k * kPvThreads;
+            const int row = r0 + q / (kPvCh / 4);
+            dst[k] = row < n ? *reinterpret_cast<const float4*>(vb + int64_t(row) * kw + 4 * (q % (kPvCh / 4))) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        for (; t < n; ++t) acc += sc[t] * v[int64_t(t) * kw];
-        const float gate = a.proj[int64_t(b) * a.proj_stride + int64_t(h) * 2 * kAttnDim + kAttnDim + tid];
-        const float out = acc * sigmoid_f32(gate);
+        adst = (tid < kPvTile && r0 + tid < n) ? alpha[r0 + tid] : 0.f;
+    };
+#pragma unroll
+    for (int s = 0; s < kPvRing; ++s)
+        if (s < ntiles) load(s, ring[s], aring[s]);
 
+    float acc = 0.f;
+    for (int base = 0; base < ntiles; base += kPvRing) {
+#pragma unroll
+        for (int s = 0; s < kPvRing; ++s) {
+            const int tile = base + s;
+            if (tile >= ntiles) break;
+            float* buf = vt[tile & 1];
+            float* abuf = at[tile & 1];
+#pragma unroll
+            for (int k = 0; k < kPvVec; ++k) reinterpret_cast<float4*>(buf)[tid + k * kPvThreads] = ring[s][k];
+            if (tid < kPvTile) abuf[tid] = aring[s];
+            // one barrier per tile: the other buffer's readers finished before it
+            __syncthreads();
+            if (tile + kPvRing < ntiles) load(tile + kPvRing, ring[s], aring[s]);
+            if (tid < kPvCh) {
+                const int rows = min(kPvTile, n - tile * kPvTile);
+#pragma unroll 16
+                for (int r = 0; r < rows; ++r) acc += abuf[r] * buf[r * kPvCh + tid];
+            }
+        }
+    }
+
+    if (tid < kPvCh) {
+        const int c = part * kPvCh + tid;
+        const float gate = a.proj[int64_t(b) * a.proj_stride + int64_t(h) * 2 * kAttnDim + kAttnDim + c];
+        const float out = acc * sigmoid_f32(gate);
         const int64_t width = int64_t(a.Hq) * kAttnDim;
-        const int64_t idx = int64_t(h) * kAttnDim + tid;
+        const int64_t idx = int64_t(h) * kAttnDim + c;
         if (a.out_f32) a.out_f32[int64_t(b) * width + idx] = out;
         float amax = fabsf(out);
         for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
@@ -174,14 +226,15 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnDecodeArgs a) {
         int8_t* qs = static_cast<int8_t*>(a.act_out);
         float* qd = reinterpret_cast<float*>(qs + int64_t(a.B) * width);
         qs[int64_t(b) * width + idx] = int8_t(int(roundf(out * id)));
-        if ((tid & 31) == 0) qd[(int64_t(b) * width + idx) >> 5] = half_bits_to_f32(fp32_to_fp16_ref(d));
+        if (tid == 0) qd[(int64_t(b) * width + idx) >> 5] = half_bits_to_f32(fp32_to_fp16_ref(d));
     }
 }
 
 void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(attn_prep_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, a);
     hipLaunchKernelGGL(attn_scores_kernel, dim3(unsigned(a.Hq), kScoreTiles, unsigned(a.B)), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(attn_reduce_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(attn_softmax_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(seqsum::kThreads), 0, s, a);
+    hipLaunchKernelGGL(attn_pv_kernel, dim3(unsigned(a.Hq * kPvSplit), unsigned(a.B)), dim3(kPvThreads), 0, s, a);
 }
 
 }  // namespace hero

@@ -11,13 +11,13 @@
 
 namespace hero {
 
-__global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restrict__ x, const float* __restrict__ gamma, float eps, float* __restrict__ y, int8_t* __restrict__ qs, float* __restrict__ qd, int D) {
+__global__ __launch_bounds__(seqsum::kThreads) void rmsnorm_quant_kernel(const float* __restrict__ x, const float* __restrict__ gamma, float eps, float* __restrict__ y, int8_t* __restrict__ qs, float* __restrict__ qd, int D) {
     extern __shared__ __align__(16) float sq[];  // [D] squares
     __shared__ seqsum::Shared sm;
     const int64_t row = blockIdx.x;
     const float* xr = x + row * D;
     const int tid = threadIdx.x;
-    for (int i = tid; i < D; i += 256) {
+    for (int i = tid; i < D; i += seqsum::kThreads) {
         const float v = xr[i];
         sq[i] = v * v;
     }
@@ -32,7 +32,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restr
     }
     const float inv = 1.f / sqrtf(s / float(D) + eps);
     const int groups = D >> 3;
-    for (int g = tid; g < groups; g += 256) {
+    for (int g = tid; g < groups; g += seqsum::kThreads) {
         const float4 a = reinterpret_cast<const float4*>(xr)[2 * g];
         const float4 b = reinterpret_cast<const float4*>(xr)[2 * g + 1];
         const float4 ga = reinterpret_cast<const float4*>(gamma)[2 * g];
@@ -54,7 +54,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restr
 void launch_rmsnorm_quant(const float* x, const float* gamma, float eps, float* y, void* act, int64_t M, int64_t D, hipStream_t s) {
     int8_t* qs = static_cast<int8_t*>(act);
     float* qd = act ? reinterpret_cast<float*>(qs + M * D) : nullptr;
-    hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(unsigned(M)), dim3(256), size_t(D) * 4, s, x, gamma, eps, y, qs, qd, int(D));
+    hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(unsigned(M)), dim3(seqsum::kThreads), size_t(D) * 4, s, x, gamma, eps, y, qs, qd, int(D));
 }
 
 }  // namespace hero

@@ -17,10 +17,10 @@ int main(int argc, char** argv) {
     std::normal_distribution<float> N01(0.f, 1.f);
     std::uniform_real_distribution<float> U01(0.f, 1.f);
     static seqsum::Shared sm;
-    long bad = 0, fallbacks = 0, fb_kind[10] = {0};
+    long bad = 0, fallbacks = 0, fb_kind[11] = {0};
     std::vector<float> p(seqsum::kMaxN);
     for (int t = 0; t < trials; ++t) {
-        const int kind = t % 10;
+        const int kind = t % 11;
         int n = kind < 5 ? seqsum::kMaxN : 1 + int(rng() % seqsum::kMaxN);
         if (t % 97 == 0) n = 1 + int(rng() % 40);
         const float scale = std::ldexp(1.f, int(rng() % 60) - 30);
@@ -34,7 +34,8 @@ int main(int argc, char** argv) {
                 case 6: p[i] = U01(rng) < 0.01f ? x * x * 1e6f : x * x; break;          // outliers
                 case 7: p[i] = std::ldexp(1.f, int(rng() % 40) - 20) * (1.f + float(rng() % 4) / 4); break;
                 case 8: p[i] = x * x * 1e-30f; break;                                  // subnormal range
-                default: p[i] = (i < 8) ? 0.f : std::fabs(x); break;                   // leading zeros
+                case 9: p[i] = (i < 8) ? 0.f : std::fabs(x); break;                    // leading zeros
+                default: p[i] = i == 0 ? 3000.f * U01(rng) : std::exp(-4.f * std::fabs(N01(rng))); break;  // softmax chunk
             }
         }
         if (t % 211 == 0) p[rng() % n] = INFINITY;
@@ -53,6 +54,6 @@ int main(int argc, char** argv) {
     }
     std::printf("%d %ld %ld\n", trials, bad, fallbacks);
     if (argc > 2)
-        for (int k = 0; k < 10; ++k) std::fprintf(stderr, "kind %d fallbacks %ld\n", k, fb_kind[k]);
+        for (int k = 0; k < 11; ++k) std::fprintf(stderr, "kind %d fallbacks %ld\n", k, fb_kind[k]);
     return bad == 0 ? 0 : 1;
 }

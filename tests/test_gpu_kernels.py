@@ -51,7 +51,8 @@ def math_inputs():
 def test_device_exp_log1p_equal_glibc_and_activations_equal_oracle(lib):
     x = math_inputs()
     out = empty(5 * x.size * 4)
-    check(lib.hero_math_eval(ptr(dev(x)), ptr(out), x.size, stream()))
+    xd = dev(x)
+    check(lib.hero_math_eval(ptr(xd), ptr(out), x.size, stream()))
     got = host(out, np.float32, (5, x.size))
     same = lambda a, b: bool(np.all((bits(a) == bits(b)) | (np.isnan(a) & np.isnan(b))))  # noqa: E731
     assert same(got[0], oracle.expf(x)), "expf differs from glibc"
@@ -151,6 +152,41 @@ def test_rmsnorm_quant_matches_oracle(lib, d):
         assert blocks[r].tobytes() == oracle.quantize_row_q8_0(expect[r]).tobytes()
 
 
+def _hard_rows(d: int) -> np.ndarray:
+    """Rows whose sums of squares stress the exact parallel sum: ties, zeros,
+    subnormal and near-overflow squares, outliers, many binade crossings."""
+    rng = np.random.default_rng(d + 1)
+    i = np.arange(d, dtype=np.float64)
+    rows = [
+        rng.standard_normal(d) * 2,
+        rng.standard_normal(d) * 1e-21,                       # subnormal squares
+        rng.standard_normal(d) * 3e17,                        # squares near 1e36
+        np.where(rng.random(d) < 0.5, 0.0, rng.standard_normal(d)),
+        np.where(i < d // 2, 0.0, rng.standard_normal(d)),    # leading zeros
+        np.ones(d),                                           # exact integer sums
+        rng.integers(-4, 5, d) * 0.5,                         # many ties
+        rng.standard_normal(d) * np.where(rng.random(d) < 0.01, 1e3, 1.0),
+        np.exp2(i / 300.0) * np.sign(rng.standard_normal(d)), # growing terms
+        np.zeros(d),
+        np.full(d, 2.0 ** 60),                                # sum overflows to inf
+    ]
+    return np.stack(rows).astype(np.float32)
+
+
+@pytest.mark.parametrize("d", [4096, 1024, 2080])
+def test_rmsnorm_exact_on_hard_rows(lib, d):
+    x = _hard_rows(d)
+    m = x.shape[0]
+    g = np.ones(d, np.float32)
+    y = empty(m * d * 4)
+    xd, gd = dev(x), dev(g)
+    check(lib.hero_rmsnorm_quant(ptr(xd), ptr(gd), np.float32(1e-6), ptr(y), None, m, d, stream()))
+    got = host(y, np.float32, (m, d))
+    expect = oracle.rmsnorm(x, g)
+    for r in range(m):
+        assert np.array_equal(bits(got[r]), bits(expect[r])), f"row {r}"
+
+
 def test_rmsnorm_matches_reference_golden(lib, kernels_golden):
     for n in (1024, 4096):
         v = kernels_golden[f"in_rms{n}"]
@@ -165,7 +201,8 @@ def test_swiglu_quant_matches_oracle(lib):
     m, ff = 2, 12288
     gu = (rng.standard_normal((m, 2 * ff)) * 1.5).astype(np.float32)
     act = empty(lib.hero_q8_0_act_bytes(m, ff))
-    check(lib.hero_swiglu_quant(ptr(dev(gu)), ptr(act), m, ff, stream()))
+    gud = dev(gu)
+    check(lib.hero_swiglu_quant(ptr(gud), ptr(act), m, ff, stream()))
     got = act_to_blocks(host(act, np.uint8), m, ff)
     for r in range(m):
         g = oracle.silu(gu[r, :ff]) * gu[r, ff:]
@@ -180,7 +217,8 @@ def test_embed_matches_oracle(lib):
     packed = pack_weight(lib, w, v, d)
     ids = np.array([0, 999, 5, 5, 123], np.int32)
     out = empty(len(ids) * d * 4)
-    check(lib.hero_q8_0_embed(ptr(packed), v, d, ptr(dev(ids)), len(ids), ptr(out), stream()))
+    idd = dev(ids)
+    check(lib.hero_q8_0_embed(ptr(packed), v, d, ptr(idd), len(ids), ptr(out), stream()))
     got = host(out, np.float32, (len(ids), d))
     wb = w.reshape(v, d // 32)
     for i, t in enumerate(ids):
@@ -200,7 +238,8 @@ def test_argmax_ties_go_to_lowest_index(lib):
     logits[3, n - 1] = 99.0                       # last element
     out = empty(m * 4)
     scratch = empty(m * 128 * 8)
-    check(lib.hero_argmax(ptr(dev(logits)), m, n, ptr(out), ptr(scratch), stream()))
+    ld = dev(logits)
+    check(lib.hero_argmax(ptr(ld), m, n, ptr(out), ptr(scratch), stream()))
     got = host(out, np.int32)
     assert list(got) == [int(np.argmax(r)) for r in logits]
     assert list(got[1:]) == [5, 50, n - 1]

@@ -12,8 +12,11 @@ namespace hero {
 
 enum : int { kEpiStore = 0, kEpiResidual = 1 };
 
-// bytes of a packed Q8_0 weight / a quantized activation block set
-inline int64_t packed_q8_bytes(int64_t N, int64_t K) { return N * K + N * (K / 32) * 2; }
+// packed Q8_0 weight: [N][K] int8, then the fp16 scales block-major,
+// [K/32][Npad] with Npad = N rounded up to 8 (rows past N unused), so the scales of
+// 8 consecutive rows of one block are one 16-byte load
+inline int64_t packed_rows_pad(int64_t N) { return (N + 7) / 8 * 8; }
+inline int64_t packed_q8_bytes(int64_t N, int64_t K) { return N * K + packed_rows_pad(N) * (K / 32) * 2; }
 inline int64_t act_q8_bytes(int64_t M, int64_t K) { return M * K + M * (K / 32) * 4; }
 
 // q8.hip
@@ -21,7 +24,6 @@ void launch_quantize_act(const float* x, void* act, int64_t M, int64_t K, hipStr
 void launch_pack_q8(const void* gguf_blocks, void* packed, int64_t N_total, int64_t K, int64_t row0, int64_t rows, hipStream_t s);
 void launch_gemv_q8(const void* packed, const void* act, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s);
 void launch_block_sums(const void* packed, const void* act, int32_t* out, int64_t N, int64_t K, hipStream_t s);
-int gemv_rows_per_group(int64_t N, int64_t K);
 
 // norm.hip: rows x [M][D] -> RMSNorm (gamma, eps) -> quantized act; y (fp32) optional
 void launch_rmsnorm_quant(const float* x, const float* gamma, float eps, float* y, void* act, int64_t M, int64_t D, hipStream_t s);

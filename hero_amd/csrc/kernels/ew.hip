@@ -31,11 +31,11 @@ void launch_swiglu_quant(const float* gate_up, void* act, int64_t M, int64_t FF,
 }
 
 // nm/src/quant.hpp:306-313: row = d * q
-__global__ __launch_bounds__(256) void embed_kernel(const int8_t* __restrict__ qs, const uint16_t* __restrict__ d, int64_t D, const int32_t* __restrict__ ids, float* __restrict__ out) {
+__global__ __launch_bounds__(256) void embed_kernel(const int8_t* __restrict__ qs, const uint16_t* __restrict__ d, int64_t D, int64_t Vpad, const int32_t* __restrict__ ids, float* __restrict__ out) {
     const int64_t t = blockIdx.y;
     const int64_t id = ids[t];
     for (int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; c < D; c += int64_t(gridDim.x) * blockDim.x) {
-        const float scale = half_bits_to_f32(d[id * (D >> 5) + (c >> 5)]);
+        const float scale = half_bits_to_f32(d[(c >> 5) * Vpad + id]);  // block-major scales
         out[t * D + c] = scale * float(qs[id * D + c]);
     }
 }
@@ -43,7 +43,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const int8_t* __restrict__ q
 void launch_embed_q8(const void* packed, int64_t V, int64_t D, const int32_t* ids, int64_t n, float* out, hipStream_t s) {
     const int8_t* qs = static_cast<const int8_t*>(packed);
     const uint16_t* d = reinterpret_cast<const uint16_t*>(qs + V * D);
-    hipLaunchKernelGGL(embed_kernel, dim3(unsigned((D + 255) / 256), unsigned(n)), dim3(256), 0, s, qs, d, D, ids, out);
+    hipLaunchKernelGGL(embed_kernel, dim3(unsigned((D + 255) / 256), unsigned(n)), dim3(256), 0, s, qs, d, D, packed_rows_pad(V), ids, out);
 }
 
 // Greedy argmax (nm/src/logits.hpp:61-66): largest value, ties to the lowest

@@ -2,11 +2,14 @@
 // and the int8-activation matvec (GEMV) with the reference's accumulation
 // order.
 //
-// Device layouts (all row-major by output row, like the GGUF tensor):
-//   packed weight  [ qs: N*K int8 ][ d: N*(K/32) fp16 ]      34 bytes / 32 weights
+// Device layouts:
+//   packed weight  [ qs: N*K int8, row-major ][ d: (K/32) x Npad fp16, block-major ]
+//                  Npad = N rounded up to 8 (zero rows): the scales of 8
+//                  consecutive rows of one block are one 16-byte load.
 //   quantized act  [ qs: M*K int8 ][ d: M*(K/32) fp32 ]      d = fp16-decoded scale
-// The planar split lets a lane fetch 16 weight bytes with one aligned
-// global_load_dwordx4, which the 34-byte GGUF block stride does not allow.
+// Splitting quants from scales lets a lane fetch 16 weight bytes with one
+// aligned global_load_dwordx4, which the 34-byte GGUF block stride does not
+// allow.
 //
 // GEMV numerics (nm/src/quant_i8.hpp:85-100): for output row o,
 //   y[o] = sum over blocks b, IN BLOCK ORDER, of float(sumi_b) * (d_w * d_x)
@@ -45,12 +48,13 @@ void launch_quantize_act(const float* x, void* act, int64_t M, int64_t K, hipStr
 // ---------------------------------------------------------------------------
 // weight packing: GGUF Q8_0 blocks [N][K/32] x 34 B -> planar, at row offset
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void pack_q8_kernel(const uint8_t* __restrict__ src, int8_t* __restrict__ qs, uint16_t* __restrict__ d, int64_t blocks, int64_t row_blocks, int64_t row0) {
+__global__ __launch_bounds__(256) void pack_q8_kernel(const uint8_t* __restrict__ src, int8_t* __restrict__ qs, uint16_t* __restrict__ d, int64_t blocks, int64_t row_blocks, int64_t row0, int64_t Npad) {
     const int64_t blk = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (blk >= blocks) return;
     const uint8_t* b = src + blk * 34;
     const int64_t dst_blk = row0 * row_blocks + blk;
-    d[dst_blk] = uint16_t(b[0] | (b[1] << 8));
+    const int64_t row = dst_blk / row_blocks, col = dst_blk - row * row_blocks;
+    d[col * Npad + row] = uint16_t(b[0] | (b[1] << 8));
     int w[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) w[j] = int(b[2 + 4 * j]) | (int(b[3 + 4 * j]) << 8) | (int(b[4 + 4 * j]) << 16) | (int(b[5 + 4 * j]) << 24);
@@ -63,24 +67,142 @@ void launch_pack_q8(const void* gguf_blocks, void* packed, int64_t N_total, int6
     int8_t* qs = static_cast<int8_t*>(packed);
     uint16_t* d = reinterpret_cast<uint16_t*>(qs + N_total * K);
     const int64_t blocks = rows * (K / 32);
-    hipLaunchKernelGGL(pack_q8_kernel, dim3(unsigned((blocks + 255) / 256)), dim3(256), 0, s, static_cast<const uint8_t*>(gguf_blocks), qs, d, blocks, K / 32, row0);
+    hipLaunchKernelGGL(pack_q8_kernel, dim3(unsigned((blocks + 255) / 256)), dim3(256), 0, s, static_cast<const uint8_t*>(gguf_blocks), qs, d, blocks, K / 32, row0, packed_rows_pad(N_total));
 }
 
 // ---------------------------------------------------------------------------
-// GEMV, M = 1 (one activation row). Workgroup = 256 lanes, R output rows.
-// Items are (row, 16-byte chunk) pairs; item i is handled by lane i % 256 in
-// round i / 256, so the two chunks of a block sit in adjacent lanes and their
-// partial int32 sums combine with one lane swap. All weight loads of a lane
-// are issued before any is consumed (IPT in flight per lane).
+// GEMV, M = 1 (one activation row), K a multiple of 4096: the streaming kernel.
+//
+// A fixed grid of workgroups (one or two per CU) each owns a contiguous range
+// of whole 8-row groups, so every workgroup moves the same bytes and there is
+// no tail of late workgroups. Lane t always handles the K-chunks t + 256m
+// (m < CPL = K/4096), so its x chunks and act scales stay in registers. Rows
+// are processed 8 at a time (a sub-batch) through a ring of D sub-batches of
+// weight and scale registers, refilled as soon as a sub-batch is consumed, so
+// loads stay in flight while the lanes compute. Each pair of lanes forms a
+// block's exact int32 sum (DPP swap), the even lane multiplies it by
+// (d_w * d_x) and stores the term in shared memory. Every TR rows (and at the
+// end) one barrier, then lane r of wave 0 adds row r's terms in block order
+// (the reference's chain) and stores y.
+// ---------------------------------------------------------------------------
+constexpr int kStreamRB = 8;  // rows per sub-batch
+
+__device__ __forceinline__ int lane_pair_value(int v) {  // the value of lane ^ 1
+    return __builtin_amdgcn_update_dpp(0, v, 0xB1 /* quad_perm [1,0,3,2] */, 0xF, 0xF, false);
+}
+
+template <int CPL, int D, int EPI>
+__global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int N, int Npad, int TR) {
+    constexpr int K = 4096 * CPL, nb = K / 32, ts = nb + 4;  // ts: padded term row (conflict-free 16-byte reads)
+    extern __shared__ __align__(16) float terms[];          // [TR][ts]
+    const int tid = threadIdx.x;
+    const int G = gridDim.x, U = Npad / 8;
+    const int r_begin = 8 * int((int64_t(U) * blockIdx.x) / G);
+    const int r_end = min(N, 8 * int((int64_t(U) * (blockIdx.x + 1)) / G));
+    const int nsub = r_end > r_begin ? (r_end - r_begin + kStreamRB - 1) / kStreamRB : 0;
+    const bool even = (tid & 1) == 0;
+
+    int4 xv[CPL];
+    float dx[CPL];
+#pragma unroll
+    for (int m = 0; m < CPL; ++m) {
+        const int c = tid + 256 * m;
+        xv[m] = reinterpret_cast<const int4*>(xq)[c];
+        dx[m] = xd[c >> 1];
+    }
+    int4 ring[D][kStreamRB][CPL];
+    int4 sring[D][CPL];  // even lanes: scales of the sub-batch's 8 rows for each of the lane's blocks
+    auto load = [&](int j, int4 (&dst)[kStreamRB][CPL], int4 (&sdst)[CPL]) {
+        const int rb = r_begin + j * kStreamRB;
+#pragma unroll
+        for (int r = 0; r < kStreamRB; ++r)
+#pragma unroll
+            for (int m = 0; m < CPL; ++m)
+                dst[r][m] = rb + r < r_end ? reinterpret_cast<const int4*>(wq + int64_t(rb + r) * K)[tid + 256 * m] : make_int4(0, 0, 0, 0);
+#pragma unroll
+        for (int m = 0; m < CPL; ++m)  // rb is a multiple of 8 and rb + 8 <= Npad
+            sdst[m] = even ? *reinterpret_cast<const int4*>(wd + int64_t((tid + 256 * m) >> 1) * Npad + rb) : make_int4(0, 0, 0, 0);
+    };
+#pragma unroll
+    for (int s = 0; s < D; ++s)
+        if (s < nsub) load(s, ring[s], sring[s]);
+
+    int chain_row0 = r_begin;  // first row of the pending chain pass
+    for (int base = 0; base < nsub; base += D) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) {
+            const int j = base + s;
+            if (j < nsub) {
+                const int rb = r_begin + j * kStreamRB;
+#pragma unroll
+                for (int r = 0; r < kStreamRB; ++r) {
+                    const uint32_t pair = uint32_t(r < 4 ? (r < 2 ? 0 : 1) : (r < 6 ? 2 : 3));
+#pragma unroll
+                    for (int m = 0; m < CPL; ++m) {
+                        int v = dot16_i8(ring[s][r][m], xv[m], 0);
+                        v += lane_pair_value(v);  // the block's other 16 bytes (exact)
+                        if (even && rb + r < r_end) {
+                            const int4 sc = sring[s][m];
+                            const uint32_t two = uint32_t(pair == 0 ? sc.x : pair == 1 ? sc.y : pair == 2 ? sc.z : sc.w);
+                            const uint16_t h = uint16_t((r & 1) ? (two >> 16) : (two & 0xFFFFu));
+                            terms[(rb + r - chain_row0) * ts + ((tid + 256 * m) >> 1)] = float(v) * (half_bits_to_f32(h) * dx[m]);
+                        }
+                    }
+                }
+                if (j + D < nsub) load(j + D, ring[s], sring[s]);
+                const int done = rb + kStreamRB - chain_row0;  // rows whose terms are all stored
+                if (done >= TR || j + 1 == nsub) {
+                    const int rows = min(done, r_end - chain_row0);
+                    __syncthreads();
+                    if (tid < rows) {
+                        const float4* t = reinterpret_cast<const float4*>(terms + tid * ts);
+                        float acc = 0.f;
+                        float4 q[4];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) q[u] = t[u];
+                        for (int b4 = 0; b4 < nb / 4; b4 += 4) {
+                            float4 nq[4];
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) nq[u] = b4 + 4 + u < nb / 4 ? t[b4 + 4 + u] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) {
+                                acc += q[u].x;
+                                acc += q[u].y;
+                                acc += q[u].z;
+                                acc += q[u].w;
+                            }
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) q[u] = nq[u];
+                        }
+                        const int64_t o = chain_row0 + tid;
+                        if constexpr (EPI == kEpiResidual)
+                            y[o] = resid[o] + acc;  // h = x + m (nm/src/qwen35.hpp:321)
+                        else
+                            y[o] = acc;
+                    }
+                    __syncthreads();
+                    chain_row0 += rows;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GEMV for any K % 32 == 0 (used where K is not a multiple of 4096). One-shot
+// workgroups of 256 lanes over R rows; items are (row, 16-byte chunk) pairs,
+// item i handled by lane i % 256, so a block's two chunks sit in adjacent
+// lanes. Terms go to shared memory, then lane r adds row r's terms in order.
 // ---------------------------------------------------------------------------
 template <int IPT, int EPI>
-__global__ __launch_bounds__(256) void gemv_q8_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int N, int K, int R) {
+__global__ __launch_bounds__(256) void gemv_q8_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int N, int Npad, int K, int R) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x;
     const int nb = K >> 5, cpr = K >> 4;
-    int4* xs = reinterpret_cast<int4*>(smem);                     // [cpr]
+    int4* xs = reinterpret_cast<int4*>(smem);                        // [cpr]
     float* xds = reinterpret_cast<float*>(smem + size_t(cpr) * 16);  // [nb]
-    float* terms = xds + nb;                                       // [nb][R]
+    float* terms = xds + nb;                                          // [R][nb + 4]
+    const int ts = nb + 4;
     const int row0 = blockIdx.x * R;
     const int rows_here = min(R, N - row0);
     const int items = rows_here * cpr;
@@ -94,7 +216,7 @@ __global__ __launch_bounds__(256) void gemv_q8_kernel(const int8_t* __restrict__
             const int r = it / cpr, c = it - r * cpr;
             const int64_t row = row0 + r;
             w[k] = reinterpret_cast<const int4*>(wq + row * K)[c];
-            dw[k] = (c & 1) == 0 ? half_bits_to_f32(wd[row * nb + (c >> 1)]) : 0.f;
+            dw[k] = (c & 1) == 0 ? half_bits_to_f32(wd[int64_t(c >> 1) * Npad + row]) : 0.f;
         }
     }
     for (int i = tid; i < cpr; i += 256) xs[i] = reinterpret_cast<const int4*>(xq)[i];
@@ -110,60 +232,103 @@ __global__ __launch_bounds__(256) void gemv_q8_kernel(const int8_t* __restrict__
             s += __shfl_xor(s, 1);  // the other half of this block (exact)
             if ((c & 1) == 0) {
                 const int b = c >> 1;
-                terms[b * R + r] = float(s) * (dw[k] * xds[b]);
+                terms[r * ts + b] = float(s) * (dw[k] * xds[b]);
             }
         }
     }
     __syncthreads();
 
     if (tid < rows_here) {
+        const float* t = terms + tid * ts;
         float acc = 0.f;
-        for (int b = 0; b < nb; ++b) acc += terms[b * R + tid];
+        int b = 0;
+        for (; b + 16 <= nb; b += 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u += 4) {
+                const float4 q = *reinterpret_cast<const float4*>(t + b + u);
+                v[u] = q.x, v[u + 1] = q.y, v[u + 2] = q.z, v[u + 3] = q.w;
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) acc += v[u];
+        }
+        for (; b < nb; ++b) acc += t[b];
         const int64_t o = row0 + tid;
         if constexpr (EPI == kEpiResidual)
-            y[o] = resid[o] + acc;  // h = x + m (nm/src/qwen35.hpp:321)
+            y[o] = resid[o] + acc;
         else
             y[o] = acc;
     }
 }
 
 namespace {
+
+int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+template <int CPL, int D>
+void stream_dispatch(int epi, const int8_t* wq, const uint16_t* wd, const int8_t* xq, const float* xd, float* y, const float* resid, int N, int Npad, int G, int TR, size_t smem, hipStream_t s) {
+    if (epi == kEpiResidual)
+        hipLaunchKernelGGL((gemv_q8_stream_kernel<CPL, D, kEpiResidual>), dim3(unsigned(G)), dim3(256), smem, s, wq, wd, xq, xd, y, resid, N, Npad, TR);
+    else
+        hipLaunchKernelGGL((gemv_q8_stream_kernel<CPL, D, kEpiStore>), dim3(unsigned(G)), dim3(256), smem, s, wq, wd, xq, xd, y, resid, N, Npad, TR);
+}
+
 template <int IPT>
-void gemv_dispatch_epi(int epi, const int8_t* wq, const uint16_t* wd, const int8_t* xq, const float* xd, float* y, const float* resid, int N, int K, int R, size_t smem, hipStream_t s) {
+void gemv_dispatch_epi(int epi, const int8_t* wq, const uint16_t* wd, const int8_t* xq, const float* xd, float* y, const float* resid, int N, int Npad, int K, int R, size_t smem, hipStream_t s) {
     const dim3 grid(unsigned((N + R - 1) / R));
     if (epi == kEpiResidual)
-        hipLaunchKernelGGL((gemv_q8_kernel<IPT, kEpiResidual>), grid, dim3(256), smem, s, wq, wd, xq, xd, y, resid, N, K, R);
+        hipLaunchKernelGGL((gemv_q8_kernel<IPT, kEpiResidual>), grid, dim3(256), smem, s, wq, wd, xq, xd, y, resid, N, Npad, K, R);
     else
-        hipLaunchKernelGGL((gemv_q8_kernel<IPT, kEpiStore>), grid, dim3(256), smem, s, wq, wd, xq, xd, y, resid, N, K, R);
+        hipLaunchKernelGGL((gemv_q8_kernel<IPT, kEpiStore>), grid, dim3(256), smem, s, wq, wd, xq, xd, y, resid, N, Npad, K, R);
 }
-}  // namespace
 
-int gemv_rows_per_group(int64_t N, int64_t K) {
-    const int64_t cpr = K / 16;
-    // aim for 8 chunk loads in flight per lane, at least one row
-    int64_t R = std::max<int64_t>(1, (8 * 256) / cpr);
-    R = std::min<int64_t>(R, 64);
-    (void)N;
-    return int(R);
-}
+}  // namespace
 
 void launch_gemv_q8(const void* packed, const void* act, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s) {
     const int8_t* wq = static_cast<const int8_t*>(packed);
     const uint16_t* wd = reinterpret_cast<const uint16_t*>(wq + N * K);
     const int8_t* xq = static_cast<const int8_t*>(act);
     const float* xd = reinterpret_cast<const float*>(xq + K);
-    const int R = gemv_rows_per_group(N, K);
-    const int cpr = int(K / 16), nb = int(K / 32);
-    const int ipt = (R * cpr + 255) / 256;
-    const size_t smem = size_t(cpr) * 16 + size_t(nb) * 4 + size_t(nb) * R * 4;
+    const int Npad = int(packed_rows_pad(N));
+    if (K % 4096 == 0 && K / 4096 <= 3) {
+        // one workgroup per CU, two for the tall matrices; row ranges in whole 8-row groups
+        const int cus = device_cus();
+        const int G = std::min<int64_t>(N >= 16384 ? 2 * cus : cus, Npad / 8);
+        const int64_t rows_per = (Npad / 8 + G - 1) / G * 8;
+        const int nb = int(K / 32);
+        // rows per chain pass: at most 64 (one wave) and 64 KB of terms
+        int64_t TR = std::min<int64_t>({64, rows_per, (65536 / ((nb + 4) * 4)) / 8 * 8});
+        const size_t smem = size_t(TR) * (nb + 4) * 4;
+        switch (K / 4096) {
+            case 1: stream_dispatch<1, 2>(epi, wq, wd, xq, xd, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+            case 2: stream_dispatch<2, 1>(epi, wq, wd, xq, xd, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+            default: stream_dispatch<3, 1>(epi, wq, wd, xq, xd, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+        }
+        return;
+    }
+    const int64_t cpr = K / 16;
+    const int R = int(std::min<int64_t>(64, std::max<int64_t>(1, (8 * 256) / cpr)));  // ~8 chunk loads in flight per lane
+    const int nb = int(K / 32);
+    const int ipt = int((R * cpr + 255) / 256);
+    const size_t smem = size_t(cpr) * 16 + size_t(nb) * 4 + size_t(nb + 4) * R * 4;
     if (ipt <= 4)
-        gemv_dispatch_epi<4>(epi, wq, wd, xq, xd, y, resid, int(N), int(K), R, smem, s);
+        gemv_dispatch_epi<4>(epi, wq, wd, xq, xd, y, resid, int(N), Npad, int(K), R, smem, s);
     else if (ipt <= 8)
-        gemv_dispatch_epi<8>(epi, wq, wd, xq, xd, y, resid, int(N), int(K), R, smem, s);
+        gemv_dispatch_epi<8>(epi, wq, wd, xq, xd, y, resid, int(N), Npad, int(K), R, smem, s);
     else if (ipt <= 12)
-        gemv_dispatch_epi<12>(epi, wq, wd, xq, xd, y, resid, int(N), int(K), R, smem, s);
+        gemv_dispatch_epi<12>(epi, wq, wd, xq, xd, y, resid, int(N), Npad, int(K), R, smem, s);
     else
-        gemv_dispatch_epi<16>(epi, wq, wd, xq, xd, y, resid, int(N), int(K), R, smem, s);
+        gemv_dispatch_epi<16>(epi, wq, wd, xq, xd, y, resid, int(N), Npad, int(K), R, smem, s);
 }
 
 // ---------------------------------------------------------------------------

@@ -93,7 +93,10 @@ def test_gemv_matches_reference_golden(lib, kernels_golden):
         assert np.array_equal(bits(host(y, np.float32)), bits(golden[r + 1] if r else golden[0])), f"row {r}"
 
 
-GEMV_SHAPES = [(4096, 4096), (16448, 4096), (4096, 12288), (10240, 1024), (5632, 1024), (1024, 2816), (32000, 1024), (64, 256), (96, 4096)]
+# K % 4096 == 0 takes the streaming kernel (incl. N not a multiple of 8 and
+# fewer rows than workgroups); other K the general one
+GEMV_SHAPES = [(4096, 4096), (16448, 4096), (4096, 12288), (4100, 4096), (33, 8192), (1003, 12288), (96, 4096),
+               (10240, 1024), (5632, 1024), (1024, 2816), (32000, 1024), (64, 256)]
 
 
 @pytest.mark.parametrize("n,k", GEMV_SHAPES)

@@ -115,3 +115,48 @@ def test_tiny_model_greedy_ids_match_reference(tiny_run, tiny_golden):
 @pytest.mark.parametrize("which", ["prefill", "mid", "last"])
 def test_tiny_model_logits_match_reference_bitwise(tiny_run, tiny_golden, which):
     assert np.array_equal(bits(tiny_run[which]), bits(tiny_golden[f"logits_{which}"]))
+
+
+def test_fp16_decoder_is_ieee_half_on_all_inputs():
+    """nm/src/core.hpp:34-59 decodes IEEE binary16 exactly: all 65536 codes
+    against numpy's float16 -> float32 conversion, bit for bit."""
+    h = np.arange(65536, dtype=np.uint16)
+    got = oracle.fp16_to_fp32(h)
+    want = h.view(np.float16).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def _fp16_nearest_ties_away(x: np.ndarray) -> np.ndarray:
+    """fp32 -> fp16 bits: round to nearest, ties away from zero, overflow and
+    NaN to signed infinity -- the rule of nm/src/core.hpp:61-79, computed here
+    from the fp16 grid in float64 rather than from the bits."""
+    x = np.asarray(x, np.float32)
+    sign = (x.view(np.uint32) >> 16).astype(np.uint16) & np.uint16(0x8000)
+    v = np.abs(x.astype(np.float64))
+    with np.errstate(over="ignore", invalid="ignore"):
+        h = v.astype(np.float16)  # nearest-even, used only to find the neighbours
+        lo = np.where(h.astype(np.float64) <= v, h, np.nextafter(h, np.float16(-np.inf)))
+        lo = np.where(np.isinf(lo), np.float16(65504.0), lo)
+        hi = np.nextafter(lo, np.float16(np.inf))
+        hi_val = np.where(np.isinf(hi), 65536.0, hi.astype(np.float64))
+        d_lo = v - lo.astype(np.float64)
+        d_hi = hi_val - v
+        pick = np.where(d_hi <= d_lo, hi, lo)
+    bits = pick.view(np.uint16)
+    bits = np.where(np.isnan(x), np.uint16(0x7C00), bits)
+    return (bits | sign).astype(np.uint16)
+
+
+def test_fp16_encoder_is_nearest_ties_away():
+    """The encoder against a closed form on 2^21 random fp32 patterns plus every
+    fp16 midpoint (the ties), zeros, infinities and NaN."""
+    rng = np.random.default_rng(11)
+    rand = rng.integers(0, 2**32, 1 << 21, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    grid = np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float64)
+    mids = ((grid[:-1] + grid[1:]) / 2).astype(np.float32)  # exact in fp32
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 65504.0, 65519.99, 65520.0, 2.0**-25, 2.0**-26, 3 * 2.0**-26], np.float32)
+    x = np.concatenate([rand, mids, -mids, special])
+    got = oracle.fp32_to_fp16(x)
+    want = _fp16_nearest_ties_away(x)
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, [(float(x[i]), hex(int(got[i])), hex(int(want[i]))) for i in bad[:5]]

@@ -70,4 +70,29 @@ __device__ __forceinline__ int2 quantize8_in_quad(const float (&x)[8], uint16_t*
     return make_int2(packed[0], packed[1]);
 }
 
+// The value of lane ^ 1 (DPP quad_perm [1,0,3,2]; all lanes active).
+__device__ __forceinline__ int pair_swap_i32(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ float pair_swap_f32(float v) { return __int_as_float(pair_swap_i32(__float_as_int(v))); }
+
+// quantize_row_q8_0 (nm/src/quant_i8.hpp:70-80) for one 32-value block held
+// 16 per lane by an even/odd lane pair: the same rules as quantize8_in_quad.
+// Returns the lane's 16 int8 values packed in an int4; *dh receives the fp16
+// bits of d (identical on both lanes). All lanes of the wave must be active.
+__device__ __forceinline__ int4 quantize16_in_pair(const float (&x)[16], uint16_t* dh) {
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(x[j]));
+    amax = fmaxf(amax, pair_swap_f32(amax));
+    const float d = amax / 127.f;
+    const float id = d != 0.f ? 1.f / d : 0.f;
+    *dh = fp32_to_fp16_ref(d);
+    int packed[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int q = int(roundf(x[j] * id));
+        packed[j / 4] |= (q & 0xFF) << (8 * (j % 4));
+    }
+    return make_int4(packed[0], packed[1], packed[2], packed[3]);
+}
+
 }  // namespace hero

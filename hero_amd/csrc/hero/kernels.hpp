@@ -10,7 +10,10 @@
 
 namespace hero {
 
-enum : int { kEpiStore = 0, kEpiResidual = 1 };
+// GEMV epilogues: y = Wx; y = r + Wx; and, for a [gate|up] matrix packed in
+// alternating 32-row chunks (K = 4096, N % 64 == 0), y <- the quantized
+// activation of silu(gate) * up ([N/2] int8 + [N/64] fp32 scales)
+enum : int { kEpiStore = 0, kEpiResidual = 1, kEpiSwigluQuant = 2 };
 
 // packed Q8_0 weight: [N][K] int8, then the fp16 scales block-major,
 // [K/32][Npad] with Npad = N rounded up to 8 (rows past N unused), so the scales of
@@ -21,8 +24,22 @@ inline int64_t act_q8_bytes(int64_t M, int64_t K) { return M * K + M * (K / 32) 
 
 // q8.hip
 void launch_quantize_act(const float* x, void* act, int64_t M, int64_t K, hipStream_t s);
-void launch_pack_q8(const void* gguf_blocks, void* packed, int64_t N_total, int64_t K, int64_t row0, int64_t rows, hipStream_t s);
+void launch_pack_q8(const void* gguf_blocks, void* packed, int64_t N_total, int64_t K, int64_t row0, int64_t rows, hipStream_t s, int64_t interleave = 0);
 void launch_gemv_q8(const void* packed, const void* act, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s);
+// The streaming GEMV (K a multiple of 4096, at most 12288) with its input
+// formed in the prologue from one of three sources.
+enum : int { kInAct = 0, kInRmsNorm = 1, kInSwiglu = 2 };
+struct GemvInput {
+    int mode;
+    const int8_t* xq;        // kInAct: quantized activation [K] + fp32 scales [K/32]
+    const float* xd;
+    const float* x;          // kInRmsNorm: residual row [K] (K == 4096), RMSNorm weight, eps
+    const float* gamma;
+    float eps;
+    const float* gate_up;    // kInSwiglu: [gate K | up K]
+};
+bool gemv_streams(int64_t K);
+void launch_gemv_q8_in(const void* packed, const GemvInput& in, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s);
 void launch_block_sums(const void* packed, const void* act, int32_t* out, int64_t N, int64_t K, hipStream_t s);
 
 // norm.hip: rows x [M][D] -> RMSNorm (gamma, eps) -> quantized act; y (fp32) optional

@@ -117,6 +117,9 @@ private:
     ModelConfig c_;
     std::vector<LayerWeights> layers_;
     DeviceBuffer embedding_, output_, final_norm_, rope_cs_;
+    // d_model 4096: gate and up packed in alternating 32-row chunks, so the
+    // gate/up GEMV ends in SwiGLU and writes the down projection's input
+    bool ffn_fused_ = false;
     int64_t rope_positions_ = 0;
     int64_t device_bytes_ = 0;
     hipStream_t stream_ = nullptr;
@@ -140,6 +143,7 @@ private:
     // per-step device scalars: [0] position, [1] token id, [2] step counter
     DeviceBuffer step_;
     DeviceBuffer x_, h_, rows_, proj_, act_d_, act_mix_, act_ff_, gate_up_, logits_, argmax_scratch_, out_ids_, q_rot_;
+    DeviceBuffer gemv_scratch_;  // [D] output of the GEMV timing runs
     int64_t rows_capacity_ = 0, out_ids_capacity_ = 0;
     std::vector<DeviceBuffer> k_cache_, v_cache_, scores_, conv_hist_, delta_;
     hipGraphExec_t graph_ = nullptr;  // one greedy decode step, replayed

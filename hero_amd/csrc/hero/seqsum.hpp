@@ -1,6 +1,6 @@
 // seqsum.hpp -- the sequential fp32 sum of n >= 0 terms,
 //     s = 0; for i in 0..n-1: s = fl(s + p[i])
-// computed by a 1024-lane workgroup, bit-identical to the loop.
+// computed by a workgroup of 1024 or 256 lanes, bit-identical to the loop.
 //
 // The reference's RMSNorm and L2 norms sum squares in index order
 // (nm/src/core.hpp:496-500) and its softmax sums exponentials in index order
@@ -31,9 +31,10 @@
 //    partial sums stay far closer than m to the speculated ones except in
 //    contrived inputs, so that fallback is rare.
 //
-// Lane t holds elements 4t .. 4t+3. The cross-lane steps are wave shuffles
-// plus exchanges of per-wave totals through shared memory; the host emulation
-// at the end runs the same per-lane functions in the same order.
+// Lane t holds elements PT*t .. PT*t+PT-1 (PT = 4096 / lanes). The cross-lane
+// steps are wave shuffles plus exchanges of per-wave totals through shared
+// memory; the host emulation at the end runs the same per-lane functions in
+// the same order.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -45,12 +46,15 @@
 namespace hero {
 namespace seqsum {
 
-constexpr int kThreads = 1024;
+// Workgroups of 1024 lanes (4 elements each) or 256 lanes (16 each); both sum
+// up to 4096 terms. The 1024-lane form is the faster; the 256-lane form runs
+// inside other kernels' workgroups.
+constexpr int kThreads = 1024;  // the default workgroup
 constexpr int kWaveSize = 64;
-constexpr int kWaves = kThreads / kWaveSize;
-constexpr int kPerThread = 4;
-constexpr int kMaxN = kThreads * kPerThread;  // 4096
+constexpr int kMaxWaves = 16;
+constexpr int kMaxN = 4096;
 constexpr int kMaxSerial = 512;
+constexpr int kWaves = kThreads / kWaveSize;  // of the default workgroup
 constexpr float kMarginLo = 1.0f - 1.0f / 16384.0f;
 constexpr float kMarginHi = 1.0f + 1.0f / 16384.0f;
 
@@ -62,8 +66,8 @@ __host__ __device__ inline int binade_f32(float s) {
 }
 
 struct Shared {
-    float wsum[kWaves];              // wave totals of the speculation scan
-    uint32_t wc[kWaves], wn[kWaves]; // wave totals of the increment and serial-count scans
+    float wsum[kMaxWaves];                 // wave totals of the speculation scan
+    uint32_t wc[kMaxWaves], wn[kMaxWaves]; // wave totals of the increment and serial-count scans
     int32_t ser_idx[kMaxSerial];     // index of serial element r
     float ser_val[kMaxSerial];       // its term
     uint32_t ser_cx[kMaxSerial];     // increments of all non-serial elements before it (mod 2^32)
@@ -74,34 +78,43 @@ struct Shared {
     float result;
 };
 
-struct Lane {  // what a lane keeps in registers between steps
-    float v[kPerThread];
-    uint32_t c[kPerThread];       // increment of each non-serial element, in its run's units
-    int32_t e_after[kPerThread];  // binade of the speculated sum after each element
-    uint32_t serial;              // bit k: element k is serial
-    uint32_t csum, cnt;           // the lane's increment total and serial count
+template <int PT>  // elements per lane
+struct Lane {     // what a lane keeps in registers between steps
+    static constexpr int kPerThread = PT;
+    float v[PT];
+    uint32_t c[PT];       // increment of each non-serial element, in its run's units
+    int32_t e_after[PT];  // binade of the speculated sum after each element
+    uint32_t serial;      // bit k: element k is serial
+    uint32_t csum, cnt;   // the lane's increment total and serial count
 };
 
-__host__ __device__ inline void lane_load(const float* p, int n, int i0, Lane& L) {
-    if (i0 + kPerThread <= n) {
-        const float4 q = *reinterpret_cast<const float4*>(p + i0);
-        L.v[0] = q.x, L.v[1] = q.y, L.v[2] = q.z, L.v[3] = q.w;
+template <int PT>
+__host__ __device__ inline void lane_load(const float* p, int n, int i0, Lane<PT>& L) {
+    if (i0 + PT <= n) {
+#pragma unroll
+        for (int k = 0; k < PT; k += 4) {
+            const float4 q = *reinterpret_cast<const float4*>(p + i0 + k);
+            L.v[k] = q.x, L.v[k + 1] = q.y, L.v[k + 2] = q.z, L.v[k + 3] = q.w;
+        }
     } else {
 #pragma unroll
-        for (int k = 0; k < kPerThread; ++k) L.v[k] = i0 + k < n ? p[i0 + k] : 0.f;
+        for (int k = 0; k < PT; ++k) L.v[k] = i0 + k < n ? p[i0 + k] : 0.f;
     }
 }
 
-__host__ __device__ inline float lane_sum(const Lane& L) {
+template <int PT>
+__host__ __device__ inline float lane_sum(const Lane<PT>& L) {
     float d = L.v[0];
 #pragma unroll
-    for (int k = 1; k < kPerThread; ++k) d += L.v[k];
+    for (int k = 1; k < PT; ++k) d += L.v[k];
     return d;
 }
 
 // pre: speculated sum of everything before the lane's first element; next:
 // the same value as the following lane sees it (its `pre`)
-__host__ __device__ inline void lane_classify(Lane& L, int i0, int n, float pre, float next) {
+template <int PT>
+__host__ __device__ inline void lane_classify(Lane<PT>& L, int i0, int n, float pre, float next) {
+    constexpr int kPerThread = PT;
     float S[kPerThread + 1];
     S[0] = pre;
 #pragma unroll
@@ -109,10 +122,9 @@ __host__ __device__ inline void lane_classify(Lane& L, int i0, int n, float pre,
     S[kPerThread] = next;
     uint32_t serial = 0, csum = 0, cnt = 0;
 #pragma unroll
-    for (int k = 0; k < kPerThread; ++k) {
-        L.c[k] = 0;
+    for (int k = 0; k < kPerThread; ++k) {  // straight-line: no early exits
         L.e_after[k] = binade_f32(S[k + 1]);
-        if (i0 + k >= n) continue;
+        const bool in = i0 + k < n;
         const float v = L.v[k];
         const float hi = S[k + 1] * kMarginHi;
         const int e = binade_f32(S[k]);
@@ -122,13 +134,11 @@ __host__ __device__ inline void lane_classify(Lane& L, int i0, int n, float pre,
         const float f = P - m;
         const bool ser = binade_f32(S[k] * kMarginLo) != binade_f32(hi) || !(v >= 0.f) || !(v <= 3.0e38f) || !(hi <= 3.0e38f) ||
                          !(P < 67108864.f) || f == 0.5f;
-        if (ser) {
-            serial |= 1u << k;
-            ++cnt;
-        } else {
-            L.c[k] = uint32_t(m) + (f > 0.5f ? 1u : 0u);
-            csum += L.c[k];
-        }
+        const uint32_t ck = in && !ser ? uint32_t(m) + (f > 0.5f ? 1u : 0u) : 0u;
+        L.c[k] = ck;
+        csum += ck;
+        serial |= (in && ser ? 1u : 0u) << k;
+        cnt += in && ser ? 1u : 0u;
     }
     L.serial = serial;
     L.csum = csum;
@@ -138,22 +148,22 @@ __host__ __device__ inline void lane_classify(Lane& L, int i0, int n, float pre,
 // cx, r: increments and serial elements before the lane's first element.
 // Writes the table entries of the lane's serial elements, and the totals if
 // the lane holds element n-1.
-__host__ __device__ inline void lane_emit(const Lane& L, int i0, int n, uint32_t cx, uint32_t r, Shared& sm) {
+template <int PT>
+__host__ __device__ inline void lane_emit(const Lane<PT>& L, int i0, int n, uint32_t cx, uint32_t r, Shared& sm) {
+    constexpr int kPerThread = PT;
+    // straight-line: c[k] is 0 for serial and out-of-range elements, and
+    // serial bits are only set in range
 #pragma unroll
     for (int k = 0; k < kPerThread; ++k) {
-        const int i = i0 + k;
-        if (i >= n) break;
-        if ((L.serial >> k) & 1u) {
-            if (r < uint32_t(kMaxSerial)) {
-                sm.ser_idx[r] = i;
-                sm.ser_val[r] = L.v[k];
-                sm.ser_cx[r] = cx;
-                sm.ser_e[r] = L.e_after[k];
-            }
-            ++r;
-        } else {
-            cx += L.c[k];
+        const bool ser = (L.serial >> k) & 1u;
+        if (ser && r < uint32_t(kMaxSerial)) {
+            sm.ser_idx[r] = i0 + k;
+            sm.ser_val[r] = L.v[k];
+            sm.ser_cx[r] = cx;
+            sm.ser_e[r] = L.e_after[k];
         }
+        r += ser ? 1u : 0u;
+        cx += L.c[k];
     }
     if (i0 < n && n <= i0 + kPerThread) {
         sm.nser = int32_t(r);
@@ -193,21 +203,27 @@ __host__ __device__ inline Step walk_entry(const Shared& sm, int r, int n) {
     return st;
 }
 
-// the dependent chain is s -> s + a -> s + val; the checks only read it
-__host__ __device__ inline void walk_apply(float& s, bool& ok, const Step& st, bool serial) {
+// the dependent chain is s -> s + a -> s + val (a = 0 for an empty run, val =
+// 0 after the final run: adding +0 to s >= 0 leaves it unchanged); the checks
+// only read it
+__host__ __device__ inline void walk_apply(float& s, bool& ok, float a, float val, int32_t e, int32_t flags) {
     const float s0 = s;
-    s = s + st.a;
-    if (st.flags & 1) ok = ok && !(st.flags & 2) && s0 >= 0.f && binade_f32(s0) == st.e && binade_f32(s) == st.e;
-    if (serial) s = s + st.val;
+    const float s1 = s0 + a;
+    const bool good = !(flags & 2) && s0 >= 0.f && binade_f32(s0) == e && binade_f32(s1) == e;
+    ok = ok && (!(flags & 1) || good);
+    s = s1 + val;
 }
 
-// ---- the whole sum on the device: 1024 lanes, p in shared memory (16-byte
-// aligned), 0 <= n <= 4096 ---------------------------------------------------------
+// ---- the whole sum on the device: NT lanes (the whole workgroup), p in shared
+// memory (16-byte aligned), 0 <= n <= 4096 ---------------------------------------------
+template <int NT = kThreads>
 __device__ inline float sum_nonneg(const float* p, int n, Shared& sm) {
+    static_assert(NT == 256 || NT == 1024, "256 or 1024 lanes");
+    constexpr int kPerThread = kMaxN / NT, kWaves = NT / kWaveSize;
     if (n <= 0) return 0.f;
     const int tid = int(threadIdx.x), lane = tid & (kWaveSize - 1), w = tid / kWaveSize;
     const int i0 = tid * kPerThread;
-    Lane L;
+    Lane<kPerThread> L;
     lane_load(p, n, i0, L);
 
     // speculation: inclusive scan of lane sums inside the wave, then of the
@@ -265,14 +281,24 @@ __device__ inline float sum_nonneg(const float* p, int n, Shared& sm) {
             Step st{0.f, 0.f, 0, 0};
             if (r <= nser) st = walk_entry(sm, r, n);
             const int cnt = min(kWaveSize, nser + 1 - base);
-            for (int l = 0; l < cnt; ++l) {
-                Step q;
-                q.a = bits_f32(uint32_t(__builtin_amdgcn_readlane(int(f32_bits(st.a)), l)));
-                q.val = bits_f32(uint32_t(__builtin_amdgcn_readlane(int(f32_bits(st.val)), l)));
-                q.e = __builtin_amdgcn_readlane(st.e, l);
-                q.flags = __builtin_amdgcn_readlane(st.flags, l);
-                walk_apply(s, ok, q, base + l < nser);
+            const int ia = int(f32_bits(st.a)), iv = int(f32_bits(st.val));
+            int l = 0;
+            for (; l + 8 <= cnt; l += 8) {  // the step data of 8 steps first, then the chain
+                float a[8], v[8];
+                int32_t e[8], f[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    a[u] = bits_f32(uint32_t(__builtin_amdgcn_readlane(ia, l + u)));
+                    v[u] = bits_f32(uint32_t(__builtin_amdgcn_readlane(iv, l + u)));
+                    e[u] = __builtin_amdgcn_readlane(st.e, l + u);
+                    f[u] = __builtin_amdgcn_readlane(st.flags, l + u);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) walk_apply(s, ok, a[u], v[u], e[u], f[u]);
             }
+            for (; l < cnt; ++l)
+                walk_apply(s, ok, bits_f32(uint32_t(__builtin_amdgcn_readlane(ia, l))), bits_f32(uint32_t(__builtin_amdgcn_readlane(iv, l))),
+                           __builtin_amdgcn_readlane(st.e, l), __builtin_amdgcn_readlane(st.flags, l));
         }
         if (!ok) s = serial_loop(p, n);
         if (lane == 0) {
@@ -285,9 +311,11 @@ __device__ inline float sum_nonneg(const float* p, int n, Shared& sm) {
 }
 
 // ---- the same steps on the host, lane after lane, in the device's order -------------
+template <int NT = kThreads>
 inline float sum_nonneg_host(const float* p, int n, Shared& sm) {
+    constexpr int kThreads = NT, kPerThread = kMaxN / NT, kWaves = NT / kWaveSize;
     if (n <= 0) return 0.f;
-    static Lane L[kThreads];
+    static Lane<kPerThread> L[kThreads];
     static float d[kThreads], pre[kThreads], next[kThreads];
     static uint32_t c[kThreads], m[kThreads];
     for (int t = 0; t < kThreads; ++t) {
@@ -337,7 +365,10 @@ inline float sum_nonneg_host(const float* p, int n, Shared& sm) {
     const int nser = sm.nser;
     bool ok = nser <= kMaxSerial;
     float s = 0.f;
-    for (int r = 0; ok && r <= nser; ++r) walk_apply(s, ok, walk_entry(sm, r, n), r < nser);
+    for (int r = 0; ok && r <= nser; ++r) {
+        const Step st = walk_entry(sm, r, n);
+        walk_apply(s, ok, st.a, st.val, st.e, st.flags);
+    }
     if (!ok) s = serial_loop(p, n);
     sm.result = s;
     sm.fell_back = ok ? 0 : 1;

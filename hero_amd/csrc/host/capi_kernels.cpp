@@ -66,6 +66,75 @@ int hero_q8_0_gemv(const void* packed, const void* act, float* y, const float* r
     });
 }
 
+int hero_rmsnorm_q8_0_gemv(const void* packed, const float* x, const float* gamma, float eps, float* y, const float* residual, int64_t n, int64_t k, void* act_scratch, void* stream) {
+    return guard([&] {
+        check_q8_shape(n, k);
+        require(packed && x && gamma && y, "null pointer");
+        require(k <= 16384, "row width above 16384 is not supported");
+        require(aligned(packed, 16) && aligned(x, 16) && aligned(gamma, 16), "packed, x and gamma must be 16-byte aligned");
+        if (k == 4096) {
+            GemvInput in{};
+            in.mode = kInRmsNorm;
+            in.x = x;
+            in.gamma = gamma;
+            in.eps = eps;
+            launch_gemv_q8_in(packed, in, y, residual, n, k, residual ? kEpiResidual : kEpiStore, as_stream(stream));
+        } else {
+            require(act_scratch && aligned(act_scratch, 16), "act_scratch (16-byte aligned) is required when K != 4096");
+            launch_rmsnorm_quant(x, gamma, eps, nullptr, act_scratch, 1, k, as_stream(stream));
+            launch_gemv_q8(packed, act_scratch, y, residual, n, k, residual ? kEpiResidual : kEpiStore, as_stream(stream));
+        }
+        check_launch("hero_rmsnorm_q8_0_gemv");
+    });
+}
+
+int hero_swiglu_q8_0_gemv(const void* packed, const float* gate_up, float* y, const float* residual, int64_t n, int64_t k, void* act_scratch, void* stream) {
+    return guard([&] {
+        check_q8_shape(n, k);
+        require(packed && gate_up && y, "null pointer");
+        require(aligned(packed, 16) && aligned(gate_up, 16), "packed and gate_up must be 16-byte aligned");
+        if (gemv_streams(k)) {
+            GemvInput in{};
+            in.mode = kInSwiglu;
+            in.gate_up = gate_up;
+            launch_gemv_q8_in(packed, in, y, residual, n, k, residual ? kEpiResidual : kEpiStore, as_stream(stream));
+        } else {
+            require(act_scratch && aligned(act_scratch, 16), "act_scratch (16-byte aligned) is required when K is not 4096, 8192 or 12288");
+            launch_swiglu_quant(gate_up, act_scratch, 1, k, as_stream(stream));
+            launch_gemv_q8(packed, act_scratch, y, residual, n, k, residual ? kEpiResidual : kEpiStore, as_stream(stream));
+        }
+        check_launch("hero_swiglu_q8_0_gemv");
+    });
+}
+
+int hero_q8_0_pack_interleaved(const void* src, void* packed, int64_t n_total, int64_t k, int64_t row0, int64_t rows, int64_t interleave, void* stream) {
+    return guard([&] {
+        check_q8_shape(n_total, k);
+        require(src && packed, "null pointer");
+        require(aligned(packed, 16), "packed buffer must be 16-byte aligned");
+        require(interleave > 0 && rows > 0 && rows % interleave == 0, "rows must be a positive multiple of interleave");
+        require(row0 >= 0 && row0 + (rows / interleave - 1) * 2 * interleave + interleave <= n_total, "rows outside the packed matrix");
+        launch_pack_q8(src, packed, n_total, k, row0, rows, as_stream(stream), interleave);
+        check_launch("hero_q8_0_pack_interleaved");
+    });
+}
+
+int hero_rmsnorm_q8_0_gemv_swiglu(const void* packed, const float* x, const float* gamma, float eps, void* act_out, int64_t ff, int64_t k, void* stream) {
+    return guard([&] {
+        require(k == 4096, "K must be 4096");
+        require(ff > 0 && ff % 32 == 0 && 2 * ff <= (int64_t(1) << 31), "ff must be a positive multiple of 32");
+        require(packed && x && gamma && act_out, "null pointer");
+        require(aligned(packed, 16) && aligned(x, 16) && aligned(gamma, 16) && aligned(act_out, 16), "buffers must be 16-byte aligned");
+        GemvInput in{};
+        in.mode = kInRmsNorm;
+        in.x = x;
+        in.gamma = gamma;
+        in.eps = eps;
+        launch_gemv_q8_in(packed, in, static_cast<float*>(act_out), nullptr, 2 * ff, k, kEpiSwigluQuant, as_stream(stream));
+        check_launch("hero_rmsnorm_q8_0_gemv_swiglu");
+    });
+}
+
 int hero_q8_0_block_sums(const void* packed, const void* act, int32_t* out, int64_t n, int64_t k, void* stream) {
     return guard([&] {
         check_q8_shape(n, k);

@@ -94,7 +94,7 @@ struct Packer {
     hipStream_t stream;
     int64_t* counter;
     // copy one Q8_0 GGUF tensor [K, rows] into rows [row0, row0+rows) of a packed matrix
-    void put(const GgufFile& g, const std::string& name, DeviceBuffer& dst, int64_t n_total, int64_t K, int64_t row0, int64_t rows) {
+    void put(const GgufFile& g, const std::string& name, DeviceBuffer& dst, int64_t n_total, int64_t K, int64_t row0, int64_t rows, int64_t interleave = 0) {
         const GgufFile::Tensor& t = g.require(name);
         expect(t.dims.size() == 2 && int64_t(t.dims[0]) == K && int64_t(t.dims[1]) == rows, name + " has the wrong shape");
         expect(t.type == 8, name + " must be Q8_0");
@@ -104,7 +104,7 @@ struct Packer {
         }
         hip_check(hipStreamSynchronize(stream), "pack sync");
         hip_check(hipMemcpy(staging.get(), t.data, t.nbytes, hipMemcpyHostToDevice), "weight upload");
-        launch_pack_q8(staging.get(), dst.get(), n_total, K, row0, rows, stream);
+        launch_pack_q8(staging.get(), dst.get(), n_total, K, row0, rows, stream, interleave);
         check_launch("pack");
     }
     DeviceBuffer alloc(int64_t n, int64_t K) {
@@ -194,14 +194,20 @@ void Qwen35Model::load(const GgufFile& g) {
     final_norm_ = upload(host_vector(g, "output_norm.weight", c.D));
 
     const int64_t CC = c.conv_channels(), VW = c.v_width(), QW = c.q_width(), KW = c.kv_width();
+    ffn_fused_ = c.D == 4096 && c.FF % 32 == 0;
     for (int64_t l = 0; l < c.L; ++l) {
         LayerWeights L;
         L.recurrent = c.is_recurrent(l);
         L.mixer_norm = upload(host_vector(g, blk(l, "attn_norm.weight"), c.D));
         L.channel_norm = upload(host_vector(g, blk(l, "post_attention_norm.weight"), c.D));
         L.w_gate_up = pk.alloc(2 * c.FF, c.D);
-        pk.put(g, blk(l, "ffn_gate.weight"), L.w_gate_up, 2 * c.FF, c.D, 0, c.FF);
-        pk.put(g, blk(l, "ffn_up.weight"), L.w_gate_up, 2 * c.FF, c.D, c.FF, c.FF);
+        if (ffn_fused_) {  // [gate 0..31 | up 0..31 | gate 32..63 | ...]
+            pk.put(g, blk(l, "ffn_gate.weight"), L.w_gate_up, 2 * c.FF, c.D, 0, c.FF, 32);
+            pk.put(g, blk(l, "ffn_up.weight"), L.w_gate_up, 2 * c.FF, c.D, 32, c.FF, 32);
+        } else {
+            pk.put(g, blk(l, "ffn_gate.weight"), L.w_gate_up, 2 * c.FF, c.D, 0, c.FF);
+            pk.put(g, blk(l, "ffn_up.weight"), L.w_gate_up, 2 * c.FF, c.D, c.FF, c.FF);
+        }
         L.w_down = pk.alloc(c.D, c.FF);
         pk.put(g, blk(l, "ffn_down.weight"), L.w_down, c.D, c.FF, 0, c.D);
         if (L.recurrent) {
@@ -277,6 +283,7 @@ Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens) : m_(m), max
     step_ = DeviceBuffer(16);
     x_ = DeviceBuffer(size_t(c.D) * 4);
     h_ = DeviceBuffer(size_t(c.D) * 4);
+    gemv_scratch_ = DeviceBuffer(size_t(c.D) * 4);
     proj_ = DeviceBuffer(size_t(n_in_max) * 4);
     act_d_ = DeviceBuffer(size_t(act_q8_bytes(1, c.D)));
     act_mix_ = DeviceBuffer(size_t(act_q8_bytes(1, std::max(c.q_width(), c.v_width()))));
@@ -324,6 +331,50 @@ void Qwen35Model::State::reset() {
 }
 
 // ---- the step -------------------------------------------------------------------------
+namespace {
+
+// The three GEMV forms of a layer; each returns its algorithmic bytes (weights
+// and scales, inputs as read, outputs, residual reads).
+//  norm:   y = W quantize(RMSNorm(x)) (+ r), one launch when K == 4096
+//  swiglu: y = W quantize(silu(gate) up) (+ r), one launch when K streams
+//  act:    y = W act (+ r), act already quantized
+int64_t gemv_norm(const void* w, const float* x, const float* gamma, float eps, void* act_scratch, float* y, const float* r, int64_t N, int64_t K, hipStream_t s, int epi_swiglu = 0) {
+    const int epi = epi_swiglu ? kEpiSwigluQuant : r ? kEpiResidual : kEpiStore;
+    if (K == 4096) {
+        GemvInput in{};
+        in.mode = kInRmsNorm;
+        in.x = x;
+        in.gamma = gamma;
+        in.eps = eps;
+        launch_gemv_q8_in(w, in, y, r, N, K, epi, s);
+    } else {
+        launch_rmsnorm_quant(x, gamma, eps, nullptr, act_scratch, 1, K, s);
+        launch_gemv_q8(w, act_scratch, y, r, N, K, epi, s);
+    }
+    return packed_q8_bytes(N, K) + 2 * K * 4 + (epi_swiglu ? act_q8_bytes(1, N / 2) : N * 4) + (r ? N * 4 : 0);
+}
+
+int64_t gemv_swiglu(const void* w, const float* gate_up, void* act_scratch, float* y, const float* r, int64_t N, int64_t K, hipStream_t s) {
+    const int epi = r ? kEpiResidual : kEpiStore;
+    if (gemv_streams(K)) {
+        GemvInput in{};
+        in.mode = kInSwiglu;
+        in.gate_up = gate_up;
+        launch_gemv_q8_in(w, in, y, r, N, K, epi, s);
+    } else {
+        launch_swiglu_quant(gate_up, act_scratch, 1, K, s);
+        launch_gemv_q8(w, act_scratch, y, r, N, K, epi, s);
+    }
+    return packed_q8_bytes(N, K) + 2 * K * 4 + N * 4 + (r ? N * 4 : 0);
+}
+
+int64_t gemv_act(const void* w, const void* act, float* y, const float* r, int64_t N, int64_t K, hipStream_t s) {
+    launch_gemv_q8(w, act, y, r, N, K, r ? kEpiResidual : kEpiStore, s);
+    return packed_q8_bytes(N, K) + act_q8_bytes(1, K) + N * 4 + (r ? N * 4 : 0);
+}
+
+}  // namespace
+
 void Qwen35Model::enqueue_step(State& st, bool from_ids, bool with_head) const {
     const ModelConfig& c = c_;
     hipStream_t s = stream_;
@@ -334,8 +385,8 @@ void Qwen35Model::enqueue_step(State& st, bool from_ids, bool with_head) const {
     if (from_ids) launch_embed_q8(embedding_.get(), c.V, c.D, step + 1, 1, x, s);
     for (int64_t l = 0; l < c.L; ++l) {
         const LayerWeights& L = layers_[size_t(l)];
-        launch_rmsnorm_quant(x, L.mixer_norm.get<float>(), c.eps, nullptr, st.act_d_.get(), 1, c.D, s);
-        launch_gemv_q8(L.w_in.get(), st.act_d_.get(), proj, nullptr, L.n_in, c.D, kEpiStore, s);
+        // h = x + mix(rms(x)); x' = h + mlp(rms(h))  (nm/src/qwen35.hpp:318-327)
+        gemv_norm(L.w_in.get(), x, L.mixer_norm.get<float>(), c.eps, st.act_d_.get(), proj, nullptr, L.n_in, c.D, s);
         int64_t k_mix;
         if (L.recurrent) {
             GdnDecodeArgs a{};
@@ -389,15 +440,17 @@ void Qwen35Model::enqueue_step(State& st, bool from_ids, bool with_head) const {
             launch_attn_decode(a, s);
             k_mix = c.q_width();
         }
-        launch_gemv_q8(L.w_out.get(), st.act_mix_.get(), h, x, c.D, k_mix, kEpiResidual, s);
-        launch_rmsnorm_quant(h, L.channel_norm.get<float>(), c.eps, nullptr, st.act_d_.get(), 1, c.D, s);
-        launch_gemv_q8(L.w_gate_up.get(), st.act_d_.get(), st.gate_up_.get<float>(), nullptr, 2 * c.FF, c.D, kEpiStore, s);
-        launch_swiglu_quant(st.gate_up_.get<float>(), st.act_ff_.get(), 1, c.FF, s);
-        launch_gemv_q8(L.w_down.get(), st.act_ff_.get(), x, h, c.D, c.FF, kEpiResidual, s);
+        gemv_act(L.w_out.get(), st.act_mix_.get(), h, x, c.D, k_mix, s);
+        if (ffn_fused_) {
+            gemv_norm(L.w_gate_up.get(), h, L.channel_norm.get<float>(), c.eps, st.act_d_.get(), static_cast<float*>(st.act_ff_.get()), nullptr, 2 * c.FF, c.D, s, 1);
+            gemv_act(L.w_down.get(), st.act_ff_.get(), x, h, c.D, c.FF, s);
+        } else {
+            gemv_norm(L.w_gate_up.get(), h, L.channel_norm.get<float>(), c.eps, st.act_d_.get(), st.gate_up_.get<float>(), nullptr, 2 * c.FF, c.D, s);
+            gemv_swiglu(L.w_down.get(), st.gate_up_.get<float>(), st.act_ff_.get(), x, h, c.D, c.FF, s);
+        }
     }
     if (with_head) {
-        launch_rmsnorm_quant(x, final_norm_.get<float>(), c.eps, nullptr, st.act_d_.get(), 1, c.D, s);
-        launch_gemv_q8(c.tied ? embedding_.get() : output_.get(), st.act_d_.get(), st.logits_.get<float>(), nullptr, c.V, c.D, kEpiStore, s);
+        gemv_norm(c.tied ? embedding_.get() : output_.get(), x, final_norm_.get<float>(), c.eps, st.act_d_.get(), st.logits_.get<float>(), nullptr, c.V, c.D, s);
         launch_argmax(st.logits_.get<float>(), 1, c.V, step + 1, st.argmax_scratch_.get<uint64_t>(), s);
     }
     hipLaunchKernelGGL(advance_step_kernel, dim3(1), dim3(1), 0, s, step, st.out_ids_.get<int32_t>(), int32_t(with_head && from_ids));
@@ -483,20 +536,27 @@ double Qwen35Model::time_gemvs(State& st, int reps, int64_t* launches, int64_t* 
     const ModelConfig& c = c_;
     hipStream_t s = stream_;
     int64_t n_launch = 0, n_bytes = 0;
-    auto gemv = [&](const DeviceBuffer& w, const DeviceBuffer& act, float* y, const float* resid, int64_t N, int64_t K) {
-        launch_gemv_q8(w.get(), act.get(), y, resid, N, K, resid ? kEpiResidual : kEpiStore, s);
-        ++n_launch;
-        n_bytes += packed_q8_bytes(N, K) + act_q8_bytes(1, K) + N * 4 + (resid ? N * 4 : 0);
-    };
+    // the GEMVs exactly as a decode step launches them (fused input forms
+    // included), on scratch outputs: x and h are read, never written
+    float* x = st.x_.get<float>();
+    float* h = st.h_.get<float>();
+    float* y_d = st.gemv_scratch_.get<float>();
     auto one_step = [&] {
         for (const LayerWeights& L : layers_) {
             const int64_t k_mix = L.recurrent ? c.v_width() : c.q_width();
-            gemv(L.w_in, st.act_d_, st.proj_.get<float>(), nullptr, L.n_in, c.D);
-            gemv(L.w_out, st.act_mix_, st.h_.get<float>(), st.x_.get<float>(), c.D, k_mix);
-            gemv(L.w_gate_up, st.act_d_, st.gate_up_.get<float>(), nullptr, 2 * c.FF, c.D);
-            gemv(L.w_down, st.act_ff_, st.x_.get<float>(), st.h_.get<float>(), c.D, c.FF);
+            n_bytes += gemv_norm(L.w_in.get(), x, L.mixer_norm.get<float>(), c.eps, st.act_d_.get(), st.proj_.get<float>(), nullptr, L.n_in, c.D, s);
+            n_bytes += gemv_act(L.w_out.get(), st.act_mix_.get(), y_d, x, c.D, k_mix, s);
+            if (ffn_fused_) {
+                n_bytes += gemv_norm(L.w_gate_up.get(), h, L.channel_norm.get<float>(), c.eps, st.act_d_.get(), static_cast<float*>(st.act_ff_.get()), nullptr, 2 * c.FF, c.D, s, 1);
+                n_bytes += gemv_act(L.w_down.get(), st.act_ff_.get(), y_d, h, c.D, c.FF, s);
+            } else {
+                n_bytes += gemv_norm(L.w_gate_up.get(), h, L.channel_norm.get<float>(), c.eps, st.act_d_.get(), st.gate_up_.get<float>(), nullptr, 2 * c.FF, c.D, s);
+                n_bytes += gemv_swiglu(L.w_down.get(), st.gate_up_.get<float>(), st.act_ff_.get(), y_d, h, c.D, c.FF, s);
+            }
+            n_launch += 4;
         }
-        gemv(c.tied ? embedding_ : output_, st.act_d_, st.logits_.get<float>(), nullptr, c.V, c.D);
+        n_bytes += gemv_norm(c.tied ? embedding_.get() : output_.get(), x, final_norm_.get<float>(), c.eps, st.act_d_.get(), st.logits_.get<float>(), nullptr, c.V, c.D, s);
+        n_launch += 1;
     };
     one_step();  // warm the instruction cache and the launch path
     hip_check(hipStreamSynchronize(s), "gemv warmup");

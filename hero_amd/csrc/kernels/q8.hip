@@ -18,6 +18,7 @@
 // is a sequential chain per row, so y is bit-identical to the reference.
 #include "hero/device.hpp"
 #include "hero/kernels.hpp"
+#include "hero/seqsum.hpp"
 
 namespace hero {
 
@@ -46,28 +47,32 @@ void launch_quantize_act(const float* x, void* act, int64_t M, int64_t K, hipStr
 }
 
 // ---------------------------------------------------------------------------
-// weight packing: GGUF Q8_0 blocks [N][K/32] x 34 B -> planar, at row offset
+// weight packing: GGUF Q8_0 blocks [rows][K/32] x 34 B -> planar. Source row r
+// lands on row row0 + r, or, with interleave il > 0, on row
+// row0 + (r / il) * 2 il + r % il (two tensors sharing a matrix in alternating
+// il-row chunks).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void pack_q8_kernel(const uint8_t* __restrict__ src, int8_t* __restrict__ qs, uint16_t* __restrict__ d, int64_t blocks, int64_t row_blocks, int64_t row0, int64_t Npad) {
+__global__ __launch_bounds__(256) void pack_q8_kernel(const uint8_t* __restrict__ src, int8_t* __restrict__ qs, uint16_t* __restrict__ d, int64_t blocks, int64_t row_blocks, int64_t row0, int64_t Npad, int64_t il) {
     const int64_t blk = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (blk >= blocks) return;
     const uint8_t* b = src + blk * 34;
-    const int64_t dst_blk = row0 * row_blocks + blk;
-    const int64_t row = dst_blk / row_blocks, col = dst_blk - row * row_blocks;
+    const int64_t r = blk / row_blocks, col = blk - r * row_blocks;
+    const int64_t row = row0 + (il > 0 ? (r / il) * 2 * il + r % il : r);
     d[col * Npad + row] = uint16_t(b[0] | (b[1] << 8));
     int w[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) w[j] = int(b[2 + 4 * j]) | (int(b[3 + 4 * j]) << 8) | (int(b[4 + 4 * j]) << 16) | (int(b[5 + 4 * j]) << 24);
-    int4* dst = reinterpret_cast<int4*>(qs + dst_blk * 32);
+    int4* dst = reinterpret_cast<int4*>(qs + (row * row_blocks + col) * 32);
     dst[0] = make_int4(w[0], w[1], w[2], w[3]);
     dst[1] = make_int4(w[4], w[5], w[6], w[7]);
 }
 
-void launch_pack_q8(const void* gguf_blocks, void* packed, int64_t N_total, int64_t K, int64_t row0, int64_t rows, hipStream_t s) {
+void launch_pack_q8(const void* gguf_blocks, void* packed, int64_t N_total, int64_t K, int64_t row0, int64_t rows, hipStream_t s, int64_t interleave) {
     int8_t* qs = static_cast<int8_t*>(packed);
     uint16_t* d = reinterpret_cast<uint16_t*>(qs + N_total * K);
     const int64_t blocks = rows * (K / 32);
-    hipLaunchKernelGGL(pack_q8_kernel, dim3(unsigned((blocks + 255) / 256)), dim3(256), 0, s, static_cast<const uint8_t*>(gguf_blocks), qs, d, blocks, K / 32, row0, packed_rows_pad(N_total));
+    hipLaunchKernelGGL(pack_q8_kernel, dim3(unsigned((blocks + 255) / 256)), dim3(256), 0, s, static_cast<const uint8_t*>(gguf_blocks), qs, d, blocks, K / 32, row0,
+                       packed_rows_pad(N_total), interleave);
 }
 
 // ---------------------------------------------------------------------------
@@ -87,29 +92,20 @@ void launch_pack_q8(const void* gguf_blocks, void* packed, int64_t N_total, int6
 // ---------------------------------------------------------------------------
 constexpr int kStreamRB = 8;  // rows per sub-batch
 
-__device__ __forceinline__ int lane_pair_value(int v) {  // the value of lane ^ 1
-    return __builtin_amdgcn_update_dpp(0, v, 0xB1 /* quad_perm [1,0,3,2] */, 0xF, 0xF, false);
-}
-
-template <int CPL, int D, int EPI>
-__global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int N, int Npad, int TR) {
+template <int CPL, int D, int EPI, int XM>
+__global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, GemvInput in, float* __restrict__ y, const float* __restrict__ resid, int N, int Npad, int TR) {
     constexpr int K = 4096 * CPL, nb = K / 32, ts = nb + 4;  // ts: padded term row (conflict-free 16-byte reads)
-    extern __shared__ __align__(16) float terms[];          // [TR][ts]
+    // row ranges in whole units: 8-row groups, or for the SwiGLU epilogue
+    // 64-row groups of [32 gate rows | 32 up rows]
+    constexpr int UR = EPI == kEpiSwigluQuant ? 64 : 8;
+    extern __shared__ __align__(16) float terms[];          // [TR][ts]; the prologue's squares before that
     const int tid = threadIdx.x;
-    const int G = gridDim.x, U = Npad / 8;
-    const int r_begin = 8 * int((int64_t(U) * blockIdx.x) / G);
-    const int r_end = min(N, 8 * int((int64_t(U) * (blockIdx.x + 1)) / G));
+    const int G = gridDim.x, U = Npad / UR;
+    const int r_begin = UR * int((int64_t(U) * blockIdx.x) / G);
+    const int r_end = min(N, UR * int((int64_t(U) * (blockIdx.x + 1)) / G));
     const int nsub = r_end > r_begin ? (r_end - r_begin + kStreamRB - 1) / kStreamRB : 0;
     const bool even = (tid & 1) == 0;
 
-    int4 xv[CPL];
-    float dx[CPL];
-#pragma unroll
-    for (int m = 0; m < CPL; ++m) {
-        const int c = tid + 256 * m;
-        xv[m] = reinterpret_cast<const int4*>(xq)[c];
-        dx[m] = xd[c >> 1];
-    }
     int4 ring[D][kStreamRB][CPL];
     int4 sring[D][CPL];  // even lanes: scales of the sub-batch's 8 rows for each of the lane's blocks
     auto load = [&](int j, int4 (&dst)[kStreamRB][CPL], int4 (&sdst)[CPL]) {
@@ -127,6 +123,65 @@ __global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __res
     for (int s = 0; s < D; ++s)
         if (s < nsub) load(s, ring[s], sring[s]);
 
+    // The lane's x chunks (tid + 256m) as Q8_0, while the first weights load.
+    int4 xv[CPL];
+    float dx[CPL];
+    if constexpr (XM == kInAct) {
+#pragma unroll
+        for (int m = 0; m < CPL; ++m) {
+            const int c = tid + 256 * m;
+            xv[m] = reinterpret_cast<const int4*>(in.xq)[c];
+            dx[m] = in.xd[c >> 1];
+        }
+    } else if constexpr (XM == kInRmsNorm) {
+        // RMSNorm (nm/src/components.hpp:176-181) of the whole row, then the
+        // reference's quantize_row_q8_0: the sum of squares is the exact
+        // sequential sum (hero/seqsum.hpp), lane t holding elements 16t..16t+15
+        static_assert(CPL == 1, "RMSNorm input needs K == 4096");
+        __shared__ seqsum::Shared sm;
+        float* sq = terms;
+        float xr[16];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 a = reinterpret_cast<const float4*>(in.x)[4 * tid + k];
+            xr[4 * k] = a.x, xr[4 * k + 1] = a.y, xr[4 * k + 2] = a.z, xr[4 * k + 3] = a.w;
+        }
+#pragma unroll
+        for (int k = 0; k < 16; k += 4) reinterpret_cast<float4*>(sq)[(16 * tid + k) / 4] = make_float4(xr[k] * xr[k], xr[k + 1] * xr[k + 1], xr[k + 2] * xr[k + 2], xr[k + 3] * xr[k + 3]);
+        __syncthreads();
+        const float ss = seqsum::sum_nonneg<256>(sq, K, sm);  // ends with a barrier
+        const float inv = 1.f / sqrtf(ss / float(K) + in.eps);
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 g = reinterpret_cast<const float4*>(in.gamma)[4 * tid + k];
+            v[4 * k] = g.x * xr[4 * k] * inv, v[4 * k + 1] = g.y * xr[4 * k + 1] * inv;
+            v[4 * k + 2] = g.z * xr[4 * k + 2] * inv, v[4 * k + 3] = g.w * xr[4 * k + 3] * inv;
+        }
+        uint16_t dh;
+        xv[0] = quantize16_in_pair(v, &dh);
+        dx[0] = half_bits_to_f32(dh);
+    } else {
+        // SwiGLU (nm/src/components.hpp:300-304): silu(gate) * up over the row
+        // [gate K | up K], then quantize_row_q8_0
+#pragma unroll
+        for (int m = 0; m < CPL; ++m) {
+            const int c = tid + 256 * m;
+            const float4* g4 = reinterpret_cast<const float4*>(in.gate_up) + 4 * c;
+            const float4* u4 = reinterpret_cast<const float4*>(in.gate_up + K) + 4 * c;
+            float v[16];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 g = g4[k], u = u4[k];
+                v[4 * k] = silu_f32(g.x) * u.x, v[4 * k + 1] = silu_f32(g.y) * u.y;
+                v[4 * k + 2] = silu_f32(g.z) * u.z, v[4 * k + 3] = silu_f32(g.w) * u.w;
+            }
+            uint16_t dh;
+            xv[m] = quantize16_in_pair(v, &dh);
+            dx[m] = half_bits_to_f32(dh);
+        }
+    }
+
     int chain_row0 = r_begin;  // first row of the pending chain pass
     for (int base = 0; base < nsub; base += D) {
 #pragma unroll
@@ -140,7 +195,7 @@ __global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __res
 #pragma unroll
                     for (int m = 0; m < CPL; ++m) {
                         int v = dot16_i8(ring[s][r][m], xv[m], 0);
-                        v += lane_pair_value(v);  // the block's other 16 bytes (exact)
+                        v += pair_swap_i32(v);  // the block's other 16 bytes (exact)
                         if (even && rb + r < r_end) {
                             const int4 sc = sring[s][m];
                             const uint32_t two = uint32_t(pair == 0 ? sc.x : pair == 1 ? sc.y : pair == 2 ? sc.z : sc.w);
@@ -177,8 +232,26 @@ __global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __res
                         const int64_t o = chain_row0 + tid;
                         if constexpr (EPI == kEpiResidual)
                             y[o] = resid[o] + acc;  // h = x + m (nm/src/qwen35.hpp:321)
-                        else
+                        else if constexpr (EPI == kEpiStore)
                             y[o] = acc;
+                        else {
+                            // rows chain_row0 .. +63 are 32 gate rows then the 32 up rows of
+                            // the same FF indices: g = silu(gate) * up
+                            // (nm/src/components.hpp:300-304), then quantize_row_q8_0 of the
+                            // block, written as the down projection's input
+                            const float up = __shfl_down(acc, 32, 64);
+                            if (tid < 32) {
+                                const float v = silu_f32(acc) * up;
+                                float amax = fabsf(v);
+                                for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+                                const float d = amax / 127.f;
+                                const float id = d != 0.f ? 1.f / d : 0.f;
+                                const int64_t blk = chain_row0 / 64;
+                                int8_t* qs = reinterpret_cast<int8_t*>(y);
+                                qs[blk * 32 + tid] = int8_t(int(roundf(v * id)));
+                                if (tid == 0) reinterpret_cast<float*>(qs + N / 2)[blk] = half_bits_to_f32(fp32_to_fp16_ref(d));
+                            }
+                        }
                     }
                     __syncthreads();
                     chain_row0 += rows;
@@ -275,12 +348,30 @@ int device_cus() {
     return cached[dev];
 }
 
-template <int CPL, int D>
-void stream_dispatch(int epi, const int8_t* wq, const uint16_t* wd, const int8_t* xq, const float* xd, float* y, const float* resid, int N, int Npad, int G, int TR, size_t smem, hipStream_t s) {
+template <int CPL, int D, int XM>
+void stream_dispatch(int epi, const int8_t* wq, const uint16_t* wd, const GemvInput& in, float* y, const float* resid, int N, int Npad, int G, int TR, size_t smem, hipStream_t s) {
     if (epi == kEpiResidual)
-        hipLaunchKernelGGL((gemv_q8_stream_kernel<CPL, D, kEpiResidual>), dim3(unsigned(G)), dim3(256), smem, s, wq, wd, xq, xd, y, resid, N, Npad, TR);
+        hipLaunchKernelGGL((gemv_q8_stream_kernel<CPL, D, kEpiResidual, XM>), dim3(unsigned(G)), dim3(256), smem, s, wq, wd, in, y, resid, N, Npad, TR);
+    else if constexpr (CPL == 1)
+        if (epi == kEpiSwigluQuant)
+            hipLaunchKernelGGL((gemv_q8_stream_kernel<CPL, D, kEpiSwigluQuant, XM>), dim3(unsigned(G)), dim3(256), smem, s, wq, wd, in, y, resid, N, Npad, TR);
+        else
+            hipLaunchKernelGGL((gemv_q8_stream_kernel<CPL, D, kEpiStore, XM>), dim3(unsigned(G)), dim3(256), smem, s, wq, wd, in, y, resid, N, Npad, TR);
     else
-        hipLaunchKernelGGL((gemv_q8_stream_kernel<CPL, D, kEpiStore>), dim3(unsigned(G)), dim3(256), smem, s, wq, wd, xq, xd, y, resid, N, Npad, TR);
+        hipLaunchKernelGGL((gemv_q8_stream_kernel<CPL, D, kEpiStore, XM>), dim3(unsigned(G)), dim3(256), smem, s, wq, wd, in, y, resid, N, Npad, TR);
+}
+
+template <int CPL, int D>
+void stream_dispatch_in(int epi, const int8_t* wq, const uint16_t* wd, const GemvInput& in, float* y, const float* resid, int N, int Npad, int G, int TR, size_t smem, hipStream_t s) {
+    if (in.mode == kInSwiglu)
+        stream_dispatch<CPL, D, kInSwiglu>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
+    else if constexpr (CPL == 1)
+        if (in.mode == kInRmsNorm)
+            stream_dispatch<CPL, D, kInRmsNorm>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
+        else
+            stream_dispatch<CPL, D, kInAct>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
+    else
+        stream_dispatch<CPL, D, kInAct>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
 }
 
 template <int IPT>
@@ -294,28 +385,44 @@ void gemv_dispatch_epi(int epi, const int8_t* wq, const uint16_t* wd, const int8
 
 }  // namespace
 
-void launch_gemv_q8(const void* packed, const void* act, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s) {
+bool gemv_streams(int64_t K) { return K % 4096 == 0 && K / 4096 <= 3; }
+
+void launch_gemv_q8_in(const void* packed, const GemvInput& in, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s) {
     const int8_t* wq = static_cast<const int8_t*>(packed);
     const uint16_t* wd = reinterpret_cast<const uint16_t*>(wq + N * K);
+    const int Npad = int(packed_rows_pad(N));
+    // one workgroup per CU, two for the tall matrices; row ranges in whole
+    // 8-row groups (64-row groups for the SwiGLU epilogue: one chain pass each)
+    const int cus = device_cus();
+    const int64_t unit = epi == kEpiSwigluQuant ? 64 : 8;
+    const int G = int(std::min<int64_t>(N >= 16384 ? 2 * cus : cus, Npad / unit));
+    const int64_t rows_per = (Npad / unit + G - 1) / G * unit;
+    const int nb = int(K / 32);
+    // rows per chain pass: at most 64 (one wave) and 64 KB of terms
+    const int64_t TR = epi == kEpiSwigluQuant ? 64 : std::min<int64_t>({64, rows_per, (65536 / ((nb + 4) * 4)) / 8 * 8});
+    size_t smem = size_t(TR) * (nb + 4) * 4;
+    if (in.mode == kInRmsNorm) smem = std::max(smem, size_t(K) * 4);  // the squares
+    switch (K / 4096) {
+        case 1: stream_dispatch_in<1, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+        case 2: stream_dispatch_in<2, 1>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+        default: stream_dispatch_in<3, 1>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+    }
+}
+
+void launch_gemv_q8(const void* packed, const void* act, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s) {
     const int8_t* xq = static_cast<const int8_t*>(act);
     const float* xd = reinterpret_cast<const float*>(xq + K);
-    const int Npad = int(packed_rows_pad(N));
-    if (K % 4096 == 0 && K / 4096 <= 3) {
-        // one workgroup per CU, two for the tall matrices; row ranges in whole 8-row groups
-        const int cus = device_cus();
-        const int G = std::min<int64_t>(N >= 16384 ? 2 * cus : cus, Npad / 8);
-        const int64_t rows_per = (Npad / 8 + G - 1) / G * 8;
-        const int nb = int(K / 32);
-        // rows per chain pass: at most 64 (one wave) and 64 KB of terms
-        int64_t TR = std::min<int64_t>({64, rows_per, (65536 / ((nb + 4) * 4)) / 8 * 8});
-        const size_t smem = size_t(TR) * (nb + 4) * 4;
-        switch (K / 4096) {
-            case 1: stream_dispatch<1, 2>(epi, wq, wd, xq, xd, y, resid, int(N), Npad, G, int(TR), smem, s); break;
-            case 2: stream_dispatch<2, 1>(epi, wq, wd, xq, xd, y, resid, int(N), Npad, G, int(TR), smem, s); break;
-            default: stream_dispatch<3, 1>(epi, wq, wd, xq, xd, y, resid, int(N), Npad, G, int(TR), smem, s); break;
-        }
+    if (gemv_streams(K)) {
+        GemvInput in{};
+        in.mode = kInAct;
+        in.xq = xq;
+        in.xd = xd;
+        launch_gemv_q8_in(packed, in, y, resid, N, K, epi, s);
         return;
     }
+    const int8_t* wq = static_cast<const int8_t*>(packed);
+    const uint16_t* wd = reinterpret_cast<const uint16_t*>(wq + N * K);
+    const int Npad = int(packed_rows_pad(N));
     const int64_t cpr = K / 16;
     const int R = int(std::min<int64_t>(64, std::max<int64_t>(1, (8 * 256) / cpr)));  // ~8 chunk loads in flight per lane
     const int nb = int(K / 32);

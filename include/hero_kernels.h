@@ -58,6 +58,33 @@ int hero_q8_0_quantize(const float* x, void* act, int64_t m, int64_t k, void* st
  * nm/src/qwen35.hpp:321,326). */
 int hero_q8_0_gemv(const void* packed, const void* act, float* y, const float* residual, int64_t n, int64_t k, void* stream);
 
+/* y = W * quantize(RMSNorm(x)) (+ residual): RMSNorm
+ * (nm/src/components.hpp:176-181), quantize_row_q8_0 and Weight::matvec
+ * (nm/src/quant_i8.hpp:70-80,352-383) in one launch when K == 4096, the norm
+ * formed in the GEMV's prologue while its first weights load; otherwise as
+ * two launches through `act_scratch` (hero_q8_0_act_bytes(1, K) bytes).
+ * x, gamma: [K] fp32. Bit-exact. */
+int hero_rmsnorm_q8_0_gemv(const void* packed, const float* x, const float* gamma, float eps, float* y, const float* residual, int64_t n, int64_t k, void* act_scratch, void* stream);
+
+/* y = W * quantize(silu(gate) * up) (+ residual): the SwiGLU of
+ * nm/src/components.hpp:300-304 followed by the down projection, in one
+ * launch when K (= FF) is 4096, 8192 or 12288, else through `act_scratch`.
+ * gate_up: [gate K | up K] fp32. Bit-exact. */
+int hero_swiglu_q8_0_gemv(const void* packed, const float* gate_up, float* y, const float* residual, int64_t n, int64_t k, void* act_scratch, void* stream);
+
+/* Pack two [rows][K] GGUF Q8_0 tensors into one matrix in alternating
+ * `interleave`-row chunks: source row r lands on row
+ * row0 + (r / interleave) * 2 * interleave + r % interleave. Used for the
+ * SwiGLU gate (row0 = 0) and up (row0 = interleave) projections, interleave 32. */
+int hero_q8_0_pack_interleaved(const void* gguf_blocks, void* packed, int64_t n_total, int64_t k, int64_t row0, int64_t rows, int64_t interleave, void* stream);
+
+/* RMSNorm, the gate and up projections and SwiGLU in one launch: act_out =
+ * quantize(silu(W_gate x') * (W_up x')), x' = quantize(RMSNorm(x)), i.e.
+ * nm/src/components.hpp:176-181 and :300-304 up to the down projection's
+ * input. `packed` is [2*ff][k] from hero_q8_0_pack_interleaved with
+ * interleave 32; k == 4096; act_out: hero_q8_0_act_bytes(1, ff). Bit-exact. */
+int hero_rmsnorm_q8_0_gemv_swiglu(const void* packed, const float* x, const float* gamma, float eps, void* act_out, int64_t ff, int64_t k, void* stream);
+
 /* Exact int32 block dot products out[N][K/32] of one activation row: the
  * `sumi` of nm/src/quant_i8.hpp:94-95, exported for parity checks. */
 int hero_q8_0_block_sums(const void* packed, const void* act, int32_t* out, int64_t n, int64_t k, void* stream);

@@ -117,6 +117,69 @@ def test_gemv_matches_oracle_bitwise(lib, n, k):
     assert np.array_equal(bits(host(y, np.float32)), bits(r + expect))
 
 
+@pytest.mark.parametrize("n,k", [(4096, 4096), (16448, 4096), (33, 4096), (1000, 1024)])
+def test_rmsnorm_gemv_matches_oracle_bitwise(lib, n, k):
+    """RMSNorm + quantize + matvec; K == 4096 runs as one launch with the norm
+    in the GEMV prologue, other K through the act scratch."""
+    rng = np.random.default_rng(n + 3 * k)
+    w = oracle.quantize_q8_0((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    packed = pack_weight(lib, w, n, k)
+    g = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    gd = dev(g)
+    scratch = empty(lib.hero_q8_0_act_bytes(1, k))
+    y = empty(n * 4)
+    rows = [rng.standard_normal(k) * 3] + ([_hard_rows(k)[i] for i in (1, 5, 6, 8, 9)] if k == 4096 else [])
+    for i, row in enumerate(rows):
+        x = np.asarray(row, np.float32)
+        xd = dev(x)
+        r = rng.standard_normal(n).astype(np.float32)
+        rd = dev(r)
+        check(lib.hero_rmsnorm_q8_0_gemv(ptr(packed), ptr(xd), ptr(gd), np.float32(1e-6), ptr(y), ptr(rd), n, k, ptr(scratch), stream()))
+        expect = r + oracle.matvec(w, n, k, oracle.rmsnorm(x[None, :], g)[0])
+        assert np.array_equal(bits(host(y, np.float32)), bits(expect)), f"row {i}"
+
+
+@pytest.mark.parametrize("n,k", [(4096, 12288), (1003, 4096), (64, 8192), (1024, 2816)])
+def test_swiglu_gemv_matches_oracle_bitwise(lib, n, k):
+    """silu(gate) * up + quantize + matvec (the down projection)."""
+    rng = np.random.default_rng(n + 5 * k)
+    w = oracle.quantize_q8_0((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    packed = pack_weight(lib, w, n, k)
+    gu = (rng.standard_normal(2 * k) * 1.5).astype(np.float32)
+    gud = dev(gu)
+    scratch = empty(lib.hero_q8_0_act_bytes(1, k))
+    y = empty(n * 4)
+    check(lib.hero_swiglu_q8_0_gemv(ptr(packed), ptr(gud), ptr(y), None, n, k, ptr(scratch), stream()))
+    expect = oracle.matvec(w, n, k, oracle.silu(gu[:k]) * gu[k:])
+    assert np.array_equal(bits(host(y, np.float32)), bits(expect))
+
+
+@pytest.mark.parametrize("ff", [12288, 96])
+def test_rmsnorm_gate_up_swiglu_matches_oracle_bytes(lib, ff):
+    """RMSNorm -> [gate|up] GEMV -> silu(gate)*up -> quantize in one launch
+    (gate and up packed in alternating 32-row chunks) against the oracle's
+    separate steps, byte for byte."""
+    k = 4096
+    rng = np.random.default_rng(ff)
+    wg = oracle.quantize_q8_0((rng.standard_normal((ff, k)) * 0.02).astype(np.float32))
+    wu = oracle.quantize_q8_0((rng.standard_normal((ff, k)) * 0.02).astype(np.float32))
+    packed = empty(lib.hero_q8_0_packed_bytes(2 * ff, k))
+    srcg, srcu = dev(wg), dev(wu)
+    check(lib.hero_q8_0_pack_interleaved(ptr(srcg), ptr(packed), 2 * ff, k, 0, ff, 32, stream()))
+    check(lib.hero_q8_0_pack_interleaved(ptr(srcu), ptr(packed), 2 * ff, k, 32, ff, 32, stream()))
+    x = (rng.standard_normal(k) * 2).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    xd, gd = dev(x), dev(g)
+    act = empty(lib.hero_q8_0_act_bytes(1, ff))
+    check(lib.hero_rmsnorm_q8_0_gemv_swiglu(ptr(packed), ptr(xd), ptr(gd), np.float32(1e-6), ptr(act), ff, k, stream()))
+    xn = oracle.rmsnorm(x[None, :], g)[0]
+    gate = oracle.matvec(wg, ff, k, xn)
+    up = oracle.matvec(wu, ff, k, xn)
+    want = oracle.quantize_row_q8_0(oracle.silu(gate) * up)
+    got = act_to_blocks(host(act, np.uint8), 1, ff)[0]
+    assert got.tobytes() == want.tobytes()
+
+
 def test_block_sums_are_exact(lib):
     n, k = 257 * 2, 4096
     rng = np.random.default_rng(3)

@@ -135,3 +135,35 @@ def test_context_exhaustion_is_reported_and_clears_state(model):
         model.forward(state, ids=[model.V])  # bad id
     with pytest.raises(hero_amd.ContextExhausted):
         model.decode_greedy(state, 1, 2)
+
+
+def test_d4096_model_matches_oracle_bitwise():
+    """A 4-layer hybrid at the ~8B model's widths (d_model 4096, 32 q / 8 kv
+    heads, 32 delta-net heads, SwiGLU 12288), so the decode step takes the
+    fused forms: RMSNorm in the in-projection and gate/up GEMV prologues,
+    SwiGLU in the down projection's, the final norm in the LM head's. Prefill,
+    then greedy decode, against the oracle: identical ids, bit-identical
+    logits."""
+    import oracle
+
+    shape = hero_amd.HybridShape(vocab=32000, d_model=4096, layers=4, ffn=12288, q_heads=32, kv_heads=8, head_dim=128,
+                                 key_heads=32, value_heads=32)
+    image = hero_amd.synthetic_gguf_image(shape, seed=99, ctx=256)
+    rng = np.random.default_rng(99)
+    prompt = rng.integers(0, shape.vocab, 8).astype(np.int32)
+    steps = 8
+    ref = oracle.Model(image=image)
+    ref_ids, ref_last, _, _ = ref.greedy(prompt, steps)
+    ref.close()
+    m = hero_amd.Qwen35Model.open_image(image)
+    try:
+        state = m.new_state(64)
+        lg = m.forward(state, ids=prompt)
+        ids = [lg.argmax()]
+        for _ in range(steps):
+            lg = m.forward(state, ids=[ids[-1]])
+            ids.append(lg.argmax())
+        assert ids == [int(v) for v in ref_ids]
+        same_bits(lg.values, ref_last)
+    finally:
+        m.close()

@@ -119,13 +119,13 @@ __global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __res
         for (int m = 0; m < CPL; ++m)  // rb is a multiple of 8 and rb + 8 <= Npad
             sdst[m] = even ? *reinterpret_cast<const int4*>(wd + int64_t((tid + 256 * m) >> 1) * Npad + rb) : make_int4(0, 0, 0, 0);
     };
-#pragma unroll
-    for (int s = 0; s < D; ++s)
-        if (s < nsub) load(s, ring[s], sring[s]);
-
-    // The lane's x chunks (tid + 256m) as Q8_0, while the first weights load.
+    // The lane's x chunks (tid + 256m) as Q8_0. Their global reads are issued
+    // before the weight ring's: loads retire in order, so a read issued after
+    // the ring would wait for every weight in flight.
     int4 xv[CPL];
     float dx[CPL];
+    float xr[16], gr[16];                       // kInRmsNorm: the lane's 16 inputs and weights
+    float4 gv[CPL][4], uv[CPL][4];              // kInSwiglu: the lane's gate and up values
     if constexpr (XM == kInAct) {
 #pragma unroll
         for (int m = 0; m < CPL; ++m) {
@@ -134,18 +134,35 @@ __global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __res
             dx[m] = in.xd[c >> 1];
         }
     } else if constexpr (XM == kInRmsNorm) {
-        // RMSNorm (nm/src/components.hpp:176-181) of the whole row, then the
-        // reference's quantize_row_q8_0: the sum of squares is the exact
-        // sequential sum (hero/seqsum.hpp), lane t holding elements 16t..16t+15
         static_assert(CPL == 1, "RMSNorm input needs K == 4096");
-        __shared__ seqsum::Shared sm;
-        float* sq = terms;
-        float xr[16];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const float4 a = reinterpret_cast<const float4*>(in.x)[4 * tid + k];
+            const float4 g = reinterpret_cast<const float4*>(in.gamma)[4 * tid + k];
             xr[4 * k] = a.x, xr[4 * k + 1] = a.y, xr[4 * k + 2] = a.z, xr[4 * k + 3] = a.w;
+            gr[4 * k] = g.x, gr[4 * k + 1] = g.y, gr[4 * k + 2] = g.z, gr[4 * k + 3] = g.w;
         }
+    } else {
+#pragma unroll
+        for (int m = 0; m < CPL; ++m) {
+            const int c = tid + 256 * m;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                gv[m][k] = reinterpret_cast<const float4*>(in.gate_up)[4 * c + k];
+                uv[m][k] = reinterpret_cast<const float4*>(in.gate_up + K)[4 * c + k];
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < D; ++s)
+        if (s < nsub) load(s, ring[s], sring[s]);
+
+    if constexpr (XM == kInRmsNorm) {
+        // RMSNorm (nm/src/components.hpp:176-181) of the whole row, then the
+        // reference's quantize_row_q8_0: the sum of squares is the exact
+        // sequential sum (hero/seqsum.hpp), lane t holding elements 16t..16t+15
+        __shared__ seqsum::Shared sm;
+        float* sq = terms;
 #pragma unroll
         for (int k = 0; k < 16; k += 4) reinterpret_cast<float4*>(sq)[(16 * tid + k) / 4] = make_float4(xr[k] * xr[k], xr[k + 1] * xr[k + 1], xr[k + 2] * xr[k + 2], xr[k + 3] * xr[k + 3]);
         __syncthreads();
@@ -153,26 +170,19 @@ __global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __res
         const float inv = 1.f / sqrtf(ss / float(K) + in.eps);
         float v[16];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float4 g = reinterpret_cast<const float4*>(in.gamma)[4 * tid + k];
-            v[4 * k] = g.x * xr[4 * k] * inv, v[4 * k + 1] = g.y * xr[4 * k + 1] * inv;
-            v[4 * k + 2] = g.z * xr[4 * k + 2] * inv, v[4 * k + 3] = g.w * xr[4 * k + 3] * inv;
-        }
+        for (int k = 0; k < 16; ++k) v[k] = gr[k] * xr[k] * inv;
         uint16_t dh;
         xv[0] = quantize16_in_pair(v, &dh);
         dx[0] = half_bits_to_f32(dh);
-    } else {
+    } else if constexpr (XM == kInSwiglu) {
         // SwiGLU (nm/src/components.hpp:300-304): silu(gate) * up over the row
         // [gate K | up K], then quantize_row_q8_0
 #pragma unroll
         for (int m = 0; m < CPL; ++m) {
-            const int c = tid + 256 * m;
-            const float4* g4 = reinterpret_cast<const float4*>(in.gate_up) + 4 * c;
-            const float4* u4 = reinterpret_cast<const float4*>(in.gate_up + K) + 4 * c;
             float v[16];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const float4 g = g4[k], u = u4[k];
+                const float4 g = gv[m][k], u = uv[m][k];
                 v[4 * k] = silu_f32(g.x) * u.x, v[4 * k + 1] = silu_f32(g.y) * u.y;
                 v[4 * k + 2] = silu_f32(g.z) * u.z, v[4 * k + 3] = silu_f32(g.w) * u.w;
             }

@@ -125,7 +125,7 @@ def main() -> int:
     log(f"GEMV: {launches} launches/step, {nbytes / 1e9:.3f} GB/step, avg {avg_launch * 1e6:.2f} us/launch, {achieved:.0f} GB/s")
 
     out = {
-        "metric": "decode tok/s @bs1, Q8_0 ~8B hybrid",
+        "metric": "decode tok/s @bs1, Q8_0 ~8B hybrid; Q8 GEMV GB/s as % of HBM peak",
         "value": args.steps / wall,
         "unit": "tok/s",
         "n_gpus": 1,
@@ -146,7 +146,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None, "kernel": "gemv_q8_kernel (all Q8_0 matvecs of a decode step)",
+            "traffic": None, "kernel": "gemv_q8_stream_kernel (every Q8_0 GEMV of a decode step, as the step launches it: RMSNorm / SwiGLU fused forms included)",
             "bytes_per_launch": nbytes / launches, "avg_launch_us": avg_launch * 1e6,
         },
     }

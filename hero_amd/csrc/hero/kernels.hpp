@@ -40,6 +40,9 @@ struct GemvInput {
 };
 bool gemv_streams(int64_t K);
 void launch_gemv_q8_in(const void* packed, const GemvInput& in, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s);
+// Y[M][N] (+ R) = the M quantized activation rows (act_q8 layout, M rows)
+// times W^T, each element in the reference's block order; int8 MFMA.
+void launch_gemm_q8(const void* packed, const void* act, float* y, const float* resid, int64_t M, int64_t N, int64_t K, int epi, hipStream_t s);
 void launch_block_sums(const void* packed, const void* act, int32_t* out, int64_t N, int64_t K, hipStream_t s);
 
 // norm.hip: rows x [M][D] -> RMSNorm (gamma, eps) -> quantized act; y (fp32) optional

@@ -135,6 +135,17 @@ int hero_rmsnorm_q8_0_gemv_swiglu(const void* packed, const float* x, const floa
     });
 }
 
+int hero_q8_0_gemm(const void* packed, const void* act, float* y, const float* residual, int64_t m, int64_t n, int64_t k, void* stream) {
+    return guard([&] {
+        check_q8_shape(n, k);
+        require(m > 0 && m <= (int64_t(1) << 20), "bad row count");
+        require(packed && act && y, "null pointer");
+        require(aligned(packed, 16) && aligned(act, 16), "packed and act must be 16-byte aligned");
+        launch_gemm_q8(packed, act, y, residual, m, n, k, residual ? kEpiResidual : kEpiStore, as_stream(stream));
+        check_launch("hero_q8_0_gemm");
+    });
+}
+
 int hero_q8_0_block_sums(const void* packed, const void* act, int32_t* out, int64_t n, int64_t k, void* stream) {
     return guard([&] {
         check_q8_shape(n, k);

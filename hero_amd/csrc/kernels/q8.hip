@@ -468,3 +468,127 @@ void launch_block_sums(const void* packed, const void* act, int32_t* out, int64_
 }
 
 }  // namespace hero
+
+namespace hero {
+
+// ---------------------------------------------------------------------------
+// GEMM, M > 1 rows (prefill, batched decode): Y[M][N] = X W^T in the
+// reference's per-element order (Weight::matmul, nm/src/quant_i8.hpp:430-474:
+// each y[m][n] is vec_dot_q8_0_q8_0 of weight row n and activation row m).
+//
+// int8 MFMA v_mfma_i32_16x16x32_i8 with K = 32 gives exactly one Q8_0 block's
+// int32 sums for a 16x16 (m, n) tile (C zero per block); each lane then adds
+// float(sumi) * (d_w * d_x) to its fp32 accumulators, blocks in order.
+// Lane layout (checked on the device): A lane l = row l%16, k bytes
+// 8*(l/16)..+7; B lane l = column l%16, the same k bytes; C lane l, register r
+// = row 4*(l/16)+r, column l%16.
+//
+// Workgroup: 256 lanes, a BM x 64 tile of Y; wave w owns columns 16w..16w+15
+// and all BM rows. K streams through shared memory 8 blocks (256 bytes) at a
+// time; tile rows are padded to 272 bytes (2-way bank conflicts on the 8-byte
+// operand reads).
+// ---------------------------------------------------------------------------
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+constexpr int kGemmBN = 64, kGemmKC = 8, kGemmRow = kGemmKC * 32 + 16;
+
+template <int BM, int EPI>
+__global__ __launch_bounds__(256) void gemm_q8_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {
+    __shared__ __align__(16) int8_t Xs[BM * kGemmRow];
+    __shared__ __align__(16) int8_t Ws[kGemmBN * kGemmRow];
+    __shared__ float dxs[BM][kGemmKC];
+    __shared__ float dws[kGemmKC][kGemmBN];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int n0 = blockIdx.x * kGemmBN, m0 = blockIdx.y * BM;
+    const int nb = K >> 5;
+    constexpr int MT = BM / 16;  // m sub-tiles per wave
+    float acc[MT][4];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][r] = 0.f;
+
+    for (int b0 = 0; b0 < nb; b0 += kGemmKC) {
+        const int kc = min(kGemmKC, nb - b0);  // blocks in this chunk
+        // stage X (BM rows) and W (64 rows) of this chunk: 16-byte pieces
+        for (int e = tid; e < BM * 16; e += 256) {
+            const int r = e >> 4, c = e & 15;
+            int4 v = make_int4(0, 0, 0, 0);
+            if (m0 + r < M && c < 2 * kc) v = reinterpret_cast<const int4*>(xq + int64_t(m0 + r) * K + int64_t(b0) * 32)[c];
+            *reinterpret_cast<int4*>(Xs + r * kGemmRow + c * 16) = v;
+        }
+        for (int e = tid; e < kGemmBN * 16; e += 256) {
+            const int r = e >> 4, c = e & 15;
+            int4 v = make_int4(0, 0, 0, 0);
+            if (n0 + r < N && c < 2 * kc) v = reinterpret_cast<const int4*>(wq + int64_t(n0 + r) * K + int64_t(b0) * 32)[c];
+            *reinterpret_cast<int4*>(Ws + r * kGemmRow + c * 16) = v;
+        }
+        for (int e = tid; e < BM * kGemmKC; e += 256) {
+            const int r = e / kGemmKC, bb = e % kGemmKC;
+            dxs[r][bb] = (m0 + r < M && bb < kc) ? xd[int64_t(m0 + r) * nb + b0 + bb] : 0.f;
+        }
+        for (int e = tid; e < kGemmKC * kGemmBN; e += 256) {
+            const int bb = e / kGemmBN, c = e % kGemmBN;
+            dws[bb][c] = (n0 + c < N && bb < kc) ? half_bits_to_f32(wd[int64_t(b0 + bb) * Npad + n0 + c]) : 0.f;
+        }
+        __syncthreads();
+        const int n_l = 16 * w + (lane & 15);
+        for (int bb = 0; bb < kc; ++bb) {
+            const int koff = bb * 32 + (lane >> 4) * 8;
+            const long bop = *reinterpret_cast<const long*>(Ws + n_l * kGemmRow + koff);
+            const float dw = dws[bb][n_l];
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+                const long aop = *reinterpret_cast<const long*>(Xs + (16 * i + (lane & 15)) * kGemmRow + koff);
+                const v4i_t zero = {0, 0, 0, 0};
+                const v4i_t c = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, zero, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m_l = 16 * i + (lane >> 4) * 4 + r;
+                    acc[i][r] = acc[i][r] + float(c[r]) * (dw * dxs[m_l][bb]);
+                }
+            }
+        }
+        __syncthreads();
+    }
+    const int n = n0 + 16 * w + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = m0 + 16 * i + (lane >> 4) * 4 + r;
+            if (m < M && n < N) {
+                const int64_t o = int64_t(m) * N + n;
+                if constexpr (EPI == kEpiResidual)
+                    y[o] = resid[o] + acc[i][r];
+                else
+                    y[o] = acc[i][r];
+            }
+        }
+}
+
+namespace {
+template <int BM>
+void gemm_dispatch(int epi, const int8_t* wq, const uint16_t* wd, const int8_t* xq, const float* xd, float* y, const float* resid, int M, int N, int Npad, int K, hipStream_t s) {
+    const dim3 grid(unsigned((N + kGemmBN - 1) / kGemmBN), unsigned((M + BM - 1) / BM));
+    if (epi == kEpiResidual)
+        hipLaunchKernelGGL((gemm_q8_kernel<BM, kEpiResidual>), grid, dim3(256), 0, s, wq, wd, xq, xd, y, resid, M, N, Npad, K);
+    else
+        hipLaunchKernelGGL((gemm_q8_kernel<BM, kEpiStore>), grid, dim3(256), 0, s, wq, wd, xq, xd, y, resid, M, N, Npad, K);
+}
+}  // namespace
+
+void launch_gemm_q8(const void* packed, const void* act, float* y, const float* resid, int64_t M, int64_t N, int64_t K, int epi, hipStream_t s) {
+    const int8_t* wq = static_cast<const int8_t*>(packed);
+    const uint16_t* wd = reinterpret_cast<const uint16_t*>(wq + N * K);
+    const int8_t* xq = static_cast<const int8_t*>(act);
+    const float* xd = reinterpret_cast<const float*>(xq + M * K);
+    const int Npad = int(packed_rows_pad(N));
+    if (M <= 16)
+        gemm_dispatch<16>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s);
+    else if (M <= 32)
+        gemm_dispatch<32>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s);
+    else
+        gemm_dispatch<64>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s);
+}
+
+}  // namespace hero

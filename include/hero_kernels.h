@@ -85,6 +85,13 @@ int hero_q8_0_pack_interleaved(const void* gguf_blocks, void* packed, int64_t n_
  * interleave 32; k == 4096; act_out: hero_q8_0_act_bytes(1, ff). Bit-exact. */
 int hero_rmsnorm_q8_0_gemv_swiglu(const void* packed, const float* x, const float* gamma, float eps, void* act_out, int64_t ff, int64_t k, void* stream);
 
+/* Y[M][N] = X W^T for M quantized activation rows (hero_q8_0_quantize with
+ * m = M): Weight::matmul (nm/src/quant_i8.hpp:430-474), every element equal
+ * to the single-row vec_dot_q8_0_q8_0 (block order kept, bit-exact). The int32
+ * block sums come from int8 MFMA. If `residual` is non-NULL, Y = R + X W^T
+ * ([M][N]). For prefill and batched decode. */
+int hero_q8_0_gemm(const void* packed, const void* act, float* y, const float* residual, int64_t m, int64_t n, int64_t k, void* stream);
+
 /* Exact int32 block dot products out[N][K/32] of one activation row: the
  * `sumi` of nm/src/quant_i8.hpp:94-95, exported for parity checks. */
 int hero_q8_0_block_sums(const void* packed, const void* act, int32_t* out, int64_t n, int64_t k, void* stream);

@@ -180,6 +180,26 @@ def test_rmsnorm_gate_up_swiglu_matches_oracle_bytes(lib, ff):
     assert got.tobytes() == want.tobytes()
 
 
+@pytest.mark.parametrize("m,n,k", [(16, 4096, 4096), (64, 1000, 1024), (5, 96, 12288), (130, 4100, 4096), (33, 64, 2816), (1, 64, 256)])
+def test_gemm_matches_oracle_bitwise(lib, m, n, k):
+    """M-row GEMM on int8 MFMA: every element equals the reference's matmul
+    (per-row vec_dot in block order), with and without the residual."""
+    rng = np.random.default_rng(m * 31 + n + k)
+    w = oracle.quantize_q8_0((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    packed = pack_weight(lib, w, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    act = quantize_dev(lib, x)
+    y = empty(m * n * 4)
+    check(lib.hero_q8_0_gemm(ptr(packed), ptr(act), ptr(y), None, m, n, k, stream()))
+    expect = oracle.matmul(w, n, k, x)
+    got = host(y, np.float32, (m, n))
+    assert np.array_equal(bits(got), bits(expect))
+    r = rng.standard_normal((m, n)).astype(np.float32)
+    rd = dev(r)
+    check(lib.hero_q8_0_gemm(ptr(packed), ptr(act), ptr(y), ptr(rd), m, n, k, stream()))
+    assert np.array_equal(bits(host(y, np.float32, (m, n))), bits(r + expect))
+
+
 def test_block_sums_are_exact(lib):
     n, k = 257 * 2, 4096
     rng = np.random.default_rng(3)

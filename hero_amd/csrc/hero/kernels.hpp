@@ -49,7 +49,9 @@ void launch_block_sums(const void* packed, const void* act, int32_t* out, int64_
 void launch_rmsnorm_quant(const float* x, const float* gamma, float eps, float* y, void* act, int64_t M, int64_t D, hipStream_t s);
 
 // ew.hip
-void launch_swiglu_quant(const float* gate_up, void* act, int64_t M, int64_t FF, hipStream_t s);
+// gate_up rows [M][2FF]: gate then up, or with interleave > 0 alternating
+// chunks [gate il | up il | gate il | ...]
+void launch_swiglu_quant(const float* gate_up, void* act, int64_t M, int64_t FF, hipStream_t s, int64_t interleave = 0);
 void launch_embed_q8(const void* packed_embedding, int64_t V, int64_t D, const int32_t* ids, int64_t n, float* out, hipStream_t s);
 // argmax over n logits per row (ties -> lowest index); out_index[M]
 void launch_argmax(const float* logits, int64_t M, int64_t n, int32_t* out_index, uint64_t* scratch_keys, hipStream_t s);
@@ -62,7 +64,7 @@ struct GdnDecodeArgs {
     const float* proj;      // [B][proj_stride]: qkv at 0, z at z_off, beta at beta_off, alpha at alpha_off
     int64_t proj_stride, z_off, beta_off, alpha_off;
     const float* conv_taps; // [CC][W]
-    float* conv_hist;       // [B][W-1][CC], ring: slot p % (W-1) holds position p
+    float* conv_hist;       // [B][W][CC], ring: slot p % W holds the input at position p
     float* state;           // [B][Hv][Dk][Dv]
     const float* dt_bias;   // [Hv]
     const float* decay;     // [Hv], -exp(A_log)
@@ -74,6 +76,10 @@ struct GdnDecodeArgs {
     int B, Hk, Hv, Dk, Dv, W;
 };
 void launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t s);
+// The same for T = a.B consecutive tokens of ONE sequence at positions
+// a.positions[0] + t (proj and act_out have T rows; state and ring are that
+// sequence's), then the ring update.
+void launch_gdn_prefill(const GdnDecodeArgs& a, hipStream_t s);
 
 // attn.hip: gated GQA decode over an fp32 K/V cache (one token per sequence)
 struct AttnDecodeArgs {
@@ -87,6 +93,10 @@ struct AttnDecodeArgs {
     float* v_cache;          // [B][max_ctx][Hkv*Dh]
     int64_t max_ctx;
     const int32_t* positions;// [B]
+    // 0: row b is sequence b (its own cache). 1: all B rows are consecutive
+    // tokens of ONE sequence (prefill): they share cache 0, every row's k/v is
+    // appended before any row's scores, and row b sees positions <= positions[b].
+    int shared_cache;
     float* scores;           // scratch [B][Hq][max_ctx]
     float* q_rot;            // scratch [B][Hq][Dh]
     float score_scale;

@@ -113,6 +113,14 @@ private:
     // one token at the state's device position; `with_head` adds the final
     // norm, LM head and argmax (the reference computes logits for the last row only)
     void enqueue_step(State& s, bool from_ids, bool with_head) const;
+    // T rows of one sequence at positions pos0 .. pos0+T-1, already in the
+    // state's chunk input rows: each layer as batched GEMMs around the
+    // token-serial delta-net and the causal attention; `with_head` adds the
+    // final norm, LM head and argmax of the last row
+    void enqueue_chunk(State& s, int64_t pos0, int64_t T, bool with_head) const;
+    // rows per prefill chunk: at most 512, and the chunk's attention scores
+    // (rows x query heads x max_tokens fp32) within 256 MiB
+    int64_t chunk_rows(const State& s) const;
 
     ModelConfig c_;
     std::vector<LayerWeights> layers_;
@@ -142,9 +150,13 @@ private:
     int64_t tokens_ = 0, max_tokens_ = 0;
     // per-step device scalars: [0] position, [1] token id, [2] step counter
     DeviceBuffer step_;
-    DeviceBuffer x_, h_, rows_, proj_, act_d_, act_mix_, act_ff_, gate_up_, logits_, argmax_scratch_, out_ids_, q_rot_;
+    DeviceBuffer x_, h_, proj_, act_d_, act_mix_, act_ff_, gate_up_, logits_, argmax_scratch_, out_ids_, q_rot_;
     DeviceBuffer gemv_scratch_;  // [D] output of the GEMV timing runs
-    int64_t rows_capacity_ = 0, out_ids_capacity_ = 0;
+    int64_t out_ids_capacity_ = 0;
+    // prefill chunk buffers (row-major, chunk_capacity_ rows), made on first use
+    DeviceBuffer cx_, ch_, cproj_, cact_d_, cact_mix_, cgate_up_, cact_ff_, cq_rot_, cscores_, cpos_, cids_;
+    int64_t chunk_capacity_ = 0;
+    void ensure_chunk(int64_t rows);
     std::vector<DeviceBuffer> k_cache_, v_cache_, scores_, conv_hist_, delta_;
     hipGraphExec_t graph_ = nullptr;  // one greedy decode step, replayed
 };

@@ -203,20 +203,54 @@ int hero_math_eval(const float* x, float* out, int64_t n, void* stream) {
     });
 }
 
+namespace {
+GdnDecodeArgs gdn_args(const hero_gdn_decode_args* p) {
+    require(p != nullptr, "null args");
+    const hero_gdn_decode_args& a = *p;
+    require(a.dk == 128 && a.dv == 128, "delta-net heads must be 128x128");
+    require(a.b > 0 && a.hk > 0 && a.hv > 0 && a.hv % a.hk == 0, "bad head counts");
+    require(a.conv_width >= 1 && a.conv_width <= 8, "conv width must be 1..8");
+    require(a.proj && a.conv_taps && a.conv_hist && a.state && a.dt_bias && a.decay && a.norm_gamma && a.positions && a.act_out, "null pointer");
+    const int64_t cc = 2 * int64_t(a.hk) * 128 + int64_t(a.hv) * 128;
+    require(a.proj_stride >= cc && a.z_off >= cc && a.z_off + int64_t(a.hv) * 128 <= a.proj_stride, "z slice outside the projection row");
+    require(a.beta_off >= 0 && a.beta_off + a.hv <= a.proj_stride && a.alpha_off >= 0 && a.alpha_off + a.hv <= a.proj_stride, "gate slices outside the projection row");
+    GdnDecodeArgs g{};
+    g.proj = a.proj;
+    g.proj_stride = a.proj_stride;
+    g.z_off = a.z_off;
+    g.beta_off = a.beta_off;
+    g.alpha_off = a.alpha_off;
+    g.conv_taps = a.conv_taps;
+    g.conv_hist = a.conv_hist;
+    g.state = a.state;
+    g.dt_bias = a.dt_bias;
+    g.decay = a.decay;
+    g.norm_gamma = a.norm_gamma;
+    g.eps = a.eps;
+    g.positions = a.positions;
+    g.act_out = a.act_out;
+    g.out_f32 = a.out_f32;
+    g.B = a.b;
+    g.Hk = a.hk;
+    g.Hv = a.hv;
+    g.Dk = a.dk;
+    g.Dv = a.dv;
+    g.W = a.conv_width;
+    return g;
+}
+}  // namespace
+
 int hero_gdn_decode(const hero_gdn_decode_args* p, void* stream) {
     return guard([&] {
-        require(p != nullptr, "null args");
-        const hero_gdn_decode_args& a = *p;
-        require(a.dk == 128 && a.dv == 128, "delta-net heads must be 128x128");
-        require(a.b > 0 && a.hk > 0 && a.hv > 0 && a.hv % a.hk == 0, "bad head counts");
-        require(a.conv_width >= 1 && a.conv_width <= 8, "conv width must be 1..8");
-        require(a.proj && a.conv_taps && a.conv_hist && a.state && a.dt_bias && a.decay && a.norm_gamma && a.positions && a.act_out, "null pointer");
-        const int64_t cc = 2 * int64_t(a.hk) * 128 + int64_t(a.hv) * 128;
-        require(a.proj_stride >= cc && a.z_off >= cc && a.z_off + int64_t(a.hv) * 128 <= a.proj_stride, "z slice outside the projection row");
-        require(a.beta_off >= 0 && a.beta_off + a.hv <= a.proj_stride && a.alpha_off >= 0 && a.alpha_off + a.hv <= a.proj_stride, "gate slices outside the projection row");
-        GdnDecodeArgs g{a.proj, a.proj_stride, a.z_off, a.beta_off, a.alpha_off, a.conv_taps, a.conv_hist, a.state, a.dt_bias, a.decay, a.norm_gamma, a.eps, a.positions, a.act_out, a.out_f32, a.b, a.hk, a.hv, a.dk, a.dv, a.conv_width};
-        launch_gdn_decode(g, as_stream(stream));
+        launch_gdn_decode(gdn_args(p), as_stream(stream));
         check_launch("hero_gdn_decode");
+    });
+}
+
+int hero_gdn_prefill(const hero_gdn_decode_args* p, void* stream) {
+    return guard([&] {
+        launch_gdn_prefill(gdn_args(p), as_stream(stream));
+        check_launch("hero_gdn_prefill");
     });
 }
 
@@ -231,7 +265,30 @@ int hero_attn_decode(const hero_attn_decode_args* p, void* stream) {
         const int64_t kw = int64_t(a.hkv) * 128;
         require(a.proj_stride >= 2 * int64_t(a.hq) * 128 && a.k_off + kw <= a.proj_stride && a.v_off + kw <= a.proj_stride, "k/v slices outside the projection row");
         require(a.max_ctx <= (int64_t(1) << 24), "max_ctx too large");
-        AttnDecodeArgs g{a.proj, a.proj_stride, a.k_off, a.v_off, a.q_gamma, a.k_gamma, a.eps, a.rope_cs, a.k_cache, a.v_cache, a.max_ctx, a.positions, a.scores, a.q_rot, a.score_scale, a.window, a.act_out, a.out_f32, a.b, a.hq, a.hkv, a.dh};
+        AttnDecodeArgs g{};
+        g.proj = a.proj;
+        g.proj_stride = a.proj_stride;
+        g.k_off = a.k_off;
+        g.v_off = a.v_off;
+        g.q_gamma = a.q_gamma;
+        g.k_gamma = a.k_gamma;
+        g.eps = a.eps;
+        g.rope_cs = a.rope_cs;
+        g.k_cache = a.k_cache;
+        g.v_cache = a.v_cache;
+        g.max_ctx = a.max_ctx;
+        g.positions = a.positions;
+        g.shared_cache = 0;
+        g.scores = a.scores;
+        g.q_rot = a.q_rot;
+        g.score_scale = a.score_scale;
+        g.window = a.window;
+        g.act_out = a.act_out;
+        g.out_f32 = a.out_f32;
+        g.B = a.b;
+        g.Hq = a.hq;
+        g.Hkv = a.hkv;
+        g.Dh = a.dh;
         launch_attn_decode(g, as_stream(stream));
         check_launch("hero_attn_decode");
     });

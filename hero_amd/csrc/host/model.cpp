@@ -13,6 +13,13 @@
 // argmax (qwen35.hpp:296-302, logits.hpp:61-66). The position and the token
 // id of a step live in device memory and are advanced by the device, so a
 // greedy decode step has no host input and is replayed as one hipGraph.
+//
+// A forward of T > 1 rows (prefill) runs in chunks of rows. Per chunk and layer
+// the matvecs become int8-MFMA GEMMs over all the chunk's rows (one weight read
+// per chunk), the norms and the SwiGLU work row-wise, the delta-net runs its
+// tokens in order with the state in shared memory, and attention appends the
+// chunk's keys and values before every row attends causally -- the same
+// per-row arithmetic as T single steps, so the two agree bit for bit.
 #include "hero/model.hpp"
 
 #include <cmath>
@@ -32,6 +39,10 @@ __global__ void set_step_kernel(int32_t* step, int32_t position, int32_t token, 
     if (position >= 0) step[0] = position;
     if (token >= 0) step[1] = token;
     if (counter >= 0) step[2] = counter;
+}
+__global__ void positions_kernel(int32_t* pos, int32_t pos0, int32_t n) {
+    const int32_t i = int32_t(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i < n) pos[i] = pos0 + i;
 }
 __global__ void advance_step_kernel(int32_t* step, int32_t* out_ids, int32_t record) {
     step[0] += 1;
@@ -330,6 +341,31 @@ void Qwen35Model::State::reset() {
     tokens_ = 0;
 }
 
+int64_t Qwen35Model::chunk_rows(const State& st) const {
+    const int64_t per_row = c_.Hq * st.max_tokens_ * 4;  // attention scores of one row
+    return std::max<int64_t>(1, std::min<int64_t>(512, (int64_t(256) << 20) / per_row));
+}
+
+void Qwen35Model::State::ensure_chunk(int64_t rows) {
+    if (rows <= chunk_capacity_) return;
+    const ModelConfig& c = m_.c_;
+    int64_t n_in_max = 0;
+    for (const LayerWeights& L : m_.layers_) n_in_max = std::max(n_in_max, L.n_in);
+    hip_check(hipStreamSynchronize(m_.stream_), "chunk buffers");
+    cx_ = DeviceBuffer(size_t(rows * c.D) * 4);
+    ch_ = DeviceBuffer(size_t(rows * c.D) * 4);
+    cproj_ = DeviceBuffer(size_t(rows * n_in_max) * 4);
+    cact_d_ = DeviceBuffer(size_t(act_q8_bytes(rows, c.D)));
+    cact_mix_ = DeviceBuffer(size_t(act_q8_bytes(rows, std::max(c.q_width(), c.v_width()))));
+    cgate_up_ = DeviceBuffer(size_t(rows * 2 * c.FF) * 4);
+    cact_ff_ = DeviceBuffer(size_t(act_q8_bytes(rows, c.FF)));
+    cq_rot_ = DeviceBuffer(size_t(rows * c.q_width()) * 4);
+    cscores_ = DeviceBuffer(size_t(rows * c.Hq * max_tokens_) * 4);
+    cpos_ = DeviceBuffer(size_t(rows) * 4);
+    cids_ = DeviceBuffer(size_t(rows) * 4);
+    chunk_capacity_ = rows;
+}
+
 // ---- the step -------------------------------------------------------------------------
 namespace {
 
@@ -457,6 +493,87 @@ void Qwen35Model::enqueue_step(State& st, bool from_ids, bool with_head) const {
     check_launch("decode step");
 }
 
+void Qwen35Model::enqueue_chunk(State& st, int64_t pos0, int64_t T, bool with_head) const {
+    const ModelConfig& c = c_;
+    hipStream_t s = stream_;
+    float* x = st.cx_.get<float>();
+    float* h = st.ch_.get<float>();
+    float* proj = st.cproj_.get<float>();
+    int32_t* pos = st.cpos_.get<int32_t>();
+    hipLaunchKernelGGL(positions_kernel, dim3(unsigned((T + 255) / 256)), dim3(256), 0, s, pos, int32_t(pos0), int32_t(T));
+    for (int64_t l = 0; l < c.L; ++l) {
+        const LayerWeights& L = layers_[size_t(l)];
+        // H = X + mix(rms(X)); X' = H + mlp(rms(H))  (nm/src/qwen35.hpp:318-327)
+        launch_rmsnorm_quant(x, L.mixer_norm.get<float>(), c.eps, nullptr, st.cact_d_.get(), T, c.D, s);
+        launch_gemm_q8(L.w_in.get(), st.cact_d_.get(), proj, nullptr, T, L.n_in, c.D, kEpiStore, s);
+        int64_t k_mix;
+        if (L.recurrent) {
+            GdnDecodeArgs a{};
+            a.proj = proj;
+            a.proj_stride = L.n_in;
+            a.z_off = L.z_off;
+            a.beta_off = L.beta_off;
+            a.alpha_off = L.alpha_off;
+            a.conv_taps = L.conv.get<float>();
+            a.conv_hist = st.conv_hist_[size_t(l)].get<float>();
+            a.state = st.delta_[size_t(l)].get<float>();
+            a.dt_bias = L.dt_bias.get<float>();
+            a.decay = L.decay.get<float>();
+            a.norm_gamma = L.ssm_norm.get<float>();
+            a.eps = c.eps;
+            a.positions = pos;
+            a.act_out = st.cact_mix_.get();
+            a.out_f32 = nullptr;
+            a.B = int(T);
+            a.Hk = int(c.Hk);
+            a.Hv = int(c.Hv);
+            a.Dk = int(c.Dk);
+            a.Dv = int(c.Dv);
+            a.W = int(c.W);
+            launch_gdn_prefill(a, s);
+            k_mix = c.v_width();
+        } else {
+            AttnDecodeArgs a{};
+            a.proj = proj;
+            a.proj_stride = L.n_in;
+            a.k_off = L.k_off;
+            a.v_off = L.v_off;
+            a.q_gamma = L.q_norm.get<float>();
+            a.k_gamma = L.k_norm.get<float>();
+            a.eps = c.eps;
+            a.rope_cs = rope_cs_.get<float>();
+            a.k_cache = st.k_cache_[size_t(l)].get<float>();
+            a.v_cache = st.v_cache_[size_t(l)].get<float>();
+            a.max_ctx = st.max_tokens_;
+            a.positions = pos;
+            a.shared_cache = 1;
+            a.scores = st.cscores_.get<float>();
+            a.q_rot = st.cq_rot_.get<float>();
+            a.score_scale = 1.f / std::sqrt(float(c.Dh));  // qwen35.hpp:359
+            a.window = 0;
+            a.act_out = st.cact_mix_.get();
+            a.out_f32 = nullptr;
+            a.B = int(T);
+            a.Hq = int(c.Hq);
+            a.Hkv = int(c.Hkv);
+            a.Dh = int(c.Dh);
+            launch_attn_decode(a, s);
+            k_mix = c.q_width();
+        }
+        launch_gemm_q8(L.w_out.get(), st.cact_mix_.get(), h, x, T, c.D, k_mix, kEpiResidual, s);
+        launch_rmsnorm_quant(h, L.channel_norm.get<float>(), c.eps, nullptr, st.cact_d_.get(), T, c.D, s);
+        launch_gemm_q8(L.w_gate_up.get(), st.cact_d_.get(), st.cgate_up_.get<float>(), nullptr, T, 2 * c.FF, c.D, kEpiStore, s);
+        launch_swiglu_quant(st.cgate_up_.get<float>(), st.cact_ff_.get(), T, c.FF, s, ffn_fused_ ? 32 : 0);
+        launch_gemm_q8(L.w_down.get(), st.cact_ff_.get(), x, h, T, c.D, c.FF, kEpiResidual, s);
+    }
+    if (with_head) {
+        int32_t* step = st.step_.get<int32_t>();
+        gemv_norm(c.tied ? embedding_.get() : output_.get(), x + (T - 1) * c.D, final_norm_.get<float>(), c.eps, st.act_d_.get(), st.logits_.get<float>(), nullptr, c.V, c.D, s);
+        launch_argmax(st.logits_.get<float>(), 1, c.V, step + 1, st.argmax_scratch_.get<uint64_t>(), s);
+    }
+    check_launch("prefill chunk");
+}
+
 void Qwen35Model::forward(State& st, const float* rows, const int32_t* ids, int64_t T, float* logits, int32_t* next_id) const {
     const ModelConfig& c = c_;
     if (&st.m_ != this) throw Error(HERO_EINVAL, "forward: state belongs to another model");
@@ -468,21 +585,25 @@ void Qwen35Model::forward(State& st, const float* rows, const int32_t* ids, int6
             if (ids[t] < 0 || ids[t] >= c.V) throw Error(HERO_EINVAL, "forward: token id out of range");
     hipStream_t s = stream_;
     try {
-        if (rows) {
-            if (st.rows_capacity_ < T) {
-                hip_check(hipStreamSynchronize(s), "sync");
-                st.rows_ = DeviceBuffer(size_t(T * c.D) * 4);
-                st.rows_capacity_ = T;
+        if (T == 1) {
+            hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, s, st.step_.get<int32_t>(), int32_t(st.tokens_), ids ? ids[0] : -1, 0);
+            if (rows) hip_check(hipMemcpyAsync(st.x_.get(), rows, size_t(c.D) * 4, hipMemcpyHostToDevice, s), "row upload");
+            enqueue_step(st, rows == nullptr, true);
+        } else {
+            const int64_t cap = chunk_rows(st);
+            st.ensure_chunk(std::min(cap, T));
+            for (int64_t t0 = 0; t0 < T; t0 += cap) {
+                const int64_t n = std::min(cap, T - t0);
+                if (rows) {
+                    hip_check(hipMemcpyAsync(st.cx_.get(), rows + t0 * c.D, size_t(n * c.D) * 4, hipMemcpyHostToDevice, s), "rows upload");
+                } else {
+                    hip_check(hipMemcpyAsync(st.cids_.get(), ids + t0, size_t(n) * 4, hipMemcpyHostToDevice, s), "ids upload");
+                    launch_embed_q8(embedding_.get(), c.V, c.D, st.cids_.get<int32_t>(), n, st.cx_.get<float>(), s);
+                }
+                enqueue_chunk(st, st.tokens_ + t0, n, t0 + n == T);
             }
-            hip_check(hipMemcpyAsync(st.rows_.get(), rows, size_t(T * c.D) * 4, hipMemcpyHostToDevice, s), "rows upload");
-        }
-        hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, s, st.step_.get<int32_t>(), int32_t(st.tokens_), -1, 0);
-        for (int64_t t = 0; t < T; ++t) {
-            if (rows)
-                hip_check(hipMemcpyAsync(st.x_.get(), st.rows_.get<float>() + t * c.D, size_t(c.D) * 4, hipMemcpyDeviceToDevice, s), "row copy");
-            else
-                hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, s, st.step_.get<int32_t>(), -1, ids[t], -1);
-            enqueue_step(st, rows == nullptr, t == T - 1);
+            // the position of the next single step
+            hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, s, st.step_.get<int32_t>(), int32_t(st.tokens_ + T), -1, -1);
         }
         if (logits) hip_check(hipMemcpyAsync(logits, st.logits_.get(), size_t(c.V) * 4, hipMemcpyDeviceToHost, s), "logits download");
         int32_t scalars[4] = {0, 0, 0, 0};

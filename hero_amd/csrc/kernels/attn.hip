@@ -21,6 +21,11 @@
 //             (qwen35.hpp:390-393) and quantizes the output (one Q8_0 block).
 // RoPE reads a host-built cos/sin table made with the reference's float
 // expressions (attention.hpp:76-91).
+// With shared_cache set, the B rows are consecutive tokens of one sequence
+// (prefill): prep appends all their keys and values to the one cache before
+// the scores kernel runs, and row b attends to positions <= positions[b] only,
+// as the reference appends the whole batch and then reduces each row over its
+// visible rows (qwen35.hpp:363, 386-387).
 #include "hero/device.hpp"
 #include "hero/kernels.hpp"
 #include "hero/seqsum.hpp"
@@ -29,6 +34,9 @@ namespace hero {
 
 constexpr int kAttnDim = 128;
 constexpr int kScoreTiles = 8;
+
+// the cache row b reads and appends to
+__device__ __forceinline__ int64_t cache_of(const AttnDecodeArgs& a, int b) { return a.shared_cache ? 0 : b; }
 
 // ---- 1. prep ----------------------------------------------------------------------
 // RMSNorm over one head held one value per lane (sequential 128-term sum of
@@ -77,9 +85,10 @@ __global__ __launch_bounds__(kAttnDim) void attn_prep_kernel(AttnDecodeArgs a) {
     if (h % group == 0) {
         const float k = norm_rope_head(P[a.k_off + int64_t(g) * kAttnDim + j], a.k_gamma, a.eps, cs, buf, scal, j);
         const float v = P[a.v_off + int64_t(g) * kAttnDim + j];
-        const int64_t kv = int64_t(b) * a.Hkv + g;
+        const int64_t cb = cache_of(a, b);
+        const int64_t kv = cb * a.Hkv + g;
         a.k_cache[(kv * kAttnDim + j) * a.max_ctx + pos] = k;  // [B][Hkv][Dh][max_ctx]
-        a.v_cache[(int64_t(b) * a.max_ctx + pos) * (int64_t(a.Hkv) * kAttnDim) + int64_t(g) * kAttnDim + j] = v;  // [B][max_ctx][Hkv*Dh]
+        a.v_cache[(cb * a.max_ctx + pos) * (int64_t(a.Hkv) * kAttnDim) + int64_t(g) * kAttnDim + j] = v;  // [B][max_ctx][Hkv*Dh]
     }
 }
 
@@ -96,7 +105,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnDecodeArgs a) {
     __shared__ float q[kAttnDim];
     if (threadIdx.x < kAttnDim) q[threadIdx.x] = a.q_rot[(int64_t(b) * a.Hq + h) * kAttnDim + threadIdx.x];
     __syncthreads();
-    const float* kh = a.k_cache + (int64_t(b) * a.Hkv + g) * kAttnDim * a.max_ctx;
+    const float* kh = a.k_cache + (cache_of(a, b) * a.Hkv + g) * kAttnDim * a.max_ctx;
     float* sc = a.scores + (int64_t(b) * a.Hq + h) * a.max_ctx;
     for (int t = tile0 * 256 + int(threadIdx.x); t < n; t += kScoreTiles * 256) {
         const float* kj = kh + first + t;
@@ -168,7 +177,7 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(AttnDecodeArgs a) {
     const int n = pos + 1 - first;
     const float* alpha = a.scores + (int64_t(b) * a.Hq + h) * a.max_ctx;
     const int64_t kw = int64_t(a.Hkv) * kAttnDim;
-    const float* vb = a.v_cache + (int64_t(b) * a.max_ctx + first) * kw + int64_t(g) * kAttnDim + part * kPvCh;
+    const float* vb = a.v_cache + (cache_of(a, b) * a.max_ctx + first) * kw + int64_t(g) * kAttnDim + part * kPvCh;
     __shared__ __align__(16) float vt[2][kPvTile * kPvCh];
     __shared__ float at[2][kPvTile];
     const int ntiles = (n + kPvTile - 1) / kPvTile;

@@ -7,13 +7,14 @@ namespace hero {
 
 // nm/src/components.hpp:300-304 (GatedMLP): g = silu(gate(x)) * up(x), then
 // the down projection quantizes g. gate_up row = [gate FF | up FF].
-__global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restrict__ gu, int8_t* __restrict__ qs, float* __restrict__ qd, int64_t FF, int64_t total8) {
+__global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restrict__ gu, int8_t* __restrict__ qs, float* __restrict__ qd, int64_t FF, int64_t total8, int64_t il) {
     const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= total8) return;
     const int64_t per_row = FF >> 3;
-    const int64_t row = i / per_row, g = i - row * per_row;
-    const float* gate = gu + row * 2 * FF + g * 8;
-    const float* up = gate + FF;
+    const int64_t row = i / per_row, c = (i - row * per_row) * 8;
+    // 8 consecutive outputs never straddle an interleave chunk (il % 8 == 0)
+    const float* gate = gu + row * 2 * FF + (il ? (c / il) * 2 * il + c % il : c);
+    const float* up = gate + (il ? il : FF);
     float v[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = silu_f32(gate[j]) * up[j];
@@ -23,11 +24,11 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restri
     if ((i & 3) == 0) qd[i >> 2] = half_bits_to_f32(dh);
 }
 
-void launch_swiglu_quant(const float* gate_up, void* act, int64_t M, int64_t FF, hipStream_t s) {
+void launch_swiglu_quant(const float* gate_up, void* act, int64_t M, int64_t FF, hipStream_t s, int64_t interleave) {
     int8_t* qs = static_cast<int8_t*>(act);
     float* qd = reinterpret_cast<float*>(qs + M * FF);
     const int64_t total8 = M * FF / 8;
-    hipLaunchKernelGGL(swiglu_quant_kernel, dim3(unsigned((total8 + 255) / 256)), dim3(256), 0, s, gate_up, qs, qd, FF, total8);
+    hipLaunchKernelGGL(swiglu_quant_kernel, dim3(unsigned((total8 + 255) / 256)), dim3(256), 0, s, gate_up, qs, qd, FF, total8, interleave);
 }
 
 // nm/src/quant.hpp:306-313: row = d * q

@@ -143,6 +143,15 @@ typedef struct hero_gdn_decode_args {
 } hero_gdn_decode_args;
 int hero_gdn_decode(const hero_gdn_decode_args* args, void* stream);
 
+/* Delta-net prefill: the same work for T = args->b consecutive tokens of ONE
+ * sequence at positions positions[0] .. positions[0]+T-1 (only positions[0]
+ * is read). proj, act_out and out_f32 have T rows; conv_hist and state are
+ * that sequence's ([W][CC] and [Hv][Dk][Dv]). The tokens run in order, as the
+ * reference's token loop does (nm/src/qwen35.hpp:436-455), so the result equals
+ * T calls of hero_gdn_decode bit for bit; the conv ring then holds the chunk's
+ * last W positions. */
+int hero_gdn_prefill(const hero_gdn_decode_args* args, void* stream);
+
 /* Gated GQA attention decode over an fp32 K/V cache, one token for each of
  * B sequences: head-pair split, q/k RMSNorm + RoPE (host table), cache
  * append, softmax(scale*q.k) over the visible rows, sum alpha*v,

@@ -389,6 +389,50 @@ def test_gdn_decode_matches_oracle(lib, hk, hv):
             assert np.array_equal(bits(gstate[b]), bits(o_state[b])), f"state after step {step} seq {b}"
 
 
+@pytest.mark.parametrize("W,chunks", [(4, [2, 7, 1, 3, 5]), (3, [1, 1, 6, 2]), (1, [3, 1, 4])])
+def test_gdn_prefill_chunks_match_oracle(lib, W, chunks):
+    """Delta-net prefill in ragged chunks (shorter and longer than the conv
+    window, single tokens through the decode entry point in between): every
+    output row, its Q8_0 blocks and the state after each chunk equal the
+    oracle's token-serial recurrence bit for bit."""
+    from hero_amd._lib import GdnDecodeArgs
+
+    hk, hv, dk = 2, 4, 128
+    rng = np.random.default_rng(1000 + W)
+    cc = 2 * hk * dk + hv * dk
+    stride = cc + hv * dk + 2 * hv
+    taps = (rng.standard_normal((cc, W)) * 0.5).astype(np.float32)
+    dt = (rng.standard_normal(hv) * 0.1).astype(np.float32)
+    decay = (-np.exp(rng.standard_normal(hv) * 0.5)).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(dk)).astype(np.float32)
+    eps = np.float32(1e-6)
+    d_taps, d_dt, d_decay, d_gamma = dev(taps), dev(dt), dev(decay), dev(gamma)
+    d_hist = empty(W * cc * 4)
+    d_state = empty(hv * dk * dk * 4)
+    o_hist = np.zeros((max(W - 1, 0), cc), np.float32)
+    o_state = np.zeros((hv, dk, dk), np.float32)
+    tmax = max(chunks)
+    act = empty(lib.hero_q8_0_act_bytes(tmax, hv * dk))
+    out = empty(tmax * hv * dk * 4)
+    pos = 0
+    for i, T in enumerate(chunks):
+        proj = (rng.standard_normal((T, stride)) * 0.7).astype(np.float32)
+        d_proj, d_pos = dev(proj), dev(np.array([pos], np.int32))
+        a = GdnDecodeArgs(ptr(d_proj), stride, cc, cc + hv * dk, cc + hv * dk + hv, ptr(d_taps), ptr(d_hist), ptr(d_state),
+                          ptr(d_dt), ptr(d_decay), ptr(d_gamma), eps, ptr(d_pos), ptr(act), ptr(out), T, hk, hv, dk, dk, W)
+        entry = lib.hero_gdn_decode if (T == 1 and i % 2) else lib.hero_gdn_prefill
+        check(entry(a, stream()))
+        got = host(out, np.float32, (tmax, hv * dk))[:T]
+        got_blocks = act_to_blocks(host(act, np.uint8)[: T * hv * dk + T * hv * dk // 32 * 4], T, hv * dk)
+        for t in range(T):
+            expect = gdn_reference(proj[t], taps, o_hist, o_state, dt, decay, gamma, eps, hk, hv, pos + t)
+            assert np.array_equal(bits(got[t]), bits(expect)), f"chunk {i} row {t}: max ulp {ulp_diff(got[t], expect).max()}"
+            assert got_blocks[t].tobytes() == oracle.quantize_row_q8_0(expect).tobytes(), f"chunk {i} row {t} blocks"
+        gstate = host(d_state, np.float32, (hv, dk, dk))
+        assert np.array_equal(bits(gstate), bits(o_state)), f"state after chunk {i}"
+        pos += T
+
+
 # ---- attention decode ------------------------------------------------------------------
 @pytest.mark.parametrize("window", [0, 3])
 def test_attn_decode_matches_oracle(lib, window):

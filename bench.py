@@ -110,7 +110,7 @@ def main() -> int:
     prefill_s = time.perf_counter() - t
     log(f"prefill {args.prompt} tokens: {prefill_s:.2f} s ({args.prompt / prefill_s:.1f} tok/s)")
 
-    warm_ids, _ = model.decode_greedy(state, first, args.warmup)
+    warm_ids = model.decode_greedy(state, first, args.warmup)[0] if args.warmup > 0 else np.array([first], np.int32)
     torch.cuda.synchronize()
     t = time.perf_counter()
     ids, _ = model.decode_greedy(state, int(warm_ids[-1]), args.steps)

@@ -87,7 +87,8 @@ SIGNATURES = {
     "hero_argmax": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
     "hero_math_eval": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
     "hero_gdn_decode": (c_int, [POINTER(GdnDecodeArgs), c_void_p]),
-    "hero_gdn_prefill": (c_int, [POINTER(GdnDecodeArgs), c_void_p]),
+    "hero_gdn_prefill_work_bytes": (c_int64, [c_int64, c_int32, c_int32]),
+    "hero_gdn_prefill": (c_int, [POINTER(GdnDecodeArgs), c_void_p, c_int64, c_void_p]),
     "hero_attn_decode": (c_int, [POINTER(AttnDecodeArgs), c_void_p]),
     "hero_model_open": (c_int, [c_char_p, POINTER(c_void_p)]),
     "hero_model_open_image": (c_int, [c_void_p, c_size_t, POINTER(c_void_p)]),

@@ -78,8 +78,16 @@ struct GdnDecodeArgs {
 void launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t s);
 // The same for T = a.B consecutive tokens of ONE sequence at positions
 // a.positions[0] + t (proj and act_out have T rows; state and ring are that
-// sequence's), then the ring update.
-void launch_gdn_prefill(const GdnDecodeArgs& a, hipStream_t s);
+// sequence's), then the ring update. `work` holds gdn_prefill_work_bytes.
+struct GdnPrefillWork {
+    float* q;   // [T][Hk][128] normalised, query-scaled
+    float* k;   // [T][Hk][128] normalised
+    float* v;   // [T][Hv][128]
+    float* o;   // [T][Hv][128] delta-rule outputs before the head norm
+    float* bd;  // [T][Hv][2] beta, decay
+};
+int64_t gdn_prefill_work_bytes(int64_t T, int64_t Hk, int64_t Hv);
+void launch_gdn_prefill(const GdnDecodeArgs& a, void* work, hipStream_t s);
 
 // attn.hip: gated GQA decode over an fp32 K/V cache (one token per sequence)
 struct AttnDecodeArgs {

@@ -154,7 +154,7 @@ private:
     DeviceBuffer gemv_scratch_;  // [D] output of the GEMV timing runs
     int64_t out_ids_capacity_ = 0;
     // prefill chunk buffers (row-major, chunk_capacity_ rows), made on first use
-    DeviceBuffer cx_, ch_, cproj_, cact_d_, cact_mix_, cgate_up_, cact_ff_, cq_rot_, cscores_, cpos_, cids_;
+    DeviceBuffer cx_, ch_, cproj_, cact_d_, cact_mix_, cgate_up_, cact_ff_, cq_rot_, cscores_, cpos_, cids_, cgdn_work_;
     int64_t chunk_capacity_ = 0;
     void ensure_chunk(int64_t rows);
     std::vector<DeviceBuffer> k_cache_, v_cache_, scores_, conv_hist_, delta_;

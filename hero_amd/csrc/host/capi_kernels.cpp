@@ -247,9 +247,16 @@ int hero_gdn_decode(const hero_gdn_decode_args* p, void* stream) {
     });
 }
 
-int hero_gdn_prefill(const hero_gdn_decode_args* p, void* stream) {
+int64_t hero_gdn_prefill_work_bytes(int64_t t, int32_t hk, int32_t hv) {
+    if (t <= 0 || hk <= 0 || hv <= 0) return -1;
+    return gdn_prefill_work_bytes(t, hk, hv);
+}
+
+int hero_gdn_prefill(const hero_gdn_decode_args* p, void* work, int64_t work_bytes, void* stream) {
     return guard([&] {
-        launch_gdn_prefill(gdn_args(p), as_stream(stream));
+        const GdnDecodeArgs g = gdn_args(p);
+        require(work != nullptr && work_bytes >= gdn_prefill_work_bytes(g.B, g.Hk, g.Hv), "prefill workspace too small");
+        launch_gdn_prefill(g, work, as_stream(stream));
         check_launch("hero_gdn_prefill");
     });
 }

@@ -363,6 +363,7 @@ void Qwen35Model::State::ensure_chunk(int64_t rows) {
     cscores_ = DeviceBuffer(size_t(rows * c.Hq * max_tokens_) * 4);
     cpos_ = DeviceBuffer(size_t(rows) * 4);
     cids_ = DeviceBuffer(size_t(rows) * 4);
+    cgdn_work_ = DeviceBuffer(size_t(gdn_prefill_work_bytes(rows, c.Hk, c.Hv)));
     chunk_capacity_ = rows;
 }
 
@@ -530,7 +531,7 @@ void Qwen35Model::enqueue_chunk(State& st, int64_t pos0, int64_t T, bool with_he
             a.Dk = int(c.Dk);
             a.Dv = int(c.Dv);
             a.W = int(c.W);
-            launch_gdn_prefill(a, s);
+            launch_gdn_prefill(a, st.cgdn_work_.get(), s);
             k_mix = c.v_width();
         } else {
             AttnDecodeArgs a{};

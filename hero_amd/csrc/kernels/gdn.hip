@@ -255,69 +255,248 @@ __global__ __launch_bounds__(kGdnDim) void gdn_decode_kernel(GdnDecodeArgs a) {
 
 // ---- prefill: tokens t = 0..T-1 of one sequence at positions pos0 + t -------------
 // a.B is T (rows of proj and of act_out); a.positions[0] is pos0; the state
-// and the ring are sequence 0's.
+// and the ring are sequence 0's. Three kernels:
+//  prep  (token, head) in parallel: conv + SiLU, L2 norms and the query scale,
+//        beta and the decay -- nothing here depends on the state;
+//  scan  one workgroup per value head runs the delta rule over the tokens in
+//        order, the state column of lane j in registers for the whole chunk;
+//  out   (token, head) in parallel: head RMSNorm, SiLU(z) gate, quantize.
+// The scan's critical path per token is one 128-term chain: token t's output
+// chain and token t+1's decay and prediction chain read the same updated
+// column, so they run in one pass over i. Every value is computed by the same
+// operations in the same order as in gdn_decode_kernel.
+constexpr int kScanTile = 16;   // tokens staged in shared memory per tile
+constexpr int kScanChunk = 32;  // state rows per fenced step of the token loop
+__device__ __forceinline__ void scan_fence() { __asm__ volatile("" ::: "memory"); }
+
+__device__ __forceinline__ GdnPrefillWork gdn_work(void* ws, int64_t T, int Hk, int Hv) {
+    GdnPrefillWork w;
+    float* f = static_cast<float*>(ws);
+    w.q = f;
+    w.k = w.q + T * Hk * kGdnDim;
+    w.v = w.k + T * Hk * kGdnDim;
+    w.o = w.v + T * Hv * kGdnDim;
+    w.bd = w.o + T * Hv * kGdnDim;
+    return w;
+}
+
 template <int W>
-__global__ __launch_bounds__(kGdnDim) void gdn_prefill_kernel(GdnDecodeArgs a) {
-    extern __shared__ __align__(16) float sh[];
-    const int j = threadIdx.x;
-    const int h = blockIdx.x;
-    const int hk = h % a.Hk;
+__global__ __launch_bounds__(kGdnDim) void gdn_prep_kernel(GdnDecodeArgs a, void* ws) {
+    const int j = threadIdx.x, slot = blockIdx.x, t = blockIdx.y;
     const int pos0 = a.positions[0];
     const int T = a.B;
     if (pos0 < 0) return;
+    const GdnPrefillWork w = gdn_work(ws, T, a.Hk, a.Hv);
     const int64_t KW = int64_t(a.Hk) * kGdnDim;
     const int64_t CC = 2 * KW + int64_t(a.Hv) * kGdnDim;
-    const float* hist = a.conv_hist;
-    float* S = a.state + int64_t(h) * kGdnState;
-    const int64_t cq = int64_t(hk) * kGdnDim + j, ck = KW + int64_t(hk) * kGdnDim + j, cv = 2 * KW + int64_t(h) * kGdnDim + j;
-
-    float4 sv[kGdnVec];
-#pragma unroll
-    for (int k = 0; k < kGdnVec; ++k) sv[k] = reinterpret_cast<const float4*>(S)[j + kGdnDim * k];
-    float tq[W], tk[W], tv[W];
-    ConvPast<W> pq, pk, pv;  // inputs before pos0 come from the ring
-    load_taps<W>(a.conv_taps, cq, tq);
-    load_taps<W>(a.conv_taps, ck, tk);
-    load_taps<W>(a.conv_taps, cv, tv);
-    load_past<W>(hist, CC, cq, pos0, pq);
-    load_past<W>(hist, CC, ck, pos0, pk);
-    load_past<W>(hist, CC, cv, pos0, pv);
-    const float gamma = a.norm_gamma[j];
-    const float A = a.decay[h], dtb = a.dt_bias[h];
-    // the first token's inputs; each iteration reads the next token's ahead
-    auto row_in = [&](int t, float& xq, float& xk, float& xv, float& z, float& bi, float& ai) {
-        const float* P = a.proj + int64_t(t) * a.proj_stride;
-        xq = P[cq];
-        xk = P[ck];
-        xv = P[cv];
-        z = P[a.z_off + int64_t(h) * kGdnDim + j];
-        bi = P[a.beta_off + h];
-        ai = P[a.alpha_off + h];
+    const float* P = a.proj + int64_t(t) * a.proj_stride;
+    // the conv input of channel c at token index u (< 0: before the chunk, from the ring)
+    auto input = [&](int64_t c, int u) -> float {
+        if (u >= 0) return a.proj[int64_t(u) * a.proj_stride + c];
+        const int p = pos0 + u;
+        return p >= 0 ? a.conv_hist[int64_t(p % W) * CC + c] : 0.f;
     };
-    float xq, xk, xv, z, bi, ai;
-    row_in(0, xq, xk, xv, z, bi, ai);
+    auto conv_silu = [&](int64_t c) -> float {
+        float taps[W];
+        load_taps<W>(a.conv_taps, c, taps);
+        ConvPast<W> past;
 #pragma unroll
-    for (int k = 0; k < kGdnVec; ++k) reinterpret_cast<float4*>(sh)[j + kGdnDim * k] = sv[k];
+        for (int i = 0; i < W - 1; ++i) past.v[i] = input(c, t - (W - 1) + i);
+        return silu_f32(conv_channel<W>(taps, past, P[c]));
+    };
+    __shared__ __align__(16) float buf[2][kGdnDim];
+    __shared__ float inv[2];
+    if (slot < a.Hk) {  // q and k of key head `slot`
+        const float sq = conv_silu(int64_t(slot) * kGdnDim + j);
+        const float sk = conv_silu(KW + int64_t(slot) * kGdnDim + j);
+        buf[0][j] = sq;
+        buf[1][j] = sk;
+        __syncthreads();
+        if (j == 0 || j == 64) {  // L2 norms (nm/src/recurrent.hpp:40-48)
+            const float ss = sum_squares_128(buf[j == 0 ? 0 : 1]);
+            inv[j == 0 ? 0 : 1] = 1.f / fmaxf(sqrtf(ss), 1e-6f);
+        }
+        __syncthreads();
+        const float query_scale = 1.f / sqrtf(float(kGdnDim));
+        const int64_t o = (int64_t(t) * a.Hk + slot) * kGdnDim + j;
+        w.q[o] = (sq * inv[0]) * query_scale;
+        w.k[o] = sk * inv[1];
+    } else {  // v of value head h, and its beta and decay
+        const int h = slot - a.Hk;
+        w.v[(int64_t(t) * a.Hv + h) * kGdnDim + j] = conv_silu(2 * KW + int64_t(h) * kGdnDim + j);
+        if (j == 0) {
+            const float beta = sigmoid_f32(P[a.beta_off + h]);
+            const float g = a.decay[h] * softplus_f32(P[a.alpha_off + h] + a.dt_bias[h]);
+            w.bd[(int64_t(t) * a.Hv + h) * 2] = beta;
+            w.bd[(int64_t(t) * a.Hv + h) * 2 + 1] = exp_f32(g);
+        }
+    }
+}
 
+// one tile of kScanTile tokens of a head: q, k (its key head), v, (beta, decay)
+struct ScanTile {
+    float q[kScanTile][kGdnDim];
+    float k[kScanTile][kGdnDim];
+    float v[kScanTile][kGdnDim];
+    float bd[kScanTile][2];
+};
+constexpr int kScanVec = 3 * kScanTile * kGdnDim / 4 / kGdnDim;  // float4 per lane per tile (12)
+
+__global__ __launch_bounds__(kGdnDim) void gdn_scan_kernel(GdnDecodeArgs a, void* ws) {
+    const int j = threadIdx.x, h = blockIdx.x, hk = h % a.Hk;
+    const int T = a.B;
+    if (a.positions[0] < 0) return;
+    const GdnPrefillWork w = gdn_work(ws, T, a.Hk, a.Hv);
+    float* S = a.state + int64_t(h) * kGdnState;
+    __shared__ __align__(16) ScanTile tiles[2];
+    const int ntiles = (T + kScanTile - 1) / kScanTile;
+
+    // tile loads: float4 f = j + 128u; u < 4: q, u < 8: k, else v; token (f % 512) / 32
+    float4 pre[kScanVec];
+    float2 pre_bd = make_float2(0.f, 0.f);
+    auto load = [&](int tile) {
+        const int t0 = tile * kScanTile;
+#pragma unroll
+        for (int u = 0; u < kScanVec; ++u) {
+            const int f = (j + kGdnDim * u) % (kScanTile * kGdnDim / 4);
+            const int tt = t0 + f / (kGdnDim / 4), c4 = f % (kGdnDim / 4);
+            const float* src = u < 4 ? w.q + (int64_t(tt) * a.Hk + hk) * kGdnDim : u < 8 ? w.k + (int64_t(tt) * a.Hk + hk) * kGdnDim : w.v + (int64_t(tt) * a.Hv + h) * kGdnDim;
+            pre[u] = tt < T ? reinterpret_cast<const float4*>(src)[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (j < kScanTile && t0 + j < T) pre_bd = reinterpret_cast<const float2*>(w.bd)[int64_t(t0 + j) * a.Hv + h];
+    };
+    auto store = [&](ScanTile& dst) {
+#pragma unroll
+        for (int u = 0; u < kScanVec; ++u) {
+            const int f = (j + kGdnDim * u) % (kScanTile * kGdnDim / 4);
+            float* base = u < 4 ? &dst.q[0][0] : u < 8 ? &dst.k[0][0] : &dst.v[0][0];
+            reinterpret_cast<float4*>(base)[f] = pre[u];
+        }
+        if (j < kScanTile) {
+            dst.bd[j][0] = pre_bd.x;
+            dst.bd[j][1] = pre_bd.y;
+        }
+    };
+
+    float col[kGdnDim];  // S[i][j], i = 0..127: this lane's state column
+#pragma unroll
+    for (int i = 0; i < kGdnDim; ++i) col[i] = S[i * kGdnDim + j];
+    load(0);
+    store(tiles[0]);
+    if (ntiles > 1) {
+        load(1);
+        store(tiles[1]);
+    }
+    if (ntiles > 2) load(2);
+    __syncthreads();
+
+    // token 0: decay and prediction chain
+    float pred = 0.f;
+    {
+        const float dec = tiles[0].bd[0][1];
+        const float* kn = tiles[0].k[0];
+#pragma unroll
+        for (int i0 = 0; i0 < kGdnDim; i0 += 4) {
+            const float4 k4 = *reinterpret_cast<const float4*>(kn + i0);
+            col[i0 + 0] = col[i0 + 0] * dec;
+            pred = pred + col[i0 + 0] * k4.x;
+            col[i0 + 1] = col[i0 + 1] * dec;
+            pred = pred + col[i0 + 1] * k4.y;
+            col[i0 + 2] = col[i0 + 2] * dec;
+            pred = pred + col[i0 + 2] * k4.z;
+            col[i0 + 3] = col[i0 + 3] * dec;
+            pred = pred + col[i0 + 3] * k4.w;
+        }
+    }
+    for (int t = 0; t < T; ++t) {
+        const int tile = t / kScanTile, r = t % kScanTile;
+        if (r == 0 && tile > 0) {
+            // tile-1's buffer is free: it takes tile+1 (loaded a tile ago)
+            __syncthreads();
+            if (tile + 1 < ntiles) store(tiles[(tile + 1) & 1]);
+            if (tile + 2 < ntiles) load(tile + 2);
+            __syncthreads();
+        }
+        const ScanTile& cur = tiles[tile & 1];
+        const float* qt = cur.q[r];
+        const float* kt = cur.k[r];
+        const float delta = (cur.v[r][j] - pred) * cur.bd[r][0];
+        float o = 0.f;
+        if (t + 1 < T) {
+            const ScanTile& nxt = tiles[((t + 1) / kScanTile) & 1];
+            const int rn = (t + 1) % kScanTile;
+            const float* kn = nxt.k[rn];
+            const float dec = nxt.bd[rn][1];
+            float pn = 0.f;
+#pragma unroll
+            for (int i1 = 0; i1 < kGdnDim; i1 += kScanChunk) {
+                // the shared-memory reads of one chunk stay within it: without
+                // the fence the compiler hoists all 3 x 128 of them
+                scan_fence();
+#pragma unroll
+                for (int i0 = i1; i0 < i1 + kScanChunk; i0 += 4) {
+                    const float4 k4 = *reinterpret_cast<const float4*>(kt + i0);
+                    const float4 q4 = *reinterpret_cast<const float4*>(qt + i0);
+                    const float4 n4 = *reinterpret_cast<const float4*>(kn + i0);
+                    const float kk[4] = {k4.x, k4.y, k4.z, k4.w}, qq[4] = {q4.x, q4.y, q4.z, q4.w}, nn[4] = {n4.x, n4.y, n4.z, n4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float c = col[i0 + e] + kk[e] * delta;  // S[i][j] += k[i] * delta
+                        o = o + c * qq[e];                      // o += S[i][j] * q[i]
+                        c = c * dec;                            // next token: S[i][j] *= decay
+                        pn = pn + c * nn[e];                    //             pred += S[i][j] * k[i]
+                        col[i0 + e] = c;
+                    }
+                }
+            }
+            pred = pn;
+        } else {
+#pragma unroll
+            for (int i1 = 0; i1 < kGdnDim; i1 += kScanChunk) {
+                scan_fence();
+#pragma unroll
+                for (int i0 = i1; i0 < i1 + kScanChunk; i0 += 4) {
+                    const float4 k4 = *reinterpret_cast<const float4*>(kt + i0);
+                    const float4 q4 = *reinterpret_cast<const float4*>(qt + i0);
+                    const float kk[4] = {k4.x, k4.y, k4.z, k4.w}, qq[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float c = col[i0 + e] + kk[e] * delta;
+                        o = o + c * qq[e];
+                        col[i0 + e] = c;
+                    }
+                }
+            }
+        }
+        w.o[(int64_t(t) * a.Hv + h) * kGdnDim + j] = o;
+    }
+    // a fresh base pointer: otherwise the 128 row addresses of the first
+    // loads are kept alive across the token loop for these stores
+    float* Sw = S;
+    __asm__ volatile("" : "+s"(Sw));
+#pragma unroll
+    for (int i = 0; i < kGdnDim; ++i) Sw[i * kGdnDim + j] = col[i];
+}
+
+__global__ __launch_bounds__(kGdnDim) void gdn_out_kernel(GdnDecodeArgs a, void* ws) {
+    const int j = threadIdx.x, h = blockIdx.x, t = blockIdx.y;
+    const int T = a.B;
+    if (a.positions[0] < 0) return;
+    const GdnPrefillWork w = gdn_work(ws, T, a.Hk, a.Hv);
+    __shared__ __align__(16) float ov[kGdnDim];
+    __shared__ float scal;
+    const float o = w.o[(int64_t(t) * a.Hv + h) * kGdnDim + j];
+    const float z = a.proj[int64_t(t) * a.proj_stride + a.z_off + int64_t(h) * kGdnDim + j];
+    ov[j] = o;
+    __syncthreads();
+    // per-head RMSNorm (components.hpp:176-181) and the SiLU(z) gate
+    if (j == 0) scal = 1.f / sqrtf(sum_squares_128(ov) / float(kGdnDim) + a.eps);
+    __syncthreads();
+    const float out = (a.norm_gamma[j] * o * scal) * silu_f32(z);
     const int64_t width = int64_t(a.Hv) * kGdnDim;
     const int64_t idx = int64_t(h) * kGdnDim + j;
-    for (int t = 0; t < T; ++t) {
-        float nxq = 0.f, nxk = 0.f, nxv = 0.f, nz = 0.f, nbi = 0.f, nai = 0.f;
-        if (t + 1 < T) row_in(t + 1, nxq, nxk, nxv, nz, nbi, nai);
-        const float sq = silu_f32(conv_channel<W>(tq, pq, xq));
-        const float sk = silu_f32(conv_channel<W>(tk, pk, xk));
-        const float v = silu_f32(conv_channel<W>(tv, pv, xv));
-        conv_shift<W>(pq, xq);
-        conv_shift<W>(pk, xk);
-        conv_shift<W>(pv, xv);
-        const float out = gdn_token(sh, j, sq, sk, v, bi, ai, A, dtb, gamma, z, a.eps);
-        if (a.out_f32) a.out_f32[int64_t(t) * width + idx] = out;
-        gdn_quantize(out, t, T, width, idx, j, a.act_out);
-        xq = nxq, xk = nxk, xv = nxv, z = nz, bi = nbi, ai = nai;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < kGdnVec; ++k) reinterpret_cast<float4*>(S)[j + kGdnDim * k] = reinterpret_cast<const float4*>(sh)[j + kGdnDim * k];
+    if (a.out_f32) a.out_f32[int64_t(t) * width + idx] = out;
+    gdn_quantize(out, t, T, width, idx, j, a.act_out);
 }
 
 // After a prefill of T tokens at pos0: the ring takes the inputs of the last
@@ -346,18 +525,22 @@ void launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t s) {
     }
 }
 
-void launch_gdn_prefill(const GdnDecodeArgs& a, hipStream_t s) {
-    const dim3 grid(unsigned(a.Hv));
+int64_t gdn_prefill_work_bytes(int64_t T, int64_t Hk, int64_t Hv) { return T * (2 * Hk * kGdnDim + 2 * Hv * kGdnDim + 2 * Hv) * 4; }
+
+void launch_gdn_prefill(const GdnDecodeArgs& a, void* work, hipStream_t s) {
+    const dim3 prep(unsigned(a.Hk + a.Hv), unsigned(a.B));
     switch (a.W) {
-        case 1: hipLaunchKernelGGL(gdn_prefill_kernel<1>, grid, dim3(kGdnDim), kGdnShared, s, a); break;
-        case 2: hipLaunchKernelGGL(gdn_prefill_kernel<2>, grid, dim3(kGdnDim), kGdnShared, s, a); break;
-        case 3: hipLaunchKernelGGL(gdn_prefill_kernel<3>, grid, dim3(kGdnDim), kGdnShared, s, a); break;
-        case 4: hipLaunchKernelGGL(gdn_prefill_kernel<4>, grid, dim3(kGdnDim), kGdnShared, s, a); break;
-        case 5: hipLaunchKernelGGL(gdn_prefill_kernel<5>, grid, dim3(kGdnDim), kGdnShared, s, a); break;
-        case 6: hipLaunchKernelGGL(gdn_prefill_kernel<6>, grid, dim3(kGdnDim), kGdnShared, s, a); break;
-        case 7: hipLaunchKernelGGL(gdn_prefill_kernel<7>, grid, dim3(kGdnDim), kGdnShared, s, a); break;
-        default: hipLaunchKernelGGL(gdn_prefill_kernel<8>, grid, dim3(kGdnDim), kGdnShared, s, a); break;
+        case 1: hipLaunchKernelGGL(gdn_prep_kernel<1>, prep, dim3(kGdnDim), 0, s, a, work); break;
+        case 2: hipLaunchKernelGGL(gdn_prep_kernel<2>, prep, dim3(kGdnDim), 0, s, a, work); break;
+        case 3: hipLaunchKernelGGL(gdn_prep_kernel<3>, prep, dim3(kGdnDim), 0, s, a, work); break;
+        case 4: hipLaunchKernelGGL(gdn_prep_kernel<4>, prep, dim3(kGdnDim), 0, s, a, work); break;
+        case 5: hipLaunchKernelGGL(gdn_prep_kernel<5>, prep, dim3(kGdnDim), 0, s, a, work); break;
+        case 6: hipLaunchKernelGGL(gdn_prep_kernel<6>, prep, dim3(kGdnDim), 0, s, a, work); break;
+        case 7: hipLaunchKernelGGL(gdn_prep_kernel<7>, prep, dim3(kGdnDim), 0, s, a, work); break;
+        default: hipLaunchKernelGGL(gdn_prep_kernel<8>, prep, dim3(kGdnDim), 0, s, a, work); break;
     }
+    hipLaunchKernelGGL(gdn_scan_kernel, dim3(unsigned(a.Hv)), dim3(kGdnDim), 0, s, a, work);
+    hipLaunchKernelGGL(gdn_out_kernel, dim3(unsigned(a.Hv), unsigned(a.B)), dim3(kGdnDim), 0, s, a, work);
     const int64_t CC = 2 * int64_t(a.Hk) * kGdnDim + int64_t(a.Hv) * kGdnDim;
     const int64_t n = int64_t(std::min(a.B, a.W)) * CC;
     hipLaunchKernelGGL(gdn_hist_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, s, a.proj, a.proj_stride, a.conv_hist, CC, a.W, a.positions, a.B);

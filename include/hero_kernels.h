@@ -149,8 +149,10 @@ int hero_gdn_decode(const hero_gdn_decode_args* args, void* stream);
  * that sequence's ([W][CC] and [Hv][Dk][Dv]). The tokens run in order, as the
  * reference's token loop does (nm/src/qwen35.hpp:436-455), so the result equals
  * T calls of hero_gdn_decode bit for bit; the conv ring then holds the chunk's
- * last W positions. */
-int hero_gdn_prefill(const hero_gdn_decode_args* args, void* stream);
+ * last W positions. `work` is device scratch of at least
+ * hero_gdn_prefill_work_bytes(T, hk, hv) bytes. */
+int64_t hero_gdn_prefill_work_bytes(int64_t t, int32_t hk, int32_t hv);
+int hero_gdn_prefill(const hero_gdn_decode_args* args, void* work, int64_t work_bytes, void* stream);
 
 /* Gated GQA attention decode over an fp32 K/V cache, one token for each of
  * B sequences: head-pair split, q/k RMSNorm + RoPE (host table), cache

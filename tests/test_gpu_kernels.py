@@ -389,7 +389,7 @@ def test_gdn_decode_matches_oracle(lib, hk, hv):
             assert np.array_equal(bits(gstate[b]), bits(o_state[b])), f"state after step {step} seq {b}"
 
 
-@pytest.mark.parametrize("W,chunks", [(4, [2, 7, 1, 3, 5]), (3, [1, 1, 6, 2]), (1, [3, 1, 4])])
+@pytest.mark.parametrize("W,chunks", [(4, [2, 7, 1, 3, 5, 40, 17]), (3, [1, 1, 6, 2, 33]), (1, [3, 1, 4, 16])])
 def test_gdn_prefill_chunks_match_oracle(lib, W, chunks):
     """Delta-net prefill in ragged chunks (shorter and longer than the conv
     window, single tokens through the decode entry point in between): every
@@ -414,14 +414,18 @@ def test_gdn_prefill_chunks_match_oracle(lib, W, chunks):
     tmax = max(chunks)
     act = empty(lib.hero_q8_0_act_bytes(tmax, hv * dk))
     out = empty(tmax * hv * dk * 4)
+    work_bytes = lib.hero_gdn_prefill_work_bytes(tmax, hk, hv)
+    work = empty(work_bytes)
     pos = 0
     for i, T in enumerate(chunks):
         proj = (rng.standard_normal((T, stride)) * 0.7).astype(np.float32)
         d_proj, d_pos = dev(proj), dev(np.array([pos], np.int32))
         a = GdnDecodeArgs(ptr(d_proj), stride, cc, cc + hv * dk, cc + hv * dk + hv, ptr(d_taps), ptr(d_hist), ptr(d_state),
                           ptr(d_dt), ptr(d_decay), ptr(d_gamma), eps, ptr(d_pos), ptr(act), ptr(out), T, hk, hv, dk, dk, W)
-        entry = lib.hero_gdn_decode if (T == 1 and i % 2) else lib.hero_gdn_prefill
-        check(entry(a, stream()))
+        if T == 1 and i % 2:
+            check(lib.hero_gdn_decode(a, stream()))
+        else:
+            check(lib.hero_gdn_prefill(a, ptr(work), work_bytes, stream()))
         got = host(out, np.float32, (tmax, hv * dk))[:T]
         got_blocks = act_to_blocks(host(act, np.uint8)[: T * hv * dk + T * hv * dk // 32 * 4], T, hv * dk)
         for t in range(T):

@@ -266,8 +266,11 @@ __global__ __launch_bounds__(kGdnDim) void gdn_decode_kernel(GdnDecodeArgs a) {
 // column, so they run in one pass over i. Every value is computed by the same
 // operations in the same order as in gdn_decode_kernel.
 constexpr int kScanTile = 16;   // tokens staged in shared memory per tile
-constexpr int kScanChunk = 32;  // state rows per fenced step of the token loop
-__device__ __forceinline__ void scan_fence() { __asm__ volatile("" ::: "memory"); }
+constexpr int kScanChunk = 16;  // state rows per fenced step of the token loop
+__device__ __forceinline__ void scan_fence() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);  // and no instruction scheduled across it
+}
 
 __device__ __forceinline__ GdnPrefillWork gdn_work(void* ws, int64_t T, int Hk, int Hv) {
     GdnPrefillWork w;
@@ -428,24 +431,34 @@ __global__ __launch_bounds__(kGdnDim) void gdn_scan_kernel(GdnDecodeArgs a, void
             const float* kn = nxt.k[rn];
             const float dec = nxt.bd[rn][1];
             float pn = 0.f;
+            // k, q and the next k in chunks of kScanChunk rows, the next
+            // chunk's shared-memory reads in flight while this one computes
+            float4 bk[2][kScanChunk / 4], bq[2][kScanChunk / 4], bn[2][kScanChunk / 4];
+            auto fetch = [&](int c, int buf) {
 #pragma unroll
-            for (int i1 = 0; i1 < kGdnDim; i1 += kScanChunk) {
-                // the shared-memory reads of one chunk stay within it: without
-                // the fence the compiler hoists all 3 x 128 of them
+                for (int u = 0; u < kScanChunk / 4; ++u) {
+                    bk[buf][u] = *reinterpret_cast<const float4*>(kt + c * kScanChunk + 4 * u);
+                    bq[buf][u] = *reinterpret_cast<const float4*>(qt + c * kScanChunk + 4 * u);
+                    bn[buf][u] = *reinterpret_cast<const float4*>(kn + c * kScanChunk + 4 * u);
+                }
+            };
+            fetch(0, 0);
+#pragma unroll
+            for (int c = 0; c < kGdnDim / kScanChunk; ++c) {
+                if (c + 1 < kGdnDim / kScanChunk) fetch(c + 1, (c + 1) & 1);
                 scan_fence();
 #pragma unroll
-                for (int i0 = i1; i0 < i1 + kScanChunk; i0 += 4) {
-                    const float4 k4 = *reinterpret_cast<const float4*>(kt + i0);
-                    const float4 q4 = *reinterpret_cast<const float4*>(qt + i0);
-                    const float4 n4 = *reinterpret_cast<const float4*>(kn + i0);
+                for (int u = 0; u < kScanChunk / 4; ++u) {
+                    const float4 k4 = bk[c & 1][u], q4 = bq[c & 1][u], n4 = bn[c & 1][u];
                     const float kk[4] = {k4.x, k4.y, k4.z, k4.w}, qq[4] = {q4.x, q4.y, q4.z, q4.w}, nn[4] = {n4.x, n4.y, n4.z, n4.w};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        float c = col[i0 + e] + kk[e] * delta;  // S[i][j] += k[i] * delta
-                        o = o + c * qq[e];                      // o += S[i][j] * q[i]
-                        c = c * dec;                            // next token: S[i][j] *= decay
-                        pn = pn + c * nn[e];                    //             pred += S[i][j] * k[i]
-                        col[i0 + e] = c;
+                        const int i = c * kScanChunk + 4 * u + e;
+                        float v = col[i] + kk[e] * delta;  // S[i][j] += k[i] * delta
+                        o = o + v * qq[e];                 // o += S[i][j] * q[i]
+                        v = v * dec;                       // next token: S[i][j] *= decay
+                        pn = pn + v * nn[e];               //             pred += S[i][j] * k[i]
+                        col[i] = v;
                     }
                 }
             }
@@ -461,9 +474,9 @@ __global__ __launch_bounds__(kGdnDim) void gdn_scan_kernel(GdnDecodeArgs a, void
                     const float kk[4] = {k4.x, k4.y, k4.z, k4.w}, qq[4] = {q4.x, q4.y, q4.z, q4.w};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const float c = col[i0 + e] + kk[e] * delta;
-                        o = o + c * qq[e];
-                        col[i0 + e] = c;
+                        const float v = col[i0 + e] + kk[e] * delta;
+                        o = o + v * qq[e];
+                        col[i0 + e] = v;
                     }
                 }
             }

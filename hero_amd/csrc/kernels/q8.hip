@@ -566,6 +566,169 @@ __global__ __launch_bounds__(256) void gemm_q8_kernel(const int8_t* __restrict__
         }
 }
 
+// ---------------------------------------------------------------------------
+// Skinny GEMM, 1 < M <= 16 activation rows (batched decode): the weights are
+// streamed once, as in the GEMV, and each block's int32 sums come from the
+// int8 MFMA 16x16x32 (16 activation rows x 16 weight rows x 32 k).
+//
+// A workgroup owns a contiguous range of 16-row weight groups and walks each
+// in rounds of kSkRound blocks; each of the four waves takes 8 blocks of a
+// round. A lane reads 16 bytes of a block pair (b, b+1): lane group q = 0
+// holds bytes 0-15 of b, q = 1 bytes 16-31 of b, q = 2 and 3 the same of
+// b+1, for weight row n = lane % 16 and activation row m = lane % 16. The
+// MFMA sums over all four lane groups, so each block takes two MFMAs (the
+// low, then the high 8 bytes of each lane) with the activation operand
+// zeroed in the lane groups that hold the other block: the int32 result is
+// exactly that block's dot product. A lane turns its 4 results (rows
+// m = 4q + r of column n) into terms float(sumi) * (d_w * d_x) in shared
+// memory; after a barrier lane p = 16 m + n adds the round's terms to its
+// chain in block order (the reference's order), and after the last round
+// stores y. A ring of kSkRing rounds of loads stays in flight.
+// ---------------------------------------------------------------------------
+constexpr int kSkRound = 32;                   // blocks per round
+constexpr int kSkWaveBlocks = kSkRound / 4;    // blocks per wave per round
+constexpr int kSkPairs = kSkWaveBlocks / 2;    // 16-byte loads per lane per round
+constexpr int kSkMaxK = 16384;
+constexpr int kSkRing = 3;                     // steps (group, round) in flight per lane
+// Every global access of the skinny kernel is a raw buffer access: an offset
+// at or past the buffer's size reads 0 and drops a store, so invalid rows,
+// blocks and padded steps need no branch and every loop iteration issues the
+// same memory instructions (which lets the compiler wait for exactly the
+// oldest loads instead of all of them).
+constexpr uint32_t kOOB = 0x80000000u;         // beyond every buffer (sizes < 2 GiB)
+constexpr uint32_t kBufWord3 = 0x00020000u;    // raw dword buffer, gfx9 family
+
+typedef int v4b_t __attribute__((ext_vector_type(4)));
+
+struct SkLoads {
+    v4b_t w[kSkPairs];
+    v4b_t x[kSkPairs];
+    uint32_t d;  // two weight scales of the wave's 8 blocks x 16 rows (see load)
+};
+
+__device__ __forceinline__ long lo64(v4b_t v) { return long((uint64_t(uint32_t(v.y)) << 32) | uint32_t(v.x)); }
+__device__ __forceinline__ long hi64(v4b_t v) { return long((uint64_t(uint32_t(v.w)) << 32) | uint32_t(v.z)); }
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, int(bytes), int(kBufWord3));
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_q8_skinny_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {
+    __shared__ __align__(16) float terms[kSkRound][256];   // [block of the round][16 m + n]
+    extern __shared__ __align__(16) float dxs_raw[];        // [block][m] activation scales, 0 for m >= M
+    float (*dxs)[16] = reinterpret_cast<float (*)[16]>(dxs_raw);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int q = lane >> 4, c = lane & 15;
+    const int nb = K >> 5, rounds = (nb + kSkRound - 1) / kSkRound;
+    const int groups = (N + 15) >> 4, G = gridDim.x;
+    const int g_begin = int(int64_t(groups) * blockIdx.x / G), g_end = int(int64_t(groups) * (blockIdx.x + 1) / G);
+    const int steps = (g_end - g_begin) * rounds;
+    const int steps_pad = (steps + kSkRing - 1) / kSkRing * kSkRing;
+    const __amdgpu_buffer_rsrc_t bw = buffer_of(wq, uint32_t(N) * uint32_t(K));
+    const __amdgpu_buffer_rsrc_t bx = buffer_of(xq, uint32_t(M) * uint32_t(K));
+    const __amdgpu_buffer_rsrc_t bd = buffer_of(wd, uint32_t(nb) * uint32_t(Npad) * 2u);
+    const __amdgpu_buffer_rsrc_t by = buffer_of(y, uint32_t(M) * uint32_t(N) * 4u);
+    for (int e = tid; e < nb * 16; e += 256) {
+        const int b = e >> 4, m = e & 15;
+        dxs[b][m] = m < M ? xd[int64_t(m) * nb + b] : 0.f;
+    }
+
+    // the loads of one step (group, round) for this lane; past the last step
+    // (padding) every offset is out of range
+    auto load = [&](int step, SkLoads& L) {
+        const int g = g_begin + step / rounds, r = step % rounds;
+        const int n = g * 16 + c;
+        const int b0 = r * kSkRound + wv * kSkWaveBlocks;
+        const bool on = step < steps && b0 < nb;  // nb % 8 == 0: a wave's blocks are all in or all out
+        const bool wrow = on && n < N, xrow = on && c < M;
+#pragma unroll
+        for (int i = 0; i < kSkPairs; ++i) {
+            const uint32_t off = uint32_t(b0 + 2 * i) * 32u + 16u * uint32_t(q);
+            L.w[i] = __builtin_amdgcn_raw_buffer_load_b128(bw, wrow ? uint32_t(n) * uint32_t(K) + off : kOOB, 0, 0);
+            L.x[i] = __builtin_amdgcn_raw_buffer_load_b128(bx, xrow ? uint32_t(c) * uint32_t(K) + off : kOOB, 0, 0);
+        }
+        // the wave's 8 x 16 scales in one dword per lane: lane 8j + c' holds
+        // rows 2c', 2c'+1 of block b0 + j (block-major: 16 rows of a block are
+        // contiguous); compute() fetches its own with ds_bpermute
+        const int j = lane >> 3, c2 = 2 * (lane & 7);
+        const bool drow = on && g * 16 + c2 < N;
+        L.d = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(bd, drow ? (uint32_t(b0 + j) * uint32_t(Npad) + uint32_t(g * 16 + c2)) * 2u : kOOB, 0, 0));
+    };
+
+    // a ring of kSkRing steps in flight; slot k is refilled with step s + kSkRing
+    // as soon as step s has been consumed
+    SkLoads ring[kSkRing];
+#pragma unroll
+    for (int k = 0; k < kSkRing; ++k) load(k, ring[k]);
+    __syncthreads();  // dxs
+    float acc = 0.f;
+    for (int s0 = 0; s0 < steps_pad; s0 += kSkRing) {
+#pragma unroll
+        for (int k = 0; k < kSkRing; ++k) {
+            const int s = s0 + k;
+            const int g = g_begin + s / rounds, r = s % rounds;
+            const int b0 = r * kSkRound + wv * kSkWaveBlocks;
+            if (b0 < nb) {
+                const bool first = q < 2;  // lane groups 0, 1 hold block b; 2, 3 hold block b+1
+#pragma unroll
+                for (int i = 0; i < kSkPairs; ++i) {
+                    const long wl = lo64(ring[k].w[i]), wh = hi64(ring[k].w[i]);
+                    const long xl = lo64(ring[k].x[i]), xh = hi64(ring[k].x[i]);
+                    const v4i_t zero = {0, 0, 0, 0};
+                    v4i_t c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(first ? xl : 0L, wl, zero, 0, 0, 0);
+                    c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(first ? xh : 0L, wh, c0, 0, 0, 0);
+                    v4i_t c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(first ? 0L : xl, wl, zero, 0, 0, 0);
+                    c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(first ? 0L : xh, wh, c1, 0, 0, 0);
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const int jb = wv * kSkWaveBlocks + 2 * i + h;  // block within the round
+                        const v4i_t& cc = h ? c1 : c0;
+                        const int jj = 2 * i + h;
+                        const uint32_t two = uint32_t(__builtin_amdgcn_ds_bpermute(4 * (8 * jj + (c >> 1)), int(ring[k].d)));
+                        const float dw = half_bits_to_f32(uint16_t((c & 1) ? (two >> 16) : (two & 0xFFFFu)));
+                        const float4 dx = *reinterpret_cast<const float4*>(&dxs[b0 + 2 * i + h][4 * q]);
+                        // [m][n] with n = lane % 16 fastest: consecutive lanes,
+                        // consecutive banks
+                        terms[jb][(4 * q + 0) * 16 + c] = float(cc[0]) * (dw * dx.x);
+                        terms[jb][(4 * q + 1) * 16 + c] = float(cc[1]) * (dw * dx.y);
+                        terms[jb][(4 * q + 2) * 16 + c] = float(cc[2]) * (dw * dx.z);
+                        terms[jb][(4 * q + 3) * 16 + c] = float(cc[3]) * (dw * dx.w);
+                    }
+                }
+            }
+            load(s + kSkRing, ring[k]);
+            __syncthreads();
+            const int kc = min(kSkRound, nb - r * kSkRound);
+            float tv[kSkRound];  // every read first, then the chain: lane tid = 16 m + n
+#pragma unroll
+            for (int j = 0; j < kSkRound; ++j) tv[j] = terms[j][tid];
+#pragma unroll
+            for (int j = 0; j < kSkRound; ++j)
+                if (j < kc) acc = acc + tv[j];
+            const bool last = r == rounds - 1;
+            const int n = g * 16 + (tid & 15), m = tid >> 4;
+            const bool out = last && s < steps && m < M && n < N;
+            // the b32 buffer builtins move int: the float's bits go through unchanged
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, acc), by, out ? (uint32_t(m) * uint32_t(N) + uint32_t(n)) * 4u : kOOB, 0, 0);
+            acc = last ? 0.f : acc;
+            __syncthreads();
+        }
+    }
+    if constexpr (EPI == kEpiResidual) {
+        // y = r + acc for this workgroup's outputs (the same arithmetic as the
+        // reference's H = X + M); each lane reads back only what it stored
+        __threadfence();
+        for (int g = g_begin; g < g_end; ++g) {
+            const int n = g * 16 + (tid & 15), m = tid >> 4;
+            if (m < M && n < N) {
+                const int64_t o = int64_t(m) * N + n;
+                // aux 1 (sc0): past the L1, from L2 where the store landed
+                y[o] = resid[o] + __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(by, uint32_t(o) * 4u, 0, 1));
+            }
+        }
+    }
+}
+
 namespace {
 template <int BM>
 void gemm_dispatch(int epi, const int8_t* wq, const uint16_t* wd, const int8_t* xq, const float* xd, float* y, const float* resid, int M, int N, int Npad, int K, hipStream_t s) {
@@ -583,7 +746,15 @@ void launch_gemm_q8(const void* packed, const void* act, float* y, const float* 
     const int8_t* xq = static_cast<const int8_t*>(act);
     const float* xd = reinterpret_cast<const float*>(xq + M * K);
     const int Npad = int(packed_rows_pad(N));
-    if (M <= 16)
+    if (M <= 16 && K % 256 == 0 && K <= kSkMaxK && N * K < (int64_t(1) << 31)) {
+        const int64_t groups = (N + 15) / 16;
+        const unsigned G = unsigned(std::min<int64_t>(3 * device_cus(), groups));
+        const size_t smem = size_t(K / 32) * 16 * 4;  // the activation scales
+        if (epi == kEpiResidual)
+            hipLaunchKernelGGL(gemm_q8_skinny_kernel<kEpiResidual>, dim3(G), dim3(256), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
+        else
+            hipLaunchKernelGGL(gemm_q8_skinny_kernel<kEpiStore>, dim3(G), dim3(256), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
+    } else if (M <= 16)
         gemm_dispatch<16>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s);
     else if (M <= 32)
         gemm_dispatch<32>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s);

@@ -1,0 +1,325 @@
+"""hero_amd.microbench -- the kernel microbenchmarks of the hot path on one GPU.
+
+    python -m hero_amd.microbench [--suite gemv,gdn,attn] [--out results.md]
+
+Suites (synthetic, seeded inputs; every launch goes through the C ABI):
+
+gemv   Q8_0 matvec / matmul. W is N x K int8 uniform in [-127, 127] with fp16
+       block scales |N(0, 0.02)| * 4/127; activations are N(0, 1) rows
+       quantized to Q8_0 beforehand. (K, N) in {(4096, 4096), (4096, 12288),
+       (4096, 151936), (12288, 4096)} x M in {1, 8, 64, 512}: M = 1 runs the
+       streaming GEMV, M > 1 the int8-MFMA GEMM. Enough distinct weight copies
+       (>= 512 MB) rotate to keep the 256 MB last-level cache cold.
+gdn    the fused delta-net layer body (conv + SiLU, L2 norms, gates, the delta
+       rule on the fp32 state, head norm, gate, quantize) with 16 heads of
+       128 x 128: one decode step at B in {1, 8, 32} from a state warmed by 64
+       steps, and the bit-exact token-serial prefill of 4096 tokens.
+attn   gated GQA decode (32 q / 8 kv heads of 128, fp32 K/V cache) at context
+       {1k, 8k, 32k} x B {1, 16}: full causal (scale 1/sqrt(128)) and a 1024
+       sliding window (scale 1).
+
+Each case is captured once as a hipGraph (one pass over its inputs) and
+replayed; the time per launch is the replay time divided by the launches,
+so it includes the graph's inter-kernel gaps (about 1.7 us each) and is an
+upper bound on the kernel's own duration (rocprofv3 --kernel-trace --stats
+gives the latter). Algorithmic bytes follow the unit of work of each kernel:
+GEMV/GEMM weights + scales + activations + outputs; delta-net state read and
+write plus its per-token inputs and outputs; attention the visible K and V
+rows plus q and the output.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import sys
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def _stream() -> int:
+    return _torch().cuda.current_stream().cuda_stream
+
+
+def _p(t) -> int:
+    return t.data_ptr()
+
+
+def _bytes(n: int):
+    t = _torch()
+    return t.empty(int(n), dtype=t.uint8, device="cuda")
+
+
+def _time_graph(body, launches: int, replays: int, budget_s: float = 1.0) -> float:
+    """seconds per launch of `body` (which makes `launches` launches), from
+    hipGraph replays timed with events on the replay stream; at most
+    `replays` replays and about `budget_s` seconds of them"""
+    t = _torch()
+    body()  # warm: code objects, caches
+    t.cuda.synchronize()
+    g = t.cuda.CUDAGraph()
+    s = t.cuda.Stream()
+    s.wait_stream(t.cuda.current_stream())
+    with t.cuda.stream(s):
+        with t.cuda.graph(g, stream=s):
+            body()
+    t.cuda.synchronize()
+    e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    e1.synchronize()
+    once = e0.elapsed_time(e1) * 1e-3
+    n = max(1, min(replays, int(budget_s / max(once, 1e-9))))
+    e0.record()
+    for _ in range(n):
+        g.replay()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / (n * launches)
+
+
+# ---- Q8_0 GEMV / GEMM ----------------------------------------------------------------------
+GEMV_SHAPES = [(4096, 4096), (4096, 12288), (4096, 151936), (12288, 4096)]
+GEMV_BATCHES = [1, 8, 64, 512]
+
+
+def _q8_weight_copies(lib, n: int, k: int, copies: int, gen):
+    """`copies` packed Q8_0 weights of the benchmark distribution"""
+    from ._lib import check
+
+    t = _torch()
+    nb = n * (k // 32)
+    out = []
+    for _ in range(copies):
+        qs = t.randint(-127, 128, (nb, 32), dtype=t.int8, device="cuda", generator=gen)
+        d = (t.randn(nb, device="cuda", generator=gen).abs() * (0.02 * 4 / 127)).half()
+        blocks = t.cat([d.view(t.uint8).view(nb, 2), qs.view(t.uint8)], dim=1).contiguous()
+        packed = _bytes(lib.hero_q8_0_packed_bytes(n, k))
+        check(lib.hero_q8_0_pack(_p(blocks), _p(packed), n, k, 0, n, _stream()))
+        del blocks, qs, d
+        out.append(packed)
+    t.cuda.synchronize()
+    return out
+
+
+def bench_gemv(lib, replays: int = 20):
+    from ._lib import check
+
+    t = _torch()
+    gen = t.Generator(device="cuda")
+    gen.manual_seed(1234)
+    rows = []
+    for k, n in GEMV_SHAPES:
+        wbytes = n * k * 34 // 32
+        copies = max(1, math.ceil(512e6 / wbytes))
+        weights = _q8_weight_copies(lib, n, k, copies, gen)
+        for m in GEMV_BATCHES:
+            x = t.randn(m, k, device="cuda", generator=gen)
+            act = _bytes(lib.hero_q8_0_act_bytes(m, k))
+            check(lib.hero_q8_0_quantize(_p(x), _p(act), m, k, _stream()))
+            y = t.empty(m, n, device="cuda")
+
+            def body():
+                for w in weights:
+                    if m == 1:
+                        check(lib.hero_q8_0_gemv(_p(w), _p(act), _p(y), None, n, k, _stream()))
+                    else:
+                        check(lib.hero_q8_0_gemm(_p(w), _p(act), _p(y), None, m, n, k, _stream()))
+
+            sec = _time_graph(body, len(weights), replays)
+            nbytes = wbytes + m * k * 4 + m * n * 4  # the unit of work: weights + fp32 x in + fp32 y out
+            ops = 2.0 * m * n * k
+            rows.append({
+                "suite": "gemv", "kernel": "gemv_q8_stream" if m == 1 else "gemm_q8 (int8 MFMA)",
+                "K": k, "N": n, "M": m, "copies": copies, "us": sec * 1e6,
+                "GB/s": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS,
+                "TOPS": ops / sec / 1e12, "int8_frac": ops / sec / 1e12 / INT8_PEAK_TOPS,
+            })
+            print(json.dumps(rows[-1]), flush=True)
+            del act, y, x
+        del weights
+        t.cuda.empty_cache()
+    return rows
+
+
+# ---- gated delta-net -----------------------------------------------------------------------------
+def _gdn_case(lib, hk: int, hv: int, B: int, W: int, gen):
+    from ._lib import GdnDecodeArgs
+
+    t = _torch()
+    dk = 128
+    cc = 2 * hk * dk + hv * dk
+    stride = cc + hv * dk + 2 * hv
+    bufs = {
+        "taps": (t.randn(cc, W, device="cuda", generator=gen) * 0.5),
+        "dt": t.randn(hv, device="cuda", generator=gen) * 0.1,
+        "decay": -t.exp(t.randn(hv, device="cuda", generator=gen) * 0.5),
+        "gamma": 1 + 0.1 * t.randn(dk, device="cuda", generator=gen),
+        "hist": t.zeros(B * W * cc, device="cuda"),
+        "state": t.zeros(B * hv * dk * dk, device="cuda"),
+        "proj": t.randn(B, stride, device="cuda", generator=gen),
+        "act": _bytes(lib.hero_q8_0_act_bytes(B, hv * dk)),
+        "pos": t.zeros(B, dtype=t.int32, device="cuda"),
+    }
+    a = GdnDecodeArgs(_p(bufs["proj"]), stride, cc, cc + hv * dk, cc + hv * dk + hv, _p(bufs["taps"]), _p(bufs["hist"]),
+                      _p(bufs["state"]), _p(bufs["dt"]), _p(bufs["decay"]), _p(bufs["gamma"]), 1e-6, _p(bufs["pos"]),
+                      _p(bufs["act"]), None, B, hk, hv, dk, dk, W)
+    return a, bufs
+
+
+def bench_gdn(lib, replays: int = 50):
+    from ._lib import check
+
+    t = _torch()
+    gen = t.Generator(device="cuda")
+    gen.manual_seed(4321)
+    rows = []
+    H, W, dk = 16, 4, 128
+    for B in (1, 8, 32):
+        a, bufs = _gdn_case(lib, H, H, B, W, gen)
+        for step in range(64):  # a seeded non-zero state
+            bufs["pos"].fill_(step)
+            check(lib.hero_gdn_decode(a, _stream()))
+        bufs["pos"].fill_(64)
+        sec = _time_graph(lambda: check(lib.hero_gdn_decode(a, _stream())), 1, replays)
+        nbytes = B * H * dk * dk * 4 * 2 + B * H * (3 * 128 + 2) * 4 + B * H * 128 * 4
+        rows.append({"suite": "gdn", "kernel": "gdn_decode (fused layer body)", "mode": "decode", "H": H, "B": B,
+                     "us": sec * 1e6, "GB/s": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS})
+        print(json.dumps(rows[-1]), flush=True)
+        del bufs
+    T = 4096
+    a, bufs = _gdn_case(lib, H, H, T, W, gen)
+    wb = lib.hero_gdn_prefill_work_bytes(T, H, H)
+    work = _bytes(wb)
+
+    def prefill():
+        bufs["state"].zero_()
+        bufs["hist"].zero_()
+        check(lib.hero_gdn_prefill(a, _p(work), wb, _stream()))
+
+    prefill()
+    t.cuda.synchronize()
+    e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+    reps = 5
+    e0.record()
+    for _ in range(reps):
+        prefill()
+    e1.record()
+    e1.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / reps
+    serial_flops = 7.0 * T * H * dk * dk
+    rows.append({"suite": "gdn", "kernel": "gdn_prefill (prep + token-serial scan + out, bit-exact)", "mode": "prefill",
+                 "H": H, "T": T, "us": sec * 1e6, "tok/s": T / sec, "GFLOP/s (serial-equivalent)": serial_flops / sec / 1e9})
+    print(json.dumps(rows[-1]), flush=True)
+    return rows
+
+
+# ---- GQA decode attention ------------------------------------------------------------------------
+def bench_attn(lib, replays: int = 20):
+    from ._lib import AttnDecodeArgs, check
+
+    t = _torch()
+    gen = t.Generator(device="cuda")
+    gen.manual_seed(999)
+    rows = []
+    hq, hkv, dh = 32, 8, 128
+    qw, kw = hq * dh, hkv * dh
+    stride = 2 * qw + 2 * kw
+    for ctx in (1024, 8192, 32768):
+        for B in (1, 16):
+            cache_bytes = B * ctx * kw * 4 * 2
+            copies = max(1, min(16, math.ceil(512e6 / cache_bytes)))
+            scale = 1.0 / math.sqrt(dh)
+            caches = []
+            for _ in range(copies):
+                kc = t.randn(B * ctx * kw, device="cuda", generator=gen) * scale
+                vc = t.randn(B * ctx * kw, device="cuda", generator=gen) * scale
+                caches.append((kc, vc))
+            proj = t.randn(B, stride, device="cuda", generator=gen) * scale
+            gq, gk = t.ones(dh, device="cuda"), t.ones(dh, device="cuda")
+            cs = t.zeros(ctx, dh // 2, 2, device="cuda")
+            cs[..., 0] = 1.0
+            pos = t.full((B,), ctx - 1, dtype=t.int32, device="cuda")
+            scores = t.empty(B * hq * ctx, device="cuda")
+            qrot = t.empty(B * qw, device="cuda")
+            act = _bytes(lib.hero_q8_0_act_bytes(B, qw))
+            for name, window, sc in (("full", 0, scale), ("swa1024", 1024, 1.0)):
+                args = [AttnDecodeArgs(_p(proj), stride, 2 * qw, 2 * qw + kw, _p(gq), _p(gk), 1e-6, _p(cs), _p(kc), _p(vc), ctx,
+                                       _p(pos), _p(scores), _p(qrot), sc, window, _p(act), None, B, hq, hkv, dh)
+                        for kc, vc in caches]
+
+                def body():
+                    for a in args:
+                        check(lib.hero_attn_decode(a, _stream()))
+
+                sec = _time_graph(body, len(args), replays)
+                l_eff = ctx if window == 0 else min(ctx, window)
+                nbytes = B * l_eff * kw * 4 * 2 + B * (qw + 2 * kw + qw) * 4
+                rows.append({"suite": "attn", "kernel": "attn_decode (prep + scores + softmax + pv), fp32 K/V",
+                             "variant": name, "ctx": ctx, "B": B, "copies": copies, "us": sec * 1e6,
+                             "GB/s": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS})
+                print(json.dumps(rows[-1]), flush=True)
+            del caches, scores
+            t.cuda.empty_cache()
+    return rows
+
+
+def _markdown(rows) -> str:
+    out = []
+    for suite in ("gemv", "gdn", "attn"):
+        rs = [r for r in rows if r["suite"] == suite]
+        if not rs:
+            continue
+        keys = [k for k in rs[0] if k != "suite"]
+        for r in rs[1:]:
+            keys += [k for k in r if k not in keys and k != "suite"]
+        out.append(f"### {suite}\n")
+        out.append("| " + " | ".join(keys) + " |")
+        out.append("|" + "---|" * len(keys))
+        for r in rs:
+            cells = []
+            for k in keys:
+                v = r.get(k, "")
+                cells.append(f"{v:.4g}" if isinstance(v, float) else str(v))
+            out.append("| " + " | ".join(cells) + " |")
+        out.append("")
+    return "\n".join(out)
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--suite", default="gemv,gdn,attn")
+    ap.add_argument("--out", default=None, help="write a markdown table here")
+    args = ap.parse_args(argv)
+    t = _torch()
+    if not t.cuda.is_available():
+        print("microbench: needs a GPU", file=sys.stderr)
+        return 2
+    from ._lib import lib
+
+    rows = []
+    suites = args.suite.split(",")
+    if "gemv" in suites:
+        rows += bench_gemv(lib)
+    if "gdn" in suites:
+        rows += bench_gdn(lib)
+    if "attn" in suites:
+        rows += bench_attn(lib)
+    md = _markdown(rows)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(md + "\n")
+    print(md, file=sys.stderr)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -26,7 +26,7 @@ from ._lib import ContextExhausted, HeroError, ModelDims, SynthConfig, check, li
 
 __all__ = [
     "ContextExhausted", "HeroError", "Logits", "Qwen35Model", "PrefixState", "PrefixCache",
-    "EmbeddedSequence", "TINY_CONFIG", "HYBRID_8B_CONFIG", "synth_config", "write_synthetic_gguf",
+    "EmbeddedSequence", "BatchState", "TINY_CONFIG", "HYBRID_8B_CONFIG", "synth_config", "write_synthetic_gguf",
     "synthetic_gguf_image", "lib",
 ]
 
@@ -61,6 +61,36 @@ class PrefixState:
 
     def tokens(self) -> int:
         return int(lib.hero_state_tokens(self._h))
+
+    def reset(self) -> None:
+        check(lib.hero_state_reset(self._h))
+
+    def close(self) -> None:
+        if self._h:
+            lib.hero_state_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class BatchState:
+    """`batch` independent sequences in one device state, decoded together
+    (no counterpart in the reference, which carries one sequence per state)."""
+
+    def __init__(self, model: "Qwen35Model", max_tokens: int, batch: int):
+        h = c_void_p()
+        check(lib.hero_batch_state_create(model._h, max_tokens, batch, byref(h)))
+        self._h = h
+        self.model = model
+        self.max_tokens = max_tokens
+        self.batch = batch
+
+    def tokens(self, seq: int) -> int:
+        return int(lib.hero_state_seq_tokens(self._h, seq))
 
     def reset(self) -> None:
         check(lib.hero_state_reset(self._h))
@@ -114,6 +144,31 @@ class Qwen35Model:
 
     def new_state(self, max_tokens: int | None = None) -> PrefixState:
         return PrefixState(self, max_tokens or min(self.CTX, 4096))
+
+    def new_batch_state(self, max_tokens: int, batch: int) -> BatchState:
+        return BatchState(self, max_tokens, batch)
+
+    def forward_seq(self, state: BatchState, seq: int, rows: np.ndarray | None = None, ids=None, want_logits: bool = True) -> Logits | int:
+        """forward() for sequence `seq` of a batch state."""
+        logits = np.empty(self.V, dtype=np.float32) if want_logits else None
+        nxt = c_int32(-1)
+        if rows is not None:
+            rows = np.ascontiguousarray(rows, dtype=np.float32).reshape(-1, self.D)
+            check(lib.hero_model_forward_seq(self._h, state._h, seq, _ptr(rows), None, rows.shape[0], _ptr(logits) if want_logits else None, byref(nxt)))
+        else:
+            ids = np.ascontiguousarray(ids, dtype=np.int32)
+            check(lib.hero_model_forward_seq(self._h, state._h, seq, None, _ptr(ids), len(ids), _ptr(logits) if want_logits else None, byref(nxt)))
+        return Logits(logits) if want_logits else int(nxt.value)
+
+    def decode_batch(self, state: BatchState, first_ids, steps: int, want_logits: bool = False):
+        """Greedy decode of every sequence at once (one hipGraph replay per
+        pass). Returns (ids[steps][B], logits [B][V] of the last pass)."""
+        first = np.ascontiguousarray(first_ids, dtype=np.int32)
+        assert first.shape == (state.batch,)
+        out = np.empty((steps, state.batch), dtype=np.int32)
+        logits = np.empty((state.batch, self.V), dtype=np.float32) if want_logits else None
+        check(lib.hero_model_decode_batch(self._h, state._h, _ptr(first), steps, _ptr(out), _ptr(logits) if want_logits else None))
+        return out, logits
 
     def embed(self, ids) -> np.ndarray:
         ids = np.ascontiguousarray(ids, dtype=np.int32)

@@ -98,6 +98,11 @@ SIGNATURES = {
     "hero_state_destroy": (None, [c_void_p]),
     "hero_state_reset": (c_int, [c_void_p]),
     "hero_state_tokens": (c_int64, [c_void_p]),
+    "hero_batch_state_create": (c_int, [c_void_p, c_int64, c_int32, POINTER(c_void_p)]),
+    "hero_state_batch": (c_int64, [c_void_p]),
+    "hero_state_seq_tokens": (c_int64, [c_void_p, c_int32]),
+    "hero_model_forward_seq": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+    "hero_model_decode_batch": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
     "hero_model_embed": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
     "hero_model_forward": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
     "hero_model_decode_greedy": (c_int, [c_void_p, c_void_p, c_int32, c_int64, c_void_p, c_void_p]),

@@ -81,6 +81,7 @@ struct LayerWeights {
 class Qwen35Model {
 public:
     class State;
+    static constexpr int64_t kMaxBatch = 16;  // sequences per state (the skinny GEMM's rows)
 
     static std::unique_ptr<Qwen35Model> open(const std::string& gguf_path);
     static std::unique_ptr<Qwen35Model> open_image(const uint8_t* image, uint64_t size);
@@ -92,13 +93,19 @@ public:
     int64_t device_bytes() const { return device_bytes_; }
     hipStream_t stream() const { return stream_; }
 
-    std::unique_ptr<State> new_state(int64_t max_tokens) const;
+    // `batch` independent sequences of up to `max_tokens` each
+    std::unique_ptr<State> new_state(int64_t max_tokens, int64_t batch = 1) const;
     // host rows out[n][D]
     void embed(const int32_t* ids, int64_t n, float* out) const;
     // T rows from host `rows` or from `ids`; logits / greedy id of the last row
     void forward(State& s, const float* rows, const int32_t* ids, int64_t T, float* logits, int32_t* next_id) const;
+    // the same for sequence `seq` of a batch state
+    void forward_seq(State& s, int64_t seq, const float* rows, const int32_t* ids, int64_t T, float* logits, int32_t* next_id) const;
     // greedy loop from `first_id`; out_ids[steps] on the host
     void decode_greedy(State& s, int32_t first_id, int64_t steps, int32_t* out_ids, float* logits) const;
+    // greedy loop of every sequence of a batch state at once, each from its own
+    // position: first_ids[B]; out_ids[steps][B]; logits [B][V] of the last pass
+    void decode_batch(State& s, const int32_t* first_ids, int64_t steps, int32_t* out_ids, float* logits) const;
     double last_decode_seconds() const { return last_decode_seconds_; }
     // Every Q8_0 matvec of one decode step (all layers + LM head), `reps`
     // times back to back, between two events on the model's stream.
@@ -117,7 +124,10 @@ private:
     // state's chunk input rows: each layer as batched GEMMs around the
     // token-serial delta-net and the causal attention; `with_head` adds the
     // final norm, LM head and argmax of the last row
-    void enqueue_chunk(State& s, int64_t pos0, int64_t T, bool with_head) const;
+    void enqueue_chunk(State& s, int64_t seq, int64_t pos0, int64_t T, bool with_head) const;
+    // one token of every sequence of a batch state (positions and ids on the
+    // device): the matvecs as skinny GEMMs over the B rows
+    void enqueue_batch_step(State& s) const;
     // rows per prefill chunk: at most 512, and the chunk's attention scores
     // (rows x query heads x max_tokens fp32) within 256 MiB
     int64_t chunk_rows(const State& s) const;
@@ -138,16 +148,22 @@ private:
 class Qwen35Model::State {
 public:
     ~State();
-    int64_t tokens() const { return tokens_; }
+    int64_t tokens() const { return seq_tokens_[0]; }
+    int64_t tokens(int64_t seq) const { return seq_tokens_.at(size_t(seq)); }
     int64_t max_tokens() const { return max_tokens_; }
+    int64_t batch() const { return batch_; }
     void reset();
 
 private:
     friend class Qwen35Model;
-    explicit State(const Qwen35Model& m, int64_t max_tokens);
+    explicit State(const Qwen35Model& m, int64_t max_tokens, int64_t batch);
 
     const Qwen35Model& m_;
-    int64_t tokens_ = 0, max_tokens_ = 0;
+    int64_t max_tokens_ = 0, batch_ = 1;
+    std::vector<int64_t> seq_tokens_;
+    // batch step scalars: [0, B) positions, [B, 2B) token ids, [2B] step counter
+    DeviceBuffer bstep_;
+    hipGraphExec_t bgraph_ = nullptr;  // one batch greedy step, replayed
     // per-step device scalars: [0] position, [1] token id, [2] step counter
     DeviceBuffer step_;
     DeviceBuffer x_, h_, proj_, act_d_, act_mix_, act_ff_, gate_up_, logits_, argmax_scratch_, out_ids_, q_rot_;
@@ -157,6 +173,7 @@ private:
     DeviceBuffer cx_, ch_, cproj_, cact_d_, cact_mix_, cgate_up_, cact_ff_, cq_rot_, cscores_, cpos_, cids_, cgdn_work_;
     int64_t chunk_capacity_ = 0;
     void ensure_chunk(int64_t rows);
+    // per layer, every sequence's: [B][...]
     std::vector<DeviceBuffer> k_cache_, v_cache_, scores_, conv_hist_, delta_;
     hipGraphExec_t graph_ = nullptr;  // one greedy decode step, replayed
 };

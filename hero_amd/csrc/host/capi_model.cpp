@@ -100,6 +100,22 @@ int hero_state_create(const hero_model* model, int64_t max_tokens, hero_state** 
     });
 }
 
+int hero_batch_state_create(const hero_model* model, int64_t max_tokens, int32_t batch, hero_state** out) {
+    return guard([&] {
+        need(model && out, "null argument");
+        auto s = std::make_unique<hero_state>();
+        s->impl = model->impl->new_state(max_tokens, batch);
+        *out = s.release();
+    });
+}
+
+int64_t hero_state_batch(const hero_state* state) { return state ? state->impl->batch() : -1; }
+
+int64_t hero_state_seq_tokens(const hero_state* state, int32_t seq) {
+    if (!state || seq < 0 || seq >= state->impl->batch()) return -1;
+    return state->impl->tokens(seq);
+}
+
 void hero_state_destroy(hero_state* state) { delete state; }
 
 int hero_state_reset(hero_state* state) {
@@ -122,6 +138,20 @@ int hero_model_forward(const hero_model* model, hero_state* state, const float* 
     return guard([&] {
         need(model && state, "null argument");
         model->impl->forward(*state->impl, rows, ids, t, logits, next_id);
+    });
+}
+
+int hero_model_forward_seq(const hero_model* model, hero_state* state, int32_t seq, const float* rows, const int32_t* ids, int64_t t, float* logits, int32_t* next_id) {
+    return guard([&] {
+        need(model && state, "null argument");
+        model->impl->forward_seq(*state->impl, seq, rows, ids, t, logits, next_id);
+    });
+}
+
+int hero_model_decode_batch(const hero_model* model, hero_state* state, const int32_t* first_ids, int64_t steps, int32_t* out_ids, float* logits) {
+    return guard([&] {
+        need(model && state && first_ids && out_ids, "null argument");
+        model->impl->decode_batch(*state->impl, first_ids, steps, out_ids, logits);
     });
 }
 

@@ -22,6 +22,7 @@
 // per-row arithmetic as T single steps, so the two agree bit for bit.
 #include "hero/model.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -43,6 +44,17 @@ __global__ void set_step_kernel(int32_t* step, int32_t position, int32_t token, 
 __global__ void positions_kernel(int32_t* pos, int32_t pos0, int32_t n) {
     const int32_t i = int32_t(blockIdx.x * blockDim.x + threadIdx.x);
     if (i < n) pos[i] = pos0 + i;
+}
+// batch: bstep[0, B) positions, [B, 2B) token ids, [2B] step counter
+__global__ void advance_batch_kernel(int32_t* bstep, int32_t* out_ids, int32_t B) {
+    int32_t* pos = bstep;
+    const int32_t* ids = bstep + B;
+    int32_t* counter = bstep + 2 * B;
+    for (int32_t b = 0; b < B; ++b) {
+        pos[b] += 1;
+        out_ids[int64_t(*counter) * B + b] = ids[b];
+    }
+    *counter += 1;
 }
 __global__ void advance_step_kernel(int32_t* step, int32_t* out_ids, int32_t record) {
     step[0] += 1;
@@ -282,40 +294,43 @@ void Qwen35Model::build_rope_table(int64_t positions) {
 }
 
 // ---- state --------------------------------------------------------------------------
-std::unique_ptr<Qwen35Model::State> Qwen35Model::new_state(int64_t max_tokens) const {
+std::unique_ptr<Qwen35Model::State> Qwen35Model::new_state(int64_t max_tokens, int64_t batch) const {
     if (max_tokens <= 0 || max_tokens > c_.CTX || max_tokens > rope_positions_) throw Error(HERO_ERANGE, "state: max_tokens must be in 1.." + std::to_string(std::min(c_.CTX, rope_positions_)));
-    return std::unique_ptr<State>(new State(*this, max_tokens));
+    if (batch < 1 || batch > kMaxBatch) throw Error(HERO_EINVAL, "state: batch must be in 1.." + std::to_string(kMaxBatch));
+    return std::unique_ptr<State>(new State(*this, max_tokens, batch));
 }
 
-Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens) : m_(m), max_tokens_(max_tokens) {
+Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batch) : m_(m), max_tokens_(max_tokens), batch_(batch), seq_tokens_(size_t(batch), 0) {
     const ModelConfig& c = m.c_;
+    const int64_t B = batch;
     int64_t n_in_max = 0;
     for (const LayerWeights& L : m.layers_) n_in_max = std::max(n_in_max, L.n_in);
     step_ = DeviceBuffer(16);
-    x_ = DeviceBuffer(size_t(c.D) * 4);
-    h_ = DeviceBuffer(size_t(c.D) * 4);
+    bstep_ = DeviceBuffer(size_t(2 * B + 4) * 4);
+    x_ = DeviceBuffer(size_t(B * c.D) * 4);
+    h_ = DeviceBuffer(size_t(B * c.D) * 4);
     gemv_scratch_ = DeviceBuffer(size_t(c.D) * 4);
-    proj_ = DeviceBuffer(size_t(n_in_max) * 4);
-    act_d_ = DeviceBuffer(size_t(act_q8_bytes(1, c.D)));
-    act_mix_ = DeviceBuffer(size_t(act_q8_bytes(1, std::max(c.q_width(), c.v_width()))));
-    act_ff_ = DeviceBuffer(size_t(act_q8_bytes(1, c.FF)));
-    gate_up_ = DeviceBuffer(size_t(2 * c.FF) * 4);
-    logits_ = DeviceBuffer(size_t(c.V) * 4);
-    argmax_scratch_ = DeviceBuffer(128 * 8);
-    out_ids_ = DeviceBuffer(size_t(max_tokens) * 4);
-    q_rot_ = DeviceBuffer(size_t(c.q_width()) * 4);
+    proj_ = DeviceBuffer(size_t(B * n_in_max) * 4);
+    act_d_ = DeviceBuffer(size_t(act_q8_bytes(B, c.D)));
+    act_mix_ = DeviceBuffer(size_t(act_q8_bytes(B, std::max(c.q_width(), c.v_width()))));
+    act_ff_ = DeviceBuffer(size_t(act_q8_bytes(B, c.FF)));
+    gate_up_ = DeviceBuffer(size_t(B * 2 * c.FF) * 4);
+    logits_ = DeviceBuffer(size_t(B * c.V) * 4);
+    argmax_scratch_ = DeviceBuffer(size_t(B) * 128 * 8);
+    out_ids_ = DeviceBuffer(size_t(max_tokens * B) * 4);
+    q_rot_ = DeviceBuffer(size_t(B * c.q_width()) * 4);
     out_ids_capacity_ = max_tokens;
     for (int64_t l = 0; l < c.L; ++l) {
         if (c.is_recurrent(l)) {
             k_cache_.emplace_back();
             v_cache_.emplace_back();
             scores_.emplace_back();
-            conv_hist_.emplace_back(size_t(c.W * c.conv_channels()) * 4);
-            delta_.emplace_back(size_t(c.Hv * c.Dk * c.Dv) * 4);
+            conv_hist_.emplace_back(size_t(B * c.W * c.conv_channels()) * 4);
+            delta_.emplace_back(size_t(B * c.Hv * c.Dk * c.Dv) * 4);
         } else {
-            k_cache_.emplace_back(size_t(max_tokens * c.kv_width()) * 4);
-            v_cache_.emplace_back(size_t(max_tokens * c.kv_width()) * 4);
-            scores_.emplace_back(size_t(max_tokens * c.Hq) * 4);
+            k_cache_.emplace_back(size_t(B * max_tokens * c.kv_width()) * 4);
+            v_cache_.emplace_back(size_t(B * max_tokens * c.kv_width()) * 4);
+            scores_.emplace_back(size_t(B * max_tokens * c.Hq) * 4);
             conv_hist_.emplace_back();
             delta_.emplace_back();
         }
@@ -325,6 +340,7 @@ Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens) : m_(m), max
 
 Qwen35Model::State::~State() {
     if (graph_) (void)hipGraphExecDestroy(graph_);
+    if (bgraph_) (void)hipGraphExecDestroy(bgraph_);
 }
 
 void Qwen35Model::State::reset() {
@@ -337,8 +353,9 @@ void Qwen35Model::State::reset() {
     for (auto& b : conv_hist_) zero(b);
     for (auto& b : delta_) zero(b);
     zero(step_);
+    zero(bstep_);
     hip_check(hipStreamSynchronize(s), "state reset");
-    tokens_ = 0;
+    std::fill(seq_tokens_.begin(), seq_tokens_.end(), 0);
 }
 
 int64_t Qwen35Model::chunk_rows(const State& st) const {
@@ -494,7 +511,7 @@ void Qwen35Model::enqueue_step(State& st, bool from_ids, bool with_head) const {
     check_launch("decode step");
 }
 
-void Qwen35Model::enqueue_chunk(State& st, int64_t pos0, int64_t T, bool with_head) const {
+void Qwen35Model::enqueue_chunk(State& st, int64_t seq, int64_t pos0, int64_t T, bool with_head) const {
     const ModelConfig& c = c_;
     hipStream_t s = stream_;
     float* x = st.cx_.get<float>();
@@ -516,8 +533,8 @@ void Qwen35Model::enqueue_chunk(State& st, int64_t pos0, int64_t T, bool with_he
             a.beta_off = L.beta_off;
             a.alpha_off = L.alpha_off;
             a.conv_taps = L.conv.get<float>();
-            a.conv_hist = st.conv_hist_[size_t(l)].get<float>();
-            a.state = st.delta_[size_t(l)].get<float>();
+            a.conv_hist = st.conv_hist_[size_t(l)].get<float>() + seq * c.W * c.conv_channels();
+            a.state = st.delta_[size_t(l)].get<float>() + seq * c.Hv * c.Dk * c.Dv;
             a.dt_bias = L.dt_bias.get<float>();
             a.decay = L.decay.get<float>();
             a.norm_gamma = L.ssm_norm.get<float>();
@@ -543,8 +560,8 @@ void Qwen35Model::enqueue_chunk(State& st, int64_t pos0, int64_t T, bool with_he
             a.k_gamma = L.k_norm.get<float>();
             a.eps = c.eps;
             a.rope_cs = rope_cs_.get<float>();
-            a.k_cache = st.k_cache_[size_t(l)].get<float>();
-            a.v_cache = st.v_cache_[size_t(l)].get<float>();
+            a.k_cache = st.k_cache_[size_t(l)].get<float>() + seq * st.max_tokens_ * c.kv_width();
+            a.v_cache = st.v_cache_[size_t(l)].get<float>() + seq * st.max_tokens_ * c.kv_width();
             a.max_ctx = st.max_tokens_;
             a.positions = pos;
             a.shared_cache = 1;
@@ -576,18 +593,25 @@ void Qwen35Model::enqueue_chunk(State& st, int64_t pos0, int64_t T, bool with_he
 }
 
 void Qwen35Model::forward(State& st, const float* rows, const int32_t* ids, int64_t T, float* logits, int32_t* next_id) const {
+    if (st.batch_ != 1) throw Error(HERO_EINVAL, "forward: a batch state takes forward_seq");
+    forward_seq(st, 0, rows, ids, T, logits, next_id);
+}
+
+void Qwen35Model::forward_seq(State& st, int64_t seq, const float* rows, const int32_t* ids, int64_t T, float* logits, int32_t* next_id) const {
     const ModelConfig& c = c_;
     if (&st.m_ != this) throw Error(HERO_EINVAL, "forward: state belongs to another model");
+    if (seq < 0 || seq >= st.batch_) throw Error(HERO_EINVAL, "forward: sequence index out of range");
     if (T <= 0) throw Error(HERO_EINVAL, "forward: empty input");
     if (!rows && !ids) throw Error(HERO_EINVAL, "forward: need rows or ids");
-    if (T > st.max_tokens_ - st.tokens_) throw Error(HERO_ERANGE, "Qwen35Model: context exhausted");
+    const int64_t pos0 = st.seq_tokens_[size_t(seq)];
+    if (T > st.max_tokens_ - pos0) throw Error(HERO_ERANGE, "Qwen35Model: context exhausted");
     if (ids)
         for (int64_t t = 0; t < T; ++t)
             if (ids[t] < 0 || ids[t] >= c.V) throw Error(HERO_EINVAL, "forward: token id out of range");
     hipStream_t s = stream_;
     try {
-        if (T == 1) {
-            hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, s, st.step_.get<int32_t>(), int32_t(st.tokens_), ids ? ids[0] : -1, 0);
+        if (T == 1 && st.batch_ == 1) {
+            hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, s, st.step_.get<int32_t>(), int32_t(pos0), ids ? ids[0] : -1, 0);
             if (rows) hip_check(hipMemcpyAsync(st.x_.get(), rows, size_t(c.D) * 4, hipMemcpyHostToDevice, s), "row upload");
             enqueue_step(st, rows == nullptr, true);
         } else {
@@ -601,17 +625,17 @@ void Qwen35Model::forward(State& st, const float* rows, const int32_t* ids, int6
                     hip_check(hipMemcpyAsync(st.cids_.get(), ids + t0, size_t(n) * 4, hipMemcpyHostToDevice, s), "ids upload");
                     launch_embed_q8(embedding_.get(), c.V, c.D, st.cids_.get<int32_t>(), n, st.cx_.get<float>(), s);
                 }
-                enqueue_chunk(st, st.tokens_ + t0, n, t0 + n == T);
+                enqueue_chunk(st, seq, pos0 + t0, n, t0 + n == T);
             }
             // the position of the next single step
-            hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, s, st.step_.get<int32_t>(), int32_t(st.tokens_ + T), -1, -1);
+            if (st.batch_ == 1) hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, s, st.step_.get<int32_t>(), int32_t(pos0 + T), -1, -1);
         }
         if (logits) hip_check(hipMemcpyAsync(logits, st.logits_.get(), size_t(c.V) * 4, hipMemcpyDeviceToHost, s), "logits download");
         int32_t scalars[4] = {0, 0, 0, 0};
         hip_check(hipMemcpyAsync(scalars, st.step_.get(), 16, hipMemcpyDeviceToHost, s), "step download");
         hip_check(hipStreamSynchronize(s), "forward");
         if (next_id) *next_id = scalars[1];
-        st.tokens_ += T;
+        st.seq_tokens_[size_t(seq)] += T;
     } catch (...) {
         // the carried state is now unknown: forget it (transformer.hpp:139-142)
         (void)hipStreamSynchronize(s);
@@ -625,7 +649,8 @@ void Qwen35Model::decode_greedy(State& st, int32_t first_id, int64_t steps, int3
     if (&st.m_ != this) throw Error(HERO_EINVAL, "decode: state belongs to another model");
     if (steps <= 0) throw Error(HERO_EINVAL, "decode: steps must be positive");
     if (first_id < 0 || first_id >= c.V) throw Error(HERO_EINVAL, "decode: token id out of range");
-    if (steps > st.max_tokens_ - st.tokens_) throw Error(HERO_ERANGE, "Qwen35Model: context exhausted");
+    if (st.batch_ != 1) throw Error(HERO_EINVAL, "decode: a batch state takes decode_batch");
+    if (steps > st.max_tokens_ - st.seq_tokens_[0]) throw Error(HERO_ERANGE, "Qwen35Model: context exhausted");
     hipStream_t s = stream_;
     try {
         if (!st.graph_) {
@@ -636,7 +661,7 @@ void Qwen35Model::decode_greedy(State& st, int32_t first_id, int64_t steps, int3
             hip_check(hipGraphInstantiate(&st.graph_, graph, nullptr, nullptr, 0), "graph instantiate");
             (void)hipGraphDestroy(graph);
         }
-        hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, s, st.step_.get<int32_t>(), int32_t(st.tokens_), first_id, 0);
+        hipLaunchKernelGGL(set_step_kernel, dim3(1), dim3(1), 0, s, st.step_.get<int32_t>(), int32_t(st.seq_tokens_[0]), first_id, 0);
         hip_check(hipEventRecord(ev_start_, s), "event");
         for (int64_t i = 0; i < steps; ++i) hip_check(hipGraphLaunch(st.graph_, s), "graph launch");
         hip_check(hipEventRecord(ev_stop_, s), "event");
@@ -646,7 +671,130 @@ void Qwen35Model::decode_greedy(State& st, int32_t first_id, int64_t steps, int3
         float ms = 0.f;
         hip_check(hipEventElapsedTime(&ms, ev_start_, ev_stop_), "event time");
         last_decode_seconds_ = double(ms) * 1e-3;
-        st.tokens_ += steps;
+        st.seq_tokens_[0] += steps;
+    } catch (...) {
+        (void)hipStreamSynchronize(s);
+        st.reset();
+        throw;
+    }
+}
+
+void Qwen35Model::enqueue_batch_step(State& st) const {
+    const ModelConfig& c = c_;
+    hipStream_t s = stream_;
+    const int64_t B = st.batch_;
+    int32_t* pos = st.bstep_.get<int32_t>();
+    int32_t* ids = pos + B;
+    float* x = st.x_.get<float>();
+    float* h = st.h_.get<float>();
+    float* proj = st.proj_.get<float>();
+    launch_embed_q8(embedding_.get(), c.V, c.D, ids, B, x, s);
+    for (int64_t l = 0; l < c.L; ++l) {
+        const LayerWeights& L = layers_[size_t(l)];
+        // per row the arithmetic of enqueue_step (nm/src/qwen35.hpp:318-327)
+        launch_rmsnorm_quant(x, L.mixer_norm.get<float>(), c.eps, nullptr, st.act_d_.get(), B, c.D, s);
+        launch_gemm_q8(L.w_in.get(), st.act_d_.get(), proj, nullptr, B, L.n_in, c.D, kEpiStore, s);
+        int64_t k_mix;
+        if (L.recurrent) {
+            GdnDecodeArgs a{};
+            a.proj = proj;
+            a.proj_stride = L.n_in;
+            a.z_off = L.z_off;
+            a.beta_off = L.beta_off;
+            a.alpha_off = L.alpha_off;
+            a.conv_taps = L.conv.get<float>();
+            a.conv_hist = st.conv_hist_[size_t(l)].get<float>();
+            a.state = st.delta_[size_t(l)].get<float>();
+            a.dt_bias = L.dt_bias.get<float>();
+            a.decay = L.decay.get<float>();
+            a.norm_gamma = L.ssm_norm.get<float>();
+            a.eps = c.eps;
+            a.positions = pos;
+            a.act_out = st.act_mix_.get();
+            a.out_f32 = nullptr;
+            a.B = int(B);
+            a.Hk = int(c.Hk);
+            a.Hv = int(c.Hv);
+            a.Dk = int(c.Dk);
+            a.Dv = int(c.Dv);
+            a.W = int(c.W);
+            launch_gdn_decode(a, s);
+            k_mix = c.v_width();
+        } else {
+            AttnDecodeArgs a{};
+            a.proj = proj;
+            a.proj_stride = L.n_in;
+            a.k_off = L.k_off;
+            a.v_off = L.v_off;
+            a.q_gamma = L.q_norm.get<float>();
+            a.k_gamma = L.k_norm.get<float>();
+            a.eps = c.eps;
+            a.rope_cs = rope_cs_.get<float>();
+            a.k_cache = st.k_cache_[size_t(l)].get<float>();
+            a.v_cache = st.v_cache_[size_t(l)].get<float>();
+            a.max_ctx = st.max_tokens_;
+            a.positions = pos;
+            a.shared_cache = 0;
+            a.scores = st.scores_[size_t(l)].get<float>();
+            a.q_rot = st.q_rot_.get<float>();
+            a.score_scale = 1.f / std::sqrt(float(c.Dh));  // qwen35.hpp:359
+            a.window = 0;
+            a.act_out = st.act_mix_.get();
+            a.out_f32 = nullptr;
+            a.B = int(B);
+            a.Hq = int(c.Hq);
+            a.Hkv = int(c.Hkv);
+            a.Dh = int(c.Dh);
+            launch_attn_decode(a, s);
+            k_mix = c.q_width();
+        }
+        launch_gemm_q8(L.w_out.get(), st.act_mix_.get(), h, x, B, c.D, k_mix, kEpiResidual, s);
+        launch_rmsnorm_quant(h, L.channel_norm.get<float>(), c.eps, nullptr, st.act_d_.get(), B, c.D, s);
+        launch_gemm_q8(L.w_gate_up.get(), st.act_d_.get(), st.gate_up_.get<float>(), nullptr, B, 2 * c.FF, c.D, kEpiStore, s);
+        launch_swiglu_quant(st.gate_up_.get<float>(), st.act_ff_.get(), B, c.FF, s, ffn_fused_ ? 32 : 0);
+        launch_gemm_q8(L.w_down.get(), st.act_ff_.get(), x, h, B, c.D, c.FF, kEpiResidual, s);
+    }
+    launch_rmsnorm_quant(x, final_norm_.get<float>(), c.eps, nullptr, st.act_d_.get(), B, c.D, s);
+    launch_gemm_q8(c.tied ? embedding_.get() : output_.get(), st.act_d_.get(), st.logits_.get<float>(), nullptr, B, c.V, c.D, kEpiStore, s);
+    launch_argmax(st.logits_.get<float>(), B, c.V, ids, st.argmax_scratch_.get<uint64_t>(), s);
+    hipLaunchKernelGGL(advance_batch_kernel, dim3(1), dim3(1), 0, s, pos, st.out_ids_.get<int32_t>(), int32_t(B));
+    check_launch("batch decode step");
+}
+
+void Qwen35Model::decode_batch(State& st, const int32_t* first_ids, int64_t steps, int32_t* out_ids, float* logits) const {
+    const ModelConfig& c = c_;
+    const int64_t B = st.batch_;
+    if (&st.m_ != this) throw Error(HERO_EINVAL, "decode: state belongs to another model");
+    if (steps <= 0) throw Error(HERO_EINVAL, "decode: steps must be positive");
+    if (!first_ids) throw Error(HERO_EINVAL, "decode: need the first ids");
+    std::vector<int32_t> init(size_t(2 * B + 4), 0);
+    for (int64_t b = 0; b < B; ++b) {
+        if (first_ids[b] < 0 || first_ids[b] >= c.V) throw Error(HERO_EINVAL, "decode: token id out of range");
+        if (steps > st.max_tokens_ - st.seq_tokens_[size_t(b)]) throw Error(HERO_ERANGE, "Qwen35Model: context exhausted");
+        init[size_t(b)] = int32_t(st.seq_tokens_[size_t(b)]);
+        init[size_t(B + b)] = first_ids[b];
+    }
+    hipStream_t s = stream_;
+    try {
+        if (!st.bgraph_) {
+            hipGraph_t graph = nullptr;
+            hip_check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "capture begin");
+            enqueue_batch_step(st);
+            hip_check(hipStreamEndCapture(s, &graph), "capture end");
+            hip_check(hipGraphInstantiate(&st.bgraph_, graph, nullptr, nullptr, 0), "graph instantiate");
+            (void)hipGraphDestroy(graph);
+        }
+        hip_check(hipMemcpyAsync(st.bstep_.get(), init.data(), init.size() * 4, hipMemcpyHostToDevice, s), "batch step upload");
+        hip_check(hipEventRecord(ev_start_, s), "event");
+        for (int64_t i = 0; i < steps; ++i) hip_check(hipGraphLaunch(st.bgraph_, s), "graph launch");
+        hip_check(hipEventRecord(ev_stop_, s), "event");
+        hip_check(hipMemcpyAsync(out_ids, st.out_ids_.get(), size_t(steps * B) * 4, hipMemcpyDeviceToHost, s), "ids download");
+        if (logits) hip_check(hipMemcpyAsync(logits, st.logits_.get(), size_t(B * c.V) * 4, hipMemcpyDeviceToHost, s), "logits download");
+        hip_check(hipStreamSynchronize(s), "decode");
+        float ms = 0.f;
+        hip_check(hipEventElapsedTime(&ms, ev_start_, ev_stop_), "event time");
+        last_decode_seconds_ = double(ms) * 1e-3;
+        for (int64_t b = 0; b < B; ++b) st.seq_tokens_[size_t(b)] += steps;
     } catch (...) {
         (void)hipStreamSynchronize(s);
         st.reset();

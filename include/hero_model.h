@@ -72,7 +72,24 @@ int hero_model_forward(const hero_model* model, hero_state* state, const float* 
  * Logits of the final pass are written to `logits` if non-NULL. */
 int hero_model_decode_greedy(const hero_model* model, hero_state* state, int32_t first_id, int64_t steps, int32_t* out_ids, float* logits);
 
-/* Seconds of device time of the last hero_model_decode_greedy call (HIP
+/* ---- batched decode --------------------------------------------------------
+ * No counterpart in the reference, whose model contract carries one sequence
+ * per state (nm/src/transformer.hpp:70-78). For callers that decode several
+ * independent sequences at once: a batch state holds `batch` (1..16)
+ * sequences, each with its own caches and position; every sequence's results
+ * equal those of its own single-sequence state, bit for bit. */
+int hero_batch_state_create(const hero_model* model, int64_t max_tokens, int32_t batch, hero_state** out);
+int64_t hero_state_batch(const hero_state* state);
+int64_t hero_state_seq_tokens(const hero_state* state, int32_t seq);
+/* hero_model_forward for sequence `seq` of a batch state. */
+int hero_model_forward_seq(const hero_model* model, hero_state* state, int32_t seq, const float* rows, const int32_t* ids, int64_t t, float* logits, int32_t* next_id);
+/* Greedy decode of every sequence at once, each from its own position:
+ * first_ids[B]; out_ids[steps][B] (row i = the greedy ids after pass i);
+ * logits [B][V] of the final pass if non-NULL. */
+int hero_model_decode_batch(const hero_model* model, hero_state* state, const int32_t* first_ids, int64_t steps, int32_t* out_ids, float* logits);
+
+/* Seconds of device time of the last hero_model_decode_greedy or
+ * hero_model_decode_batch call (HIP
  * events around the decode passes on the model's stream). */
 double hero_model_last_decode_seconds(const hero_model* model);
 

@@ -126,6 +126,43 @@ def test_long_prefill_runs_in_chunks_and_matches_oracle(model, tiny_gguf):
     assert np.array_equal(d1, d2) and np.array_equal(bits(l1.values), bits(l2.values))
 
 
+def test_batch_decode_equals_independent_sequences(model, tiny_golden):
+    """Four sequences with prompts of different lengths (so different
+    positions) decoded together: each one's greedy ids and final logits equal
+    those of the same sequence in its own single-sequence state, bit for bit."""
+    rng = np.random.default_rng(11)
+    prompts = [tiny_golden["prompt"][:3], rng.integers(0, model.V, 7), tiny_golden["prompt"], rng.integers(0, model.V, 1)]
+    steps = 12
+    bs = model.new_batch_state(256, len(prompts))
+    firsts = [model.forward_seq(bs, b, ids=p).argmax() for b, p in enumerate(prompts)]
+    out, logits = model.decode_batch(bs, firsts, steps, want_logits=True)
+    for b, p in enumerate(prompts):
+        assert bs.tokens(b) == len(p) + steps
+        st = model.new_state(256)
+        first = model.forward(st, ids=p).argmax()
+        assert first == firsts[b]
+        ids, lg = model.decode_greedy(st, first, steps, want_logits=True)
+        assert np.array_equal(out[:, b], ids), f"sequence {b}"
+        assert np.array_equal(bits(logits[b]), bits(lg.values)), f"sequence {b} logits"
+    # a second call continues every sequence from where it stopped
+    more, _ = model.decode_batch(bs, out[-1], 3)
+    st = model.new_state(256)
+    model.forward(st, ids=prompts[2])
+    model.decode_greedy(st, firsts[2], steps)
+    ids, _ = model.decode_greedy(st, int(out[-1, 2]), 3)
+    assert np.array_equal(more[:, 2], ids)
+
+
+def test_batch_state_rejects_single_sequence_calls(model):
+    bs = model.new_batch_state(16, 2)
+    with pytest.raises(hero_amd.HeroError):
+        model.forward(bs, ids=[1, 2])
+    with pytest.raises(hero_amd.HeroError):
+        model.forward_seq(bs, 2, ids=[1])
+    with pytest.raises(hero_amd.HeroError):
+        model.new_batch_state(16, 17)
+
+
 def test_prefix_cache_reuse_and_divergence(model, tiny_golden):
     prompt = tiny_golden["prompt"][:5]
     cache = hero_amd.PrefixCache(model, 64)
@@ -184,5 +221,14 @@ def test_d4096_model_matches_oracle_bitwise():
             ids.append(lg.argmax())
         assert ids == [int(v) for v in ref_ids]
         same_bits(lg.values, ref_last)
+        # the same prompt as sequence 1 of a batch of 2 (the GEMM forms over
+        # B rows): the same ids and logits
+        bs = m.new_batch_state(64, 2)
+        other = m.forward_seq(bs, 0, ids=prompt[:3])
+        first = m.forward_seq(bs, 1, ids=prompt)
+        assert np.array_equal(bits(first.values), bits(m.forward(m.new_state(64), ids=prompt).values))
+        out, logits = m.decode_batch(bs, [other.argmax(), first.argmax()], steps, want_logits=True)
+        assert [first.argmax()] + [int(v) for v in out[:, 1]] == [int(v) for v in ref_ids]
+        same_bits(logits[1], ref_last)
     finally:
         m.close()

@@ -11,6 +11,10 @@ prompt of --prompt tokens is prefilled first, then --warmup untimed steps, then
 exactly --steps timed steps (all on the device: each step is one hipGraph
 replay, no host input).
 
+With --batch B (default 16) it also prefills B independent prompts into one
+batch state and times greedy decode of all B at once (config.batch_decode:
+aggregate tok/s), the 8B workload's batch-16 leg.
+
 The JSON line also carries
   roofline      the Q8_0 GEMV (the dominant kernel): algorithmic bytes per
                 launch / average launch duration, from HIP events around every
@@ -80,6 +84,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--gemv-reps", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=16, help="also time greedy decode of this many sequences at once (0: skip)")
+    ap.add_argument("--batch-steps", type=int, default=64)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -123,6 +129,31 @@ def main() -> int:
     avg_launch = sec / (args.gemv_reps * launches)
     achieved = (nbytes / launches) / avg_launch / 1e9
     log(f"GEMV: {launches} launches/step, {nbytes / 1e9:.3f} GB/step, avg {avg_launch * 1e6:.2f} us/launch, {achieved:.0f} GB/s")
+    batch = None
+    if args.batch > 0:
+        # B independent sequences (prompts of --prompt ids from distinct seeds),
+        # each prefilled into its slot, then decoded together
+        state.close()
+        bctx = ((args.prompt + args.batch_steps + 8 + 255) // 256) * 256
+        bs = model.new_batch_state(bctx, args.batch)
+        t = time.perf_counter()
+        firsts = []
+        for b in range(args.batch):
+            p = np.random.default_rng(SEED + 1 + b).integers(0, shape.vocab, args.prompt).astype(np.int32)
+            firsts.append(model.forward_seq(bs, b, ids=p, want_logits=False))
+        torch.cuda.synchronize()
+        bprefill = time.perf_counter() - t
+        warm, _ = model.decode_batch(bs, firsts, 4)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        model.decode_batch(bs, warm[-1], args.batch_steps)
+        torch.cuda.synchronize()
+        bwall = time.perf_counter() - t
+        batch = {"sequences": args.batch, "steps": args.batch_steps, "tok_s": args.batch * args.batch_steps / bwall,
+                 "ms_per_step": bwall * 1e3 / args.batch_steps, "prefill_tok_s": args.batch * args.prompt / bprefill}
+        log(f"batch {args.batch}: prefill {args.batch * args.prompt} tokens in {bprefill:.2f} s; decode {args.batch_steps} steps "
+            f"{bwall * 1e3 / args.batch_steps:.2f} ms/step, {batch['tok_s']:.0f} tok/s aggregate")
+        bs.close()
 
     out = {
         "metric": "decode tok/s @bs1, Q8_0 ~8B hybrid; Q8 GEMV GB/s as % of HBM peak",
@@ -143,6 +174,8 @@ def main() -> int:
             "batch": 1, "prompt_tokens": args.prompt, "context_at_timed_start": args.prompt + args.warmup + 1,
             "prefill_seconds": prefill_s, "device_decode_seconds": device_s,
             "gemv_gbs_per_step": nbytes / (device_s / args.steps) / 1e9,
+            "prefill_tok_s": args.prompt / prefill_s,
+            "batch_decode": batch,
         },
         "roofline": {
             "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,

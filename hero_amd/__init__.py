@@ -22,6 +22,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
+from . import _lib
 from ._lib import ContextExhausted, HeroError, ModelDims, SynthConfig, check, lib
 
 __all__ = [
@@ -50,11 +51,15 @@ class Logits:
 
 
 class PrefixState:
-    """Device-resident carried state of one sequence (nm/src/qwen35.hpp:206-241)."""
+    """Device-resident carried state of one sequence (nm/src/qwen35.hpp:206-241).
+    kv_fp16 keeps the attention cache as fp16 pages (split-K attention)."""
 
-    def __init__(self, model: "Qwen35Model", max_tokens: int):
+    def __init__(self, model: "Qwen35Model", max_tokens: int, kv_fp16: bool = False):
         h = c_void_p()
-        check(lib.hero_state_create(model._h, max_tokens, byref(h)))
+        if kv_fp16:
+            check(lib.hero_batch_state_create(model._h, max_tokens, 1, _lib.HERO_STATE_KV_FP16, byref(h)))
+        else:
+            check(lib.hero_state_create(model._h, max_tokens, byref(h)))
         self._h = h
         self.model = model
         self.max_tokens = max_tokens
@@ -81,9 +86,9 @@ class BatchState:
     """`batch` independent sequences in one device state, decoded together
     (no counterpart in the reference, which carries one sequence per state)."""
 
-    def __init__(self, model: "Qwen35Model", max_tokens: int, batch: int):
+    def __init__(self, model: "Qwen35Model", max_tokens: int, batch: int, kv_fp16: bool = False):
         h = c_void_p()
-        check(lib.hero_batch_state_create(model._h, max_tokens, batch, byref(h)))
+        check(lib.hero_batch_state_create(model._h, max_tokens, batch, _lib.HERO_STATE_KV_FP16 if kv_fp16 else 0, byref(h)))
         self._h = h
         self.model = model
         self.max_tokens = max_tokens
@@ -142,11 +147,11 @@ class Qwen35Model:
         except Exception:
             pass
 
-    def new_state(self, max_tokens: int | None = None) -> PrefixState:
-        return PrefixState(self, max_tokens or min(self.CTX, 4096))
+    def new_state(self, max_tokens: int | None = None, kv_fp16: bool = False) -> PrefixState:
+        return PrefixState(self, max_tokens or min(self.CTX, 4096), kv_fp16)
 
-    def new_batch_state(self, max_tokens: int, batch: int) -> BatchState:
-        return BatchState(self, max_tokens, batch)
+    def new_batch_state(self, max_tokens: int, batch: int, kv_fp16: bool = False) -> BatchState:
+        return BatchState(self, max_tokens, batch, kv_fp16)
 
     def forward_seq(self, state: BatchState, seq: int, rows: np.ndarray | None = None, ids=None, want_logits: bool = True) -> Logits | int:
         """forward() for sequence `seq` of a batch state."""

@@ -14,6 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libhero_amd.so")
 
 HERO_OK, HERO_EINVAL, HERO_EHIP, HERO_ERANGE, HERO_ENOMEM, HERO_EIO = range(6)
+HERO_STATE_KV_FP16 = 1  # hero_batch_state_create flag: fp16 paged attention cache
 
 
 class HeroError(RuntimeError):
@@ -44,6 +45,13 @@ class AttnDecodeArgs(ctypes.Structure):
         ("k_cache", c_void_p), ("v_cache", c_void_p), ("max_ctx", c_int64), ("positions", c_void_p),
         ("scores", c_void_p), ("q_rot", c_void_p), ("score_scale", c_float), ("window", c_int32), ("act_out", c_void_p), ("out_f32", c_void_p),
         ("b", c_int32), ("hq", c_int32), ("hkv", c_int32), ("dh", c_int32),
+    ]
+
+
+class AttnPagedArgs(ctypes.Structure):
+    _fields_ = [
+        ("a", AttnDecodeArgs), ("pages", c_void_p), ("page_table", c_void_p),
+        ("page_size", c_int32), ("max_pages", c_int32), ("work", c_void_p), ("work_bytes", c_int64),
     ]
 
 
@@ -90,6 +98,8 @@ SIGNATURES = {
     "hero_gdn_prefill_work_bytes": (c_int64, [c_int64, c_int32, c_int32]),
     "hero_gdn_prefill": (c_int, [POINTER(GdnDecodeArgs), c_void_p, c_int64, c_void_p]),
     "hero_attn_decode": (c_int, [POINTER(AttnDecodeArgs), c_void_p]),
+    "hero_attn_paged_work_bytes": (c_int64, [c_int64, c_int32, c_int32, c_int32, c_int32]),
+    "hero_attn_decode_paged": (c_int, [POINTER(AttnPagedArgs), c_void_p]),
     "hero_model_open": (c_int, [c_char_p, POINTER(c_void_p)]),
     "hero_model_open_image": (c_int, [c_void_p, c_size_t, POINTER(c_void_p)]),
     "hero_model_close": (None, [c_void_p]),
@@ -98,7 +108,7 @@ SIGNATURES = {
     "hero_state_destroy": (None, [c_void_p]),
     "hero_state_reset": (c_int, [c_void_p]),
     "hero_state_tokens": (c_int64, [c_void_p]),
-    "hero_batch_state_create": (c_int, [c_void_p, c_int64, c_int32, POINTER(c_void_p)]),
+    "hero_batch_state_create": (c_int, [c_void_p, c_int64, c_int32, ctypes.c_uint32, POINTER(c_void_p)]),
     "hero_state_batch": (c_int64, [c_void_p]),
     "hero_state_seq_tokens": (c_int64, [c_void_p, c_int32]),
     "hero_model_forward_seq": (c_int, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),

@@ -115,4 +115,27 @@ struct AttnDecodeArgs {
 };
 void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s);
 
+// attn.hip, paged fp16 form: the same gated attention over a paged fp16 K/V
+// cache, the visible keys of each (row, KV head) split across workgroups
+// (split-K: per-split max, exp-sum and weighted V sum, merged per head).
+// Fields of `a` used: proj, proj_stride, k_off, v_off, q_gamma, k_gamma, eps,
+// rope_cs, positions, shared_cache, q_rot, score_scale, window, act_out,
+// out_f32, B, Hq, Hkv, Dh (k_cache, v_cache, scores and max_ctx are not).
+struct AttnPagedArgs {
+    AttnDecodeArgs a;
+    uint16_t* pages;            // fp16 pool [page][2 = K, V][Hkv][page_size][Dh]
+    const int32_t* page_table;  // [B][max_pages] pool page of each page_size tokens (row 0 for all rows when shared_cache)
+    int page_size;              // tokens per page
+    int max_pages;              // pages per sequence: positions < max_pages * page_size
+    int split;                  // keys per split, a multiple of 64, at most kAttnMaxSplit
+    int nsplit;                 // splits per (row, KV head): ceil(visible keys at most / split)
+    float* work;                // [B][Hq][nsplit][2 + Dh]: max, exp-sum, weighted V sum
+};
+constexpr int kAttnMaxSplit = 512;
+constexpr int kAttnMaxGroup = 8;  // query heads per KV head
+// split and nsplit for B rows over at most max_ctx positions (window 0 = full)
+void attn_paged_plan(int64_t max_ctx, int window, int B, int Hkv, int* split, int* nsplit);
+int64_t attn_paged_work_floats(int B, int Hq, int nsplit);
+void launch_attn_paged(const AttnPagedArgs& p, hipStream_t s);
+
 }  // namespace hero

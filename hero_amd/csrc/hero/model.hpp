@@ -19,6 +19,8 @@
 #include <string>
 #include <vector>
 
+#include "hero/kernels.hpp"
+
 namespace hero {
 
 class GgufFile;
@@ -81,7 +83,8 @@ struct LayerWeights {
 class Qwen35Model {
 public:
     class State;
-    static constexpr int64_t kMaxBatch = 16;  // sequences per state (the skinny GEMM's rows)
+    static constexpr int64_t kMaxBatch = 16;    // sequences per state (the skinny GEMM's rows)
+    static constexpr int64_t kPageTokens = 64;  // positions per page of the fp16 attention cache
 
     static std::unique_ptr<Qwen35Model> open(const std::string& gguf_path);
     static std::unique_ptr<Qwen35Model> open_image(const uint8_t* image, uint64_t size);
@@ -93,8 +96,10 @@ public:
     int64_t device_bytes() const { return device_bytes_; }
     hipStream_t stream() const { return stream_; }
 
-    // `batch` independent sequences of up to `max_tokens` each
-    std::unique_ptr<State> new_state(int64_t max_tokens, int64_t batch = 1) const;
+    // `batch` independent sequences of up to `max_tokens` each; `kv_fp16`
+    // keeps the attention cache as fp16 pages (split-K attention) instead of
+    // the reference's fp32 rows
+    std::unique_ptr<State> new_state(int64_t max_tokens, int64_t batch = 1, bool kv_fp16 = false) const;
     // host rows out[n][D]
     void embed(const int32_t* ids, int64_t n, float* out) const;
     // T rows from host `rows` or from `ids`; logits / greedy id of the last row
@@ -128,6 +133,9 @@ private:
     // one token of every sequence of a batch state (positions and ids on the
     // device): the matvecs as skinny GEMMs over the B rows
     void enqueue_batch_step(State& s) const;
+    // attention of rows a.B (their positions in a.positions): fp32 rows, or
+    // the fp16 pages of the sequences whose page-table rows start at `pt`
+    void attention(State& s, size_t layer, AttnDecodeArgs a, const int32_t* pt, float* work, hipStream_t stream) const;
     // rows per prefill chunk: at most 512, and the chunk's attention scores
     // (rows x query heads x max_tokens fp32) within 256 MiB
     int64_t chunk_rows(const State& s) const;
@@ -156,10 +164,17 @@ public:
 
 private:
     friend class Qwen35Model;
-    explicit State(const Qwen35Model& m, int64_t max_tokens, int64_t batch);
+    explicit State(const Qwen35Model& m, int64_t max_tokens, int64_t batch, bool kv_fp16);
 
     const Qwen35Model& m_;
     int64_t max_tokens_ = 0, batch_ = 1;
+    // fp16 paged attention cache: per attention layer a pool of batch x
+    // max_pages pages; page_table_ [batch][max_pages] (sequence b owns pages
+    // b * max_pages ...); attn_work_ the split-K partials of a decode step
+    bool kv_fp16_ = false;
+    int64_t max_pages_ = 0;
+    std::vector<DeviceBuffer> kv_pages_;
+    DeviceBuffer page_table_, attn_work_;
     std::vector<int64_t> seq_tokens_;
     // batch step scalars: [0, B) positions, [B, 2B) token ids, [2B] step counter
     DeviceBuffer bstep_;
@@ -170,7 +185,7 @@ private:
     DeviceBuffer gemv_scratch_;  // [D] output of the GEMV timing runs
     int64_t out_ids_capacity_ = 0;
     // prefill chunk buffers (row-major, chunk_capacity_ rows), made on first use
-    DeviceBuffer cx_, ch_, cproj_, cact_d_, cact_mix_, cgate_up_, cact_ff_, cq_rot_, cscores_, cpos_, cids_, cgdn_work_;
+    DeviceBuffer cx_, ch_, cproj_, cact_d_, cact_mix_, cgate_up_, cact_ff_, cq_rot_, cscores_, cpos_, cids_, cgdn_work_, cattn_work_;
     int64_t chunk_capacity_ = 0;
     void ensure_chunk(int64_t rows);
     // per layer, every sequence's: [B][...]

@@ -261,43 +261,77 @@ int hero_gdn_prefill(const hero_gdn_decode_args* p, void* work, int64_t work_byt
     });
 }
 
+namespace {
+AttnDecodeArgs attn_args(const hero_attn_decode_args& a) {
+    require(a.dh == 128, "attention head dim must be 128");
+    require(a.b > 0 && a.hkv > 0 && a.hq > 0 && a.hq % a.hkv == 0, "bad head counts");
+    require(a.window >= 0, "bad window");
+    require(a.proj && a.q_gamma && a.k_gamma && a.rope_cs && a.positions && a.q_rot && a.act_out, "null pointer");
+    const int64_t kw = int64_t(a.hkv) * 128;
+    require(a.proj_stride >= 2 * int64_t(a.hq) * 128 && a.k_off + kw <= a.proj_stride && a.v_off + kw <= a.proj_stride, "k/v slices outside the projection row");
+    AttnDecodeArgs g{};
+    g.proj = a.proj;
+    g.proj_stride = a.proj_stride;
+    g.k_off = a.k_off;
+    g.v_off = a.v_off;
+    g.q_gamma = a.q_gamma;
+    g.k_gamma = a.k_gamma;
+    g.eps = a.eps;
+    g.rope_cs = a.rope_cs;
+    g.k_cache = a.k_cache;
+    g.v_cache = a.v_cache;
+    g.max_ctx = a.max_ctx;
+    g.positions = a.positions;
+    g.shared_cache = 0;
+    g.scores = a.scores;
+    g.q_rot = a.q_rot;
+    g.score_scale = a.score_scale;
+    g.window = a.window;
+    g.act_out = a.act_out;
+    g.out_f32 = a.out_f32;
+    g.B = a.b;
+    g.Hq = a.hq;
+    g.Hkv = a.hkv;
+    g.Dh = a.dh;
+    return g;
+}
+}  // namespace
+
 int hero_attn_decode(const hero_attn_decode_args* p, void* stream) {
     return guard([&] {
         require(p != nullptr, "null args");
         const hero_attn_decode_args& a = *p;
-        require(a.dh == 128, "attention head dim must be 128");
-        require(a.b > 0 && a.hkv > 0 && a.hq > 0 && a.hq % a.hkv == 0, "bad head counts");
-        require(a.window >= 0 && a.max_ctx > 0, "bad window or cache size");
-        require(a.proj && a.q_gamma && a.k_gamma && a.rope_cs && a.k_cache && a.v_cache && a.positions && a.scores && a.q_rot && a.act_out, "null pointer");
-        const int64_t kw = int64_t(a.hkv) * 128;
-        require(a.proj_stride >= 2 * int64_t(a.hq) * 128 && a.k_off + kw <= a.proj_stride && a.v_off + kw <= a.proj_stride, "k/v slices outside the projection row");
-        require(a.max_ctx <= (int64_t(1) << 24), "max_ctx too large");
-        AttnDecodeArgs g{};
-        g.proj = a.proj;
-        g.proj_stride = a.proj_stride;
-        g.k_off = a.k_off;
-        g.v_off = a.v_off;
-        g.q_gamma = a.q_gamma;
-        g.k_gamma = a.k_gamma;
-        g.eps = a.eps;
-        g.rope_cs = a.rope_cs;
-        g.k_cache = a.k_cache;
-        g.v_cache = a.v_cache;
-        g.max_ctx = a.max_ctx;
-        g.positions = a.positions;
-        g.shared_cache = 0;
-        g.scores = a.scores;
-        g.q_rot = a.q_rot;
-        g.score_scale = a.score_scale;
-        g.window = a.window;
-        g.act_out = a.act_out;
-        g.out_f32 = a.out_f32;
-        g.B = a.b;
-        g.Hq = a.hq;
-        g.Hkv = a.hkv;
-        g.Dh = a.dh;
-        launch_attn_decode(g, as_stream(stream));
+        require(a.k_cache && a.v_cache && a.scores, "null pointer");
+        require(a.max_ctx > 0 && a.max_ctx <= (int64_t(1) << 24), "max_ctx out of range");
+        launch_attn_decode(attn_args(a), as_stream(stream));
         check_launch("hero_attn_decode");
+    });
+}
+
+int64_t hero_attn_paged_work_bytes(int64_t max_ctx, int32_t window, int32_t b, int32_t hq, int32_t hkv) {
+    if (max_ctx <= 0 || b <= 0 || hkv <= 0 || hq <= 0 || window < 0) return -1;
+    int split = 0, nsplit = 0;
+    attn_paged_plan(max_ctx, window, b, hkv, &split, &nsplit);
+    return attn_paged_work_floats(b, hq, nsplit) * 4;
+}
+
+int hero_attn_decode_paged(const hero_attn_paged_args* p, void* stream) {
+    return guard([&] {
+        require(p != nullptr, "null args");
+        AttnPagedArgs g{};
+        g.a = attn_args(p->a);
+        require(g.a.Hq / g.a.Hkv <= kAttnMaxGroup, "at most 8 query heads per KV head");
+        require(p->pages && p->page_table && p->work, "null pointer");
+        require(p->page_size > 0 && p->max_pages > 0 && int64_t(p->page_size) * p->max_pages <= (int64_t(1) << 24), "bad page geometry");
+        g.pages = p->pages;
+        g.page_table = p->page_table;
+        g.page_size = p->page_size;
+        g.max_pages = p->max_pages;
+        attn_paged_plan(int64_t(p->page_size) * p->max_pages, g.a.window, g.a.B, g.a.Hkv, &g.split, &g.nsplit);
+        require(p->work_bytes >= attn_paged_work_floats(g.a.B, g.a.Hq, g.nsplit) * 4, "split workspace too small");
+        g.work = p->work;
+        launch_attn_paged(g, as_stream(stream));
+        check_launch("hero_attn_decode_paged");
     });
 }
 

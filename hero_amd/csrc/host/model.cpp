@@ -294,13 +294,15 @@ void Qwen35Model::build_rope_table(int64_t positions) {
 }
 
 // ---- state --------------------------------------------------------------------------
-std::unique_ptr<Qwen35Model::State> Qwen35Model::new_state(int64_t max_tokens, int64_t batch) const {
+std::unique_ptr<Qwen35Model::State> Qwen35Model::new_state(int64_t max_tokens, int64_t batch, bool kv_fp16) const {
     if (max_tokens <= 0 || max_tokens > c_.CTX || max_tokens > rope_positions_) throw Error(HERO_ERANGE, "state: max_tokens must be in 1.." + std::to_string(std::min(c_.CTX, rope_positions_)));
     if (batch < 1 || batch > kMaxBatch) throw Error(HERO_EINVAL, "state: batch must be in 1.." + std::to_string(kMaxBatch));
-    return std::unique_ptr<State>(new State(*this, max_tokens, batch));
+    if (kv_fp16 && c_.Hq / c_.Hkv > kAttnMaxGroup) throw Error(HERO_EINVAL, "state: the fp16 cache takes at most 8 query heads per KV head");
+    return std::unique_ptr<State>(new State(*this, max_tokens, batch, kv_fp16));
 }
 
-Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batch) : m_(m), max_tokens_(max_tokens), batch_(batch), seq_tokens_(size_t(batch), 0) {
+Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batch, bool kv_fp16)
+    : m_(m), max_tokens_(max_tokens), batch_(batch), seq_tokens_(size_t(batch), 0), kv_fp16_(kv_fp16) {
     const ModelConfig& c = m.c_;
     const int64_t B = batch;
     int64_t n_in_max = 0;
@@ -327,6 +329,12 @@ Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batc
             scores_.emplace_back();
             conv_hist_.emplace_back(size_t(B * c.W * c.conv_channels()) * 4);
             delta_.emplace_back(size_t(B * c.Hv * c.Dk * c.Dv) * 4);
+        } else if (kv_fp16) {
+            k_cache_.emplace_back();
+            v_cache_.emplace_back();
+            scores_.emplace_back();
+            conv_hist_.emplace_back();
+            delta_.emplace_back();
         } else {
             k_cache_.emplace_back(size_t(B * max_tokens * c.kv_width()) * 4);
             v_cache_.emplace_back(size_t(B * max_tokens * c.kv_width()) * 4);
@@ -334,6 +342,21 @@ Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batc
             conv_hist_.emplace_back();
             delta_.emplace_back();
         }
+    }
+    kv_pages_.resize(size_t(c.L));
+    if (kv_fp16) {
+        max_pages_ = (max_tokens + kPageTokens - 1) / kPageTokens;
+        const int64_t page_bytes = 2 * c.Hkv * kPageTokens * c.Dh * 2;
+        for (int64_t l = 0; l < c.L; ++l)
+            if (!c.is_recurrent(l)) kv_pages_[size_t(l)] = DeviceBuffer(size_t(B * max_pages_ * page_bytes));
+        // sequence b owns pool pages b * max_pages ... (a server would map pages on demand)
+        std::vector<int32_t> table(size_t(B * max_pages_));
+        for (size_t i = 0; i < table.size(); ++i) table[i] = int32_t(i);
+        page_table_ = DeviceBuffer(table.size() * 4);
+        hip_check(hipMemcpy(page_table_.get(), table.data(), table.size() * 4, hipMemcpyHostToDevice), "page table");
+        int split = 0, nsplit = 0;
+        attn_paged_plan(max_pages_ * kPageTokens, 0, int(B), int(c.Hkv), &split, &nsplit);
+        attn_work_ = DeviceBuffer(size_t(attn_paged_work_floats(int(B), int(c.Hq), nsplit)) * 4);
     }
     reset();
 }
@@ -352,6 +375,7 @@ void Qwen35Model::State::reset() {
     for (auto& b : v_cache_) zero(b);
     for (auto& b : conv_hist_) zero(b);
     for (auto& b : delta_) zero(b);
+    for (auto& b : kv_pages_) zero(b);
     zero(step_);
     zero(bstep_);
     hip_check(hipStreamSynchronize(s), "state reset");
@@ -377,10 +401,15 @@ void Qwen35Model::State::ensure_chunk(int64_t rows) {
     cgate_up_ = DeviceBuffer(size_t(rows * 2 * c.FF) * 4);
     cact_ff_ = DeviceBuffer(size_t(act_q8_bytes(rows, c.FF)));
     cq_rot_ = DeviceBuffer(size_t(rows * c.q_width()) * 4);
-    cscores_ = DeviceBuffer(size_t(rows * c.Hq * max_tokens_) * 4);
+    if (!kv_fp16_) cscores_ = DeviceBuffer(size_t(rows * c.Hq * max_tokens_) * 4);
     cpos_ = DeviceBuffer(size_t(rows) * 4);
     cids_ = DeviceBuffer(size_t(rows) * 4);
     cgdn_work_ = DeviceBuffer(size_t(gdn_prefill_work_bytes(rows, c.Hk, c.Hv)));
+    if (kv_fp16_) {
+        int split = 0, nsplit = 0;
+        attn_paged_plan(max_pages_ * kPageTokens, 0, int(rows), int(c.Hkv), &split, &nsplit);
+        cattn_work_ = DeviceBuffer(size_t(attn_paged_work_floats(int(rows), int(c.Hq), nsplit)) * 4);
+    }
     chunk_capacity_ = rows;
 }
 
@@ -428,6 +457,22 @@ int64_t gemv_act(const void* w, const void* act, float* y, const float* r, int64
 }
 
 }  // namespace
+
+void Qwen35Model::attention(State& st, size_t layer, AttnDecodeArgs a, const int32_t* pt, float* work, hipStream_t s) const {
+    if (!st.kv_fp16_) {
+        launch_attn_decode(a, s);
+        return;
+    }
+    AttnPagedArgs p{};
+    p.a = a;
+    p.pages = st.kv_pages_[layer].get<uint16_t>();
+    p.page_table = pt;
+    p.page_size = int(kPageTokens);
+    p.max_pages = int(st.max_pages_);
+    attn_paged_plan(st.max_pages_ * kPageTokens, a.window, a.B, a.Hkv, &p.split, &p.nsplit);
+    p.work = work;
+    launch_attn_paged(p, s);
+}
 
 void Qwen35Model::enqueue_step(State& st, bool from_ids, bool with_head) const {
     const ModelConfig& c = c_;
@@ -491,7 +536,7 @@ void Qwen35Model::enqueue_step(State& st, bool from_ids, bool with_head) const {
             a.Hq = int(c.Hq);
             a.Hkv = int(c.Hkv);
             a.Dh = int(c.Dh);
-            launch_attn_decode(a, s);
+            attention(st, size_t(l), a, st.page_table_.get<int32_t>(), st.attn_work_.get<float>(), s);
             k_mix = c.q_width();
         }
         gemv_act(L.w_out.get(), st.act_mix_.get(), h, x, c.D, k_mix, s);
@@ -560,8 +605,10 @@ void Qwen35Model::enqueue_chunk(State& st, int64_t seq, int64_t pos0, int64_t T,
             a.k_gamma = L.k_norm.get<float>();
             a.eps = c.eps;
             a.rope_cs = rope_cs_.get<float>();
-            a.k_cache = st.k_cache_[size_t(l)].get<float>() + seq * st.max_tokens_ * c.kv_width();
-            a.v_cache = st.v_cache_[size_t(l)].get<float>() + seq * st.max_tokens_ * c.kv_width();
+            if (!st.kv_fp16_) {  // the fp16 pages are found through the page table
+                a.k_cache = st.k_cache_[size_t(l)].get<float>() + seq * st.max_tokens_ * c.kv_width();
+                a.v_cache = st.v_cache_[size_t(l)].get<float>() + seq * st.max_tokens_ * c.kv_width();
+            }
             a.max_ctx = st.max_tokens_;
             a.positions = pos;
             a.shared_cache = 1;
@@ -575,7 +622,7 @@ void Qwen35Model::enqueue_chunk(State& st, int64_t seq, int64_t pos0, int64_t T,
             a.Hq = int(c.Hq);
             a.Hkv = int(c.Hkv);
             a.Dh = int(c.Dh);
-            launch_attn_decode(a, s);
+            attention(st, size_t(l), a, st.page_table_.get<int32_t>() + seq * st.max_pages_, st.cattn_work_.get<float>(), s);
             k_mix = c.q_width();
         }
         launch_gemm_q8(L.w_out.get(), st.cact_mix_.get(), h, x, T, c.D, k_mix, kEpiResidual, s);
@@ -745,7 +792,7 @@ void Qwen35Model::enqueue_batch_step(State& st) const {
             a.Hq = int(c.Hq);
             a.Hkv = int(c.Hkv);
             a.Dh = int(c.Dh);
-            launch_attn_decode(a, s);
+            attention(st, size_t(l), a, st.page_table_.get<int32_t>(), st.attn_work_.get<float>(), s);
             k_mix = c.q_width();
         }
         launch_gemm_q8(L.w_out.get(), st.act_mix_.get(), h, x, B, c.D, k_mix, kEpiResidual, s);

@@ -239,6 +239,222 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(AttnDecodeArgs a) {
     }
 }
 
+// ---- paged fp16 cache, split-K ------------------------------------------------------------
+// The keys and values are stored as fp16 (round to nearest even) in pages of
+// page_size positions; a page table maps each sequence's pages into the pool.
+// Scores are the reference's fp32 dot products over the fp16-rounded keys, in
+// channel order; the softmax and the weighted sum are split over the keys
+// (exp(s - m_split) per split, merged with exp(m_split - m)), so they agree
+// with the sequential reference to a few ulp, not bit for bit.
+constexpr int kPgTile = 64;  // keys per shared-memory tile
+
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float x) {
+    const _Float16 h = _Float16(x);
+    uint16_t b;
+    __builtin_memcpy(&b, &h, 2);
+    return b;
+}
+
+__device__ __forceinline__ const int32_t* page_row(const AttnPagedArgs& p, int b) { return p.page_table + int64_t(p.a.shared_cache ? 0 : b) * p.max_pages; }
+
+// the fp16 row of position t, KV head g, K (kv = 0) or V (kv = 1)
+__device__ __forceinline__ int64_t page_offset(const AttnPagedArgs& p, const int32_t* pt, int t, int g, int kv) {
+    const int64_t page = pt[t / p.page_size];
+    return ((page * 2 + kv) * p.a.Hkv + g) * int64_t(p.page_size) * kAttnDim + int64_t(t % p.page_size) * kAttnDim;
+}
+
+__global__ __launch_bounds__(kAttnDim) void attn_paged_prep_kernel(AttnPagedArgs p) {
+    const AttnDecodeArgs& a = p.a;
+    const int j = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
+    const int group = a.Hq / a.Hkv;
+    const int g = h / group;
+    const int pos = a.positions[b];
+    if (pos < 0 || pos >= p.max_pages * p.page_size) return;  // the host keeps positions in range
+    const float* P = a.proj + int64_t(b) * a.proj_stride;
+    const float* cs = a.rope_cs + int64_t(pos) * kAttnDim;
+    __shared__ __align__(16) float buf[kAttnDim];
+    __shared__ float scal[2];
+    const float q = norm_rope_head(P[int64_t(h) * 2 * kAttnDim + j], a.q_gamma, a.eps, cs, buf, scal, j);
+    a.q_rot[(int64_t(b) * a.Hq + h) * kAttnDim + j] = q;
+    if (h % group == 0) {
+        const float k = norm_rope_head(P[a.k_off + int64_t(g) * kAttnDim + j], a.k_gamma, a.eps, cs, buf, scal, j);
+        const float v = P[a.v_off + int64_t(g) * kAttnDim + j];
+        const int32_t* pt = page_row(p, b);
+        p.pages[page_offset(p, pt, pos, g, 0) + j] = f32_to_f16_rne(k);
+        p.pages[page_offset(p, pt, pos, g, 1) + j] = f32_to_f16_rne(v);
+    }
+}
+
+// one workgroup per (KV head, split, row): the split's keys in tiles of 64
+__global__ __launch_bounds__(256) void attn_split_kernel(AttnPagedArgs p) {
+    const AttnDecodeArgs& a = p.a;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int g = blockIdx.x, sp = blockIdx.y, b = blockIdx.z;
+    const int Gs = a.Hq / a.Hkv;
+    const int pos = a.positions[b];
+    if (pos < 0 || pos >= p.max_pages * p.page_size) return;
+    const int first = visible_first(pos, a.window);
+    const int t0 = first + sp * p.split, t1 = min(pos + 1, t0 + p.split);
+    const int64_t rec = 2 + kAttnDim;
+    float* out = p.work + ((int64_t(b) * a.Hq + int64_t(g) * Gs) * p.nsplit + sp) * rec;  // head h of the group: + h * nsplit * rec
+    const int64_t hstride = int64_t(p.nsplit) * rec;
+    if (t0 >= t1) {  // nothing visible in this split
+        for (int e = tid; e < Gs * rec; e += 256) out[(e / rec) * hstride + e % rec] = (e % rec) == 0 ? -INFINITY : 0.f;
+        return;
+    }
+    const int n = t1 - t0;
+    const int32_t* pt = page_row(p, b);
+    __shared__ float qs[kAttnMaxGroup][kAttnDim];
+    __shared__ float kt[kAttnDim][kPgTile + 1];  // K tile, channel-major
+    __shared__ uint32_t vt[kPgTile][kAttnDim / 2 + 1];  // V tile, rows of fp16 pairs
+    __shared__ float sc[kAttnMaxGroup][kAttnMaxSplit];
+    for (int e = tid; e < Gs * kAttnDim; e += 256) qs[e / kAttnDim][e % kAttnDim] = a.q_rot[(int64_t(b) * a.Hq + int64_t(g) * Gs) * kAttnDim + e];
+
+    // tile loads: thread -> row r = tid / 4, channels 32 * (tid % 4) .. +31 (four 16-byte loads)
+    const int r = tid >> 2, cq = (tid & 3) * 32;
+    const int ntiles = (n + kPgTile - 1) / kPgTile;
+    for (int tile = 0; tile < ntiles; ++tile) {
+        const int t = t0 + tile * kPgTile + r;
+        uint4 raw[4] = {};
+        if (t < t1) {
+            const uint4* src = reinterpret_cast<const uint4*>(p.pages + page_offset(p, pt, t, g, 0) + cq);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) raw[u] = src[u];
+        }
+        __syncthreads();  // the previous tile's readers are done
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                kt[cq + 8 * u + 2 * e][r] = half_bits_to_f32(uint16_t(w[e] & 0xFFFFu));
+                kt[cq + 8 * u + 2 * e + 1][r] = half_bits_to_f32(uint16_t(w[e] >> 16));
+            }
+        }
+        __syncthreads();
+        // score of key lane for query head h: scale * sequential dot (core.hpp:496-500)
+        for (int h = wv; h < Gs; h += 4) {
+            float dot = 0.f;
+#pragma unroll 16
+            for (int c = 0; c < kAttnDim; ++c) dot += qs[h][c] * kt[c][lane];
+            const int jj = tile * kPgTile + lane;
+            if (jj < n) sc[h][jj] = a.score_scale * dot;
+        }
+    }
+    __syncthreads();
+    // per head (one wave each): local max, p = exp(s - m), local sum
+    for (int h = wv; h < Gs; h += 4) {
+        float m = -INFINITY;
+        for (int jj = lane; jj < n; jj += 64) m = fmaxf(m, sc[h][jj]);
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        float l = 0.f;
+        for (int jj = lane; jj < n; jj += 64) {
+            const float e = exp_f32(sc[h][jj] - m);
+            sc[h][jj] = e;
+            l += e;
+        }
+        for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
+        if (lane == 0) {
+            out[h * hstride] = m;
+            out[h * hstride + 1] = l;
+        }
+    }
+    // weighted sum of values: thread -> head wv (+4), channel pair lane
+    float o0[kAttnMaxGroup / 4] = {}, o1[kAttnMaxGroup / 4] = {};
+    for (int tile = 0; tile < ntiles; ++tile) {
+        const int t = t0 + tile * kPgTile + r;
+        uint4 raw[4] = {};
+        if (t < t1) {
+            const uint4* src = reinterpret_cast<const uint4*>(p.pages + page_offset(p, pt, t, g, 1) + cq);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) raw[u] = src[u];
+        }
+        __syncthreads();  // sc complete (first tile) / previous tile's readers done
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            vt[r][cq / 2 + 4 * u + 0] = raw[u].x;
+            vt[r][cq / 2 + 4 * u + 1] = raw[u].y;
+            vt[r][cq / 2 + 4 * u + 2] = raw[u].z;
+            vt[r][cq / 2 + 4 * u + 3] = raw[u].w;
+        }
+        __syncthreads();
+        const int rows = min(kPgTile, n - tile * kPgTile);
+#pragma unroll
+        for (int hh = 0; hh < kAttnMaxGroup / 4; ++hh) {
+            const int h = wv + 4 * hh;
+            if (h < Gs) {
+                for (int jr = 0; jr < rows; ++jr) {
+                    const float pj = sc[h][tile * kPgTile + jr];
+                    const uint32_t v2 = vt[jr][lane];
+                    o0[hh] += pj * half_bits_to_f32(uint16_t(v2 & 0xFFFFu));
+                    o1[hh] += pj * half_bits_to_f32(uint16_t(v2 >> 16));
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int hh = 0; hh < kAttnMaxGroup / 4; ++hh) {
+        const int h = wv + 4 * hh;
+        if (h < Gs) {
+            out[h * hstride + 2 + 2 * lane] = o0[hh];
+            out[h * hstride + 2 + 2 * lane + 1] = o1[hh];
+        }
+    }
+}
+
+// one workgroup per (query head, row), a lane per channel: merge the splits,
+// then the gate (qwen35.hpp:390-393) and the Q8_0 quantization for W_o
+__global__ __launch_bounds__(kAttnDim) void attn_combine_kernel(AttnPagedArgs p) {
+    const AttnDecodeArgs& a = p.a;
+    const int c = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
+    const int pos = a.positions[b];
+    if (pos < 0 || pos >= p.max_pages * p.page_size) return;
+    const int64_t rec = 2 + kAttnDim;
+    const float* w = p.work + (int64_t(b) * a.Hq + h) * p.nsplit * rec;
+    float m = -INFINITY;
+    for (int s = 0; s < p.nsplit; ++s) m = fmaxf(m, w[s * rec]);
+    float l = 0.f, o = 0.f;
+    for (int s = 0; s < p.nsplit; ++s) {
+        const float ms = w[s * rec];
+        if (ms == -INFINITY) continue;
+        const float f = exp_f32(ms - m);
+        l += w[s * rec + 1] * f;
+        o += w[s * rec + 2 + c] * f;
+    }
+    const float gate = a.proj[int64_t(b) * a.proj_stride + int64_t(h) * 2 * kAttnDim + kAttnDim + c];
+    const float out = (o / l) * sigmoid_f32(gate);
+    const int64_t width = int64_t(a.Hq) * kAttnDim;
+    const int64_t idx = int64_t(h) * kAttnDim + c;
+    if (a.out_f32) a.out_f32[int64_t(b) * width + idx] = out;
+    float amax = fabsf(out);
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    const float d = amax / 127.f;
+    const float id = d != 0.f ? 1.f / d : 0.f;
+    int8_t* qs = static_cast<int8_t*>(a.act_out);
+    float* qd = reinterpret_cast<float*>(qs + int64_t(a.B) * width);
+    qs[int64_t(b) * width + idx] = int8_t(int(roundf(out * id)));
+    if ((c & 31) == 0) qd[(int64_t(b) * width + idx) >> 5] = half_bits_to_f32(fp32_to_fp16_ref(d));
+}
+
+void attn_paged_plan(int64_t max_ctx, int window, int B, int Hkv, int* split, int* nsplit) {
+    const int64_t vis = window > 0 ? std::min<int64_t>(max_ctx, window) : max_ctx;
+    // about two workgroups per CU over all rows and KV heads
+    const int64_t want = std::max<int64_t>(1, 512 / std::max<int64_t>(1, int64_t(B) * Hkv));
+    int64_t sp = (vis + want - 1) / want;
+    sp = std::min<int64_t>(kAttnMaxSplit, std::max<int64_t>(kPgTile, (sp + kPgTile - 1) / kPgTile * kPgTile));
+    *split = int(sp);
+    *nsplit = int((vis + sp - 1) / sp);
+}
+
+int64_t attn_paged_work_floats(int B, int Hq, int nsplit) { return int64_t(B) * Hq * nsplit * (2 + kAttnDim); }
+
+void launch_attn_paged(const AttnPagedArgs& p, hipStream_t s) {
+    const AttnDecodeArgs& a = p.a;
+    hipLaunchKernelGGL(attn_paged_prep_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, p);
+    hipLaunchKernelGGL(attn_split_kernel, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), 0, s, p);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, p);
+}
+
 void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(attn_prep_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, a);
     hipLaunchKernelGGL(attn_scores_kernel, dim3(unsigned(a.Hq), kScoreTiles, unsigned(a.B)), dim3(256), 0, s, a);

@@ -14,9 +14,10 @@ gdn    the fused delta-net layer body (conv + SiLU, L2 norms, gates, the delta
        rule on the fp32 state, head norm, gate, quantize) with 16 heads of
        128 x 128: one decode step at B in {1, 8, 32} from a state warmed by 64
        steps, and the bit-exact token-serial prefill of 4096 tokens.
-attn   gated GQA decode (32 q / 8 kv heads of 128, fp32 K/V cache) at context
-       {1k, 8k, 32k} x B {1, 16}: full causal (scale 1/sqrt(128)) and a 1024
-       sliding window (scale 1).
+attn   gated GQA decode (32 q / 8 kv heads of 128) at context {1k, 8k, 32k} x
+       B {1, 16}: full causal (scale 1/sqrt(128)) and a 1024 sliding window
+       (scale 1), over the fp32 cache (the reference's precision, bit-exact
+       kernels) and over the paged fp16 cache (split-K kernels).
 
 Each case is captured once as a hipGraph (one pass over its inputs) and
 replayed; the time per launch is the replay time divided by the launches,
@@ -224,7 +225,7 @@ def bench_gdn(lib, replays: int = 50):
 
 # ---- GQA decode attention ------------------------------------------------------------------------
 def bench_attn(lib, replays: int = 20):
-    from ._lib import AttnDecodeArgs, check
+    from ._lib import AttnDecodeArgs, AttnPagedArgs, check
 
     t = _torch()
     gen = t.Generator(device="cuda")
@@ -268,6 +269,35 @@ def bench_attn(lib, replays: int = 20):
                              "GB/s": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS})
                 print(json.dumps(rows[-1]), flush=True)
             del caches, scores
+            t.cuda.empty_cache()
+            # the same over the paged fp16 cache (pages of 64 positions, split-K)
+            page = 64
+            max_pages = ctx // page
+            pages = [(t.randn(B * max_pages * 2 * hkv * page * dh, device="cuda", generator=gen) * scale).half()
+                      for _ in range(max(1, min(16, math.ceil(512e6 / (cache_bytes // 2)))))]
+            table = t.arange(B * max_pages, dtype=t.int32, device="cuda")
+            for name, window, sc in (("full", 0, scale), ("swa1024", 1024, 1.0)):
+                wbytes = lib.hero_attn_paged_work_bytes(ctx, window, B, hq, hkv)
+                work = _bytes(wbytes)
+                args = []
+                for pg in pages:
+                    a = AttnDecodeArgs(_p(proj), stride, 2 * qw, 2 * qw + kw, _p(gq), _p(gk), 1e-6, _p(cs), None, None, 0,
+                                       _p(pos), None, _p(qrot), sc, window, _p(act), None, B, hq, hkv, dh)
+                    args.append(AttnPagedArgs(a, _p(pg), _p(table), page, max_pages, _p(work), wbytes))
+
+                def body():
+                    for pa in args:
+                        check(lib.hero_attn_decode_paged(pa, _stream()))
+
+                sec = _time_graph(body, len(args), replays)
+                l_eff = ctx if window == 0 else min(ctx, window)
+                nbytes = B * l_eff * kw * 2 * 2 + B * (qw + 2 * kw + qw) * 4
+                rows.append({"suite": "attn", "kernel": "attn_decode_paged (prep + split-K + combine), fp16 K/V",
+                             "variant": name, "ctx": ctx, "B": B, "copies": len(pages), "us": sec * 1e6,
+                             "GB/s": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS})
+                print(json.dumps(rows[-1]), flush=True)
+                del work
+            del pages
             t.cuda.empty_cache()
     return rows
 

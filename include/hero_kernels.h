@@ -181,6 +181,26 @@ typedef struct hero_attn_decode_args {
 } hero_attn_decode_args;
 int hero_attn_decode(const hero_attn_decode_args* args, void* stream);
 
+/* The same attention over a paged fp16 K/V cache (north-star format; the
+ * reference keeps fp32 rows, nm/src/attention.hpp:248-249). Keys and values
+ * are stored rounded to nearest-even fp16; the visible keys of each (sequence,
+ * KV head) are split across workgroups and the per-split softmax partials
+ * merged, so results equal the reference over fp16-rounded K/V to a few ulp
+ * (not bit for bit). Pages hold page_size positions: pool layout
+ * [page][2 = K, V][hkv][page_size][dh] fp16; page_table [b][max_pages].
+ * In `a`, k_cache, v_cache, scores and max_ctx are unused; the cache spans
+ * max_pages * page_size positions. */
+typedef struct hero_attn_paged_args {
+    hero_attn_decode_args a;
+    uint16_t* pages;
+    const int32_t* page_table;
+    int32_t page_size, max_pages;
+    float* work;                /* split partials, hero_attn_paged_work_bytes */
+    int64_t work_bytes;
+} hero_attn_paged_args;
+int64_t hero_attn_paged_work_bytes(int64_t max_ctx, int32_t window, int32_t b, int32_t hq, int32_t hkv);
+int hero_attn_decode_paged(const hero_attn_paged_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

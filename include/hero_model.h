@@ -78,7 +78,11 @@ int hero_model_decode_greedy(const hero_model* model, hero_state* state, int32_t
  * independent sequences at once: a batch state holds `batch` (1..16)
  * sequences, each with its own caches and position; every sequence's results
  * equal those of its own single-sequence state, bit for bit. */
-int hero_batch_state_create(const hero_model* model, int64_t max_tokens, int32_t batch, hero_state** out);
+int hero_batch_state_create(const hero_model* model, int64_t max_tokens, int32_t batch, uint32_t flags, hero_state** out);
+/* flags: keep the attention cache as fp16 pages with split-K attention (the
+ * north-star cache format; the reference's cache is fp32). Results then equal
+ * the reference over fp16-rounded keys and values to a few ulp. */
+#define HERO_STATE_KV_FP16 1u
 int64_t hero_state_batch(const hero_state* state);
 int64_t hero_state_seq_tokens(const hero_state* state, int32_t seq);
 /* hero_model_forward for sequence `seq` of a batch state. */

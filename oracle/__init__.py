@@ -43,6 +43,8 @@ _sigs = {
     "oracle_rope_table": (None, [c_size_t, c_double, c_size_t, c_size_t, c_void_p]),
     "oracle_rope_apply": (None, [c_void_p, c_size_t, c_void_p, c_size_t, c_size_t]),
     "oracle_attend_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_size_t, c_size_t, c_float, c_void_p]),
+    "oracle_model_set_kv_fp16": (None, [c_void_p, c_int]),
+    "oracle_round_fp16": (None, [c_void_p, c_size_t, c_void_p]),
     "oracle_model_open": (c_void_p, [c_char_p]),
     "oracle_model_open_image": (c_void_p, [c_void_p, c_size_t]),
     "oracle_model_close": (None, [c_void_p]),
@@ -230,6 +232,14 @@ def rope_apply(heads, inv_freq, position):
     return heads
 
 
+def round_fp16(x):
+    """IEEE fp16 round-to-nearest-even of fp32 values (the fp16 cache's storage)"""
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib.oracle_round_fp16(_p(x), x.size, _p(out))
+    return out
+
+
 def attend_decode(q, keys, values, hq, hkv, head_dim, window, scale):
     q, keys, values = _f32(q), _f32(keys), _f32(values)
     ctx = keys.shape[0]
@@ -268,6 +278,10 @@ class Model:
 
     def reset(self):
         lib.oracle_model_reset(self._h)
+
+    def set_kv_fp16(self, on: bool) -> None:
+        """store attention K/V rounded to fp16 (the GPU's fp16 paged cache)"""
+        lib.oracle_model_set_kv_fp16(self._h, 1 if on else 0)
 
     def tokens(self) -> int:
         return int(lib.oracle_model_tokens(self._h))

@@ -14,6 +14,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <immintrin.h>
 #include <mutex>
 #include <stdexcept>
 #include <thread>
@@ -390,6 +391,9 @@ void attend_one(const float* q, const float* keys, const float* values, size_t k
     }
 }
 
+// F16C's conversion with imm 0 rounds to nearest even (IEEE 754 default).
+float round_fp16_rne(float x) { return _cvtsh_ss(_cvtss_sh(x, 0)); }
+
 // ---------------------------------------------------------------------------
 // Qwen 3.5 hybrid (qwen35.hpp:288-462)
 // ---------------------------------------------------------------------------
@@ -456,6 +460,11 @@ std::vector<float> attention_mixer(const Model& m, const Layer& L, size_t layer,
     // append all T rows, then reduce (qwen35.hpp:386-387)
     s.keys[layer].insert(s.keys[layer].end(), K.begin(), K.end());
     s.values[layer].insert(s.values[layer].end(), V.begin(), V.end());
+    if (s.kv_fp16)
+        for (size_t i = s.keys[layer].size() - K.size(); i < s.keys[layer].size(); ++i) {
+            s.keys[layer][i] = round_fp16_rne(s.keys[layer][i]);
+            s.values[layer][i] = round_fp16_rne(s.values[layer][i]);
+        }
     const float score_scale = 1.f / std::sqrt(float(Dh));
     std::vector<float> A(T * QW);
     const size_t group = c.Hq / c.Hkv;

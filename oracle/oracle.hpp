@@ -135,12 +135,21 @@ struct Model {
 
 struct State {
     size_t tokens = 0;
+    // diagnosis switch (not in the reference, whose cache is fp32): store the
+    // attention keys and values rounded to IEEE fp16, nearest-even, as the
+    // GPU's fp16 paged cache does; reset() keeps it
+    bool kv_fp16 = false;
     // attention layers: fp32 K/V rows [tokens][Hkv*head_dim]
     std::vector<std::vector<float>> keys, values;
     // recurrent layers: conv history [(W-1)][CC] oldest first, delta state [Hv][Dk][Dv]
     std::vector<std::vector<float>> conv_hist, delta;
     void reset(const Config& c);
 };
+
+// IEEE binary16 rounding (nearest even) of fp32 values, returned as fp32:
+// the storage of the fp16 attention cache. Not the reference's fp16 encoder,
+// whose ties go away from zero (core.hpp:61-79).
+float round_fp16_rne(float x);
 
 // gather_rows / dequant_row (quant.hpp:464-480)
 void embed(const Model& m, const int32_t* ids, size_t n, float* out);

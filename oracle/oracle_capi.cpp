@@ -166,6 +166,10 @@ void oracle_model_reset(void* h) {
     Session* s = static_cast<Session*>(h);
     s->state.reset(s->model.c);
 }
+void oracle_model_set_kv_fp16(void* h, int on) { static_cast<Session*>(h)->state.kv_fp16 = on != 0; }
+void oracle_round_fp16(const float* x, size_t n, float* out) {
+    for (size_t i = 0; i < n; ++i) out[i] = round_fp16_rne(x[i]);
+}
 size_t oracle_model_tokens(void* h) { return static_cast<Session*>(h)->state.tokens; }
 int oracle_model_embed(void* h, const int32_t* ids, size_t n, float* out) {
     return guarded([&] { embed(static_cast<Session*>(h)->model, ids, n, out); });

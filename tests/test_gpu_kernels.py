@@ -484,3 +484,67 @@ def test_attn_decode_matches_oracle(lib, window):
         blocks = act_to_blocks(host(act, np.uint8), B, qw)
         for b in range(B):
             assert blocks[b].tobytes() == oracle.quantize_row_q8_0(got[b]).tobytes()
+
+
+@pytest.mark.parametrize("hq,window", [(8, 0), (8, 50), (16, 0)])
+def test_attn_paged_fp16_matches_oracle_over_fp16_kv(lib, hq, window):
+    """Split-K attention over the paged fp16 cache: pages of 16 positions in a
+    shuffled pool, contexts up to 300 (several pages per tile, several
+    splits), 4 and 8 query heads per KV head, full and windowed. The oracle
+    attends over the same K/V rounded to fp16 (its storage), sequentially; the
+    split softmax merges in another order, so the outputs agree to a few ulp,
+    the quantized W_o input to one step of its scale."""
+    from hero_amd._lib import AttnDecodeArgs, AttnPagedArgs
+
+    rng = np.random.default_rng(23 + hq + window)
+    B, hkv, dh, page, max_pages, steps = 2, 2, 128, 16, 20, 300
+    max_ctx = page * max_pages
+    qw, kw = hq * dh, hkv * dh
+    stride = 2 * qw + 2 * kw
+    qg = (1 + 0.1 * rng.standard_normal(dh)).astype(np.float32)
+    kg = (1 + 0.1 * rng.standard_normal(dh)).astype(np.float32)
+    eps = np.float32(1e-6)
+    scale = np.float32(1.0) / np.sqrt(np.float32(dh)) if window == 0 else np.float32(1.0)
+    inv = oracle.rope_inv_freq(dh, 1e6, 32)
+    d_cs = dev(oracle.rope_table(dh, 1e6, 32, max_ctx))
+    table = rng.permutation(B * max_pages).astype(np.int32).reshape(B, max_pages)
+    d_table = dev(table)
+    d_pages = empty(B * max_pages * 2 * hkv * page * dh * 2)
+    wbytes = lib.hero_attn_paged_work_bytes(max_ctx, window, B, hq, hkv)
+    d_work = empty(wbytes)
+    d_qr = empty(B * qw * 4)
+    act = empty(lib.hero_q8_0_act_bytes(B, qw))
+    out = empty(B * qw * 4)
+    keys = [np.zeros((0, kw), np.float32) for _ in range(B)]
+    vals = [np.zeros((0, kw), np.float32) for _ in range(B)]
+    d_qg, d_kg = dev(qg), dev(kg)
+    checked = 0
+    for step in range(steps):
+        proj = (rng.standard_normal((B, stride))).astype(np.float32)
+        d_proj, d_pos = dev(proj), dev(np.array([step, step], np.int32))
+        a = AttnDecodeArgs(ptr(d_proj), stride, 2 * qw, 2 * qw + kw, ptr(d_qg), ptr(d_kg), eps, ptr(d_cs), None, None,
+                           0, ptr(d_pos), None, ptr(d_qr), scale, window, ptr(act), ptr(out), B, hq, hkv, dh)
+        pa = AttnPagedArgs(a, ptr(d_pages), ptr(d_table), page, max_pages, ptr(d_work), wbytes)
+        check(lib.hero_attn_decode_paged(pa, stream()))
+        last = step in (0, 1, 63, 64, 65, 130, 200) or step == steps - 1
+        for b in range(B):
+            p = proj[b]
+            k = oracle.rope_apply(oracle.rmsnorm(p[2 * qw: 2 * qw + kw].reshape(hkv, dh), kg, eps), inv, step)
+            keys[b] = np.concatenate([keys[b], oracle.round_fp16(k.reshape(1, kw))])
+            vals[b] = np.concatenate([vals[b], oracle.round_fp16(p[2 * qw + kw:].reshape(1, kw))])
+        if not last:
+            continue
+        got = host(out, np.float32, (B, qw))
+        blocks = act_to_blocks(host(act, np.uint8), B, qw)
+        for b in range(B):
+            p = proj[b]
+            q = np.stack([p[h * 2 * dh: h * 2 * dh + dh] for h in range(hq)])
+            g = np.concatenate([p[h * 2 * dh + dh: h * 2 * dh + 2 * dh] for h in range(hq)])
+            q = oracle.rope_apply(oracle.rmsnorm(q, qg, eps), inv, step)
+            att = oracle.attend_decode(q.reshape(-1), keys[b], vals[b], hq, hkv, dh, window, scale).reshape(-1)
+            expect = (att * oracle.sigmoid(g)).astype(np.float32)
+            np.testing.assert_allclose(got[b], expect, rtol=2e-5, atol=2e-6, err_msg=f"step {step} seq {b}")
+            want = oracle.quantize_row_q8_0(got[b])
+            assert blocks[b].tobytes() == want.tobytes()  # the kernel quantizes its own output exactly
+            checked += 1
+    assert checked == 16

@@ -160,3 +160,19 @@ def test_fp16_encoder_is_nearest_ties_away():
     want = _fp16_nearest_ties_away(x)
     bad = np.flatnonzero(got != want)
     assert bad.size == 0, [(float(x[i]), hex(int(got[i])), hex(int(want[i]))) for i in bad[:5]]
+
+
+def test_fp16_cache_rounding_is_ieee_nearest_even():
+    """The oracle's fp16 cache rounding (F16C) equals numpy's IEEE binary16
+    conversion: normals at every scale, subnormals, exact midpoints (ties to
+    even), the overflow edge, signed zeros and infinities."""
+    rng = np.random.default_rng(5)
+    x = np.concatenate([
+        rng.standard_normal(100000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 5, 100000).astype(np.float32),
+        (np.arange(0, 2048, dtype=np.float32) + 0.5) * np.float32(2.0 ** -24),   # subnormal midpoints
+        (np.arange(1024, 2048, dtype=np.float32) + 0.5) * np.float32(2.0 ** -10),  # normal midpoints in [1, 2)
+        np.array([65504, 65519.99, 65520, 7e4, -65520, 0.0, -0.0, np.inf, -np.inf, 6e-8, 2.9e-8, 3.0e-8], np.float32),
+    ]).astype(np.float32)
+    want = x.astype(np.float16).astype(np.float32)
+    got = oracle.round_fp16(x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

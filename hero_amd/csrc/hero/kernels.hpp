@@ -85,9 +85,19 @@ struct GdnPrefillWork {
     float* v;   // [T][Hv][128]
     float* o;   // [T][Hv][128] delta-rule outputs before the head norm
     float* bd;  // [T][Hv][2] beta, decay
+    float* g;   // [T][Hv] log of the decay (decay = exp(g))
+    // the chunked form only (chunks of 64 tokens, c = t / 64):
+    float* u;   // [T][Hv][128] (I + L)^-1 beta v
+    float* wm;  // [T][Hv][128] (I + L)^-1 beta gamma k
+    float* p;   // [c][Hv][64][64] exp(G_t - G_s) q_t . k_s, s <= t
+    float* G;   // [T][Hv] cumulative log-decay within the chunk
 };
 int64_t gdn_prefill_work_bytes(int64_t T, int64_t Hk, int64_t Hv);
-void launch_gdn_prefill(const GdnDecodeArgs& a, void* work, hipStream_t s);
+// chunked = false: the token-serial scan, bit-exact with T decode steps.
+// chunked = true: the chunked (WY) form of the same recurrence over chunks of
+// 64 tokens -- matrix products instead of a 128-long chain per token; equal to
+// the serial form up to fp32 rounding order, not bit for bit.
+void launch_gdn_prefill(const GdnDecodeArgs& a, void* work, hipStream_t s, bool chunked = false);
 
 // attn.hip: gated GQA decode over an fp32 K/V cache (one token per sequence)
 struct AttnDecodeArgs {

@@ -252,6 +252,15 @@ int64_t hero_gdn_prefill_work_bytes(int64_t t, int32_t hk, int32_t hv) {
     return gdn_prefill_work_bytes(t, hk, hv);
 }
 
+int hero_gdn_prefill_chunked(const hero_gdn_decode_args* p, void* work, int64_t work_bytes, void* stream) {
+    return guard([&] {
+        const GdnDecodeArgs g = gdn_args(p);
+        require(work != nullptr && work_bytes >= gdn_prefill_work_bytes(g.B, g.Hk, g.Hv), "prefill workspace too small");
+        launch_gdn_prefill(g, work, as_stream(stream), true);
+        check_launch("hero_gdn_prefill_chunked");
+    });
+}
+
 int hero_gdn_prefill(const hero_gdn_decode_args* p, void* work, int64_t work_bytes, void* stream) {
     return guard([&] {
         const GdnDecodeArgs g = gdn_args(p);

@@ -280,6 +280,11 @@ __device__ __forceinline__ GdnPrefillWork gdn_work(void* ws, int64_t T, int Hk, 
     w.v = w.k + T * Hk * kGdnDim;
     w.o = w.v + T * Hv * kGdnDim;
     w.bd = w.o + T * Hv * kGdnDim;
+    w.g = w.bd + T * Hv * 2;
+    w.u = w.g + T * Hv;
+    w.wm = w.u + T * Hv * kGdnDim;
+    w.p = w.wm + T * Hv * kGdnDim;
+    w.G = w.p + (T + 63) / 64 * Hv * 64 * 64;
     return w;
 }
 
@@ -332,6 +337,7 @@ __global__ __launch_bounds__(kGdnDim) void gdn_prep_kernel(GdnDecodeArgs a, void
             const float g = a.decay[h] * softplus_f32(P[a.alpha_off + h] + a.dt_bias[h]);
             w.bd[(int64_t(t) * a.Hv + h) * 2] = beta;
             w.bd[(int64_t(t) * a.Hv + h) * 2 + 1] = exp_f32(g);
+            w.g[int64_t(t) * a.Hv + h] = g;
         }
     }
 }
@@ -491,6 +497,288 @@ __global__ __launch_bounds__(kGdnDim) void gdn_scan_kernel(GdnDecodeArgs a, void
     for (int i = 0; i < kGdnDim; ++i) Sw[i * kGdnDim + j] = col[i];
 }
 
+// ---- the chunked form (WY representation) ------------------------------------------------
+// Within a chunk of C tokens starting from state S0, with G_t = sum_{s<=t} g_s
+// (cumulative log-decay) and gamma_t = exp(G_t), the recurrence
+//   S_t = decay_t S_{t-1} + k_t delta_t^T,  delta_t = beta_t (v_t - (decay_t S_{t-1})^T k_t),
+//   o_t = S_t^T q_t
+// unrolls to (I + L) delta = beta V - beta gamma K S0, L[t][s] = beta_t exp(G_t - G_s) k_t.k_s (s < t):
+//   delta = U - W S0,  U = (I + L)^-1 beta V,  W = (I + L)^-1 beta gamma K,
+//   o_t   = gamma_t (Q S0)_t + sum_{s<=t} P[t][s] delta_s,  P[t][s] = exp(G_t - G_s) q_t.k_s,
+//   S_C   = gamma_C S0 + sum_s exp(G_C - G_s) k_s delta_s^T.
+// U, W and P do not depend on the state: gdn_chunk_prep_kernel forms them for
+// every (chunk, head) at once; gdn_chunk_scan_kernel then carries the state
+// through the chunks in order with three small matrix products per chunk.
+// This form is pinned to the serial one by tolerance (its sums run in another
+// order), so it uses fused multiply-adds.
+constexpr int kChunk = 64;             // tokens per chunk
+constexpr int kChunkCols = 32;         // state columns per scan workgroup
+constexpr int kChunkKp = kGdnDim + 4;  // padded rows
+
+struct ChunkPrepShared {
+    float K[kChunk][kChunkKp];
+    float Q[kChunk][kChunkKp];
+    float L[kChunk][kChunk + 4];
+    float X[kChunk][2 * kGdnDim];  // the U and W columns being solved, one per thread
+    float G[kChunk], beta[kChunk];
+};
+constexpr size_t kChunkPrepShared = sizeof(ChunkPrepShared);
+
+// one workgroup per (chunk, value head)
+__global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(GdnDecodeArgs a, void* ws_) {
+    extern __shared__ __align__(16) float cp_raw[];
+    ChunkPrepShared& sh = *reinterpret_cast<ChunkPrepShared*>(cp_raw);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int c = blockIdx.x, h = blockIdx.y, hk = h % a.Hk;
+    const int T = a.B;
+    if (a.positions[0] < 0) return;
+    const GdnPrefillWork w = gdn_work(ws_, T, a.Hk, a.Hv);
+    const int t0 = c * kChunk, n = min(kChunk, T - t0);
+    for (int e = tid; e < kChunk * (kGdnDim / 4); e += 256) {
+        const int t = e / (kGdnDim / 4), c4 = e % (kGdnDim / 4);
+        float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), qv = kv;
+        if (t < n) {
+            const int64_t row = (int64_t(t0 + t) * a.Hk + hk) * kGdnDim;
+            kv = reinterpret_cast<const float4*>(w.k + row)[c4];
+            qv = reinterpret_cast<const float4*>(w.q + row)[c4];
+        }
+        *reinterpret_cast<float4*>(&sh.K[t][4 * c4]) = kv;
+        *reinterpret_cast<float4*>(&sh.Q[t][4 * c4]) = qv;
+    }
+    if (tid < kChunk) {  // wave 0: beta and the cumulative log-decay (an inclusive scan)
+        const bool on = tid < n;
+        sh.beta[tid] = on ? w.bd[(int64_t(t0 + tid) * a.Hv + h) * 2] : 0.f;
+        float G = on ? w.g[int64_t(t0 + tid) * a.Hv + h] : 0.f;
+        for (int off = 1; off < 64; off <<= 1) {
+            const float o = __shfl_up(G, off);
+            if (lane >= off) G += o;
+        }
+        sh.G[tid] = G;
+        if (on) w.G[int64_t(t0 + tid) * a.Hv + h] = G;
+    }
+    __syncthreads();
+    // L (s < t) and P (s <= t): a 4x4 block of (row t, column s) per thread
+    {
+        const int br = tid >> 4, bc = tid & 15;
+        float kk[4][4] = {}, qk[4][4] = {};
+        for (int i = 0; i < kGdnDim; i += 4) {
+            float4 kr[4], qr[4], kc[4];
+#pragma unroll
+            for (int uu = 0; uu < 4; ++uu) {
+                kr[uu] = *reinterpret_cast<const float4*>(&sh.K[4 * br + uu][i]);
+                qr[uu] = *reinterpret_cast<const float4*>(&sh.Q[4 * br + uu][i]);
+                kc[uu] = *reinterpret_cast<const float4*>(&sh.K[4 * bc + uu][i]);
+            }
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) {
+                    kk[rr][cc] = fmaf(kr[rr].x, kc[cc].x, fmaf(kr[rr].y, kc[cc].y, fmaf(kr[rr].z, kc[cc].z, fmaf(kr[rr].w, kc[cc].w, kk[rr][cc]))));
+                    qk[rr][cc] = fmaf(qr[rr].x, kc[cc].x, fmaf(qr[rr].y, kc[cc].y, fmaf(qr[rr].z, kc[cc].z, fmaf(qr[rr].w, kc[cc].w, qk[rr][cc]))));
+                }
+        }
+        float* P = w.p + (int64_t(c) * a.Hv + h) * kChunk * kChunk;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                const int t = 4 * br + rr, s = 4 * bc + cc;
+                const float f = s <= t ? exp_f32(sh.G[t] - sh.G[s]) : 0.f;
+                sh.L[t][s] = s < t ? sh.beta[t] * f * kk[rr][cc] : 0.f;
+                P[t * kChunk + s] = f * qk[rr][cc];
+            }
+    }
+    __syncthreads();
+    // U and W by forward substitution, one column per thread:
+    // x_t = b_t - sum_{s<t} L[t][s] x_s; columns 0..127 of beta v, 128..255 of beta gamma k
+    {
+        const bool is_u = tid < kGdnDim;
+        const int col = tid & (kGdnDim - 1);
+        for (int t = 0; t < kChunk; ++t) {
+            float b = 0.f;
+            if (t < n) b = is_u ? sh.beta[t] * w.v[(int64_t(t0 + t) * a.Hv + h) * kGdnDim + col] : sh.beta[t] * exp_f32(sh.G[t]) * sh.K[t][col];
+            sh.X[t][tid] = b;
+        }
+        for (int t = 1; t < n; ++t) {
+            float acc = sh.X[t][tid];
+            for (int s2 = 0; s2 < t; ++s2) acc = fmaf(-sh.L[t][s2], sh.X[s2][tid], acc);
+            sh.X[t][tid] = acc;
+        }
+        float* dst = is_u ? w.u : w.wm;
+        for (int t = 0; t < n; ++t) dst[(int64_t(t0 + t) * a.Hv + h) * kGdnDim + col] = sh.X[t][tid];
+    }
+}
+
+struct ChunkScanShared {
+    float Wm[kChunk][kChunkKp];
+    float Q[kChunk][kChunkKp];
+    float K[kChunk][kChunkKp];
+    float P[kChunk][kChunk + 4];
+    float S[kGdnDim][kChunkCols + 4];  // rows of 16-byte multiples
+    float D[kChunk][kChunkCols + 4];   // U, then delta
+    float G[kChunk], wsf[kChunk];
+};
+constexpr size_t kChunkScanShared = sizeof(ChunkScanShared);
+
+// one workgroup per (value head, 32 state columns); the chunks in order, the
+// next chunk's inputs loading while this one computes
+// v or zeros, component by component (a select of the whole float4 is lowered
+// through scratch memory)
+__device__ __forceinline__ float4 sel4(bool keep, float4 v) {
+    return make_float4(keep ? v.x : 0.f, keep ? v.y : 0.f, keep ? v.z : 0.f, keep ? v.w : 0.f);
+}
+
+// one workgroup per CU (its shared memory): the whole register file is this wave's
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gdn_chunk_scan_kernel(GdnDecodeArgs a, void* ws_) {
+    extern __shared__ __align__(16) float cs_raw[];
+    ChunkScanShared& sh = *reinterpret_cast<ChunkScanShared*>(cs_raw);
+    const int tid = threadIdx.x;
+    const int h = blockIdx.x, hk = h % a.Hk, j0 = blockIdx.y * kChunkCols;
+    const int T = a.B;
+    if (a.positions[0] < 0) return;
+    const GdnPrefillWork w = gdn_work(ws_, T, a.Hk, a.Hv);
+    float* S = a.state + int64_t(h) * kGdnState;
+    const int nchunks = (T + kChunk - 1) / kChunk;
+
+    // the chunk's inputs in flight in registers: thread -> rows t = tid/32 + 8m,
+    // 16-byte piece tid % 32 of W, Q, K; 16 values of P; 8 of U. Rows past the
+    // chunk's end load row 0 (in range) and are zeroed.
+    float4 rw[8], rq[8], rk[8];
+    float rp[16], ru[8], rg;
+    auto load = [&](int c) __attribute__((always_inline)) {
+        const int t0 = c * kChunk, n = min(kChunk, T - t0);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const int t = (tid >> 5) + 8 * m, c4 = tid & 31;
+            const int tc = t < n ? t : 0;
+            const int64_t krow = (int64_t(t0 + tc) * a.Hk + hk) * kGdnDim;
+            const float4 wv = reinterpret_cast<const float4*>(w.wm + (int64_t(t0 + tc) * a.Hv + h) * kGdnDim)[c4];
+            const float4 qv = reinterpret_cast<const float4*>(w.q + krow)[c4];
+            const float4 kv = reinterpret_cast<const float4*>(w.k + krow)[c4];
+            rw[m] = sel4(t < n, wv);
+            rq[m] = sel4(t < n, qv);
+            rk[m] = sel4(t < n, kv);
+        }
+        const float* P = w.p + (int64_t(c) * a.Hv + h) * kChunk * kChunk;
+#pragma unroll
+        for (int m = 0; m < 16; ++m) rp[m] = P[tid + 256 * m];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const int e = tid + 256 * m, t = e / kChunkCols, jj = e % kChunkCols;
+            const float uv = w.u[(int64_t(t0 + (t < n ? t : 0)) * a.Hv + h) * kGdnDim + j0 + jj];
+            ru[m] = t < n ? uv : 0.f;
+        }
+        const float gv = w.G[int64_t(t0 + (tid < n ? tid : 0)) * a.Hv + h];
+        rg = tid < n ? gv : 0.f;
+    };
+    auto store = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const int t = (tid >> 5) + 8 * m, c4 = tid & 31;
+            *reinterpret_cast<float4*>(&sh.Wm[t][4 * c4]) = rw[m];
+            *reinterpret_cast<float4*>(&sh.Q[t][4 * c4]) = rq[m];
+            *reinterpret_cast<float4*>(&sh.K[t][4 * c4]) = rk[m];
+        }
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+            const int e = tid + 256 * m;
+            sh.P[e / kChunk][e % kChunk] = rp[m];
+        }
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const int e = tid + 256 * m;
+            sh.D[e / kChunkCols][e % kChunkCols] = ru[m];
+        }
+        if (tid < kChunk) sh.G[tid] = rg;
+    };
+
+    for (int e = tid; e < kGdnDim * kChunkCols; e += 256) {
+        const int i = e / kChunkCols, jj = e % kChunkCols;
+        sh.S[i][jj] = S[i * kGdnDim + j0 + jj];
+    }
+    load(0);
+    store();
+    if (nchunks > 1) load(1);
+    for (int c = 0; c < nchunks; ++c) {
+        const int t0 = c * kChunk, n = min(kChunk, T - t0);
+        __syncthreads();  // the chunk's tiles are in shared memory
+        if (tid < kChunk) sh.wsf[tid] = exp_f32(sh.G[n - 1] - sh.G[tid]);
+        // delta = U - W S0 and gamma (Q S0): thread -> row t, 8 columns
+        const int t = tid >> 2, jq = (tid & 3) * 8;
+        float qs0[8], ws0[8];
+#pragma unroll
+        for (int uu = 0; uu < 8; ++uu) qs0[uu] = ws0[uu] = 0.f;
+        for (int i = 0; i < kGdnDim; i += 4) {
+            const float4 w4 = *reinterpret_cast<const float4*>(&sh.Wm[t][i]);
+            const float4 q4 = *reinterpret_cast<const float4*>(&sh.Q[t][i]);
+            const float wv[4] = {w4.x, w4.y, w4.z, w4.w}, qv[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+                const float4 s0 = *reinterpret_cast<const float4*>(&sh.S[i + ii][jq]);
+                const float4 s1 = *reinterpret_cast<const float4*>(&sh.S[i + ii][jq + 4]);
+                const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+                for (int uu = 0; uu < 8; ++uu) {
+                    ws0[uu] = fmaf(wv[ii], sv[uu], ws0[uu]);
+                    qs0[uu] = fmaf(qv[ii], sv[uu], qs0[uu]);
+                }
+            }
+        }
+        const float gt = exp_f32(sh.G[t]);
+#pragma unroll
+        for (int uu = 0; uu < 8; ++uu) {
+            sh.D[t][jq + uu] -= ws0[uu];
+            qs0[uu] *= gt;
+        }
+        __syncthreads();
+        // outputs: o_t = gamma_t (Q S0)_t + sum_{s<=t} P[t][s] delta_s
+        if (t < n) {
+            for (int s2 = 0; s2 <= t; ++s2) {
+                const float pv = sh.P[t][s2];
+                const float4 d0 = *reinterpret_cast<const float4*>(&sh.D[s2][jq]);
+                const float4 d1 = *reinterpret_cast<const float4*>(&sh.D[s2][jq + 4]);
+                const float dv[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+#pragma unroll
+                for (int uu = 0; uu < 8; ++uu) qs0[uu] = fmaf(pv, dv[uu], qs0[uu]);
+            }
+            float* dst = w.o + (int64_t(t0 + t) * a.Hv + h) * kGdnDim + j0 + jq;
+            reinterpret_cast<float4*>(dst)[0] = make_float4(qs0[0], qs0[1], qs0[2], qs0[3]);
+            reinterpret_cast<float4*>(dst)[1] = make_float4(qs0[4], qs0[5], qs0[6], qs0[7]);
+        }
+        // state: S = gamma_n S0 + sum_s exp(G_n - G_s) k_s delta_s^T: thread -> row i, 16 columns
+        {
+            const int i = tid >> 1, jh = (tid & 1) * 16;
+            const float gl = exp_f32(sh.G[n - 1]);
+            float acc[16];
+#pragma unroll
+            for (int uu = 0; uu < 16; ++uu) acc[uu] = gl * sh.S[i][jh + uu];
+            for (int s2 = 0; s2 < n; ++s2) {
+                const float f = sh.wsf[s2] * sh.K[s2][i];
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const float4 d = *reinterpret_cast<const float4*>(&sh.D[s2][jh + 4 * q4]);
+                    acc[4 * q4 + 0] = fmaf(f, d.x, acc[4 * q4 + 0]);
+                    acc[4 * q4 + 1] = fmaf(f, d.y, acc[4 * q4 + 1]);
+                    acc[4 * q4 + 2] = fmaf(f, d.z, acc[4 * q4 + 2]);
+                    acc[4 * q4 + 3] = fmaf(f, d.w, acc[4 * q4 + 3]);
+                }
+            }
+#pragma unroll
+            for (int uu = 0; uu < 16; ++uu) sh.S[i][jh + uu] = acc[uu];  // row i, this thread's columns only
+        }
+        __syncthreads();  // every tile of this chunk is consumed
+        if (c + 1 < nchunks) {
+            store();
+            if (c + 2 < nchunks) load(c + 2);
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < kGdnDim * kChunkCols; e += 256) {
+        const int i = e / kChunkCols, jj = e % kChunkCols;
+        S[i * kGdnDim + j0 + jj] = sh.S[i][jj];
+    }
+}
+
 __global__ __launch_bounds__(kGdnDim) void gdn_out_kernel(GdnDecodeArgs a, void* ws) {
     const int j = threadIdx.x, h = blockIdx.x, t = blockIdx.y;
     const int T = a.B;
@@ -538,9 +826,12 @@ void launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t s) {
     }
 }
 
-int64_t gdn_prefill_work_bytes(int64_t T, int64_t Hk, int64_t Hv) { return T * (2 * Hk * kGdnDim + 2 * Hv * kGdnDim + 2 * Hv) * 4; }
+int64_t gdn_prefill_work_bytes(int64_t T, int64_t Hk, int64_t Hv) {
+    // q, k; v, o; beta, decay, g; u, wm; G; p
+    return (T * (2 * Hk * kGdnDim + 2 * Hv * kGdnDim + 3 * Hv + 2 * Hv * kGdnDim + Hv) + (T + 63) / 64 * Hv * 64 * 64) * 4;
+}
 
-void launch_gdn_prefill(const GdnDecodeArgs& a, void* work, hipStream_t s) {
+void launch_gdn_prefill(const GdnDecodeArgs& a, void* work, hipStream_t s, bool chunked) {
     const dim3 prep(unsigned(a.Hk + a.Hv), unsigned(a.B));
     switch (a.W) {
         case 1: hipLaunchKernelGGL(gdn_prep_kernel<1>, prep, dim3(kGdnDim), 0, s, a, work); break;
@@ -552,7 +843,13 @@ void launch_gdn_prefill(const GdnDecodeArgs& a, void* work, hipStream_t s) {
         case 7: hipLaunchKernelGGL(gdn_prep_kernel<7>, prep, dim3(kGdnDim), 0, s, a, work); break;
         default: hipLaunchKernelGGL(gdn_prep_kernel<8>, prep, dim3(kGdnDim), 0, s, a, work); break;
     }
-    hipLaunchKernelGGL(gdn_scan_kernel, dim3(unsigned(a.Hv)), dim3(kGdnDim), 0, s, a, work);
+    if (chunked)
+    {
+        hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(unsigned((a.B + kChunk - 1) / kChunk), unsigned(a.Hv)), dim3(256), kChunkPrepShared, s, a, work);
+        hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(unsigned(a.Hv), unsigned(kGdnDim / kChunkCols)), dim3(256), kChunkScanShared, s, a, work);
+    }
+    else
+        hipLaunchKernelGGL(gdn_scan_kernel, dim3(unsigned(a.Hv)), dim3(kGdnDim), 0, s, a, work);
     hipLaunchKernelGGL(gdn_out_kernel, dim3(unsigned(a.Hv), unsigned(a.B)), dim3(kGdnDim), 0, s, a, work);
     const int64_t CC = 2 * int64_t(a.Hk) * kGdnDim + int64_t(a.Hv) * kGdnDim;
     const int64_t n = int64_t(std::min(a.B, a.W)) * CC;

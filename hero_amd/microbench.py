@@ -13,7 +13,8 @@ gemv   Q8_0 matvec / matmul. W is N x K int8 uniform in [-127, 127] with fp16
 gdn    the fused delta-net layer body (conv + SiLU, L2 norms, gates, the delta
        rule on the fp32 state, head norm, gate, quantize) with 16 heads of
        128 x 128: one decode step at B in {1, 8, 32} from a state warmed by 64
-       steps, and the bit-exact token-serial prefill of 4096 tokens.
+       steps, and the prefill of 4096 tokens: the bit-exact token-serial scan
+       and the chunked (WY) form with chunks of 64.
 attn   gated GQA decode (32 q / 8 kv heads of 128) at context {1k, 8k, 32k} x
        B {1, 16}: full causal (scale 1/sqrt(128)) and a 1024 sliding window
        (scale 1), over the fp32 cache (the reference's precision, bit-exact
@@ -201,25 +202,29 @@ def bench_gdn(lib, replays: int = 50):
     wb = lib.hero_gdn_prefill_work_bytes(T, H, H)
     work = _bytes(wb)
 
-    def prefill():
-        bufs["state"].zero_()
-        bufs["hist"].zero_()
-        check(lib.hero_gdn_prefill(a, _p(work), wb, _stream()))
-
-    prefill()
-    t.cuda.synchronize()
-    e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
-    reps = 5
-    e0.record()
-    for _ in range(reps):
-        prefill()
-    e1.record()
-    e1.synchronize()
-    sec = e0.elapsed_time(e1) * 1e-3 / reps
     serial_flops = 7.0 * T * H * dk * dk
-    rows.append({"suite": "gdn", "kernel": "gdn_prefill (prep + token-serial scan + out, bit-exact)", "mode": "prefill",
-                 "H": H, "T": T, "us": sec * 1e6, "tok/s": T / sec, "GFLOP/s (serial-equivalent)": serial_flops / sec / 1e9})
-    print(json.dumps(rows[-1]), flush=True)
+    C = 64
+    chunk_flops = (T / C) * H * (6 * C * dk * dk + 8 * C * C * dk + C ** 3 / 3)  # the chunked form's unit of work
+    for name, fn, flops in (("gdn_prefill (prep + token-serial scan + out, bit-exact)", lib.hero_gdn_prefill, serial_flops),
+                            ("gdn_prefill_chunked (prep + chunked WY form, chunk 64 + out)", lib.hero_gdn_prefill_chunked, chunk_flops)):
+        def prefill():
+            bufs["state"].zero_()
+            bufs["hist"].zero_()
+            check(fn(a, _p(work), wb, _stream()))
+
+        prefill()
+        t.cuda.synchronize()
+        e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        reps = 5
+        e0.record()
+        for _ in range(reps):
+            prefill()
+        e1.record()
+        e1.synchronize()
+        sec = e0.elapsed_time(e1) * 1e-3 / reps
+        rows.append({"suite": "gdn", "kernel": name, "mode": "prefill", "H": H, "T": T, "us": sec * 1e6, "tok/s": T / sec,
+                     "GFLOP/s": flops / sec / 1e9})
+        print(json.dumps(rows[-1]), flush=True)
     return rows
 
 

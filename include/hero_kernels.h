@@ -154,6 +154,13 @@ int hero_gdn_decode(const hero_gdn_decode_args* args, void* stream);
 int64_t hero_gdn_prefill_work_bytes(int64_t t, int32_t hk, int32_t hv);
 int hero_gdn_prefill(const hero_gdn_decode_args* args, void* work, int64_t work_bytes, void* stream);
 
+/* The same prefill in the chunked (WY) form of the delta rule over chunks of 64
+ * tokens: the per-token recurrence unrolled into small matrix products per
+ * chunk (the chunked-prefill form the reference's serial loop,
+ * nm/src/qwen35.hpp:436-455, is pinned against). Equal to hero_gdn_prefill up
+ * to fp32 rounding order (tolerance, not bit for bit); same workspace. */
+int hero_gdn_prefill_chunked(const hero_gdn_decode_args* args, void* work, int64_t work_bytes, void* stream);
+
 /* Gated GQA attention decode over an fp32 K/V cache, one token for each of
  * B sequences: head-pair split, q/k RMSNorm + RoPE (host table), cache
  * append, softmax(scale*q.k) over the visible rows, sum alpha*v,

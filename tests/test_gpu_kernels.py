@@ -440,6 +440,56 @@ def test_gdn_prefill_chunks_match_oracle(lib, W, chunks):
         pos += T
 
 
+@pytest.mark.parametrize("T,hk,hv", [(70, 2, 4), (300, 4, 4)])
+def test_gdn_chunked_prefill_matches_serial(lib, T, hk, hv):
+    """The chunked (WY) delta-net prefill against the token-serial one (which
+    is bit-exact with the oracle) and, for the shorter case, the oracle's own
+    serial recurrence: outputs and the final state within fp32 rounding-order
+    tolerance, over a partial last chunk and several chunks, from a non-zero
+    state and a non-empty conv ring (a first chunk of 37 tokens)."""
+    from hero_amd._lib import GdnDecodeArgs
+
+    rng = np.random.default_rng(T + hk)
+    dk, W = 128, 4
+    cc = 2 * hk * dk + hv * dk
+    stride = cc + hv * dk + 2 * hv
+    taps = (rng.standard_normal((cc, W)) * 0.5).astype(np.float32)
+    dt = (rng.standard_normal(hv) * 0.1).astype(np.float32)
+    decay = (-np.exp(rng.standard_normal(hv) * 0.5)).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(dk)).astype(np.float32)
+    eps = np.float32(1e-6)
+    d_taps, d_dt, d_decay, d_gamma = dev(taps), dev(dt), dev(decay), dev(gamma)
+    warm = (rng.standard_normal((37, stride)) * 0.7).astype(np.float32)
+    proj = (rng.standard_normal((T, stride)) * 0.7).astype(np.float32)
+    wbytes = lib.hero_gdn_prefill_work_bytes(T, hk, hv)
+    results = []
+    for entry in (lib.hero_gdn_prefill, lib.hero_gdn_prefill_chunked):
+        d_hist = empty(W * cc * 4)
+        d_state = empty(hv * dk * dk * 4)
+        work = empty(wbytes)
+        act = empty(lib.hero_q8_0_act_bytes(T, hv * dk))
+        out = empty(T * hv * dk * 4)
+        for rows, pos0, fn in ((warm, 0, lib.hero_gdn_prefill), (proj, 37, entry)):
+            d_proj, d_pos = dev(rows), dev(np.array([pos0], np.int32))
+            n = rows.shape[0]
+            a = GdnDecodeArgs(ptr(d_proj), stride, cc, cc + hv * dk, cc + hv * dk + hv, ptr(d_taps), ptr(d_hist), ptr(d_state),
+                              ptr(d_dt), ptr(d_decay), ptr(d_gamma), eps, ptr(d_pos), ptr(act), ptr(out), n, hk, hv, dk, dk, W)
+            check(fn(a, ptr(work), wbytes, stream()))
+        results.append((host(out, np.float32, (T, hv * dk)).copy(), host(d_state, np.float32, (hv, dk, dk)).copy()))
+    (o_ser, s_ser), (o_chk, s_chk) = results
+    scale_o, scale_s = np.abs(o_ser).max(), np.abs(s_ser).max()
+    np.testing.assert_allclose(o_chk, o_ser, rtol=1e-3, atol=1e-4 * scale_o)
+    np.testing.assert_allclose(s_chk, s_ser, rtol=1e-3, atol=1e-4 * scale_s)
+    if T <= 100:  # the oracle's serial recurrence, token by token
+        hist = np.zeros((W - 1, cc), np.float32)
+        state = np.zeros((hv, dk, dk), np.float32)
+        for t in range(37):
+            gdn_reference(warm[t], taps, hist, state, dt, decay, gamma, eps, hk, hv, t)
+        for t in range(T):
+            expect = gdn_reference(proj[t], taps, hist, state, dt, decay, gamma, eps, hk, hv, 37 + t)
+            np.testing.assert_allclose(o_chk[t], expect, rtol=1e-3, atol=1e-4 * scale_o)
+
+
 # ---- attention decode ------------------------------------------------------------------
 @pytest.mark.parametrize("window", [0, 3])
 def test_attn_decode_matches_oracle(lib, window):

@@ -52,12 +52,14 @@ class Logits:
 
 class PrefixState:
     """Device-resident carried state of one sequence (nm/src/qwen35.hpp:206-241).
-    kv_fp16 keeps the attention cache as fp16 pages (split-K attention)."""
+    kv_fp16 keeps the attention cache as fp16 pages (split-K attention);
+    gdn_chunked runs the delta-net prefill in its chunked form."""
 
-    def __init__(self, model: "Qwen35Model", max_tokens: int, kv_fp16: bool = False):
+    def __init__(self, model: "Qwen35Model", max_tokens: int, kv_fp16: bool = False, gdn_chunked: bool = False):
         h = c_void_p()
-        if kv_fp16:
-            check(lib.hero_batch_state_create(model._h, max_tokens, 1, _lib.HERO_STATE_KV_FP16, byref(h)))
+        flags = (_lib.HERO_STATE_KV_FP16 if kv_fp16 else 0) | (_lib.HERO_STATE_GDN_CHUNKED if gdn_chunked else 0)
+        if flags:
+            check(lib.hero_batch_state_create(model._h, max_tokens, 1, flags, byref(h)))
         else:
             check(lib.hero_state_create(model._h, max_tokens, byref(h)))
         self._h = h
@@ -147,8 +149,8 @@ class Qwen35Model:
         except Exception:
             pass
 
-    def new_state(self, max_tokens: int | None = None, kv_fp16: bool = False) -> PrefixState:
-        return PrefixState(self, max_tokens or min(self.CTX, 4096), kv_fp16)
+    def new_state(self, max_tokens: int | None = None, kv_fp16: bool = False, gdn_chunked: bool = False) -> PrefixState:
+        return PrefixState(self, max_tokens or min(self.CTX, 4096), kv_fp16, gdn_chunked)
 
     def new_batch_state(self, max_tokens: int, batch: int, kv_fp16: bool = False) -> BatchState:
         return BatchState(self, max_tokens, batch, kv_fp16)

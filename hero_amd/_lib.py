@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(HERE, "libhero_amd.so")
 
 HERO_OK, HERO_EINVAL, HERO_EHIP, HERO_ERANGE, HERO_ENOMEM, HERO_EIO = range(6)
 HERO_STATE_KV_FP16 = 1  # hero_batch_state_create flag: fp16 paged attention cache
+HERO_STATE_GDN_CHUNKED = 2  # hero_batch_state_create flag: chunked delta-net prefill
 
 
 class HeroError(RuntimeError):

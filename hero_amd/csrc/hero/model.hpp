@@ -99,7 +99,9 @@ public:
     // `batch` independent sequences of up to `max_tokens` each; `kv_fp16`
     // keeps the attention cache as fp16 pages (split-K attention) instead of
     // the reference's fp32 rows
-    std::unique_ptr<State> new_state(int64_t max_tokens, int64_t batch = 1, bool kv_fp16 = false) const;
+    // gdn_chunked runs the delta-net prefill in its chunked form (tolerance-equal
+    // to the token-serial recurrence instead of bit-equal)
+    std::unique_ptr<State> new_state(int64_t max_tokens, int64_t batch = 1, bool kv_fp16 = false, bool gdn_chunked = false) const;
     // host rows out[n][D]
     void embed(const int32_t* ids, int64_t n, float* out) const;
     // T rows from host `rows` or from `ids`; logits / greedy id of the last row
@@ -171,7 +173,7 @@ private:
     // fp16 paged attention cache: per attention layer a pool of batch x
     // max_pages pages; page_table_ [batch][max_pages] (sequence b owns pages
     // b * max_pages ...); attn_work_ the split-K partials of a decode step
-    bool kv_fp16_ = false;
+    bool kv_fp16_ = false, gdn_chunked_ = false;
     int64_t max_pages_ = 0;
     std::vector<DeviceBuffer> kv_pages_;
     DeviceBuffer page_table_, attn_work_;

@@ -103,9 +103,9 @@ int hero_state_create(const hero_model* model, int64_t max_tokens, hero_state** 
 int hero_batch_state_create(const hero_model* model, int64_t max_tokens, int32_t batch, uint32_t flags, hero_state** out) {
     return guard([&] {
         need(model && out, "null argument");
-        need((flags & ~HERO_STATE_KV_FP16) == 0, "unknown state flags");
+        need((flags & ~(HERO_STATE_KV_FP16 | HERO_STATE_GDN_CHUNKED)) == 0, "unknown state flags");
         auto s = std::make_unique<hero_state>();
-        s->impl = model->impl->new_state(max_tokens, batch, (flags & HERO_STATE_KV_FP16) != 0);
+        s->impl = model->impl->new_state(max_tokens, batch, (flags & HERO_STATE_KV_FP16) != 0, (flags & HERO_STATE_GDN_CHUNKED) != 0);
         *out = s.release();
     });
 }

@@ -294,11 +294,13 @@ void Qwen35Model::build_rope_table(int64_t positions) {
 }
 
 // ---- state --------------------------------------------------------------------------
-std::unique_ptr<Qwen35Model::State> Qwen35Model::new_state(int64_t max_tokens, int64_t batch, bool kv_fp16) const {
+std::unique_ptr<Qwen35Model::State> Qwen35Model::new_state(int64_t max_tokens, int64_t batch, bool kv_fp16, bool gdn_chunked) const {
     if (max_tokens <= 0 || max_tokens > c_.CTX || max_tokens > rope_positions_) throw Error(HERO_ERANGE, "state: max_tokens must be in 1.." + std::to_string(std::min(c_.CTX, rope_positions_)));
     if (batch < 1 || batch > kMaxBatch) throw Error(HERO_EINVAL, "state: batch must be in 1.." + std::to_string(kMaxBatch));
     if (kv_fp16 && c_.Hq / c_.Hkv > kAttnMaxGroup) throw Error(HERO_EINVAL, "state: the fp16 cache takes at most 8 query heads per KV head");
-    return std::unique_ptr<State>(new State(*this, max_tokens, batch, kv_fp16));
+    std::unique_ptr<State> st(new State(*this, max_tokens, batch, kv_fp16));
+    st->gdn_chunked_ = gdn_chunked;
+    return st;
 }
 
 Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batch, bool kv_fp16)
@@ -593,7 +595,7 @@ void Qwen35Model::enqueue_chunk(State& st, int64_t seq, int64_t pos0, int64_t T,
             a.Dk = int(c.Dk);
             a.Dv = int(c.Dv);
             a.W = int(c.W);
-            launch_gdn_prefill(a, st.cgdn_work_.get(), s);
+            launch_gdn_prefill(a, st.cgdn_work_.get(), s, st.gdn_chunked_);
             k_mix = c.v_width();
         } else {
             AttnDecodeArgs a{};

@@ -83,6 +83,10 @@ int hero_batch_state_create(const hero_model* model, int64_t max_tokens, int32_t
  * north-star cache format; the reference's cache is fp32). Results then equal
  * the reference over fp16-rounded keys and values to a few ulp. */
 #define HERO_STATE_KV_FP16 1u
+/* flags: run the delta-net prefill in its chunked form (chunks of 64 tokens,
+ * matrix products instead of the token-serial chain; equal to the reference
+ * to fp32 rounding order instead of bit for bit). */
+#define HERO_STATE_GDN_CHUNKED 2u
 int64_t hero_state_batch(const hero_state* state);
 int64_t hero_state_seq_tokens(const hero_state* state, int32_t seq);
 /* hero_model_forward for sequence `seq` of a batch state. */

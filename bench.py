@@ -115,6 +115,16 @@ def main() -> int:
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t
     log(f"prefill {args.prompt} tokens: {prefill_s:.2f} s ({args.prompt / prefill_s:.1f} tok/s)")
+    # the same prefill with the chunked delta-net form (a throughput option,
+    # tolerance-equal instead of bit-equal to the reference)
+    st_c = model.new_state(ctx, gdn_chunked=True)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    model.forward(st_c, ids=prompt, want_logits=False)
+    torch.cuda.synchronize()
+    prefill_chunked_s = time.perf_counter() - t
+    st_c.close()
+    log(f"prefill {args.prompt} tokens, chunked delta-net: {prefill_chunked_s:.2f} s ({args.prompt / prefill_chunked_s:.1f} tok/s)")
 
     warm_ids = model.decode_greedy(state, first, args.warmup)[0] if args.warmup > 0 else np.array([first], np.int32)
     torch.cuda.synchronize()
@@ -175,6 +185,7 @@ def main() -> int:
             "prefill_seconds": prefill_s, "device_decode_seconds": device_s,
             "gemv_gbs_per_step": nbytes / (device_s / args.steps) / 1e9,
             "prefill_tok_s": args.prompt / prefill_s,
+            "prefill_tok_s_chunked_delta_net": args.prompt / prefill_chunked_s,
             "batch_decode": batch,
         },
         "roofline": {

@@ -47,6 +47,18 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def measured_traffic():
+    """HBM bytes per GEMV launch of a decode step, from the committed summary of
+    two rocprofv3 counter runs (FETCH_SIZE, WRITE_SIZE) of `bench.py
+    --profile-gemvs`, calibrated with the weight-packing kernel
+    (hero_amd/traffic.py)"""
+    path = os.path.join(ROOT, "profiles", "hybrid8b_gemv_traffic.json")
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        return float(json.load(f)["bytes_per_launch"]), "profiles/hybrid8b_gemv_traffic.json"
+
+
 def cpu_baseline(image, prompt, seconds: float) -> dict:
     import oracle
 
@@ -86,6 +98,9 @@ def main() -> int:
     ap.add_argument("--gemv-reps", type=int, default=5)
     ap.add_argument("--batch", type=int, default=16, help="also time greedy decode of this many sequences at once (0: skip)")
     ap.add_argument("--batch-steps", type=int, default=64)
+    ap.add_argument("--profile-gemvs", action="store_true",
+                    help="only launch a decode step's GEMVs --gemv-reps times (+1 warm-up) and print their timing: "
+                         "the program the HBM-traffic counter runs profile")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -106,6 +121,12 @@ def main() -> int:
     model = hero_amd.Qwen35Model.open_image(image)
     log(f"loaded and packed: {model.dims.device_bytes / 1e9:.2f} GB of weights on the device in {time.perf_counter() - t:.1f} s")
     state = model.new_state(ctx)
+    if args.profile_gemvs:
+        sec, launches, nbytes = model.time_gemvs(state, args.gemv_reps)
+        print(json.dumps({"gemv_launches_per_step": launches, "gemv_bytes_per_step": nbytes,
+                          "avg_launch_us": sec / (args.gemv_reps * launches) * 1e6}), flush=True)
+        model.close()
+        return 0
     rng = np.random.default_rng(SEED)
     prompt = rng.integers(0, shape.vocab, args.prompt).astype(np.int32)
 
@@ -165,6 +186,7 @@ def main() -> int:
             f"{bwall * 1e3 / args.batch_steps:.2f} ms/step, {batch['tok_s']:.0f} tok/s aggregate")
         bs.close()
 
+    traffic, traffic_source = measured_traffic()
     out = {
         "metric": "decode tok/s @bs1, Q8_0 ~8B hybrid; Q8 GEMV GB/s as % of HBM peak",
         "value": args.steps / wall,
@@ -190,8 +212,9 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None, "kernel": "gemv_q8_stream_kernel (every Q8_0 GEMV of a decode step, as the step launches it: RMSNorm / SwiGLU fused forms included)",
+            "traffic": traffic, "kernel": "gemv_q8_stream_kernel (every Q8_0 GEMV of a decode step, as the step launches it: RMSNorm / SwiGLU fused forms included)",
             "bytes_per_launch": nbytes / launches, "avg_launch_us": avg_launch * 1e6,
+            "traffic_source": traffic_source,
         },
     }
     if not args.no_cpu:

@@ -15,10 +15,13 @@ namespace hero {
 // activation of silu(gate) * up ([N/2] int8 + [N/64] fp32 scales)
 enum : int { kEpiStore = 0, kEpiResidual = 1, kEpiSwigluQuant = 2 };
 
-// packed Q8_0 weight: [N][K] int8, then the fp16 scales block-major,
-// [K/32][Npad] with Npad = N rounded up to 8 (rows past N unused), so the scales of
-// 8 consecutive rows of one block are one 16-byte load
+// packed Q8_0 weight: [N][K] int8, then the fp16 scales by 8-row group,
+// [Npad/8][K/32][8] with Npad = N rounded up to 8 (rows past N unused): the
+// scales of 8 consecutive rows of one block are one 16-byte load, and those of
+// one 8-row group for every block are contiguous (one sweep per sub-batch)
 inline int64_t packed_rows_pad(int64_t N) { return (N + 7) / 8 * 8; }
+// index of the scale of (row, block) among the fp16 scales; nb = K/32
+__host__ __device__ inline int64_t scale_index(int64_t row, int64_t block, int64_t nb) { return ((row >> 3) * nb + block) * 8 + (row & 7); }
 inline int64_t packed_q8_bytes(int64_t N, int64_t K) { return N * K + packed_rows_pad(N) * (K / 32) * 2; }
 inline int64_t act_q8_bytes(int64_t M, int64_t K) { return M * K + M * (K / 32) * 4; }
 

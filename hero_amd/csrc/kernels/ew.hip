@@ -36,7 +36,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const int8_t* __restrict__ q
     const int64_t t = blockIdx.y;
     const int64_t id = ids[t];
     for (int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; c < D; c += int64_t(gridDim.x) * blockDim.x) {
-        const float scale = half_bits_to_f32(d[(c >> 5) * Vpad + id]);  // block-major scales
+        const float scale = half_bits_to_f32(d[scale_index(id, c >> 5, D >> 5)]);
         out[t * D + c] = scale * float(qs[id * D + c]);
     }
 }

@@ -3,7 +3,7 @@
 // order.
 //
 // Device layouts:
-//   packed weight  [ qs: N*K int8, row-major ][ d: (K/32) x Npad fp16, block-major ]
+//   packed weight  [ qs: N*K int8, row-major ][ d: (Npad/8) x (K/32) x 8 fp16 ]
 //                  Npad = N rounded up to 8 (zero rows): the scales of 8
 //                  consecutive rows of one block are one 16-byte load.
 //   quantized act  [ qs: M*K int8 ][ d: M*(K/32) fp32 ]      d = fp16-decoded scale
@@ -58,7 +58,7 @@ __global__ __launch_bounds__(256) void pack_q8_kernel(const uint8_t* __restrict_
     const uint8_t* b = src + blk * 34;
     const int64_t r = blk / row_blocks, col = blk - r * row_blocks;
     const int64_t row = row0 + (il > 0 ? (r / il) * 2 * il + r % il : r);
-    d[col * Npad + row] = uint16_t(b[0] | (b[1] << 8));
+    d[scale_index(row, col, row_blocks)] = uint16_t(b[0] | (b[1] << 8));
     int w[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) w[j] = int(b[2 + 4 * j]) | (int(b[3 + 4 * j]) << 8) | (int(b[4 + 4 * j]) << 16) | (int(b[5 + 4 * j]) << 24);
@@ -116,8 +116,8 @@ __global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __res
             for (int m = 0; m < CPL; ++m)
                 dst[r][m] = rb + r < r_end ? reinterpret_cast<const int4*>(wq + int64_t(rb + r) * K)[tid + 256 * m] : make_int4(0, 0, 0, 0);
 #pragma unroll
-        for (int m = 0; m < CPL; ++m)  // rb is a multiple of 8 and rb + 8 <= Npad
-            sdst[m] = even ? *reinterpret_cast<const int4*>(wd + int64_t((tid + 256 * m) >> 1) * Npad + rb) : make_int4(0, 0, 0, 0);
+        for (int m = 0; m < CPL; ++m)  // rb is a multiple of 8 and rb + 8 <= Npad: the group's 8 scales of block (tid + 256m) / 2
+            sdst[m] = even ? *reinterpret_cast<const int4*>(wd + scale_index(rb, (tid + 256 * m) >> 1, nb)) : make_int4(0, 0, 0, 0);
     };
     // The lane's x chunks (tid + 256m) as Q8_0. Their global reads are issued
     // before the weight ring's: loads retire in order, so a read issued after
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(256) void gemv_q8_kernel(const int8_t* __restrict__
             const int r = it / cpr, c = it - r * cpr;
             const int64_t row = row0 + r;
             w[k] = reinterpret_cast<const int4*>(wq + row * K)[c];
-            dw[k] = (c & 1) == 0 ? half_bits_to_f32(wd[int64_t(c >> 1) * Npad + row]) : 0.f;
+            dw[k] = (c & 1) == 0 ? half_bits_to_f32(wd[scale_index(row, c >> 1, K >> 5)]) : 0.f;
         }
     }
     for (int i = tid; i < cpr; i += 256) xs[i] = reinterpret_cast<const int4*>(xq)[i];
@@ -528,7 +528,7 @@ __global__ __launch_bounds__(256) void gemm_q8_kernel(const int8_t* __restrict__
         }
         for (int e = tid; e < kGemmKC * kGemmBN; e += 256) {
             const int bb = e / kGemmBN, c = e % kGemmBN;
-            dws[bb][c] = (n0 + c < N && bb < kc) ? half_bits_to_f32(wd[int64_t(b0 + bb) * Npad + n0 + c]) : 0.f;
+            dws[bb][c] = (n0 + c < N && bb < kc) ? half_bits_to_f32(wd[scale_index(n0 + c, b0 + bb, nb)]) : 0.f;
         }
         __syncthreads();
         const int n_l = 16 * w + (lane & 15);
@@ -648,11 +648,11 @@ __global__ __launch_bounds__(256) void gemm_q8_skinny_kernel(const int8_t* __res
             L.x[i] = __builtin_amdgcn_raw_buffer_load_b128(bx, xrow ? uint32_t(c) * uint32_t(K) + off : kOOB, 0, 0);
         }
         // the wave's 8 x 16 scales in one dword per lane: lane 8j + c' holds
-        // rows 2c', 2c'+1 of block b0 + j (block-major: 16 rows of a block are
-        // contiguous); compute() fetches its own with ds_bpermute
+        // rows 2c', 2c'+1 of block b0 + j (adjacent in their 8-row group);
+        // compute() fetches its own with ds_bpermute
         const int j = lane >> 3, c2 = 2 * (lane & 7);
         const bool drow = on && g * 16 + c2 < N;
-        L.d = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(bd, drow ? (uint32_t(b0 + j) * uint32_t(Npad) + uint32_t(g * 16 + c2)) * 2u : kOOB, 0, 0));
+        L.d = uint32_t(__builtin_amdgcn_raw_buffer_load_b32(bd, drow ? uint32_t(scale_index(g * 16 + c2, b0 + j, nb)) * 2u : kOOB, 0, 0));
     };
 
     // a ring of kSkRing steps in flight; slot k is refilled with step s + kSkRing

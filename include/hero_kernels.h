@@ -11,8 +11,9 @@
  * Layouts
  *   Q8_0 GGUF blocks   [N][K/32] x 34 bytes {fp16 d; int8 q[32]}, row-major by
  *                      output row (the GGUF / ggml tensor layout).
- *   packed weight      [N*K int8 q, row-major][(K/32) x Npad fp16 d, block-major]
- *                      Npad = N rounded up to 8 (rows past N unused);
+ *   packed weight      [N*K int8 q, row-major][(Npad/8) x (K/32) x 8 fp16 d]
+ *                      Npad = N rounded up to 8 (rows past N unused); the scale
+ *                      of (row n, block b) at ((n/8)*(K/32) + b)*8 + n%8;
  *                      hero_q8_0_packed_bytes()
  *   quantized act      [M*K int8 q][M*(K/32) fp32 d]        hero_q8_0_act_bytes()
  *                      (d is the fp16-rounded scale, decoded exactly)

@@ -35,6 +35,36 @@ __device__ __forceinline__ float half_bits_to_f32(uint16_t h) {
     return float(v);
 }
 
+// Raw buffer accesses: a load at an offset at or past the buffer's size reads
+// 0 and a store there is dropped, so a kernel can give invalid rows or padded
+// steps an out-of-range offset instead of a branch. Every loop iteration then
+// issues the same memory instructions, which lets the compiler wait for
+// exactly the oldest loads instead of all of them.
+constexpr uint32_t kOOB = 0x80000000u;       // beyond every buffer (sizes < 2 GiB)
+constexpr uint32_t kBufWord3 = 0x00020000u;  // raw dword buffer, gfx9 family
+
+typedef int v4b_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, int(bytes), int(kBufWord3));
+}
+__device__ __forceinline__ int4 load_b128(__amdgpu_buffer_rsrc_t b, uint32_t off) {
+    const v4b_t v = __builtin_amdgcn_raw_buffer_load_b128(b, off, 0, 0);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float load_f32(__amdgpu_buffer_rsrc_t b, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(b, off, 0, 0));
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and
+// lgkmcnt left at their maxima, i.e. not waited for): at most N vector memory
+// operations of this wave still outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 // 4-way int8 dot product into an int32 accumulator (v_dot4_i32_i8), exact.
 __device__ __forceinline__ int dot4_i8(int a, int b, int acc) { return __builtin_amdgcn_sdot4(a, b, acc, false); }
 

@@ -31,15 +31,23 @@
 //    partial sums stay far closer than m to the speculated ones except in
 //    contrived inputs, so that fallback is rare.
 //
-// Lane t holds elements PT*t .. PT*t+PT-1 (PT = 4096 / lanes). The cross-lane
-// steps are wave shuffles plus exchanges of per-wave totals through shared
-// memory; the host emulation at the end runs the same per-lane functions in
-// the same order.
+// Lane t holds elements PT*t .. PT*t+PT-1 (PT = 4096 / lanes). Every
+// cross-lane step inside a wave is a DPP scan (no shared memory); the
+// workgroup needs two barriers: one for the wave totals of the speculation,
+// one for the serial-element tables, which each wave writes into its own
+// region with wave-local increment prefixes. Every wave then runs the walk
+// itself (so the result needs no broadcast): its lanes prepare one step each,
+// the dependent chain s -> s + a -> s + val runs over the steps with the
+// step data read lane by lane, each lane keeps the chain values of its own
+// step, and the binade checks of all steps run in parallel afterwards. The
+// host emulation at the end runs the same per-lane functions and the same
+// operations in the same order.
 #pragma once
 #include <hip/hip_runtime.h>
 
 #include <cmath>
 #include <cstdint>
+#include <type_traits>
 
 #include "hero/fp16.hpp"
 
@@ -53,7 +61,7 @@ constexpr int kThreads = 1024;  // the default workgroup
 constexpr int kWaveSize = 64;
 constexpr int kMaxWaves = 16;
 constexpr int kMaxN = 4096;
-constexpr int kMaxSerial = 512;
+constexpr int kMaxSerial = 512;  // table entries, split evenly over the waves
 constexpr int kWaves = kThreads / kWaveSize;  // of the default workgroup
 constexpr float kMarginLo = 1.0f - 1.0f / 16384.0f;
 constexpr float kMarginHi = 1.0f + 1.0f / 16384.0f;
@@ -66,16 +74,15 @@ __host__ __device__ inline int binade_f32(float s) {
 }
 
 struct Shared {
-    float wsum[kMaxWaves];                 // wave totals of the speculation scan
-    uint32_t wc[kMaxWaves], wn[kMaxWaves]; // wave totals of the increment and serial-count scans
-    int32_t ser_idx[kMaxSerial];     // index of serial element r
-    float ser_val[kMaxSerial];       // its term
-    uint32_t ser_cx[kMaxSerial];     // increments of all non-serial elements before it (mod 2^32)
-    int32_t ser_e[kMaxSerial];       // binade of the run that follows it
-    uint32_t c_total;
-    int32_t nser;
-    int32_t fell_back;  // 1 if the walk ran the plain loop
-    float result;
+    float wsum[kMaxWaves];                  // wave totals of the speculation scan
+    uint32_t wc[kMaxWaves], wn[kMaxWaves];  // wave totals of the increments and of the serial counts
+    // serial-element tables, region w (kMaxSerial / waves entries) for wave w
+    int32_t ser_idx[kMaxSerial];  // index of the element
+    float ser_val[kMaxSerial];    // its term
+    uint32_t ser_cx[kMaxSerial];  // increments of the wave's non-serial elements before it (mod 2^32)
+    int32_t ser_e[kMaxSerial];    // binade of the run that follows it
+    int32_t fell_back;            // 1 if the last sum ran the plain loop (written by wave 0)
+    float result;                 // for callers that broadcast a value of their own
 };
 
 template <int PT>  // elements per lane
@@ -145,29 +152,26 @@ __host__ __device__ inline void lane_classify(Lane<PT>& L, int i0, int n, float 
     L.cnt = cnt;
 }
 
-// cx, r: increments and serial elements before the lane's first element.
-// Writes the table entries of the lane's serial elements, and the totals if
-// the lane holds element n-1.
+// Writes the table entries of the lane's serial elements into its wave's
+// region: r = serial elements of the wave before the lane, cx = increments of
+// the wave's non-serial elements before the lane; entries past the region's
+// capacity are dropped (the walk then runs the plain loop).
 template <int PT>
-__host__ __device__ inline void lane_emit(const Lane<PT>& L, int i0, int n, uint32_t cx, uint32_t r, Shared& sm) {
-    constexpr int kPerThread = PT;
+__host__ __device__ inline void lane_emit(const Lane<PT>& L, int i0, uint32_t cx, uint32_t r, int region, int cap, Shared& sm) {
     // straight-line: c[k] is 0 for serial and out-of-range elements, and
     // serial bits are only set in range
 #pragma unroll
-    for (int k = 0; k < kPerThread; ++k) {
+    for (int k = 0; k < PT; ++k) {
         const bool ser = (L.serial >> k) & 1u;
-        if (ser && r < uint32_t(kMaxSerial)) {
-            sm.ser_idx[r] = i0 + k;
-            sm.ser_val[r] = L.v[k];
-            sm.ser_cx[r] = cx;
-            sm.ser_e[r] = L.e_after[k];
+        if (ser && r < uint32_t(cap)) {
+            const int slot = region * cap + int(r);
+            sm.ser_idx[slot] = i0 + k;
+            sm.ser_val[slot] = L.v[k];
+            sm.ser_cx[slot] = cx;
+            sm.ser_e[slot] = L.e_after[k];
         }
         r += ser ? 1u : 0u;
         cx += L.c[k];
-    }
-    if (i0 < n && n <= i0 + kPerThread) {
-        sm.nser = int32_t(r);
-        sm.c_total = cx;
     }
 }
 
@@ -175,6 +179,44 @@ __host__ __device__ inline float serial_loop(const float* p, int n) {
     float s = 0.f;
     for (int i = 0; i < n; ++i) s += p[i];
     return s;
+}
+
+// The walk's view of the tables: wave totals and their exclusive prefixes.
+template <int W>
+struct Tables {
+    uint32_t nbase[W], cbase[W], wn[W];  // serial entries / increments of the waves before w; entries of w
+    uint32_t nser, c_total;
+    bool overflow;  // a wave had more serial elements than its region holds
+};
+
+template <int W>
+__host__ __device__ inline void read_tables(const Shared& sm, int cap, Tables<W>& T) {
+    uint32_t nb = 0, cb = 0;
+    bool of = false;
+#pragma unroll
+    for (int u = 0; u < W; ++u) {
+        const uint32_t n = sm.wn[u];
+        T.nbase[u] = nb, T.cbase[u] = cb, T.wn[u] = n;
+        of = of || n > uint32_t(cap);
+        nb += n, cb += sm.wc[u];
+    }
+    T.nser = nb, T.c_total = cb, T.overflow = of;
+}
+
+// slot of serial entry q < nser in the tables, and the increments of every
+// non-serial element before it (mod 2^32)
+template <int W>
+__host__ __device__ inline void locate(const Tables<W>& T, const Shared& sm, int cap, uint32_t q, int& slot, uint32_t& cx) {
+    int sl = 0;
+    uint32_t cb = 0;
+#pragma unroll
+    for (int u = 0; u < W; ++u) {
+        const bool here = q >= T.nbase[u] && q < T.nbase[u] + T.wn[u];
+        sl = here ? u * cap + int(q - T.nbase[u]) : sl;
+        cb = here ? T.cbase[u] : cb;
+    }
+    slot = sl;
+    cx = cb + sm.ser_cx[sl];
 }
 
 // step r of the walk: the run before serial element r (for r == nser, the
@@ -186,191 +228,223 @@ struct Step {
     int32_t flags;  // bit 0: the run is non-empty, bit 1: its C is too large
 };
 
-__host__ __device__ inline Step walk_entry(const Shared& sm, int r, int n) {
-    const int nser = sm.nser;
-    const int idx = r < nser ? sm.ser_idx[r] : n;
-    const int idx_prev = r > 0 ? sm.ser_idx[r - 1] : -1;
-    const uint32_t cx = r < nser ? sm.ser_cx[r] : sm.c_total;
-    const uint32_t cx_prev = r > 0 ? sm.ser_cx[r - 1] : 0u;
+template <int W>
+__host__ __device__ inline Step walk_entry(const Tables<W>& T, const Shared& sm, int cap, uint32_t r, int n) {
+    int slot = 0, slot_prev = 0;
+    uint32_t cx = T.c_total, cx_prev = 0;
+    if (r < T.nser) locate(T, sm, cap, r, slot, cx);
+    if (r > 0) locate(T, sm, cap, r - 1, slot_prev, cx_prev);
+    const int idx = r < T.nser ? sm.ser_idx[slot] : n;
+    const int idx_prev = r > 0 ? sm.ser_idx[slot_prev] : -1;
     Step st;
-    st.e = r > 0 ? sm.ser_e[r - 1] : -126;
+    st.e = r > 0 ? sm.ser_e[slot_prev] : -126;
     const uint32_t C = cx - cx_prev;
     const bool nonempty = idx > idx_prev + 1;
     const bool big = C >= (1u << 24);
     st.a = nonempty && !big ? ldexpf(float(C), st.e - 23) : 0.f;
-    st.val = r < nser ? sm.ser_val[r] : 0.f;
+    st.val = r < T.nser ? sm.ser_val[slot] : 0.f;
     st.flags = (nonempty ? 1 : 0) | (big ? 2 : 0);
     return st;
 }
 
-// the dependent chain is s -> s + a -> s + val (a = 0 for an empty run, val =
-// 0 after the final run: adding +0 to s >= 0 leaves it unchanged); the checks
-// only read it
-__host__ __device__ inline void walk_apply(float& s, bool& ok, float a, float val, int32_t e, int32_t flags) {
-    const float s0 = s;
-    const float s1 = s0 + a;
-    const bool good = !(flags & 2) && s0 >= 0.f && binade_f32(s0) == e && binade_f32(s1) == e;
-    ok = ok && (!(flags & 1) || good);
-    s = s1 + val;
+// the checks of one step, given the chain value before it (s0) and after its
+// run (s1 = s0 + a): a non-empty run must keep s in the binade it was
+// classified in
+__host__ __device__ inline bool step_ok(const Step& st, float s0, float s1) {
+    const bool good = !(st.flags & 2) && s0 >= 0.f && binade_f32(s0) == st.e && binade_f32(s1) == st.e;
+    return !(st.flags & 1) || good;
 }
 
-// ---- the whole sum on the device: NT lanes (the whole workgroup), p in shared
-// memory (16-byte aligned), 0 <= n <= 4096 ---------------------------------------------
-template <int NT = kThreads>
-__device__ inline float sum_nonneg(const float* p, int n, Shared& sm) {
+// ---- wave-level scans (DPP) --------------------------------------------------------------
+// Inclusive scan over the 64 lanes, in this order: inside each row of 16
+// lanes, Hillis-Steele steps of 1, 2, 4 and 8 lanes (a lane without a source
+// adds +0); then rows 1 and 3 add the last lane of the row before
+// (row_bcast:15), then rows 2 and 3 add lane 31 (row_bcast:31); rows without
+// a source add +0 in both steps.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ inline int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xF, true);
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ inline float dpp_f(float v) {
+    return bits_f32(uint32_t(dpp_i<CTRL, ROW_MASK>(int(f32_bits(v)))));
+}
+__device__ inline float scan_f32(float v) {
+    v += dpp_f<0x111>(v);  // row_shr:1
+    v += dpp_f<0x112>(v);  // row_shr:2
+    v += dpp_f<0x114>(v);  // row_shr:4
+    v += dpp_f<0x118>(v);  // row_shr:8
+    v += dpp_f<0x142, 0xA>(v);  // row_bcast:15
+    v += dpp_f<0x143, 0xC>(v);  // row_bcast:31
+    return v;
+}
+__device__ inline uint32_t scan_u32(uint32_t v) {
+    v += uint32_t(dpp_i<0x111>(int(v)));
+    v += uint32_t(dpp_i<0x112>(int(v)));
+    v += uint32_t(dpp_i<0x114>(int(v)));
+    v += uint32_t(dpp_i<0x118>(int(v)));
+    v += uint32_t(dpp_i<0x142, 0xA>(int(v)));
+    v += uint32_t(dpp_i<0x143, 0xC>(int(v)));
+    return v;
+}
+
+// ---- the whole sum on the device: NT lanes (the whole workgroup) -----------------------
+// L holds the lane's PT terms (elements PT*tid ..); p holds all n terms in
+// shared memory, read only by the plain-loop fallback (it runs after two
+// barriers, so p may be written right before the call). Every wave returns
+// the result; there is no barrier at the end unless the fallback ran.
+template <int NT>
+__device__ inline float sum_lanes(Lane<kMaxN / NT>& L, const float* p, int n, Shared& sm) {
     static_assert(NT == 256 || NT == 1024, "256 or 1024 lanes");
-    constexpr int kPerThread = kMaxN / NT, kWaves = NT / kWaveSize;
+    constexpr int PT = kMaxN / NT, W = NT / kWaveSize, cap = kMaxSerial / W;
     if (n <= 0) return 0.f;
     const int tid = int(threadIdx.x), lane = tid & (kWaveSize - 1), w = tid / kWaveSize;
-    const int i0 = tid * kPerThread;
-    Lane<kPerThread> L;
-    lane_load(p, n, i0, L);
+    const int i0 = tid * PT;
 
-    // speculation: inclusive scan of lane sums inside the wave, then of the
-    // wave totals (every wave scans all of them in its lanes 0..15)
-    float d = lane_sum(L);
-#pragma unroll
-    for (int off = 1; off < kWaveSize; off <<= 1) {
-        const float y = __shfl_up(d, off, kWaveSize);
-        if (lane >= off) d += y;
-    }
-    if (lane == kWaveSize - 1) sm.wsum[w] = d;
+    // speculation: the lane sums, scanned in the wave, then the totals of the
+    // waves before (left to right)
+    const float incl = scan_f32(lane_sum(L));
+    if (lane == kWaveSize - 1) sm.wsum[w] = incl;
+    const float excl = dpp_f<0x138>(incl);  // wave_shr:1, lane 0 reads +0
     __syncthreads();
-    float ws = lane < kWaves ? sm.wsum[lane] : 0.f;
-#pragma unroll
-    for (int off = 1; off < kWaves; off <<= 1) {
-        const float y = __shfl_up(ws, off, kWaveSize);
-        if (lane >= off) ws += y;
-    }
-    float P = __shfl(ws, w > 0 ? w - 1 : 0, kWaveSize);
-    if (w == 0) P = 0.f;
-    const float P_next = __shfl(ws, w, kWaveSize);  // the next wave's P
-    float excl = __shfl_up(d, 1, kWaveSize);
-    if (lane == 0) excl = 0.f;
+    float P = 0.f;
+    for (int u = 0; u < w; ++u) P = P + sm.wsum[u];
     const float pre = P + excl;
-    float next = __shfl_down(pre, 1, kWaveSize);
-    if (lane == kWaveSize - 1) next = P_next + 0.f;  // what the next wave's lane 0 computes
+    const float P_next = P + sm.wsum[w];
+    float next = dpp_f<0x130>(pre);  // wave_shl:1: the next lane's pre
+    if (lane == kWaveSize - 1) next = P_next + 0.f;                           // what the next wave's lane 0 computes
 
     lane_classify(L, i0, n, pre, next);
 
-    // prefix sums of the increments (mod 2^32) and of the serial counts
-    uint32_t c = L.csum, m = L.cnt;
-#pragma unroll
-    for (int off = 1; off < kWaveSize; off <<= 1) {
-        const uint32_t yc = __shfl_up(c, off, kWaveSize), ym = __shfl_up(m, off, kWaveSize);
-        if (lane >= off) c += yc, m += ym;
-    }
+    // wave-local prefixes of the increments (mod 2^32) and serial counts
+    const uint32_t c = scan_u32(L.csum), m = scan_u32(L.cnt);
     if (lane == kWaveSize - 1) {
         sm.wc[w] = c;
         sm.wn[w] = m;
     }
-    __syncthreads();
-    uint32_t bc = 0, bm = 0;
-    for (int u = 0; u < w; ++u) bc += sm.wc[u], bm += sm.wn[u];
-    lane_emit(L, i0, n, bc + c - L.csum, bm + m - L.cnt, sm);
+    lane_emit(L, i0, c - L.csum, m - L.cnt, w, cap, sm);
     __syncthreads();
 
-    // the walk: wave 0; lane l prepares step base+l, then the steps run in
-    // order, reading each lane's values with readlane
-    if (w == 0) {
-        const int nser = sm.nser;
-        bool ok = nser <= kMaxSerial;
-        float s = 0.f;
-        for (int base = 0; ok && base <= nser; base += kWaveSize) {
-            const int r = base + lane;
-            Step st{0.f, 0.f, 0, 0};
-            if (r <= nser) st = walk_entry(sm, r, n);
-            const int cnt = min(kWaveSize, nser + 1 - base);
-            const int ia = int(f32_bits(st.a)), iv = int(f32_bits(st.val));
-            int l = 0;
-            for (; l + 8 <= cnt; l += 8) {  // the step data of 8 steps first, then the chain
-                float a[8], v[8];
-                int32_t e[8], f[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    a[u] = bits_f32(uint32_t(__builtin_amdgcn_readlane(ia, l + u)));
-                    v[u] = bits_f32(uint32_t(__builtin_amdgcn_readlane(iv, l + u)));
-                    e[u] = __builtin_amdgcn_readlane(st.e, l + u);
-                    f[u] = __builtin_amdgcn_readlane(st.flags, l + u);
-                }
-#pragma unroll
-                for (int u = 0; u < 8; ++u) walk_apply(s, ok, a[u], v[u], e[u], f[u]);
-            }
-            for (; l < cnt; ++l)
-                walk_apply(s, ok, bits_f32(uint32_t(__builtin_amdgcn_readlane(ia, l))), bits_f32(uint32_t(__builtin_amdgcn_readlane(iv, l))),
-                           __builtin_amdgcn_readlane(st.e, l), __builtin_amdgcn_readlane(st.flags, l));
+    // the walk, in every wave: lane l prepares step base + l
+    Tables<W> T;
+    read_tables(sm, cap, T);
+    bool ok = !T.overflow;
+    float s = 0.f;
+    for (uint32_t base = 0; ok && base <= T.nser; base += kWaveSize) {
+        const uint32_t r = base + uint32_t(lane);
+        Step st{0.f, 0.f, 0, 0};
+        if (r <= T.nser) st = walk_entry(T, sm, cap, r, n);
+        const int cnt = int(min(uint32_t(kWaveSize), T.nser + 1 - base));
+        const int ia = int(f32_bits(st.a)), iv = int(f32_bits(st.val));
+        float my0 = 0.f, my1 = 0.f;  // the chain before this lane's step and after its run
+        for (int l = 0; l < cnt; ++l) {
+            const float a = bits_f32(uint32_t(__builtin_amdgcn_readlane(ia, l)));
+            const float v = bits_f32(uint32_t(__builtin_amdgcn_readlane(iv, l)));
+            const float s1 = s + a;
+            my0 = lane == l ? s : my0;
+            my1 = lane == l ? s1 : my1;
+            s = s1 + v;
         }
-        if (!ok) s = serial_loop(p, n);
-        if (lane == 0) {
-            sm.result = s;
-            sm.fell_back = ok ? 0 : 1;
-        }
+        const bool bad = lane < cnt && !step_ok(st, my0, my1);
+        ok = ok && !__any(bad);
     }
-    __syncthreads();
-    return sm.result;
+    if (!ok) {  // the same decision in every wave
+        s = serial_loop(p, n);
+        __syncthreads();
+    }
+    if (tid == 0) sm.fell_back = ok ? 0 : 1;
+    return s;
+}
+
+// p: n terms in shared memory (16-byte aligned), 0 <= n <= 4096; written
+// before a barrier
+template <int NT = kThreads>
+__device__ inline float sum_nonneg(const float* p, int n, Shared& sm) {
+    Lane<kMaxN / NT> L;
+    lane_load(p, n, int(threadIdx.x) * (kMaxN / NT), L);
+    return sum_lanes<NT>(L, p, n, sm);
+}
+
+// v: the lane's terms (elements PT*tid ..), n = 4096 or fewer with the terms
+// past n zero; they are also stored into p (shared memory, 4096 floats) for
+// the fallback
+template <int NT>
+__device__ inline float sum_nonneg_regs(const float (&v)[kMaxN / NT], float* p, int n, Shared& sm) {
+    constexpr int PT = kMaxN / NT;
+    Lane<PT> L;
+#pragma unroll
+    for (int k = 0; k < PT; ++k) L.v[k] = v[k];
+#pragma unroll
+    for (int k = 0; k < PT; k += 4) reinterpret_cast<float4*>(p)[(int(threadIdx.x) * PT + k) / 4] = make_float4(v[k], v[k + 1], v[k + 2], v[k + 3]);
+    return sum_lanes<NT>(L, p, n, sm);
 }
 
 // ---- the same steps on the host, lane after lane, in the device's order -------------
 template <int NT = kThreads>
 inline float sum_nonneg_host(const float* p, int n, Shared& sm) {
-    constexpr int kThreads = NT, kPerThread = kMaxN / NT, kWaves = NT / kWaveSize;
+    constexpr int PT = kMaxN / NT, W = NT / kWaveSize, cap = kMaxSerial / W;
     if (n <= 0) return 0.f;
-    static Lane<kPerThread> L[kThreads];
-    static float d[kThreads], pre[kThreads], next[kThreads];
-    static uint32_t c[kThreads], m[kThreads];
-    for (int t = 0; t < kThreads; ++t) {
-        lane_load(p, n, t * kPerThread, L[t]);
-        d[t] = lane_sum(L[t]);
+    static Lane<PT> L[NT];
+    static float incl[NT], pre[NT], next[NT];
+    static uint32_t c[NT], m[NT];
+    for (int t = 0; t < NT; ++t) {
+        lane_load(p, n, t * PT, L[t]);
+        incl[t] = lane_sum(L[t]);
     }
-    for (int w = 0; w < kWaves; ++w) {
-        float* x = d + w * kWaveSize;
-        for (int off = 1; off < kWaveSize; off <<= 1) {
-            float y[kWaveSize];
+    // the device's wave scan, step by step
+    auto scan = [](auto* x) {
+        using T = std::remove_reference_t<decltype(x[0])>;
+        for (int k = 1; k <= 8; k <<= 1) {
+            T y[kWaveSize];
             for (int l = 0; l < kWaveSize; ++l) y[l] = x[l];
-            for (int l = off; l < kWaveSize; ++l) x[l] += y[l - off];
+            for (int l = 0; l < kWaveSize; ++l) x[l] = x[l] + ((l & 15) >= k ? y[l - k] : T(0));
         }
-        sm.wsum[w] = x[kWaveSize - 1];
+        {
+            T y[kWaveSize];
+            for (int l = 0; l < kWaveSize; ++l) y[l] = x[l];
+            for (int l = 0; l < kWaveSize; ++l) x[l] = x[l] + ((l >> 4) == 1 ? y[15] : (l >> 4) == 3 ? y[47] : T(0));
+        }
+        {
+            T y[kWaveSize];
+            for (int l = 0; l < kWaveSize; ++l) y[l] = x[l];
+            for (int l = 0; l < kWaveSize; ++l) x[l] = x[l] + ((l >> 4) >= 2 ? y[31] : T(0));
+        }
+    };
+    for (int w = 0; w < W; ++w) {
+        scan(incl + w * kWaveSize);
+        sm.wsum[w] = incl[w * kWaveSize + kWaveSize - 1];
     }
-    float ws[kWaves];
-    for (int u = 0; u < kWaves; ++u) ws[u] = sm.wsum[u];
-    for (int off = 1; off < kWaves; off <<= 1) {
-        float y[kWaves];
-        for (int l = 0; l < kWaves; ++l) y[l] = ws[l];
-        for (int l = off; l < kWaves; ++l) ws[l] += y[l - off];
-    }
-    for (int w = 0; w < kWaves; ++w) {
-        const float P = w > 0 ? ws[w - 1] : 0.f;
-        for (int l = 0; l < kWaveSize; ++l) pre[w * kWaveSize + l] = P + (l > 0 ? d[w * kWaveSize + l - 1] : 0.f);
+    for (int w = 0; w < W; ++w) {
+        float P = 0.f;
+        for (int u = 0; u < w; ++u) P = P + sm.wsum[u];
+        const float P_next = P + sm.wsum[w];
+        for (int l = 0; l < kWaveSize; ++l) pre[w * kWaveSize + l] = P + (l > 0 ? incl[w * kWaveSize + l - 1] : 0.f);
         for (int l = 0; l + 1 < kWaveSize; ++l) next[w * kWaveSize + l] = pre[w * kWaveSize + l + 1];
-        next[w * kWaveSize + kWaveSize - 1] = ws[w] + 0.f;
+        next[w * kWaveSize + kWaveSize - 1] = P_next + 0.f;
     }
-    for (int t = 0; t < kThreads; ++t) {
-        lane_classify(L[t], t * kPerThread, n, pre[t], next[t]);
+    for (int t = 0; t < NT; ++t) {
+        lane_classify(L[t], t * PT, n, pre[t], next[t]);
         c[t] = L[t].csum;
         m[t] = L[t].cnt;
     }
-    for (int w = 0; w < kWaves; ++w) {
-        uint32_t* xc = c + w * kWaveSize;
-        uint32_t* xm = m + w * kWaveSize;
-        for (int l = 1; l < kWaveSize; ++l) xc[l] += xc[l - 1], xm[l] += xm[l - 1];
-        sm.wc[w] = xc[kWaveSize - 1];
-        sm.wn[w] = xm[kWaveSize - 1];
+    for (int w = 0; w < W; ++w) {
+        scan(c + w * kWaveSize);
+        scan(m + w * kWaveSize);
+        sm.wc[w] = c[w * kWaveSize + kWaveSize - 1];
+        sm.wn[w] = m[w * kWaveSize + kWaveSize - 1];
     }
-    for (int t = 0; t < kThreads; ++t) {
-        const int w = t / kWaveSize;
-        uint32_t bc = 0, bm = 0;
-        for (int u = 0; u < w; ++u) bc += sm.wc[u], bm += sm.wn[u];
-        lane_emit(L[t], t * kPerThread, n, bc + c[t] - L[t].csum, bm + m[t] - L[t].cnt, sm);
-    }
-    const int nser = sm.nser;
-    bool ok = nser <= kMaxSerial;
+    for (int t = 0; t < NT; ++t) lane_emit(L[t], t * PT, c[t] - L[t].csum, m[t] - L[t].cnt, t / kWaveSize, cap, sm);
+    Tables<W> T;
+    read_tables(sm, cap, T);
+    bool ok = !T.overflow;
     float s = 0.f;
-    for (int r = 0; ok && r <= nser; ++r) {
-        const Step st = walk_entry(sm, r, n);
-        walk_apply(s, ok, st.a, st.val, st.e, st.flags);
+    for (uint32_t r = 0; ok && r <= T.nser; ++r) {
+        const Step st = walk_entry(T, sm, cap, r, n);
+        const float s1 = s + st.a;
+        ok = ok && step_ok(st, s, s1);
+        s = s1 + st.val;
     }
     if (!ok) s = serial_loop(p, n);
-    sm.result = s;
     sm.fell_back = ok ? 0 : 1;
     return s;
 }

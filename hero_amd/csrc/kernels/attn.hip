@@ -151,7 +151,7 @@ __global__ __launch_bounds__(seqsum::kThreads) void attn_softmax_kernel(AttnDeco
         }
         if (tid == 0) chunk[0] = total;
         __syncthreads();
-        total = seqsum::sum_nonneg(chunk, len + 1, sm);  // ends with a barrier
+        total = seqsum::sum_nonneg(chunk, len + 1, sm);  // every wave gets the total
     }
     for (int t = tid; t < n; t += seqsum::kThreads) sc[t] = sc[t] / total;
 }

@@ -89,6 +89,15 @@ void launch_pack_q8(const void* gguf_blocks, void* packed, int64_t N_total, int6
 // (d_w * d_x) and stores the term in shared memory. Every TR rows (and at the
 // end) one barrier, then lane r of wave 0 adds row r's terms in block order
 // (the reference's chain) and stores y.
+//
+// The workgroup reads its rows, their scale groups and (residual epilogue)
+// its slice of the residual through raw buffers sized to exactly that range.
+// Rows past the range, the ring's padding sub-batches and the odd lanes'
+// scale loads use out-of-range offsets that read zeros, so every ring refill
+// is the same unconditional loads and each sub-batch waits only for its own
+// loads, with the later sub-batches still in flight. The residual of the
+// next chain pass is fetched right after the previous pass, long before its
+// store needs it.
 // ---------------------------------------------------------------------------
 constexpr int kStreamRB = 8;  // rows per sub-batch
 
@@ -103,25 +112,35 @@ __global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __res
     const int G = gridDim.x, U = Npad / UR;
     const int r_begin = UR * int((int64_t(U) * blockIdx.x) / G);
     const int r_end = min(N, UR * int((int64_t(U) * (blockIdx.x + 1)) / G));
-    const int nsub = r_end > r_begin ? (r_end - r_begin + kStreamRB - 1) / kStreamRB : 0;
+    const int rows = max(r_end - r_begin, 0);
+    const int nsub = (rows + kStreamRB - 1) / kStreamRB;
     const bool even = (tid & 1) == 0;
+    // the workgroup's rows (rows * K bytes) and their scale groups (nsub groups
+    // of nb blocks x 8 fp16; r_begin is a multiple of 8)
+    const __amdgpu_buffer_rsrc_t bw = buffer_of(wq + int64_t(r_begin) * K, uint32_t(rows) * uint32_t(K));
+    const __amdgpu_buffer_rsrc_t bd = buffer_of(wd + scale_index(r_begin, 0, nb), uint32_t(nsub) * uint32_t(nb) * 16u);
 
     int4 ring[D][kStreamRB][CPL];
     int4 sring[D][CPL];  // even lanes: scales of the sub-batch's 8 rows for each of the lane's blocks
+    // one sub-batch: its scales first, then its rows in order (the order the
+    // compute consumes them); the scheduling fences keep that issue order, on
+    // which the compiler's counted waits depend
     auto load = [&](int j, int4 (&dst)[kStreamRB][CPL], int4 (&sdst)[CPL]) {
-        const int rb = r_begin + j * kStreamRB;
+        const uint32_t row0 = uint32_t(j * kStreamRB);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int m = 0; m < CPL; ++m)  // the group's 8 scales of block (tid + 256m) / 2
+            sdst[m] = load_b128(bd, even ? (uint32_t(j) * uint32_t(nb) + uint32_t((tid + 256 * m) >> 1)) * 16u : kOOB);
 #pragma unroll
         for (int r = 0; r < kStreamRB; ++r)
 #pragma unroll
-            for (int m = 0; m < CPL; ++m)
-                dst[r][m] = rb + r < r_end ? reinterpret_cast<const int4*>(wq + int64_t(rb + r) * K)[tid + 256 * m] : make_int4(0, 0, 0, 0);
-#pragma unroll
-        for (int m = 0; m < CPL; ++m)  // rb is a multiple of 8 and rb + 8 <= Npad: the group's 8 scales of block (tid + 256m) / 2
-            sdst[m] = even ? *reinterpret_cast<const int4*>(wd + scale_index(rb, (tid + 256 * m) >> 1, nb)) : make_int4(0, 0, 0, 0);
+            for (int m = 0; m < CPL; ++m) dst[r][m] = load_b128(bw, (row0 + uint32_t(r)) * uint32_t(K) + uint32_t(tid + 256 * m) * 16u);
+        __builtin_amdgcn_sched_barrier(0);
     };
-    // The lane's x chunks (tid + 256m) as Q8_0. Their global reads are issued
-    // before the weight ring's: loads retire in order, so a read issued after
-    // the ring would wait for every weight in flight.
+    // The lane's x chunks (tid + 256m) as Q8_0, and the residual of the first
+    // chain pass. Their global reads are issued before the weight ring's:
+    // loads retire in order, so a read issued after the ring would wait for
+    // every weight in flight.
     int4 xv[CPL];
     float dx[CPL];
     float xr[16], gr[16];                       // kInRmsNorm: the lane's 16 inputs and weights
@@ -153,20 +172,29 @@ __global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __res
             }
         }
     }
+    // residual epilogue: the workgroup's slice of the residual (empty otherwise)
+    const __amdgpu_buffer_rsrc_t br = buffer_of(EPI == kEpiResidual ? resid + r_begin : y, EPI == kEpiResidual ? uint32_t(rows) * 4u : 0u);
+    float rnext = 0.f;  // residual of the lane's row in the next chain pass
+    if constexpr (EPI == kEpiResidual) rnext = load_f32(br, uint32_t(tid) * 4u);
 #pragma unroll
-    for (int s = 0; s < D; ++s)
-        if (s < nsub) load(s, ring[s], sring[s]);
+    for (int s = 0; s < D; ++s) load(s, ring[s], sring[s]);
+    // the input loads are complete once at most the ring's loads are
+    // outstanding; said explicitly, so the loop below does not inherit them as
+    // pending (which makes the compiler wait for every load at its head)
+    wait_vmcnt<D * (kStreamRB + 1) * CPL>();
 
     if constexpr (XM == kInRmsNorm) {
         // RMSNorm (nm/src/components.hpp:176-181) of the whole row, then the
         // reference's quantize_row_q8_0: the sum of squares is the exact
         // sequential sum (hero/seqsum.hpp), lane t holding elements 16t..16t+15
         __shared__ seqsum::Shared sm;
-        float* sq = terms;
+        float sq[16];
 #pragma unroll
-        for (int k = 0; k < 16; k += 4) reinterpret_cast<float4*>(sq)[(16 * tid + k) / 4] = make_float4(xr[k] * xr[k], xr[k + 1] * xr[k + 1], xr[k + 2] * xr[k + 2], xr[k + 3] * xr[k + 3]);
-        __syncthreads();
-        const float ss = seqsum::sum_nonneg<256>(sq, K, sm);  // ends with a barrier
+        for (int k = 0; k < 16; ++k) sq[k] = xr[k] * xr[k];
+        // terms holds the squares for the sum's plain-loop fallback, which ends
+        // with a barrier; otherwise nothing reads them after the sum's second
+        // barrier, so the main loop may overwrite them at once
+        const float ss = seqsum::sum_nonneg_regs<256>(sq, terms, K, sm);
         const float inv = 1.f / sqrtf(ss / float(K) + in.eps);
         float v[16];
 #pragma unroll
@@ -193,79 +221,79 @@ __global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __res
     }
 
     int chain_row0 = r_begin;  // first row of the pending chain pass
-    for (int base = 0; base < nsub; base += D) {
+    const int nsub_pad = (nsub + D - 1) / D * D;
+    for (int base = 0; base < nsub_pad; base += D) {
 #pragma unroll
         for (int s = 0; s < D; ++s) {
             const int j = base + s;
-            if (j < nsub) {
-                const int rb = r_begin + j * kStreamRB;
+            const int rb = r_begin + j * kStreamRB;
 #pragma unroll
-                for (int r = 0; r < kStreamRB; ++r) {
-                    const uint32_t pair = uint32_t(r < 4 ? (r < 2 ? 0 : 1) : (r < 6 ? 2 : 3));
+            for (int r = 0; r < kStreamRB; ++r) {
+                const uint32_t pair = uint32_t(r < 4 ? (r < 2 ? 0 : 1) : (r < 6 ? 2 : 3));
 #pragma unroll
-                    for (int m = 0; m < CPL; ++m) {
-                        int v = dot16_i8(ring[s][r][m], xv[m], 0);
-                        v += pair_swap_i32(v);  // the block's other 16 bytes (exact)
-                        if (even && rb + r < r_end) {
-                            const int4 sc = sring[s][m];
-                            const uint32_t two = uint32_t(pair == 0 ? sc.x : pair == 1 ? sc.y : pair == 2 ? sc.z : sc.w);
-                            const uint16_t h = uint16_t((r & 1) ? (two >> 16) : (two & 0xFFFFu));
-                            terms[(rb + r - chain_row0) * ts + ((tid + 256 * m) >> 1)] = float(v) * (half_bits_to_f32(h) * dx[m]);
+                for (int m = 0; m < CPL; ++m) {
+                    int v = dot16_i8(ring[s][r][m], xv[m], 0);
+                    v += pair_swap_i32(v);  // the block's other 16 bytes (exact)
+                    if (even && rb + r < r_end) {
+                        const int4 sc = sring[s][m];
+                        const uint32_t two = uint32_t(pair == 0 ? sc.x : pair == 1 ? sc.y : pair == 2 ? sc.z : sc.w);
+                        const uint16_t h = uint16_t((r & 1) ? (two >> 16) : (two & 0xFFFFu));
+                        terms[(rb + r - chain_row0) * ts + ((tid + 256 * m) >> 1)] = float(v) * (half_bits_to_f32(h) * dx[m]);
+                    }
+                }
+            }
+            load(j + D, ring[s], sring[s]);  // zeros past the last sub-batch
+            const int done = rb + kStreamRB - chain_row0;  // rows whose terms are all stored
+            if (j < nsub && (done >= TR || j + 1 == nsub)) {
+                const int prow = min(done, r_end - chain_row0);
+                __syncthreads();
+                if (tid < prow) {
+                    const float4* t = reinterpret_cast<const float4*>(terms + tid * ts);
+                    float acc = 0.f;
+                    float4 q[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) q[u] = t[u];
+                    for (int b4 = 0; b4 < nb / 4; b4 += 4) {
+                        float4 nq[4];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) nq[u] = b4 + 4 + u < nb / 4 ? t[b4 + 4 + u] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            acc += q[u].x;
+                            acc += q[u].y;
+                            acc += q[u].z;
+                            acc += q[u].w;
+                        }
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) q[u] = nq[u];
+                    }
+                    const int64_t o = chain_row0 + tid;
+                    if constexpr (EPI == kEpiResidual)
+                        y[o] = rnext + acc;  // h = x + m (nm/src/qwen35.hpp:321)
+                    else if constexpr (EPI == kEpiStore)
+                        y[o] = acc;
+                    else {
+                        // rows chain_row0 .. +63 are 32 gate rows then the 32 up rows of
+                        // the same FF indices: g = silu(gate) * up
+                        // (nm/src/components.hpp:300-304), then quantize_row_q8_0 of the
+                        // block, written as the down projection's input
+                        const float up = __shfl_down(acc, 32, 64);
+                        if (tid < 32) {
+                            const float v = silu_f32(acc) * up;
+                            float amax = fabsf(v);
+                            for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+                            const float d = amax / 127.f;
+                            const float id = d != 0.f ? 1.f / d : 0.f;
+                            const int64_t blk = chain_row0 / 64;
+                            int8_t* qs = reinterpret_cast<int8_t*>(y);
+                            qs[blk * 32 + tid] = int8_t(int(roundf(v * id)));
+                            if (tid == 0) reinterpret_cast<float*>(qs + N / 2)[blk] = half_bits_to_f32(fp32_to_fp16_ref(d));
                         }
                     }
                 }
-                if (j + D < nsub) load(j + D, ring[s], sring[s]);
-                const int done = rb + kStreamRB - chain_row0;  // rows whose terms are all stored
-                if (done >= TR || j + 1 == nsub) {
-                    const int rows = min(done, r_end - chain_row0);
-                    __syncthreads();
-                    if (tid < rows) {
-                        const float4* t = reinterpret_cast<const float4*>(terms + tid * ts);
-                        float acc = 0.f;
-                        float4 q[4];
-#pragma unroll
-                        for (int u = 0; u < 4; ++u) q[u] = t[u];
-                        for (int b4 = 0; b4 < nb / 4; b4 += 4) {
-                            float4 nq[4];
-#pragma unroll
-                            for (int u = 0; u < 4; ++u) nq[u] = b4 + 4 + u < nb / 4 ? t[b4 + 4 + u] : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                            for (int u = 0; u < 4; ++u) {
-                                acc += q[u].x;
-                                acc += q[u].y;
-                                acc += q[u].z;
-                                acc += q[u].w;
-                            }
-#pragma unroll
-                            for (int u = 0; u < 4; ++u) q[u] = nq[u];
-                        }
-                        const int64_t o = chain_row0 + tid;
-                        if constexpr (EPI == kEpiResidual)
-                            y[o] = resid[o] + acc;  // h = x + m (nm/src/qwen35.hpp:321)
-                        else if constexpr (EPI == kEpiStore)
-                            y[o] = acc;
-                        else {
-                            // rows chain_row0 .. +63 are 32 gate rows then the 32 up rows of
-                            // the same FF indices: g = silu(gate) * up
-                            // (nm/src/components.hpp:300-304), then quantize_row_q8_0 of the
-                            // block, written as the down projection's input
-                            const float up = __shfl_down(acc, 32, 64);
-                            if (tid < 32) {
-                                const float v = silu_f32(acc) * up;
-                                float amax = fabsf(v);
-                                for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-                                const float d = amax / 127.f;
-                                const float id = d != 0.f ? 1.f / d : 0.f;
-                                const int64_t blk = chain_row0 / 64;
-                                int8_t* qs = reinterpret_cast<int8_t*>(y);
-                                qs[blk * 32 + tid] = int8_t(int(roundf(v * id)));
-                                if (tid == 0) reinterpret_cast<float*>(qs + N / 2)[blk] = half_bits_to_f32(fp32_to_fp16_ref(d));
-                            }
-                        }
-                    }
-                    __syncthreads();
-                    chain_row0 += rows;
-                }
+                __syncthreads();
+                chain_row0 += prow;
+                if constexpr (EPI == kEpiResidual) rnext = load_f32(br, uint32_t(chain_row0 - r_begin + tid) * 4u);
             }
         }
     }
@@ -414,8 +442,8 @@ void launch_gemv_q8_in(const void* packed, const GemvInput& in, float* y, const 
     if (in.mode == kInRmsNorm) smem = std::max(smem, size_t(K) * 4);  // the squares
     switch (K / 4096) {
         case 1: stream_dispatch_in<1, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
-        case 2: stream_dispatch_in<2, 1>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
-        default: stream_dispatch_in<3, 1>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+        case 2: stream_dispatch_in<2, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+        default: stream_dispatch_in<3, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
     }
 }
 
@@ -590,15 +618,8 @@ constexpr int kSkWaveBlocks = kSkRound / 4;    // blocks per wave per round
 constexpr int kSkPairs = kSkWaveBlocks / 2;    // 16-byte loads per lane per round
 constexpr int kSkMaxK = 16384;
 constexpr int kSkRing = 3;                     // steps (group, round) in flight per lane
-// Every global access of the skinny kernel is a raw buffer access: an offset
-// at or past the buffer's size reads 0 and drops a store, so invalid rows,
-// blocks and padded steps need no branch and every loop iteration issues the
-// same memory instructions (which lets the compiler wait for exactly the
-// oldest loads instead of all of them).
-constexpr uint32_t kOOB = 0x80000000u;         // beyond every buffer (sizes < 2 GiB)
-constexpr uint32_t kBufWord3 = 0x00020000u;    // raw dword buffer, gfx9 family
-
-typedef int v4b_t __attribute__((ext_vector_type(4)));
+// Every global access of the skinny kernel is a raw buffer access (kOOB),
+// so invalid rows, blocks and padded steps need no branch.
 
 struct SkLoads {
     v4b_t w[kSkPairs];
@@ -608,9 +629,6 @@ struct SkLoads {
 
 __device__ __forceinline__ long lo64(v4b_t v) { return long((uint64_t(uint32_t(v.y)) << 32) | uint32_t(v.x)); }
 __device__ __forceinline__ long hi64(v4b_t v) { return long((uint64_t(uint32_t(v.w)) << 32) | uint32_t(v.z)); }
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, int(bytes), int(kBufWord3));
-}
 
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_q8_skinny_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {

@@ -112,7 +112,7 @@ def _q8_weight_copies(lib, n: int, k: int, copies: int, gen):
     return out
 
 
-def bench_gemv(lib, replays: int = 20):
+def bench_gemv(lib, replays: int = 20, batches=GEMV_BATCHES):
     from ._lib import check
 
     t = _torch()
@@ -123,7 +123,7 @@ def bench_gemv(lib, replays: int = 20):
         wbytes = n * k * 34 // 32
         copies = max(1, math.ceil(512e6 / wbytes))
         weights = _q8_weight_copies(lib, n, k, copies, gen)
-        for m in GEMV_BATCHES:
+        for m in batches:
             x = t.randn(m, k, device="cuda", generator=gen)
             act = _bytes(lib.hero_q8_0_act_bytes(m, k))
             check(lib.hero_q8_0_quantize(_p(x), _p(act), m, k, _stream()))
@@ -136,16 +136,26 @@ def bench_gemv(lib, replays: int = 20):
                     else:
                         check(lib.hero_q8_0_gemm(_p(w), _p(act), _p(y), None, m, n, k, _stream()))
 
-            sec = _time_graph(body, len(weights), replays)
-            nbytes = wbytes + m * k * 4 + m * n * 4  # the unit of work: weights + fp32 x in + fp32 y out
-            ops = 2.0 * m * n * k
-            rows.append({
-                "suite": "gemv", "kernel": "gemv_q8_stream" if m == 1 else "gemm_q8 (int8 MFMA)",
-                "K": k, "N": n, "M": m, "copies": copies, "us": sec * 1e6,
-                "GB/s": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS,
-                "TOPS": ops / sec / 1e12, "int8_frac": ops / sec / 1e12 / INT8_PEAK_TOPS,
-            })
-            print(json.dumps(rows[-1]), flush=True)
+            def norm_body():
+                # the decode step's form: RMSNorm + quantize of x fused as the GEMV's prologue
+                for w in weights:
+                    check(lib.hero_rmsnorm_q8_0_gemv(_p(w), _p(x), _p(gamma), 1e-6, _p(y), None, n, k, _p(act), _stream()))
+
+            variants = [("gemv_q8_stream" if m == 1 else "gemm_q8 (int8 MFMA)", body)]
+            if m == 1 and k == 4096:
+                gamma = 1.0 + 0.1 * t.randn(k, device="cuda", generator=gen)
+                variants.append(("gemv_q8_stream, RMSNorm prologue", norm_body))
+            for name, fn in variants:
+                sec = _time_graph(fn, len(weights), replays)
+                nbytes = wbytes + m * k * 4 + m * n * 4  # the unit of work: weights + fp32 x in + fp32 y out
+                ops = 2.0 * m * n * k
+                rows.append({
+                    "suite": "gemv", "kernel": name,
+                    "K": k, "N": n, "M": m, "copies": copies, "us": sec * 1e6,
+                    "GB/s": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS,
+                    "TOPS": ops / sec / 1e12, "int8_frac": ops / sec / 1e12 / INT8_PEAK_TOPS,
+                })
+                print(json.dumps(rows[-1]), flush=True)
             del act, y, x
         del weights
         t.cuda.empty_cache()
@@ -333,6 +343,7 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--suite", default="gemv,gdn,attn")
     ap.add_argument("--out", default=None, help="write a markdown table here")
+    ap.add_argument("--gemv-batches", default=",".join(map(str, GEMV_BATCHES)), help="activation rows M of the gemv suite")
     args = ap.parse_args(argv)
     t = _torch()
     if not t.cuda.is_available():
@@ -343,7 +354,7 @@ def main(argv=None) -> int:
     rows = []
     suites = args.suite.split(",")
     if "gemv" in suites:
-        rows += bench_gemv(lib)
+        rows += bench_gemv(lib, batches=[int(v) for v in args.gemv_batches.split(",")])
     if "gdn" in suites:
         rows += bench_gdn(lib)
     if "attn" in suites:

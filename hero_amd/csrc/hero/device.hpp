@@ -56,6 +56,26 @@ __device__ __forceinline__ float load_f32(__amdgpu_buffer_rsrc_t b, uint32_t off
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(b, off, 0, 0));
 }
 
+// Loads straight into shared memory (global_load_lds): every lane's 16 or 4
+// bytes land at lds_base + lane * size, lds_base uniform over the wave. They
+// are issued from inline assembly so the compiler does not track them: it
+// would otherwise wait for every such load in flight before any shared-memory
+// read. The caller waits for them itself (wait_vmcnt) and publishes them with
+// a barrier. M0 carries the base and is restored afterwards.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+    return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
+}
+__device__ __forceinline__ void lds_dma_b128(const void* g, uint32_t lds_base) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_base)) : "memory");
+}
+__device__ __forceinline__ void lds_dma_b32(const void* g, uint32_t lds_base) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_base)) : "memory");
+}
+
 // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and
 // lgkmcnt left at their maxima, i.e. not waited for): at most N vector memory
 // operations of this wave still outstanding.

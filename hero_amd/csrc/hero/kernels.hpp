@@ -20,6 +20,7 @@ enum : int { kEpiStore = 0, kEpiResidual = 1, kEpiSwigluQuant = 2 };
 // scales of 8 consecutive rows of one block are one 16-byte load, and those of
 // one 8-row group for every block are contiguous (one sweep per sub-batch)
 inline int64_t packed_rows_pad(int64_t N) { return (N + 7) / 8 * 8; }
+int device_cus();  // compute units of the current device (cached per device)
 // index of the scale of (row, block) among the fp16 scales; nb = K/32
 __host__ __device__ inline int64_t scale_index(int64_t row, int64_t block, int64_t nb) { return ((row >> 3) * nb + block) * 8 + (row & 7); }
 inline int64_t packed_q8_bytes(int64_t N, int64_t K) { return N * K + packed_rows_pad(N) * (K / 32) * 2; }

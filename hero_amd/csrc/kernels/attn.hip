@@ -7,18 +7,20 @@
 //             split of the packed [q | gate] pair, q RMSNorm + RoPE; the first
 //             query head of each K/V group also normalises and rotates k and
 //             appends k and v to the cache.
-//  2. scores  a lane per visible key: s_j = scale * dot(q, k_j), the dot a
-//             sequential 128-term sum (nm/src/core.hpp:496-500). K is cached
-//             channel-major per head, [Dh][max_ctx], so lanes reading
-//             consecutive keys read consecutive addresses.
+//  2. scores  a lane per visible key and KV head: s_j = scale * dot(q, k_j)
+//             for each query head of the group, every dot a sequential
+//             128-term sum (nm/src/core.hpp:496-500). K is cached channel-major
+//             per head, [Dh][max_ctx], so lanes reading consecutive keys read
+//             consecutive addresses.
 //  3. softmax one workgroup per (sequence, query head): max, e_j = exp(s_j -
 //             max), the softmax total as the sequential sum over j
 //             (components.hpp:132-141) computed exactly in parallel
 //             (hero/seqsum.hpp), alpha_j = e_j / total.
-//  4. pv      four workgroups per (sequence, query head), 32 channels each:
-//             a lane per channel accumulates alpha_j * v_j[c] in row order
-//             (core.hpp:206-208), multiplies by sigmoid(gate)
-//             (qwen35.hpp:390-393) and quantizes the output (one Q8_0 block).
+//  4. pv      a workgroup per (sequence, query head, 32 channels): the
+//             products alpha_j * v_j[c] are formed in parallel, then a lane per
+//             channel adds them in row order (core.hpp:206-208), multiplies by
+//             sigmoid(gate) (qwen35.hpp:390-393) and quantizes the output (one
+//             Q8_0 block).
 // RoPE reads a host-built cos/sin table made with the reference's float
 // expressions (attention.hpp:76-91).
 // With shared_cache set, the B rows are consecutive tokens of one sequence
@@ -33,7 +35,7 @@
 namespace hero {
 
 constexpr int kAttnDim = 128;
-constexpr int kScoreTiles = 8;
+constexpr int kScoreTiles = 128;  // most score tiles of 256 keys per head
 
 // the cache row b reads and appends to
 __device__ __forceinline__ int64_t cache_of(const AttnDecodeArgs& a, int b) { return a.shared_cache ? 0 : b; }
@@ -95,24 +97,44 @@ __global__ __launch_bounds__(kAttnDim) void attn_prep_kernel(AttnDecodeArgs a) {
 __device__ __forceinline__ int visible_first(int pos, int window) { return (window > 0 && pos + 1 > window) ? pos + 1 - window : 0; }
 
 // ---- 2. scores -------------------------------------------------------------------------
+// A lane per visible key and KV head: it reads the key's 128 cached channels
+// once and forms the dot products of every query head of the group (up to
+// kScoreHeads at a time), each the sequential 128-term sum, side by side. The
+// grid covers max_ctx in tiles of 256 keys (at most kScoreTiles tiles; lanes
+// loop when the context is longer).
+constexpr int kScoreHeads = 4;
+
 __global__ __launch_bounds__(256) void attn_scores_kernel(AttnDecodeArgs a) {
-    const int h = blockIdx.x, tile0 = blockIdx.y, b = blockIdx.z;
+    const int tile0 = blockIdx.y, b = blockIdx.z;
+    const int group = a.Hq / a.Hkv, nchunk = (group + kScoreHeads - 1) / kScoreHeads;
+    const int g = int(blockIdx.x) / nchunk, hq0 = g * group + (int(blockIdx.x) % nchunk) * kScoreHeads;
+    const int nh = min(kScoreHeads, g * group + group - hq0);
     const int pos = a.positions[b];
     if (pos < 0 || pos >= a.max_ctx) return;
-    const int g = h / (a.Hq / a.Hkv);
     const int first = visible_first(pos, a.window);
     const int n = pos + 1 - first;
-    __shared__ float q[kAttnDim];
-    if (threadIdx.x < kAttnDim) q[threadIdx.x] = a.q_rot[(int64_t(b) * a.Hq + h) * kAttnDim + threadIdx.x];
+    if (tile0 * 256 >= n) return;
+    __shared__ float q[kScoreHeads][kAttnDim];
+    for (int i = threadIdx.x; i < kScoreHeads * kAttnDim; i += 256) {
+        const int hh = min(i / kAttnDim, nh - 1);
+        q[i / kAttnDim][i % kAttnDim] = a.q_rot[(int64_t(b) * a.Hq + hq0 + hh) * kAttnDim + i % kAttnDim];
+    }
     __syncthreads();
     const float* kh = a.k_cache + (cache_of(a, b) * a.Hkv + g) * kAttnDim * a.max_ctx;
-    float* sc = a.scores + (int64_t(b) * a.Hq + h) * a.max_ctx;
-    for (int t = tile0 * 256 + int(threadIdx.x); t < n; t += kScoreTiles * 256) {
+    float* sc = a.scores + (int64_t(b) * a.Hq + hq0) * a.max_ctx;
+    const int step = int(gridDim.y) * 256;
+    for (int t = tile0 * 256 + int(threadIdx.x); t < n; t += step) {
         const float* kj = kh + first + t;
-        float dot = 0.f;
+        float dot[kScoreHeads] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 16
-        for (int c = 0; c < kAttnDim; ++c) dot += q[c] * kj[int64_t(c) * a.max_ctx];
-        sc[t] = a.score_scale * dot;
+        for (int c = 0; c < kAttnDim; ++c) {
+            const float k = kj[int64_t(c) * a.max_ctx];
+#pragma unroll
+            for (int hh = 0; hh < kScoreHeads; ++hh) dot[hh] += q[hh][c] * k;
+        }
+#pragma unroll
+        for (int hh = 0; hh < kScoreHeads; ++hh)
+            if (hh < nh) sc[int64_t(hh) * a.max_ctx + t] = a.score_scale * dot[hh];
     }
 }
 
@@ -157,19 +179,155 @@ __global__ __launch_bounds__(seqsum::kThreads) void attn_softmax_kernel(AttnDeco
 }
 
 // ---- 4. weighted sum of values, gate, quantize -----------------------------------------------
-// out[c] = sum_j alpha_j * v_j[c] with the rows in order (core.hpp:206-208),
-// one lane per channel. Each workgroup owns 32 channels (one Q8_0 block) of a
-// head; its 256 lanes stream the V rows through a ring of register tiles into
-// two shared-memory tiles so the 32 chain lanes read V from shared memory.
-constexpr int kPvSplit = 4;
-constexpr int kPvCh = kAttnDim / kPvSplit;                  // 32
-constexpr int kPvThreads = 256;
-constexpr int kPvTile = 128;                                // rows per tile
-constexpr int kPvVec = kPvTile * kPvCh / 4 / kPvThreads;    // float4 per lane per tile
-constexpr int kPvRing = 4;                                  // tiles in flight
+// out[c] = sum_j alpha_j * v_j[c] with the rows in order (core.hpp:206-208).
+// A workgroup per (sequence, query head, 32 channels = one Q8_0 block of the
+// output), in tiles of kPvRows rows, with three roles:
+//  * wave 3 streams the V rows and alpha values of the tiles straight into a
+//    ring of kPvRing shared-memory slots (global_load_lds: the same nine
+//    loads per lane every tile, so it waits for exactly its oldest tile);
+//  * waves 1..2 form the products alpha_j * v_j[c] (the reference's product,
+//    one rounding) and store them transposed, [channel][row], into one of two
+//    product buffers;
+//  * lanes 0..31 of wave 0 each hold one channel's sum and only add, four
+//    products per 16-byte read, which is the dependent chain the reference's
+//    loop is.
+// One barrier per tile: after it the loader refills the freed slot, the
+// producers fill the next tile's products and the chain adds the current
+// tile's.
+constexpr int kPvCh = 32;                                   // channels per workgroup
+constexpr int kPvRows = 64;                                 // rows per tile
+constexpr int kPvStride = kPvRows + 4;                      // product row stride (conflict-free 16-byte reads)
+constexpr int kPvRing = 6;                                  // tiles of V and alpha in flight
+constexpr int kPvThreads = 256;                             // chain wave, two producer waves, loader wave
+constexpr int kPvVTile = kPvRows * kPvCh;                   // floats of V per tile
+constexpr int kPvVLoads = kPvVTile / 4 / 64;                // 16-byte V loads per loader lane per tile: 8
+constexpr int kPvLoads = kPvVLoads + 1;                     // plus one alpha value
+constexpr size_t kPvShared = (size_t(kPvRing) * (kPvVTile + kPvRows) + size_t(2) * kPvCh * kPvStride) * 4;
+static_assert(kPvVLoads == 8 && kPvRows == 64 && kPvCh * kPvRows / 4 / 4 == 128, "tile geometry");
 
 __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(AttnDecodeArgs a) {
-    const int tid = threadIdx.x, h = blockIdx.x / kPvSplit, part = blockIdx.x % kPvSplit, b = blockIdx.y;
+    extern __shared__ __align__(16) float pv_smem[];  // [kPvRing][V tile] [kPvRing][alpha tile] [2][kPvCh][kPvStride]
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64, b = blockIdx.y;
+    constexpr int parts = kAttnDim / kPvCh;
+    const int h = int(blockIdx.x) / parts, part = int(blockIdx.x) % parts;
+    const int g = h / (a.Hq / a.Hkv);
+    const int pos = a.positions[b];
+    if (pos < 0 || pos >= a.max_ctx) return;
+    const int first = visible_first(pos, a.window);
+    const int n = pos + 1 - first;
+    const float* alpha = a.scores + (int64_t(b) * a.Hq + h) * a.max_ctx;
+    const int64_t kw = int64_t(a.Hkv) * kAttnDim;
+    const float* vb = a.v_cache + (cache_of(a, b) * a.max_ctx + first) * kw + int64_t(g) * kAttnDim + part * kPvCh;
+    const int ntiles = (n + kPvRows - 1) / kPvRows;
+    float* vring = pv_smem;
+    float* aring = vring + kPvRing * kPvVTile;
+    float* prod = aring + kPvRing * kPvRows;
+    constexpr int pstride = kPvCh * kPvStride;
+
+    // loader: V rows (rows past n read row n - 1, whose products the chain
+    // never adds) and alpha values of a tile
+    auto issue = [&](int tile) {
+        const int slot = tile % kPvRing;
+#pragma unroll
+        for (int j = 0; j < kPvVLoads; ++j) {
+            const int q = lane + 64 * j;  // 16-byte slot: row q / 8, channels 4 (q % 8) ..
+            const int row = min(tile * kPvRows + q / 8, n - 1);
+            lds_dma_b128(vb + int64_t(row) * kw + 4 * (q % 8), lds_offset(vring + slot * kPvVTile + 256 * j));
+        }
+        lds_dma_b32(alpha + min(tile * kPvRows + lane, n - 1), lds_offset(aring + slot * kPvRows));
+    };
+    // producers: channels c4 .. c4 + 3 and rows r4 .. r4 + 3 of a tile
+    auto produce = [&](int tile) {
+        const int slot = tile % kPvRing;
+        const int c4 = (lane % 8) * 4, r4 = ((wave - 1) * 8 + lane / 8) * 4;
+        const float* vt = vring + slot * kPvVTile;
+        float4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = reinterpret_cast<const float4*>(vt + (r4 + k) * kPvCh + c4)[0];
+        const float4 al = reinterpret_cast<const float4*>(aring + slot * kPvRows + r4)[0];
+        float* d = prod + (tile & 1) * pstride + c4 * kPvStride + r4;
+        reinterpret_cast<float4*>(d)[0] = make_float4(al.x * v[0].x, al.y * v[1].x, al.z * v[2].x, al.w * v[3].x);
+        reinterpret_cast<float4*>(d + kPvStride)[0] = make_float4(al.x * v[0].y, al.y * v[1].y, al.z * v[2].y, al.w * v[3].y);
+        reinterpret_cast<float4*>(d + 2 * kPvStride)[0] = make_float4(al.x * v[0].z, al.y * v[1].z, al.z * v[2].z, al.w * v[3].z);
+        reinterpret_cast<float4*>(d + 3 * kPvStride)[0] = make_float4(al.x * v[0].w, al.y * v[1].w, al.z * v[2].w, al.w * v[3].w);
+    };
+
+    if (wave == 3) {
+        for (int t = 0; t < kPvRing; ++t)
+            if (t < ntiles) issue(t);
+        if (ntiles >= kPvRing)
+            wait_vmcnt<(kPvRing - 1) * kPvLoads>();
+        else
+            wait_vmcnt<0>();
+    }
+    __syncthreads();
+    if (wave == 1 || wave == 2) produce(0);
+    float acc = 0.f;
+    for (int tile = 0; tile < ntiles; ++tile) {
+        if (wave == 3) {
+            // tile + 1 has landed
+            if (tile + kPvRing <= ntiles)
+                wait_vmcnt<(kPvRing - 2) * kPvLoads>();
+            else
+                wait_vmcnt<0>();
+        }
+        __syncthreads();
+        if (wave == 3) {
+            if (tile + kPvRing < ntiles) issue(tile + kPvRing);  // into the slot of tile, whose products exist
+        } else if (wave > 0) {
+            if (tile + 1 < ntiles) produce(tile + 1);  // the other buffer: its last reader was the chain before the barrier
+        } else if (lane < kPvCh) {
+            const float* row = prod + (tile & 1) * pstride + lane * kPvStride;
+            const int rows = min(kPvRows, n - tile * kPvRows);
+            if (rows == kPvRows) {
+                float4 p[kPvRows / 4];
+#pragma unroll
+                for (int i = 0; i < kPvRows / 4; ++i) p[i] = reinterpret_cast<const float4*>(row)[i];
+#pragma unroll
+                for (int i = 0; i < kPvRows / 4; ++i) {
+                    acc += p[i].x;
+                    acc += p[i].y;
+                    acc += p[i].z;
+                    acc += p[i].w;
+                }
+            } else {
+                for (int r = 0; r < rows; ++r) acc += row[r];
+            }
+        }
+    }
+
+    if (wave == 0 && lane < kPvCh) {
+        const int ch = part * kPvCh + lane;
+        const float gate = a.proj[int64_t(b) * a.proj_stride + int64_t(h) * 2 * kAttnDim + kAttnDim + ch];
+        const float out = acc * sigmoid_f32(gate);
+        const int64_t width = int64_t(a.Hq) * kAttnDim;
+        const int64_t idx = int64_t(h) * kAttnDim + ch;
+        if (a.out_f32) a.out_f32[int64_t(b) * width + idx] = out;
+        float amax = fabsf(out);
+        for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+        const float d = amax / 127.f;
+        const float id = d != 0.f ? 1.f / d : 0.f;
+        int8_t* qs = static_cast<int8_t*>(a.act_out);
+        float* qd = reinterpret_cast<float*>(qs + int64_t(a.B) * width);
+        qs[int64_t(b) * width + idx] = int8_t(int(roundf(out * id)));
+        if (lane == 0) qd[(int64_t(b) * width + idx) >> 5] = half_bits_to_f32(fp32_to_fp16_ref(d));
+    }
+}
+
+// The same sum for many sequences at once (where the per-head workgroups above
+// would outnumber the CUs several times): a workgroup per (sequence, query
+// head, 32 channels) whose 256 lanes stream the V rows through a ring of
+// register tiles into two shared-memory tiles, 32 chain lanes multiplying and
+// adding from shared memory; small shared memory, so many fit per CU.
+constexpr int kPvbSplit = 4;
+constexpr int kPvbCh = kAttnDim / kPvbSplit;                  // 32
+constexpr int kPvbThreads = 256;
+constexpr int kPvbTile = 128;                                // rows per tile
+constexpr int kPvbVec = kPvbTile * kPvbCh / 4 / kPvbThreads;    // float4 per lane per tile
+constexpr int kPvbRing = 4;                                  // tiles in flight
+
+__global__ __launch_bounds__(kPvbThreads) void attn_pv_batch_kernel(AttnDecodeArgs a) {
+    const int tid = threadIdx.x, h = blockIdx.x / kPvbSplit, part = blockIdx.x % kPvbSplit, b = blockIdx.y;
     const int pos = a.positions[b];
     if (pos < 0 || pos >= a.max_ctx) return;
     const int g = h / (a.Hq / a.Hkv);
@@ -177,52 +335,52 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(AttnDecodeArgs a) {
     const int n = pos + 1 - first;
     const float* alpha = a.scores + (int64_t(b) * a.Hq + h) * a.max_ctx;
     const int64_t kw = int64_t(a.Hkv) * kAttnDim;
-    const float* vb = a.v_cache + (cache_of(a, b) * a.max_ctx + first) * kw + int64_t(g) * kAttnDim + part * kPvCh;
-    __shared__ __align__(16) float vt[2][kPvTile * kPvCh];
-    __shared__ float at[2][kPvTile];
-    const int ntiles = (n + kPvTile - 1) / kPvTile;
+    const float* vb = a.v_cache + (cache_of(a, b) * a.max_ctx + first) * kw + int64_t(g) * kAttnDim + part * kPvbCh;
+    __shared__ __align__(16) float vt[2][kPvbTile * kPvbCh];
+    __shared__ float at[2][kPvbTile];
+    const int ntiles = (n + kPvbTile - 1) / kPvbTile;
 
-    float4 ring[kPvRing][kPvVec];
-    float aring[kPvRing];
+    float4 ring[kPvbRing][kPvbVec];
+    float aring[kPvbRing];
     // lane slot k of a tile: float4 q = tid + k*256 -> row q/8, channels 4*(q%8)..+3
     auto load = [&](int tile, float4* dst, float& adst) {
-        const int r0 = tile * kPvTile;
+        const int r0 = tile * kPvbTile;
 #pragma unroll
-        for (int k = 0; k < kPvVec; ++k) {
-            const int q = tid + k * kPvThreads;
-            const int row = r0 + q / (kPvCh / 4);
-            dst[k] = row < n ? *reinterpret_cast<const float4*>(vb + int64_t(row) * kw + 4 * (q % (kPvCh / 4))) : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int k = 0; k < kPvbVec; ++k) {
+            const int q = tid + k * kPvbThreads;
+            const int row = r0 + q / (kPvbCh / 4);
+            dst[k] = row < n ? *reinterpret_cast<const float4*>(vb + int64_t(row) * kw + 4 * (q % (kPvbCh / 4))) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        adst = (tid < kPvTile && r0 + tid < n) ? alpha[r0 + tid] : 0.f;
+        adst = (tid < kPvbTile && r0 + tid < n) ? alpha[r0 + tid] : 0.f;
     };
 #pragma unroll
-    for (int s = 0; s < kPvRing; ++s)
+    for (int s = 0; s < kPvbRing; ++s)
         if (s < ntiles) load(s, ring[s], aring[s]);
 
     float acc = 0.f;
-    for (int base = 0; base < ntiles; base += kPvRing) {
+    for (int base = 0; base < ntiles; base += kPvbRing) {
 #pragma unroll
-        for (int s = 0; s < kPvRing; ++s) {
+        for (int s = 0; s < kPvbRing; ++s) {
             const int tile = base + s;
             if (tile >= ntiles) break;
             float* buf = vt[tile & 1];
             float* abuf = at[tile & 1];
 #pragma unroll
-            for (int k = 0; k < kPvVec; ++k) reinterpret_cast<float4*>(buf)[tid + k * kPvThreads] = ring[s][k];
-            if (tid < kPvTile) abuf[tid] = aring[s];
+            for (int k = 0; k < kPvbVec; ++k) reinterpret_cast<float4*>(buf)[tid + k * kPvbThreads] = ring[s][k];
+            if (tid < kPvbTile) abuf[tid] = aring[s];
             // one barrier per tile: the other buffer's readers finished before it
             __syncthreads();
-            if (tile + kPvRing < ntiles) load(tile + kPvRing, ring[s], aring[s]);
-            if (tid < kPvCh) {
-                const int rows = min(kPvTile, n - tile * kPvTile);
+            if (tile + kPvbRing < ntiles) load(tile + kPvbRing, ring[s], aring[s]);
+            if (tid < kPvbCh) {
+                const int rows = min(kPvbTile, n - tile * kPvbTile);
 #pragma unroll 16
-                for (int r = 0; r < rows; ++r) acc += abuf[r] * buf[r * kPvCh + tid];
+                for (int r = 0; r < rows; ++r) acc += abuf[r] * buf[r * kPvbCh + tid];
             }
         }
     }
 
-    if (tid < kPvCh) {
-        const int c = part * kPvCh + tid;
+    if (tid < kPvbCh) {
+        const int c = part * kPvbCh + tid;
         const float gate = a.proj[int64_t(b) * a.proj_stride + int64_t(h) * 2 * kAttnDim + kAttnDim + c];
         const float out = acc * sigmoid_f32(gate);
         const int64_t width = int64_t(a.Hq) * kAttnDim;
@@ -457,9 +615,16 @@ void launch_attn_paged(const AttnPagedArgs& p, hipStream_t s) {
 
 void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(attn_prep_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, a);
-    hipLaunchKernelGGL(attn_scores_kernel, dim3(unsigned(a.Hq), kScoreTiles, unsigned(a.B)), dim3(256), 0, s, a);
+    const int64_t vis = a.window > 0 ? std::min<int64_t>(a.max_ctx, a.window) : a.max_ctx;
+    const unsigned tiles = unsigned(std::min<int64_t>(kScoreTiles, (vis + 255) / 256));
+    const int group = a.Hq / a.Hkv;
+    hipLaunchKernelGGL(attn_scores_kernel, dim3(unsigned(a.Hkv * ((group + kScoreHeads - 1) / kScoreHeads)), tiles, unsigned(a.B)), dim3(256), 0, s, a);
     hipLaunchKernelGGL(attn_softmax_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(seqsum::kThreads), 0, s, a);
-    hipLaunchKernelGGL(attn_pv_kernel, dim3(unsigned(a.Hq * kPvSplit), unsigned(a.B)), dim3(kPvThreads), 0, s, a);
+    // the per-head pipeline while its workgroups fit the CUs about twice over
+    if (int64_t(a.B) * a.Hq * (kAttnDim / kPvCh) <= 2 * device_cus())
+        hipLaunchKernelGGL(attn_pv_kernel, dim3(unsigned(a.Hq * (kAttnDim / kPvCh)), unsigned(a.B)), dim3(kPvThreads), kPvShared, s, a);
+    else
+        hipLaunchKernelGGL(attn_pv_batch_kernel, dim3(unsigned(a.Hq * kPvbSplit), unsigned(a.B)), dim3(kPvbThreads), 0, s, a);
 }
 
 }  // namespace hero

@@ -372,8 +372,6 @@ __global__ __launch_bounds__(256) void gemv_q8_kernel(const int8_t* __restrict__
     }
 }
 
-namespace {
-
 int device_cus() {
     static int cached[64] = {0};
     int dev = 0;
@@ -385,6 +383,8 @@ int device_cus() {
     }
     return cached[dev];
 }
+
+namespace {
 
 template <int CPL, int D, int XM>
 void stream_dispatch(int epi, const int8_t* wq, const uint16_t* wd, const GemvInput& in, float* y, const float* resid, int N, int Npad, int G, int TR, size_t smem, hipStream_t s) {

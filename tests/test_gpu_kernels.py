@@ -536,6 +536,59 @@ def test_attn_decode_matches_oracle(lib, window):
             assert blocks[b].tobytes() == oracle.quantize_row_q8_0(got[b]).tobytes()
 
 
+# long contexts over pre-filled caches: several tiles of the weighted sum
+# (64 rows each, a ring of 6), score tiles of 256 keys, GQA groups of 1, 4 and
+# 6 (score head chunks of 4 and 2), a sliding window, and enough sequences x
+# heads to take the many-sequence form of the weighted sum (B * Hq * 4 > 512)
+@pytest.mark.parametrize("B,hq,hkv,pos,window", [(2, 8, 2, 700, 0), (1, 6, 1, 1500, 0), (2, 4, 4, 450, 300), (5, 32, 8, 333, 0)])
+def test_attn_decode_long_context_matches_oracle(lib, B, hq, hkv, pos, window):
+    from hero_amd._lib import AttnDecodeArgs
+
+    rng = np.random.default_rng(pos + hq)
+    dh, max_ctx = 128, pos + 9
+    qw, kw = hq * dh, hkv * dh
+    stride = 2 * qw + 2 * kw
+    qg = (1 + 0.1 * rng.standard_normal(dh)).astype(np.float32)
+    kg = (1 + 0.1 * rng.standard_normal(dh)).astype(np.float32)
+    eps = np.float32(1e-6)
+    scale = np.float32(1.0) / np.sqrt(np.float32(dh)) if window == 0 else np.float32(1.0)
+    inv = oracle.rope_inv_freq(dh, 1e6, 32)
+    d_cs = dev(oracle.rope_table(dh, 1e6, 32, max_ctx))
+    # cached rows 0 .. pos-1: K channel-major [B][Hkv][Dh][max_ctx], V [B][max_ctx][Hkv*Dh]
+    keys = (rng.standard_normal((B, pos, kw)) * 0.5).astype(np.float32)
+    vals = rng.standard_normal((B, pos, kw)).astype(np.float32)
+    kc = np.zeros((B, hkv, dh, max_ctx), np.float32)
+    kc[:, :, :, :pos] = keys.reshape(B, pos, hkv, dh).transpose(0, 2, 3, 1)
+    vc = np.zeros((B, max_ctx, kw), np.float32)
+    vc[:, :pos] = vals
+    d_kc, d_vc = dev(kc), dev(vc)
+    d_sc = empty(B * hq * max_ctx * 4)
+    d_qr = empty(B * hq * dh * 4)
+    act = empty(lib.hero_q8_0_act_bytes(B, qw))
+    out = empty(B * qw * 4)
+    proj = rng.standard_normal((B, stride)).astype(np.float32)
+    d_proj, d_pos = dev(proj), dev(np.full(B, pos, np.int32))
+    d_qg, d_kg = dev(qg), dev(kg)
+    a = AttnDecodeArgs(ptr(d_proj), stride, 2 * qw, 2 * qw + kw, ptr(d_qg), ptr(d_kg), eps, ptr(d_cs), ptr(d_kc), ptr(d_vc),
+                       max_ctx, ptr(d_pos), ptr(d_sc), ptr(d_qr), scale, window, ptr(act), ptr(out), B, hq, hkv, dh)
+    check(lib.hero_attn_decode(a, stream()))
+    got = host(out, np.float32, (B, qw))
+    for b in range(B):
+        p = proj[b]
+        q = np.stack([p[h * 2 * dh: h * 2 * dh + dh] for h in range(hq)])
+        g = np.concatenate([p[h * 2 * dh + dh: h * 2 * dh + 2 * dh] for h in range(hq)])
+        q = oracle.rope_apply(oracle.rmsnorm(q, qg, eps), inv, pos)
+        k = oracle.rope_apply(oracle.rmsnorm(p[2 * qw: 2 * qw + kw].reshape(hkv, dh), kg, eps), inv, pos)
+        kk = np.concatenate([keys[b], k.reshape(1, kw)])
+        vv = np.concatenate([vals[b], p[2 * qw + kw:].reshape(1, kw)])
+        att = oracle.attend_decode(q.reshape(-1), kk, vv, hq, hkv, dh, window, scale).reshape(-1)
+        expect = (att * oracle.sigmoid(g)).astype(np.float32)
+        assert np.array_equal(bits(got[b]), bits(expect)), f"seq {b}: max ulp {ulp_diff(got[b], expect).max()}"
+    blocks = act_to_blocks(host(act, np.uint8), B, qw)
+    for b in range(B):
+        assert blocks[b].tobytes() == oracle.quantize_row_q8_0(got[b]).tobytes()
+
+
 @pytest.mark.parametrize("hq,window", [(8, 0), (8, 50), (16, 0)])
 def test_attn_paged_fp16_matches_oracle_over_fp16_kv(lib, hq, window):
     """Split-K attention over the paged fp16 cache: pages of 16 positions in a

@@ -76,11 +76,11 @@ __host__ __device__ inline int binade_f32(float s) {
 struct Shared {
     float wsum[kMaxWaves];                  // wave totals of the speculation scan
     uint32_t wc[kMaxWaves], wn[kMaxWaves];  // wave totals of the increments and of the serial counts
-    // serial-element tables, region w (kMaxSerial / waves entries) for wave w
-    int32_t ser_idx[kMaxSerial];  // index of the element
-    float ser_val[kMaxSerial];    // its term
-    uint32_t ser_cx[kMaxSerial];  // increments of the wave's non-serial elements before it (mod 2^32)
-    int32_t ser_e[kMaxSerial];    // binade of the run that follows it
+    // serial-element tables, region w (kMaxSerial / waves entries) for wave w;
+    // one 16-byte entry per element: x = its index, y = its term (bits), z =
+    // increments of the wave's non-serial elements before it (mod 2^32), w =
+    // binade of the run that follows it
+    uint4 ser[kMaxSerial];
     int32_t fell_back;            // 1 if the last sum ran the plain loop (written by wave 0)
     float result;                 // for callers that broadcast a value of their own
 };
@@ -90,7 +90,7 @@ struct Lane {     // what a lane keeps in registers between steps
     static constexpr int kPerThread = PT;
     float v[PT];
     uint32_t c[PT];       // increment of each non-serial element, in its run's units
-    int32_t e_after[PT];  // binade of the speculated sum after each element
+    uint32_t be_after[PT];// exponent field of the speculated sum after each element
     uint32_t serial;      // bit k: element k is serial
     uint32_t csum, cnt;   // the lane's increment total and serial count
 };
@@ -118,38 +118,46 @@ __host__ __device__ inline float lane_sum(const Lane<PT>& L) {
 }
 
 // pre: speculated sum of everything before the lane's first element; next:
-// the same value as the following lane sees it (its `pre`)
+// the same value as the following lane sees it (its `pre`). Terms past the
+// end of the data are +0 (the loaders fill them): adding +0 to a sum >= +0
+// changes nothing, so they need no special case. An element is serial when
+//  * the speculated interval [S (1 - m), S' (1 + m)] has two exponent fields
+//    (a binade change; comparing raw fields also splits the two fields that
+//    share the finest grid, which only adds serial elements),
+//  * the term is not a finite value in [+0, 2^127) or S' (1 + m) is not finite
+//    and <= 3e38,
+//  * or p / u is a tie.
+// A non-serial term is below 2^(e+1) (S' >= p and S' (1 + m) < 2^(e+1)), so
+// p / u < 2^24 and its rounding to an integer is exact.
 template <int PT>
-__host__ __device__ inline void lane_classify(Lane<PT>& L, int i0, int n, float pre, float next) {
-    constexpr int kPerThread = PT;
-    float S[kPerThread + 1];
-    S[0] = pre;
+__host__ __device__ inline void lane_classify(Lane<PT>& L, float pre, float next) {
+    float S = pre;
+    uint32_t be = f32_bits(S) >> 23;
+    uint32_t serial = 0, csum = 0;
 #pragma unroll
-    for (int k = 0; k + 1 < kPerThread; ++k) S[k + 1] = S[k] + L.v[k];
-    S[kPerThread] = next;
-    uint32_t serial = 0, csum = 0, cnt = 0;
-#pragma unroll
-    for (int k = 0; k < kPerThread; ++k) {  // straight-line: no early exits
-        L.e_after[k] = binade_f32(S[k + 1]);
-        const bool in = i0 + k < n;
+    for (int k = 0; k < PT; ++k) {  // straight-line: no early exits
         const float v = L.v[k];
-        const float hi = S[k + 1] * kMarginHi;
-        const int e = binade_f32(S[k]);
-        // v * 2^(23-e): exact for every term that can stay in the binade
-        const float P = ldexpf(v, 23 - e);
-        const float m = floorf(P);
-        const float f = P - m;
-        const bool ser = binade_f32(S[k] * kMarginLo) != binade_f32(hi) || !(v >= 0.f) || !(v <= 3.0e38f) || !(hi <= 3.0e38f) ||
-                         !(P < 67108864.f) || f == 0.5f;
-        const uint32_t ck = in && !ser ? uint32_t(m) + (f > 0.5f ? 1u : 0u) : 0u;
+        const float S1 = k + 1 < PT ? S + v : next;
+        const uint32_t be1 = f32_bits(S1) >> 23;
+        const float hi = S1 * kMarginHi;
+        const bool cross = (f32_bits(S * kMarginLo) ^ f32_bits(hi)) > 0x007FFFFFu;
+        const bool weird = f32_bits(v) >= 0x7F000000u || !(hi <= 3.0e38f);
+        // v / u, u = 2^(e-23), e = max(be, 1) - 127: exact while it can stay in the binade
+        const float P = ldexpf(v, 150 - int(be > 1u ? be : 1u));
+        const float r = rintf(P);
+        const bool tie = fabsf(r - P) == 0.5f;
+        const bool ser = cross || weird || tie;
+        const uint32_t ck = ser ? 0u : uint32_t(r);
         L.c[k] = ck;
+        L.be_after[k] = be1;
         csum += ck;
-        serial |= (in && ser ? 1u : 0u) << k;
-        cnt += in && ser ? 1u : 0u;
+        serial |= (ser ? 1u : 0u) << k;
+        S = S1;
+        be = be1;
     }
     L.serial = serial;
     L.csum = csum;
-    L.cnt = cnt;
+    L.cnt = uint32_t(__builtin_popcount(serial));
 }
 
 // Writes the table entries of the lane's serial elements into its wave's
@@ -158,17 +166,13 @@ __host__ __device__ inline void lane_classify(Lane<PT>& L, int i0, int n, float 
 // capacity are dropped (the walk then runs the plain loop).
 template <int PT>
 __host__ __device__ inline void lane_emit(const Lane<PT>& L, int i0, uint32_t cx, uint32_t r, int region, int cap, Shared& sm) {
-    // straight-line: c[k] is 0 for serial and out-of-range elements, and
-    // serial bits are only set in range
+    // straight-line: c[k] is 0 for serial elements
 #pragma unroll
     for (int k = 0; k < PT; ++k) {
         const bool ser = (L.serial >> k) & 1u;
         if (ser && r < uint32_t(cap)) {
-            const int slot = region * cap + int(r);
-            sm.ser_idx[slot] = i0 + k;
-            sm.ser_val[slot] = L.v[k];
-            sm.ser_cx[slot] = cx;
-            sm.ser_e[slot] = L.e_after[k];
+            const uint32_t be = L.be_after[k];
+            sm.ser[region * cap + int(r)] = make_uint4(uint32_t(i0 + k), f32_bits(L.v[k]), cx, uint32_t(int(be > 1u ? be : 1u) - 127));
         }
         r += ser ? 1u : 0u;
         cx += L.c[k];
@@ -203,10 +207,10 @@ __host__ __device__ inline void read_tables(const Shared& sm, int cap, Tables<W>
     T.nser = nb, T.c_total = cb, T.overflow = of;
 }
 
-// slot of serial entry q < nser in the tables, and the increments of every
+// serial entry q < nser, its cx made global: the increments of every
 // non-serial element before it (mod 2^32)
 template <int W>
-__host__ __device__ inline void locate(const Tables<W>& T, const Shared& sm, int cap, uint32_t q, int& slot, uint32_t& cx) {
+__host__ __device__ inline uint4 locate(const Tables<W>& T, const Shared& sm, int cap, uint32_t q) {
     int sl = 0;
     uint32_t cb = 0;
 #pragma unroll
@@ -215,8 +219,9 @@ __host__ __device__ inline void locate(const Tables<W>& T, const Shared& sm, int
         sl = here ? u * cap + int(q - T.nbase[u]) : sl;
         cb = here ? T.cbase[u] : cb;
     }
-    slot = sl;
-    cx = cb + sm.ser_cx[sl];
+    uint4 e = sm.ser[sl];
+    e.z += cb;
+    return e;
 }
 
 // step r of the walk: the run before serial element r (for r == nser, the
@@ -230,19 +235,15 @@ struct Step {
 
 template <int W>
 __host__ __device__ inline Step walk_entry(const Tables<W>& T, const Shared& sm, int cap, uint32_t r, int n) {
-    int slot = 0, slot_prev = 0;
-    uint32_t cx = T.c_total, cx_prev = 0;
-    if (r < T.nser) locate(T, sm, cap, r, slot, cx);
-    if (r > 0) locate(T, sm, cap, r - 1, slot_prev, cx_prev);
-    const int idx = r < T.nser ? sm.ser_idx[slot] : n;
-    const int idx_prev = r > 0 ? sm.ser_idx[slot_prev] : -1;
+    const uint4 cur = r < T.nser ? locate(T, sm, cap, r) : make_uint4(uint32_t(n), 0u, T.c_total, 0u);
+    const uint4 prev = r > 0 ? locate(T, sm, cap, r - 1) : make_uint4(0xFFFFFFFFu, 0u, 0u, uint32_t(-126));
     Step st;
-    st.e = r > 0 ? sm.ser_e[slot_prev] : -126;
-    const uint32_t C = cx - cx_prev;
-    const bool nonempty = idx > idx_prev + 1;
+    st.e = int32_t(prev.w);
+    const uint32_t C = cur.z - prev.z;
+    const bool nonempty = int(cur.x) > int(prev.x) + 1;
     const bool big = C >= (1u << 24);
     st.a = nonempty && !big ? ldexpf(float(C), st.e - 23) : 0.f;
-    st.val = r < T.nser ? sm.ser_val[slot] : 0.f;
+    st.val = bits_f32(cur.y);
     st.flags = (nonempty ? 1 : 0) | (big ? 2 : 0);
     return st;
 }
@@ -314,7 +315,7 @@ __device__ inline float sum_lanes(Lane<kMaxN / NT>& L, const float* p, int n, Sh
     float next = dpp_f<0x130>(pre);  // wave_shl:1: the next lane's pre
     if (lane == kWaveSize - 1) next = P_next + 0.f;                           // what the next wave's lane 0 computes
 
-    lane_classify(L, i0, n, pre, next);
+    lane_classify(L, pre, next);
 
     // wave-local prefixes of the increments (mod 2^32) and serial counts
     const uint32_t c = scan_u32(L.csum), m = scan_u32(L.cnt);
@@ -325,7 +326,10 @@ __device__ inline float sum_lanes(Lane<kMaxN / NT>& L, const float* p, int n, Sh
     lane_emit(L, i0, c - L.csum, m - L.cnt, w, cap, sm);
     __syncthreads();
 
-    // the walk, in every wave: lane l prepares step base + l
+    // the walk, in every wave: lane l prepares step base + l (steps past the
+    // last add +0 twice), then the chain runs 8 steps at a time with the step
+    // data read from fixed lanes, each lane keeping the chain values of its
+    // own step for the checks
     Tables<W> T;
     read_tables(sm, cap, T);
     bool ok = !T.overflow;
@@ -337,13 +341,17 @@ __device__ inline float sum_lanes(Lane<kMaxN / NT>& L, const float* p, int n, Sh
         const int cnt = int(min(uint32_t(kWaveSize), T.nser + 1 - base));
         const int ia = int(f32_bits(st.a)), iv = int(f32_bits(st.val));
         float my0 = 0.f, my1 = 0.f;  // the chain before this lane's step and after its run
-        for (int l = 0; l < cnt; ++l) {
-            const float a = bits_f32(uint32_t(__builtin_amdgcn_readlane(ia, l)));
-            const float v = bits_f32(uint32_t(__builtin_amdgcn_readlane(iv, l)));
-            const float s1 = s + a;
-            my0 = lane == l ? s : my0;
-            my1 = lane == l ? s1 : my1;
-            s = s1 + v;
+        for (int l0 = 0; l0 < cnt; l0 += 8) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int l = l0 + u;
+                const float a = bits_f32(uint32_t(__builtin_amdgcn_readlane(ia, l)));
+                const float v = bits_f32(uint32_t(__builtin_amdgcn_readlane(iv, l)));
+                const float s1 = s + a;
+                my0 = lane == l ? s : my0;
+                my1 = lane == l ? s1 : my1;
+                s = s1 + v;
+            }
         }
         const bool bad = lane < cnt && !step_ok(st, my0, my1);
         ok = ok && !__any(bad);
@@ -423,7 +431,7 @@ inline float sum_nonneg_host(const float* p, int n, Shared& sm) {
         next[w * kWaveSize + kWaveSize - 1] = P_next + 0.f;
     }
     for (int t = 0; t < NT; ++t) {
-        lane_classify(L[t], t * PT, n, pre[t], next[t]);
+        lane_classify(L[t], pre[t], next[t]);
         c[t] = L[t].csum;
         m[t] = L[t].cnt;
     }

@@ -32,9 +32,6 @@ namespace hero {
 
 constexpr int kGdnDim = 128;
 constexpr int kGdnState = kGdnDim * kGdnDim;
-constexpr int kGdnVec = kGdnState / 4 / kGdnDim;  // 16-byte pieces of the state per lane
-// dynamic shared memory: the state [Dk][Dv], q, k, the head output (128 each), scalars
-constexpr size_t kGdnShared = size_t(kGdnState + 3 * kGdnDim + 4) * 4;
 
 // sequential sum of squares of v[0..128) (nm/src/core.hpp:496-500 order):
 // all 128 values are read from shared memory first, then the chain of adds
@@ -92,98 +89,6 @@ __device__ __forceinline__ void load_past(const float* hist, int64_t CC, int64_t
     }
 }
 
-// dynamic shared memory layout: the state [i][j] (row i = key, column j =
-// value), then q, k, the head output (128 each) and 4 scalars
-constexpr int kShQ = kGdnState, kShK = kShQ + kGdnDim, kShO = kShK + kGdnDim, kShScal = kShO + kGdnDim;
-
-// One token of one head, lane j; q, k, v are the conv+SiLU outputs of the
-// lane's channels. Returns the gated output of column j. The state lives in
-// sh[0 .. kGdnState); the shared vectors are free again when this returns.
-__device__ __forceinline__ float gdn_token(float* sh, int j, float sq, float sk, float v, float beta_in, float alpha_in, float A, float dtb, float gamma, float z, float eps) {
-    float* qv = sh + kShQ;
-    float* kv = sh + kShK;
-    float* ov = sh + kShO;
-    float* scal = sh + kShScal;
-    qv[j] = sq;
-    kv[j] = sk;
-    __syncthreads();
-    // ---- L2 norms (nm/src/recurrent.hpp:40-48), sequential sums ----
-    if (j == 0 || j == 64) {
-        const float ss = sum_squares_128(j == 0 ? qv : kv);
-        scal[j == 0 ? 0 : 1] = 1.f / fmaxf(sqrtf(ss), 1e-6f);
-    }
-    __syncthreads();
-    const float query_scale = 1.f / sqrtf(float(kGdnDim));
-    const float qn = (sq * scal[0]) * query_scale;
-    const float kn = sk * scal[1];
-    __syncthreads();
-    qv[j] = qn;
-    kv[j] = kn;
-    __syncthreads();
-
-    // ---- beta and the decay gate ----
-    const float beta = sigmoid_f32(beta_in);
-    const float g = A * softplus_f32(alpha_in + dtb);
-    const float decay = exp_f32(g);
-
-    // ---- the delta rule on column j (recurrent.hpp:146-177) ----
-    // The column is read from shared memory into registers once; the k and q
-    // vectors are read 32 at a time ahead of the chains.
-    float col[kGdnDim];
-#pragma unroll
-    for (int i = 0; i < kGdnDim; ++i) col[i] = sh[i * kGdnDim + j] * decay;  // pass 1: S[i][j] *= decay
-    float pred = 0.f;
-#pragma unroll
-    for (int i0 = 0; i0 < kGdnDim; i0 += 32) {
-        float4 k4[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) k4[u] = *reinterpret_cast<const float4*>(kv + i0 + 4 * u);
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {  // pred += S[i][j] * k[i]
-            pred = pred + col[i0 + 4 * u + 0] * k4[u].x;
-            pred = pred + col[i0 + 4 * u + 1] * k4[u].y;
-            pred = pred + col[i0 + 4 * u + 2] * k4[u].z;
-            pred = pred + col[i0 + 4 * u + 3] * k4[u].w;
-        }
-    }
-    const float delta = (v - pred) * beta;
-    // pass 2: S[i][j] += k[i] * delta; o += S[i][j] * q[i]
-    float o = 0.f;
-#pragma unroll
-    for (int i0 = 0; i0 < kGdnDim; i0 += 32) {
-        float4 k4[8], q4[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            k4[u] = *reinterpret_cast<const float4*>(kv + i0 + 4 * u);
-            q4[u] = *reinterpret_cast<const float4*>(qv + i0 + 4 * u);
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            col[i0 + 4 * u + 0] = col[i0 + 4 * u + 0] + k4[u].x * delta;
-            col[i0 + 4 * u + 1] = col[i0 + 4 * u + 1] + k4[u].y * delta;
-            col[i0 + 4 * u + 2] = col[i0 + 4 * u + 2] + k4[u].z * delta;
-            col[i0 + 4 * u + 3] = col[i0 + 4 * u + 3] + k4[u].w * delta;
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            o = o + col[i0 + 4 * u + 0] * q4[u].x;
-            o = o + col[i0 + 4 * u + 1] * q4[u].y;
-            o = o + col[i0 + 4 * u + 2] * q4[u].z;
-            o = o + col[i0 + 4 * u + 3] * q4[u].w;
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < kGdnDim; ++i) sh[i * kGdnDim + j] = col[i];  // column j: this lane's own
-
-    // ---- per-head RMSNorm (components.hpp:176-181) and the SiLU(z) gate ----
-    ov[j] = o;
-    __syncthreads();
-    if (j == 0) scal[2] = 1.f / sqrtf(sum_squares_128(ov) / float(kGdnDim) + eps);
-    __syncthreads();
-    const float normed = gamma * o * scal[2];
-    return normed * silu_f32(z);
-}
-
 // Q8_0 quantization of the head's outputs, 32 lanes per block (quant_i8.hpp:70-80)
 __device__ __forceinline__ void gdn_quantize(float out, int64_t row, int64_t rows, int64_t width, int64_t idx, int j, void* act_out) {
     float amax = fabsf(out);
@@ -197,10 +102,34 @@ __device__ __forceinline__ void gdn_quantize(float out, int64_t row, int64_t row
 }
 
 // ---- decode: one token for each of B sequences --------------------------------------
+// A workgroup of 512 lanes per (sequence, value head). Lanes j < 128 own value
+// column j and every sequential chain of it; all 512 lanes (column t % 128,
+// key rows 32 (t / 128) .. +31) do the elementwise work on the state in
+// registers and hand their products to the chains through shared memory,
+// transposed [column][row], so a chain lane only adds, four terms per 16-byte
+// read:
+//  1. conv + SiLU of the head's q, k, v channels; the L2 norms of q and k
+//     (one 128-term chain each, on two waves) while the state loads land;
+//  2. S[i][j] *= decay and the products S[i][j] * k[i]; chain: pred_j;
+//  3. S[i][j] += k[i] * delta_j (stored back), products S[i][j] * q[i];
+//     chain: o_j;
+//  4. the head RMSNorm chain over o_j^2 (lane 0), the SiLU(z) gate, quantize.
+constexpr int kGdnThreads = 512;
+constexpr int kGdnRows = kGdnDim * kGdnDim / kGdnThreads;  // state rows per lane: 32
+constexpr int kGdnPStride = kGdnDim + 4;                    // product row stride (conflict-free 16-byte access)
+struct GdnDecodeShared {
+    float prod[kGdnDim][kGdnPStride];  // [column j][row i]
+    float q[kGdnDim], k[kGdnDim];      // conv + SiLU outputs, then normalised
+    float sq[2][kGdnDim];              // squares of q and k, then of the outputs
+    float delta[kGdnDim];
+    float scal[4];                     // 1/||q||, 1/||k||, 1/rms(o)
+};
+
 template <int W>
-__global__ __launch_bounds__(kGdnDim) void gdn_decode_kernel(GdnDecodeArgs a) {
-    extern __shared__ __align__(16) float sh[];
-    const int j = threadIdx.x;
+__global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(GdnDecodeArgs a) {
+    extern __shared__ __align__(16) float gdn_raw[];
+    GdnDecodeShared& sh = *reinterpret_cast<GdnDecodeShared*>(gdn_raw);
+    const int t = threadIdx.x, j = t % kGdnDim, i0 = (t / kGdnDim) * kGdnRows;
     const int h = blockIdx.x, b = blockIdx.y;
     const int hk = h % a.Hk;  // tiled key heads (nm/src/qwen35.hpp:172)
     const int pos = a.positions[b];
@@ -210,47 +139,160 @@ __global__ __launch_bounds__(kGdnDim) void gdn_decode_kernel(GdnDecodeArgs a) {
     const float* P = a.proj + int64_t(b) * a.proj_stride;
     float* hist = a.conv_hist + int64_t(b) * W * CC;
     float* S = a.state + (int64_t(b) * a.Hv + h) * kGdnState;
+    const bool owner = t < kGdnDim;  // column j's chains
 
-    // ---- every global read first, so their latencies overlap ----
-    float4 sv[kGdnVec];  // coalesced
-#pragma unroll
-    for (int k = 0; k < kGdnVec; ++k) sv[k] = reinterpret_cast<const float4*>(S)[j + kGdnDim * k];
+    // ---- the owners' inputs first (loads retire in order: the conv and the
+    // q/k norms then run while the state is still arriving), then the state
+    // rows i0 .. i0+31 of column j ----
     const int64_t cq = int64_t(hk) * kGdnDim + j, ck = KW + int64_t(hk) * kGdnDim + j, cv = 2 * KW + int64_t(h) * kGdnDim + j;
-    const float xq = P[cq], xk = P[ck], xv = P[cv];
+    float xq = 0.f, xk = 0.f, xv = 0.f, z = 0.f, gamma = 0.f;
     float tq[W], tk[W], tv[W];
     ConvPast<W> pq, pk, pv;
-    load_taps<W>(a.conv_taps, cq, tq);
-    load_taps<W>(a.conv_taps, ck, tk);
-    load_taps<W>(a.conv_taps, cv, tv);
-    load_past<W>(hist, CC, cq, pos, pq);
-    load_past<W>(hist, CC, ck, pos, pk);
-    load_past<W>(hist, CC, cv, pos, pv);
-    const float z = P[a.z_off + int64_t(h) * kGdnDim + j];
-    const float gamma = a.norm_gamma[j];
-    const float beta_in = P[a.beta_off + h], alpha_in = P[a.alpha_off + h];
-    const float A = a.decay[h], dtb = a.dt_bias[h];
-#pragma unroll
-    for (int k = 0; k < kGdnVec; ++k) reinterpret_cast<float4*>(sh)[j + kGdnDim * k] = sv[k];
-
-    // ---- conv + SiLU on this head's channels; the ring takes this position ----
-    const float sq = silu_f32(conv_channel<W>(tq, pq, xq));
-    const float sk = silu_f32(conv_channel<W>(tk, pk, xk));
-    const float v = silu_f32(conv_channel<W>(tv, pv, xv));
-    const int slot = pos % W;
-    if (h < a.Hk) {  // the first value head of each key head owns its q/k history
-        hist[int64_t(slot) * CC + cq] = xq;
-        hist[int64_t(slot) * CC + ck] = xk;
+    if (owner) {
+        xq = P[cq], xk = P[ck], xv = P[cv];
+        load_taps<W>(a.conv_taps, cq, tq);
+        load_taps<W>(a.conv_taps, ck, tk);
+        load_taps<W>(a.conv_taps, cv, tv);
+        load_past<W>(hist, CC, cq, pos, pq);
+        load_past<W>(hist, CC, ck, pos, pk);
+        load_past<W>(hist, CC, cv, pos, pv);
+        z = P[a.z_off + int64_t(h) * kGdnDim + j];
+        gamma = a.norm_gamma[j];
     }
-    hist[int64_t(slot) * CC + cv] = xv;
-
-    const float out = gdn_token(sh, j, sq, sk, v, beta_in, alpha_in, A, dtb, gamma, z, a.eps);
-    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    float col[kGdnRows];
 #pragma unroll
-    for (int k = 0; k < kGdnVec; ++k) reinterpret_cast<float4*>(S)[j + kGdnDim * k] = reinterpret_cast<const float4*>(sh)[j + kGdnDim * k];
-    const int64_t width = int64_t(a.Hv) * kGdnDim;
-    const int64_t idx = int64_t(h) * kGdnDim + j;
-    if (a.out_f32) a.out_f32[int64_t(b) * width + idx] = out;
-    gdn_quantize(out, b, a.B, width, idx, j, a.act_out);
+    for (int r = 0; r < kGdnRows; ++r) col[r] = S[(i0 + r) * kGdnDim + j];
+    __builtin_amdgcn_sched_barrier(0);
+    const float beta = sigmoid_f32(P[a.beta_off + h]);
+    const float decay = exp_f32(a.decay[h] * softplus_f32(P[a.alpha_off + h] + a.dt_bias[h]));
+
+    // ---- 1. conv + SiLU on the head's channels; the ring takes this position ----
+    float v = 0.f;
+    if (owner) {
+        const float q = silu_f32(conv_channel<W>(tq, pq, xq));
+        const float k = silu_f32(conv_channel<W>(tk, pk, xk));
+        v = silu_f32(conv_channel<W>(tv, pv, xv));
+        const int slot = pos % W;
+        if (h < a.Hk) {  // the first value head of each key head owns its q/k history
+            hist[int64_t(slot) * CC + cq] = xq;
+            hist[int64_t(slot) * CC + ck] = xk;
+        }
+        hist[int64_t(slot) * CC + cv] = xv;
+        sh.q[j] = q;
+        sh.k[j] = k;
+        sh.sq[0][j] = q * q;
+        sh.sq[1][j] = k * k;
+    }
+    __syncthreads();
+    // ---- L2 norms (nm/src/recurrent.hpp:40-48), sequential sums ----
+    if (t == 0 || t == 64) {
+        const float4* s4 = reinterpret_cast<const float4*>(sh.sq[t == 0 ? 0 : 1]);
+        float4 x[kGdnDim / 4];
+#pragma unroll
+        for (int i = 0; i < kGdnDim / 4; ++i) x[i] = s4[i];
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < kGdnDim / 4; ++i) {
+            ss += x[i].x;
+            ss += x[i].y;
+            ss += x[i].z;
+            ss += x[i].w;
+        }
+        sh.scal[t == 0 ? 0 : 1] = 1.f / fmaxf(sqrtf(ss), 1e-6f);
+    }
+    __syncthreads();
+    if (owner) {
+        const float query_scale = 1.f / sqrtf(float(kGdnDim));
+        sh.q[j] = (sh.q[j] * sh.scal[0]) * query_scale;
+        sh.k[j] = sh.k[j] * sh.scal[1];
+    }
+    __syncthreads();
+
+    // ---- 2. decay and the prediction products (recurrent.hpp:146-177) ----
+    float kr[kGdnRows];
+#pragma unroll
+    for (int r = 0; r < kGdnRows; r += 4) {
+        const float4 k4 = *reinterpret_cast<const float4*>(sh.k + i0 + r);
+        kr[r] = k4.x, kr[r + 1] = k4.y, kr[r + 2] = k4.z, kr[r + 3] = k4.w;
+    }
+    float* prow = &sh.prod[j][i0];
+#pragma unroll
+    for (int r = 0; r < kGdnRows; r += 4) {
+        col[r] = col[r] * decay, col[r + 1] = col[r + 1] * decay, col[r + 2] = col[r + 2] * decay, col[r + 3] = col[r + 3] * decay;
+        *reinterpret_cast<float4*>(prow + r) = make_float4(col[r] * kr[r], col[r + 1] * kr[r + 1], col[r + 2] * kr[r + 2], col[r + 3] * kr[r + 3]);
+    }
+    __syncthreads();
+    if (owner) {  // pred_j = sum_i S[i][j] * k[i], in i order
+        const float4* p4 = reinterpret_cast<const float4*>(&sh.prod[j][0]);
+        float4 x[kGdnDim / 4];
+#pragma unroll
+        for (int i = 0; i < kGdnDim / 4; ++i) x[i] = p4[i];
+        float pred = 0.f;
+#pragma unroll
+        for (int i = 0; i < kGdnDim / 4; ++i) {
+            pred = pred + x[i].x;
+            pred = pred + x[i].y;
+            pred = pred + x[i].z;
+            pred = pred + x[i].w;
+        }
+        sh.delta[j] = (v - pred) * beta;
+    }
+    __syncthreads();
+
+    // ---- 3. the update, stored back, and the output products ----
+    const float delta = sh.delta[j];
+#pragma unroll
+    for (int r = 0; r < kGdnRows; ++r) col[r] = col[r] + kr[r] * delta;
+#pragma unroll
+    for (int r = 0; r < kGdnRows; ++r) S[(i0 + r) * kGdnDim + j] = col[r];
+#pragma unroll
+    for (int r = 0; r < kGdnRows; r += 4) {
+        const float4 q4 = *reinterpret_cast<const float4*>(sh.q + i0 + r);
+        *reinterpret_cast<float4*>(prow + r) = make_float4(col[r] * q4.x, col[r + 1] * q4.y, col[r + 2] * q4.z, col[r + 3] * q4.w);
+    }
+    __syncthreads();
+    float o = 0.f;
+    if (owner) {  // o_j = sum_i S[i][j] * q[i], in i order
+        const float4* p4 = reinterpret_cast<const float4*>(&sh.prod[j][0]);
+        float4 x[kGdnDim / 4];
+#pragma unroll
+        for (int i = 0; i < kGdnDim / 4; ++i) x[i] = p4[i];
+#pragma unroll
+        for (int i = 0; i < kGdnDim / 4; ++i) {
+            o = o + x[i].x;
+            o = o + x[i].y;
+            o = o + x[i].z;
+            o = o + x[i].w;
+        }
+        sh.sq[0][j] = o * o;
+    }
+    __syncthreads();
+
+    // ---- 4. per-head RMSNorm (components.hpp:176-181), SiLU(z) gate, quantize ----
+    if (t == 0) {
+        const float4* s4 = reinterpret_cast<const float4*>(sh.sq[0]);
+        float4 x[kGdnDim / 4];
+#pragma unroll
+        for (int i = 0; i < kGdnDim / 4; ++i) x[i] = s4[i];
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < kGdnDim / 4; ++i) {
+            ss += x[i].x;
+            ss += x[i].y;
+            ss += x[i].z;
+            ss += x[i].w;
+        }
+        sh.scal[2] = 1.f / sqrtf(ss / float(kGdnDim) + a.eps);
+    }
+    __syncthreads();
+    if (owner) {
+        const float out = (gamma * o * sh.scal[2]) * silu_f32(z);
+        const int64_t width = int64_t(a.Hv) * kGdnDim;
+        const int64_t idx = int64_t(h) * kGdnDim + j;
+        if (a.out_f32) a.out_f32[int64_t(b) * width + idx] = out;
+        gdn_quantize(out, b, a.B, width, idx, j, a.act_out);
+    }
 }
 
 // ---- prefill: tokens t = 0..T-1 of one sequence at positions pos0 + t -------------
@@ -814,15 +856,16 @@ __global__ __launch_bounds__(256) void gdn_hist_kernel(const float* __restrict__
 
 void launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t s) {
     const dim3 grid(unsigned(a.Hv), unsigned(a.B));
+    const size_t sm = sizeof(GdnDecodeShared);
     switch (a.W) {
-        case 1: hipLaunchKernelGGL(gdn_decode_kernel<1>, grid, dim3(kGdnDim), kGdnShared, s, a); break;
-        case 2: hipLaunchKernelGGL(gdn_decode_kernel<2>, grid, dim3(kGdnDim), kGdnShared, s, a); break;
-        case 3: hipLaunchKernelGGL(gdn_decode_kernel<3>, grid, dim3(kGdnDim), kGdnShared, s, a); break;
-        case 4: hipLaunchKernelGGL(gdn_decode_kernel<4>, grid, dim3(kGdnDim), kGdnShared, s, a); break;
-        case 5: hipLaunchKernelGGL(gdn_decode_kernel<5>, grid, dim3(kGdnDim), kGdnShared, s, a); break;
-        case 6: hipLaunchKernelGGL(gdn_decode_kernel<6>, grid, dim3(kGdnDim), kGdnShared, s, a); break;
-        case 7: hipLaunchKernelGGL(gdn_decode_kernel<7>, grid, dim3(kGdnDim), kGdnShared, s, a); break;
-        default: hipLaunchKernelGGL(gdn_decode_kernel<8>, grid, dim3(kGdnDim), kGdnShared, s, a); break;
+        case 1: hipLaunchKernelGGL(gdn_decode_kernel<1>, grid, dim3(kGdnThreads), sm, s, a); break;
+        case 2: hipLaunchKernelGGL(gdn_decode_kernel<2>, grid, dim3(kGdnThreads), sm, s, a); break;
+        case 3: hipLaunchKernelGGL(gdn_decode_kernel<3>, grid, dim3(kGdnThreads), sm, s, a); break;
+        case 4: hipLaunchKernelGGL(gdn_decode_kernel<4>, grid, dim3(kGdnThreads), sm, s, a); break;
+        case 5: hipLaunchKernelGGL(gdn_decode_kernel<5>, grid, dim3(kGdnThreads), sm, s, a); break;
+        case 6: hipLaunchKernelGGL(gdn_decode_kernel<6>, grid, dim3(kGdnThreads), sm, s, a); break;
+        case 7: hipLaunchKernelGGL(gdn_decode_kernel<7>, grid, dim3(kGdnThreads), sm, s, a); break;
+        default: hipLaunchKernelGGL(gdn_decode_kernel<8>, grid, dim3(kGdnThreads), sm, s, a); break;
     }
 }
 

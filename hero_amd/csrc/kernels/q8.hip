@@ -80,8 +80,9 @@ void launch_pack_q8(const void* gguf_blocks, void* packed, int64_t N_total, int6
 //
 // A fixed grid of workgroups (one or two per CU) each owns a contiguous range
 // of whole 8-row groups, so every workgroup moves the same bytes and there is
-// no tail of late workgroups. Lane t always handles the K-chunks t + 256m
-// (m < CPL = K/4096), so its x chunks and act scales stay in registers. Rows
+// no tail of late workgroups. A workgroup has K/16 lanes (LG = K/4096 groups
+// of 256) and lane t always handles the 16-byte K-chunk t of every row, so its
+// x chunk and act scale stay in registers. Rows
 // are processed 8 at a time (a sub-batch) through a ring of D sub-batches of
 // weight and scale registers, refilled as soon as a sub-batch is consumed, so
 // loads stay in flight while the lanes compute. Each pair of lanes forms a
@@ -101,9 +102,10 @@ void launch_pack_q8(const void* gguf_blocks, void* packed, int64_t N_total, int6
 // ---------------------------------------------------------------------------
 constexpr int kStreamRB = 8;  // rows per sub-batch
 
-template <int CPL, int D, int EPI, int XM>
-__global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, GemvInput in, float* __restrict__ y, const float* __restrict__ resid, int N, int Npad, int TR) {
-    constexpr int K = 4096 * CPL, nb = K / 32, ts = nb + 4;  // ts: padded term row (conflict-free 16-byte reads)
+template <int LG, int D, int EPI, int XM>
+__global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, GemvInput in, float* __restrict__ y, const float* __restrict__ resid, int N, int Npad, int TR) {
+    constexpr int K = 4096 * LG, nb = K / 32, ts = nb + 4;  // ts: padded term row (conflict-free 16-byte reads)
+    constexpr int CPL = 1;  // K-chunks per lane
     // row ranges in whole units: 8-row groups, or for the SwiGLU epilogue
     // 64-row groups of [32 gate rows | 32 up rows]
     constexpr int UR = EPI == kEpiSwigluQuant ? 64 : 8;
@@ -129,15 +131,15 @@ __global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __res
         const uint32_t row0 = uint32_t(j * kStreamRB);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int m = 0; m < CPL; ++m)  // the group's 8 scales of block (tid + 256m) / 2
-            sdst[m] = load_b128(bd, even ? (uint32_t(j) * uint32_t(nb) + uint32_t((tid + 256 * m) >> 1)) * 16u : kOOB);
+        for (int m = 0; m < CPL; ++m)  // the group's 8 scales of block tid / 2
+            sdst[m] = load_b128(bd, even ? (uint32_t(j) * uint32_t(nb) + uint32_t(tid >> 1)) * 16u : kOOB);
 #pragma unroll
         for (int r = 0; r < kStreamRB; ++r)
 #pragma unroll
-            for (int m = 0; m < CPL; ++m) dst[r][m] = load_b128(bw, (row0 + uint32_t(r)) * uint32_t(K) + uint32_t(tid + 256 * m) * 16u);
+            for (int m = 0; m < CPL; ++m) dst[r][m] = load_b128(bw, (row0 + uint32_t(r)) * uint32_t(K) + uint32_t(tid) * 16u);
         __builtin_amdgcn_sched_barrier(0);
     };
-    // The lane's x chunks (tid + 256m) as Q8_0, and the residual of the first
+    // The lane's x chunk tid as Q8_0, and the residual of the first
     // chain pass. Their global reads are issued before the weight ring's:
     // loads retire in order, so a read issued after the ring would wait for
     // every weight in flight.
@@ -148,12 +150,12 @@ __global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __res
     if constexpr (XM == kInAct) {
 #pragma unroll
         for (int m = 0; m < CPL; ++m) {
-            const int c = tid + 256 * m;
+            const int c = tid;
             xv[m] = reinterpret_cast<const int4*>(in.xq)[c];
             dx[m] = in.xd[c >> 1];
         }
     } else if constexpr (XM == kInRmsNorm) {
-        static_assert(CPL == 1, "RMSNorm input needs K == 4096");
+        static_assert(LG == 1, "RMSNorm input needs K == 4096");
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const float4 a = reinterpret_cast<const float4*>(in.x)[4 * tid + k];
@@ -164,7 +166,7 @@ __global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __res
     } else {
 #pragma unroll
         for (int m = 0; m < CPL; ++m) {
-            const int c = tid + 256 * m;
+            const int c = tid;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 gv[m][k] = reinterpret_cast<const float4*>(in.gate_up)[4 * c + k];
@@ -238,7 +240,7 @@ __global__ __launch_bounds__(256) void gemv_q8_stream_kernel(const int8_t* __res
                         const int4 sc = sring[s][m];
                         const uint32_t two = uint32_t(pair == 0 ? sc.x : pair == 1 ? sc.y : pair == 2 ? sc.z : sc.w);
                         const uint16_t h = uint16_t((r & 1) ? (two >> 16) : (two & 0xFFFFu));
-                        terms[(rb + r - chain_row0) * ts + ((tid + 256 * m) >> 1)] = float(v) * (half_bits_to_f32(h) * dx[m]);
+                        terms[(rb + r - chain_row0) * ts + (tid >> 1)] = float(v) * (half_bits_to_f32(h) * dx[m]);
                     }
                 }
             }
@@ -386,30 +388,31 @@ int device_cus() {
 
 namespace {
 
-template <int CPL, int D, int XM>
+template <int LG, int D, int XM>
 void stream_dispatch(int epi, const int8_t* wq, const uint16_t* wd, const GemvInput& in, float* y, const float* resid, int N, int Npad, int G, int TR, size_t smem, hipStream_t s) {
+    const dim3 block(256 * LG);
     if (epi == kEpiResidual)
-        hipLaunchKernelGGL((gemv_q8_stream_kernel<CPL, D, kEpiResidual, XM>), dim3(unsigned(G)), dim3(256), smem, s, wq, wd, in, y, resid, N, Npad, TR);
-    else if constexpr (CPL == 1)
+        hipLaunchKernelGGL((gemv_q8_stream_kernel<LG, D, kEpiResidual, XM>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
+    else if constexpr (LG == 1)
         if (epi == kEpiSwigluQuant)
-            hipLaunchKernelGGL((gemv_q8_stream_kernel<CPL, D, kEpiSwigluQuant, XM>), dim3(unsigned(G)), dim3(256), smem, s, wq, wd, in, y, resid, N, Npad, TR);
+            hipLaunchKernelGGL((gemv_q8_stream_kernel<LG, D, kEpiSwigluQuant, XM>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
         else
-            hipLaunchKernelGGL((gemv_q8_stream_kernel<CPL, D, kEpiStore, XM>), dim3(unsigned(G)), dim3(256), smem, s, wq, wd, in, y, resid, N, Npad, TR);
+            hipLaunchKernelGGL((gemv_q8_stream_kernel<LG, D, kEpiStore, XM>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
     else
-        hipLaunchKernelGGL((gemv_q8_stream_kernel<CPL, D, kEpiStore, XM>), dim3(unsigned(G)), dim3(256), smem, s, wq, wd, in, y, resid, N, Npad, TR);
+        hipLaunchKernelGGL((gemv_q8_stream_kernel<LG, D, kEpiStore, XM>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
 }
 
-template <int CPL, int D>
+template <int LG, int D>
 void stream_dispatch_in(int epi, const int8_t* wq, const uint16_t* wd, const GemvInput& in, float* y, const float* resid, int N, int Npad, int G, int TR, size_t smem, hipStream_t s) {
     if (in.mode == kInSwiglu)
-        stream_dispatch<CPL, D, kInSwiglu>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
-    else if constexpr (CPL == 1)
+        stream_dispatch<LG, D, kInSwiglu>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
+    else if constexpr (LG == 1)
         if (in.mode == kInRmsNorm)
-            stream_dispatch<CPL, D, kInRmsNorm>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
+            stream_dispatch<LG, D, kInRmsNorm>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
         else
-            stream_dispatch<CPL, D, kInAct>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
+            stream_dispatch<LG, D, kInAct>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
     else
-        stream_dispatch<CPL, D, kInAct>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
+        stream_dispatch<LG, D, kInAct>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
 }
 
 template <int IPT>
@@ -441,6 +444,8 @@ void launch_gemv_q8_in(const void* packed, const GemvInput& in, float* y, const 
     size_t smem = size_t(TR) * (nb + 4) * 4;
     if (in.mode == kInRmsNorm) smem = std::max(smem, size_t(K) * 4);  // the squares
     switch (K / 4096) {
+        // a ring of two 8-row sub-batches: deeper rings only add padding
+        // sub-batches where a workgroup has few rows
         case 1: stream_dispatch_in<1, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
         case 2: stream_dispatch_in<2, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
         default: stream_dispatch_in<3, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;

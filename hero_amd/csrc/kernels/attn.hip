@@ -182,31 +182,32 @@ __global__ __launch_bounds__(seqsum::kThreads) void attn_softmax_kernel(AttnDeco
 // out[c] = sum_j alpha_j * v_j[c] with the rows in order (core.hpp:206-208).
 // A workgroup per (sequence, query head, 32 channels = one Q8_0 block of the
 // output), in tiles of kPvRows rows, with three roles:
-//  * wave 3 streams the V rows and alpha values of the tiles straight into a
-//    ring of kPvRing shared-memory slots (global_load_lds: the same nine
-//    loads per lane every tile, so it waits for exactly its oldest tile);
+//  * waves 3..4 stream the V rows (32 each) and the alpha values (wave 4) of
+//    the tiles straight into a ring of R shared-memory slots (global_load_lds:
+//    the same loads per lane every tile, so each wave waits for exactly its
+//    oldest tile); R - 2 tiles stay in flight;
 //  * waves 1..2 form the products alpha_j * v_j[c] (the reference's product,
 //    one rounding) and store them transposed, [channel][row], into one of two
 //    product buffers;
 //  * lanes 0..31 of wave 0 each hold one channel's sum and only add, four
 //    products per 16-byte read, which is the dependent chain the reference's
 //    loop is.
-// One barrier per tile: after it the loader refills the freed slot, the
+// One barrier per tile: after it the loaders refill a freed slot, the
 // producers fill the next tile's products and the chain adds the current
 // tile's.
 constexpr int kPvCh = 32;                                   // channels per workgroup
 constexpr int kPvRows = 64;                                 // rows per tile
 constexpr int kPvStride = kPvRows + 4;                      // product row stride (conflict-free 16-byte reads)
-constexpr int kPvRing = 6;                                  // tiles of V and alpha in flight
-constexpr int kPvThreads = 256;                             // chain wave, two producer waves, loader wave
+constexpr int kPvThreads = 320;                             // chain wave, two producer waves, two loader waves
 constexpr int kPvVTile = kPvRows * kPvCh;                   // floats of V per tile
-constexpr int kPvVLoads = kPvVTile / 4 / 64;                // 16-byte V loads per loader lane per tile: 8
-constexpr int kPvLoads = kPvVLoads + 1;                     // plus one alpha value
-constexpr size_t kPvShared = (size_t(kPvRing) * (kPvVTile + kPvRows) + size_t(2) * kPvCh * kPvStride) * 4;
-static_assert(kPvVLoads == 8 && kPvRows == 64 && kPvCh * kPvRows / 4 / 4 == 128, "tile geometry");
+constexpr int kPvVLoads = kPvVTile / 4 / 128;               // 16-byte V loads per loader lane per tile: 4
+static_assert(kPvVLoads == 4 && kPvRows == 64 && kPvCh * kPvRows / 4 / 4 == 128, "tile geometry");
+constexpr size_t pv_shared_bytes(int R) { return (size_t(R) * (kPvVTile + kPvRows) + size_t(2) * kPvCh * kPvStride) * 4; }
 
+template <int R>
 __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(AttnDecodeArgs a) {
-    extern __shared__ __align__(16) float pv_smem[];  // [kPvRing][V tile] [kPvRing][alpha tile] [2][kPvCh][kPvStride]
+    static_assert(R >= 4 && (R - 2) * (kPvVLoads + 1) <= 63, "the oldest tile's wait count fits vmcnt");
+    extern __shared__ __align__(16) float pv_smem[];  // [R][V tile] [R][alpha tile] [2][kPvCh][kPvStride]
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64, b = blockIdx.y;
     constexpr int parts = kAttnDim / kPvCh;
     const int h = int(blockIdx.x) / parts, part = int(blockIdx.x) % parts;
@@ -220,25 +221,38 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(AttnDecodeArgs a) {
     const float* vb = a.v_cache + (cache_of(a, b) * a.max_ctx + first) * kw + int64_t(g) * kAttnDim + part * kPvCh;
     const int ntiles = (n + kPvRows - 1) / kPvRows;
     float* vring = pv_smem;
-    float* aring = vring + kPvRing * kPvVTile;
-    float* prod = aring + kPvRing * kPvRows;
+    float* aring = vring + R * kPvVTile;
+    float* prod = aring + R * kPvRows;
     constexpr int pstride = kPvCh * kPvStride;
+    const bool loader = wave >= 3;
+    const int half = wave - 3;  // loader: V rows 32 half .. 32 half + 31
 
-    // loader: V rows (rows past n read row n - 1, whose products the chain
-    // never adds) and alpha values of a tile
+    // loaders: V rows (rows past n read row n - 1, whose products the chain
+    // never adds) and, on wave 4, the alpha values of a tile
     auto issue = [&](int tile) {
-        const int slot = tile % kPvRing;
+        const int slot = tile % R;
 #pragma unroll
         for (int j = 0; j < kPvVLoads; ++j) {
-            const int q = lane + 64 * j;  // 16-byte slot: row q / 8, channels 4 (q % 8) ..
+            const int q = half * 256 + lane + 64 * j;  // 16-byte slot: row q / 8, channels 4 (q % 8) ..
             const int row = min(tile * kPvRows + q / 8, n - 1);
-            lds_dma_b128(vb + int64_t(row) * kw + 4 * (q % 8), lds_offset(vring + slot * kPvVTile + 256 * j));
+            lds_dma_b128(vb + int64_t(row) * kw + 4 * (q % 8), lds_offset(vring + slot * kPvVTile + 4 * (half * 256 + 64 * j)));
         }
-        lds_dma_b32(alpha + min(tile * kPvRows + lane, n - 1), lds_offset(aring + slot * kPvRows));
+        if (half == 1) lds_dma_b32(alpha + min(tile * kPvRows + lane, n - 1), lds_offset(aring + slot * kPvRows));
+    };
+    // this loader wave's loads of tile t have landed, given how many tiles it issued after t
+    auto wait_tile = [&](bool full) {
+        if (full) {
+            if (half == 0)
+                wait_vmcnt<(R - 3) * kPvVLoads>();
+            else
+                wait_vmcnt<(R - 3) * (kPvVLoads + 1)>();
+        } else {
+            wait_vmcnt<0>();
+        }
     };
     // producers: channels c4 .. c4 + 3 and rows r4 .. r4 + 3 of a tile
     auto produce = [&](int tile) {
-        const int slot = tile % kPvRing;
+        const int slot = tile % R;
         const int c4 = (lane % 8) * 4, r4 = ((wave - 1) * 8 + lane / 8) * 4;
         const float* vt = vring + slot * kPvVTile;
         float4 v[4];
@@ -252,28 +266,29 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(AttnDecodeArgs a) {
         reinterpret_cast<float4*>(d + 3 * kPvStride)[0] = make_float4(al.x * v[0].w, al.y * v[1].w, al.z * v[2].w, al.w * v[3].w);
     };
 
-    if (wave == 3) {
-        for (int t = 0; t < kPvRing; ++t)
+    // tiles 0 .. R-2 in flight before the loop; iteration t issues tile
+    // t + R - 1 into the slot of tile t - 1, whose products were formed two
+    // barriers earlier
+    if (loader) {
+        for (int t = 0; t + 1 < R; ++t)
             if (t < ntiles) issue(t);
-        if (ntiles >= kPvRing)
-            wait_vmcnt<(kPvRing - 1) * kPvLoads>();
-        else
+        if (ntiles >= R - 1) {
+            if (half == 0)
+                wait_vmcnt<(R - 2) * kPvVLoads>();
+            else
+                wait_vmcnt<(R - 2) * (kPvVLoads + 1)>();
+        } else {
             wait_vmcnt<0>();
+        }
     }
     __syncthreads();
     if (wave == 1 || wave == 2) produce(0);
     float acc = 0.f;
     for (int tile = 0; tile < ntiles; ++tile) {
-        if (wave == 3) {
-            // tile + 1 has landed
-            if (tile + kPvRing <= ntiles)
-                wait_vmcnt<(kPvRing - 2) * kPvLoads>();
-            else
-                wait_vmcnt<0>();
-        }
+        if (loader) wait_tile(tile + R - 1 <= ntiles);  // tile + 1 has landed
         __syncthreads();
-        if (wave == 3) {
-            if (tile + kPvRing < ntiles) issue(tile + kPvRing);  // into the slot of tile, whose products exist
+        if (loader) {
+            if (tile + R - 1 < ntiles) issue(tile + R - 1);
         } else if (wave > 0) {
             if (tile + 1 < ntiles) produce(tile + 1);  // the other buffer: its last reader was the chain before the barrier
         } else if (lane < kPvCh) {
@@ -620,9 +635,14 @@ void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
     const int group = a.Hq / a.Hkv;
     hipLaunchKernelGGL(attn_scores_kernel, dim3(unsigned(a.Hkv * ((group + kScoreHeads - 1) / kScoreHeads)), tiles, unsigned(a.B)), dim3(256), 0, s, a);
     hipLaunchKernelGGL(attn_softmax_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(seqsum::kThreads), 0, s, a);
-    // the per-head pipeline while its workgroups fit the CUs about twice over
-    if (int64_t(a.B) * a.Hq * (kAttnDim / kPvCh) <= 2 * device_cus())
-        hipLaunchKernelGGL(attn_pv_kernel, dim3(unsigned(a.Hq * (kAttnDim / kPvCh)), unsigned(a.B)), dim3(kPvThreads), kPvShared, s, a);
+    // the per-head pipeline while its workgroups fit the CUs (a deep ring, one
+    // workgroup per CU) or fit them twice over (a shallower ring)
+    const int64_t pv_blocks = int64_t(a.B) * a.Hq * (kAttnDim / kPvCh);
+    const dim3 pv_grid(unsigned(a.Hq * (kAttnDim / kPvCh)), unsigned(a.B));
+    if (pv_blocks <= device_cus())
+        hipLaunchKernelGGL(attn_pv_kernel<14>, pv_grid, dim3(kPvThreads), pv_shared_bytes(14), s, a);
+    else if (pv_blocks <= 2 * device_cus())
+        hipLaunchKernelGGL(attn_pv_kernel<7>, pv_grid, dim3(kPvThreads), pv_shared_bytes(7), s, a);
     else
         hipLaunchKernelGGL(attn_pv_batch_kernel, dim3(unsigned(a.Hq * kPvbSplit), unsigned(a.B)), dim3(kPvbThreads), 0, s, a);
 }

@@ -511,7 +511,8 @@ namespace hero {
 //
 // int8 MFMA v_mfma_i32_16x16x32_i8 with K = 32 gives exactly one Q8_0 block's
 // int32 sums for a 16x16 (m, n) tile (C zero per block); each lane then adds
-// float(sumi) * (d_w * d_x) to its fp32 accumulators, blocks in order.
+// float(sumi) * (d_w * d_x) to its fp32 accumulators, blocks in order. That
+// fp32 work (4 VALU operations per output and block) is the kernel's bound.
 // Lane layout (checked on the device): A lane l = row l%16, k bytes
 // 8*(l/16)..+7; B lane l = column l%16, the same k bytes; C lane l, register r
 // = row 4*(l/16)+r, column l%16.
@@ -519,7 +520,10 @@ namespace hero {
 // Workgroup: 256 lanes, a BM x 64 tile of Y; wave w owns columns 16w..16w+15
 // and all BM rows. K streams through shared memory 8 blocks (256 bytes) at a
 // time; tile rows are padded to 272 bytes (2-way bank conflicts on the 8-byte
-// operand reads).
+// operand reads). The next chunk's bytes and scales are loaded into registers
+// while the current chunk is computed (raw buffer loads sized to the tile, so
+// rows, blocks and scales past the edges read zeros without a branch), then
+// stored to shared memory between two barriers.
 // ---------------------------------------------------------------------------
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 constexpr int kGemmBN = 64, kGemmKC = 8, kGemmRow = kGemmKC * 32 + 16;
@@ -528,42 +532,85 @@ template <int BM, int EPI>
 __global__ __launch_bounds__(256) void gemm_q8_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {
     __shared__ __align__(16) int8_t Xs[BM * kGemmRow];
     __shared__ __align__(16) int8_t Ws[kGemmBN * kGemmRow];
-    __shared__ float dxs[BM][kGemmKC];
+    __shared__ __align__(16) float dxs[kGemmKC][BM];  // [block][row]: a lane's 4 rows are one 16-byte read
     __shared__ float dws[kGemmKC][kGemmBN];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int n0 = blockIdx.x * kGemmBN, m0 = blockIdx.y * BM;
     const int nb = K >> 5;
-    constexpr int MT = BM / 16;  // m sub-tiles per wave
+    const int mrows = min(BM, M - m0), nrows = min(kGemmBN, N - n0);
+    constexpr int MT = BM / 16;                    // m sub-tiles per wave
+    constexpr int XP = BM * 16 / 256;              // 16-byte X pieces per lane per chunk
+    constexpr int WP = kGemmBN * 16 / 256;         // 16-byte W pieces per lane per chunk: 4
+    constexpr int DXP = (BM * kGemmKC + 255) / 256;
+    constexpr int DWP = kGemmKC * kGemmBN / 256;   // 2
+    // the tile's rows of X and W, their scales (n0 is a multiple of 8, so the
+    // scale groups of W rows n0.. are contiguous)
+    const __amdgpu_buffer_rsrc_t bx = buffer_of(xq + int64_t(m0) * K, uint32_t(mrows) * uint32_t(K));
+    const __amdgpu_buffer_rsrc_t bw = buffer_of(wq + int64_t(n0) * K, uint32_t(nrows) * uint32_t(K));
+    const __amdgpu_buffer_rsrc_t bdx = buffer_of(xd + int64_t(m0) * nb, uint32_t(mrows) * uint32_t(nb) * 4u);
+    const __amdgpu_buffer_rsrc_t bdw = buffer_of(wd + scale_index(n0, 0, nb), uint32_t((min(kGemmBN, Npad - n0) + 7) / 8) * uint32_t(nb) * 16u);
     float acc[MT][4];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[i][r] = 0.f;
 
+    int4 xr[XP], wr[WP];
+    float dxr[DXP], dwr[DWP];
+    // chunk b0's bytes (16-byte piece c < 2*kc of each row) and scales into registers
+    auto fetch = [&](int b0) {
+        const int kc = min(kGemmKC, nb - b0);
+#pragma unroll
+        for (int q = 0; q < XP; ++q) {
+            const int e = tid + 256 * q, r = e >> 4, c = e & 15;
+            xr[q] = load_b128(bx, c < 2 * kc ? uint32_t(r) * uint32_t(K) + uint32_t(b0) * 32u + uint32_t(c) * 16u : kOOB);
+        }
+#pragma unroll
+        for (int q = 0; q < WP; ++q) {
+            const int e = tid + 256 * q, r = e >> 4, c = e & 15;
+            wr[q] = load_b128(bw, c < 2 * kc ? uint32_t(r) * uint32_t(K) + uint32_t(b0) * 32u + uint32_t(c) * 16u : kOOB);
+        }
+#pragma unroll
+        for (int q = 0; q < DXP; ++q) {
+            const int e = tid + 256 * q, r = e / kGemmKC, bb = e % kGemmKC;
+            dxr[q] = load_f32(bdx, e < BM * kGemmKC && bb < kc ? (uint32_t(r) * uint32_t(nb) + uint32_t(b0 + bb)) * 4u : kOOB);
+        }
+#pragma unroll
+        for (int q = 0; q < DWP; ++q) {
+            const int e = tid + 256 * q, bb = e / kGemmBN, c = e % kGemmBN;
+            const uint32_t off = (uint32_t(c >> 3) * uint32_t(nb) + uint32_t(b0 + bb)) * 16u + uint32_t(c & 7) * 2u;
+            dwr[q] = half_bits_to_f32(uint16_t(__builtin_amdgcn_raw_buffer_load_b16(bdw, bb < kc ? off : kOOB, 0, 0)));
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int q = 0; q < XP; ++q) {
+            const int e = tid + 256 * q;
+            *reinterpret_cast<int4*>(Xs + (e >> 4) * kGemmRow + (e & 15) * 16) = xr[q];
+        }
+#pragma unroll
+        for (int q = 0; q < WP; ++q) {
+            const int e = tid + 256 * q;
+            *reinterpret_cast<int4*>(Ws + (e >> 4) * kGemmRow + (e & 15) * 16) = wr[q];
+        }
+#pragma unroll
+        for (int q = 0; q < DXP; ++q) {
+            const int e = tid + 256 * q;
+            if (e < BM * kGemmKC) dxs[e % kGemmKC][e / kGemmKC] = dxr[q];
+        }
+#pragma unroll
+        for (int q = 0; q < DWP; ++q) {
+            const int e = tid + 256 * q;
+            dws[e / kGemmBN][e % kGemmBN] = dwr[q];
+        }
+    };
+
+    fetch(0);
     for (int b0 = 0; b0 < nb; b0 += kGemmKC) {
         const int kc = min(kGemmKC, nb - b0);  // blocks in this chunk
-        // stage X (BM rows) and W (64 rows) of this chunk: 16-byte pieces
-        for (int e = tid; e < BM * 16; e += 256) {
-            const int r = e >> 4, c = e & 15;
-            int4 v = make_int4(0, 0, 0, 0);
-            if (m0 + r < M && c < 2 * kc) v = reinterpret_cast<const int4*>(xq + int64_t(m0 + r) * K + int64_t(b0) * 32)[c];
-            *reinterpret_cast<int4*>(Xs + r * kGemmRow + c * 16) = v;
-        }
-        for (int e = tid; e < kGemmBN * 16; e += 256) {
-            const int r = e >> 4, c = e & 15;
-            int4 v = make_int4(0, 0, 0, 0);
-            if (n0 + r < N && c < 2 * kc) v = reinterpret_cast<const int4*>(wq + int64_t(n0 + r) * K + int64_t(b0) * 32)[c];
-            *reinterpret_cast<int4*>(Ws + r * kGemmRow + c * 16) = v;
-        }
-        for (int e = tid; e < BM * kGemmKC; e += 256) {
-            const int r = e / kGemmKC, bb = e % kGemmKC;
-            dxs[r][bb] = (m0 + r < M && bb < kc) ? xd[int64_t(m0 + r) * nb + b0 + bb] : 0.f;
-        }
-        for (int e = tid; e < kGemmKC * kGemmBN; e += 256) {
-            const int bb = e / kGemmBN, c = e % kGemmBN;
-            dws[bb][c] = (n0 + c < N && bb < kc) ? half_bits_to_f32(wd[scale_index(n0 + c, b0 + bb, nb)]) : 0.f;
-        }
+        stage();
         __syncthreads();
+        if (b0 + kGemmKC < nb) fetch(b0 + kGemmKC);  // in flight during this chunk's compute
         const int n_l = 16 * w + (lane & 15);
         for (int bb = 0; bb < kc; ++bb) {
             const int koff = bb * 32 + (lane >> 4) * 8;
@@ -574,11 +621,11 @@ __global__ __launch_bounds__(256) void gemm_q8_kernel(const int8_t* __restrict__
                 const long aop = *reinterpret_cast<const long*>(Xs + (16 * i + (lane & 15)) * kGemmRow + koff);
                 const v4i_t zero = {0, 0, 0, 0};
                 const v4i_t c = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, zero, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int m_l = 16 * i + (lane >> 4) * 4 + r;
-                    acc[i][r] = acc[i][r] + float(c[r]) * (dw * dxs[m_l][bb]);
-                }
+                const float4 dx4 = *reinterpret_cast<const float4*>(&dxs[bb][16 * i + (lane >> 4) * 4]);
+                acc[i][0] = acc[i][0] + float(c[0]) * (dw * dx4.x);
+                acc[i][1] = acc[i][1] + float(c[1]) * (dw * dx4.y);
+                acc[i][2] = acc[i][2] + float(c[2]) * (dw * dx4.z);
+                acc[i][3] = acc[i][3] + float(c[3]) * (dw * dx4.w);
             }
         }
         __syncthreads();
@@ -777,12 +824,20 @@ void launch_gemm_q8(const void* packed, const void* act, float* y, const float* 
             hipLaunchKernelGGL(gemm_q8_skinny_kernel<kEpiResidual>, dim3(G), dim3(256), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
         else
             hipLaunchKernelGGL(gemm_q8_skinny_kernel<kEpiStore>, dim3(G), dim3(256), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
-    } else if (M <= 16)
-        gemm_dispatch<16>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s);
-    else if (M <= 32)
-        gemm_dispatch<32>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s);
-    else
-        gemm_dispatch<64>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s);
+    } else {
+        // the tallest tile that still gives every CU two workgroups (the fp32
+        // term work per CU is the same; more workgroups hide more latency)
+        const int64_t tiles_n = (N + kGemmBN - 1) / kGemmBN, want = 2 * device_cus();
+        auto grid_of = [&](int64_t bm) { return tiles_n * ((M + bm - 1) / bm); };
+        if (M > 64 && grid_of(128) >= want)
+            gemm_dispatch<128>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s);
+        else if (M > 32 && grid_of(64) >= want)
+            gemm_dispatch<64>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s);
+        else if (M > 16 && grid_of(32) >= want)
+            gemm_dispatch<32>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s);
+        else
+            gemm_dispatch<16>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s);
+    }
 }
 
 }  // namespace hero

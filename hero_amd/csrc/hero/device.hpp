@@ -76,6 +76,22 @@ __device__ __forceinline__ void lds_dma_b32(const void* g, uint32_t lds_base) {
                  : "=&s"(saved) : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_base)) : "memory");
 }
 
+// Sixteen 16-byte shared-memory reads (256 consecutive bytes from lds_addr)
+// the compiler does not track (inline assembly): the results may only be used
+// after a barrier or an explicit lgkmcnt wait. For reads issued one pipeline
+// step ahead of their use, where the compiler's own counted waits would hold
+// the current step's work until they land.
+__device__ __forceinline__ void lds_read_b128x16_untracked(uint32_t lds_addr, float4 (&dst)[16]) {
+    typedef float v4f_t __attribute__((ext_vector_type(4)));
+    v4f_t v[16];
+#define HERO_LDS_RD(i) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v[i]) : "v"(lds_addr), "i"(16 * (i)) : "memory")
+    HERO_LDS_RD(0); HERO_LDS_RD(1); HERO_LDS_RD(2); HERO_LDS_RD(3); HERO_LDS_RD(4); HERO_LDS_RD(5); HERO_LDS_RD(6); HERO_LDS_RD(7);
+    HERO_LDS_RD(8); HERO_LDS_RD(9); HERO_LDS_RD(10); HERO_LDS_RD(11); HERO_LDS_RD(12); HERO_LDS_RD(13); HERO_LDS_RD(14); HERO_LDS_RD(15);
+#undef HERO_LDS_RD
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dst[i] = make_float4(v[i].x, v[i].y, v[i].z, v[i].w);
+}
+
 // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and
 // lgkmcnt left at their maxima, i.e. not waited for): at most N vector memory
 // operations of this wave still outstanding.

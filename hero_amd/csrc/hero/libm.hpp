@@ -58,7 +58,11 @@ __host__ __device__ inline uint64_t exp2_table(int i) {
     return t[i];
 }
 
-__host__ __device__ inline float expf_glibc(float x) {
+// `tab(i)` returns exp2_table(i); kernels that cannot afford a global-memory
+// read per call (one in flight behind other loads waits for all of them) pass
+// a copy of the table held in shared memory
+template <class Tab>
+__host__ __device__ inline float expf_glibc_with(float x, const Tab& tab) {
     const uint32_t ix = f32_bits(x);
     const uint32_t abstop = (ix >> 20) & 0x7ff;
     if (abstop >= 0x42b) {  // |x| >= 88, inf or nan
@@ -76,13 +80,17 @@ __host__ __device__ inline float expf_glibc(float x) {
     const uint64_t ki = f64_bits(kd);
     kd -= shift;
     const double r = ::fma(inv_ln2_n, xd, -kd);
-    const double s = bits_f64(exp2_table(int(ki % 32)) + (ki << 47));
+    const double s = bits_f64(tab(int(ki % 32)) + (ki << 47));
     const double p = c0 * r + c1;
     const double r2 = r * r;
     double y = c2 * r + 1.0;
     y = p * r2 + y;
     y = y * s;
     return float(y);
+}
+
+__host__ __device__ inline float expf_glibc(float x) {
+    return expf_glibc_with(x, [](int i) { return exp2_table(i); });
 }
 
 __host__ __device__ inline float log1pf_glibc(float x) {

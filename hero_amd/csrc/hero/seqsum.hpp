@@ -1,6 +1,6 @@
 // seqsum.hpp -- the sequential fp32 sum of n >= 0 terms,
 //     s = 0; for i in 0..n-1: s = fl(s + p[i])
-// computed by a workgroup of 1024 or 256 lanes, bit-identical to the loop.
+// computed by a workgroup of 1024, 512 or 256 lanes, bit-identical to the loop.
 //
 // The reference's RMSNorm and L2 norms sum squares in index order
 // (nm/src/core.hpp:496-500) and its softmax sums exponentials in index order
@@ -54,8 +54,8 @@
 namespace hero {
 namespace seqsum {
 
-// Workgroups of 1024 lanes (4 elements each) or 256 lanes (16 each); both sum
-// up to 4096 terms. The 1024-lane form is the faster; the 256-lane form runs
+// Workgroups of 1024, 512 or 256 lanes (4, 8 or 16 elements each); all sum up
+// to 4096 terms. The 1024-lane form is the fastest; the smaller forms run
 // inside other kernels' workgroups.
 constexpr int kThreads = 1024;  // the default workgroup
 constexpr int kWaveSize = 64;
@@ -296,7 +296,7 @@ __device__ inline uint32_t scan_u32(uint32_t v) {
 // the result; there is no barrier at the end unless the fallback ran.
 template <int NT>
 __device__ inline float sum_lanes(Lane<kMaxN / NT>& L, const float* p, int n, Shared& sm) {
-    static_assert(NT == 256 || NT == 1024, "256 or 1024 lanes");
+    static_assert(NT == 256 || NT == 512 || NT == 1024, "256, 512 or 1024 lanes");
     constexpr int PT = kMaxN / NT, W = NT / kWaveSize, cap = kMaxSerial / W;
     if (n <= 0) return 0.f;
     const int tid = int(threadIdx.x), lane = tid & (kWaveSize - 1), w = tid / kWaveSize;

@@ -329,6 +329,246 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(AttnDecodeArgs a) {
     }
 }
 
+// ---- 3+4 fused: softmax and weighted sum ------------------------------------------------------
+// For up to 4096 visible keys, one workgroup per (sequence, query head, 32
+// channels) runs the softmax of its head itself and then the weighted sum, so
+// the V stream starts at once and the weights never leave shared memory.
+// Eight waves:
+//  * all copy the head's scores into shared memory (global_load_lds); waves
+//    4-7 (the loaders) then put the whole V ring in flight;
+//  * max; e_j = exp(s_j - max), lane t taking j = t, t + 512, ...; the total
+//    as the exact sequential sum (hero/seqsum.hpp, 512 lanes); alpha_j =
+//    e_j / total -- the operations of attn_softmax_kernel;
+//  * the weighted sum as a pipeline of 64-row tiles with one barrier per tile:
+//    the loaders stream V tiles into a ring of R slots (global_load_lds, two
+//    16-byte loads per lane per tile, each tile's chunks placed so the
+//    producers' reads are conflict-free), waves 1-2 form the products
+//    alpha_j * v_j[c] of tile t + 2 from registers read during the previous
+//    tile, and wave 0 adds tile t from registers while it reads tile t + 1's
+//    products (a 3-slot product ring). Lanes 0-31 of wave 0 run the chains
+//    (one per channel, rows in order); wave 3 only keeps the barriers.
+constexpr int kSpvThreads = 512;
+constexpr int kSpvMaxN = seqsum::kMaxN;        // visible keys at most
+constexpr int kSpvR = 13;                      // V ring slots
+constexpr int kSpvLoaders = 4;                 // waves 4 .. 7
+constexpr int kSpvVLoads = kPvVTile / 4 / 64 / kSpvLoaders;  // 16-byte V loads per loader lane per tile: 2
+constexpr int kSpvAhead = 4;                   // the tile the loaders wait for: t + 4 at the end of iteration t
+static_assert(kSpvVLoads == 2 && 2 + kSpvR * kSpvVLoads <= 63, "vmcnt range");
+constexpr size_t spv_shared_bytes() {
+    return (size_t(kSpvR) * kPvVTile + size_t(3) * kPvCh * kPvStride + kSpvMaxN) * 4 + sizeof(seqsum::Shared) + 32 + 32 * 8;
+}
+// 16-byte chunk cc (4 channels) of V row r sits at chunk r * 8 + (cc ^ spv_swz(r)) of its slot
+__device__ __forceinline__ int spv_swz(int r) { return (r >> 2) & 7; }
+
+__global__ __launch_bounds__(kSpvThreads) void attn_softmax_pv_kernel(AttnDecodeArgs a) {
+    extern __shared__ __align__(16) float spv_smem[];  // [R][V tile] [3][kPvCh][kPvStride] [kSpvMaxN] seqsum red etab
+    float* vring = spv_smem;
+    float* prod = vring + kSpvR * kPvVTile;
+    float* al = prod + 3 * kPvCh * kPvStride;
+    seqsum::Shared& sm = *reinterpret_cast<seqsum::Shared*>(al + kSpvMaxN);
+    float* red = reinterpret_cast<float*>(&sm + 1);         // [8]
+    uint64_t* etab = reinterpret_cast<uint64_t*>(red + 8);  // expf's table, read from shared memory
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64, b = blockIdx.y;
+    constexpr int parts = kAttnDim / kPvCh;
+    const int h = int(blockIdx.x) / parts, part = int(blockIdx.x) % parts;
+    const int g = h / (a.Hq / a.Hkv);
+    const int pos = a.positions[b];
+    if (pos < 0 || pos >= a.max_ctx) return;
+    const int first = visible_first(pos, a.window);
+    const int n = pos + 1 - first;  // <= kSpvMaxN (the host's condition for this kernel)
+    const float* sc = a.scores + (int64_t(b) * a.Hq + h) * a.max_ctx;
+    const int64_t kw = int64_t(a.Hkv) * kAttnDim;
+    const float* vb = a.v_cache + (cache_of(a, b) * a.max_ctx + first) * kw + int64_t(g) * kAttnDim + part * kPvCh;
+    const int ntiles = (n + kPvRows - 1) / kPvRows;
+    constexpr int pstride = kPvCh * kPvStride;
+    const bool loader = wave >= 8 - kSpvLoaders;
+    const int li = wave - (8 - kSpvLoaders);
+
+    // V tile `tile` into its slot: loader li's load j fills chunk
+    // p = 64 (kSpvVLoads li + j) + lane, i.e. row p / 8 and channel chunk
+    // (p % 8) ^ spv_swz(row); rows past n read row n - 1, whose products the
+    // chain never adds
+    auto issue = [&](int tile) {
+        float* slot = vring + (tile % kSpvR) * kPvVTile;
+#pragma unroll
+        for (int j = 0; j < kSpvVLoads; ++j) {
+            const int c0 = 64 * (kSpvVLoads * li + j), p = c0 + lane, r = p / 8;
+            const int row = min(tile * kPvRows + r, n - 1);
+            lds_dma_b128(vb + int64_t(row) * kw + 4 * ((p % 8) ^ spv_swz(r)), lds_offset(slot + 4 * c0));
+        }
+    };
+
+    // ---- the scores into shared memory: chunk q = 4 consecutive scores;
+    // chunks past the visible ones read the last visible chunk (never used) ----
+    if (tid < 32) etab[tid] = exp2_table(tid);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int q = min(wave * 128 + k * 64 + lane, (n - 1) / 4);
+        lds_dma_b128(sc + 4 * q, lds_offset(al + 4 * (wave * 128 + k * 64)));
+    }
+    if (loader) {
+        for (int t = 0; t < kSpvR; ++t)
+            if (t < ntiles) issue(t);
+        if (ntiles >= kSpvR)
+            wait_vmcnt<kSpvR * kSpvVLoads>();  // the scores have landed
+        else
+            wait_vmcnt<0>();
+    } else {
+        wait_vmcnt<0>();
+    }
+    __syncthreads();
+
+    // ---- softmax (nm/src/components.hpp:132-141) ----
+    float s[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const int j = tid + kSpvThreads * m;
+        s[m] = al[j];
+        if (j < n) mx = fmaxf(mx, s[m]);
+    }
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) mx = fmaxf(mx, red[w]);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const int j = tid + kSpvThreads * m;
+        if (j < n) al[j] = expf_glibc_with(s[m] - mx, [etab](int i) { return etab[i]; });
+    }
+    __syncthreads();
+    const float total = seqsum::sum_nonneg<kSpvThreads>(al, n, sm);  // every wave gets the total
+    // alpha over the terms (zero past n, up to the last tile's end): no wave
+    // reads the terms after the sum unless it fell back to the plain loop,
+    // which ends with a barrier
+    {
+        const int j0 = 8 * tid;
+#pragma unroll
+        for (int k = 0; k < 8; k += 4) {
+            float4 e4 = reinterpret_cast<const float4*>(al + j0)[k / 4];
+            e4.x = j0 + k < n ? e4.x / total : 0.f;
+            e4.y = j0 + k + 1 < n ? e4.y / total : 0.f;
+            e4.z = j0 + k + 2 < n ? e4.z / total : 0.f;
+            e4.w = j0 + k + 3 < n ? e4.w / total : 0.f;
+            reinterpret_cast<float4*>(al + j0)[k / 4] = e4;
+        }
+    }
+
+    // ---- the weighted sum (core.hpp:206-208) ----
+    // tiles 0 .. 3 have landed: after them at most tiles 4 .. R - 1 are in flight
+    if (loader) {
+        if (ntiles >= kSpvR)
+            wait_vmcnt<(kSpvR - kSpvAhead) * kSpvVLoads>();
+        else
+            wait_vmcnt<0>();
+    }
+    __syncthreads();
+    // producers: channels c4 .. c4 + 3 of rows r4 .. r4 + 3
+    const int c4 = ((wave - 1) * 4 + lane / 16) * 4, r4 = (lane % 16) * 4;
+    float4 pv[4], pa;  // the V chunks and weights of the next tile to form
+    auto read_tile = [&](int tile) {
+        const float* vt = vring + (tile % kSpvR) * kPvVTile;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int r = r4 + k;
+            pv[k] = reinterpret_cast<const float4*>(vt)[r * 8 + ((c4 / 4) ^ spv_swz(r))];
+        }
+        pa = reinterpret_cast<const float4*>(al + tile * kPvRows + r4)[0];
+    };
+    auto form = [&](int tile) {  // the products alpha_j * v_j[c] (the reference's product, one rounding)
+        float* d = prod + (tile % 3) * pstride + c4 * kPvStride + r4;
+        reinterpret_cast<float4*>(d)[0] = make_float4(pa.x * pv[0].x, pa.y * pv[1].x, pa.z * pv[2].x, pa.w * pv[3].x);
+        reinterpret_cast<float4*>(d + kPvStride)[0] = make_float4(pa.x * pv[0].y, pa.y * pv[1].y, pa.z * pv[2].y, pa.w * pv[3].y);
+        reinterpret_cast<float4*>(d + 2 * kPvStride)[0] = make_float4(pa.x * pv[0].z, pa.y * pv[1].z, pa.z * pv[2].z, pa.w * pv[3].z);
+        reinterpret_cast<float4*>(d + 3 * kPvStride)[0] = make_float4(pa.x * pv[0].w, pa.y * pv[1].w, pa.z * pv[2].w, pa.w * pv[3].w);
+    };
+    const bool producer = wave == 1 || wave == 2;
+    if (producer) {
+        read_tile(0);
+        form(0);
+        if (ntiles > 1) {
+            read_tile(1);
+            form(1);
+        }
+        if (ntiles > 2) read_tile(2);
+    }
+    __syncthreads();
+    // chain: lane c < 32 adds channel c; cur / nxt hold a tile's products
+    const bool chain = wave == 0 && lane < kPvCh;
+    float4 cur[kPvRows / 4], nxt[kPvRows / 4];
+    // tile t + 1's products, read while tile t is added: the reads land
+    // before the iteration's closing barrier, which waits for them
+    auto read_prod = [&](int tile, float4 (&dst)[kPvRows / 4]) {
+        const uint32_t row = lds_offset(prod + (tile % 3) * pstride + lane * kPvStride);
+        lds_read_b128x16_untracked(row, dst);
+    };
+    float acc = 0.f;
+    auto add_tile = [&](const float4 (&p)[kPvRows / 4], int rows) {
+        if (rows == kPvRows) {
+#pragma unroll
+            for (int i = 0; i < kPvRows / 4; ++i) {
+                acc += p[i].x;
+                acc += p[i].y;
+                acc += p[i].z;
+                acc += p[i].w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kPvRows / 4; ++i) {
+                acc = 4 * i < rows ? acc + p[i].x : acc;
+                acc = 4 * i + 1 < rows ? acc + p[i].y : acc;
+                acc = 4 * i + 2 < rows ? acc + p[i].z : acc;
+                acc = 4 * i + 3 < rows ? acc + p[i].w : acc;
+            }
+        }
+    };
+    // one tile of the pipeline: the chain adds `have` (tile t) and reads tile
+    // t + 1 into `next`; the loop runs tiles in pairs so the two buffers keep
+    // their registers
+    auto iteration = [&](int tile, const float4 (&have)[kPvRows / 4], float4 (&next)[kPvRows / 4]) {
+        if (loader) {
+            if (tile + kSpvR < ntiles) issue(tile + kSpvR);  // into the slot of tile `tile`, read three tiles ago
+            // tile + kSpvAhead has landed: after it at most the tiles up to tile + kSpvR were issued
+            if (tile + kSpvR < ntiles)
+                wait_vmcnt<(kSpvR - kSpvAhead) * kSpvVLoads>();
+            else
+                wait_vmcnt<0>();
+        } else if (producer) {
+            if (tile + 2 < ntiles) form(tile + 2);  // from the registers read last iteration
+            if (tile + 3 < ntiles) read_tile(tile + 3);
+        } else if (chain) {
+            if (tile + 1 < ntiles) read_prod(tile + 1, next);
+            add_tile(have, min(kPvRows, n - tile * kPvRows));
+        }
+        __syncthreads();
+    };
+    if (chain) read_prod(0, cur);
+    __syncthreads();  // tile 0's products in registers
+    for (int tile = 0; tile < ntiles; tile += 2) {
+        iteration(tile, cur, nxt);
+        if (tile + 1 < ntiles) iteration(tile + 1, nxt, cur);
+    }
+
+    if (chain) {
+        const int ch = part * kPvCh + lane;
+        const float gate = a.proj[int64_t(b) * a.proj_stride + int64_t(h) * 2 * kAttnDim + kAttnDim + ch];
+        const float out = acc * sigmoid_f32(gate);
+        const int64_t width = int64_t(a.Hq) * kAttnDim;
+        const int64_t idx = int64_t(h) * kAttnDim + ch;
+        if (a.out_f32) a.out_f32[int64_t(b) * width + idx] = out;
+        float amax = fabsf(out);
+        for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+        const float d = amax / 127.f;
+        const float id = d != 0.f ? 1.f / d : 0.f;
+        int8_t* qs = static_cast<int8_t*>(a.act_out);
+        float* qd = reinterpret_cast<float*>(qs + int64_t(a.B) * width);
+        qs[int64_t(b) * width + idx] = int8_t(int(roundf(out * id)));
+        if (lane == 0) qd[(int64_t(b) * width + idx) >> 5] = half_bits_to_f32(fp32_to_fp16_ref(d));
+    }
+}
+
 // The same sum for many sequences at once (where the per-head workgroups above
 // would outnumber the CUs several times): a workgroup per (sequence, query
 // head, 32 channels) whose 256 lanes stream the V rows through a ring of
@@ -634,11 +874,16 @@ void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
     const unsigned tiles = unsigned(std::min<int64_t>(kScoreTiles, (vis + 255) / 256));
     const int group = a.Hq / a.Hkv;
     hipLaunchKernelGGL(attn_scores_kernel, dim3(unsigned(a.Hkv * ((group + kScoreHeads - 1) / kScoreHeads)), tiles, unsigned(a.B)), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(attn_softmax_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(seqsum::kThreads), 0, s, a);
     // the per-head pipeline while its workgroups fit the CUs (a deep ring, one
-    // workgroup per CU) or fit them twice over (a shallower ring)
+    // workgroup per CU) or fit them twice over (a shallower ring); for up to
+    // 4096 visible keys it runs the softmax itself
     const int64_t pv_blocks = int64_t(a.B) * a.Hq * (kAttnDim / kPvCh);
     const dim3 pv_grid(unsigned(a.Hq * (kAttnDim / kPvCh)), unsigned(a.B));
+    if (pv_blocks <= device_cus() && vis <= kSpvMaxN && a.max_ctx % 4 == 0) {
+        hipLaunchKernelGGL(attn_softmax_pv_kernel, pv_grid, dim3(kSpvThreads), spv_shared_bytes(), s, a);
+        return;
+    }
+    hipLaunchKernelGGL(attn_softmax_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(seqsum::kThreads), 0, s, a);
     if (pv_blocks <= device_cus())
         hipLaunchKernelGGL(attn_pv_kernel<14>, pv_grid, dim3(kPvThreads), pv_shared_bytes(14), s, a);
     else if (pv_blocks <= 2 * device_cus())

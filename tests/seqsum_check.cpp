@@ -1,5 +1,5 @@
 // seqsum_check.cpp -- the workgroup sum of hero/seqsum.hpp, run phase by phase
-// on the host (1024- and 256-lane forms), against the plain sequential loop,
+// on the host (1024-, 512- and 256-lane forms), against the plain sequential loop,
 // bit for bit.
 // Usage: seqsum_check TRIALS   prints "<trials> <mismatches> <fallbacks>"
 #include <cstdio>
@@ -42,8 +42,10 @@ int main(int argc, char** argv) {
         if (t % 211 == 0) p[rng() % n] = INFINITY;
         if (t % 307 == 0) p[rng() % n] = NAN;
         const float want = seqsum::serial_loop(p.data(), n);
-        // alternate the 1024-lane and the 256-lane workgroup forms
-        const float got = (t & 1) ? seqsum::sum_nonneg_host<256>(p.data(), n, sm) : seqsum::sum_nonneg_host<1024>(p.data(), n, sm);
+        // rotate through the 1024-, 512- and 256-lane workgroup forms
+        const float got = t % 3 == 1 ? seqsum::sum_nonneg_host<256>(p.data(), n, sm)
+                          : t % 3 == 2 ? seqsum::sum_nonneg_host<512>(p.data(), n, sm)
+                                       : seqsum::sum_nonneg_host<1024>(p.data(), n, sm);
         uint32_t a, b;
         std::memcpy(&a, &want, 4);
         std::memcpy(&b, &got, 4);

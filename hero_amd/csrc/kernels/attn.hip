@@ -138,6 +138,67 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnDecodeArgs a) {
     }
 }
 
+// The same scores over 64-key tiles staged in shared memory: a workgroup per
+// (KV group chunk of up to four query heads, tile, sequence) copies the tile's
+// keys (128 channels x 64 keys, channel-major as cached) with global_load_lds,
+// then wave w forms the dots of query head w of the chunk, a lane per key,
+// the query held in registers. Tiles start at a multiple of 4 keys (the
+// 16-byte copies need aligned keys; the host runs this form for max_ctx % 4 ==
+// 0); keys before the window's first are formed but not stored.
+constexpr int kScTileKeys = 64;
+constexpr int kScTiles = 1024;  // most tiles per head; workgroups loop beyond
+
+__global__ __launch_bounds__(256) void attn_scores_tile_kernel(AttnDecodeArgs a) {
+    __shared__ __align__(16) float kt[kAttnDim * kScTileKeys];  // [channel][key]
+    const int b = blockIdx.z;
+    const int group = a.Hq / a.Hkv, nchunk = (group + kScoreHeads - 1) / kScoreHeads;
+    const int g = int(blockIdx.x) / nchunk, hq0 = g * group + (int(blockIdx.x) % nchunk) * kScoreHeads;
+    const int nh = min(kScoreHeads, g * group + group - hq0);
+    const int pos = a.positions[b];
+    if (pos < 0 || pos >= a.max_ctx) return;
+    const int first = visible_first(pos, a.window);
+    const int n = pos + 1 - first;
+    const int base0 = first & ~3;  // keys from base0 on, in tiles of 64
+    const int span = pos + 1 - base0;
+    if (int(blockIdx.y) * kScTileKeys >= span) return;
+    const int tid = int(threadIdx.x), wave = tid / 64, lane = tid % 64;
+    const int hh = __builtin_amdgcn_readfirstlane(min(wave, nh - 1));  // waves past nh repeat the last head (not stored)
+    const float* kh = a.k_cache + (cache_of(a, b) * a.Hkv + g) * kAttnDim * a.max_ctx;
+    const float* q = a.q_rot + (int64_t(b) * a.Hq + hq0 + hh) * kAttnDim;
+    float* sc = a.scores + (int64_t(b) * a.Hq + hq0 + hh) * a.max_ctx;
+    // the wave's query, the same in every lane, in vector registers for all of
+    // its tiles (a lane-varying zero keeps the compiler from moving it into
+    // scalar registers, of which 128 would spill)
+    int vzero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
+    float qv[kAttnDim];
+#pragma unroll
+    for (int c = 0; c < kAttnDim; c += 4) {
+        const float4 v = reinterpret_cast<const float4*>(q)[c / 4 + vzero];
+        qv[c] = v.x, qv[c + 1] = v.y, qv[c + 2] = v.z, qv[c + 3] = v.w;
+    }
+    for (int t0 = int(blockIdx.y) * kScTileKeys; t0 < span; t0 += int(gridDim.y) * kScTileKeys) {
+        const int key0 = base0 + t0;
+        // 2048 16-byte chunks: chunk p = channel p / 16, keys key0 + 4 (p % 16) ..;
+        // chunks past the cache's end read its last chunk (never stored)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int p = 256 * j + tid, c = p / 16;
+            const int k4 = min(key0 + 4 * (p % 16), int(a.max_ctx) - 4);
+            lds_dma_b128(kh + int64_t(c) * a.max_ctx + k4, lds_offset(kt + 4 * 256 * j + 4 * 64 * wave));
+        }
+        wait_vmcnt<0>();
+        __syncthreads();
+        // s_j = scale * dot(q, k_j), the dot a sequential 128-term sum (core.hpp:496-500)
+        float dot = 0.f;
+#pragma unroll
+        for (int c = 0; c < kAttnDim; ++c) dot += qv[c] * kt[c * kScTileKeys + lane];
+        const int t = key0 + lane - first;  // index among the visible keys
+        if (wave < nh && t >= 0 && t < n) sc[t] = a.score_scale * dot;
+        __syncthreads();  // the tile is read before the next one lands
+    }
+}
+
 // ---- 3. softmax ------------------------------------------------------------------------------
 // max over the visible scores (order free), e_j = exp(s_j - max), the total as
 // the sequential sum over j computed exactly in parallel, alpha_j = e_j / total
@@ -334,8 +395,8 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(AttnDecodeArgs a) {
 // channels) runs the softmax of its head itself and then the weighted sum, so
 // the V stream starts at once and the weights never leave shared memory.
 // Eight waves:
-//  * all copy the head's scores into shared memory (global_load_lds); waves
-//    4-7 (the loaders) then put the whole V ring in flight;
+//  * all copy the head's scores into shared memory (global_load_lds), then
+//    put the first R tiles of V in flight (one load per tile each);
 //  * max; e_j = exp(s_j - max), lane t taking j = t, t + 512, ...; the total
 //    as the exact sequential sum (hero/seqsum.hpp, 512 lanes); alpha_j =
 //    e_j / total -- the operations of attn_softmax_kernel;
@@ -353,7 +414,7 @@ constexpr int kSpvR = 13;                      // V ring slots
 constexpr int kSpvLoaders = 4;                 // waves 4 .. 7
 constexpr int kSpvVLoads = kPvVTile / 4 / 64 / kSpvLoaders;  // 16-byte V loads per loader lane per tile: 2
 constexpr int kSpvAhead = 4;                   // the tile the loaders wait for: t + 4 at the end of iteration t
-static_assert(kSpvVLoads == 2 && 2 + kSpvR * kSpvVLoads <= 63, "vmcnt range");
+static_assert(kSpvVLoads == 2 && 2 + kSpvR <= 63 && (kSpvR - kSpvAhead) * kSpvVLoads <= 63, "vmcnt range");
 constexpr size_t spv_shared_bytes() {
     return (size_t(kSpvR) * kPvVTile + size_t(3) * kPvCh * kPvStride + kSpvMaxN) * 4 + sizeof(seqsum::Shared) + 32 + 32 * 8;
 }
@@ -388,34 +449,33 @@ __global__ __launch_bounds__(kSpvThreads) void attn_softmax_pv_kernel(AttnDecode
     // p = 64 (kSpvVLoads li + j) + lane, i.e. row p / 8 and channel chunk
     // (p % 8) ^ spv_swz(row); rows past n read row n - 1, whose products the
     // chain never adds
+    auto issue_chunk = [&](int tile, int q) {  // load q (of 8) of a tile: chunks 64 q .. 64 q + 63
+        const int p = 64 * q + lane, r = p / 8;
+        const int row = min(tile * kPvRows + r, n - 1);
+        lds_dma_b128(vb + int64_t(row) * kw + 4 * ((p % 8) ^ spv_swz(r)), lds_offset(vring + (tile % kSpvR) * kPvVTile + 4 * 64 * q));
+    };
     auto issue = [&](int tile) {
-        float* slot = vring + (tile % kSpvR) * kPvVTile;
 #pragma unroll
-        for (int j = 0; j < kSpvVLoads; ++j) {
-            const int c0 = 64 * (kSpvVLoads * li + j), p = c0 + lane, r = p / 8;
-            const int row = min(tile * kPvRows + r, n - 1);
-            lds_dma_b128(vb + int64_t(row) * kw + 4 * ((p % 8) ^ spv_swz(r)), lds_offset(slot + 4 * c0));
-        }
+        for (int j = 0; j < kSpvVLoads; ++j) issue_chunk(tile, kSpvVLoads * li + j);
     };
 
     // ---- the scores into shared memory: chunk q = 4 consecutive scores;
-    // chunks past the visible ones read the last visible chunk (never used) ----
+    // chunks past the visible ones read the last visible chunk (never used).
+    // Then the whole V ring: every wave issues one of each tile's eight loads
+    // (a load takes the issuing wave ~100 cycles, so the loaders alone would
+    // hold up the softmax); all of them have landed by the end of the softmax ----
     if (tid < 32) etab[tid] = exp2_table(tid);
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int q = min(wave * 128 + k * 64 + lane, (n - 1) / 4);
         lds_dma_b128(sc + 4 * q, lds_offset(al + 4 * (wave * 128 + k * 64)));
     }
-    if (loader) {
-        for (int t = 0; t < kSpvR; ++t)
-            if (t < ntiles) issue(t);
-        if (ntiles >= kSpvR)
-            wait_vmcnt<kSpvR * kSpvVLoads>();  // the scores have landed
-        else
-            wait_vmcnt<0>();
-    } else {
+    for (int t = 0; t < kSpvR; ++t)
+        if (t < ntiles) issue_chunk(t, wave);
+    if (ntiles >= kSpvR)
+        wait_vmcnt<kSpvR>();  // the scores have landed
+    else
         wait_vmcnt<0>();
-    }
     __syncthreads();
 
     // ---- softmax (nm/src/components.hpp:132-141) ----
@@ -440,30 +500,17 @@ __global__ __launch_bounds__(kSpvThreads) void attn_softmax_pv_kernel(AttnDecode
     }
     __syncthreads();
     const float total = seqsum::sum_nonneg<kSpvThreads>(al, n, sm);  // every wave gets the total
-    // alpha over the terms (zero past n, up to the last tile's end): no wave
-    // reads the terms after the sum unless it fell back to the plain loop,
-    // which ends with a barrier
-    {
-        const int j0 = 8 * tid;
+    // alpha over the terms, zero past n up to the last tile's end (the same
+    // lanes as the exps): no wave reads the terms after the sum unless it fell
+    // back to the plain loop, which ends with a barrier
 #pragma unroll
-        for (int k = 0; k < 8; k += 4) {
-            float4 e4 = reinterpret_cast<const float4*>(al + j0)[k / 4];
-            e4.x = j0 + k < n ? e4.x / total : 0.f;
-            e4.y = j0 + k + 1 < n ? e4.y / total : 0.f;
-            e4.z = j0 + k + 2 < n ? e4.z / total : 0.f;
-            e4.w = j0 + k + 3 < n ? e4.w / total : 0.f;
-            reinterpret_cast<float4*>(al + j0)[k / 4] = e4;
-        }
+    for (int m = 0; m < 8; ++m) {
+        const int j = tid + kSpvThreads * m;
+        if (j < ntiles * kPvRows) al[j] = j < n ? al[j] / total : 0.f;
     }
 
     // ---- the weighted sum (core.hpp:206-208) ----
-    // tiles 0 .. 3 have landed: after them at most tiles 4 .. R - 1 are in flight
-    if (loader) {
-        if (ntiles >= kSpvR)
-            wait_vmcnt<(kSpvR - kSpvAhead) * kSpvVLoads>();
-        else
-            wait_vmcnt<0>();
-    }
+    wait_vmcnt<0>();  // the ring's first R tiles have landed
     __syncthreads();
     // producers: channels c4 .. c4 + 3 of rows r4 .. r4 + 3
     const int c4 = ((wave - 1) * 4 + lane / 16) * 4, r4 = (lane % 16) * 4;
@@ -530,7 +577,9 @@ __global__ __launch_bounds__(kSpvThreads) void attn_softmax_pv_kernel(AttnDecode
     auto iteration = [&](int tile, const float4 (&have)[kPvRows / 4], float4 (&next)[kPvRows / 4]) {
         if (loader) {
             if (tile + kSpvR < ntiles) issue(tile + kSpvR);  // into the slot of tile `tile`, read three tiles ago
-            // tile + kSpvAhead has landed: after it at most the tiles up to tile + kSpvR were issued
+            // tile + kSpvAhead has landed: it is one of the ring's first R tiles,
+            // or at most the loads of the tiles after it up to tile + kSpvR
+            // were issued after its own
             if (tile + kSpvR < ntiles)
                 wait_vmcnt<(kSpvR - kSpvAhead) * kSpvVLoads>();
             else
@@ -873,7 +922,13 @@ void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
     const int64_t vis = a.window > 0 ? std::min<int64_t>(a.max_ctx, a.window) : a.max_ctx;
     const unsigned tiles = unsigned(std::min<int64_t>(kScoreTiles, (vis + 255) / 256));
     const int group = a.Hq / a.Hkv;
-    hipLaunchKernelGGL(attn_scores_kernel, dim3(unsigned(a.Hkv * ((group + kScoreHeads - 1) / kScoreHeads)), tiles, unsigned(a.B)), dim3(256), 0, s, a);
+    const unsigned chunks = unsigned(a.Hkv * ((group + kScoreHeads - 1) / kScoreHeads));
+    // few sequences: 64-key tiles spread the keys over the CUs; many
+    // sequences (and prefill rows) fill them with the 256-key form
+    if (a.max_ctx % 4 == 0 && a.B <= 2 && !a.shared_cache)
+        hipLaunchKernelGGL(attn_scores_tile_kernel, dim3(chunks, unsigned(std::min<int64_t>(kScTiles, (vis + 3 + kScTileKeys - 1) / kScTileKeys)), unsigned(a.B)), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(attn_scores_kernel, dim3(chunks, tiles, unsigned(a.B)), dim3(256), 0, s, a);
     // the per-head pipeline while its workgroups fit the CUs (a deep ring, one
     // workgroup per CU) or fit them twice over (a shallower ring); for up to
     // 4096 visible keys it runs the softmax itself

@@ -29,6 +29,30 @@ __device__ __forceinline__ float silu_f32(float x) { return x / (1.f + exp_f32(-
 // nm/src/recurrent.hpp:35
 __device__ __forceinline__ float softplus_f32(float x) { return x > 20.f ? x : log1p_f32(exp_f32(x)); }
 
+// 0, in a vector register the compiler cannot see through: added to an
+// address, it keeps a load of a wave-uniform value a per-lane vector load
+// (no scalar copy, no early wait for it)
+__device__ __forceinline__ uint32_t lane_zero() {
+    uint32_t z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    return z;
+}
+
+// The same functions with expf's 32-entry table read from shared memory
+// (filled by fill_exp_table before a barrier). The plain forms read it from
+// global memory: behind other loads still in flight (vector memory operations
+// retire in order) each call would wait for all of them.
+struct ExpTab {
+    const uint64_t* t;
+    __device__ __forceinline__ float exp(float x) const { return expf_glibc_with(x, [p = t](int i) { return p[i]; }); }
+    __device__ __forceinline__ float sigmoid(float x) const { return 1.f / (1.f + exp(-x)); }
+    __device__ __forceinline__ float silu(float x) const { return x / (1.f + exp(-x)); }
+    __device__ __forceinline__ float softplus(float x) const { return x > 20.f ? x : log1p_f32(exp(x)); }
+};
+__device__ __forceinline__ void fill_exp_table(uint64_t* lds, int tid) {
+    if (tid < 32) lds[tid] = exp2_table(tid);
+}
+
 __device__ __forceinline__ float half_bits_to_f32(uint16_t h) {
     _Float16 v;
     __builtin_memcpy(&v, &h, 2);

@@ -123,7 +123,29 @@ struct GdnDecodeShared {
     float sq[2][kGdnDim];              // squares of q and k, then of the outputs
     float delta[kGdnDim];
     float scal[4];                     // 1/||q||, 1/||k||, 1/rms(o)
+    uint64_t etab[32];                 // expf's table
 };
+
+// the ring's W slots of channel c (slot s holds the input of the latest
+// position p with p % W == s), read without knowing the position
+template <int W>
+__device__ __forceinline__ void load_ring(const float* hist, int64_t CC, int64_t c, float (&ring)[W]) {
+#pragma unroll
+    for (int s = 0; s < W; ++s) ring[s] = hist[int64_t(s) * CC + c];
+}
+// the inputs at positions pos-(W-1) .. pos-1 out of the ring (zero before position 0)
+template <int W>
+__device__ __forceinline__ void past_from_ring(const float (&ring)[W], int pos, ConvPast<W>& past) {
+#pragma unroll
+    for (int i = 0; i < W - 1; ++i) {
+        const int p = pos - (W - 1) + i;
+        const int slot = p >= 0 ? p % W : -1;
+        float v = 0.f;
+#pragma unroll
+        for (int s = 0; s < W; ++s) v = s == slot ? ring[s] : v;
+        past.v[i] = v;
+    }
+}
 
 template <int W>
 __global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(GdnDecodeArgs a) {
@@ -132,30 +154,39 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(GdnDecodeArgs a
     const int t = threadIdx.x, j = t % kGdnDim, i0 = (t / kGdnDim) * kGdnRows;
     const int h = blockIdx.x, b = blockIdx.y;
     const int hk = h % a.Hk;  // tiled key heads (nm/src/qwen35.hpp:172)
-    const int pos = a.positions[b];
-    if (pos < 0) return;  // the host keeps positions in range
     const int64_t KW = int64_t(a.Hk) * kGdnDim;
     const int64_t CC = 2 * KW + int64_t(a.Hv) * kGdnDim;
     const float* P = a.proj + int64_t(b) * a.proj_stride;
     float* hist = a.conv_hist + int64_t(b) * W * CC;
     float* S = a.state + (int64_t(b) * a.Hv + h) * kGdnState;
     const bool owner = t < kGdnDim;  // column j's chains
+    const ExpTab et{sh.etab};
 
-    // ---- the owners' inputs first (loads retire in order: the conv and the
-    // q/k norms then run while the state is still arriving), then the state
-    // rows i0 .. i0+31 of column j ----
+    // ---- every load is issued before anything waits, none depends on the
+    // position: expf's table, the gate inputs and the owners' conv inputs
+    // first (loads retire in order: the conv and the q/k norms then run while
+    // the state is still arriving), then the state rows i0 .. i0+31 of
+    // column j ----
+    const uint64_t etv = exp2_table(t & 31);  // lanes < 32 store it in shared memory below
+    const int pos = a.positions[b];
+    // the gate inputs as vector loads (the same in every lane), issued here
+    // rather than where they are first used
+    const uint32_t z0 = lane_zero();
+    const float g_beta = load_f32(buffer_of(P, uint32_t(a.proj_stride) * 4u), uint32_t(a.beta_off + h) * 4u + z0);
+    const float g_alpha = load_f32(buffer_of(P, uint32_t(a.proj_stride) * 4u), uint32_t(a.alpha_off + h) * 4u + z0);
+    const float g_dt = load_f32(buffer_of(a.dt_bias, uint32_t(a.Hv) * 4u), uint32_t(h) * 4u + z0);
+    const float g_a = load_f32(buffer_of(a.decay, uint32_t(a.Hv) * 4u), uint32_t(h) * 4u + z0);
     const int64_t cq = int64_t(hk) * kGdnDim + j, ck = KW + int64_t(hk) * kGdnDim + j, cv = 2 * KW + int64_t(h) * kGdnDim + j;
     float xq = 0.f, xk = 0.f, xv = 0.f, z = 0.f, gamma = 0.f;
-    float tq[W], tk[W], tv[W];
-    ConvPast<W> pq, pk, pv;
+    float tq[W], tk[W], tv[W], rq[W], rk[W], rv[W];
     if (owner) {
         xq = P[cq], xk = P[ck], xv = P[cv];
         load_taps<W>(a.conv_taps, cq, tq);
         load_taps<W>(a.conv_taps, ck, tk);
         load_taps<W>(a.conv_taps, cv, tv);
-        load_past<W>(hist, CC, cq, pos, pq);
-        load_past<W>(hist, CC, ck, pos, pk);
-        load_past<W>(hist, CC, cv, pos, pv);
+        load_ring<W>(hist, CC, cq, rq);
+        load_ring<W>(hist, CC, ck, rk);
+        load_ring<W>(hist, CC, cv, rv);
         z = P[a.z_off + int64_t(h) * kGdnDim + j];
         gamma = a.norm_gamma[j];
     }
@@ -164,15 +195,25 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(GdnDecodeArgs a
 #pragma unroll
     for (int r = 0; r < kGdnRows; ++r) col[r] = S[(i0 + r) * kGdnDim + j];
     __builtin_amdgcn_sched_barrier(0);
-    const float beta = sigmoid_f32(P[a.beta_off + h]);
-    const float decay = exp_f32(a.decay[h] * softplus_f32(P[a.alpha_off + h] + a.dt_bias[h]));
+    if (t < 32) sh.etab[t] = etv;
+    __syncthreads();  // the table
+    if (pos < 0) {  // the host keeps positions in range; idle batch rows store nothing
+        wait_vmcnt<0>();
+        return;
+    }
+    const float beta = et.sigmoid(g_beta);
+    const float decay = et.exp(g_a * et.softplus(g_alpha + g_dt));
 
     // ---- 1. conv + SiLU on the head's channels; the ring takes this position ----
     float v = 0.f;
     if (owner) {
-        const float q = silu_f32(conv_channel<W>(tq, pq, xq));
-        const float k = silu_f32(conv_channel<W>(tk, pk, xk));
-        v = silu_f32(conv_channel<W>(tv, pv, xv));
+        ConvPast<W> pq, pk, pv;
+        past_from_ring<W>(rq, pos, pq);
+        past_from_ring<W>(rk, pos, pk);
+        past_from_ring<W>(rv, pos, pv);
+        const float q = et.silu(conv_channel<W>(tq, pq, xq));
+        const float k = et.silu(conv_channel<W>(tk, pk, xk));
+        v = et.silu(conv_channel<W>(tv, pv, xv));
         const int slot = pos % W;
         if (h < a.Hk) {  // the first value head of each key head owns its q/k history
             hist[int64_t(slot) * CC + cq] = xq;
@@ -287,7 +328,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(GdnDecodeArgs a
     }
     __syncthreads();
     if (owner) {
-        const float out = (gamma * o * sh.scal[2]) * silu_f32(z);
+        const float out = (gamma * o * sh.scal[2]) * et.silu(z);
         const int64_t width = int64_t(a.Hv) * kGdnDim;
         const int64_t idx = int64_t(h) * kGdnDim + j;
         if (a.out_f32) a.out_f32[int64_t(b) * width + idx] = out;

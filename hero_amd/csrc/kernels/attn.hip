@@ -138,18 +138,50 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnDecodeArgs a) {
     }
 }
 
-// The same scores over 64-key tiles staged in shared memory: a workgroup per
-// (KV group chunk of up to four query heads, tile, sequence) copies the tile's
-// keys (128 channels x 64 keys, channel-major as cached) with global_load_lds,
-// then wave w forms the dots of query head w of the chunk, a lane per key,
-// the query held in registers. Tiles start at a multiple of 4 keys (the
-// 16-byte copies need aligned keys; the host runs this form for max_ctx % 4 ==
-// 0); keys before the window's first are formed but not stored.
+// The decode form for one or two sequences, with the prep step folded in:
+// 64-key tiles staged in shared memory, a workgroup per (KV group chunk of up
+// to four query heads, tile, sequence). It copies the tile's keys (128
+// channels x 64 keys, channel-major as cached) with global_load_lds; while
+// they land, wave w forms query head w of the chunk (RMSNorm + RoPE, a lane per
+// plane (i, i + 64)) and the workgroup whose tile holds the new position forms
+// its key the same way, patches it into the tile and appends k and v to the
+// cache (the prep kernel's work). Then wave w forms the dots of head w, a lane
+// per key, the query held in registers. Tiles start at a multiple of 4 keys
+// (the 16-byte copies need aligned keys; the host runs this form for
+// max_ctx % 4 == 0); keys before the window's first are formed but not stored.
 constexpr int kScTileKeys = 64;
 constexpr int kScTiles = 1024;  // most tiles per head; workgroups loop beyond
 
+// RMSNorm (sequential 128-term sum of squares by lane 0) and RoPE of one head
+// held by a wave as x0 = channel lane, x1 = channel lane + 64 -- the
+// operations of norm_rope_head; buf: 128 floats of the wave's own
+__device__ __forceinline__ void norm_rope_pair(float& x0, float& x1, const float* gamma, float eps, const float* cs, float* buf, int lane) {
+    buf[lane] = x0 * x0;
+    buf[lane + 64] = x1 * x1;
+    float scal = 0.f;
+    if (lane == 0) {
+        float ss = 0.f;
+        const float4* b4 = reinterpret_cast<const float4*>(buf);
+#pragma unroll
+        for (int i = 0; i < kAttnDim / 4; ++i) {
+            const float4 v = b4[i];
+            ss += v.x;
+            ss += v.y;
+            ss += v.z;
+            ss += v.w;
+        }
+        scal = 1.f / sqrtf(ss / float(kAttnDim) + eps);
+    }
+    scal = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(scal)));  // lane 0's value (it is active here)
+    const float n0 = gamma[lane] * x0 * scal, n1 = gamma[lane + 64] * x1 * scal;
+    const float c = cs[2 * lane], s = cs[2 * lane + 1];
+    x0 = n0 * c - n1 * s;
+    x1 = n1 * c + n0 * s;
+}
+
 __global__ __launch_bounds__(256) void attn_scores_tile_kernel(AttnDecodeArgs a) {
     __shared__ __align__(16) float kt[kAttnDim * kScTileKeys];  // [channel][key]
+    __shared__ __align__(16) float qb[kScoreHeads][kAttnDim];    // per wave: squares, then its rotated query
     const int b = blockIdx.z;
     const int group = a.Hq / a.Hkv, nchunk = (group + kScoreHeads - 1) / kScoreHeads;
     const int g = int(blockIdx.x) / nchunk, hq0 = g * group + (int(blockIdx.x) % nchunk) * kScoreHeads;
@@ -163,32 +195,72 @@ __global__ __launch_bounds__(256) void attn_scores_tile_kernel(AttnDecodeArgs a)
     if (int(blockIdx.y) * kScTileKeys >= span) return;
     const int tid = int(threadIdx.x), wave = tid / 64, lane = tid % 64;
     const int hh = __builtin_amdgcn_readfirstlane(min(wave, nh - 1));  // waves past nh repeat the last head (not stored)
-    const float* kh = a.k_cache + (cache_of(a, b) * a.Hkv + g) * kAttnDim * a.max_ctx;
-    const float* q = a.q_rot + (int64_t(b) * a.Hq + hq0 + hh) * kAttnDim;
+    const int64_t kv = cache_of(a, b) * a.Hkv + g;
+    const float* kh = a.k_cache + kv * kAttnDim * a.max_ctx;
     float* sc = a.scores + (int64_t(b) * a.Hq + hq0 + hh) * a.max_ctx;
-    // the wave's query, the same in every lane, in vector registers for all of
-    // its tiles (a lane-varying zero keeps the compiler from moving it into
-    // scalar registers, of which 128 would spill)
-    int vzero;
-    asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
-    float qv[kAttnDim];
-#pragma unroll
-    for (int c = 0; c < kAttnDim; c += 4) {
-        const float4 v = reinterpret_cast<const float4*>(q)[c / 4 + vzero];
-        qv[c] = v.x, qv[c + 1] = v.y, qv[c + 2] = v.z, qv[c + 3] = v.w;
-    }
-    for (int t0 = int(blockIdx.y) * kScTileKeys; t0 < span; t0 += int(gridDim.y) * kScTileKeys) {
-        const int key0 = base0 + t0;
-        // 2048 16-byte chunks: chunk p = channel p / 16, keys key0 + 4 (p % 16) ..;
-        // chunks past the cache's end read its last chunk (never stored)
+    const float* P = a.proj + int64_t(b) * a.proj_stride;
+    const float* cs = a.rope_cs + int64_t(pos) * kAttnDim;  // [Dh/2][2]
+    const int pos_tile = (pos - base0) / kScTileKeys;
+    const bool has_pos = pos_tile % int(gridDim.y) == int(blockIdx.y);
+
+    // 2048 16-byte chunks: chunk p = channel p / 16, keys key0 + 4 (p % 16) ..;
+    // chunks past the cache's end read its last chunk (never stored)
+    auto issue_tile = [&](int key0) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int p = 256 * j + tid, c = p / 16;
             const int k4 = min(key0 + 4 * (p % 16), int(a.max_ctx) - 4);
             lds_dma_b128(kh + int64_t(c) * a.max_ctx + k4, lds_offset(kt + 4 * 256 * j + 4 * 64 * wave));
         }
+    };
+    int t0 = int(blockIdx.y) * kScTileKeys;
+    issue_tile(base0 + t0);
+
+    // ---- the prep step (nm/src/qwen35.hpp:343-362): the wave's query ----
+    float q0 = P[int64_t(hq0 + hh) * 2 * kAttnDim + lane], q1 = P[int64_t(hq0 + hh) * 2 * kAttnDim + 64 + lane];
+    norm_rope_pair(q0, q1, a.q_gamma, a.eps, cs, qb[wave], lane);
+    qb[wave][lane] = q0;
+    qb[wave][lane + 64] = q1;
+    // the new key's inputs (the workgroups whose tiles hold it; wave 0 forms it)
+    float k0 = 0.f, k1 = 0.f;
+    if (has_pos && wave == 0) {
+        k0 = P[a.k_off + int64_t(g) * kAttnDim + lane];
+        k1 = P[a.k_off + int64_t(g) * kAttnDim + 64 + lane];
+    }
+    // the query in vector registers, the same in every lane, for all of the
+    // wave's tiles (a lane-varying zero keeps it out of scalar registers)
+    float qv[kAttnDim];
+    {
+        const uint32_t z0 = lane_zero();
+#pragma unroll
+        for (int c = 0; c < kAttnDim; c += 4) {
+            const float4 v = reinterpret_cast<const float4*>(qb[wave])[c / 4 + z0];
+            qv[c] = v.x, qv[c + 1] = v.y, qv[c + 2] = v.z, qv[c + 3] = v.w;
+        }
+    }
+    if (has_pos && wave == 0) {  // qb[0] is free again: wave 0's query is in its registers
+        norm_rope_pair(k0, k1, a.k_gamma, a.eps, cs, qb[0], lane);
+        if (int(blockIdx.x) % nchunk == 0) {  // the cache, once per K/V head
+            a.k_cache[(kv * kAttnDim + lane) * a.max_ctx + pos] = k0;  // [B][Hkv][Dh][max_ctx]
+            a.k_cache[(kv * kAttnDim + 64 + lane) * a.max_ctx + pos] = k1;
+            float* vrow = a.v_cache + (cache_of(a, b) * a.max_ctx + pos) * (int64_t(a.Hkv) * kAttnDim) + int64_t(g) * kAttnDim;
+            vrow[lane] = P[a.v_off + int64_t(g) * kAttnDim + lane];  // [B][max_ctx][Hkv*Dh]
+            vrow[64 + lane] = P[a.v_off + int64_t(g) * kAttnDim + 64 + lane];
+        }
+    }
+
+    for (; t0 < span; t0 += int(gridDim.y) * kScTileKeys) {
+        const int key0 = base0 + t0;
+        if (t0 != int(blockIdx.y) * kScTileKeys) issue_tile(key0);
         wait_vmcnt<0>();
         __syncthreads();
+        if (has_pos && (pos - base0) / kScTileKeys * kScTileKeys == t0) {  // the new key into its column
+            if (wave == 0) {
+                kt[lane * kScTileKeys + (pos - key0)] = k0;
+                kt[(lane + 64) * kScTileKeys + (pos - key0)] = k1;
+            }
+            __syncthreads();
+        }
         // s_j = scale * dot(q, k_j), the dot a sequential 128-term sum (core.hpp:496-500)
         float dot = 0.f;
 #pragma unroll
@@ -918,17 +990,18 @@ void launch_attn_paged(const AttnPagedArgs& p, hipStream_t s) {
 }
 
 void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(attn_prep_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, a);
     const int64_t vis = a.window > 0 ? std::min<int64_t>(a.max_ctx, a.window) : a.max_ctx;
     const unsigned tiles = unsigned(std::min<int64_t>(kScoreTiles, (vis + 255) / 256));
     const int group = a.Hq / a.Hkv;
     const unsigned chunks = unsigned(a.Hkv * ((group + kScoreHeads - 1) / kScoreHeads));
     // few sequences: 64-key tiles spread the keys over the CUs; many
     // sequences (and prefill rows) fill them with the 256-key form
-    if (a.max_ctx % 4 == 0 && a.B <= 2 && !a.shared_cache)
+    if (a.max_ctx % 4 == 0 && a.B <= 2 && !a.shared_cache) {  // prep folded in
         hipLaunchKernelGGL(attn_scores_tile_kernel, dim3(chunks, unsigned(std::min<int64_t>(kScTiles, (vis + 3 + kScTileKeys - 1) / kScTileKeys)), unsigned(a.B)), dim3(256), 0, s, a);
-    else
+    } else {
+        hipLaunchKernelGGL(attn_prep_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, a);
         hipLaunchKernelGGL(attn_scores_kernel, dim3(chunks, tiles, unsigned(a.B)), dim3(256), 0, s, a);
+    }
     // the per-head pipeline while its workgroups fit the CUs (a deep ring, one
     // workgroup per CU) or fit them twice over (a shallower ring); for up to
     // 4096 visible keys it runs the softmax itself

@@ -33,15 +33,16 @@
 //
 // Lane t holds elements PT*t .. PT*t+PT-1 (PT = 4096 / lanes). Every
 // cross-lane step inside a wave is a DPP scan (no shared memory); the
-// workgroup needs two barriers: one for the wave totals of the speculation,
-// one for the serial-element tables, which each wave writes into its own
-// region with wave-local increment prefixes. Every wave then runs the walk
-// itself (so the result needs no broadcast): its lanes prepare one step each,
-// the dependent chain s -> s + a -> s + val runs over the steps with the
-// step data read lane by lane, each lane keeps the chain values of its own
-// step, and the binade checks of all steps run in parallel afterwards. The
-// host emulation at the end runs the same per-lane functions and the same
-// operations in the same order.
+// workgroup needs three barriers: one for the wave totals of the speculation,
+// one for the wave totals of the serial counts and increments, after which
+// every lane writes its serial elements' entries at their places in one table,
+// and one for that table. Every wave then runs the walk itself (so the result
+// needs no broadcast): its lanes prepare one step each, the dependent chain
+// s -> s + a -> s + val runs over the steps with the step data read lane by
+// lane, each lane keeps the chain values of its own step, and the binade
+// checks of all steps run in parallel afterwards. The host emulation at the
+// end runs the same per-lane functions and the same operations in the same
+// order.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -61,7 +62,7 @@ constexpr int kThreads = 1024;  // the default workgroup
 constexpr int kWaveSize = 64;
 constexpr int kMaxWaves = 16;
 constexpr int kMaxN = 4096;
-constexpr int kMaxSerial = 512;  // table entries, split evenly over the waves
+constexpr int kMaxSerial = 512;  // table entries
 constexpr int kWaves = kThreads / kWaveSize;  // of the default workgroup
 constexpr float kMarginLo = 1.0f - 1.0f / 16384.0f;
 constexpr float kMarginHi = 1.0f + 1.0f / 16384.0f;
@@ -76,10 +77,9 @@ __host__ __device__ inline int binade_f32(float s) {
 struct Shared {
     float wsum[kMaxWaves];                  // wave totals of the speculation scan
     uint32_t wc[kMaxWaves], wn[kMaxWaves];  // wave totals of the increments and of the serial counts
-    // serial-element tables, region w (kMaxSerial / waves entries) for wave w;
-    // one 16-byte entry per element: x = its index, y = its term (bits), z =
-    // increments of the wave's non-serial elements before it (mod 2^32), w =
-    // binade of the run that follows it
+    // the serial elements in index order, one 16-byte entry each: x = its
+    // index, y = its term (bits), z = increments of the non-serial elements
+    // before it (mod 2^32), w = binade of the run that follows it
     uint4 ser[kMaxSerial];
     int32_t fell_back;            // 1 if the last sum ran the plain loop (written by wave 0)
     float result;                 // for callers that broadcast a value of their own
@@ -160,19 +160,20 @@ __host__ __device__ inline void lane_classify(Lane<PT>& L, float pre, float next
     L.cnt = uint32_t(__builtin_popcount(serial));
 }
 
-// Writes the table entries of the lane's serial elements into its wave's
-// region: r = serial elements of the wave before the lane, cx = increments of
-// the wave's non-serial elements before the lane; entries past the region's
-// capacity are dropped (the walk then runs the plain loop).
+// Writes the table entries of the lane's serial elements at their places in
+// the whole table: r = serial elements before the lane (all waves), cx =
+// increments of the non-serial elements before the lane (mod 2^32); entries
+// past the table's capacity are dropped (the walk then runs the plain loop).
 template <int PT>
-__host__ __device__ inline void lane_emit(const Lane<PT>& L, int i0, uint32_t cx, uint32_t r, int region, int cap, Shared& sm) {
-    // straight-line: c[k] is 0 for serial elements
+__host__ __device__ inline void lane_emit(const Lane<PT>& L, int i0, uint32_t cx, uint32_t r, Shared& sm) {
+    if (L.serial == 0) return;  // most lanes
+    // c[k] is 0 for serial elements
 #pragma unroll
     for (int k = 0; k < PT; ++k) {
         const bool ser = (L.serial >> k) & 1u;
-        if (ser && r < uint32_t(cap)) {
+        if (ser && r < uint32_t(kMaxSerial)) {
             const uint32_t be = L.be_after[k];
-            sm.ser[region * cap + int(r)] = make_uint4(uint32_t(i0 + k), f32_bits(L.v[k]), cx, uint32_t(int(be > 1u ? be : 1u) - 127));
+            sm.ser[r] = make_uint4(uint32_t(i0 + k), f32_bits(L.v[k]), cx, uint32_t(int(be > 1u ? be : 1u) - 127));
         }
         r += ser ? 1u : 0u;
         cx += L.c[k];
@@ -185,43 +186,19 @@ __host__ __device__ inline float serial_loop(const float* p, int n) {
     return s;
 }
 
-// The walk's view of the tables: wave totals and their exclusive prefixes.
+// the wave totals of serial counts and increments: the exclusive prefixes of
+// wave w and the grand totals
 template <int W>
-struct Tables {
-    uint32_t nbase[W], cbase[W], wn[W];  // serial entries / increments of the waves before w; entries of w
-    uint32_t nser, c_total;
-    bool overflow;  // a wave had more serial elements than its region holds
-};
-
-template <int W>
-__host__ __device__ inline void read_tables(const Shared& sm, int cap, Tables<W>& T) {
-    uint32_t nb = 0, cb = 0;
-    bool of = false;
+__host__ __device__ inline void wave_prefix(const Shared& sm, int w, uint32_t& nbase, uint32_t& cbase, uint32_t& nser, uint32_t& c_total) {
+    nbase = cbase = nser = c_total = 0;
 #pragma unroll
     for (int u = 0; u < W; ++u) {
-        const uint32_t n = sm.wn[u];
-        T.nbase[u] = nb, T.cbase[u] = cb, T.wn[u] = n;
-        of = of || n > uint32_t(cap);
-        nb += n, cb += sm.wc[u];
+        const uint32_t n = sm.wn[u], c = sm.wc[u];
+        nbase += u < w ? n : 0u;
+        cbase += u < w ? c : 0u;
+        nser += n;
+        c_total += c;
     }
-    T.nser = nb, T.c_total = cb, T.overflow = of;
-}
-
-// serial entry q < nser, its cx made global: the increments of every
-// non-serial element before it (mod 2^32)
-template <int W>
-__host__ __device__ inline uint4 locate(const Tables<W>& T, const Shared& sm, int cap, uint32_t q) {
-    int sl = 0;
-    uint32_t cb = 0;
-#pragma unroll
-    for (int u = 0; u < W; ++u) {
-        const bool here = q >= T.nbase[u] && q < T.nbase[u] + T.wn[u];
-        sl = here ? u * cap + int(q - T.nbase[u]) : sl;
-        cb = here ? T.cbase[u] : cb;
-    }
-    uint4 e = sm.ser[sl];
-    e.z += cb;
-    return e;
 }
 
 // step r of the walk: the run before serial element r (for r == nser, the
@@ -233,10 +210,10 @@ struct Step {
     int32_t flags;  // bit 0: the run is non-empty, bit 1: its C is too large
 };
 
-template <int W>
-__host__ __device__ inline Step walk_entry(const Tables<W>& T, const Shared& sm, int cap, uint32_t r, int n) {
-    const uint4 cur = r < T.nser ? locate(T, sm, cap, r) : make_uint4(uint32_t(n), 0u, T.c_total, 0u);
-    const uint4 prev = r > 0 ? locate(T, sm, cap, r - 1) : make_uint4(0xFFFFFFFFu, 0u, 0u, uint32_t(-126));
+// r <= nser <= kMaxSerial
+__host__ __device__ inline Step walk_entry(const Shared& sm, uint32_t nser, uint32_t c_total, uint32_t r, int n) {
+    const uint4 cur = r < nser ? sm.ser[r] : make_uint4(uint32_t(n), 0u, c_total, 0u);
+    const uint4 prev = r > 0 ? sm.ser[r - 1] : make_uint4(0xFFFFFFFFu, 0u, 0u, uint32_t(-126));
     Step st;
     st.e = int32_t(prev.w);
     const uint32_t C = cur.z - prev.z;
@@ -291,16 +268,16 @@ __device__ inline uint32_t scan_u32(uint32_t v) {
 
 // ---- the whole sum on the device: NT lanes (the whole workgroup) -----------------------
 // L holds the lane's PT terms (elements PT*tid ..); p holds all n terms in
-// shared memory, read only by the plain-loop fallback (it runs after two
+// shared memory, read only by the plain-loop fallback (it runs after three
 // barriers, so p may be written right before the call). Every wave returns
 // the result; there is no barrier at the end unless the fallback ran.
 template <int NT>
 __device__ inline float sum_lanes(Lane<kMaxN / NT>& L, const float* p, int n, Shared& sm) {
     static_assert(NT == 256 || NT == 512 || NT == 1024, "256, 512 or 1024 lanes");
-    constexpr int PT = kMaxN / NT, W = NT / kWaveSize, cap = kMaxSerial / W;
+    constexpr int W = NT / kWaveSize;
     if (n <= 0) return 0.f;
     const int tid = int(threadIdx.x), lane = tid & (kWaveSize - 1), w = tid / kWaveSize;
-    const int i0 = tid * PT;
+    const int i0 = tid * (kMaxN / NT);
 
     // speculation: the lane sums, scanned in the wave, then the totals of the
     // waves before (left to right)
@@ -317,40 +294,47 @@ __device__ inline float sum_lanes(Lane<kMaxN / NT>& L, const float* p, int n, Sh
 
     lane_classify(L, pre, next);
 
-    // wave-local prefixes of the increments (mod 2^32) and serial counts
+    // wave-local prefixes of the increments (mod 2^32) and serial counts,
+    // then the wave totals' prefixes: every entry goes to its global place
     const uint32_t c = scan_u32(L.csum), m = scan_u32(L.cnt);
     if (lane == kWaveSize - 1) {
         sm.wc[w] = c;
         sm.wn[w] = m;
     }
-    lane_emit(L, i0, c - L.csum, m - L.cnt, w, cap, sm);
+    __syncthreads();
+    uint32_t nbase, cbase, nser, c_total;
+    wave_prefix<W>(sm, w, nbase, cbase, nser, c_total);
+    lane_emit(L, i0, cbase + c - L.csum, nbase + m - L.cnt, sm);
     __syncthreads();
 
     // the walk, in every wave: lane l prepares step base + l (steps past the
-    // last add +0 twice), then the chain runs 8 steps at a time with the step
-    // data read from fixed lanes, each lane keeping the chain values of its
-    // own step for the checks
-    Tables<W> T;
-    read_tables(sm, cap, T);
-    bool ok = !T.overflow;
+    // last add +0 twice), then the chain runs 8 steps at a time, the step data
+    // of the 8 read from their lanes first, each lane keeping the chain values
+    // of its own step for the checks
+    bool ok = nser <= uint32_t(kMaxSerial);
     float s = 0.f;
-    for (uint32_t base = 0; ok && base <= T.nser; base += kWaveSize) {
+    for (uint32_t base = 0; ok && base <= nser; base += kWaveSize) {
         const uint32_t r = base + uint32_t(lane);
         Step st{0.f, 0.f, 0, 0};
-        if (r <= T.nser) st = walk_entry(T, sm, cap, r, n);
-        const int cnt = int(min(uint32_t(kWaveSize), T.nser + 1 - base));
+        if (r <= nser) st = walk_entry(sm, nser, c_total, r, n);
+        const int cnt = int(min(uint32_t(kWaveSize), nser + 1 - base));
         const int ia = int(f32_bits(st.a)), iv = int(f32_bits(st.val));
         float my0 = 0.f, my1 = 0.f;  // the chain before this lane's step and after its run
         for (int l0 = 0; l0 < cnt; l0 += 8) {
+            float av[8], vv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                av[u] = bits_f32(uint32_t(__builtin_amdgcn_readlane(ia, l0 + u)));
+                vv[u] = bits_f32(uint32_t(__builtin_amdgcn_readlane(iv, l0 + u)));
+            }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int l = l0 + u;
-                const float a = bits_f32(uint32_t(__builtin_amdgcn_readlane(ia, l)));
-                const float v = bits_f32(uint32_t(__builtin_amdgcn_readlane(iv, l)));
-                const float s1 = s + a;
+                const float s1 = s + av[u];
                 my0 = lane == l ? s : my0;
                 my1 = lane == l ? s1 : my1;
-                s = s1 + v;
+                s = s1 + vv[u];
             }
         }
         const bool bad = lane < cnt && !step_ok(st, my0, my1);
@@ -390,7 +374,7 @@ __device__ inline float sum_nonneg_regs(const float (&v)[kMaxN / NT], float* p, 
 // ---- the same steps on the host, lane after lane, in the device's order -------------
 template <int NT = kThreads>
 inline float sum_nonneg_host(const float* p, int n, Shared& sm) {
-    constexpr int PT = kMaxN / NT, W = NT / kWaveSize, cap = kMaxSerial / W;
+    constexpr int PT = kMaxN / NT, W = NT / kWaveSize;
     if (n <= 0) return 0.f;
     static Lane<PT> L[NT];
     static float incl[NT], pre[NT], next[NT];
@@ -441,13 +425,16 @@ inline float sum_nonneg_host(const float* p, int n, Shared& sm) {
         sm.wc[w] = c[w * kWaveSize + kWaveSize - 1];
         sm.wn[w] = m[w * kWaveSize + kWaveSize - 1];
     }
-    for (int t = 0; t < NT; ++t) lane_emit(L[t], t * PT, c[t] - L[t].csum, m[t] - L[t].cnt, t / kWaveSize, cap, sm);
-    Tables<W> T;
-    read_tables(sm, cap, T);
-    bool ok = !T.overflow;
+    uint32_t nser = 0, c_total = 0;
+    for (int t = 0; t < NT; ++t) {
+        uint32_t nbase, cbase;
+        wave_prefix<W>(sm, t / kWaveSize, nbase, cbase, nser, c_total);
+        lane_emit(L[t], t * PT, cbase + c[t] - L[t].csum, nbase + m[t] - L[t].cnt, sm);
+    }
+    bool ok = nser <= uint32_t(kMaxSerial);
     float s = 0.f;
-    for (uint32_t r = 0; ok && r <= T.nser; ++r) {
-        const Step st = walk_entry(T, sm, cap, r, n);
+    for (uint32_t r = 0; ok && r <= nser; ++r) {
+        const Step st = walk_entry(sm, nser, c_total, r, n);
         const float s1 = s + st.a;
         ok = ok && step_ok(st, s, s1);
         s = s1 + st.val;

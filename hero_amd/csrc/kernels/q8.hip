@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
 #pragma unroll
         for (int k = 0; k < 16; ++k) sq[k] = xr[k] * xr[k];
         // terms holds the squares for the sum's plain-loop fallback, which ends
-        // with a barrier; otherwise nothing reads them after the sum's second
+        // with a barrier; otherwise nothing reads them after the sum's last
         // barrier, so the main loop may overwrite them at once
         const float ss = seqsum::sum_nonneg_regs<256>(sq, terms, K, sm);
         const float inv = 1.f / sqrtf(ss / float(K) + in.eps);

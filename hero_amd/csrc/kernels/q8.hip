@@ -697,7 +697,6 @@ __global__ __launch_bounds__(256) void gemm_q8_skinny_kernel(const int8_t* __res
     const __amdgpu_buffer_rsrc_t bw = buffer_of(wq, uint32_t(N) * uint32_t(K));
     const __amdgpu_buffer_rsrc_t bx = buffer_of(xq, uint32_t(M) * uint32_t(K));
     const __amdgpu_buffer_rsrc_t bd = buffer_of(wd, uint32_t(nb) * uint32_t(Npad) * 2u);
-    const __amdgpu_buffer_rsrc_t by = buffer_of(y, uint32_t(M) * uint32_t(N) * 4u);
     for (int e = tid; e < nb * 16; e += 256) {
         const int b = e >> 4, m = e & 15;
         dxs[b][m] = m < M ? xd[int64_t(m) * nb + b] : 0.f;
@@ -777,23 +776,140 @@ __global__ __launch_bounds__(256) void gemm_q8_skinny_kernel(const int8_t* __res
                 if (j < kc) acc = acc + tv[j];
             const bool last = r == rounds - 1;
             const int n = g * 16 + (tid & 15), m = tid >> 4;
-            const bool out = last && s < steps && m < M && n < N;
-            // the b32 buffer builtins move int: the float's bits go through unchanged
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, acc), by, out ? (uint32_t(m) * uint32_t(N) + uint32_t(n)) * 4u : kOOB, 0, 0);
+            if (last && s < steps && m < M && n < N) {
+                const int64_t o = int64_t(m) * N + n;
+                if constexpr (EPI == kEpiResidual)
+                    y[o] = resid[o] + acc;  // h = x + m (nm/src/qwen35.hpp:321)
+                else
+                    y[o] = acc;
+            }
             acc = last ? 0.f : acc;
             __syncthreads();
         }
     }
-    if constexpr (EPI == kEpiResidual) {
-        // y = r + acc for this workgroup's outputs (the same arithmetic as the
-        // reference's H = X + M); each lane reads back only what it stored
-        __threadfence();
-        for (int g = g_begin; g < g_end; ++g) {
-            const int n = g * 16 + (tid & 15), m = tid >> 4;
-            if (m < M && n < N) {
-                const int64_t o = int64_t(m) * N + n;
-                // aux 1 (sc0): past the L1, from L2 where the store landed
-                y[o] = resid[o] + __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(by, uint32_t(o) * 4u, 0, 1));
+}
+
+// The same for tall matrices (many 16-row groups): every workgroup is one wave and owns a contiguous range of 16-row weight
+// groups, walked in rounds of kSkwRound blocks with kSkwRing rounds of loads in
+// flight. A lane reads 16 bytes of a block pair (b, b+1) of weight row
+// n = lane % 16 and the same bytes of activation row m = lane % 16: lane group
+// q = 0 holds bytes 0-15 of b, q = 1 bytes 16-31 of b, q = 2 and 3 the same of
+// b+1. The MFMA sums over all four lane groups, so each block takes two MFMAs
+// (the low, then the high 8 bytes of each lane) with the activation operand
+// zeroed in the lane groups that hold the other block: the int32 result is
+// exactly that block's dot product, and lane (q, c) receives it for weight
+// rows n = 4q + r (r = 0..3) and activation row m = c. The lane turns them
+// into terms float(sumi) * (d_w * d_x) and adds each to the chain of its
+// (n, m) output in block order (the reference's order): four independent
+// chains per lane, all in registers, and no barrier in the loop.
+// ---------------------------------------------------------------------------
+constexpr int kSkwRound = 8;                    // blocks per round
+constexpr int kSkwPairs = kSkwRound / 2;         // 16-byte weight (and activation) loads per lane per round
+constexpr int kSkwMaxK = 16384;
+constexpr int kSkwRing = 3;                     // rounds in flight per wave
+// Every global access of the skinny kernel is a raw buffer access (kOOB),
+// so invalid rows, blocks and padded steps need no branch.
+
+struct SkwLoads {
+    v4b_t w[kSkwPairs];
+    v4b_t x[kSkwPairs];
+    v4b_t d;                   // weight scales: 8 rows (group q / 2 of the 16) of block c < kSkwRound of the round
+    v4b_t dx[kSkwRound / 4];    // activation scales of row c for the round's blocks
+};
+
+
+template <int EPI>
+__global__ __launch_bounds__(64) void gemm_q8_skinny_wave_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {
+    __shared__ __align__(16) uint16_t dws[kSkwRing][2][kSkwRound][8];  // a round's weight scales: [8-row group][block][row]
+    const int lane = threadIdx.x, q = lane >> 4, c = lane & 15;
+    const int nb = K >> 5, rounds = nb / kSkwRound;
+    const int groups = (N + 15) >> 4, G = gridDim.x;
+    const int g_begin = int(int64_t(groups) * blockIdx.x / G), g_end = int(int64_t(groups) * (blockIdx.x + 1) / G);
+    const int steps = (g_end - g_begin) * rounds;
+    const int steps_pad = (steps + kSkwRing - 1) / kSkwRing * kSkwRing;
+    const __amdgpu_buffer_rsrc_t bw = buffer_of(wq, uint32_t(N) * uint32_t(K));
+    const __amdgpu_buffer_rsrc_t bx = buffer_of(xq, uint32_t(M) * uint32_t(K));
+    const __amdgpu_buffer_rsrc_t bd = buffer_of(wd, uint32_t(nb) * uint32_t(Npad) * 2u);
+    const __amdgpu_buffer_rsrc_t bxd = buffer_of(xd, uint32_t(M) * uint32_t(nb) * 4u);
+
+    // the loads of one step (group, round) for this lane; past the last step
+    // (padding) every offset is out of range
+    auto load = [&](int step, SkwLoads& L) {
+        const int g = g_begin + step / rounds, r = step % rounds;
+        const bool on = step < steps;
+        const int n = g * 16 + c, b0 = r * kSkwRound;
+        const bool wrow = on && n < N, xrow = on && c < M;
+#pragma unroll
+        for (int i = 0; i < kSkwPairs; ++i) {
+            const uint32_t off = uint32_t(b0 + 2 * i) * 32u + 16u * uint32_t(q);
+            L.w[i] = __builtin_amdgcn_raw_buffer_load_b128(bw, wrow ? uint32_t(n) * uint32_t(K) + off : kOOB, 0, 0);
+            L.x[i] = __builtin_amdgcn_raw_buffer_load_b128(bx, xrow ? uint32_t(c) * uint32_t(K) + off : kOOB, 0, 0);
+        }
+        // 8 rows x block b0 + c of 8-row group 2g + q / 2 (16 bytes; lanes q
+        // and q ^ 1 read the same)
+        const bool drow = on && c < kSkwRound && g * 16 + 8 * (q >> 1) < N;
+        L.d = __builtin_amdgcn_raw_buffer_load_b128(bd, drow ? uint32_t(scale_index(g * 16 + 8 * (q >> 1), b0 + c, nb)) * 2u : kOOB, 0, 0);
+#pragma unroll
+        for (int i = 0; i < kSkwRound / 4; ++i)
+            L.dx[i] = __builtin_amdgcn_raw_buffer_load_b128(bxd, xrow ? (uint32_t(c) * uint32_t(nb) + uint32_t(b0 + 4 * i)) * 4u : kOOB, 0, 0);
+    };
+
+    SkwLoads ring[kSkwRing];
+#pragma unroll
+    for (int k = 0; k < kSkwRing; ++k) load(k, ring[k]);
+
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // outputs (n = g*16 + 4q + r, m = c)
+    for (int s0 = 0; s0 < steps_pad; s0 += kSkwRing) {
+#pragma unroll
+        for (int k = 0; k < kSkwRing; ++k) {
+            const int s = s0 + k;
+            const int g = g_begin + s / rounds, r = s % rounds;
+            // the round's weight scales through shared memory: lane (q, c < kSkwRound)
+            // stores block c's 8 rows of its group; block j's rows 4q .. 4q+3
+            // are then 8 bytes at [q / 2][j][4 (q % 2)]
+            // (one wave: its shared-memory accesses take effect in order)
+            if ((q & 1) == 0 && c < kSkwRound) *reinterpret_cast<v4b_t*>(&dws[k][q >> 1][c][0]) = ring[k].d;
+            const bool first = q < 2;  // lane groups 0, 1 hold block b; 2, 3 hold block b+1
+#pragma unroll
+            for (int i = 0; i < kSkwPairs; ++i) {
+                const long wl = lo64(ring[k].w[i]), wh = hi64(ring[k].w[i]);
+                const long xl = lo64(ring[k].x[i]), xh = hi64(ring[k].x[i]);
+                const v4i_t zero = {0, 0, 0, 0};
+                v4i_t c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(wl, first ? xl : 0L, zero, 0, 0, 0);
+                c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(wh, first ? xh : 0L, c0, 0, 0, 0);
+                v4i_t c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(wl, first ? 0L : xl, zero, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(wh, first ? 0L : xh, c1, 0, 0, 0);
+                const v4b_t dx4 = ring[k].dx[i / 2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int j = 2 * i + h;  // block within the round
+                    const v4i_t& cc = h ? c1 : c0;
+                    const uint2 d2 = *reinterpret_cast<const uint2*>(&dws[k][q >> 1][j][4 * (q & 1)]);
+                    const float dx = __builtin_bit_cast(float, (j & 3) == 0 ? dx4.x : (j & 3) == 1 ? dx4.y : (j & 3) == 2 ? dx4.z : dx4.w);
+                    acc[0] = acc[0] + float(cc[0]) * (half_bits_to_f32(uint16_t(d2.x & 0xFFFFu)) * dx);
+                    acc[1] = acc[1] + float(cc[1]) * (half_bits_to_f32(uint16_t(d2.x >> 16)) * dx);
+                    acc[2] = acc[2] + float(cc[2]) * (half_bits_to_f32(uint16_t(d2.y & 0xFFFFu)) * dx);
+                    acc[3] = acc[3] + float(cc[3]) * (half_bits_to_f32(uint16_t(d2.y >> 16)) * dx);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // pair by pair: few MFMA results live at once
+            }
+            // the slot's next loads after its last use (keeps one set of ring registers)
+            __builtin_amdgcn_sched_barrier(0);
+            load(s + kSkwRing, ring[k]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (r == rounds - 1 && s < steps) {  // the group's outputs
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int n = g * 16 + 4 * q + rr;
+                    if (n < N && c < M) {
+                        const int64_t o = int64_t(c) * N + n;
+                        if constexpr (EPI == kEpiResidual)
+                            y[o] = resid[o] + acc[rr];  // h = x + m (nm/src/qwen35.hpp:321)
+                        else
+                            y[o] = acc[rr];
+                    }
+                    acc[rr] = 0.f;
+                }
             }
         }
     }
@@ -816,14 +932,27 @@ void launch_gemm_q8(const void* packed, const void* act, float* y, const float* 
     const int8_t* xq = static_cast<const int8_t*>(act);
     const float* xd = reinterpret_cast<const float*>(xq + M * K);
     const int Npad = int(packed_rows_pad(N));
-    if (M <= 16 && K % 256 == 0 && K <= kSkMaxK && N * K < (int64_t(1) << 31)) {
-        const int64_t groups = (N + 15) / 16;
-        const unsigned G = unsigned(std::min<int64_t>(3 * device_cus(), groups));
+    const int64_t groups = (N + 15) / 16;
+    // as many workgroups as are resident at once: a second wave of
+    // workgroups would run after the first
+    auto grid_for = [&](auto kernel, int threads, size_t smem) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, smem) != hipSuccess || per_cu <= 0) per_cu = 1;
+        return unsigned(std::min<int64_t>(int64_t(per_cu) * device_cus(), groups));
+    };
+    if (M <= 16 && groups >= 2 * device_cus() && K % (32 * kSkwRound) == 0 && K <= kSkwMaxK && N * K < (int64_t(1) << 31)) {
+        // tall: a wave per group range, every chain in registers
+        if (epi == kEpiResidual)
+            hipLaunchKernelGGL(gemm_q8_skinny_wave_kernel<kEpiResidual>, dim3(grid_for(gemm_q8_skinny_wave_kernel<kEpiResidual>, 64, 0)), dim3(64), 0, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
+        else
+            hipLaunchKernelGGL(gemm_q8_skinny_wave_kernel<kEpiStore>, dim3(grid_for(gemm_q8_skinny_wave_kernel<kEpiStore>, 64, 0)), dim3(64), 0, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
+    } else if (M <= 16 && K % 256 == 0 && K <= kSkMaxK && N * K < (int64_t(1) << 31)) {
+        // few groups: four waves share each group's blocks
         const size_t smem = size_t(K / 32) * 16 * 4;  // the activation scales
         if (epi == kEpiResidual)
-            hipLaunchKernelGGL(gemm_q8_skinny_kernel<kEpiResidual>, dim3(G), dim3(256), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
+            hipLaunchKernelGGL(gemm_q8_skinny_kernel<kEpiResidual>, dim3(grid_for(gemm_q8_skinny_kernel<kEpiResidual>, 256, smem)), dim3(256), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
         else
-            hipLaunchKernelGGL(gemm_q8_skinny_kernel<kEpiStore>, dim3(G), dim3(256), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
+            hipLaunchKernelGGL(gemm_q8_skinny_kernel<kEpiStore>, dim3(grid_for(gemm_q8_skinny_kernel<kEpiStore>, 256, smem)), dim3(256), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
     } else {
         // the tallest tile that still gives every CU two workgroups (the fp32
         // term work per CU is the same; more workgroups hide more latency)

@@ -183,7 +183,10 @@ def test_rmsnorm_gate_up_swiglu_matches_oracle_bytes(lib, ff):
 @pytest.mark.parametrize("m,n,k", [(16, 4096, 4096), (64, 1000, 1024), (5, 96, 12288), (130, 4100, 4096), (33, 64, 2816), (1, 64, 256),
                                    # the skinny path (M <= 16): ragged 16-row groups, a partial round
                                    # (768 = 24 blocks), fewer rows than one group, the largest K
-                                   (2, 4100, 4096), (8, 33, 12288), (16, 1003, 768), (13, 12288, 4096), (3, 7, 256), (16, 40, 16384)])
+                                   (2, 4100, 4096), (8, 33, 12288), (16, 1003, 768), (13, 12288, 4096), (3, 7, 256), (16, 40, 16384),
+                                   # its one-wave form for tall matrices (at least two 16-row groups per CU):
+                                   # a ragged last group, K = 12288
+                                   (16, 8200, 4096), (7, 9000, 12288)])
 def test_gemm_matches_oracle_bitwise(lib, m, n, k):
     """M-row GEMM on int8 MFMA: every element equals the reference's matmul
     (per-row vec_dot in block order), with and without the residual."""

@@ -651,9 +651,10 @@ __global__ __launch_bounds__(256) void gemm_q8_kernel(const int8_t* __restrict__
 // streamed once, as in the GEMV, and each block's int32 sums come from the
 // int8 MFMA 16x16x32 (16 activation rows x 16 weight rows x 32 k).
 //
-// A workgroup owns a contiguous range of 16-row weight groups and walks each
-// in rounds of kSkRound blocks; each of the four waves takes 8 blocks of a
-// round. A lane reads 16 bytes of a block pair (b, b+1): lane group q = 0
+// A workgroup of NW waves owns a contiguous range of 16-row weight groups
+// and walks each in rounds of kSkRound blocks; each wave takes kSkRound / NW
+// blocks of a round (more waves for fewer groups: the rounds are what take
+// the time). A lane reads 16 bytes of a block pair (b, b+1): lane group q = 0
 // holds bytes 0-15 of b, q = 1 bytes 16-31 of b, q = 2 and 3 the same of
 // b+1, for weight row n = lane % 16 and activation row m = lane % 16. The
 // MFMA sums over all four lane groups, so each block takes two MFMAs (the
@@ -666,27 +667,29 @@ __global__ __launch_bounds__(256) void gemm_q8_kernel(const int8_t* __restrict__
 // stores y. A ring of kSkRing rounds of loads stays in flight.
 // ---------------------------------------------------------------------------
 constexpr int kSkRound = 32;                   // blocks per round
-constexpr int kSkWaveBlocks = kSkRound / 4;    // blocks per wave per round
-constexpr int kSkPairs = kSkWaveBlocks / 2;    // 16-byte loads per lane per round
 constexpr int kSkMaxK = 16384;
 constexpr int kSkRing = 3;                     // steps (group, round) in flight per lane
 // Every global access of the skinny kernel is a raw buffer access (kOOB),
 // so invalid rows, blocks and padded steps need no branch.
 
+template <int P>  // block pairs per wave per round
 struct SkLoads {
-    v4b_t w[kSkPairs];
-    v4b_t x[kSkPairs];
-    uint32_t d;  // two weight scales of the wave's 8 blocks x 16 rows (see load)
+    v4b_t w[P];
+    v4b_t x[P];
+    uint32_t d;  // two weight scales of the wave's blocks x 16 rows (see load)
 };
 
 __device__ __forceinline__ long lo64(v4b_t v) { return long((uint64_t(uint32_t(v.y)) << 32) | uint32_t(v.x)); }
 __device__ __forceinline__ long hi64(v4b_t v) { return long((uint64_t(uint32_t(v.w)) << 32) | uint32_t(v.z)); }
 
-template <int EPI>
-__global__ __launch_bounds__(256) void gemm_q8_skinny_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {
+template <int EPI, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_q8_skinny_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {
     __shared__ __align__(16) float terms[kSkRound][256];   // [block of the round][16 m + n]
     extern __shared__ __align__(16) float dxs_raw[];        // [block][m] activation scales, 0 for m >= M
     float (*dxs)[16] = reinterpret_cast<float (*)[16]>(dxs_raw);
+    constexpr int kSkWaveBlocks = kSkRound / NW;  // blocks per wave per round
+    constexpr int kSkPairs = kSkWaveBlocks / 2;   // 16-byte loads per lane per round
+    static_assert(NW >= 4 && kSkPairs >= 1, "4 to 16 waves");
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int q = lane >> 4, c = lane & 15;
     const int nb = K >> 5, rounds = (nb + kSkRound - 1) / kSkRound;
@@ -697,14 +700,14 @@ __global__ __launch_bounds__(256) void gemm_q8_skinny_kernel(const int8_t* __res
     const __amdgpu_buffer_rsrc_t bw = buffer_of(wq, uint32_t(N) * uint32_t(K));
     const __amdgpu_buffer_rsrc_t bx = buffer_of(xq, uint32_t(M) * uint32_t(K));
     const __amdgpu_buffer_rsrc_t bd = buffer_of(wd, uint32_t(nb) * uint32_t(Npad) * 2u);
-    for (int e = tid; e < nb * 16; e += 256) {
+    for (int e = tid; e < nb * 16; e += 64 * NW) {
         const int b = e >> 4, m = e & 15;
         dxs[b][m] = m < M ? xd[int64_t(m) * nb + b] : 0.f;
     }
 
     // the loads of one step (group, round) for this lane; past the last step
     // (padding) every offset is out of range
-    auto load = [&](int step, SkLoads& L) {
+    auto load = [&](int step, SkLoads<kSkPairs>& L) {
         const int g = g_begin + step / rounds, r = step % rounds;
         const int n = g * 16 + c;
         const int b0 = r * kSkRound + wv * kSkWaveBlocks;
@@ -726,7 +729,7 @@ __global__ __launch_bounds__(256) void gemm_q8_skinny_kernel(const int8_t* __res
 
     // a ring of kSkRing steps in flight; slot k is refilled with step s + kSkRing
     // as soon as step s has been consumed
-    SkLoads ring[kSkRing];
+    SkLoads<kSkPairs> ring[kSkRing];
 #pragma unroll
     for (int k = 0; k < kSkRing; ++k) load(k, ring[k]);
     __syncthreads();  // dxs
@@ -768,15 +771,17 @@ __global__ __launch_bounds__(256) void gemm_q8_skinny_kernel(const int8_t* __res
             load(s + kSkRing, ring[k]);
             __syncthreads();
             const int kc = min(kSkRound, nb - r * kSkRound);
-            float tv[kSkRound];  // every read first, then the chain: lane tid = 16 m + n
+            if (tid < 256) {  // the chains: lane tid = 16 m + n, every read first
+                float tv[kSkRound];
 #pragma unroll
-            for (int j = 0; j < kSkRound; ++j) tv[j] = terms[j][tid];
+                for (int j = 0; j < kSkRound; ++j) tv[j] = terms[j][tid];
 #pragma unroll
-            for (int j = 0; j < kSkRound; ++j)
-                if (j < kc) acc = acc + tv[j];
+                for (int j = 0; j < kSkRound; ++j)
+                    if (j < kc) acc = acc + tv[j];
+            }
             const bool last = r == rounds - 1;
             const int n = g * 16 + (tid & 15), m = tid >> 4;
-            if (last && s < steps && m < M && n < N) {
+            if (tid < 256 && last && s < steps && m < M && n < N) {
                 const int64_t o = int64_t(m) * N + n;
                 if constexpr (EPI == kEpiResidual)
                     y[o] = resid[o] + acc;  // h = x + m (nm/src/qwen35.hpp:321)
@@ -947,12 +952,13 @@ void launch_gemm_q8(const void* packed, const void* act, float* y, const float* 
         else
             hipLaunchKernelGGL(gemm_q8_skinny_wave_kernel<kEpiStore>, dim3(grid_for(gemm_q8_skinny_wave_kernel<kEpiStore>, 64, 0)), dim3(64), 0, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
     } else if (M <= 16 && K % 256 == 0 && K <= kSkMaxK && N * K < (int64_t(1) << 31)) {
-        // few groups: four waves share each group's blocks
+        // few groups: sixteen waves share each group's blocks
+        constexpr int NW = 16;
         const size_t smem = size_t(K / 32) * 16 * 4;  // the activation scales
         if (epi == kEpiResidual)
-            hipLaunchKernelGGL(gemm_q8_skinny_kernel<kEpiResidual>, dim3(grid_for(gemm_q8_skinny_kernel<kEpiResidual>, 256, smem)), dim3(256), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
+            hipLaunchKernelGGL((gemm_q8_skinny_kernel<kEpiResidual, NW>), dim3(grid_for(gemm_q8_skinny_kernel<kEpiResidual, NW>, 64 * NW, smem)), dim3(64 * NW), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
         else
-            hipLaunchKernelGGL(gemm_q8_skinny_kernel<kEpiStore>, dim3(grid_for(gemm_q8_skinny_kernel<kEpiStore>, 256, smem)), dim3(256), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
+            hipLaunchKernelGGL((gemm_q8_skinny_kernel<kEpiStore, NW>), dim3(grid_for(gemm_q8_skinny_kernel<kEpiStore, NW>, 64 * NW, smem)), dim3(64 * NW), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
     } else {
         // the tallest tile that still gives every CU two workgroups (the fp32
         // term work per CU is the same; more workgroups hide more latency)

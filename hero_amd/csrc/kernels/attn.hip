@@ -691,35 +691,43 @@ __global__ __launch_bounds__(kSpvThreads) void attn_softmax_pv_kernel(AttnDecode
 }
 
 // The same sum for many sequences at once (where the per-head workgroups above
-// would outnumber the CUs several times): a workgroup per (sequence, query
-// head, 32 channels) whose 256 lanes stream the V rows through a ring of
-// register tiles into two shared-memory tiles, 32 chain lanes multiplying and
-// adding from shared memory; small shared memory, so many fit per CU.
+// would outnumber the CUs several times): a workgroup per (sequence, K/V head,
+// up to four query heads of its group, 32 channels) whose 256 lanes stream
+// the V rows through a ring of register tiles into two shared-memory tiles
+// that all of its query heads read (one V read for the group's heads), lane
+// 32 hh + c multiplying and adding channel c of head hh from shared memory;
+// small shared memory, so many fit per CU.
 constexpr int kPvbSplit = 4;
 constexpr int kPvbCh = kAttnDim / kPvbSplit;                  // 32
 constexpr int kPvbThreads = 256;
+constexpr int kPvbHeads = 4;                                  // query heads per workgroup
 constexpr int kPvbTile = 128;                                // rows per tile
 constexpr int kPvbVec = kPvbTile * kPvbCh / 4 / kPvbThreads;    // float4 per lane per tile
+constexpr int kPvbAlpha = kPvbHeads * kPvbTile / kPvbThreads;   // weights per lane per tile
 constexpr int kPvbRing = 4;                                  // tiles in flight
 
 __global__ __launch_bounds__(kPvbThreads) void attn_pv_batch_kernel(AttnDecodeArgs a) {
-    const int tid = threadIdx.x, h = blockIdx.x / kPvbSplit, part = blockIdx.x % kPvbSplit, b = blockIdx.y;
+    const int tid = threadIdx.x, b = blockIdx.y;
+    const int group = a.Hq / a.Hkv, nchunk = (group + kPvbHeads - 1) / kPvbHeads;
+    const int part = int(blockIdx.x) % kPvbSplit, gc = int(blockIdx.x) / kPvbSplit;
+    const int g = gc / nchunk, h0 = g * group + (gc % nchunk) * kPvbHeads;
+    const int nh = min(kPvbHeads, g * group + group - h0);
     const int pos = a.positions[b];
     if (pos < 0 || pos >= a.max_ctx) return;
-    const int g = h / (a.Hq / a.Hkv);
     const int first = visible_first(pos, a.window);
     const int n = pos + 1 - first;
-    const float* alpha = a.scores + (int64_t(b) * a.Hq + h) * a.max_ctx;
+    const float* alpha = a.scores + (int64_t(b) * a.Hq + h0) * a.max_ctx;  // head h0 + hh at hh * max_ctx
     const int64_t kw = int64_t(a.Hkv) * kAttnDim;
     const float* vb = a.v_cache + (cache_of(a, b) * a.max_ctx + first) * kw + int64_t(g) * kAttnDim + part * kPvbCh;
     __shared__ __align__(16) float vt[2][kPvbTile * kPvbCh];
-    __shared__ float at[2][kPvbTile];
+    __shared__ float at[2][kPvbHeads][kPvbTile];
     const int ntiles = (n + kPvbTile - 1) / kPvbTile;
 
     float4 ring[kPvbRing][kPvbVec];
-    float aring[kPvbRing];
-    // lane slot k of a tile: float4 q = tid + k*256 -> row q/8, channels 4*(q%8)..+3
-    auto load = [&](int tile, float4* dst, float& adst) {
+    float aring[kPvbRing][kPvbAlpha];
+    // lane slot k of a tile: float4 q = tid + k*256 -> row q/8, channels
+    // 4*(q%8)..+3; weight slot k: e = tid + k*256 -> head e / 128, row e % 128
+    auto load = [&](int tile, float4* dst, float* adst) {
         const int r0 = tile * kPvbTile;
 #pragma unroll
         for (int k = 0; k < kPvbVec; ++k) {
@@ -727,12 +735,18 @@ __global__ __launch_bounds__(kPvbThreads) void attn_pv_batch_kernel(AttnDecodeAr
             const int row = r0 + q / (kPvbCh / 4);
             dst[k] = row < n ? *reinterpret_cast<const float4*>(vb + int64_t(row) * kw + 4 * (q % (kPvbCh / 4))) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        adst = (tid < kPvbTile && r0 + tid < n) ? alpha[r0 + tid] : 0.f;
+#pragma unroll
+        for (int k = 0; k < kPvbAlpha; ++k) {
+            const int e = tid + k * kPvbThreads, hh = e / kPvbTile, r = r0 + e % kPvbTile;
+            adst[k] = (hh < nh && r < n) ? alpha[int64_t(hh) * a.max_ctx + r] : 0.f;
+        }
     };
 #pragma unroll
     for (int s = 0; s < kPvbRing; ++s)
         if (s < ntiles) load(s, ring[s], aring[s]);
 
+    const int hh = tid / kPvbCh, c = tid % kPvbCh;  // chain lanes: tid < 32 * nh
+    const bool chain = hh < nh;
     float acc = 0.f;
     for (int base = 0; base < ntiles; base += kPvbRing) {
 #pragma unroll
@@ -740,36 +754,40 @@ __global__ __launch_bounds__(kPvbThreads) void attn_pv_batch_kernel(AttnDecodeAr
             const int tile = base + s;
             if (tile >= ntiles) break;
             float* buf = vt[tile & 1];
-            float* abuf = at[tile & 1];
 #pragma unroll
             for (int k = 0; k < kPvbVec; ++k) reinterpret_cast<float4*>(buf)[tid + k * kPvbThreads] = ring[s][k];
-            if (tid < kPvbTile) abuf[tid] = aring[s];
+#pragma unroll
+            for (int k = 0; k < kPvbAlpha; ++k) {
+                const int e = tid + k * kPvbThreads;
+                at[tile & 1][e / kPvbTile][e % kPvbTile] = aring[s][k];
+            }
             // one barrier per tile: the other buffer's readers finished before it
             __syncthreads();
             if (tile + kPvbRing < ntiles) load(tile + kPvbRing, ring[s], aring[s]);
-            if (tid < kPvbCh) {
+            if (chain) {
+                const float* abuf = at[tile & 1][hh];
                 const int rows = min(kPvbTile, n - tile * kPvbTile);
 #pragma unroll 16
-                for (int r = 0; r < rows; ++r) acc += abuf[r] * buf[r * kPvbCh + tid];
+                for (int r = 0; r < rows; ++r) acc += abuf[r] * buf[r * kPvbCh + c];
             }
         }
     }
 
-    if (tid < kPvbCh) {
-        const int c = part * kPvbCh + tid;
-        const float gate = a.proj[int64_t(b) * a.proj_stride + int64_t(h) * 2 * kAttnDim + kAttnDim + c];
+    if (chain) {
+        const int h = h0 + hh, ch = part * kPvbCh + c;
+        const float gate = a.proj[int64_t(b) * a.proj_stride + int64_t(h) * 2 * kAttnDim + kAttnDim + ch];
         const float out = acc * sigmoid_f32(gate);
         const int64_t width = int64_t(a.Hq) * kAttnDim;
-        const int64_t idx = int64_t(h) * kAttnDim + c;
+        const int64_t idx = int64_t(h) * kAttnDim + ch;
         if (a.out_f32) a.out_f32[int64_t(b) * width + idx] = out;
         float amax = fabsf(out);
-        for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+        for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
         const float d = amax / 127.f;
         const float id = d != 0.f ? 1.f / d : 0.f;
         int8_t* qs = static_cast<int8_t*>(a.act_out);
         float* qd = reinterpret_cast<float*>(qs + int64_t(a.B) * width);
         qs[int64_t(b) * width + idx] = int8_t(int(roundf(out * id)));
-        if (tid == 0) qd[(int64_t(b) * width + idx) >> 5] = half_bits_to_f32(fp32_to_fp16_ref(d));
+        if (c == 0) qd[(int64_t(b) * width + idx) >> 5] = half_bits_to_f32(fp32_to_fp16_ref(d));
     }
 }
 
@@ -1017,7 +1035,7 @@ void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
     else if (pv_blocks <= 2 * device_cus())
         hipLaunchKernelGGL(attn_pv_kernel<7>, pv_grid, dim3(kPvThreads), pv_shared_bytes(7), s, a);
     else
-        hipLaunchKernelGGL(attn_pv_batch_kernel, dim3(unsigned(a.Hq * kPvbSplit), unsigned(a.B)), dim3(kPvbThreads), 0, s, a);
+        hipLaunchKernelGGL(attn_pv_batch_kernel, dim3(unsigned(a.Hkv * ((group + kPvbHeads - 1) / kPvbHeads) * kPvbSplit), unsigned(a.B)), dim3(kPvbThreads), 0, s, a);
 }
 
 }  // namespace hero

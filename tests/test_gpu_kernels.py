@@ -542,8 +542,10 @@ def test_attn_decode_matches_oracle(lib, window):
 # long contexts over pre-filled caches: several tiles of the weighted sum
 # (64 rows each, a ring of 6), score tiles of 256 keys, GQA groups of 1, 4 and
 # 6 (score head chunks of 4 and 2), a sliding window, and enough sequences x
-# heads to take the many-sequence form of the weighted sum (B * Hq * 4 > 512)
-@pytest.mark.parametrize("B,hq,hkv,pos,window", [(2, 8, 2, 700, 0), (1, 6, 1, 1500, 0), (2, 4, 4, 450, 300), (5, 32, 8, 333, 0)])
+# heads to take the many-sequence form of the weighted sum (B * Hq * 4 > 512),
+# whose workgroups serve up to four heads of a group (6 = one of 4, one of 2)
+@pytest.mark.parametrize("B,hq,hkv,pos,window", [(2, 8, 2, 700, 0), (1, 6, 1, 1500, 0), (2, 4, 4, 450, 300), (5, 32, 8, 333, 0),
+                                                 (12, 12, 2, 260, 0)])
 def test_attn_decode_long_context_matches_oracle(lib, B, hq, hkv, pos, window):
     from hero_amd._lib import AttnDecodeArgs
 

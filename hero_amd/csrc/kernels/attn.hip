@@ -693,10 +693,11 @@ __global__ __launch_bounds__(kSpvThreads) void attn_softmax_pv_kernel(AttnDecode
 // The same sum for many sequences at once (where the per-head workgroups above
 // would outnumber the CUs several times): a workgroup per (sequence, K/V head,
 // up to four query heads of its group, 32 channels) whose 256 lanes stream
-// the V rows through a ring of register tiles into two shared-memory tiles
-// that all of its query heads read (one V read for the group's heads), lane
-// 32 hh + c multiplying and adding channel c of head hh from shared memory;
-// small shared memory, so many fit per CU.
+// the V rows through a ring of register tiles into two channel-major
+// shared-memory tiles that all of its query heads read (one V read for the
+// group's heads), lane 32 hh + c multiplying and adding channel c of head hh
+// from shared memory, four rows per read; small shared memory, so many fit
+// per CU.
 constexpr int kPvbSplit = 4;
 constexpr int kPvbCh = kAttnDim / kPvbSplit;                  // 32
 constexpr int kPvbThreads = 256;
@@ -705,6 +706,7 @@ constexpr int kPvbTile = 128;                                // rows per tile
 constexpr int kPvbVec = kPvbTile * kPvbCh / 4 / kPvbThreads;    // float4 per lane per tile
 constexpr int kPvbAlpha = kPvbHeads * kPvbTile / kPvbThreads;   // weights per lane per tile
 constexpr int kPvbRing = 4;                                  // tiles in flight
+constexpr int kPvbLd = kPvbTile + 4;                         // channel stride in a tile (16-byte rows, 2-way stores)
 
 __global__ __launch_bounds__(kPvbThreads) void attn_pv_batch_kernel(AttnDecodeArgs a) {
     const int tid = threadIdx.x, b = blockIdx.y;
@@ -719,26 +721,27 @@ __global__ __launch_bounds__(kPvbThreads) void attn_pv_batch_kernel(AttnDecodeAr
     const float* alpha = a.scores + (int64_t(b) * a.Hq + h0) * a.max_ctx;  // head h0 + hh at hh * max_ctx
     const int64_t kw = int64_t(a.Hkv) * kAttnDim;
     const float* vb = a.v_cache + (cache_of(a, b) * a.max_ctx + first) * kw + int64_t(g) * kAttnDim + part * kPvbCh;
-    __shared__ __align__(16) float vt[2][kPvbTile * kPvbCh];
-    __shared__ float at[2][kPvbHeads][kPvbTile];
+    __shared__ __align__(16) float vt[2][kPvbCh * kPvbLd];  // [channel][row]
+    __shared__ __align__(16) float at[2][kPvbHeads][kPvbTile];
     const int ntiles = (n + kPvbTile - 1) / kPvbTile;
 
     float4 ring[kPvbRing][kPvbVec];
     float aring[kPvbRing][kPvbAlpha];
     // lane slot k of a tile: float4 q = tid + k*256 -> row q/8, channels
-    // 4*(q%8)..+3; weight slot k: e = tid + k*256 -> head e / 128, row e % 128
+    // 4*(q%8)..+3; weight slot k: e = tid + k*256 -> head e / 128, row e % 128;
+    // rows clamped to n - 1 and heads to nh - 1 (never used past the end)
     auto load = [&](int tile, float4* dst, float* adst) {
         const int r0 = tile * kPvbTile;
 #pragma unroll
         for (int k = 0; k < kPvbVec; ++k) {
             const int q = tid + k * kPvbThreads;
-            const int row = r0 + q / (kPvbCh / 4);
-            dst[k] = row < n ? *reinterpret_cast<const float4*>(vb + int64_t(row) * kw + 4 * (q % (kPvbCh / 4))) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const int row = min(r0 + q / (kPvbCh / 4), n - 1);
+            dst[k] = *reinterpret_cast<const float4*>(vb + int64_t(row) * kw + 4 * (q % (kPvbCh / 4)));
         }
 #pragma unroll
         for (int k = 0; k < kPvbAlpha; ++k) {
-            const int e = tid + k * kPvbThreads, hh = e / kPvbTile, r = r0 + e % kPvbTile;
-            adst[k] = (hh < nh && r < n) ? alpha[int64_t(hh) * a.max_ctx + r] : 0.f;
+            const int e = tid + k * kPvbThreads, hh = min(e / kPvbTile, nh - 1), r = min(r0 + e % kPvbTile, n - 1);
+            adst[k] = alpha[int64_t(hh) * a.max_ctx + r];
         }
     };
 #pragma unroll
@@ -755,7 +758,13 @@ __global__ __launch_bounds__(kPvbThreads) void attn_pv_batch_kernel(AttnDecodeAr
             if (tile >= ntiles) break;
             float* buf = vt[tile & 1];
 #pragma unroll
-            for (int k = 0; k < kPvbVec; ++k) reinterpret_cast<float4*>(buf)[tid + k * kPvbThreads] = ring[s][k];
+            for (int k = 0; k < kPvbVec; ++k) {
+                const int q = tid + k * kPvbThreads, row = q / (kPvbCh / 4), c0 = 4 * (q % (kPvbCh / 4));
+                buf[(c0 + 0) * kPvbLd + row] = ring[s][k].x;
+                buf[(c0 + 1) * kPvbLd + row] = ring[s][k].y;
+                buf[(c0 + 2) * kPvbLd + row] = ring[s][k].z;
+                buf[(c0 + 3) * kPvbLd + row] = ring[s][k].w;
+            }
 #pragma unroll
             for (int k = 0; k < kPvbAlpha; ++k) {
                 const int e = tid + k * kPvbThreads;
@@ -765,10 +774,43 @@ __global__ __launch_bounds__(kPvbThreads) void attn_pv_batch_kernel(AttnDecodeAr
             __syncthreads();
             if (tile + kPvbRing < ntiles) load(tile + kPvbRing, ring[s], aring[s]);
             if (chain) {
+                // 16 rows at a time from two register sets (4 weight reads,
+                // 4 V reads each), the next 16 rows' reads issued before the
+                // current ones chain (scheduling barriers keep them there) so
+                // that each chain waits for its own set only. Fetches are
+                // unconditional (rows clamped into the tile; one past the last
+                // group goes unused).
                 const float* abuf = at[tile & 1][hh];
-                const int rows = min(kPvbTile, n - tile * kPvbTile);
-#pragma unroll 16
-                for (int r = 0; r < rows; ++r) acc += abuf[r] * buf[r * kPvbCh + c];
+                const float* vcol = buf + c * kPvbLd;
+                const int rows = min(kPvbTile, n - tile * kPvbTile), full = rows & ~15;
+                float4 s0[8], s1[8];
+                auto fetch = [&](int r0, float4 (&d)[8]) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        d[i] = *reinterpret_cast<const float4*>(abuf + r0 + 4 * i);
+                        d[4 + i] = *reinterpret_cast<const float4*>(vcol + r0 + 4 * i);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                };
+                auto chain16 = [&](const float4 (&d)[8]) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        acc += d[i].x * d[4 + i].x;
+                        acc += d[i].y * d[4 + i].y;
+                        acc += d[i].z * d[4 + i].z;
+                        acc += d[i].w * d[4 + i].w;
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                };
+                fetch(0, s0);
+                for (int r0 = 0; r0 < full; r0 += 32) {
+                    fetch(min(r0 + 16, kPvbTile - 16), s1);
+                    chain16(s0);
+                    if (r0 + 16 >= full) break;
+                    fetch(min(r0 + 32, kPvbTile - 16), s0);
+                    chain16(s1);
+                }
+                for (int r = full; r < rows; ++r) acc += abuf[r] * vcol[r];
             }
         }
     }

@@ -25,6 +25,12 @@ int device_cus();  // compute units of the current device (cached per device)
 __host__ __device__ inline int64_t scale_index(int64_t row, int64_t block, int64_t nb) { return ((row >> 3) * nb + block) * 8 + (row & 7); }
 inline int64_t packed_q8_bytes(int64_t N, int64_t K) { return N * K + packed_rows_pad(N) * (K / 32) * 2; }
 inline int64_t act_q8_bytes(int64_t M, int64_t K) { return M * K + M * (K / 32) * 4; }
+// K-quants (kquant.hip): Q8_K activations (292 bytes per 256) and the Q4_K
+// (type 12) / Q6_K (type 14) products over GGUF-layout weights
+int64_t act_q8_K_bytes(int64_t m, int64_t k);
+int kquant_rows_per_group(int type, int64_t K);  // output rows per workgroup (0: K too large)
+void launch_quantize_q8_K(const float* x, void* act, int64_t M, int64_t K, hipStream_t s);
+void launch_kquant_gemm(int type, const void* w, const void* act, float* y, int64_t M, int64_t N, int64_t K, hipStream_t s);
 
 // q8.hip
 void launch_quantize_act(const float* x, void* act, int64_t M, int64_t K, hipStream_t s);

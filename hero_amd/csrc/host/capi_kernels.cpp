@@ -56,6 +56,32 @@ int hero_q8_0_quantize(const float* x, void* act, int64_t m, int64_t k, void* st
     });
 }
 
+int64_t hero_q8_K_act_bytes(int64_t m, int64_t k) { return act_q8_K_bytes(m, k); }
+
+int hero_q8_K_quantize(const float* x, void* act, int64_t m, int64_t k, void* stream) {
+    return guard([&] {
+        require(m > 0 && k > 0 && k % 256 == 0, "K must be a positive multiple of 256 (Q8_K block)");
+        require(m * (k / 256) <= (int64_t(1) << 31), "shape too large");
+        require(x && act, "null pointer");
+        require(aligned(x, 16) && aligned(act, 16), "x and act must be 16-byte aligned");
+        launch_quantize_q8_K(x, act, m, k, as_stream(stream));
+        check_launch("hero_q8_K_quantize");
+    });
+}
+
+int hero_kquant_gemm(int32_t type, const void* w, const void* act, float* y, int64_t m, int64_t n, int64_t k, void* stream) {
+    return guard([&] {
+        require(type == 12 || type == 14, "type must be 12 (Q4_K) or 14 (Q6_K)");
+        require(m > 0 && n > 0 && k > 0 && k % 256 == 0, "K must be a positive multiple of 256 (K-quant super-block)");
+        require(k <= 65536 && m <= 65535 && n <= (int64_t(1) << 31), "shape too large");
+        require(w && act && y, "null pointer");
+        require(aligned(w, 16) && aligned(act, 16) && aligned(y, 4), "w and act must be 16-byte aligned");
+        require(kquant_rows_per_group(type, k) > 0, "K too large for one workgroup's rows");
+        launch_kquant_gemm(type, w, act, y, m, n, k, as_stream(stream));
+        check_launch("hero_kquant_gemm");
+    });
+}
+
 int hero_q8_0_gemv(const void* packed, const void* act, float* y, const float* residual, int64_t n, int64_t k, void* stream) {
     return guard([&] {
         check_q8_shape(n, k);

@@ -1,0 +1,257 @@
+// kquant.hip -- GGUF K-quant weights (Q4_K, Q6_K) against Q8_K activations:
+// the activation quantizer and the matrix-vector / matrix products, bit-exact
+// to the reference's x86 integer-activation dots.
+//
+//   quantize_row_q8_K      nm/src/quant_i8.hpp:31-64
+//   vec_dot_q4_K_q8_K      nm/src/quant_i8.hpp:129-191 (scalar form)
+//   vec_dot_q6_K_q8_K      nm/src/quant_i8.hpp:239-278 (scalar form)
+//   Weight::matvec/matmul  nm/src/quant_i8.hpp:352-383, 430-474
+//
+// Layouts are GGUF's own (no repacking): a weight row is K/256 super-blocks
+// of 144 (Q4_K) or 210 (Q6_K) bytes; a Q8_K activation row is K/256 blocks of
+// 292 bytes {fp32 d, int8 qs[256], int16 bsums[16]}.
+//
+// Exactness: per super-block, the reference forms eight int32 sums aux[l]
+// over the positions p with p % 8 == l (each product weighted by its
+// sub-block's integer scale) and, for Q4_K, the integer mins term; all of
+// that is exact, so any order gives the same integers. The fp32 part runs per
+// row in block order exactly as written: d = fp16(w.d) * x.d;
+// sums[l] += d * float(aux[l]); (Q4_K) sumf -= (fp16(w.dmin) * x.d) * float(summin);
+// then sumf += sums[0..7].
+//
+// Work split: a workgroup takes R consecutive output rows of one activation
+// row; its weight bytes (R rows, contiguous) and the activation row are staged
+// in shared memory with coalesced 16-byte loads; lane (r, b) forms block b of
+// row r's integers; lane r then chains row r's fp32 terms.
+#include "hero/device.hpp"
+#include "hero/kernels.hpp"
+
+namespace hero {
+
+namespace {
+
+constexpr int kQ8KBytes = 292;
+constexpr int kKqThreads = 256;
+constexpr int kKqLdsMax = 65536;
+
+__device__ __forceinline__ int nearest_int_magic(float v) {
+    const float t = v + 12582912.f;  // 1.5 * 2^23: rounds to nearest, ties to even
+    return (__float_as_int(t) & 0x007fffff) - 0x00400000;
+}
+
+// One wave per 256-element block; lane i holds elements 4i .. 4i+3.
+__global__ __launch_bounds__(64) void quantize_q8_K_kernel(const float* __restrict__ x, uint8_t* __restrict__ act, int64_t nblocks) {
+    const int64_t blk = blockIdx.x;
+    if (blk >= nblocks) return;
+    const int lane = threadIdx.x;
+    const float4 v = reinterpret_cast<const float4*>(x + blk * 256)[lane];
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    // first element of largest magnitude (strict >, in index order)
+    float amax = 0.f;
+    int idx = 1 << 30;
+    for (int u = 0; u < 4; ++u) {
+        const float a = fabsf(e[u]);
+        if (a > amax) amax = a, idx = 4 * lane + u;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float oa = __shfl_xor(amax, off);
+        const int oi = __shfl_xor(idx, off);
+        if (oa > amax || (oa == amax && oi < idx)) amax = oa, idx = oi;
+    }
+    uint8_t* out = act + blk * kQ8KBytes;
+    if (amax == 0.f) {  // the zero block: d = 0, quants and sums 0
+        reinterpret_cast<uint32_t*>(out)[lane] = 0u;
+        if (lane < 9) reinterpret_cast<uint32_t*>(out + 256)[lane] = 0u;
+        return;
+    }
+    const float mx = __shfl(e[idx & 3], idx >> 2);
+    const float iscale = -127.f / mx;
+    int q[4];
+    for (int u = 0; u < 4; ++u) q[u] = min(127, nearest_int_magic(iscale * e[u]));
+    reinterpret_cast<uint32_t*>(out + 4)[lane] = (uint32_t(q[0]) & 0xFF) | ((uint32_t(q[1]) & 0xFF) << 8) | ((uint32_t(q[2]) & 0xFF) << 16) | (uint32_t(q[3]) << 24);
+    int s = q[0] + q[1] + q[2] + q[3];  // sums of 16 = four lanes
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    if ((lane & 3) == 0) reinterpret_cast<int16_t*>(out + 260)[lane >> 2] = int16_t(s);
+    if (lane == 0) reinterpret_cast<float*>(out)[0] = 1.f / iscale;
+}
+
+template <int TYPE>
+struct KqFormat;
+template <>
+struct KqFormat<12> {  // Q4_K
+    static constexpr int kBytes = 144;
+};
+template <>
+struct KqFormat<14> {  // Q6_K
+    static constexpr int kBytes = 210;
+};
+
+// Per-block integer part. w = the 144/210 weight bytes, xq = 256 activation
+// int8, xs = its 16 sums. Returns aux[8], summin (Q4_K) and the weight scales.
+__device__ __forceinline__ void q4k_block(const uint8_t* w, const int8_t* xq, const int16_t* xs, int (&aux)[8], int& summin) {
+    const uint8_t* sc = w + 4;
+    const uint8_t* qs = w + 16;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) aux[l] = 0;
+    summin = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int s = j < 4 ? (sc[j] & 63) : ((sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4));
+        const int m = j < 4 ? (sc[j + 4] & 63) : ((sc[j + 4] >> 4) | ((sc[j] >> 6) << 4));
+        const uint32_t* q32 = reinterpret_cast<const uint32_t*>(qs + (j >> 1) * 32);
+        const uint32_t* x32 = reinterpret_cast<const uint32_t*>(xq + 32 * j);
+        const int shift = (j & 1) * 4;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t qw = q32[t] >> shift, xw = x32[t];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int qv = int((qw >> (8 * u)) & 0xF);
+                const int xv = int(int8_t(xw >> (8 * u)));
+                aux[4 * (t & 1) + u] += (s * qv) * xv;
+            }
+        }
+        summin += m * (int(xs[2 * j]) + int(xs[2 * j + 1]));
+    }
+}
+
+__device__ __forceinline__ void q6k_block(const uint8_t* w, const int8_t* xq, int (&aux)[8]) {
+    const uint8_t* ql = w;
+    const uint8_t* qh = w + 128;
+    const int8_t* sc = reinterpret_cast<const int8_t*>(w + 192);
+#pragma unroll
+    for (int l = 0; l < 8; ++l) aux[l] = 0;
+#pragma unroll 2
+    for (int p = 0; p < 256; p += 4) {
+        const int h = p >> 7, e = p & 127;
+        const uint8_t* lo = ql + 64 * h + (e & 63);
+        const uint8_t* hi = qh + 32 * h + (e & 31);
+        const int shl = (e >> 6) * 4, shh = 2 * (e >> 5);
+        const int s = sc[p >> 4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int q = (((lo[u] >> shl) & 0xF) | (((hi[u] >> shh) & 3) << 4)) - 32;
+            aux[(p + u) & 7] += s * (q * int(xq[p + u]));
+        }
+    }
+}
+
+// grid (ceil(N / R), M); dynamic shared: weights R * nb * B, activation nb * 292,
+// per-block terms R * nb * 10 ints
+template <int TYPE>
+__global__ __launch_bounds__(kKqThreads) void kquant_gemm_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ act, float* __restrict__ y,
+                                                                int64_t N, int64_t K, int R) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int B = KqFormat<TYPE>::kBytes;
+    const int nb = int(K / 256), tid = threadIdx.x;
+    const int64_t n0 = int64_t(blockIdx.x) * R, m = blockIdx.y;
+    const int rows = int(min<int64_t>(R, N - n0));
+    const int64_t rb = int64_t(nb) * B;
+    // the rows' bytes start at an even offset of the (16-byte aligned) tensor;
+    // in shared memory they start at the same offset modulo 16, so the
+    // 16-byte copies below are aligned on both sides
+    const int64_t start = n0 * rb, len = int64_t(rows) * rb;
+    const int head = int(start & 15);
+    uint8_t* ws = smem + head;
+    uint8_t* xs = smem + ((16 + int64_t(R) * rb + 15) & ~int64_t(15));
+    int* terms = reinterpret_cast<int*>(xs + ((int64_t(nb) * kQ8KBytes + 15) & ~int64_t(15)));
+
+    // stage: the rows' bytes (16-byte copies between 2-byte copies of the
+    // unaligned head and tail) and the activation row (a multiple of 4 bytes)
+    {
+        const int64_t a0 = (start + 15) & ~int64_t(15), a1 = (start + len) & ~int64_t(15);
+        if (a1 > a0) {
+            const uint4* src = reinterpret_cast<const uint4*>(w + a0);
+            uint4* dst = reinterpret_cast<uint4*>(smem + 16 * ((a0 - start + head) / 16));
+            for (int64_t i = tid; i < (a1 - a0) / 16; i += kKqThreads) dst[i] = src[i];
+            for (int64_t i = start + 2 * tid; i < a0; i += 2 * kKqThreads)
+                *reinterpret_cast<uint16_t*>(ws + (i - start)) = *reinterpret_cast<const uint16_t*>(w + i);
+            for (int64_t i = a1 + 2 * tid; i < start + len; i += 2 * kKqThreads)
+                *reinterpret_cast<uint16_t*>(ws + (i - start)) = *reinterpret_cast<const uint16_t*>(w + i);
+        } else {
+            for (int64_t i = start + 2 * tid; i < start + len; i += 2 * kKqThreads)
+                *reinterpret_cast<uint16_t*>(ws + (i - start)) = *reinterpret_cast<const uint16_t*>(w + i);
+        }
+        const uint32_t* xa = reinterpret_cast<const uint32_t*>(act + m * int64_t(nb) * kQ8KBytes);
+        const int n4 = nb * kQ8KBytes / 4;
+        for (int i = tid; i < n4; i += kKqThreads) reinterpret_cast<uint32_t*>(xs)[i] = xa[i];
+    }
+    __syncthreads();
+
+    for (int item = tid; item < rows * nb; item += kKqThreads) {
+        const int r = item / nb, b = item % nb;
+        const uint8_t* wb = ws + int64_t(r) * rb + int64_t(b) * B;
+        const uint8_t* xb = xs + b * kQ8KBytes;
+        int aux[8], summin = 0;
+        if constexpr (TYPE == 12)
+            q4k_block(wb, reinterpret_cast<const int8_t*>(xb + 4), reinterpret_cast<const int16_t*>(xb + 260), aux, summin);
+        else
+            q6k_block(wb, reinterpret_cast<const int8_t*>(xb + 4), aux);
+        int* t = terms + item * 10;
+#pragma unroll
+        for (int l = 0; l < 8; ++l) t[l] = aux[l];
+        t[8] = summin;
+    }
+    __syncthreads();
+
+    // fp32, in block order per row (one lane per row)
+    for (int r = tid; r < rows; r += kKqThreads) {
+        float sums[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        float sumf = 0.f;
+        for (int b = 0; b < nb; ++b) {
+            const uint8_t* wb = ws + int64_t(r) * rb + int64_t(b) * B;
+            const float xd = *reinterpret_cast<const float*>(xs + b * kQ8KBytes);
+            const int* t = terms + (r * nb + b) * 10;
+            uint16_t dbits;
+            if constexpr (TYPE == 12)
+                dbits = uint16_t(wb[0] | (wb[1] << 8));
+            else
+                dbits = uint16_t(wb[208] | (wb[209] << 8));
+            const float d = half_bits_to_f32(dbits) * xd;
+#pragma unroll
+            for (int l = 0; l < 8; ++l) sums[l] += d * float(t[l]);
+            if constexpr (TYPE == 12) {
+                const float dmin = half_bits_to_f32(uint16_t(wb[2] | (wb[3] << 8))) * xd;
+                sumf -= dmin * float(t[8]);
+            }
+        }
+#pragma unroll
+        for (int l = 0; l < 8; ++l) sumf += sums[l];
+        y[m * N + n0 + r] = sumf;
+    }
+}
+
+}  // namespace
+
+int64_t act_q8_K_bytes(int64_t m, int64_t k) { return m * (k / 256) * kQ8KBytes; }
+
+void launch_quantize_q8_K(const float* x, void* act, int64_t M, int64_t K, hipStream_t s) {
+    const int64_t nblocks = M * (K / 256);
+    hipLaunchKernelGGL(quantize_q8_K_kernel, dim3(unsigned(nblocks)), dim3(64), 0, s, x, static_cast<uint8_t*>(act), nblocks);
+}
+
+int kquant_rows_per_group(int type, int64_t K) {
+    const int64_t nb = K / 256;
+    const int64_t rb = nb * (type == 12 ? 144 : 210);
+    const int64_t fixed = ((nb * kQ8KBytes + 15) & ~int64_t(15));
+    int64_t r = std::min<int64_t>(kKqThreads / std::max<int64_t>(1, nb), 64);
+    while (r > 0 && ((16 + r * rb + 15) & ~int64_t(15)) + fixed + r * nb * 10 * 4 > kKqLdsMax) --r;
+    return int(std::max<int64_t>(r, 0));
+}
+
+void launch_kquant_gemm(int type, const void* w, const void* act, float* y, int64_t M, int64_t N, int64_t K, hipStream_t s) {
+    const int R = kquant_rows_per_group(type, K);
+    const int64_t nb = K / 256;
+    const int64_t rb = nb * (type == 12 ? 144 : 210);
+    const size_t lds = size_t(((16 + R * rb + 15) & ~int64_t(15)) + ((nb * kQ8KBytes + 15) & ~int64_t(15)) + int64_t(R) * nb * 10 * 4);
+    const dim3 grid(unsigned((N + R - 1) / R), unsigned(M));
+    const auto* wb = static_cast<const uint8_t*>(w);
+    const auto* ab = static_cast<const uint8_t*>(act);
+    if (type == 12)
+        hipLaunchKernelGGL(kquant_gemm_kernel<12>, grid, dim3(kKqThreads), lds, s, wb, ab, y, N, K, R);
+    else
+        hipLaunchKernelGGL(kquant_gemm_kernel<14>, grid, dim3(kKqThreads), lds, s, wb, ab, y, N, K, R);
+}
+
+}  // namespace hero

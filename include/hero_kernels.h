@@ -114,6 +114,20 @@ int hero_q8_0_embed(const void* packed, int64_t v, int64_t d, const int32_t* ids
  * (Logits::argmax, nm/src/logits.hpp:61-66). scratch: M*128 uint64. */
 int hero_argmax(const float* logits, int64_t m, int64_t n, int32_t* out, uint64_t* scratch, void* stream);
 
+/* ---- K-quant weights (GGUF Q4_K = type 12, Q6_K = type 14) ----------------
+ * Replaces the int8-activation branch of Weight<In,Out>::matvec / ::matmul
+ * for these types (nm/src/quant_i8.hpp:352-383, 430-474): the activation rows
+ * are quantized to Q8_K (quantize_row_q8_K, nm/src/quant_i8.hpp:31-64), then
+ * y[m][n] = vec_dot_q{4,6}_K_q8_K(k, W row n, act row m) (the x86 scalar
+ * forms, nm/src/quant_i8.hpp:146-191, 239-278), bit for bit.
+ * W is the GGUF tensor as stored (n rows of k/256 blocks of 144 / 210 bytes),
+ * 16-byte aligned. act holds hero_q8_K_act_bytes(m, k) bytes of GGUF Q8_K
+ * blocks (fp32 d, 256 int8, 16 int16 sums). k: a multiple of 256, at most
+ * 65536. */
+int64_t hero_q8_K_act_bytes(int64_t m, int64_t k);
+int hero_q8_K_quantize(const float* x, void* act, int64_t m, int64_t k, void* stream);
+int hero_kquant_gemm(int32_t type, const void* w, const void* act, float* y, int64_t m, int64_t n, int64_t k, void* stream);
+
 /* The scalar functions of the path evaluated on the device, for parity
  * checks: out[0..n) = expf, [n..2n) = log1pf, then silu
  * (nm/src/components.hpp:105), sigmoid (nm/src/core.hpp:579), softplus

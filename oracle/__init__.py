@@ -28,6 +28,9 @@ _sigs = {
     "oracle_vec_dot_q8_0": (c_float, [c_size_t, c_void_p, c_void_p]),
     "oracle_block_sums_q8_0": (None, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
     "oracle_matvec_q8_0": (None, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+    "oracle_quantize_row_q8_K": (None, [c_void_p, c_void_p, c_size_t]),
+    "oracle_vec_dot_kquant": (c_float, [c_int, c_void_p, c_void_p, c_size_t]),
+    "oracle_matmul_kquant": (None, [c_int, c_void_p, c_size_t, c_size_t, c_void_p, c_size_t, c_void_p]),
     "oracle_matmul_q8_0": (None, [c_void_p, c_size_t, c_size_t, c_void_p, c_size_t, c_void_p]),
     "oracle_rmsnorm_rows": (None, [c_void_p, c_void_p, c_size_t, c_size_t, c_float]),
     "oracle_l2_normalize": (None, [c_void_p, c_void_p, c_size_t, c_float]),
@@ -142,6 +145,37 @@ def matmul(w_blocks, n, k, X):
     t = X.shape[0]
     Y = np.empty((t, n), np.float32)
     lib.oracle_matmul_q8_0(_p(w_blocks), n, k, _p(X), t, _p(Y))
+    return Y
+
+
+# ---- K-quants (GGUF types 12 = Q4_K, 14 = Q6_K; activations as Q8_K) ----------
+Q4_K, Q6_K = 12, 14
+KBLOCK_BYTES = {Q4_K: 144, Q6_K: 210}
+Q8K_BYTES = 292
+
+
+def quantize_row_q8_K(x):
+    """K-quant activation quantizer -> raw Q8_K blocks, uint8 [K/256, 292]"""
+    x = _f32(x).ravel()
+    out = np.zeros((x.size // 256, Q8K_BYTES), np.uint8)
+    lib.oracle_quantize_row_q8_K(_p(x), _p(out), x.size)
+    return out
+
+
+def vec_dot_kquant(wtype, w_row, x_blocks) -> np.float32:
+    """one row of raw Q4_K/Q6_K blocks against raw Q8_K blocks"""
+    w_row = np.ascontiguousarray(w_row, np.uint8)
+    x_blocks = np.ascontiguousarray(x_blocks, np.uint8)
+    return np.float32(lib.oracle_vec_dot_kquant(wtype, _p(w_row), _p(x_blocks), x_blocks.size // Q8K_BYTES * 256))
+
+
+def matmul_kquant(wtype, w, n, k, X):
+    """Weight::matvec/matmul for a raw Q4_K/Q6_K tensor [n rows of k/256 blocks]"""
+    w = np.ascontiguousarray(w, np.uint8)
+    assert w.size == n * (k // 256) * KBLOCK_BYTES[wtype]
+    X = _f32(X).reshape(-1, k)
+    Y = np.empty((X.shape[0], n), np.float32)
+    lib.oracle_matmul_kquant(wtype, _p(w), n, k, _p(X), X.shape[0], _p(Y))
     return Y
 
 

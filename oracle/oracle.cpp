@@ -280,6 +280,131 @@ void matmul_q8_0(const BlockQ8* W, size_t N, size_t K, const float* X, size_t T,
 }
 
 // ---------------------------------------------------------------------------
+// K-quants
+// ---------------------------------------------------------------------------
+// nm/src/quant_i8.hpp:31-36: round to nearest, ties to even, through the
+// 1.5 * 2^23 offset (valid for |v| < 2^22).
+static int nearest_int_magic(float v) {
+    const float t = v + 12582912.f;
+    int32_t i;
+    std::memcpy(&i, &t, 4);
+    return (i & 0x007fffff) - 0x00400000;
+}
+
+// nm/src/quant_i8.hpp:39-64. The scale is -127 over the signed value of the
+// first element of largest magnitude, so that element maps to -127 exactly.
+void quantize_row_q8_K(const float* x, BlockQ8K* y, size_t k) {
+    for (size_t b = 0; b < k / 256; ++b, x += 256) {
+        float mx = 0.f, amax = 0.f;
+        for (size_t j = 0; j < 256; ++j) {
+            const float a = std::fabs(x[j]);
+            if (a > amax) {
+                amax = a;
+                mx = x[j];
+            }
+        }
+        BlockQ8K& o = y[b];
+        if (amax == 0.f) {
+            std::memset(&o, 0, sizeof o);
+            continue;
+        }
+        const float iscale = -127.f / mx;
+        for (size_t j = 0; j < 256; ++j) o.qs[j] = int8_t(std::min(127, nearest_int_magic(iscale * x[j])));
+        for (size_t g = 0; g < 16; ++g) {
+            int s = 0;
+            for (size_t l = 0; l < 16; ++l) s += o.qs[g * 16 + l];
+            o.bsums[g] = int16_t(s);
+        }
+        o.d = 1.f / iscale;
+    }
+}
+
+// 6-bit scales and mins of a Q4_K block: entries 0..3 in the low 6 bits of
+// bytes 0..3 (scales) and 4..7 (mins); entries 4..7 from the nibbles of bytes
+// 8..11 plus the top two bits of bytes 0..7 (nm/src/quant_i8.hpp:129-142
+// computes the same values with word masks).
+static void q4k_scale_min(const uint8_t* p, int j, int& sc, int& mn) {
+    if (j < 4) {
+        sc = p[j] & 63;
+        mn = p[j + 4] & 63;
+    } else {
+        sc = (p[j + 4] & 0xF) | ((p[j - 4] >> 6) << 4);
+        mn = (p[j + 4] >> 4) | ((p[j] >> 6) << 4);
+    }
+}
+
+// nm/src/quant_i8.hpp:146-191. Per block: eight integer sums aux[l] over the
+// positions l mod 8 (each product scaled by its 32-weight sub-block's scale),
+// the mins term from the activation's 16-element sums; then in fp32 and block
+// order: sums[l] += d * aux[l], sumf -= dmin * summin; finally sumf += sums[l]
+// for l = 0..7.
+float vec_dot_q4_K_q8_K(size_t n, const BlockQ4K* w, const BlockQ8K* x) {
+    float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float sumf = 0.f;
+    for (size_t b = 0; b < n / 256; ++b) {
+        const BlockQ4K& wb = w[b];
+        const BlockQ8K& xb = x[b];
+        int32_t aux[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        int summin = 0;
+        for (int j = 0; j < 8; ++j) {  // sub-block j: weights 32j .. 32j+31
+            int sc, mn;
+            q4k_scale_min(wb.scales, j, sc, mn);
+            for (int i = 0; i < 32; ++i) {
+                const uint8_t byte = wb.qs[(j / 2) * 32 + i];
+                const int q = (j & 1) ? (byte >> 4) : (byte & 0xF);
+                aux[i % 8] += sc * (q * xb.qs[32 * j + i]);
+            }
+            summin += mn * (xb.bsums[2 * j] + xb.bsums[2 * j + 1]);
+        }
+        const float d = fp16_to_fp32(wb.d) * xb.d;
+        for (int l = 0; l < 8; ++l) sums[l] += d * float(aux[l]);
+        const float dmin = fp16_to_fp32(wb.dmin) * xb.d;
+        sumf -= dmin * float(summin);
+    }
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
+// nm/src/quant_i8.hpp:239-278. Weight e of a 128-weight half h: low nibble
+// from ql (byte e % 64 of the half's 64, high nibble for e >= 64), two high
+// bits from qh byte e % 32 at shift 2 * (e / 32), minus 32; the int8 scale of
+// each 16 weights; then sums[l] += d * aux[l] per block and sumf = sum of
+// sums[l].
+float vec_dot_q6_K_q8_K(size_t n, const BlockQ6K* w, const BlockQ8K* x) {
+    float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (size_t b = 0; b < n / 256; ++b) {
+        const BlockQ6K& wb = w[b];
+        const BlockQ8K& xb = x[b];
+        int32_t aux[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int p = 0; p < 256; ++p) {
+            const int h = p / 128, e = p % 128;
+            const uint8_t lo = wb.ql[64 * h + e % 64];
+            const int low = e < 64 ? (lo & 0xF) : (lo >> 4);
+            const int high = (wb.qh[32 * h + e % 32] >> (2 * (e / 32))) & 3;
+            const int q = (low | (high << 4)) - 32;
+            aux[p % 8] += int(wb.scales[p / 16]) * (q * xb.qs[p]);
+        }
+        const float d = fp16_to_fp32(wb.d) * xb.d;
+        for (int l = 0; l < 8; ++l) sums[l] += d * float(aux[l]);
+    }
+    float sumf = 0.f;
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
+void matmul_kquant(int type, const void* W, size_t N, size_t K, const float* X, size_t T, float* Y) {
+    if (T == 0) return;
+    const size_t nb = K / 256;
+    std::vector<BlockQ8K> act(T * nb);
+    par_for_lambda(T, [&](size_t t) { quantize_row_q8_K(X + t * K, act.data() + t * nb, K); });
+    par_for_lambda(N, [&](size_t o) {
+        for (size_t t = 0; t < T; ++t)
+            Y[t * N + o] = type == 12 ? vec_dot_q4_K_q8_K(K, static_cast<const BlockQ4K*>(W) + o * nb, act.data() + t * nb)
+                                      : vec_dot_q6_K_q8_K(K, static_cast<const BlockQ6K*>(W) + o * nb, act.data() + t * nb);
+    });
+}
+
+// ---------------------------------------------------------------------------
 // small ops
 // ---------------------------------------------------------------------------
 float dot(const float* a, const float* b, size_t n) {  // core.hpp:496-500

@@ -33,6 +33,40 @@ namespace oracle {
 float fp16_to_fp32(uint16_t h);
 uint16_t fp32_to_fp16(float f);
 
+// ---- K-quant blocks (nm/src/quant.hpp:52,63-86; nm/src/quant_i8.hpp:22-28) -----
+// Super-blocks of 256 weights. Q4_K: fp16 d, dmin, 12 bytes of packed 6-bit
+// scales/mins, 128 bytes of nibbles (144). Q6_K: 128 bytes low nibbles, 64
+// bytes of 2-bit high parts, 16 int8 scales, fp16 d (210). Activations go to
+// Q8_K: fp32 d, 256 int8, 16 int16 sums of 16 (292).
+#pragma pack(push, 1)
+struct BlockQ4K {
+    uint16_t d, dmin;
+    uint8_t scales[12];
+    uint8_t qs[128];
+};
+struct BlockQ6K {
+    uint8_t ql[128];
+    uint8_t qh[64];
+    int8_t scales[16];
+    uint16_t d;
+};
+struct BlockQ8K {
+    float d;
+    int8_t qs[256];
+    int16_t bsums[16];
+};
+#pragma pack(pop)
+static_assert(sizeof(BlockQ4K) == 144 && sizeof(BlockQ6K) == 210 && sizeof(BlockQ8K) == 292, "K-quant block sizes");
+
+// activation quantizer for K-quant weights (nm/src/quant_i8.hpp:31-64)
+void quantize_row_q8_K(const float* x, BlockQ8K* y, size_t k);
+// the x86 (scalar) dots (nm/src/quant_i8.hpp:146-191, 239-278)
+float vec_dot_q4_K_q8_K(size_t n, const BlockQ4K* w, const BlockQ8K* x);
+float vec_dot_q6_K_q8_K(size_t n, const BlockQ6K* w, const BlockQ8K* x);
+// Weight::matvec / ::matmul for Q4_K (type 12) and Q6_K (type 14): T rows of
+// X quantized to Q8_K, each output = the dot above (nm/src/quant_i8.hpp:352-383,430-474)
+void matmul_kquant(int type, const void* W, size_t N, size_t K, const float* X, size_t T, float* Y);
+
 // ---- Q8_0 block (nm/src/quant.hpp:59-62): fp16 d + 32 int8, 34 bytes ------
 #pragma pack(push, 1)
 struct BlockQ8 {

@@ -63,6 +63,12 @@ void oracle_block_sums_q8_0(const void* W, size_t N, size_t K, const void* xq, i
         }
 }
 
+void oracle_quantize_row_q8_K(const float* x, void* blocks, size_t k) { quantize_row_q8_K(x, static_cast<BlockQ8K*>(blocks), k); }
+float oracle_vec_dot_kquant(int type, const void* w, const void* x, size_t k) {
+    return type == 12 ? vec_dot_q4_K_q8_K(k, static_cast<const BlockQ4K*>(w), static_cast<const BlockQ8K*>(x))
+                      : vec_dot_q6_K_q8_K(k, static_cast<const BlockQ6K*>(w), static_cast<const BlockQ8K*>(x));
+}
+void oracle_matmul_kquant(int type, const void* W, size_t N, size_t K, const float* X, size_t T, float* Y) { matmul_kquant(type, W, N, K, X, T, Y); }
 void oracle_matvec_q8_0(const void* W, size_t N, size_t K, const float* x, float* y) { matvec_q8_0(static_cast<const BlockQ8*>(W), N, K, x, y); }
 void oracle_matmul_q8_0(const void* W, size_t N, size_t K, const float* X, size_t T, float* Y) { matmul_q8_0(static_cast<const BlockQ8*>(W), N, K, X, T, Y); }
 

@@ -154,6 +154,30 @@ int run_kernels(const std::string& dir) {
             for (size_t n = 0; n < N; ++n) yy.push_back(Y.row(r)[n]);
         out("gemm_y", yy);
     }
+    {  // K-quants: Q8_K activation quantizer and Weight<4096,64>::matvec /
+       // ::matmul over raw Q4_K and Q6_K blocks (int8-activation, x86 scalar dots)
+        const std::vector<float> x = in("kq_x");  // [4][4096]
+        constexpr size_t K = 4096, N = 64, T = 4;
+        std::vector<block_q8_K> act(T * K / QK_K);
+        for (size_t r = 0; r < T; ++r) quantize_row_q8_K(x.data() + r * K, act.data() + r * K / QK_K, K);
+        write_bin(dir + "/kq_act.out.bin", act.data(), act.size());
+        auto run = [&](const char* wname, GT type, const char* yname) {
+            auto raw = std::make_shared<std::vector<uint8_t>>(read_bin<uint8_t>(dir + "/" + wname + ".in.bin"));
+            if (raw->size() != type_size_bytes(type, N * K)) throw std::runtime_error(std::string("bad size for ") + wname);
+            const Weight<K, N> weight(type, raw->data(), raw);
+            std::vector<float> yy;
+            const Vec<N> y = weight.matvec(vec_from<K>(x.data()));
+            yy.insert(yy.end(), y.p.get(), y.p.get() + N);
+            Matrix<K> X;
+            for (size_t r = 0; r < T; ++r) X.append(vec_from<K>(x.data() + r * K));
+            const Matrix<N> Y = weight.matmul(X.view());
+            for (size_t r = 0; r < T; ++r)
+                for (size_t n = 0; n < N; ++n) yy.push_back(Y.row(r)[n]);
+            out(yname, yy);
+        };
+        run("kq_w4", GT::Q4_K, "kq_y4");
+        run("kq_w6", GT::Q6_K, "kq_y6");
+    }
     {  // RMSNorm at the three widths the path uses; gamma is [width] after x
         auto norm = [&]<size_t N>(const char* name, std::integral_constant<size_t, N>) {
             const std::vector<float> v = in(name);  // [x | gamma]

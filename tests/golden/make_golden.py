@@ -87,6 +87,25 @@ def kernel_inputs(rng: np.random.Generator) -> dict[str, np.ndarray]:
     inp["attn_q"] = f32(rng.standard_normal(128) / np.sqrt(128))
     inp["attn_k"] = f32(rng.standard_normal((ctx, 128)) / np.sqrt(128))
     inp["attn_v"] = f32(rng.standard_normal((ctx, 128)) / np.sqrt(128))
+    # K-quants: activations [4][4096] with crafted Q8_K blocks in row 1, and
+    # raw Q4_K / Q6_K weight blocks [64 rows][16 blocks] from random bytes
+    kx = (rng.standard_normal((4, 4096)) * np.repeat(np.exp(rng.uniform(-6, 3, (4, 16))), 256, axis=1)).astype(np.float32)
+    kx[1, 0:256] = 0.0                                    # zero block: d = 0, all zero
+    kx[1, 256 + 7] = kx[1, 256 + 99] = -3 * np.abs(kx[1, 256:512]).max()  # negative max, twice
+    kx[1, 512:768] = rng.integers(-126, 127, 256) + 0.5   # max -127 below: scale 1, exact ties
+    kx[1, 512 + 3] = -127.0
+    kx[1, 768 + 10], kx[1, 768 + 20] = 5.0, -5.0          # equal magnitudes: the first sets the sign
+    kx[1, 768:1024] = np.clip(kx[1, 768:1024], -4.9, 4.9)
+    kx[1, 768 + 10], kx[1, 768 + 20] = 5.0, -5.0
+    inp["kq_x"] = f32(kx)
+    f16 = lambda a: np.asarray(a, np.float16).view(np.uint8).reshape(*np.shape(a), 2)  # noqa: E731
+    nb = 64 * 16
+    w4 = np.concatenate([f16(rng.uniform(0.2, 2.0, nb) * 1e-2), f16(rng.uniform(0.0, 2.0, nb) * 1e-2),
+                         rng.integers(0, 256, (nb, 12)).astype(np.uint8), rng.integers(0, 256, (nb, 128)).astype(np.uint8)], axis=1)
+    inp["kq_w4"] = np.ascontiguousarray(w4.astype(np.uint8))
+    w6 = np.concatenate([rng.integers(0, 256, (nb, 128 + 64)).astype(np.uint8), rng.integers(-128, 128, (nb, 16)).astype(np.int8).view(np.uint8),
+                         f16(rng.uniform(0.2, 2.0, nb) * 1e-3)], axis=1)
+    inp["kq_w6"] = np.ascontiguousarray(w6.astype(np.uint8))
     return inp
 
 
@@ -95,6 +114,7 @@ OUTPUTS = {  # name -> dtype of the .out.bin
     "gemv_y": np.float32, "gemm_y": np.float32, "rms128": np.float32, "rms1024": np.float32, "rms4096": np.float32,
     "l2": np.float32, "silu": np.float32, "sigmoid": np.float32, "softplus": np.float32, "conv": np.float32,
     "delta_out": np.float32, "delta_state": np.float32, "rope": np.float32, "attn_scaled": np.float32, "attn_unit": np.float32,
+    "kq_act": np.uint8, "kq_y4": np.float32, "kq_y6": np.float32,
 }
 
 

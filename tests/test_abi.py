@@ -16,7 +16,7 @@ def declared_symbols():
     names = set()
     for h in ("hero_kernels.h", "hero_model.h"):
         text = open(os.path.join(ROOT, "include", h)).read()
-        names |= set(re.findall(r"\b(hero_[a-z0-9_]+)\s*\(", text))
+        names |= set(re.findall(r"\b(hero_[A-Za-z0-9_]+)\s*\(", text))
     return names
 
 
@@ -27,6 +27,18 @@ def test_every_declared_symbol_is_exported_and_bound():
     for name in declared:
         assert hasattr(lib, name), name
     assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+
+
+def test_kquant_argument_errors_are_reported_before_any_launch():
+    lib = _lib.lib
+    assert lib.hero_q8_K_act_bytes(3, 4096) == 3 * 16 * 292
+    assert lib.hero_kquant_gemm(13, 16, 16, 16, 1, 64, 4096, None) == _lib.HERO_EINVAL
+    assert b"Q4_K" in lib.hero_last_error()
+    assert lib.hero_kquant_gemm(12, 16, 16, 16, 1, 64, 4000, None) == _lib.HERO_EINVAL
+    assert b"multiple of 256" in lib.hero_last_error()
+    assert lib.hero_kquant_gemm(14, None, 16, 16, 1, 64, 4096, None) == _lib.HERO_EINVAL
+    assert lib.hero_kquant_gemm(12, 8, 16, 16, 1, 64, 4096, None) == _lib.HERO_EINVAL  # alignment
+    assert lib.hero_q8_K_quantize(16, 16, 1, 300, None) == _lib.HERO_EINVAL
 
 
 def test_size_helpers():

@@ -656,3 +656,55 @@ def test_attn_paged_fp16_matches_oracle_over_fp16_kv(lib, hq, window):
             assert blocks[b].tobytes() == want.tobytes()  # the kernel quantizes its own output exactly
             checked += 1
     assert checked == 16
+
+
+# ---- K-quant weights (Q4_K / Q6_K against Q8_K activations) -------------------
+def kquant_weights(rng, wtype, n, k):
+    """random GGUF Q4_K / Q6_K blocks: random quants and scales, sane fp16 d"""
+    nb = n * (k // 256)
+    f16 = lambda a: np.asarray(a, np.float16).view(np.uint8).reshape(-1, 2)  # noqa: E731
+    if wtype == oracle.Q4_K:
+        w = np.concatenate([f16(rng.uniform(0.2, 2.0, nb) * 1e-2), f16(rng.uniform(0.0, 2.0, nb) * 1e-2),
+                            rng.integers(0, 256, (nb, 140)).astype(np.uint8)], axis=1)
+    else:
+        w = np.concatenate([rng.integers(0, 256, (nb, 208)).astype(np.uint8), f16(rng.uniform(0.2, 2.0, nb) * 1e-3)], axis=1)
+    return np.ascontiguousarray(w, np.uint8)
+
+
+def kquant_dev(lib, wtype, w, x, n, k):
+    m = x.shape[0]
+    xd, wd = dev(x.astype(np.float32)), dev(w)
+    act = empty(lib.hero_q8_K_act_bytes(m, k))
+    check(lib.hero_q8_K_quantize(ptr(xd), ptr(act), m, k, stream()))
+    y = empty(m * n * 4)
+    check(lib.hero_kquant_gemm(wtype, ptr(wd), ptr(act), ptr(y), m, n, k, stream()))
+    return host(act, np.uint8), host(y, np.float32).reshape(m, n)
+
+
+def test_q8_K_quantizer_and_kquant_products_match_reference_golden(lib, kernels_golden):
+    """the reference's own outputs: Q8_K blocks of 4 crafted rows, and
+    Weight<4096,64>::matvec / ::matmul over raw Q4_K and Q6_K blocks"""
+    x = kernels_golden["in_kq_x"].reshape(4, 4096)
+    for wtype, name, out in [(oracle.Q4_K, "kq_w4", "kq_y4"), (oracle.Q6_K, "kq_w6", "kq_y6")]:
+        act, y = kquant_dev(lib, wtype, kernels_golden[f"in_{name}"], x, 64, 4096)
+        assert act.tobytes() == kernels_golden["out_kq_act"].tobytes()
+        expect = kernels_golden[f"out_{out}"].reshape(5, 64)
+        assert np.array_equal(bits(y[0]), bits(expect[0]))
+        assert np.array_equal(bits(y), bits(expect[1:])), name
+
+
+# K = 4096 / 12288 (the model's widths), 1024 and 2816 (blocks per row 4 and
+# 11: Q6_K rows start off 16-byte boundaries), row counts not a multiple of a
+# workgroup's rows, several activation rows
+@pytest.mark.parametrize("wtype", [12, 14])
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (1, 12288, 4096), (2, 4096, 12288), (3, 1001, 1024), (1, 517, 2816), (16, 300, 4096)])
+def test_kquant_gemm_matches_oracle_bitwise(lib, wtype, m, n, k):
+    rng = np.random.default_rng(wtype * 1000 + m * 100 + n + k)
+    w = kquant_weights(rng, wtype, n, k)
+    x = (rng.standard_normal((m, k)) * np.exp(rng.uniform(-3, 3, (m, 1)))).astype(np.float32)
+    act, y = kquant_dev(lib, wtype, w, x, n, k)
+    expect_act = np.concatenate([oracle.quantize_row_q8_K(x[r]) for r in range(m)])
+    assert act.tobytes() == expect_act.tobytes()
+    expect = oracle.matmul_kquant(wtype, w, n, k, x)
+    bad = np.flatnonzero(bits(y).ravel() != bits(expect).ravel())
+    assert bad.size == 0, f"{bad.size} outputs differ, first {bad[:5]}: {y.ravel()[bad[:3]]} vs {expect.ravel()[bad[:3]]}"

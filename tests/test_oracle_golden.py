@@ -31,6 +31,70 @@ def test_matvec_and_matmul_match_reference(kernels_golden):
     assert np.array_equal(bits(Y).ravel(), bits(kernels_golden["out_gemm_y"]))
 
 
+def test_q8_K_quantizer_matches_reference(kernels_golden):
+    """zero block, a negative maximum (twice), exact .5 ties at scale 1, equal
+    magnitudes of both signs (the first sets the sign) in row 1"""
+    x = kernels_golden["in_kq_x"].reshape(4, 4096)
+    got = np.concatenate([oracle.quantize_row_q8_K(x[r]) for r in range(4)])
+    assert got.tobytes() == kernels_golden["out_kq_act"].tobytes()
+    blocks = got.reshape(4, 16, 292)
+    assert not blocks[1, 0].any()                                   # the zero block
+    assert blocks[1, 1, 4 + 7].view(np.int8) == -127                # first element of largest magnitude
+    assert blocks[1, 3, 4 + 10].view(np.int8) == -127 and blocks[1, 3, 4 + 20].view(np.int8) == 127
+
+
+@pytest.mark.parametrize("wtype,name", [(oracle.Q4_K, "kq_w4"), (oracle.Q6_K, "kq_w6")])
+def test_kquant_matvec_and_matmul_match_reference(kernels_golden, wtype, name):
+    w = kernels_golden[f"in_{name}"]
+    x = kernels_golden["in_kq_x"].reshape(4, 4096)
+    expect = kernels_golden["out_kq_y" + ("4" if wtype == oracle.Q4_K else "6")].reshape(5, 64)
+    Y = oracle.matmul_kquant(wtype, w, 64, 4096, x)
+    assert np.array_equal(bits(Y[0]), bits(expect[0]))   # Weight::matvec
+    assert np.array_equal(bits(Y), bits(expect[1:]))     # Weight::matmul, 4 rows
+
+
+def test_kquant_dots_equal_dequantized_sums_in_exact_arithmetic(kernels_golden):
+    """Independent of the reference: decode the K-quant weights from their
+    bit layout (ggml's published block formats) and the Q8_K activation, form
+    the exact dot in float64 from the same per-block fp32 scales, and compare
+    with the oracle's fp32 dot to a rounding bound. A wrong nibble, high-bit
+    shift, scale or min index moves the result far outside it."""
+    x = kernels_golden["in_kq_x"].reshape(4, 4096)[2]
+    act = oracle.quantize_row_q8_K(x)
+    ad = act[:, :4].copy().view(np.float32).ravel()
+    aq = act[:, 4:260].view(np.int8).astype(np.int64)
+    f16 = lambda b: b.copy().view(np.float16).astype(np.float32)  # noqa: E731
+    for wtype, name in [(oracle.Q4_K, "kq_w4"), (oracle.Q6_K, "kq_w6")]:
+        w = kernels_golden[f"in_{name}"].reshape(64, 16, -1)
+        for row in range(0, 64, 9):
+            exact = 0.0
+            for b in range(16):
+                blk = w[row, b]
+                if wtype == oracle.Q4_K:
+                    d, dmin = f16(blk[0:2])[0], f16(blk[2:4])[0]
+                    sc_bytes, qs = blk[4:16].astype(np.int64), blk[16:144].astype(np.int64)
+                    sc = [(sc_bytes[j] & 63) if j < 4 else ((sc_bytes[j + 4] & 15) | ((sc_bytes[j - 4] >> 6) << 4)) for j in range(8)]
+                    mn = [(sc_bytes[j + 4] & 63) if j < 4 else ((sc_bytes[j + 4] >> 4) | ((sc_bytes[j] >> 6) << 4)) for j in range(8)]
+                    q = np.concatenate([np.concatenate([qs[32 * c:32 * c + 32] & 15, qs[32 * c:32 * c + 32] >> 4]) for c in range(4)])
+                    scale = np.repeat(sc, 32)
+                    mins = np.repeat(mn, 32)
+                    dd, dm = np.float32(d * ad[b]), np.float32(dmin * ad[b])
+                    exact += float(dd) * float((scale * q * aq[b]).sum()) - float(dm) * float((mins * aq[b]).sum())
+                else:
+                    ql, qh = blk[0:128].astype(np.int64), blk[128:192].astype(np.int64)
+                    sc = blk[192:208].view(np.int8).astype(np.int64)
+                    d = f16(blk[208:210])[0]
+                    q = np.empty(256, np.int64)
+                    for h in range(2):
+                        for e in range(128):
+                            low = ql[64 * h + e % 64] & 15 if e < 64 else ql[64 * h + e % 64] >> 4
+                            q[128 * h + e] = (low | (((qh[32 * h + e % 32] >> (2 * (e // 32))) & 3) << 4)) - 32
+                    exact += float(np.float32(d * ad[b])) * float((np.repeat(sc, 16) * q * aq[b]).sum())
+            got = float(oracle.vec_dot_kquant(wtype, w[row].ravel(), act))
+            scale_sum = sum(abs(float(v)) for v in [exact]) + 1e-30
+            assert abs(got - exact) <= 1e-5 * max(scale_sum, 1.0), (name, row, got, exact)
+
+
 @pytest.mark.parametrize("n", [128, 1024, 4096])
 def test_rmsnorm_matches_reference(kernels_golden, n):
     v = kernels_golden[f"in_rms{n}"]

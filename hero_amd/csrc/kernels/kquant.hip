@@ -87,32 +87,44 @@ struct KqFormat<14> {  // Q6_K
     static constexpr int kBytes = 210;
 };
 
-// Per-block integer part. w = the 144/210 weight bytes, xq = 256 activation
-// int8, xs = its 16 sums. Returns aux[8], summin (Q4_K) and the weight scales.
-__device__ __forceinline__ void q4k_block(const uint8_t* w, const int8_t* xq, const int16_t* xs, int (&aux)[8], int& summin) {
+// Per-block integer part of Q4_K. w = the 144 weight bytes; xt = the block's
+// 256 activation int8 regrouped per 32-element sub-block j as eight dwords
+// xt[8j + l] = bytes (x[32j+l], x[32j+8+l], x[32j+16+l], x[32j+24+l]): the
+// four positions that share both aux[l] and the sub-block's scale, so each
+// (j, l) term is one 4-way int8 dot of the same four weight nibbles, gathered
+// with byte permutes. xs = the 16 activation sums. Exact integers.
+__device__ __forceinline__ void q4k_block(const uint8_t* w, const uint32_t* xt, const int16_t* xs, int (&aux)[8], int& summin) {
     const uint8_t* sc = w + 4;
-    const uint8_t* qs = w + 16;
+    const uint32_t* qs = reinterpret_cast<const uint32_t*>(w + 16);
 #pragma unroll
     for (int l = 0; l < 8; ++l) aux[l] = 0;
     summin = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int s = j < 4 ? (sc[j] & 63) : ((sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4));
-        const int m = j < 4 ? (sc[j + 4] & 63) : ((sc[j + 4] >> 4) | ((sc[j] >> 6) << 4));
-        const uint32_t* q32 = reinterpret_cast<const uint32_t*>(qs + (j >> 1) * 32);
-        const uint32_t* x32 = reinterpret_cast<const uint32_t*>(xq + 32 * j);
-        const int shift = (j & 1) * 4;
+    for (int c = 0; c < 4; ++c) {  // sub-blocks 2c (low nibbles) and 2c+1 (high)
+        uint32_t D[8];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const uint32_t qw = q32[t] >> shift, xw = x32[t];
+        for (int t = 0; t < 8; ++t) D[t] = qs[8 * c + t];
+        int s[2], m[2];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int qv = int((qw >> (8 * u)) & 0xF);
-                const int xv = int(int8_t(xw >> (8 * u)));
-                aux[4 * (t & 1) + u] += (s * qv) * xv;
-            }
+        for (int h = 0; h < 2; ++h) {
+            const int j = 2 * c + h;
+            s[h] = j < 4 ? (sc[j] & 63) : ((sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4));
+            m[h] = j < 4 ? (sc[j + 4] & 63) : ((sc[j + 4] >> 4) | ((sc[j] >> 6) << 4));
+            summin += m[h] * (int(xs[2 * j]) + int(xs[2 * j + 1]));
         }
-        summin += m * (int(xs[2 * j]) + int(xs[2 * j + 1]));
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            // bytes l, 8+l, 16+l, 24+l of the 32 = byte l%4 of dwords l/4, l/4+2, l/4+4, l/4+6
+            const int u = l & 3, o = l >> 2;
+            const uint32_t sel = uint32_t(u) | (uint32_t(4 + u) << 8) | 0x0C0C0000u;
+            const uint32_t lo2 = __builtin_amdgcn_perm(D[o + 2], D[o], sel);
+            const uint32_t hi2 = __builtin_amdgcn_perm(D[o + 6], D[o + 4], sel);
+            const uint32_t g = __builtin_amdgcn_perm(hi2, lo2, 0x05040100u);
+            const int dl = dot4_i8(int(g & 0x0F0F0F0Fu), int(xt[8 * (2 * c) + l]), 0);
+            const int dh = dot4_i8(int((g >> 4) & 0x0F0F0F0Fu), int(xt[8 * (2 * c + 1) + l]), 0);
+            aux[l] += s[0] * dl;
+            aux[l] += s[1] * dh;
+        }
     }
 }
 
@@ -138,7 +150,7 @@ __device__ __forceinline__ void q6k_block(const uint8_t* w, const int8_t* xq, in
 }
 
 // grid (ceil(N / R), M); dynamic shared: weights R * nb * B, activation nb * 292,
-// per-block terms R * nb * 10 ints
+// its regrouped copy nb * 256 (Q4_K), per-block terms R * nb * 10 ints
 template <int TYPE>
 __global__ __launch_bounds__(kKqThreads) void kquant_gemm_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ act, float* __restrict__ y,
                                                                 int64_t N, int64_t K, int R) {
@@ -155,7 +167,8 @@ __global__ __launch_bounds__(kKqThreads) void kquant_gemm_kernel(const uint8_t* 
     const int head = int(start & 15);
     uint8_t* ws = smem + head;
     uint8_t* xs = smem + ((16 + int64_t(R) * rb + 15) & ~int64_t(15));
-    int* terms = reinterpret_cast<int*>(xs + ((int64_t(nb) * kQ8KBytes + 15) & ~int64_t(15)));
+    uint32_t* xt = reinterpret_cast<uint32_t*>(xs + ((int64_t(nb) * kQ8KBytes + 15) & ~int64_t(15)));  // nb * 64 dwords
+    int* terms = reinterpret_cast<int*>(xt + nb * 64);
 
     // stage: the rows' bytes (16-byte copies between 2-byte copies of the
     // unaligned head and tail) and the activation row (a multiple of 4 bytes)
@@ -178,6 +191,13 @@ __global__ __launch_bounds__(kKqThreads) void kquant_gemm_kernel(const uint8_t* 
         for (int i = tid; i < n4; i += kKqThreads) reinterpret_cast<uint32_t*>(xs)[i] = xa[i];
     }
     __syncthreads();
+    if constexpr (TYPE == 12) {  // the activation regrouped for the 4-way dots
+        for (int i = tid; i < nb * 64; i += kKqThreads) {
+            const uint8_t* q = xs + (i >> 6) * kQ8KBytes + 4 + ((i >> 3) & 7) * 32 + (i & 7);
+            xt[i] = uint32_t(q[0]) | (uint32_t(q[8]) << 8) | (uint32_t(q[16]) << 16) | (uint32_t(q[24]) << 24);
+        }
+        __syncthreads();
+    }
 
     for (int item = tid; item < rows * nb; item += kKqThreads) {
         const int r = item / nb, b = item % nb;
@@ -185,7 +205,7 @@ __global__ __launch_bounds__(kKqThreads) void kquant_gemm_kernel(const uint8_t* 
         const uint8_t* xb = xs + b * kQ8KBytes;
         int aux[8], summin = 0;
         if constexpr (TYPE == 12)
-            q4k_block(wb, reinterpret_cast<const int8_t*>(xb + 4), reinterpret_cast<const int16_t*>(xb + 260), aux, summin);
+            q4k_block(wb, xt + b * 64, reinterpret_cast<const int16_t*>(xb + 260), aux, summin);
         else
             q6k_block(wb, reinterpret_cast<const int8_t*>(xb + 4), aux);
         int* t = terms + item * 10;
@@ -236,7 +256,7 @@ int kquant_rows_per_group(int type, int64_t K) {
     const int64_t rb = nb * (type == 12 ? 144 : 210);
     const int64_t fixed = ((nb * kQ8KBytes + 15) & ~int64_t(15));
     int64_t r = std::min<int64_t>(kKqThreads / std::max<int64_t>(1, nb), 64);
-    while (r > 0 && ((16 + r * rb + 15) & ~int64_t(15)) + fixed + r * nb * 10 * 4 > kKqLdsMax) --r;
+    while (r > 0 && ((16 + r * rb + 15) & ~int64_t(15)) + fixed + nb * 256 + r * nb * 10 * 4 > kKqLdsMax) --r;
     return int(std::max<int64_t>(r, 0));
 }
 
@@ -244,7 +264,7 @@ void launch_kquant_gemm(int type, const void* w, const void* act, float* y, int6
     const int R = kquant_rows_per_group(type, K);
     const int64_t nb = K / 256;
     const int64_t rb = nb * (type == 12 ? 144 : 210);
-    const size_t lds = size_t(((16 + R * rb + 15) & ~int64_t(15)) + ((nb * kQ8KBytes + 15) & ~int64_t(15)) + int64_t(R) * nb * 10 * 4);
+    const size_t lds = size_t(((16 + R * rb + 15) & ~int64_t(15)) + ((nb * kQ8KBytes + 15) & ~int64_t(15)) + nb * 256 + int64_t(R) * nb * 10 * 4);
     const dim3 grid(unsigned((N + R - 1) / R), unsigned(M));
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* ab = static_cast<const uint8_t*>(act);

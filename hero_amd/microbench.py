@@ -1,6 +1,6 @@
 """hero_amd.microbench -- the kernel microbenchmarks of the hot path on one GPU.
 
-    python -m hero_amd.microbench [--suite gemv,gdn,attn] [--out results.md]
+    python -m hero_amd.microbench [--suite gemv,kquant,gdn,attn] [--out results.md]
 
 Suites (synthetic, seeded inputs; every launch goes through the C ABI):
 
@@ -162,6 +162,53 @@ def bench_gemv(lib, replays: int = 20, batches=GEMV_BATCHES):
     return rows
 
 
+# ---- K-quant GEMV / GEMM (Q4_K, Q6_K over GGUF-layout weights) ---------------------------------------
+KQUANT_SHAPES = [(4096, 4096), (4096, 12288), (12288, 4096)]
+
+
+def bench_kquant(lib, replays: int = 20, batches=(1, 16)):
+    from ._lib import check
+
+    t = _torch()
+    gen = t.Generator(device="cuda")
+    gen.manual_seed(4321)
+    rows = []
+    for wtype, name, bb in ((12, "Q4_K", 144), (14, "Q6_K", 210)):
+        for k, n in KQUANT_SHAPES:
+            nb = n * (k // 256)
+            wbytes = nb * bb
+            copies = max(1, math.ceil(512e6 / wbytes))
+            weights = []
+            for _ in range(copies):
+                w = t.randint(0, 256, (nb, bb), dtype=t.uint8, device="cuda", generator=gen)
+                d = (t.rand(nb, device="cuda", generator=gen) * 0.01 + 0.002).half().view(t.uint8).view(nb, 2)
+                if wtype == 12:
+                    w[:, 0:2] = d
+                    w[:, 2:4] = d
+                else:
+                    w[:, 208:210] = d
+                weights.append(w.contiguous())
+            for m in batches:
+                x = t.randn(m, k, device="cuda", generator=gen)
+                act = _bytes(lib.hero_q8_K_act_bytes(m, k))
+                check(lib.hero_q8_K_quantize(_p(x), _p(act), m, k, _stream()))
+                y = t.empty(m, n, device="cuda")
+
+                def body():
+                    for w in weights:
+                        check(lib.hero_kquant_gemm(wtype, _p(w), _p(act), _p(y), m, n, k, _stream()))
+
+                sec = _time_graph(body, len(weights), replays)
+                nbytes = wbytes + m * k * 4 + m * n * 4
+                rows.append({"suite": "kquant", "kernel": f"kquant_gemm {name}", "K": k, "N": n, "M": m, "copies": copies,
+                             "us": sec * 1e6, "GB/s": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS})
+                print(json.dumps(rows[-1]), flush=True)
+                del act, y, x
+            del weights
+            t.cuda.empty_cache()
+    return rows
+
+
 # ---- gated delta-net -----------------------------------------------------------------------------
 def _gdn_case(lib, hk: int, hv: int, B: int, W: int, gen):
     from ._lib import GdnDecodeArgs
@@ -319,7 +366,7 @@ def bench_attn(lib, replays: int = 20):
 
 def _markdown(rows) -> str:
     out = []
-    for suite in ("gemv", "gdn", "attn"):
+    for suite in ("gemv", "kquant", "gdn", "attn"):
         rs = [r for r in rows if r["suite"] == suite]
         if not rs:
             continue
@@ -355,6 +402,8 @@ def main(argv=None) -> int:
     suites = args.suite.split(",")
     if "gemv" in suites:
         rows += bench_gemv(lib, batches=[int(v) for v in args.gemv_batches.split(",")])
+    if "kquant" in suites:
+        rows += bench_kquant(lib)
     if "gdn" in suites:
         rows += bench_gdn(lib)
     if "attn" in suites:

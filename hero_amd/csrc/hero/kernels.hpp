@@ -31,6 +31,9 @@ int64_t act_q8_K_bytes(int64_t m, int64_t k);
 int kquant_rows_per_group(int type, int64_t K);  // output rows per workgroup (0: K too large)
 void launch_quantize_q8_K(const float* x, void* act, int64_t M, int64_t K, hipStream_t s);
 void launch_kquant_gemm(int type, const void* w, const void* act, float* y, int64_t M, int64_t N, int64_t K, hipStream_t s);
+// top-k / top-p sampling of one logits row (sample.hip); top_k in 1 .. sample_max_top_k()
+int sample_max_top_k();
+void launch_sample_topk(const float* logits, int64_t V, int top_k, float temp, float top_p, float u, int32_t* out, hipStream_t s);
 
 // q8.hip
 void launch_quantize_act(const float* x, void* act, int64_t M, int64_t K, hipStream_t s);

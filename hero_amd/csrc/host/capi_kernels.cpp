@@ -56,6 +56,18 @@ int hero_q8_0_quantize(const float* x, void* act, int64_t m, int64_t k, void* st
     });
 }
 
+int hero_sample_topk(const float* logits, int64_t v, int32_t top_k, float temp, float top_p, float u, int32_t* out, void* stream) {
+    return guard([&] {
+        require(logits && out, "null pointer");
+        require(v > 0 && v <= (int64_t(1) << 30), "vocabulary size out of range");
+        require(top_k >= 1 && top_k <= sample_max_top_k(), "top_k must be in 1 .. 1024 on the device");
+        require(temp > 0.f, "temp must be positive (temp <= 0 is greedy: hero_argmax)");
+        require(u >= 0.f && u < 1.f, "u must be in [0, 1)");
+        launch_sample_topk(logits, v, top_k, temp, top_p, u, out, as_stream(stream));
+        check_launch("hero_sample_topk");
+    });
+}
+
 int64_t hero_q8_K_act_bytes(int64_t m, int64_t k) { return act_q8_K_bytes(m, k); }
 
 int hero_q8_K_quantize(const float* x, void* act, int64_t m, int64_t k, void* stream) {

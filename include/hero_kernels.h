@@ -128,6 +128,16 @@ int64_t hero_q8_K_act_bytes(int64_t m, int64_t k);
 int hero_q8_K_quantize(const float* x, void* act, int64_t m, int64_t k, void* stream);
 int hero_kquant_gemm(int32_t type, const void* w, const void* act, float* y, int64_t m, int64_t n, int64_t k, void* stream);
 
+/* Logits::sample with temp > 0 (nm/src/logits.hpp:71-105) on one row of v
+ * logits: the top_k candidates (1 <= top_k <= 1024; top_k > v means v), sorted
+ * by logit descending with equal logits by ascending id, p = expf((l - max) /
+ * temp), the top_p prefix, and the draw. u in [0, 1) is the value the caller's
+ * generator gives std::generate_canonical<float, 24> (what the reference's
+ * uniform_real_distribution<float>(0, s2) scales by s2). out: two int32 of
+ * device memory; the token id goes to out[0], out[1] is used as a flag between
+ * the two kernels of the call. temp <= 0 is greedy: use hero_argmax. */
+int hero_sample_topk(const float* logits, int64_t v, int32_t top_k, float temp, float top_p, float u, int32_t* out, void* stream);
+
 /* The scalar functions of the path evaluated on the device, for parity
  * checks: out[0..n) = expf, [n..2n) = log1pf, then silu
  * (nm/src/components.hpp:105), sigmoid (nm/src/core.hpp:579), softplus

@@ -28,6 +28,7 @@ _sigs = {
     "oracle_vec_dot_q8_0": (c_float, [c_size_t, c_void_p, c_void_p]),
     "oracle_block_sums_q8_0": (None, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
     "oracle_matvec_q8_0": (None, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]),
+    "oracle_sample_topk": (c_int32, [c_void_p, c_size_t, c_size_t, c_float, c_float, c_float]),
     "oracle_quantize_row_q8_K": (None, [c_void_p, c_void_p, c_size_t]),
     "oracle_vec_dot_kquant": (c_float, [c_int, c_void_p, c_void_p, c_size_t]),
     "oracle_matmul_kquant": (None, [c_int, c_void_p, c_size_t, c_size_t, c_void_p, c_size_t, c_void_p]),
@@ -146,6 +147,12 @@ def matmul(w_blocks, n, k, X):
     Y = np.empty((t, n), np.float32)
     lib.oracle_matmul_q8_0(_p(w_blocks), n, k, _p(X), t, _p(Y))
     return Y
+
+
+def sample_topk(logits, top_k, temp, top_p, u) -> int:
+    """Logits::sample (temp > 0) given the uniform draw u in [0, 1)"""
+    x = _f32(logits).ravel()
+    return int(lib.oracle_sample_topk(_p(x), x.size, int(top_k), float(temp), float(top_p), float(u)))
 
 
 # ---- K-quants (GGUF types 12 = Q4_K, 14 = Q6_K; activations as Q8_K) ----------

@@ -665,6 +665,44 @@ void forward(const Model& m, State& s, const float* rows, size_t T, float* logit
     matvec_q8_0(m.output.w, m.output.N, m.output.K, last.data(), logits);
 }
 
+// nm/src/logits.hpp:71-105: sort down to k candidates, exp((v - max) / temp)
+// and their sequential sum, the first prefix whose sequential sum of p / sum
+// reaches top_p, the kept prefix's sequential sum s2, r = u * s2, and the
+// first candidate whose running sum reaches r.
+int32_t sample_topk(const float* logits, size_t V, size_t top_k, float temp, float top_p, float u) {
+    std::vector<int32_t> idx(V);
+    for (size_t i = 0; i < V; ++i) idx[i] = int32_t(i);
+    const size_t k = top_k > 0 ? std::min(top_k, V) : V;
+    std::partial_sort(idx.begin(), idx.begin() + k, idx.end(), [&](int32_t a, int32_t b) {
+        return logits[a] > logits[b] || (logits[a] == logits[b] && a < b);
+    });
+    const float mx = logits[idx[0]];
+    std::vector<float> pr(k);
+    float sum = 0.f;
+    for (size_t i = 0; i < k; ++i) {
+        pr[i] = std::exp((logits[idx[i]] - mx) / temp);
+        sum += pr[i];
+    }
+    float cum = 0.f;
+    size_t keep = k;
+    for (size_t i = 0; i < k; ++i) {
+        cum += pr[i] / sum;
+        if (cum >= top_p) {
+            keep = i + 1;
+            break;
+        }
+    }
+    float s2 = 0.f;
+    for (size_t i = 0; i < keep; ++i) s2 += pr[i];
+    const float r = u * (s2 - 0.f) + 0.f;
+    float acc = 0.f;
+    for (size_t i = 0; i < keep; ++i) {
+        acc += pr[i];
+        if (r <= acc) return idx[i];
+    }
+    return idx[keep - 1];
+}
+
 int32_t argmax(const float* logits, size_t n) {
     size_t best = 0;
     for (size_t v = 1; v < n; ++v)

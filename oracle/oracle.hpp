@@ -67,6 +67,13 @@ float vec_dot_q6_K_q8_K(size_t n, const BlockQ6K* w, const BlockQ8K* x);
 // X quantized to Q8_K, each output = the dot above (nm/src/quant_i8.hpp:352-383,430-474)
 void matmul_kquant(int type, const void* W, size_t N, size_t K, const float* X, size_t T, float* Y);
 
+// ---- sampling (nm/src/logits.hpp:71-105) -----------------------------------------
+// Logits::sample with temp > 0, given u = the uniform draw the caller's RNG
+// makes for std::uniform_real_distribution<float>(0, s2) (libstdc++:
+// r = u * (s2 - 0) + 0 with u = generate_canonical<float, 24>(rng)).
+// Candidates are ordered by logit, descending; equal logits by ascending id.
+int32_t sample_topk(const float* logits, size_t V, size_t top_k, float temp, float top_p, float u);
+
 // ---- Q8_0 block (nm/src/quant.hpp:59-62): fp16 d + 32 int8, 34 bytes ------
 #pragma pack(push, 1)
 struct BlockQ8 {

@@ -63,6 +63,7 @@ void oracle_block_sums_q8_0(const void* W, size_t N, size_t K, const void* xq, i
         }
 }
 
+int32_t oracle_sample_topk(const float* logits, size_t V, size_t top_k, float temp, float top_p, float u) { return sample_topk(logits, V, top_k, temp, top_p, u); }
 void oracle_quantize_row_q8_K(const float* x, void* blocks, size_t k) { quantize_row_q8_K(x, static_cast<BlockQ8K*>(blocks), k); }
 float oracle_vec_dot_kquant(int type, const void* w, const void* x, size_t k) {
     return type == 12 ? vec_dot_q4_K_q8_K(k, static_cast<const BlockQ4K*>(w), static_cast<const BlockQ8K*>(x))

@@ -12,6 +12,10 @@
 // Each kernel case instantiates the reference template at a fixed size and
 // applies it to the inputs the golden script wrote.
 #include "src/qwen35_loader.hpp"
+#include "src/logits.hpp"
+
+#include <limits>
+#include <random>
 
 #include <chrono>
 #include <cstdio>
@@ -177,6 +181,27 @@ int run_kernels(const std::string& dir) {
         };
         run("kq_w4", GT::Q4_K, "kq_y4");
         run("kq_w6", GT::Q6_K, "kq_y6");
+    }
+    {  // Logits<32000>::sample over 8 logit rows x 6 configurations; the
+       // uniform draw it makes is recorded from a copy of the generator
+        const std::vector<float> lg = in("sample_logits");  // [8][32000]
+        constexpr size_t V = 32000;
+        const SamplerCfg cfgs[6] = {{0.7f, 40, 0.9f, 1}, {1.0f, 1, 1.0f, 2}, {1.3f, 1000, 0.95f, 3}, {0.5f, 0, 1.0f, 4}, {2.0f, 200, 0.5f, 5}, {0.9f, 64, 0.0f, 6}};
+        std::vector<float> res;  // per (row, cfg): token, u
+        for (size_t r = 0; r < 8; ++r) {
+            Vec<V> v;
+            for (size_t i = 0; i < V; ++i) v[i] = lg[r * V + i];
+            const Logits<V> logits(std::move(v));
+            for (const SamplerCfg& c : cfgs) {
+                std::mt19937_64 rng(c.seed * 1000 + r);
+                std::mt19937_64 copy = rng;
+                const float u = std::generate_canonical<float, std::numeric_limits<float>::digits>(copy);
+                const TokenId t = logits.sample(c, rng);
+                res.push_back(float(int32_t(t)));
+                res.push_back(u);
+            }
+        }
+        out("sample", res);
     }
     {  // RMSNorm at the three widths the path uses; gamma is [width] after x
         auto norm = [&]<size_t N>(const char* name, std::integral_constant<size_t, N>) {

@@ -106,6 +106,8 @@ def kernel_inputs(rng: np.random.Generator) -> dict[str, np.ndarray]:
     w6 = np.concatenate([rng.integers(0, 256, (nb, 128 + 64)).astype(np.uint8), rng.integers(-128, 128, (nb, 16)).astype(np.int8).view(np.uint8),
                          f16(rng.uniform(0.2, 2.0, nb) * 1e-3)], axis=1)
     inp["kq_w6"] = np.ascontiguousarray(w6.astype(np.uint8))
+    # sampling: 8 rows of 32000 distinct logits at a few temperatures' scales
+    inp["sample_logits"] = f32(rng.standard_normal((8, 32000)) * np.array([1, 2, 3, 4, 6, 8, 0.5, 12])[:, None])
     return inp
 
 
@@ -114,7 +116,7 @@ OUTPUTS = {  # name -> dtype of the .out.bin
     "gemv_y": np.float32, "gemm_y": np.float32, "rms128": np.float32, "rms1024": np.float32, "rms4096": np.float32,
     "l2": np.float32, "silu": np.float32, "sigmoid": np.float32, "softplus": np.float32, "conv": np.float32,
     "delta_out": np.float32, "delta_state": np.float32, "rope": np.float32, "attn_scaled": np.float32, "attn_unit": np.float32,
-    "kq_act": np.uint8, "kq_y4": np.float32, "kq_y6": np.float32,
+    "kq_act": np.uint8, "kq_y4": np.float32, "kq_y6": np.float32, "sample": np.float32,
 }
 
 

@@ -708,3 +708,38 @@ def test_kquant_gemm_matches_oracle_bitwise(lib, wtype, m, n, k):
     expect = oracle.matmul_kquant(wtype, w, n, k, x)
     bad = np.flatnonzero(bits(y).ravel() != bits(expect).ravel())
     assert bad.size == 0, f"{bad.size} outputs differ, first {bad[:5]}: {y.ravel()[bad[:3]]} vs {expect.ravel()[bad[:3]]}"
+
+
+# ---- top-k / top-p sampling -------------------------------------------------------------
+def sample_dev(lib, logits_dev, v, k, temp, p, u):
+    out = empty(8)
+    check(lib.hero_sample_topk(ptr(logits_dev), v, k, temp, p, float(u), ptr(out), stream()))
+    return int(host(out, np.int32)[0])
+
+
+def test_sampler_matches_reference_golden(lib, kernels_golden):
+    """Logits<32000>::sample, the reference's own picks (top_k 0, the whole
+    vocabulary, is not a device form)"""
+    cfgs = [(0.7, 40, 0.9), (1.0, 1, 1.0), (1.3, 1000, 0.95), (0.5, 0, 1.0), (2.0, 200, 0.5), (0.9, 64, 0.0)]
+    lg = kernels_golden["in_sample_logits"].reshape(8, 32000)
+    res = kernels_golden["out_sample"].reshape(8, len(cfgs), 2)
+    for r in range(8):
+        d = dev(lg[r])
+        for c, (temp, k, p) in enumerate(cfgs):
+            if k == 0:
+                continue
+            assert sample_dev(lib, d, 32000, k, temp, p, res[r, c, 1]) == int(res[r, c, 0]), (r, c)
+
+
+# the model's vocabulary, k up to the device limit, top_p cuts, and a row of
+# many equal logits (ties ordered by ascending id, as in the oracle)
+@pytest.mark.parametrize("k,temp,p", [(1, 1.0, 1.0), (7, 0.6, 0.8), (40, 0.7, 0.9), (256, 1.5, 0.99), (1000, 1.0, 0.5), (1024, 3.0, 1.0)])
+def test_sampler_matches_oracle(lib, k, temp, p):
+    rng = np.random.default_rng(k)
+    v = 151936
+    rows = [rng.standard_normal(v).astype(np.float32) * 4,
+            np.round(rng.standard_normal(v) * 8).astype(np.float32)]  # heavy ties
+    for x in rows:
+        d = dev(x)
+        for u in (0.0, 0.123, 0.5, 0.987654):
+            assert sample_dev(lib, d, v, k, temp, p, u) == oracle.sample_topk(x, k, temp, p, u), (k, temp, p, u)

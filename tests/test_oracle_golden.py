@@ -95,6 +95,34 @@ def test_kquant_dots_equal_dequantized_sums_in_exact_arithmetic(kernels_golden):
             assert abs(got - exact) <= 1e-5 * max(scale_sum, 1.0), (name, row, got, exact)
 
 
+SAMPLER_CFGS = [(0.7, 40, 0.9), (1.0, 1, 1.0), (1.3, 1000, 0.95), (0.5, 0, 1.0), (2.0, 200, 0.5), (0.9, 64, 0.0)]
+
+
+def test_sampler_matches_reference(kernels_golden):
+    """Logits<32000>::sample over 8 rows x 6 configurations (top_k 0 = the
+    whole vocabulary, top_p 0 = the first candidate), given the uniform draw
+    the reference's generator made"""
+    lg = kernels_golden["in_sample_logits"].reshape(8, 32000)
+    res = kernels_golden["out_sample"].reshape(8, len(SAMPLER_CFGS), 2)
+    for r in range(8):
+        for c, (temp, k, p) in enumerate(SAMPLER_CFGS):
+            assert oracle.sample_topk(lg[r], k, temp, p, res[r, c, 1]) == int(res[r, c, 0]), (r, c)
+
+
+def test_sampler_limits():
+    """closed forms: top_k 1 and top_p 0 are greedy; u -> 0 picks the first
+    kept candidate; a large temperature spreads the draw over the kept set"""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(5000).astype(np.float32)
+    best = int(np.argmax(x))
+    assert oracle.sample_topk(x, 1, 0.8, 1.0, 0.99) == best
+    assert oracle.sample_topk(x, 50, 0.8, 0.0, 0.99) == best
+    assert oracle.sample_topk(x, 50, 0.8, 1.0, 0.0) == best
+    top = set(np.argsort(-x, kind="stable")[:10].tolist())
+    picks = {oracle.sample_topk(x, 10, 1e6, 1.0, u) for u in np.linspace(0, 0.999, 40)}
+    assert picks == top
+
+
 @pytest.mark.parametrize("n", [128, 1024, 4096])
 def test_rmsnorm_matches_reference(kernels_golden, n):
     v = kernels_golden[f"in_rms{n}"]

@@ -40,7 +40,13 @@ __device__ __forceinline__ int nearest_int_magic(float v) {
 }
 
 // One wave per 256-element block; lane i holds elements 4i .. 4i+3.
-__global__ __launch_bounds__(64) void quantize_q8_K_kernel(const float* __restrict__ x, uint8_t* __restrict__ act, int64_t nblocks) {
+// Besides the GGUF block, each block's 256 int8 are written regrouped (xt):
+// per 32-element sub-block j, dword 8j + l = bytes (q[32j+l], q[32j+8+l],
+// q[32j+16+l], q[32j+24+l]) -- the four positions that share a Q4_K integer
+// sum and scale, so a Q4_K block's terms are 4-way int8 dots.
+__global__ __launch_bounds__(64) void quantize_q8_K_kernel(const float* __restrict__ x, uint8_t* __restrict__ act, uint32_t* __restrict__ xt,
+                                                           int64_t nblocks) {
+    __shared__ uint32_t qsh[64];
     const int64_t blk = blockIdx.x;
     if (blk >= nblocks) return;
     const int lane = threadIdx.x;
@@ -62,13 +68,21 @@ __global__ __launch_bounds__(64) void quantize_q8_K_kernel(const float* __restri
     if (amax == 0.f) {  // the zero block: d = 0, quants and sums 0
         reinterpret_cast<uint32_t*>(out)[lane] = 0u;
         if (lane < 9) reinterpret_cast<uint32_t*>(out + 256)[lane] = 0u;
+        xt[blk * 64 + lane] = 0u;
         return;
     }
     const float mx = __shfl(e[idx & 3], idx >> 2);
     const float iscale = -127.f / mx;
     int q[4];
     for (int u = 0; u < 4; ++u) q[u] = min(127, nearest_int_magic(iscale * e[u]));
-    reinterpret_cast<uint32_t*>(out + 4)[lane] = (uint32_t(q[0]) & 0xFF) | ((uint32_t(q[1]) & 0xFF) << 8) | ((uint32_t(q[2]) & 0xFF) << 16) | (uint32_t(q[3]) << 24);
+    const uint32_t packed = (uint32_t(q[0]) & 0xFF) | ((uint32_t(q[1]) & 0xFF) << 8) | ((uint32_t(q[2]) & 0xFF) << 16) | (uint32_t(q[3]) << 24);
+    reinterpret_cast<uint32_t*>(out + 4)[lane] = packed;
+    qsh[lane] = packed;
+    __syncthreads();
+    {
+        const uint8_t* qb = reinterpret_cast<const uint8_t*>(qsh) + 32 * (lane >> 3) + (lane & 7);
+        xt[blk * 64 + lane] = uint32_t(qb[0]) | (uint32_t(qb[8]) << 8) | (uint32_t(qb[16]) << 16) | (uint32_t(qb[24]) << 24);
+    }
     int s = q[0] + q[1] + q[2] + q[3];  // sums of 16 = four lanes
     s += __shfl_xor(s, 1);
     s += __shfl_xor(s, 2);
@@ -149,8 +163,69 @@ __device__ __forceinline__ void q6k_block(const uint8_t* w, const int8_t* xq, in
     }
 }
 
-// grid (ceil(N / R), M); dynamic shared: weights R * nb * B, activation nb * 292,
-// its regrouped copy nb * 256 (Q4_K), per-block terms R * nb * 10 ints
+// Q4_K: lane (r, b) loads its 144-byte block and the activation's regrouped
+// block straight from memory (no staging), forms the block's integers, and
+// leaves them with the block's scales in shared memory; lane r chains row r.
+// grid (ceil(N / R), M), R * nb <= 256.
+constexpr int kQ4Terms = 11;  // aux[8], summin, weight d | dmin << 16, activation d
+constexpr int kQ4Threads = 256;
+
+__global__ __launch_bounds__(kQ4Threads) void q4k_gemm_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ act, const uint32_t* __restrict__ xt,
+                                                              float* __restrict__ y, int64_t N, int64_t K, int R) {
+    __shared__ int terms[kQ4Threads * kQ4Terms];
+    const int nb = int(K / 256), tid = threadIdx.x;
+    const int64_t n0 = int64_t(blockIdx.x) * R, m = blockIdx.y;
+    const int rows = int(min<int64_t>(R, N - n0));
+    if (tid < rows * nb) {
+        const int r = tid / nb, b = tid % nb;
+        uint4 wv[9];
+        const uint4* wsrc = reinterpret_cast<const uint4*>(w + ((n0 + r) * nb + b) * 144);
+#pragma unroll
+        for (int i = 0; i < 9; ++i) wv[i] = wsrc[i];
+        uint4 xv[16];
+        const uint4* xsrc = reinterpret_cast<const uint4*>(xt + (m * nb + b) * 64);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) xv[i] = xsrc[i];
+        const uint8_t* xb = act + (m * nb + b) * kQ8KBytes;
+        int16_t bs[16];
+        const uint32_t* bsrc = reinterpret_cast<const uint32_t*>(xb + 260);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t v = bsrc[i];
+            bs[2 * i] = int16_t(v & 0xFFFF), bs[2 * i + 1] = int16_t(v >> 16);
+        }
+        const uint32_t xd_bits = *reinterpret_cast<const uint32_t*>(xb);
+        int aux[8], summin;
+        q4k_block(reinterpret_cast<const uint8_t*>(wv), reinterpret_cast<const uint32_t*>(xv), bs, aux, summin);
+        int* t = terms + tid * kQ4Terms;
+#pragma unroll
+        for (int l = 0; l < 8; ++l) t[l] = aux[l];
+        t[8] = summin;
+        t[9] = int(wv[0].x);  // fp16 d | fp16 dmin << 16
+        t[10] = int(xd_bits);
+    }
+    __syncthreads();
+    for (int r = tid; r < rows; r += kQ4Threads) {
+        float sums[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        float sumf = 0.f;
+        for (int b = 0; b < nb; ++b) {
+            const int* t = terms + (r * nb + b) * kQ4Terms;
+            const float xd = __int_as_float(t[10]);
+            const uint32_t dd = uint32_t(t[9]);
+            const float d = half_bits_to_f32(uint16_t(dd & 0xFFFF)) * xd;
+#pragma unroll
+            for (int l = 0; l < 8; ++l) sums[l] += d * float(t[l]);
+            const float dmin = half_bits_to_f32(uint16_t(dd >> 16)) * xd;
+            sumf -= dmin * float(t[8]);
+        }
+#pragma unroll
+        for (int l = 0; l < 8; ++l) sumf += sums[l];
+        y[m * N + n0 + r] = sumf;
+    }
+}
+
+// Q6_K: grid (ceil(N / R), M); dynamic shared: weights R * nb * 210 (+16),
+// activation nb * 292, per-block terms R * nb * 10 ints
 template <int TYPE>
 __global__ __launch_bounds__(kKqThreads) void kquant_gemm_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ act, float* __restrict__ y,
                                                                 int64_t N, int64_t K, int R) {
@@ -167,8 +242,7 @@ __global__ __launch_bounds__(kKqThreads) void kquant_gemm_kernel(const uint8_t* 
     const int head = int(start & 15);
     uint8_t* ws = smem + head;
     uint8_t* xs = smem + ((16 + int64_t(R) * rb + 15) & ~int64_t(15));
-    uint32_t* xt = reinterpret_cast<uint32_t*>(xs + ((int64_t(nb) * kQ8KBytes + 15) & ~int64_t(15)));  // nb * 64 dwords
-    int* terms = reinterpret_cast<int*>(xt + nb * 64);
+    int* terms = reinterpret_cast<int*>(xs + ((int64_t(nb) * kQ8KBytes + 15) & ~int64_t(15)));
 
     // stage: the rows' bytes (16-byte copies between 2-byte copies of the
     // unaligned head and tail) and the activation row (a multiple of 4 bytes)
@@ -191,23 +265,13 @@ __global__ __launch_bounds__(kKqThreads) void kquant_gemm_kernel(const uint8_t* 
         for (int i = tid; i < n4; i += kKqThreads) reinterpret_cast<uint32_t*>(xs)[i] = xa[i];
     }
     __syncthreads();
-    if constexpr (TYPE == 12) {  // the activation regrouped for the 4-way dots
-        for (int i = tid; i < nb * 64; i += kKqThreads) {
-            const uint8_t* q = xs + (i >> 6) * kQ8KBytes + 4 + ((i >> 3) & 7) * 32 + (i & 7);
-            xt[i] = uint32_t(q[0]) | (uint32_t(q[8]) << 8) | (uint32_t(q[16]) << 16) | (uint32_t(q[24]) << 24);
-        }
-        __syncthreads();
-    }
 
     for (int item = tid; item < rows * nb; item += kKqThreads) {
         const int r = item / nb, b = item % nb;
         const uint8_t* wb = ws + int64_t(r) * rb + int64_t(b) * B;
         const uint8_t* xb = xs + b * kQ8KBytes;
         int aux[8], summin = 0;
-        if constexpr (TYPE == 12)
-            q4k_block(wb, xt + b * 64, reinterpret_cast<const int16_t*>(xb + 260), aux, summin);
-        else
-            q6k_block(wb, reinterpret_cast<const int8_t*>(xb + 4), aux);
+        q6k_block(wb, reinterpret_cast<const int8_t*>(xb + 4), aux);
         int* t = terms + item * 10;
 #pragma unroll
         for (int l = 0; l < 8; ++l) t[l] = aux[l];
@@ -223,18 +287,9 @@ __global__ __launch_bounds__(kKqThreads) void kquant_gemm_kernel(const uint8_t* 
             const uint8_t* wb = ws + int64_t(r) * rb + int64_t(b) * B;
             const float xd = *reinterpret_cast<const float*>(xs + b * kQ8KBytes);
             const int* t = terms + (r * nb + b) * 10;
-            uint16_t dbits;
-            if constexpr (TYPE == 12)
-                dbits = uint16_t(wb[0] | (wb[1] << 8));
-            else
-                dbits = uint16_t(wb[208] | (wb[209] << 8));
-            const float d = half_bits_to_f32(dbits) * xd;
+            const float d = half_bits_to_f32(uint16_t(wb[208] | (wb[209] << 8))) * xd;
 #pragma unroll
             for (int l = 0; l < 8; ++l) sums[l] += d * float(t[l]);
-            if constexpr (TYPE == 12) {
-                const float dmin = half_bits_to_f32(uint16_t(wb[2] | (wb[3] << 8))) * xd;
-                sumf -= dmin * float(t[8]);
-            }
         }
 #pragma unroll
         for (int l = 0; l < 8; ++l) sumf += sums[l];
@@ -244,11 +299,17 @@ __global__ __launch_bounds__(kKqThreads) void kquant_gemm_kernel(const uint8_t* 
 
 }  // namespace
 
-int64_t act_q8_K_bytes(int64_t m, int64_t k) { return m * (k / 256) * kQ8KBytes; }
+// GGUF Q8_K blocks, then (16-byte aligned) the regrouped int8 copy: 256 bytes per block
+int64_t act_q8_K_bytes(int64_t m, int64_t k) { return ((m * (k / 256) * kQ8KBytes + 15) & ~int64_t(15)) + m * (k / 256) * 256; }
+
+static const uint32_t* regrouped_of(const void* act, int64_t nblocks) {
+    return reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(act) + ((nblocks * kQ8KBytes + 15) & ~int64_t(15)));
+}
 
 void launch_quantize_q8_K(const float* x, void* act, int64_t M, int64_t K, hipStream_t s) {
     const int64_t nblocks = M * (K / 256);
-    hipLaunchKernelGGL(quantize_q8_K_kernel, dim3(unsigned(nblocks)), dim3(64), 0, s, x, static_cast<uint8_t*>(act), nblocks);
+    auto* xt = const_cast<uint32_t*>(regrouped_of(act, nblocks));
+    hipLaunchKernelGGL(quantize_q8_K_kernel, dim3(unsigned(nblocks)), dim3(64), 0, s, x, static_cast<uint8_t*>(act), xt, nblocks);
 }
 
 int kquant_rows_per_group(int type, int64_t K) {
@@ -256,22 +317,27 @@ int kquant_rows_per_group(int type, int64_t K) {
     const int64_t rb = nb * (type == 12 ? 144 : 210);
     const int64_t fixed = ((nb * kQ8KBytes + 15) & ~int64_t(15));
     int64_t r = std::min<int64_t>(kKqThreads / std::max<int64_t>(1, nb), 64);
-    while (r > 0 && ((16 + r * rb + 15) & ~int64_t(15)) + fixed + nb * 256 + r * nb * 10 * 4 > kKqLdsMax) --r;
+    if (type == 12) return nb <= kQ4Threads ? int(std::max<int64_t>(1, kQ4Threads / nb)) : 0;  // no staging
+    while (r > 0 && ((16 + r * rb + 15) & ~int64_t(15)) + fixed + r * nb * 10 * 4 > kKqLdsMax) --r;
     return int(std::max<int64_t>(r, 0));
 }
 
 void launch_kquant_gemm(int type, const void* w, const void* act, float* y, int64_t M, int64_t N, int64_t K, hipStream_t s) {
+    if (type == 12) {
+        const int nb = int(K / 256), R = std::max(1, kQ4Threads / nb);
+        const dim3 grid(unsigned((N + R - 1) / R), unsigned(M));
+        hipLaunchKernelGGL(q4k_gemm_kernel, grid, dim3(kQ4Threads), 0, s, static_cast<const uint8_t*>(w), static_cast<const uint8_t*>(act),
+                           regrouped_of(act, M * nb), y, N, K, R);
+        return;
+    }
     const int R = kquant_rows_per_group(type, K);
     const int64_t nb = K / 256;
     const int64_t rb = nb * (type == 12 ? 144 : 210);
-    const size_t lds = size_t(((16 + R * rb + 15) & ~int64_t(15)) + ((nb * kQ8KBytes + 15) & ~int64_t(15)) + nb * 256 + int64_t(R) * nb * 10 * 4);
+    const size_t lds = size_t(((16 + R * rb + 15) & ~int64_t(15)) + ((nb * kQ8KBytes + 15) & ~int64_t(15)) + int64_t(R) * nb * 10 * 4);
     const dim3 grid(unsigned((N + R - 1) / R), unsigned(M));
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* ab = static_cast<const uint8_t*>(act);
-    if (type == 12)
-        hipLaunchKernelGGL(kquant_gemm_kernel<12>, grid, dim3(kKqThreads), lds, s, wb, ab, y, N, K, R);
-    else
-        hipLaunchKernelGGL(kquant_gemm_kernel<14>, grid, dim3(kKqThreads), lds, s, wb, ab, y, N, K, R);
+    hipLaunchKernelGGL(kquant_gemm_kernel<14>, grid, dim3(kKqThreads), lds, s, wb, ab, y, N, K, R);
 }
 
 }  // namespace hero

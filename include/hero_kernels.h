@@ -121,9 +121,10 @@ int hero_argmax(const float* logits, int64_t m, int64_t n, int32_t* out, uint64_
  * y[m][n] = vec_dot_q{4,6}_K_q8_K(k, W row n, act row m) (the x86 scalar
  * forms, nm/src/quant_i8.hpp:146-191, 239-278), bit for bit.
  * W is the GGUF tensor as stored (n rows of k/256 blocks of 144 / 210 bytes),
- * 16-byte aligned. act holds hero_q8_K_act_bytes(m, k) bytes of GGUF Q8_K
- * blocks (fp32 d, 256 int8, 16 int16 sums). k: a multiple of 256, at most
- * 65536. */
+ * 16-byte aligned. act holds hero_q8_K_act_bytes(m, k) bytes: the m rows of
+ * GGUF Q8_K blocks (fp32 d, 256 int8, 16 int16 sums), then, 16-byte aligned, a
+ * copy of each block's int8 regrouped for 4-way dots (256 bytes per block).
+ * k: a multiple of 256, at most 65536. */
 int64_t hero_q8_K_act_bytes(int64_t m, int64_t k);
 int hero_q8_K_quantize(const float* x, void* act, int64_t m, int64_t k, void* stream);
 int hero_kquant_gemm(int32_t type, const void* w, const void* act, float* y, int64_t m, int64_t n, int64_t k, void* stream);

@@ -31,7 +31,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 def test_kquant_argument_errors_are_reported_before_any_launch():
     lib = _lib.lib
-    assert lib.hero_q8_K_act_bytes(3, 4096) == 3 * 16 * 292
+    assert lib.hero_q8_K_act_bytes(3, 4096) == 3 * 16 * 292 + 3 * 16 * 256  # blocks, then the regrouped copy
     assert lib.hero_kquant_gemm(13, 16, 16, 16, 1, 64, 4096, None) == _lib.HERO_EINVAL
     assert b"Q4_K" in lib.hero_last_error()
     assert lib.hero_kquant_gemm(12, 16, 16, 16, 1, 64, 4000, None) == _lib.HERO_EINVAL

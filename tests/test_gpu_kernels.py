@@ -687,7 +687,8 @@ def test_q8_K_quantizer_and_kquant_products_match_reference_golden(lib, kernels_
     x = kernels_golden["in_kq_x"].reshape(4, 4096)
     for wtype, name, out in [(oracle.Q4_K, "kq_w4", "kq_y4"), (oracle.Q6_K, "kq_w6", "kq_y6")]:
         act, y = kquant_dev(lib, wtype, kernels_golden[f"in_{name}"], x, 64, 4096)
-        assert act.tobytes() == kernels_golden["out_kq_act"].tobytes()
+        golden_act = kernels_golden["out_kq_act"]
+        assert act[:golden_act.size].tobytes() == golden_act.tobytes()
         expect = kernels_golden[f"out_{out}"].reshape(5, 64)
         assert np.array_equal(bits(y[0]), bits(expect[0]))
         assert np.array_equal(bits(y), bits(expect[1:])), name
@@ -704,7 +705,13 @@ def test_kquant_gemm_matches_oracle_bitwise(lib, wtype, m, n, k):
     x = (rng.standard_normal((m, k)) * np.exp(rng.uniform(-3, 3, (m, 1)))).astype(np.float32)
     act, y = kquant_dev(lib, wtype, w, x, n, k)
     expect_act = np.concatenate([oracle.quantize_row_q8_K(x[r]) for r in range(m)])
-    assert act.tobytes() == expect_act.tobytes()
+    assert act[:expect_act.size].tobytes() == expect_act.tobytes()
+    # the regrouped copy after the blocks: per sub-block j, dword 8j + l holds
+    # the int8 at 32j + l, +8, +16, +24
+    off = (expect_act.size + 15) // 16 * 16
+    q = expect_act[:, 4:260].reshape(-1, 8, 4, 8)             # [block][j][rep][l]
+    regrouped = np.ascontiguousarray(q.transpose(0, 1, 3, 2))  # [block][j][l][rep]
+    assert act[off:off + regrouped.size].tobytes() == regrouped.tobytes()
     expect = oracle.matmul_kquant(wtype, w, n, k, x)
     bad = np.flatnonzero(bits(y).ravel() != bits(expect).ravel())
     assert bad.size == 0, f"{bad.size} outputs differ, first {bad[:5]}: {y.ravel()[bad[:3]]} vs {expect.ravel()[bad[:3]]}"

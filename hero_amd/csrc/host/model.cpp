@@ -304,7 +304,7 @@ std::unique_ptr<Qwen35Model::State> Qwen35Model::new_state(int64_t max_tokens, i
 }
 
 Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batch, bool kv_fp16)
-    : m_(m), max_tokens_(max_tokens), batch_(batch), seq_tokens_(size_t(batch), 0), kv_fp16_(kv_fp16) {
+    : m_(m), max_tokens_(max_tokens), batch_(batch), kv_fp16_(kv_fp16), seq_tokens_(size_t(batch), 0) {
     const ModelConfig& c = m.c_;
     const int64_t B = batch;
     int64_t n_in_max = 0;

@@ -750,3 +750,14 @@ def test_sampler_matches_oracle(lib, k, temp, p):
         d = dev(x)
         for u in (0.0, 0.123, 0.5, 0.987654):
             assert sample_dev(lib, d, v, k, temp, p, u) == oracle.sample_topk(x, k, temp, p, u), (k, temp, p, u)
+
+
+@pytest.mark.parametrize("v,k", [(100, 1024), (1, 1), (1023, 500), (5000, 1024)])
+def test_sampler_small_vocabularies(lib, v, k):
+    """fewer logits than lanes (top_k above V means V), a single logit, and a
+    vocabulary where k reaches past the lane-maximum bound"""
+    rng = np.random.default_rng(v + k)
+    x = (rng.standard_normal(v) * 3).astype(np.float32)
+    d = dev(x)
+    for u in (0.0, 0.31, 0.999):
+        assert sample_dev(lib, d, v, k, 0.8, 0.95, u) == oracle.sample_topk(x, k, 0.8, 0.95, u), (v, k, u)

@@ -89,6 +89,7 @@ SIGNATURES = {
     "hero_q8_0_pack_interleaved": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p]),
     "hero_rmsnorm_q8_0_gemv_swiglu": (c_int, [c_void_p, c_void_p, c_void_p, c_float, c_void_p, c_int64, c_int64, c_void_p]),
     "hero_q8_0_gemm": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p]),
+    "hero_q8_0_gemm_plan": (c_int, [c_int64, c_int64, c_int64, c_void_p]),
     "hero_q8_0_block_sums": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "hero_rmsnorm_quant": (c_int, [c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "hero_swiglu_quant": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p]),

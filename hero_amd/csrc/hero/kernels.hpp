@@ -56,6 +56,10 @@ void launch_gemv_q8_in(const void* packed, const GemvInput& in, float* y, const 
 // Y[M][N] (+ R) = the M quantized activation rows (act_q8 layout, M rows)
 // times W^T, each element in the reference's block order; int8 MFMA.
 void launch_gemm_q8(const void* packed, const void* act, float* y, const float* resid, int64_t M, int64_t N, int64_t K, int epi, hipStream_t s);
+// Which kernel launch_gemm_q8 runs for a shape: one of the two skinny forms
+// (M <= 16) or the tiled kernel's row-tile height BM (16, 32, 64, 128).
+enum : int { kGemmPlanSkinnyWave = 1, kGemmPlanSkinnyShared = 2 };
+int gemm_q8_plan(int64_t M, int64_t N, int64_t K);
 void launch_block_sums(const void* packed, const void* act, int32_t* out, int64_t N, int64_t K, hipStream_t s);
 
 // norm.hip: rows x [M][D] -> RMSNorm (gamma, eps) -> quantized act; y (fp32) optional

@@ -184,6 +184,15 @@ int hero_q8_0_gemm(const void* packed, const void* act, float* y, const float* r
     });
 }
 
+int hero_q8_0_gemm_plan(int64_t m, int64_t n, int64_t k, int32_t* kernel) {
+    return guard([&] {
+        check_q8_shape(n, k);
+        require(m > 0 && m <= (int64_t(1) << 20), "bad row count");
+        require(kernel, "null pointer");
+        *kernel = gemm_q8_plan(m, n, k);
+    });
+}
+
 int hero_q8_0_block_sums(const void* packed, const void* act, int32_t* out, int64_t n, int64_t k, void* stream) {
     return guard([&] {
         check_q8_shape(n, k);

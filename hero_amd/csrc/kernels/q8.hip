@@ -931,6 +931,21 @@ void gemm_dispatch(int epi, const int8_t* wq, const uint16_t* wd, const int8_t* 
 }
 }  // namespace
 
+int gemm_q8_plan(int64_t M, int64_t N, int64_t K) {
+    const int64_t groups = (N + 15) / 16;
+    if (M <= 16 && groups >= 2 * device_cus() && K % (32 * kSkwRound) == 0 && K <= kSkwMaxK && N * K < (int64_t(1) << 31))
+        return kGemmPlanSkinnyWave;
+    if (M <= 16 && K % 256 == 0 && K <= kSkMaxK && N * K < (int64_t(1) << 31)) return kGemmPlanSkinnyShared;
+    // the tallest tile that still gives every CU two workgroups (the fp32
+    // term work per CU is the same; more workgroups hide more latency)
+    const int64_t tiles_n = (N + kGemmBN - 1) / kGemmBN, want = 2 * device_cus();
+    auto grid_of = [&](int64_t bm) { return tiles_n * ((M + bm - 1) / bm); };
+    if (M > 64 && grid_of(128) >= want) return 128;
+    if (M > 32 && grid_of(64) >= want) return 64;
+    if (M > 16 && grid_of(32) >= want) return 32;
+    return 16;
+}
+
 void launch_gemm_q8(const void* packed, const void* act, float* y, const float* resid, int64_t M, int64_t N, int64_t K, int epi, hipStream_t s) {
     const int8_t* wq = static_cast<const int8_t*>(packed);
     const uint16_t* wd = reinterpret_cast<const uint16_t*>(wq + N * K);
@@ -945,13 +960,15 @@ void launch_gemm_q8(const void* packed, const void* act, float* y, const float* 
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, smem) != hipSuccess || per_cu <= 0) per_cu = 1;
         return unsigned(std::min<int64_t>(int64_t(per_cu) * device_cus(), groups));
     };
-    if (M <= 16 && groups >= 2 * device_cus() && K % (32 * kSkwRound) == 0 && K <= kSkwMaxK && N * K < (int64_t(1) << 31)) {
+    switch (gemm_q8_plan(M, N, K)) {
+    case kGemmPlanSkinnyWave:
         // tall: a wave per group range, every chain in registers
         if (epi == kEpiResidual)
             hipLaunchKernelGGL(gemm_q8_skinny_wave_kernel<kEpiResidual>, dim3(grid_for(gemm_q8_skinny_wave_kernel<kEpiResidual>, 64, 0)), dim3(64), 0, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
         else
             hipLaunchKernelGGL(gemm_q8_skinny_wave_kernel<kEpiStore>, dim3(grid_for(gemm_q8_skinny_wave_kernel<kEpiStore>, 64, 0)), dim3(64), 0, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
-    } else if (M <= 16 && K % 256 == 0 && K <= kSkMaxK && N * K < (int64_t(1) << 31)) {
+        break;
+    case kGemmPlanSkinnyShared: {
         // few groups: sixteen waves share each group's blocks
         constexpr int NW = 16;
         const size_t smem = size_t(K / 32) * 16 * 4;  // the activation scales
@@ -959,19 +976,12 @@ void launch_gemm_q8(const void* packed, const void* act, float* y, const float* 
             hipLaunchKernelGGL((gemm_q8_skinny_kernel<kEpiResidual, NW>), dim3(grid_for(gemm_q8_skinny_kernel<kEpiResidual, NW>, 64 * NW, smem)), dim3(64 * NW), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
         else
             hipLaunchKernelGGL((gemm_q8_skinny_kernel<kEpiStore, NW>), dim3(grid_for(gemm_q8_skinny_kernel<kEpiStore, NW>, 64 * NW, smem)), dim3(64 * NW), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
-    } else {
-        // the tallest tile that still gives every CU two workgroups (the fp32
-        // term work per CU is the same; more workgroups hide more latency)
-        const int64_t tiles_n = (N + kGemmBN - 1) / kGemmBN, want = 2 * device_cus();
-        auto grid_of = [&](int64_t bm) { return tiles_n * ((M + bm - 1) / bm); };
-        if (M > 64 && grid_of(128) >= want)
-            gemm_dispatch<128>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s);
-        else if (M > 32 && grid_of(64) >= want)
-            gemm_dispatch<64>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s);
-        else if (M > 16 && grid_of(32) >= want)
-            gemm_dispatch<32>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s);
-        else
-            gemm_dispatch<16>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s);
+        break;
+    }
+    case 128: gemm_dispatch<128>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s); break;
+    case 64: gemm_dispatch<64>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s); break;
+    case 32: gemm_dispatch<32>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s); break;
+    default: gemm_dispatch<16>(epi, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K), s); break;
     }
 }
 

@@ -93,6 +93,15 @@ int hero_rmsnorm_q8_0_gemv_swiglu(const void* packed, const float* x, const floa
  * ([M][N]). For prefill and batched decode. */
 int hero_q8_0_gemm(const void* packed, const void* act, float* y, const float* residual, int64_t m, int64_t n, int64_t k, void* stream);
 
+/* Which kernel hero_q8_0_gemm runs for an (m, n, k) on the current device,
+ * without running it: *kernel = 1 (skinny, one wave per range of 16-row
+ * groups), 2 (skinny, sixteen waves sharing each group) or the tiled
+ * kernel's rows per tile (16, 32, 64, 128). The choice depends on the
+ * device's compute-unit count. No counterpart in the reference (its matmul
+ * has one form, nm/src/quant_i8.hpp:430-474); lets tests show that every
+ * form was checked. */
+int hero_q8_0_gemm_plan(int64_t m, int64_t n, int64_t k, int32_t* kernel);
+
 /* Exact int32 block dot products out[N][K/32] of one activation row: the
  * `sumi` of nm/src/quant_i8.hpp:94-95, exported for parity checks. */
 int hero_q8_0_block_sums(const void* packed, const void* act, int32_t* out, int64_t n, int64_t k, void* stream);

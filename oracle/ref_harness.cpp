@@ -4,8 +4,9 @@
 // committed); it needs the reference tree at build time only.
 //
 //   ref_harness kernels DIR          read DIR/*.in.bin, write DIR/*.out.bin
+//   ref_harness window DIR           causal / sliding-window attention cases
 //   ref_harness model CFG GGUF PROMPT STEPS OUTDIR
-//        CFG = tiny | 8b. Prefill the int32 ids in PROMPT through
+//        CFG = tiny | tiny_hk4u | 8b. Prefill the int32 ids in PROMPT through
 //        PrefixCache::evaluate, then STEPS greedy decode passes, exactly as
 //        tools/qwen35_check.cpp:43-70 does (minus the tokenizer).
 //
@@ -61,6 +62,20 @@ struct TinyConfig {
     static constexpr Scalar RMS_EPS = 1e-6f;
     static constexpr size_t FULL_ATTENTION_INTERVAL = 4;
     using OutputWeight = std::monostate;
+    static constexpr bool is_recurrent(size_t layer) { return (layer + 1) % FULL_ATTENTION_INTERVAL != 0; }
+};
+// the tiny shape with 4 key heads tiled over 8 value heads in the delta-net
+// (nm/src/qwen35.hpp:164-172) and a separate output.weight (untied head,
+// nm/src/qwen35_loader.hpp:132-139)
+struct TinyHk4UntiedConfig {
+    static constexpr size_t V = 32000, D = 1024, L = 4, CTX = 4096;
+    static constexpr size_t Hq = 8, Hkv = 2, HEAD_DIM = 128;
+    static constexpr size_t ROPE_BASE = 1000000, ROTARY_NUM = 1, ROTARY_DEN = 4;
+    static constexpr size_t KEY_HEAD_DIM = 128, VALUE_HEAD_DIM = 128, KEY_HEADS = 4, VALUE_HEADS = 8, CONV_WIDTH = 4;
+    static constexpr size_t FF = 2816;
+    static constexpr Scalar RMS_EPS = 1e-6f;
+    static constexpr size_t FULL_ATTENTION_INTERVAL = 4;
+    using OutputWeight = Weight<D, V>;
     static constexpr bool is_recurrent(size_t layer) { return (layer + 1) % FULL_ATTENTION_INTERVAL != 0; }
 };
 struct Hybrid8BConfig {
@@ -298,17 +313,85 @@ int run_kernels(const std::string& dir) {
     return 0;
 }
 
+// ---- causal and sliding-window attention over the reference's own caches ------
+// Keys and values of `ctx` consecutive positions are appended one at a time to
+// a FullAttentionCache (width 0) or a LocalAttentionCache ring (widths 3 and
+// 1024, evicting); at each probe position the query of that position attends
+// over cache.visible_rows(), the reduction of nm/src/gemma4.hpp:586-606
+// (score = scale * dot, Softmax, sum of alpha * value, K/V head = head / group).
+// Four query heads over two K/V heads of 128.
+int run_window(const std::string& dir) {
+    constexpr size_t Hq = 4, Hkv = 2, Dh = 128, KW = Hkv * Dh, QW = Hq * Dh;
+    const std::vector<float> k = read_bin<float>(dir + "/window_k.in.bin");  // [ctx][KW]
+    const std::vector<float> v = read_bin<float>(dir + "/window_v.in.bin");  // [ctx][KW]
+    const std::vector<float> q = read_bin<float>(dir + "/window_q.in.bin");  // [ctx][QW]
+    const std::vector<float> probes_f = read_bin<float>(dir + "/window_probes.in.bin");
+    const size_t ctx = k.size() / KW;
+    std::vector<size_t> probes;
+    for (float p : probes_f) probes.push_back(size_t(p));
+    Matrix<KW> K, V;
+    Matrix<QW> Q;
+    for (size_t t = 0; t < ctx; ++t) {
+        K.append(vec_from<KW>(k.data() + t * KW));
+        V.append(vec_from<KW>(v.data() + t * KW));
+        Q.append(vec_from<QW>(q.data() + t * QW));
+    }
+    auto attend = [&](auto& cache, size_t t, float scale, std::vector<float>& outv) {
+        const VisibleRows rows = cache.visible_rows(Position{t});
+        for (size_t head = 0; head < Hq; ++head) {
+            const VecView<Dh> query = slice<Dh>(Q.row(t), head);
+            const KVHead group{head / (Hq / Hkv)};
+            std::vector<Scalar> alpha;
+            for (size_t j = rows.first; j < rows.end; ++j) alpha.push_back(scale * dot(query, cache.key(j, group)));
+            alpha = Softmax{}(std::move(alpha));
+            Vec<Dh> o;
+            for (size_t n = 0; n < alpha.size(); ++n) o.scaled_add(cache.value(rows.first + n, group), alpha[n]);
+            outv.insert(outv.end(), o.p.get(), o.p.get() + Dh);
+        }
+        outv.push_back(float(rows.first));
+        outv.push_back(float(rows.end));
+    };
+    auto run = [&](auto& cache, float scale, const char* name) {
+        std::vector<float> outv;
+        size_t next = 0;
+        for (size_t t = 0; t < ctx; ++t) {
+            cache.append(Position{t}, K.row(t), V.row(t));
+            if (next < probes.size() && probes[next] == t) {
+                attend(cache, t, scale, outv);
+                ++next;
+            }
+        }
+        write_bin(dir + "/" + name + ".out.bin", outv.data(), outv.size());
+    };
+    {
+        FullAttentionCache<Hkv, Dh> cache;
+        run(cache, 1.f / std::sqrt(128.f), "window_full");
+    }
+    {
+        LocalAttentionCache<Hkv, Dh> cache(3);
+        run(cache, 1.f, "window_w3");
+    }
+    {
+        LocalAttentionCache<Hkv, Dh> cache(1024);
+        run(cache, 1.f, "window_w1024");
+    }
+    std::printf("window golden vectors written to %s\n", dir.c_str());
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
     try {
         if (argc == 3 && std::strcmp(argv[1], "kernels") == 0) return run_kernels(argv[2]);
+        if (argc == 3 && std::strcmp(argv[1], "window") == 0) return run_window(argv[2]);
         if (argc == 7 && std::strcmp(argv[1], "model") == 0) {
             const size_t steps = std::strtoull(argv[5], nullptr, 10);
             if (std::strcmp(argv[2], "tiny") == 0) return run_model<TinyConfig>(argv[3], argv[4], steps, argv[6]);
+            if (std::strcmp(argv[2], "tiny_hk4u") == 0) return run_model<TinyHk4UntiedConfig>(argv[3], argv[4], steps, argv[6]);
             if (std::strcmp(argv[2], "8b") == 0) return run_model<Hybrid8BConfig>(argv[3], argv[4], steps, argv[6]);
         }
-        std::fprintf(stderr, "usage: %s kernels DIR | model {tiny|8b} GGUF PROMPT STEPS OUTDIR\n", argv[0]);
+        std::fprintf(stderr, "usage: %s kernels DIR | window DIR | model {tiny|tiny_hk4u|8b} GGUF PROMPT STEPS OUTDIR\n", argv[0]);
         return 2;
     } catch (const std::exception& e) {
         std::fprintf(stderr, "ref_harness: %s\n", e.what());

@@ -69,3 +69,36 @@ def ulp_diff(a, b) -> np.ndarray:
         return np.where(u & 0x80000000, 0x80000000 - u, u)
 
     return np.abs(key(a) - key(b))
+
+
+def check(rc):
+    from hero_amd._lib import check as _check
+
+    _check(rc)
+
+
+def quantize_dev(lib, x: np.ndarray):
+    m, k = x.shape
+    xd = dev(x.astype(np.float32))
+    act = empty(lib.hero_q8_0_act_bytes(m, k))
+    check(lib.hero_q8_0_quantize(ptr(xd), ptr(act), m, k, stream()))
+    return act
+
+
+def gdn_reference(proj, taps, hist, state, dt, decay, gamma, eps, hk, hv, pos):
+    """one token through the oracle's pieces, in mix_tokens order (qwen35.hpp:420-462)"""
+    dk = 128
+    kw, cc = hk * dk, 2 * hk * dk + hv * dk
+    stream_ = oracle.silu(oracle.conv_step(proj[:cc], taps, hist))
+    q = np.concatenate([oracle.l2_normalize(stream_[i * dk:(i + 1) * dk]) for i in range(hk)])
+    qs = np.float32(1.0) / np.sqrt(np.float32(dk))
+    q = (q * qs).astype(np.float32)
+    k = np.concatenate([oracle.l2_normalize(stream_[kw + i * dk: kw + (i + 1) * dk]) for i in range(hk)])
+    v = stream_[2 * kw:]
+    beta = oracle.sigmoid(proj[cc + hv * dk: cc + hv * dk + hv])
+    alpha = proj[cc + hv * dk + hv: cc + hv * dk + 2 * hv]
+    gate = (decay * oracle.softplus((alpha + dt).astype(np.float32))).astype(np.float32)
+    o = oracle.gated_delta_step(state, q, k, v, gate, beta, hk)
+    o = oracle.rmsnorm(o, gamma, eps).reshape(-1)
+    z = proj[cc: cc + hv * dk]
+    return (o * oracle.silu(z)).astype(np.float32)

@@ -1,0 +1,123 @@
+"""The ~8B Q8_0 hybrid (32 layers: 24 gated delta-net + 8 GQA every 4th layer;
+d_model 4096, 32 q / 8 kv heads of 128, delta-net 32 heads of 128, SwiGLU
+12288, vocab 151936) against the oracle on the same model bytes, the way the
+reference's check tool drives it (tools/qwen35_check.cpp:43-70): prefill a
+prompt, then feed each greedy id back in.
+
+The prompt is 600 tokens long: it prefills as row chunks of 512 + 88, whose
+delta-net in-projection and gate/up GEMMs take the 128-row tile (the 88-row
+chunk and the narrower matrices take 64, 32 or 16); the decode passes run the
+batch-1 hipGraph (fused RMSNorm / SwiGLU GEMV forms, the 151936-row LM head).
+The same prompt then runs as one sequence of a 16-sequence batch state, whose
+decode takes the skinny GEMMs at their real shapes.
+
+Bar: greedy ids identical and logits bit-identical (the kernels replay the
+reference's fp32 operation order; the north star's 1e-2 abs / 1e-3 rel is the
+stated tolerance, bit equality is what this path delivers). The top-2 margin of
+every step is printed, so a near tie would be visible (none can flip while the
+logits are bit-identical)."""
+import os
+import time
+
+import numpy as np
+import pytest
+
+import hero_amd
+import oracle
+from gpu_util import bits, check
+
+pytestmark = pytest.mark.gpu
+
+SEED = 20260101
+PROMPT = 600
+STEPS = 32
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def margin(v):
+    top = np.partition(v, -2)[-2:]
+    return float(top[1] - top[0])
+
+
+def oracle_greedy(ref, prompt, steps):
+    ref.reset()
+    prefill = ref.forward_ids(prompt)
+    ids = [int(np.argmax(prefill))]
+    last = prefill
+    for _ in range(steps):
+        last = ref.forward_ids([ids[-1]])
+        ids.append(int(np.argmax(last)))
+    return prefill, ids, last
+
+
+@pytest.fixture(scope="module")
+def hybrid8b():
+    import torch
+
+    assert torch.cuda.is_available()
+    oracle.set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    t = time.perf_counter()
+    image = hero_amd.synthetic_gguf_image(hero_amd.HYBRID_8B_CONFIG, seed=SEED, ctx=512)
+    say(f"[8b] synthetic GGUF image {image.nbytes / 1e9:.2f} GB in {time.perf_counter() - t:.1f} s")
+    model = hero_amd.Qwen35Model.open_image(image)
+    ref = oracle.Model(image=image)
+    yield image, model, ref
+    model.close()
+    ref.close()
+
+
+@pytest.mark.timeout(1200)
+def test_hybrid8b_prefill_and_greedy_decode_match_oracle(hybrid8b):
+    import ctypes
+
+    _, model, ref = hybrid8b
+    from hero_amd._lib import lib
+
+    tiles = {}
+    for m in (512, PROMPT - 512):
+        for n in (16448, 24576, 10240, 4096):  # delta-net in-proj, gate|up, attention in-proj, out-proj
+            tile = ctypes.c_int32()
+            check(lib.hero_q8_0_gemm_plan(m, n, 4096, ctypes.byref(tile)))
+            tiles[(m, n)] = tile.value
+    say(f"[8b] prefill GEMM tiles ((rows, N): rows per tile): {tiles}")
+    assert tiles[(512, 16448)] == 128 and tiles[(512, 24576)] == 128
+    prompt = np.random.default_rng(SEED).integers(0, model.V, PROMPT).astype(np.int32)
+    t = time.perf_counter()
+    ref_prefill, ref_ids, ref_last = oracle_greedy(ref, prompt, STEPS)
+    say(f"[8b] oracle: {PROMPT}-token prefill + {STEPS} greedy passes in {time.perf_counter() - t:.1f} s; ids {ref_ids}")
+
+    state = model.new_state(512)
+    lg = model.forward(state, ids=prompt)
+    exact = float(np.mean(bits(lg.values) == bits(ref_prefill)))
+    say(f"[8b] prefill logits: exact fraction {exact:.6f}, max|d| {np.abs(lg.values - ref_prefill).max():.3g}, "
+        f"top-2 margin {margin(lg.values):.4g}")
+    assert np.array_equal(bits(lg.values), bits(ref_prefill))
+    ids, last = model.decode_greedy(state, lg.argmax(), STEPS, want_logits=True)
+    got = [lg.argmax()] + [int(i) for i in ids]
+    say(f"[8b] GPU greedy ids {got}; last-step top-2 margin {margin(last.values):.4g}")
+    assert got == ref_ids, f"first divergence at step {next(i for i, (a, b) in enumerate(zip(got, ref_ids)) if a != b)}"
+    assert np.array_equal(bits(last.values), bits(ref_last))
+    assert state.tokens() == PROMPT + STEPS
+    state.close()
+
+    # the same prompt as sequence 5 of a 16-sequence batch, next to sequences
+    # with short prompts; sequence 0's prompt also runs through the oracle
+    short = np.random.default_rng(SEED + 1).integers(0, model.V, 6).astype(np.int32)
+    bs = model.new_batch_state(512, 16)
+    firsts = []
+    for b in range(16):
+        p = prompt if b == 5 else (short if b == 0 else np.random.default_rng(SEED + 2 + b).integers(0, model.V, 1 + b % 9).astype(np.int32))
+        firsts.append(model.forward_seq(bs, b, ids=p).argmax())
+    out, logits = model.decode_batch(bs, firsts, STEPS, want_logits=True)
+    assert [firsts[5]] + [int(v) for v in out[:, 5]] == ref_ids
+    assert np.array_equal(bits(logits[5]), bits(ref_last))
+    t = time.perf_counter()
+    _, ref_ids0, ref_last0 = oracle_greedy(ref, short, STEPS)
+    say(f"[8b] oracle short prompt in {time.perf_counter() - t:.1f} s")
+    assert [firsts[0]] + [int(v) for v in out[:, 0]] == ref_ids0
+    assert np.array_equal(bits(logits[0]), bits(ref_last0))
+    say("[8b] batch of 16: sequences 0 and 5 equal the oracle bit for bit")
+    bs.close()

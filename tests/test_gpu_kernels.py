@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import oracle
-from gpu_util import act_to_blocks, bits, dev, empty, host, pack_weight, ptr, stream, ulp_diff
+from gpu_util import act_to_blocks, bits, check, dev, empty, gdn_reference, host, pack_weight, ptr, quantize_dev, stream, ulp_diff
 
 pytestmark = pytest.mark.gpu
 
@@ -20,20 +20,6 @@ def lib():
 
     assert torch.cuda.is_available(), "GPU tests need a GPU"
     return _lib
-
-
-def check(rc):
-    from hero_amd._lib import check as _check
-
-    _check(rc)
-
-
-def quantize_dev(lib, x: np.ndarray):
-    m, k = x.shape
-    xd = dev(x.astype(np.float32))
-    act = empty(lib.hero_q8_0_act_bytes(m, k))
-    check(lib.hero_q8_0_quantize(ptr(xd), ptr(act), m, k, stream()))
-    return act
 
 
 # ---- scalar functions --------------------------------------------------------------
@@ -338,25 +324,6 @@ def test_argmax_ties_go_to_lowest_index(lib):
 
 
 # ---- gated delta-net decode ---------------------------------------------------------
-def gdn_reference(proj, taps, hist, state, dt, decay, gamma, eps, hk, hv, pos):
-    """one token through the oracle's pieces, in mix_tokens order (qwen35.hpp:420-462)"""
-    dk = 128
-    kw, cc = hk * dk, 2 * hk * dk + hv * dk
-    stream_ = oracle.silu(oracle.conv_step(proj[:cc], taps, hist))
-    q = np.concatenate([oracle.l2_normalize(stream_[i * dk:(i + 1) * dk]) for i in range(hk)])
-    qs = np.float32(1.0) / np.sqrt(np.float32(dk))
-    q = (q * qs).astype(np.float32)
-    k = np.concatenate([oracle.l2_normalize(stream_[kw + i * dk: kw + (i + 1) * dk]) for i in range(hk)])
-    v = stream_[2 * kw:]
-    beta = oracle.sigmoid(proj[cc + hv * dk: cc + hv * dk + hv])
-    alpha = proj[cc + hv * dk + hv: cc + hv * dk + 2 * hv]
-    gate = (decay * oracle.softplus((alpha + dt).astype(np.float32))).astype(np.float32)
-    o = oracle.gated_delta_step(state, q, k, v, gate, beta, hk)
-    o = oracle.rmsnorm(o, gamma, eps).reshape(-1)
-    z = proj[cc: cc + hv * dk]
-    return (o * oracle.silu(z)).astype(np.float32)
-
-
 @pytest.mark.parametrize("hk,hv", [(8, 8), (4, 8)])
 def test_gdn_decode_matches_oracle(lib, hk, hv):
     from hero_amd._lib import GdnDecodeArgs

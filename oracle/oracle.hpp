@@ -11,17 +11,23 @@
 // result from the reference compiled with the same flags matches bit for bit.
 // Citations are file:line into nm/src of the reference.
 //
-// Parity status per function (what pins it; see tests/test_oracle_*.py):
-//   fp16 codec            exhaustive 2^16 decode check + closed-form encode cases + golden vectors
-//   quantize_row_q8_0     golden vectors from the compiled reference + invariants
-//   quantize_q8_0         golden vectors + round-trip bound
+// Parity status per function (what pins it; tests/test_oracle_golden.py holds
+// the golden-vector checks, tests/test_oracle_properties.py the closed forms):
+//   fp16 codec            exhaustive 2^16 decode check + nearest-ties-away encode sweep + golden vectors
+//   quantize_row_q8_0     golden vectors from the compiled reference
+//   quantize_q8_0         golden vectors + round trip within one quantum, |q| <= 127, zero block
 //   vec_dot_q8_0_q8_0     golden vectors; int32 block sums by brute force
-//   rmsnorm / l2 / silu   golden vectors + closed forms
-//   conv_step             closed form 100/210/321
-//   gated_delta_step      associative-memory identities + golden vectors + fp64 brute force
-//   rope                  golden vectors (tables) + offset identity
-//   attention             hand-worked causal/window cases + golden vectors
-//   Qwen35 forward        full-model golden logits and greedy ids of the tiny Q8_0 model
+//   rmsnorm / l2 / silu   golden vectors + scale invariance, row = batch, float64 closed form
+//   conv_step             golden vectors + closed form 100/210/321
+//   gated_delta_step      golden vectors + associative-memory identities + float64 brute force
+//                         (tiled key heads h % Hk, Hk != Hv)
+//   rope                  golden vectors (8 positions to 65535) + offset identity, position 0
+//   attention             golden vectors (scale 1/sqrt(128) and 1) + the reference's own
+//                         Full / Local (ring, width 3 and 1024) caches at 12 probes + hand-worked
+//                         causal / window-of-one cases + float64 brute force (grouped K/V heads)
+//   Qwen35 forward        golden logits and greedy ids of the tiny Q8_0 model, of its variant
+//                         with 4 key heads over 8 value heads and an untied output.weight, and
+//                         the greedy ids of the ~8B model (600-token prompt, 32 passes)
 #pragma once
 #include <cstddef>
 #include <cstdint>

@@ -57,3 +57,34 @@ def gpu_available() -> bool:
         return torch.cuda.is_available()
     except Exception:
         return False
+
+
+@pytest.fixture(scope="session")
+def window_golden():
+    return dict(np.load(os.path.join(GOLDEN, "window.npz")))
+
+
+@pytest.fixture(scope="session")
+def variant_golden():
+    return dict(np.load(os.path.join(GOLDEN, "tiny_hk4u_model.npz")))
+
+
+# the tiny shape with 4 delta-net key heads tiled over 8 value heads and an
+# untied output.weight (the golden's model)
+def variant_shape():
+    import hero_amd
+
+    return hero_amd.HybridShape(vocab=32000, d_model=1024, layers=4, ffn=2816, q_heads=8, kv_heads=2, head_dim=128,
+                                key_heads=4, value_heads=8)
+
+
+@pytest.fixture(scope="session")
+def variant_gguf(tmp_path_factory, manifest):
+    import hero_amd
+
+    t = manifest["tiny_hk4u_model"]
+    path = str(tmp_path_factory.mktemp("variant") / "tiny_hk4u.gguf")
+    hero_amd.write_synthetic_gguf(path, variant_shape(), seed=t["seed"], ctx=t["ctx"], tied=False)
+    with open(path, "rb") as f:
+        assert hashlib.sha256(f.read()).hexdigest() == t["gguf_sha256"], "synthetic variant model bytes changed"
+    return path

@@ -9,12 +9,21 @@ so it runs in the build container only). This script:
   2. writes the tiny Q8_0 hybrid model as GGUF with the package's seeded
      synthetic writer, runs `ref_harness model tiny` (16-token random prompt,
      128 greedy decode passes through PrefixCache::evaluate) and stores the
-     greedy ids, per-step top-5 and three full logit vectors in tiny_model.npz.
+     greedy ids, per-step top-5 and three full logit vectors in tiny_model.npz;
+  3. `window`: causal and sliding-window attention over the reference's own
+     FullAttentionCache / LocalAttentionCache (widths 3 and 1024, 1100
+     positions, probes before and after the ring starts evicting) -> window.npz;
+  4. `variant`: the tiny shape with 4 delta-net key heads tiled over 8 value
+     heads and an untied output.weight -> tiny_hk4u_model.npz;
+  5. `hybrid8b`: the ~8B shape (the benchmark's model, seed 20260101, a
+     600-token prompt, 32 greedy passes) -> hybrid8b_model.npz with the ids,
+     per-step top-5 and the sha256 of the prefill and last logit vectors.
 
 manifest.json records seeds, shapes, the GGUF's sha256 and the compiler
 flags (-O3 -march=x86-64-v3 -ffp-contract=off: no FMA contraction).
 
-Run:  python tests/golden/make_golden.py
+Run:  python tests/golden/make_golden.py [kernels] [tiny] [window] [variant] [hybrid8b]
+      (no argument: all parts; the manifest keeps the entries of parts not rerun)
 """
 from __future__ import annotations
 
@@ -163,17 +172,109 @@ def make_tiny(tmp: str) -> dict:
             "logits_mid_after_pass": DECODE_STEPS // 2}
 
 
+WINDOW_SEED = 1103
+WINDOW_CTX = 1100
+WINDOW_PROBES = [0, 1, 2, 3, 4, 7, 500, 1022, 1023, 1024, 1025, 1099]
+
+
+def make_window(tmp: str) -> dict:
+    """4 query heads over 2 K/V heads of 128; K, V, q N(0,1)/sqrt(128)"""
+    rng = np.random.default_rng(WINDOW_SEED)
+    s = np.float32(1 / np.sqrt(128.0))
+    k = f32(rng.standard_normal((WINDOW_CTX, 256)) * s)
+    v = f32(rng.standard_normal((WINDOW_CTX, 256)) * s)
+    q = f32(rng.standard_normal((WINDOW_CTX, 512)))
+    for name, a in (("window_k", k), ("window_v", v), ("window_q", q), ("window_probes", f32(WINDOW_PROBES))):
+        a.tofile(os.path.join(tmp, f"{name}.in.bin"))
+    subprocess.run([HARNESS, "window", tmp], check=True)
+    out = {"k": k, "v": v, "q": q, "probes": np.array(WINDOW_PROBES, np.int32)}
+    for name in ("window_full", "window_w3", "window_w1024"):
+        r = np.fromfile(os.path.join(tmp, f"{name}.out.bin"), np.float32).reshape(len(WINDOW_PROBES), 512 + 2)
+        out[name] = r[:, :512].copy()
+        out[name + "_rows"] = r[:, 512:].astype(np.int64)  # [first, end) of the visible cache rows
+    np.savez_compressed(os.path.join(HERE, "window.npz"), **out)
+    return {"seed": WINDOW_SEED, "ctx": WINDOW_CTX, "probes": WINDOW_PROBES, "q_heads": 4, "kv_heads": 2, "head_dim": 128,
+            "cases": {"window_full": "FullAttentionCache, scale 1/sqrt(128)", "window_w3": "LocalAttentionCache(3), scale 1",
+                      "window_w1024": "LocalAttentionCache(1024), scale 1"}}
+
+
+VARIANT_SEED = 4321
+HYBRID8B_SEED = 20260101
+HYBRID8B_PROMPT = 600
+HYBRID8B_STEPS = 32
+
+
+def run_model_case(tmp: str, cfg: str, shape, seed: int, ctx: int, tied: bool, prompt: np.ndarray, steps: int, where: str):
+    import hero_amd
+
+    gguf = os.path.join(where, f"{cfg}.gguf")
+    hero_amd.write_synthetic_gguf(gguf, shape, seed=seed, ctx=ctx, tied=tied)
+    h = hashlib.sha256()
+    with open(gguf, "rb") as f:
+        for chunk in iter(lambda: f.read(1 << 24), b""):
+            h.update(chunk)
+    size = os.path.getsize(gguf)
+    prompt.tofile(os.path.join(tmp, f"{cfg}_prompt.i32"))
+    outdir = os.path.join(tmp, f"{cfg}_out")
+    os.makedirs(outdir, exist_ok=True)
+    subprocess.run([HARNESS, "model", cfg, gguf, os.path.join(tmp, f"{cfg}_prompt.i32"), str(steps), outdir], check=True)
+    os.remove(gguf)
+    rd = lambda n, dt: np.fromfile(os.path.join(outdir, n), dtype=dt)  # noqa: E731
+    times = open(os.path.join(outdir, "times.txt")).read()
+    return rd, h.hexdigest(), size, times
+
+
+def make_variant(tmp: str) -> dict:
+    import hero_amd
+
+    shape = hero_amd.HybridShape(vocab=32000, d_model=1024, layers=4, ffn=2816, q_heads=8, kv_heads=2, head_dim=128,
+                                 key_heads=4, value_heads=8)
+    prompt = np.random.default_rng(VARIANT_SEED + 1).integers(0, 32000, 16).astype(np.int32)
+    rd, sha, size, times = run_model_case(tmp, "tiny_hk4u", shape, VARIANT_SEED, 4096, False, prompt, 32, tmp)
+    np.savez_compressed(
+        os.path.join(HERE, "tiny_hk4u_model.npz"), prompt=prompt, ids=rd("ids.i32", np.int32),
+        top5_ids=rd("top5_ids.i32", np.int32).reshape(-1, 5), top5_logits=rd("top5_logits.f32", np.float32).reshape(-1, 5),
+        logits_prefill=rd("logits_prefill.f32", np.float32), logits_last=rd("logits_last.f32", np.float32))
+    return {"seed": VARIANT_SEED, "key_heads": 4, "value_heads": 8, "tied": False, "ctx": 4096, "prompt_len": 16,
+            "decode_steps": 32, "gguf_sha256": sha, "gguf_bytes": size, "reference_times": times}
+
+
+def make_hybrid8b(tmp: str) -> dict:
+    import hero_amd
+
+    prompt = np.random.default_rng(HYBRID8B_SEED).integers(0, 151936, HYBRID8B_PROMPT).astype(np.int32)
+    shm = "/dev/shm" if os.path.isdir("/dev/shm") else tmp  # the 8.45 GB GGUF, mmapped by the harness
+    rd, sha, size, times = run_model_case(tmp, "8b", hero_amd.HYBRID_8B_CONFIG, HYBRID8B_SEED, 1024, True, prompt,
+                                          HYBRID8B_STEPS, shm)
+    digest = lambda a: hashlib.sha256(np.ascontiguousarray(a, np.float32).tobytes()).hexdigest()  # noqa: E731
+    np.savez_compressed(
+        os.path.join(HERE, "hybrid8b_model.npz"), prompt=prompt, ids=rd("ids.i32", np.int32),
+        top5_ids=rd("top5_ids.i32", np.int32).reshape(-1, 5), top5_logits=rd("top5_logits.f32", np.float32).reshape(-1, 5))
+    return {"seed": HYBRID8B_SEED, "ctx": 1024, "prompt_len": HYBRID8B_PROMPT, "decode_steps": HYBRID8B_STEPS,
+            "gguf_sha256": sha, "gguf_bytes": size, "reference_times": times,
+            "logits_prefill_sha256": digest(rd("logits_prefill.f32", np.float32)),
+            "logits_last_sha256": digest(rd("logits_last.f32", np.float32))}
+
+
+PARTS = {"kernels": make_kernels, "tiny": make_tiny, "window": make_window, "variant": make_variant, "hybrid8b": make_hybrid8b}
+MANIFEST_KEYS = {"kernels": "kernels", "tiny": "tiny_model", "window": "window", "variant": "tiny_hk4u_model",
+                 "hybrid8b": "hybrid8b_model"}
+
+
 def main():
     if not os.path.exists(HARNESS):
         sys.exit(f"{HARNESS} missing: build it with `make -C oracle` (needs the reference tree)")
+    parts = sys.argv[1:] or list(PARTS)
+    path = os.path.join(HERE, "manifest.json")
+    manifest = json.load(open(path)) if os.path.exists(path) else {}
+    manifest.update({
+        "generator": "tests/golden/make_golden.py",
+        "reference": "flywithfang/hero nm/src compiled by oracle/Makefile",
+        "flags": "g++ -std=c++20 -O3 -march=x86-64-v3 -ffp-contract=off",
+    })
     with tempfile.TemporaryDirectory() as tmp:
-        manifest = {
-            "generator": "tests/golden/make_golden.py",
-            "reference": "flywithfang/hero nm/src compiled by oracle/Makefile",
-            "flags": "g++ -std=c++20 -O3 -march=x86-64-v3 -ffp-contract=off",
-            "kernels": make_kernels(tmp),
-            "tiny_model": make_tiny(tmp),
-        }
+        for part in parts:
+            manifest[MANIFEST_KEYS[part]] = PARTS[part](tmp)
     with open(os.path.join(HERE, "manifest.json"), "w") as f:
         json.dump(manifest, f, indent=1, sort_keys=True)
     print(json.dumps(manifest, indent=1))

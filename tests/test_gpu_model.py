@@ -290,3 +290,21 @@ def test_d4096_model_matches_oracle_bitwise():
         same_bits(logits[1], ref_last)
     finally:
         m.close()
+
+
+def test_variant_model_matches_reference(variant_gguf, variant_golden):
+    """4 delta-net key heads tiled over 8 value heads (value head h reads key
+    head h % 4) and an untied output.weight, against the reference's own
+    outputs: prefill logits, the greedy ids of 32 graph-replayed decode passes
+    and the last logits, bit for bit."""
+    m = hero_amd.Qwen35Model.open(variant_gguf)
+    try:
+        assert (m.dims.key_heads, m.dims.value_heads, m.dims.tied) == (4, 8, 0)
+        state = m.new_state(256)
+        lg = m.forward(state, ids=variant_golden["prompt"])
+        same_bits(lg.values, variant_golden["logits_prefill"])
+        ids, last = m.decode_greedy(state, lg.argmax(), len(variant_golden["ids"]) - 1, want_logits=True)
+        assert np.array_equal(np.array([lg.argmax()] + [int(i) for i in ids], np.int32), variant_golden["ids"])
+        same_bits(last.values, variant_golden["logits_last"])
+    finally:
+        m.close()

@@ -268,3 +268,51 @@ def test_fp16_cache_rounding_is_ieee_nearest_even():
     want = x.astype(np.float16).astype(np.float32)
     got = oracle.round_fp16(x)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ---- causal and sliding-window visibility (CausalWindow / LocalAttentionCache) ----------
+WINDOW_CASES = [("window_full", 0, np.float32(1.0) / np.sqrt(np.float32(128.0))), ("window_w3", 3, np.float32(1.0)),
+                ("window_w1024", 1024, np.float32(1.0))]
+
+
+@pytest.mark.parametrize("name,window,scale", WINDOW_CASES)
+def test_window_attention_matches_reference(window_golden, name, window, scale):
+    """The oracle's attention over positions 0..t with a window, against the
+    reference's own caches (a full append-only cache; rings of 3 and 1024 rows
+    that evict) at probes before, at and after the ring fills: bit for bit."""
+    k, v, q = window_golden["k"], window_golden["v"], window_golden["q"]
+    for i, t in enumerate(window_golden["probes"]):
+        out = oracle.attend_decode(q[t], k[: t + 1], v[: t + 1], 4, 2, 128, window, scale)
+        assert np.array_equal(bits(out.ravel()), bits(window_golden[name][i])), f"{name} probe {t}"
+
+
+@pytest.mark.parametrize("name,window", [(c[0], c[1]) for c in WINDOW_CASES])
+def test_window_visible_positions_follow_the_reference_rule(window_golden, name, window):
+    """The reference's visible rows, mapped back to positions, are the closed
+    form the kernels and the oracle use: [max(0, t - W + 1), t] (all of 0..t
+    without a window)."""
+    for i, t in enumerate(window_golden["probes"]):
+        first, end = window_golden[name + "_rows"][i]
+        size = t + 1 if window == 0 else min(t + 1, window)  # rows the cache holds after appending position t
+        oldest = t + 1 - size
+        lo = 0 if window == 0 else max(0, t - window + 1)
+        assert (oldest + first, oldest + end) == (lo, t + 1), f"{name} probe {t}"
+
+
+# ---- Hk != Hv (tiled key heads) and an untied head -------------------------------------
+def test_variant_model_matches_reference(variant_gguf, variant_golden):
+    """4 key heads tiled over 8 value heads (value head h reads key head h % 4,
+    nm/src/qwen35.hpp:172) and a separate output.weight: the oracle's greedy
+    ids and its prefill / last logits equal the reference's bit for bit."""
+    m = oracle.Model(path=variant_gguf)
+    assert (m.Hk, m.Hv, m.tied) == (4, 8, 0)
+    prompt = variant_golden["prompt"]
+    prefill = m.forward_ids(prompt)
+    assert np.array_equal(bits(prefill), bits(variant_golden["logits_prefill"]))
+    ids = [oracle.argmax(prefill)]
+    for _ in range(len(variant_golden["ids"]) - 1):
+        last = m.forward_ids([ids[-1]])
+        ids.append(oracle.argmax(last))
+    assert np.array_equal(np.array(ids, np.int32), variant_golden["ids"])
+    assert np.array_equal(bits(last), bits(variant_golden["logits_last"]))
+    m.close()

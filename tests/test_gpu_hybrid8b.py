@@ -60,7 +60,7 @@ def hybrid8b():
     assert torch.cuda.is_available()
     oracle.set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
     t = time.perf_counter()
-    image = hero_amd.synthetic_gguf_image(hero_amd.HYBRID_8B_CONFIG, seed=SEED, ctx=512)
+    image = hero_amd.synthetic_gguf_image(hero_amd.HYBRID_8B_CONFIG, seed=SEED, ctx=1024)
     say(f"[8b] synthetic GGUF image {image.nbytes / 1e9:.2f} GB in {time.perf_counter() - t:.1f} s")
     model = hero_amd.Qwen35Model.open_image(image)
     ref = oracle.Model(image=image)
@@ -89,7 +89,7 @@ def test_hybrid8b_prefill_and_greedy_decode_match_oracle(hybrid8b):
     ref_prefill, ref_ids, ref_last = oracle_greedy(ref, prompt, STEPS)
     say(f"[8b] oracle: {PROMPT}-token prefill + {STEPS} greedy passes in {time.perf_counter() - t:.1f} s; ids {ref_ids}")
 
-    state = model.new_state(512)
+    state = model.new_state(1024)
     lg = model.forward(state, ids=prompt)
     exact = float(np.mean(bits(lg.values) == bits(ref_prefill)))
     say(f"[8b] prefill logits: exact fraction {exact:.6f}, max|d| {np.abs(lg.values - ref_prefill).max():.3g}, "
@@ -106,7 +106,7 @@ def test_hybrid8b_prefill_and_greedy_decode_match_oracle(hybrid8b):
     # the same prompt as sequence 5 of a 16-sequence batch, next to sequences
     # with short prompts; sequence 0's prompt also runs through the oracle
     short = np.random.default_rng(SEED + 1).integers(0, model.V, 6).astype(np.int32)
-    bs = model.new_batch_state(512, 16)
+    bs = model.new_batch_state(1024, 16)
     firsts = []
     for b in range(16):
         p = prompt if b == 5 else (short if b == 0 else np.random.default_rng(SEED + 2 + b).integers(0, model.V, 1 + b % 9).astype(np.int32))

@@ -95,6 +95,7 @@ SIGNATURES = {
     "hero_swiglu_quant": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "hero_q8_0_embed": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
     "hero_argmax": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
+    "hero_argmax_noalloc": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
     "hero_math_eval": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
     "hero_sample_topk": (c_int, [c_void_p, c_int64, c_int32, c_float, c_float, c_float, c_void_p, c_void_p]),
     "hero_q8_K_act_bytes": (c_int64, [c_int64, c_int64]),

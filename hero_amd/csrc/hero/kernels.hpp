@@ -72,6 +72,9 @@ void launch_swiglu_quant(const float* gate_up, void* act, int64_t M, int64_t FF,
 void launch_embed_q8(const void* packed_embedding, int64_t V, int64_t D, const int32_t* ids, int64_t n, float* out, hipStream_t s);
 // argmax over n logits per row (ties -> lowest index); out_index[M]
 void launch_argmax(const float* logits, int64_t M, int64_t n, int32_t* out_index, uint64_t* scratch_keys, hipStream_t s);
+// the same with the keys in a static device array (no allocation); M <= 64
+constexpr int kArgmaxGroups = 128, kArgmaxNoallocRows = 64;
+void launch_argmax_noalloc(const float* logits, int64_t M, int64_t n, int32_t* out_index, hipStream_t s);
 
 // exp, log1p, silu, sigmoid, softplus of x[n] -> out[5][n] (parity export)
 void launch_math_eval(const float* x, float* out, int64_t n, hipStream_t s);

@@ -242,6 +242,15 @@ int hero_argmax(const float* logits, int64_t m, int64_t n, int32_t* out, uint64_
     });
 }
 
+int hero_argmax_noalloc(const float* logits, int64_t m, int64_t n, int32_t* out, void* stream) {
+    return guard([&] {
+        require(m > 0 && n > 0 && n < (int64_t(1) << 31), "bad shape");
+        require(logits && out, "null pointer");
+        launch_argmax_noalloc(logits, m, n, out, as_stream(stream));
+        check_launch("hero_argmax_noalloc");
+    });
+}
+
 int hero_math_eval(const float* x, float* out, int64_t n, void* stream) {
     return guard([&] {
         require(x && out && n > 0 && n < (int64_t(1) << 40), "bad arguments");

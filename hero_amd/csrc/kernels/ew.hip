@@ -1,6 +1,9 @@
 // ew.hip -- small elementwise kernels around the GEMVs: SwiGLU + quantize,
 // the Q8_0 embedding gather, and the greedy argmax.
+#include <mutex>
+
 #include "hero/device.hpp"
+#include "hero/errors.hpp"
 #include "hero/kernels.hpp"
 
 namespace hero {
@@ -64,7 +67,6 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
     return k;
 }
 
-constexpr int kArgmaxGroups = 128;
 
 __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ logits, int64_t n, uint64_t* __restrict__ partial) {
     const int64_t row = blockIdx.y;
@@ -96,6 +98,40 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const uint64_t* __rest
 void launch_argmax(const float* logits, int64_t M, int64_t n, int32_t* out_index, uint64_t* scratch, hipStream_t s) {
     hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxGroups, unsigned(M)), dim3(256), 0, s, logits, n, scratch);
     hipLaunchKernelGGL(argmax_final_kernel, dim3(unsigned(M)), dim3(64), 0, s, scratch, kArgmaxGroups, out_index);
+}
+
+// ---- argmax without allocation ---------------------------------------------
+// The partial keys of hero_argmax_noalloc live in this file-scope device array
+// (kArgmaxNoallocRows rows of kArgmaxGroups keys, 64 KiB per GPU, held until
+// the process ends). Host code never passes the array's name to a kernel: the
+// name is a host-side stand-in, not a device address. Each device's address
+// comes from hipGetSymbolAddress, called once per device with that device
+// current. Every key is written before it is read, so no call clears it. Calls
+// that overlap on one GPU (two streams at once) share the array and race.
+static __device__ __align__(256) uint64_t scratch[kArgmaxNoallocRows * kArgmaxGroups];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint64_t* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+uint64_t* argmax_noalloc_scratch() {
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) throw Error(1, "device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        g_scratch_ptr[dev] = static_cast<uint64_t*>(ptr);
+    }
+    return g_scratch_ptr[dev];
+}
+
+void launch_argmax_noalloc(const float* logits, int64_t M, int64_t n, int32_t* out_index, hipStream_t s) {
+    if (M > kArgmaxNoallocRows) throw Error(1, "hero_argmax_noalloc: at most 64 rows (the static key array's size)");
+    launch_argmax(logits, M, n, out_index, argmax_noalloc_scratch(), s);
 }
 
 // Elementwise evaluation of the scalar functions the path uses, for parity

@@ -123,6 +123,15 @@ int hero_q8_0_embed(const void* packed, int64_t v, int64_t d, const int32_t* ids
  * (Logits::argmax, nm/src/logits.hpp:61-66). scratch: M*128 uint64. */
 int hero_argmax(const float* logits, int64_t m, int64_t n, int32_t* out, uint64_t* scratch, void* stream);
 
+/* hero_argmax without the scratch argument and without any allocation: the
+ * partial keys live in a static device array of 64 rows x 128 keys (64 KiB
+ * per GPU, kept until the process ends). No counterpart in the reference; for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops that forbid hipMalloc). m <= 64, else HERO_EINVAL. Every call
+ * on one GPU shares the array: calls that overlap on one GPU (on two streams
+ * at once) race. Results equal hero_argmax's. */
+int hero_argmax_noalloc(const float* logits, int64_t m, int64_t n, int32_t* out, void* stream);
+
 /* ---- K-quant weights (GGUF Q4_K = type 12, Q6_K = type 14) ----------------
  * Replaces the int8-activation branch of Weight<In,Out>::matvec / ::matmul
  * for these types (nm/src/quant_i8.hpp:352-383, 430-474): the activation rows

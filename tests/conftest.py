@@ -60,8 +60,18 @@ def gpu_available() -> bool:
 
 
 @pytest.fixture(scope="session")
-def window_golden():
-    return dict(np.load(os.path.join(GOLDEN, "window.npz")))
+def window_golden(manifest):
+    """the reference's windowed-attention outputs; the inputs are regenerated
+    from the seed as tests/golden/make_golden.py made them, and their sha256
+    must match the one recorded then"""
+    w = manifest["window"]
+    rng = np.random.default_rng(w["seed"])
+    s = np.float32(1 / np.sqrt(128.0))
+    k = np.ascontiguousarray(rng.standard_normal((w["ctx"], 256)) * s, np.float32)
+    v = np.ascontiguousarray(rng.standard_normal((w["ctx"], 256)) * s, np.float32)
+    q = np.ascontiguousarray(rng.standard_normal((w["ctx"], 512)), np.float32)
+    assert hashlib.sha256(k.tobytes() + v.tobytes() + q.tobytes()).hexdigest() == w["inputs_sha256"], "window inputs changed"
+    return dict(np.load(os.path.join(GOLDEN, "window.npz")), k=k, v=v, q=q)
 
 
 @pytest.fixture(scope="session")

@@ -177,23 +177,31 @@ WINDOW_CTX = 1100
 WINDOW_PROBES = [0, 1, 2, 3, 4, 7, 500, 1022, 1023, 1024, 1025, 1099]
 
 
-def make_window(tmp: str) -> dict:
-    """4 query heads over 2 K/V heads of 128; K, V, q N(0,1)/sqrt(128)"""
-    rng = np.random.default_rng(WINDOW_SEED)
+def window_inputs(seed: int = WINDOW_SEED, ctx: int = WINDOW_CTX):
+    """4 query heads over 2 K/V heads of 128: K, V N(0,1)/sqrt(128), q N(0,1)
+    (tests/conftest.py regenerates the same arrays and checks their sha256)"""
+    rng = np.random.default_rng(seed)
     s = np.float32(1 / np.sqrt(128.0))
-    k = f32(rng.standard_normal((WINDOW_CTX, 256)) * s)
-    v = f32(rng.standard_normal((WINDOW_CTX, 256)) * s)
-    q = f32(rng.standard_normal((WINDOW_CTX, 512)))
+    k = f32(rng.standard_normal((ctx, 256)) * s)
+    v = f32(rng.standard_normal((ctx, 256)) * s)
+    q = f32(rng.standard_normal((ctx, 512)))
+    return k, v, q
+
+
+def make_window(tmp: str) -> dict:
+    k, v, q = window_inputs()
     for name, a in (("window_k", k), ("window_v", v), ("window_q", q), ("window_probes", f32(WINDOW_PROBES))):
         a.tofile(os.path.join(tmp, f"{name}.in.bin"))
     subprocess.run([HARNESS, "window", tmp], check=True)
-    out = {"k": k, "v": v, "q": q, "probes": np.array(WINDOW_PROBES, np.int32)}
+    out = {"probes": np.array(WINDOW_PROBES, np.int32)}
     for name in ("window_full", "window_w3", "window_w1024"):
         r = np.fromfile(os.path.join(tmp, f"{name}.out.bin"), np.float32).reshape(len(WINDOW_PROBES), 512 + 2)
         out[name] = r[:, :512].copy()
         out[name + "_rows"] = r[:, 512:].astype(np.int64)  # [first, end) of the visible cache rows
     np.savez_compressed(os.path.join(HERE, "window.npz"), **out)
+    inputs_sha = hashlib.sha256(k.tobytes() + v.tobytes() + q.tobytes()).hexdigest()
     return {"seed": WINDOW_SEED, "ctx": WINDOW_CTX, "probes": WINDOW_PROBES, "q_heads": 4, "kv_heads": 2, "head_dim": 128,
+            "inputs_sha256": inputs_sha,
             "cases": {"window_full": "FullAttentionCache, scale 1/sqrt(128)", "window_w3": "LocalAttentionCache(3), scale 1",
                       "window_w1024": "LocalAttentionCache(1024), scale 1"}}
 

@@ -11,11 +11,17 @@ batch-1 hipGraph (fused RMSNorm / SwiGLU GEMV forms, the 151936-row LM head).
 The same prompt then runs as one sequence of a 16-sequence batch state, whose
 decode takes the skinny GEMMs at their real shapes.
 
+The reference itself, compiled from its sources, ran the same model bytes and
+prompt (tests/golden/hybrid8b_model.npz, manifest "hybrid8b_model": its greedy
+ids and the sha256 of its prefill and last logit vectors); both the GPU and
+the oracle must reproduce them.
+
 Bar: greedy ids identical and logits bit-identical (the kernels replay the
 reference's fp32 operation order; the north star's 1e-2 abs / 1e-3 rel is the
 stated tolerance, bit equality is what this path delivers). The top-2 margin of
 every step is printed, so a near tie would be visible (none can flip while the
 logits are bit-identical)."""
+import hashlib
 import os
 import time
 
@@ -70,8 +76,16 @@ def hybrid8b():
 
 
 @pytest.mark.timeout(1200)
-def test_hybrid8b_prefill_and_greedy_decode_match_oracle(hybrid8b):
+def digest(a):
+    return hashlib.sha256(np.ascontiguousarray(a, np.float32).tobytes()).hexdigest()
+
+
+def test_hybrid8b_prefill_and_greedy_decode_match_oracle(hybrid8b, manifest):
     import ctypes
+
+    golden = np.load(os.path.join(os.path.dirname(__file__), "golden", "hybrid8b_model.npz"))
+    g = manifest["hybrid8b_model"]
+    assert (g["prompt_len"], g["decode_steps"], g["seed"], g["ctx"]) == (PROMPT, STEPS, SEED, 1024)
 
     _, model, ref = hybrid8b
     from hero_amd._lib import lib
@@ -85,9 +99,12 @@ def test_hybrid8b_prefill_and_greedy_decode_match_oracle(hybrid8b):
     say(f"[8b] prefill GEMM tiles ((rows, N): rows per tile): {tiles}")
     assert tiles[(512, 16448)] == 128 and tiles[(512, 24576)] == 128
     prompt = np.random.default_rng(SEED).integers(0, model.V, PROMPT).astype(np.int32)
+    assert np.array_equal(prompt, golden["prompt"])
     t = time.perf_counter()
     ref_prefill, ref_ids, ref_last = oracle_greedy(ref, prompt, STEPS)
     say(f"[8b] oracle: {PROMPT}-token prefill + {STEPS} greedy passes in {time.perf_counter() - t:.1f} s; ids {ref_ids}")
+    assert ref_ids == [int(i) for i in golden["ids"]], "oracle ids differ from the reference's"
+    assert digest(ref_prefill) == g["logits_prefill_sha256"] and digest(ref_last) == g["logits_last_sha256"]
 
     state = model.new_state(1024)
     lg = model.forward(state, ids=prompt)
@@ -100,6 +117,8 @@ def test_hybrid8b_prefill_and_greedy_decode_match_oracle(hybrid8b):
     say(f"[8b] GPU greedy ids {got}; last-step top-2 margin {margin(last.values):.4g}")
     assert got == ref_ids, f"first divergence at step {next(i for i, (a, b) in enumerate(zip(got, ref_ids)) if a != b)}"
     assert np.array_equal(bits(last.values), bits(ref_last))
+    assert digest(lg.values) == g["logits_prefill_sha256"] and digest(last.values) == g["logits_last_sha256"]
+    say("[8b] GPU ids and prefill / last logits equal the reference's (sha256)")
     assert state.tokens() == PROMPT + STEPS
     state.close()
 

@@ -59,19 +59,37 @@ def measured_traffic():
         return float(json.load(f)["bytes_per_launch"]), "profiles/hybrid8b_gemv_traffic.json"
 
 
-def cpu_baseline(image, prompt, seconds: float) -> dict:
+def host_cpu() -> dict:
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "model": model}
+
+
+def cpu_baseline(image, prompt, seconds: float, prefix: int) -> tuple[dict, np.ndarray]:
+    """The oracle (the reference's CPU algorithm restated: int8-activation Q8_0
+    dots, row-parallel pool with chunk = rows/(threads*16)) on the same model
+    bytes, with one thread per CPU this process may run on (the reference's
+    default is hardware_concurrency, nm/src/core.cpp:67-73). It prefills the
+    first `prefix` prompt ids (timed), then runs greedy decode passes for about
+    `seconds`. Returns the JSON object and the greedy ids."""
     import oracle
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    cpu = host_cpu()
+    threads = max(1, cpu["affinity"])
     oracle.set_threads(threads)
     m = oracle.Model(image=image)
-    short = prompt[:4]
-    logits = m.forward_ids(short)
-    nxt = int(np.argmax(logits))
+    t0 = time.perf_counter()
+    logits = m.forward_ids(prompt[:prefix])
+    prefill_s = time.perf_counter() - t0
+    ids = [int(np.argmax(logits))]
     passes, t0 = 0, time.perf_counter()
     while True:
-        logits = m.forward_ids([nxt])
-        nxt = int(np.argmax(logits))
+        logits = m.forward_ids([ids[-1]])
+        ids.append(int(np.argmax(logits)))
         passes += 1
         elapsed = time.perf_counter() - t0
         if elapsed >= seconds:
@@ -82,9 +100,21 @@ def cpu_baseline(image, prompt, seconds: float) -> dict:
         "unit": "tok/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"oracle on the same 8B model bytes: prefill 4 tokens, then {passes} greedy decode passes "
-                  f"(context 4..{4 + passes}) in {elapsed:.1f} s, {threads} threads, g++ -O3 -ffp-contract=off",
-    }
+        "host": cpu,
+        "prefill_tok_s": prefix / prefill_s,
+        "sample": f"oracle on the same 8B model bytes, {threads} threads (one per CPU of the process's affinity set; "
+                  f"{cpu['nproc']} CPUs on the host, {cpu['model']}), g++ -O3 -march=x86-64-v3 -ffp-contract=off: "
+                  f"prefill of the prompt's first {prefix} ids in {prefill_s:.1f} s, then {passes} greedy decode passes "
+                  f"(context {prefix}..{prefix + passes}) in {elapsed:.1f} s. At the GPU's context of ~{len(prompt)} the "
+                  f"attention adds about {100 * attention_share(len(prompt)):.1f}% to a pass's multiply-adds.",
+    }, np.array(ids, np.int32)
+
+
+def attention_share(ctx: int) -> float:
+    """multiply-adds of the 8 attention layers' score and weighted-sum loops at
+    context ctx (32 heads of 128) relative to the weight dot products of one
+    pass (8.44e9 weights)"""
+    return 8 * 32 * ctx * 128 * 2 / 7.94e9
 
 
 def main() -> int:
@@ -93,7 +123,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--prompt", type=int, default=2048)
-    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-prefix", type=int, default=128, help="prompt ids the CPU baseline prefills before its decode passes")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--gemv-reps", type=int, default=5)
     ap.add_argument("--batch", type=int, default=16, help="also time greedy decode of this many sequences at once (0: skip)")
@@ -207,7 +238,15 @@ def main() -> int:
             "prefill_seconds": prefill_s, "device_decode_seconds": device_s,
             "gemv_gbs_per_step": nbytes / (device_s / args.steps) / 1e9,
             "prefill_tok_s": args.prompt / prefill_s,
-            "prefill_tok_s_chunked_delta_net": args.prompt / prefill_chunked_s,
+            # not parity-preserving: the chunked (WY) delta-net prefill agrees with
+            # the exact form to ~1e-6 in the recurrence, but the model's Q8_0
+            # re-quantization turns that into logit differences of up to ~0.06
+            # abs, outside the 1e-2 abs / 1e-3 rel bar; prefill_tok_s is the
+            # exact, bit-identical form
+            "throughput_option_outside_parity": {
+                "prefill_tok_s_chunked_delta_net": args.prompt / prefill_chunked_s,
+                "parity": "tolerance only: logits up to ~0.06 abs from the exact prefill (tests/test_gpu_model.py)",
+            },
             "batch_decode": batch,
         },
         "roofline": {
@@ -218,9 +257,19 @@ def main() -> int:
         },
     }
     if not args.no_cpu:
-        log(f"CPU baseline: about {args.cpu_seconds:.0f} s of decode on the host")
-        out["cpu_baseline"] = cpu_baseline(image, prompt, args.cpu_seconds)
+        log(f"CPU baseline: {args.cpu_prefix}-token prefill, then about {args.cpu_seconds:.0f} s of decode on the host")
+        out["cpu_baseline"], cpu_ids = cpu_baseline(image, prompt, args.cpu_seconds, args.cpu_prefix)
         log(f"CPU baseline: {out['cpu_baseline']['value']:.3f} tok/s on {out['cpu_baseline']['cores']} threads")
+        # the reference's check (tools/qwen35_check.cpp:43-70): the GPU's greedy
+        # ids from the same prefix equal the CPU path's
+        st = model.new_state(ctx)
+        first = model.forward(st, ids=prompt[:args.cpu_prefix], want_logits=False)
+        gpu_ids, _ = model.decode_greedy(st, first, len(cpu_ids) - 1)
+        gpu_ids = np.concatenate([[first], gpu_ids]).astype(np.int32)
+        st.close()
+        out["greedy_match"] = {"equal": bool(np.array_equal(gpu_ids, cpu_ids)), "ids": int(len(cpu_ids)),
+                               "prefix": args.cpu_prefix}
+        log(f"greedy ids, GPU vs CPU path over {len(cpu_ids)} passes: {'identical' if out['greedy_match']['equal'] else 'DIFFERENT'}")
     print(json.dumps(out), flush=True)
     model.close()
     return 0

@@ -93,6 +93,17 @@ __host__ __device__ inline float expf_glibc(float x) {
     return expf_glibc_with(x, [](int i) { return exp2_table(i); });
 }
 
+// log1pf below restates fdlibm's single-precision log1p (s_log1pf.c, the
+// algorithm glibc uses), whose permission notice follows:
+//
+// ====================================================
+// Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+//
+// Developed at SunPro, a Sun Microsystems, Inc. business.
+// Permission to use, copy, modify, and distribute this
+// software is freely granted, provided that this notice
+// is preserved.
+// ====================================================
 __host__ __device__ inline float log1pf_glibc(float x) {
     const float ln2_hi = bits_f32(0x3f317180u), ln2_lo = bits_f32(0x3717f7d1u);
     const float lp1 = bits_f32(0x3f2aaaabu), lp2 = bits_f32(0x3ecccccdu), lp3 = bits_f32(0x3e924925u), lp4 = bits_f32(0x3e638e29u),

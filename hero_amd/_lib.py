@@ -102,6 +102,9 @@ SIGNATURES = {
     "hero_q8_K_quantize": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "hero_kquant_gemm": (c_int, [c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p]),
     "hero_gdn_decode": (c_int, [POINTER(GdnDecodeArgs), c_void_p]),
+    "hero_gdn_decode_cols": (c_int, [POINTER(GdnDecodeArgs), c_void_p, c_void_p, c_void_p]),
+    "hero_gdn_norm_gate": (c_int, [c_void_p, POINTER(GdnDecodeArgs), c_void_p]),
+    "hero_headgate_q8_0_gemv": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "hero_gdn_prefill_work_bytes": (c_int64, [c_int64, c_int32, c_int32]),
     "hero_gdn_prefill": (c_int, [POINTER(GdnDecodeArgs), c_void_p, c_int64, c_void_p]),
     "hero_gdn_prefill_chunked": (c_int, [POINTER(GdnDecodeArgs), c_void_p, c_int64, c_void_p]),

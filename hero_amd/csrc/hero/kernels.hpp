@@ -41,15 +41,16 @@ void launch_pack_q8(const void* gguf_blocks, void* packed, int64_t N_total, int6
 void launch_gemv_q8(const void* packed, const void* act, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s);
 // The streaming GEMV (K a multiple of 4096, at most 12288) with its input
 // formed in the prologue from one of three sources.
-enum : int { kInAct = 0, kInRmsNorm = 1, kInSwiglu = 2 };
+enum : int { kInAct = 0, kInRmsNorm = 1, kInSwiglu = 2, kInHeadGate = 3 };
 struct GemvInput {
     int mode;
     const int8_t* xq;        // kInAct: quantized activation [K] + fp32 scales [K/32]
     const float* xd;
     const float* x;          // kInRmsNorm: residual row [K] (K == 4096), RMSNorm weight, eps
-    const float* gamma;
-    float eps;
+    const float* gamma;      // kInHeadGate: raw delta-net outputs [K] (K == 4096) in x, the
+    float eps;               //   head norm's weight [128] in gamma, eps, and the gates silu(z) [K] in z
     const float* gate_up;    // kInSwiglu: [gate K | up K]
+    const float* z;
 };
 bool gemv_streams(int64_t K);
 void launch_gemv_q8_in(const void* packed, const GemvInput& in, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s);
@@ -96,6 +97,14 @@ struct GdnDecodeArgs {
     int B, Hk, Hv, Dk, Dv, W;
 };
 void launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t s);
+// The same step split over value columns (8 workgroups of one wave per head):
+// writes the raw delta-rule outputs o_raw [B][Hv*128] (before the head norm),
+// the gates silu(z) into g_raw [B][Hv*128] if non-null, and the new state and
+// ring; a.act_out / a.out_f32 are not written.
+void launch_gdn_decode_cols(const GdnDecodeArgs& a, float* o_raw, float* g_raw, hipStream_t s);
+// head RMSNorm, SiLU(z) gate and quantization of o_raw into a.act_out (and
+// a.out_f32 if set), for a.B rows
+void launch_gdn_norm_gate(const float* o_raw, const GdnDecodeArgs& a, hipStream_t s);
 // The same for T = a.B consecutive tokens of ONE sequence at positions
 // a.positions[0] + t (proj and act_out have T rows; state and ring are that
 // sequence's), then the ring update. `work` holds gdn_prefill_work_bytes.

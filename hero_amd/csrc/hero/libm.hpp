@@ -61,16 +61,14 @@ __host__ __device__ inline uint64_t exp2_table(int i) {
 // `tab(i)` returns exp2_table(i); kernels that cannot afford a global-memory
 // read per call (one in flight behind other loads waits for all of them) pass
 // a copy of the table held in shared memory
+//
+// Branch-free: the table path runs for every input (for |x| >= 88, inf and nan
+// its value is discarded) and the special cases are selected afterwards, so a
+// wave never splits and independent calls interleave.
 template <class Tab>
 __host__ __device__ inline float expf_glibc_with(float x, const Tab& tab) {
     const uint32_t ix = f32_bits(x);
     const uint32_t abstop = (ix >> 20) & 0x7ff;
-    if (abstop >= 0x42b) {  // |x| >= 88, inf or nan
-        if (ix == 0xff800000u) return 0.f;           // exp(-inf) = 0
-        if (abstop >= 0x7f8) return x + x;           // +inf, nan
-        if (x > 0x1.62e42ep6f) return bits_f32(0x7f800000u);  // overflow
-        if (x < -0x1.9fe368p6f) return 0.f;          // underflow
-    }
     constexpr double inv_ln2_n = 0x1.71547652b82fep0 * 32;
     constexpr double shift = 0x1.8p+52;
     constexpr double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32, c2 = 0x1.62e42ff0c52d6p-1 / 32;
@@ -86,7 +84,15 @@ __host__ __device__ inline float expf_glibc_with(float x, const Tab& tab) {
     double y = c2 * r + 1.0;
     y = p * r2 + y;
     y = y * s;
-    return float(y);
+    const float main = float(y);
+    // |x| >= 88, inf or nan: exp(-inf) = 0; +inf and nan give x + x; overflow
+    // to +inf; underflow to 0; otherwise the table path's value
+    const float special = ix == 0xff800000u ? 0.f
+                          : abstop >= 0x7f8 ? x + x
+                          : x > 0x1.62e42ep6f ? bits_f32(0x7f800000u)
+                          : x < -0x1.9fe368p6f ? 0.f
+                          : main;
+    return abstop >= 0x42b ? special : main;
 }
 
 __host__ __device__ inline float expf_glibc(float x) {

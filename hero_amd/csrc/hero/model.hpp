@@ -184,6 +184,8 @@ private:
     // per-step device scalars: [0] position, [1] token id, [2] step counter
     DeviceBuffer step_;
     DeviceBuffer x_, h_, proj_, act_d_, act_mix_, act_ff_, gate_up_, logits_, argmax_scratch_, out_ids_, q_rot_;
+    DeviceBuffer o_raw_;  // [B][Hv*Dv] raw delta-net outputs of a decode step (before the head norm)
+    DeviceBuffer g_raw_;  // [B][Hv*Dv] its output gates silu(z)
     DeviceBuffer gemv_scratch_;  // [D] output of the GEMV timing runs
     int64_t out_ids_capacity_ = 0;
     // prefill chunk buffers (row-major, chunk_capacity_ rows), made on first use

@@ -260,13 +260,13 @@ int hero_math_eval(const float* x, float* out, int64_t n, void* stream) {
 }
 
 namespace {
-GdnDecodeArgs gdn_args(const hero_gdn_decode_args* p) {
+GdnDecodeArgs gdn_args(const hero_gdn_decode_args* p, bool need_act = true) {
     require(p != nullptr, "null args");
     const hero_gdn_decode_args& a = *p;
     require(a.dk == 128 && a.dv == 128, "delta-net heads must be 128x128");
     require(a.b > 0 && a.hk > 0 && a.hv > 0 && a.hv % a.hk == 0, "bad head counts");
     require(a.conv_width >= 1 && a.conv_width <= 8, "conv width must be 1..8");
-    require(a.proj && a.conv_taps && a.conv_hist && a.state && a.dt_bias && a.decay && a.norm_gamma && a.positions && a.act_out, "null pointer");
+    require(a.proj && a.conv_taps && a.conv_hist && a.state && a.dt_bias && a.decay && a.norm_gamma && a.positions && (a.act_out || !need_act), "null pointer");
     const int64_t cc = 2 * int64_t(a.hk) * 128 + int64_t(a.hv) * 128;
     require(a.proj_stride >= cc && a.z_off >= cc && a.z_off + int64_t(a.hv) * 128 <= a.proj_stride, "z slice outside the projection row");
     require(a.beta_off >= 0 && a.beta_off + a.hv <= a.proj_stride && a.alpha_off >= 0 && a.alpha_off + a.hv <= a.proj_stride, "gate slices outside the projection row");
@@ -300,6 +300,42 @@ int hero_gdn_decode(const hero_gdn_decode_args* p, void* stream) {
     return guard([&] {
         launch_gdn_decode(gdn_args(p), as_stream(stream));
         check_launch("hero_gdn_decode");
+    });
+}
+
+int hero_gdn_decode_cols(const hero_gdn_decode_args* p, float* o_raw, float* gates, void* stream) {
+    return guard([&] {
+        const GdnDecodeArgs a = gdn_args(p, false);
+        require(o_raw != nullptr, "null pointer");
+        require(aligned(a.state, 16), "state must be 16-byte aligned");
+        launch_gdn_decode_cols(a, o_raw, gates, as_stream(stream));
+        check_launch("hero_gdn_decode_cols");
+    });
+}
+
+int hero_gdn_norm_gate(const float* o_raw, const hero_gdn_decode_args* p, void* stream) {
+    return guard([&] {
+        const GdnDecodeArgs a = gdn_args(p);
+        require(o_raw != nullptr, "null pointer");
+        launch_gdn_norm_gate(o_raw, a, as_stream(stream));
+        check_launch("hero_gdn_norm_gate");
+    });
+}
+
+int hero_headgate_q8_0_gemv(const void* packed, const float* o_raw, const float* gates, const float* gamma, float eps, float* y, const float* residual, int64_t n, int64_t k, void* stream) {
+    return guard([&] {
+        check_q8_shape(n, k);
+        require(k == 4096, "the head-gated input form needs K == 4096 (32 heads of 128)");
+        require(packed && o_raw && gates && gamma && y, "null pointer");
+        require(aligned(packed, 16) && aligned(o_raw, 16) && aligned(gates, 16) && aligned(gamma, 16), "packed, o_raw, gates and gamma must be 16-byte aligned");
+        GemvInput in{};
+        in.mode = kInHeadGate;
+        in.x = o_raw;
+        in.z = gates;
+        in.gamma = gamma;
+        in.eps = eps;
+        launch_gemv_q8_in(packed, in, y, residual, n, k, residual ? kEpiResidual : kEpiStore, as_stream(stream));
+        check_launch("hero_headgate_q8_0_gemv");
     });
 }
 

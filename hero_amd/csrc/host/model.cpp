@@ -323,6 +323,8 @@ Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batc
     argmax_scratch_ = DeviceBuffer(size_t(B) * 128 * 8);
     out_ids_ = DeviceBuffer(size_t(max_tokens * B) * 4);
     q_rot_ = DeviceBuffer(size_t(B * c.q_width()) * 4);
+    o_raw_ = DeviceBuffer(size_t(B * c.v_width()) * 4);
+    g_raw_ = DeviceBuffer(size_t(B * c.v_width()) * 4);
     out_ids_capacity_ = max_tokens;
     for (int64_t l = 0; l < c.L; ++l) {
         if (c.is_recurrent(l)) {
@@ -488,7 +490,6 @@ void Qwen35Model::enqueue_step(State& st, bool from_ids, bool with_head) const {
         const LayerWeights& L = layers_[size_t(l)];
         // h = x + mix(rms(x)); x' = h + mlp(rms(h))  (nm/src/qwen35.hpp:318-327)
         gemv_norm(L.w_in.get(), x, L.mixer_norm.get<float>(), c.eps, st.act_d_.get(), proj, nullptr, L.n_in, c.D, s);
-        int64_t k_mix;
         if (L.recurrent) {
             GdnDecodeArgs a{};
             a.proj = proj;
@@ -512,8 +513,24 @@ void Qwen35Model::enqueue_step(State& st, bool from_ids, bool with_head) const {
             a.Dk = int(c.Dk);
             a.Dv = int(c.Dv);
             a.W = int(c.W);
-            launch_gdn_decode(a, s);
-            k_mix = c.v_width();
+            // the step split over value columns; the head norm, SiLU(z) gate and
+            // quantization then run in the output projection's prologue
+            // (K = 4096) or in their own kernel
+            float* o_raw = st.o_raw_.get<float>();
+            const bool fused = c.v_width() == 4096;
+            launch_gdn_decode_cols(a, o_raw, fused ? st.g_raw_.get<float>() : nullptr, s);
+            if (fused) {
+                GemvInput in{};
+                in.mode = kInHeadGate;
+                in.x = o_raw;
+                in.z = st.g_raw_.get<float>();
+                in.gamma = L.ssm_norm.get<float>();
+                in.eps = c.eps;
+                launch_gemv_q8_in(L.w_out.get(), in, h, x, c.D, c.v_width(), kEpiResidual, s);
+            } else {
+                launch_gdn_norm_gate(o_raw, a, s);
+                gemv_act(L.w_out.get(), st.act_mix_.get(), h, x, c.D, c.v_width(), s);
+            }
         } else {
             AttnDecodeArgs a{};
             a.proj = proj;
@@ -539,9 +556,8 @@ void Qwen35Model::enqueue_step(State& st, bool from_ids, bool with_head) const {
             a.Hkv = int(c.Hkv);
             a.Dh = int(c.Dh);
             attention(st, size_t(l), a, st.page_table_.get<int32_t>(), st.attn_work_.get<float>(), s);
-            k_mix = c.q_width();
+            gemv_act(L.w_out.get(), st.act_mix_.get(), h, x, c.D, c.q_width(), s);
         }
-        gemv_act(L.w_out.get(), st.act_mix_.get(), h, x, c.D, k_mix, s);
         if (ffn_fused_) {
             gemv_norm(L.w_gate_up.get(), h, L.channel_norm.get<float>(), c.eps, st.act_d_.get(), static_cast<float*>(st.act_ff_.get()), nullptr, 2 * c.FF, c.D, s, 1);
             gemv_act(L.w_down.get(), st.act_ff_.get(), x, h, c.D, c.FF, s);
@@ -864,7 +880,18 @@ double Qwen35Model::time_gemvs(State& st, int reps, int64_t* launches, int64_t* 
         for (const LayerWeights& L : layers_) {
             const int64_t k_mix = L.recurrent ? c.v_width() : c.q_width();
             n_bytes += gemv_norm(L.w_in.get(), x, L.mixer_norm.get<float>(), c.eps, st.act_d_.get(), st.proj_.get<float>(), nullptr, L.n_in, c.D, s);
-            n_bytes += gemv_act(L.w_out.get(), st.act_mix_.get(), y_d, x, c.D, k_mix, s);
+            if (L.recurrent && c.v_width() == 4096) {  // the head-norm-gated input form
+                GemvInput in{};
+                in.mode = kInHeadGate;
+                in.x = st.o_raw_.get<float>();
+                in.z = st.g_raw_.get<float>();
+                in.gamma = L.ssm_norm.get<float>();
+                in.eps = c.eps;
+                launch_gemv_q8_in(L.w_out.get(), in, y_d, x, c.D, k_mix, kEpiResidual, s);
+                n_bytes += packed_q8_bytes(c.D, k_mix) + 2 * k_mix * 4 + c.Dv * 4 + 2 * c.D * 4;
+            } else {
+                n_bytes += gemv_act(L.w_out.get(), st.act_mix_.get(), y_d, x, c.D, k_mix, s);
+            }
             if (ffn_fused_) {
                 n_bytes += gemv_norm(L.w_gate_up.get(), h, L.channel_norm.get<float>(), c.eps, st.act_d_.get(), static_cast<float*>(st.act_ff_.get()), nullptr, 2 * c.FF, c.D, s, 1);
                 n_bytes += gemv_act(L.w_down.get(), st.act_ff_.get(), y_d, h, c.D, c.FF, s);

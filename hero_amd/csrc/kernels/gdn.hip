@@ -336,6 +336,231 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(GdnDecodeArgs a
     }
 }
 
+// ---- decode, split over value columns --------------------------------------------------
+// One workgroup (one wave) per (sequence, value head, 16 value columns): the
+// columns of the delta rule are independent (nm/src/recurrent.hpp:146-177:
+// predicted[j], delta[j] and output[j] read only column j of the state), so
+// 8 workgroups share a head and each recomputes the head's conv, SiLU and
+// L2 norms of q and k. The four lanes 4j .. 4j+3 (one quad) own column
+// c0 + j; lane 4j + r holds its rows 32r .. 32r+31 in registers with the
+// matching k and q values. A column's 128-term chains (the decayed
+// prediction, then the output) run in row order as four 32-term segments:
+// the quad's lane r continues the running sum from lane r-1, handed over by
+// a DPP quad permutation, so every term is added from registers.
+// The kernel writes the raw outputs o (before the head RMSNorm) and, if asked,
+// the gates SiLU(z); the output projection's prologue (or
+// gdn_norm_gate_kernel) normalises, gates and quantizes.
+constexpr int kGdnCols = 16;                      // value columns per workgroup
+constexpr int kGdnSlices = kGdnDim / kGdnCols;    // workgroups per head
+constexpr int kGdnSeg = kGdnDim / 4;              // rows per lane: 32
+struct GdnColsShared {
+    float q[kGdnDim], k[kGdnDim];                 // conv + SiLU outputs, then normalised
+    float sq[2][kGdnDim];                         // their squares
+    uint64_t etab[32];                            // expf's table
+};
+
+// the running sum of lane r-1 of each quad, in lane r (quad_perm 0,0,1,2)
+__device__ __forceinline__ float quad_prev(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x90, 0xF, 0xF, false));
+}
+// lane 3's value of each quad, in all four lanes (quad_perm 3,3,3,3)
+__device__ __forceinline__ float quad_last(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xFF, 0xF, 0xF, false));
+}
+
+template <int W>
+__global__ __launch_bounds__(64) void gdn_decode_cols_kernel(GdnDecodeArgs a, float* __restrict__ o_raw, float* __restrict__ g_raw) {
+    __shared__ __align__(16) GdnColsShared sh;
+    const int t = threadIdx.x, j = t / 4, r = t % 4;
+    const int h = blockIdx.x / kGdnSlices, slice = blockIdx.x % kGdnSlices, c0 = slice * kGdnCols, b = blockIdx.y;
+    const int hk = h % a.Hk;  // tiled key heads (nm/src/qwen35.hpp:172)
+    const int64_t KW = int64_t(a.Hk) * kGdnDim;
+    const int64_t CC = 2 * KW + int64_t(a.Hv) * kGdnDim;
+    const float* P = a.proj + int64_t(b) * a.proj_stride;
+    float* hist = a.conv_hist + int64_t(b) * W * CC;
+    float* S = a.state + (int64_t(b) * a.Hv + h) * kGdnState + c0 + j;  // column c0 + j
+    // expf's table first: its read then waits for no other load
+    const uint64_t etv = exp2_table(t & 31);
+    const int pos = a.positions[b];
+
+    // ---- every load first: gates, the q/k channels t and t + 64 and the v
+    // channel c0 + j with their taps and ring slots, then the lane's 32 state
+    // rows of its column ----
+    const float g_beta = P[a.beta_off + h], g_alpha = P[a.alpha_off + h];
+    const float g_dt = a.dt_bias[h], g_a = a.decay[h];
+    const float zv = P[a.z_off + int64_t(h) * kGdnDim + c0 + j];
+    float xq[2], xk[2], tq[2][W], tk[2][W], rq[2][W], rk[2][W];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int64_t cq = int64_t(hk) * kGdnDim + t + 64 * u, ck = KW + cq;
+        xq[u] = P[cq];
+        xk[u] = P[ck];
+        load_taps<W>(a.conv_taps, cq, tq[u]);
+        load_taps<W>(a.conv_taps, ck, tk[u]);
+        load_ring<W>(hist, CC, cq, rq[u]);
+        load_ring<W>(hist, CC, ck, rk[u]);
+    }
+    const int64_t cv = 2 * KW + int64_t(h) * kGdnDim + c0 + j;
+    float tv[W], rv[W];
+    const float xv = P[cv];
+    load_taps<W>(a.conv_taps, cv, tv);
+    load_ring<W>(hist, CC, cv, rv);
+    float col[kGdnSeg];
+#pragma unroll
+    for (int m = 0; m < kGdnSeg; ++m) col[m] = S[(kGdnSeg * r + m) * kGdnDim];
+    if (t < 32) sh.etab[t] = etv;
+    __syncthreads();
+    if (pos < 0) return;  // the host keeps positions in range; idle batch rows store nothing
+    const ExpTab et{sh.etab};
+    // the gates first, while the conv inputs and the state are still arriving
+    const float beta = et.sigmoid(g_beta);
+    const float decay = et.exp(g_a * et.softplus(g_alpha + g_dt));
+    const float gate = et.silu(zv);  // the output gate SiLU(z) of column c0 + j (nm/src/qwen35.hpp:458)
+
+    // ---- conv + SiLU; the ring takes this position (the state loads are
+    // still in flight: they were issued last) ----
+    const int slot = pos % W;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int c = t + 64 * u;
+        ConvPast<W> pq, pk;
+        past_from_ring<W>(rq[u], pos, pq);
+        past_from_ring<W>(rk[u], pos, pk);
+        const float q = et.silu(conv_channel<W>(tq[u], pq, xq[u]));
+        const float k = et.silu(conv_channel<W>(tk[u], pk, xk[u]));
+        if (h < a.Hk && slice == 0) {  // one workgroup per key head owns its q/k history
+            const int64_t cq = int64_t(hk) * kGdnDim + c;
+            hist[int64_t(slot) * CC + cq] = xq[u];
+            hist[int64_t(slot) * CC + KW + cq] = xk[u];
+        }
+        sh.q[c] = q;
+        sh.k[c] = k;
+        sh.sq[0][c] = q * q;
+        sh.sq[1][c] = k * k;
+    }
+    float v;
+    {
+        ConvPast<W> pv;
+        past_from_ring<W>(rv, pos, pv);
+        v = et.silu(conv_channel<W>(tv, pv, xv));
+        if (r == 0) hist[int64_t(slot) * CC + cv] = xv;
+    }
+    __syncthreads();
+    // ---- L2 norms of q and k (nm/src/recurrent.hpp:40-48): every lane runs
+    // both sequential sums (broadcast reads) ----
+    float ssq = 0.f, ssk = 0.f;
+    {
+        const float4* q4 = reinterpret_cast<const float4*>(sh.sq[0]);
+        const float4* k4 = reinterpret_cast<const float4*>(sh.sq[1]);
+        float4 qc[8], kc[8], qn[8], kn[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) qc[u] = q4[u], kc[u] = k4[u];
+#pragma unroll
+        for (int c = 0; c < kGdnDim / 32; ++c) {
+            if (c + 1 < kGdnDim / 32) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) qn[u] = q4[8 * (c + 1) + u], kn[u] = k4[8 * (c + 1) + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                ssq += qc[u].x, ssk += kc[u].x;
+                ssq += qc[u].y, ssk += kc[u].y;
+                ssq += qc[u].z, ssk += kc[u].z;
+                ssq += qc[u].w, ssk += kc[u].w;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) qc[u] = qn[u], kc[u] = kn[u];
+        }
+    }
+    const float inv_q = 1.f / fmaxf(sqrtf(ssq), 1e-6f), inv_k = 1.f / fmaxf(sqrtf(ssk), 1e-6f);
+    {
+        const float query_scale = 1.f / sqrtf(float(kGdnDim));
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int c = t + 64 * u;
+            sh.q[c] = (sh.q[c] * inv_q) * query_scale;
+            sh.k[c] = sh.k[c] * inv_k;
+        }
+    }
+    __syncthreads();
+    // ---- the delta rule on column c0 + j, rows 32r .. 32r+31 in this lane ----
+    float ks[kGdnSeg], qs[kGdnSeg];
+    {
+        const float4* k4 = reinterpret_cast<const float4*>(sh.k + kGdnSeg * r);
+        const float4* q4 = reinterpret_cast<const float4*>(sh.q + kGdnSeg * r);
+#pragma unroll
+        for (int i = 0; i < kGdnSeg / 4; ++i) {
+            const float4 kk = k4[i], qq = q4[i];
+            ks[4 * i] = kk.x, ks[4 * i + 1] = kk.y, ks[4 * i + 2] = kk.z, ks[4 * i + 3] = kk.w;
+            qs[4 * i] = qq.x, qs[4 * i + 1] = qq.y, qs[4 * i + 2] = qq.z, qs[4 * i + 3] = qq.w;
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < kGdnSeg; ++m) col[m] = col[m] * decay;
+    // pred = sum_i S[i][j] * k[i] in i order: segment r in lane r, handed on
+    float acc = 0.f;
+#pragma unroll
+    for (int seg = 0; seg < 4; ++seg) {
+        if (r == seg) {
+#pragma unroll
+            for (int m = 0; m < kGdnSeg; ++m) acc = acc + col[m] * ks[m];
+        }
+        if (seg < 3) acc = quad_prev(acc);
+    }
+    const float pred = quad_last(acc);
+    const float delta = (v - pred) * beta;
+#pragma unroll
+    for (int m = 0; m < kGdnSeg; ++m) col[m] = col[m] + ks[m] * delta;
+    // o = sum_i S'[i][j] * q[i] in i order, the same way
+    acc = 0.f;
+#pragma unroll
+    for (int seg = 0; seg < 4; ++seg) {
+        if (r == seg) {
+#pragma unroll
+            for (int m = 0; m < kGdnSeg; ++m) acc = acc + col[m] * qs[m];
+        }
+        if (seg < 3) acc = quad_prev(acc);
+    }
+    if (r == 3) {
+        o_raw[(int64_t(b) * a.Hv + h) * kGdnDim + c0 + j] = acc;
+        if (g_raw) g_raw[(int64_t(b) * a.Hv + h) * kGdnDim + c0 + j] = gate;
+    }
+#pragma unroll
+    for (int m = 0; m < kGdnSeg; ++m) S[(kGdnSeg * r + m) * kGdnDim] = col[m];
+}
+
+// The per-head RMSNorm (nm/src/components.hpp:176-181), the SiLU(z) gate and
+// Q8_0 quantization of raw delta-net outputs, one workgroup of 128 lanes per
+// (row, head): o [rows][Hv*128], z at proj + row * proj_stride + z_off.
+__global__ __launch_bounds__(kGdnDim) void gdn_norm_gate_kernel(const float* __restrict__ o_raw, const float* __restrict__ proj, int64_t proj_stride, int64_t z_off,
+                                                                const float* __restrict__ gamma, float eps, void* act_out, float* out_f32, int rows, int Hv) {
+    const int j = threadIdx.x, h = blockIdx.x, row = blockIdx.y;
+    __shared__ __align__(16) float ov[kGdnDim];
+    __shared__ float scal;
+    const int64_t width = int64_t(Hv) * kGdnDim, idx = int64_t(h) * kGdnDim + j;
+    const float o = o_raw[int64_t(row) * width + idx];
+    const float z = proj[int64_t(row) * proj_stride + z_off + idx];
+    ov[j] = o * o;
+    __syncthreads();
+    if (j == 0) {
+        const float4* s4 = reinterpret_cast<const float4*>(ov);
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < kGdnDim / 4; ++i) {
+            const float4 x = s4[i];
+            ss += x.x;
+            ss += x.y;
+            ss += x.z;
+            ss += x.w;
+        }
+        scal = 1.f / sqrtf(ss / float(kGdnDim) + eps);
+    }
+    __syncthreads();
+    const float out = (gamma[j] * o * scal) * silu_f32(z);
+    if (out_f32) out_f32[int64_t(row) * width + idx] = out;
+    gdn_quantize(out, row, rows, width, idx, j, act_out);
+}
+
 // ---- prefill: tokens t = 0..T-1 of one sequence at positions pos0 + t -------------
 // a.B is T (rows of proj and of act_out); a.positions[0] is pos0; the state
 // and the ring are sequence 0's. Three kernels:
@@ -908,6 +1133,25 @@ void launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t s) {
         case 7: hipLaunchKernelGGL(gdn_decode_kernel<7>, grid, dim3(kGdnThreads), sm, s, a); break;
         default: hipLaunchKernelGGL(gdn_decode_kernel<8>, grid, dim3(kGdnThreads), sm, s, a); break;
     }
+}
+
+void launch_gdn_decode_cols(const GdnDecodeArgs& a, float* o_raw, float* g_raw, hipStream_t s) {
+    const dim3 grid(unsigned(a.Hv * kGdnSlices), unsigned(a.B));
+    switch (a.W) {
+        case 1: hipLaunchKernelGGL(gdn_decode_cols_kernel<1>, grid, dim3(64), 0, s, a, o_raw, g_raw); break;
+        case 2: hipLaunchKernelGGL(gdn_decode_cols_kernel<2>, grid, dim3(64), 0, s, a, o_raw, g_raw); break;
+        case 3: hipLaunchKernelGGL(gdn_decode_cols_kernel<3>, grid, dim3(64), 0, s, a, o_raw, g_raw); break;
+        case 4: hipLaunchKernelGGL(gdn_decode_cols_kernel<4>, grid, dim3(64), 0, s, a, o_raw, g_raw); break;
+        case 5: hipLaunchKernelGGL(gdn_decode_cols_kernel<5>, grid, dim3(64), 0, s, a, o_raw, g_raw); break;
+        case 6: hipLaunchKernelGGL(gdn_decode_cols_kernel<6>, grid, dim3(64), 0, s, a, o_raw, g_raw); break;
+        case 7: hipLaunchKernelGGL(gdn_decode_cols_kernel<7>, grid, dim3(64), 0, s, a, o_raw, g_raw); break;
+        default: hipLaunchKernelGGL(gdn_decode_cols_kernel<8>, grid, dim3(64), 0, s, a, o_raw, g_raw); break;
+    }
+}
+
+void launch_gdn_norm_gate(const float* o_raw, const GdnDecodeArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(gdn_norm_gate_kernel, dim3(unsigned(a.Hv), unsigned(a.B)), dim3(kGdnDim), 0, s, o_raw, a.proj, a.proj_stride, a.z_off, a.norm_gamma, a.eps,
+                       a.act_out, a.out_f32, a.B, a.Hv);
 }
 
 int64_t gdn_prefill_work_bytes(int64_t T, int64_t Hk, int64_t Hv) {

@@ -145,7 +145,7 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
     // every weight in flight.
     int4 xv[CPL];
     float dx[CPL];
-    float xr[16], gr[16];                       // kInRmsNorm: the lane's 16 inputs and weights
+    float xr[16], gr[16], zr[16];               // kInRmsNorm / kInHeadGate: the lane's 16 inputs, weights (and gates)
     float4 gv[CPL][4], uv[CPL][4];              // kInSwiglu: the lane's gate and up values
     if constexpr (XM == kInAct) {
 #pragma unroll
@@ -161,6 +161,18 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
             const float4 a = reinterpret_cast<const float4*>(in.x)[4 * tid + k];
             const float4 g = reinterpret_cast<const float4*>(in.gamma)[4 * tid + k];
             xr[4 * k] = a.x, xr[4 * k + 1] = a.y, xr[4 * k + 2] = a.z, xr[4 * k + 3] = a.w;
+            gr[4 * k] = g.x, gr[4 * k + 1] = g.y, gr[4 * k + 2] = g.z, gr[4 * k + 3] = g.w;
+        }
+    } else if constexpr (XM == kInHeadGate) {
+        static_assert(LG == 1, "head-gate input needs K == 4096");
+        // elements 16 tid .. +15: head tid / 8, columns 16 (tid % 8) .. +15
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 a = reinterpret_cast<const float4*>(in.x)[4 * tid + k];
+            const float4 zz = reinterpret_cast<const float4*>(in.z)[4 * tid + k];
+            const float4 g = reinterpret_cast<const float4*>(in.gamma)[4 * (tid % 8) + k];
+            xr[4 * k] = a.x, xr[4 * k + 1] = a.y, xr[4 * k + 2] = a.z, xr[4 * k + 3] = a.w;
+            zr[4 * k] = zz.x, zr[4 * k + 1] = zz.y, zr[4 * k + 2] = zz.z, zr[4 * k + 3] = zz.w;
             gr[4 * k] = g.x, gr[4 * k + 1] = g.y, gr[4 * k + 2] = g.z, gr[4 * k + 3] = g.w;
         }
     } else {
@@ -201,6 +213,37 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
         float v[16];
 #pragma unroll
         for (int k = 0; k < 16; ++k) v[k] = gr[k] * xr[k] * inv;
+        uint16_t dh;
+        xv[0] = quantize16_in_pair(v, &dh);
+        dx[0] = half_bits_to_f32(dh);
+    } else if constexpr (XM == kInHeadGate) {
+        // the delta-net's per-head RMSNorm (nm/src/components.hpp:176-181) over
+        // 32 heads of 128 and the gate silu(z) (nm/src/qwen35.hpp:457-460, the
+        // gates computed by the delta-net kernel), then quantize_row_q8_0:
+        // lane h < 32 chains head h's squares in order
+        __shared__ float head_inv[32];
+        float4* sq4 = reinterpret_cast<float4*>(terms);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) sq4[4 * tid + k] = make_float4(xr[4 * k] * xr[4 * k], xr[4 * k + 1] * xr[4 * k + 1], xr[4 * k + 2] * xr[4 * k + 2], xr[4 * k + 3] * xr[4 * k + 3]);
+        __syncthreads();
+        if (tid < 32) {
+            const float4* h4 = sq4 + tid * 32;
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const float4 v = h4[i];
+                ss += v.x;
+                ss += v.y;
+                ss += v.z;
+                ss += v.w;
+            }
+            head_inv[tid] = 1.f / sqrtf(ss / 128.f + in.eps);
+        }
+        __syncthreads();  // after it the main loop may overwrite the squares
+        const float inv = head_inv[tid / 8];
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = (gr[k] * xr[k] * inv) * zr[k];  // zr: the gates silu(z)
         uint16_t dh;
         xv[0] = quantize16_in_pair(v, &dh);
         dx[0] = half_bits_to_f32(dh);
@@ -409,6 +452,8 @@ void stream_dispatch_in(int epi, const int8_t* wq, const uint16_t* wd, const Gem
     else if constexpr (LG == 1)
         if (in.mode == kInRmsNorm)
             stream_dispatch<LG, D, kInRmsNorm>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
+        else if (in.mode == kInHeadGate)
+            stream_dispatch<LG, D, kInHeadGate>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
         else
             stream_dispatch<LG, D, kInAct>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
     else
@@ -442,7 +487,7 @@ void launch_gemv_q8_in(const void* packed, const GemvInput& in, float* y, const 
     // rows per chain pass: at most 64 (one wave) and 64 KB of terms
     const int64_t TR = epi == kEpiSwigluQuant ? 64 : std::min<int64_t>({64, rows_per, (65536 / ((nb + 4) * 4)) / 8 * 8});
     size_t smem = size_t(TR) * (nb + 4) * 4;
-    if (in.mode == kInRmsNorm) smem = std::max(smem, size_t(K) * 4);  // the squares
+    if (in.mode == kInRmsNorm || in.mode == kInHeadGate) smem = std::max(smem, size_t(K) * 4);  // the squares
     switch (K / 4096) {
         // a ring of two 8-row sub-batches: deeper rings only add padding
         // sub-batches where a workgroup has few rows

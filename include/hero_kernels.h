@@ -187,6 +187,29 @@ typedef struct hero_gdn_decode_args {
 } hero_gdn_decode_args;
 int hero_gdn_decode(const hero_gdn_decode_args* args, void* stream);
 
+/* The same decode step split over value columns: 8 workgroups of one wave
+ * per (sequence, head), 16 value columns each (the delta rule's columns are
+ * independent, nm/src/recurrent.hpp:146-177). Writes the raw delta-rule
+ * outputs o_raw [B][Hv*128] (before the head RMSNorm), the output gates
+ * silu(z) into `gates` [B][Hv*128] if non-NULL, the new state and the conv
+ * ring; args->act_out and args->out_f32 are not written (act_out may be
+ * NULL). Followed by hero_gdn_norm_gate, or by hero_headgate_q8_0_gemv, the
+ * results equal hero_gdn_decode's bit for bit. */
+int hero_gdn_decode_cols(const hero_gdn_decode_args* args, float* o_raw, float* gates, void* stream);
+
+/* The per-head RMSNorm, SiLU(z) gate and Q8_0 quantization of raw delta-net
+ * outputs (the tail of nm/src/qwen35.hpp:457-460 and quantize_row_q8_0):
+ * o_raw [args->b][Hv*128] -> args->act_out (and args->out_f32 if set); z is
+ * read from args->proj at z_off. */
+int hero_gdn_norm_gate(const float* o_raw, const hero_gdn_decode_args* args, void* stream);
+
+/* y = W * quantize(head_rmsnorm(o_raw) * gates) (+ residual) in one launch:
+ * the delta-net output projection (nm/src/qwen35.hpp:457-460) with the head
+ * norm (32 heads of 128, weight gamma [128]), the gate (gates = silu(z), as
+ * hero_gdn_decode_cols writes them) and the quantization formed in the GEMV's
+ * prologue. k == 4096. Bit-exact. */
+int hero_headgate_q8_0_gemv(const void* packed, const float* o_raw, const float* gates, const float* gamma, float eps, float* y, const float* residual, int64_t n, int64_t k, void* stream);
+
 /* Delta-net prefill: the same work for T = args->b consecutive tokens of ONE
  * sequence at positions positions[0] .. positions[0]+T-1 (only positions[0]
  * is read). proj, act_out and out_f32 have T rows; conv_hist and state are

@@ -158,6 +158,19 @@ def test_gdn_decode_16_heads_matches_oracle(lib, B):
         assert blocks[b].tobytes() == oracle.quantize_row_q8_0(expect).tobytes(), f"seq {b} quantized output"
         assert np.array_equal(bits(gstate[b]), bits(st)), f"seq {b} state"
     say(f"[gdn decode H=16 B={B}] output, quantized output and state bit-exact")
+    # the column-split form from the same state: raw outputs, then the head
+    # norm + gate + quantize kernel; everything equal bit for bit
+    d_hist2, d_state2 = dev(ring), dev(state0)
+    o_raw, act2, out2 = empty(B * hv * dk * 4), empty(lib.hero_q8_0_act_bytes(B, hv * dk)), empty(B * hv * dk * 4)
+    a2 = GdnDecodeArgs(ptr(d_proj), stride, cc, cc + hv * dk, cc + hv * dk + hv, ptr(d_taps), ptr(d_hist2), ptr(d_state2),
+                       ptr(d_dt), ptr(d_decay), ptr(d_gamma), eps, ptr(d_pos), ptr(act2), ptr(out2), B, hk, hv, dk, dk, GDN_W)
+    check(lib.hero_gdn_decode_cols(a2, ptr(o_raw), None, stream()))
+    check(lib.hero_gdn_norm_gate(ptr(o_raw), a2, stream()))
+    assert np.array_equal(bits(host(out2, np.float32, (B, hv * dk))), bits(got))
+    assert np.array_equal(host(act2, np.uint8), host(act, np.uint8))
+    assert np.array_equal(bits(host(d_state2, np.float32, (B, hv, dk, dk))), bits(gstate))
+    assert np.array_equal(host(d_hist2, np.uint8), host(d_hist, np.uint8))
+    say(f"[gdn decode H=16 B={B}] column-split form: the same outputs, state and ring")
 
 
 @pytest.mark.timeout(900)

@@ -362,6 +362,61 @@ def test_gdn_decode_matches_oracle(lib, hk, hv):
             assert np.array_equal(bits(gstate[b]), bits(o_state[b])), f"state after step {step} seq {b}"
 
 
+@pytest.mark.parametrize("hk,hv,W", [(4, 8, 4), (32, 32, 4), (2, 4, 3)])
+def test_gdn_decode_column_split_equals_fused_kernel(lib, hk, hv, W):
+    """The column-split decode (8 workgroups per head) followed by the head
+    norm + gate, or by the head-gated output projection (32 heads: the GEMV
+    prologue form), over 3 steps from zero state: outputs, quantized outputs,
+    the W_o product, state and ring equal the one-workgroup-per-head kernel's
+    bit for bit (tiled key heads with hk < hv)."""
+    from hero_amd._lib import GdnDecodeArgs
+
+    rng = np.random.default_rng(hk * 7 + hv + W)
+    B, dk = 2, 128
+    cc = 2 * hk * dk + hv * dk
+    stride = cc + hv * dk + 2 * hv
+    taps = (rng.standard_normal((cc, W)) * 0.5).astype(np.float32)
+    dt = (rng.standard_normal(hv) * 0.1).astype(np.float32)
+    decay = (-np.exp(rng.standard_normal(hv) * 0.5)).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(dk)).astype(np.float32)
+    eps = np.float32(1e-6)
+    d_taps, d_dt, d_decay, d_gamma = dev(taps), dev(dt), dev(decay), dev(gamma)
+    width = hv * dk
+    if width == 4096:
+        wo = np.zeros((1000, width // 32), oracle.BLOCK)
+        wo["qs"] = rng.integers(-127, 128, (1000, width // 32, 32), dtype=np.int8)
+        wo["d"] = oracle.fp32_to_fp16(np.abs(rng.standard_normal((1000, width // 32))).astype(np.float32) * np.float32(1e-3))
+        packed = pack_weight(lib, wo, 1000, width)
+        resid = dev(rng.standard_normal(1000).astype(np.float32))
+    bufs = {}
+    for name in ("fused", "split"):
+        bufs[name] = dict(hist=empty(B * W * cc * 4), state=empty(B * hv * dk * dk * 4), act=empty(lib.hero_q8_0_act_bytes(B, width)),
+                          out=empty(B * width * 4), o_raw=empty(B * width * 4), gates=empty(B * width * 4), y=empty(1000 * 4))
+    for step in range(3):
+        proj = (rng.standard_normal((B, stride)) * 0.7).astype(np.float32)
+        d_proj, d_pos = dev(proj), dev(np.array([step, step + 5], np.int32))
+        res = {}
+        for name, bf in bufs.items():
+            a = GdnDecodeArgs(ptr(d_proj), stride, cc, cc + width, cc + width + hv, ptr(d_taps), ptr(bf["hist"]), ptr(bf["state"]),
+                              ptr(d_dt), ptr(d_decay), ptr(d_gamma), eps, ptr(d_pos), ptr(bf["act"]), ptr(bf["out"]), B, hk, hv, dk, dk, W)
+            if name == "fused":
+                check(lib.hero_gdn_decode(a, stream()))
+            else:
+                check(lib.hero_gdn_decode_cols(a, ptr(bf["o_raw"]), ptr(bf["gates"]), stream()))
+                check(lib.hero_gdn_norm_gate(ptr(bf["o_raw"]), a, stream()))
+            res[name] = [host(bf[k], np.uint8).copy() for k in ("out", "act", "state", "hist")]
+        for i, what in enumerate(("output", "quantized output", "state", "ring")):
+            assert np.array_equal(res["fused"][i], res["split"][i]), f"step {step}: {what}"
+        if width == 4096:  # sequence 0 through W_o: plain GEMV on the fused act vs the head-gated prologue
+            fb, sb = bufs["fused"], bufs["split"]
+            a_all = host(fb["act"], np.uint8)  # [B*K int8][B*K/32 fp32]: sequence 0's row as a 1-row act
+            act0 = dev(np.concatenate([a_all[:width], a_all[B * width: B * width + width // 32 * 4]]))
+            check(lib.hero_q8_0_gemv(ptr(packed), ptr(act0), ptr(fb["y"]), ptr(resid), 1000, width, stream()))
+            check(lib.hero_headgate_q8_0_gemv(ptr(packed), ptr(sb["o_raw"]), ptr(sb["gates"]), ptr(d_gamma), eps, ptr(sb["y"]), ptr(resid),
+                                              1000, width, stream()))
+            assert np.array_equal(host(fb["y"], np.uint32), host(sb["y"], np.uint32)), f"step {step}: W_o product"
+
+
 @pytest.mark.parametrize("W,chunks", [(4, [2, 7, 1, 3, 5, 40, 17]), (3, [1, 1, 6, 2, 33]), (1, [3, 1, 4, 16])])
 def test_gdn_prefill_chunks_match_oracle(lib, W, chunks):
     """Delta-net prefill in ragged chunks (shorter and longer than the conv

@@ -153,6 +153,14 @@ def main() -> int:
     log(f"loaded and packed: {model.dims.device_bytes / 1e9:.2f} GB of weights on the device in {time.perf_counter() - t:.1f} s")
     state = model.new_state(ctx)
     if args.profile_gemvs:
+        # three 512 MiB device-to-device copies first: the known-size
+        # dispatches hero_amd.traffic calibrates the byte counters with
+        src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
         sec, launches, nbytes = model.time_gemvs(state, args.gemv_reps)
         print(json.dumps({"gemv_launches_per_step": launches, "gemv_bytes_per_step": nbytes,
                           "avg_launch_us": sec / (args.gemv_reps * launches) * 1e6}), flush=True)

@@ -38,6 +38,8 @@ import sys
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+CALIBRATION_BYTES = 512 << 20  # one known-size device-to-device copy (read and written once)
+CALIBRATION_COPIES = 3
 
 
 def _torch():
@@ -59,11 +61,24 @@ def _bytes(n: int):
     return t.empty(int(n), dtype=t.uint8, device="cuda")
 
 
+DIRECT = 0  # --direct N: run each case N times as plain launches (no graph), for counter collection
+
+
 def _time_graph(body, launches: int, replays: int, budget_s: float = 1.0) -> float:
     """seconds per launch of `body` (which makes `launches` launches), from
     hipGraph replays timed with events on the replay stream; at most
-    `replays` replays and about `budget_s` seconds of them"""
+    `replays` replays and about `budget_s` seconds of them. With DIRECT set,
+    `body` instead runs DIRECT times as plain launches (what a per-dispatch
+    counter collection profiles)."""
     t = _torch()
+    if DIRECT:
+        e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(DIRECT):
+            body()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / (DIRECT * launches)
     body()  # warm: code objects, caches
     t.cuda.synchronize()
     g = t.cuda.CUDAGraph()
@@ -391,12 +406,26 @@ def main(argv=None) -> int:
     ap.add_argument("--suite", default="gemv,gdn,attn")
     ap.add_argument("--out", default=None, help="write a markdown table here")
     ap.add_argument("--gemv-batches", default=",".join(map(str, GEMV_BATCHES)), help="activation rows M of the gemv suite")
+    ap.add_argument("--direct", type=int, default=0, help="run each case this many times as plain launches instead of graph replays")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="first copy 512 MiB device to device three times: the known-size dispatches hero_amd.traffic calibrates "
+                         "FETCH_SIZE / WRITE_SIZE with")
     args = ap.parse_args(argv)
     t = _torch()
     if not t.cuda.is_available():
         print("microbench: needs a GPU", file=sys.stderr)
         return 2
     from ._lib import lib
+
+    global DIRECT
+    DIRECT = args.direct
+    if args.calibrate:
+        src = t.empty(CALIBRATION_BYTES, dtype=t.uint8, device="cuda").fill_(1)
+        dst = t.empty_like(src)
+        for _ in range(CALIBRATION_COPIES):
+            dst.copy_(src)
+        t.cuda.synchronize()
+        del src, dst
 
     rows = []
     suites = args.suite.split(",")

@@ -315,19 +315,26 @@ TINY_CONFIG = HybridShape(vocab=32000, d_model=1024, layers=4, ffn=2816, q_heads
 HYBRID_8B_CONFIG = HybridShape(vocab=151936, d_model=4096, layers=32, ffn=12288, q_heads=32, kv_heads=8, head_dim=128, key_heads=32, value_heads=32)
 
 
-def synth_config(shape: HybridShape, seed: int, ctx: int = 4096, tied: bool = True) -> SynthConfig:
+# weight_mix values of the synthetic writer
+WEIGHTS_Q8_0 = 0  # every 2-D weight Q8_0
+WEIGHTS_K_MIX = 1  # the tensor types of a Q4_K_M checkpoint: Q4_K, Q5_K, Q6_K and Q8_0
+
+
+def synth_config(shape: HybridShape, seed: int, ctx: int = 4096, tied: bool = True, weight_mix: int = WEIGHTS_Q8_0) -> SynthConfig:
     return SynthConfig(shape.vocab, shape.d_model, shape.layers, shape.ffn, shape.q_heads, shape.kv_heads, shape.head_dim,
                        shape.key_head_dim, shape.value_head_dim, shape.key_heads, shape.value_heads, shape.conv_width,
-                       ctx, shape.rope_base, 1 if tied else 0, seed)
+                       ctx, shape.rope_base, 1 if tied else 0, seed, weight_mix)
 
 
-def write_synthetic_gguf(path: str, shape: HybridShape = TINY_CONFIG, seed: int = 1, ctx: int = 4096, tied: bool = True) -> None:
-    cfg = synth_config(shape, seed, ctx, tied)
+def write_synthetic_gguf(path: str, shape: HybridShape = TINY_CONFIG, seed: int = 1, ctx: int = 4096, tied: bool = True,
+                         weight_mix: int = WEIGHTS_Q8_0) -> None:
+    cfg = synth_config(shape, seed, ctx, tied, weight_mix)
     check(lib.hero_synth_qwen35_file(byref(cfg), path.encode()))
 
 
-def synthetic_gguf_image(shape: HybridShape = TINY_CONFIG, seed: int = 1, ctx: int = 4096, tied: bool = True) -> np.ndarray:
-    cfg = synth_config(shape, seed, ctx, tied)
+def synthetic_gguf_image(shape: HybridShape = TINY_CONFIG, seed: int = 1, ctx: int = 4096, tied: bool = True,
+                         weight_mix: int = WEIGHTS_Q8_0) -> np.ndarray:
+    cfg = synth_config(shape, seed, ctx, tied, weight_mix)
     n = lib.hero_synth_qwen35_size(byref(cfg))
     if n < 0:
         check(1)

@@ -72,6 +72,7 @@ class SynthConfig(ctypes.Structure):
         ("q_heads", c_int64), ("kv_heads", c_int64), ("head_dim", c_int64),
         ("key_head_dim", c_int64), ("value_head_dim", c_int64), ("key_heads", c_int64), ("value_heads", c_int64),
         ("conv_width", c_int64), ("ctx", c_int64), ("rope_base", c_double), ("tied", c_int32), ("seed", c_uint64),
+        ("weight_mix", c_int32),
     ]
 
 

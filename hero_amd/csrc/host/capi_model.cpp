@@ -38,6 +38,7 @@ SynthConfig to_synth(const hero_synth_config* c) {
     s.rope_base = c->rope_base;
     s.tied = c->tied != 0;
     s.seed = c->seed;
+    s.weight_mix = uint32_t(c->weight_mix);
     need(c->vocab > 0 && c->d_model > 0 && c->layers > 0 && c->ffn > 0 && c->q_heads > 0 && c->kv_heads > 0 && c->head_dim > 0, "synth: dimensions must be positive");
     need(c->key_head_dim > 0 && c->value_head_dim > 0 && c->key_heads > 0 && c->value_heads > 0 && c->conv_width > 0 && c->ctx > 0, "synth: dimensions must be positive");
     return s;

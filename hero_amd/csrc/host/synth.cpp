@@ -69,6 +69,98 @@ void quantize_block_lround(const float* x, uint8_t* out34) {
     for (int j = 0; j < 32; ++j) out34[2 + j] = uint8_t(int8_t(std::lround(x[j] * id)));
 }
 
+// ---- K-quant blocks of 256 weights (GGUF types 12, 13, 14) -------------------
+// A plain min/max quantizer per 32 (Q4_K, Q5_K) or 16 (Q6_K) weights, with the
+// sub-block scales and mins quantized against the block's largest ones; the
+// byte layouts are ggml's (the ones nm/src/quant.hpp:153-300 decodes). These
+// synthetic fixtures only need to be valid blocks whose decoded weights follow
+// the floats roughly; both the reference and this build decode the bytes.
+inline int nearest(float v) { return int(std::lround(v)); }
+
+// 6-bit scale / min j (0..7) into the 12-byte packing get_scale_min_k4 reads
+void put_scale_min_k4(uint8_t* q, int j, int sc, int m) {
+    if (j < 4) {
+        q[j] = uint8_t((q[j] & 0xC0) | sc);
+        q[j + 4] = uint8_t((q[j + 4] & 0xC0) | m);
+    } else {
+        q[j + 4] = uint8_t((sc & 0xF) | ((m & 0xF) << 4));
+        q[j - 4] = uint8_t(q[j - 4] | ((sc >> 4) << 6));
+        q[j] = uint8_t(q[j] | ((m >> 4) << 6));
+    }
+}
+
+// Q4_K (bits = 4, 144 bytes) or Q5_K (bits = 5, 176 bytes): weight i of
+// sub-block j (32 weights) = d*sc_j*q - dmin*m_j, q in [0, 2^bits - 1]
+void quantize_block_q45_k(const float* x, uint8_t* out, int bits) {
+    const int qmax = (1 << bits) - 1;
+    float scale[8], minv[8];
+    for (int j = 0; j < 8; ++j) {
+        float lo = x[32 * j], hi = x[32 * j];
+        for (int i = 1; i < 32; ++i) lo = std::min(lo, x[32 * j + i]), hi = std::max(hi, x[32 * j + i]);
+        lo = std::min(lo, 0.f);  // the min term subtracts: keep it >= 0
+        scale[j] = (hi - lo) / float(qmax);
+        minv[j] = -lo;
+    }
+    const float max_scale = *std::max_element(scale, scale + 8), max_min = *std::max_element(minv, minv + 8);
+    const uint16_t dh = fp32_to_fp16_ref(max_scale / 63.f), mh = fp32_to_fp16_ref(max_min / 63.f);
+    const float d = fp16_to_fp32_ref(dh), dmin = fp16_to_fp32_ref(mh);
+    uint8_t scales[12] = {0};
+    int sc[8], mn[8];
+    for (int j = 0; j < 8; ++j) {
+        sc[j] = d > 0.f ? std::min(63, std::max(0, nearest(scale[j] / d))) : 0;
+        mn[j] = dmin > 0.f ? std::min(63, std::max(0, nearest(minv[j] / dmin))) : 0;
+        put_scale_min_k4(scales, j, sc[j], mn[j]);
+    }
+    uint8_t qs[128] = {0}, qh[32] = {0};
+    for (int j = 0; j < 8; ++j) {
+        const float step = d * float(sc[j]), off = dmin * float(mn[j]);
+        for (int i = 0; i < 32; ++i) {
+            const int q = step > 0.f ? std::min(qmax, std::max(0, nearest((x[32 * j + i] + off) / step))) : 0;
+            // sub-blocks 2p and 2p+1 share qs[32p .. 32p+31]: low and high nibbles
+            qs[32 * (j / 2) + i] = uint8_t(qs[32 * (j / 2) + i] | ((q & 0xF) << (4 * (j & 1))));
+            if (bits == 5 && (q & 16)) qh[i] = uint8_t(qh[i] | (1 << j));  // bit j of qh[i]
+        }
+    }
+    std::memcpy(out, &dh, 2);
+    std::memcpy(out + 2, &mh, 2);
+    std::memcpy(out + 4, scales, 12);
+    if (bits == 5) {
+        std::memcpy(out + 16, qh, 32);
+        std::memcpy(out + 48, qs, 128);
+    } else {
+        std::memcpy(out + 16, qs, 128);
+    }
+}
+
+// Q6_K (210 bytes): weight = d*sc_g*q, q in [-32, 31], an int8 scale per 16
+void quantize_block_q6_k(const float* x, uint8_t* out) {
+    float scale[16];
+    for (int g = 0; g < 16; ++g) {
+        float amax = 0.f;
+        for (int i = 0; i < 16; ++i) amax = std::max(amax, std::fabs(x[16 * g + i]));
+        scale[g] = amax / 31.f;
+    }
+    const float max_scale = *std::max_element(scale, scale + 16);
+    const uint16_t dh = fp32_to_fp16_ref(max_scale / 127.f);
+    const float d = fp16_to_fp32_ref(dh);
+    int8_t sc[16];
+    for (int g = 0; g < 16; ++g) sc[g] = int8_t(d > 0.f ? std::min(127, nearest(scale[g] / d)) : 0);
+    uint8_t ql[128] = {0}, qh[64] = {0};
+    for (int p = 0; p < 256; ++p) {
+        const float step = d * float(sc[p / 16]);
+        const int q = (step > 0.f ? std::min(31, std::max(-32, nearest(x[p] / step))) : 0) + 32;  // 0..63
+        // half h (128 weights): element e lives in ql[64h + e % 64] (low nibble for
+        // e < 64, high for e >= 64) and qh[32h + e % 32] at bit 2 (e / 32)
+        const int h = p / 128, e = p % 128;
+        ql[64 * h + e % 64] = uint8_t(ql[64 * h + e % 64] | ((q & 0xF) << (e < 64 ? 0 : 4)));
+        qh[32 * h + e % 32] = uint8_t(qh[32 * h + e % 32] | ((q >> 4) << (2 * (e / 32))));
+    }
+    std::memcpy(out, ql, 128);
+    std::memcpy(out + 128, qh, 64);
+    std::memcpy(out + 192, sc, 16);
+    std::memcpy(out + 208, &dh, 2);
+}
+
 template <class F>
 void parallel_rows(size_t rows, F&& f) {
     size_t threads = std::max<size_t>(1, std::min<size_t>(std::thread::hardware_concurrency(), 16));
@@ -88,7 +180,17 @@ void parallel_rows(size_t rows, F&& f) {
 
 // ---- GGUF image builder ------------------------------------------------------
 enum : uint32_t { GGUF_U32 = 4, GGUF_F32 = 6, GGUF_STRING = 8, GGUF_ARRAY = 9 };
-enum : uint32_t { T_F32 = 0, T_Q8_0 = 8 };
+enum : uint32_t { T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14 };
+
+uint64_t type_bytes(uint32_t type, uint64_t n) {
+    switch (type) {
+        case T_Q8_0: return n / 32 * 34;
+        case T_Q4_K: return n / 256 * 144;
+        case T_Q5_K: return n / 256 * 176;
+        case T_Q6_K: return n / 256 * 210;
+        default: return n * 4;
+    }
+}
 
 struct TensorSpec {
     std::string name;
@@ -139,13 +241,16 @@ struct Writer {
 
 std::vector<TensorSpec> tensor_specs(const SynthConfig& c) {
     std::vector<TensorSpec> t;
-    auto mat = [&](const std::string& name, uint64_t in, uint64_t out) {
+    // weight_mix 1: the tensor types of a Q4_K_M checkpoint (Q4_K for most
+    // projections, Q5_K and Q6_K for some, Q8_0 for the small gate
+    // projections); 0: Q8_0 everywhere
+    auto mat = [&](const std::string& name, uint64_t in, uint64_t out, uint32_t mixed_type = T_Q8_0) {
         TensorSpec s;
         s.name = name;
         s.in = in;
         s.out = out;
         s.matrix = true;
-        s.type = T_Q8_0;
+        s.type = c.weight_mix == 1 ? mixed_type : T_Q8_0;
         t.push_back(s);
     };
     auto vec = [&](const std::string& name, uint64_t n, TensorSpec::Kind kind, double scale = 0.0) {
@@ -157,19 +262,19 @@ std::vector<TensorSpec> tensor_specs(const SynthConfig& c) {
         t.push_back(s);
     };
     const uint64_t D = c.D, CC = 2 * c.Hk * c.Dk + c.Hv * c.Dv;
-    mat("token_embd.weight", D, c.V);
+    mat("token_embd.weight", D, c.V, T_Q6_K);
     vec("output_norm.weight", D, TensorSpec::Ones);
-    if (!c.tied) mat("output.weight", D, c.V);
+    if (!c.tied) mat("output.weight", D, c.V, T_Q6_K);
     for (uint64_t l = 0; l < c.L; ++l) {
         const std::string b = "blk." + std::to_string(l) + ".";
         vec(b + "attn_norm.weight", D, TensorSpec::Ones);
         vec(b + "post_attention_norm.weight", D, TensorSpec::Ones);
-        mat(b + "ffn_gate.weight", D, c.FF);
-        mat(b + "ffn_up.weight", D, c.FF);
-        mat(b + "ffn_down.weight", c.FF, D);
+        mat(b + "ffn_gate.weight", D, c.FF, T_Q4_K);
+        mat(b + "ffn_up.weight", D, c.FF, T_Q4_K);
+        mat(b + "ffn_down.weight", c.FF, D, T_Q6_K);
         if ((l + 1) % 4 != 0) {
-            mat(b + "attn_qkv.weight", D, CC);
-            mat(b + "attn_gate.weight", D, c.Hv * c.Dv);
+            mat(b + "attn_qkv.weight", D, CC, T_Q5_K);
+            mat(b + "attn_gate.weight", D, c.Hv * c.Dv, T_Q4_K);
             TensorSpec conv;
             conv.name = b + "ssm_conv1d.weight";
             conv.in = c.conv_width;
@@ -183,14 +288,14 @@ std::vector<TensorSpec> tensor_specs(const SynthConfig& c) {
             mat(b + "ssm_alpha.weight", D, c.Hv);
             vec(b + "ssm_dt.bias", c.Hv, TensorSpec::Zeros);
             vec(b + "ssm_norm.weight", c.Dv, TensorSpec::Ones);
-            mat(b + "ssm_out.weight", c.Hv * c.Dv, D);
+            mat(b + "ssm_out.weight", c.Hv * c.Dv, D, T_Q4_K);
         } else {
-            mat(b + "attn_q.weight", D, 2 * c.Hq * c.head_dim);
+            mat(b + "attn_q.weight", D, 2 * c.Hq * c.head_dim, T_Q4_K);
             vec(b + "attn_q_norm.weight", c.head_dim, TensorSpec::Ones);
-            mat(b + "attn_k.weight", D, c.Hkv * c.head_dim);
+            mat(b + "attn_k.weight", D, c.Hkv * c.head_dim, T_Q4_K);
             vec(b + "attn_k_norm.weight", c.head_dim, TensorSpec::Ones);
-            mat(b + "attn_v.weight", D, c.Hkv * c.head_dim);
-            mat(b + "attn_output.weight", c.Hq * c.head_dim, D);
+            mat(b + "attn_v.weight", D, c.Hkv * c.head_dim, T_Q6_K);
+            mat(b + "attn_output.weight", c.Hq * c.head_dim, D, T_Q5_K);
         }
     }
     return t;
@@ -228,7 +333,7 @@ std::vector<uint8_t> header_bytes(const SynthConfig& c, std::vector<TensorSpec>&
     uint64_t offset = 0;
     for (TensorSpec& s : specs) {
         const uint64_t n = s.in * s.out;
-        s.bytes = s.type == T_Q8_0 ? n / 32 * 34 : n * 4;
+        s.bytes = type_bytes(s.type, n);
         s.offset = offset;
         offset = (offset + s.bytes + 31) & ~uint64_t(31);
         w.str(s.name);
@@ -251,6 +356,27 @@ std::vector<uint8_t> header_bytes(const SynthConfig& c, std::vector<TensorSpec>&
 
 void fill_tensor(const SynthConfig& c, const TensorSpec& s, uint64_t tensor_index, uint8_t* dst) {
     const uint64_t stream = stream_of(c.seed, tensor_index);
+    if (s.type == T_Q4_K || s.type == T_Q5_K || s.type == T_Q6_K) {
+        const uint64_t in = s.in, blocks = in / 256, bb = type_bytes(s.type, 256);
+        parallel_rows(s.out, [&](size_t r) {
+            std::vector<float> row(in);
+            const uint64_t base = uint64_t(r) * in;
+            for (uint64_t i = 0; i < in; i += 2) {
+                float z0, z1;
+                normal_pair(stream, (base + i) >> 1, &z0, &z1);
+                row[i] = 0.02f * z0;
+                row[i + 1] = 0.02f * z1;
+            }
+            for (uint64_t b = 0; b < blocks; ++b) {
+                uint8_t* o = dst + (uint64_t(r) * blocks + b) * bb;
+                if (s.type == T_Q6_K)
+                    quantize_block_q6_k(row.data() + b * 256, o);
+                else
+                    quantize_block_q45_k(row.data() + b * 256, o, s.type == T_Q5_K ? 5 : 4);
+            }
+        });
+        return;
+    }
     if (s.type == T_Q8_0) {
         const uint64_t in = s.in, blocks = in / 32;
         parallel_rows(s.out, [&](size_t r) {
@@ -281,6 +407,9 @@ void fill_tensor(const SynthConfig& c, const TensorSpec& s, uint64_t tensor_inde
 void check_config(const SynthConfig& c) {
     if (c.L == 0 || c.L % 4 != 0) throw std::invalid_argument("synth: L must be a positive multiple of 4");
     if (c.D % 32 || c.FF % 32 || (c.Hv * c.Dv) % 32 || (c.Hq * c.head_dim) % 32) throw std::invalid_argument("synth: every Q8_0 input width must be a multiple of 32");
+    if (c.weight_mix > 1) throw std::invalid_argument("synth: weight_mix must be 0 (Q8_0) or 1 (K-quant mix)");
+    if (c.weight_mix == 1 && (c.D % 256 || c.FF % 256 || (c.Hv * c.Dv) % 256 || (c.Hq * c.head_dim) % 256))
+        throw std::invalid_argument("synth: K-quant input widths must be multiples of 256");
     if (c.Hkv == 0 || c.Hq % c.Hkv || c.Hk == 0 || c.Hv % c.Hk || c.Dk != c.Dv || c.head_dim % 8) throw std::invalid_argument("synth: inconsistent head shapes");
 }
 

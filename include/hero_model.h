@@ -118,11 +118,15 @@ typedef struct hero_synth_config {
     double rope_base;
     int32_t tied;
     uint64_t seed;
+    int32_t weight_mix;
 } hero_synth_config;
 
-/* Seeded random-init qwen35 GGUF (Q8_0 2-D weights, N(0,0.02) before
- * quantization). size -> bytes of the image; image -> fill a caller buffer;
- * file -> write to a path. */
+/* Seeded random-init qwen35 GGUF, N(0,0.02) weights before quantization.
+ * weight_mix 0: every 2-D weight Q8_0; 1: the tensor types of a Q4_K_M
+ * checkpoint (Q6_K embedding, LM head, ffn_down and attn_v; Q5_K attn_qkv and
+ * attn_output; Q4_K the other projections; Q8_0 ssm_alpha/ssm_beta), every
+ * input width a multiple of 256. size -> bytes of the image; image -> fill a
+ * caller buffer; file -> write to a path. */
 int64_t hero_synth_qwen35_size(const hero_synth_config* config);
 int hero_synth_qwen35_image(const hero_synth_config* config, void* image, size_t capacity);
 int hero_synth_qwen35_file(const hero_synth_config* config, const char* path);

@@ -32,6 +32,9 @@ _sigs = {
     "oracle_quantize_row_q8_K": (None, [c_void_p, c_void_p, c_size_t]),
     "oracle_vec_dot_kquant": (c_float, [c_int, c_void_p, c_void_p, c_size_t]),
     "oracle_matmul_kquant": (None, [c_int, c_void_p, c_size_t, c_size_t, c_void_p, c_size_t, c_void_p]),
+    "oracle_dot_block_q5_K": (c_float, [c_void_p, c_void_p]),
+    "oracle_linear_rows": (c_int, [c_int, c_void_p, c_size_t, c_size_t, c_void_p, c_size_t, c_void_p]),
+    "oracle_dequant_rows": (c_int, [c_int, c_void_p, c_size_t, c_size_t, c_void_p]),
     "oracle_matmul_q8_0": (None, [c_void_p, c_size_t, c_size_t, c_void_p, c_size_t, c_void_p]),
     "oracle_rmsnorm_rows": (None, [c_void_p, c_void_p, c_size_t, c_size_t, c_float]),
     "oracle_l2_normalize": (None, [c_void_p, c_void_p, c_size_t, c_float]),
@@ -156,8 +159,12 @@ def sample_topk(logits, top_k, temp, top_p, u) -> int:
 
 
 # ---- K-quants (GGUF types 12 = Q4_K, 14 = Q6_K; activations as Q8_K) ----------
-Q4_K, Q6_K = 12, 14
-KBLOCK_BYTES = {Q4_K: 144, Q6_K: 210}
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
+KBLOCK_BYTES = {Q4_K: 144, Q5_K: 176, Q6_K: 210}
+
+
+def row_bytes(wtype, k):
+    return k // 32 * 34 if wtype == Q8_0 else k // 256 * KBLOCK_BYTES[wtype]
 Q8K_BYTES = 292
 
 
@@ -184,6 +191,36 @@ def matmul_kquant(wtype, w, n, k, X):
     Y = np.empty((X.shape[0], n), np.float32)
     lib.oracle_matmul_kquant(wtype, _p(w), n, k, _p(X), X.shape[0], _p(Y))
     return Y
+
+
+def dot_block_q5_K(block, x) -> np.float32:
+    """fp32-activation dot of one raw Q5_K block (176 bytes) with 256 floats"""
+    block = np.ascontiguousarray(block, np.uint8)
+    x = _f32(x).ravel()
+    assert block.size == 176 and x.size == 256
+    return np.float32(lib.oracle_dot_block_q5_K(_p(block), _p(x)))
+
+
+def linear(wtype, w, n, k, X):
+    """Weight::matmul of a raw tensor of any linear type (Q8_0 as stored in the
+    GGUF, Q4_K, Q5_K, Q6_K): Y[T, n]"""
+    w = np.ascontiguousarray(w, np.uint8)
+    assert w.size == n * row_bytes(wtype, k)
+    X = _f32(X).reshape(-1, k)
+    Y = np.empty((X.shape[0], n), np.float32)
+    if lib.oracle_linear_rows(wtype, _p(w), n, k, _p(X), X.shape[0], _p(Y)) != 0:
+        raise ValueError(f"linear: unsupported type {wtype}")
+    return Y
+
+
+def dequant_rows(wtype, w, rows, k):
+    """rows of a raw tensor dequantized to fp32 (the embedding gather)"""
+    w = np.ascontiguousarray(w, np.uint8)
+    assert w.size >= rows * row_bytes(wtype, k)
+    out = np.empty((rows, k), np.float32)
+    if lib.oracle_dequant_rows(wtype, _p(w), rows, k, _p(out)) != 0:
+        raise ValueError(f"dequant: unsupported type {wtype}")
+    return out
 
 
 def rmsnorm(x, gamma, eps=1e-6):

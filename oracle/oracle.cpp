@@ -404,6 +404,108 @@ void matmul_kquant(int type, const void* W, size_t N, size_t K, const float* X, 
     });
 }
 
+// nm/src/quant.hpp:207-229. Sub-block pair p (64 weights) uses scale/min
+// entries 2p and 2p+1 and the nibbles of qs[32p .. 32p+31] (low for the first
+// 32 weights, high for the next); its fifth bits are bits 2p and 2p+1 of qh[l].
+// One fp32 accumulator over the 256 products in order, each product
+// (d1*q - m1)*x rounded step by step.
+float dot_block_q5_K(const BlockQ5K& b, const float* x) {
+    const float d = fp16_to_fp32(b.d), mn = fp16_to_fp32(b.dmin);
+    float acc = 0.f;
+    for (int p = 0; p < 4; ++p) {
+        int sc, m;
+        q4k_scale_min(b.scales, 2 * p, sc, m);
+        const float d1 = d * float(sc), m1 = mn * float(m);
+        q4k_scale_min(b.scales, 2 * p + 1, sc, m);
+        const float d2 = d * float(sc), m2 = mn * float(m);
+        const uint8_t* ql = b.qs + 32 * p;
+        for (int l = 0; l < 32; ++l) {
+            const int q = (ql[l] & 0xF) + ((b.qh[l] >> (2 * p)) & 1) * 16;
+            acc += (d1 * float(q) - m1) * x[64 * p + l];
+        }
+        for (int l = 0; l < 32; ++l) {
+            const int q = (ql[l] >> 4) + ((b.qh[l] >> (2 * p + 1)) & 1) * 16;
+            acc += (d2 * float(q) - m2) * x[64 * p + 32 + l];
+        }
+    }
+    return acc;
+}
+
+// nm/src/quant_i8.hpp:487-495 (the fp32-activation branch of Weight::matmul):
+// each output the sequential sum of its blocks' dots
+void matmul_q5_K(const BlockQ5K* W, size_t N, size_t K, const float* X, size_t T, float* Y) {
+    const size_t nb = K / 256;
+    par_for_lambda(N, [&](size_t o) {
+        for (size_t t = 0; t < T; ++t) {
+            float acc = 0.f;
+            for (size_t i = 0; i < nb; ++i) acc += dot_block_q5_K(W[o * nb + i], X + t * K + i * 256);
+            Y[t * N + o] = acc;
+        }
+    });
+}
+
+size_t row_bytes(int type, size_t k) {
+    switch (type) {
+        case 8: return k / 32 * 34;
+        case 12: return k / 256 * 144;
+        case 13: return k / 256 * 176;
+        case 14: return k / 256 * 210;
+        default: throw std::invalid_argument("row_bytes: unsupported ggml type " + std::to_string(type));
+    }
+}
+
+// nm/src/quant.hpp:322-395
+void dequant_row(int type, const void* row, float* out, size_t k) {
+    if (type == 8) return dequant_row_q8_0(static_cast<const BlockQ8*>(row), out, k);
+    for (size_t i = 0; i < k / 256; ++i) {
+        float* y = out + 256 * i;
+        if (type == 12 || type == 13) {  // Q4_K, Q5_K: d1*q - m1
+            const uint8_t* blk = static_cast<const uint8_t*>(row) + i * (type == 12 ? 144 : 176);
+            uint16_t dh, mh;
+            std::memcpy(&dh, blk, 2);
+            std::memcpy(&mh, blk + 2, 2);
+            const uint8_t* scales = blk + 4;
+            const uint8_t* qh = type == 13 ? blk + 16 : nullptr;
+            const uint8_t* qs = blk + (type == 13 ? 48 : 16);
+            const float d = fp16_to_fp32(dh), mn = fp16_to_fp32(mh);
+            for (int p = 0; p < 4; ++p) {
+                for (int h = 0; h < 2; ++h) {
+                    int sc, m;
+                    q4k_scale_min(scales, 2 * p + h, sc, m);
+                    const float d1 = d * float(sc), m1 = mn * float(m);
+                    for (int l = 0; l < 32; ++l) {
+                        int q = h ? (qs[32 * p + l] >> 4) : (qs[32 * p + l] & 0xF);
+                        if (qh) q += ((qh[l] >> (2 * p + h)) & 1) * 16;
+                        y[64 * p + 32 * h + l] = d1 * float(q) - m1;
+                    }
+                }
+            }
+        } else if (type == 14) {  // Q6_K: (d * scale) * q per group of 16
+            const BlockQ6K& b = static_cast<const BlockQ6K*>(row)[i];
+            const float d = fp16_to_fp32(b.d);
+            for (int p = 0; p < 256; ++p) {
+                const int h = p / 128, e = p % 128;
+                const uint8_t lo = b.ql[64 * h + e % 64];
+                const int low = e < 64 ? (lo & 0xF) : (lo >> 4);
+                const int high = (b.qh[32 * h + e % 32] >> (2 * (e / 32))) & 3;
+                y[p] = d * float(b.scales[p / 16]) * float((low | (high << 4)) - 32);
+            }
+        } else {
+            throw std::invalid_argument("dequant_row: unsupported ggml type " + std::to_string(type));
+        }
+    }
+}
+
+void linear_rows(const Linear& lin, const float* X, size_t T, float* Y) {
+    switch (lin.type) {
+        case 8: return matmul_q8_0(static_cast<const BlockQ8*>(lin.w), lin.N, lin.K, X, T, Y);
+        case 12:
+        case 14: return matmul_kquant(lin.type, lin.w, lin.N, lin.K, X, T, Y);
+        case 13: return matmul_q5_K(static_cast<const BlockQ5K*>(lin.w), lin.N, lin.K, X, T, Y);
+        default: throw std::invalid_argument("linear: unsupported ggml type " + std::to_string(lin.type));
+    }
+}
+
 // ---------------------------------------------------------------------------
 // small ops
 // ---------------------------------------------------------------------------
@@ -540,7 +642,7 @@ void embed(const Model& m, const int32_t* ids, size_t n, float* out) {
     const size_t D = m.c.D;
     for (size_t i = 0; i < n; ++i) {
         if (ids[i] < 0 || size_t(ids[i]) >= m.c.V) throw std::out_of_range("embed: token id out of range");
-        dequant_row_q8_0(m.embedding.w + size_t(ids[i]) * (D / 32), out + i * D, D);
+        dequant_row(m.embedding.type, static_cast<const uint8_t*>(m.embedding.w) + size_t(ids[i]) * row_bytes(m.embedding.type, D), out + i * D, D);
     }
 }
 
@@ -548,7 +650,7 @@ namespace {
 
 std::vector<float> linear(const Linear& lin, const float* X, size_t T) {
     std::vector<float> Y(T * lin.N);
-    matmul_q8_0(lin.w, lin.N, lin.K, X, T, Y.data());
+    linear_rows(lin, X, T, Y.data());
     return Y;
 }
 
@@ -662,7 +764,7 @@ void forward(const Model& m, State& s, const float* rows, size_t T, float* logit
     s.tokens += T;
     std::vector<float> last(X.begin() + (T - 1) * D, X.begin() + T * D);
     rmsnorm(last.data(), m.final_norm.data(), D, c.eps);
-    matvec_q8_0(m.output.w, m.output.N, m.output.K, last.data(), logits);
+    linear_rows(m.output, last.data(), 1, logits);  // matvec = the one-row matmul, output by output
 }
 
 // nm/src/logits.hpp:71-105: sort down to k candidates, exp((v - max) / temp)

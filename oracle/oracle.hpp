@@ -25,8 +25,13 @@
 //   attention             golden vectors (scale 1/sqrt(128) and 1) + the reference's own
 //                         Full / Local (ring, width 3 and 1024) caches at 12 probes + hand-worked
 //                         causal / window-of-one cases + float64 brute force (grouped K/V heads)
+//   Q4_K / Q6_K dots      golden vectors from the compiled reference
+//   dot_block_q5_K        golden vectors from the compiled reference + float64 dequant-dot
+//   dequant_row (K-quants) golden rows from the compiled reference + integer decode of the
+//                         packed fields written independently in the test
 //   Qwen35 forward        golden logits and greedy ids of the tiny Q8_0 model, of its variant
-//                         with 4 key heads over 8 value heads and an untied output.weight, and
+//                         with 4 key heads over 8 value heads and an untied output.weight, of
+//                         the tiny model with Q4_K/Q5_K/Q6_K/Q8_0 tensors (a Q4_K_M mix), and
 //                         the greedy ids of the ~8B model (600-token prompt, 32 passes)
 #pragma once
 #include <cstddef>
@@ -61,8 +66,16 @@ struct BlockQ8K {
     int8_t qs[256];
     int16_t bsums[16];
 };
+// Q5_K (nm/src/quant.hpp:70-76): Q4_K's scales plus a fifth bit per weight in
+// qh (bit j of qh[l] for element l of 32-element sub-block j): 176 bytes
+struct BlockQ5K {
+    uint16_t d, dmin;
+    uint8_t scales[12];
+    uint8_t qh[32];
+    uint8_t qs[128];
+};
 #pragma pack(pop)
-static_assert(sizeof(BlockQ4K) == 144 && sizeof(BlockQ6K) == 210 && sizeof(BlockQ8K) == 292, "K-quant block sizes");
+static_assert(sizeof(BlockQ4K) == 144 && sizeof(BlockQ5K) == 176 && sizeof(BlockQ6K) == 210 && sizeof(BlockQ8K) == 292, "K-quant block sizes");
 
 // activation quantizer for K-quant weights (nm/src/quant_i8.hpp:31-64)
 void quantize_row_q8_K(const float* x, BlockQ8K* y, size_t k);
@@ -72,6 +85,16 @@ float vec_dot_q6_K_q8_K(size_t n, const BlockQ6K* w, const BlockQ8K* x);
 // Weight::matvec / ::matmul for Q4_K (type 12) and Q6_K (type 14): T rows of
 // X quantized to Q8_K, each output = the dot above (nm/src/quant_i8.hpp:352-383,430-474)
 void matmul_kquant(int type, const void* W, size_t N, size_t K, const float* X, size_t T, float* Y);
+// Q5_K has no integer-activation kernel (has_i8_kernel, nm/src/quant_i8.hpp:325):
+// the fp32-activation dequant-in-dot of one block (nm/src/quant.hpp:207-229)
+// and its row sum over blocks in order (nm/src/quant_i8.hpp:403-407)
+float dot_block_q5_K(const BlockQ5K& b, const float* x);
+void matmul_q5_K(const BlockQ5K* W, size_t N, size_t K, const float* X, size_t T, float* Y);
+// one row of a Q4_K (12) / Q5_K (13) / Q6_K (14) / Q8_0 (8) tensor as fp32
+// (dequant_to_f32, nm/src/quant.hpp:291-400)
+void dequant_row(int type, const void* row, float* out, size_t k);
+// bytes of one row of k elements of a ggml type (8, 12, 13, 14)
+size_t row_bytes(int type, size_t k);
 
 // ---- sampling (nm/src/logits.hpp:71-105) -----------------------------------------
 // Logits::sample with temp > 0, given u = the uniform draw the caller's RNG
@@ -151,11 +174,16 @@ struct Config {
     size_t conv_channels() const { return 2 * Hk * Dk + Hv * Dv; }
 };
 
-// A linear weight: Q8_0 blocks, row-major by output (N rows of K/32 blocks).
+// A linear weight as stored in the GGUF, row-major by output: N rows of K
+// elements of ggml type `type` (8 Q8_0, 12 Q4_K, 13 Q5_K, 14 Q6_K).
 struct Linear {
-    const BlockQ8* w = nullptr;
+    const void* w = nullptr;
+    int type = 8;
     size_t N = 0, K = 0;
 };
+// Weight::matmul (nm/src/quant_i8.hpp:415-495): the integer-activation form
+// for Q8_0 / Q4_K / Q6_K, the fp32-activation form for Q5_K
+void linear_rows(const Linear& lin, const float* X, size_t T, float* Y);
 
 struct Layer {
     std::vector<float> mixer_norm, channel_norm;  // [D]

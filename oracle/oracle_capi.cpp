@@ -70,6 +70,26 @@ float oracle_vec_dot_kquant(int type, const void* w, const void* x, size_t k) {
                       : vec_dot_q6_K_q8_K(k, static_cast<const BlockQ6K*>(w), static_cast<const BlockQ8K*>(x));
 }
 void oracle_matmul_kquant(int type, const void* W, size_t N, size_t K, const float* X, size_t T, float* Y) { matmul_kquant(type, W, N, K, X, T, Y); }
+float oracle_dot_block_q5_K(const void* block, const float* x) { return dot_block_q5_K(*static_cast<const BlockQ5K*>(block), x); }
+// any linear weight type (8, 12, 13, 14): the Weight::matmul the model calls
+int oracle_linear_rows(int type, const void* W, size_t N, size_t K, const float* X, size_t T, float* Y) {
+    try {
+        linear_rows(Linear{W, type, N, K}, X, T, Y);
+        return 0;
+    } catch (...) {
+        return 1;
+    }
+}
+// `rows` rows of a tensor of `type`, k elements each, dequantized to fp32
+int oracle_dequant_rows(int type, const void* W, size_t rows, size_t k, float* out) {
+    try {
+        const size_t rb = row_bytes(type, k);
+        for (size_t r = 0; r < rows; ++r) dequant_row(type, static_cast<const uint8_t*>(W) + r * rb, out + r * k, k);
+        return 0;
+    } catch (...) {
+        return 1;
+    }
+}
 void oracle_matvec_q8_0(const void* W, size_t N, size_t K, const float* x, float* y) { matvec_q8_0(static_cast<const BlockQ8*>(W), N, K, x, y); }
 void oracle_matmul_q8_0(const void* W, size_t N, size_t K, const float* X, size_t T, float* Y) { matmul_q8_0(static_cast<const BlockQ8*>(W), N, K, X, T, Y); }
 

@@ -62,10 +62,13 @@ size_t type_bytes(uint32_t type, uint64_t nelem) {
         case 0: return nelem * 4;            // F32
         case 1: return nelem * 2;            // F16
         case 8: return nelem / 32 * 34;      // Q8_0
-        default: throw std::runtime_error("GGUF: tensor type " + std::to_string(type) + " is not supported by this path (F32/F16/Q8_0)");
+        case 12: return nelem / 256 * 144;   // Q4_K
+        case 13: return nelem / 256 * 176;   // Q5_K
+        case 14: return nelem / 256 * 210;   // Q6_K
+        default: throw std::runtime_error("GGUF: tensor type " + std::to_string(type) + " is not supported by this path (F32/F16/Q8_0/Q4_K/Q5_K/Q6_K)");
     }
 }
-size_t type_block(uint32_t type) { return type == 8 ? 32 : 1; }
+size_t type_block(uint32_t type) { return type == 8 ? 32 : type >= 12 && type <= 14 ? 256 : 1; }
 }  // namespace
 
 void Gguf::parse(const uint8_t* base, size_t size) {
@@ -169,9 +172,10 @@ std::string blk(size_t l, const char* s) { return "blk." + std::to_string(l) + "
 Linear load_linear(const Gguf& g, const std::string& name, size_t in, size_t out) {
     const Gguf::Tensor& t = g.require(name);
     expect(t.dims.size() == 2 && t.dims[0] == in && t.dims[1] == out, name + " has the wrong shape");
-    expect(t.type == 8, name + " is not Q8_0");
-    expect(in % 32 == 0, name + " In not divisible by 32");
-    return Linear{reinterpret_cast<const BlockQ8*>(t.data), out, in};
+    // tensor_loader::load_weight (tensor_loader.hpp:17-35) for the quantized types
+    expect(t.type == 8 || t.type == 12 || t.type == 13 || t.type == 14, name + " is not Q8_0, Q4_K, Q5_K or Q6_K");
+    expect(in % type_block(t.type) == 0, name + " In not divisible by its block length");
+    return Linear{t.data, int(t.type), out, in};
 }
 
 std::vector<float> load_vector(const Gguf& g, const std::string& name, size_t n) {

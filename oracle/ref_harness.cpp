@@ -196,6 +196,23 @@ int run_kernels(const std::string& dir) {
         };
         run("kq_w4", GT::Q4_K, "kq_y4");
         run("kq_w6", GT::Q6_K, "kq_y6");
+        // Q5_K: no integer-activation kernel, so matvec / matmul take the
+        // fp32-activation dequant-in-dot form
+        run("kq_w5", GT::Q5_K, "kq_y5");
+        // Weight::dequant_row (the embedding gather) of rows 0 and 37
+        auto dequant = [&](const char* wname, GT type, const char* yname) {
+            auto raw = std::make_shared<std::vector<uint8_t>>(read_bin<uint8_t>(dir + "/" + wname + ".in.bin"));
+            const Weight<K, N> weight(type, raw->data(), raw);
+            std::vector<float> yy;
+            for (size_t row : {size_t(0), size_t(37)}) {
+                const Vec<K> r = weight.dequant_row(row);
+                yy.insert(yy.end(), r.p.get(), r.p.get() + K);
+            }
+            out(yname, yy);
+        };
+        dequant("kq_w4", GT::Q4_K, "kq_dq4");
+        dequant("kq_w5", GT::Q5_K, "kq_dq5");
+        dequant("kq_w6", GT::Q6_K, "kq_dq6");
     }
     {  // Logits<32000>::sample over 8 logit rows x 6 configurations; the
        // uniform draw it makes is recorded from a copy of the generator

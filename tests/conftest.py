@@ -98,3 +98,23 @@ def variant_gguf(tmp_path_factory, manifest):
     with open(path, "rb") as f:
         assert hashlib.sha256(f.read()).hexdigest() == t["gguf_sha256"], "synthetic variant model bytes changed"
     return path
+
+
+# the tiny shape with the tensor types of a Q4_K_M checkpoint (Q4_K, Q5_K, Q6_K
+# and Q8_0 tensors; the golden's model)
+@pytest.fixture(scope="session")
+def kmix_gguf(tmp_path_factory, manifest):
+    import hero_amd
+
+    t = manifest["tiny_kmix_model"]
+    path = str(tmp_path_factory.mktemp("kmix") / "tiny_kmix.gguf")
+    hero_amd.write_synthetic_gguf(path, hero_amd.TINY_CONFIG, seed=t["seed"], ctx=t["ctx"], tied=t["tied"],
+                                  weight_mix=t["weight_mix"])
+    with open(path, "rb") as f:
+        assert hashlib.sha256(f.read()).hexdigest() == t["gguf_sha256"], "synthetic K-quant model bytes changed"
+    return path
+
+
+@pytest.fixture(scope="session")
+def kmix_golden():
+    return dict(np.load(os.path.join(GOLDEN, "tiny_kmix_model.npz")))

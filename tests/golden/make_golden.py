@@ -15,14 +15,16 @@ so it runs in the build container only). This script:
      positions, probes before and after the ring starts evicting) -> window.npz;
   4. `variant`: the tiny shape with 4 delta-net key heads tiled over 8 value
      heads and an untied output.weight -> tiny_hk4u_model.npz;
-  5. `hybrid8b`: the ~8B shape (the benchmark's model, seed 20260101, a
+  5. `kmix`: the tiny shape with the tensor types of a Q4_K_M checkpoint
+     (Q4_K, Q5_K, Q6_K and Q8_0 tensors) -> tiny_kmix_model.npz;
+  6. `hybrid8b`: the ~8B shape (the benchmark's model, seed 20260101, a
      600-token prompt, 32 greedy passes) -> hybrid8b_model.npz with the ids,
      per-step top-5 and the sha256 of the prefill and last logit vectors.
 
 manifest.json records seeds, shapes, the GGUF's sha256 and the compiler
 flags (-O3 -march=x86-64-v3 -ffp-contract=off: no FMA contraction).
 
-Run:  python tests/golden/make_golden.py [kernels] [tiny] [window] [variant] [hybrid8b]
+Run:  python tests/golden/make_golden.py [kernels] [tiny] [window] [variant] [kmix] [hybrid8b]
       (no argument: all parts; the manifest keeps the entries of parts not rerun)
 """
 from __future__ import annotations
@@ -117,6 +119,11 @@ def kernel_inputs(rng: np.random.Generator) -> dict[str, np.ndarray]:
     inp["kq_w6"] = np.ascontiguousarray(w6.astype(np.uint8))
     # sampling: 8 rows of 32000 distinct logits at a few temperatures' scales
     inp["sample_logits"] = f32(rng.standard_normal((8, 32000)) * np.array([1, 2, 3, 4, 6, 8, 0.5, 12])[:, None])
+    # raw Q5_K weight blocks [64 rows][16 blocks] from random bytes (drawn last,
+    # so the inputs above keep their values)
+    w5 = np.concatenate([f16(rng.uniform(0.2, 2.0, nb) * 1e-2), f16(rng.uniform(0.0, 2.0, nb) * 1e-2),
+                         rng.integers(0, 256, (nb, 12 + 32 + 128)).astype(np.uint8)], axis=1)
+    inp["kq_w5"] = np.ascontiguousarray(w5.astype(np.uint8))
     return inp
 
 
@@ -126,6 +133,7 @@ OUTPUTS = {  # name -> dtype of the .out.bin
     "l2": np.float32, "silu": np.float32, "sigmoid": np.float32, "softplus": np.float32, "conv": np.float32,
     "delta_out": np.float32, "delta_state": np.float32, "rope": np.float32, "attn_scaled": np.float32, "attn_unit": np.float32,
     "kq_act": np.uint8, "kq_y4": np.float32, "kq_y6": np.float32, "sample": np.float32,
+    "kq_y5": np.float32, "kq_dq4": np.float32, "kq_dq5": np.float32, "kq_dq6": np.float32,
 }
 
 
@@ -212,11 +220,12 @@ HYBRID8B_PROMPT = 600
 HYBRID8B_STEPS = 32
 
 
-def run_model_case(tmp: str, cfg: str, shape, seed: int, ctx: int, tied: bool, prompt: np.ndarray, steps: int, where: str):
+def run_model_case(tmp: str, cfg: str, shape, seed: int, ctx: int, tied: bool, prompt: np.ndarray, steps: int, where: str,
+                   weight_mix: int = 0):
     import hero_amd
 
     gguf = os.path.join(where, f"{cfg}.gguf")
-    hero_amd.write_synthetic_gguf(gguf, shape, seed=seed, ctx=ctx, tied=tied)
+    hero_amd.write_synthetic_gguf(gguf, shape, seed=seed, ctx=ctx, tied=tied, weight_mix=weight_mix)
     h = hashlib.sha256()
     with open(gguf, "rb") as f:
         for chunk in iter(lambda: f.read(1 << 24), b""):
@@ -247,6 +256,25 @@ def make_variant(tmp: str) -> dict:
             "decode_steps": 32, "gguf_sha256": sha, "gguf_bytes": size, "reference_times": times}
 
 
+KMIX_SEED = 5150
+
+
+def make_kmix(tmp: str) -> dict:
+    import hero_amd
+
+    prompt = np.random.default_rng(KMIX_SEED + 1).integers(0, 32000, 16).astype(np.int32)
+    rd, sha, size, times = run_model_case(tmp, "tiny", hero_amd.TINY_CONFIG, KMIX_SEED, 4096, True, prompt, 32, tmp,
+                                          weight_mix=hero_amd.WEIGHTS_K_MIX)
+    np.savez_compressed(
+        os.path.join(HERE, "tiny_kmix_model.npz"), prompt=prompt, ids=rd("ids.i32", np.int32),
+        top5_ids=rd("top5_ids.i32", np.int32).reshape(-1, 5), top5_logits=rd("top5_logits.f32", np.float32).reshape(-1, 5),
+        logits_prefill=rd("logits_prefill.f32", np.float32), logits_last=rd("logits_last.f32", np.float32))
+    return {"seed": KMIX_SEED, "weight_mix": hero_amd.WEIGHTS_K_MIX, "tied": True, "ctx": 4096, "prompt_len": 16,
+            "decode_steps": 32, "gguf_sha256": sha, "gguf_bytes": size, "reference_times": times,
+            "types": "token_embd Q6_K; attn_qkv, attn_output Q5_K; ffn_down, attn_v Q6_K; ssm_alpha, ssm_beta Q8_0; "
+                     "other projections Q4_K"}
+
+
 def make_hybrid8b(tmp: str) -> dict:
     import hero_amd
 
@@ -264,9 +292,10 @@ def make_hybrid8b(tmp: str) -> dict:
             "logits_last_sha256": digest(rd("logits_last.f32", np.float32))}
 
 
-PARTS = {"kernels": make_kernels, "tiny": make_tiny, "window": make_window, "variant": make_variant, "hybrid8b": make_hybrid8b}
+PARTS = {"kernels": make_kernels, "tiny": make_tiny, "window": make_window, "variant": make_variant, "kmix": make_kmix,
+         "hybrid8b": make_hybrid8b}
 MANIFEST_KEYS = {"kernels": "kernels", "tiny": "tiny_model", "window": "window", "variant": "tiny_hk4u_model",
-                 "hybrid8b": "hybrid8b_model"}
+                 "kmix": "tiny_kmix_model", "hybrid8b": "hybrid8b_model"}
 
 
 def main():

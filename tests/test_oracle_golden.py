@@ -95,6 +95,57 @@ def test_kquant_dots_equal_dequantized_sums_in_exact_arithmetic(kernels_golden):
             assert abs(got - exact) <= 1e-5 * max(scale_sum, 1.0), (name, row, got, exact)
 
 
+def test_q5_K_fp32_matvec_and_matmul_match_reference(kernels_golden):
+    """Q5_K has no integer-activation kernel: Weight::matvec / ::matmul take the
+    fp32 dequant-in-dot form (nm/src/quant.hpp:207-229)"""
+    w = kernels_golden["in_kq_w5"]
+    x = kernels_golden["in_kq_x"].reshape(4, 4096)
+    expect = kernels_golden["out_kq_y5"].reshape(5, 64)
+    Y = oracle.linear(oracle.Q5_K, w, 64, 4096, x)
+    assert np.array_equal(bits(Y[0]), bits(expect[0]))
+    assert np.array_equal(bits(Y), bits(expect[1:]))
+
+
+@pytest.mark.parametrize("wtype,name", [(oracle.Q4_K, "kq_w4"), (oracle.Q5_K, "kq_w5"), (oracle.Q6_K, "kq_w6")])
+def test_kquant_dequant_rows_match_reference(kernels_golden, wtype, name):
+    """Weight::dequant_row (the embedding gather) of rows 0 and 37 of random-byte blocks"""
+    w = kernels_golden[f"in_{name}"].reshape(64, -1)
+    got = np.concatenate([oracle.dequant_rows(wtype, w[r], 1, 4096).ravel() for r in (0, 37)])
+    expect = kernels_golden["out_kq_dq" + {oracle.Q4_K: "4", oracle.Q5_K: "5", oracle.Q6_K: "6"}[wtype]]
+    assert np.array_equal(bits(got), bits(expect))
+
+
+def test_q5_K_dot_equals_dequantized_sum_in_float64(kernels_golden):
+    """Independent of the reference: the Q5_K fields decoded from ggml's layout
+    (fifth bit j of qh[l] for element l of sub-block j) against the oracle's
+    fp32 dot, to a rounding bound. A wrong qh bit, nibble or scale index moves
+    the result far outside it."""
+    x = kernels_golden["in_kq_x"].reshape(4, 4096)[3].astype(np.float64)
+    w = kernels_golden["in_kq_w5"].reshape(64, 16, 176)
+    f16 = lambda b: float(b.copy().view(np.float16)[0])  # noqa: E731
+    for row in range(0, 64, 7):
+        exact, mag, block0 = 0.0, 0.0, None
+        for b in range(16):
+            blk = w[row, b]
+            d, dmin = f16(blk[0:2]), f16(blk[2:4])
+            sb, qh, qs = blk[4:16].astype(np.int64), blk[16:48].astype(np.int64), blk[48:176].astype(np.int64)
+            for j in range(8):
+                sc = (sb[j] & 63) if j < 4 else ((sb[j + 4] & 15) | ((sb[j - 4] >> 6) << 4))
+                mn = (sb[j + 4] & 63) if j < 4 else ((sb[j + 4] >> 4) | ((sb[j] >> 6) << 4))
+                nib = qs[32 * (j // 2):32 * (j // 2) + 32]
+                q = (nib & 15 if j % 2 == 0 else nib >> 4) + ((qh >> j) & 1) * 16
+                wv = d * sc * q - dmin * mn
+                xs = x[256 * b + 32 * j:256 * b + 32 * j + 32]
+                exact += float((wv * xs).sum())
+                mag += float(np.abs(wv * xs).sum())
+            if b == 0:
+                block0 = (exact, mag)
+        got0 = float(oracle.dot_block_q5_K(w[row, 0], x[:256].astype(np.float32)))  # one block
+        assert abs(got0 - block0[0]) <= 4e-6 * block0[1], (row, got0, block0)
+        got = float(oracle.linear(oracle.Q5_K, w[row].ravel(), 1, 4096, x.astype(np.float32))[0, 0])  # the row
+        assert abs(got - exact) <= 4e-6 * mag, (row, got, exact, mag)
+
+
 SAMPLER_CFGS = [(0.7, 40, 0.9), (1.0, 1, 1.0), (1.3, 1000, 0.95), (0.5, 0, 1.0), (2.0, 200, 0.5), (0.9, 64, 0.0)]
 
 
@@ -315,4 +366,23 @@ def test_variant_model_matches_reference(variant_gguf, variant_golden):
         ids.append(oracle.argmax(last))
     assert np.array_equal(np.array(ids, np.int32), variant_golden["ids"])
     assert np.array_equal(bits(last), bits(variant_golden["logits_last"]))
+    m.close()
+
+
+# ---- K-quant tensors: the tensor types of a Q4_K_M checkpoint -----------------------
+def test_kquant_model_matches_reference(kmix_gguf, kmix_golden):
+    """The tiny shape with a Q6_K embedding (the tied head), Q5_K attn_qkv and
+    attn_output (fp32-activation dots), Q6_K ffn_down and attn_v, Q8_0
+    ssm_alpha / ssm_beta and Q4_K elsewhere: the oracle's greedy ids and its
+    prefill / last logits equal the reference's bit for bit."""
+    m = oracle.Model(path=kmix_gguf)
+    prompt = kmix_golden["prompt"]
+    prefill = m.forward_ids(prompt)
+    assert np.array_equal(bits(prefill), bits(kmix_golden["logits_prefill"]))
+    ids = [oracle.argmax(prefill)]
+    for _ in range(len(kmix_golden["ids"]) - 1):
+        last = m.forward_ids([ids[-1]])
+        ids.append(oracle.argmax(last))
+    assert np.array_equal(np.array(ids, np.int32), kmix_golden["ids"])
+    assert np.array_equal(bits(last), bits(kmix_golden["logits_last"]))
     m.close()

@@ -102,6 +102,10 @@ SIGNATURES = {
     "hero_q8_K_act_bytes": (c_int64, [c_int64, c_int64]),
     "hero_q8_K_quantize": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "hero_kquant_gemm": (c_int, [c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p]),
+    "hero_kquant_packed_bytes": (c_int64, [c_int32, c_int64, c_int64]),
+    "hero_kquant_pack": (c_int, [c_int32, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
+    "hero_q5_K_gemm": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p]),
+    "hero_kquant_dequant_rows": (c_int, [c_int32, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
     "hero_gdn_decode": (c_int, [POINTER(GdnDecodeArgs), c_void_p]),
     "hero_gdn_decode_cols": (c_int, [POINTER(GdnDecodeArgs), c_void_p, c_void_p, c_void_p]),
     "hero_gdn_norm_gate": (c_int, [c_void_p, POINTER(GdnDecodeArgs), c_void_p]),

@@ -25,12 +25,23 @@ int device_cus();  // compute units of the current device (cached per device)
 __host__ __device__ inline int64_t scale_index(int64_t row, int64_t block, int64_t nb) { return ((row >> 3) * nb + block) * 8 + (row & 7); }
 inline int64_t packed_q8_bytes(int64_t N, int64_t K) { return N * K + packed_rows_pad(N) * (K / 32) * 2; }
 inline int64_t act_q8_bytes(int64_t M, int64_t K) { return M * K + M * (K / 32) * 4; }
-// K-quants (kquant.hip): Q8_K activations (292 bytes per 256) and the Q4_K
-// (type 12) / Q6_K (type 14) products over GGUF-layout weights
+// K-quants (kquant.hip): Q8_K activations (292 bytes per 256 plus the
+// residue-regrouped int8), the Q4_K (type 12) / Q6_K (type 14) products over
+// packed weights, the Q5_K (type 13) product over fp32 rows, and the
+// embedding gather. Packed: Q4_K / Q6_K residue-regrouped (launch_kquant_pack),
+// Q5_K as in the GGUF; the same bytes as the GGUF tensor.
 int64_t act_q8_K_bytes(int64_t m, int64_t k);
-int kquant_rows_per_group(int type, int64_t K);  // output rows per workgroup (0: K too large)
+int64_t kquant_packed_bytes(int type, int64_t N, int64_t K);
+int kquant_max_k(int type);  // 65536 (Q4_K, Q6_K), 16384 (Q5_K)
+void launch_kquant_pack(int type, const void* gguf, void* packed, int64_t N, int64_t K, hipStream_t s);
 void launch_quantize_q8_K(const float* x, void* act, int64_t M, int64_t K, hipStream_t s);
+// y[m * ldy + n] (+= resid[m * ldy + n], added after the product)
+void launch_kquant_gemm_ld(int type, const void* w, const void* act, float* y, const float* resid, int64_t M, int64_t N, int64_t K, int64_t ldy,
+                           hipStream_t s);
 void launch_kquant_gemm(int type, const void* w, const void* act, float* y, int64_t M, int64_t N, int64_t K, hipStream_t s);
+void launch_q5k_gemm(const void* w, const float* x, int64_t ldx, float* y, const float* resid, int64_t M, int64_t N, int64_t K, int64_t ldy, hipStream_t s);
+// out[t][K] = row ids[t] of a packed K-quant tensor [N][K] as fp32
+void launch_kquant_dequant_rows(int type, const void* w, int64_t N, int64_t K, const int32_t* ids, int64_t n, float* out, hipStream_t s);
 // top-k / top-p sampling of one logits row (sample.hip); top_k in 1 .. sample_max_top_k()
 int sample_max_top_k();
 void launch_sample_topk(const float* logits, int64_t V, int top_k, float temp, float top_p, float u, int32_t* out, hipStream_t s);
@@ -70,6 +81,8 @@ void launch_rmsnorm_quant(const float* x, const float* gamma, float eps, float* 
 // gate_up rows [M][2FF]: gate then up, or with interleave > 0 alternating
 // chunks [gate il | up il | gate il | ...]
 void launch_swiglu_quant(const float* gate_up, void* act, int64_t M, int64_t FF, hipStream_t s, int64_t interleave = 0);
+// the same products as fp32 rows y [M][FF] (gate_up [M][gate FF | up FF])
+void launch_swiglu_f32(const float* gate_up, float* y, int64_t M, int64_t FF, hipStream_t s);
 void launch_embed_q8(const void* packed_embedding, int64_t V, int64_t D, const int32_t* ids, int64_t n, float* out, hipStream_t s);
 // argmax over n logits per row (ties -> lowest index); out_index[M]
 void launch_argmax(const float* logits, int64_t M, int64_t n, int32_t* out_index, uint64_t* scratch_keys, hipStream_t s);

@@ -24,6 +24,7 @@
 namespace hero {
 
 class GgufFile;
+struct WeightPacker;
 
 struct ModelConfig {
     int64_t V = 0, D = 0, L = 0, CTX = 0;
@@ -64,6 +65,14 @@ private:
     size_t bytes_ = 0;
 };
 
+// One linear weight of a model with K-quant tensors, kept in the tensor's
+// own type: packed Q8_0 (type 8), packed Q4_K (12) / Q6_K (14), or Q5_K (13).
+struct TypedLinear {
+    DeviceBuffer w;
+    int type = 8;
+    int64_t N = 0, K = 0;
+};
+
 struct LayerWeights {
     bool recurrent = true;
     DeviceBuffer mixer_norm, channel_norm;  // [D] fp32
@@ -78,6 +87,12 @@ struct LayerWeights {
     // attention: w_in rows = [q|gate pairs 2*Hq*Dh | k Hkv*Dh | v Hkv*Dh]
     DeviceBuffer q_norm, k_norm;
     int64_t k_off = 0, v_off = 0;
+    // K-quant models: every linear in its own type (the packed Q8_0 buffers
+    // above stay empty). tin[i] writes proj columns [tin_off[i], + tin[i].N):
+    // recurrent qkv, z, beta, alpha; attention q|gate, k, v
+    std::vector<TypedLinear> tin;
+    std::vector<int64_t> tin_off;
+    TypedLinear tout, tgate, tup, tdown;
 };
 
 class Qwen35Model {
@@ -114,6 +129,9 @@ public:
     // position: first_ids[B]; out_ids[steps][B]; logits [B][V] of the last pass
     void decode_batch(State& s, const int32_t* first_ids, int64_t steps, int32_t* out_ids, float* logits) const;
     double last_decode_seconds() const { return last_decode_seconds_; }
+    // true when some linear weight is not Q8_0 (Q4_K / Q5_K / Q6_K): every
+    // linear then runs in its own type, one product per tensor
+    bool typed() const { return typed_; }
     // Every Q8_0 matvec of one decode step (all layers + LM head), `reps`
     // times back to back, between two events on the model's stream.
     // Returns seconds; *launches and *bytes are per repetition (algorithmic
@@ -123,6 +141,7 @@ public:
 private:
     Qwen35Model() = default;
     void load(const GgufFile& g);
+    void load_typed(const GgufFile& g, WeightPacker& pk);
     void build_rope_table(int64_t positions);
     // one token at the state's device position; `with_head` adds the final
     // norm, LM head and argmax (the reference computes logits for the last row only)
@@ -141,6 +160,18 @@ private:
     // rows per prefill chunk: at most 512, and the chunk's attention scores
     // (rows x query heads x max_tokens fp32) within 256 MiB
     int64_t chunk_rows(const State& s) const;
+    // ---- models with K-quant tensors ----
+    struct TypedScratch;
+    // y[m * ldy + n] (+ resid, same stride) = the M fp32 rows x [M][K] times
+    // W^T, in the reference's arithmetic for W's type
+    void typed_linear(const TypedLinear& w, const float* x, int64_t M, float* y, int64_t ldy, const float* resid, TypedScratch& ts,
+                      hipStream_t s) const;
+    // the layers over M rows in x: one token of one sequence (chunk = false,
+    // position positions[0]) or M consecutive tokens of sequence `seq` (chunk)
+    void typed_layers(State& st, TypedScratch& ts, float* x, float* h, float* proj, float* gate_up, int64_t M, const int32_t* positions, int64_t seq,
+                      bool chunk, hipStream_t s) const;
+    void typed_head(State& st, TypedScratch& ts, const float* x_last, hipStream_t s) const;
+    void embed_rows(const int32_t* ids, int64_t n, float* out, hipStream_t s) const;
 
     ModelConfig c_;
     std::vector<LayerWeights> layers_;
@@ -148,6 +179,8 @@ private:
     // d_model 4096: gate and up packed in alternating 32-row chunks, so the
     // gate/up GEMV ends in SwiGLU and writes the down projection's input
     bool ffn_fused_ = false;
+    bool typed_ = false;
+    TypedLinear t_embedding_, t_output_;  // typed models; t_output_ empty when tied
     int64_t rope_positions_ = 0;
     int64_t device_bytes_ = 0;
     hipStream_t stream_ = nullptr;
@@ -194,6 +227,9 @@ private:
     void ensure_chunk(int64_t rows);
     // per layer, every sequence's: [B][...]
     std::vector<DeviceBuffer> k_cache_, v_cache_, scores_, conv_hist_, delta_;
+    // models with K-quant tensors: fp32 intermediates and activation scratch
+    // of a decode step and of a prefill chunk
+    std::unique_ptr<TypedScratch> tstep_, tchunk_;
     hipGraphExec_t graph_ = nullptr;  // one greedy decode step, replayed
 };
 

@@ -81,16 +81,61 @@ int hero_q8_K_quantize(const float* x, void* act, int64_t m, int64_t k, void* st
     });
 }
 
+namespace {
+void check_kquant_shape(int32_t type, int64_t n, int64_t k) {
+    require(n > 0 && k > 0 && k % 256 == 0, "K must be a positive multiple of 256 (K-quant super-block)");
+    require(k <= kquant_max_k(type) && n <= (int64_t(1) << 31) && n * (k / 256) <= (int64_t(1) << 31), "shape too large");
+}
+}  // namespace
+
+int64_t hero_kquant_packed_bytes(int32_t type, int64_t n, int64_t k) {
+    if (!(type == 12 || type == 13 || type == 14) || n <= 0 || k <= 0 || k % 256 != 0) return -1;
+    return kquant_packed_bytes(type, n, k);
+}
+
+int hero_kquant_pack(int32_t type, const void* gguf, void* packed, int64_t n, int64_t k, void* stream) {
+    return guard([&] {
+        require(type == 12 || type == 13 || type == 14, "type must be 12 (Q4_K), 13 (Q5_K) or 14 (Q6_K)");
+        check_kquant_shape(type, n, k);
+        require(gguf && packed, "null pointer");
+        require(aligned(packed, 16), "packed must be 16-byte aligned");
+        require(gguf != packed, "the packed copy cannot overwrite its source");
+        launch_kquant_pack(type, gguf, packed, n, k, as_stream(stream));
+        check_launch("hero_kquant_pack");
+    });
+}
+
 int hero_kquant_gemm(int32_t type, const void* w, const void* act, float* y, int64_t m, int64_t n, int64_t k, void* stream) {
     return guard([&] {
         require(type == 12 || type == 14, "type must be 12 (Q4_K) or 14 (Q6_K)");
-        require(m > 0 && n > 0 && k > 0 && k % 256 == 0, "K must be a positive multiple of 256 (K-quant super-block)");
-        require(k <= 65536 && m <= 65535 && n <= (int64_t(1) << 31), "shape too large");
+        check_kquant_shape(type, n, k);
+        require(m > 0 && m <= (int64_t(1) << 31) / (k / 256), "m out of range");
         require(w && act && y, "null pointer");
         require(aligned(w, 16) && aligned(act, 16) && aligned(y, 4), "w and act must be 16-byte aligned");
-        require(kquant_rows_per_group(type, k) > 0, "K too large for one workgroup's rows");
         launch_kquant_gemm(type, w, act, y, m, n, k, as_stream(stream));
         check_launch("hero_kquant_gemm");
+    });
+}
+
+int hero_q5_K_gemm(const void* w, const float* x, float* y, int64_t m, int64_t n, int64_t k, void* stream) {
+    return guard([&] {
+        check_kquant_shape(13, n, k);
+        require(m > 0 && m <= (int64_t(1) << 31) / (k / 256), "m out of range");
+        require(w && x && y, "null pointer");
+        require(aligned(w, 16) && aligned(x, 16) && aligned(y, 4), "w and x must be 16-byte aligned");
+        launch_q5k_gemm(w, x, k, y, nullptr, m, n, k, n, as_stream(stream));
+        check_launch("hero_q5_K_gemm");
+    });
+}
+
+int hero_kquant_dequant_rows(int32_t type, const void* w, int64_t n, int64_t k, const int32_t* ids, int64_t n_ids, float* out, void* stream) {
+    return guard([&] {
+        require(type == 12 || type == 13 || type == 14, "type must be 12 (Q4_K), 13 (Q5_K) or 14 (Q6_K)");
+        check_kquant_shape(type, n, k);
+        require(n_ids > 0 && n_ids <= 65535, "n_ids out of range");
+        require(w && ids && out, "null pointer");
+        launch_kquant_dequant_rows(type, w, n, k, ids, n_ids, out, as_stream(stream));
+        check_launch("hero_kquant_dequant_rows");
     });
 }
 

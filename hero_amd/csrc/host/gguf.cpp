@@ -58,7 +58,12 @@ uint64_t tensor_bytes(uint32_t type, uint64_t n, const std::string& name) {
         case 8:
             if (n % 32) fail("tensor '" + name + "' has a partial quant block");
             return n / 32 * 34;
-        default: fail("tensor '" + name + "' has ggml type " + std::to_string(type) + "; this path reads F32, F16 and Q8_0");
+        case 12:  // Q4_K, Q5_K, Q6_K: super-blocks of 256 (nm/src/quant.hpp:52-86)
+        case 13:
+        case 14:
+            if (n % 256) fail("tensor '" + name + "' has a partial quant block");
+            return n / 256 * (type == 12 ? 144 : type == 13 ? 176 : 210);
+        default: fail("tensor '" + name + "' has ggml type " + std::to_string(type) + "; this path reads F32, F16, Q8_0, Q4_K, Q5_K and Q6_K");
     }
 }
 }  // namespace

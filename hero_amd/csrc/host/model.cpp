@@ -112,7 +112,9 @@ DeviceBuffer upload(const std::vector<float>& v) {
     return b;
 }
 
-struct Packer {
+}  // namespace
+
+struct WeightPacker {
     DeviceBuffer staging;
     hipStream_t stream;
     int64_t* counter;
@@ -134,7 +136,60 @@ struct Packer {
         *counter += packed_q8_bytes(n, K);
         return DeviceBuffer(size_t(packed_q8_bytes(n, K)));
     }
+    // one linear weight in its own type: Q8_0 packed as above, Q4_K / Q6_K
+    // regrouped (launch_kquant_pack), Q5_K as stored
+    TypedLinear typed(const GgufFile& g, const std::string& name, int64_t K, int64_t N) {
+        const GgufFile::Tensor& t = g.require(name);
+        expect(t.dims.size() == 2 && int64_t(t.dims[0]) == K && int64_t(t.dims[1]) == N, name + " has the wrong shape");
+        TypedLinear L;
+        L.type = int(t.type);
+        L.N = N;
+        L.K = K;
+        if (t.type == 8) {
+            expect(K % 32 == 0, name + ": In not divisible by the Q8_0 block length");
+            L.w = alloc(N, K);
+            put(g, name, L.w, N, K, 0, N);
+            return L;
+        }
+        expect(t.type == 12 || t.type == 13 || t.type == 14, name + " has ggml type " + std::to_string(t.type) + "; this build runs Q8_0, Q4_K, Q5_K and Q6_K weights");
+        expect(K % 256 == 0, name + ": In not divisible by the K-quant block length");
+        expect(K <= kquant_max_k(L.type), name + ": In too large for this type");
+        if (staging.bytes() < t.nbytes) {
+            hip_check(hipStreamSynchronize(stream), "pack sync");
+            staging = DeviceBuffer(t.nbytes);
+        }
+        hip_check(hipStreamSynchronize(stream), "pack sync");
+        hip_check(hipMemcpy(staging.get(), t.data, t.nbytes, hipMemcpyHostToDevice), "weight upload");
+        const int64_t bytes = kquant_packed_bytes(L.type, N, K);
+        L.w = DeviceBuffer(size_t(bytes));
+        *counter += bytes;
+        launch_kquant_pack(L.type, staging.get(), L.w.get(), N, K, stream);
+        check_launch("pack");
+        return L;
+    }
 };
+
+namespace {
+
+// The linear weights of a layer, by GGUF name, with their (In, Out).
+std::vector<std::pair<std::string, std::pair<int64_t, int64_t>>> layer_linears(const ModelConfig& c, int64_t l) {
+    const int64_t CC = c.conv_channels(), VW = c.v_width(), QW = c.q_width(), KW = c.kv_width();
+    std::vector<std::pair<std::string, std::pair<int64_t, int64_t>>> v = {
+        {blk(l, "ffn_gate.weight"), {c.D, c.FF}}, {blk(l, "ffn_up.weight"), {c.D, c.FF}}, {blk(l, "ffn_down.weight"), {c.FF, c.D}}};
+    if (c.is_recurrent(l)) {
+        v.push_back({blk(l, "attn_qkv.weight"), {c.D, CC}});
+        v.push_back({blk(l, "attn_gate.weight"), {c.D, VW}});
+        v.push_back({blk(l, "ssm_beta.weight"), {c.D, c.Hv}});
+        v.push_back({blk(l, "ssm_alpha.weight"), {c.D, c.Hv}});
+        v.push_back({blk(l, "ssm_out.weight"), {VW, c.D}});
+    } else {
+        v.push_back({blk(l, "attn_q.weight"), {c.D, 2 * QW}});
+        v.push_back({blk(l, "attn_k.weight"), {c.D, KW}});
+        v.push_back({blk(l, "attn_v.weight"), {c.D, KW}});
+        v.push_back({blk(l, "attn_output.weight"), {QW, c.D}});
+    }
+    return v;
+}
 
 }  // namespace
 
@@ -207,7 +262,18 @@ void Qwen35Model::load(const GgufFile& g) {
     hip_check(hipEventCreate(&ev_start_), "event");
     hip_check(hipEventCreate(&ev_stop_), "event");
 
-    Packer pk{DeviceBuffer(), stream_, &device_bytes_};
+    WeightPacker pk{DeviceBuffer(), stream_, &device_bytes_};
+    // any linear weight not in Q8_0: every linear runs in its own type
+    auto type_of = [&](const std::string& name) { return g.require(name).type; };
+    typed_ = type_of("token_embd.weight") != 8 || (!c.tied && type_of("output.weight") != 8);
+    for (int64_t l = 0; l < c.L && !typed_; ++l)
+        for (const auto& lin : layer_linears(c, l)) typed_ = typed_ || type_of(lin.first) != 8;
+    if (typed_) {
+        load_typed(g, pk);
+        hip_check(hipStreamSynchronize(stream_), "load sync");
+        build_rope_table(std::min<int64_t>(c.CTX, 65536));
+        return;
+    }
     embedding_ = pk.alloc(c.V, c.D);
     pk.put(g, "token_embd.weight", embedding_, c.V, c.D, 0, c.V);
     if (!c.tied) {
@@ -275,6 +341,61 @@ void Qwen35Model::load(const GgufFile& g) {
     build_rope_table(std::min<int64_t>(c.CTX, 65536));
 }
 
+// The same schema as load() with every linear kept in its own type
+// (tensor_loader::load_weight, nm/src/tensor_loader.hpp:17-35).
+void Qwen35Model::load_typed(const GgufFile& g, WeightPacker& pk) {
+    const ModelConfig& c = c_;
+    expect(c.D % 256 == 0, "embedding_length must be a multiple of 256");
+    t_embedding_ = pk.typed(g, "token_embd.weight", c.D, c.V);
+    if (!c.tied) t_output_ = pk.typed(g, "output.weight", c.D, c.V);
+    final_norm_ = upload(host_vector(g, "output_norm.weight", c.D));
+    const int64_t CC = c.conv_channels(), VW = c.v_width(), QW = c.q_width(), KW = c.kv_width();
+    for (int64_t l = 0; l < c.L; ++l) {
+        LayerWeights L;
+        L.recurrent = c.is_recurrent(l);
+        L.mixer_norm = upload(host_vector(g, blk(l, "attn_norm.weight"), c.D));
+        L.channel_norm = upload(host_vector(g, blk(l, "post_attention_norm.weight"), c.D));
+        L.tgate = pk.typed(g, blk(l, "ffn_gate.weight"), c.D, c.FF);
+        L.tup = pk.typed(g, blk(l, "ffn_up.weight"), c.D, c.FF);
+        L.tdown = pk.typed(g, blk(l, "ffn_down.weight"), c.FF, c.D);
+        if (L.recurrent) {
+            L.n_in = CC + VW + 2 * c.Hv;
+            L.z_off = CC;
+            L.beta_off = CC + VW;
+            L.alpha_off = CC + VW + c.Hv;
+            L.tin.push_back(pk.typed(g, blk(l, "attn_qkv.weight"), c.D, CC));
+            L.tin.push_back(pk.typed(g, blk(l, "attn_gate.weight"), c.D, VW));
+            L.tin.push_back(pk.typed(g, blk(l, "ssm_beta.weight"), c.D, c.Hv));
+            L.tin.push_back(pk.typed(g, blk(l, "ssm_alpha.weight"), c.D, c.Hv));
+            L.tin_off = {0, L.z_off, L.beta_off, L.alpha_off};
+            L.tout = pk.typed(g, blk(l, "ssm_out.weight"), VW, c.D);
+            const GgufFile::Tensor& conv = g.require(blk(l, "ssm_conv1d.weight"));
+            expect(conv.dims.size() == 2 && int64_t(conv.dims[0]) == c.W && int64_t(conv.dims[1]) == CC, blk(l, "ssm_conv1d.weight") + " has the wrong shape");
+            L.conv = upload(host_vector(g, blk(l, "ssm_conv1d.weight"), CC * c.W));
+            L.dt_bias = upload(host_vector(g, blk(l, "ssm_dt.bias"), c.Hv));
+            std::vector<float> a = host_vector(g, blk(l, "ssm_a"), c.Hv);
+            for (float& x : a) {  // nm/src/qwen35_loader.hpp:108-119
+                if (x > 0.f) x = -std::exp(x);
+                expect(x <= 0.f, blk(l, "ssm_a") + ": decay scale must be <= 0 (-exp(A_log))");
+            }
+            L.decay = upload(a);
+            L.ssm_norm = upload(host_vector(g, blk(l, "ssm_norm.weight"), c.Dv));
+        } else {
+            L.n_in = 2 * QW + 2 * KW;
+            L.k_off = 2 * QW;
+            L.v_off = 2 * QW + KW;
+            L.tin.push_back(pk.typed(g, blk(l, "attn_q.weight"), c.D, 2 * QW));
+            L.tin.push_back(pk.typed(g, blk(l, "attn_k.weight"), c.D, KW));
+            L.tin.push_back(pk.typed(g, blk(l, "attn_v.weight"), c.D, KW));
+            L.tin_off = {0, L.k_off, L.v_off};
+            L.tout = pk.typed(g, blk(l, "attn_output.weight"), QW, c.D);
+            L.q_norm = upload(host_vector(g, blk(l, "attn_q_norm.weight"), c.Dh));
+            L.k_norm = upload(host_vector(g, blk(l, "attn_k_norm.weight"), c.Dh));
+        }
+        layers_.push_back(std::move(L));
+    }
+}
+
 // cos/sin per (position, plane) with the reference's float expressions
 // (nm/src/attention.hpp:76-91): inv_freq = float(pow(double base, -2i/Dh)) for
 // the rotary planes and 0 otherwise; angle = float(pos) * inv_freq.
@@ -326,6 +447,7 @@ Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batc
     o_raw_ = DeviceBuffer(size_t(B * c.v_width()) * 4);
     g_raw_ = DeviceBuffer(size_t(B * c.v_width()) * 4);
     out_ids_capacity_ = max_tokens;
+    if (m.typed_) tstep_ = std::make_unique<TypedScratch>(m, B);
     for (int64_t l = 0; l < c.L; ++l) {
         if (c.is_recurrent(l)) {
             k_cache_.emplace_back();
@@ -409,6 +531,7 @@ void Qwen35Model::State::ensure_chunk(int64_t rows) {
     cpos_ = DeviceBuffer(size_t(rows) * 4);
     cids_ = DeviceBuffer(size_t(rows) * 4);
     cgdn_work_ = DeviceBuffer(size_t(gdn_prefill_work_bytes(rows, c.Hk, c.Hv)));
+    if (m_.typed_) tchunk_ = std::make_unique<TypedScratch>(m_, rows);
     if (kv_fp16_) {
         int split = 0, nsplit = 0;
         attn_paged_plan(max_pages_ * kPageTokens, 0, int(rows), int(c.Hkv), &split, &nsplit);
@@ -478,6 +601,168 @@ void Qwen35Model::attention(State& st, size_t layer, AttnDecodeArgs a, const int
     launch_attn_paged(p, s);
 }
 
+// ---- models with K-quant tensors -------------------------------------------------------
+// fp32 intermediates of `rows` rows and the activation scratch of each type;
+// k_for / q_for remember which input rows the Q8_K / Q8_0 scratch holds, so
+// linears sharing an input quantize it once (new_input() forgets)
+struct Qwen35Model::TypedScratch {
+    int64_t rows = 0;
+    DeviceBuffer xn, mix, ff, kact, qact, qtmp, act_mix;
+    const float* k_for = nullptr;
+    const float* q_for = nullptr;
+    int64_t k_rows = 0, k_k = 0, q_rows = 0, q_k = 0;
+    void new_input() { k_for = q_for = nullptr; }
+    TypedScratch(const Qwen35Model& m, int64_t n) : rows(n) {
+        const ModelConfig& c = m.c_;
+        const int64_t kmax = std::max({c.D, c.FF, c.q_width(), c.v_width()});
+        int64_t nmax = 0;
+        for (const LayerWeights& L : m.layers_)
+            for (const TypedLinear& t : L.tin) nmax = std::max(nmax, t.N);
+        xn = DeviceBuffer(size_t(n * c.D) * 4);
+        mix = DeviceBuffer(size_t(n * std::max(c.q_width(), c.v_width())) * 4);
+        ff = DeviceBuffer(size_t(n * c.FF) * 4);
+        kact = DeviceBuffer(size_t(act_q8_K_bytes(n, (kmax + 255) / 256 * 256)));
+        qact = DeviceBuffer(size_t(act_q8_bytes(n, kmax)));
+        qtmp = DeviceBuffer(size_t(n * nmax) * 4);
+        act_mix = DeviceBuffer(size_t(act_q8_bytes(n, std::max(c.q_width(), c.v_width()))));
+    }
+};
+
+void Qwen35Model::typed_linear(const TypedLinear& w, const float* x, int64_t M, float* y, int64_t ldy, const float* resid, TypedScratch& ts,
+                               hipStream_t s) const {
+    const int64_t N = w.N, K = w.K;
+    if (w.type == 13) {  // Q5_K: fp32 activations (quant_i8.hpp:325)
+        launch_q5k_gemm(w.w.get(), x, K, y, resid, M, N, K, ldy, s);
+        return;
+    }
+    if (w.type == 12 || w.type == 14) {  // Q8_K activations (quant_i8.hpp:332-336)
+        if (ts.k_for != x || ts.k_rows != M || ts.k_k != K) {
+            launch_quantize_q8_K(x, ts.kact.get(), M, K, s);
+            ts.k_for = x, ts.k_rows = M, ts.k_k = K;
+        }
+        launch_kquant_gemm_ld(w.type, w.w.get(), ts.kact.get(), y, resid, M, N, K, ldy, s);
+        return;
+    }
+    // Q8_0 (quant_i8.hpp:338-339)
+    if (ts.q_for != x || ts.q_rows != M || ts.q_k != K) {
+        launch_quantize_act(x, ts.qact.get(), M, K, s);
+        ts.q_for = x, ts.q_rows = M, ts.q_k = K;
+    }
+    const int epi = resid ? kEpiResidual : kEpiStore;
+    if (ldy == N) {
+        if (M == 1)
+            launch_gemv_q8(w.w.get(), ts.qact.get(), y, resid, N, K, epi, s);
+        else
+            launch_gemm_q8(w.w.get(), ts.qact.get(), y, resid, M, N, K, epi, s);
+        return;
+    }
+    if (resid) throw Error(HERO_EINVAL, "typed_linear: a strided Q8_0 output takes no residual");
+    float* tmp = ts.qtmp.get<float>();
+    if (M == 1)
+        launch_gemv_q8(w.w.get(), ts.qact.get(), tmp, nullptr, N, K, kEpiStore, s);
+    else
+        launch_gemm_q8(w.w.get(), ts.qact.get(), tmp, nullptr, M, N, K, kEpiStore, s);
+    hip_check(hipMemcpy2DAsync(y, size_t(ldy) * 4, tmp, size_t(N) * 4, size_t(N) * 4, size_t(M), hipMemcpyDeviceToDevice, s), "strided copy");
+}
+
+// nm/src/qwen35.hpp:318-327 for every layer, each linear in its own type:
+// U = rms(X); mix(U) from its input projections; H = X + W_o mix;
+// Z = rms(H); X' = H + W_down (silu(W_gate Z) * W_up Z)
+void Qwen35Model::typed_layers(State& st, TypedScratch& ts, float* x, float* h, float* proj, float* gate_up, int64_t M, const int32_t* positions,
+                               int64_t seq, bool chunk, hipStream_t s) const {
+    const ModelConfig& c = c_;
+    float* xn = ts.xn.get<float>();
+    float* mix = ts.mix.get<float>();
+    for (int64_t l = 0; l < c.L; ++l) {
+        const LayerWeights& L = layers_[size_t(l)];
+        launch_rmsnorm_quant(x, L.mixer_norm.get<float>(), c.eps, xn, nullptr, M, c.D, s);
+        ts.new_input();
+        for (size_t i = 0; i < L.tin.size(); ++i) typed_linear(L.tin[i], xn, M, proj + L.tin_off[i], L.n_in, nullptr, ts, s);
+        if (L.recurrent) {
+            GdnDecodeArgs a{};
+            a.proj = proj;
+            a.proj_stride = L.n_in;
+            a.z_off = L.z_off;
+            a.beta_off = L.beta_off;
+            a.alpha_off = L.alpha_off;
+            a.conv_taps = L.conv.get<float>();
+            a.conv_hist = st.conv_hist_[size_t(l)].get<float>() + seq * c.W * c.conv_channels();
+            a.state = st.delta_[size_t(l)].get<float>() + seq * c.Hv * c.Dk * c.Dv;
+            a.dt_bias = L.dt_bias.get<float>();
+            a.decay = L.decay.get<float>();
+            a.norm_gamma = L.ssm_norm.get<float>();
+            a.eps = c.eps;
+            a.positions = positions;
+            a.act_out = ts.act_mix.get();  // the kernels' Q8_0 copy, unused here
+            a.out_f32 = mix;
+            a.B = int(M);
+            a.Hk = int(c.Hk);
+            a.Hv = int(c.Hv);
+            a.Dk = int(c.Dk);
+            a.Dv = int(c.Dv);
+            a.W = int(c.W);
+            if (chunk)
+                launch_gdn_prefill(a, st.cgdn_work_.get(), s, st.gdn_chunked_);
+            else
+                launch_gdn_decode(a, s);
+        } else {
+            AttnDecodeArgs a{};
+            a.proj = proj;
+            a.proj_stride = L.n_in;
+            a.k_off = L.k_off;
+            a.v_off = L.v_off;
+            a.q_gamma = L.q_norm.get<float>();
+            a.k_gamma = L.k_norm.get<float>();
+            a.eps = c.eps;
+            a.rope_cs = rope_cs_.get<float>();
+            if (!st.kv_fp16_) {
+                a.k_cache = st.k_cache_[size_t(l)].get<float>() + seq * st.max_tokens_ * c.kv_width();
+                a.v_cache = st.v_cache_[size_t(l)].get<float>() + seq * st.max_tokens_ * c.kv_width();
+            }
+            a.max_ctx = st.max_tokens_;
+            a.positions = positions;
+            a.shared_cache = chunk ? 1 : 0;
+            a.scores = chunk ? st.cscores_.get<float>() : st.scores_[size_t(l)].get<float>() + seq * st.max_tokens_ * c.Hq;
+            a.q_rot = chunk ? st.cq_rot_.get<float>() : st.q_rot_.get<float>();
+            a.score_scale = 1.f / std::sqrt(float(c.Dh));  // qwen35.hpp:359
+            a.window = 0;
+            a.act_out = ts.act_mix.get();
+            a.out_f32 = mix;
+            a.B = int(M);
+            a.Hq = int(c.Hq);
+            a.Hkv = int(c.Hkv);
+            a.Dh = int(c.Dh);
+            attention(st, size_t(l), a, st.page_table_.get<int32_t>() + seq * st.max_pages_, chunk ? st.cattn_work_.get<float>() : st.attn_work_.get<float>(), s);
+        }
+        ts.new_input();
+        typed_linear(L.tout, mix, M, h, c.D, x, ts, s);
+        launch_rmsnorm_quant(h, L.channel_norm.get<float>(), c.eps, xn, nullptr, M, c.D, s);
+        ts.new_input();
+        typed_linear(L.tgate, xn, M, gate_up, 2 * c.FF, nullptr, ts, s);
+        typed_linear(L.tup, xn, M, gate_up + c.FF, 2 * c.FF, nullptr, ts, s);
+        launch_swiglu_f32(gate_up, ts.ff.get<float>(), M, c.FF, s);
+        ts.new_input();
+        typed_linear(L.tdown, ts.ff.get<float>(), M, x, c.D, h, ts, s);
+    }
+}
+
+// the final norm, the LM head and the argmax of one row (qwen35.hpp:296-302)
+void Qwen35Model::typed_head(State& st, TypedScratch& ts, const float* x_last, hipStream_t s) const {
+    const ModelConfig& c = c_;
+    launch_rmsnorm_quant(x_last, final_norm_.get<float>(), c.eps, ts.xn.get<float>(), nullptr, 1, c.D, s);
+    ts.new_input();
+    typed_linear(c.tied ? t_embedding_ : t_output_, ts.xn.get<float>(), 1, st.logits_.get<float>(), c.V, nullptr, ts, s);
+    launch_argmax(st.logits_.get<float>(), 1, c.V, st.step_.get<int32_t>() + 1, st.argmax_scratch_.get<uint64_t>(), s);
+}
+
+// gather_rows (quant.hpp:464-480) of device ids
+void Qwen35Model::embed_rows(const int32_t* ids, int64_t n, float* out, hipStream_t s) const {
+    if (!typed_ || t_embedding_.type == 8)
+        launch_embed_q8(typed_ ? t_embedding_.w.get() : embedding_.get(), c_.V, c_.D, ids, n, out, s);
+    else
+        launch_kquant_dequant_rows(t_embedding_.type, t_embedding_.w.get(), c_.V, c_.D, ids, n, out, s);
+}
+
 void Qwen35Model::enqueue_step(State& st, bool from_ids, bool with_head) const {
     const ModelConfig& c = c_;
     hipStream_t s = stream_;
@@ -485,6 +770,14 @@ void Qwen35Model::enqueue_step(State& st, bool from_ids, bool with_head) const {
     float* x = st.x_.get<float>();
     float* h = st.h_.get<float>();
     float* proj = st.proj_.get<float>();
+    if (typed_) {
+        if (from_ids) embed_rows(step + 1, 1, x, s);
+        typed_layers(st, *st.tstep_, x, h, proj, st.gate_up_.get<float>(), 1, step, 0, false, s);
+        if (with_head) typed_head(st, *st.tstep_, x, s);
+        hipLaunchKernelGGL(advance_step_kernel, dim3(1), dim3(1), 0, s, step, st.out_ids_.get<int32_t>(), int32_t(with_head && from_ids));
+        check_launch("decode step");
+        return;
+    }
     if (from_ids) launch_embed_q8(embedding_.get(), c.V, c.D, step + 1, 1, x, s);
     for (int64_t l = 0; l < c.L; ++l) {
         const LayerWeights& L = layers_[size_t(l)];
@@ -582,6 +875,12 @@ void Qwen35Model::enqueue_chunk(State& st, int64_t seq, int64_t pos0, int64_t T,
     float* proj = st.cproj_.get<float>();
     int32_t* pos = st.cpos_.get<int32_t>();
     hipLaunchKernelGGL(positions_kernel, dim3(unsigned((T + 255) / 256)), dim3(256), 0, s, pos, int32_t(pos0), int32_t(T));
+    if (typed_) {
+        typed_layers(st, *st.tchunk_, x, h, proj, st.cgate_up_.get<float>(), T, pos, seq, true, s);
+        if (with_head) typed_head(st, *st.tchunk_, x + (T - 1) * c.D, s);
+        check_launch("prefill chunk");
+        return;
+    }
     for (int64_t l = 0; l < c.L; ++l) {
         const LayerWeights& L = layers_[size_t(l)];
         // H = X + mix(rms(X)); X' = H + mlp(rms(H))  (nm/src/qwen35.hpp:318-327)
@@ -688,7 +987,7 @@ void Qwen35Model::forward_seq(State& st, int64_t seq, const float* rows, const i
                     hip_check(hipMemcpyAsync(st.cx_.get(), rows + t0 * c.D, size_t(n * c.D) * 4, hipMemcpyHostToDevice, s), "rows upload");
                 } else {
                     hip_check(hipMemcpyAsync(st.cids_.get(), ids + t0, size_t(n) * 4, hipMemcpyHostToDevice, s), "ids upload");
-                    launch_embed_q8(embedding_.get(), c.V, c.D, st.cids_.get<int32_t>(), n, st.cx_.get<float>(), s);
+                    embed_rows(st.cids_.get<int32_t>(), n, st.cx_.get<float>(), s);
                 }
                 enqueue_chunk(st, seq, pos0 + t0, n, t0 + n == T);
             }
@@ -753,6 +1052,18 @@ void Qwen35Model::enqueue_batch_step(State& st) const {
     float* x = st.x_.get<float>();
     float* h = st.h_.get<float>();
     float* proj = st.proj_.get<float>();
+    if (typed_) {  // row b is sequence b: the decode forms of the mixers over B rows
+        TypedScratch& ts = *st.tstep_;
+        embed_rows(ids, B, x, s);
+        typed_layers(st, ts, x, h, proj, st.gate_up_.get<float>(), B, pos, 0, false, s);
+        launch_rmsnorm_quant(x, final_norm_.get<float>(), c.eps, ts.xn.get<float>(), nullptr, B, c.D, s);
+        ts.new_input();
+        typed_linear(c.tied ? t_embedding_ : t_output_, ts.xn.get<float>(), B, st.logits_.get<float>(), c.V, nullptr, ts, s);
+        launch_argmax(st.logits_.get<float>(), B, c.V, ids, st.argmax_scratch_.get<uint64_t>(), s);
+        hipLaunchKernelGGL(advance_batch_kernel, dim3(1), dim3(1), 0, s, pos, st.out_ids_.get<int32_t>(), int32_t(B));
+        check_launch("batch decode step");
+        return;
+    }
     launch_embed_q8(embedding_.get(), c.V, c.D, ids, B, x, s);
     for (int64_t l = 0; l < c.L; ++l) {
         const LayerWeights& L = layers_[size_t(l)];
@@ -869,6 +1180,7 @@ void Qwen35Model::decode_batch(State& st, const int32_t* first_ids, int64_t step
 
 double Qwen35Model::time_gemvs(State& st, int reps, int64_t* launches, int64_t* bytes) const {
     const ModelConfig& c = c_;
+    if (typed_) throw Error(HERO_EINVAL, "time_gemvs: the Q8_0 matvec timing takes a model whose linears are all Q8_0");
     hipStream_t s = stream_;
     int64_t n_launch = 0, n_bytes = 0;
     // the GEMVs exactly as a decode step launches them (fused input forms
@@ -925,7 +1237,7 @@ void Qwen35Model::embed(const int32_t* ids, int64_t n, float* out) const {
         if (ids[i] < 0 || ids[i] >= c_.V) throw Error(HERO_EINVAL, "embed: token id out of range");
     DeviceBuffer d_ids(size_t(n) * 4), d_out(size_t(n * c_.D) * 4);
     hip_check(hipMemcpyAsync(d_ids.get(), ids, size_t(n) * 4, hipMemcpyHostToDevice, stream_), "ids upload");
-    launch_embed_q8(embedding_.get(), c_.V, c_.D, d_ids.get<int32_t>(), n, d_out.get<float>(), stream_);
+    embed_rows(d_ids.get<int32_t>(), n, d_out.get<float>(), stream_);
     check_launch("embed");
     hip_check(hipMemcpyAsync(out, d_out.get(), size_t(n * c_.D) * 4, hipMemcpyDeviceToHost, stream_), "rows download");
     hip_check(hipStreamSynchronize(stream_), "embed");

@@ -10,7 +10,10 @@ namespace hero {
 
 // nm/src/components.hpp:300-304 (GatedMLP): g = silu(gate(x)) * up(x), then
 // the down projection quantizes g. gate_up row = [gate FF | up FF].
-__global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restrict__ gu, int8_t* __restrict__ qs, float* __restrict__ qd, int64_t FF, int64_t total8, int64_t il) {
+// With y set the products are written as fp32 [M][FF] (the input of a
+// K-quant down projection); with qs set, quantized to Q8_0.
+__global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restrict__ gu, int8_t* __restrict__ qs, float* __restrict__ qd, float* __restrict__ y, int64_t FF,
+                                                           int64_t total8, int64_t il) {
     const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= total8) return;
     const int64_t per_row = FF >> 3;
@@ -21,6 +24,11 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restri
     float v[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = silu_f32(gate[j]) * up[j];
+    if (y) {
+        reinterpret_cast<float4*>(y)[2 * i] = make_float4(v[0], v[1], v[2], v[3]);
+        reinterpret_cast<float4*>(y)[2 * i + 1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    if (!qs) return;
     uint16_t dh;
     const int2 q = quantize8_in_quad(v, &dh);
     reinterpret_cast<int2*>(qs)[i] = q;
@@ -31,7 +39,12 @@ void launch_swiglu_quant(const float* gate_up, void* act, int64_t M, int64_t FF,
     int8_t* qs = static_cast<int8_t*>(act);
     float* qd = reinterpret_cast<float*>(qs + M * FF);
     const int64_t total8 = M * FF / 8;
-    hipLaunchKernelGGL(swiglu_quant_kernel, dim3(unsigned((total8 + 255) / 256)), dim3(256), 0, s, gate_up, qs, qd, FF, total8, interleave);
+    hipLaunchKernelGGL(swiglu_quant_kernel, dim3(unsigned((total8 + 255) / 256)), dim3(256), 0, s, gate_up, qs, qd, nullptr, FF, total8, interleave);
+}
+
+void launch_swiglu_f32(const float* gate_up, float* y, int64_t M, int64_t FF, hipStream_t s) {
+    const int64_t total8 = M * FF / 8;
+    hipLaunchKernelGGL(swiglu_quant_kernel, dim3(unsigned((total8 + 255) / 256)), dim3(256), 0, s, gate_up, nullptr, nullptr, y, FF, total8, int64_t(0));
 }
 
 // nm/src/quant.hpp:306-313: row = d * q

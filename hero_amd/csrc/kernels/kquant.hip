@@ -1,29 +1,33 @@
-// kquant.hip -- GGUF K-quant weights (Q4_K, Q6_K) against Q8_K activations:
-// the activation quantizer and the matrix-vector / matrix products, bit-exact
-// to the reference's x86 integer-activation dots.
+// kquant.hip -- GGUF K-quant weights: Q4_K and Q6_K against Q8_K
+// activations (the reference's integer-activation dots), Q5_K against fp32
+// activations (its dequant-in-dot form), the activation quantizer, and the
+// row gather of the embedding. Bit-exact to the reference.
 //
 //   quantize_row_q8_K      nm/src/quant_i8.hpp:31-64
-//   vec_dot_q4_K_q8_K      nm/src/quant_i8.hpp:129-191 (scalar form)
+//   vec_dot_q4_K_q8_K      nm/src/quant_i8.hpp:146-191 (scalar form)
 //   vec_dot_q6_K_q8_K      nm/src/quant_i8.hpp:239-278 (scalar form)
-//   Weight::matvec/matmul  nm/src/quant_i8.hpp:352-383, 430-474
+//   dot_block_q5_K         nm/src/quant.hpp:207-229
+//   Weight::matvec/matmul  nm/src/quant_i8.hpp:352-383, 415-495
+//   dequant_to_f32         nm/src/quant.hpp:322-395
 //
-// Layouts are GGUF's own (no repacking): a weight row is K/256 super-blocks
-// of 144 (Q4_K) or 210 (Q6_K) bytes; a Q8_K activation row is K/256 blocks of
-// 292 bytes {fp32 d, int8 qs[256], int16 bsums[16]}.
+// Weights are repacked once at load by a byte permutation per super-block
+// (same size as GGUF; kq_pack_kernel): the bytes of the four positions
+// 32j + 8i + l (i = 0..3) that share sub-block j and residue l = p % 8 -- the
+// positions whose products the reference adds into one of its eight sums --
+// become one dword, so each such group is one 4-way int8 dot. A Q8_K
+// activation row is K/256 GGUF blocks of 292 bytes {fp32 d, int8 qs[256],
+// int16 bsums[16]} followed by the same residue regrouping of its int8.
 //
-// Exactness: per super-block, the reference forms eight int32 sums aux[l]
-// over the positions p with p % 8 == l (each product weighted by its
-// sub-block's integer scale) and, for Q4_K, the integer mins term; all of
-// that is exact, so any order gives the same integers. The fp32 part runs per
-// row in block order exactly as written: d = fp16(w.d) * x.d;
-// sums[l] += d * float(aux[l]); (Q4_K) sumf -= (fp16(w.dmin) * x.d) * float(summin);
-// then sumf += sums[0..7].
-//
-// Work split: a workgroup takes R consecutive output rows of one activation
-// row; its weight bytes (R rows, contiguous) and the activation row are staged
-// in shared memory with coalesced 16-byte loads; lane (r, b) forms block b of
-// row r's integers; lane r then chains row r's fp32 terms.
+// Exactness: per super-block the reference forms eight int32 sums aux[l]
+// (each product weighted by its sub-block's integer scale) and, for Q4_K, the
+// integer mins term; all of that is exact, so any order gives the same
+// integers. The fp32 part runs per output in block order exactly as written:
+// d = fp16(w.d) * x.d; sums[l] += d * float(aux[l]); (Q4_K)
+// sumf -= (fp16(w.dmin) * x.d) * float(summin); then sumf += sums[0..7].
+#include <algorithm>
+
 #include "hero/device.hpp"
+#include "hero/errors.hpp"
 #include "hero/kernels.hpp"
 
 namespace hero {
@@ -32,7 +36,6 @@ namespace {
 
 constexpr int kQ8KBytes = 292;
 constexpr int kKqThreads = 256;
-constexpr int kKqLdsMax = 65536;
 
 __device__ __forceinline__ int nearest_int_magic(float v) {
     const float t = v + 12582912.f;  // 1.5 * 2^23: rounds to nearest, ties to even
@@ -90,211 +93,362 @@ __global__ __launch_bounds__(64) void quantize_q8_K_kernel(const float* __restri
     if (lane == 0) reinterpret_cast<float*>(out)[0] = 1.f / iscale;
 }
 
+// Sign-extend four packed 6-bit values (bytes 0..63) minus 32 to int8:
+// t = q ^ 32 has its sign in bit 5; the top two bits copy it (0x20 * 6 = 0xC0).
+__device__ __forceinline__ uint32_t sext6_minus32(uint32_t q) {
+    const uint32_t t = q ^ 0x20202020u;
+    return t | ((t & 0x20202020u) * 6u);
+}
+
+// get_scale_min_k4 (nm/src/quant.hpp:153-162): 6-bit scale and min of sub-block j
+__device__ __forceinline__ void scale_min_k4(const uint8_t* q, int j, int& sc, int& m) {
+    if (j < 4) {
+        sc = q[j] & 63;
+        m = q[j + 4] & 63;
+    } else {
+        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+constexpr int kKqTile = 4;  // activation rows per pass of the K-quant GEMM
+
+// Q4_K / Q6_K GEMM over packed weights (kq_pack_kernel) and Q8_K activations.
+//
+// A workgroup owns R consecutive output rows; lane (b, r) = (tid / R, tid % R)
+// holds super-block b of row n0 + r in registers for the whole kernel (each
+// weight byte is read once per workgroup) and walks the workgroup's
+// activation rows kKqTile at a time: per row it forms the block's eight
+// residue sums aux[l] (exact integers, dot4 over the residue-grouped bytes)
+// and the reference's per-block fp32 products d * aux[l] (and, for Q4_K,
+// dmin * sum_of_mins), leaving them in shared memory; then lane (row, r)
+// chains row r's blocks in order: sums[l] += P[b][l]; sumf -= Q[b]; and
+// finally sumf += sums[0..7] (nm/src/quant_i8.hpp:146-191, 239-278).
+// grid (ceil(N / R), ceil(M / rows_per_group)); R * nb <= 256.
 template <int TYPE>
-struct KqFormat;
-template <>
-struct KqFormat<12> {  // Q4_K
-    static constexpr int kBytes = 144;
-};
-template <>
-struct KqFormat<14> {  // Q6_K
-    static constexpr int kBytes = 210;
-};
+__global__ __launch_bounds__(kKqThreads) void kq_gemm_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ act, const uint32_t* __restrict__ xt,
+                                                             float* __restrict__ y, const float* __restrict__ resid, int64_t M, int64_t N, int K, int64_t ldy,
+                                                             int R, int rows_per_group) {
+    extern __shared__ float terms[];  // [kKqTile][R * nb][T]
+    constexpr int T = TYPE == 12 ? 9 : 8;
+    const int nb = K >> 8, tid = threadIdx.x, items = R * nb;
+    const int64_t n0 = int64_t(blockIdx.x) * R;
+    const int64_t m_begin = int64_t(blockIdx.y) * rows_per_group;
+    const int64_t m_end = min(M, m_begin + rows_per_group);
+    const int b = tid / R, r = tid % R;
+    const bool active = tid < items && n0 + r < N;
+    const int64_t blk = (n0 + r) * nb + b;
 
-// Per-block integer part of Q4_K. w = the 144 weight bytes; xt = the block's
-// 256 activation int8 regrouped per 32-element sub-block j as eight dwords
-// xt[8j + l] = bytes (x[32j+l], x[32j+8+l], x[32j+16+l], x[32j+24+l]): the
-// four positions that share both aux[l] and the sub-block's scale, so each
-// (j, l) term is one 4-way int8 dot of the same four weight nibbles, gathered
-// with byte permutes. xs = the 16 activation sums. Exact integers.
-__device__ __forceinline__ void q4k_block(const uint8_t* w, const uint32_t* xt, const int16_t* xs, int (&aux)[8], int& summin) {
-    const uint8_t* sc = w + 4;
-    const uint32_t* qs = reinterpret_cast<const uint32_t*>(w + 16);
+    // the block: Q4_K 16-byte header (d, dmin, packed scales) + 32 residue
+    // dwords; Q6_K 32 low-nibble dwords, 16 high-bit dwords, 16 int8 scales, d
+    uint32_t q[TYPE == 12 ? 32 : 48];
+    int sc[TYPE == 12 ? 8 : 16], mn[8];
+    float wd = 0.f, wdmin = 0.f;
+    if (active) {
+        if constexpr (TYPE == 12) {
+            const uint4* src = reinterpret_cast<const uint4*>(w + blk * 144);
+            const uint4 hdr = src[0];
+            const uint8_t* hb = reinterpret_cast<const uint8_t*>(&hdr);
 #pragma unroll
-    for (int l = 0; l < 8; ++l) aux[l] = 0;
-    summin = 0;
+            for (int j = 0; j < 8; ++j) scale_min_k4(hb + 4, j, sc[j], mn[j]);
+            wd = half_bits_to_f32(uint16_t(hdr.x & 0xFFFF));
+            wdmin = half_bits_to_f32(uint16_t(hdr.x >> 16));
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {  // sub-blocks 2c (low nibbles) and 2c+1 (high)
-        uint32_t D[8];
+            for (int i = 0; i < 8; ++i) {
+                const uint4 v = src[1 + i];
+                q[4 * i] = v.x, q[4 * i + 1] = v.y, q[4 * i + 2] = v.z, q[4 * i + 3] = v.w;
+            }
+        } else {
+            const uint4* src = reinterpret_cast<const uint4*>(w + blk * 208);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) D[t] = qs[8 * c + t];
-        int s[2], m[2];
+            for (int i = 0; i < 12; ++i) {
+                const uint4 v = src[i];
+                q[4 * i] = v.x, q[4 * i + 1] = v.y, q[4 * i + 2] = v.z, q[4 * i + 3] = v.w;
+            }
+            const uint4 sv = src[12];
+            const int8_t* s8 = reinterpret_cast<const int8_t*>(&sv);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int j = 2 * c + h;
-            s[h] = j < 4 ? (sc[j] & 63) : ((sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4));
-            m[h] = j < 4 ? (sc[j + 4] & 63) : ((sc[j + 4] >> 4) | ((sc[j] >> 6) << 4));
-            summin += m[h] * (int(xs[2 * j]) + int(xs[2 * j + 1]));
+            for (int g = 0; g < 16; ++g) sc[g] = s8[g];
+            const uint16_t* dplane = reinterpret_cast<const uint16_t*>(w + N * nb * 208);
+            wd = half_bits_to_f32(dplane[blk]);
         }
+    }
+
+    for (int64_t mt = m_begin; mt < m_end; mt += kKqTile) {
+        const int mrows = int(min<int64_t>(kKqTile, m_end - mt));
+        if (active) {
+#pragma unroll 1
+            for (int mi = 0; mi < mrows; ++mi) {
+                const int64_t ab = (mt + mi) * nb + b;
+                const float xd = *reinterpret_cast<const float*>(act + ab * kQ8KBytes);
+                const uint4* xv = reinterpret_cast<const uint4*>(xt + ab * 64);
+                int aux[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                float* t = terms + (int64_t(mi) * items + tid) * T;
+                if constexpr (TYPE == 12) {
 #pragma unroll
-        for (int l = 0; l < 8; ++l) {
-            // bytes l, 8+l, 16+l, 24+l of the 32 = byte l%4 of dwords l/4, l/4+2, l/4+4, l/4+6
-            const int u = l & 3, o = l >> 2;
-            const uint32_t sel = uint32_t(u) | (uint32_t(4 + u) << 8) | 0x0C0C0000u;
-            const uint32_t lo2 = __builtin_amdgcn_perm(D[o + 2], D[o], sel);
-            const uint32_t hi2 = __builtin_amdgcn_perm(D[o + 6], D[o + 4], sel);
-            const uint32_t g = __builtin_amdgcn_perm(hi2, lo2, 0x05040100u);
-            const int dl = dot4_i8(int(g & 0x0F0F0F0Fu), int(xt[8 * (2 * c) + l]), 0);
-            const int dh = dot4_i8(int((g >> 4) & 0x0F0F0F0Fu), int(xt[8 * (2 * c + 1) + l]), 0);
-            aux[l] += s[0] * dl;
-            aux[l] += s[1] * dh;
+                    for (int c = 0; c < 4; ++c) {
+                        const uint4 xl0 = xv[4 * c], xl1 = xv[4 * c + 1], xh0 = xv[4 * c + 2], xh1 = xv[4 * c + 3];
+                        const uint32_t xlo[8] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w};
+                        const uint32_t xhi[8] = {xh0.x, xh0.y, xh0.z, xh0.w, xh1.x, xh1.y, xh1.z, xh1.w};
+#pragma unroll
+                        for (int l = 0; l < 8; ++l) {
+                            const uint32_t g = q[8 * c + l];
+                            aux[l] += sc[2 * c] * dot4_i8(int(g & 0x0F0F0F0Fu), int(xlo[l]), 0);
+                            aux[l] += sc[2 * c + 1] * dot4_i8(int((g >> 4) & 0x0F0F0F0Fu), int(xhi[l]), 0);
+                        }
+                    }
+                    const uint32_t* bw = reinterpret_cast<const uint32_t*>(act + ab * kQ8KBytes + 260);  // 16 int16 sums
+                    int sumi = 0;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const uint32_t v = bw[i];
+                        sumi += int(int16_t(v & 0xFFFF)) * mn[i];  // sums 2i and 2i+1 share min i
+                        sumi += int(int16_t(v >> 16)) * mn[i];
+                    }
+                    const float d = wd * xd;
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) t[l] = d * float(aux[l]);
+                    const float dmin = wdmin * xd;
+                    t[8] = dmin * float(sumi);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int cp = 2 * (j / 4) + (j % 2), nib = 4 * ((j % 4) / 2), hh = j / 4, sh = 2 * (j % 4);
+                        const uint4 x0 = xv[2 * j], x1 = xv[2 * j + 1];
+                        const uint32_t xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                        for (int l = 0; l < 8; ++l) {
+                            const uint32_t lo = (q[8 * cp + l] >> nib) & 0x0F0F0F0Fu;
+                            const uint32_t hi = ((q[32 + 8 * hh + l] >> sh) & 0x03030303u) << 4;
+                            const uint32_t a = sext6_minus32(lo | hi);
+                            // bytes 0, 1: positions of group 2j; bytes 2, 3: group 2j + 1
+                            aux[l] += sc[2 * j] * dot4_i8(int(a & 0x0000FFFFu), int(xs[l]), 0);
+                            aux[l] += sc[2 * j + 1] * dot4_i8(int(a & 0xFFFF0000u), int(xs[l]), 0);
+                        }
+                    }
+                    const float d = wd * xd;
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) t[l] = d * float(aux[l]);
+                }
+            }
         }
+        __syncthreads();
+        for (int idx = tid; idx < mrows * R; idx += kKqThreads) {
+            const int mi = idx / R, rr = idx % R;
+            const int64_t n = n0 + rr;
+            if (n >= N) continue;
+            float sums[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            float sumf = 0.f;
+            for (int bb = 0; bb < nb; ++bb) {
+                const float* t = terms + (int64_t(mi) * items + bb * R + rr) * T;
+#pragma unroll
+                for (int l = 0; l < 8; ++l) sums[l] += t[l];
+                if constexpr (TYPE == 12) sumf -= t[8];
+            }
+#pragma unroll
+            for (int l = 0; l < 8; ++l) sumf += sums[l];
+            const int64_t o = (mt + mi) * ldy + n;
+            y[o] = resid ? resid[o] + sumf : sumf;
+        }
+        __syncthreads();
     }
 }
 
-__device__ __forceinline__ void q6k_block(const uint8_t* w, const int8_t* xq, int (&aux)[8]) {
-    const uint8_t* ql = w;
-    const uint8_t* qh = w + 128;
-    const int8_t* sc = reinterpret_cast<const int8_t*>(w + 192);
+// Q5_K against fp32 activations (no integer-activation kernel in the
+// reference): per block the dequant-in-dot chain of nm/src/quant.hpp:207-229
+// -- acc += (d1 * q - m1) * x, 256 products in order from acc = 0 -- and per
+// output the sum of its blocks' results in order (quant_i8.hpp:403-407).
+// Lane (b, r) keeps its 176-byte block in registers; TILE activation rows at a
+// time are staged in shared memory and each weight is decoded once for all of
+// them. grid (ceil(N / R), ceil(M / rows_per_group)).
+template <int TILE>
+__global__ __launch_bounds__(kKqThreads) void q5k_gemm_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x, int64_t ldx, float* __restrict__ y,
+                                                              const float* __restrict__ resid, int64_t M, int64_t N, int K, int64_t ldy, int R,
+                                                              int rows_per_group) {
+    // x position-major [K][TILE] (the TILE rows' values of one position are
+    // adjacent: one read, constant offsets from the lane's block); once every
+    // lane has its results the same memory holds the block results
+    // [TILE][R * nb] (R * nb <= 256 <= K)
+    extern __shared__ __align__(16) float smem[];
+    float* xs = smem;
+    float* res = smem;
+    const int nb = K >> 8, tid = threadIdx.x, items = R * nb;
+    const int64_t n0 = int64_t(blockIdx.x) * R;
+    const int64_t m_begin = int64_t(blockIdx.y) * rows_per_group;
+    const int64_t m_end = min(M, m_begin + rows_per_group);
+    const int b = tid / R, r = tid % R;
+    const bool active = tid < items && n0 + r < N;
+
+    uint32_t qh[8], qs[32];
+    float d1[8], m1[8];
+    if (active) {
+        const uint4* src = reinterpret_cast<const uint4*>(w + ((n0 + r) * nb + b) * 176);
+        const uint4 hdr = src[0];
+        const uint8_t* hb = reinterpret_cast<const uint8_t*>(&hdr);
+        const float d = half_bits_to_f32(uint16_t(hdr.x & 0xFFFF)), dmin = half_bits_to_f32(uint16_t(hdr.x >> 16));
 #pragma unroll
-    for (int l = 0; l < 8; ++l) aux[l] = 0;
-#pragma unroll 2
-    for (int p = 0; p < 256; p += 4) {
-        const int h = p >> 7, e = p & 127;
-        const uint8_t* lo = ql + 64 * h + (e & 63);
-        const uint8_t* hi = qh + 32 * h + (e & 31);
-        const int shl = (e >> 6) * 4, shh = 2 * (e >> 5);
-        const int s = sc[p >> 4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int q = (((lo[u] >> shl) & 0xF) | (((hi[u] >> shh) & 3) << 4)) - 32;
-            aux[(p + u) & 7] += s * (q * int(xq[p + u]));
+        for (int j = 0; j < 8; ++j) {
+            int sc, m;
+            scale_min_k4(hb + 4, j, sc, m);
+            d1[j] = d * float(sc);
+            m1[j] = dmin * float(m);
         }
-    }
-}
-
-// Q4_K: lane (r, b) loads its 144-byte block and the activation's regrouped
-// block straight from memory (no staging), forms the block's integers, and
-// leaves them with the block's scales in shared memory; lane r chains row r.
-// grid (ceil(N / R), M), R * nb <= 256.
-constexpr int kQ4Terms = 11;  // aux[8], summin, weight d | dmin << 16, activation d
-constexpr int kQ4Threads = 256;
-
-__global__ __launch_bounds__(kQ4Threads) void q4k_gemm_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ act, const uint32_t* __restrict__ xt,
-                                                              float* __restrict__ y, int64_t N, int64_t K, int R) {
-    __shared__ int terms[kQ4Threads * kQ4Terms];
-    const int nb = int(K / 256), tid = threadIdx.x;
-    const int64_t n0 = int64_t(blockIdx.x) * R, m = blockIdx.y;
-    const int rows = int(min<int64_t>(R, N - n0));
-    if (tid < rows * nb) {
-        const int r = tid / nb, b = tid % nb;
-        uint4 wv[9];
-        const uint4* wsrc = reinterpret_cast<const uint4*>(w + ((n0 + r) * nb + b) * 144);
-#pragma unroll
-        for (int i = 0; i < 9; ++i) wv[i] = wsrc[i];
-        uint4 xv[16];
-        const uint4* xsrc = reinterpret_cast<const uint4*>(xt + (m * nb + b) * 64);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) xv[i] = xsrc[i];
-        const uint8_t* xb = act + (m * nb + b) * kQ8KBytes;
-        int16_t bs[16];
-        const uint32_t* bsrc = reinterpret_cast<const uint32_t*>(xb + 260);
+        const uint4 h0 = src[1], h1 = src[2];
+        qh[0] = h0.x, qh[1] = h0.y, qh[2] = h0.z, qh[3] = h0.w, qh[4] = h1.x, qh[5] = h1.y, qh[6] = h1.z, qh[7] = h1.w;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint32_t v = bsrc[i];
-            bs[2 * i] = int16_t(v & 0xFFFF), bs[2 * i + 1] = int16_t(v >> 16);
+            const uint4 v = src[3 + i];
+            qs[4 * i] = v.x, qs[4 * i + 1] = v.y, qs[4 * i + 2] = v.z, qs[4 * i + 3] = v.w;
         }
-        const uint32_t xd_bits = *reinterpret_cast<const uint32_t*>(xb);
-        int aux[8], summin;
-        q4k_block(reinterpret_cast<const uint8_t*>(wv), reinterpret_cast<const uint32_t*>(xv), bs, aux, summin);
-        int* t = terms + tid * kQ4Terms;
-#pragma unroll
-        for (int l = 0; l < 8; ++l) t[l] = aux[l];
-        t[8] = summin;
-        t[9] = int(wv[0].x);  // fp16 d | fp16 dmin << 16
-        t[10] = int(xd_bits);
     }
-    __syncthreads();
-    for (int r = tid; r < rows; r += kQ4Threads) {
-        float sums[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        float sumf = 0.f;
-        for (int b = 0; b < nb; ++b) {
-            const int* t = terms + (r * nb + b) * kQ4Terms;
-            const float xd = __int_as_float(t[10]);
-            const uint32_t dd = uint32_t(t[9]);
-            const float d = half_bits_to_f32(uint16_t(dd & 0xFFFF)) * xd;
-#pragma unroll
-            for (int l = 0; l < 8; ++l) sums[l] += d * float(t[l]);
-            const float dmin = half_bits_to_f32(uint16_t(dd >> 16)) * xd;
-            sumf -= dmin * float(t[8]);
+
+    for (int64_t mt = m_begin; mt < m_end; mt += TILE) {
+        const int mrows = int(min<int64_t>(TILE, m_end - mt));
+        for (int i = tid; i < TILE * (K >> 2); i += kKqThreads) {
+            const int mi = i / (K >> 2), c4 = i % (K >> 2);
+            const float4 v = mi < mrows ? reinterpret_cast<const float4*>(x + (mt + mi) * ldx)[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+            xs[(4 * c4) * TILE + mi] = v.x;
+            xs[(4 * c4 + 1) * TILE + mi] = v.y;
+            xs[(4 * c4 + 2) * TILE + mi] = v.z;
+            xs[(4 * c4 + 3) * TILE + mi] = v.w;
         }
+        __syncthreads();
+        float acc[TILE];
 #pragma unroll
-        for (int l = 0; l < 8; ++l) sumf += sums[l];
-        y[m * N + n0 + r] = sumf;
+        for (int mi = 0; mi < TILE; ++mi) acc[mi] = 0.f;
+        if (active) {
+            const float* xb = xs + 256 * TILE * b;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int j = 2 * c + h;
+#pragma unroll
+                    for (int i4 = 0; i4 < 8; ++i4) {  // 4 weights: bytes 4 i4 .. 4 i4 + 3 of the 32
+                        // opaque copies: decoded per pass instead of 256 decoded
+                        // weights hoisted out of the row loop into registers
+                        uint32_t qw = qs[8 * c + i4], fifth = qh[i4];
+                        asm volatile("" : "+v"(qw), "+v"(fifth) : : "memory");
+                        const uint32_t nibs = (qw >> (4 * h)) & 0x0F0F0F0Fu;
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            const int qv = int((nibs >> (8 * u)) & 0xFF) + int(((fifth >> (8 * u + j)) & 1u) << 4);
+                            const float wv = d1[j] * float(qv) - m1[j];
+                            const float* xp = xb + (64 * c + 32 * h + 4 * i4 + u) * TILE;
+#pragma unroll
+                            for (int mi = 0; mi < TILE; ++mi) acc[mi] += wv * xp[mi];
+                        }
+                        // the chains advance group by group (not deferred behind
+                        // every group's decoded weights and reads)
+#pragma unroll
+                        for (int mi = 0; mi < TILE; ++mi) asm volatile("" : "+v"(acc[mi]));
+                    }
+                }
+            }
+        }
+        __syncthreads();  // every lane's reads of xs are done
+        if (active) {
+#pragma unroll
+            for (int mi = 0; mi < TILE; ++mi)
+                if (mi < mrows) res[mi * items + tid] = acc[mi];
+        }
+        __syncthreads();
+        for (int idx = tid; idx < mrows * R; idx += kKqThreads) {
+            const int mi = idx / R, rr = idx % R;
+            const int64_t n = n0 + rr;
+            if (n >= N) continue;
+            float s = 0.f;
+            for (int bb = 0; bb < nb; ++bb) s += res[mi * items + bb * R + rr];
+            const int64_t o = (mt + mi) * ldy + n;
+            y[o] = resid ? resid[o] + s : s;
+        }
+        __syncthreads();
     }
 }
 
-// Q6_K: grid (ceil(N / R), M); dynamic shared: weights R * nb * 210 (+16),
-// activation nb * 292, per-block terms R * nb * 10 ints
-template <int TYPE>
-__global__ __launch_bounds__(kKqThreads) void kquant_gemm_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ act, float* __restrict__ y,
-                                                                int64_t N, int64_t K, int R) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int B = KqFormat<TYPE>::kBytes;
-    const int nb = int(K / 256), tid = threadIdx.x;
-    const int64_t n0 = int64_t(blockIdx.x) * R, m = blockIdx.y;
-    const int rows = int(min<int64_t>(R, N - n0));
-    const int64_t rb = int64_t(nb) * B;
-    // the rows' bytes start at an even offset of the (16-byte aligned) tensor;
-    // in shared memory they start at the same offset modulo 16, so the
-    // 16-byte copies below are aligned on both sides
-    const int64_t start = n0 * rb, len = int64_t(rows) * rb;
-    const int head = int(start & 15);
-    uint8_t* ws = smem + head;
-    uint8_t* xs = smem + ((16 + int64_t(R) * rb + 15) & ~int64_t(15));
-    int* terms = reinterpret_cast<int*>(xs + ((int64_t(nb) * kQ8KBytes + 15) & ~int64_t(15)));
+// GGUF -> packed K-quant layout: a byte permutation per super-block.
+// Q4_K keeps its 16-byte header; its 128 quant bytes become 32 residue dwords:
+// dword 8c + l, byte i = qs[32c + 8i + l] (low nibbles: sub-block 2c, high:
+// 2c + 1). Q6_K's 128 ql bytes take the same permutation (pair c = sub-blocks
+// {j, j + 2} of half c / 2), its 64 qh bytes too (dword 8h + l, byte i =
+// qh[32h + 8i + l]: 2-bit fields of sub-blocks 4h .. 4h + 3), then the 16
+// scales: 208 bytes; the fp16 d of every block follow in a plane of their own.
+__global__ __launch_bounds__(256) void kq_pack_kernel(int type, const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t nblocks) {
+    const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    constexpr int kWords = 56;  // output dwords handled per block: 4 header/scales + 32 + 16 + 4
+    if (gid >= nblocks * kWords) return;
+    const int64_t blk = gid / kWords;
+    const int wi = int(gid % kWords);
+    if (type == 12) {
+        const uint8_t* s = src + blk * 144;
+        uint8_t* o = dst + blk * 144;
+        if (wi < 4) {
+            reinterpret_cast<uint32_t*>(o)[wi] = uint32_t(s[4 * wi]) | (uint32_t(s[4 * wi + 1]) << 8) | (uint32_t(s[4 * wi + 2]) << 16) | (uint32_t(s[4 * wi + 3]) << 24);
+        } else if (wi < 36) {
+            const int dw = wi - 4, c = dw / 8, l = dw % 8;
+            const uint8_t* g = s + 16 + 32 * c + l;
+            reinterpret_cast<uint32_t*>(o + 16)[dw] = uint32_t(g[0]) | (uint32_t(g[8]) << 8) | (uint32_t(g[16]) << 16) | (uint32_t(g[24]) << 24);
+        }
+        return;
+    }
+    // Q6_K
+    const uint8_t* s = src + blk * 210;
+    uint8_t* o = dst + blk * 208;
+    if (wi < 32) {
+        const int c = wi / 8, l = wi % 8;
+        const uint8_t* g = s + 32 * c + l;
+        reinterpret_cast<uint32_t*>(o)[wi] = uint32_t(g[0]) | (uint32_t(g[8]) << 8) | (uint32_t(g[16]) << 16) | (uint32_t(g[24]) << 24);
+    } else if (wi < 48) {
+        const int dw = wi - 32, h = dw / 8, l = dw % 8;
+        const uint8_t* g = s + 128 + 32 * h + l;
+        reinterpret_cast<uint32_t*>(o + 128)[dw] = uint32_t(g[0]) | (uint32_t(g[8]) << 8) | (uint32_t(g[16]) << 16) | (uint32_t(g[24]) << 24);
+    } else if (wi < 52) {
+        const int dw = wi - 48;
+        const uint8_t* g = s + 192 + 4 * dw;
+        reinterpret_cast<uint32_t*>(o + 192)[dw] = uint32_t(g[0]) | (uint32_t(g[1]) << 8) | (uint32_t(g[2]) << 16) | (uint32_t(g[3]) << 24);
+    } else if (wi == 52) {
+        reinterpret_cast<uint16_t*>(dst + nblocks * 208)[blk] = uint16_t(s[208] | (s[209] << 8));
+    }
+}
 
-    // stage: the rows' bytes (16-byte copies between 2-byte copies of the
-    // unaligned head and tail) and the activation row (a multiple of 4 bytes)
-    {
-        const int64_t a0 = (start + 15) & ~int64_t(15), a1 = (start + len) & ~int64_t(15);
-        if (a1 > a0) {
-            const uint4* src = reinterpret_cast<const uint4*>(w + a0);
-            uint4* dst = reinterpret_cast<uint4*>(smem + 16 * ((a0 - start + head) / 16));
-            for (int64_t i = tid; i < (a1 - a0) / 16; i += kKqThreads) dst[i] = src[i];
-            for (int64_t i = start + 2 * tid; i < a0; i += 2 * kKqThreads)
-                *reinterpret_cast<uint16_t*>(ws + (i - start)) = *reinterpret_cast<const uint16_t*>(w + i);
-            for (int64_t i = a1 + 2 * tid; i < start + len; i += 2 * kKqThreads)
-                *reinterpret_cast<uint16_t*>(ws + (i - start)) = *reinterpret_cast<const uint16_t*>(w + i);
+// Weight::dequant_row (nm/src/quant.hpp:322-395) of the rows `ids` of a
+// packed Q4_K / Q6_K or GGUF Q5_K tensor: Q4_K / Q5_K d1 * q - m1 with
+// d1 = d * sc, m1 = dmin * m; Q6_K (d * sc) * (q - 32). grid (nb, n_ids), 256 lanes.
+__global__ __launch_bounds__(256) void kq_dequant_rows_kernel(int type, const uint8_t* __restrict__ w, int64_t N, int K, const int32_t* __restrict__ ids,
+                                                              float* __restrict__ out) {
+    const int nb = K >> 8, b = blockIdx.x, p = threadIdx.x;
+    const int64_t t = blockIdx.y;
+    const int32_t id = ids[t];
+    float* o = out + t * K + 256 * b + p;
+    if (id < 0 || id >= N) {  // the host validates ids; a bad one gives zeros, never a stray read
+        *o = 0.f;
+        return;
+    }
+    const int64_t blk = int64_t(id) * nb + b;
+    const int j = p >> 5, i = (p & 31) >> 3, l = p & 7;
+    if (type == 12 || type == 13) {
+        const uint8_t* s = w + blk * (type == 12 ? 144 : 176);
+        const float d = half_bits_to_f32(uint16_t(s[0] | (s[1] << 8))), dmin = half_bits_to_f32(uint16_t(s[2] | (s[3] << 8)));
+        int sc, m;
+        scale_min_k4(s + 4, j, sc, m);
+        const float dd = d * float(sc), mm = dmin * float(m);
+        int q;
+        if (type == 12) {
+            q = (s[16 + 4 * (8 * (j >> 1) + l) + i] >> (4 * (j & 1))) & 0xF;
         } else {
-            for (int64_t i = start + 2 * tid; i < start + len; i += 2 * kKqThreads)
-                *reinterpret_cast<uint16_t*>(ws + (i - start)) = *reinterpret_cast<const uint16_t*>(w + i);
+            const int e = p & 31;
+            q = ((s[48 + 32 * (j >> 1) + e] >> (4 * (j & 1))) & 0xF) + (((s[16 + e] >> j) & 1) << 4);
         }
-        const uint32_t* xa = reinterpret_cast<const uint32_t*>(act + m * int64_t(nb) * kQ8KBytes);
-        const int n4 = nb * kQ8KBytes / 4;
-        for (int i = tid; i < n4; i += kKqThreads) reinterpret_cast<uint32_t*>(xs)[i] = xa[i];
+        *o = dd * float(q) - mm;
+        return;
     }
-    __syncthreads();
-
-    for (int item = tid; item < rows * nb; item += kKqThreads) {
-        const int r = item / nb, b = item % nb;
-        const uint8_t* wb = ws + int64_t(r) * rb + int64_t(b) * B;
-        const uint8_t* xb = xs + b * kQ8KBytes;
-        int aux[8], summin = 0;
-        q6k_block(wb, reinterpret_cast<const int8_t*>(xb + 4), aux);
-        int* t = terms + item * 10;
-#pragma unroll
-        for (int l = 0; l < 8; ++l) t[l] = aux[l];
-        t[8] = summin;
-    }
-    __syncthreads();
-
-    // fp32, in block order per row (one lane per row)
-    for (int r = tid; r < rows; r += kKqThreads) {
-        float sums[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        float sumf = 0.f;
-        for (int b = 0; b < nb; ++b) {
-            const uint8_t* wb = ws + int64_t(r) * rb + int64_t(b) * B;
-            const float xd = *reinterpret_cast<const float*>(xs + b * kQ8KBytes);
-            const int* t = terms + (r * nb + b) * 10;
-            const float d = half_bits_to_f32(uint16_t(wb[208] | (wb[209] << 8))) * xd;
-#pragma unroll
-            for (int l = 0; l < 8; ++l) sums[l] += d * float(t[l]);
-        }
-#pragma unroll
-        for (int l = 0; l < 8; ++l) sumf += sums[l];
-        y[m * N + n0 + r] = sumf;
-    }
+    const uint8_t* s = w + blk * 208;
+    const int cp = 2 * (j >> 2) + (j & 1);
+    const int lo = (s[4 * (8 * cp + l) + i] >> (4 * ((j & 3) >> 1))) & 0xF;
+    const int hi = (s[128 + 4 * (8 * (j >> 2) + l) + i] >> (2 * (j & 3))) & 3;
+    const float d = half_bits_to_f32(reinterpret_cast<const uint16_t*>(w + N * nb * 208)[blk]);
+    const int sc = int(int8_t(s[192 + (p >> 4)]));
+    *o = d * float(sc) * float((lo | (hi << 4)) - 32);
 }
 
 }  // namespace
@@ -312,32 +466,78 @@ void launch_quantize_q8_K(const float* x, void* act, int64_t M, int64_t K, hipSt
     hipLaunchKernelGGL(quantize_q8_K_kernel, dim3(unsigned(nblocks)), dim3(64), 0, s, x, static_cast<uint8_t*>(act), xt, nblocks);
 }
 
-int kquant_rows_per_group(int type, int64_t K) {
+int64_t kquant_packed_bytes(int type, int64_t N, int64_t K) {
     const int64_t nb = K / 256;
-    const int64_t rb = nb * (type == 12 ? 144 : 210);
-    const int64_t fixed = ((nb * kQ8KBytes + 15) & ~int64_t(15));
-    int64_t r = std::min<int64_t>(kKqThreads / std::max<int64_t>(1, nb), 64);
-    if (type == 12) return nb <= kQ4Threads ? int(std::max<int64_t>(1, kQ4Threads / nb)) : 0;  // no staging
-    while (r > 0 && ((16 + r * rb + 15) & ~int64_t(15)) + fixed + r * nb * 10 * 4 > kKqLdsMax) --r;
-    return int(std::max<int64_t>(r, 0));
+    return N * nb * (type == 12 ? 144 : type == 13 ? 176 : 210);
+}
+
+void launch_kquant_pack(int type, const void* gguf, void* packed, int64_t N, int64_t K, hipStream_t s) {
+    const int64_t nblocks = N * (K / 256);
+    if (type == 13) {  // Q5_K keeps the GGUF layout
+        hip_check(hipMemcpyAsync(packed, gguf, size_t(nblocks * 176), hipMemcpyDeviceToDevice, s), "Q5_K copy");
+        return;
+    }
+    const int64_t work = nblocks * 56;
+    hipLaunchKernelGGL(kq_pack_kernel, dim3(unsigned((work + 255) / 256)), dim3(256), 0, s, type, static_cast<const uint8_t*>(gguf),
+                       static_cast<uint8_t*>(packed), nblocks);
+}
+
+// rows per workgroup (R) and activation rows per workgroup for an (M, N, K)
+// product: R * nb <= 256 lanes; rows split over grid.y while that leaves at
+// least ~2048 workgroups
+static void kq_plan(int64_t M, int64_t N, int64_t K, int tile, int* R, int* rows_per_group) {
+    const int nb = int(K / 256);
+    *R = std::max(1, kKqThreads / nb);
+    const int64_t gx = (N + *R - 1) / *R;
+    const int64_t want_y = std::max<int64_t>(1, (2048 + gx - 1) / gx);
+    const int64_t gy = std::min<int64_t>(want_y, (M + tile - 1) / tile);
+    int64_t per = (M + gy - 1) / gy;
+    per = (per + tile - 1) / tile * tile;
+    *rows_per_group = int(per);
+}
+
+int kquant_max_k(int type) { return type == 13 ? 16384 : 65536; }
+
+void launch_kquant_gemm_ld(int type, const void* w, const void* act, float* y, const float* resid, int64_t M, int64_t N, int64_t K, int64_t ldy,
+                           hipStream_t s) {
+    int R, per;
+    kq_plan(M, N, K, kKqTile, &R, &per);
+    const dim3 grid(unsigned((N + R - 1) / R), unsigned((M + per - 1) / per));
+    const int nb = int(K / 256);
+    const auto* wb = static_cast<const uint8_t*>(w);
+    const auto* ab = static_cast<const uint8_t*>(act);
+    const uint32_t* xt = regrouped_of(act, M * nb);
+    if (type == 12) {
+        const size_t lds = size_t(kKqTile) * R * nb * 9 * 4;
+        hipLaunchKernelGGL(kq_gemm_kernel<12>, grid, dim3(kKqThreads), lds, s, wb, ab, xt, y, resid, M, N, int(K), ldy, R, per);
+    } else {
+        const size_t lds = size_t(kKqTile) * R * nb * 8 * 4;
+        hipLaunchKernelGGL(kq_gemm_kernel<14>, grid, dim3(kKqThreads), lds, s, wb, ab, xt, y, resid, M, N, int(K), ldy, R, per);
+    }
 }
 
 void launch_kquant_gemm(int type, const void* w, const void* act, float* y, int64_t M, int64_t N, int64_t K, hipStream_t s) {
-    if (type == 12) {
-        const int nb = int(K / 256), R = std::max(1, kQ4Threads / nb);
-        const dim3 grid(unsigned((N + R - 1) / R), unsigned(M));
-        hipLaunchKernelGGL(q4k_gemm_kernel, grid, dim3(kQ4Threads), 0, s, static_cast<const uint8_t*>(w), static_cast<const uint8_t*>(act),
-                           regrouped_of(act, M * nb), y, N, K, R);
-        return;
-    }
-    const int R = kquant_rows_per_group(type, K);
-    const int64_t nb = K / 256;
-    const int64_t rb = nb * (type == 12 ? 144 : 210);
-    const size_t lds = size_t(((16 + R * rb + 15) & ~int64_t(15)) + ((nb * kQ8KBytes + 15) & ~int64_t(15)) + int64_t(R) * nb * 10 * 4);
-    const dim3 grid(unsigned((N + R - 1) / R), unsigned(M));
+    launch_kquant_gemm_ld(type, w, act, y, nullptr, M, N, K, N, s);
+}
+
+void launch_q5k_gemm(const void* w, const float* x, int64_t ldx, float* y, const float* resid, int64_t M, int64_t N, int64_t K, int64_t ldy, hipStream_t s) {
+    // activation rows per pass: shared memory holds TILE rows of K floats (<= 64 KiB)
+    const int tile = M == 1 ? 1 : K <= 4096 ? 4 : K <= 8192 ? 2 : 1;
+    int R, per;
+    kq_plan(M, N, K, tile, &R, &per);
+    const dim3 grid(unsigned((N + R - 1) / R), unsigned((M + per - 1) / per));
+    const size_t lds = size_t(tile) * K * 4;  // <= 64 KiB
     const auto* wb = static_cast<const uint8_t*>(w);
-    const auto* ab = static_cast<const uint8_t*>(act);
-    hipLaunchKernelGGL(kquant_gemm_kernel<14>, grid, dim3(kKqThreads), lds, s, wb, ab, y, N, K, R);
+    if (tile == 4)
+        hipLaunchKernelGGL(q5k_gemm_kernel<4>, grid, dim3(kKqThreads), lds, s, wb, x, ldx, y, resid, M, N, int(K), ldy, R, per);
+    else if (tile == 2)
+        hipLaunchKernelGGL(q5k_gemm_kernel<2>, grid, dim3(kKqThreads), lds, s, wb, x, ldx, y, resid, M, N, int(K), ldy, R, per);
+    else
+        hipLaunchKernelGGL(q5k_gemm_kernel<1>, grid, dim3(kKqThreads), lds, s, wb, x, ldx, y, resid, M, N, int(K), ldy, R, per);
+}
+
+void launch_kquant_dequant_rows(int type, const void* w, int64_t N, int64_t K, const int32_t* ids, int64_t n, float* out, hipStream_t s) {
+    hipLaunchKernelGGL(kq_dequant_rows_kernel, dim3(unsigned(K / 256), unsigned(n)), dim3(256), 0, s, type, static_cast<const uint8_t*>(w), N, int(K), ids, out);
 }
 
 }  // namespace hero

@@ -132,20 +132,33 @@ int hero_argmax(const float* logits, int64_t m, int64_t n, int32_t* out, uint64_
  * at once) race. Results equal hero_argmax's. */
 int hero_argmax_noalloc(const float* logits, int64_t m, int64_t n, int32_t* out, void* stream);
 
-/* ---- K-quant weights (GGUF Q4_K = type 12, Q6_K = type 14) ----------------
- * Replaces the int8-activation branch of Weight<In,Out>::matvec / ::matmul
- * for these types (nm/src/quant_i8.hpp:352-383, 430-474): the activation rows
- * are quantized to Q8_K (quantize_row_q8_K, nm/src/quant_i8.hpp:31-64), then
- * y[m][n] = vec_dot_q{4,6}_K_q8_K(k, W row n, act row m) (the x86 scalar
- * forms, nm/src/quant_i8.hpp:146-191, 239-278), bit for bit.
- * W is the GGUF tensor as stored (n rows of k/256 blocks of 144 / 210 bytes),
- * 16-byte aligned. act holds hero_q8_K_act_bytes(m, k) bytes: the m rows of
- * GGUF Q8_K blocks (fp32 d, 256 int8, 16 int16 sums), then, 16-byte aligned, a
- * copy of each block's int8 regrouped for 4-way dots (256 bytes per block).
- * k: a multiple of 256, at most 65536. */
+/* ---- K-quant weights (GGUF Q4_K = 12, Q5_K = 13, Q6_K = 14) ----------------
+ * Weights are used in a packed form with the same byte count as the GGUF
+ * tensor: hero_kquant_pack copies a device GGUF tensor (n rows of k/256
+ * super-blocks of 144 / 176 / 210 bytes) into it (Q4_K and Q6_K regroup their
+ * quant bytes by sub-block and residue; Q5_K is copied as is).
+ * hero_kquant_gemm replaces the int8-activation branch of Weight<In,Out>::matvec
+ * / ::matmul (nm/src/quant_i8.hpp:352-383, 430-474) for Q4_K / Q6_K: the
+ * activation rows are quantized to Q8_K (quantize_row_q8_K,
+ * nm/src/quant_i8.hpp:31-64), then y[m][n] = vec_dot_q{4,6}_K_q8_K(k, W row n,
+ * act row m) (the x86 scalar forms, nm/src/quant_i8.hpp:146-191, 239-278), bit
+ * for bit. act holds hero_q8_K_act_bytes(m, k) bytes: the m rows of GGUF Q8_K
+ * blocks (fp32 d, 256 int8, 16 int16 sums), then, 16-byte aligned, a copy of
+ * each block's int8 regrouped for 4-way dots (256 bytes per block).
+ * hero_q5_K_gemm is the fp32-activation branch for Q5_K, which has no integer
+ * kernel (has_i8_kernel, nm/src/quant_i8.hpp:325): y[m][n] = sum over blocks in
+ * order of dot_block_q5_K (nm/src/quant.hpp:207-229) on the fp32 rows x [m][k].
+ * hero_kquant_dequant_rows is Weight::dequant_row / gather_rows
+ * (nm/src/quant.hpp:464-480) on a packed tensor: out[t][k] = row ids[t] (device
+ * ids; an id outside [0, n) gives a row of zeros).
+ * k: a multiple of 256, at most 65536 (16384 for Q5_K). */
 int64_t hero_q8_K_act_bytes(int64_t m, int64_t k);
 int hero_q8_K_quantize(const float* x, void* act, int64_t m, int64_t k, void* stream);
+int64_t hero_kquant_packed_bytes(int32_t type, int64_t n, int64_t k);
+int hero_kquant_pack(int32_t type, const void* gguf, void* packed, int64_t n, int64_t k, void* stream);
 int hero_kquant_gemm(int32_t type, const void* w, const void* act, float* y, int64_t m, int64_t n, int64_t k, void* stream);
+int hero_q5_K_gemm(const void* w, const float* x, float* y, int64_t m, int64_t n, int64_t k, void* stream);
+int hero_kquant_dequant_rows(int32_t type, const void* w, int64_t n, int64_t k, const int32_t* ids, int64_t n_ids, float* out, void* stream);
 
 /* Logits::sample with temp > 0 (nm/src/logits.hpp:71-105) on one row of v
  * logits: the top_k candidates (1 <= top_k <= 1024; top_k > v means v), sorted

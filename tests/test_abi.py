@@ -32,13 +32,21 @@ def test_every_declared_symbol_is_exported_and_bound():
 def test_kquant_argument_errors_are_reported_before_any_launch():
     lib = _lib.lib
     assert lib.hero_q8_K_act_bytes(3, 4096) == 3 * 16 * 292 + 3 * 16 * 256  # blocks, then the regrouped copy
-    assert lib.hero_kquant_gemm(13, 16, 16, 16, 1, 64, 4096, None) == _lib.HERO_EINVAL
+    assert lib.hero_kquant_gemm(13, 16, 16, 16, 1, 64, 4096, None) == _lib.HERO_EINVAL  # Q5_K has its own form
     assert b"Q4_K" in lib.hero_last_error()
     assert lib.hero_kquant_gemm(12, 16, 16, 16, 1, 64, 4000, None) == _lib.HERO_EINVAL
     assert b"multiple of 256" in lib.hero_last_error()
     assert lib.hero_kquant_gemm(14, None, 16, 16, 1, 64, 4096, None) == _lib.HERO_EINVAL
     assert lib.hero_kquant_gemm(12, 8, 16, 16, 1, 64, 4096, None) == _lib.HERO_EINVAL  # alignment
     assert lib.hero_q8_K_quantize(16, 16, 1, 300, None) == _lib.HERO_EINVAL
+    assert lib.hero_q5_K_gemm(16, 16, 16, 1, 64, 16384 + 256, None) == _lib.HERO_EINVAL  # Q5_K: k <= 16384
+    assert b"too large" in lib.hero_last_error()
+    assert lib.hero_kquant_pack(11, 16, 32, 64, 4096, None) == _lib.HERO_EINVAL
+    assert lib.hero_kquant_pack(12, 16, 16, 64, 4096, None) == _lib.HERO_EINVAL  # in place
+    assert lib.hero_kquant_dequant_rows(14, 16, 64, 4096, 16, 0, 16, None) == _lib.HERO_EINVAL
+    for t, per_block in ((12, 144), (13, 176), (14, 210)):  # the packed form has the GGUF tensor's size
+        assert lib.hero_kquant_packed_bytes(t, 3, 512) == 3 * 2 * per_block
+    assert lib.hero_kquant_packed_bytes(8, 3, 512) == -1
 
 
 def test_size_helpers():

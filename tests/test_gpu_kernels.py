@@ -693,9 +693,17 @@ def kquant_weights(rng, wtype, n, k):
     return np.ascontiguousarray(w, np.uint8)
 
 
+def kquant_pack_dev(lib, wtype, w, n, k):
+    """a GGUF K-quant tensor on the device in its packed form"""
+    raw = dev(np.ascontiguousarray(w, np.uint8))
+    packed = empty(lib.hero_kquant_packed_bytes(wtype, n, k))
+    check(lib.hero_kquant_pack(wtype, ptr(raw), ptr(packed), n, k, stream()))
+    return packed
+
+
 def kquant_dev(lib, wtype, w, x, n, k):
     m = x.shape[0]
-    xd, wd = dev(x.astype(np.float32)), dev(w)
+    xd, wd = dev(x.astype(np.float32)), kquant_pack_dev(lib, wtype, w, n, k)
     act = empty(lib.hero_q8_K_act_bytes(m, k))
     check(lib.hero_q8_K_quantize(ptr(xd), ptr(act), m, k, stream()))
     y = empty(m * n * 4)
@@ -737,6 +745,90 @@ def test_kquant_gemm_matches_oracle_bitwise(lib, wtype, m, n, k):
     expect = oracle.matmul_kquant(wtype, w, n, k, x)
     bad = np.flatnonzero(bits(y).ravel() != bits(expect).ravel())
     assert bad.size == 0, f"{bad.size} outputs differ, first {bad[:5]}: {y.ravel()[bad[:3]]} vs {expect.ravel()[bad[:3]]}"
+
+
+# many activation rows (the prefill form: rows split over workgroups, each
+# workgroup's weights reused across its rows) and the LM-head shape
+@pytest.mark.parametrize("wtype", [12, 14])
+@pytest.mark.parametrize("m,n,k", [(130, 256, 1024), (37, 1024, 2816), (64, 8192, 4096)])
+def test_kquant_gemm_many_rows_matches_oracle_bitwise(lib, wtype, m, n, k):
+    rng = np.random.default_rng(wtype * 7 + m + n + k)
+    w = kquant_weights(rng, wtype, n, k)
+    x = (rng.standard_normal((m, k)) * np.exp(rng.uniform(-3, 3, (m, 1)))).astype(np.float32)
+    _, y = kquant_dev(lib, wtype, w, x, n, k)
+    expect = oracle.matmul_kquant(wtype, w, n, k, x)
+    bad = np.flatnonzero(bits(y).ravel() != bits(expect).ravel())
+    assert bad.size == 0, f"{bad.size} outputs differ, first {bad[:5]}"
+
+
+def q5k_weights(rng, n, k):
+    nb = n * (k // 256)
+    f16 = lambda a: np.asarray(a, np.float16).view(np.uint8).reshape(-1, 2)  # noqa: E731
+    w = np.concatenate([f16(rng.uniform(0.2, 2.0, nb) * 1e-2), f16(rng.uniform(0.0, 2.0, nb) * 1e-2),
+                        rng.integers(0, 256, (nb, 172)).astype(np.uint8)], axis=1)
+    return np.ascontiguousarray(w, np.uint8)
+
+
+def q5k_dev(lib, w, x, n, k):
+    m = x.shape[0]
+    wd, xd = kquant_pack_dev(lib, 13, w, n, k), dev(np.ascontiguousarray(x, np.float32))
+    y = empty(m * n * 4)
+    check(lib.hero_q5_K_gemm(ptr(wd), ptr(xd), ptr(y), m, n, k, stream()))
+    return host(y, np.float32).reshape(m, n)
+
+
+def test_q5_K_gemm_matches_reference_golden(lib, kernels_golden):
+    """Weight<4096,64>::matvec / ::matmul over random Q5_K blocks: the
+    reference's fp32-activation dequant-in-dot results"""
+    x = kernels_golden["in_kq_x"].reshape(4, 4096)
+    y = q5k_dev(lib, kernels_golden["in_kq_w5"], x, 64, 4096)
+    expect = kernels_golden["out_kq_y5"].reshape(5, 64)
+    assert np.array_equal(bits(y[0]), bits(expect[0]))
+    assert np.array_equal(bits(y), bits(expect[1:]))
+
+
+# the row-tile forms: 1 (decode), 4 (k <= 4096), 2 (k 8192), 1 (k 12288)
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (1, 12288, 1024), (3, 1001, 1024), (130, 512, 4096), (9, 300, 8192),
+                                   (5, 256, 12288), (17, 517, 2816)])
+def test_q5_K_gemm_matches_oracle_bitwise(lib, m, n, k):
+    rng = np.random.default_rng(m * 31 + n + k)
+    w = q5k_weights(rng, n, k)
+    x = (rng.standard_normal((m, k)) * np.exp(rng.uniform(-3, 3, (m, 1)))).astype(np.float32)
+    y = q5k_dev(lib, w, x, n, k)
+    expect = oracle.linear(oracle.Q5_K, w, n, k, x)
+    bad = np.flatnonzero(bits(y).ravel() != bits(expect).ravel())
+    assert bad.size == 0, f"{bad.size} outputs differ, first {bad[:5]}"
+
+
+@pytest.mark.parametrize("wtype,name", [(12, "kq_w4"), (13, "kq_w5"), (14, "kq_w6")])
+def test_kquant_dequant_rows_match_reference_golden(lib, kernels_golden, wtype, name):
+    """Weight::dequant_row of rows 0 and 37 (the embedding gather), the
+    reference's own values; plus rows of a random tensor against the oracle
+    and an out-of-range id, which gives zeros"""
+    w = kernels_golden[f"in_{name}"]
+    wd = kquant_pack_dev(lib, wtype, w, 64, 4096)
+    ids = dev(np.array([0, 37, 63, 64], np.int32))
+    out = empty(4 * 4096 * 4)
+    check(lib.hero_kquant_dequant_rows(wtype, ptr(wd), 64, 4096, ptr(ids), 4, ptr(out), stream()))
+    got = host(out, np.float32).reshape(4, 4096)
+    expect = kernels_golden["out_kq_dq" + {12: "4", 13: "5", 14: "6"}[wtype]].reshape(2, 4096)
+    assert np.array_equal(bits(got[:2]), bits(expect))
+    assert np.array_equal(bits(got[2]), bits(oracle.dequant_rows(wtype, np.ascontiguousarray(w).reshape(64, -1)[63], 1, 4096)[0]))
+    assert not got[3].any()
+
+
+def test_kquant_pack_permutes_bytes_within_blocks(lib):
+    """the packed Q4_K / Q6_K tensor holds each super-block's bytes (Q6_K: all
+    but d, whose plane follows) as a permutation of the GGUF block"""
+    rng = np.random.default_rng(5)
+    for wtype, per in ((12, 144), (14, 210)):
+        w = kquant_weights(rng, wtype, 40, 1024)
+        got = host(kquant_pack_dev(lib, wtype, w, 40, 1024), np.uint8)
+        raw = w.reshape(-1, per)
+        body = got[:raw.shape[0] * (144 if wtype == 12 else 208)].reshape(raw.shape[0], -1)
+        assert np.array_equal(np.sort(body, axis=1), np.sort(raw[:, :body.shape[1]], axis=1))
+        if wtype == 14:
+            assert np.array_equal(got[raw.shape[0] * 208:], raw[:, 208:].ravel())
 
 
 # ---- top-k / top-p sampling -------------------------------------------------------------

@@ -50,14 +50,18 @@ class Logits:
         return len(self.values)
 
 
+def _kv_flags(kv_fp16: bool, kv_q8: bool) -> int:
+    return (_lib.HERO_STATE_KV_FP16 if kv_fp16 else 0) | (_lib.HERO_STATE_KV_Q8_0 if kv_q8 else 0)
+
+
 class PrefixState:
     """Device-resident carried state of one sequence (nm/src/qwen35.hpp:206-241).
-    kv_fp16 keeps the attention cache as fp16 pages (split-K attention);
-    gdn_chunked runs the delta-net prefill in its chunked form."""
+    kv_fp16 / kv_q8 keep the attention cache as fp16 / Q8_0 pages (split-K
+    attention); gdn_chunked runs the delta-net prefill in its chunked form."""
 
-    def __init__(self, model: "Qwen35Model", max_tokens: int, kv_fp16: bool = False, gdn_chunked: bool = False):
+    def __init__(self, model: "Qwen35Model", max_tokens: int, kv_fp16: bool = False, gdn_chunked: bool = False, kv_q8: bool = False):
         h = c_void_p()
-        flags = (_lib.HERO_STATE_KV_FP16 if kv_fp16 else 0) | (_lib.HERO_STATE_GDN_CHUNKED if gdn_chunked else 0)
+        flags = _kv_flags(kv_fp16, kv_q8) | (_lib.HERO_STATE_GDN_CHUNKED if gdn_chunked else 0)
         if flags:
             check(lib.hero_batch_state_create(model._h, max_tokens, 1, flags, byref(h)))
         else:
@@ -88,9 +92,9 @@ class BatchState:
     """`batch` independent sequences in one device state, decoded together
     (no counterpart in the reference, which carries one sequence per state)."""
 
-    def __init__(self, model: "Qwen35Model", max_tokens: int, batch: int, kv_fp16: bool = False):
+    def __init__(self, model: "Qwen35Model", max_tokens: int, batch: int, kv_fp16: bool = False, kv_q8: bool = False):
         h = c_void_p()
-        check(lib.hero_batch_state_create(model._h, max_tokens, batch, _lib.HERO_STATE_KV_FP16 if kv_fp16 else 0, byref(h)))
+        check(lib.hero_batch_state_create(model._h, max_tokens, batch, _kv_flags(kv_fp16, kv_q8), byref(h)))
         self._h = h
         self.model = model
         self.max_tokens = max_tokens
@@ -149,11 +153,11 @@ class Qwen35Model:
         except Exception:
             pass
 
-    def new_state(self, max_tokens: int | None = None, kv_fp16: bool = False, gdn_chunked: bool = False) -> PrefixState:
-        return PrefixState(self, max_tokens or min(self.CTX, 4096), kv_fp16, gdn_chunked)
+    def new_state(self, max_tokens: int | None = None, kv_fp16: bool = False, gdn_chunked: bool = False, kv_q8: bool = False) -> PrefixState:
+        return PrefixState(self, max_tokens or min(self.CTX, 4096), kv_fp16, gdn_chunked, kv_q8)
 
-    def new_batch_state(self, max_tokens: int, batch: int, kv_fp16: bool = False) -> BatchState:
-        return BatchState(self, max_tokens, batch, kv_fp16)
+    def new_batch_state(self, max_tokens: int, batch: int, kv_fp16: bool = False, kv_q8: bool = False) -> BatchState:
+        return BatchState(self, max_tokens, batch, kv_fp16, kv_q8)
 
     def forward_seq(self, state: BatchState, seq: int, rows: np.ndarray | None = None, ids=None, want_logits: bool = True) -> Logits | int:
         """forward() for sequence `seq` of a batch state."""

@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(HERE, "libhero_amd.so")
 HERO_OK, HERO_EINVAL, HERO_EHIP, HERO_ERANGE, HERO_ENOMEM, HERO_EIO = range(6)
 HERO_STATE_KV_FP16 = 1  # hero_batch_state_create flag: fp16 paged attention cache
 HERO_STATE_GDN_CHUNKED = 2  # hero_batch_state_create flag: chunked delta-net prefill
+HERO_STATE_KV_Q8_0 = 4  # hero_batch_state_create flag: Q8_0 paged attention cache
 
 
 class HeroError(RuntimeError):
@@ -53,6 +54,7 @@ class AttnPagedArgs(ctypes.Structure):
     _fields_ = [
         ("a", AttnDecodeArgs), ("pages", c_void_p), ("page_table", c_void_p),
         ("page_size", c_int32), ("max_pages", c_int32), ("work", c_void_p), ("work_bytes", c_int64),
+        ("q8", c_int32),
     ]
 
 
@@ -115,6 +117,7 @@ SIGNATURES = {
     "hero_gdn_prefill_chunked": (c_int, [POINTER(GdnDecodeArgs), c_void_p, c_int64, c_void_p]),
     "hero_attn_decode": (c_int, [POINTER(AttnDecodeArgs), c_void_p]),
     "hero_attn_paged_work_bytes": (c_int64, [c_int64, c_int32, c_int32, c_int32, c_int32]),
+    "hero_attn_page_bytes": (c_int64, [c_int32, c_int32, c_int32]),
     "hero_attn_decode_paged": (c_int, [POINTER(AttnPagedArgs), c_void_p]),
     "hero_model_open": (c_int, [c_char_p, POINTER(c_void_p)]),
     "hero_model_open_image": (c_int, [c_void_p, c_size_t, POINTER(c_void_p)]),

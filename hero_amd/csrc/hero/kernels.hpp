@@ -175,7 +175,11 @@ void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s);
 // out_f32, B, Hq, Hkv, Dh (k_cache, v_cache, scores and max_ctx are not).
 struct AttnPagedArgs {
     AttnDecodeArgs a;
-    uint16_t* pages;            // fp16 pool [page][2 = K, V][Hkv][page_size][Dh]
+    // fp16 pool [page][2 = K, V][Hkv][page_size][Dh]; with q8 set the pool is
+    // bytes, each page [2][Hkv][page_size][Dh] int8 then [2][Hkv][page_size][Dh/32]
+    // fp16 scales (Q8_0 rows: the reference's activation quantizer at append)
+    uint16_t* pages;
+    int q8;
     const int32_t* page_table;  // [B][max_pages] pool page of each page_size tokens (row 0 for all rows when shared_cache)
     int page_size;              // tokens per page
     int max_pages;              // pages per sequence: positions < max_pages * page_size
@@ -184,6 +188,8 @@ struct AttnPagedArgs {
     float* work;                // [B][Hq][nsplit][2 + Dh]: max, exp-sum, weighted V sum
 };
 constexpr int kAttnMaxSplit = 512;
+// bytes of one page of the pool
+inline int64_t attn_page_bytes(int64_t Hkv, int64_t page_size, bool q8) { return q8 ? 2 * Hkv * page_size * (128 + 8) : 2 * Hkv * page_size * 128 * 2; }
 constexpr int kAttnMaxGroup = 8;  // query heads per KV head
 // split and nsplit for B rows over at most max_ctx positions (window 0 = full)
 void attn_paged_plan(int64_t max_ctx, int window, int B, int Hkv, int* split, int* nsplit);

@@ -99,7 +99,10 @@ class Qwen35Model {
 public:
     class State;
     static constexpr int64_t kMaxBatch = 16;    // sequences per state (the skinny GEMM's rows)
-    static constexpr int64_t kPageTokens = 64;  // positions per page of the fp16 attention cache
+    static constexpr int64_t kPageTokens = 64;  // positions per page of the paged attention cache
+    // attention cache formats: the reference's fp32 rows (exact), fp16 pages
+    // or Q8_0 pages (split-K attention over either)
+    enum KvFormat : int { kKvF32 = 0, kKvF16 = 1, kKvQ8 = 2 };
 
     static std::unique_ptr<Qwen35Model> open(const std::string& gguf_path);
     static std::unique_ptr<Qwen35Model> open_image(const uint8_t* image, uint64_t size);
@@ -111,12 +114,12 @@ public:
     int64_t device_bytes() const { return device_bytes_; }
     hipStream_t stream() const { return stream_; }
 
-    // `batch` independent sequences of up to `max_tokens` each; `kv_fp16`
-    // keeps the attention cache as fp16 pages (split-K attention) instead of
-    // the reference's fp32 rows
-    // gdn_chunked runs the delta-net prefill in its chunked form (tolerance-equal
-    // to the token-serial recurrence instead of bit-equal)
-    std::unique_ptr<State> new_state(int64_t max_tokens, int64_t batch = 1, bool kv_fp16 = false, bool gdn_chunked = false) const;
+    // `batch` independent sequences of up to `max_tokens` each; `kv_format`
+    // keeps the attention cache as the reference's fp32 rows, or as fp16 /
+    // Q8_0 pages (split-K attention); gdn_chunked runs the delta-net prefill
+    // in its chunked form (tolerance-equal to the token-serial recurrence
+    // instead of bit-equal)
+    std::unique_ptr<State> new_state(int64_t max_tokens, int64_t batch = 1, int kv_format = kKvF32, bool gdn_chunked = false) const;
     // host rows out[n][D]
     void embed(const int32_t* ids, int64_t n, float* out) const;
     // T rows from host `rows` or from `ids`; logits / greedy id of the last row
@@ -199,14 +202,14 @@ public:
 
 private:
     friend class Qwen35Model;
-    explicit State(const Qwen35Model& m, int64_t max_tokens, int64_t batch, bool kv_fp16);
+    explicit State(const Qwen35Model& m, int64_t max_tokens, int64_t batch, int kv_format);
 
     const Qwen35Model& m_;
     int64_t max_tokens_ = 0, batch_ = 1;
-    // fp16 paged attention cache: per attention layer a pool of batch x
-    // max_pages pages; page_table_ [batch][max_pages] (sequence b owns pages
-    // b * max_pages ...); attn_work_ the split-K partials of a decode step
-    bool kv_fp16_ = false, gdn_chunked_ = false;
+    // paged attention cache (fp16 or Q8_0 rows): per attention layer a pool
+    // of batch x max_pages pages; page_table_ [batch][max_pages] (sequence b
+    // owns pages b * max_pages ...); attn_work_ the split-K partials of a step
+    bool kv_paged_ = false, kv_q8_ = false, gdn_chunked_ = false;
     int64_t max_pages_ = 0;
     std::vector<DeviceBuffer> kv_pages_;
     DeviceBuffer page_table_, attn_work_;

@@ -461,6 +461,11 @@ int64_t hero_attn_paged_work_bytes(int64_t max_ctx, int32_t window, int32_t b, i
     return attn_paged_work_floats(b, hq, nsplit) * 4;
 }
 
+int64_t hero_attn_page_bytes(int32_t hkv, int32_t page_size, int32_t q8) {
+    if (hkv <= 0 || page_size <= 0 || (q8 != 0 && q8 != 1)) return -1;
+    return attn_page_bytes(hkv, page_size, q8 != 0);
+}
+
 int hero_attn_decode_paged(const hero_attn_paged_args* p, void* stream) {
     return guard([&] {
         require(p != nullptr, "null args");
@@ -469,7 +474,10 @@ int hero_attn_decode_paged(const hero_attn_paged_args* p, void* stream) {
         require(g.a.Hq / g.a.Hkv <= kAttnMaxGroup, "at most 8 query heads per KV head");
         require(p->pages && p->page_table && p->work, "null pointer");
         require(p->page_size > 0 && p->max_pages > 0 && int64_t(p->page_size) * p->max_pages <= (int64_t(1) << 24), "bad page geometry");
+        require(p->q8 == 0 || p->q8 == 1, "q8 must be 0 or 1");
+        require(p->q8 == 0 || aligned(p->pages, 16), "Q8_0 pages must be 16-byte aligned");
         g.pages = p->pages;
+        g.q8 = p->q8;
         g.page_table = p->page_table;
         g.page_size = p->page_size;
         g.max_pages = p->max_pages;

@@ -104,9 +104,11 @@ int hero_state_create(const hero_model* model, int64_t max_tokens, hero_state** 
 int hero_batch_state_create(const hero_model* model, int64_t max_tokens, int32_t batch, uint32_t flags, hero_state** out) {
     return guard([&] {
         need(model && out, "null argument");
-        need((flags & ~(HERO_STATE_KV_FP16 | HERO_STATE_GDN_CHUNKED)) == 0, "unknown state flags");
+        need((flags & ~(HERO_STATE_KV_FP16 | HERO_STATE_KV_Q8_0 | HERO_STATE_GDN_CHUNKED)) == 0, "unknown state flags");
+        need((flags & HERO_STATE_KV_FP16) == 0 || (flags & HERO_STATE_KV_Q8_0) == 0, "choose one attention cache format");
         auto s = std::make_unique<hero_state>();
-        s->impl = model->impl->new_state(max_tokens, batch, (flags & HERO_STATE_KV_FP16) != 0, (flags & HERO_STATE_GDN_CHUNKED) != 0);
+        const int kv = (flags & HERO_STATE_KV_Q8_0) ? Qwen35Model::kKvQ8 : (flags & HERO_STATE_KV_FP16) ? Qwen35Model::kKvF16 : Qwen35Model::kKvF32;
+        s->impl = model->impl->new_state(max_tokens, batch, kv, (flags & HERO_STATE_GDN_CHUNKED) != 0);
         *out = s.release();
     });
 }

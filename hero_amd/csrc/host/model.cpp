@@ -415,17 +415,19 @@ void Qwen35Model::build_rope_table(int64_t positions) {
 }
 
 // ---- state --------------------------------------------------------------------------
-std::unique_ptr<Qwen35Model::State> Qwen35Model::new_state(int64_t max_tokens, int64_t batch, bool kv_fp16, bool gdn_chunked) const {
+std::unique_ptr<Qwen35Model::State> Qwen35Model::new_state(int64_t max_tokens, int64_t batch, int kv_format, bool gdn_chunked) const {
     if (max_tokens <= 0 || max_tokens > c_.CTX || max_tokens > rope_positions_) throw Error(HERO_ERANGE, "state: max_tokens must be in 1.." + std::to_string(std::min(c_.CTX, rope_positions_)));
     if (batch < 1 || batch > kMaxBatch) throw Error(HERO_EINVAL, "state: batch must be in 1.." + std::to_string(kMaxBatch));
-    if (kv_fp16 && c_.Hq / c_.Hkv > kAttnMaxGroup) throw Error(HERO_EINVAL, "state: the fp16 cache takes at most 8 query heads per KV head");
-    std::unique_ptr<State> st(new State(*this, max_tokens, batch, kv_fp16));
+    if (kv_format != kKvF32 && kv_format != kKvF16 && kv_format != kKvQ8) throw Error(HERO_EINVAL, "state: unknown attention cache format");
+    if (kv_format != kKvF32 && c_.Hq / c_.Hkv > kAttnMaxGroup) throw Error(HERO_EINVAL, "state: the paged cache takes at most 8 query heads per KV head");
+    std::unique_ptr<State> st(new State(*this, max_tokens, batch, kv_format));
     st->gdn_chunked_ = gdn_chunked;
     return st;
 }
 
-Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batch, bool kv_fp16)
-    : m_(m), max_tokens_(max_tokens), batch_(batch), kv_fp16_(kv_fp16), seq_tokens_(size_t(batch), 0) {
+Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batch, int kv_format)
+    : m_(m), max_tokens_(max_tokens), batch_(batch), kv_paged_(kv_format != kKvF32), kv_q8_(kv_format == kKvQ8), seq_tokens_(size_t(batch), 0) {
+    const bool kv_paged = kv_paged_;
     const ModelConfig& c = m.c_;
     const int64_t B = batch;
     int64_t n_in_max = 0;
@@ -455,7 +457,7 @@ Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batc
             scores_.emplace_back();
             conv_hist_.emplace_back(size_t(B * c.W * c.conv_channels()) * 4);
             delta_.emplace_back(size_t(B * c.Hv * c.Dk * c.Dv) * 4);
-        } else if (kv_fp16) {
+        } else if (kv_paged) {
             k_cache_.emplace_back();
             v_cache_.emplace_back();
             scores_.emplace_back();
@@ -470,9 +472,9 @@ Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batc
         }
     }
     kv_pages_.resize(size_t(c.L));
-    if (kv_fp16) {
+    if (kv_paged) {
         max_pages_ = (max_tokens + kPageTokens - 1) / kPageTokens;
-        const int64_t page_bytes = 2 * c.Hkv * kPageTokens * c.Dh * 2;
+        const int64_t page_bytes = attn_page_bytes(c.Hkv, kPageTokens, kv_q8_);
         for (int64_t l = 0; l < c.L; ++l)
             if (!c.is_recurrent(l)) kv_pages_[size_t(l)] = DeviceBuffer(size_t(B * max_pages_ * page_bytes));
         // sequence b owns pool pages b * max_pages ... (a server would map pages on demand)
@@ -527,12 +529,12 @@ void Qwen35Model::State::ensure_chunk(int64_t rows) {
     cgate_up_ = DeviceBuffer(size_t(rows * 2 * c.FF) * 4);
     cact_ff_ = DeviceBuffer(size_t(act_q8_bytes(rows, c.FF)));
     cq_rot_ = DeviceBuffer(size_t(rows * c.q_width()) * 4);
-    if (!kv_fp16_) cscores_ = DeviceBuffer(size_t(rows * c.Hq * max_tokens_) * 4);
+    if (!kv_paged_) cscores_ = DeviceBuffer(size_t(rows * c.Hq * max_tokens_) * 4);
     cpos_ = DeviceBuffer(size_t(rows) * 4);
     cids_ = DeviceBuffer(size_t(rows) * 4);
     cgdn_work_ = DeviceBuffer(size_t(gdn_prefill_work_bytes(rows, c.Hk, c.Hv)));
     if (m_.typed_) tchunk_ = std::make_unique<TypedScratch>(m_, rows);
-    if (kv_fp16_) {
+    if (kv_paged_) {
         int split = 0, nsplit = 0;
         attn_paged_plan(max_pages_ * kPageTokens, 0, int(rows), int(c.Hkv), &split, &nsplit);
         cattn_work_ = DeviceBuffer(size_t(attn_paged_work_floats(int(rows), int(c.Hq), nsplit)) * 4);
@@ -586,13 +588,14 @@ int64_t gemv_act(const void* w, const void* act, float* y, const float* r, int64
 }  // namespace
 
 void Qwen35Model::attention(State& st, size_t layer, AttnDecodeArgs a, const int32_t* pt, float* work, hipStream_t s) const {
-    if (!st.kv_fp16_) {
+    if (!st.kv_paged_) {
         launch_attn_decode(a, s);
         return;
     }
     AttnPagedArgs p{};
     p.a = a;
     p.pages = st.kv_pages_[layer].get<uint16_t>();
+    p.q8 = st.kv_q8_ ? 1 : 0;
     p.page_table = pt;
     p.page_size = int(kPageTokens);
     p.max_pages = int(st.max_pages_);
@@ -715,7 +718,7 @@ void Qwen35Model::typed_layers(State& st, TypedScratch& ts, float* x, float* h, 
             a.k_gamma = L.k_norm.get<float>();
             a.eps = c.eps;
             a.rope_cs = rope_cs_.get<float>();
-            if (!st.kv_fp16_) {
+            if (!st.kv_paged_) {
                 a.k_cache = st.k_cache_[size_t(l)].get<float>() + seq * st.max_tokens_ * c.kv_width();
                 a.v_cache = st.v_cache_[size_t(l)].get<float>() + seq * st.max_tokens_ * c.kv_width();
             }
@@ -922,7 +925,7 @@ void Qwen35Model::enqueue_chunk(State& st, int64_t seq, int64_t pos0, int64_t T,
             a.k_gamma = L.k_norm.get<float>();
             a.eps = c.eps;
             a.rope_cs = rope_cs_.get<float>();
-            if (!st.kv_fp16_) {  // the fp16 pages are found through the page table
+            if (!st.kv_paged_) {  // the fp16 pages are found through the page table
                 a.k_cache = st.k_cache_[size_t(l)].get<float>() + seq * st.max_tokens_ * c.kv_width();
                 a.v_cache = st.v_cache_[size_t(l)].get<float>() + seq * st.max_tokens_ * c.kv_width();
             }

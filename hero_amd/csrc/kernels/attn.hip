@@ -857,6 +857,26 @@ __device__ __forceinline__ int64_t page_offset(const AttnPagedArgs& p, const int
     return ((page * 2 + kv) * p.a.Hkv + g) * int64_t(p.page_size) * kAttnDim + int64_t(t % p.page_size) * kAttnDim;
 }
 
+// Q8_0 pages: byte offsets of the int8 row and of its four fp16 scales
+__device__ __forceinline__ int64_t q8_page_base(const AttnPagedArgs& p, const int32_t* pt, int t) {
+    return int64_t(pt[t / p.page_size]) * (2 * int64_t(p.a.Hkv) * p.page_size * (kAttnDim + 8));
+}
+__device__ __forceinline__ int64_t q8_row(const AttnPagedArgs& p, int t, int g, int kv) {
+    return ((int64_t(kv) * p.a.Hkv + g) * p.page_size + t % p.page_size);
+}
+
+// quantize_row_q8_0 (nm/src/quant_i8.hpp:70-80) of one 32-lane block held one
+// value per lane (lanes j .. j of a 32-aligned group): d = amax / 127 stored
+// through the reference's fp16 encoder, q = roundf(x / d)
+__device__ __forceinline__ int8_t q8_of_block(float x, uint16_t* dh) {
+    float amax = fabsf(x);
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    const float d = amax / 127.f;
+    const float id = d != 0.f ? 1.f / d : 0.f;
+    *dh = fp32_to_fp16_ref(d);
+    return int8_t(int(roundf(x * id)));
+}
+
 __global__ __launch_bounds__(kAttnDim) void attn_paged_prep_kernel(AttnPagedArgs p) {
     const AttnDecodeArgs& a = p.a;
     const int j = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
@@ -874,12 +894,29 @@ __global__ __launch_bounds__(kAttnDim) void attn_paged_prep_kernel(AttnPagedArgs
         const float k = norm_rope_head(P[a.k_off + int64_t(g) * kAttnDim + j], a.k_gamma, a.eps, cs, buf, scal, j);
         const float v = P[a.v_off + int64_t(g) * kAttnDim + j];
         const int32_t* pt = page_row(p, b);
-        p.pages[page_offset(p, pt, pos, g, 0) + j] = f32_to_f16_rne(k);
-        p.pages[page_offset(p, pt, pos, g, 1) + j] = f32_to_f16_rne(v);
+        if (p.q8) {
+            uint8_t* pool = reinterpret_cast<uint8_t*>(p.pages);
+            const int64_t base = q8_page_base(p, pt, pos);
+            const int64_t scales = base + 2 * int64_t(a.Hkv) * p.page_size * kAttnDim;
+            uint16_t dk, dv;
+            const int8_t qk = q8_of_block(k, &dk), qv = q8_of_block(v, &dv);
+            pool[base + q8_row(p, pos, g, 0) * kAttnDim + j] = uint8_t(qk);
+            pool[base + q8_row(p, pos, g, 1) * kAttnDim + j] = uint8_t(qv);
+            if ((j & 31) == 0) {
+                reinterpret_cast<uint16_t*>(pool + scales)[q8_row(p, pos, g, 0) * 4 + j / 32] = dk;
+                reinterpret_cast<uint16_t*>(pool + scales)[q8_row(p, pos, g, 1) * 4 + j / 32] = dv;
+            }
+        } else {
+            p.pages[page_offset(p, pt, pos, g, 0) + j] = f32_to_f16_rne(k);
+            p.pages[page_offset(p, pt, pos, g, 1) + j] = f32_to_f16_rne(v);
+        }
     }
 }
 
-// one workgroup per (KV head, split, row): the split's keys in tiles of 64
+// one workgroup per (KV head, split, row): the split's keys in tiles of 64.
+// Q8: the rows are Q8_0, each value read back as d * q (dequant_row_q8_0,
+// nm/src/quant.hpp:306-313), the fp32 value the oracle's Q8_0 cache holds.
+template <bool Q8>
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnPagedArgs p) {
     const AttnDecodeArgs& a = p.a;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -900,8 +937,10 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnPagedArgs p) {
     const int32_t* pt = page_row(p, b);
     __shared__ float qs[kAttnMaxGroup][kAttnDim];
     __shared__ float kt[kAttnDim][kPgTile + 1];  // K tile, channel-major
-    __shared__ uint32_t vt[kPgTile][kAttnDim / 2 + 1];  // V tile, rows of fp16 pairs
+    __shared__ uint32_t vt[kPgTile][kAttnDim / 2 + 1];  // V tile: rows of fp16 pairs, or (Q8) of int8 quads
+    __shared__ float vsc[Q8 ? kPgTile : 1][4];          // Q8: the V rows' block scales
     __shared__ float sc[kAttnMaxGroup][kAttnMaxSplit];
+    const uint8_t* pool = reinterpret_cast<const uint8_t*>(p.pages);
     for (int e = tid; e < Gs * kAttnDim; e += 256) qs[e / kAttnDim][e % kAttnDim] = a.q_rot[(int64_t(b) * a.Hq + int64_t(g) * Gs) * kAttnDim + e];
 
     // tile loads: thread -> row r = tid / 4, channels 32 * (tid % 4) .. +31 (four 16-byte loads)
@@ -909,20 +948,40 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnPagedArgs p) {
     const int ntiles = (n + kPgTile - 1) / kPgTile;
     for (int tile = 0; tile < ntiles; ++tile) {
         const int t = t0 + tile * kPgTile + r;
-        uint4 raw[4] = {};
-        if (t < t1) {
-            const uint4* src = reinterpret_cast<const uint4*>(p.pages + page_offset(p, pt, t, g, 0) + cq);
+        if constexpr (Q8) {
+            // 32 int8 (block tid % 4 of the row) and the block's scale
+            uint4 raw[2] = {};
+            uint16_t dh = 0;
+            if (t < t1) {
+                const int64_t base = q8_page_base(p, pt, t), row = q8_row(p, t, g, 0);
+                const uint4* src = reinterpret_cast<const uint4*>(pool + base + row * kAttnDim + cq);
+                raw[0] = src[0], raw[1] = src[1];
+                dh = reinterpret_cast<const uint16_t*>(pool + base + 2 * int64_t(a.Hkv) * p.page_size * kAttnDim)[row * 4 + cq / 32];
+            }
+            __syncthreads();  // the previous tile's readers are done
+            const float d = half_bits_to_f32(dh);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) raw[u] = src[u];
-        }
-        __syncthreads();  // the previous tile's readers are done
+            for (int u = 0; u < 2; ++u) {
+                const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+                for (int e = 0; e < 16; ++e) kt[cq + 16 * u + e][r] = d * float(int8_t((w[e / 4] >> (8 * (e % 4))) & 0xFFu));
+            }
+        } else {
+            uint4 raw[4] = {};
+            if (t < t1) {
+                const uint4* src = reinterpret_cast<const uint4*>(p.pages + page_offset(p, pt, t, g, 0) + cq);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                kt[cq + 8 * u + 2 * e][r] = half_bits_to_f32(uint16_t(w[e] & 0xFFFFu));
-                kt[cq + 8 * u + 2 * e + 1][r] = half_bits_to_f32(uint16_t(w[e] >> 16));
+                for (int u = 0; u < 4; ++u) raw[u] = src[u];
+            }
+            __syncthreads();  // the previous tile's readers are done
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    kt[cq + 8 * u + 2 * e][r] = half_bits_to_f32(uint16_t(w[e] & 0xFFFFu));
+                    kt[cq + 8 * u + 2 * e + 1][r] = half_bits_to_f32(uint16_t(w[e] >> 16));
+                }
             }
         }
         __syncthreads();
@@ -957,19 +1016,34 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnPagedArgs p) {
     float o0[kAttnMaxGroup / 4] = {}, o1[kAttnMaxGroup / 4] = {};
     for (int tile = 0; tile < ntiles; ++tile) {
         const int t = t0 + tile * kPgTile + r;
-        uint4 raw[4] = {};
-        if (t < t1) {
-            const uint4* src = reinterpret_cast<const uint4*>(p.pages + page_offset(p, pt, t, g, 1) + cq);
+        if constexpr (Q8) {
+            uint4 raw[2] = {};
+            uint16_t dh = 0;
+            if (t < t1) {
+                const int64_t base = q8_page_base(p, pt, t), row = q8_row(p, t, g, 1);
+                const uint4* src = reinterpret_cast<const uint4*>(pool + base + row * kAttnDim + cq);
+                raw[0] = src[0], raw[1] = src[1];
+                dh = reinterpret_cast<const uint16_t*>(pool + base + 2 * int64_t(a.Hkv) * p.page_size * kAttnDim)[row * 4 + cq / 32];
+            }
+            __syncthreads();  // sc complete (first tile) / previous tile's readers done
+            vt[r][cq / 4 + 0] = raw[0].x, vt[r][cq / 4 + 1] = raw[0].y, vt[r][cq / 4 + 2] = raw[0].z, vt[r][cq / 4 + 3] = raw[0].w;
+            vt[r][cq / 4 + 4] = raw[1].x, vt[r][cq / 4 + 5] = raw[1].y, vt[r][cq / 4 + 6] = raw[1].z, vt[r][cq / 4 + 7] = raw[1].w;
+            vsc[r][cq / 32] = half_bits_to_f32(dh);
+        } else {
+            uint4 raw[4] = {};
+            if (t < t1) {
+                const uint4* src = reinterpret_cast<const uint4*>(p.pages + page_offset(p, pt, t, g, 1) + cq);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) raw[u] = src[u];
-        }
-        __syncthreads();  // sc complete (first tile) / previous tile's readers done
+                for (int u = 0; u < 4; ++u) raw[u] = src[u];
+            }
+            __syncthreads();  // sc complete (first tile) / previous tile's readers done
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            vt[r][cq / 2 + 4 * u + 0] = raw[u].x;
-            vt[r][cq / 2 + 4 * u + 1] = raw[u].y;
-            vt[r][cq / 2 + 4 * u + 2] = raw[u].z;
-            vt[r][cq / 2 + 4 * u + 3] = raw[u].w;
+            for (int u = 0; u < 4; ++u) {
+                vt[r][cq / 2 + 4 * u + 0] = raw[u].x;
+                vt[r][cq / 2 + 4 * u + 1] = raw[u].y;
+                vt[r][cq / 2 + 4 * u + 2] = raw[u].z;
+                vt[r][cq / 2 + 4 * u + 3] = raw[u].w;
+            }
         }
         __syncthreads();
         const int rows = min(kPgTile, n - tile * kPgTile);
@@ -979,9 +1053,18 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnPagedArgs p) {
             if (h < Gs) {
                 for (int jr = 0; jr < rows; ++jr) {
                     const float pj = sc[h][tile * kPgTile + jr];
-                    const uint32_t v2 = vt[jr][lane];
-                    o0[hh] += pj * half_bits_to_f32(uint16_t(v2 & 0xFFFFu));
-                    o1[hh] += pj * half_bits_to_f32(uint16_t(v2 >> 16));
+                    if constexpr (Q8) {
+                        // channels 2 lane, 2 lane + 1: bytes (2 lane) % 4 .. +1 of dword lane / 2
+                        const uint32_t q4 = vt[jr][lane >> 1];
+                        const int sh = 16 * (lane & 1);
+                        const float d = vsc[jr][lane >> 4];
+                        o0[hh] += pj * (d * float(int8_t((q4 >> sh) & 0xFFu)));
+                        o1[hh] += pj * (d * float(int8_t((q4 >> (sh + 8)) & 0xFFu)));
+                    } else {
+                        const uint32_t v2 = vt[jr][lane];
+                        o0[hh] += pj * half_bits_to_f32(uint16_t(v2 & 0xFFFFu));
+                        o1[hh] += pj * half_bits_to_f32(uint16_t(v2 >> 16));
+                    }
                 }
             }
         }
@@ -1045,7 +1128,10 @@ int64_t attn_paged_work_floats(int B, int Hq, int nsplit) { return int64_t(B) * 
 void launch_attn_paged(const AttnPagedArgs& p, hipStream_t s) {
     const AttnDecodeArgs& a = p.a;
     hipLaunchKernelGGL(attn_paged_prep_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, p);
-    hipLaunchKernelGGL(attn_split_kernel, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), 0, s, p);
+    if (p.q8)
+        hipLaunchKernelGGL(attn_split_kernel<true>, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL(attn_split_kernel<false>, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), 0, s, p);
     hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, p);
 }
 

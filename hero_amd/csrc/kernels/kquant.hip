@@ -10,11 +10,12 @@
 //   Weight::matvec/matmul  nm/src/quant_i8.hpp:352-383, 415-495
 //   dequant_to_f32         nm/src/quant.hpp:322-395
 //
-// Weights are repacked once at load by a byte permutation per super-block
-// (same size as GGUF; kq_pack_kernel): the bytes of the four positions
-// 32j + 8i + l (i = 0..3) that share sub-block j and residue l = p % 8 -- the
-// positions whose products the reference adds into one of its eight sums --
-// become one dword, so each such group is one 4-way int8 dot. A Q8_K
+// Weights are repacked once at load (kq_pack_kernel): within a super-block the
+// bytes of the four positions 32j + 8i + l (i = 0..3) that share sub-block j
+// and residue l = p % 8 -- the positions whose products the reference adds
+// into one of its eight sums -- become one dword, so each such group is one
+// 4-way int8 dot; the blocks are laid out so that each wave's weight loads
+// are contiguous (the tiled layout below). A Q8_K
 // activation row is K/256 GGUF blocks of 292 bytes {fp32 d, int8 qs[256],
 // int16 bsums[16]} followed by the same residue regrouping of its int8.
 //
@@ -36,6 +37,31 @@ namespace {
 
 constexpr int kQ8KBytes = 292;
 constexpr int kKqThreads = 256;
+
+// ---- the packed weight layout -------------------------------------------------------
+// A workgroup owns R = 256 / nb consecutive output rows (a tile) and its lane
+// `item` = b * R + r the super-block b of row r. Packed, each tile's blocks are
+// stored wave by wave (64 items) as structure-of-arrays: 16-byte chunk u of the
+// 64 blocks of a wave is 1 KiB of contiguous memory, so each weight load of a
+// wave is one coalesced access. Chunks per block: Q4_K 9 (16-byte header, 8 of
+// residue-regrouped quants), Q5_K 11 (the GGUF bytes), Q6_K 13 (8 of ql, 4 of
+// qh, both regrouped, 1 of scales) plus a plane of fp16 d, one per slot.
+__host__ __device__ inline int kq_rows_per_tile(int64_t K) { return int(K / 256) >= kKqThreads ? 1 : kKqThreads / int(K / 256); }
+__host__ __device__ inline int kq_waves_per_tile(int64_t K) { return (kq_rows_per_tile(K) * int(K / 256) + 63) / 64; }
+__host__ __device__ inline int kq_chunks(int type) { return type == 12 ? 9 : type == 13 ? 11 : 13; }
+// slot of block (n, b): (tile * waves_per_tile + wave) * 64 + lane
+__host__ __device__ inline int64_t kq_slot(int64_t n, int b, int64_t K) {
+    const int R = kq_rows_per_tile(K);
+    const int64_t t = n / R;
+    const int item = b * R + int(n % R);
+    return (t * kq_waves_per_tile(K) + item / 64) * 64 + item % 64;
+}
+// uint4 index of chunk u of the block in `slot`
+__host__ __device__ inline int64_t kq_chunk_index(int64_t slot, int u, int U) { return ((slot / 64) * U + u) * 64 + slot % 64; }
+__host__ __device__ inline int64_t kq_slots(int64_t N, int64_t K) {
+    const int R = kq_rows_per_tile(K);
+    return (N + R - 1) / R * kq_waves_per_tile(K) * 64;
+}
 
 __device__ __forceinline__ int nearest_int_magic(float v) {
     const float t = v + 12582912.f;  // 1.5 * 2^23: rounds to nearest, ties to even
@@ -137,7 +163,8 @@ __global__ __launch_bounds__(kKqThreads) void kq_gemm_kernel(const uint8_t* __re
     const int64_t m_end = min(M, m_begin + rows_per_group);
     const int b = tid / R, r = tid % R;
     const bool active = tid < items && n0 + r < N;
-    const int64_t blk = (n0 + r) * nb + b;
+    // this lane's slot: tile blockIdx.x, item tid
+    const int64_t slot = (int64_t(blockIdx.x) * ((items + 63) / 64) + tid / 64) * 64 + tid % 64;
 
     // the block: Q4_K 16-byte header (d, dmin, packed scales) + 32 residue
     // dwords; Q6_K 32 low-nibble dwords, 16 high-bit dwords, 16 int8 scales, d
@@ -145,8 +172,9 @@ __global__ __launch_bounds__(kKqThreads) void kq_gemm_kernel(const uint8_t* __re
     int sc[TYPE == 12 ? 8 : 16], mn[8];
     float wd = 0.f, wdmin = 0.f;
     if (active) {
+        const uint4* w4 = reinterpret_cast<const uint4*>(w);
         if constexpr (TYPE == 12) {
-            const uint4* src = reinterpret_cast<const uint4*>(w + blk * 144);
+            const uint4* src = w4 + kq_chunk_index(slot, 0, 9);  // chunk u at src[64 u]
             const uint4 hdr = src[0];
             const uint8_t* hb = reinterpret_cast<const uint8_t*>(&hdr);
 #pragma unroll
@@ -155,22 +183,22 @@ __global__ __launch_bounds__(kKqThreads) void kq_gemm_kernel(const uint8_t* __re
             wdmin = half_bits_to_f32(uint16_t(hdr.x >> 16));
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const uint4 v = src[1 + i];
+                const uint4 v = src[64 * (1 + i)];
                 q[4 * i] = v.x, q[4 * i + 1] = v.y, q[4 * i + 2] = v.z, q[4 * i + 3] = v.w;
             }
         } else {
-            const uint4* src = reinterpret_cast<const uint4*>(w + blk * 208);
+            const uint4* src = w4 + kq_chunk_index(slot, 0, 13);
 #pragma unroll
             for (int i = 0; i < 12; ++i) {
-                const uint4 v = src[i];
+                const uint4 v = src[64 * i];
                 q[4 * i] = v.x, q[4 * i + 1] = v.y, q[4 * i + 2] = v.z, q[4 * i + 3] = v.w;
             }
-            const uint4 sv = src[12];
+            const uint4 sv = src[64 * 12];
             const int8_t* s8 = reinterpret_cast<const int8_t*>(&sv);
 #pragma unroll
             for (int g = 0; g < 16; ++g) sc[g] = s8[g];
-            const uint16_t* dplane = reinterpret_cast<const uint16_t*>(w + N * nb * 208);
-            wd = half_bits_to_f32(dplane[blk]);
+            const uint16_t* dplane = reinterpret_cast<const uint16_t*>(w4 + kq_slots(N, K) * 13);
+            wd = half_bits_to_f32(dplane[slot]);
         }
     }
 
@@ -282,7 +310,8 @@ __global__ __launch_bounds__(kKqThreads) void q5k_gemm_kernel(const uint8_t* __r
     uint32_t qh[8], qs[32];
     float d1[8], m1[8];
     if (active) {
-        const uint4* src = reinterpret_cast<const uint4*>(w + ((n0 + r) * nb + b) * 176);
+        const int64_t slot = (int64_t(blockIdx.x) * ((items + 63) / 64) + tid / 64) * 64 + tid % 64;
+        const uint4* src = reinterpret_cast<const uint4*>(w) + kq_chunk_index(slot, 0, 11);  // chunk u at src[64 u]
         const uint4 hdr = src[0];
         const uint8_t* hb = reinterpret_cast<const uint8_t*>(&hdr);
         const float d = half_bits_to_f32(uint16_t(hdr.x & 0xFFFF)), dmin = half_bits_to_f32(uint16_t(hdr.x >> 16));
@@ -293,11 +322,11 @@ __global__ __launch_bounds__(kKqThreads) void q5k_gemm_kernel(const uint8_t* __r
             d1[j] = d * float(sc);
             m1[j] = dmin * float(m);
         }
-        const uint4 h0 = src[1], h1 = src[2];
+        const uint4 h0 = src[64], h1 = src[128];
         qh[0] = h0.x, qh[1] = h0.y, qh[2] = h0.z, qh[3] = h0.w, qh[4] = h1.x, qh[5] = h1.y, qh[6] = h1.z, qh[7] = h1.w;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint4 v = src[3 + i];
+            const uint4 v = src[64 * (3 + i)];
             qs[4 * i] = v.x, qs[4 * i + 1] = v.y, qs[4 * i + 2] = v.z, qs[4 * i + 3] = v.w;
         }
     }
@@ -366,49 +395,51 @@ __global__ __launch_bounds__(kKqThreads) void q5k_gemm_kernel(const uint8_t* __r
     }
 }
 
-// GGUF -> packed K-quant layout: a byte permutation per super-block.
-// Q4_K keeps its 16-byte header; its 128 quant bytes become 32 residue dwords:
-// dword 8c + l, byte i = qs[32c + 8i + l] (low nibbles: sub-block 2c, high:
-// 2c + 1). Q6_K's 128 ql bytes take the same permutation (pair c = sub-blocks
-// {j, j + 2} of half c / 2), its 64 qh bytes too (dword 8h + l, byte i =
-// qh[32h + 8i + l]: 2-bit fields of sub-blocks 4h .. 4h + 3), then the 16
-// scales: 208 bytes; the fp16 d of every block follow in a plane of their own.
-__global__ __launch_bounds__(256) void kq_pack_kernel(int type, const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t nblocks) {
+// GGUF -> packed K-quant layout. Within a block: Q4_K keeps its 16-byte
+// header; its 128 quant bytes become 32 residue dwords: dword 8c + l, byte i =
+// qs[32c + 8i + l] (low nibbles: sub-block 2c, high: 2c + 1). Q6_K's 128 ql
+// bytes take the same permutation (pair c = sub-blocks {j, j + 2} of half
+// c / 2), its 64 qh bytes too (dword 8h + l, byte i = qh[32h + 8i + l]: 2-bit
+// fields of sub-blocks 4h .. 4h + 3), then the 16 scales; its d goes to the d
+// plane. Q5_K keeps its bytes. The blocks then take the slots of the tiled
+// structure-of-arrays layout above. One lane per output dword of a block.
+__global__ __launch_bounds__(256) void kq_pack_kernel(int type, const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t N, int64_t K) {
+    const int nb = int(K / 256), U = kq_chunks(type), words = 4 * U + 1;  // + the Q6_K d
     const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    constexpr int kWords = 56;  // output dwords handled per block: 4 header/scales + 32 + 16 + 4
-    if (gid >= nblocks * kWords) return;
-    const int64_t blk = gid / kWords;
-    const int wi = int(gid % kWords);
-    if (type == 12) {
-        const uint8_t* s = src + blk * 144;
-        uint8_t* o = dst + blk * 144;
-        if (wi < 4) {
-            reinterpret_cast<uint32_t*>(o)[wi] = uint32_t(s[4 * wi]) | (uint32_t(s[4 * wi + 1]) << 8) | (uint32_t(s[4 * wi + 2]) << 16) | (uint32_t(s[4 * wi + 3]) << 24);
-        } else if (wi < 36) {
-            const int dw = wi - 4, c = dw / 8, l = dw % 8;
-            const uint8_t* g = s + 16 + 32 * c + l;
-            reinterpret_cast<uint32_t*>(o + 16)[dw] = uint32_t(g[0]) | (uint32_t(g[8]) << 8) | (uint32_t(g[16]) << 16) | (uint32_t(g[24]) << 24);
-        }
+    if (gid >= N * nb * words) return;
+    const int64_t f = gid / words;  // GGUF block: row f / nb, block f % nb
+    const int wi = int(gid % words);
+    const int64_t slot = kq_slot(f / nb, int(f % nb), K);
+    const int bytes = type == 12 ? 144 : type == 13 ? 176 : 210;
+    const uint8_t* s = src + f * bytes;
+    if (wi == 4 * U) {  // Q6_K d
+        if (type == 14) reinterpret_cast<uint16_t*>(dst + kq_slots(N, K) * 13 * 16)[slot] = uint16_t(s[208] | (s[209] << 8));
         return;
     }
-    // Q6_K
-    const uint8_t* s = src + blk * 210;
-    uint8_t* o = dst + blk * 208;
-    if (wi < 32) {
-        const int c = wi / 8, l = wi % 8;
-        const uint8_t* g = s + 32 * c + l;
-        reinterpret_cast<uint32_t*>(o)[wi] = uint32_t(g[0]) | (uint32_t(g[8]) << 8) | (uint32_t(g[16]) << 16) | (uint32_t(g[24]) << 24);
+    const uint8_t* g;   // the dword's four source bytes: g[0], g[step], g[2 step], g[3 step]
+    int step = 1;
+    if (type == 13) {
+        g = s + 4 * wi;
+    } else if (type == 12) {
+        if (wi < 4) {
+            g = s + 4 * wi;
+        } else {
+            const int dw = wi - 4;
+            g = s + 16 + 32 * (dw / 8) + dw % 8;
+            step = 8;
+        }
+    } else if (wi < 32) {
+        g = s + 32 * (wi / 8) + wi % 8;
+        step = 8;
     } else if (wi < 48) {
-        const int dw = wi - 32, h = dw / 8, l = dw % 8;
-        const uint8_t* g = s + 128 + 32 * h + l;
-        reinterpret_cast<uint32_t*>(o + 128)[dw] = uint32_t(g[0]) | (uint32_t(g[8]) << 8) | (uint32_t(g[16]) << 16) | (uint32_t(g[24]) << 24);
-    } else if (wi < 52) {
-        const int dw = wi - 48;
-        const uint8_t* g = s + 192 + 4 * dw;
-        reinterpret_cast<uint32_t*>(o + 192)[dw] = uint32_t(g[0]) | (uint32_t(g[1]) << 8) | (uint32_t(g[2]) << 16) | (uint32_t(g[3]) << 24);
-    } else if (wi == 52) {
-        reinterpret_cast<uint16_t*>(dst + nblocks * 208)[blk] = uint16_t(s[208] | (s[209] << 8));
+        const int dw = wi - 32;
+        g = s + 128 + 32 * (dw / 8) + dw % 8;
+        step = 8;
+    } else {
+        g = s + 192 + 4 * (wi - 48);
     }
+    const uint32_t v = uint32_t(g[0]) | (uint32_t(g[step]) << 8) | (uint32_t(g[2 * step]) << 16) | (uint32_t(g[3 * step]) << 24);
+    reinterpret_cast<uint32_t*>(dst)[kq_chunk_index(slot, wi / 4, U) * 4 + wi % 4] = v;
 }
 
 // Weight::dequant_row (nm/src/quant.hpp:322-395) of the rows `ids` of a
@@ -416,7 +447,7 @@ __global__ __launch_bounds__(256) void kq_pack_kernel(int type, const uint8_t* _
 // d1 = d * sc, m1 = dmin * m; Q6_K (d * sc) * (q - 32). grid (nb, n_ids), 256 lanes.
 __global__ __launch_bounds__(256) void kq_dequant_rows_kernel(int type, const uint8_t* __restrict__ w, int64_t N, int K, const int32_t* __restrict__ ids,
                                                               float* __restrict__ out) {
-    const int nb = K >> 8, b = blockIdx.x, p = threadIdx.x;
+    const int b = blockIdx.x, p = threadIdx.x;
     const int64_t t = blockIdx.y;
     const int32_t id = ids[t];
     float* o = out + t * K + 256 * b + p;
@@ -424,30 +455,35 @@ __global__ __launch_bounds__(256) void kq_dequant_rows_kernel(int type, const ui
         *o = 0.f;
         return;
     }
-    const int64_t blk = int64_t(id) * nb + b;
+    const int64_t slot = kq_slot(id, b, K);
+    const int U = kq_chunks(type);
+    // byte o of the block in `slot`
+    auto at = [&](int o) { return w[kq_chunk_index(slot, o >> 4, U) * 16 + (o & 15)]; };
     const int j = p >> 5, i = (p & 31) >> 3, l = p & 7;
     if (type == 12 || type == 13) {
-        const uint8_t* s = w + blk * (type == 12 ? 144 : 176);
+        uint8_t hdr[16];
+#pragma unroll
+        for (int o = 0; o < 16; ++o) hdr[o] = at(o);
+        const uint8_t* s = hdr;
         const float d = half_bits_to_f32(uint16_t(s[0] | (s[1] << 8))), dmin = half_bits_to_f32(uint16_t(s[2] | (s[3] << 8)));
         int sc, m;
         scale_min_k4(s + 4, j, sc, m);
         const float dd = d * float(sc), mm = dmin * float(m);
         int q;
         if (type == 12) {
-            q = (s[16 + 4 * (8 * (j >> 1) + l) + i] >> (4 * (j & 1))) & 0xF;
+            q = (at(16 + 4 * (8 * (j >> 1) + l) + i) >> (4 * (j & 1))) & 0xF;
         } else {
             const int e = p & 31;
-            q = ((s[48 + 32 * (j >> 1) + e] >> (4 * (j & 1))) & 0xF) + (((s[16 + e] >> j) & 1) << 4);
+            q = ((at(48 + 32 * (j >> 1) + e) >> (4 * (j & 1))) & 0xF) + (((at(16 + e) >> j) & 1) << 4);
         }
         *o = dd * float(q) - mm;
         return;
     }
-    const uint8_t* s = w + blk * 208;
     const int cp = 2 * (j >> 2) + (j & 1);
-    const int lo = (s[4 * (8 * cp + l) + i] >> (4 * ((j & 3) >> 1))) & 0xF;
-    const int hi = (s[128 + 4 * (8 * (j >> 2) + l) + i] >> (2 * (j & 3))) & 3;
-    const float d = half_bits_to_f32(reinterpret_cast<const uint16_t*>(w + N * nb * 208)[blk]);
-    const int sc = int(int8_t(s[192 + (p >> 4)]));
+    const int lo = (at(4 * (8 * cp + l) + i) >> (4 * ((j & 3) >> 1))) & 0xF;
+    const int hi = (at(128 + 4 * (8 * (j >> 2) + l) + i) >> (2 * (j & 3))) & 3;
+    const float d = half_bits_to_f32(reinterpret_cast<const uint16_t*>(w + kq_slots(N, K) * 13 * 16)[slot]);
+    const int sc = int(int8_t(at(192 + (p >> 4))));
     *o = d * float(sc) * float((lo | (hi << 4)) - 32);
 }
 
@@ -467,27 +503,23 @@ void launch_quantize_q8_K(const float* x, void* act, int64_t M, int64_t K, hipSt
 }
 
 int64_t kquant_packed_bytes(int type, int64_t N, int64_t K) {
-    const int64_t nb = K / 256;
-    return N * nb * (type == 12 ? 144 : type == 13 ? 176 : 210);
+    const int64_t slots = kq_slots(N, K);
+    return slots * kq_chunks(type) * 16 + (type == 14 ? slots * 2 : 0);
 }
 
 void launch_kquant_pack(int type, const void* gguf, void* packed, int64_t N, int64_t K, hipStream_t s) {
-    const int64_t nblocks = N * (K / 256);
-    if (type == 13) {  // Q5_K keeps the GGUF layout
-        hip_check(hipMemcpyAsync(packed, gguf, size_t(nblocks * 176), hipMemcpyDeviceToDevice, s), "Q5_K copy");
-        return;
-    }
-    const int64_t work = nblocks * 56;
+    // the padding slots stay zero (never read)
+    hip_check(hipMemsetAsync(packed, 0, size_t(kquant_packed_bytes(type, N, K)), s), "pack clear");
+    const int64_t work = N * (K / 256) * (4 * kq_chunks(type) + 1);
     hipLaunchKernelGGL(kq_pack_kernel, dim3(unsigned((work + 255) / 256)), dim3(256), 0, s, type, static_cast<const uint8_t*>(gguf),
-                       static_cast<uint8_t*>(packed), nblocks);
+                       static_cast<uint8_t*>(packed), N, K);
 }
 
 // rows per workgroup (R) and activation rows per workgroup for an (M, N, K)
 // product: R * nb <= 256 lanes; rows split over grid.y while that leaves at
 // least ~2048 workgroups
 static void kq_plan(int64_t M, int64_t N, int64_t K, int tile, int* R, int* rows_per_group) {
-    const int nb = int(K / 256);
-    *R = std::max(1, kKqThreads / nb);
+    *R = kq_rows_per_tile(K);  // the packed layout's tile
     const int64_t gx = (N + *R - 1) / *R;
     const int64_t want_y = std::max<int64_t>(1, (2048 + gx - 1) / gx);
     const int64_t gy = std::min<int64_t>(want_y, (M + tile - 1) / tile);

@@ -177,18 +177,22 @@ def bench_gemv(lib, replays: int = 20, batches=GEMV_BATCHES):
     return rows
 
 
-# ---- K-quant GEMV / GEMM (Q4_K, Q6_K over GGUF-layout weights) ---------------------------------------
+# ---- K-quant GEMV / GEMM (Q4_K, Q6_K against Q8_K rows; Q5_K against fp32 rows) ---------------------
 KQUANT_SHAPES = [(4096, 4096), (4096, 12288), (12288, 4096)]
+KQUANT_BATCHES = (1, 16, 512)
 
 
-def bench_kquant(lib, replays: int = 20, batches=(1, 16)):
+def bench_kquant(lib, replays: int = 20, batches=KQUANT_BATCHES):
+    """packed K-quant weights (hero_kquant_pack of random GGUF blocks with sane
+    fp16 scales); algorithmic bytes = weights + activation rows as read (Q8_K
+    blocks and their regrouped copy, or fp32) + outputs"""
     from ._lib import check
 
     t = _torch()
     gen = t.Generator(device="cuda")
     gen.manual_seed(4321)
     rows = []
-    for wtype, name, bb in ((12, "Q4_K", 144), (14, "Q6_K", 210)):
+    for wtype, name, bb in ((12, "Q4_K", 144), (13, "Q5_K", 176), (14, "Q6_K", 210)):
         for k, n in KQUANT_SHAPES:
             nb = n * (k // 256)
             wbytes = nb * bb
@@ -197,28 +201,40 @@ def bench_kquant(lib, replays: int = 20, batches=(1, 16)):
             for _ in range(copies):
                 w = t.randint(0, 256, (nb, bb), dtype=t.uint8, device="cuda", generator=gen)
                 d = (t.rand(nb, device="cuda", generator=gen) * 0.01 + 0.002).half().view(t.uint8).view(nb, 2)
-                if wtype == 12:
+                if wtype in (12, 13):
                     w[:, 0:2] = d
                     w[:, 2:4] = d
                 else:
                     w[:, 208:210] = d
-                weights.append(w.contiguous())
+                packed = _bytes(lib.hero_kquant_packed_bytes(wtype, n, k))
+                check(lib.hero_kquant_pack(wtype, _p(w), _p(packed), n, k, _stream()))
+                weights.append(packed)
+                del w
             for m in batches:
                 x = t.randn(m, k, device="cuda", generator=gen)
-                act = _bytes(lib.hero_q8_K_act_bytes(m, k))
-                check(lib.hero_q8_K_quantize(_p(x), _p(act), m, k, _stream()))
                 y = t.empty(m, n, device="cuda")
+                if wtype == 13:
+                    act_bytes = m * k * 4
 
-                def body():
-                    for w in weights:
-                        check(lib.hero_kquant_gemm(wtype, _p(w), _p(act), _p(y), m, n, k, _stream()))
+                    def body():
+                        for w in weights:
+                            check(lib.hero_q5_K_gemm(_p(w), _p(x), _p(y), m, n, k, _stream()))
+                else:
+                    act = _bytes(lib.hero_q8_K_act_bytes(m, k))
+                    act_bytes = lib.hero_q8_K_act_bytes(m, k)
+                    check(lib.hero_q8_K_quantize(_p(x), _p(act), m, k, _stream()))
 
-                sec = _time_graph(body, len(weights), replays)
-                nbytes = wbytes + m * k * 4 + m * n * 4
-                rows.append({"suite": "kquant", "kernel": f"kquant_gemm {name}", "K": k, "N": n, "M": m, "copies": copies,
-                             "us": sec * 1e6, "GB/s": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS})
+                    def body():
+                        for w in weights:
+                            check(lib.hero_kquant_gemm(wtype, _p(w), _p(act), _p(y), m, n, k, _stream()))
+
+                sec = _time_graph(body, len(weights), replays if m < 512 else 3)
+                nbytes = wbytes + act_bytes + m * n * 4
+                rows.append({"suite": "kquant", "kernel": f"kquant {name}", "K": k, "N": n, "M": m, "copies": copies,
+                             "us": sec * 1e6, "GB/s": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS,
+                             "Gweight/s": m * n * k / sec / 1e9})
                 print(json.dumps(rows[-1]), flush=True)
-                del act, y, x
+                del y, x
             del weights
             t.cuda.empty_cache()
     return rows

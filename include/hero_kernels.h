@@ -133,10 +133,12 @@ int hero_argmax(const float* logits, int64_t m, int64_t n, int32_t* out, uint64_
 int hero_argmax_noalloc(const float* logits, int64_t m, int64_t n, int32_t* out, void* stream);
 
 /* ---- K-quant weights (GGUF Q4_K = 12, Q5_K = 13, Q6_K = 14) ----------------
- * Weights are used in a packed form with the same byte count as the GGUF
- * tensor: hero_kquant_pack copies a device GGUF tensor (n rows of k/256
- * super-blocks of 144 / 176 / 210 bytes) into it (Q4_K and Q6_K regroup their
- * quant bytes by sub-block and residue; Q5_K is copied as is).
+ * Weights are used in a packed form of hero_kquant_packed_bytes(type, n, k)
+ * bytes (the GGUF tensor's bytes, its blocks in slots of a tiled layout with
+ * each wave's loads contiguous, padded to whole waves): hero_kquant_pack
+ * copies a device GGUF tensor (n rows of k/256 super-blocks of 144 / 176 / 210
+ * bytes) into it (Q4_K and Q6_K also regroup their quant bytes by sub-block
+ * and residue within each block).
  * hero_kquant_gemm replaces the int8-activation branch of Weight<In,Out>::matvec
  * / ::matmul (nm/src/quant_i8.hpp:352-383, 430-474) for Q4_K / Q6_K: the
  * activation rows are quantized to Q8_K (quantize_row_q8_K,
@@ -276,7 +278,14 @@ int hero_attn_decode(const hero_attn_decode_args* args, void* stream);
  * (not bit for bit). Pages hold page_size positions: pool layout
  * [page][2 = K, V][hkv][page_size][dh] fp16; page_table [b][max_pages].
  * In `a`, k_cache, v_cache, scores and max_ctx are unused; the cache spans
- * max_pages * page_size positions. */
+ * max_pages * page_size positions.
+ * q8 = 1: the pages hold Q8_0 rows instead (the K/V storage the reference
+ * plans, nm/INFERENCE_PLAN.md:235-236): each page is [2][hkv][page_size][dh]
+ * int8 followed by [2][hkv][page_size][dh/32] fp16 scales
+ * (hero_attn_page_bytes); a row is appended through the reference's
+ * activation quantizer (quant_i8.hpp:70-80) and read back as d * q
+ * (quant.hpp:306-313), so results equal the reference over those values to a
+ * few ulp. */
 typedef struct hero_attn_paged_args {
     hero_attn_decode_args a;
     uint16_t* pages;
@@ -284,7 +293,9 @@ typedef struct hero_attn_paged_args {
     int32_t page_size, max_pages;
     float* work;                /* split partials, hero_attn_paged_work_bytes */
     int64_t work_bytes;
+    int32_t q8;
 } hero_attn_paged_args;
+int64_t hero_attn_page_bytes(int32_t hkv, int32_t page_size, int32_t q8);
 int64_t hero_attn_paged_work_bytes(int64_t max_ctx, int32_t window, int32_t b, int32_t hq, int32_t hkv);
 int hero_attn_decode_paged(const hero_attn_paged_args* args, void* stream);
 

@@ -87,6 +87,13 @@ int hero_batch_state_create(const hero_model* model, int64_t max_tokens, int32_t
  * matrix products instead of the token-serial chain; equal to the reference
  * to fp32 rounding order instead of bit for bit). */
 #define HERO_STATE_GDN_CHUNKED 2u
+/* flags: keep the attention cache as Q8_0 pages (int8 rows with an fp16 scale
+ * per 32, 1.0625 bytes per value) with split-K attention: the K/V storage of
+ * the reference's plan (nm/INFERENCE_PLAN.md:235-236), each appended row
+ * quantized by its activation quantizer (quant_i8.hpp:70-80) and read back as
+ * d * q (quant.hpp:306-313). Results equal the oracle's Q8_0-cache switch to a
+ * few ulp (the split-K sums). Exclusive with HERO_STATE_KV_FP16. */
+#define HERO_STATE_KV_Q8_0 4u
 int64_t hero_state_batch(const hero_state* state);
 int64_t hero_state_seq_tokens(const hero_state* state, int32_t seq);
 /* hero_model_forward for sequence `seq` of a batch state. */

@@ -51,6 +51,7 @@ _sigs = {
     "oracle_rope_apply": (None, [c_void_p, c_size_t, c_void_p, c_size_t, c_size_t]),
     "oracle_attend_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_size_t, c_size_t, c_float, c_void_p]),
     "oracle_model_set_kv_fp16": (None, [c_void_p, c_int]),
+    "oracle_model_set_kv_q8": (None, [c_void_p, c_int]),
     "oracle_round_fp16": (None, [c_void_p, c_size_t, c_void_p]),
     "oracle_model_open": (c_void_p, [c_char_p]),
     "oracle_model_open_image": (c_void_p, [c_void_p, c_size_t]),
@@ -360,6 +361,10 @@ class Model:
     def set_kv_fp16(self, on: bool) -> None:
         """store attention K/V rounded to fp16 (the GPU's fp16 paged cache)"""
         lib.oracle_model_set_kv_fp16(self._h, 1 if on else 0)
+
+    def set_kv_q8(self, on: bool) -> None:
+        """keep attention K/V rows as their Q8_0 round trip (the GPU's Q8_0 pages)"""
+        lib.oracle_model_set_kv_q8(self._h, 1 if on else 0)
 
     def tokens(self) -> int:
         return int(lib.oracle_model_tokens(self._h))

@@ -692,6 +692,15 @@ std::vector<float> attention_mixer(const Model& m, const Layer& L, size_t layer,
             s.keys[layer][i] = round_fp16_rne(s.keys[layer][i]);
             s.values[layer][i] = round_fp16_rne(s.values[layer][i]);
         }
+    if (s.kv_q8) {  // rows of KW values, blocks of 32 within a row
+        const size_t first = s.keys[layer].size() - K.size();
+        std::vector<BlockQ8> blocks(KW / 32);
+        for (std::vector<float>* cache : {&s.keys[layer], &s.values[layer]})
+            for (size_t r = first; r < cache->size(); r += KW) {
+                quantize_row_q8_0(cache->data() + r, blocks.data(), KW);
+                dequant_row_q8_0(blocks.data(), cache->data() + r, KW);
+            }
+    }
     const float score_scale = 1.f / std::sqrt(float(Dh));
     std::vector<float> A(T * QW);
     const size_t group = c.Hq / c.Hkv;

@@ -214,6 +214,10 @@ struct State {
     // attention keys and values rounded to IEEE fp16, nearest-even, as the
     // GPU's fp16 paged cache does; reset() keeps it
     bool kv_fp16 = false;
+    // the same for Q8_0 storage (the reference's plan, nm/INFERENCE_PLAN.md:235-236):
+    // each appended K and V row goes through quantize_row_q8_0 (the activation
+    // quantizer) and is kept as its dequantized values d * q; reset() keeps it
+    bool kv_q8 = false;
     // attention layers: fp32 K/V rows [tokens][Hkv*head_dim]
     std::vector<std::vector<float>> keys, values;
     // recurrent layers: conv history [(W-1)][CC] oldest first, delta state [Hv][Dk][Dv]

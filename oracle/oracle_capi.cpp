@@ -194,6 +194,7 @@ void oracle_model_reset(void* h) {
     s->state.reset(s->model.c);
 }
 void oracle_model_set_kv_fp16(void* h, int on) { static_cast<Session*>(h)->state.kv_fp16 = on != 0; }
+void oracle_model_set_kv_q8(void* h, int on) { static_cast<Session*>(h)->state.kv_q8 = on != 0; }
 void oracle_round_fp16(const float* x, size_t n, float* out) {
     for (size_t i = 0; i < n; ++i) out[i] = round_fp16_rne(x[i]);
 }

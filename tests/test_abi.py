@@ -44,8 +44,11 @@ def test_kquant_argument_errors_are_reported_before_any_launch():
     assert lib.hero_kquant_pack(11, 16, 32, 64, 4096, None) == _lib.HERO_EINVAL
     assert lib.hero_kquant_pack(12, 16, 16, 64, 4096, None) == _lib.HERO_EINVAL  # in place
     assert lib.hero_kquant_dequant_rows(14, 16, 64, 4096, 16, 0, 16, None) == _lib.HERO_EINVAL
-    for t, per_block in ((12, 144), (13, 176), (14, 210)):  # the packed form has the GGUF tensor's size
-        assert lib.hero_kquant_packed_bytes(t, 3, 512) == 3 * 2 * per_block
+    # the packed form: the GGUF bytes in tiles of 256 / (k / 256) rows, each tile
+    # padded to whole waves of 64 blocks (k 512: tiles of 128 rows, 4 waves)
+    for t, per_block in ((12, 144), (13, 176), (14, 210)):
+        assert lib.hero_kquant_packed_bytes(t, 3, 512) == 256 * per_block
+        assert lib.hero_kquant_packed_bytes(t, 4096, 4096) == 4096 * 16 * per_block  # whole tiles: no padding
     assert lib.hero_kquant_packed_bytes(8, 3, 512) == -1
 
 

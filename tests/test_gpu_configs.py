@@ -347,3 +347,97 @@ def test_attn_baseline_sizes_match_oracle(lib, B, ctx):
             worst = max(worst, float(np.abs(got[b] - expect).max() / np.abs(expect).max()))
             assert blocks[b].tobytes() == oracle.quantize_row_q8_0(got[b]).tobytes()
         say(f"[attn B={B} ctx={ctx}] paged fp16 cache, window={window}: max|d|/max = {worst:.3g}")
+
+
+def q8_round_trip(x):
+    """rows of 128-value heads through quantize_row_q8_0 (the reference's
+    activation quantizer) and back as d * q: the values a Q8_0 cache holds;
+    also returns the int8 quants and fp16 scale bits, [rows][128], [rows][4]"""
+    flat = np.ascontiguousarray(x, np.float32).reshape(-1, ATT_DH)
+    blocks = oracle.quantize_row_q8_0(flat.reshape(-1))
+    d16 = np.ascontiguousarray(blocks["d"]).view(np.uint16).reshape(-1)
+    q = np.ascontiguousarray(blocks["qs"]).view(np.int8).reshape(-1, 32)
+    deq = (oracle.fp16_to_fp32(d16).astype(np.float32)[:, None] * q.astype(np.float32)).astype(np.float32)
+    return deq.reshape(x.shape), q.reshape(flat.shape[0], ATT_DH), d16.reshape(flat.shape[0], 4)
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("B,ctx", [(1, 8192), (16, 1024), (3, 9000)])
+def test_attn_q8_pages_match_oracle(lib, B, ctx):
+    """32q/8kv attention decode over a Q8_0 paged cache (pages of 64 positions
+    in a shuffled pool; int8 rows and fp16 block scales per page): against the
+    oracle over the same Q8_0 round-tripped K/V, full causal and window 1024,
+    within rtol 1e-4 + atol 1e-4 * max|out| (the split-K merge reorders the
+    softmax sums); the row the kernel appends equals the oracle's quantization
+    of the new key and value."""
+    from hero_amd._lib import AttnDecodeArgs, AttnPagedArgs
+
+    rng = np.random.default_rng(B * 7919 + ctx)
+    dh, hq, hkv = ATT_DH, ATT_HQ, ATT_HKV
+    qw, kw = hq * dh, hkv * dh
+    pos, keys, vals, proj, qg, kg = attn_inputs(rng, B, ctx)
+    inv = oracle.rope_inv_freq(dh, 1e6, 32)
+    d_cs = dev(oracle.rope_table(dh, 1e6, 32, ctx))
+    d_qg, d_kg = dev(qg), dev(kg)
+    d_proj, d_pos = dev(proj), dev(np.full(B, pos, np.int32))
+    stride = 2 * qw + 2 * kw
+    eps = np.float32(1e-6)
+    act = empty(lib.hero_q8_0_act_bytes(B, qw))
+    out = empty(B * qw * 4)
+    d_qr = empty(B * hq * dh * 4)
+    page = 64
+    max_pages = (ctx + page - 1) // page
+    page_bytes = lib.hero_attn_page_bytes(hkv, page, 1)
+    assert page_bytes == 2 * hkv * page * (dh + 8)
+    table = rng.permutation(B * max_pages).astype(np.int32).reshape(B, max_pages)
+    pool = np.zeros((B * max_pages, page_bytes), np.uint8)
+    qpart = pool[:, :2 * hkv * page * dh].reshape(-1, 2, hkv, page, dh)
+    spart = pool[:, 2 * hkv * page * dh:].view(np.uint16).reshape(-1, 2, hkv, page, 4)
+    deq = {}
+    for which, src in ((0, keys), (1, vals)):
+        d, q, sc = q8_round_trip(src.reshape(B, pos, hkv, dh))
+        deq[which] = d.reshape(B, pos, kw)
+        qp = np.zeros((B, max_pages * page, hkv, dh), np.int8)
+        sp = np.zeros((B, max_pages * page, hkv, 4), np.uint16)
+        qp[:, :pos] = q.reshape(B, pos, hkv, dh)
+        sp[:, :pos] = sc.reshape(B, pos, hkv, 4)
+        qpart[table.reshape(-1), which] = qp.reshape(B, max_pages, page, hkv, dh).transpose(0, 1, 3, 2, 4).reshape(-1, hkv, page, dh).view(np.uint8)
+        spart[table.reshape(-1), which] = sp.reshape(B, max_pages, page, hkv, 4).transpose(0, 1, 3, 2, 4).reshape(-1, hkv, page, 4)
+        del qp, sp
+    d_pages, d_table = dev(pool), dev(table)
+    for window, scale in VARIANTS:
+        wbytes = lib.hero_attn_paged_work_bytes(max_pages * page, window, B, hq, hkv)
+        d_work = empty(wbytes)
+        a = AttnDecodeArgs(ptr(d_proj), stride, 2 * qw, 2 * qw + kw, ptr(d_qg), ptr(d_kg), eps, ptr(d_cs), None, None,
+                           0, ptr(d_pos), None, ptr(d_qr), scale, window, ptr(act), ptr(out), B, hq, hkv, dh)
+        pa = AttnPagedArgs(a, ptr(d_pages), ptr(d_table), page, max_pages, ptr(d_work), wbytes, 1)
+        check(lib.hero_attn_decode_paged(pa, stream()))
+        got = host(out, np.float32, (B, qw))
+        worst = 0.0
+        for b in range(B):
+            # the oracle appends the new row through the same round trip
+            qv = proj[b, 2 * qw:].reshape(2, hkv, dh)
+            k_new = oracle.rope_apply(oracle.rmsnorm(qv[0], kg, eps), inv, pos).reshape(1, kw)
+            k_new, _, _ = q8_round_trip(k_new)
+            v_new, _, _ = q8_round_trip(qv[1].reshape(1, kw))
+            qh = np.stack([proj[b, h * 2 * dh: h * 2 * dh + dh] for h in range(hq)])
+            g = np.concatenate([proj[b, h * 2 * dh + dh: h * 2 * dh + 2 * dh] for h in range(hq)])
+            q = oracle.rope_apply(oracle.rmsnorm(qh, qg, eps), inv, pos)
+            kk = np.concatenate([deq[0][b], k_new])
+            vv = np.concatenate([deq[1][b], v_new])
+            expect = (oracle.attend_decode(q.reshape(-1), kk, vv, hq, hkv, dh, window, scale).reshape(-1) * oracle.sigmoid(g)).astype(np.float32)
+            tol = 1e-4 * np.abs(expect).max()
+            np.testing.assert_allclose(got[b], expect, rtol=1e-4, atol=tol, err_msg=f"q8 window={window} seq {b}")
+            worst = max(worst, float(np.abs(got[b] - expect).max() / np.abs(expect).max()))
+        say(f"[attn B={B} ctx={ctx}] paged Q8_0 cache, window={window}: max|d|/max = {worst:.3g}")
+    # the appended row (position pos) of sequence 0, K and V: the oracle's quantization
+    pool_after = host(d_pages, np.uint8).reshape(B * max_pages, page_bytes)
+    pg = table[0, pos // page]
+    qa = pool_after[:, :2 * hkv * page * dh].reshape(-1, 2, hkv, page, dh)[pg, :, :, pos % page].view(np.int8)
+    sa = pool_after[:, 2 * hkv * page * dh:].copy().view(np.uint16).reshape(-1, 2, hkv, page, 4)[pg, :, :, pos % page]
+    qv = proj[0, 2 * qw:].reshape(2, hkv, dh)
+    k_new = oracle.rope_apply(oracle.rmsnorm(qv[0], kg, eps), inv, pos)
+    for which, row in ((0, k_new), (1, qv[1])):
+        _, q, sc = q8_round_trip(row.reshape(1, kw))
+        assert np.array_equal(qa[which], q.reshape(hkv, dh)), which
+        assert np.array_equal(sa[which], sc.reshape(hkv, 4)), which

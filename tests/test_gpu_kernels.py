@@ -817,18 +817,16 @@ def test_kquant_dequant_rows_match_reference_golden(lib, kernels_golden, wtype, 
     assert not got[3].any()
 
 
-def test_kquant_pack_permutes_bytes_within_blocks(lib):
-    """the packed Q4_K / Q6_K tensor holds each super-block's bytes (Q6_K: all
-    but d, whose plane follows) as a permutation of the GGUF block"""
+def test_kquant_pack_permutes_the_tensor_bytes(lib):
+    """the packed tensor holds the GGUF tensor's bytes, permuted, and zeros in
+    its padding slots (40 rows of 4 blocks: one tile of 64 rows, 4 waves)"""
     rng = np.random.default_rng(5)
-    for wtype, per in ((12, 144), (14, 210)):
-        w = kquant_weights(rng, wtype, 40, 1024)
+    for wtype in (12, 13, 14):
+        w = q5k_weights(rng, 40, 1024) if wtype == 13 else kquant_weights(rng, wtype, 40, 1024)
         got = host(kquant_pack_dev(lib, wtype, w, 40, 1024), np.uint8)
-        raw = w.reshape(-1, per)
-        body = got[:raw.shape[0] * (144 if wtype == 12 else 208)].reshape(raw.shape[0], -1)
-        assert np.array_equal(np.sort(body, axis=1), np.sort(raw[:, :body.shape[1]], axis=1))
-        if wtype == 14:
-            assert np.array_equal(got[raw.shape[0] * 208:], raw[:, 208:].ravel())
+        assert got.size == lib.hero_kquant_packed_bytes(wtype, 40, 1024)
+        expect = np.concatenate([w.ravel(), np.zeros(got.size - w.size, np.uint8)])
+        assert np.array_equal(np.sort(got), np.sort(expect)), wtype
 
 
 # ---- top-k / top-p sampling -------------------------------------------------------------

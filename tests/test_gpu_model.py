@@ -195,6 +195,40 @@ def test_fp16_paged_cache_matches_oracle_over_fp16_kv(model, tiny_gguf, tiny_gol
     assert np.array_equal(bits(logits[1]), bits(lg2.values))
 
 
+def test_q8_paged_cache_matches_oracle_over_q8_kv(model, tiny_gguf, tiny_golden):
+    """The Q8_0 paged attention cache on the whole model: against the oracle
+    with its Q8_0-cache switch on (each appended K/V row through
+    quantize_row_q8_0 and back), greedy ids over a 16-token prefill and 48
+    decode passes are identical and the logits agree within 1e-2 abs / 1e-3
+    rel; a batch state with the Q8_0 cache gives a sequence the results of its
+    own state bit for bit."""
+    import oracle
+
+    prompt = tiny_golden["prompt"]
+    steps = 48
+    ref = oracle.Model(path=tiny_gguf)
+    ref.set_kv_q8(True)
+    ref_ids, ref_last, _, _ = ref.greedy(prompt, steps)
+    ref.close()
+    st = model.new_state(256, kv_q8=True)
+    first = model.forward(st, ids=prompt)
+    ids, last = model.decode_greedy(st, first.argmax(), steps, want_logits=True)
+    assert [first.argmax()] + [int(v) for v in ids[:-1]] == [int(v) for v in ref_ids[:-1]]
+    report("q8 cache", last.values, ref_last)
+    assert np.all(close(last.values, ref_last))
+    bs = model.new_batch_state(256, 2, kv_q8=True)
+    f0 = model.forward_seq(bs, 0, ids=prompt[:5]).argmax()
+    f1 = model.forward_seq(bs, 1, ids=prompt).argmax()
+    out, logits = model.decode_batch(bs, [f0, f1], 8, want_logits=True)
+    st2 = model.new_state(256, kv_q8=True)
+    model.forward(st2, ids=prompt)
+    ids2, lg2 = model.decode_greedy(st2, f1, 8, want_logits=True)
+    assert np.array_equal(out[:, 1], ids2)
+    assert np.array_equal(bits(logits[1]), bits(lg2.values))
+    with pytest.raises(hero_amd.HeroError):  # one cache format per state
+        model.new_state(64, kv_fp16=True, kv_q8=True)
+
+
 def test_chunked_delta_net_prefill_tracks_exact(model, tiny_gguf):
     """A 300-token prefill with the chunked delta-net form against the exact
     (token-serial, bit-exact) prefill. The two recurrences differ by ~1e-6

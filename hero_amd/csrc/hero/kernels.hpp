@@ -90,6 +90,9 @@ void launch_argmax(const float* logits, int64_t M, int64_t n, int32_t* out_index
 constexpr int kArgmaxGroups = 128, kArgmaxNoallocRows = 64;
 void launch_argmax_noalloc(const float* logits, int64_t M, int64_t n, int32_t* out_index, hipStream_t s);
 
+// a plain read of `bytes` (a multiple of 16) by `workgroups` workgroups of
+// 256 lanes (measurement: the read bandwidth ceiling)
+void launch_read_probe(const void* p, int64_t bytes, int workgroups, uint32_t* out, hipStream_t s);
 // exp, log1p, silu, sigmoid, softplus of x[n] -> out[5][n] (parity export)
 void launch_math_eval(const float* x, float* out, int64_t n, hipStream_t s);
 

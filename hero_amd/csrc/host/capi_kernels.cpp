@@ -461,6 +461,16 @@ int64_t hero_attn_paged_work_bytes(int64_t max_ctx, int32_t window, int32_t b, i
     return attn_paged_work_floats(b, hq, nsplit) * 4;
 }
 
+int hero_read_probe(const void* p, int64_t bytes, int32_t workgroups, uint32_t* out, void* stream) {
+    return guard([&] {
+        require(p && out, "null pointer");
+        require(bytes > 0 && bytes % 16 == 0 && aligned(p, 16), "bytes: a positive multiple of 16, 16-byte aligned");
+        require(workgroups > 0 && workgroups <= 65536, "workgroups out of range");
+        launch_read_probe(p, bytes, workgroups, out, as_stream(stream));
+        check_launch("hero_read_probe");
+    });
+}
+
 int64_t hero_attn_page_bytes(int32_t hkv, int32_t page_size, int32_t q8) {
     if (hkv <= 0 || page_size <= 0 || (q8 != 0 && q8 != 1)) return -1;
     return attn_page_bytes(hkv, page_size, q8 != 0);

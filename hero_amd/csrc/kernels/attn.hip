@@ -913,9 +913,26 @@ __global__ __launch_bounds__(kAttnDim) void attn_paged_prep_kernel(AttnPagedArgs
     }
 }
 
-// one workgroup per (KV head, split, row): the split's keys in tiles of 64.
+// One workgroup per (KV head, split, row): the split's keys in tiles of 64.
+// Lane (key r = tid / 4 of the tile, channel quarter cq = 32 (tid % 4)) loads
+// its 32 channels of the key, and of the next tile's key before it uses the
+// current one (a register double buffer: a tile's global reads are in flight
+// while the previous tile computes).
+// Scores: the lane's partial dots for every query head of the group (fused
+// multiply-adds: this path is not the reference's operation order anyway),
+// summed over the four quarter lanes. Softmax: a wave per head, local max and
+// exp-sum. Weighted sum: the V tile stays in shared memory as stored (fp16
+// pairs, or Q8_0 quads and scales); lane (channel c = tid % 128, half kh =
+// tid / 128 of the tile's keys) adds p_h(j) v_j[c] for all heads of the group,
+// the weights read four keys at a time.
 // Q8: the rows are Q8_0, each value read back as d * q (dequant_row_q8_0,
 // nm/src/quant.hpp:306-313), the fp32 value the oracle's Q8_0 cache holds.
+template <bool Q8>
+struct PgRaw {  // one lane's 32 channels of a row as stored
+    uint4 w[Q8 ? 2 : 4];
+    uint16_t d;  // Q8: the block scale
+};
+
 template <bool Q8>
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnPagedArgs p) {
     const AttnDecodeArgs& a = p.a;
@@ -935,74 +952,99 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnPagedArgs p) {
     }
     const int n = t1 - t0;
     const int32_t* pt = page_row(p, b);
-    __shared__ float qs[kAttnMaxGroup][kAttnDim];
-    __shared__ float kt[kAttnDim][kPgTile + 1];  // K tile, channel-major
-    __shared__ uint32_t vt[kPgTile][kAttnDim / 2 + 1];  // V tile: rows of fp16 pairs, or (Q8) of int8 quads
-    __shared__ float vsc[Q8 ? kPgTile : 1][4];          // Q8: the V rows' block scales
-    __shared__ float sc[kAttnMaxGroup][kAttnMaxSplit];
     const uint8_t* pool = reinterpret_cast<const uint8_t*>(p.pages);
+    __shared__ __align__(16) float qs[kAttnMaxGroup][kAttnDim];
+    __shared__ __align__(16) float sc[kAttnMaxGroup][kAttnMaxSplit];
+    constexpr int kVw = Q8 ? kAttnDim / 4 : kAttnDim / 2;  // dwords per stored V row
+    __shared__ uint32_t vt[kPgTile][kVw + 1];
+    __shared__ float vsc[Q8 ? kPgTile : 1][4];
+    __shared__ float part[kAttnMaxGroup][kAttnDim];  // the second half's sums of the weighted sum
     for (int e = tid; e < Gs * kAttnDim; e += 256) qs[e / kAttnDim][e % kAttnDim] = a.q_rot[(int64_t(b) * a.Hq + int64_t(g) * Gs) * kAttnDim + e];
 
-    // tile loads: thread -> row r = tid / 4, channels 32 * (tid % 4) .. +31 (four 16-byte loads)
     const int r = tid >> 2, cq = (tid & 3) * 32;
-    const int ntiles = (n + kPgTile - 1) / kPgTile;
-    for (int tile = 0; tile < ntiles; ++tile) {
-        const int t = t0 + tile * kPgTile + r;
+    auto load_raw = [&](int t, int kv, PgRaw<Q8>& x) {
+        if (t >= t1) {
+#pragma unroll
+            for (int u = 0; u < (Q8 ? 2 : 4); ++u) x.w[u] = make_uint4(0u, 0u, 0u, 0u);
+            x.d = 0;
+            return;
+        }
         if constexpr (Q8) {
-            // 32 int8 (block tid % 4 of the row) and the block's scale
-            uint4 raw[2] = {};
-            uint16_t dh = 0;
-            if (t < t1) {
-                const int64_t base = q8_page_base(p, pt, t), row = q8_row(p, t, g, 0);
-                const uint4* src = reinterpret_cast<const uint4*>(pool + base + row * kAttnDim + cq);
-                raw[0] = src[0], raw[1] = src[1];
-                dh = reinterpret_cast<const uint16_t*>(pool + base + 2 * int64_t(a.Hkv) * p.page_size * kAttnDim)[row * 4 + cq / 32];
-            }
-            __syncthreads();  // the previous tile's readers are done
-            const float d = half_bits_to_f32(dh);
+            const int64_t base = q8_page_base(p, pt, t), row = q8_row(p, t, g, kv);
+            const uint4* src = reinterpret_cast<const uint4*>(pool + base + row * kAttnDim + cq);
+            x.w[0] = src[0], x.w[1] = src[1];
+            x.d = reinterpret_cast<const uint16_t*>(pool + base + 2 * int64_t(a.Hkv) * p.page_size * kAttnDim)[row * 4 + cq / 32];
+        } else {
+            const uint4* src = reinterpret_cast<const uint4*>(p.pages + page_offset(p, pt, t, g, kv) + cq);
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+            for (int u = 0; u < 4; ++u) x.w[u] = src[u];
+            x.d = 0;
+        }
+    };
+    auto to_f32 = [&](const PgRaw<Q8>& x, float (&v)[32]) {
+        if constexpr (Q8) {
+            const float d = half_bits_to_f32(x.d);
 #pragma unroll
-                for (int e = 0; e < 16; ++e) kt[cq + 16 * u + e][r] = d * float(int8_t((w[e / 4] >> (8 * (e % 4))) & 0xFFu));
+            for (int e = 0; e < 32; ++e) {
+                const uint4 w = x.w[e / 16];
+                const uint32_t dw = (e % 16) < 4 ? w.x : (e % 16) < 8 ? w.y : (e % 16) < 12 ? w.z : w.w;
+                v[e] = d * float(int8_t((dw >> (8 * (e % 4))) & 0xFFu));
             }
         } else {
-            uint4 raw[4] = {};
-            if (t < t1) {
-                const uint4* src = reinterpret_cast<const uint4*>(p.pages + page_offset(p, pt, t, g, 0) + cq);
-#pragma unroll
-                for (int u = 0; u < 4; ++u) raw[u] = src[u];
-            }
-            __syncthreads();  // the previous tile's readers are done
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+                const uint32_t w[4] = {x.w[u].x, x.w[u].y, x.w[u].z, x.w[u].w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    kt[cq + 8 * u + 2 * e][r] = half_bits_to_f32(uint16_t(w[e] & 0xFFFFu));
-                    kt[cq + 8 * u + 2 * e + 1][r] = half_bits_to_f32(uint16_t(w[e] >> 16));
+                    v[8 * u + 2 * e] = half_bits_to_f32(uint16_t(w[e] & 0xFFFFu));
+                    v[8 * u + 2 * e + 1] = half_bits_to_f32(uint16_t(w[e] >> 16));
                 }
             }
         }
-        __syncthreads();
-        // score of key lane for query head h: scale * sequential dot (core.hpp:496-500)
-        for (int h = wv; h < Gs; h += 4) {
-            float dot = 0.f;
-#pragma unroll 16
-            for (int c = 0; c < kAttnDim; ++c) dot += qs[h][c] * kt[c][lane];
-            const int jj = tile * kPgTile + lane;
-            if (jj < n) sc[h][jj] = a.score_scale * dot;
+    };
+    __syncthreads();  // qs
+
+    // scores (core.hpp:496-500's dot, reordered): partial dots over the lane's
+    // quarter, then the four quarters of the key
+    const int ntiles = (n + kPgTile - 1) / kPgTile;
+    PgRaw<Q8> cur, nxt;
+    load_raw(t0 + r, 0, cur);
+    for (int tile = 0; tile < ntiles; ++tile) {
+        load_raw(t0 + (tile + 1) * kPgTile + r, 0, nxt);  // zeros past the split
+        float kx[32];
+        to_f32(cur, kx);
+        const int jj = tile * kPgTile + r;
+#pragma unroll
+        for (int h = 0; h < kAttnMaxGroup; ++h) {
+            if (h < Gs) {
+                float dot = 0.f;
+                const float4* q4 = reinterpret_cast<const float4*>(&qs[h][cq]);
+#pragma unroll
+                for (int e4 = 0; e4 < 8; ++e4) {
+                    const float4 q = q4[e4];
+                    dot = fmaf(q.x, kx[4 * e4], dot);
+                    dot = fmaf(q.y, kx[4 * e4 + 1], dot);
+                    dot = fmaf(q.z, kx[4 * e4 + 2], dot);
+                    dot = fmaf(q.w, kx[4 * e4 + 3], dot);
+                }
+                dot += __shfl_xor(dot, 1);
+                dot += __shfl_xor(dot, 2);
+                if ((tid & 3) == 0 && jj < n) sc[h][jj] = a.score_scale * dot;
+            }
         }
+        cur = nxt;
     }
+    load_raw(t0 + r, 1, cur);  // the first V tile, in flight during the softmax
     __syncthreads();
-    // per head (one wave each): local max, p = exp(s - m), local sum
+    // per head (a wave each): local max, p = exp(s - m), local sum; the
+    // weights past n are zero so the weighted sum reads whole quads
     for (int h = wv; h < Gs; h += 4) {
         float m = -INFINITY;
         for (int jj = lane; jj < n; jj += 64) m = fmaxf(m, sc[h][jj]);
         for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
         float l = 0.f;
-        for (int jj = lane; jj < n; jj += 64) {
-            const float e = exp_f32(sc[h][jj] - m);
+        for (int jj = lane; jj < ntiles * kPgTile; jj += 64) {
+            const float e = jj < n ? exp_f32(sc[h][jj] - m) : 0.f;
             sc[h][jj] = e;
             l += e;
         }
@@ -1012,70 +1054,66 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnPagedArgs p) {
             out[h * hstride + 1] = l;
         }
     }
-    // weighted sum of values: thread -> head wv (+4), channel pair lane
-    float o0[kAttnMaxGroup / 4] = {}, o1[kAttnMaxGroup / 4] = {};
-    for (int tile = 0; tile < ntiles; ++tile) {
-        const int t = t0 + tile * kPgTile + r;
-        if constexpr (Q8) {
-            uint4 raw[2] = {};
-            uint16_t dh = 0;
-            if (t < t1) {
-                const int64_t base = q8_page_base(p, pt, t), row = q8_row(p, t, g, 1);
-                const uint4* src = reinterpret_cast<const uint4*>(pool + base + row * kAttnDim + cq);
-                raw[0] = src[0], raw[1] = src[1];
-                dh = reinterpret_cast<const uint16_t*>(pool + base + 2 * int64_t(a.Hkv) * p.page_size * kAttnDim)[row * 4 + cq / 32];
-            }
-            __syncthreads();  // sc complete (first tile) / previous tile's readers done
-            vt[r][cq / 4 + 0] = raw[0].x, vt[r][cq / 4 + 1] = raw[0].y, vt[r][cq / 4 + 2] = raw[0].z, vt[r][cq / 4 + 3] = raw[0].w;
-            vt[r][cq / 4 + 4] = raw[1].x, vt[r][cq / 4 + 5] = raw[1].y, vt[r][cq / 4 + 6] = raw[1].z, vt[r][cq / 4 + 7] = raw[1].w;
-            vsc[r][cq / 32] = half_bits_to_f32(dh);
-        } else {
-            uint4 raw[4] = {};
-            if (t < t1) {
-                const uint4* src = reinterpret_cast<const uint4*>(p.pages + page_offset(p, pt, t, g, 1) + cq);
+    // weighted sum of values: lane -> channel c, keys kh * 32 .. +31 of each tile
+    const int c = tid & (kAttnDim - 1), kh = tid >> 7;
+    float o[kAttnMaxGroup];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) raw[u] = src[u];
-            }
-            __syncthreads();  // sc complete (first tile) / previous tile's readers done
+    for (int h = 0; h < kAttnMaxGroup; ++h) o[h] = 0.f;
+    for (int tile = 0; tile < ntiles; ++tile) {
+        load_raw(t0 + (tile + 1) * kPgTile + r, 1, nxt);
+        __syncthreads();  // sc complete (first tile) / the previous tile's readers done
+        if constexpr (Q8) {
+            vt[r][cq / 4 + 0] = cur.w[0].x, vt[r][cq / 4 + 1] = cur.w[0].y, vt[r][cq / 4 + 2] = cur.w[0].z, vt[r][cq / 4 + 3] = cur.w[0].w;
+            vt[r][cq / 4 + 4] = cur.w[1].x, vt[r][cq / 4 + 5] = cur.w[1].y, vt[r][cq / 4 + 6] = cur.w[1].z, vt[r][cq / 4 + 7] = cur.w[1].w;
+            vsc[r][cq / 32] = half_bits_to_f32(cur.d);
+        } else {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                vt[r][cq / 2 + 4 * u + 0] = raw[u].x;
-                vt[r][cq / 2 + 4 * u + 1] = raw[u].y;
-                vt[r][cq / 2 + 4 * u + 2] = raw[u].z;
-                vt[r][cq / 2 + 4 * u + 3] = raw[u].w;
+                vt[r][cq / 2 + 4 * u + 0] = cur.w[u].x;
+                vt[r][cq / 2 + 4 * u + 1] = cur.w[u].y;
+                vt[r][cq / 2 + 4 * u + 2] = cur.w[u].z;
+                vt[r][cq / 2 + 4 * u + 3] = cur.w[u].w;
             }
         }
         __syncthreads();
-        const int rows = min(kPgTile, n - tile * kPgTile);
+        const int j0 = tile * kPgTile + 32 * kh;
+#pragma unroll 2
+        for (int q4i = 0; q4i < 8; ++q4i) {
+            float v[4];
 #pragma unroll
-        for (int hh = 0; hh < kAttnMaxGroup / 4; ++hh) {
-            const int h = wv + 4 * hh;
-            if (h < Gs) {
-                for (int jr = 0; jr < rows; ++jr) {
-                    const float pj = sc[h][tile * kPgTile + jr];
-                    if constexpr (Q8) {
-                        // channels 2 lane, 2 lane + 1: bytes (2 lane) % 4 .. +1 of dword lane / 2
-                        const uint32_t q4 = vt[jr][lane >> 1];
-                        const int sh = 16 * (lane & 1);
-                        const float d = vsc[jr][lane >> 4];
-                        o0[hh] += pj * (d * float(int8_t((q4 >> sh) & 0xFFu)));
-                        o1[hh] += pj * (d * float(int8_t((q4 >> (sh + 8)) & 0xFFu)));
-                    } else {
-                        const uint32_t v2 = vt[jr][lane];
-                        o0[hh] += pj * half_bits_to_f32(uint16_t(v2 & 0xFFFFu));
-                        o1[hh] += pj * half_bits_to_f32(uint16_t(v2 >> 16));
-                    }
+            for (int u = 0; u < 4; ++u) {
+                const int jr = 32 * kh + 4 * q4i + u;
+                if constexpr (Q8) {
+                    const uint32_t dw = vt[jr][c >> 2];
+                    v[u] = vsc[jr][c >> 5] * float(int8_t((dw >> (8 * (c & 3))) & 0xFFu));
+                } else {
+                    const uint32_t dw = vt[jr][c >> 1];
+                    v[u] = half_bits_to_f32(uint16_t((c & 1) ? (dw >> 16) : (dw & 0xFFFFu)));
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < kAttnMaxGroup; ++h) {
+                if (h < Gs) {
+                    const float4 w = *reinterpret_cast<const float4*>(&sc[h][j0 + 4 * q4i]);
+                    o[h] = fmaf(w.x, v[0], o[h]);
+                    o[h] = fmaf(w.y, v[1], o[h]);
+                    o[h] = fmaf(w.z, v[2], o[h]);
+                    o[h] = fmaf(w.w, v[3], o[h]);
                 }
             }
         }
+        cur = nxt;
     }
+    if (kh == 1) {
 #pragma unroll
-    for (int hh = 0; hh < kAttnMaxGroup / 4; ++hh) {
-        const int h = wv + 4 * hh;
-        if (h < Gs) {
-            out[h * hstride + 2 + 2 * lane] = o0[hh];
-            out[h * hstride + 2 + 2 * lane + 1] = o1[hh];
-        }
+        for (int h = 0; h < kAttnMaxGroup; ++h)
+            if (h < Gs) part[h][c] = o[h];
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+        for (int h = 0; h < kAttnMaxGroup; ++h)
+            if (h < Gs) out[h * hstride + 2 + c] = o[h] + part[h][c];
     }
 }
 

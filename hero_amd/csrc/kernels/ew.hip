@@ -164,4 +164,32 @@ void launch_math_eval(const float* x, float* out, int64_t n, hipStream_t s) {
     hipLaunchKernelGGL(math_eval_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, s, x, out, n);
 }
 
+// ---- measurement: a plain HBM read ---------------------------------------------------
+// Workgroup g reads its contiguous share of the buffer with 16-byte loads, 8
+// in flight per lane, folded with XOR into one value that is stored only if
+// it equals a constant nothing produces: the bandwidth a kernel that only
+// reads reaches, the ceiling the memory-bound kernels are compared with.
+__global__ __launch_bounds__(256) void read_probe_kernel(const uint4* __restrict__ p, int64_t n16, uint32_t* __restrict__ out) {
+    const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+    const int64_t b0 = per * blockIdx.x, b1 = min(n16, b0 + per);
+    uint32_t acc = 0;
+    int64_t i = b0 + threadIdx.x;
+    for (; i + 7 * 256 < b1; i += 8 * 256) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = p[i + u * 256];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < b1; i += 256) {
+        const uint4 v = p[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9E3779B9u) out[0] = acc;
+}
+
+void launch_read_probe(const void* p, int64_t bytes, int workgroups, uint32_t* out, hipStream_t s) {
+    hipLaunchKernelGGL(read_probe_kernel, dim3(unsigned(workgroups)), dim3(256), 0, s, static_cast<const uint4*>(p), bytes / 16, out);
+}
+
 }  // namespace hero

@@ -1,8 +1,13 @@
 """hero_amd.microbench -- the kernel microbenchmarks of the hot path on one GPU.
 
-    python -m hero_amd.microbench [--suite gemv,kquant,gdn,attn] [--out results.md]
+    python -m hero_amd.microbench [--suite hbm,gemv,kquant,gdn,attn] [--out results.md]
 
 Suites (synthetic, seeded inputs; every launch goes through the C ABI):
+
+hbm    the read ceiling: a kernel that only reads (hero_read_probe) over
+       18 MB .. 2 GB fresh regions, 512 / 2048 / 8192 workgroups.
+kquant Q4_K / Q5_K / Q6_K products over packed random blocks, (K, N) as in
+       gemv, M in {1, 16, 512}.
 
 gemv   Q8_0 matvec / matmul. W is N x K int8 uniform in [-127, 127] with fp16
        block scales |N(0, 0.02)| * 4/127; activations are N(0, 1) rows
@@ -18,7 +23,7 @@ gdn    the fused delta-net layer body (conv + SiLU, L2 norms, gates, the delta
 attn   gated GQA decode (32 q / 8 kv heads of 128) at context {1k, 8k, 32k} x
        B {1, 16}: full causal (scale 1/sqrt(128)) and a 1024 sliding window
        (scale 1), over the fp32 cache (the reference's precision, bit-exact
-       kernels) and over the paged fp16 cache (split-K kernels).
+       kernels) and over the paged fp16 and Q8_0 caches (split-K kernels).
 
 Each case is captured once as a hipGraph (one pass over its inputs) and
 replayed; the time per launch is the replay time divided by the launches,
@@ -240,6 +245,41 @@ def bench_kquant(lib, replays: int = 20, batches=KQUANT_BATCHES):
     return rows
 
 
+# ---- plain HBM read (the ceiling) ------------------------------------------------------------
+HBM_READ_SIZES_MB = (18, 54, 107, 622, 2048)
+
+
+def bench_hbm(lib, reps: int = 5):
+    """hero_read_probe: contiguous shares, 16-byte loads, 8 in flight per lane.
+    Each size reads a fresh region of a 4 GiB buffer per repetition (cold for
+    the 256 MB MALL); best of `reps`, timed with HIP events."""
+    from ._lib import check
+
+    t = _torch()
+    buf = t.empty(4 << 30, dtype=t.uint8, device="cuda").fill_(1)
+    out = t.zeros(4, dtype=t.int32, device="cuda")
+    rows = []
+    for mb in HBM_READ_SIZES_MB:
+        nbytes = mb << 20
+        for wg in (512, 2048, 8192):
+            best = 1e9
+            for r in range(reps + 1):
+                off = ((r * nbytes) % ((4 << 30) - nbytes)) // 256 * 256
+                e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+                e0.record()
+                check(lib.hero_read_probe(buf.data_ptr() + off, nbytes, wg, _p(out), _stream()))
+                e1.record()
+                e1.synchronize()
+                if r:  # the first launch warms the code path
+                    best = min(best, e0.elapsed_time(e1) * 1e-3)
+            rows.append({"suite": "hbm", "kernel": "read_probe", "MB": mb, "workgroups": wg, "us": best * 1e6,
+                         "GB/s": nbytes / best / 1e9, "hbm_frac": nbytes / best / 1e9 / HBM_PEAK_GBS})
+            print(json.dumps(rows[-1]), flush=True)
+    del buf
+    t.cuda.empty_cache()
+    return rows
+
+
 # ---- gated delta-net -----------------------------------------------------------------------------
 def _gdn_case(lib, hk: int, hv: int, B: int, W: int, gen):
     from ._lib import GdnDecodeArgs
@@ -392,12 +432,45 @@ def bench_attn(lib, replays: int = 20):
                 del work
             del pages
             t.cuda.empty_cache()
+            # the same over Q8_0 pages: int8 rows (random) and fp16 block
+            # scales of the inputs' size (|N(0,1)|/sqrt(128) max / 127)
+            pb = lib.hero_attn_page_bytes(hkv, page, 1)
+            pages8 = []
+            for _ in range(max(1, min(16, math.ceil(512e6 / (B * max_pages * pb))))):
+                pg = t.randint(-127, 128, (B * max_pages, pb), dtype=t.int8, device="cuda", generator=gen).view(t.uint8)
+                q_bytes = 2 * hkv * page * dh
+                d = t.full((B * max_pages, (pb - q_bytes) // 2), 3.0 * scale / 127.0, device="cuda").half()
+                pg[:, q_bytes:] = d.view(t.uint8)
+                pages8.append(pg.contiguous())
+            for name, window, sc in (("full", 0, scale), ("swa1024", 1024, 1.0)):
+                wbytes = lib.hero_attn_paged_work_bytes(ctx, window, B, hq, hkv)
+                work = _bytes(wbytes)
+                args = []
+                for pg in pages8:
+                    a = AttnDecodeArgs(_p(proj), stride, 2 * qw, 2 * qw + kw, _p(gq), _p(gk), 1e-6, _p(cs), None, None, 0,
+                                       _p(pos), None, _p(qrot), sc, window, _p(act), None, B, hq, hkv, dh)
+                    args.append(AttnPagedArgs(a, _p(pg), _p(table), page, max_pages, _p(work), wbytes, 1))
+
+                def body():
+                    for pa in args:
+                        check(lib.hero_attn_decode_paged(pa, _stream()))
+
+                sec = _time_graph(body, len(args), replays)
+                l_eff = ctx if window == 0 else min(ctx, window)
+                nbytes = B * l_eff * kw * 2 * (1 + 2 / 32) + B * (qw + 2 * kw + qw) * 4
+                rows.append({"suite": "attn", "kernel": "attn_decode_paged (prep + split-K + combine), Q8_0 K/V",
+                             "variant": name, "ctx": ctx, "B": B, "copies": len(pages8), "us": sec * 1e6,
+                             "GB/s": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS})
+                print(json.dumps(rows[-1]), flush=True)
+                del work
+            del pages8
+            t.cuda.empty_cache()
     return rows
 
 
 def _markdown(rows) -> str:
     out = []
-    for suite in ("gemv", "kquant", "gdn", "attn"):
+    for suite in ("hbm", "gemv", "kquant", "gdn", "attn"):
         rs = [r for r in rows if r["suite"] == suite]
         if not rs:
             continue
@@ -447,6 +520,8 @@ def main(argv=None) -> int:
     suites = args.suite.split(",")
     if "gemv" in suites:
         rows += bench_gemv(lib, batches=[int(v) for v in args.gemv_batches.split(",")])
+    if "hbm" in suites:
+        rows += bench_hbm(lib)
     if "kquant" in suites:
         rows += bench_kquant(lib)
     if "gdn" in suites:

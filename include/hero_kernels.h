@@ -297,6 +297,13 @@ typedef struct hero_attn_paged_args {
 } hero_attn_paged_args;
 int64_t hero_attn_page_bytes(int32_t hkv, int32_t page_size, int32_t q8);
 int64_t hero_attn_paged_work_bytes(int64_t max_ctx, int32_t window, int32_t b, int32_t hq, int32_t hkv);
+
+/* Measurement (no counterpart in the reference): `workgroups` workgroups of
+ * 256 lanes read `bytes` of p (a multiple of 16, 16-byte aligned) with 16-byte
+ * loads, each its contiguous share, and store nothing (out is written only on
+ * an impossible fold): the read bandwidth the memory-bound kernels are
+ * compared with. */
+int hero_read_probe(const void* p, int64_t bytes, int32_t workgroups, uint32_t* out, void* stream);
 int hero_attn_decode_paged(const hero_attn_paged_args* args, void* stream);
 
 #ifdef __cplusplus

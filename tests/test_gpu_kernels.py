@@ -622,8 +622,10 @@ def test_attn_paged_fp16_matches_oracle_over_fp16_kv(lib, hq, window):
     shuffled pool, contexts up to 300 (several pages per tile, several
     splits), 4 and 8 query heads per KV head, full and windowed. The oracle
     attends over the same K/V rounded to fp16 (its storage), sequentially; the
-    split softmax merges in another order, so the outputs agree to a few ulp,
-    the quantized W_o input to one step of its scale."""
+    split kernel sums dot products by channel quarters with fused multiply-adds
+    and merges the split softmax in another order, so the outputs agree within
+    rtol 1e-4 + atol 1e-4 * max|out| (measured: a few 1e-6 absolute), and the
+    quantized W_o input is the quantization of the kernel's own output."""
     from hero_amd._lib import AttnDecodeArgs, AttnPagedArgs
 
     rng = np.random.default_rng(23 + hq + window)
@@ -673,7 +675,7 @@ def test_attn_paged_fp16_matches_oracle_over_fp16_kv(lib, hq, window):
             q = oracle.rope_apply(oracle.rmsnorm(q, qg, eps), inv, step)
             att = oracle.attend_decode(q.reshape(-1), keys[b], vals[b], hq, hkv, dh, window, scale).reshape(-1)
             expect = (att * oracle.sigmoid(g)).astype(np.float32)
-            np.testing.assert_allclose(got[b], expect, rtol=2e-5, atol=2e-6, err_msg=f"step {step} seq {b}")
+            np.testing.assert_allclose(got[b], expect, rtol=1e-4, atol=1e-4 * np.abs(expect).max(), err_msg=f"step {step} seq {b}")
             want = oracle.quantize_row_q8_0(got[b])
             assert blocks[b].tobytes() == want.tobytes()  # the kernel quantizes its own output exactly
             checked += 1

@@ -704,10 +704,14 @@ void Qwen35Model::typed_layers(State& st, TypedScratch& ts, float* x, float* h, 
             a.Dk = int(c.Dk);
             a.Dv = int(c.Dv);
             a.W = int(c.W);
-            if (chunk)
+            if (chunk) {
                 launch_gdn_prefill(a, st.cgdn_work_.get(), s, st.gdn_chunked_);
-            else
+            } else if (M == 1) {  // one row: the step split over value columns, then the head norm and gate
+                launch_gdn_decode_cols(a, st.o_raw_.get<float>(), nullptr, s);
+                launch_gdn_norm_gate(st.o_raw_.get<float>(), a, s);
+            } else {  // many sequences fill the GPU with the fused kernel
                 launch_gdn_decode(a, s);
+            }
         } else {
             AttnDecodeArgs a{};
             a.proj = proj;

@@ -566,19 +566,13 @@ __global__ __launch_bounds__(kGdnDim) void gdn_norm_gate_kernel(const float* __r
 // and the ring are sequence 0's. Three kernels:
 //  prep  (token, head) in parallel: conv + SiLU, L2 norms and the query scale,
 //        beta and the decay -- nothing here depends on the state;
-//  scan  one workgroup per value head runs the delta rule over the tokens in
-//        order, the state column of lane j in registers for the whole chunk;
+//  scan  the delta rule over the tokens in order, 8 workgroups per value
+//        head, the state in registers for the whole chunk (below);
 //  out   (token, head) in parallel: head RMSNorm, SiLU(z) gate, quantize.
 // The scan's critical path per token is one 128-term chain: token t's output
 // chain and token t+1's decay and prediction chain read the same updated
-// column, so they run in one pass over i. Every value is computed by the same
+// column, so they run side by side. Every value is computed by the same
 // operations in the same order as in gdn_decode_kernel.
-constexpr int kScanTile = 16;   // tokens staged in shared memory per tile
-constexpr int kScanChunk = 16;  // state rows per fenced step of the token loop
-__device__ __forceinline__ void scan_fence() {
-    __asm__ volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);  // and no instruction scheduled across it
-}
 
 __device__ __forceinline__ GdnPrefillWork gdn_work(void* ws, int64_t T, int Hk, int Hv) {
     GdnPrefillWork w;
@@ -650,54 +644,113 @@ __global__ __launch_bounds__(kGdnDim) void gdn_prep_kernel(GdnDecodeArgs a, void
     }
 }
 
-// one tile of kScanTile tokens of a head: q, k (its key head), v, (beta, decay)
-struct ScanTile {
-    float q[kScanTile][kGdnDim];
-    float k[kScanTile][kGdnDim];
-    float v[kScanTile][kGdnDim];
-    float bd[kScanTile][2];
+// ---- the token-serial scan, split over value columns and state rows ----------------------
+// The delta rule over the chunk's tokens in order, each value column spread
+// over 16 lanes (one DPP row): the columns of the delta rule are independent
+// (nm/src/recurrent.hpp:146-177), so a workgroup of 256 lanes owns 16 columns
+// and a head takes 8 workgroups. Lane 2s + c of a row holds rows 16s .. 16s+15
+// of its column (segment s); lanes c = 0 run token t+1's decay-and-prediction
+// chain and lanes c = 1 token t's output chain, both over the same updated
+// rows, so one instruction stream advances both chains. A chain visits the
+// segments in row order: segment s adds its 16 terms to the running sum that
+// segment s-1 handed on (a DPP shift by two lanes), so every sum is the
+// reference's left-to-right chain. Both lanes of a segment keep the same
+// copy of the segment's rows. Per token and wave that is 16 rows of updates
+// and products plus the chains' 128 steps, against 128 rows of each for a
+// lane owning a whole column.
+constexpr int kScCols = 16;                  // value columns per workgroup
+constexpr int kScSeg = 8;                    // row segments per column
+constexpr int kScRows = kGdnDim / kScSeg;    // rows per lane (16)
+constexpr int kScTile = 16;                  // tokens per shared-memory tile
+struct ScanColsTile {
+    float k[kScTile][kGdnDim];
+    float q[kScTile][kGdnDim];
+    float v[kScTile][kScCols];
+    float bd[kScTile][2];
 };
-constexpr int kScanVec = 3 * kScanTile * kGdnDim / 4 / kGdnDim;  // float4 per lane per tile (12)
 
-__global__ __launch_bounds__(kGdnDim) void gdn_scan_kernel(GdnDecodeArgs a, void* ws) {
-    const int j = threadIdx.x, h = blockIdx.x, hk = h % a.Hk;
+// the running sum of lane i-2 of each row of 16 lanes, in lane i
+__device__ __forceinline__ float row_shr2(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x112, 0xF, 0xF, false));
+}
+// segment s (lanes 2s, 2s+1 of each row) adds its terms, in row order, to the
+// sum handed on by segment s-1; the final sums end in lanes 14 and 15
+__device__ __forceinline__ float seg_chain(const float (&prod)[kScRows], int seg) {
+    float acc = 0.f;
+#pragma unroll
+    for (int s = 0; s < kScSeg; ++s) {
+        if (seg == s) {
+#pragma unroll
+            for (int m = 0; m < kScRows; ++m) acc = acc + prod[m];
+        }
+        if (s + 1 < kScSeg) acc = row_shr2(acc);
+    }
+    return acc;
+}
+// lane 14 of each row of the wave, in every lane of that row
+__device__ __forceinline__ float row_lane14(float v, int row) {
+    const int b = __float_as_int(v);
+    const int r0 = __builtin_amdgcn_readlane(b, 14), r1 = __builtin_amdgcn_readlane(b, 30);
+    const int r2 = __builtin_amdgcn_readlane(b, 46), r3 = __builtin_amdgcn_readlane(b, 62);
+    return __int_as_float(row == 0 ? r0 : row == 1 ? r1 : row == 2 ? r2 : r3);
+}
+
+__global__ __launch_bounds__(256) void gdn_scan_cols_kernel(GdnDecodeArgs a, void* ws) {
+    const int lane = threadIdx.x;
+    const int h = blockIdx.x / (kGdnDim / kScCols), c0 = (blockIdx.x % (kGdnDim / kScCols)) * kScCols, hk = h % a.Hk;
+    const int jl = lane / 16, seg = (lane % 16) / 2, ch = lane % 2, row = (lane % 64) / 16;
+    const int j = c0 + jl, r0 = seg * kScRows;
     const int T = a.B;
     if (a.positions[0] < 0) return;
     const GdnPrefillWork w = gdn_work(ws, T, a.Hk, a.Hv);
-    float* S = a.state + int64_t(h) * kGdnState;
-    __shared__ __align__(16) ScanTile tiles[2];
-    const int ntiles = (T + kScanTile - 1) / kScanTile;
+    float* S = a.state + int64_t(h) * kGdnState + j;
+    __shared__ __align__(16) ScanColsTile tiles[2];
+    const int ntiles = (T + kScTile - 1) / kScTile;
 
-    // tile loads: float4 f = j + 128u; u < 4: q, u < 8: k, else v; token (f % 512) / 32
-    float4 pre[kScanVec];
-    float2 pre_bd = make_float2(0.f, 0.f);
+    // a tile: k and q (2 float4 each per lane), v of the 16 columns (lanes
+    // 0..63) and (beta, decay) (lanes 64..79); zeros past the last token
+    float4 pk[2], pq[2], pv = make_float4(0.f, 0.f, 0.f, 0.f);
+    float2 pbd = make_float2(0.f, 0.f);
     auto load = [&](int tile) {
-        const int t0 = tile * kScanTile;
+        const int t0 = tile * kScTile;
 #pragma unroll
-        for (int u = 0; u < kScanVec; ++u) {
-            const int f = (j + kGdnDim * u) % (kScanTile * kGdnDim / 4);
-            const int tt = t0 + f / (kGdnDim / 4), c4 = f % (kGdnDim / 4);
-            const float* src = u < 4 ? w.q + (int64_t(tt) * a.Hk + hk) * kGdnDim : u < 8 ? w.k + (int64_t(tt) * a.Hk + hk) * kGdnDim : w.v + (int64_t(tt) * a.Hv + h) * kGdnDim;
-            pre[u] = tt < T ? reinterpret_cast<const float4*>(src)[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int u = 0; u < 2; ++u) {
+            const int f = lane + 256 * u, tt = t0 + f / (kGdnDim / 4), c4 = f % (kGdnDim / 4);
+            const int64_t o = (int64_t(tt) * a.Hk + hk) * kGdnDim;
+            pk[u] = tt < T ? reinterpret_cast<const float4*>(w.k + o)[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+            pq[u] = tt < T ? reinterpret_cast<const float4*>(w.q + o)[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        if (j < kScanTile && t0 + j < T) pre_bd = reinterpret_cast<const float2*>(w.bd)[int64_t(t0 + j) * a.Hv + h];
+        if (lane < 64) {
+            const int tt = t0 + lane / 4;
+            pv = tt < T ? reinterpret_cast<const float4*>(w.v + (int64_t(tt) * a.Hv + h) * kGdnDim + c0)[lane % 4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        } else if (lane < 64 + kScTile) {
+            const int tt = t0 + lane - 64;
+            pbd = tt < T ? reinterpret_cast<const float2*>(w.bd)[int64_t(tt) * a.Hv + h] : make_float2(0.f, 0.f);
+        }
     };
-    auto store = [&](ScanTile& dst) {
+    auto store = [&](ScanColsTile& dst) {
 #pragma unroll
-        for (int u = 0; u < kScanVec; ++u) {
-            const int f = (j + kGdnDim * u) % (kScanTile * kGdnDim / 4);
-            float* base = u < 4 ? &dst.q[0][0] : u < 8 ? &dst.k[0][0] : &dst.v[0][0];
-            reinterpret_cast<float4*>(base)[f] = pre[u];
+        for (int u = 0; u < 2; ++u) {
+            reinterpret_cast<float4*>(&dst.k[0][0])[lane + 256 * u] = pk[u];
+            reinterpret_cast<float4*>(&dst.q[0][0])[lane + 256 * u] = pq[u];
         }
-        if (j < kScanTile) {
-            dst.bd[j][0] = pre_bd.x;
-            dst.bd[j][1] = pre_bd.y;
+        if (lane < 64)
+            reinterpret_cast<float4*>(&dst.v[0][0])[lane] = pv;
+        else if (lane < 64 + kScTile)
+            reinterpret_cast<float2*>(&dst.bd[0][0])[lane - 64] = pbd;
+    };
+    auto rows16 = [&](const float* src, float (&dst)[kScRows]) {
+        const float4* s4 = reinterpret_cast<const float4*>(src + r0);
+#pragma unroll
+        for (int u = 0; u < kScRows / 4; ++u) {
+            const float4 x = s4[u];
+            dst[4 * u] = x.x, dst[4 * u + 1] = x.y, dst[4 * u + 2] = x.z, dst[4 * u + 3] = x.w;
         }
     };
 
-    float col[kGdnDim];  // S[i][j], i = 0..127: this lane's state column
+    float col[kScRows];  // S[r0 + m][j]
 #pragma unroll
-    for (int i = 0; i < kGdnDim; ++i) col[i] = S[i * kGdnDim + j];
+    for (int m = 0; m < kScRows; ++m) col[m] = S[int64_t(r0 + m) * kGdnDim];
     load(0);
     store(tiles[0]);
     if (ntiles > 1) {
@@ -707,26 +760,22 @@ __global__ __launch_bounds__(kGdnDim) void gdn_scan_kernel(GdnDecodeArgs a, void
     if (ntiles > 2) load(2);
     __syncthreads();
 
-    // token 0: decay and prediction chain
-    float pred = 0.f;
+    // token 0: decay and prediction chain (nm/src/recurrent.hpp:152-160)
+    float delta;
     {
+        float kk[kScRows], prod[kScRows];
+        rows16(tiles[0].k[0], kk);
         const float dec = tiles[0].bd[0][1];
-        const float* kn = tiles[0].k[0];
 #pragma unroll
-        for (int i0 = 0; i0 < kGdnDim; i0 += 4) {
-            const float4 k4 = *reinterpret_cast<const float4*>(kn + i0);
-            col[i0 + 0] = col[i0 + 0] * dec;
-            pred = pred + col[i0 + 0] * k4.x;
-            col[i0 + 1] = col[i0 + 1] * dec;
-            pred = pred + col[i0 + 1] * k4.y;
-            col[i0 + 2] = col[i0 + 2] * dec;
-            pred = pred + col[i0 + 2] * k4.z;
-            col[i0 + 3] = col[i0 + 3] * dec;
-            pred = pred + col[i0 + 3] * k4.w;
+        for (int m = 0; m < kScRows; ++m) {
+            col[m] = col[m] * dec;
+            prod[m] = col[m] * kk[m];
         }
+        const float pred = row_lane14(seg_chain(prod, seg), row);
+        delta = (tiles[0].v[0][jl] - pred) * tiles[0].bd[0][0];
     }
     for (int t = 0; t < T; ++t) {
-        const int tile = t / kScanTile, r = t % kScanTile;
+        const int tile = t / kScTile, r = t % kScTile;
         if (r == 0 && tile > 0) {
             // tile-1's buffer is free: it takes tile+1 (loaded a tile ago)
             __syncthreads();
@@ -734,75 +783,42 @@ __global__ __launch_bounds__(kGdnDim) void gdn_scan_kernel(GdnDecodeArgs a, void
             if (tile + 2 < ntiles) load(tile + 2);
             __syncthreads();
         }
-        const ScanTile& cur = tiles[tile & 1];
-        const float* qt = cur.q[r];
-        const float* kt = cur.k[r];
-        const float delta = (cur.v[r][j] - pred) * cur.bd[r][0];
-        float o = 0.f;
+        const ScanColsTile& cur = tiles[tile & 1];
+        const ScanColsTile& nxt = tiles[((t + 1) / kScTile) & 1];
+        const int rn = (t + 1) % kScTile;
+        float kc[kScRows], f[kScRows], prod[kScRows];
+        rows16(cur.k[r], kc);
+        // lanes c = 0: token t+1's key (zeros past the last token); c = 1: token t's query
+        rows16(ch == 0 ? nxt.k[rn] : cur.q[r], f);
+        float o;
         if (t + 1 < T) {
-            const ScanTile& nxt = tiles[((t + 1) / kScanTile) & 1];
-            const int rn = (t + 1) % kScanTile;
-            const float* kn = nxt.k[rn];
             const float dec = nxt.bd[rn][1];
-            float pn = 0.f;
-            // k, q and the next k in chunks of kScanChunk rows, the next
-            // chunk's shared-memory reads in flight while this one computes
-            float4 bk[2][kScanChunk / 4], bq[2][kScanChunk / 4], bn[2][kScanChunk / 4];
-            auto fetch = [&](int c, int buf) {
 #pragma unroll
-                for (int u = 0; u < kScanChunk / 4; ++u) {
-                    bk[buf][u] = *reinterpret_cast<const float4*>(kt + c * kScanChunk + 4 * u);
-                    bq[buf][u] = *reinterpret_cast<const float4*>(qt + c * kScanChunk + 4 * u);
-                    bn[buf][u] = *reinterpret_cast<const float4*>(kn + c * kScanChunk + 4 * u);
-                }
-            };
-            fetch(0, 0);
-#pragma unroll
-            for (int c = 0; c < kGdnDim / kScanChunk; ++c) {
-                if (c + 1 < kGdnDim / kScanChunk) fetch(c + 1, (c + 1) & 1);
-                scan_fence();
-#pragma unroll
-                for (int u = 0; u < kScanChunk / 4; ++u) {
-                    const float4 k4 = bk[c & 1][u], q4 = bq[c & 1][u], n4 = bn[c & 1][u];
-                    const float kk[4] = {k4.x, k4.y, k4.z, k4.w}, qq[4] = {q4.x, q4.y, q4.z, q4.w}, nn[4] = {n4.x, n4.y, n4.z, n4.w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int i = c * kScanChunk + 4 * u + e;
-                        float v = col[i] + kk[e] * delta;  // S[i][j] += k[i] * delta
-                        o = o + v * qq[e];                 // o += S[i][j] * q[i]
-                        v = v * dec;                       // next token: S[i][j] *= decay
-                        pn = pn + v * nn[e];               //             pred += S[i][j] * k[i]
-                        col[i] = v;
-                    }
-                }
+            for (int m = 0; m < kScRows; ++m) {
+                const float v = col[m] + kc[m] * delta;  // S[i][j] += k[i] * delta
+                const float vd = v * dec;                // next token: S[i][j] *= decay
+                col[m] = vd;
+                prod[m] = (ch == 0 ? vd : v) * f[m];     // pred += S[i][j] * k'[i]  |  o += S[i][j] * q[i]
             }
-            pred = pn;
+            const float acc = seg_chain(prod, seg);
+            o = acc;
+            const float pred = row_lane14(acc, row);
+            delta = (nxt.v[rn][jl] - pred) * nxt.bd[rn][0];
         } else {
 #pragma unroll
-            for (int i1 = 0; i1 < kGdnDim; i1 += kScanChunk) {
-                scan_fence();
-#pragma unroll
-                for (int i0 = i1; i0 < i1 + kScanChunk; i0 += 4) {
-                    const float4 k4 = *reinterpret_cast<const float4*>(kt + i0);
-                    const float4 q4 = *reinterpret_cast<const float4*>(qt + i0);
-                    const float kk[4] = {k4.x, k4.y, k4.z, k4.w}, qq[4] = {q4.x, q4.y, q4.z, q4.w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float v = col[i0 + e] + kk[e] * delta;
-                        o = o + v * qq[e];
-                        col[i0 + e] = v;
-                    }
-                }
+            for (int m = 0; m < kScRows; ++m) {
+                const float v = col[m] + kc[m] * delta;
+                col[m] = v;
+                prod[m] = v * f[m];
             }
+            o = seg_chain(prod, seg);
         }
-        w.o[(int64_t(t) * a.Hv + h) * kGdnDim + j] = o;
+        if (lane % 16 == 15) w.o[(int64_t(t) * a.Hv + h) * kGdnDim + j] = o;
     }
-    // a fresh base pointer: otherwise the 128 row addresses of the first
-    // loads are kept alive across the token loop for these stores
-    float* Sw = S;
-    __asm__ volatile("" : "+s"(Sw));
+    if (ch == 1) {
 #pragma unroll
-    for (int i = 0; i < kGdnDim; ++i) Sw[i * kGdnDim + j] = col[i];
+        for (int m = 0; m < kScRows; ++m) S[int64_t(r0 + m) * kGdnDim] = col[m];
+    }
 }
 
 // ---- the chunked form (WY representation) ------------------------------------------------
@@ -1177,7 +1193,7 @@ void launch_gdn_prefill(const GdnDecodeArgs& a, void* work, hipStream_t s, bool 
         hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(unsigned(a.Hv), unsigned(kGdnDim / kChunkCols)), dim3(256), kChunkScanShared, s, a, work);
     }
     else
-        hipLaunchKernelGGL(gdn_scan_kernel, dim3(unsigned(a.Hv)), dim3(kGdnDim), 0, s, a, work);
+        hipLaunchKernelGGL(gdn_scan_cols_kernel, dim3(unsigned(a.Hv * (kGdnDim / kScCols))), dim3(256), 0, s, a, work);
     hipLaunchKernelGGL(gdn_out_kernel, dim3(unsigned(a.Hv), unsigned(a.B)), dim3(kGdnDim), 0, s, a, work);
     const int64_t CC = 2 * int64_t(a.Hk) * kGdnDim + int64_t(a.Hv) * kGdnDim;
     const int64_t n = int64_t(std::min(a.B, a.W)) * CC;

@@ -102,25 +102,31 @@ void launch_pack_q8(const void* gguf_blocks, void* packed, int64_t N_total, int6
 // ---------------------------------------------------------------------------
 constexpr int kStreamRB = 8;  // rows per sub-batch
 
-template <int LG, int D, int EPI, int XM>
+template <int LG, int D, int EPI, int XM, int IL>
 __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, GemvInput in, float* __restrict__ y, const float* __restrict__ resid, int N, int Npad, int TR) {
     constexpr int K = 4096 * LG, nb = K / 32, ts = nb + 4;  // ts: padded term row (conflict-free 16-byte reads)
     constexpr int CPL = 1;  // K-chunks per lane
     // row ranges in whole units: 8-row groups, or for the SwiGLU epilogue
     // 64-row groups of [32 gate rows | 32 up rows]
     constexpr int UR = EPI == kEpiSwigluQuant ? 64 : 8;
+    static_assert(!IL || UR == 8, "interleaved groups are 8-row groups");
     extern __shared__ __align__(16) float terms[];          // [TR][ts]; the prologue's squares before that
     const int tid = threadIdx.x;
     const int G = gridDim.x, U = Npad / UR;
-    const int r_begin = UR * int((int64_t(U) * blockIdx.x) / G);
-    const int r_end = min(N, UR * int((int64_t(U) * (blockIdx.x + 1)) / G));
+    // IL: the 8-row groups g, g + G, g + 2G, ... of workgroup g (at any moment
+    // the grid reads one contiguous stretch of the matrix); otherwise a
+    // contiguous range of units
+    const int r_begin = IL ? 0 : UR * int((int64_t(U) * blockIdx.x) / G);
+    const int r_end = IL ? N : min(N, UR * int((int64_t(U) * (blockIdx.x + 1)) / G));
     const int rows = max(r_end - r_begin, 0);
-    const int nsub = (rows + kStreamRB - 1) / kStreamRB;
+    const int nsub = IL ? (U - int(blockIdx.x) + G - 1) / G : (rows + kStreamRB - 1) / kStreamRB;
+    auto grp = [&](int j) { return IL ? int(blockIdx.x) + j * G : r_begin / kStreamRB + j; };  // 8-row group of sub-batch j
     const bool even = (tid & 1) == 0;
     // the workgroup's rows (rows * K bytes) and their scale groups (nsub groups
-    // of nb blocks x 8 fp16; r_begin is a multiple of 8)
+    // of nb blocks x 8 fp16; r_begin is a multiple of 8); IL: the whole matrix
     const __amdgpu_buffer_rsrc_t bw = buffer_of(wq + int64_t(r_begin) * K, uint32_t(rows) * uint32_t(K));
-    const __amdgpu_buffer_rsrc_t bd = buffer_of(wd + scale_index(r_begin, 0, nb), uint32_t(nsub) * uint32_t(nb) * 16u);
+    const __amdgpu_buffer_rsrc_t bd = IL ? buffer_of(wd, uint32_t(Npad / 8) * uint32_t(nb) * 16u)
+                                         : buffer_of(wd + scale_index(r_begin, 0, nb), uint32_t(nsub) * uint32_t(nb) * 16u);
 
     int4 ring[D][kStreamRB][CPL];
     int4 sring[D][CPL];  // even lanes: scales of the sub-batch's 8 rows for each of the lane's blocks
@@ -128,15 +134,18 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
     // compute consumes them); the scheduling fences keep that issue order, on
     // which the compiler's counted waits depend
     auto load = [&](int j, int4 (&dst)[kStreamRB][CPL], int4 (&sdst)[CPL]) {
-        const uint32_t row0 = uint32_t(j * kStreamRB);
+        // past the workgroup's last sub-batch: out-of-range offsets (zeros)
+        const bool live = !IL || j < nsub;
+        const uint32_t gj = IL ? uint32_t(grp(j)) : uint32_t(j);
+        const uint32_t row0 = gj * kStreamRB;
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int m = 0; m < CPL; ++m)  // the group's 8 scales of block tid / 2
-            sdst[m] = load_b128(bd, even ? (uint32_t(j) * uint32_t(nb) + uint32_t(tid >> 1)) * 16u : kOOB);
+            sdst[m] = load_b128(bd, even && live ? (gj * uint32_t(nb) + uint32_t(tid >> 1)) * 16u : kOOB);
 #pragma unroll
         for (int r = 0; r < kStreamRB; ++r)
 #pragma unroll
-            for (int m = 0; m < CPL; ++m) dst[r][m] = load_b128(bw, (row0 + uint32_t(r)) * uint32_t(K) + uint32_t(tid) * 16u);
+            for (int m = 0; m < CPL; ++m) dst[r][m] = load_b128(bw, live ? (row0 + uint32_t(r)) * uint32_t(K) + uint32_t(tid) * 16u : kOOB);
         __builtin_amdgcn_sched_barrier(0);
     };
     // The lane's x chunk tid as Q8_0, and the residual of the first
@@ -188,8 +197,10 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
     }
     // residual epilogue: the workgroup's slice of the residual (empty otherwise)
     const __amdgpu_buffer_rsrc_t br = buffer_of(EPI == kEpiResidual ? resid + r_begin : y, EPI == kEpiResidual ? uint32_t(rows) * 4u : 0u);
+    // chain lane t's row in a pass that starts at sub-batch j0 (IL) or row r0
+    auto chain_row = [&](int j0, int r0) { return IL ? grp(j0 + tid / kStreamRB) * kStreamRB + (tid % kStreamRB) : r0 + tid; };
     float rnext = 0.f;  // residual of the lane's row in the next chain pass
-    if constexpr (EPI == kEpiResidual) rnext = load_f32(br, uint32_t(tid) * 4u);
+    if constexpr (EPI == kEpiResidual) rnext = load_f32(br, uint32_t(chain_row(0, 0)) * 4u);
 #pragma unroll
     for (int s = 0; s < D; ++s) load(s, ring[s], sring[s]);
     // the input loads are complete once at most the ring's loads are
@@ -265,13 +276,16 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
         }
     }
 
-    int chain_row0 = r_begin;  // first row of the pending chain pass
+    int chain_row0 = r_begin;  // first row (IL: first term slot) of the pending chain pass
+    int chain_j0 = 0;          // its first sub-batch
     const int nsub_pad = (nsub + D - 1) / D * D;
     for (int base = 0; base < nsub_pad; base += D) {
 #pragma unroll
         for (int s = 0; s < D; ++s) {
             const int j = base + s;
-            const int rb = r_begin + j * kStreamRB;
+            // rb - chain_row0: the sub-batch's first term slot; rvalid: its rows inside the matrix / range
+            const int rb = IL ? chain_row0 + (j - chain_j0) * kStreamRB : r_begin + j * kStreamRB;
+            const int rvalid = IL ? (j < nsub ? min(kStreamRB, N - grp(j) * kStreamRB) : 0) : r_end - rb;
 #pragma unroll
             for (int r = 0; r < kStreamRB; ++r) {
                 const uint32_t pair = uint32_t(r < 4 ? (r < 2 ? 0 : 1) : (r < 6 ? 2 : 3));
@@ -279,7 +293,7 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
                 for (int m = 0; m < CPL; ++m) {
                     int v = dot16_i8(ring[s][r][m], xv[m], 0);
                     v += pair_swap_i32(v);  // the block's other 16 bytes (exact)
-                    if (even && rb + r < r_end) {
+                    if (even && r < rvalid) {
                         const int4 sc = sring[s][m];
                         const uint32_t two = uint32_t(pair == 0 ? sc.x : pair == 1 ? sc.y : pair == 2 ? sc.z : sc.w);
                         const uint16_t h = uint16_t((r & 1) ? (two >> 16) : (two & 0xFFFFu));
@@ -290,7 +304,7 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
             load(j + D, ring[s], sring[s]);  // zeros past the last sub-batch
             const int done = rb + kStreamRB - chain_row0;  // rows whose terms are all stored
             if (j < nsub && (done >= TR || j + 1 == nsub)) {
-                const int prow = min(done, r_end - chain_row0);
+                const int prow = IL ? done : min(done, r_end - chain_row0);
                 __syncthreads();
                 if (tid < prow) {
                     const float4* t = reinterpret_cast<const float4*>(terms + tid * ts);
@@ -312,8 +326,10 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
 #pragma unroll
                         for (int u = 0; u < 4; ++u) q[u] = nq[u];
                     }
-                    const int64_t o = chain_row0 + tid;
-                    if constexpr (EPI == kEpiResidual)
+                    const int64_t o = chain_row(chain_j0, chain_row0);
+                    if (IL && o >= N) {
+                        // a padding row of the last 8-row group
+                    } else if constexpr (EPI == kEpiResidual)
                         y[o] = rnext + acc;  // h = x + m (nm/src/qwen35.hpp:321)
                     else if constexpr (EPI == kEpiStore)
                         y[o] = acc;
@@ -338,7 +354,8 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
                 }
                 __syncthreads();
                 chain_row0 += prow;
-                if constexpr (EPI == kEpiResidual) rnext = load_f32(br, uint32_t(chain_row0 - r_begin + tid) * 4u);
+                chain_j0 = j + 1;
+                if constexpr (EPI == kEpiResidual) rnext = load_f32(br, uint32_t(chain_row(chain_j0, chain_row0) - r_begin) * 4u);
             }
         }
     }
@@ -431,18 +448,22 @@ int device_cus() {
 
 namespace {
 
+// K = 4096 outside the SwiGLU epilogue: interleaved 8-row groups (the grid
+// reads one contiguous stretch of the matrix at a time: 0.3-2.7 us less per
+// launch at the decode shapes); K = 8192, 12288 keep contiguous ranges
 template <int LG, int D, int XM>
 void stream_dispatch(int epi, const int8_t* wq, const uint16_t* wd, const GemvInput& in, float* y, const float* resid, int N, int Npad, int G, int TR, size_t smem, hipStream_t s) {
     const dim3 block(256 * LG);
+    constexpr int IL = LG == 1;
     if (epi == kEpiResidual)
-        hipLaunchKernelGGL((gemv_q8_stream_kernel<LG, D, kEpiResidual, XM>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
+        hipLaunchKernelGGL((gemv_q8_stream_kernel<LG, D, kEpiResidual, XM, IL>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
     else if constexpr (LG == 1)
         if (epi == kEpiSwigluQuant)
-            hipLaunchKernelGGL((gemv_q8_stream_kernel<LG, D, kEpiSwigluQuant, XM>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
+            hipLaunchKernelGGL((gemv_q8_stream_kernel<LG, D, kEpiSwigluQuant, XM, 0>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
         else
-            hipLaunchKernelGGL((gemv_q8_stream_kernel<LG, D, kEpiStore, XM>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
+            hipLaunchKernelGGL((gemv_q8_stream_kernel<LG, D, kEpiStore, XM, IL>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
     else
-        hipLaunchKernelGGL((gemv_q8_stream_kernel<LG, D, kEpiStore, XM>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
+        hipLaunchKernelGGL((gemv_q8_stream_kernel<LG, D, kEpiStore, XM, 0>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
 }
 
 template <int LG, int D>

@@ -446,31 +446,34 @@ __global__ __launch_bounds__(64) void gdn_decode_cols_kernel(GdnDecodeArgs a, fl
         if (r == 0) hist[int64_t(slot) * CC + cv] = xv;
     }
     __syncthreads();
-    // ---- L2 norms of q and k (nm/src/recurrent.hpp:40-48): every lane runs
-    // both sequential sums (broadcast reads) ----
-    float ssq = 0.f, ssk = 0.f;
+    // ---- L2 norms of q and k (nm/src/recurrent.hpp:40-48): even lanes run
+    // the sequential sum of q's squares, odd lanes k's (broadcast reads), and
+    // lanes 0 and 1 hand the two sums to the wave ----
+    float ssq, ssk;
     {
-        const float4* q4 = reinterpret_cast<const float4*>(sh.sq[0]);
-        const float4* k4 = reinterpret_cast<const float4*>(sh.sq[1]);
-        float4 qc[8], kc[8], qn[8], kn[8];
+        const float4* s4 = reinterpret_cast<const float4*>(sh.sq[t & 1]);
+        float4 cur[8], nxt[8];
+        float ss = 0.f;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) qc[u] = q4[u], kc[u] = k4[u];
+        for (int u = 0; u < 8; ++u) cur[u] = s4[u];
 #pragma unroll
         for (int c = 0; c < kGdnDim / 32; ++c) {
             if (c + 1 < kGdnDim / 32) {
 #pragma unroll
-                for (int u = 0; u < 8; ++u) qn[u] = q4[8 * (c + 1) + u], kn[u] = k4[8 * (c + 1) + u];
+                for (int u = 0; u < 8; ++u) nxt[u] = s4[8 * (c + 1) + u];
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                ssq += qc[u].x, ssk += kc[u].x;
-                ssq += qc[u].y, ssk += kc[u].y;
-                ssq += qc[u].z, ssk += kc[u].z;
-                ssq += qc[u].w, ssk += kc[u].w;
+                ss += cur[u].x;
+                ss += cur[u].y;
+                ss += cur[u].z;
+                ss += cur[u].w;
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) qc[u] = qn[u], kc[u] = kn[u];
+            for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
         }
+        ssq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 0));
+        ssk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 1));
     }
     const float inv_q = 1.f / fmaxf(sqrtf(ssq), 1e-6f), inv_k = 1.f / fmaxf(sqrtf(ssk), 1e-6f);
     {

@@ -129,6 +129,7 @@ def main() -> int:
     ap.add_argument("--gemv-reps", type=int, default=5)
     ap.add_argument("--batch", type=int, default=16, help="also time greedy decode of this many sequences at once (0: skip)")
     ap.add_argument("--batch-steps", type=int, default=64)
+    ap.add_argument("--no-chunked", action="store_true", help="skip the chunked delta-net prefill leg (a kernel trace then holds one exact prefill)")
     ap.add_argument("--profile-gemvs", action="store_true",
                     help="only launch a decode step's GEMVs --gemv-reps times (+1 warm-up) and print their timing: "
                          "the program the HBM-traffic counter runs profile")
@@ -177,14 +178,16 @@ def main() -> int:
     log(f"prefill {args.prompt} tokens: {prefill_s:.2f} s ({args.prompt / prefill_s:.1f} tok/s)")
     # the same prefill with the chunked delta-net form (a throughput option,
     # tolerance-equal instead of bit-equal to the reference)
-    st_c = model.new_state(ctx, gdn_chunked=True)
-    torch.cuda.synchronize()
-    t = time.perf_counter()
-    model.forward(st_c, ids=prompt, want_logits=False)
-    torch.cuda.synchronize()
-    prefill_chunked_s = time.perf_counter() - t
-    st_c.close()
-    log(f"prefill {args.prompt} tokens, chunked delta-net: {prefill_chunked_s:.2f} s ({args.prompt / prefill_chunked_s:.1f} tok/s)")
+    prefill_chunked_s = None
+    if not args.no_chunked:
+        st_c = model.new_state(ctx, gdn_chunked=True)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        model.forward(st_c, ids=prompt, want_logits=False)
+        torch.cuda.synchronize()
+        prefill_chunked_s = time.perf_counter() - t
+        st_c.close()
+        log(f"prefill {args.prompt} tokens, chunked delta-net: {prefill_chunked_s:.2f} s ({args.prompt / prefill_chunked_s:.1f} tok/s)")
 
     warm_ids = model.decode_greedy(state, first, args.warmup)[0] if args.warmup > 0 else np.array([first], np.int32)
     torch.cuda.synchronize()
@@ -251,7 +254,7 @@ def main() -> int:
             # re-quantization turns that into logit differences of up to ~0.06
             # abs, outside the 1e-2 abs / 1e-3 rel bar; prefill_tok_s is the
             # exact, bit-identical form
-            "throughput_option_outside_parity": {
+            "throughput_option_outside_parity": None if prefill_chunked_s is None else {
                 "prefill_tok_s_chunked_delta_net": args.prompt / prefill_chunked_s,
                 "parity": "tolerance only: logits up to ~0.06 abs from the exact prefill (tests/test_gpu_model.py)",
             },

@@ -454,6 +454,19 @@ int hero_attn_decode(const hero_attn_decode_args* p, void* stream) {
     });
 }
 
+int hero_attn_prefill(const hero_attn_decode_args* p, void* stream) {
+    return guard([&] {
+        require(p != nullptr, "null args");
+        const hero_attn_decode_args& a = *p;
+        require(a.k_cache && a.v_cache && a.scores, "null pointer");
+        require(a.max_ctx > 0 && a.max_ctx <= (int64_t(1) << 24), "max_ctx out of range");
+        AttnDecodeArgs g = attn_args(a);
+        g.shared_cache = 1;
+        launch_attn_decode(g, as_stream(stream));
+        check_launch("hero_attn_prefill");
+    });
+}
+
 int64_t hero_attn_paged_work_bytes(int64_t max_ctx, int32_t window, int32_t b, int32_t hq, int32_t hkv) {
     if (max_ctx <= 0 || b <= 0 || hkv <= 0 || hq <= 0 || window < 0) return -1;
     int split = 0, nsplit = 0;

@@ -275,6 +275,28 @@ __global__ __launch_bounds__(256) void attn_scores_tile_kernel(AttnDecodeArgs a)
 // max over the visible scores (order free), e_j = exp(s_j - max), the total as
 // the sequential sum over j computed exactly in parallel, alpha_j = e_j / total
 // written back over the scores.
+// e_j = exp(s_j - max) written over the scores and the total of n terms,
+// chunk by chunk, each chunk starting with the running total as its first
+// term (fl(0 + e) == e, so the first chunk matches the loop from s = 0); then
+// alpha_j = e_j / total. NT lanes; chunk: kMaxN floats of shared memory.
+template <int NT>
+__device__ inline void softmax_chunked(float* sc, int n, float mx, seqsum::Shared& sm, float* chunk) {
+    const int tid = int(threadIdx.x);
+    float total = 0.f;
+    for (int base = 0; base < n; base += seqsum::kMaxN - 1) {
+        const int len = min(n - base, seqsum::kMaxN - 1);
+        for (int t = tid; t < len; t += NT) {
+            const float e = exp_f32(sc[base + t] - mx);
+            sc[base + t] = e;
+            chunk[t + 1] = e;
+        }
+        if (tid == 0) chunk[0] = total;
+        __syncthreads();
+        total = seqsum::sum_nonneg<NT>(chunk, len + 1, sm);  // every wave gets the total
+    }
+    for (int t = tid; t < n; t += NT) sc[t] = sc[t] / total;
+}
+
 __global__ __launch_bounds__(seqsum::kThreads) void attn_softmax_kernel(AttnDecodeArgs a) {
     const int tid = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
     const int pos = a.positions[b];
@@ -293,22 +315,7 @@ __global__ __launch_bounds__(seqsum::kThreads) void attn_softmax_kernel(AttnDeco
     __syncthreads();
     mx = red[0];
     for (int w = 1; w < seqsum::kWaves; ++w) mx = fmaxf(mx, red[w]);
-
-    // chunk by chunk, each chunk starting with the running total as its first
-    // term (fl(0 + e) == e, so the first chunk matches the loop from s = 0)
-    float total = 0.f;
-    for (int base = 0; base < n; base += seqsum::kMaxN - 1) {
-        const int len = min(n - base, seqsum::kMaxN - 1);
-        for (int t = tid; t < len; t += seqsum::kThreads) {
-            const float e = exp_f32(sc[base + t] - mx);
-            sc[base + t] = e;
-            chunk[t + 1] = e;
-        }
-        if (tid == 0) chunk[0] = total;
-        __syncthreads();
-        total = seqsum::sum_nonneg(chunk, len + 1, sm);  // every wave gets the total
-    }
-    for (int t = tid; t < n; t += seqsum::kThreads) sc[t] = sc[t] / total;
+    softmax_chunked<seqsum::kThreads>(sc, n, mx, sm, chunk);
 }
 
 // ---- 4. weighted sum of values, gate, quantize -----------------------------------------------
@@ -833,6 +840,258 @@ __global__ __launch_bounds__(kPvbThreads) void attn_pv_batch_kernel(AttnDecodeAr
     }
 }
 
+// ---- prefill over the shared cache: softmax and weighted sum by row blocks ------------------
+// The softmax of one (row, query head) for n <= 4096 visible keys with the
+// scores held in registers: lane t holds elements PT t .. PT t + PT - 1, the
+// max is order-free, e_j = exp(s_j - max) stays in registers, the total is the
+// sequential sum over j computed exactly (hero/seqsum.hpp; the e_j also go to
+// shared memory for its fallback) and alpha_j = e_j / total is written back:
+// one read and one write of the scores where attn_softmax_kernel makes three
+// reads and two writes. 256-lane workgroups (16 terms a lane) let eight run
+// per CU when there are thousands of rows, as in a prefill chunk. The host
+// runs it for max_ctx % 4 == 0 (16-byte aligned rows); rows of more than 4096
+// keys take the chunked form.
+template <int NT>
+__global__ __launch_bounds__(NT) void attn_softmax_regs_kernel(AttnDecodeArgs a) {
+    constexpr int PT = seqsum::kMaxN / NT;
+    constexpr int W = NT / 64;
+    const int tid = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
+    const int pos = a.positions[b];
+    if (pos < 0 || pos >= a.max_ctx) return;
+    const int first = visible_first(pos, a.window);
+    const int n = pos + 1 - first;
+    float* sc = a.scores + (int64_t(b) * a.Hq + h) * a.max_ctx;
+    __shared__ seqsum::Shared sm;
+    __shared__ __align__(16) float terms[seqsum::kMaxN];
+    __shared__ float red[W];
+    if (n > seqsum::kMaxN) {  // longer rows: the chunked form
+        float mx = -INFINITY;
+        for (int t = tid; t < n; t += NT) mx = fmaxf(mx, sc[t]);
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        if ((tid & 63) == 0) red[tid >> 6] = mx;
+        __syncthreads();
+        mx = red[0];
+#pragma unroll
+        for (int w = 1; w < W; ++w) mx = fmaxf(mx, red[w]);
+        softmax_chunked<NT>(sc, n, mx, sm, terms);
+        return;
+    }
+
+    const int i0 = tid * PT;
+    float v[PT];
+#pragma unroll
+    for (int k = 0; k < PT; k += 4) {
+        float4 q = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        if (i0 + k + 4 <= n) {
+            q = *reinterpret_cast<const float4*>(sc + i0 + k);
+        } else if (i0 + k < n) {
+            q.x = sc[i0 + k];
+            if (i0 + k + 1 < n) q.y = sc[i0 + k + 1];
+            if (i0 + k + 2 < n) q.z = sc[i0 + k + 2];
+        }
+        v[k] = q.x, v[k + 1] = q.y, v[k + 2] = q.z, v[k + 3] = q.w;
+    }
+    float mx = v[0];
+#pragma unroll
+    for (int k = 1; k < PT; ++k) mx = fmaxf(mx, v[k]);
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) mx = fmaxf(mx, red[w]);
+    if (i0 < n) {  // whole waves past the row skip the exponentials
+#pragma unroll
+        for (int k = 0; k < PT; ++k) v[k] = i0 + k < n ? exp_f32(v[k] - mx) : 0.f;
+    } else {
+#pragma unroll
+        for (int k = 0; k < PT; ++k) v[k] = 0.f;
+    }
+    const float total = seqsum::sum_nonneg_regs<NT>(v, terms, n, sm);
+#pragma unroll
+    for (int k = 0; k < PT; k += 4) {
+        if (i0 + k + 4 <= n) {
+            *reinterpret_cast<float4*>(sc + i0 + k) = make_float4(v[k] / total, v[k + 1] / total, v[k + 2] / total, v[k + 3] / total);
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (i0 + k + u < n) sc[i0 + k + u] = v[k + u] / total;
+        }
+    }
+}
+
+// out[c] = sum_j alpha_j * v_j[c] (rows in order, core.hpp:206-208) for a
+// block of R consecutive rows of one sequence (a prefill chunk, full causal
+// visibility), all query heads of one K/V group chunk (up to 4) and all 128
+// channels: each V row and each weight is read from memory once per block
+// instead of once per row and head. Wave w owns channels 32 w .. 32 w + 31;
+// lane l owns row r = l % R and channels 32 w + CPL (l / R) .. + CPL - 1 of
+// every head of the chunk (4 x CPL chains in registers). 32-key tiles of V
+// ([key][128 channels]) and of the weights ([key quad][head, row][4 keys])
+// land in shared memory through global_load_lds, two buffers deep; per key a
+// lane reads its CPL channels (all lanes with the same channel group share
+// the address) and, per 4 keys, one 16-byte weight read per head (lanes
+// of consecutive rows read consecutive addresses), then does 8 CPL fp32
+// operations. A row only adds keys at or before its position (the tiles past
+// the block's first position test it per lane). Then the gate and the Q8_0
+// block of 32 channels (spread over 32 / CPL lanes) as attn_pv_kernel.
+// The host runs it for window 0 and max_ctx % 4 == 0 (16-byte aligned
+// weight quads and V rows).
+constexpr int kPrRows = 8;                         // rows per workgroup (16 measured 2% slower over a 2048-token prefill)
+constexpr int kPrKeys = 32;                        // keys per tile
+constexpr int kPrThreads = 256;                    // four waves: 32 channels each
+constexpr int kPrHeads = 4;                        // query heads per workgroup
+constexpr int kPrVQuads = kPrKeys * kAttnDim / 4;  // 16-byte pieces of a V tile: 1024
+
+template <int R>
+__global__ __launch_bounds__(kPrThreads) void attn_pv_rows_kernel(AttnDecodeArgs a) {
+    constexpr int CG = 64 / R;          // channel groups per wave
+    constexpr int CPL = 32 / CG;        // channels per lane
+    constexpr int NP = kPrHeads * R;    // (head, row) pairs
+    constexpr int AQuads = kPrKeys / 4 * NP;  // 16-byte pieces of a weight tile
+    static_assert(CPL % 4 == 0 && AQuads % kPrThreads == 0 && kPrVQuads % kPrThreads == 0, "tile geometry");
+    __shared__ __align__(16) float vt[2][kPrKeys * kAttnDim];  // [key][channel]
+    __shared__ __align__(16) float at[2][AQuads * 4];          // [key quad][head * R + row][4 keys]
+
+    const int tid = int(threadIdx.x), wave = tid / 64, lane = tid % 64;
+    const int r = lane % R, cg = lane / R;
+    const int group = a.Hq / a.Hkv, nchunk = (group + kPrHeads - 1) / kPrHeads;
+    const int g = int(blockIdx.x) / nchunk, h0 = g * group + (int(blockIdx.x) % nchunk) * kPrHeads;
+    const int nh = min(kPrHeads, g * group + group - h0);
+    const int row0 = int(blockIdx.y) * R;
+    const int nrows = min(R, a.B - row0);
+    // the block's positions: the first row's (every row sees keys up to it)
+    // and the largest (the last tile)
+    const int my_row = row0 + min(r, nrows - 1);
+    const int my_pos = r < nrows ? a.positions[my_row] : -1;
+    int pos_lo = INT32_MAX, pos_hi = -1;
+    for (int i = 0; i < nrows; ++i) {
+        const int p = a.positions[row0 + i];
+        pos_lo = min(pos_lo, p);
+        pos_hi = max(pos_hi, p);
+    }
+    if (pos_hi < 0 || pos_hi >= a.max_ctx || pos_lo < 0) return;  // the host keeps positions in range
+    const int ntiles = (pos_hi + kPrKeys) / kPrKeys;
+    const int full_tiles = (pos_lo + 1) / kPrKeys;  // tiles every row of the block sees whole
+    const int64_t kw = int64_t(a.Hkv) * kAttnDim;
+    const float* vb = a.v_cache + int64_t(g) * kAttnDim;  // shared cache: sequence 0
+
+    // staging: V piece q = key q / 32, channels 4 (q % 32) ..; weight piece
+    // q = key quad q / NP, pair q % NP = head * R + row; rows past the block and
+    // heads past nh read the last valid ones, keys past the cache its last
+    // rows (never used)
+    auto issue = [&](int tile) {
+        const int j0 = tile * kPrKeys;
+        float* vdst = vt[tile & 1];
+        float* adst = at[tile & 1];
+#pragma unroll
+        for (int k = 0; k < kPrVQuads / kPrThreads; ++k) {
+            const int q = k * kPrThreads + tid;
+            const int key = min(j0 + q / 32, int(a.max_ctx) - 1);
+            lds_dma_b128(vb + int64_t(key) * kw + 4 * (q % 32), lds_offset(vdst + 4 * (k * kPrThreads + wave * 64)));
+        }
+#pragma unroll
+        for (int k = 0; k < AQuads / kPrThreads; ++k) {
+            const int q = k * kPrThreads + tid;
+            const int pair = q % NP, kq = q / NP;
+            const int hh = min(pair / R, nh - 1), rr = min(pair % R, nrows - 1);
+            const int key = min(j0 + 4 * kq, int(a.max_ctx) - 4);
+            const float* src = a.scores + (int64_t(row0 + rr) * a.Hq + h0 + hh) * a.max_ctx + key;
+            lds_dma_b128(src, lds_offset(adst + 4 * (k * kPrThreads + wave * 64)));
+        }
+    };
+
+    float acc[kPrHeads][CPL];
+#pragma unroll
+    for (int hh = 0; hh < kPrHeads; ++hh)
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) acc[hh][i] = 0.f;
+
+    // one tile: keys j0 .. j0 + 31, four at a time; MASK: test each key
+    // against the lane's position
+    auto tile_sum = [&](const float* vbuf, const float* abuf, int j0, auto mask) {
+        constexpr bool M = decltype(mask)::value;
+#pragma unroll
+        for (int kq = 0; kq < kPrKeys / 4; ++kq) {
+            float4 al[kPrHeads];
+#pragma unroll
+            for (int hh = 0; hh < kPrHeads; ++hh) al[hh] = *reinterpret_cast<const float4*>(abuf + 4 * (kq * NP + hh * R + r));
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const float* vrow = vbuf + (4 * kq + kk) * kAttnDim + 32 * wave + CPL * cg;
+                float vv[CPL];
+#pragma unroll
+                for (int i = 0; i < CPL; i += 4) {
+                    const float4 q = *reinterpret_cast<const float4*>(vrow + i);
+                    vv[i] = q.x, vv[i + 1] = q.y, vv[i + 2] = q.z, vv[i + 3] = q.w;
+                }
+                const bool use = !M || j0 + 4 * kq + kk <= my_pos;
+#pragma unroll
+                for (int hh = 0; hh < kPrHeads; ++hh) {
+                    const float w = kk == 0 ? al[hh].x : kk == 1 ? al[hh].y : kk == 2 ? al[hh].z : al[hh].w;
+#pragma unroll
+                    for (int i = 0; i < CPL; ++i) {
+                        const float sum = acc[hh][i] + w * vv[i];
+                        acc[hh][i] = M ? (use ? sum : acc[hh][i]) : sum;
+                    }
+                }
+            }
+        }
+    };
+
+    issue(0);
+    for (int tile = 0; tile < ntiles; ++tile) {
+        wait_vmcnt<0>();
+        __syncthreads();  // the tile has landed everywhere; the other buffer's readers are done
+        if (tile + 1 < ntiles) issue(tile + 1);
+        const float* vbuf = vt[tile & 1];
+        const float* abuf = at[tile & 1];
+        if (tile < full_tiles)
+            tile_sum(vbuf, abuf, tile * kPrKeys, std::false_type{});
+        else
+            tile_sum(vbuf, abuf, tile * kPrKeys, std::true_type{});
+    }
+
+    // gate, Q8_0 block of each (row, head): 32 channels over the CG lanes of the row
+    const int64_t width = int64_t(a.Hq) * kAttnDim;
+    int8_t* qs = static_cast<int8_t*>(a.act_out);
+    float* qd = reinterpret_cast<float*>(qs + int64_t(a.B) * width);
+    const int ch0 = 32 * wave + CPL * cg;
+#pragma unroll
+    for (int hh = 0; hh < kPrHeads; ++hh) {
+        const int h = h0 + min(hh, nh - 1);
+        const float* gate = a.proj + int64_t(my_row) * a.proj_stride + int64_t(h) * 2 * kAttnDim + kAttnDim + ch0;
+        float out[CPL];
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            out[i] = acc[hh][i] * sigmoid_f32(gate[i]);
+            amax = fmaxf(amax, fabsf(out[i]));
+        }
+#pragma unroll
+        for (int off = R; off < 64; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+        const float d = amax / 127.f;
+        const float id = d != 0.f ? 1.f / d : 0.f;
+        if (r < nrows && hh < nh) {
+            const int64_t idx = int64_t(my_row) * width + int64_t(h) * kAttnDim + ch0;
+            if (a.out_f32)
+#pragma unroll
+                for (int i = 0; i < CPL; i += 4) *reinterpret_cast<float4*>(a.out_f32 + idx + i) = make_float4(out[i], out[i + 1], out[i + 2], out[i + 3]);
+            uint32_t pk[CPL / 4];
+#pragma unroll
+            for (int i = 0; i < CPL; i += 4) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) w |= uint32_t(uint8_t(int8_t(int(roundf(out[i + u] * id))))) << (8 * u);
+                pk[i / 4] = w;
+            }
+#pragma unroll
+            for (int i = 0; i < CPL / 4; ++i) reinterpret_cast<uint32_t*>(qs + idx)[i] = pk[i];
+            if (cg == 0) qd[idx >> 5] = half_bits_to_f32(fp32_to_fp16_ref(d));
+        }
+    }
+}
+
 // ---- paged fp16 cache, split-K ------------------------------------------------------------
 // The keys and values are stored as fp16 (round to nearest even) in pages of
 // page_size positions; a page table maps each sequence's pages into the pool.
@@ -1185,6 +1444,13 @@ void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
     } else {
         hipLaunchKernelGGL(attn_prep_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, a);
         hipLaunchKernelGGL(attn_scores_kernel, dim3(chunks, tiles, unsigned(a.B)), dim3(256), 0, s, a);
+    }
+    // a prefill chunk (rows of one sequence, full causal visibility): the
+    // register softmax and the row-block weighted sum
+    if (a.shared_cache && a.window == 0 && a.max_ctx % 4 == 0) {
+        hipLaunchKernelGGL(attn_softmax_regs_kernel<256>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(attn_pv_rows_kernel<kPrRows>, dim3(unsigned(chunks), unsigned((a.B + kPrRows - 1) / kPrRows)), dim3(kPrThreads), 0, s, a);
+        return;
     }
     // the per-head pipeline while its workgroups fit the CUs (a deep ring, one
     // workgroup per CU) or fit them twice over (a shallower ring); for up to

@@ -270,6 +270,15 @@ typedef struct hero_attn_decode_args {
 } hero_attn_decode_args;
 int hero_attn_decode(const hero_attn_decode_args* args, void* stream);
 
+/* The same attention for B consecutive tokens of ONE sequence (a prefill
+ * chunk): row b is the token at positions[b], all rows share cache 0 (k_cache
+ * [1][Hkv][Dh][max_ctx], v_cache [1][max_ctx][Hkv*Dh]), every row's k and v
+ * are appended before any row's scores, and row b attends to the rows at or
+ * before positions[b] (within the window). Replaces the T-row reduction of
+ * nm/src/qwen35.hpp:363-387: the whole batch is appended to the cache, then
+ * each (row, head) is reduced over its visible rows. */
+int hero_attn_prefill(const hero_attn_decode_args* args, void* stream);
+
 /* The same attention over a paged fp16 K/V cache (north-star format; the
  * reference keeps fp32 rows, nm/src/attention.hpp:248-249). Keys and values
  * are stored rounded to nearest-even fp16; the visible keys of each (sequence,

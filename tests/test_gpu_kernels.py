@@ -192,6 +192,28 @@ def test_gemm_matches_oracle_bitwise(lib, m, n, k):
     assert np.array_equal(bits(host(y, np.float32, (m, n))), bits(r + expect))
 
 
+# scales in fp16's subnormal range (and rows whose scale rounds to 0): the
+# GEMM forms d_x * d_w on the fp16 MFMA, which must take subnormal inputs as
+# they are; (512, 8192) selects the 128-row tile, (70, 4100) a smaller one
+@pytest.mark.parametrize("m,n,k", [(512, 8192, 1024), (70, 4100, 2048), (9, 4100, 1024)])
+def test_gemm_subnormal_scales_match_oracle_bitwise(lib, m, n, k):
+    rng = np.random.default_rng(m + n + k + 5)
+    wscale = np.where(rng.random((n, 1)) < 0.3, 1e-3, 1.0) * np.where(rng.random((n, 1)) < 0.05, 1e-6, 1.0)
+    w = oracle.quantize_q8_0((rng.standard_normal((n, k)) * 0.02 * wscale).astype(np.float32))
+    d = w["d"].view(np.float16).astype(np.float32)
+    assert np.any((d > 0) & (d < 6.1e-5)), "some weight scales are subnormal fp16"
+    packed = pack_weight(lib, w, n, k)
+    xscale = rng.choice([1.0, 3e-5, 1e-7, 1e3], size=(m, 1))
+    x = (rng.standard_normal((m, k)) * xscale).astype(np.float32)
+    act = quantize_dev(lib, x)
+    y = empty(m * n * 4)
+    check(lib.hero_q8_0_gemm(ptr(packed), ptr(act), ptr(y), None, m, n, k, stream()))
+    expect = oracle.matmul(w, n, k, x)
+    got = host(y, np.float32, (m, n))
+    bad = np.flatnonzero(bits(got).ravel() != bits(expect).ravel())
+    assert bad.size == 0, f"{bad.size} outputs differ, first {bad[:5]}: {got.ravel()[bad[:3]]} vs {expect.ravel()[bad[:3]]}"
+
+
 def test_block_sums_are_exact(lib):
     n, k = 257 * 2, 4096
     rng = np.random.default_rng(3)
@@ -614,6 +636,67 @@ def test_attn_decode_long_context_matches_oracle(lib, B, hq, hkv, pos, window):
     blocks = act_to_blocks(host(act, np.uint8), B, qw)
     for b in range(B):
         assert blocks[b].tobytes() == oracle.quantize_row_q8_0(got[b]).tobytes()
+
+
+# a prefill chunk: M consecutive tokens of one sequence after p0 cached rows,
+# all sharing cache 0 (the reference appends the whole batch, then reduces
+# each row over its visible rows). max_ctx % 4 == 0 with no window takes the
+# register softmax and the row-block weighted sum (blocks of 8 rows: 37 and
+# 603 rows leave a partial last block; group 6 makes head chunks of 4 and 2;
+# p0 = 4100 gives rows of more than 4096 keys, the chunked softmax);
+# max_ctx % 4 != 0 and the window take the per-row kernels.
+@pytest.mark.parametrize("M,p0,hq,hkv,max_ctx,window", [(37, 0, 8, 2, 40, 0), (603, 70, 32, 8, 676, 0), (20, 33, 6, 1, 56, 0),
+                                                        (64, 4100, 8, 2, 4168, 0), (10, 5, 4, 1, 17, 0), (24, 9, 8, 2, 36, 7)])
+def test_attn_prefill_rows_match_oracle(lib, M, p0, hq, hkv, max_ctx, window):
+    from hero_amd._lib import AttnDecodeArgs
+
+    rng = np.random.default_rng(M + p0 + hq)
+    dh = 128
+    qw, kw = hq * dh, hkv * dh
+    stride = 2 * qw + 2 * kw
+    qg = (1 + 0.1 * rng.standard_normal(dh)).astype(np.float32)
+    kg = (1 + 0.1 * rng.standard_normal(dh)).astype(np.float32)
+    eps = np.float32(1e-6)
+    scale = np.float32(1.0) / np.sqrt(np.float32(dh)) if window == 0 else np.float32(1.0)
+    inv = oracle.rope_inv_freq(dh, 1e6, 32)
+    d_cs = dev(oracle.rope_table(dh, 1e6, 32, max_ctx))
+    keys = (rng.standard_normal((p0, kw)) * 0.5).astype(np.float32)
+    vals = rng.standard_normal((p0, kw)).astype(np.float32)
+    kc = np.zeros((hkv, dh, max_ctx), np.float32)
+    kc[:, :, :p0] = keys.reshape(p0, hkv, dh).transpose(1, 2, 0)
+    vc = np.zeros((max_ctx, kw), np.float32)
+    vc[:p0] = vals
+    d_kc, d_vc = dev(kc), dev(vc)
+    d_sc = empty(M * hq * max_ctx * 4)
+    d_qr = empty(M * hq * dh * 4)
+    act = empty(lib.hero_q8_0_act_bytes(M, qw))
+    out = empty(M * qw * 4)
+    proj = rng.standard_normal((M, stride)).astype(np.float32)
+    d_proj, d_pos = dev(proj), dev(np.arange(p0, p0 + M, dtype=np.int32))
+    d_qg, d_kg = dev(qg), dev(kg)
+    a = AttnDecodeArgs(ptr(d_proj), stride, 2 * qw, 2 * qw + kw, ptr(d_qg), ptr(d_kg), eps, ptr(d_cs), ptr(d_kc), ptr(d_vc),
+                       max_ctx, ptr(d_pos), ptr(d_sc), ptr(d_qr), scale, window, ptr(act), ptr(out), M, hq, hkv, dh)
+    check(lib.hero_attn_prefill(a, stream()))
+    got = host(out, np.float32, (M, qw))
+    # every row's key and value appended first, then each row reduced
+    kk, vv = [keys], [vals]
+    qs, gs = [], []
+    for b in range(M):
+        p = proj[b]
+        q = np.stack([p[h * 2 * dh: h * 2 * dh + dh] for h in range(hq)])
+        gs.append(np.concatenate([p[h * 2 * dh + dh: h * 2 * dh + 2 * dh] for h in range(hq)]))
+        qs.append(oracle.rope_apply(oracle.rmsnorm(q, qg, eps), inv, p0 + b))
+        kk.append(oracle.rope_apply(oracle.rmsnorm(p[2 * qw: 2 * qw + kw].reshape(hkv, dh), kg, eps), inv, p0 + b).reshape(1, kw))
+        vv.append(p[2 * qw + kw:].reshape(1, kw))
+    kk, vv = np.concatenate(kk), np.concatenate(vv)
+    assert np.array_equal(bits(host(d_kc, np.float32, (hkv, dh, max_ctx))[:, :, :p0 + M]), bits(kk.reshape(-1, hkv, dh).transpose(1, 2, 0)))
+    for b in range(M):
+        att = oracle.attend_decode(qs[b].reshape(-1), kk[:p0 + b + 1], vv[:p0 + b + 1], hq, hkv, dh, window, scale).reshape(-1)
+        expect = (att * oracle.sigmoid(gs[b])).astype(np.float32)
+        assert np.array_equal(bits(got[b]), bits(expect)), f"row {b}: max ulp {ulp_diff(got[b], expect).max()}"
+    blocks = act_to_blocks(host(act, np.uint8), M, qw)
+    for b in range(M):
+        assert blocks[b].tobytes() == oracle.quantize_row_q8_0(got[b]).tobytes(), f"row {b}"
 
 
 @pytest.mark.parametrize("hq,window", [(8, 0), (8, 50), (16, 0)])

@@ -604,7 +604,12 @@ __global__ __launch_bounds__(256) void gemm_q8_kernel(const int8_t* __restrict__
     const int n0 = blockIdx.x * kGemmBN, m0 = blockIdx.y * BM;
     const int nb = K >> 5;
     const int mrows = min(BM, M - m0), nrows = min(kGemmBN, N - n0);
-    constexpr int MT = BM / 16;                    // m sub-tiles per wave
+    // waves as a WR x WC grid over the tile: wave (wr, wc) owns MTW 16-row
+    // and NTW 16-column sub-tiles (fewer operand and scale reads per MFMA
+    // than one column strip per wave when the tile is tall)
+    constexpr int WR = BM >= 64 ? 4 : BM / 16, WC = 4 / WR;
+    constexpr int MTW = BM / 16 / WR, NTW = 4 / WC;
+    const int wrow = w / WC, wc = w % WC;
     constexpr int XP = BM * 16 / 256;              // 16-byte X pieces per lane per chunk
     constexpr int WP = kGemmBN * 16 / 256;         // 16-byte W pieces per lane per chunk: 4
     constexpr int DXP = (BM * kGemmKC + 255) / 256;
@@ -615,11 +620,13 @@ __global__ __launch_bounds__(256) void gemm_q8_kernel(const int8_t* __restrict__
     const __amdgpu_buffer_rsrc_t bw = buffer_of(wq + int64_t(n0) * K, uint32_t(nrows) * uint32_t(K));
     const __amdgpu_buffer_rsrc_t bdx = buffer_of(xd + int64_t(m0) * nb, uint32_t(mrows) * uint32_t(nb) * 4u);
     const __amdgpu_buffer_rsrc_t bdw = buffer_of(wd + scale_index(n0, 0, nb), uint32_t((min(kGemmBN, Npad - n0) + 7) / 8) * uint32_t(nb) * 16u);
-    float acc[MT][4];
+    float acc[MTW][NTW][4];
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+    for (int i = 0; i < MTW; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[i][r] = 0.f;
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.f;
 
     int4 xr[XP], wr[WP];
     float dxr[DXP], dwr[DWP];
@@ -677,37 +684,49 @@ __global__ __launch_bounds__(256) void gemm_q8_kernel(const int8_t* __restrict__
         stage();
         __syncthreads();
         if (b0 + kGemmKC < nb) fetch(b0 + kGemmKC);  // in flight during this chunk's compute
-        const int n_l = 16 * w + (lane & 15);
         for (int bb = 0; bb < kc; ++bb) {
             const int koff = bb * 32 + (lane >> 4) * 8;
-            const long bop = *reinterpret_cast<const long*>(Ws + n_l * kGemmRow + koff);
-            const float dw = dws[bb][n_l];
+            long bop[NTW];
+            float dw[NTW];
 #pragma unroll
-            for (int i = 0; i < MT; ++i) {
-                const long aop = *reinterpret_cast<const long*>(Xs + (16 * i + (lane & 15)) * kGemmRow + koff);
-                const v4i_t zero = {0, 0, 0, 0};
-                const v4i_t c = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, zero, 0, 0, 0);
-                const float4 dx4 = *reinterpret_cast<const float4*>(&dxs[bb][16 * i + (lane >> 4) * 4]);
-                acc[i][0] = acc[i][0] + float(c[0]) * (dw * dx4.x);
-                acc[i][1] = acc[i][1] + float(c[1]) * (dw * dx4.y);
-                acc[i][2] = acc[i][2] + float(c[2]) * (dw * dx4.z);
-                acc[i][3] = acc[i][3] + float(c[3]) * (dw * dx4.w);
+            for (int j = 0; j < NTW; ++j) {
+                const int n_l = 16 * (wc * NTW + j) + (lane & 15);
+                bop[j] = *reinterpret_cast<const long*>(Ws + n_l * kGemmRow + koff);
+                dw[j] = dws[bb][n_l];
+            }
+#pragma unroll
+            for (int i = 0; i < MTW; ++i) {
+                const int mi = wrow * MTW + i;
+                const long aop = *reinterpret_cast<const long*>(Xs + (16 * mi + (lane & 15)) * kGemmRow + koff);
+                const float4 dx4 = *reinterpret_cast<const float4*>(&dxs[bb][16 * mi + (lane >> 4) * 4]);
+#pragma unroll
+                for (int j = 0; j < NTW; ++j) {
+                    const v4i_t zero = {0, 0, 0, 0};
+                    const v4i_t c = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop[j], zero, 0, 0, 0);
+                    acc[i][j][0] = acc[i][j][0] + float(c[0]) * (dw[j] * dx4.x);
+                    acc[i][j][1] = acc[i][j][1] + float(c[1]) * (dw[j] * dx4.y);
+                    acc[i][j][2] = acc[i][j][2] + float(c[2]) * (dw[j] * dx4.z);
+                    acc[i][j][3] = acc[i][j][3] + float(c[3]) * (dw[j] * dx4.w);
+                }
             }
         }
         __syncthreads();
     }
-    const int n = n0 + 16 * w + (lane & 15);
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+    for (int i = 0; i < MTW; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = m0 + 16 * i + (lane >> 4) * 4 + r;
-            if (m < M && n < N) {
-                const int64_t o = int64_t(m) * N + n;
-                if constexpr (EPI == kEpiResidual)
-                    y[o] = resid[o] + acc[i][r];
-                else
-                    y[o] = acc[i][r];
+        for (int j = 0; j < NTW; ++j) {
+            const int n = n0 + 16 * (wc * NTW + j) + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + 16 * (wrow * MTW + i) + (lane >> 4) * 4 + r;
+                if (m < M && n < N) {
+                    const int64_t o = int64_t(m) * N + n;
+                    if constexpr (EPI == kEpiResidual)
+                        y[o] = resid[o] + acc[i][j][r];
+                    else
+                        y[o] = acc[i][j][r];
+                }
             }
         }
 }

@@ -583,8 +583,11 @@ namespace hero {
 // 8*(l/16)..+7; B lane l = column l%16, the same k bytes; C lane l, register r
 // = row 4*(l/16)+r, column l%16.
 //
-// Workgroup: 256 lanes, a BM x 64 tile of Y; wave w owns columns 16w..16w+15
-// and all BM rows. K streams through shared memory 8 blocks (256 bytes) at a
+// Workgroup: 256 lanes, a BM x 64 tile of Y; the four waves form a grid over
+// it (4 x 1 for BM >= 64: 32 or 16 rows x 64 columns each; 2 x 2 at BM = 32;
+// 1 x 4 at BM = 16), so at the tall tiles a wave's operand and scale reads
+// serve two or four MFMAs each (unrolling a whole chunk of 8 blocks measured
+// slower: more registers, a worse schedule). K streams through shared memory 8 blocks (256 bytes) at a
 // time; tile rows are padded to 272 bytes (2-way bank conflicts on the 8-byte
 // operand reads). The next chunk's bytes and scales are loaded into registers
 // while the current chunk is computed (raw buffer loads sized to the tile, so

@@ -101,6 +101,8 @@ SIGNATURES = {
     "hero_argmax_noalloc": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
     "hero_math_eval": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
     "hero_sample_topk": (c_int, [c_void_p, c_int64, c_int32, c_float, c_float, c_float, c_void_p, c_void_p]),
+    "hero_sample_work_bytes": (c_int64, [c_int64]),
+    "hero_sample": (c_int, [c_void_p, c_int64, c_int32, c_float, c_float, c_float, c_void_p, c_int64, c_void_p, c_void_p]),
     "hero_q8_K_act_bytes": (c_int64, [c_int64, c_int64]),
     "hero_q8_K_quantize": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "hero_kquant_gemm": (c_int, [c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p]),

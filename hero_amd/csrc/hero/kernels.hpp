@@ -45,6 +45,9 @@ void launch_kquant_dequant_rows(int type, const void* w, int64_t N, int64_t K, c
 // top-k / top-p sampling of one logits row (sample.hip); top_k in 1 .. sample_max_top_k()
 int sample_max_top_k();
 void launch_sample_topk(const float* logits, int64_t V, int top_k, float temp, float top_p, float u, int32_t* out, hipStream_t s);
+// any top_k (0 = the whole vocabulary) over a sorted copy; work: sample_full_work_bytes(V)
+int64_t sample_full_work_bytes(int64_t V);
+void launch_sample_full(const float* logits, int64_t V, int top_k, float temp, float top_p, float u, void* work, int32_t* out, hipStream_t s);
 
 // q8.hip
 void launch_quantize_act(const float* x, void* act, int64_t M, int64_t K, hipStream_t s);

@@ -68,6 +68,33 @@ int hero_sample_topk(const float* logits, int64_t v, int32_t top_k, float temp, 
     });
 }
 
+int64_t hero_sample_work_bytes(int64_t v) {
+    if (v <= 0 || v > (int64_t(1) << 30)) return -1;
+    try {
+        return sample_full_work_bytes(v);
+    } catch (...) {
+        return -1;
+    }
+}
+
+int hero_sample(const float* logits, int64_t v, int32_t top_k, float temp, float top_p, float u, void* work, int64_t work_bytes, int32_t* out, void* stream) {
+    return guard([&] {
+        require(logits && out, "null pointer");
+        require(v > 0 && v <= (int64_t(1) << 30), "vocabulary size out of range");
+        require(top_k >= 0, "top_k must be >= 0 (0: the whole vocabulary)");
+        require(temp > 0.f, "temp must be positive (temp <= 0 is greedy: hero_argmax)");
+        require(u >= 0.f && u < 1.f, "u must be in [0, 1)");
+        if (top_k >= 1 && top_k <= sample_max_top_k()) {
+            launch_sample_topk(logits, v, top_k, temp, top_p, u, out, as_stream(stream));
+        } else {
+            require(work != nullptr && aligned(work, 256), "work: 256-byte aligned device memory");
+            require(work_bytes >= sample_full_work_bytes(v), "work_bytes below hero_sample_work_bytes(v)");
+            launch_sample_full(logits, v, top_k, temp, top_p, u, work, out, as_stream(stream));
+        }
+        check_launch("hero_sample");
+    });
+}
+
 int64_t hero_q8_K_act_bytes(int64_t m, int64_t k) { return act_q8_K_bytes(m, k); }
 
 int hero_q8_K_quantize(const float* x, void* act, int64_t m, int64_t k, void* stream) {

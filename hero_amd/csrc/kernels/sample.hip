@@ -15,9 +15,12 @@
 //   4. one lane runs the reference's sequential loops: the sum of p, the first
 //      prefix whose running sum of p / sum reaches top_p, that prefix's sum
 //      s2, r = u * s2, and the first candidate whose running sum reaches r.
+#include <rocprim/device/device_radix_sort.hpp>
+
 #include "hero/device.hpp"
 #include "hero/kernels.hpp"
 #include "hero/libm.hpp"
+#include "hero/seqsum.hpp"
 
 namespace hero {
 
@@ -280,9 +283,113 @@ __global__ __launch_bounds__(kSampleThreads) void sample_topk_kernel(const float
     if (tid == 0) out[0] = sequential_pick(pr, sidx, k, top_p, u);
 }
 
+// ---- any k, the whole vocabulary included (top_k = 0) -------------------------------------
+// The logits are sorted once, by a stable descending radix sort of (logit, id)
+// pairs (rocPRIM; ids ascending within equal logits, -0 taken as +0 as the
+// reference's comparison does), then one workgroup runs the reference's
+// loops over the first k: the sum of p_i = exp((l_i - max) / temp), the first
+// prefix whose running sum of p_i / sum reaches top_p, that prefix's sum s2,
+// r = u * s2, and the first i whose running sum of p_i reaches r. Each loop is
+// a sequential fp32 sum of non-negative terms, run in chunks of 4095 terms
+// that start from the running total (the exact parallel sum of
+// hero/seqsum.hpp equals the loop); where a loop stops early, the chunk whose
+// end total meets the condition (running sums of non-negative terms never
+// decrease) is walked term by term by one lane from its starting total.
+__global__ void sample_full_prep_kernel(const float* __restrict__ logits, int V, float* __restrict__ keys, int32_t* __restrict__ ids) {
+    const int i = int(blockIdx.x) * 256 + int(threadIdx.x);
+    if (i < V) {
+        keys[i] = logits[i] + 0.f;  // -0 -> +0; every other value unchanged
+        ids[i] = i;
+    }
+}
+
+struct FullPick {
+    seqsum::Shared sm;
+    __align__(16) float chunk[seqsum::kMaxN];
+    int found;
+};
+
+// the running sum over i < n of term(i), chunk by chunk; with `find`, stops
+// at the first i whose running sum s_i satisfies pred(s_i) and returns it in
+// `at` (-1: none); returns the running sum there (or the total)
+template <class Term, class Pred>
+__device__ float running_sum(int n, Term term, bool find, Pred pred, int& at, FullPick& sh) {
+    const int tid = int(threadIdx.x);
+    float total = 0.f;
+    at = -1;
+    for (int base = 0; base < n; base += seqsum::kMaxN - 1) {
+        const int len = min(n - base, seqsum::kMaxN - 1);
+        for (int t = tid; t < len; t += kSampleThreads) sh.chunk[t + 1] = term(base + t);
+        if (tid == 0) sh.chunk[0] = total;
+        __syncthreads();
+        const float after = seqsum::sum_nonneg<kSampleThreads>(sh.chunk, len + 1, sh.sm);
+        if (find && pred(after)) {
+            if (tid == 0) {
+                float s = sh.chunk[0];
+                int j = 1;
+                for (; j <= len; ++j) {
+                    s = s + sh.chunk[j];
+                    if (pred(s)) break;
+                }
+                sh.found = base + min(j, len) - 1;  // j <= len: the walk repeats the exact sum
+                sh.chunk[0] = s;
+            }
+            __syncthreads();
+            at = sh.found;
+            return sh.chunk[0];
+        }
+        total = after;
+        __syncthreads();  // the chunk is rewritten next
+    }
+    return total;
+}
+
+__global__ __launch_bounds__(kSampleThreads) void sample_full_pick_kernel(const float* __restrict__ keys, const int32_t* __restrict__ ids, int k, float temp, float top_p, float u,
+                                                                           int32_t* __restrict__ out) {
+    __shared__ FullPick sh;
+    const float mx = keys[0];
+    auto p = [&](int i) { return exp_f32((keys[i] - mx) / temp); };
+    auto never = [](float) { return false; };
+    int at = -1;
+    const float sum = running_sum(k, p, false, never, at, sh);
+    running_sum(k, [&](int i) { return p(i) / sum; }, true, [&](float c) { return c >= top_p; }, at, sh);
+    const int keep = at >= 0 ? at + 1 : k;
+    const float s2 = keep == k ? sum : running_sum(keep, p, false, never, at, sh);
+    const float r = u * (s2 - 0.f) + 0.f;
+    running_sum(keep, p, true, [&](float a) { return r <= a; }, at, sh);
+    if (threadIdx.x == 0) out[0] = ids[at >= 0 ? at : keep - 1];
+}
+
+// workspace: sorted and unsorted keys and ids, then rocPRIM's storage
+constexpr size_t kFullAlign = 256;
+size_t full_part(int64_t V) { return (size_t(V) * 4 + kFullAlign - 1) / kFullAlign * kFullAlign; }
+size_t full_sort_bytes(int64_t V) {
+    size_t bytes = 0;
+    const hipError_t e = rocprim::radix_sort_pairs_desc(nullptr, bytes, static_cast<float*>(nullptr), static_cast<float*>(nullptr), static_cast<int32_t*>(nullptr),
+                                                        static_cast<int32_t*>(nullptr), size_t(V));
+    if (e != hipSuccess) throw std::runtime_error("rocprim::radix_sort_pairs_desc size query failed");
+    return bytes;
+}
+
 }  // namespace
 
 int sample_max_top_k() { return kSampleThreads; }
+
+int64_t sample_full_work_bytes(int64_t V) { return int64_t(4 * full_part(V) + full_sort_bytes(V)); }
+
+void launch_sample_full(const float* logits, int64_t V, int top_k, float temp, float top_p, float u, void* work, int32_t* out, hipStream_t s) {
+    const int k = int(top_k <= 0 ? V : std::min<int64_t>(top_k, V));
+    char* w = static_cast<char*>(work);
+    float* keys_in = reinterpret_cast<float*>(w);
+    float* keys = reinterpret_cast<float*>(w + full_part(V));
+    int32_t* ids_in = reinterpret_cast<int32_t*>(w + 2 * full_part(V));
+    int32_t* ids = reinterpret_cast<int32_t*>(w + 3 * full_part(V));
+    size_t bytes = full_sort_bytes(V);
+    hipLaunchKernelGGL(sample_full_prep_kernel, dim3(unsigned((V + 255) / 256)), dim3(256), 0, s, logits, int(V), keys_in, ids_in);
+    if (rocprim::radix_sort_pairs_desc(w + 4 * full_part(V), bytes, keys_in, keys, ids_in, ids, size_t(V), 0, 32, s) != hipSuccess)
+        throw std::runtime_error("rocprim::radix_sort_pairs_desc failed");
+    hipLaunchKernelGGL(sample_full_pick_kernel, dim3(1), dim3(kSampleThreads), 0, s, keys, ids, k, temp, top_p, u, out);
+}
 
 void launch_sample_topk(const float* logits, int64_t V, int top_k, float temp, float top_p, float u, int32_t* out, hipStream_t s) {
     const int k = int(std::min<int64_t>(top_k, V));

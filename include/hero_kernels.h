@@ -172,6 +172,16 @@ int hero_kquant_dequant_rows(int32_t type, const void* w, int64_t n, int64_t k, 
  * the two kernels of the call. temp <= 0 is greedy: use hero_argmax. */
 int hero_sample_topk(const float* logits, int64_t v, int32_t top_k, float temp, float top_p, float u, int32_t* out, void* stream);
 
+/* The same Logits::sample for any top_k: 0 (the whole vocabulary,
+ * nm/src/logits.hpp:76 with k = V) or any k >= 1 (1 .. 1024 take
+ * hero_sample_topk's kernels and need no workspace). The logits are sorted on
+ * the device (logit descending, equal logits by ascending id), then the
+ * reference's sum, top_p prefix, s2 and draw run over the first k as exact
+ * sequential sums. work: hero_sample_work_bytes(v) bytes of device memory
+ * (256-byte aligned); out as for hero_sample_topk. */
+int64_t hero_sample_work_bytes(int64_t v);
+int hero_sample(const float* logits, int64_t v, int32_t top_k, float temp, float top_p, float u, void* work, int64_t work_bytes, int32_t* out, void* stream);
+
 /* The scalar functions of the path evaluated on the device, for parity
  * checks: out[0..n) = expf, [n..2n) = log1pf, then silu
  * (nm/src/components.hpp:105), sigmoid (nm/src/core.hpp:579), softplus

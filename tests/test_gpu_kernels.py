@@ -921,18 +921,41 @@ def sample_dev(lib, logits_dev, v, k, temp, p, u):
     return int(host(out, np.int32)[0])
 
 
+def sample_any_dev(lib, logits_dev, v, k, temp, p, u):
+    wbytes = lib.hero_sample_work_bytes(v)
+    assert wbytes > 0
+    work, out = empty(wbytes), empty(8)
+    check(lib.hero_sample(ptr(logits_dev), v, k, temp, p, float(u), ptr(work), wbytes, ptr(out), stream()))
+    return int(host(out, np.int32)[0])
+
+
 def test_sampler_matches_reference_golden(lib, kernels_golden):
-    """Logits<32000>::sample, the reference's own picks (top_k 0, the whole
-    vocabulary, is not a device form)"""
+    """Logits<32000>::sample, the reference's own picks; top_k 0 (the whole
+    vocabulary) through the sorted form, every configuration through it too"""
     cfgs = [(0.7, 40, 0.9), (1.0, 1, 1.0), (1.3, 1000, 0.95), (0.5, 0, 1.0), (2.0, 200, 0.5), (0.9, 64, 0.0)]
     lg = kernels_golden["in_sample_logits"].reshape(8, 32000)
     res = kernels_golden["out_sample"].reshape(8, len(cfgs), 2)
     for r in range(8):
         d = dev(lg[r])
         for c, (temp, k, p) in enumerate(cfgs):
-            if k == 0:
-                continue
-            assert sample_dev(lib, d, 32000, k, temp, p, res[r, c, 1]) == int(res[r, c, 0]), (r, c)
+            if k > 0:
+                assert sample_dev(lib, d, 32000, k, temp, p, res[r, c, 1]) == int(res[r, c, 0]), (r, c)
+            assert sample_any_dev(lib, d, 32000, k, temp, p, res[r, c, 1]) == int(res[r, c, 0]), (r, c)
+
+
+# the whole vocabulary (top_k 0) and k past the one-workgroup form, over the
+# model's vocabulary: top_p cuts that stop in the first chunk of 4095 sorted
+# logits, in a later one, and never (1.0); heavy ties (ids ascending)
+@pytest.mark.parametrize("k,temp,p", [(0, 1.0, 1.0), (0, 0.7, 0.9), (0, 2.5, 0.999), (0, 0.3, 0.0), (5000, 1.2, 0.95), (151936, 1.0, 1.0)])
+def test_sampler_whole_vocabulary_matches_oracle(lib, k, temp, p):
+    rng = np.random.default_rng(k + int(temp * 10))
+    v = 151936
+    rows = [rng.standard_normal(v).astype(np.float32) * 2,
+            np.round(rng.standard_normal(v) * 3).astype(np.float32)]  # heavy ties
+    for x in rows:
+        d = dev(x)
+        for u in (0.0, 0.25, 0.5, 0.999):
+            assert sample_any_dev(lib, d, v, k, temp, p, u) == oracle.sample_topk(x, k, temp, p, u), (k, temp, p, u)
 
 
 # the model's vocabulary, k up to the device limit, top_p cuts, and a row of

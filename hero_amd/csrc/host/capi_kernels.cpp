@@ -436,7 +436,7 @@ int hero_gdn_prefill(const hero_gdn_decode_args* p, void* work, int64_t work_byt
 
 namespace {
 AttnDecodeArgs attn_args(const hero_attn_decode_args& a) {
-    require(a.dh == 128, "attention head dim must be 128");
+    require(a.dh == 128 || a.dh == 256, "attention head dim must be 128 or 256");
     require(a.b > 0 && a.hkv > 0 && a.hq > 0 && a.hq % a.hkv == 0, "bad head counts");
     require(a.window >= 0, "bad window");
     require(a.proj && a.q_gamma && a.k_gamma && a.rope_cs && a.positions && a.q_rot && a.act_out, "null pointer");
@@ -521,6 +521,7 @@ int hero_attn_decode_paged(const hero_attn_paged_args* p, void* stream) {
         require(p != nullptr, "null args");
         AttnPagedArgs g{};
         g.a = attn_args(p->a);
+        require(g.a.Dh == 128, "the paged cache holds 128-wide heads");
         require(g.a.Hq / g.a.Hkv <= kAttnMaxGroup, "at most 8 query heads per KV head");
         require(p->pages && p->page_table && p->work, "null pointer");
         require(p->page_size > 0 && p->max_pages > 0 && int64_t(p->page_size) * p->max_pages <= (int64_t(1) << 24), "bad page geometry");

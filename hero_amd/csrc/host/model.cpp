@@ -249,7 +249,7 @@ void Qwen35Model::load(const GgufFile& g) {
     expect(c.Hkv > 0 && c.Hq % c.Hkv == 0, "query heads must be a multiple of K/V heads");
     expect(c.Hk > 0 && c.Hv % c.Hk == 0, "value heads must be a multiple of key heads");
     expect(c.Dk == 128 && c.Dv == 128, "this build runs 128x128 delta-net heads");
-    expect(c.Dh == 128, "this build runs 128-wide attention heads");
+    expect(c.Dh == 128 || c.Dh == 256, "this build runs 128- or 256-wide attention heads");
     expect(c.rotary_dims % 2 == 0 && c.rotary_dims <= c.Dh, "rope.dimension_count out of range");
     expect(c.W >= 1 && c.W <= 8, "ssm.conv_kernel must be 1..8");
     expect(c.D % 256 == 0 && c.FF % 32 == 0, "embedding_length must be a multiple of 256 and feed_forward_length of 32");
@@ -429,6 +429,7 @@ Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batc
     : m_(m), max_tokens_(max_tokens), batch_(batch), kv_paged_(kv_format != kKvF32), kv_q8_(kv_format == kKvQ8), seq_tokens_(size_t(batch), 0) {
     const bool kv_paged = kv_paged_;
     const ModelConfig& c = m.c_;
+    expect(!kv_paged || c.Dh == 128, "the paged K/V cache holds 128-wide heads; 256-wide heads use the fp32 cache");
     const int64_t B = batch;
     int64_t n_in_max = 0;
     for (const LayerWeights& L : m.layers_) n_in_max = std::max(n_in_max, L.n_in);

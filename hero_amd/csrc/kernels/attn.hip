@@ -41,8 +41,9 @@ constexpr int kScoreTiles = 128;  // most score tiles of 256 keys per head
 __device__ __forceinline__ int64_t cache_of(const AttnDecodeArgs& a, int b) { return a.shared_cache ? 0 : b; }
 
 // ---- 1. prep ----------------------------------------------------------------------
-// RMSNorm over one head held one value per lane (sequential 128-term sum of
-// squares by lane 0), then RoPE on the NEOX planes (i, i + 64).
+// RMSNorm over one head of DH channels held one value per lane (sequential
+// DH-term sum of squares by lane 0), then RoPE on the NEOX planes (i, i + DH/2).
+template <int DH>
 __device__ __forceinline__ float norm_rope_head(float x, const float* gamma, float eps, const float* cs, float* buf, float* scal, int j) {
     buf[j] = x * x;
     __syncthreads();
@@ -50,20 +51,20 @@ __device__ __forceinline__ float norm_rope_head(float x, const float* gamma, flo
         float ss = 0.f;
         const float4* b4 = reinterpret_cast<const float4*>(buf);
 #pragma unroll
-        for (int i = 0; i < kAttnDim / 4; ++i) {
+        for (int i = 0; i < DH / 4; ++i) {
             const float4 v = b4[i];
             ss += v.x;
             ss += v.y;
             ss += v.z;
             ss += v.w;
         }
-        scal[0] = 1.f / sqrtf(ss / float(kAttnDim) + eps);
+        scal[0] = 1.f / sqrtf(ss / float(DH) + eps);
     }
     __syncthreads();
     const float n = gamma[j] * x * scal[0];
     buf[j] = n;
     __syncthreads();
-    const int half = kAttnDim / 2;
+    const int half = DH / 2;
     const int i = j < half ? j : j - half;
     const float c = cs[2 * i], s = cs[2 * i + 1];
     const float xx = buf[i], yy = buf[i + half];
@@ -72,38 +73,40 @@ __device__ __forceinline__ float norm_rope_head(float x, const float* gamma, flo
     return r;
 }
 
-__global__ __launch_bounds__(kAttnDim) void attn_prep_kernel(AttnDecodeArgs a) {
+template <int DH>
+__global__ __launch_bounds__(DH) void attn_prep_kernel(AttnDecodeArgs a) {
     const int j = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
     const int group = a.Hq / a.Hkv;
     const int g = h / group;  // grouped K/V heads (nm/src/qwen35.hpp:369)
     const int pos = a.positions[b];
     if (pos < 0 || pos >= a.max_ctx) return;  // the host keeps positions in range
     const float* P = a.proj + int64_t(b) * a.proj_stride;
-    const float* cs = a.rope_cs + int64_t(pos) * kAttnDim;  // [Dh/2][2]
-    __shared__ __align__(16) float buf[kAttnDim];
+    const float* cs = a.rope_cs + int64_t(pos) * DH;  // [Dh/2][2]
+    __shared__ __align__(16) float buf[DH];
     __shared__ float scal[2];
-    const float q = norm_rope_head(P[int64_t(h) * 2 * kAttnDim + j], a.q_gamma, a.eps, cs, buf, scal, j);
-    a.q_rot[(int64_t(b) * a.Hq + h) * kAttnDim + j] = q;
+    const float q = norm_rope_head<DH>(P[int64_t(h) * 2 * DH + j], a.q_gamma, a.eps, cs, buf, scal, j);
+    a.q_rot[(int64_t(b) * a.Hq + h) * DH + j] = q;
     if (h % group == 0) {
-        const float k = norm_rope_head(P[a.k_off + int64_t(g) * kAttnDim + j], a.k_gamma, a.eps, cs, buf, scal, j);
-        const float v = P[a.v_off + int64_t(g) * kAttnDim + j];
+        const float k = norm_rope_head<DH>(P[a.k_off + int64_t(g) * DH + j], a.k_gamma, a.eps, cs, buf, scal, j);
+        const float v = P[a.v_off + int64_t(g) * DH + j];
         const int64_t cb = cache_of(a, b);
         const int64_t kv = cb * a.Hkv + g;
-        a.k_cache[(kv * kAttnDim + j) * a.max_ctx + pos] = k;  // [B][Hkv][Dh][max_ctx]
-        a.v_cache[(cb * a.max_ctx + pos) * (int64_t(a.Hkv) * kAttnDim) + int64_t(g) * kAttnDim + j] = v;  // [B][max_ctx][Hkv*Dh]
+        a.k_cache[(kv * DH + j) * a.max_ctx + pos] = k;  // [B][Hkv][Dh][max_ctx]
+        a.v_cache[(cb * a.max_ctx + pos) * (int64_t(a.Hkv) * DH) + int64_t(g) * DH + j] = v;  // [B][max_ctx][Hkv*Dh]
     }
 }
 
 __device__ __forceinline__ int visible_first(int pos, int window) { return (window > 0 && pos + 1 > window) ? pos + 1 - window : 0; }
 
 // ---- 2. scores -------------------------------------------------------------------------
-// A lane per visible key and KV head: it reads the key's 128 cached channels
+// A lane per visible key and KV head: it reads the key's DH cached channels
 // once and forms the dot products of every query head of the group (up to
-// kScoreHeads at a time), each the sequential 128-term sum, side by side. The
+// kScoreHeads at a time), each the sequential DH-term sum, side by side. The
 // grid covers max_ctx in tiles of 256 keys (at most kScoreTiles tiles; lanes
 // loop when the context is longer).
 constexpr int kScoreHeads = 4;
 
+template <int DH>
 __global__ __launch_bounds__(256) void attn_scores_kernel(AttnDecodeArgs a) {
     const int tile0 = blockIdx.y, b = blockIdx.z;
     const int group = a.Hq / a.Hkv, nchunk = (group + kScoreHeads - 1) / kScoreHeads;
@@ -114,20 +117,20 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnDecodeArgs a) {
     const int first = visible_first(pos, a.window);
     const int n = pos + 1 - first;
     if (tile0 * 256 >= n) return;
-    __shared__ float q[kScoreHeads][kAttnDim];
-    for (int i = threadIdx.x; i < kScoreHeads * kAttnDim; i += 256) {
-        const int hh = min(i / kAttnDim, nh - 1);
-        q[i / kAttnDim][i % kAttnDim] = a.q_rot[(int64_t(b) * a.Hq + hq0 + hh) * kAttnDim + i % kAttnDim];
+    __shared__ float q[kScoreHeads][DH];
+    for (int i = threadIdx.x; i < kScoreHeads * DH; i += 256) {
+        const int hh = min(i / DH, nh - 1);
+        q[i / DH][i % DH] = a.q_rot[(int64_t(b) * a.Hq + hq0 + hh) * DH + i % DH];
     }
     __syncthreads();
-    const float* kh = a.k_cache + (cache_of(a, b) * a.Hkv + g) * kAttnDim * a.max_ctx;
+    const float* kh = a.k_cache + (cache_of(a, b) * a.Hkv + g) * DH * a.max_ctx;
     float* sc = a.scores + (int64_t(b) * a.Hq + hq0) * a.max_ctx;
     const int step = int(gridDim.y) * 256;
     for (int t = tile0 * 256 + int(threadIdx.x); t < n; t += step) {
         const float* kj = kh + first + t;
         float dot[kScoreHeads] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 16
-        for (int c = 0; c < kAttnDim; ++c) {
+        for (int c = 0; c < DH; ++c) {
             const float k = kj[int64_t(c) * a.max_ctx];
 #pragma unroll
             for (int hh = 0; hh < kScoreHeads; ++hh) dot[hh] += q[hh][c] * k;
@@ -705,8 +708,7 @@ __global__ __launch_bounds__(kSpvThreads) void attn_softmax_pv_kernel(AttnDecode
 // group's heads), lane 32 hh + c multiplying and adding channel c of head hh
 // from shared memory, four rows per read; small shared memory, so many fit
 // per CU.
-constexpr int kPvbSplit = 4;
-constexpr int kPvbCh = kAttnDim / kPvbSplit;                  // 32
+constexpr int kPvbCh = 32;                                    // channels per workgroup
 constexpr int kPvbThreads = 256;
 constexpr int kPvbHeads = 4;                                  // query heads per workgroup
 constexpr int kPvbTile = 128;                                // rows per tile
@@ -715,7 +717,9 @@ constexpr int kPvbAlpha = kPvbHeads * kPvbTile / kPvbThreads;   // weights per l
 constexpr int kPvbRing = 4;                                  // tiles in flight
 constexpr int kPvbLd = kPvbTile + 4;                         // channel stride in a tile (16-byte rows, 2-way stores)
 
+template <int DH>
 __global__ __launch_bounds__(kPvbThreads) void attn_pv_batch_kernel(AttnDecodeArgs a) {
+    constexpr int kPvbSplit = DH / kPvbCh;  // channel slices per head
     const int tid = threadIdx.x, b = blockIdx.y;
     const int group = a.Hq / a.Hkv, nchunk = (group + kPvbHeads - 1) / kPvbHeads;
     const int part = int(blockIdx.x) % kPvbSplit, gc = int(blockIdx.x) / kPvbSplit;
@@ -726,8 +730,8 @@ __global__ __launch_bounds__(kPvbThreads) void attn_pv_batch_kernel(AttnDecodeAr
     const int first = visible_first(pos, a.window);
     const int n = pos + 1 - first;
     const float* alpha = a.scores + (int64_t(b) * a.Hq + h0) * a.max_ctx;  // head h0 + hh at hh * max_ctx
-    const int64_t kw = int64_t(a.Hkv) * kAttnDim;
-    const float* vb = a.v_cache + (cache_of(a, b) * a.max_ctx + first) * kw + int64_t(g) * kAttnDim + part * kPvbCh;
+    const int64_t kw = int64_t(a.Hkv) * DH;
+    const float* vb = a.v_cache + (cache_of(a, b) * a.max_ctx + first) * kw + int64_t(g) * DH + part * kPvbCh;
     __shared__ __align__(16) float vt[2][kPvbCh * kPvbLd];  // [channel][row]
     __shared__ __align__(16) float at[2][kPvbHeads][kPvbTile];
     const int ntiles = (n + kPvbTile - 1) / kPvbTile;
@@ -824,10 +828,10 @@ __global__ __launch_bounds__(kPvbThreads) void attn_pv_batch_kernel(AttnDecodeAr
 
     if (chain) {
         const int h = h0 + hh, ch = part * kPvbCh + c;
-        const float gate = a.proj[int64_t(b) * a.proj_stride + int64_t(h) * 2 * kAttnDim + kAttnDim + ch];
+        const float gate = a.proj[int64_t(b) * a.proj_stride + int64_t(h) * 2 * DH + DH + ch];
         const float out = acc * sigmoid_f32(gate);
-        const int64_t width = int64_t(a.Hq) * kAttnDim;
-        const int64_t idx = int64_t(h) * kAttnDim + ch;
+        const int64_t width = int64_t(a.Hq) * DH;
+        const int64_t idx = int64_t(h) * DH + ch;
         if (a.out_f32) a.out_f32[int64_t(b) * width + idx] = out;
         float amax = fabsf(out);
         for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
@@ -1147,10 +1151,10 @@ __global__ __launch_bounds__(kAttnDim) void attn_paged_prep_kernel(AttnPagedArgs
     const float* cs = a.rope_cs + int64_t(pos) * kAttnDim;
     __shared__ __align__(16) float buf[kAttnDim];
     __shared__ float scal[2];
-    const float q = norm_rope_head(P[int64_t(h) * 2 * kAttnDim + j], a.q_gamma, a.eps, cs, buf, scal, j);
+    const float q = norm_rope_head<kAttnDim>(P[int64_t(h) * 2 * kAttnDim + j], a.q_gamma, a.eps, cs, buf, scal, j);
     a.q_rot[(int64_t(b) * a.Hq + h) * kAttnDim + j] = q;
     if (h % group == 0) {
-        const float k = norm_rope_head(P[a.k_off + int64_t(g) * kAttnDim + j], a.k_gamma, a.eps, cs, buf, scal, j);
+        const float k = norm_rope_head<kAttnDim>(P[a.k_off + int64_t(g) * kAttnDim + j], a.k_gamma, a.eps, cs, buf, scal, j);
         const float v = P[a.v_off + int64_t(g) * kAttnDim + j];
         const int32_t* pt = page_row(p, b);
         if (p.q8) {
@@ -1432,18 +1436,41 @@ void launch_attn_paged(const AttnPagedArgs& p, hipStream_t s) {
     hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, p);
 }
 
+namespace {
+// heads of 256 channels (the reference's Qwen 3.5 4B / 9B attention): the
+// per-row kernels, each templated on the head width -- prep, 256-key score
+// tiles, the softmax and the many-sequence weighted sum (32 channels per
+// workgroup), for any B and for prefill rows
+void attn_decode_wide(const AttnDecodeArgs& a, unsigned chunks, unsigned tiles, hipStream_t s) {
+    constexpr int DH = 256;
+    const int group = a.Hq / a.Hkv;
+    hipLaunchKernelGGL(attn_prep_kernel<DH>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(DH), 0, s, a);
+    hipLaunchKernelGGL(attn_scores_kernel<DH>, dim3(chunks, tiles, unsigned(a.B)), dim3(256), 0, s, a);
+    if (a.max_ctx % 4 == 0)
+        hipLaunchKernelGGL(attn_softmax_regs_kernel<256>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(attn_softmax_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(seqsum::kThreads), 0, s, a);
+    hipLaunchKernelGGL(attn_pv_batch_kernel<DH>, dim3(unsigned(a.Hkv * ((group + kPvbHeads - 1) / kPvbHeads) * (DH / kPvbCh)), unsigned(a.B)), dim3(kPvbThreads), 0, s,
+                       a);
+}
+}  // namespace
+
 void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
     const int64_t vis = a.window > 0 ? std::min<int64_t>(a.max_ctx, a.window) : a.max_ctx;
     const unsigned tiles = unsigned(std::min<int64_t>(kScoreTiles, (vis + 255) / 256));
     const int group = a.Hq / a.Hkv;
     const unsigned chunks = unsigned(a.Hkv * ((group + kScoreHeads - 1) / kScoreHeads));
+    if (a.Dh == 256) {
+        attn_decode_wide(a, chunks, tiles, s);
+        return;
+    }
     // few sequences: 64-key tiles spread the keys over the CUs; many
     // sequences (and prefill rows) fill them with the 256-key form
     if (a.max_ctx % 4 == 0 && a.B <= 2 && !a.shared_cache) {  // prep folded in
         hipLaunchKernelGGL(attn_scores_tile_kernel, dim3(chunks, unsigned(std::min<int64_t>(kScTiles, (vis + 3 + kScTileKeys - 1) / kScTileKeys)), unsigned(a.B)), dim3(256), 0, s, a);
     } else {
-        hipLaunchKernelGGL(attn_prep_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, a);
-        hipLaunchKernelGGL(attn_scores_kernel, dim3(chunks, tiles, unsigned(a.B)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(attn_prep_kernel<kAttnDim>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, a);
+        hipLaunchKernelGGL(attn_scores_kernel<kAttnDim>, dim3(chunks, tiles, unsigned(a.B)), dim3(256), 0, s, a);
     }
     // a prefill chunk (rows of one sequence, full causal visibility): the
     // register softmax and the row-block weighted sum
@@ -1467,7 +1494,8 @@ void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
     else if (pv_blocks <= 2 * device_cus())
         hipLaunchKernelGGL(attn_pv_kernel<7>, pv_grid, dim3(kPvThreads), pv_shared_bytes(7), s, a);
     else
-        hipLaunchKernelGGL(attn_pv_batch_kernel, dim3(unsigned(a.Hkv * ((group + kPvbHeads - 1) / kPvbHeads) * kPvbSplit), unsigned(a.B)), dim3(kPvbThreads), 0, s, a);
+        hipLaunchKernelGGL(attn_pv_batch_kernel<kAttnDim>, dim3(unsigned(a.Hkv * ((group + kPvbHeads - 1) / kPvbHeads) * (kAttnDim / kPvbCh)), unsigned(a.B)), dim3(kPvbThreads),
+                           0, s, a);
 }
 
 }  // namespace hero

@@ -1008,6 +1008,134 @@ __global__ __launch_bounds__(64) void gemm_q8_skinny_wave_kernel(const int8_t* _
     }
 }
 
+// The tall form with the activation rows in shared memory: a workgroup of NW
+// waves copies the 16 activation rows (K <= 4096 bytes each) and their
+// scales into shared memory once, then each wave walks its own range of
+// 16-row weight groups exactly as gemm_q8_skinny_wave_kernel does, but reads
+// only the weights and their scales from memory: 5 load instructions per
+// 4 KB of weights instead of 11. The weight ring is issued before the copy,
+// so its first loads are in flight while the activations arrive from L2.
+constexpr int kSklMaxK = 4096;
+constexpr int kSklRowPad = 16;  // activation row stride K + 16: 16 lanes' 16-byte reads hit distinct banks
+constexpr int kSklDxPad = 4;    // activation scale row stride nb + 4 (likewise)
+constexpr int kSklRing = 2;     // rounds in flight per wave (16 waves per CU)
+
+size_t skl_shared_bytes(int nw, int K) {
+    const int nb = K / 32;
+    return size_t(16) * size_t(K + kSklRowPad) + size_t(16) * size_t(nb + kSklDxPad) * 4 + size_t(nw) * kSklRing * 2 * kSkwRound * 8 * 2;
+}
+
+template <int EPI, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) void gemm_q8_skinny_lds_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {
+    extern __shared__ __align__(16) uint8_t skl_smem[];
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, q = lane >> 4, c = lane & 15;
+    const int nb = K >> 5, rounds = nb / kSkwRound;
+    const int rowb = K + kSklRowPad, dxrow = nb + kSklDxPad;
+    int8_t* xs = reinterpret_cast<int8_t*>(skl_smem);                       // [16][K + 16]
+    float* dxs = reinterpret_cast<float*>(skl_smem + 16 * rowb);             // [16][nb + 4]
+    uint16_t (*dws)[2][kSkwRound][8] = reinterpret_cast<uint16_t (*)[2][kSkwRound][8]>(dxs + 16 * dxrow) + wv * kSklRing;  // this wave's [ring][8-row group][block][row]
+    const int groups = (N + 15) >> 4, G = gridDim.x;
+    const int wg_begin = int(int64_t(groups) * blockIdx.x / G), wg_end = int(int64_t(groups) * (blockIdx.x + 1) / G);
+    const int g_begin = wg_begin + (wg_end - wg_begin) * wv / NW, g_end = wg_begin + (wg_end - wg_begin) * (wv + 1) / NW;
+    const int steps = (g_end - g_begin) * rounds;
+    const int steps_pad = (steps + kSklRing - 1) / kSklRing * kSklRing;
+    const __amdgpu_buffer_rsrc_t bw = buffer_of(wq, uint32_t(N) * uint32_t(K));
+    const __amdgpu_buffer_rsrc_t bx = buffer_of(xq, uint32_t(M) * uint32_t(K));
+    const __amdgpu_buffer_rsrc_t bd = buffer_of(wd, uint32_t(nb) * uint32_t(Npad) * 2u);
+    const __amdgpu_buffer_rsrc_t bxd = buffer_of(xd, uint32_t(M) * uint32_t(nb) * 4u);
+
+    struct Ring {
+        v4b_t w[kSkwPairs];
+        v4b_t d;
+    };
+    auto load = [&](int step, Ring& L) {
+        const int g = g_begin + step / rounds, r = step % rounds;
+        const bool on = step < steps;
+        const int n = g * 16 + c, b0 = r * kSkwRound;
+        const bool wrow = on && n < N;
+#pragma unroll
+        for (int i = 0; i < kSkwPairs; ++i) {
+            const uint32_t off = uint32_t(b0 + 2 * i) * 32u + 16u * uint32_t(q);
+            L.w[i] = __builtin_amdgcn_raw_buffer_load_b128(bw, wrow ? uint32_t(n) * uint32_t(K) + off : kOOB, 0, 0);
+        }
+        const bool drow = on && c < kSkwRound && g * 16 + 8 * (q >> 1) < N;
+        L.d = __builtin_amdgcn_raw_buffer_load_b128(bd, drow ? uint32_t(scale_index(g * 16 + 8 * (q >> 1), b0 + c, nb)) * 2u : kOOB, 0, 0);
+    };
+    Ring ring[kSklRing];
+#pragma unroll
+    for (int k = 0; k < kSklRing; ++k) load(k, ring[k]);
+
+    // the activation rows and scales (rows >= M read as zeros)
+    const int cpr = K / 16;  // 16-byte pieces per row
+    for (int p = tid; p < 16 * cpr; p += 64 * NW) {
+        const int row = p / cpr, col = 16 * (p % cpr);
+        const v4b_t v = __builtin_amdgcn_raw_buffer_load_b128(bx, row < M ? uint32_t(row) * uint32_t(K) + uint32_t(col) : kOOB, 0, 0);
+        *reinterpret_cast<v4b_t*>(xs + row * rowb + col) = v;
+    }
+    for (int e = tid; e < 16 * nb; e += 64 * NW) {
+        const int row = e / nb, b = e % nb;
+        dxs[row * dxrow + b] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bxd, row < M ? uint32_t(row * nb + b) * 4u : kOOB, 0, 0));
+    }
+    __syncthreads();
+
+    const int8_t* xrow = xs + c * rowb + 16 * q;
+    const float* dxr = dxs + c * dxrow;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // outputs (n = g*16 + 4q + r, m = c)
+    for (int s0 = 0; s0 < steps_pad; s0 += kSklRing) {
+#pragma unroll
+        for (int k = 0; k < kSklRing; ++k) {
+            const int s = s0 + k;
+            const int g = g_begin + s / rounds, r = s % rounds;
+            const int b0 = r * kSkwRound;
+            if ((q & 1) == 0 && c < kSkwRound) *reinterpret_cast<v4b_t*>(&dws[k][q >> 1][c][0]) = ring[k].d;
+            const bool first = q < 2;
+            const float4 dxa = *reinterpret_cast<const float4*>(dxr + b0);
+            const float4 dxb = *reinterpret_cast<const float4*>(dxr + b0 + 4);
+#pragma unroll
+            for (int i = 0; i < kSkwPairs; ++i) {
+                const v4b_t xv = *reinterpret_cast<const v4b_t*>(xrow + (b0 + 2 * i) * 32);
+                const long wl = lo64(ring[k].w[i]), wh = hi64(ring[k].w[i]);
+                const long xl = lo64(xv), xh = hi64(xv);
+                const v4i_t zero = {0, 0, 0, 0};
+                v4i_t c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(wl, first ? xl : 0L, zero, 0, 0, 0);
+                c0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(wh, first ? xh : 0L, c0, 0, 0, 0);
+                v4i_t c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(wl, first ? 0L : xl, zero, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(wh, first ? 0L : xh, c1, 0, 0, 0);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int j = 2 * i + h;  // block within the round
+                    const v4i_t& cc = h ? c1 : c0;
+                    const uint2 d2 = *reinterpret_cast<const uint2*>(&dws[k][q >> 1][j][4 * (q & 1)]);
+                    const float4& d4 = j < 4 ? dxa : dxb;
+                    const float dx = (j & 3) == 0 ? d4.x : (j & 3) == 1 ? d4.y : (j & 3) == 2 ? d4.z : d4.w;
+                    acc[0] = acc[0] + float(cc[0]) * (half_bits_to_f32(uint16_t(d2.x & 0xFFFFu)) * dx);
+                    acc[1] = acc[1] + float(cc[1]) * (half_bits_to_f32(uint16_t(d2.x >> 16)) * dx);
+                    acc[2] = acc[2] + float(cc[2]) * (half_bits_to_f32(uint16_t(d2.y & 0xFFFFu)) * dx);
+                    acc[3] = acc[3] + float(cc[3]) * (half_bits_to_f32(uint16_t(d2.y >> 16)) * dx);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            load(s + kSklRing, ring[k]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (r == rounds - 1 && s < steps) {
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int n = g * 16 + 4 * q + rr;
+                    if (n < N && c < M) {
+                        const int64_t o = int64_t(c) * N + n;
+                        if constexpr (EPI == kEpiResidual)
+                            y[o] = resid[o] + acc[rr];
+                        else
+                            y[o] = acc[rr];
+                    }
+                    acc[rr] = 0.f;
+                }
+            }
+        }
+    }
+}
+
 namespace {
 template <int BM>
 void gemm_dispatch(int epi, const int8_t* wq, const uint16_t* wd, const int8_t* xq, const float* xd, float* y, const float* resid, int M, int N, int Npad, int K, hipStream_t s) {
@@ -1050,7 +1178,30 @@ void launch_gemm_q8(const void* packed, const void* act, float* y, const float* 
     };
     switch (gemm_q8_plan(M, N, K)) {
     case kGemmPlanSkinnyWave:
-        // tall: a wave per group range, every chain in registers
+        // tall: a wave per group range, every chain in registers; at K <= 4096
+        // the activations in shared memory, as many waves per workgroup as
+        // keep a workgroup on every CU
+        if (K <= kSklMaxK) {
+            const int64_t per = groups / device_cus();
+            const int nw = per >= 8 ? 8 : per >= 4 ? 4 : per >= 2 ? 2 : 1;
+            auto run = [&](auto kernel) {
+                const size_t smem = skl_shared_bytes(nw, int(K));
+                const unsigned grid = unsigned(std::max<int64_t>(1, std::min<int64_t>(grid_for(kernel, 64 * nw, smem), groups / nw)));
+                hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * nw), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
+            };
+            if (epi == kEpiResidual) {
+                if (nw == 8) run(gemm_q8_skinny_lds_kernel<kEpiResidual, 8>);
+                else if (nw == 4) run(gemm_q8_skinny_lds_kernel<kEpiResidual, 4>);
+                else if (nw == 2) run(gemm_q8_skinny_lds_kernel<kEpiResidual, 2>);
+                else run(gemm_q8_skinny_lds_kernel<kEpiResidual, 1>);
+            } else {
+                if (nw == 8) run(gemm_q8_skinny_lds_kernel<kEpiStore, 8>);
+                else if (nw == 4) run(gemm_q8_skinny_lds_kernel<kEpiStore, 4>);
+                else if (nw == 2) run(gemm_q8_skinny_lds_kernel<kEpiStore, 2>);
+                else run(gemm_q8_skinny_lds_kernel<kEpiStore, 1>);
+            }
+            break;
+        }
         if (epi == kEpiResidual)
             hipLaunchKernelGGL(gemm_q8_skinny_wave_kernel<kEpiResidual>, dim3(grid_for(gemm_q8_skinny_wave_kernel<kEpiResidual>, 64, 0)), dim3(64), 0, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
         else

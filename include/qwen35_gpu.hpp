@@ -6,9 +6,8 @@
 // This header belongs next to nm/src/qwen35.hpp: it includes the reference's
 // own headers (compile with -I<reference>/nm/src -I<this repo>/include and link
 // -lhero_amd). C is a Qwen 3.5 config type of the reference's shape
-// (qwen35.hpp:26-88); the GPU loader accepts head_dim 128 (attention and
-// delta-net heads), so configs with 256-wide attention heads (the published
-// Qwen 3.5 4B / 9B shapes) load with HERO_EINVAL.
+// (qwen35.hpp:26-88); the GPU loader accepts 128- or 256-wide attention heads
+// (the published Qwen 3.5 4B / 9B shapes have 256) and 128-wide delta-net heads.
 #pragma once
 
 #include <hero_model.h>

@@ -78,6 +78,20 @@ struct TinyHk4UntiedConfig {
     using OutputWeight = Weight<D, V>;
     static constexpr bool is_recurrent(size_t layer) { return (layer + 1) % FULL_ATTENTION_INTERVAL != 0; }
 };
+// the attention geometry of the reference's Qwen 3.5 4B / 9B (nm/src/qwen35.hpp:25-88):
+// 256-wide heads (Hq * HEAD_DIM = 2048 != D), a quarter of them rotating, RoPE
+// base 1e7, 4 key heads over 8 value heads, untied head -- at tiny width
+struct TinyDh256Config {
+    static constexpr size_t V = 32000, D = 1024, L = 4, CTX = 4096;
+    static constexpr size_t Hq = 8, Hkv = 2, HEAD_DIM = 256;
+    static constexpr size_t ROPE_BASE = 10000000, ROTARY_NUM = 1, ROTARY_DEN = 4;
+    static constexpr size_t KEY_HEAD_DIM = 128, VALUE_HEAD_DIM = 128, KEY_HEADS = 4, VALUE_HEADS = 8, CONV_WIDTH = 4;
+    static constexpr size_t FF = 2816;
+    static constexpr Scalar RMS_EPS = 1e-6f;
+    static constexpr size_t FULL_ATTENTION_INTERVAL = 4;
+    using OutputWeight = Weight<D, V>;
+    static constexpr bool is_recurrent(size_t layer) { return (layer + 1) % FULL_ATTENTION_INTERVAL != 0; }
+};
 struct Hybrid8BConfig {
     static constexpr size_t V = 151936, D = 4096, L = 32, CTX = 65536;
     static constexpr size_t Hq = 32, Hkv = 8, HEAD_DIM = 128;
@@ -406,9 +420,10 @@ int main(int argc, char** argv) {
             const size_t steps = std::strtoull(argv[5], nullptr, 10);
             if (std::strcmp(argv[2], "tiny") == 0) return run_model<TinyConfig>(argv[3], argv[4], steps, argv[6]);
             if (std::strcmp(argv[2], "tiny_hk4u") == 0) return run_model<TinyHk4UntiedConfig>(argv[3], argv[4], steps, argv[6]);
+            if (std::strcmp(argv[2], "tiny_dh256") == 0) return run_model<TinyDh256Config>(argv[3], argv[4], steps, argv[6]);
             if (std::strcmp(argv[2], "8b") == 0) return run_model<Hybrid8BConfig>(argv[3], argv[4], steps, argv[6]);
         }
-        std::fprintf(stderr, "usage: %s kernels DIR | window DIR | model {tiny|tiny_hk4u|8b} GGUF PROMPT STEPS OUTDIR\n", argv[0]);
+        std::fprintf(stderr, "usage: %s kernels DIR | window DIR | model {tiny|tiny_hk4u|tiny_dh256|8b} GGUF PROMPT STEPS OUTDIR\n", argv[0]);
         return 2;
     } catch (const std::exception& e) {
         std::fprintf(stderr, "ref_harness: %s\n", e.what());

@@ -100,6 +100,26 @@ def variant_gguf(tmp_path_factory, manifest):
     return path
 
 
+@pytest.fixture(scope="session")
+def dh256_golden():
+    return dict(np.load(os.path.join(GOLDEN, "tiny_dh256_model.npz")))
+
+
+# the attention geometry of the reference's Qwen 3.5 4B / 9B configs (256-wide
+# heads, a quarter rotating, RoPE base 1e7, 4 key heads over 8 value heads,
+# untied head) at tiny width (the golden's model)
+@pytest.fixture(scope="session")
+def dh256_gguf(tmp_path_factory, manifest):
+    import hero_amd
+
+    t = manifest["tiny_dh256_model"]
+    path = str(tmp_path_factory.mktemp("dh256") / "tiny_dh256.gguf")
+    hero_amd.write_synthetic_gguf(path, hero_amd.HybridShape(**t["shape"]), seed=t["seed"], ctx=t["ctx"], tied=False)
+    with open(path, "rb") as f:
+        assert hashlib.sha256(f.read()).hexdigest() == t["gguf_sha256"], "synthetic 256-wide-head model bytes changed"
+    return path
+
+
 # the tiny shape with the tensor types of a Q4_K_M checkpoint (Q4_K, Q5_K, Q6_K
 # and Q8_0 tensors; the golden's model)
 @pytest.fixture(scope="session")

@@ -19,12 +19,15 @@ so it runs in the build container only). This script:
      (Q4_K, Q5_K, Q6_K and Q8_0 tensors) -> tiny_kmix_model.npz;
   6. `hybrid8b`: the ~8B shape (the benchmark's model, seed 20260101, a
      600-token prompt, 32 greedy passes) -> hybrid8b_model.npz with the ids,
-     per-step top-5 and the sha256 of the prefill and last logit vectors.
+     per-step top-5 and the sha256 of the prefill and last logit vectors;
+  7. `dh256`: the attention geometry of the reference's Qwen 3.5 4B / 9B
+     configs (256-wide heads, a quarter rotating, RoPE base 1e7, Hk 4 over
+     Hv 8, untied head) at tiny width -> tiny_dh256_model.npz.
 
 manifest.json records seeds, shapes, the GGUF's sha256 and the compiler
 flags (-O3 -march=x86-64-v3 -ffp-contract=off: no FMA contraction).
 
-Run:  python tests/golden/make_golden.py [kernels] [tiny] [window] [variant] [kmix] [hybrid8b]
+Run:  python tests/golden/make_golden.py [kernels] [tiny] [window] [variant] [kmix] [hybrid8b] [dh256]
       (no argument: all parts; the manifest keeps the entries of parts not rerun)
 """
 from __future__ import annotations
@@ -256,6 +259,26 @@ def make_variant(tmp: str) -> dict:
             "decode_steps": 32, "gguf_sha256": sha, "gguf_bytes": size, "reference_times": times}
 
 
+DH256_SEED = 2560
+# the reference's Qwen 3.5 4B / 9B attention geometry at tiny width
+DH256_SHAPE = dict(vocab=32000, d_model=1024, layers=4, ffn=2816, q_heads=8, kv_heads=2, head_dim=256, key_heads=4,
+                   value_heads=8, rope_base=1e7)
+
+
+def make_dh256(tmp: str) -> dict:
+    import hero_amd
+
+    shape = hero_amd.HybridShape(**DH256_SHAPE)
+    prompt = np.random.default_rng(DH256_SEED + 1).integers(0, 32000, 24).astype(np.int32)
+    rd, sha, size, times = run_model_case(tmp, "tiny_dh256", shape, DH256_SEED, 4096, False, prompt, 32, tmp)
+    np.savez_compressed(
+        os.path.join(HERE, "tiny_dh256_model.npz"), prompt=prompt, ids=rd("ids.i32", np.int32),
+        top5_ids=rd("top5_ids.i32", np.int32).reshape(-1, 5), top5_logits=rd("top5_logits.f32", np.float32).reshape(-1, 5),
+        logits_prefill=rd("logits_prefill.f32", np.float32), logits_last=rd("logits_last.f32", np.float32))
+    return {"seed": DH256_SEED, "shape": DH256_SHAPE, "tied": False, "ctx": 4096, "prompt_len": 24, "decode_steps": 32,
+            "gguf_sha256": sha, "gguf_bytes": size, "reference_times": times}
+
+
 KMIX_SEED = 5150
 
 
@@ -293,9 +316,9 @@ def make_hybrid8b(tmp: str) -> dict:
 
 
 PARTS = {"kernels": make_kernels, "tiny": make_tiny, "window": make_window, "variant": make_variant, "kmix": make_kmix,
-         "hybrid8b": make_hybrid8b}
+         "hybrid8b": make_hybrid8b, "dh256": make_dh256}
 MANIFEST_KEYS = {"kernels": "kernels", "tiny": "tiny_model", "window": "window", "variant": "tiny_hk4u_model",
-                 "kmix": "tiny_kmix_model", "hybrid8b": "hybrid8b_model"}
+                 "kmix": "tiny_kmix_model", "hybrid8b": "hybrid8b_model", "dh256": "tiny_dh256_model"}
 
 
 def main():

@@ -170,9 +170,10 @@ def test_rmsnorm_gate_up_swiglu_matches_oracle_bytes(lib, ff):
                                    # the skinny path (M <= 16): ragged 16-row groups, a partial round
                                    # (768 = 24 blocks), fewer rows than one group, the largest K
                                    (2, 4100, 4096), (8, 33, 12288), (16, 1003, 768), (13, 12288, 4096), (3, 7, 256), (16, 40, 16384),
-                                   # its one-wave form for tall matrices (at least two 16-row groups per CU):
-                                   # a ragged last group, K = 12288
-                                   (16, 8200, 4096), (7, 9000, 12288)])
+                                   # its tall forms (at least two 16-row groups per CU): a ragged last
+                                   # group, K = 12288 (activations from memory), and the K = 4096 form with
+                                   # the activations in shared memory at 2, 4 and 8 waves per workgroup
+                                   (16, 8200, 4096), (7, 9000, 12288), (5, 16448, 4096), (16, 24576, 4096), (11, 40000, 4096)])
 def test_gemm_matches_oracle_bitwise(lib, m, n, k):
     """M-row GEMM on int8 MFMA: every element equals the reference's matmul
     (per-row vec_dot in block order), with and without the residual."""
@@ -588,13 +589,16 @@ def test_attn_decode_matches_oracle(lib, window):
 # 6 (score head chunks of 4 and 2), a sliding window, and enough sequences x
 # heads to take the many-sequence form of the weighted sum (B * Hq * 4 > 512),
 # whose workgroups serve up to four heads of a group (6 = one of 4, one of 2)
-@pytest.mark.parametrize("B,hq,hkv,pos,window", [(2, 8, 2, 700, 0), (1, 6, 1, 1500, 0), (2, 4, 4, 450, 300), (5, 32, 8, 333, 0),
-                                                 (12, 12, 2, 260, 0)])
-def test_attn_decode_long_context_matches_oracle(lib, B, hq, hkv, pos, window):
+# 256-wide heads (the reference's Qwen 3.5 4B / 9B attention) take the per-row
+# kernels at every B: one and two sequences, a window, many sequences
+@pytest.mark.parametrize("B,hq,hkv,pos,window,dh", [(2, 8, 2, 700, 0, 128), (1, 6, 1, 1500, 0, 128), (2, 4, 4, 450, 300, 128),
+                                                    (5, 32, 8, 333, 0, 128), (12, 12, 2, 260, 0, 128), (1, 16, 4, 1500, 0, 256),
+                                                    (2, 8, 2, 450, 300, 256), (16, 16, 4, 333, 0, 256), (3, 8, 2, 4200, 0, 256)])
+def test_attn_decode_long_context_matches_oracle(lib, B, hq, hkv, pos, window, dh):
     from hero_amd._lib import AttnDecodeArgs
 
     rng = np.random.default_rng(pos + hq)
-    dh, max_ctx = 128, pos + 9
+    max_ctx = pos + 9
     qw, kw = hq * dh, hkv * dh
     stride = 2 * qw + 2 * kw
     qg = (1 + 0.1 * rng.standard_normal(dh)).astype(np.float32)
@@ -645,13 +649,13 @@ def test_attn_decode_long_context_matches_oracle(lib, B, hq, hkv, pos, window):
 # 603 rows leave a partial last block; group 6 makes head chunks of 4 and 2;
 # p0 = 4100 gives rows of more than 4096 keys, the chunked softmax);
 # max_ctx % 4 != 0 and the window take the per-row kernels.
-@pytest.mark.parametrize("M,p0,hq,hkv,max_ctx,window", [(37, 0, 8, 2, 40, 0), (603, 70, 32, 8, 676, 0), (20, 33, 6, 1, 56, 0),
-                                                        (64, 4100, 8, 2, 4168, 0), (10, 5, 4, 1, 17, 0), (24, 9, 8, 2, 36, 7)])
-def test_attn_prefill_rows_match_oracle(lib, M, p0, hq, hkv, max_ctx, window):
+@pytest.mark.parametrize("M,p0,hq,hkv,max_ctx,window,dh", [(37, 0, 8, 2, 40, 0, 128), (603, 70, 32, 8, 676, 0, 128), (20, 33, 6, 1, 56, 0, 128),
+                                                           (64, 4100, 8, 2, 4168, 0, 128), (10, 5, 4, 1, 17, 0, 128), (24, 9, 8, 2, 36, 7, 128),
+                                                           (300, 40, 16, 4, 344, 0, 256), (12, 3, 8, 2, 17, 0, 256)])
+def test_attn_prefill_rows_match_oracle(lib, M, p0, hq, hkv, max_ctx, window, dh):
     from hero_amd._lib import AttnDecodeArgs
 
     rng = np.random.default_rng(M + p0 + hq)
-    dh = 128
     qw, kw = hq * dh, hkv * dh
     stride = 2 * qw + 2 * kw
     qg = (1 + 0.1 * rng.standard_normal(dh)).astype(np.float32)

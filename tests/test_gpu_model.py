@@ -342,3 +342,54 @@ def test_variant_model_matches_reference(variant_gguf, variant_golden):
         same_bits(last.values, variant_golden["logits_last"])
     finally:
         m.close()
+
+
+def test_dh256_model_matches_reference(dh256_gguf, dh256_golden):
+    """The attention geometry of the reference's Qwen 3.5 4B / 9B configs at
+    tiny width: 256-wide heads (Hq * Dh = 2048 != D), 64 rotary channels, RoPE
+    base 1e7, 4 key heads over 8 value heads, untied head. Prefill logits, the
+    greedy ids of 32 graph-replayed decode passes and the last logits equal the
+    reference's bit for bit; the same prompt as one sequence of a batch state
+    decodes to the same ids and logits; and a 700-token prompt (two prefill
+    chunks) matches the oracle."""
+    import oracle
+
+    m = hero_amd.Qwen35Model.open(dh256_gguf)
+    try:
+        assert (m.dims.head_dim, m.dims.rotary_dims, m.dims.key_heads, m.dims.value_heads, m.dims.tied) == (256, 64, 4, 8, 0)
+        steps = len(dh256_golden["ids"]) - 1
+        state = m.new_state(1024)
+        lg = m.forward(state, ids=dh256_golden["prompt"])
+        same_bits(lg.values, dh256_golden["logits_prefill"])
+        ids, last = m.decode_greedy(state, lg.argmax(), steps, want_logits=True)
+        assert np.array_equal(np.array([lg.argmax()] + [int(i) for i in ids], np.int32), dh256_golden["ids"])
+        same_bits(last.values, dh256_golden["logits_last"])
+        state.close()
+
+        bs = m.new_batch_state(1024, 3)
+        short = np.random.default_rng(7).integers(0, m.V, 5).astype(np.int32)
+        firsts = [m.forward_seq(bs, b, ids=p).argmax() for b, p in enumerate((short, dh256_golden["prompt"], short[:2]))]
+        out, logits = m.decode_batch(bs, firsts, steps, want_logits=True)
+        assert np.array_equal(np.array([firsts[1]] + [int(v) for v in out[:, 1]], np.int32), dh256_golden["ids"])
+        same_bits(logits[1], dh256_golden["logits_last"])
+        bs.close()
+
+        prompt = np.random.default_rng(8).integers(0, m.V, 700).astype(np.int32)
+        ref = oracle.Model(path=dh256_gguf)
+        try:
+            expect = ref.forward_ids(prompt)
+            state = m.new_state(1024)
+            lg = m.forward(state, ids=prompt)
+            same_bits(lg.values, expect)
+            ids, last = m.decode_greedy(state, lg.argmax(), 4, want_logits=True)
+            ref_ids = [int(np.argmax(expect))]  # first index of the maximum, the reference's tie rule
+            for _ in range(4):
+                r = ref.forward_ids([ref_ids[-1]])
+                ref_ids.append(int(np.argmax(r)))
+            assert [lg.argmax()] + [int(i) for i in ids] == ref_ids
+            same_bits(last.values, r)
+            state.close()
+        finally:
+            ref.close()
+    finally:
+        m.close()

@@ -369,6 +369,25 @@ def test_variant_model_matches_reference(variant_gguf, variant_golden):
     m.close()
 
 
+# ---- 256-wide attention heads (the reference's Qwen 3.5 4B / 9B geometry) ---------------
+def test_dh256_model_matches_reference(dh256_gguf, dh256_golden):
+    """8 query / 2 K/V heads of 256 channels (Hq * Dh = 2048 != D = 1024),
+    rope.dimension_count 64 (partial rotary), RoPE base 1e7, 4 key heads over
+    8 value heads and an untied head: the oracle's greedy ids and its prefill /
+    last logits equal the reference's bit for bit."""
+    m = oracle.Model(path=dh256_gguf)
+    prompt = dh256_golden["prompt"]
+    prefill = m.forward_ids(prompt)
+    assert np.array_equal(bits(prefill), bits(dh256_golden["logits_prefill"]))
+    ids = [oracle.argmax(prefill)]
+    for _ in range(len(dh256_golden["ids"]) - 1):
+        last = m.forward_ids([ids[-1]])
+        ids.append(oracle.argmax(last))
+    assert np.array_equal(np.array(ids, np.int32), dh256_golden["ids"])
+    assert np.array_equal(bits(last), bits(dh256_golden["logits_last"]))
+    m.close()
+
+
 # ---- K-quant tensors: the tensor types of a Q4_K_M checkpoint -----------------------
 def test_kquant_model_matches_reference(kmix_gguf, kmix_golden):
     """The tiny shape with a Q6_K embedding (the tied head), Q5_K attn_qkv and

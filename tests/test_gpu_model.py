@@ -393,3 +393,36 @@ def test_dh256_model_matches_reference(dh256_gguf, dh256_golden):
             ref.close()
     finally:
         m.close()
+
+
+def test_qwen35_4b_shape_matches_oracle(tmp_path):
+    """The reference's Qwen 3.5 4B config at 4 layers and a small vocabulary
+    (nm/src/qwen35.hpp:25-56): d_model 2560 (K = 2560 matvecs; Hq * Dh = 4096
+    != D), SwiGLU 9216, 16 query / 4 K/V heads of 256 channels, 16 key over 32
+    value delta-net heads, tied head, RoPE base 1e7. A 40-token prefill and 8
+    greedy passes equal the oracle bit for bit."""
+    import oracle
+
+    shape = hero_amd.HybridShape(vocab=32000, d_model=2560, layers=4, ffn=9216, q_heads=16, kv_heads=4, head_dim=256,
+                                 key_heads=16, value_heads=32, rope_base=1e7)
+    path = str(tmp_path / "qwen35_4b_shape.gguf")
+    hero_amd.write_synthetic_gguf(path, shape, seed=25600, ctx=1024, tied=True)
+    prompt = np.random.default_rng(25601).integers(0, 32000, 40).astype(np.int32)
+    ref = oracle.Model(path=path)
+    m = hero_amd.Qwen35Model.open(path)
+    try:
+        expect = ref.forward_ids(prompt)
+        state = m.new_state(256)
+        lg = m.forward(state, ids=prompt)
+        same_bits(lg.values, expect)
+        ids, last = m.decode_greedy(state, lg.argmax(), 8, want_logits=True)
+        ref_ids = [int(np.argmax(expect))]
+        for _ in range(8):
+            r = ref.forward_ids([ref_ids[-1]])
+            ref_ids.append(int(np.argmax(r)))
+        assert [lg.argmax()] + [int(i) for i in ids] == ref_ids
+        same_bits(last.values, r)
+        state.close()
+    finally:
+        m.close()
+        ref.close()

@@ -21,9 +21,14 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const float* __restri
     // 8 consecutive outputs never straddle an interleave chunk (il % 8 == 0)
     const float* gate = gu + row * 2 * FF + (il ? (c / il) * 2 * il + c % il : c);
     const float* up = gate + (il ? il : FF);
+    // 16-byte reads (c % 8 == 0, rows of 2 FF floats)
+    const float4 g0 = reinterpret_cast<const float4*>(gate)[0], g1 = reinterpret_cast<const float4*>(gate)[1];
+    const float4 u0 = reinterpret_cast<const float4*>(up)[0], u1 = reinterpret_cast<const float4*>(up)[1];
+    const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const float u[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
     float v[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = silu_f32(gate[j]) * up[j];
+    for (int j = 0; j < 8; ++j) v[j] = silu_f32(g[j]) * u[j];
     if (y) {
         reinterpret_cast<float4*>(y)[2 * i] = make_float4(v[0], v[1], v[2], v[3]);
         reinterpret_cast<float4*>(y)[2 * i + 1] = make_float4(v[4], v[5], v[6], v[7]);

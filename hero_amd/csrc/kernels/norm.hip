@@ -51,10 +51,56 @@ __global__ __launch_bounds__(seqsum::kThreads) void rmsnorm_quant_kernel(const f
     }
 }
 
+// The same for D <= 4096, D % 32 == 0, with the row in registers: lane t
+// holds elements 8t .. 8t+7 (one read of x), their squares go to the exact
+// sum from registers, and the lane's 8 outputs are a quarter of a Q8_0 block
+// (quantize8_in_quad). 512 lanes.
+constexpr int kNormThreads = 512;
+
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_quant_regs_kernel(const float* __restrict__ x, const float* __restrict__ gamma, float eps, float* __restrict__ y, int8_t* __restrict__ qs, float* __restrict__ qd,
+                                                                         int D) {
+    constexpr int PT = seqsum::kMaxN / kNormThreads;  // 8
+    __shared__ seqsum::Shared sm;
+    __shared__ __align__(16) float sq[seqsum::kMaxN];
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x, i0 = tid * PT;
+    const bool on = i0 < D;  // whole quads (D % 32 == 0)
+    float v[PT], s2[PT];
+    if (on) {
+        const float4 a = reinterpret_cast<const float4*>(x + row * D + i0)[0];
+        const float4 b = reinterpret_cast<const float4*>(x + row * D + i0)[1];
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int k = 0; k < PT; ++k) v[k] = 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < PT; ++k) s2[k] = v[k] * v[k];
+    const float s = seqsum::sum_nonneg_regs<kNormThreads>(s2, sq, D, sm);
+    const float inv = 1.f / sqrtf(s / float(D) + eps);
+    if (!on) return;
+    const float4 ga = reinterpret_cast<const float4*>(gamma + i0)[0];
+    const float4 gb = reinterpret_cast<const float4*>(gamma + i0)[1];
+    float o[8] = {ga.x * v[0] * inv, ga.y * v[1] * inv, ga.z * v[2] * inv, ga.w * v[3] * inv, gb.x * v[4] * inv, gb.y * v[5] * inv, gb.z * v[6] * inv, gb.w * v[7] * inv};
+    if (y) {
+        reinterpret_cast<float4*>(y + row * D + i0)[0] = make_float4(o[0], o[1], o[2], o[3]);
+        reinterpret_cast<float4*>(y + row * D + i0)[1] = make_float4(o[4], o[5], o[6], o[7]);
+    }
+    if (qs) {
+        uint16_t dh;
+        const int2 q = quantize8_in_quad(o, &dh);
+        reinterpret_cast<int2*>(qs + row * D)[tid] = q;
+        if ((tid & 3) == 0) qd[row * (D >> 5) + (tid >> 2)] = half_bits_to_f32(dh);
+    }
+}
+
 void launch_rmsnorm_quant(const float* x, const float* gamma, float eps, float* y, void* act, int64_t M, int64_t D, hipStream_t s) {
     int8_t* qs = static_cast<int8_t*>(act);
     float* qd = act ? reinterpret_cast<float*>(qs + M * D) : nullptr;
-    hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(unsigned(M)), dim3(seqsum::kThreads), size_t(D) * 4, s, x, gamma, eps, y, qs, qd, int(D));
+    if (D <= seqsum::kMaxN && D % 32 == 0)
+        hipLaunchKernelGGL(rmsnorm_quant_regs_kernel, dim3(unsigned(M)), dim3(kNormThreads), 0, s, x, gamma, eps, y, qs, qd, int(D));
+    else
+        hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(unsigned(M)), dim3(seqsum::kThreads), size_t(D) * 4, s, x, gamma, eps, y, qs, qd, int(D));
 }
 
 }  // namespace hero

@@ -1488,7 +1488,10 @@ void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
         hipLaunchKernelGGL(attn_softmax_pv_kernel, pv_grid, dim3(kSpvThreads), spv_shared_bytes(), s, a);
         return;
     }
-    hipLaunchKernelGGL(attn_softmax_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(seqsum::kThreads), 0, s, a);
+    if (a.max_ctx % 4 == 0)
+        hipLaunchKernelGGL(attn_softmax_regs_kernel<256>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(attn_softmax_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(seqsum::kThreads), 0, s, a);
     if (pv_blocks <= device_cus())
         hipLaunchKernelGGL(attn_pv_kernel<14>, pv_grid, dim3(kPvThreads), pv_shared_bytes(14), s, a);
     else if (pv_blocks <= 2 * device_cus())

@@ -1216,12 +1216,17 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnPagedArgs p) {
     const int n = t1 - t0;
     const int32_t* pt = page_row(p, b);
     const uint8_t* pool = reinterpret_cast<const uint8_t*>(p.pages);
-    __shared__ __align__(16) float qs[kAttnMaxGroup][kAttnDim];
-    __shared__ __align__(16) float sc[kAttnMaxGroup][kAttnMaxSplit];
+    // shared memory sized to the group and the split (more workgroups per CU):
+    // queries [Gs][128], scores [Gs][split], the second half's sums [Gs][128]
+    extern __shared__ __align__(16) float pg_smem[];
+    float (*qs)[kAttnDim] = reinterpret_cast<float (*)[kAttnDim]>(pg_smem);
+    float* const sc0 = pg_smem + Gs * kAttnDim;
+    const int sstride = p.split;  // a multiple of 64
+    float (*part)[kAttnDim] = reinterpret_cast<float (*)[kAttnDim]>(sc0 + Gs * sstride);
+    auto sc = [&](int h) { return sc0 + h * sstride; };
     constexpr int kVw = Q8 ? kAttnDim / 4 : kAttnDim / 2;  // dwords per stored V row
     __shared__ uint32_t vt[kPgTile][kVw + 1];
     __shared__ float vsc[Q8 ? kPgTile : 1][4];
-    __shared__ float part[kAttnMaxGroup][kAttnDim];  // the second half's sums of the weighted sum
     for (int e = tid; e < Gs * kAttnDim; e += 256) qs[e / kAttnDim][e % kAttnDim] = a.q_rot[(int64_t(b) * a.Hq + int64_t(g) * Gs) * kAttnDim + e];
 
     const int r = tid >> 2, cq = (tid & 3) * 32;
@@ -1292,7 +1297,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnPagedArgs p) {
                 }
                 dot += __shfl_xor(dot, 1);
                 dot += __shfl_xor(dot, 2);
-                if ((tid & 3) == 0 && jj < n) sc[h][jj] = a.score_scale * dot;
+                if ((tid & 3) == 0 && jj < n) sc(h)[jj] = a.score_scale * dot;
             }
         }
         cur = nxt;
@@ -1303,12 +1308,12 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnPagedArgs p) {
     // weights past n are zero so the weighted sum reads whole quads
     for (int h = wv; h < Gs; h += 4) {
         float m = -INFINITY;
-        for (int jj = lane; jj < n; jj += 64) m = fmaxf(m, sc[h][jj]);
+        for (int jj = lane; jj < n; jj += 64) m = fmaxf(m, sc(h)[jj]);
         for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
         float l = 0.f;
         for (int jj = lane; jj < ntiles * kPgTile; jj += 64) {
-            const float e = jj < n ? exp_f32(sc[h][jj] - m) : 0.f;
-            sc[h][jj] = e;
+            const float e = jj < n ? exp_f32(sc(h)[jj] - m) : 0.f;
+            sc(h)[jj] = e;
             l += e;
         }
         for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
@@ -1357,7 +1362,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnPagedArgs p) {
 #pragma unroll
             for (int h = 0; h < kAttnMaxGroup; ++h) {
                 if (h < Gs) {
-                    const float4 w = *reinterpret_cast<const float4*>(&sc[h][j0 + 4 * q4i]);
+                    const float4 w = *reinterpret_cast<const float4*>(sc(h) + j0 + 4 * q4i);
                     o[h] = fmaf(w.x, v[0], o[h]);
                     o[h] = fmaf(w.y, v[1], o[h]);
                     o[h] = fmaf(w.z, v[2], o[h]);
@@ -1429,10 +1434,12 @@ int64_t attn_paged_work_floats(int B, int Hq, int nsplit) { return int64_t(B) * 
 void launch_attn_paged(const AttnPagedArgs& p, hipStream_t s) {
     const AttnDecodeArgs& a = p.a;
     hipLaunchKernelGGL(attn_paged_prep_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, p);
+    const int Gs = a.Hq / a.Hkv;
+    const size_t smem = size_t(Gs) * (2 * kAttnDim + size_t(p.split)) * 4;
     if (p.q8)
-        hipLaunchKernelGGL(attn_split_kernel<true>, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), 0, s, p);
+        hipLaunchKernelGGL(attn_split_kernel<true>, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), smem, s, p);
     else
-        hipLaunchKernelGGL(attn_split_kernel<false>, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), 0, s, p);
+        hipLaunchKernelGGL(attn_split_kernel<false>, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), smem, s, p);
     hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, p);
 }
 

@@ -588,20 +588,25 @@ namespace hero {
 // 1 x 4 at BM = 16), so at the tall tiles a wave's operand and scale reads
 // serve two or four MFMAs each (unrolling a whole chunk of 8 blocks measured
 // slower: more registers, a worse schedule). K streams through shared memory
-// 4 blocks (128 bytes) at a time, tile rows padded to 144 bytes (16 rows'
-// 8-byte operand reads hit distinct banks); against 8-block chunks this halves
-// the staging registers (117 instead of 204 VGPRs at BM = 128: four waves per
-// SIMD instead of two) for one more barrier pair per 8 blocks, 1% faster over
-// a 2048-token prefill. The next chunk's bytes and scales are loaded into registers
+// in chunks of KC blocks (gemm_kc: 4 at BM = 128, 8 below), tile rows padded
+// by 16 bytes (16 rows' 8-byte operand reads hit distinct banks); at BM = 128
+// the 4-block chunk halves the staging registers (117 instead of 204 VGPRs:
+// four waves per SIMD instead of two). The next chunk's bytes and scales are loaded into registers
 // while the current chunk is computed (raw buffer loads sized to the tile, so
 // rows, blocks and scales past the edges read zeros without a branch), then
 // stored to shared memory between two barriers.
 // ---------------------------------------------------------------------------
 typedef int v4i_t __attribute__((ext_vector_type(4)));
-constexpr int kGemmBN = 64, kGemmKC = 4, kGemmRow = kGemmKC * 32 + 16;
+constexpr int kGemmBN = 64;
+// K blocks per shared-memory chunk: 4 at the 128-row tile (half the staging
+// registers: four waves per SIMD), 8 below (fewer barriers; at BM = 64 the
+// 4-block chunk measured 20% slower)
+template <int BM>
+constexpr int gemm_kc() { return BM >= 128 ? 4 : 8; }
 
 template <int BM, int EPI>
 __global__ __launch_bounds__(256) void gemm_q8_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {
+    constexpr int kGemmKC = gemm_kc<BM>(), kGemmRow = kGemmKC * 32 + 16;
     __shared__ __align__(16) int8_t Xs[BM * kGemmRow];
     __shared__ __align__(16) int8_t Ws[kGemmBN * kGemmRow];
     __shared__ __align__(16) float dxs[kGemmKC][BM];  // [block][row]: a lane's 4 rows are one 16-byte read
@@ -620,7 +625,7 @@ __global__ __launch_bounds__(256) void gemm_q8_kernel(const int8_t* __restrict__
     constexpr int XP = (BM * PPR + 255) / 256;     // 16-byte X pieces per lane per chunk
     constexpr int WP = kGemmBN * PPR / 256;        // 16-byte W pieces per lane per chunk
     constexpr int DXP = (BM * kGemmKC + 255) / 256;
-    constexpr int DWP = kGemmKC * kGemmBN / 256;   // 1
+    constexpr int DWP = kGemmKC * kGemmBN / 256;
     // the tile's rows of X and W, their scales (n0 is a multiple of 8, so the
     // scale groups of W rows n0.. are contiguous)
     const __amdgpu_buffer_rsrc_t bx = buffer_of(xq + int64_t(m0) * K, uint32_t(mrows) * uint32_t(K));

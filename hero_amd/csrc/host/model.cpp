@@ -513,7 +513,9 @@ void Qwen35Model::State::reset() {
 
 int64_t Qwen35Model::chunk_rows(const State& st) const {
     const int64_t per_row = c_.Hq * st.max_tokens_ * 4;  // attention scores of one row
-    return std::max<int64_t>(1, std::min<int64_t>(512, (int64_t(256) << 20) / per_row));
+    // up to 1024 rows (512 MiB of scores): taller GEMM tiles over the chunk
+    // (2048-token prefill 15.2k -> 16.1k tok/s against 512-row chunks)
+    return std::max<int64_t>(1, std::min<int64_t>(1024, (int64_t(512) << 20) / per_row));
 }
 
 void Qwen35Model::State::ensure_chunk(int64_t rows) {

@@ -4,10 +4,10 @@ d_model 4096, 32 q / 8 kv heads of 128, delta-net 32 heads of 128, SwiGLU
 reference's check tool drives it (tools/qwen35_check.cpp:43-70): prefill a
 prompt, then feed each greedy id back in.
 
-The prompt is 600 tokens long: it prefills as row chunks of 512 + 88, whose
-delta-net in-projection and gate/up GEMMs take the 128-row tile (the 88-row
-chunk and the narrower matrices take 64, 32 or 16); the decode passes run the
-batch-1 hipGraph (fused RMSNorm / SwiGLU GEMV forms, the 151936-row LM head).
+The prompt is 600 tokens long: it prefills as one chunk of 600 rows, whose
+delta-net in-projection and gate/up GEMMs take the 128-row tile (the 4096-row
+out- and down-projections the 64-row tile); the decode passes run the batch-1
+hipGraph (fused RMSNorm / SwiGLU GEMV forms, the 151936-row LM head).
 The same prompt then runs as one sequence of a 16-sequence batch state, whose
 decode takes the skinny GEMMs at their real shapes.
 
@@ -91,13 +91,12 @@ def test_hybrid8b_prefill_and_greedy_decode_match_oracle(hybrid8b, manifest):
     from hero_amd._lib import lib
 
     tiles = {}
-    for m in (512, PROMPT - 512):
-        for n in (16448, 24576, 10240, 4096):  # delta-net in-proj, gate|up, attention in-proj, out-proj
-            tile = ctypes.c_int32()
-            check(lib.hero_q8_0_gemm_plan(m, n, 4096, ctypes.byref(tile)))
-            tiles[(m, n)] = tile.value
+    for n in (16448, 24576, 10240, 4096):  # delta-net in-proj, gate|up, attention in-proj, out-proj
+        tile = ctypes.c_int32()
+        check(lib.hero_q8_0_gemm_plan(PROMPT, n, 4096, ctypes.byref(tile)))
+        tiles[(PROMPT, n)] = tile.value
     say(f"[8b] prefill GEMM tiles ((rows, N): rows per tile): {tiles}")
-    assert tiles[(512, 16448)] == 128 and tiles[(512, 24576)] == 128
+    assert tiles[(PROMPT, 16448)] == 128 and tiles[(PROMPT, 24576)] == 128
     prompt = np.random.default_rng(SEED).integers(0, model.V, PROMPT).astype(np.int32)
     assert np.array_equal(prompt, golden["prompt"])
     t = time.perf_counter()

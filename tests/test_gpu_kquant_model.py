@@ -62,18 +62,18 @@ def test_kquant_model_single_steps_and_embedding_match_oracle(model, cpu, kmix_g
 
 
 def test_kquant_model_long_prefill_in_chunks_matches_oracle(kmix_gguf, cpu):
-    """600 tokens through 512-row chunks (two chunks: the second one's rows
+    """1200 tokens through 1024-row chunks (two chunks: the second one's rows
     attend to the first's cache and continue its recurrent state), then a
     decode pass"""
     m = hero_amd.Qwen35Model.open(kmix_gguf)
     try:
         rng = np.random.default_rng(11)
-        prompt = rng.integers(0, 32000, 600).astype(np.int32)
-        state = m.new_state(1024)
+        prompt = rng.integers(0, 32000, 1200).astype(np.int32)
+        state = m.new_state(2048)
         got = m.forward(state, ids=prompt).values
         cpu.reset()
         ref = cpu.forward_ids(prompt)
-        same_bits(got, ref, "600-token prefill")
+        same_bits(got, ref, "1200-token prefill")
         nxt = int(np.argmax(ref))
         same_bits(m.forward(state, ids=[nxt]).values, cpu.forward_ids([nxt]), "decode after the prefill")
     finally:

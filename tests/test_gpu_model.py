@@ -108,17 +108,17 @@ def test_decode_equals_prefill_exactly(model, tiny_golden):
 
 
 def test_long_prefill_runs_in_chunks_and_matches_oracle(model, tiny_gguf):
-    """A 700-token prompt runs as row chunks of 512 + 188 (batched GEMMs, the
+    """A 1300-token prompt runs as row chunks of 1024 + 276 (batched GEMMs, the
     delta-net and attention across the chunk boundary): its logits equal the
-    oracle's bit for bit, equal those of the same prompt fed as 1 + 350 + 349
+    oracle's bit for bit, equal those of the same prompt fed as 1 + 650 + 649
     rows, and greedy decoding continues identically from both states."""
     import oracle
 
-    ids = np.random.default_rng(7).integers(0, model.V, 700).astype(np.int32)
-    s1, s2 = model.new_state(1024), model.new_state(1024)
+    ids = np.random.default_rng(7).integers(0, model.V, 1300).astype(np.int32)
+    s1, s2 = model.new_state(2048), model.new_state(2048)
     whole = model.forward(s1, ids=ids)
     same_bits(whole.values, oracle.Model(path=tiny_gguf).forward_ids(ids))
-    for a, b in [(0, 1), (1, 351), (351, 700)]:
+    for a, b in [(0, 1), (1, 651), (651, 1300)]:
         part = model.forward(s2, ids=ids[a:b])
     assert np.array_equal(bits(whole.values), bits(part.values))
     d1, l1 = model.decode_greedy(s1, whole.argmax(), 4, want_logits=True)
@@ -350,7 +350,7 @@ def test_dh256_model_matches_reference(dh256_gguf, dh256_golden):
     base 1e7, 4 key heads over 8 value heads, untied head. Prefill logits, the
     greedy ids of 32 graph-replayed decode passes and the last logits equal the
     reference's bit for bit; the same prompt as one sequence of a batch state
-    decodes to the same ids and logits; and a 700-token prompt (two prefill
+    decodes to the same ids and logits; and a 1100-token prompt (two prefill
     chunks) matches the oracle."""
     import oracle
 
@@ -374,11 +374,11 @@ def test_dh256_model_matches_reference(dh256_gguf, dh256_golden):
         same_bits(logits[1], dh256_golden["logits_last"])
         bs.close()
 
-        prompt = np.random.default_rng(8).integers(0, m.V, 700).astype(np.int32)
+        prompt = np.random.default_rng(8).integers(0, m.V, 1100).astype(np.int32)
         ref = oracle.Model(path=dh256_gguf)
         try:
             expect = ref.forward_ids(prompt)
-            state = m.new_state(1024)
+            state = m.new_state(2048)
             lg = m.forward(state, ids=prompt)
             same_bits(lg.values, expect)
             ids, last = m.decode_greedy(state, lg.argmax(), 4, want_logits=True)

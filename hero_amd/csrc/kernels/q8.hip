@@ -1187,28 +1187,21 @@ void launch_gemm_q8(const void* packed, const void* act, float* y, const float* 
     };
     switch (gemm_q8_plan(M, N, K)) {
     case kGemmPlanSkinnyWave:
-        // tall: a wave per group range, every chain in registers; at K <= 4096
-        // the activations in shared memory, as many waves per workgroup as
-        // keep a workgroup on every CU
-        if (K <= kSklMaxK) {
-            const int64_t per = groups / device_cus();
-            const int nw = per >= 8 ? 8 : per >= 4 ? 4 : per >= 2 ? 2 : 1;
+        // tall: a wave per group range, every chain in registers; for the
+        // tallest (8 or more groups per CU, the LM head) at K <= 4096 the
+        // activations in shared memory, eight waves per workgroup (152 us
+        // instead of 205 us for 151936 x 4096; with fewer groups per CU the
+        // workgroup's activation copy costs more than it saves)
+        if (K <= kSklMaxK && groups >= 8 * device_cus()) {
             auto run = [&](auto kernel) {
-                const size_t smem = skl_shared_bytes(nw, int(K));
-                const unsigned grid = unsigned(std::max<int64_t>(1, std::min<int64_t>(grid_for(kernel, 64 * nw, smem), groups / nw)));
-                hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * nw), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
+                const size_t smem = skl_shared_bytes(8, int(K));
+                const unsigned grid = unsigned(std::max<int64_t>(1, std::min<int64_t>(grid_for(kernel, 64 * 8, smem), groups / 8)));
+                hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * 8), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
             };
-            if (epi == kEpiResidual) {
-                if (nw == 8) run(gemm_q8_skinny_lds_kernel<kEpiResidual, 8>);
-                else if (nw == 4) run(gemm_q8_skinny_lds_kernel<kEpiResidual, 4>);
-                else if (nw == 2) run(gemm_q8_skinny_lds_kernel<kEpiResidual, 2>);
-                else run(gemm_q8_skinny_lds_kernel<kEpiResidual, 1>);
-            } else {
-                if (nw == 8) run(gemm_q8_skinny_lds_kernel<kEpiStore, 8>);
-                else if (nw == 4) run(gemm_q8_skinny_lds_kernel<kEpiStore, 4>);
-                else if (nw == 2) run(gemm_q8_skinny_lds_kernel<kEpiStore, 2>);
-                else run(gemm_q8_skinny_lds_kernel<kEpiStore, 1>);
-            }
+            if (epi == kEpiResidual)
+                run(gemm_q8_skinny_lds_kernel<kEpiResidual, 8>);
+            else
+                run(gemm_q8_skinny_lds_kernel<kEpiStore, 8>);
             break;
         }
         if (epi == kEpiResidual)

@@ -117,6 +117,44 @@ def attention_share(ctx: int) -> float:
     return 8 * 32 * ctx * 128 * 2 / 7.94e9
 
 
+def qwen35_9b_leg(prompt_len: int, steps: int, warmup: int) -> dict:
+    """The same prefill and batch-1 greedy decode on synthetic Q8_0 weights of
+    the reference's own Qwen 3.5 9B configuration (nm/src/qwen35.hpp:62-88:
+    vocab 248320, untied head, 16 query / 4 K/V heads of 256 channels with a
+    quarter rotating at RoPE base 1e7, 16 delta-net key heads over 32 value
+    heads); a separate model, closed after."""
+    import torch
+
+    import hero_amd
+
+    shape = hero_amd.HybridShape(vocab=248320, d_model=4096, layers=32, ffn=12288, q_heads=16, kv_heads=4, head_dim=256,
+                                 key_heads=16, value_heads=32, rope_base=1e7)
+    ctx = ((prompt_len + steps + warmup + 8 + 255) // 256) * 256
+    image = hero_amd.synthetic_gguf_image(shape, seed=SEED + 9, ctx=ctx, tied=False)
+    m = hero_amd.Qwen35Model.open_image(image)
+    try:
+        prompt = np.random.default_rng(SEED + 9).integers(0, shape.vocab, prompt_len).astype(np.int32)
+        st = m.new_state(ctx)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        first = m.forward(st, ids=prompt).argmax()
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t
+        warm = m.decode_greedy(st, first, warmup)[0] if warmup > 0 else np.array([first], np.int32)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        m.decode_greedy(st, int(warm[-1]), steps)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t
+        st.close()
+    finally:
+        m.close()
+    out = {"model": "Qwen 3.5 9B configuration, synthetic Q8_0 weights (9.5 GB)", "prefill_tok_s": prompt_len / prefill_s,
+           "decode_tok_s": steps / wall, "ms_per_token": wall * 1e3 / steps}
+    log(f"Qwen 3.5 9B configuration: prefill {out['prefill_tok_s']:.0f} tok/s, decode {out['decode_tok_s']:.1f} tok/s")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -130,6 +168,7 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=16, help="also time greedy decode of this many sequences at once (0: skip)")
     ap.add_argument("--batch-steps", type=int, default=64)
     ap.add_argument("--no-chunked", action="store_true", help="skip the chunked delta-net prefill leg (a kernel trace then holds one exact prefill)")
+    ap.add_argument("--no-9b", action="store_true", help="skip the Qwen 3.5 9B configuration leg")
     ap.add_argument("--profile-gemvs", action="store_true",
                     help="only launch a decode step's GEMVs --gemv-reps times (+1 warm-up) and print their timing: "
                          "the program the HBM-traffic counter runs profile")
@@ -228,6 +267,8 @@ def main() -> int:
             f"{bwall * 1e3 / args.batch_steps:.2f} ms/step, {batch['tok_s']:.0f} tok/s aggregate")
         bs.close()
 
+    q9 = None if args.no_9b else qwen35_9b_leg(args.prompt, args.steps, args.warmup)
+
     traffic, traffic_source = measured_traffic()
     out = {
         "metric": "decode tok/s @bs1, Q8_0 ~8B hybrid; Q8 GEMV GB/s as % of HBM peak",
@@ -259,6 +300,7 @@ def main() -> int:
                 "parity": "tolerance only: logits up to ~0.06 abs from the exact prefill (tests/test_gpu_model.py)",
             },
             "batch_decode": batch,
+            "qwen35_9b_config": q9,
         },
         "roofline": {
             "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,

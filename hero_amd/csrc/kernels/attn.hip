@@ -947,8 +947,9 @@ constexpr int kPrThreads = 256;                    // four waves: 32 channels ea
 constexpr int kPrHeads = 4;                        // query heads per workgroup
 constexpr int kPrVQuads = kPrKeys * kAttnDim / 4;  // 16-byte pieces of a V tile: 1024
 
-template <int R>
+template <int R, int DH>
 __global__ __launch_bounds__(kPrThreads) void attn_pv_rows_kernel(AttnDecodeArgs a) {
+    constexpr int kParts = DH / kAttnDim;  // 128-channel parts of a head (one workgroup each)
     constexpr int CG = 64 / R;          // channel groups per wave
     constexpr int CPL = 32 / CG;        // channels per lane
     constexpr int NP = kPrHeads * R;    // (head, row) pairs
@@ -960,7 +961,8 @@ __global__ __launch_bounds__(kPrThreads) void attn_pv_rows_kernel(AttnDecodeArgs
     const int tid = int(threadIdx.x), wave = tid / 64, lane = tid % 64;
     const int r = lane % R, cg = lane / R;
     const int group = a.Hq / a.Hkv, nchunk = (group + kPrHeads - 1) / kPrHeads;
-    const int g = int(blockIdx.x) / nchunk, h0 = g * group + (int(blockIdx.x) % nchunk) * kPrHeads;
+    const int part = int(blockIdx.x) % kParts, gcx = int(blockIdx.x) / kParts;
+    const int g = gcx / nchunk, h0 = g * group + (gcx % nchunk) * kPrHeads;
     const int nh = min(kPrHeads, g * group + group - h0);
     const int row0 = int(blockIdx.y) * R;
     const int nrows = min(R, a.B - row0);
@@ -977,8 +979,8 @@ __global__ __launch_bounds__(kPrThreads) void attn_pv_rows_kernel(AttnDecodeArgs
     if (pos_hi < 0 || pos_hi >= a.max_ctx || pos_lo < 0) return;  // the host keeps positions in range
     const int ntiles = (pos_hi + kPrKeys) / kPrKeys;
     const int full_tiles = (pos_lo + 1) / kPrKeys;  // tiles every row of the block sees whole
-    const int64_t kw = int64_t(a.Hkv) * kAttnDim;
-    const float* vb = a.v_cache + int64_t(g) * kAttnDim;  // shared cache: sequence 0
+    const int64_t kw = int64_t(a.Hkv) * DH;
+    const float* vb = a.v_cache + int64_t(g) * DH + part * kAttnDim;  // shared cache: sequence 0; this part's channels
 
     // staging: V piece q = key q / 32, channels 4 (q % 32) ..; weight piece
     // q = key quad q / NP, pair q % NP = head * R + row; rows past the block and
@@ -1057,14 +1059,14 @@ __global__ __launch_bounds__(kPrThreads) void attn_pv_rows_kernel(AttnDecodeArgs
     }
 
     // gate, Q8_0 block of each (row, head): 32 channels over the CG lanes of the row
-    const int64_t width = int64_t(a.Hq) * kAttnDim;
+    const int64_t width = int64_t(a.Hq) * DH;
     int8_t* qs = static_cast<int8_t*>(a.act_out);
     float* qd = reinterpret_cast<float*>(qs + int64_t(a.B) * width);
-    const int ch0 = 32 * wave + CPL * cg;
+    const int ch0 = part * kAttnDim + 32 * wave + CPL * cg;
 #pragma unroll
     for (int hh = 0; hh < kPrHeads; ++hh) {
         const int h = h0 + min(hh, nh - 1);
-        const float* gate = a.proj + int64_t(my_row) * a.proj_stride + int64_t(h) * 2 * kAttnDim + kAttnDim + ch0;
+        const float* gate = a.proj + int64_t(my_row) * a.proj_stride + int64_t(h) * 2 * DH + DH + ch0;
         float out[CPL];
         float amax = 0.f;
 #pragma unroll
@@ -1077,7 +1079,7 @@ __global__ __launch_bounds__(kPrThreads) void attn_pv_rows_kernel(AttnDecodeArgs
         const float d = amax / 127.f;
         const float id = d != 0.f ? 1.f / d : 0.f;
         if (r < nrows && hh < nh) {
-            const int64_t idx = int64_t(my_row) * width + int64_t(h) * kAttnDim + ch0;
+            const int64_t idx = int64_t(my_row) * width + int64_t(h) * DH + ch0;
             if (a.out_f32)
 #pragma unroll
                 for (int i = 0; i < CPL; i += 4) *reinterpret_cast<float4*>(a.out_f32 + idx + i) = make_float4(out[i], out[i + 1], out[i + 2], out[i + 3]);
@@ -1457,6 +1459,10 @@ void attn_decode_wide(const AttnDecodeArgs& a, unsigned chunks, unsigned tiles, 
         hipLaunchKernelGGL(attn_softmax_regs_kernel<256>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(256), 0, s, a);
     else
         hipLaunchKernelGGL(attn_softmax_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(seqsum::kThreads), 0, s, a);
+    if (a.shared_cache && a.window == 0 && a.max_ctx % 4 == 0) {  // a prefill chunk: the row-block weighted sum, per 128-channel part
+        hipLaunchKernelGGL((attn_pv_rows_kernel<kPrRows, DH>), dim3(chunks * (DH / kAttnDim), unsigned((a.B + kPrRows - 1) / kPrRows)), dim3(kPrThreads), 0, s, a);
+        return;
+    }
     hipLaunchKernelGGL(attn_pv_batch_kernel<DH>, dim3(unsigned(a.Hkv * ((group + kPvbHeads - 1) / kPvbHeads) * (DH / kPvbCh)), unsigned(a.B)), dim3(kPvbThreads), 0, s,
                        a);
 }
@@ -1483,7 +1489,7 @@ void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
     // register softmax and the row-block weighted sum
     if (a.shared_cache && a.window == 0 && a.max_ctx % 4 == 0) {
         hipLaunchKernelGGL(attn_softmax_regs_kernel<256>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(256), 0, s, a);
-        hipLaunchKernelGGL(attn_pv_rows_kernel<kPrRows>, dim3(unsigned(chunks), unsigned((a.B + kPrRows - 1) / kPrRows)), dim3(kPrThreads), 0, s, a);
+        hipLaunchKernelGGL((attn_pv_rows_kernel<kPrRows, kAttnDim>), dim3(unsigned(chunks), unsigned((a.B + kPrRows - 1) / kPrRows)), dim3(kPrThreads), 0, s, a);
         return;
     }
     // the per-head pipeline while its workgroups fit the CUs (a deep ring, one

@@ -503,6 +503,7 @@ constexpr size_t spv_shared_bytes() {
 // 16-byte chunk cc (4 channels) of V row r sits at chunk r * 8 + (cc ^ spv_swz(r)) of its slot
 __device__ __forceinline__ int spv_swz(int r) { return (r >> 2) & 7; }
 
+template <int DH>
 __global__ __launch_bounds__(kSpvThreads) void attn_softmax_pv_kernel(AttnDecodeArgs a) {
     extern __shared__ __align__(16) float spv_smem[];  // [R][V tile] [3][kPvCh][kPvStride] [kSpvMaxN] seqsum red etab
     float* vring = spv_smem;
@@ -512,7 +513,7 @@ __global__ __launch_bounds__(kSpvThreads) void attn_softmax_pv_kernel(AttnDecode
     float* red = reinterpret_cast<float*>(&sm + 1);         // [8]
     uint64_t* etab = reinterpret_cast<uint64_t*>(red + 8);  // expf's table, read from shared memory
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64, b = blockIdx.y;
-    constexpr int parts = kAttnDim / kPvCh;
+    constexpr int parts = DH / kPvCh;
     const int h = int(blockIdx.x) / parts, part = int(blockIdx.x) % parts;
     const int g = h / (a.Hq / a.Hkv);
     const int pos = a.positions[b];
@@ -520,8 +521,8 @@ __global__ __launch_bounds__(kSpvThreads) void attn_softmax_pv_kernel(AttnDecode
     const int first = visible_first(pos, a.window);
     const int n = pos + 1 - first;  // <= kSpvMaxN (the host's condition for this kernel)
     const float* sc = a.scores + (int64_t(b) * a.Hq + h) * a.max_ctx;
-    const int64_t kw = int64_t(a.Hkv) * kAttnDim;
-    const float* vb = a.v_cache + (cache_of(a, b) * a.max_ctx + first) * kw + int64_t(g) * kAttnDim + part * kPvCh;
+    const int64_t kw = int64_t(a.Hkv) * DH;
+    const float* vb = a.v_cache + (cache_of(a, b) * a.max_ctx + first) * kw + int64_t(g) * DH + part * kPvCh;
     const int ntiles = (n + kPvRows - 1) / kPvRows;
     constexpr int pstride = kPvCh * kPvStride;
     const bool loader = wave >= 8 - kSpvLoaders;
@@ -684,10 +685,10 @@ __global__ __launch_bounds__(kSpvThreads) void attn_softmax_pv_kernel(AttnDecode
 
     if (chain) {
         const int ch = part * kPvCh + lane;
-        const float gate = a.proj[int64_t(b) * a.proj_stride + int64_t(h) * 2 * kAttnDim + kAttnDim + ch];
+        const float gate = a.proj[int64_t(b) * a.proj_stride + int64_t(h) * 2 * DH + DH + ch];
         const float out = acc * sigmoid_f32(gate);
-        const int64_t width = int64_t(a.Hq) * kAttnDim;
-        const int64_t idx = int64_t(h) * kAttnDim + ch;
+        const int64_t width = int64_t(a.Hq) * DH;
+        const int64_t idx = int64_t(h) * DH + ch;
         if (a.out_f32) a.out_f32[int64_t(b) * width + idx] = out;
         float amax = fabsf(out);
         for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
@@ -1455,6 +1456,13 @@ void attn_decode_wide(const AttnDecodeArgs& a, unsigned chunks, unsigned tiles, 
     const int group = a.Hq / a.Hkv;
     hipLaunchKernelGGL(attn_prep_kernel<DH>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(DH), 0, s, a);
     hipLaunchKernelGGL(attn_scores_kernel<DH>, dim3(chunks, tiles, unsigned(a.B)), dim3(256), 0, s, a);
+    // few sequences: the per-head pipeline (softmax and weighted sum in one
+    // kernel, a workgroup per head and 32 channels) while it fits the CUs
+    const int64_t vis = a.window > 0 ? std::min<int64_t>(a.max_ctx, a.window) : a.max_ctx;
+    if (!a.shared_cache && int64_t(a.B) * a.Hq * (DH / kPvCh) <= device_cus() && vis <= kSpvMaxN && a.max_ctx % 4 == 0) {
+        hipLaunchKernelGGL(attn_softmax_pv_kernel<DH>, dim3(unsigned(a.Hq * (DH / kPvCh)), unsigned(a.B)), dim3(kSpvThreads), spv_shared_bytes(), s, a);
+        return;
+    }
     if (a.max_ctx % 4 == 0)
         hipLaunchKernelGGL(attn_softmax_regs_kernel<256>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(256), 0, s, a);
     else
@@ -1498,7 +1506,7 @@ void launch_attn_decode(const AttnDecodeArgs& a, hipStream_t s) {
     const int64_t pv_blocks = int64_t(a.B) * a.Hq * (kAttnDim / kPvCh);
     const dim3 pv_grid(unsigned(a.Hq * (kAttnDim / kPvCh)), unsigned(a.B));
     if (pv_blocks <= device_cus() && vis <= kSpvMaxN && a.max_ctx % 4 == 0) {
-        hipLaunchKernelGGL(attn_softmax_pv_kernel, pv_grid, dim3(kSpvThreads), spv_shared_bytes(), s, a);
+        hipLaunchKernelGGL(attn_softmax_pv_kernel<kAttnDim>, pv_grid, dim3(kSpvThreads), spv_shared_bytes(), s, a);
         return;
     }
     if (a.max_ctx % 4 == 0)

@@ -1,15 +1,21 @@
-// attn.hip -- gated GQA attention decode over an fp32 K/V cache, one token
-// per sequence (nm/src/qwen35.hpp:343-395; with window > 0 the sliding-window
-// visibility of nm/src/attention.hpp:159-176).
+// attn.hip -- gated GQA attention over an fp32 K/V cache: decode, one token
+// per sequence, and prefill chunks, many tokens of one sequence
+// (nm/src/qwen35.hpp:343-395; with window > 0 the sliding-window visibility of
+// nm/src/attention.hpp:159-176); and over a paged fp16 / Q8_0 cache (split-K,
+// at the end of the file). Heads of 128 channels, and of 256 (the reference's
+// Qwen 3.5 4B / 9B) through the kernels templated on the head width.
 //
-// Four kernels, each keeping the reference's fp32 operation order:
+// Four stages, each keeping the reference's fp32 operation order (the fused
+// and tiled forms further down -- score tiles with the prep folded in, the
+// softmax and weighted sum in one kernel, the register softmax, the row-block
+// weighted sum of prefill -- compute the same values):
 //  1. prep    one workgroup per (sequence, query head), a lane per channel:
 //             split of the packed [q | gate] pair, q RMSNorm + RoPE; the first
 //             query head of each K/V group also normalises and rotates k and
 //             appends k and v to the cache.
 //  2. scores  a lane per visible key and KV head: s_j = scale * dot(q, k_j)
 //             for each query head of the group, every dot a sequential
-//             128-term sum (nm/src/core.hpp:496-500). K is cached channel-major
+//             Dh-term sum (nm/src/core.hpp:496-500). K is cached channel-major
 //             per head, [Dh][max_ctx], so lanes reading consecutive keys read
 //             consecutive addresses.
 //  3. softmax one workgroup per (sequence, query head): max, e_j = exp(s_j -

@@ -721,7 +721,7 @@ constexpr int kPvbHeads = 4;                                  // query heads per
 constexpr int kPvbTile = 128;                                // rows per tile
 constexpr int kPvbVec = kPvbTile * kPvbCh / 4 / kPvbThreads;    // float4 per lane per tile
 constexpr int kPvbAlpha = kPvbHeads * kPvbTile / kPvbThreads;   // weights per lane per tile
-constexpr int kPvbRing = 4;                                  // tiles in flight
+constexpr int kPvbRing = 2;                                  // tiles in flight (4 and 6 measured no faster)
 constexpr int kPvbLd = kPvbTile + 4;                         // channel stride in a tile (16-byte rows, 2-way stores)
 
 template <int DH>

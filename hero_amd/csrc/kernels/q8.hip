@@ -761,11 +761,15 @@ __global__ __launch_bounds__(256) void gemm_q8_kernel(const int8_t* __restrict__
 // m = 4q + r of column n) into terms float(sumi) * (d_w * d_x) in shared
 // memory; after a barrier lane p = 16 m + n adds the round's terms to its
 // chain in block order (the reference's order), and after the last round
-// stores y. A ring of kSkRing rounds of loads stays in flight.
+// stores y. The terms alternate between two halves of shared memory, so the
+// next round's MFMAs run while the chains read this one (one barrier a
+// round), and each lane issues the next round's loads as soon as it has
+// consumed this round's: deeper rings (2, 3, 4 rounds in flight) measured
+// slower at batch 16.
 // ---------------------------------------------------------------------------
 constexpr int kSkRound = 32;                   // blocks per round
 constexpr int kSkMaxK = 16384;
-constexpr int kSkRing = 3;                     // steps (group, round) in flight per lane
+constexpr int kSkRing = 1;                     // steps (group, round) in flight per lane
 // Every global access of the skinny kernel is a raw buffer access (kOOB),
 // so invalid rows, blocks and padded steps need no branch.
 
@@ -781,7 +785,9 @@ __device__ __forceinline__ long hi64(v4b_t v) { return long((uint64_t(uint32_t(v
 
 template <int EPI, int NW>
 __global__ __launch_bounds__(64 * NW) void gemm_q8_skinny_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {
-    __shared__ __align__(16) float terms[kSkRound][256];   // [block of the round][16 m + n]
+    // [step parity][block of the round][16 m + n]: step s writes half s % 2 while the
+    // chains may still read the other half, so a step needs one barrier
+    __shared__ __align__(16) float terms2[2][kSkRound][256];
     extern __shared__ __align__(16) float dxs_raw[];        // [block][m] activation scales, 0 for m >= M
     float (*dxs)[16] = reinterpret_cast<float (*)[16]>(dxs_raw);
     constexpr int kSkWaveBlocks = kSkRound / NW;  // blocks per wave per round
@@ -837,6 +843,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_q8_skinny_kernel(const int8_t* _
             const int s = s0 + k;
             const int g = g_begin + s / rounds, r = s % rounds;
             const int b0 = r * kSkRound + wv * kSkWaveBlocks;
+            float (*terms)[256] = terms2[s & 1];
             if (b0 < nb) {
                 const bool first = q < 2;  // lane groups 0, 1 hold block b; 2, 3 hold block b+1
 #pragma unroll
@@ -886,7 +893,6 @@ __global__ __launch_bounds__(64 * NW) void gemm_q8_skinny_kernel(const int8_t* _
                     y[o] = acc;
             }
             acc = last ? 0.f : acc;
-            __syncthreads();
         }
     }
 }
@@ -908,7 +914,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_q8_skinny_kernel(const int8_t* _
 constexpr int kSkwRound = 8;                    // blocks per round
 constexpr int kSkwPairs = kSkwRound / 2;         // 16-byte weight (and activation) loads per lane per round
 constexpr int kSkwMaxK = 16384;
-constexpr int kSkwRing = 3;                     // rounds in flight per wave
+constexpr int kSkwRing = 4;                     // rounds in flight per wave
 // Every global access of the skinny kernel is a raw buffer access (kOOB),
 // so invalid rows, blocks and padded steps need no branch.
 

@@ -193,9 +193,10 @@ def test_gemm_matches_oracle_bitwise(lib, m, n, k):
     assert np.array_equal(bits(host(y, np.float32, (m, n))), bits(r + expect))
 
 
-# scales in fp16's subnormal range (and rows whose scale rounds to 0): the
-# GEMM forms d_x * d_w on the fp16 MFMA, which must take subnormal inputs as
-# they are; (512, 8192) selects the 128-row tile, (70, 4100) a smaller one
+# scales in fp16's subnormal range (and rows whose scale rounds to 0): every
+# GEMM form must turn them into fp32 and form d_x * d_w with no flush to zero;
+# (512, 8192) selects the 128-row tile, (70, 4100) a smaller one, (9, 4100)
+# the skinny form
 @pytest.mark.parametrize("m,n,k", [(512, 8192, 1024), (70, 4100, 2048), (9, 4100, 1024)])
 def test_gemm_subnormal_scales_match_oracle_bitwise(lib, m, n, k):
     rng = np.random.default_rng(m + n + k + 5)

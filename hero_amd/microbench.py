@@ -249,31 +249,30 @@ def bench_kquant(lib, replays: int = 20, batches=KQUANT_BATCHES):
 HBM_READ_SIZES_MB = (18, 54, 107, 622, 2048)
 
 
-def bench_hbm(lib, reps: int = 5):
+def bench_hbm(lib, replays: int = 20):
     """hero_read_probe: contiguous shares, 16-byte loads, 8 in flight per lane.
-    Each size reads a fresh region of a 4 GiB buffer per repetition (cold for
-    the 256 MB MALL); best of `reps`, timed with HIP events."""
+    Timed like the kernels (hipGraph replays, so each launch includes the
+    graph's inter-kernel gap): a replay reads up to 32 distinct regions of a
+    4 GiB buffer back to back, more bytes than the 256 MB MALL holds, so every
+    launch reads cold data."""
     from ._lib import check
 
     t = _torch()
-    buf = t.empty(4 << 30, dtype=t.uint8, device="cuda").fill_(1)
+    total = 4 << 30
+    buf = t.empty(total, dtype=t.uint8, device="cuda").fill_(1)
     out = t.zeros(4, dtype=t.int32, device="cuda")
     rows = []
     for mb in HBM_READ_SIZES_MB:
         nbytes = mb << 20
+        copies = max(1, min(32, total // nbytes - 1))
         for wg in (512, 2048, 8192):
-            best = 1e9
-            for r in range(reps + 1):
-                off = ((r * nbytes) % ((4 << 30) - nbytes)) // 256 * 256
-                e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
-                e0.record()
-                check(lib.hero_read_probe(buf.data_ptr() + off, nbytes, wg, _p(out), _stream()))
-                e1.record()
-                e1.synchronize()
-                if r:  # the first launch warms the code path
-                    best = min(best, e0.elapsed_time(e1) * 1e-3)
-            rows.append({"suite": "hbm", "kernel": "read_probe", "MB": mb, "workgroups": wg, "us": best * 1e6,
-                         "GB/s": nbytes / best / 1e9, "hbm_frac": nbytes / best / 1e9 / HBM_PEAK_GBS})
+            def body():
+                for c in range(copies):
+                    check(lib.hero_read_probe(buf.data_ptr() + c * nbytes, nbytes, wg, _p(out), _stream()))
+
+            sec = _time_graph(body, copies, replays)
+            rows.append({"suite": "hbm", "kernel": "read_probe", "MB": mb, "workgroups": wg, "copies": copies, "us": sec * 1e6,
+                         "GB/s": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS})
             print(json.dumps(rows[-1]), flush=True)
     del buf
     t.cuda.empty_cache()

@@ -322,6 +322,7 @@ HYBRID_8B_CONFIG = HybridShape(vocab=151936, d_model=4096, layers=32, ffn=12288,
 # weight_mix values of the synthetic writer
 WEIGHTS_Q8_0 = 0  # every 2-D weight Q8_0
 WEIGHTS_K_MIX = 1  # the tensor types of a Q4_K_M checkpoint: Q4_K, Q5_K, Q6_K and Q8_0
+WEIGHTS_Q8_FFN_MIX = 2  # Q8_0 in-projections, gate and up; Q6_K embedding and down; Q4_K output projections
 
 
 def synth_config(shape: HybridShape, seed: int, ctx: int = 4096, tied: bool = True, weight_mix: int = WEIGHTS_Q8_0) -> SynthConfig:

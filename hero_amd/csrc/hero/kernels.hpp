@@ -92,6 +92,8 @@ void launch_argmax(const float* logits, int64_t M, int64_t n, int32_t* out_index
 // the same with the keys in a static device array (no allocation); M <= 64
 constexpr int kArgmaxGroups = 128, kArgmaxNoallocRows = 64;
 void launch_argmax_noalloc(const float* logits, int64_t M, int64_t n, int32_t* out_index, hipStream_t s);
+// the current device's address of hero_argmax_noalloc's static key array (looked up once per device)
+uint64_t* argmax_noalloc_scratch();
 
 // a plain read of `bytes` (a multiple of 16) by `workgroups` workgroups of
 // 256 lanes (measurement: the read bandwidth ceiling)

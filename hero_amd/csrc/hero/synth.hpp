@@ -13,7 +13,7 @@ struct SynthConfig {
     double rope_base = 1e6;
     bool tied = true;
     uint64_t seed = 1;
-    uint32_t weight_mix = 0;  // 0: Q8_0 2-D weights; 1: a Q4_K_M-style mix of Q4_K, Q5_K, Q6_K and Q8_0
+    uint32_t weight_mix = 0;  // 0: Q8_0 2-D weights; 1: a Q4_K_M-style mix of Q4_K, Q5_K, Q6_K and Q8_0; 2: Q8_0 projections with K-quant embedding, down and output projections
 };
 
 uint64_t synth_qwen35_size(const SynthConfig& c);

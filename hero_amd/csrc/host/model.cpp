@@ -259,6 +259,7 @@ void Qwen35Model::load(const GgufFile& g) {
     c.tied = g.find("output.weight") == nullptr;
 
     hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "stream");
+    (void)argmax_noalloc_scratch();  // resolve the static key array's address outside any capture
     hip_check(hipEventCreate(&ev_start_), "event");
     hip_check(hipEventCreate(&ev_stop_), "event");
 
@@ -613,6 +614,7 @@ void Qwen35Model::attention(State& st, size_t layer, AttnDecodeArgs a, const int
 // linears sharing an input quantize it once (new_input() forgets)
 struct Qwen35Model::TypedScratch {
     int64_t rows = 0;
+    int64_t qtmp_floats = 0;
     DeviceBuffer xn, mix, ff, kact, qact, qtmp, act_mix;
     const float* k_for = nullptr;
     const float* q_for = nullptr;
@@ -621,9 +623,14 @@ struct Qwen35Model::TypedScratch {
     TypedScratch(const Qwen35Model& m, int64_t n) : rows(n) {
         const ModelConfig& c = m.c_;
         const int64_t kmax = std::max({c.D, c.FF, c.q_width(), c.v_width()});
+        // every linear whose output is strided (ldy != N) goes through qtmp:
+        // the input projections (ldy = n_in) and gate / up (ldy = 2 FF)
         int64_t nmax = 0;
-        for (const LayerWeights& L : m.layers_)
+        for (const LayerWeights& L : m.layers_) {
             for (const TypedLinear& t : L.tin) nmax = std::max(nmax, t.N);
+            nmax = std::max({nmax, L.tgate.N, L.tup.N});
+        }
+        qtmp_floats = n * nmax;
         xn = DeviceBuffer(size_t(n * c.D) * 4);
         mix = DeviceBuffer(size_t(n * std::max(c.q_width(), c.v_width())) * 4);
         ff = DeviceBuffer(size_t(n * c.FF) * 4);
@@ -663,6 +670,7 @@ void Qwen35Model::typed_linear(const TypedLinear& w, const float* x, int64_t M, 
         return;
     }
     if (resid) throw Error(HERO_EINVAL, "typed_linear: a strided Q8_0 output takes no residual");
+    if (M * N > ts.qtmp_floats) throw Error(HERO_EINVAL, "typed_linear: a strided Q8_0 output larger than its scratch");
     float* tmp = ts.qtmp.get<float>();
     if (M == 1)
         launch_gemv_q8(w.w.get(), ts.qact.get(), tmp, nullptr, N, K, kEpiStore, s);

@@ -243,14 +243,16 @@ std::vector<TensorSpec> tensor_specs(const SynthConfig& c) {
     std::vector<TensorSpec> t;
     // weight_mix 1: the tensor types of a Q4_K_M checkpoint (Q4_K for most
     // projections, Q5_K and Q6_K for some, Q8_0 for the small gate
-    // projections); 0: Q8_0 everywhere
-    auto mat = [&](const std::string& name, uint64_t in, uint64_t out, uint32_t mixed_type = T_Q8_0) {
+    // projections); 2: Q8_0 projections (the in-projections, gate and up)
+    // beside a Q6_K embedding, a Q6_K down projection and Q4_K output
+    // projections; 0: Q8_0 everywhere
+    auto mat = [&](const std::string& name, uint64_t in, uint64_t out, uint32_t mix1_type = T_Q8_0, uint32_t mix2_type = T_Q8_0) {
         TensorSpec s;
         s.name = name;
         s.in = in;
         s.out = out;
         s.matrix = true;
-        s.type = c.weight_mix == 1 ? mixed_type : T_Q8_0;
+        s.type = c.weight_mix == 1 ? mix1_type : c.weight_mix == 2 ? mix2_type : T_Q8_0;
         t.push_back(s);
     };
     auto vec = [&](const std::string& name, uint64_t n, TensorSpec::Kind kind, double scale = 0.0) {
@@ -262,7 +264,7 @@ std::vector<TensorSpec> tensor_specs(const SynthConfig& c) {
         t.push_back(s);
     };
     const uint64_t D = c.D, CC = 2 * c.Hk * c.Dk + c.Hv * c.Dv;
-    mat("token_embd.weight", D, c.V, T_Q6_K);
+    mat("token_embd.weight", D, c.V, T_Q6_K, T_Q6_K);
     vec("output_norm.weight", D, TensorSpec::Ones);
     if (!c.tied) mat("output.weight", D, c.V, T_Q6_K);
     for (uint64_t l = 0; l < c.L; ++l) {
@@ -271,7 +273,7 @@ std::vector<TensorSpec> tensor_specs(const SynthConfig& c) {
         vec(b + "post_attention_norm.weight", D, TensorSpec::Ones);
         mat(b + "ffn_gate.weight", D, c.FF, T_Q4_K);
         mat(b + "ffn_up.weight", D, c.FF, T_Q4_K);
-        mat(b + "ffn_down.weight", c.FF, D, T_Q6_K);
+        mat(b + "ffn_down.weight", c.FF, D, T_Q6_K, T_Q6_K);
         if ((l + 1) % 4 != 0) {
             mat(b + "attn_qkv.weight", D, CC, T_Q5_K);
             mat(b + "attn_gate.weight", D, c.Hv * c.Dv, T_Q4_K);
@@ -288,14 +290,14 @@ std::vector<TensorSpec> tensor_specs(const SynthConfig& c) {
             mat(b + "ssm_alpha.weight", D, c.Hv);
             vec(b + "ssm_dt.bias", c.Hv, TensorSpec::Zeros);
             vec(b + "ssm_norm.weight", c.Dv, TensorSpec::Ones);
-            mat(b + "ssm_out.weight", c.Hv * c.Dv, D, T_Q4_K);
+            mat(b + "ssm_out.weight", c.Hv * c.Dv, D, T_Q4_K, T_Q4_K);
         } else {
             mat(b + "attn_q.weight", D, 2 * c.Hq * c.head_dim, T_Q4_K);
             vec(b + "attn_q_norm.weight", c.head_dim, TensorSpec::Ones);
             mat(b + "attn_k.weight", D, c.Hkv * c.head_dim, T_Q4_K);
             vec(b + "attn_k_norm.weight", c.head_dim, TensorSpec::Ones);
             mat(b + "attn_v.weight", D, c.Hkv * c.head_dim, T_Q6_K);
-            mat(b + "attn_output.weight", c.Hq * c.head_dim, D, T_Q5_K);
+            mat(b + "attn_output.weight", c.Hq * c.head_dim, D, T_Q5_K, T_Q4_K);
         }
     }
     return t;
@@ -407,8 +409,8 @@ void fill_tensor(const SynthConfig& c, const TensorSpec& s, uint64_t tensor_inde
 void check_config(const SynthConfig& c) {
     if (c.L == 0 || c.L % 4 != 0) throw std::invalid_argument("synth: L must be a positive multiple of 4");
     if (c.D % 32 || c.FF % 32 || (c.Hv * c.Dv) % 32 || (c.Hq * c.head_dim) % 32) throw std::invalid_argument("synth: every Q8_0 input width must be a multiple of 32");
-    if (c.weight_mix > 1) throw std::invalid_argument("synth: weight_mix must be 0 (Q8_0) or 1 (K-quant mix)");
-    if (c.weight_mix == 1 && (c.D % 256 || c.FF % 256 || (c.Hv * c.Dv) % 256 || (c.Hq * c.head_dim) % 256))
+    if (c.weight_mix > 2) throw std::invalid_argument("synth: weight_mix must be 0 (Q8_0), 1 (K-quant mix) or 2 (Q8_0 projections with K-quant down and output projections)");
+    if (c.weight_mix >= 1 && (c.D % 256 || c.FF % 256 || (c.Hv * c.Dv) % 256 || (c.Hq * c.head_dim) % 256))
         throw std::invalid_argument("synth: K-quant input widths must be multiples of 256");
     if (c.Hkv == 0 || c.Hq % c.Hkv || c.Hk == 0 || c.Hv % c.Hk || c.Dk != c.Dv || c.head_dim % 8) throw std::invalid_argument("synth: inconsistent head shapes");
 }

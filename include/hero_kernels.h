@@ -129,7 +129,10 @@ int hero_argmax(const float* logits, int64_t m, int64_t n, int32_t* out, uint64_
  * callers that cannot allocate device memory (code under HIP graph capture,
  * serving loops that forbid hipMalloc). m <= 64, else HERO_EINVAL. Every call
  * on one GPU shares the array: calls that overlap on one GPU (on two streams
- * at once) race. Results equal hero_argmax's. */
+ * at once) race. Results equal hero_argmax's. The array's device address is
+ * looked up once per device, with the current device, on the first call or
+ * when a model is opened on that device: make that first call (or open a
+ * model) outside graph capture, and pass a stream of the current device. */
 int hero_argmax_noalloc(const float* logits, int64_t m, int64_t n, int32_t* out, void* stream);
 
 /* ---- K-quant weights (GGUF Q4_K = 12, Q5_K = 13, Q6_K = 14) ----------------

@@ -88,11 +88,13 @@ int hero_batch_state_create(const hero_model* model, int64_t max_tokens, int32_t
  * to fp32 rounding order instead of bit for bit). */
 #define HERO_STATE_GDN_CHUNKED 2u
 /* flags: keep the attention cache as Q8_0 pages (int8 rows with an fp16 scale
- * per 32, 1.0625 bytes per value) with split-K attention: the K/V storage of
- * the reference's plan (nm/INFERENCE_PLAN.md:235-236), each appended row
- * quantized by its activation quantizer (quant_i8.hpp:70-80) and read back as
- * d * q (quant.hpp:306-313). Results equal the oracle's Q8_0-cache switch to a
- * few ulp (the split-K sums). Exclusive with HERO_STATE_KV_FP16. */
+ * per 32, 1.0625 bytes per value) with split-K attention. The reference has
+ * no such cache, only a plan line for one (nm/INFERENCE_PLAN.md:235-236); here
+ * each appended row is quantized by the reference's activation quantizer
+ * (quant_i8.hpp:70-80) and read back as d * q (quant.hpp:306-313). Results
+ * are checked against the oracle's own Q8_0-cache switch (equal to a few ulp:
+ * the split-K sums), not against reference outputs: parity with the
+ * reference is unpinned for this format. Exclusive with HERO_STATE_KV_FP16. */
 #define HERO_STATE_KV_Q8_0 4u
 int64_t hero_state_batch(const hero_state* state);
 int64_t hero_state_seq_tokens(const hero_state* state, int32_t seq);
@@ -131,8 +133,10 @@ typedef struct hero_synth_config {
 /* Seeded random-init qwen35 GGUF, N(0,0.02) weights before quantization.
  * weight_mix 0: every 2-D weight Q8_0; 1: the tensor types of a Q4_K_M
  * checkpoint (Q6_K embedding, LM head, ffn_down and attn_v; Q5_K attn_qkv and
- * attn_output; Q4_K the other projections; Q8_0 ssm_alpha/ssm_beta), every
- * input width a multiple of 256. size -> bytes of the image; image -> fill a
+ * attn_output; Q4_K the other projections; Q8_0 ssm_alpha/ssm_beta); 2: Q8_0
+ * in-projections, gate and up beside a Q6_K embedding and ffn_down and Q4_K
+ * ssm_out / attn_output. Mixes 1 and 2 need every K-quant input width a
+ * multiple of 256. size -> bytes of the image; image -> fill a
  * caller buffer; file -> write to a path. */
 int64_t hero_synth_qwen35_size(const hero_synth_config* config);
 int hero_synth_qwen35_image(const hero_synth_config* config, void* image, size_t capacity);

@@ -92,6 +92,19 @@ struct TinyDh256Config {
     using OutputWeight = Weight<D, V>;
     static constexpr bool is_recurrent(size_t layer) { return (layer + 1) % FULL_ATTENTION_INTERVAL != 0; }
 };
+// the tiny shape with a SwiGLU width (3584) above every input projection's
+// width (3072), the model of the Q8_0-gate/up mix beside K-quant tensors
+struct TinyFf3584Config {
+    static constexpr size_t V = 32000, D = 1024, L = 4, CTX = 4096;
+    static constexpr size_t Hq = 8, Hkv = 2, HEAD_DIM = 128;
+    static constexpr size_t ROPE_BASE = 1000000, ROTARY_NUM = 1, ROTARY_DEN = 4;
+    static constexpr size_t KEY_HEAD_DIM = 128, VALUE_HEAD_DIM = 128, KEY_HEADS = 8, VALUE_HEADS = 8, CONV_WIDTH = 4;
+    static constexpr size_t FF = 3584;
+    static constexpr Scalar RMS_EPS = 1e-6f;
+    static constexpr size_t FULL_ATTENTION_INTERVAL = 4;
+    using OutputWeight = std::monostate;
+    static constexpr bool is_recurrent(size_t layer) { return (layer + 1) % FULL_ATTENTION_INTERVAL != 0; }
+};
 struct Hybrid8BConfig {
     static constexpr size_t V = 151936, D = 4096, L = 32, CTX = 65536;
     static constexpr size_t Hq = 32, Hkv = 8, HEAD_DIM = 128;
@@ -421,6 +434,7 @@ int main(int argc, char** argv) {
             if (std::strcmp(argv[2], "tiny") == 0) return run_model<TinyConfig>(argv[3], argv[4], steps, argv[6]);
             if (std::strcmp(argv[2], "tiny_hk4u") == 0) return run_model<TinyHk4UntiedConfig>(argv[3], argv[4], steps, argv[6]);
             if (std::strcmp(argv[2], "tiny_dh256") == 0) return run_model<TinyDh256Config>(argv[3], argv[4], steps, argv[6]);
+            if (std::strcmp(argv[2], "tiny_ff3584") == 0) return run_model<TinyFf3584Config>(argv[3], argv[4], steps, argv[6]);
             if (std::strcmp(argv[2], "8b") == 0) return run_model<Hybrid8BConfig>(argv[3], argv[4], steps, argv[6]);
         }
         std::fprintf(stderr, "usage: %s kernels DIR | window DIR | model {tiny|tiny_hk4u|tiny_dh256|8b} GGUF PROMPT STEPS OUTDIR\n", argv[0]);

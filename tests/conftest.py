@@ -138,3 +138,25 @@ def kmix_gguf(tmp_path_factory, manifest):
 @pytest.fixture(scope="session")
 def kmix_golden():
     return dict(np.load(os.path.join(GOLDEN, "tiny_kmix_model.npz")))
+
+
+# the tiny shape with SwiGLU width 3584 (above every input projection's width)
+# and Q8_0 in-projections, gate and up beside a Q6_K embedding and down
+# projection and Q4_K output projections (the golden's model): every Q8_0
+# linear here writes a strided output through the typed path's scratch
+@pytest.fixture(scope="session")
+def q8ffn_gguf(tmp_path_factory, manifest):
+    import hero_amd
+
+    t = manifest["tiny_q8ffn_model"]
+    path = str(tmp_path_factory.mktemp("q8ffn") / "tiny_q8ffn.gguf")
+    hero_amd.write_synthetic_gguf(path, hero_amd.HybridShape(**t["shape"]), seed=t["seed"], ctx=t["ctx"], tied=t["tied"],
+                                  weight_mix=t["weight_mix"])
+    with open(path, "rb") as f:
+        assert hashlib.sha256(f.read()).hexdigest() == t["gguf_sha256"], "synthetic Q8_0-FFN mix model bytes changed"
+    return path
+
+
+@pytest.fixture(scope="session")
+def q8ffn_golden():
+    return dict(np.load(os.path.join(GOLDEN, "tiny_q8ffn_model.npz")))

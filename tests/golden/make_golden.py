@@ -20,6 +20,10 @@ so it runs in the build container only). This script:
   6. `hybrid8b`: the ~8B shape (the benchmark's model, seed 20260101, a
      600-token prompt, 32 greedy passes) -> hybrid8b_model.npz with the ids,
      per-step top-5 and the sha256 of the prefill and last logit vectors;
+  8. `q8ffn`: the tiny shape with SwiGLU width 3584 (above every input
+     projection's width) and Q8_0 in-projections, gate and up beside a Q6_K
+     embedding and down projection and Q4_K output projections ->
+     tiny_q8ffn_model.npz;
   7. `dh256`: the attention geometry of the reference's Qwen 3.5 4B / 9B
      configs (256-wide heads, a quarter rotating, RoPE base 1e7, Hk 4 over
      Hv 8, untied head) at tiny width -> tiny_dh256_model.npz.
@@ -27,7 +31,7 @@ so it runs in the build container only). This script:
 manifest.json records seeds, shapes, the GGUF's sha256 and the compiler
 flags (-O3 -march=x86-64-v3 -ffp-contract=off: no FMA contraction).
 
-Run:  python tests/golden/make_golden.py [kernels] [tiny] [window] [variant] [kmix] [hybrid8b] [dh256]
+Run:  python tests/golden/make_golden.py [kernels] [tiny] [window] [variant] [kmix] [hybrid8b] [dh256] [q8ffn]
       (no argument: all parts; the manifest keeps the entries of parts not rerun)
 """
 from __future__ import annotations
@@ -298,6 +302,28 @@ def make_kmix(tmp: str) -> dict:
                      "other projections Q4_K"}
 
 
+Q8FFN_SEED = 3584
+Q8FFN_SHAPE = dict(vocab=32000, d_model=1024, layers=4, ffn=3584, q_heads=8, kv_heads=2, head_dim=128, key_heads=8,
+                   value_heads=8)
+
+
+def make_q8ffn(tmp: str) -> dict:
+    import hero_amd
+
+    shape = hero_amd.HybridShape(**Q8FFN_SHAPE)
+    prompt = np.random.default_rng(Q8FFN_SEED + 1).integers(0, 32000, 20).astype(np.int32)
+    rd, sha, size, times = run_model_case(tmp, "tiny_ff3584", shape, Q8FFN_SEED, 4096, True, prompt, 32, tmp,
+                                          weight_mix=hero_amd.WEIGHTS_Q8_FFN_MIX)
+    np.savez_compressed(
+        os.path.join(HERE, "tiny_q8ffn_model.npz"), prompt=prompt, ids=rd("ids.i32", np.int32),
+        top5_ids=rd("top5_ids.i32", np.int32).reshape(-1, 5), top5_logits=rd("top5_logits.f32", np.float32).reshape(-1, 5),
+        logits_prefill=rd("logits_prefill.f32", np.float32), logits_last=rd("logits_last.f32", np.float32))
+    return {"seed": Q8FFN_SEED, "shape": Q8FFN_SHAPE, "weight_mix": hero_amd.WEIGHTS_Q8_FFN_MIX, "tied": True,
+            "ctx": 4096, "prompt_len": 20, "decode_steps": 32, "gguf_sha256": sha, "gguf_bytes": size,
+            "reference_times": times,
+            "types": "token_embd, ffn_down Q6_K; ssm_out, attn_output Q4_K; in-projections, ffn_gate, ffn_up Q8_0"}
+
+
 def make_hybrid8b(tmp: str) -> dict:
     import hero_amd
 
@@ -316,9 +342,10 @@ def make_hybrid8b(tmp: str) -> dict:
 
 
 PARTS = {"kernels": make_kernels, "tiny": make_tiny, "window": make_window, "variant": make_variant, "kmix": make_kmix,
-         "hybrid8b": make_hybrid8b, "dh256": make_dh256}
+         "hybrid8b": make_hybrid8b, "dh256": make_dh256, "q8ffn": make_q8ffn}
 MANIFEST_KEYS = {"kernels": "kernels", "tiny": "tiny_model", "window": "window", "variant": "tiny_hk4u_model",
-                 "kmix": "tiny_kmix_model", "hybrid8b": "hybrid8b_model", "dh256": "tiny_dh256_model"}
+                 "kmix": "tiny_kmix_model", "hybrid8b": "hybrid8b_model", "dh256": "tiny_dh256_model",
+                 "q8ffn": "tiny_q8ffn_model"}
 
 
 def main():

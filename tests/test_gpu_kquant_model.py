@@ -97,3 +97,27 @@ def test_kquant_model_batch_decode_matches_single_sequences(model, cpu):
         ids, _ = cpu.greedy(p, steps)[:2]
         assert ids[0] == firsts[i]
         assert np.array_equal(out[:, i], ids[1:]), (i, out[:, i], ids[1:])
+
+
+def test_q8_ffn_mix_model_matches_reference(q8ffn_gguf, q8ffn_golden):
+    """SwiGLU width 3584, wider than every input projection, with Q8_0 gate and
+    up (strided outputs through the typed path's scratch) beside K-quant
+    tensors: the 20-token prefill, 32 decode passes and a 3-sequence batch
+    step equal the reference's golden bit for bit"""
+    m = hero_amd.Qwen35Model.open(q8ffn_gguf)
+    try:
+        state = m.new_state(256)
+        lg = m.forward(state, ids=q8ffn_golden["prompt"])
+        same_bits(lg.values, q8ffn_golden["logits_prefill"], "prefill")
+        ids, last = m.decode_greedy(state, lg.argmax(), len(q8ffn_golden["ids"]) - 1, want_logits=True)
+        assert np.array_equal(np.array([lg.argmax()] + [int(i) for i in ids], np.int32), q8ffn_golden["ids"])
+        same_bits(last.values, q8ffn_golden["logits_last"], "last pass")
+        bs = m.new_batch_state(64, 3)
+        firsts = [m.forward_seq(bs, i, ids=q8ffn_golden["prompt"]).argmax() for i in range(3)]
+        assert firsts == [int(q8ffn_golden["ids"][0])] * 3
+        out = m.decode_batch(bs, firsts, 4)
+        out = np.asarray(out[0] if isinstance(out, tuple) else out).reshape(4, 3)
+        for i in range(3):
+            assert np.array_equal(out[:, i], q8ffn_golden["ids"][1:5]), (i, out[:, i])
+    finally:
+        m.close()

@@ -405,3 +405,20 @@ def test_kquant_model_matches_reference(kmix_gguf, kmix_golden):
     assert np.array_equal(np.array(ids, np.int32), kmix_golden["ids"])
     assert np.array_equal(bits(last), bits(kmix_golden["logits_last"]))
     m.close()
+
+
+def test_q8_ffn_mix_model_matches_reference(q8ffn_gguf, q8ffn_golden):
+    """SwiGLU width 3584 with Q8_0 in-projections, gate and up beside a Q6_K
+    embedding and down projection and Q4_K output projections: the oracle's
+    greedy ids and its prefill / last logits equal the reference's bit for bit."""
+    m = oracle.Model(path=q8ffn_gguf)
+    prompt = q8ffn_golden["prompt"]
+    prefill = m.forward_ids(prompt)
+    assert np.array_equal(bits(prefill), bits(q8ffn_golden["logits_prefill"]))
+    ids = [oracle.argmax(prefill)]
+    for _ in range(len(q8ffn_golden["ids"]) - 1):
+        last = m.forward_ids([ids[-1]])
+        ids.append(oracle.argmax(last))
+    assert np.array_equal(np.array(ids, np.int32), q8ffn_golden["ids"])
+    assert np.array_equal(bits(last), bits(q8ffn_golden["logits_last"]))
+    m.close()

@@ -46,3 +46,32 @@ def test_noalloc_argmax_equals_argmax_on_two_calls(lib, first, second):
         assert np.array_equal(a, b), f"m={m} n={n}"
         assert list(b) == [int(np.argmax(r)) for r in x]
     assert lib.hero_argmax_noalloc(ptr(d_x), 65, 16, ptr(out_b), stream()) == HERO_EINVAL
+
+
+def test_noalloc_argmax_under_graph_capture(lib):
+    """hero_argmax_noalloc recorded into a HIP graph (its documented use: the
+    scratch address is resolved by an eager call first) and replayed three
+    times over new logits written between the replays, each replay checked
+    against hero_argmax run eagerly"""
+    import torch
+
+    m, n = 5, 151936
+    rng = np.random.default_rng(77)
+    d_x = dev(logits_with_ties(rng, m, n))
+    out_g, out_e = empty(m * 4), empty(m * 4)
+    scratch = empty(m * 128 * 8)
+    check(lib.hero_argmax_noalloc(ptr(d_x), m, n, ptr(out_g), stream()))
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        check(lib.hero_argmax_noalloc(ptr(d_x), m, n, ptr(out_g), stream()))
+    for i in range(3):
+        x = logits_with_ties(rng, m, n)
+        x[2, rng.integers(0, n)] = 60.0 + i
+        d_x.copy_(dev(x))
+        g.replay()
+        torch.cuda.synchronize()
+        check(lib.hero_argmax(ptr(d_x), m, n, ptr(out_e), ptr(scratch), stream()))
+        got, ref = host(out_g, np.int32), host(out_e, np.int32)
+        assert np.array_equal(got, ref), f"replay {i}: {got} vs {ref}"
+        assert list(got) == [int(np.argmax(r)) for r in x]

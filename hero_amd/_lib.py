@@ -122,6 +122,7 @@ SIGNATURES = {
     "hero_attn_paged_work_bytes": (c_int64, [c_int64, c_int32, c_int32, c_int32, c_int32]),
     "hero_attn_page_bytes": (c_int64, [c_int32, c_int32, c_int32]),
     "hero_read_probe": (c_int, [c_void_p, c_int64, c_int32, c_void_p, c_void_p]),
+    "hero_q8_0_gemv_prefetch": (c_int, [c_void_p, c_int64, c_int64, c_void_p]),
     "hero_attn_decode_paged": (c_int, [POINTER(AttnPagedArgs), c_void_p]),
     "hero_model_open": (c_int, [c_char_p, POINTER(c_void_p)]),
     "hero_model_open_image": (c_int, [c_void_p, c_size_t, POINTER(c_void_p)]),

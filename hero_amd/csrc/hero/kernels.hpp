@@ -8,6 +8,8 @@
 #include <cstddef>
 #include <cstdint>
 
+#include "hero/prefetch.hpp"
+
 namespace hero {
 
 // GEMV epilogues: y = Wx; y = r + Wx; and, for a [gate|up] matrix packed in
@@ -67,6 +69,15 @@ struct GemvInput {
     const float* z;
 };
 bool gemv_streams(int64_t K);
+// workgroups of the streaming GEMV's launch for N rows under epilogue epi
+int gemv_stream_grid(int64_t N, int epi);
+// what another kernel's workgroups read ahead of the streaming GEMV over a
+// packed N x K matrix (epilogue epi): of each GEMV workgroup's rows the first
+// part / 8; .packed == nullptr where the GEMV does not stream (K not a
+// multiple of 4096 up to 12288)
+GemvPrefetch gemv_prefetch_of(const void* packed, int64_t N, int64_t K, int epi, int part = 8);
+// G workgroups of 64 lanes, workgroup g reading what GEMV workgroup g reads (measurement)
+void launch_gemv_prefetch(const GemvPrefetch& p, hipStream_t s);
 void launch_gemv_q8_in(const void* packed, const GemvInput& in, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s);
 // Y[M][N] (+ R) = the M quantized activation rows (act_q8 layout, M rows)
 // times W^T, each element in the reference's block order; int8 MFMA.

@@ -511,6 +511,15 @@ int hero_read_probe(const void* p, int64_t bytes, int32_t workgroups, uint32_t* 
     });
 }
 
+int hero_q8_0_gemv_prefetch(const void* packed, int64_t n, int64_t k, void* stream) {
+    return guard([&] {
+        require(packed && aligned(packed, 16), "packed: a 16-byte aligned device pointer");
+        require(n > 0 && n <= (int64_t(1) << 24) && k == 4096, "n in 1..2^24 and k == 4096 (the interleaved GEMV form)");
+        launch_gemv_prefetch(gemv_prefetch_of(packed, n, k, kEpiStore), as_stream(stream));
+        check_launch("hero_q8_0_gemv_prefetch");
+    });
+}
+
 int64_t hero_attn_page_bytes(int32_t hkv, int32_t page_size, int32_t q8) {
     if (hkv <= 0 || page_size <= 0 || (q8 != 0 && q8 != 1)) return -1;
     return attn_page_bytes(hkv, page_size, q8 != 0);

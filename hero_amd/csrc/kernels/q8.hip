@@ -494,15 +494,40 @@ void gemv_dispatch_epi(int epi, const int8_t* wq, const uint16_t* wd, const int8
 
 bool gemv_streams(int64_t K) { return K % 4096 == 0 && K / 4096 <= 3; }
 
+int gemv_stream_grid(int64_t N, int epi) {
+    const int64_t unit = epi == kEpiSwigluQuant ? 64 : 8;
+    return int(std::min<int64_t>(N >= 16384 ? 2 * device_cus() : device_cus(), packed_rows_pad(N) / unit));
+}
+
+GemvPrefetch gemv_prefetch_of(const void* packed, int64_t N, int64_t K, int epi, int part) {
+    if (!packed || !gemv_streams(K) || part < 1 || part > 8) return GemvPrefetch{};
+    // the workgroup -> rows map of launch_gemv_q8_in: interleaved 8-row groups
+    // at K = 4096 outside the SwiGLU epilogue, contiguous ranges of 8-row (or
+    // 64-row, SwiGLU) units otherwise
+    const bool il = K == 4096 && epi != kEpiSwigluQuant;
+    return GemvPrefetch{packed, int32_t(N), int32_t(K), int32_t(gemv_stream_grid(N, epi)), epi == kEpiSwigluQuant ? 64 : 8, il ? 1 : 0, part};
+}
+
+__global__ __launch_bounds__(64) void gemv_prefetch_kernel(PrefetchList list) {
+    __shared__ __align__(16) int4 sink[kPrefetchSinkBytes / 16];
+    prefetch_gemvs(list, int(blockIdx.x), int(gridDim.x), lds_offset(sink));
+}
+
+void launch_gemv_prefetch(const GemvPrefetch& p, hipStream_t s) {
+    if (!p.packed) return;
+    PrefetchList list{};
+    list.m[0] = p;
+    hipLaunchKernelGGL(gemv_prefetch_kernel, dim3(unsigned(p.G)), dim3(64), 0, s, list);
+}
+
 void launch_gemv_q8_in(const void* packed, const GemvInput& in, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s) {
     const int8_t* wq = static_cast<const int8_t*>(packed);
     const uint16_t* wd = reinterpret_cast<const uint16_t*>(wq + N * K);
     const int Npad = int(packed_rows_pad(N));
     // one workgroup per CU, two for the tall matrices; row ranges in whole
     // 8-row groups (64-row groups for the SwiGLU epilogue: one chain pass each)
-    const int cus = device_cus();
     const int64_t unit = epi == kEpiSwigluQuant ? 64 : 8;
-    const int G = int(std::min<int64_t>(N >= 16384 ? 2 * cus : cus, Npad / unit));
+    const int G = gemv_stream_grid(N, epi);
     const int64_t rows_per = (Npad / unit + G - 1) / G * unit;
     const int nb = int(K / 32);
     // rows per chain pass: at most 64 (one wave) and 64 KB of terms

@@ -6,6 +6,9 @@ Suites (synthetic, seeded inputs; every launch goes through the C ABI):
 
 hbm    the read ceiling: a kernel that only reads (hero_read_probe) over
        18 MB .. 2 GB fresh regions, 512 / 2048 / 8192 workgroups.
+mall   the batch-1 GEMV of the decode step's shapes over cold weights and
+       right after another kernel read the same weights (warm last-level
+       cache), to price a prefetch into that cache.
 kquant Q4_K / Q5_K / Q6_K products over packed random blocks, (K, N) as in
        gemv, M in {1, 16, 512}.
 
@@ -279,6 +282,64 @@ def bench_hbm(lib, replays: int = 20):
     return rows
 
 
+# ---- GEMV over weights another kernel has just read (warm last-level cache) ------------------------
+MALL_SHAPES = [(4096, 4096), (12288, 4096), (4096, 16448), (4096, 24576)]  # (K, N): the decode step's GEMVs
+
+
+def bench_mall(lib, replays: int = 20):
+    """A batch-1 GEMV over cold weights (rotating copies, >= 512 MB, more than
+    the 256 MB last-level cache holds) against the same GEMV right after a
+    kernel that read its weights (hero_read_probe over the packed matrix, 512
+    workgroups, or the same GEMV run once before). warm = time(reader, GEMV)
+    - time(reader alone), per copy; all timed as graph replays, so each launch
+    includes the graph's inter-kernel gap."""
+    from ._lib import check
+
+    t = _torch()
+    gen = t.Generator(device="cuda")
+    gen.manual_seed(4321)
+    out = t.zeros(4, dtype=t.int32, device="cuda")
+    rows = []
+    for k, n in MALL_SHAPES:
+        wbytes = lib.hero_q8_0_packed_bytes(n, k)
+        copies = max(2, math.ceil(600e6 / wbytes))
+        weights = _q8_weight_copies(lib, n, k, copies, gen)
+        x = t.randn(1, k, device="cuda", generator=gen)
+        act = _bytes(lib.hero_q8_0_act_bytes(1, k))
+        check(lib.hero_q8_0_quantize(_p(x), _p(act), 1, k, _stream()))
+        y = t.empty(1, n, device="cuda")
+
+        def gemv(w):
+            check(lib.hero_q8_0_gemv(_p(w), _p(act), _p(y), None, n, k, _stream()))
+
+        def probe(w):
+            check(lib.hero_read_probe(_p(w), wbytes, 512, _p(out), _stream()))
+
+        def xcd_prefetch(w):
+            check(lib.hero_q8_0_gemv_prefetch(_p(w), n, k, _stream()))
+
+        cold = _time_graph(lambda: [gemv(w) for w in weights], len(weights), replays)
+        probe_only = _time_graph(lambda: [probe(w) for w in weights], len(weights), replays)
+        pair = _time_graph(lambda: [(probe(w), gemv(w)) for w in weights], len(weights), replays)
+        twice = _time_graph(lambda: [(gemv(w), gemv(w)) for w in weights], len(weights), replays)
+        cases = [("cold", cold), ("after read_probe", pair - probe_only), ("after the same GEMV", twice - cold),
+                 ("read_probe alone (cold)", probe_only)]
+        if k == 4096:
+            pf_only = _time_graph(lambda: [xcd_prefetch(w) for w in weights], len(weights), replays)
+            pf_pair = _time_graph(lambda: [(xcd_prefetch(w), gemv(w)) for w in weights], len(weights), replays)
+            cases += [("after the XCD-matched prefetch", pf_pair - pf_only), ("XCD-matched prefetch alone (cold)", pf_only)]
+        for name, sec in cases:
+            kernel = "gemv_q8_stream" if "alone" not in name else "read_probe" if "read_probe" in name else "gemv_prefetch"
+            rows.append({"suite": "mall", "kernel": kernel,
+                         "K": k, "N": n, "MB": wbytes / 1e6, "weights": name, "copies": copies, "us": sec * 1e6,
+                         "GB/s": wbytes / sec / 1e9, "hbm_frac": wbytes / sec / 1e9 / HBM_PEAK_GBS,
+                         "vs_cold": cold / sec})
+            print(json.dumps(rows[-1]), flush=True)
+        del weights, act, y, x
+        t.cuda.empty_cache()
+    return rows
+
+
 # ---- gated delta-net -----------------------------------------------------------------------------
 def _gdn_case(lib, hk: int, hv: int, B: int, W: int, gen):
     from ._lib import GdnDecodeArgs
@@ -469,7 +530,7 @@ def bench_attn(lib, replays: int = 20):
 
 def _markdown(rows) -> str:
     out = []
-    for suite in ("hbm", "gemv", "kquant", "gdn", "attn"):
+    for suite in ("hbm", "mall", "gemv", "kquant", "gdn", "attn"):
         rs = [r for r in rows if r["suite"] == suite]
         if not rs:
             continue
@@ -521,6 +582,8 @@ def main(argv=None) -> int:
         rows += bench_gemv(lib, batches=[int(v) for v in args.gemv_batches.split(",")])
     if "hbm" in suites:
         rows += bench_hbm(lib)
+    if "mall" in suites:
+        rows += bench_mall(lib)
     if "kquant" in suites:
         rows += bench_kquant(lib)
     if "gdn" in suites:

@@ -326,6 +326,11 @@ int64_t hero_attn_paged_work_bytes(int64_t max_ctx, int32_t window, int32_t b, i
  * an impossible fold): the read bandwidth the memory-bound kernels are
  * compared with. */
 int hero_read_probe(const void* p, int64_t bytes, int32_t workgroups, uint32_t* out, void* stream);
+/* Measurement (no counterpart in the reference): read every byte of a packed
+ * n x 4096 Q8_0 matrix as hero_q8_0_gemv will read it, workgroup g of this
+ * launch what the GEMV's workgroup g reads (so on the same XCD), and store
+ * nothing: the GEMV that follows finds its weights in its XCDs' L2. */
+int hero_q8_0_gemv_prefetch(const void* packed, int64_t n, int64_t k, void* stream);
 int hero_attn_decode_paged(const hero_attn_paged_args* args, void* stream);
 
 #ifdef __cplusplus

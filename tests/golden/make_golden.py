@@ -24,6 +24,10 @@ so it runs in the build container only). This script:
      projection's width) and Q8_0 in-projections, gate and up beside a Q6_K
      embedding and down projection and Q4_K output projections ->
      tiny_q8ffn_model.npz;
+  9. `hybrid8b_2k`: the ~8B shape on the benchmark's workload: 2048-token
+     prompts (the batch-1 prompt and sequences 0 and 15 of the 16-sequence
+     batch) and 64 greedy passes each -> hybrid8b_2k_model.npz (ids, top-5,
+     and the sha256 of the prefill and last logit vectors in the manifest);
   7. `dh256`: the attention geometry of the reference's Qwen 3.5 4B / 9B
      configs (256-wide heads, a quarter rotating, RoPE base 1e7, Hk 4 over
      Hv 8, untied head) at tiny width -> tiny_dh256_model.npz.
@@ -31,7 +35,7 @@ so it runs in the build container only). This script:
 manifest.json records seeds, shapes, the GGUF's sha256 and the compiler
 flags (-O3 -march=x86-64-v3 -ffp-contract=off: no FMA contraction).
 
-Run:  python tests/golden/make_golden.py [kernels] [tiny] [window] [variant] [kmix] [hybrid8b] [dh256] [q8ffn]
+Run:  python tests/golden/make_golden.py [kernels] [tiny] [window] [variant] [kmix] [hybrid8b] [dh256] [q8ffn] [hybrid8b_2k]
       (no argument: all parts; the manifest keeps the entries of parts not rerun)
 """
 from __future__ import annotations
@@ -341,11 +345,60 @@ def make_hybrid8b(tmp: str) -> dict:
             "logits_last_sha256": digest(rd("logits_last.f32", np.float32))}
 
 
+HYBRID8B_2K_PROMPT = 2048
+HYBRID8B_2K_STEPS = 64
+HYBRID8B_2K_CTX = 4096
+# the benchmark's own prompts: batch 1 (seed SEED) and sequences 0 and 15 of
+# its 16-sequence batch (seeds SEED + 1 + b)
+HYBRID8B_2K_RUNS = {"b1": HYBRID8B_SEED, "seq0": HYBRID8B_SEED + 1, "seq15": HYBRID8B_SEED + 16}
+
+
+def make_hybrid8b_2k(tmp: str) -> dict:
+    """the ~8B model on the benchmark's workload: 2048-token prompts (two
+    1024-row prefill chunks), then 64 greedy passes, for the batch-1 prompt and
+    two of the batch leg's prompts; about 15 minutes of reference CPU time each"""
+    import hero_amd
+
+    shm = "/dev/shm" if os.path.isdir("/dev/shm") else tmp
+    gguf = os.path.join(shm, "8b_2k.gguf")
+    hero_amd.write_synthetic_gguf(gguf, hero_amd.HYBRID_8B_CONFIG, seed=HYBRID8B_SEED, ctx=HYBRID8B_2K_CTX)
+    h = hashlib.sha256()
+    with open(gguf, "rb") as f:
+        for chunk in iter(lambda: f.read(1 << 24), b""):
+            h.update(chunk)
+    digest = lambda a: hashlib.sha256(np.ascontiguousarray(a, np.float32).tobytes()).hexdigest()  # noqa: E731
+    out, entry = {}, {"seed": HYBRID8B_SEED, "ctx": HYBRID8B_2K_CTX, "prompt_len": HYBRID8B_2K_PROMPT,
+                      "decode_steps": HYBRID8B_2K_STEPS, "gguf_sha256": h.hexdigest(), "gguf_bytes": os.path.getsize(gguf),
+                      "runs": {}}
+    try:
+        for name, seed in HYBRID8B_2K_RUNS.items():
+            prompt = np.random.default_rng(seed).integers(0, 151936, HYBRID8B_2K_PROMPT).astype(np.int32)
+            prompt.tofile(os.path.join(tmp, f"{name}_prompt.i32"))
+            outdir = os.path.join(tmp, f"8b2k_{name}")
+            os.makedirs(outdir, exist_ok=True)
+            subprocess.run([HARNESS, "model", "8b", gguf, os.path.join(tmp, f"{name}_prompt.i32"), str(HYBRID8B_2K_STEPS), outdir],
+                           check=True)
+            rd = lambda n, dt: np.fromfile(os.path.join(outdir, n), dtype=dt)  # noqa: E731
+            out[f"{name}_prompt_seed"] = np.array([seed], np.int64)
+            out[f"{name}_ids"] = rd("ids.i32", np.int32)
+            out[f"{name}_top5_ids"] = rd("top5_ids.i32", np.int32).reshape(-1, 5)
+            out[f"{name}_top5_logits"] = rd("top5_logits.f32", np.float32).reshape(-1, 5)
+            entry["runs"][name] = {"prompt_seed": seed,
+                                   "logits_prefill_sha256": digest(rd("logits_prefill.f32", np.float32)),
+                                   "logits_last_sha256": digest(rd("logits_last.f32", np.float32)),
+                                   "reference_times": open(os.path.join(outdir, "times.txt")).read()}
+    finally:
+        os.remove(gguf)
+    np.savez_compressed(os.path.join(HERE, "hybrid8b_2k_model.npz"), **out)
+    return entry
+
+
 PARTS = {"kernels": make_kernels, "tiny": make_tiny, "window": make_window, "variant": make_variant, "kmix": make_kmix,
-         "hybrid8b": make_hybrid8b, "dh256": make_dh256, "q8ffn": make_q8ffn}
+         "hybrid8b": make_hybrid8b, "dh256": make_dh256, "q8ffn": make_q8ffn,
+         "hybrid8b_2k": make_hybrid8b_2k}
 MANIFEST_KEYS = {"kernels": "kernels", "tiny": "tiny_model", "window": "window", "variant": "tiny_hk4u_model",
                  "kmix": "tiny_kmix_model", "hybrid8b": "hybrid8b_model", "dh256": "tiny_dh256_model",
-                 "q8ffn": "tiny_q8ffn_model"}
+                 "q8ffn": "tiny_q8ffn_model", "hybrid8b_2k": "hybrid8b_2k_model"}
 
 
 def main():

@@ -1394,24 +1394,263 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnPagedArgs p) {
     }
 }
 
-// one workgroup per (query head, row), a lane per channel: merge the splits,
-// then the gate (qwen35.hpp:390-393) and the Q8_0 quantization for W_o
-__global__ __launch_bounds__(kAttnDim) void attn_combine_kernel(AttnPagedArgs p) {
+// Pages of 64 positions, fp16 (the model's paged cache): one workgroup per
+// (KV head, split, row) streams the pages its split touches, the K block of
+// each page (64 keys x 128 channels, 16 KB, contiguous in the pool) and then
+// the V blocks, through a ring of kRgSlots shared-memory slots filled by
+// global_load_lds: up to three pages in flight while one is computed, instead
+// of one register tile. The arithmetic is attn_split_kernel's: a lane's
+// partial dot over a channel quarter with fused multiply-adds, the quarters
+// summed, the split's max, exp and sum, and the weighted sum by fused
+// multiply-adds (four key quarters summed at the end). Keys of a page outside
+// the split [t0, t1) get no weight, and the rows past the newest position read
+// as zero (the pool may hold anything there).
+constexpr int kRgSlots = 4;
+constexpr int kRgSlot = kPgTile * kAttnDim * 2;  // bytes of one page's K (or V) block of one KV head
+
+size_t attn_split_ring_smem(int Gs, int split) {
+    return size_t(kRgSlots) * kRgSlot + size_t(Gs) * kAttnDim * 4 + size_t(Gs) * (split / kPgTile + 1) * kPgTile * 4;
+}
+
+__global__ __launch_bounds__(256) void attn_split_ring_kernel(AttnPagedArgs p) {
     const AttnDecodeArgs& a = p.a;
-    const int c = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int g = blockIdx.x, sp = blockIdx.y, b = blockIdx.z;
+    const int Gs = a.Hq / a.Hkv;
+    const int pos = a.positions[b];
+    if (pos < 0 || pos >= p.max_pages * p.page_size) return;
+    const int first = visible_first(pos, a.window);
+    const int t0 = first + sp * p.split, t1 = min(pos + 1, t0 + p.split);
+    const int64_t rec = 2 + kAttnDim;
+    float* out = p.work + ((int64_t(b) * a.Hq + int64_t(g) * Gs) * p.nsplit + sp) * rec;  // head h of the group: + h * nsplit * rec
+    const int64_t hstride = int64_t(p.nsplit) * rec;
+    if (t0 >= t1) {  // nothing visible in this split
+        for (int e = tid; e < Gs * rec; e += 256) out[(e / rec) * hstride + e % rec] = (e % rec) == 0 ? -INFINITY : 0.f;
+        return;
+    }
+    const int pg0 = t0 / kPgTile, np = (t1 - 1) / kPgTile - pg0 + 1;  // pages the split touches
+    const int nblk = 2 * np;                                          // their K blocks, then their V blocks
+    const int32_t* pt = page_row(p, b);
+    extern __shared__ __align__(16) float rg_smem[];
+    uint8_t* ring = reinterpret_cast<uint8_t*>(rg_smem);                                   // [kRgSlots][16 KB]
+    float* qs = reinterpret_cast<float*>(ring + kRgSlots * kRgSlot);                        // [Gs][128]
+    float* sc0 = qs + Gs * kAttnDim;                                                        // [Gs][np * 64]
+    const int sstride = np * kPgTile;
+    auto sc = [&](int h) { return sc0 + h * sstride; };
+
+    // The pool page of each page the split touches (np <= 9) and expf's table
+    // go to shared memory before any ring load: a global read issued after the
+    // ring loads (the compiler cannot see them) would wait for all of them.
+    __shared__ int pages_sh[kAttnMaxSplit / kPgTile + 1];
+    __shared__ uint64_t etab[32];
+    if (tid < np) pages_sh[tid] = pt[pg0 + tid];
+    fill_exp_table(etab, tid);
+    __syncthreads();
+    const ExpTab et{etab};
+    // block i of the split into slot i % kRgSlots: wave w's four loads move
+    // 1 KB pieces 4w .. 4w + 3 of the block, lane by lane
+    auto issue = [&](int i) {
+        const int kv = i < np ? 0 : 1;
+        const int64_t page = pages_sh[i < np ? i : i - np];
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(p.pages) + ((page * 2 + kv) * a.Hkv + g) * int64_t(kRgSlot);
+        const uint32_t dst = lds_offset(ring + (i % kRgSlots) * kRgSlot);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) lds_dma_b128(src + ((wv * 4 + u) * 64 + lane) * 16, dst + (wv * 4 + u) * 1024);
+    };
+    // the group's rotated queries, through the same path, issued first
+    if (tid < Gs * kAttnDim / 4) lds_dma_b128(a.q_rot + (int64_t(b) * a.Hq + int64_t(g) * Gs) * kAttnDim + 4 * tid, lds_offset(qs + 4 * (tid & ~63)));
+    int issued = 0;  // blocks issued so far (uniform)
+    for (; issued < kRgSlots && issued < nblk; ++issued) issue(issued);
+    // block i has landed everywhere: this wave's loads of the blocks issued
+    // after it may still be in flight (four per block), then the barrier
+    auto wait_block = [&](int i) {
+        switch (issued - i - 1) {
+            case 3: wait_vmcnt<12>(); break;
+            case 2: wait_vmcnt<8>(); break;
+            case 1: wait_vmcnt<4>(); break;
+            default: wait_vmcnt<0>(); break;
+        }
+        __syncthreads();
+    };
+
+    // ---- scores: lane (key kr of the page, channel quarter qq), four query
+    // heads at a time with their quarter in registers. The lane visits its
+    // four 16-byte chunks from a key-dependent one (no bank conflicts), and
+    // its query registers hold chunk (u + kr) & 3 in slot u ----
+    const int qq = lane & 3, kr = wv * 16 + (lane >> 2);
+    float qv[4][32];
+    auto load_q = [&](int hp) {
+#pragma unroll
+        for (int hh = 0; hh < 4; ++hh) {
+            if (hp + hh < Gs) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float4* q4 = reinterpret_cast<const float4*>(qs + (hp + hh) * kAttnDim + 32 * qq + 8 * ((u + kr) & 3));
+                    const float4 qa = q4[0], qb = q4[1];
+                    qv[hh][8 * u] = qa.x, qv[hh][8 * u + 1] = qa.y, qv[hh][8 * u + 2] = qa.z, qv[hh][8 * u + 3] = qa.w;
+                    qv[hh][8 * u + 4] = qb.x, qv[hh][8 * u + 5] = qb.y, qv[hh][8 * u + 6] = qb.z, qv[hh][8 * u + 7] = qb.w;
+                }
+            }
+        }
+    };
+    for (int i = 0; i < np; ++i) {
+        wait_block(i);
+        if (issued < nblk && i > 0) issue(issued++);  // into the slot the previous block left
+        const uint8_t* blk = ring + (i % kRgSlots) * kRgSlot + kr * (kAttnDim * 2);
+        const int t = (pg0 + i) * kPgTile + kr;
+        const bool live = t >= t0 && t < t1;
+        for (int hp = 0; hp < Gs; hp += 4) {
+            if (i == 0 || Gs > 4) load_q(hp);
+            float dot[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint4 w = *reinterpret_cast<const uint4*>(blk + (4 * qq + ((u + kr) & 3)) * 16);
+                const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+                float kx[8];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    kx[2 * e] = half_bits_to_f32(uint16_t(wd[e] & 0xFFFFu));
+                    kx[2 * e + 1] = half_bits_to_f32(uint16_t(wd[e] >> 16));
+                }
+#pragma unroll
+                for (int hh = 0; hh < 4; ++hh)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) dot[hh] = fmaf(qv[hh][8 * u + e], kx[e], dot[hh]);
+            }
+#pragma unroll
+            for (int hh = 0; hh < 4; ++hh) {
+                if (hp + hh < Gs) {
+                    float d = dot[hh];
+                    d += __shfl_xor(d, 1);
+                    d += __shfl_xor(d, 2);
+                    if (qq == 0) sc(hp + hh)[i * kPgTile + kr] = live ? a.score_scale * d : -INFINITY;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // ---- per head (a wave each): the split's max, p = exp(s - m), the sum ----
+    for (int h = wv; h < Gs; h += 4) {
+        float m = -INFINITY;
+        for (int jj = lane; jj < sstride; jj += 64) m = fmaxf(m, sc(h)[jj]);
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        float l = 0.f;
+        for (int jj = lane; jj < sstride; jj += 64) {
+            const float sv = sc(h)[jj];
+            const float e = sv == -INFINITY ? 0.f : et.exp(sv - m);
+            sc(h)[jj] = e;
+            l += e;
+        }
+        for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
+        if (lane == 0) {
+            out[h * hstride] = m;
+            out[h * hstride + 1] = l;
+        }
+    }
+    // ---- weighted sum: lane (channel pair 2 lane, 2 lane + 1), keys 16 wv .. +15 of each page ----
+    float o[kAttnMaxGroup][2];
+#pragma unroll
+    for (int h = 0; h < kAttnMaxGroup; ++h) o[h][0] = o[h][1] = 0.f;
+    for (int i = np; i < nblk; ++i) {
+        wait_block(i);  // its barrier also publishes the weights (first V block)
+        if (issued < nblk) issue(issued++);  // into the slot block i - 1 left
+        const uint8_t* blk = ring + (i % kRgSlots) * kRgSlot;
+        const int jb = (i - np) * kPgTile + wv * 16;  // the wave's first key of the page (weight index)
+        const int tb = (pg0 + i - np) * kPgTile + wv * 16;
+#pragma unroll
+        for (int j4 = 0; j4 < 16; j4 += 4) {
+            float4 w[kAttnMaxGroup];
+#pragma unroll
+            for (int h = 0; h < kAttnMaxGroup; ++h)
+                if (h < Gs) w[h] = *reinterpret_cast<const float4*>(sc(h) + jb + j4);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t dw = *reinterpret_cast<const uint32_t*>(blk + (wv * 16 + j4 + u) * (kAttnDim * 2) + lane * 4);
+                const bool live = tb + j4 + u < t1;
+                const float v0 = live ? half_bits_to_f32(uint16_t(dw & 0xFFFFu)) : 0.f;
+                const float v1 = live ? half_bits_to_f32(uint16_t(dw >> 16)) : 0.f;
+#pragma unroll
+                for (int h = 0; h < kAttnMaxGroup; ++h) {
+                    if (h < Gs) {
+                        const float wu = u == 0 ? w[h].x : u == 1 ? w[h].y : u == 2 ? w[h].z : w[h].w;
+                        o[h][0] = fmaf(wu, v0, o[h][0]);
+                        o[h][1] = fmaf(wu, v1, o[h][1]);
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();  // every wave is done with the ring: it holds the key quarters' sums now
+    float* red = reinterpret_cast<float*>(ring);  // [4][Gs][128]
+#pragma unroll
+    for (int h = 0; h < kAttnMaxGroup; ++h) {
+        if (h < Gs) {
+            red[(wv * Gs + h) * kAttnDim + 2 * lane] = o[h][0];
+            red[(wv * Gs + h) * kAttnDim + 2 * lane + 1] = o[h][1];
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < Gs * kAttnDim; e += 256) {
+        const int h = e / kAttnDim, c = e % kAttnDim;
+        float v = red[(0 * Gs + h) * kAttnDim + c];
+        v += red[(1 * Gs + h) * kAttnDim + c];
+        v += red[(2 * Gs + h) * kAttnDim + c];
+        v += red[(3 * Gs + h) * kAttnDim + c];
+        out[h * hstride + 2 + c] = v;
+    }
+}
+
+// One workgroup per (query head, row): merge the splits, then the gate
+// (qwen35.hpp:390-393) and the Q8_0 quantization for W_o. Lane (channel c,
+// split group sg of 4) adds its channel over splits sg, sg + 4, ... with all
+// of its record reads issued at once (up to kCombineLanesSplits per pass);
+// the four groups' partial sums are then added in group order.
+constexpr int kCombineGroups = 4;
+constexpr int kCombinePass = 16;  // splits per lane per pass
+__global__ __launch_bounds__(kAttnDim * kCombineGroups) void attn_combine_kernel(AttnPagedArgs p) {
+    const AttnDecodeArgs& a = p.a;
+    const int tid = threadIdx.x, c = tid % kAttnDim, sg = tid / kAttnDim, h = blockIdx.x, b = blockIdx.y;
     const int pos = a.positions[b];
     if (pos < 0 || pos >= p.max_pages * p.page_size) return;
     const int64_t rec = 2 + kAttnDim;
     const float* w = p.work + (int64_t(b) * a.Hq + h) * p.nsplit * rec;
-    float m = -INFINITY;
-    for (int s = 0; s < p.nsplit; ++s) m = fmaxf(m, w[s * rec]);
+    __shared__ float red[kAttnDim * kCombineGroups / 64];
+    __shared__ float part[kCombineGroups][2][kAttnDim];
+    float mloc = -INFINITY;
+    for (int s = tid; s < p.nsplit; s += kAttnDim * kCombineGroups) mloc = fmaxf(mloc, w[s * rec]);
+    for (int off = 32; off > 0; off >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, off));
+    if ((tid & 63) == 0) red[tid >> 6] = mloc;
+    __syncthreads();
+    float m = red[0];
+    for (int i = 1; i < kAttnDim * kCombineGroups / 64; ++i) m = fmaxf(m, red[i]);
     float l = 0.f, o = 0.f;
-    for (int s = 0; s < p.nsplit; ++s) {
-        const float ms = w[s * rec];
-        if (ms == -INFINITY) continue;
-        const float f = exp_f32(ms - m);
-        l += w[s * rec + 1] * f;
-        o += w[s * rec + 2 + c] * f;
+    for (int base = sg; base < p.nsplit; base += kCombineGroups * kCombinePass) {
+        float mv[kCombinePass], lv[kCombinePass], ov[kCombinePass];
+#pragma unroll
+        for (int u = 0; u < kCombinePass; ++u) {
+            const int s = min(base + u * kCombineGroups, p.nsplit - 1);
+            mv[u] = w[s * rec];
+            lv[u] = w[s * rec + 1];
+            ov[u] = w[s * rec + 2 + c];
+        }
+#pragma unroll
+        for (int u = 0; u < kCombinePass; ++u) {
+            if (base + u * kCombineGroups < p.nsplit && mv[u] != -INFINITY) {
+                const float f = exp_f32(mv[u] - m);
+                l += lv[u] * f;
+                o += ov[u] * f;
+            }
+        }
+    }
+    part[sg][0][c] = l;
+    part[sg][1][c] = o;
+    __syncthreads();
+    if (sg != 0) return;
+    l = part[0][0][c], o = part[0][1][c];
+#pragma unroll
+    for (int g2 = 1; g2 < kCombineGroups; ++g2) {
+        l += part[g2][0][c];
+        o += part[g2][1][c];
     }
     const float gate = a.proj[int64_t(b) * a.proj_stride + int64_t(h) * 2 * kAttnDim + kAttnDim + c];
     const float out = (o / l) * sigmoid_f32(gate);
@@ -1445,11 +1684,17 @@ void launch_attn_paged(const AttnPagedArgs& p, hipStream_t s) {
     hipLaunchKernelGGL(attn_paged_prep_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, p);
     const int Gs = a.Hq / a.Hkv;
     const size_t smem = size_t(Gs) * (2 * kAttnDim + size_t(p.split)) * 4;
-    if (p.q8)
+    // the page-streaming form for one or two sequences (the pages of a split
+    // in flight at once); with more sequences the grid alone keeps enough
+    // loads in flight, and the per-key form, with more workgroups per CU,
+    // streams faster (32k context, 16 sequences: 536 vs 727 us)
+    if (!p.q8 && p.page_size == kPgTile && a.B <= 2)
+        hipLaunchKernelGGL(attn_split_ring_kernel, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), attn_split_ring_smem(Gs, p.split), s, p);
+    else if (p.q8)
         hipLaunchKernelGGL(attn_split_kernel<true>, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), smem, s, p);
     else
         hipLaunchKernelGGL(attn_split_kernel<false>, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), smem, s, p);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, p);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim * kCombineGroups), 0, s, p);
 }
 
 namespace {

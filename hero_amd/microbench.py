@@ -417,7 +417,15 @@ def bench_gdn(lib, replays: int = 50):
 
 
 # ---- GQA decode attention ------------------------------------------------------------------------
-def bench_attn(lib, replays: int = 20):
+ATTN_CTX = (1024, 8192, 32768)
+ATTN_BATCH = (1, 16)
+ATTN_CACHES = ("fp32", "fp16", "q8")
+
+
+ATTN_VARIANTS = ("full", "swa1024")
+
+
+def bench_attn(lib, replays: int = 20, contexts=ATTN_CTX, batches=ATTN_BATCH, caches_run=ATTN_CACHES, variants=ATTN_VARIANTS):
     from ._lib import AttnDecodeArgs, AttnPagedArgs, check
 
     t = _torch()
@@ -427,13 +435,13 @@ def bench_attn(lib, replays: int = 20):
     hq, hkv, dh = 32, 8, 128
     qw, kw = hq * dh, hkv * dh
     stride = 2 * qw + 2 * kw
-    for ctx in (1024, 8192, 32768):
-        for B in (1, 16):
+    for ctx in contexts:
+        for B in batches:
             cache_bytes = B * ctx * kw * 4 * 2
             copies = max(1, min(16, math.ceil(512e6 / cache_bytes)))
             scale = 1.0 / math.sqrt(dh)
             caches = []
-            for _ in range(copies):
+            for _ in range(copies if "fp32" in caches_run else 0):
                 kc = t.randn(B * ctx * kw, device="cuda", generator=gen) * scale
                 vc = t.randn(B * ctx * kw, device="cuda", generator=gen) * scale
                 caches.append((kc, vc))
@@ -445,7 +453,7 @@ def bench_attn(lib, replays: int = 20):
             scores = t.empty(B * hq * ctx, device="cuda")
             qrot = t.empty(B * qw, device="cuda")
             act = _bytes(lib.hero_q8_0_act_bytes(B, qw))
-            for name, window, sc in (("full", 0, scale), ("swa1024", 1024, 1.0)):
+            for name, window, sc in [v for v in (("full", 0, scale), ("swa1024", 1024, 1.0)) if v[0] in variants] if caches else ():
                 args = [AttnDecodeArgs(_p(proj), stride, 2 * qw, 2 * qw + kw, _p(gq), _p(gk), 1e-6, _p(cs), _p(kc), _p(vc), ctx,
                                        _p(pos), _p(scores), _p(qrot), sc, window, _p(act), None, B, hq, hkv, dh)
                         for kc, vc in caches]
@@ -467,9 +475,9 @@ def bench_attn(lib, replays: int = 20):
             page = 64
             max_pages = ctx // page
             pages = [(t.randn(B * max_pages * 2 * hkv * page * dh, device="cuda", generator=gen) * scale).half()
-                      for _ in range(max(1, min(16, math.ceil(512e6 / (cache_bytes // 2)))))]
+                      for _ in range(max(1, min(16, math.ceil(512e6 / (cache_bytes // 2)))) if "fp16" in caches_run else 0)]
             table = t.arange(B * max_pages, dtype=t.int32, device="cuda")
-            for name, window, sc in (("full", 0, scale), ("swa1024", 1024, 1.0)):
+            for name, window, sc in [v for v in (("full", 0, scale), ("swa1024", 1024, 1.0)) if v[0] in variants] if pages else ():
                 wbytes = lib.hero_attn_paged_work_bytes(ctx, window, B, hq, hkv)
                 work = _bytes(wbytes)
                 args = []
@@ -496,13 +504,13 @@ def bench_attn(lib, replays: int = 20):
             # scales of the inputs' size (|N(0,1)|/sqrt(128) max / 127)
             pb = lib.hero_attn_page_bytes(hkv, page, 1)
             pages8 = []
-            for _ in range(max(1, min(16, math.ceil(512e6 / (B * max_pages * pb))))):
+            for _ in range(max(1, min(16, math.ceil(512e6 / (B * max_pages * pb)))) if "q8" in caches_run else 0):
                 pg = t.randint(-127, 128, (B * max_pages, pb), dtype=t.int8, device="cuda", generator=gen).view(t.uint8)
                 q_bytes = 2 * hkv * page * dh
                 d = t.full((B * max_pages, (pb - q_bytes) // 2), 3.0 * scale / 127.0, device="cuda").half()
                 pg[:, q_bytes:] = d.view(t.uint8)
                 pages8.append(pg.contiguous())
-            for name, window, sc in (("full", 0, scale), ("swa1024", 1024, 1.0)):
+            for name, window, sc in [v for v in (("full", 0, scale), ("swa1024", 1024, 1.0)) if v[0] in variants] if pages8 else ():
                 wbytes = lib.hero_attn_paged_work_bytes(ctx, window, B, hq, hkv)
                 work = _bytes(wbytes)
                 args = []
@@ -555,6 +563,10 @@ def main(argv=None) -> int:
     ap.add_argument("--suite", default="gemv,gdn,attn")
     ap.add_argument("--out", default=None, help="write a markdown table here")
     ap.add_argument("--gemv-batches", default=",".join(map(str, GEMV_BATCHES)), help="activation rows M of the gemv suite")
+    ap.add_argument("--attn-ctx", default=",".join(map(str, ATTN_CTX)), help="contexts of the attn suite")
+    ap.add_argument("--attn-batch", default=",".join(map(str, ATTN_BATCH)), help="batches of the attn suite")
+    ap.add_argument("--attn-cache", default=",".join(ATTN_CACHES), help="caches of the attn suite: fp32, fp16 (paged), q8 (paged)")
+    ap.add_argument("--attn-variant", default=",".join(ATTN_VARIANTS), help="variants of the attn suite: full, swa1024")
     ap.add_argument("--direct", type=int, default=0, help="run each case this many times as plain launches instead of graph replays")
     ap.add_argument("--calibrate", action="store_true",
                     help="first copy 512 MiB device to device three times: the known-size dispatches hero_amd.traffic calibrates "
@@ -589,7 +601,8 @@ def main(argv=None) -> int:
     if "gdn" in suites:
         rows += bench_gdn(lib)
     if "attn" in suites:
-        rows += bench_attn(lib)
+        rows += bench_attn(lib, contexts=[int(v) for v in args.attn_ctx.split(",")], batches=[int(v) for v in args.attn_batch.split(",")],
+                           caches_run=args.attn_cache.split(","), variants=args.attn_variant.split(","))
     md = _markdown(rows)
     if args.out:
         with open(args.out, "w") as f:

@@ -704,11 +704,13 @@ def test_attn_prefill_rows_match_oracle(lib, M, p0, hq, hkv, max_ctx, window, dh
         assert blocks[b].tobytes() == oracle.quantize_row_q8_0(got[b]).tobytes(), f"row {b}"
 
 
-@pytest.mark.parametrize("hq,window", [(8, 0), (8, 50), (16, 0)])
-def test_attn_paged_fp16_matches_oracle_over_fp16_kv(lib, hq, window):
-    """Split-K attention over the paged fp16 cache: pages of 16 positions in a
-    shuffled pool, contexts up to 300 (several pages per tile, several
-    splits), 4 and 8 query heads per KV head, full and windowed. The oracle
+@pytest.mark.parametrize("hq,window,page", [(8, 0, 16), (8, 50, 16), (16, 0, 16), (8, 0, 64), (8, 50, 64), (8, 70, 64), (16, 0, 64)])
+def test_attn_paged_fp16_matches_oracle_over_fp16_kv(lib, hq, window, page):
+    """Split-K attention over the paged fp16 cache: pages of 16 positions (the
+    per-key kernel: several pages per tile) or 64 (the page-streaming kernel:
+    splits that start and end inside a page) in a shuffled pool, contexts up to
+    300 (several splits), 4 and 8 query heads per KV head, full and windowed
+    (windows of 50 and 70: splits not aligned to pages). The oracle
     attends over the same K/V rounded to fp16 (its storage), sequentially; the
     split kernel sums dot products by channel quarters with fused multiply-adds
     and merges the split softmax in another order, so the outputs agree within
@@ -716,8 +718,9 @@ def test_attn_paged_fp16_matches_oracle_over_fp16_kv(lib, hq, window):
     quantized W_o input is the quantization of the kernel's own output."""
     from hero_amd._lib import AttnDecodeArgs, AttnPagedArgs
 
-    rng = np.random.default_rng(23 + hq + window)
-    B, hkv, dh, page, max_pages, steps = 2, 2, 128, 16, 20, 300
+    rng = np.random.default_rng(23 + hq + window + page)
+    B, hkv, dh, steps = 2, 2, 128, 300
+    max_pages = (320 + page - 1) // page
     max_ctx = page * max_pages
     qw, kw = hq * dh, hkv * dh
     stride = 2 * qw + 2 * kw

@@ -102,6 +102,9 @@ def cpu_baseline(image, prompt, seconds: float, prefix: int) -> tuple[dict, np.n
         "kind": "port",
         "host": cpu,
         "prefill_tok_s": prefix / prefill_s,
+        # the CPU's decode passes run at a shorter context than the GPU's
+        "context": {"cpu_decode": [prefix, prefix + passes], "gpu_decode_start": len(prompt),
+                    "attention_share_at_gpu_context": attention_share(len(prompt))},
         "sample": f"oracle on the same 8B model bytes, {threads} threads (one per CPU of the process's affinity set; "
                   f"{cpu['nproc']} CPUs on the host, {cpu['model']}), g++ -O3 -march=x86-64-v3 -ffp-contract=off: "
                   f"prefill of the prompt's first {prefix} ids in {prefill_s:.1f} s, then {passes} greedy decode passes "

@@ -119,8 +119,8 @@ SIGNATURES = {
     "hero_gdn_prefill_chunked": (c_int, [POINTER(GdnDecodeArgs), c_void_p, c_int64, c_void_p]),
     "hero_attn_decode": (c_int, [POINTER(AttnDecodeArgs), c_void_p]),
     "hero_attn_prefill": (c_int, [POINTER(AttnDecodeArgs), c_void_p]),
-    "hero_attn_paged_work_bytes": (c_int64, [c_int64, c_int32, c_int32, c_int32, c_int32]),
-    "hero_attn_page_bytes": (c_int64, [c_int32, c_int32, c_int32]),
+    "hero_attn_paged_work_bytes": (c_int64, [c_int64, c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "hero_attn_page_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32]),
     "hero_read_probe": (c_int, [c_void_p, c_int64, c_int32, c_void_p, c_void_p]),
     "hero_q8_0_gemv_prefetch": (c_int, [c_void_p, c_int64, c_int64, c_void_p]),
     "hero_attn_decode_paged": (c_int, [POINTER(AttnPagedArgs), c_void_p]),

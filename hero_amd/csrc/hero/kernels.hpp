@@ -208,11 +208,13 @@ struct AttnPagedArgs {
 };
 constexpr int kAttnMaxSplit = 512;
 // bytes of one page of the pool
-inline int64_t attn_page_bytes(int64_t Hkv, int64_t page_size, bool q8) { return q8 ? 2 * Hkv * page_size * (128 + 8) : 2 * Hkv * page_size * 128 * 2; }
+// bytes of one page of page_size positions: fp16 K and V rows of Dh, or (q8,
+// Dh 128) int8 rows and their four fp16 scales
+inline int64_t attn_page_bytes(int64_t Hkv, int64_t Dh, int64_t page_size, bool q8) { return q8 ? 2 * Hkv * page_size * (Dh + Dh / 32 * 2) : 2 * Hkv * page_size * Dh * 2; }
 constexpr int kAttnMaxGroup = 8;  // query heads per KV head
 // split and nsplit for B rows over at most max_ctx positions (window 0 = full)
 void attn_paged_plan(int64_t max_ctx, int window, int B, int Hkv, int* split, int* nsplit);
-int64_t attn_paged_work_floats(int B, int Hq, int nsplit);
+int64_t attn_paged_work_floats(int B, int Hq, int nsplit, int Dh);
 void launch_attn_paged(const AttnPagedArgs& p, hipStream_t s);
 
 }  // namespace hero

@@ -494,11 +494,11 @@ int hero_attn_prefill(const hero_attn_decode_args* p, void* stream) {
     });
 }
 
-int64_t hero_attn_paged_work_bytes(int64_t max_ctx, int32_t window, int32_t b, int32_t hq, int32_t hkv) {
-    if (max_ctx <= 0 || b <= 0 || hkv <= 0 || hq <= 0 || window < 0) return -1;
+int64_t hero_attn_paged_work_bytes(int64_t max_ctx, int32_t window, int32_t b, int32_t hq, int32_t hkv, int32_t head_dim) {
+    if (max_ctx <= 0 || b <= 0 || hkv <= 0 || hq <= 0 || window < 0 || (head_dim != 128 && head_dim != 256)) return -1;
     int split = 0, nsplit = 0;
     attn_paged_plan(max_ctx, window, b, hkv, &split, &nsplit);
-    return attn_paged_work_floats(b, hq, nsplit) * 4;
+    return attn_paged_work_floats(b, hq, nsplit, head_dim) * 4;
 }
 
 int hero_read_probe(const void* p, int64_t bytes, int32_t workgroups, uint32_t* out, void* stream) {
@@ -520,9 +520,9 @@ int hero_q8_0_gemv_prefetch(const void* packed, int64_t n, int64_t k, void* stre
     });
 }
 
-int64_t hero_attn_page_bytes(int32_t hkv, int32_t page_size, int32_t q8) {
-    if (hkv <= 0 || page_size <= 0 || (q8 != 0 && q8 != 1)) return -1;
-    return attn_page_bytes(hkv, page_size, q8 != 0);
+int64_t hero_attn_page_bytes(int32_t hkv, int32_t head_dim, int32_t page_size, int32_t q8) {
+    if (hkv <= 0 || page_size <= 0 || (q8 != 0 && q8 != 1) || (head_dim != 128 && head_dim != 256) || (q8 && head_dim != 128)) return -1;
+    return attn_page_bytes(hkv, head_dim, page_size, q8 != 0);
 }
 
 int hero_attn_decode_paged(const hero_attn_paged_args* p, void* stream) {
@@ -530,7 +530,8 @@ int hero_attn_decode_paged(const hero_attn_paged_args* p, void* stream) {
         require(p != nullptr, "null args");
         AttnPagedArgs g{};
         g.a = attn_args(p->a);
-        require(g.a.Dh == 128, "the paged cache holds 128-wide heads");
+        require(g.a.Dh == 128 || (g.a.Dh == 256 && p->q8 == 0 && p->page_size == 64),
+                "the paged cache holds 128-wide heads, or 256-wide heads in fp16 pages of 64 positions");
         require(g.a.Hq / g.a.Hkv <= kAttnMaxGroup, "at most 8 query heads per KV head");
         require(p->pages && p->page_table && p->work, "null pointer");
         require(p->page_size > 0 && p->max_pages > 0 && int64_t(p->page_size) * p->max_pages <= (int64_t(1) << 24), "bad page geometry");
@@ -542,7 +543,7 @@ int hero_attn_decode_paged(const hero_attn_paged_args* p, void* stream) {
         g.page_size = p->page_size;
         g.max_pages = p->max_pages;
         attn_paged_plan(int64_t(p->page_size) * p->max_pages, g.a.window, g.a.B, g.a.Hkv, &g.split, &g.nsplit);
-        require(p->work_bytes >= attn_paged_work_floats(g.a.B, g.a.Hq, g.nsplit) * 4, "split workspace too small");
+        require(p->work_bytes >= attn_paged_work_floats(g.a.B, g.a.Hq, g.nsplit, g.a.Dh) * 4, "split workspace too small");
         g.work = p->work;
         launch_attn_paged(g, as_stream(stream));
         check_launch("hero_attn_decode_paged");

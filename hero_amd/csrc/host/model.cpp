@@ -272,7 +272,7 @@ void Qwen35Model::load(const GgufFile& g) {
     if (typed_) {
         load_typed(g, pk);
         hip_check(hipStreamSynchronize(stream_), "load sync");
-        build_rope_table(std::min<int64_t>(c.CTX, 65536));
+        build_rope_table(c.CTX);
         return;
     }
     embedding_ = pk.alloc(c.V, c.D);
@@ -339,7 +339,7 @@ void Qwen35Model::load(const GgufFile& g) {
         layers_.push_back(std::move(L));
     }
     hip_check(hipStreamSynchronize(stream_), "load sync");
-    build_rope_table(std::min<int64_t>(c.CTX, 65536));
+    build_rope_table(c.CTX);
 }
 
 // The same schema as load() with every linear kept in its own type
@@ -430,7 +430,7 @@ Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batc
     : m_(m), max_tokens_(max_tokens), batch_(batch), kv_paged_(kv_format != kKvF32), kv_q8_(kv_format == kKvQ8), seq_tokens_(size_t(batch), 0) {
     const bool kv_paged = kv_paged_;
     const ModelConfig& c = m.c_;
-    expect(!kv_paged || c.Dh == 128, "the paged K/V cache holds 128-wide heads; 256-wide heads use the fp32 cache");
+    expect(!kv_q8_ || c.Dh == 128, "the Q8_0 K/V cache holds 128-wide heads; 256-wide heads use the fp32 or fp16 cache");
     const int64_t B = batch;
     int64_t n_in_max = 0;
     for (const LayerWeights& L : m.layers_) n_in_max = std::max(n_in_max, L.n_in);
@@ -476,7 +476,7 @@ Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batc
     kv_pages_.resize(size_t(c.L));
     if (kv_paged) {
         max_pages_ = (max_tokens + kPageTokens - 1) / kPageTokens;
-        const int64_t page_bytes = attn_page_bytes(c.Hkv, kPageTokens, kv_q8_);
+        const int64_t page_bytes = attn_page_bytes(c.Hkv, c.Dh, kPageTokens, kv_q8_);
         for (int64_t l = 0; l < c.L; ++l)
             if (!c.is_recurrent(l)) kv_pages_[size_t(l)] = DeviceBuffer(size_t(B * max_pages_ * page_bytes));
         // sequence b owns pool pages b * max_pages ... (a server would map pages on demand)
@@ -486,7 +486,7 @@ Qwen35Model::State::State(const Qwen35Model& m, int64_t max_tokens, int64_t batc
         hip_check(hipMemcpy(page_table_.get(), table.data(), table.size() * 4, hipMemcpyHostToDevice), "page table");
         int split = 0, nsplit = 0;
         attn_paged_plan(max_pages_ * kPageTokens, 0, int(B), int(c.Hkv), &split, &nsplit);
-        attn_work_ = DeviceBuffer(size_t(attn_paged_work_floats(int(B), int(c.Hq), nsplit)) * 4);
+        attn_work_ = DeviceBuffer(size_t(attn_paged_work_floats(int(B), int(c.Hq), nsplit, int(c.Dh))) * 4);
     }
     reset();
 }
@@ -541,7 +541,7 @@ void Qwen35Model::State::ensure_chunk(int64_t rows) {
     if (kv_paged_) {
         int split = 0, nsplit = 0;
         attn_paged_plan(max_pages_ * kPageTokens, 0, int(rows), int(c.Hkv), &split, &nsplit);
-        cattn_work_ = DeviceBuffer(size_t(attn_paged_work_floats(int(rows), int(c.Hq), nsplit)) * 4);
+        cattn_work_ = DeviceBuffer(size_t(attn_paged_work_floats(int(rows), int(c.Hq), nsplit, int(c.Dh))) * 4);
     }
     chunk_capacity_ = rows;
 }

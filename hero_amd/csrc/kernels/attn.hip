@@ -1123,10 +1123,11 @@ __device__ __forceinline__ uint16_t f32_to_f16_rne(float x) {
 
 __device__ __forceinline__ const int32_t* page_row(const AttnPagedArgs& p, int b) { return p.page_table + int64_t(p.a.shared_cache ? 0 : b) * p.max_pages; }
 
-// the fp16 row of position t, KV head g, K (kv = 0) or V (kv = 1)
+// the fp16 row of position t, KV head g, K (kv = 0) or V (kv = 1), in heads of DH
+template <int DH = kAttnDim>
 __device__ __forceinline__ int64_t page_offset(const AttnPagedArgs& p, const int32_t* pt, int t, int g, int kv) {
     const int64_t page = pt[t / p.page_size];
-    return ((page * 2 + kv) * p.a.Hkv + g) * int64_t(p.page_size) * kAttnDim + int64_t(t % p.page_size) * kAttnDim;
+    return ((page * 2 + kv) * p.a.Hkv + g) * int64_t(p.page_size) * DH + int64_t(t % p.page_size) * DH;
 }
 
 // Q8_0 pages: byte offsets of the int8 row and of its four fp16 scales
@@ -1149,7 +1150,8 @@ __device__ __forceinline__ int8_t q8_of_block(float x, uint16_t* dh) {
     return int8_t(int(roundf(x * id)));
 }
 
-__global__ __launch_bounds__(kAttnDim) void attn_paged_prep_kernel(AttnPagedArgs p) {
+template <int DH>
+__global__ __launch_bounds__(DH) void attn_paged_prep_kernel(AttnPagedArgs p) {
     const AttnDecodeArgs& a = p.a;
     const int j = threadIdx.x, h = blockIdx.x, b = blockIdx.y;
     const int group = a.Hq / a.Hkv;
@@ -1157,31 +1159,33 @@ __global__ __launch_bounds__(kAttnDim) void attn_paged_prep_kernel(AttnPagedArgs
     const int pos = a.positions[b];
     if (pos < 0 || pos >= p.max_pages * p.page_size) return;  // the host keeps positions in range
     const float* P = a.proj + int64_t(b) * a.proj_stride;
-    const float* cs = a.rope_cs + int64_t(pos) * kAttnDim;
-    __shared__ __align__(16) float buf[kAttnDim];
+    const float* cs = a.rope_cs + int64_t(pos) * DH;
+    __shared__ __align__(16) float buf[DH];
     __shared__ float scal[2];
-    const float q = norm_rope_head<kAttnDim>(P[int64_t(h) * 2 * kAttnDim + j], a.q_gamma, a.eps, cs, buf, scal, j);
-    a.q_rot[(int64_t(b) * a.Hq + h) * kAttnDim + j] = q;
+    const float q = norm_rope_head<DH>(P[int64_t(h) * 2 * DH + j], a.q_gamma, a.eps, cs, buf, scal, j);
+    a.q_rot[(int64_t(b) * a.Hq + h) * DH + j] = q;
     if (h % group == 0) {
-        const float k = norm_rope_head<kAttnDim>(P[a.k_off + int64_t(g) * kAttnDim + j], a.k_gamma, a.eps, cs, buf, scal, j);
-        const float v = P[a.v_off + int64_t(g) * kAttnDim + j];
+        const float k = norm_rope_head<DH>(P[a.k_off + int64_t(g) * DH + j], a.k_gamma, a.eps, cs, buf, scal, j);
+        const float v = P[a.v_off + int64_t(g) * DH + j];
         const int32_t* pt = page_row(p, b);
-        if (p.q8) {
-            uint8_t* pool = reinterpret_cast<uint8_t*>(p.pages);
-            const int64_t base = q8_page_base(p, pt, pos);
-            const int64_t scales = base + 2 * int64_t(a.Hkv) * p.page_size * kAttnDim;
-            uint16_t dk, dv;
-            const int8_t qk = q8_of_block(k, &dk), qv = q8_of_block(v, &dv);
-            pool[base + q8_row(p, pos, g, 0) * kAttnDim + j] = uint8_t(qk);
-            pool[base + q8_row(p, pos, g, 1) * kAttnDim + j] = uint8_t(qv);
-            if ((j & 31) == 0) {
-                reinterpret_cast<uint16_t*>(pool + scales)[q8_row(p, pos, g, 0) * 4 + j / 32] = dk;
-                reinterpret_cast<uint16_t*>(pool + scales)[q8_row(p, pos, g, 1) * 4 + j / 32] = dv;
+        if constexpr (DH == kAttnDim) {
+            if (p.q8) {
+                uint8_t* pool = reinterpret_cast<uint8_t*>(p.pages);
+                const int64_t base = q8_page_base(p, pt, pos);
+                const int64_t scales = base + 2 * int64_t(a.Hkv) * p.page_size * kAttnDim;
+                uint16_t dk, dv;
+                const int8_t qk = q8_of_block(k, &dk), qv = q8_of_block(v, &dv);
+                pool[base + q8_row(p, pos, g, 0) * kAttnDim + j] = uint8_t(qk);
+                pool[base + q8_row(p, pos, g, 1) * kAttnDim + j] = uint8_t(qv);
+                if ((j & 31) == 0) {
+                    reinterpret_cast<uint16_t*>(pool + scales)[q8_row(p, pos, g, 0) * 4 + j / 32] = dk;
+                    reinterpret_cast<uint16_t*>(pool + scales)[q8_row(p, pos, g, 1) * 4 + j / 32] = dv;
+                }
+                return;
             }
-        } else {
-            p.pages[page_offset(p, pt, pos, g, 0) + j] = f32_to_f16_rne(k);
-            p.pages[page_offset(p, pt, pos, g, 1) + j] = f32_to_f16_rne(v);
         }
+        p.pages[page_offset<DH>(p, pt, pos, g, 0) + j] = f32_to_f16_rne(k);
+        p.pages[page_offset<DH>(p, pt, pos, g, 1) + j] = f32_to_f16_rne(v);
     }
 }
 
@@ -1405,14 +1409,23 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnPagedArgs p) {
 // multiply-adds (four key quarters summed at the end). Keys of a page outside
 // the split [t0, t1) get no weight, and the rows past the newest position read
 // as zero (the pool may hold anything there).
-constexpr int kRgSlots = 4;
-constexpr int kRgSlot = kPgTile * kAttnDim * 2;  // bytes of one page's K (or V) block of one KV head
+template <int DH>
+constexpr int rg_slots() { return DH == 128 ? 4 : 3; }             // pages in flight per workgroup
+template <int DH>
+constexpr int rg_slot() { return kPgTile * DH * 2; }               // bytes of one page's K (or V) block of one KV head
 
+template <int DH>
 size_t attn_split_ring_smem(int Gs, int split) {
-    return size_t(kRgSlots) * kRgSlot + size_t(Gs) * kAttnDim * 4 + size_t(Gs) * (split / kPgTile + 1) * kPgTile * 4;
+    return size_t(rg_slots<DH>()) * rg_slot<DH>() + size_t(Gs) * DH * 4 + size_t(Gs) * (split / kPgTile + 1) * kPgTile * 4;
 }
 
+template <int DH>
 __global__ __launch_bounds__(256) void attn_split_ring_kernel(AttnPagedArgs p) {
+    constexpr int kSlots = rg_slots<DH>(), kSlot = rg_slot<DH>();
+    constexpr int kLoads = kSlot / (256 * 16);  // 16-byte loads per lane per block
+    constexpr int CQ = DH / 32;                 // 16-byte chunks of a key's channel quarter
+    constexpr int HP = DH == 128 ? 4 : 2;       // query heads per pass (their quarters in registers)
+    constexpr int CPL = DH / 64;                // channels per lane in the weighted sum
     const AttnDecodeArgs& a = p.a;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int g = blockIdx.x, sp = blockIdx.y, b = blockIdx.z;
@@ -1421,7 +1434,7 @@ __global__ __launch_bounds__(256) void attn_split_ring_kernel(AttnPagedArgs p) {
     if (pos < 0 || pos >= p.max_pages * p.page_size) return;
     const int first = visible_first(pos, a.window);
     const int t0 = first + sp * p.split, t1 = min(pos + 1, t0 + p.split);
-    const int64_t rec = 2 + kAttnDim;
+    const int64_t rec = 2 + DH;
     float* out = p.work + ((int64_t(b) * a.Hq + int64_t(g) * Gs) * p.nsplit + sp) * rec;  // head h of the group: + h * nsplit * rec
     const int64_t hstride = int64_t(p.nsplit) * rec;
     if (t0 >= t1) {  // nothing visible in this split
@@ -1432,12 +1445,11 @@ __global__ __launch_bounds__(256) void attn_split_ring_kernel(AttnPagedArgs p) {
     const int nblk = 2 * np;                                          // their K blocks, then their V blocks
     const int32_t* pt = page_row(p, b);
     extern __shared__ __align__(16) float rg_smem[];
-    uint8_t* ring = reinterpret_cast<uint8_t*>(rg_smem);                                   // [kRgSlots][16 KB]
-    float* qs = reinterpret_cast<float*>(ring + kRgSlots * kRgSlot);                        // [Gs][128]
-    float* sc0 = qs + Gs * kAttnDim;                                                        // [Gs][np * 64]
+    uint8_t* ring = reinterpret_cast<uint8_t*>(rg_smem);                  // [kSlots][kSlot]
+    float* qs = reinterpret_cast<float*>(ring + kSlots * kSlot);          // [Gs][DH]
+    float* sc0 = qs + Gs * DH;                                             // [Gs][np * 64]
     const int sstride = np * kPgTile;
     auto sc = [&](int h) { return sc0 + h * sstride; };
-
     // The pool page of each page the split touches (np <= 9) and expf's table
     // go to shared memory before any ring load: a global read issued after the
     // ring loads (the compiler cannot see them) would wait for all of them.
@@ -1447,45 +1459,46 @@ __global__ __launch_bounds__(256) void attn_split_ring_kernel(AttnPagedArgs p) {
     fill_exp_table(etab, tid);
     __syncthreads();
     const ExpTab et{etab};
-    // block i of the split into slot i % kRgSlots: wave w's four loads move
-    // 1 KB pieces 4w .. 4w + 3 of the block, lane by lane
+    // block i of the split into slot i % kSlots: wave w's loads move the 1 KB
+    // pieces kLoads w .. kLoads w + kLoads - 1 of the block, lane by lane
     auto issue = [&](int i) {
         const int kv = i < np ? 0 : 1;
         const int64_t page = pages_sh[i < np ? i : i - np];
-        const uint8_t* src = reinterpret_cast<const uint8_t*>(p.pages) + ((page * 2 + kv) * a.Hkv + g) * int64_t(kRgSlot);
-        const uint32_t dst = lds_offset(ring + (i % kRgSlots) * kRgSlot);
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(p.pages) + ((page * 2 + kv) * a.Hkv + g) * int64_t(kSlot);
+        const uint32_t dst = lds_offset(ring + (i % kSlots) * kSlot);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) lds_dma_b128(src + ((wv * 4 + u) * 64 + lane) * 16, dst + (wv * 4 + u) * 1024);
+        for (int u = 0; u < kLoads; ++u) lds_dma_b128(src + ((wv * kLoads + u) * 64 + lane) * 16, dst + (wv * kLoads + u) * 1024);
     };
     // the group's rotated queries, through the same path, issued first
-    if (tid < Gs * kAttnDim / 4) lds_dma_b128(a.q_rot + (int64_t(b) * a.Hq + int64_t(g) * Gs) * kAttnDim + 4 * tid, lds_offset(qs + 4 * (tid & ~63)));
+    for (int e = tid; e < Gs * DH / 4; e += 256)
+        lds_dma_b128(a.q_rot + (int64_t(b) * a.Hq + int64_t(g) * Gs) * DH + 4 * e, lds_offset(qs + 4 * (e & ~63)));
     int issued = 0;  // blocks issued so far (uniform)
-    for (; issued < kRgSlots && issued < nblk; ++issued) issue(issued);
+    for (; issued < kSlots && issued < nblk; ++issued) issue(issued);
     // block i has landed everywhere: this wave's loads of the blocks issued
-    // after it may still be in flight (four per block), then the barrier
+    // after it may still be in flight (kLoads per block), then the barrier
     auto wait_block = [&](int i) {
         switch (issued - i - 1) {
-            case 3: wait_vmcnt<12>(); break;
-            case 2: wait_vmcnt<8>(); break;
-            case 1: wait_vmcnt<4>(); break;
+            case 3: wait_vmcnt<3 * kLoads>(); break;
+            case 2: wait_vmcnt<2 * kLoads>(); break;
+            case 1: wait_vmcnt<kLoads>(); break;
             default: wait_vmcnt<0>(); break;
         }
         __syncthreads();
     };
 
-    // ---- scores: lane (key kr of the page, channel quarter qq), four query
-    // heads at a time with their quarter in registers. The lane visits its
-    // four 16-byte chunks from a key-dependent one (no bank conflicts), and
-    // its query registers hold chunk (u + kr) & 3 in slot u ----
+    // ---- scores: lane (key kr of the page, channel quarter qq), HP query
+    // heads at a time with their quarter in registers. The lane visits its CQ
+    // 16-byte chunks from a key-dependent one (few bank conflicts), and its
+    // query registers hold chunk (u + kr) % CQ in slot u ----
     const int qq = lane & 3, kr = wv * 16 + (lane >> 2);
-    float qv[4][32];
+    float qv[HP][DH / 4];
     auto load_q = [&](int hp) {
 #pragma unroll
-        for (int hh = 0; hh < 4; ++hh) {
+        for (int hh = 0; hh < HP; ++hh) {
             if (hp + hh < Gs) {
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const float4* q4 = reinterpret_cast<const float4*>(qs + (hp + hh) * kAttnDim + 32 * qq + 8 * ((u + kr) & 3));
+                for (int u = 0; u < CQ; ++u) {
+                    const float4* q4 = reinterpret_cast<const float4*>(qs + (hp + hh) * DH + (DH / 4) * qq + 8 * ((u + kr) % CQ));
                     const float4 qa = q4[0], qb = q4[1];
                     qv[hh][8 * u] = qa.x, qv[hh][8 * u + 1] = qa.y, qv[hh][8 * u + 2] = qa.z, qv[hh][8 * u + 3] = qa.w;
                     qv[hh][8 * u + 4] = qb.x, qv[hh][8 * u + 5] = qb.y, qv[hh][8 * u + 6] = qb.z, qv[hh][8 * u + 7] = qb.w;
@@ -1496,15 +1509,17 @@ __global__ __launch_bounds__(256) void attn_split_ring_kernel(AttnPagedArgs p) {
     for (int i = 0; i < np; ++i) {
         wait_block(i);
         if (issued < nblk && i > 0) issue(issued++);  // into the slot the previous block left
-        const uint8_t* blk = ring + (i % kRgSlots) * kRgSlot + kr * (kAttnDim * 2);
+        const uint8_t* blk = ring + (i % kSlots) * kSlot + kr * (DH * 2);
         const int t = (pg0 + i) * kPgTile + kr;
         const bool live = t >= t0 && t < t1;
-        for (int hp = 0; hp < Gs; hp += 4) {
-            if (i == 0 || Gs > 4) load_q(hp);
-            float dot[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int hp = 0; hp < Gs; hp += HP) {
+            if (i == 0 || Gs > HP) load_q(hp);
+            float dot[HP];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint4 w = *reinterpret_cast<const uint4*>(blk + (4 * qq + ((u + kr) & 3)) * 16);
+            for (int hh = 0; hh < HP; ++hh) dot[hh] = 0.f;
+#pragma unroll
+            for (int u = 0; u < CQ; ++u) {
+                const uint4 w = *reinterpret_cast<const uint4*>(blk + (CQ * qq + ((u + kr) % CQ)) * 16);
                 const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
                 float kx[8];
 #pragma unroll
@@ -1513,12 +1528,12 @@ __global__ __launch_bounds__(256) void attn_split_ring_kernel(AttnPagedArgs p) {
                     kx[2 * e + 1] = half_bits_to_f32(uint16_t(wd[e] >> 16));
                 }
 #pragma unroll
-                for (int hh = 0; hh < 4; ++hh)
+                for (int hh = 0; hh < HP; ++hh)
 #pragma unroll
                     for (int e = 0; e < 8; ++e) dot[hh] = fmaf(qv[hh][8 * u + e], kx[e], dot[hh]);
             }
 #pragma unroll
-            for (int hh = 0; hh < 4; ++hh) {
+            for (int hh = 0; hh < HP; ++hh) {
                 if (hp + hh < Gs) {
                     float d = dot[hh];
                     d += __shfl_xor(d, 1);
@@ -1547,14 +1562,17 @@ __global__ __launch_bounds__(256) void attn_split_ring_kernel(AttnPagedArgs p) {
             out[h * hstride + 1] = l;
         }
     }
-    // ---- weighted sum: lane (channel pair 2 lane, 2 lane + 1), keys 16 wv .. +15 of each page ----
-    float o[kAttnMaxGroup][2];
+    // ---- weighted sum: lane (channels CPL lane .. CPL lane + CPL - 1), keys
+    // 16 wv .. +15 of each page ----
+    float o[kAttnMaxGroup][CPL];
 #pragma unroll
-    for (int h = 0; h < kAttnMaxGroup; ++h) o[h][0] = o[h][1] = 0.f;
+    for (int h = 0; h < kAttnMaxGroup; ++h)
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) o[h][e] = 0.f;
     for (int i = np; i < nblk; ++i) {
         wait_block(i);  // its barrier also publishes the weights (first V block)
         if (issued < nblk) issue(issued++);  // into the slot block i - 1 left
-        const uint8_t* blk = ring + (i % kRgSlots) * kRgSlot;
+        const uint8_t* blk = ring + (i % kSlots) * kSlot;
         const int jb = (i - np) * kPgTile + wv * 16;  // the wave's first key of the page (weight index)
         const int tb = (pg0 + i - np) * kPgTile + wv * 16;
 #pragma unroll
@@ -1565,37 +1583,48 @@ __global__ __launch_bounds__(256) void attn_split_ring_kernel(AttnPagedArgs p) {
                 if (h < Gs) w[h] = *reinterpret_cast<const float4*>(sc(h) + jb + j4);
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const uint32_t dw = *reinterpret_cast<const uint32_t*>(blk + (wv * 16 + j4 + u) * (kAttnDim * 2) + lane * 4);
+                const uint8_t* row = blk + (wv * 16 + j4 + u) * (DH * 2) + lane * (2 * CPL);
+                uint32_t dw[CPL / 2];
+                if constexpr (CPL == 2) {
+                    dw[0] = *reinterpret_cast<const uint32_t*>(row);
+                } else {
+                    const uint2 d2 = *reinterpret_cast<const uint2*>(row);
+                    dw[0] = d2.x, dw[1] = d2.y;
+                }
                 const bool live = tb + j4 + u < t1;
-                const float v0 = live ? half_bits_to_f32(uint16_t(dw & 0xFFFFu)) : 0.f;
-                const float v1 = live ? half_bits_to_f32(uint16_t(dw >> 16)) : 0.f;
+                float v[CPL];
+#pragma unroll
+                for (int e = 0; e < CPL / 2; ++e) {
+                    v[2 * e] = live ? half_bits_to_f32(uint16_t(dw[e] & 0xFFFFu)) : 0.f;
+                    v[2 * e + 1] = live ? half_bits_to_f32(uint16_t(dw[e] >> 16)) : 0.f;
+                }
 #pragma unroll
                 for (int h = 0; h < kAttnMaxGroup; ++h) {
                     if (h < Gs) {
                         const float wu = u == 0 ? w[h].x : u == 1 ? w[h].y : u == 2 ? w[h].z : w[h].w;
-                        o[h][0] = fmaf(wu, v0, o[h][0]);
-                        o[h][1] = fmaf(wu, v1, o[h][1]);
+#pragma unroll
+                        for (int e = 0; e < CPL; ++e) o[h][e] = fmaf(wu, v[e], o[h][e]);
                     }
                 }
             }
         }
     }
     __syncthreads();  // every wave is done with the ring: it holds the key quarters' sums now
-    float* red = reinterpret_cast<float*>(ring);  // [4][Gs][128]
+    float* red = reinterpret_cast<float*>(ring);  // [4][Gs][DH]
 #pragma unroll
     for (int h = 0; h < kAttnMaxGroup; ++h) {
         if (h < Gs) {
-            red[(wv * Gs + h) * kAttnDim + 2 * lane] = o[h][0];
-            red[(wv * Gs + h) * kAttnDim + 2 * lane + 1] = o[h][1];
+#pragma unroll
+            for (int e = 0; e < CPL; ++e) red[(wv * Gs + h) * DH + CPL * lane + e] = o[h][e];
         }
     }
     __syncthreads();
-    for (int e = tid; e < Gs * kAttnDim; e += 256) {
-        const int h = e / kAttnDim, c = e % kAttnDim;
-        float v = red[(0 * Gs + h) * kAttnDim + c];
-        v += red[(1 * Gs + h) * kAttnDim + c];
-        v += red[(2 * Gs + h) * kAttnDim + c];
-        v += red[(3 * Gs + h) * kAttnDim + c];
+    for (int e = tid; e < Gs * DH; e += 256) {
+        const int h = e / DH, c = e % DH;
+        float v = red[(0 * Gs + h) * DH + c];
+        v += red[(1 * Gs + h) * DH + c];
+        v += red[(2 * Gs + h) * DH + c];
+        v += red[(3 * Gs + h) * DH + c];
         out[h * hstride + 2 + c] = v;
     }
 }
@@ -1603,26 +1632,27 @@ __global__ __launch_bounds__(256) void attn_split_ring_kernel(AttnPagedArgs p) {
 // One workgroup per (query head, row): merge the splits, then the gate
 // (qwen35.hpp:390-393) and the Q8_0 quantization for W_o. Lane (channel c,
 // split group sg of 4) adds its channel over splits sg, sg + 4, ... with all
-// of its record reads issued at once (up to kCombineLanesSplits per pass);
-// the four groups' partial sums are then added in group order.
+// of its record reads issued at once (kCombinePass per pass); the four
+// groups' partial sums are then added in group order.
 constexpr int kCombineGroups = 4;
 constexpr int kCombinePass = 16;  // splits per lane per pass
-__global__ __launch_bounds__(kAttnDim * kCombineGroups) void attn_combine_kernel(AttnPagedArgs p) {
+template <int DH>
+__global__ __launch_bounds__(DH * kCombineGroups) void attn_combine_kernel(AttnPagedArgs p) {
     const AttnDecodeArgs& a = p.a;
-    const int tid = threadIdx.x, c = tid % kAttnDim, sg = tid / kAttnDim, h = blockIdx.x, b = blockIdx.y;
+    const int tid = threadIdx.x, c = tid % DH, sg = tid / DH, h = blockIdx.x, b = blockIdx.y;
     const int pos = a.positions[b];
     if (pos < 0 || pos >= p.max_pages * p.page_size) return;
-    const int64_t rec = 2 + kAttnDim;
+    const int64_t rec = 2 + DH;
     const float* w = p.work + (int64_t(b) * a.Hq + h) * p.nsplit * rec;
-    __shared__ float red[kAttnDim * kCombineGroups / 64];
-    __shared__ float part[kCombineGroups][2][kAttnDim];
+    __shared__ float red[DH * kCombineGroups / 64];
+    __shared__ float part[kCombineGroups][2][DH];
     float mloc = -INFINITY;
-    for (int s = tid; s < p.nsplit; s += kAttnDim * kCombineGroups) mloc = fmaxf(mloc, w[s * rec]);
+    for (int s = tid; s < p.nsplit; s += DH * kCombineGroups) mloc = fmaxf(mloc, w[s * rec]);
     for (int off = 32; off > 0; off >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, off));
     if ((tid & 63) == 0) red[tid >> 6] = mloc;
     __syncthreads();
     float m = red[0];
-    for (int i = 1; i < kAttnDim * kCombineGroups / 64; ++i) m = fmaxf(m, red[i]);
+    for (int i = 1; i < DH * kCombineGroups / 64; ++i) m = fmaxf(m, red[i]);
     float l = 0.f, o = 0.f;
     for (int base = sg; base < p.nsplit; base += kCombineGroups * kCombinePass) {
         float mv[kCombinePass], lv[kCombinePass], ov[kCombinePass];
@@ -1652,10 +1682,10 @@ __global__ __launch_bounds__(kAttnDim * kCombineGroups) void attn_combine_kernel
         l += part[g2][0][c];
         o += part[g2][1][c];
     }
-    const float gate = a.proj[int64_t(b) * a.proj_stride + int64_t(h) * 2 * kAttnDim + kAttnDim + c];
+    const float gate = a.proj[int64_t(b) * a.proj_stride + int64_t(h) * 2 * DH + DH + c];
     const float out = (o / l) * sigmoid_f32(gate);
-    const int64_t width = int64_t(a.Hq) * kAttnDim;
-    const int64_t idx = int64_t(h) * kAttnDim + c;
+    const int64_t width = int64_t(a.Hq) * DH;
+    const int64_t idx = int64_t(h) * DH + c;
     if (a.out_f32) a.out_f32[int64_t(b) * width + idx] = out;
     float amax = fabsf(out);
     for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
@@ -1677,24 +1707,30 @@ void attn_paged_plan(int64_t max_ctx, int window, int B, int Hkv, int* split, in
     *nsplit = int((vis + sp - 1) / sp);
 }
 
-int64_t attn_paged_work_floats(int B, int Hq, int nsplit) { return int64_t(B) * Hq * nsplit * (2 + kAttnDim); }
+int64_t attn_paged_work_floats(int B, int Hq, int nsplit, int Dh) { return int64_t(B) * Hq * nsplit * (2 + Dh); }
 
 void launch_attn_paged(const AttnPagedArgs& p, hipStream_t s) {
     const AttnDecodeArgs& a = p.a;
-    hipLaunchKernelGGL(attn_paged_prep_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, p);
     const int Gs = a.Hq / a.Hkv;
+    if (a.Dh == 256) {  // fp16 pages of 64 positions (the host checks): the page-streaming form for any B
+        hipLaunchKernelGGL(attn_paged_prep_kernel<256>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(256), 0, s, p);
+        hipLaunchKernelGGL(attn_split_ring_kernel<256>, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), attn_split_ring_smem<256>(Gs, p.split), s, p);
+        hipLaunchKernelGGL(attn_combine_kernel<256>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(256 * kCombineGroups), 0, s, p);
+        return;
+    }
+    hipLaunchKernelGGL(attn_paged_prep_kernel<kAttnDim>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim), 0, s, p);
     const size_t smem = size_t(Gs) * (2 * kAttnDim + size_t(p.split)) * 4;
     // the page-streaming form for one or two sequences (the pages of a split
     // in flight at once); with more sequences the grid alone keeps enough
     // loads in flight, and the per-key form, with more workgroups per CU,
     // streams faster (32k context, 16 sequences: 536 vs 727 us)
     if (!p.q8 && p.page_size == kPgTile && a.B <= 2)
-        hipLaunchKernelGGL(attn_split_ring_kernel, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), attn_split_ring_smem(Gs, p.split), s, p);
+        hipLaunchKernelGGL(attn_split_ring_kernel<kAttnDim>, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), attn_split_ring_smem<kAttnDim>(Gs, p.split), s, p);
     else if (p.q8)
         hipLaunchKernelGGL(attn_split_kernel<true>, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), smem, s, p);
     else
         hipLaunchKernelGGL(attn_split_kernel<false>, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), smem, s, p);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim * kCombineGroups), 0, s, p);
+    hipLaunchKernelGGL(attn_combine_kernel<kAttnDim>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim * kCombineGroups), 0, s, p);
 }
 
 namespace {

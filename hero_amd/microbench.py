@@ -478,7 +478,7 @@ def bench_attn(lib, replays: int = 20, contexts=ATTN_CTX, batches=ATTN_BATCH, ca
                       for _ in range(max(1, min(16, math.ceil(512e6 / (cache_bytes // 2)))) if "fp16" in caches_run else 0)]
             table = t.arange(B * max_pages, dtype=t.int32, device="cuda")
             for name, window, sc in [v for v in (("full", 0, scale), ("swa1024", 1024, 1.0)) if v[0] in variants] if pages else ():
-                wbytes = lib.hero_attn_paged_work_bytes(ctx, window, B, hq, hkv)
+                wbytes = lib.hero_attn_paged_work_bytes(ctx, window, B, hq, hkv, dh)
                 work = _bytes(wbytes)
                 args = []
                 for pg in pages:
@@ -502,7 +502,7 @@ def bench_attn(lib, replays: int = 20, contexts=ATTN_CTX, batches=ATTN_BATCH, ca
             t.cuda.empty_cache()
             # the same over Q8_0 pages: int8 rows (random) and fp16 block
             # scales of the inputs' size (|N(0,1)|/sqrt(128) max / 127)
-            pb = lib.hero_attn_page_bytes(hkv, page, 1)
+            pb = lib.hero_attn_page_bytes(hkv, dh, page, 1)
             pages8 = []
             for _ in range(max(1, min(16, math.ceil(512e6 / (B * max_pages * pb)))) if "q8" in caches_run else 0):
                 pg = t.randint(-127, 128, (B * max_pages, pb), dtype=t.int8, device="cuda", generator=gen).view(t.uint8)
@@ -511,7 +511,7 @@ def bench_attn(lib, replays: int = 20, contexts=ATTN_CTX, batches=ATTN_BATCH, ca
                 pg[:, q_bytes:] = d.view(t.uint8)
                 pages8.append(pg.contiguous())
             for name, window, sc in [v for v in (("full", 0, scale), ("swa1024", 1024, 1.0)) if v[0] in variants] if pages8 else ():
-                wbytes = lib.hero_attn_paged_work_bytes(ctx, window, B, hq, hkv)
+                wbytes = lib.hero_attn_paged_work_bytes(ctx, window, B, hq, hkv, dh)
                 work = _bytes(wbytes)
                 args = []
                 for pg in pages8:

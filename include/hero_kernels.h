@@ -317,8 +317,10 @@ typedef struct hero_attn_paged_args {
     int64_t work_bytes;
     int32_t q8;
 } hero_attn_paged_args;
-int64_t hero_attn_page_bytes(int32_t hkv, int32_t page_size, int32_t q8);
-int64_t hero_attn_paged_work_bytes(int64_t max_ctx, int32_t window, int32_t b, int32_t hq, int32_t hkv);
+/* Bytes of one page (head_dim 128 or 256; Q8_0 pages for 128 only) and of
+ * the split workspace. Heads of 256 channels take fp16 pages of 64 positions. */
+int64_t hero_attn_page_bytes(int32_t hkv, int32_t head_dim, int32_t page_size, int32_t q8);
+int64_t hero_attn_paged_work_bytes(int64_t max_ctx, int32_t window, int32_t b, int32_t hq, int32_t hkv, int32_t head_dim);
 
 /* Measurement (no counterpart in the reference): `workgroups` workgroups of
  * 256 lanes read `bytes` of p (a multiple of 16, 16-byte aligned) with 16-byte

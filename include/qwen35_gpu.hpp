@@ -39,9 +39,10 @@ template <class C>
 class GpuQwen35Model {
 public:
     static constexpr size_t D = C::D, V = C::V, CTX = C::CTX;
-    // a device state holds at most this many positions (the RoPE table and
-    // the K/V caches are sized to it when the state is created)
-    static constexpr size_t kMaxStateTokens = 65536;
+    // positions of a device state when the caller names none (the K/V caches
+    // are sized to a state's positions when it is created; any count up to
+    // C::CTX may be asked for)
+    static constexpr size_t kDefaultStateTokens = 65536;
 
     // The carried state. PrefixCache owns it by value and forgets it by
     // assigning a fresh one (transformer.hpp:155), so it is
@@ -63,10 +64,10 @@ public:
     };
 
     // max_tokens: the context of the states this model creates, at most
-    // min(C::CTX, kMaxStateTokens); 0 takes that maximum.
+    // C::CTX; 0 takes min(C::CTX, kDefaultStateTokens).
     explicit GpuQwen35Model(const std::string& gguf_path, size_t max_tokens = 0)
-        : max_tokens_(max_tokens ? max_tokens : std::min(CTX, kMaxStateTokens)) {
-        if (max_tokens_ > std::min(CTX, kMaxStateTokens)) throw std::invalid_argument("GpuQwen35Model: max_tokens above the supported context");
+        : max_tokens_(max_tokens ? max_tokens : std::min(CTX, kDefaultStateTokens)) {
+        if (max_tokens_ > CTX) throw std::invalid_argument("GpuQwen35Model: max_tokens above the model's context");
         hero_model* m = nullptr;
         hero_throw(hero_model_open(gguf_path.c_str(), &m));
         model_.reset(m);

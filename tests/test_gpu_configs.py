@@ -260,7 +260,8 @@ def attn_expect(proj_b, keys_b, vals_b, qg, kg, inv, pos, window, scale, fp16):
     return (att * oracle.sigmoid(g)).astype(np.float32)
 
 
-ATTN_CASES = [(1, 1024), (16, 1024), (1, 8192), (16, 8192), (1, 32768), (16, 32768), (3, 9000)]
+# (1, 70000), (2, 66000): contexts past 65536 positions (the reference's CTX is 262144)
+ATTN_CASES = [(1, 1024), (16, 1024), (1, 8192), (16, 8192), (1, 32768), (16, 32768), (3, 9000), (1, 70000), (2, 66000)]
 
 
 @pytest.mark.timeout(900)
@@ -331,7 +332,7 @@ def test_attn_baseline_sizes_match_oracle(lib, B, ctx):
     keys16 = keys.astype(np.float16).astype(np.float32)
     vals16 = vals.astype(np.float16).astype(np.float32)
     for window, scale in VARIANTS:
-        wbytes = lib.hero_attn_paged_work_bytes(max_pages * page, window, B, hq, hkv)
+        wbytes = lib.hero_attn_paged_work_bytes(max_pages * page, window, B, hq, hkv, dh)
         d_work = empty(wbytes)
         a = AttnDecodeArgs(ptr(d_proj), stride, 2 * qw, 2 * qw + kw, ptr(d_qg), ptr(d_kg), eps, ptr(d_cs), None, None,
                            0, ptr(d_pos), None, ptr(d_qr), scale, window, ptr(act), ptr(out), B, hq, hkv, dh)
@@ -387,7 +388,7 @@ def test_attn_q8_pages_match_oracle(lib, B, ctx):
     d_qr = empty(B * hq * dh * 4)
     page = 64
     max_pages = (ctx + page - 1) // page
-    page_bytes = lib.hero_attn_page_bytes(hkv, page, 1)
+    page_bytes = lib.hero_attn_page_bytes(hkv, dh, page, 1)
     assert page_bytes == 2 * hkv * page * (dh + 8)
     table = rng.permutation(B * max_pages).astype(np.int32).reshape(B, max_pages)
     pool = np.zeros((B * max_pages, page_bytes), np.uint8)
@@ -406,7 +407,7 @@ def test_attn_q8_pages_match_oracle(lib, B, ctx):
         del qp, sp
     d_pages, d_table = dev(pool), dev(table)
     for window, scale in VARIANTS:
-        wbytes = lib.hero_attn_paged_work_bytes(max_pages * page, window, B, hq, hkv)
+        wbytes = lib.hero_attn_paged_work_bytes(max_pages * page, window, B, hq, hkv, dh)
         d_work = empty(wbytes)
         a = AttnDecodeArgs(ptr(d_proj), stride, 2 * qw, 2 * qw + kw, ptr(d_qg), ptr(d_kg), eps, ptr(d_cs), None, None,
                            0, ptr(d_pos), None, ptr(d_qr), scale, window, ptr(act), ptr(out), B, hq, hkv, dh)

@@ -552,8 +552,8 @@ def test_attn_decode_matches_oracle(lib, window):
     kg = (1 + 0.1 * rng.standard_normal(dh)).astype(np.float32)
     eps = np.float32(1e-6)
     scale = np.float32(1.0) / np.sqrt(np.float32(dh))
-    inv = oracle.rope_inv_freq(dh, 1e6, 32)
-    d_cs = dev(oracle.rope_table(dh, 1e6, 32, max_ctx))  # the reference's own cos/sin values
+    inv = oracle.rope_inv_freq(dh, 1e6, dh // 4)
+    d_cs = dev(oracle.rope_table(dh, 1e6, dh // 4, max_ctx))  # the reference's own cos/sin values
     d_kc, d_vc = empty(B * max_ctx * kw * 4), empty(B * max_ctx * kw * 4)
     d_sc = empty(B * hq * max_ctx * 4)
     d_qr = empty(B * hq * dh * 4)
@@ -704,13 +704,15 @@ def test_attn_prefill_rows_match_oracle(lib, M, p0, hq, hkv, max_ctx, window, dh
         assert blocks[b].tobytes() == oracle.quantize_row_q8_0(got[b]).tobytes(), f"row {b}"
 
 
-@pytest.mark.parametrize("hq,window,page", [(8, 0, 16), (8, 50, 16), (16, 0, 16), (8, 0, 64), (8, 50, 64), (8, 70, 64), (16, 0, 64)])
-def test_attn_paged_fp16_matches_oracle_over_fp16_kv(lib, hq, window, page):
+@pytest.mark.parametrize("hq,window,page,dh", [(8, 0, 16, 128), (8, 50, 16, 128), (16, 0, 16, 128), (8, 0, 64, 128), (8, 50, 64, 128),
+                                                (8, 70, 64, 128), (16, 0, 64, 128), (8, 0, 64, 256), (8, 70, 64, 256), (16, 50, 64, 256)])
+def test_attn_paged_fp16_matches_oracle_over_fp16_kv(lib, hq, window, page, dh):
     """Split-K attention over the paged fp16 cache: pages of 16 positions (the
     per-key kernel: several pages per tile) or 64 (the page-streaming kernel:
     splits that start and end inside a page) in a shuffled pool, contexts up to
     300 (several splits), 4 and 8 query heads per KV head, full and windowed
-    (windows of 50 and 70: splits not aligned to pages). The oracle
+    (windows of 50 and 70: splits not aligned to pages), heads of 128 and of
+    256 channels (the reference's Qwen 3.5 4B / 9B width). The oracle
     attends over the same K/V rounded to fp16 (its storage), sequentially; the
     split kernel sums dot products by channel quarters with fused multiply-adds
     and merges the split softmax in another order, so the outputs agree within
@@ -718,8 +720,8 @@ def test_attn_paged_fp16_matches_oracle_over_fp16_kv(lib, hq, window, page):
     quantized W_o input is the quantization of the kernel's own output."""
     from hero_amd._lib import AttnDecodeArgs, AttnPagedArgs
 
-    rng = np.random.default_rng(23 + hq + window + page)
-    B, hkv, dh, steps = 2, 2, 128, 300
+    rng = np.random.default_rng(23 + hq + window + page + dh)
+    B, hkv, steps = 2, 2, 300
     max_pages = (320 + page - 1) // page
     max_ctx = page * max_pages
     qw, kw = hq * dh, hkv * dh
@@ -733,7 +735,7 @@ def test_attn_paged_fp16_matches_oracle_over_fp16_kv(lib, hq, window, page):
     table = rng.permutation(B * max_pages).astype(np.int32).reshape(B, max_pages)
     d_table = dev(table)
     d_pages = empty(B * max_pages * 2 * hkv * page * dh * 2)
-    wbytes = lib.hero_attn_paged_work_bytes(max_ctx, window, B, hq, hkv)
+    wbytes = lib.hero_attn_paged_work_bytes(max_ctx, window, B, hq, hkv, dh)
     d_work = empty(wbytes)
     d_qr = empty(B * qw * 4)
     act = empty(lib.hero_q8_0_act_bytes(B, qw))

@@ -395,6 +395,53 @@ def test_dh256_model_matches_reference(dh256_gguf, dh256_golden):
         m.close()
 
 
+def test_dh256_fp16_paged_cache_matches_oracle_over_fp16_kv(dh256_gguf, dh256_golden):
+    """The fp16 paged cache with 256-wide heads (the reference's Qwen 3.5 4B /
+    9B attention width) on the whole model: against the oracle with its
+    fp16-cache switch on, a 24-token prefill and 24 decode passes give the
+    same greedy ids with the last logits within 1e-2 abs / 1e-3 rel; a
+    1100-token prefill (two chunks) agrees likewise; and a 3-sequence batch
+    state gives sequence 1 the results of its own state bit for bit."""
+    import oracle
+
+    m = hero_amd.Qwen35Model.open(dh256_gguf)
+    ref = oracle.Model(path=dh256_gguf)
+    try:
+        ref.set_kv_fp16(True)
+        prompt = dh256_golden["prompt"]
+        steps = 24
+        ref_ids, ref_last, _, _ = ref.greedy(prompt, steps)
+        st = m.new_state(2048, kv_fp16=True)
+        first = m.forward(st, ids=prompt)
+        ids, last = m.decode_greedy(st, first.argmax(), steps, want_logits=True)
+        assert [first.argmax()] + [int(v) for v in ids[:-1]] == [int(v) for v in ref_ids[:-1]]
+        report("dh256 fp16 cache", last.values, ref_last)
+        assert np.all(close(last.values, ref_last))
+        st.close()
+        long_prompt = np.random.default_rng(9).integers(0, m.V, 1100).astype(np.int32)
+        ref.reset()
+        expect = ref.forward_ids(long_prompt)
+        st = m.new_state(2048, kv_fp16=True)
+        got = m.forward(st, ids=long_prompt).values
+        report("dh256 fp16 cache, 1100-token prefill", got, expect)
+        assert np.all(close(got, expect)) and int(np.argmax(got)) == int(np.argmax(expect))
+        st.close()
+        bs = m.new_batch_state(1024, 3, kv_fp16=True)
+        short = np.random.default_rng(7).integers(0, m.V, 5).astype(np.int32)
+        firsts = [m.forward_seq(bs, b, ids=p).argmax() for b, p in enumerate((short, prompt, short[:2]))]
+        out, logits = m.decode_batch(bs, firsts, 8, want_logits=True)
+        st2 = m.new_state(1024, kv_fp16=True)
+        f1 = m.forward(st2, ids=prompt).argmax()
+        ids2, lg2 = m.decode_greedy(st2, f1, 8, want_logits=True)
+        assert np.array_equal(out[:, 1], ids2)
+        assert np.array_equal(bits(logits[1]), bits(lg2.values))
+        bs.close()
+        st2.close()
+    finally:
+        ref.close()
+        m.close()
+
+
 def test_qwen35_4b_shape_matches_oracle(tmp_path):
     """The reference's Qwen 3.5 4B config at 4 layers and a small vocabulary
     (nm/src/qwen35.hpp:25-56): d_model 2560 (K = 2560 matvecs; Hq * Dh = 4096

@@ -374,17 +374,40 @@ def bench_gdn(lib, replays: int = 50):
     rows = []
     H, W, dk = 16, 4, 128
     for B in (1, 8, 32):
-        a, bufs = _gdn_case(lib, H, H, B, W, gen)
-        for step in range(64):  # a seeded non-zero state
-            bufs["pos"].fill_(step)
-            check(lib.hero_gdn_decode(a, _stream()))
-        bufs["pos"].fill_(64)
-        sec = _time_graph(lambda: check(lib.hero_gdn_decode(a, _stream())), 1, replays)
+        # state copies enough that a replay reads the states cold (>= 512 MB,
+        # more than the 256 MB last-level cache)
+        copies = max(1, min(64, math.ceil(512e6 / (B * H * dk * dk * 4))))
+        cases = [_gdn_case(lib, H, H, B, W, gen) for _ in range(copies)]
+        for a, bufs in cases:
+            for step in range(64):  # a seeded non-zero state
+                bufs["pos"].fill_(step)
+                check(lib.hero_gdn_decode(a, _stream()))
+            bufs["pos"].fill_(64)
+        o_raw = t.empty(B * H * dk, device="cuda")
+        gates = t.empty(B * H * dk, device="cuda")
+
+        def fused():
+            for a, _ in cases:
+                check(lib.hero_gdn_decode(a, _stream()))
+
+        def cols():
+            for a, _ in cases:
+                check(lib.hero_gdn_decode_cols(a, _p(o_raw), _p(gates), _stream()))
+
+        def cols_norm():
+            for a, _ in cases:
+                check(lib.hero_gdn_decode_cols(a, _p(o_raw), None, _stream()))
+                check(lib.hero_gdn_norm_gate(_p(o_raw), a, _stream()))
+
         nbytes = B * H * dk * dk * 4 * 2 + B * H * (3 * 128 + 2) * 4 + B * H * 128 * 4
-        rows.append({"suite": "gdn", "kernel": "gdn_decode (fused layer body)", "mode": "decode", "H": H, "B": B,
-                     "us": sec * 1e6, "GB/s": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS})
-        print(json.dumps(rows[-1]), flush=True)
-        del bufs
+        for name, fn, launches in (("gdn_decode (fused layer body)", fused, 1),
+                                   ("gdn_decode_cols (column split; the head norm and gate in the next GEMV's prologue)", cols, 1),
+                                   ("gdn_decode_cols + gdn_norm_gate", cols_norm, 2)):
+            sec = _time_graph(fn, len(cases), replays)  # per layer body (both launches of the last form)
+            rows.append({"suite": "gdn", "kernel": name, "mode": "decode", "H": H, "B": B, "copies": copies,
+                         "us": sec * 1e6, "GB/s": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / 1e9 / HBM_PEAK_GBS})
+            print(json.dumps(rows[-1]), flush=True)
+        del cases
     T = 4096
     a, bufs = _gdn_case(lib, H, H, T, W, gen)
     wb = lib.hero_gdn_prefill_work_bytes(T, H, H)

@@ -1,4 +1,5 @@
-"""ctypes binding of libhero_amd.so (include/hero_kernels.h, include/hero_model.h).
+"""ctypes binding of libhero_amd.so (include/hero_kernels.h, include/hero_model.h,
+include/hero_gemma4.h).
 
 The library is built in-tree (``python -c "import __graft_entry__ as g; g.build()"``
 or ``make -C hero_amd``). There is no CPU fallback: if the library is missing,
@@ -78,6 +79,24 @@ class SynthConfig(ctypes.Structure):
     ]
 
 
+class Gemma4Dims(ctypes.Structure):
+    _fields_ = [
+        ("vocab", c_int64), ("d_model", c_int64), ("layers", c_int64), ("ctx", c_int64), ("ffn", c_int64),
+        ("q_heads", c_int64), ("kv_heads", c_int64), ("local_head_dim", c_int64), ("full_head_dim", c_int64),
+        ("per_layer_input", c_int64), ("window", c_int64), ("shared_kv_layers", c_int64),
+        ("rms_eps", c_float), ("logit_softcap", c_float), ("device_bytes", c_int64),
+    ]
+
+
+class Gemma4SynthConfig(ctypes.Structure):
+    _fields_ = [
+        ("vocab", c_int64), ("d_model", c_int64), ("layers", c_int64), ("ffn", c_int64),
+        ("q_heads", c_int64), ("kv_heads", c_int64), ("local_head_dim", c_int64), ("full_head_dim", c_int64),
+        ("per_layer_input", c_int64), ("window", c_int64), ("shared_kv_layers", c_int64), ("ctx", c_int64),
+        ("seed", c_uint64),
+    ]
+
+
 # name -> (restype, argtypes); every symbol of include/hero_*.h
 SIGNATURES = {
     "hero_last_error": (c_char_p, []),
@@ -145,6 +164,22 @@ SIGNATURES = {
     "hero_synth_qwen35_size": (c_int64, [POINTER(SynthConfig)]),
     "hero_synth_qwen35_image": (c_int, [POINTER(SynthConfig), c_void_p, c_size_t]),
     "hero_synth_qwen35_file": (c_int, [POINTER(SynthConfig), c_char_p]),
+    "hero_gemma_math_eval": (c_int, [c_void_p, c_void_p, c_int64, c_float, c_void_p]),
+    "hero_gemma4_open": (c_int, [c_char_p, POINTER(c_void_p)]),
+    "hero_gemma4_open_image": (c_int, [c_void_p, c_size_t, POINTER(c_void_p)]),
+    "hero_gemma4_close": (None, [c_void_p]),
+    "hero_gemma4_dims_get": (c_int, [c_void_p, POINTER(Gemma4Dims)]),
+    "hero_gemma4_state_create": (c_int, [c_void_p, c_int64, POINTER(c_void_p)]),
+    "hero_gemma4_state_destroy": (None, [c_void_p]),
+    "hero_gemma4_state_reset": (c_int, [c_void_p]),
+    "hero_gemma4_state_tokens": (c_int64, [c_void_p]),
+    "hero_gemma4_embed": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
+    "hero_gemma4_forward": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+    "hero_gemma4_decode_greedy": (c_int, [c_void_p, c_void_p, c_int32, c_int64, c_void_p, c_void_p]),
+    "hero_gemma4_last_decode_seconds": (c_double, [c_void_p]),
+    "hero_synth_gemma4_size": (c_int64, [POINTER(Gemma4SynthConfig)]),
+    "hero_synth_gemma4_image": (c_int, [POINTER(Gemma4SynthConfig), c_void_p, c_size_t]),
+    "hero_synth_gemma4_file": (c_int, [POINTER(Gemma4SynthConfig), c_char_p]),
 }
 
 

@@ -217,4 +217,46 @@ void attn_paged_plan(int64_t max_ctx, int window, int B, int Hkv, int* split, in
 int64_t attn_paged_work_floats(int B, int Hq, int nsplit, int Dh);
 void launch_attn_paged(const AttnPagedArgs& p, hipStream_t s);
 
+// gemma.hip: the Gemma 4 text model's own kernels (one row: a decode step)
+// x[D] = the embedding row of *id times embed_scale, act = its Q8_0 row, and
+// tok[PL] = the per-layer table's row of *id times token_scale
+void launch_gemma_embed(const void* emb, int64_t V, int64_t D, const void* ple_table, int64_t PL, const int32_t* id, float embed_scale, float token_scale, float* x,
+                        void* act, float* tok, hipStream_t s);
+// ple[l][:] = (RMSNorm_P(ctx[l][:] * proj_scale) * gamma + tok[l][:]) * comb, l < L
+void launch_gemma_ple_inputs(const float* ctx, const float* tok, const float* gamma, float eps, float proj_scale, float comb, float* ple, int64_t L, int64_t P,
+                             hipStream_t s);
+// attention of one row over a K/V cache: K [Hkv][Dh][slots] (channel-major),
+// V [Hkv][slots][Dh]; position p lives in slot p % slots (window > 0: a ring of
+// `window` slots) or slot p (full)
+struct GemmaAttnArgs {
+    const float* proj;        // [q Hq*Dh | k Hkv*Dh at k_off | v Hkv*Dh at v_off]
+    int64_t k_off, v_off;
+    const float* q_gamma;     // [Dh]
+    const float* k_gamma;     // [Dh]
+    float eps;
+    const float* rope_cs;     // [positions][Dh/2][2] (cos, sin)
+    const int32_t* pos;       // device position of the row
+    float* k_cache;
+    float* v_cache;
+    int64_t slots;
+    int window;               // 0: every earlier position is visible
+    int append;               // 1: form this row's k and v and append them
+    float* q_rot;             // scratch [Hq][Dh]
+    float* scores;            // scratch [Hq][max_ctx]
+    int64_t max_ctx;
+    void* act_out;            // Q8_0 W_o input [Hq*Dh]
+    int Hq, Hkv, Dh;          // Dh 256 or 512
+};
+void launch_gemma_attention(const GemmaAttnArgs& a, hipStream_t s);
+// out = (RMSNorm(a) * gamma + res) * scale; act = Q8_0 of next_gamma ?
+// RMSNorm(out) * next_gamma : out (D <= 4096, D % 32 == 0)
+void launch_gemma_post_norm(const float* a, const float* gamma, const float* res, float scale, float eps, float* out, const float* next_gamma, void* act, int64_t D,
+                            hipStream_t s);
+// act = Q8_0 of gelu_tanh(gate[i]) * mul[i], N % 32 == 0
+void launch_gemma_gelu_mul_quant(const float* gate, const float* mul, void* act, int64_t N, hipStream_t s);
+// logits[i] = cap * tanh(logits[i] / cap)
+void launch_gemma_softcap(float* logits, int64_t n, float cap, hipStream_t s);
+// out[2i] = gelu_tanh(x[i]), out[2i+1] = cap * tanh(x[i] / cap) (tests)
+void launch_gemma_math_eval(const float* x, float* out, int64_t n, float cap, hipStream_t s);
+
 }  // namespace hero

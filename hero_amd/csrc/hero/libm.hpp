@@ -1,5 +1,6 @@
-// libm.hpp -- single-precision exp and log1p for host and device that return
-// exactly what the x86-64 glibc 2.35 expf / log1pf return, for every input.
+// libm.hpp -- single-precision exp, log1p, expm1 and tanh for host and device
+// that return exactly what the x86-64 glibc 2.35 expf / log1pf / expm1f / tanhf
+// return, for every input.
 //
 // The reference calls std::exp and std::log1p on floats, i.e. glibc's expf
 // and log1pf, and neither is correctly rounded; a last-bit difference in one
@@ -15,7 +16,13 @@
 //             single-precision form: 1+x = 2^k (1+f) with a correction term,
 //             then log(1+f) = f - s(f - R) with s = f/(2+f) and a degree-7
 //             polynomial R in s^2, in fp32.
-// Both were checked against glibc on all 2^32 inputs (0 differences); the
+//   expm1f -- fdlibm's expm1 in single precision: x = k ln2 + r (ln2 split in
+//             hi/lo parts, with the rounding error c of the reduction), a
+//             degree-5 rational correction in r^2/2, and the scaling by 2^k
+//             folded into the exponent bits.
+//   tanhf  -- fdlibm's tanh: 1 - 2/(expm1(2|x|) + 2) for |x| >= 1,
+//             -t/(t + 2) with t = expm1(-2|x|) below, +-1 from |x| >= 22.
+// All four were checked against glibc on all 2^32 inputs (0 differences); the
 // tests repeat that check on a dense sample and on the hard cases.
 // Build with -ffp-contract=off: every operation below rounds once.
 #pragma once
@@ -168,6 +175,97 @@ __host__ __device__ inline float log1pf_glibc(float x) {
     const float R = z * (lp1 + z * (lp2 + z * (lp3 + z * (lp4 + z * (lp5 + z * (lp6 + z * lp7))))));
     if (k == 0) return f - (hfsq - s * (hfsq + R));
     return float(k) * ln2_hi - ((hfsq - (s * (hfsq + R) + (float(k) * ln2_lo + c))) - f);
+}
+
+// expm1f and tanhf below restate fdlibm's single-precision expm1 and tanh
+// (s_expm1f.c, s_tanhf.c; the algorithms glibc 2.35 uses), under the same Sun
+// Microsystems permission notice as log1pf above.
+__host__ __device__ inline float expm1f_glibc(float x) {
+    const float o_threshold = bits_f32(0x42b17180u), ln2_hi = bits_f32(0x3f317180u), ln2_lo = bits_f32(0x3717f7d1u),
+                invln2 = bits_f32(0x3fb8aa3bu);
+    const float q1 = bits_f32(0xbd088889u), q2 = bits_f32(0x3ad00d01u), q3 = bits_f32(0xb8a670cdu), q4 = bits_f32(0x36867e54u),
+                q5 = bits_f32(0xb457edbbu);
+    uint32_t hx = f32_bits(x);
+    const uint32_t xsb = hx & 0x80000000u;
+    hx &= 0x7fffffffu;
+    float hi, lo, c = 0.f, t, e, y;
+    int32_t k;
+    if (hx >= 0x4195b844u) {  // |x| >= 27 ln2
+        if (hx >= 0x42b17218u) {  // |x| >= 88.72
+            if (hx > 0x7f800000u) return x + x;  // nan
+            if (hx == 0x7f800000u) return xsb == 0 ? x : -1.f;
+            if (x > o_threshold) return bits_f32(0x7f800000u);  // overflow
+        }
+        if (xsb != 0) return -1.f;
+    }
+    if (hx > 0x3eb17218u) {  // |x| > ln2 / 2: reduce
+        if (hx < 0x3f851592u) {  // and < 1.5 ln2
+            if (xsb == 0) {
+                hi = x - ln2_hi;
+                lo = ln2_lo;
+                k = 1;
+            } else {
+                hi = x + ln2_hi;
+                lo = -ln2_lo;
+                k = -1;
+            }
+        } else {
+            k = int32_t(invln2 * x + (xsb == 0 ? 0.5f : -0.5f));
+            t = float(k);
+            hi = x - t * ln2_hi;  // exact
+            lo = t * ln2_lo;
+        }
+        x = hi - lo;
+        c = (hi - x) - lo;
+    } else if (hx < 0x33000000u) {  // |x| < 2^-25
+        return x;
+    } else {
+        k = 0;
+    }
+    const float hfx = 0.5f * x, hxs = x * hfx;
+    const float r1 = 1.f + hxs * (q1 + hxs * (q2 + hxs * (q3 + hxs * (q4 + hxs * q5))));
+    t = 3.f - r1 * hfx;
+    e = hxs * ((r1 - t) / (6.f - x * t));
+    if (k == 0) return x - (x * e - hxs);
+    e = x * (e - c) - c;
+    e -= hxs;
+    if (k == -1) return 0.5f * (x - e) - 0.5f;
+    if (k == 1) return x < -0.25f ? -2.f * (e - (x + 0.5f)) : 1.f + 2.f * (x - e);
+    if (k <= -2 || k > 56) {  // exp(x) - 1 is exp(x) to working precision
+        y = 1.f - (e - x);
+        y = k == 128 ? y * 2.f * bits_f32(0x7f000000u) : bits_f32(f32_bits(y) + (uint32_t(k) << 23));
+        return y - 1.f;
+    }
+    if (k < 23) {
+        t = bits_f32(0x3f800000u - (0x1000000u >> k));  // 1 - 2^-k
+        y = t - (e - x);
+    } else {
+        t = bits_f32(uint32_t(0x7f - k) << 23);  // 2^-k
+        y = x - (e + t);
+        y += 1.f;
+    }
+    return bits_f32(f32_bits(y) + (uint32_t(k) << 23));
+}
+
+__host__ __device__ inline float tanhf_glibc(float x) {
+    const int32_t jx = int32_t(f32_bits(x)), ix = jx & 0x7fffffff;
+    if (ix >= 0x7f800000) return jx >= 0 ? 1.f / x + 1.f : 1.f / x - 1.f;  // +-inf -> +-1, nan -> nan
+    float z;
+    if (ix < 0x41b00000) {  // |x| < 22
+        if (ix == 0) return x;
+        if (ix < 0x24000000) return x * (1.f + x);  // |x| < 2^-55
+        const float ax = jx >= 0 ? x : -x;
+        if (ix >= 0x3f800000) {
+            const float t = expm1f_glibc(2.f * ax);
+            z = 1.f - 2.f / (t + 2.f);
+        } else {
+            const float t = expm1f_glibc(-2.f * ax);
+            z = -t / (t + 2.f);
+        }
+    } else {
+        z = 1.f;
+    }
+    return jx >= 0 ? z : -z;
 }
 
 }  // namespace hero

@@ -331,6 +331,14 @@ int hero_math_eval(const float* x, float* out, int64_t n, void* stream) {
     });
 }
 
+int hero_gemma_math_eval(const float* x, float* out, int64_t n, float cap, void* stream) {
+    return guard([&] {
+        require(x && out && n > 0 && n < (int64_t(1) << 40) && cap > 0.f, "bad arguments");
+        launch_gemma_math_eval(x, out, n, cap, as_stream(stream));
+        check_launch("hero_gemma_math_eval");
+    });
+}
+
 namespace {
 GdnDecodeArgs gdn_args(const hero_gdn_decode_args* p, bool need_act = true) {
     require(p != nullptr, "null args");

@@ -197,8 +197,9 @@ struct TensorSpec {
     uint64_t in = 0, out = 1;  // ggml dims [in, out]; a vector has out == 1 and one dim
     bool matrix = false;
     uint32_t type = T_F32;
-    enum Kind { Normal, Ones, Zeros, NegExpNormal } kind = Normal;
+    enum Kind { Normal, Ones, Zeros, NegExpNormal, Affine } kind = Normal;
     double scale = 0.02;
+    double mean = 0.0;  // Affine: mean + scale * normal
     uint64_t offset = 0, bytes = 0;
 };
 
@@ -303,35 +304,16 @@ std::vector<TensorSpec> tensor_specs(const SynthConfig& c) {
     return t;
 }
 
-std::vector<uint8_t> header_bytes(const SynthConfig& c, std::vector<TensorSpec>& specs, uint64_t& data_start, uint64_t& total) {
+// magic, version, counts, the metadata `meta` writes (kv_count pairs), the
+// tensor table and the aligned data start; fills each spec's offset and size
+template <class Meta>
+std::vector<uint8_t> gguf_header(std::vector<TensorSpec>& specs, uint64_t kv_count, Meta&& meta, uint64_t& data_start, uint64_t& total) {
     Writer w;
     w.u32(0x46554747u);
     w.u32(3);
     w.u64(specs.size());
-    const uint64_t kv_count = 20;
     w.u64(kv_count);
-    w.kv_str("general.architecture", "qwen35");
-    w.kv_u32("general.alignment", 32);
-    w.kv_u32("qwen35.block_count", uint32_t(c.L));
-    w.kv_u32("qwen35.context_length", uint32_t(c.ctx));
-    w.kv_u32("qwen35.embedding_length", uint32_t(c.D));
-    w.kv_u32("qwen35.feed_forward_length", uint32_t(c.FF));
-    w.kv_u32("qwen35.attention.head_count", uint32_t(c.Hq));
-    w.kv_u32("qwen35.attention.head_count_kv", uint32_t(c.Hkv));
-    w.kv_u32("qwen35.attention.key_length", uint32_t(c.head_dim));
-    w.kv_u32("qwen35.attention.value_length", uint32_t(c.head_dim));
-    w.kv_f32("qwen35.attention.layer_norm_rms_epsilon", 1e-6f);
-    w.kv_f32("qwen35.rope.freq_base", float(c.rope_base));
-    w.kv_u32("qwen35.rope.dimension_count", uint32_t(c.head_dim / 4));
-    w.kv_u32("qwen35.ssm.conv_kernel", uint32_t(c.conv_width));
-    w.kv_u32("qwen35.ssm.state_size", uint32_t(c.Dk));
-    w.kv_u32("qwen35.ssm.group_count", uint32_t(c.Hk));
-    w.kv_u32("qwen35.ssm.time_step_rank", uint32_t(c.Hv));
-    w.kv_u32("qwen35.ssm.inner_size", uint32_t(c.Hv * c.Dv));
-    w.kv_u32("qwen35.full_attention_interval", 4);
-    std::vector<uint32_t> recurrent(c.L);
-    for (uint64_t l = 0; l < c.L; ++l) recurrent[l] = (l + 1) % 4 != 0;
-    w.kv_u32_array("qwen35.attention.recurrent_layers", recurrent);
+    meta(w);
     uint64_t offset = 0;
     for (TensorSpec& s : specs) {
         const uint64_t n = s.in * s.out;
@@ -356,8 +338,35 @@ std::vector<uint8_t> header_bytes(const SynthConfig& c, std::vector<TensorSpec>&
     return std::move(w.buf);
 }
 
-void fill_tensor(const SynthConfig& c, const TensorSpec& s, uint64_t tensor_index, uint8_t* dst) {
-    const uint64_t stream = stream_of(c.seed, tensor_index);
+std::vector<uint8_t> header_bytes(const SynthConfig& c, std::vector<TensorSpec>& specs, uint64_t& data_start, uint64_t& total) {
+    return gguf_header(specs, 20, [&](Writer& w) {
+        w.kv_str("general.architecture", "qwen35");
+        w.kv_u32("general.alignment", 32);
+        w.kv_u32("qwen35.block_count", uint32_t(c.L));
+        w.kv_u32("qwen35.context_length", uint32_t(c.ctx));
+        w.kv_u32("qwen35.embedding_length", uint32_t(c.D));
+        w.kv_u32("qwen35.feed_forward_length", uint32_t(c.FF));
+        w.kv_u32("qwen35.attention.head_count", uint32_t(c.Hq));
+        w.kv_u32("qwen35.attention.head_count_kv", uint32_t(c.Hkv));
+        w.kv_u32("qwen35.attention.key_length", uint32_t(c.head_dim));
+        w.kv_u32("qwen35.attention.value_length", uint32_t(c.head_dim));
+        w.kv_f32("qwen35.attention.layer_norm_rms_epsilon", 1e-6f);
+        w.kv_f32("qwen35.rope.freq_base", float(c.rope_base));
+        w.kv_u32("qwen35.rope.dimension_count", uint32_t(c.head_dim / 4));
+        w.kv_u32("qwen35.ssm.conv_kernel", uint32_t(c.conv_width));
+        w.kv_u32("qwen35.ssm.state_size", uint32_t(c.Dk));
+        w.kv_u32("qwen35.ssm.group_count", uint32_t(c.Hk));
+        w.kv_u32("qwen35.ssm.time_step_rank", uint32_t(c.Hv));
+        w.kv_u32("qwen35.ssm.inner_size", uint32_t(c.Hv * c.Dv));
+        w.kv_u32("qwen35.full_attention_interval", 4);
+        std::vector<uint32_t> recurrent(c.L);
+        for (uint64_t l = 0; l < c.L; ++l) recurrent[l] = (l + 1) % 4 != 0;
+        w.kv_u32_array("qwen35.attention.recurrent_layers", recurrent);
+    }, data_start, total);
+}
+
+void fill_tensor(uint64_t seed, const TensorSpec& s, uint64_t tensor_index, uint8_t* dst) {
+    const uint64_t stream = stream_of(seed, tensor_index);
     if (s.type == T_Q4_K || s.type == T_Q5_K || s.type == T_Q6_K) {
         const uint64_t in = s.in, blocks = in / 256, bb = type_bytes(s.type, 256);
         parallel_rows(s.out, [&](size_t r) {
@@ -402,6 +411,7 @@ void fill_tensor(const SynthConfig& c, const TensorSpec& s, uint64_t tensor_inde
             case TensorSpec::Zeros: f[i] = 0.f; break;
             case TensorSpec::Normal: f[i] = float(s.scale) * normal_at(stream, i); break;
             case TensorSpec::NegExpNormal: f[i] = -std::exp(float(s.scale) * normal_at(stream, i)); break;
+            case TensorSpec::Affine: f[i] = float(s.mean) + float(s.scale) * normal_at(stream, i); break;
         }
     }
 }
@@ -433,18 +443,147 @@ void synth_qwen35_image(const SynthConfig& c, uint8_t* image, uint64_t capacity)
     if (capacity < total) throw std::invalid_argument("synth: image buffer too small");
     std::memcpy(image, header.data(), header.size());
     std::memset(image + header.size(), 0, size_t(total - header.size()));
-    for (size_t i = 0; i < specs.size(); ++i) fill_tensor(c, specs[i], i, image + data_start + specs[i].offset);
+    for (size_t i = 0; i < specs.size(); ++i) fill_tensor(c.seed, specs[i], i, image + data_start + specs[i].offset);
 }
 
-void synth_qwen35_file(const SynthConfig& c, const std::string& path) {
-    const uint64_t total = synth_qwen35_size(c);
-    std::vector<uint8_t> image(total);
-    synth_qwen35_image(c, image.data(), total);
+namespace {
+void write_file(const std::vector<uint8_t>& image, const std::string& path) {
     FILE* f = std::fopen(path.c_str(), "wb");
     if (!f) throw std::runtime_error("synth: cannot write " + path);
     const size_t wrote = std::fwrite(image.data(), 1, image.size(), f);
     std::fclose(f);
     if (wrote != image.size()) throw std::runtime_error("synth: short write to " + path);
+}
+}  // namespace
+
+void synth_qwen35_file(const SynthConfig& c, const std::string& path) {
+    const uint64_t total = synth_qwen35_size(c);
+    std::vector<uint8_t> image(total);
+    synth_qwen35_image(c, image.data(), total);
+    write_file(image, path);
+}
+
+// ---- Gemma 4 (E4B text schema, nm/src/gemma4_loader.hpp:31-52,104-155) ---------
+// Fixed choices: 2-D weights N(0, 0.02) in Q8_0; norm weights 1 + N(0, 0.1);
+// q_norm 0.125 + N(0, 0.02) (Gemma folds the score scale into it); the final
+// norm 8 + N(0, 1), so the logits reach the soft-cap's curved range;
+// layer_output_scale 0.8 + N(0, 0.1), a 1-element F32 tensor on every layer.
+// Layers from L - shared_kv_layers on carry no attn_k / attn_v.
+namespace {
+
+bool gemma_full(uint64_t l) { return l % 6 == 5; }
+
+std::vector<TensorSpec> gemma4_specs(const Gemma4SynthConfig& c) {
+    std::vector<TensorSpec> t;
+    auto mat = [&](const std::string& name, uint64_t in, uint64_t out) {
+        TensorSpec s;
+        s.name = name;
+        s.in = in;
+        s.out = out;
+        s.matrix = true;
+        s.type = T_Q8_0;
+        t.push_back(s);
+    };
+    auto vec = [&](const std::string& name, uint64_t n, double mean, double scale) {
+        TensorSpec s;
+        s.name = name;
+        s.in = n;
+        s.kind = TensorSpec::Affine;
+        s.mean = mean;
+        s.scale = scale;
+        t.push_back(s);
+    };
+    const uint64_t D = c.D, P = c.ple;
+    mat("token_embd.weight", D, c.V);
+    mat("per_layer_token_embd.weight", P * c.L, c.V);
+    mat("per_layer_model_proj.weight", D, P * c.L);
+    vec("per_layer_proj_norm.weight", P, 1.0, 0.1);
+    vec("output_norm.weight", D, 8.0, 1.0);
+    for (uint64_t l = 0; l < c.L; ++l) {
+        const std::string b = "blk." + std::to_string(l) + ".";
+        const uint64_t dh = gemma_full(l) ? c.full_dim : c.local_dim;
+        const bool shared = l >= c.L - c.shared_kv_layers;
+        vec(b + "attn_norm.weight", D, 1.0, 0.1);
+        mat(b + "attn_q.weight", D, c.Hq * dh);
+        vec(b + "attn_q_norm.weight", dh, 0.125, 0.02);
+        if (!shared) {
+            mat(b + "attn_k.weight", D, c.Hkv * dh);
+            vec(b + "attn_k_norm.weight", dh, 1.0, 0.1);
+            mat(b + "attn_v.weight", D, c.Hkv * dh);
+        }
+        mat(b + "attn_output.weight", c.Hq * dh, D);
+        vec(b + "post_attention_norm.weight", D, 1.0, 0.1);
+        vec(b + "ffn_norm.weight", D, 1.0, 0.1);
+        mat(b + "ffn_gate.weight", D, c.FF);
+        mat(b + "ffn_up.weight", D, c.FF);
+        mat(b + "ffn_down.weight", c.FF, D);
+        vec(b + "post_ffw_norm.weight", D, 1.0, 0.1);
+        mat(b + "inp_gate.weight", D, P);
+        mat(b + "proj.weight", P, D);
+        vec(b + "post_norm.weight", D, 1.0, 0.1);
+        vec(b + "layer_output_scale.weight", 1, 0.8, 0.1);
+    }
+    return t;
+}
+
+std::vector<uint8_t> gemma4_header(const Gemma4SynthConfig& c, std::vector<TensorSpec>& specs, uint64_t& data_start, uint64_t& total) {
+    return gguf_header(specs, 21, [&](Writer& w) {
+        w.kv_str("general.architecture", "gemma4");
+        w.kv_u32("general.alignment", 32);
+        w.kv_u32("gemma4.block_count", uint32_t(c.L));
+        w.kv_u32("gemma4.context_length", uint32_t(c.ctx));
+        w.kv_u32("gemma4.embedding_length", uint32_t(c.D));
+        w.kv_u32("gemma4.feed_forward_length", uint32_t(c.FF));
+        w.kv_u32("gemma4.attention.head_count", uint32_t(c.Hq));
+        w.kv_u32("gemma4.attention.head_count_kv", uint32_t(c.Hkv));
+        w.kv_u32("gemma4.attention.key_length", uint32_t(c.full_dim));
+        w.kv_u32("gemma4.attention.value_length", uint32_t(c.full_dim));
+        w.kv_u32("gemma4.attention.key_length_swa", uint32_t(c.local_dim));
+        w.kv_u32("gemma4.attention.value_length_swa", uint32_t(c.local_dim));
+        w.kv_u32("gemma4.attention.sliding_window", uint32_t(c.window));
+        w.kv_u32("gemma4.attention.shared_kv_layers", uint32_t(c.shared_kv_layers));
+        w.kv_u32("gemma4.embedding_length_per_layer_input", uint32_t(c.ple));
+        w.kv_f32("gemma4.attention.layer_norm_rms_epsilon", 1e-6f);
+        w.kv_f32("gemma4.final_logit_softcapping", 30.f);
+        w.kv_f32("gemma4.rope.freq_base", 1e6f);
+        w.kv_f32("gemma4.rope.freq_base_swa", 1e4f);
+        w.kv_u32("gemma4.rope.dimension_count", uint32_t(c.full_dim / 4));
+        w.kv_u32("gemma4.rope.dimension_count_swa", uint32_t(c.local_dim));
+    }, data_start, total);
+}
+
+void check_gemma4(const Gemma4SynthConfig& c) {
+    if (c.L < 6 || c.shared_kv_layers >= c.L) throw std::invalid_argument("synth gemma4: need at least 6 layers and fewer shared-KV layers than layers");
+    if (c.D % 32 || c.FF % 32 || c.ple % 32 || c.local_dim % 32 || c.full_dim % 32) throw std::invalid_argument("synth gemma4: every Q8_0 input width must be a multiple of 32");
+    if (c.Hkv == 0 || c.Hq % c.Hkv || c.V == 0 || c.window == 0 || c.ctx == 0) throw std::invalid_argument("synth gemma4: inconsistent shapes");
+}
+
+}  // namespace
+
+uint64_t synth_gemma4_size(const Gemma4SynthConfig& c) {
+    check_gemma4(c);
+    std::vector<TensorSpec> specs = gemma4_specs(c);
+    uint64_t data_start = 0, total = 0;
+    gemma4_header(c, specs, data_start, total);
+    return total;
+}
+
+void synth_gemma4_image(const Gemma4SynthConfig& c, uint8_t* image, uint64_t capacity) {
+    check_gemma4(c);
+    std::vector<TensorSpec> specs = gemma4_specs(c);
+    uint64_t data_start = 0, total = 0;
+    const std::vector<uint8_t> header = gemma4_header(c, specs, data_start, total);
+    if (capacity < total) throw std::invalid_argument("synth: image buffer too small");
+    std::memcpy(image, header.data(), header.size());
+    std::memset(image + header.size(), 0, size_t(total - header.size()));
+    for (size_t i = 0; i < specs.size(); ++i) fill_tensor(c.seed, specs[i], i, image + data_start + specs[i].offset);
+}
+
+void synth_gemma4_file(const Gemma4SynthConfig& c, const std::string& path) {
+    const uint64_t total = synth_gemma4_size(c);
+    std::vector<uint8_t> image(total);
+    synth_gemma4_image(c, image.data(), total);
+    write_file(image, path);
 }
 
 }  // namespace hero

@@ -190,6 +190,10 @@ int hero_sample(const float* logits, int64_t v, int32_t top_k, float temp, float
  * (nm/src/components.hpp:105), sigmoid (nm/src/core.hpp:579), softplus
  * (nm/src/recurrent.hpp:35). expf and log1pf return exactly glibc's values. */
 int hero_math_eval(const float* x, float* out, int64_t n, void* stream);
+/* Gemma 4's scalar functions on the device: out[2i] = gelu_pytorch_tanh(x[i])
+ * (nm/src/components.hpp:73-81), out[2i+1] = cap * tanh(x[i] / cap)
+ * (gemma_softcap, nm/src/gemma4.hpp:79); tanh returns exactly glibc's tanhf. */
+int hero_gemma_math_eval(const float* x, float* out, int64_t n, float cap, void* stream);
 
 /* Gated delta-net decode, one token for each of B sequences, all Hv heads:
  * conv step + SiLU, q/k L2 norm, beta/decay gates, the gated delta rule,

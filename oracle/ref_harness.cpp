@@ -6,12 +6,14 @@
 //   ref_harness kernels DIR          read DIR/*.in.bin, write DIR/*.out.bin
 //   ref_harness window DIR           causal / sliding-window attention cases
 //   ref_harness model CFG GGUF PROMPT STEPS OUTDIR
-//        CFG = tiny | tiny_hk4u | 8b. Prefill the int32 ids in PROMPT through
-//        PrefixCache::evaluate, then STEPS greedy decode passes, exactly as
-//        tools/qwen35_check.cpp:43-70 does (minus the tokenizer).
+//        CFG = tiny | tiny_hk4u | tiny_dh256 | tiny_ff3584 | 8b | gemma4_e4b.
+//        Prefill the int32 ids in PROMPT through PrefixCache::evaluate, then
+//        STEPS greedy decode passes, exactly as tools/qwen35_check.cpp:43-70
+//        and tools/gemma4_text.cpp:16-52 do (minus the tokenizer).
 //
 // Each kernel case instantiates the reference template at a fixed size and
 // applies it to the inputs the golden script wrote.
+#include "src/gemma4_loader.hpp"
 #include "src/qwen35_loader.hpp"
 #include "src/logits.hpp"
 
@@ -117,21 +119,20 @@ struct Hybrid8BConfig {
     static constexpr bool is_recurrent(size_t layer) { return (layer + 1) % FULL_ATTENTION_INTERVAL != 0; }
 };
 
-template <class C>
-int run_model(const char* gguf_path, const char* prompt_path, size_t steps, const std::string& out) {
-    const GGUF gguf(gguf_path);
-    auto model = qwen35_loader::load<C>(gguf);
+template <class Model>
+int run_loaded(const Model& model, const char* prompt_path, size_t steps, const std::string& out) {
+    constexpr size_t D = Model::D, V = Model::V;
     const std::vector<int32_t> prompt_ids = read_bin<int32_t>(prompt_path);
     std::vector<TokenId> tokens;
     for (int32_t id : prompt_ids) tokens.push_back(TokenId{id});
 
-    EmbeddedSequence<C::D> sequence;
+    EmbeddedSequence<D> sequence;
     sequence.append(model.embed(tokens), tokens);
-    PrefixCache<Qwen35Model<C>> memo(model);
+    PrefixCache<Model> memo(model);
     const auto t0 = std::chrono::steady_clock::now();
-    Logits<C::V> logits = memo.evaluate(sequence);
+    Logits<V> logits = memo.evaluate(sequence);
     const auto t1 = std::chrono::steady_clock::now();
-    write_bin(out + "/logits_prefill.f32", &logits[0], C::V);
+    write_bin(out + "/logits_prefill.f32", &logits[0], V);
 
     // per step: the greedy id, and the top-5 (ids, logits)
     std::vector<int32_t> ids, top_ids;
@@ -147,10 +148,10 @@ int run_model(const char* gguf_path, const char* prompt_path, size_t steps, cons
         const std::span<const TokenId> next(&token, 1);
         sequence.append(model.embed(next), next);
         logits = memo.evaluate(sequence);
-        if (i + 1 == steps / 2) write_bin(out + "/logits_mid.f32", &logits[0], C::V);
+        if (i + 1 == steps / 2) write_bin(out + "/logits_mid.f32", &logits[0], V);
     }
     const auto t2 = std::chrono::steady_clock::now();
-    write_bin(out + "/logits_last.f32", &logits[0], C::V);
+    write_bin(out + "/logits_last.f32", &logits[0], V);
     write_bin(out + "/ids.i32", ids.data(), ids.size());
     write_bin(out + "/top5_ids.i32", top_ids.data(), top_ids.size());
     write_bin(out + "/top5_logits.f32", top_logits.data(), top_logits.size());
@@ -161,6 +162,21 @@ int run_model(const char* gguf_path, const char* prompt_path, size_t steps, cons
     std::fclose(f);
     std::printf("reference %s: prefill %zu tokens %.3fs, %zu decode passes %.3fs (%.3f passes/s, %zu threads)\n", out.c_str(), prompt_ids.size(), prefill, steps, decode, steps / decode, nm_num_threads());
     return 0;
+}
+
+template <class C>
+int run_model(const char* gguf_path, const char* prompt_path, size_t steps, const std::string& out) {
+    const GGUF gguf(gguf_path);
+    const auto model = qwen35_loader::load<C>(gguf);
+    return run_loaded(model, prompt_path, steps, out);
+}
+
+// Gemma 4 E4B text (its classes are fixed to the E4B configuration): the
+// loop of tools/gemma4_text.cpp:16-52 minus the tokenizer
+int run_gemma4(const char* gguf_path, const char* prompt_path, size_t steps, const std::string& out) {
+    const GGUF gguf(gguf_path);
+    const Gemma4E4BModel model = gemma4_loader::load_e4b_text(gguf);
+    return run_loaded(model, prompt_path, steps, out);
 }
 
 // ---- kernel-level golden vectors ------------------------------------------------
@@ -436,8 +452,9 @@ int main(int argc, char** argv) {
             if (std::strcmp(argv[2], "tiny_dh256") == 0) return run_model<TinyDh256Config>(argv[3], argv[4], steps, argv[6]);
             if (std::strcmp(argv[2], "tiny_ff3584") == 0) return run_model<TinyFf3584Config>(argv[3], argv[4], steps, argv[6]);
             if (std::strcmp(argv[2], "8b") == 0) return run_model<Hybrid8BConfig>(argv[3], argv[4], steps, argv[6]);
+            if (std::strcmp(argv[2], "gemma4_e4b") == 0) return run_gemma4(argv[3], argv[4], steps, argv[6]);
         }
-        std::fprintf(stderr, "usage: %s kernels DIR | window DIR | model {tiny|tiny_hk4u|tiny_dh256|8b} GGUF PROMPT STEPS OUTDIR\n", argv[0]);
+        std::fprintf(stderr, "usage: %s kernels DIR | window DIR | model {tiny|tiny_hk4u|tiny_dh256|tiny_ff3584|8b|gemma4_e4b} GGUF PROMPT STEPS OUTDIR\n", argv[0]);
         return 2;
     } catch (const std::exception& e) {
         std::fprintf(stderr, "ref_harness: %s\n", e.what());

@@ -28,6 +28,12 @@ so it runs in the build container only). This script:
      prompts (the batch-1 prompt and sequences 0 and 15 of the 16-sequence
      batch) and 64 greedy passes each -> hybrid8b_2k_model.npz (ids, top-5,
      and the sha256 of the prefill and last logit vectors in the manifest);
+  10. `gemma4`: the reference's Gemma 4 E4B text model (its classes are fixed
+     to the E4B configuration, so the model is full size: a seeded synthetic
+     7.9 GB Q8_0 GGUF), a 600-token prompt (past the 512-position window, so
+     the rings wrap and the K/V-sharing layers read the window) and 32 greedy
+     passes -> gemma4_e4b_model.npz (ids, top-5, the first 8192 logits of
+     the prefill and last passes) and the sha256 of both full logit vectors;
   7. `dh256`: the attention geometry of the reference's Qwen 3.5 4B / 9B
      configs (256-wide heads, a quarter rotating, RoPE base 1e7, Hk 4 over
      Hv 8, untied head) at tiny width -> tiny_dh256_model.npz.
@@ -35,7 +41,7 @@ so it runs in the build container only). This script:
 manifest.json records seeds, shapes, the GGUF's sha256 and the compiler
 flags (-O3 -march=x86-64-v3 -ffp-contract=off: no FMA contraction).
 
-Run:  python tests/golden/make_golden.py [kernels] [tiny] [window] [variant] [kmix] [hybrid8b] [dh256] [q8ffn] [hybrid8b_2k]
+Run:  python tests/golden/make_golden.py [kernels] [tiny] [window] [variant] [kmix] [hybrid8b] [dh256] [q8ffn] [hybrid8b_2k] [gemma4]
       (no argument: all parts; the manifest keeps the entries of parts not rerun)
 """
 from __future__ import annotations
@@ -393,12 +399,51 @@ def make_hybrid8b_2k(tmp: str) -> dict:
     return entry
 
 
+GEMMA4_SEED = 4242
+GEMMA4_PROMPT = 600
+GEMMA4_STEPS = 32
+GEMMA4_HEAD = 8192  # logits kept in full per vector (the rest by sha256)
+
+
+def make_gemma4(tmp: str) -> dict:
+    """Gemma 4 E4B (full size: the reference's Gemma classes take no other
+    shape), 600-token prompt, 32 greedy passes; a few minutes of reference CPU time"""
+    from hero_amd.gemma4 import GEMMA4_E4B, write_synthetic_gemma4
+
+    shm = "/dev/shm" if os.path.isdir("/dev/shm") else tmp
+    gguf = os.path.join(shm, "gemma4_e4b.gguf")
+    write_synthetic_gemma4(gguf, GEMMA4_E4B, seed=GEMMA4_SEED)
+    h = hashlib.sha256()
+    with open(gguf, "rb") as f:
+        for chunk in iter(lambda: f.read(1 << 24), b""):
+            h.update(chunk)
+    digest = lambda a: hashlib.sha256(np.ascontiguousarray(a, np.float32).tobytes()).hexdigest()  # noqa: E731
+    prompt = np.random.default_rng(GEMMA4_SEED).integers(0, GEMMA4_E4B.vocab, GEMMA4_PROMPT).astype(np.int32)
+    prompt.tofile(os.path.join(tmp, "gemma4_prompt.i32"))
+    outdir = os.path.join(tmp, "gemma4_out")
+    os.makedirs(outdir, exist_ok=True)
+    try:
+        subprocess.run([HARNESS, "model", "gemma4_e4b", gguf, os.path.join(tmp, "gemma4_prompt.i32"), str(GEMMA4_STEPS), outdir], check=True)
+        size = os.path.getsize(gguf)
+    finally:
+        os.remove(gguf)
+    rd = lambda n, dt: np.fromfile(os.path.join(outdir, n), dtype=dt)  # noqa: E731
+    prefill, last = rd("logits_prefill.f32", np.float32), rd("logits_last.f32", np.float32)
+    np.savez_compressed(os.path.join(HERE, "gemma4_e4b_model.npz"), prompt=prompt, ids=rd("ids.i32", np.int32),
+                        top5_ids=rd("top5_ids.i32", np.int32).reshape(-1, 5), top5_logits=rd("top5_logits.f32", np.float32).reshape(-1, 5),
+                        prefill_head=prefill[:GEMMA4_HEAD], last_head=last[:GEMMA4_HEAD])
+    return {"seed": GEMMA4_SEED, "prompt_len": GEMMA4_PROMPT, "decode_steps": GEMMA4_STEPS, "gguf_sha256": h.hexdigest(),
+            "gguf_bytes": size, "reference_times": open(os.path.join(outdir, "times.txt")).read(),
+            "logits_prefill_sha256": digest(prefill), "logits_last_sha256": digest(last)}
+
+
 PARTS = {"kernels": make_kernels, "tiny": make_tiny, "window": make_window, "variant": make_variant, "kmix": make_kmix,
          "hybrid8b": make_hybrid8b, "dh256": make_dh256, "q8ffn": make_q8ffn,
-         "hybrid8b_2k": make_hybrid8b_2k}
+         "hybrid8b_2k": make_hybrid8b_2k, "gemma4": make_gemma4}
 MANIFEST_KEYS = {"kernels": "kernels", "tiny": "tiny_model", "window": "window", "variant": "tiny_hk4u_model",
                  "kmix": "tiny_kmix_model", "hybrid8b": "hybrid8b_model", "dh256": "tiny_dh256_model",
-                 "q8ffn": "tiny_q8ffn_model", "hybrid8b_2k": "hybrid8b_2k_model"}
+                 "q8ffn": "tiny_q8ffn_model", "hybrid8b_2k": "hybrid8b_2k_model",
+                 "gemma4": "gemma4_e4b_model"}
 
 
 def main():

@@ -14,7 +14,7 @@ from conftest import ROOT
 
 def declared_symbols():
     names = set()
-    for h in ("hero_kernels.h", "hero_model.h"):
+    for h in ("hero_kernels.h", "hero_model.h", "hero_gemma4.h"):
         text = open(os.path.join(ROOT, "include", h)).read()
         names |= set(re.findall(r"\b(hero_[A-Za-z0-9_]+)\s*\(", text))
     return names
@@ -27,6 +27,26 @@ def test_every_declared_symbol_is_exported_and_bound():
     for name in declared:
         assert hasattr(lib, name), name
     assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+
+
+def test_gemma4_loader_rejects_a_qwen_file_and_bad_synth_configs(tmp_path):
+    """hero_gemma4_open checks general.architecture before touching the
+    device, and the synthetic writer rejects impossible shapes."""
+    from hero_amd.gemma4 import GEMMA4_TINY, gemma4_synth_config
+
+    lib = _lib.lib
+    path = str(tmp_path / "tiny_qwen.gguf")
+    hero_amd.write_synthetic_gguf(path, hero_amd.TINY_CONFIG, seed=1)
+    h = ctypes.c_void_p()
+    assert lib.hero_gemma4_open(path.encode(), ctypes.byref(h)) == _lib.HERO_EIO
+    assert b"gemma4" in lib.hero_last_error()
+    cfg = gemma4_synth_config(GEMMA4_TINY, 1)
+    assert lib.hero_synth_gemma4_size(ctypes.byref(cfg)) > 0
+    cfg.shared_kv_layers = cfg.layers
+    assert lib.hero_synth_gemma4_size(ctypes.byref(cfg)) == -1
+    cfg = gemma4_synth_config(GEMMA4_TINY, 1)
+    cfg.d_model = 500
+    assert lib.hero_synth_gemma4_size(ctypes.byref(cfg)) == -1
 
 
 def test_kquant_argument_errors_are_reported_before_any_launch():
@@ -126,9 +146,9 @@ def test_one_hip_runtime_per_process():
 
 
 def test_libm_header_equals_glibc_on_the_host(tmp_path):
-    """hero/libm.hpp's expf / log1pf (the device's exp and log1p) against
-    glibc on a dense stride of all float bit patterns; pass 1 as the stride
-    to sweep all 2^32 (a minute)."""
+    """hero/libm.hpp's expf / log1pf / expm1f / tanhf (the device's exp, log1p,
+    expm1 and tanh) against glibc on a dense stride of all float bit patterns
+    and the branch edges; pass 1 as the stride to sweep all 2^32."""
     import subprocess
 
     exe = str(tmp_path / "libm_check")
@@ -136,8 +156,8 @@ def test_libm_header_equals_glibc_on_the_host(tmp_path):
                     "--offload-arch=gfx950", "-I", os.path.join(ROOT, "hero_amd", "csrc"),
                     os.path.join(ROOT, "tests", "libm_check.cpp"), "-o", exe], check=True, capture_output=True)
     out = subprocess.run([exe, "257"], capture_output=True, text=True)
-    n, be, bl = (int(v) for v in out.stdout.split())
-    assert n > 16_000_000 and be == 0 and bl == 0, out.stdout
+    n, be, bl, bm, bt = (int(v) for v in out.stdout.split())
+    assert n > 16_000_000 and be == bl == bm == bt == 0, out.stdout
 
 
 def test_seqsum_equals_the_sequential_loop_on_the_host(tmp_path):

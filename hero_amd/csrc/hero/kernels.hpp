@@ -225,9 +225,9 @@ void launch_gemma_embed(const void* emb, int64_t V, int64_t D, const void* ple_t
 // ple[l][:] = (RMSNorm_P(ctx[l][:] * proj_scale) * gamma + tok[l][:]) * comb, l < L
 void launch_gemma_ple_inputs(const float* ctx, const float* tok, const float* gamma, float eps, float proj_scale, float comb, float* ple, int64_t L, int64_t P,
                              hipStream_t s);
-// attention of one row over a K/V cache: K [Hkv][Dh][slots] (channel-major),
-// V [Hkv][slots][Dh]; position p lives in slot p % slots (window > 0: a ring of
-// `window` slots) or slot p (full)
+// attention of one row over a K/V cache: K and V [Hkv][slots][Dh] (row-major);
+// position p lives in slot p % slots (window > 0: a ring of `window` slots)
+// or slot p (full)
 struct GemmaAttnArgs {
     const float* proj;        // [q Hq*Dh | k Hkv*Dh at k_off | v Hkv*Dh at v_off]
     int64_t k_off, v_off;

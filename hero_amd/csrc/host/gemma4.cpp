@@ -136,7 +136,7 @@ void Gemma4Model::load(const GgufFile& g) {
     expect(c.D > 0 && c.D <= 4096 && c.D % 32 == 0, "embedding_length must be a multiple of 32 up to 4096");
     expect(c.FF > 0 && c.FF % 32 == 0, "feed_forward_length must be a positive multiple of 32");
     expect(c.P > 0 && c.P <= 4096 && c.P % 32 == 0, "embedding_length_per_layer_input must be a multiple of 32 up to 4096");
-    expect(c.Hkv > 0 && c.Hq > 0 && c.Hq % c.Hkv == 0, "head_count must be a multiple of head_count_kv");
+    expect(c.Hkv > 0 && c.Hq > 0 && c.Hq % c.Hkv == 0 && c.Hq / c.Hkv <= kAttnMaxGroup, "head_count must be a multiple of head_count_kv, at most 8 per KV head");
     expect((c.Dl == 256 || c.Dl == 512) && (c.Df == 256 || c.Df == 512), "this build runs heads of 256 or 512");
     expect(c.Hq * std::max(c.Dl, c.Df) <= 65536, "too many query channels");
     expect(c.local_rot > 0 && c.local_rot <= c.Dl && c.local_rot % 2 == 0 && c.full_rot > 0 && c.full_rot <= c.Df && c.full_rot % 2 == 0, "rope dimension counts out of range");

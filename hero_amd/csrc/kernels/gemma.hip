@@ -110,27 +110,59 @@ void launch_gemma_ple_inputs(const float* ctx, const float* tok, const float* ga
 }
 
 // ---- attention -----------------------------------------------------------------------
-__device__ __forceinline__ int64_t gemma_slot(const GemmaAttnArgs& a, int64_t pos) { return a.window > 0 ? pos % a.slots : pos; }
-
-// One head of DH values, a lane per value: x (RMSNorm over the head: the
-// learned weight gamma, or none for V), then RoPE on the planes (i, i + DH/2)
-// with the position's (cos, sin) table row (RotaryEmbedding,
-// nm/src/attention.hpp:82-91; unrotated planes carry (1, 0)).
-// PerHeadNorm (components.hpp:248-258) with RMSNorm (:176-181) or RMSNormNoScale (:210-215).
-template <int DH>
-__device__ __forceinline__ float gemma_head_norm(float x, const float* gamma, float eps, float* sq, seqsum::Shared& sm) {
-    const int j = threadIdx.x;
-    for (int i = j; i < seqsum::kMaxN; i += DH) sq[i] = i == j ? x * x : 0.f;
-    __syncthreads();
-    const float s = seqsum::sum_nonneg<DH>(sq, DH, sm);
-    const float inv = 1.f / sqrtf(s / float(DH) + eps);
-    return gamma ? gamma[j] * x * inv : x * inv;
+// Position p lives in slot p % slots of a ring (window > 0) or slot p; the
+// visible positions of a row at `pos` are [first, pos], first =
+// max(0, pos + 1 - window) (CausalWindow::visible_rows, nm/src/attention.hpp:170-176).
+// Slots are walked from first's slot with one wrap (n <= slots).
+struct GemmaSpan {
+    int first, n, slot0, slots;
+    __device__ __forceinline__ int slot(int t) const {
+        const int s = slot0 + t;
+        return s >= slots ? s - slots : s;
+    }
+};
+__device__ __forceinline__ GemmaSpan gemma_span(const GemmaAttnArgs& a) {
+    const int pos = *a.pos;
+    GemmaSpan v;
+    v.first = (a.window > 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
+    v.n = pos + 1 - v.first;
+    v.slots = int(a.slots);
+    v.slot0 = a.window > 0 ? v.first % v.slots : v.first;
+    return v;
 }
 
+// The sequential sum of n <= 4096 floats in shared memory by lane 0 (float4
+// reads): the reference's loop, for sums short enough that one dependent
+// chain beats the parallel exact form.
+__device__ __forceinline__ float serial_sum_lds(const float* p, int n) {
+    float s = 0.f;
+    const float4* p4 = reinterpret_cast<const float4*>(p);
+    int i = 0;
+    for (; i + 4 <= n; i += 4) {
+        const float4 v = p4[i / 4];
+        s += v.x;
+        s += v.y;
+        s += v.z;
+        s += v.w;
+    }
+    for (; i < n; ++i) s += p[i];
+    return s;
+}
+
+// One head of DH values, a lane per value: RMSNorm over the head (the learned
+// weight gamma, or none for V; PerHeadNorm, components.hpp:248-258, with
+// RMSNorm :176-181 or RMSNormNoScale :210-215), then with cs RoPE on the
+// planes (i, i + DH/2) from the position's (cos, sin) row (RotaryEmbedding,
+// nm/src/attention.hpp:82-91; unrotated planes carry (1, 0)).
 template <int DH>
-__device__ __forceinline__ float gemma_rope(float n, const float* cs, float* buf) {
+__device__ __forceinline__ float gemma_head(float x, const float* gamma, float eps, const float* cs, float* buf, float* scal) {
     const int j = threadIdx.x;
-    __syncthreads();  // buf free
+    buf[j] = x * x;
+    __syncthreads();
+    if (j == 0) scal[0] = 1.f / sqrtf(serial_sum_lds(buf, DH) / float(DH) + eps);
+    __syncthreads();
+    const float n = gamma ? gamma[j] * x * scal[0] : x * scal[0];
+    if (!cs) return n;
     buf[j] = n;
     __syncthreads();
     constexpr int half = DH / 2;
@@ -146,124 +178,181 @@ __device__ __forceinline__ float gemma_rope(float n, const float* cs, float* buf
 // V = v_norm(WV x) (GemmaE4BLayer::attention, nm/src/gemma4.hpp:205-208).
 template <int DH>
 __global__ __launch_bounds__(DH) void gemma_attn_prep_kernel(GemmaAttnArgs a) {
-    __shared__ seqsum::Shared sm;
-    __shared__ __align__(16) float sq[seqsum::kMaxN];
-    __shared__ float buf[DH];
+    __shared__ __align__(16) float buf[DH];
+    __shared__ float scal[1];
     const int j = threadIdx.x, blk = blockIdx.x;
-    const int64_t pos = *a.pos;
-    const float* cs = a.rope_cs + pos * DH;  // [DH/2][2]
+    const int pos = *a.pos;
+    const float* cs = a.rope_cs + int64_t(pos) * DH;  // [DH/2][2]
     if (blk < a.Hq) {
-        const float n = gemma_head_norm<DH>(a.proj[int64_t(blk) * DH + j], a.q_gamma, a.eps, sq, sm);
-        a.q_rot[int64_t(blk) * DH + j] = gemma_rope<DH>(n, cs, buf);
+        a.q_rot[int64_t(blk) * DH + j] = gemma_head<DH>(a.proj[int64_t(blk) * DH + j], a.q_gamma, a.eps, cs, buf, scal);
         return;
     }
-    const int64_t slot = gemma_slot(a, pos);
+    const int64_t slot = a.window > 0 ? pos % a.slots : pos;
     const int g = blk - a.Hq;
     if (g < a.Hkv) {
-        const float n = gemma_head_norm<DH>(a.proj[a.k_off + int64_t(g) * DH + j], a.k_gamma, a.eps, sq, sm);
-        a.k_cache[(int64_t(g) * DH + j) * a.slots + slot] = gemma_rope<DH>(n, cs, buf);  // [Hkv][DH][slots]
+        a.k_cache[(int64_t(g) * a.slots + slot) * DH + j] = gemma_head<DH>(a.proj[a.k_off + int64_t(g) * DH + j], a.k_gamma, a.eps, cs, buf, scal);  // [Hkv][slots][DH]
         return;
     }
     const int gv = g - a.Hkv;
-    const float n = gemma_head_norm<DH>(a.proj[a.v_off + int64_t(gv) * DH + j], nullptr, a.eps, sq, sm);
-    a.v_cache[(int64_t(gv) * a.slots + slot) * DH + j] = n;  // [Hkv][slots][DH]
+    a.v_cache[(int64_t(gv) * a.slots + slot) * DH + j] = gemma_head<DH>(a.proj[a.v_off + int64_t(gv) * DH + j], nullptr, a.eps, nullptr, buf, scal);  // [Hkv][slots][DH]
 }
 
-// One query head per workgroup of DH lanes (Gemma's reduction,
-// nm/src/gemma4.hpp:210-230: no score scale):
-//   s_t = dot(q, k_t) over the visible positions, each the sequential DH-term sum;
-//   alpha = softmax(s) (components.hpp:131-141: e_t = exp(s_t - max), their
-//   sequential sum, e_t / total);
-//   out[c] = sum_t alpha_t v_t[c], t in order (Vec::scaled_add, core.hpp:206-208);
-// then the head's Q8_0 blocks of the W_o input.
+// Scores s_t = dot(q_h, k_t), each the sequential DH-term sum (core.hpp:496-500;
+// no score scale: Gemma folds it into the Q norm, gemma4.hpp:197-200).
+// Workgroup (KV head g, tile y): 64 positions per tile, tiles y, y + gridDim.y,
+// ...; the tile's key rows are staged in shared memory (all its 16-byte loads
+// in flight together; rows padded by one float: conflict-free column reads),
+// then wave w forms heads w, w + 4, ... of the group, a lane per position.
+constexpr int kGsTile = 64;
+
 template <int DH>
-__global__ __launch_bounds__(DH) void gemma_attn_kernel(GemmaAttnArgs a) {
+__global__ __launch_bounds__(256) void gemma_scores_kernel(GemmaAttnArgs a) {
+    constexpr int KS = DH + 1;  // padded key row
+    extern __shared__ __align__(16) float kt[];  // [kGsTile][KS], then q [group][DH]
+    float* q = kt + kGsTile * KS;
+    const int g = blockIdx.x, group = a.Hq / a.Hkv;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const GemmaSpan sp = gemma_span(a);
+    for (int i = tid; i < group * DH; i += 256) q[i] = a.q_rot[int64_t(g) * group * DH + i];
+    const float* kh = a.k_cache + int64_t(g) * a.slots * DH;
+    const int tiles = (sp.n + kGsTile - 1) / kGsTile;
+    constexpr int Q4 = DH / 4;                    // float4s per key row
+    constexpr int LOADS = kGsTile * Q4 / 256;     // per lane: 16 (DH 256) or 32 (DH 512)
+    for (int tile = blockIdx.y; tile < tiles; tile += gridDim.y) {
+        const int t0 = tile * kGsTile;
+        float4 v[LOADS];
+#pragma unroll
+        for (int k = 0; k < LOADS; ++k) {
+            const int e = tid + 256 * k, key = e / Q4, c4 = e % Q4;
+            v[k] = t0 + key < sp.n ? reinterpret_cast<const float4*>(kh + int64_t(sp.slot(t0 + key)) * DH)[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        __syncthreads();  // the previous tile's readers are done
+#pragma unroll
+        for (int k = 0; k < LOADS; ++k) {
+            const int e = tid + 256 * k, key = e / Q4, c4 = e % Q4;
+            float* dst = kt + key * KS + 4 * c4;
+            dst[0] = v[k].x, dst[1] = v[k].y, dst[2] = v[k].z, dst[3] = v[k].w;
+        }
+        __syncthreads();
+        const int t = t0 + lane;
+        if (t < sp.n) {
+            const float* kr = kt + lane * KS;
+            for (int hh = wave; hh < group; hh += 4) {
+                const float* qh = q + hh * DH;
+                float dot = 0.f;
+#pragma unroll 16
+                for (int c = 0; c < DH; ++c) dot += qh[c] * kr[c];
+                a.scores[int64_t(g * group + hh) * a.max_ctx + t] = dot;
+            }
+        }
+    }
+}
+
+// The softmax of head h's n scores (components.hpp:131-141: e_t = exp(s_t - max),
+// their sequential sum in chunks, each starting with the running total,
+// alpha_t = e_t / total) and the weighted sum of its value rows for 64
+// channels, out[c] = sum_t alpha_t v_t[c] in order (Vec::scaled_add,
+// core.hpp:206-208: out += alpha * v), then the two Q8_0 blocks of the W_o input
+// those channels make (quantize_row_q8_0, quant_i8.hpp:70-80).
+// Workgroup (head, 64 channels) of 256 lanes: chunks of kPvChunk positions,
+// each chunk's value rows loaded by all lanes (the next chunk's loads in
+// flight while wave 0, a lane per channel, runs the current chunk's chain
+// out of shared memory).
+constexpr int kPvChunk = 128;
+
+template <int DH>
+__global__ __launch_bounds__(256) void gemma_softmax_pv_kernel(GemmaAttnArgs a) {
     __shared__ seqsum::Shared sm;
     __shared__ __align__(16) float chunk[seqsum::kMaxN];
-    __shared__ __align__(16) float q[DH];
-    __shared__ float red[DH / 64];
-    const int j = threadIdx.x, h = blockIdx.x;
-    const int g = h / (a.Hq / a.Hkv);  // adjacent query heads share a K/V head
-    const int64_t pos = *a.pos;
-    const int64_t first = (a.window > 0 && pos + 1 > a.window) ? pos + 1 - a.window : 0;
-    const int64_t n = pos + 1 - first;
-    q[j] = a.q_rot[int64_t(h) * DH + j];
-    __syncthreads();
-    const float* kh = a.k_cache + int64_t(g) * DH * a.slots;
-    const float* vh = a.v_cache + int64_t(g) * a.slots * DH;
-    float* sc = a.scores + int64_t(h) * a.max_ctx;
+    __shared__ __align__(16) float vb[2][kPvChunk][64];
+    __shared__ float al[2][kPvChunk];
+    __shared__ float red[4];
+    const int tid = threadIdx.x, h = blockIdx.x, c0 = blockIdx.y * 64;
+    const int g = h / (a.Hq / a.Hkv);
+    const GemmaSpan sp = gemma_span(a);
+    const int n = sp.n;
+    const float* sc = a.scores + int64_t(h) * a.max_ctx;
+    // max, then the exponentials' sequential sum
     float mx = -INFINITY;
-    for (int64_t t = j; t < n; t += DH) {
-        const int64_t slot = gemma_slot(a, first + t);
-        float dot = 0.f;
-#pragma unroll 8
-        for (int c = 0; c < DH; ++c) dot += q[c] * kh[int64_t(c) * a.slots + slot];
-        sc[t] = dot;
-        mx = fmaxf(mx, dot);
-    }
+    for (int t = tid; t < n; t += 256) mx = fmaxf(mx, sc[t]);
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if ((j & 63) == 0) red[j >> 6] = mx;
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
-    mx = red[0];
-#pragma unroll
-    for (int w = 1; w < DH / 64; ++w) mx = fmaxf(mx, red[w]);
-    // exponentials and their sequential sum, chunk by chunk, each chunk
-    // starting with the running total (fl(0 + e) == e: the first chunk is the
-    // loop from 0). Chunks start at multiples of DH, so lane j handles the
-    // positions t == j (mod DH) throughout: the scores it wrote itself.
-    constexpr int CH = seqsum::kMaxN - DH;
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    constexpr int CH = seqsum::kMaxN - 256;
     float total = 0.f;
-    for (int64_t base = 0; base < n; base += CH) {
-        const int len = int(min<int64_t>(n - base, CH));
+    for (int base = 0; base < n; base += CH) {
+        const int len = min(n - base, CH);
         __syncthreads();  // chunk free
-        for (int u = j; u < seqsum::kMaxN; u += DH) chunk[u] = 0.f;
+        for (int u = tid; u < len; u += 256) chunk[1 + u] = exp_f32(sc[base + u] - mx);
+        if (tid == 0) chunk[0] = total;
         __syncthreads();
-        for (int u = j; u < len; u += DH) {
-            const float e = exp_f32(sc[base + u] - mx);
-            sc[base + u] = e;
-            chunk[1 + u] = e;
-        }
-        if (j == 0) chunk[0] = total;
-        __syncthreads();
-        total = seqsum::sum_nonneg<DH>(chunk, len + 1, sm);
-    }
-    // alpha_t = e_t / total, staged in shared memory chunk by chunk (again by
-    // the lanes that own them), and the weighted sum of the value rows
-    float acc = 0.f;
-    for (int64_t base = 0; base < n; base += seqsum::kMaxN) {
-        const int len = int(min<int64_t>(n - base, seqsum::kMaxN));
-        __syncthreads();
-        for (int u = j; u < len; u += DH) chunk[u] = sc[base + u] / total;
-        __syncthreads();
-        for (int u = 0; u < len; ++u) {
-            const int64_t slot = gemma_slot(a, first + base + u);
-            acc += chunk[u] * vh[slot * DH + j];
+        if (len < 1024) {  // a short chain: one lane
+            if (tid == 0) sm.result = serial_sum_lds(chunk, len + 1);
+            __syncthreads();
+            total = sm.result;
+        } else {
+            for (int u = len + 1 + tid; u < seqsum::kMaxN; u += 256) chunk[u] = 0.f;
+            __syncthreads();
+            total = seqsum::sum_nonneg<256>(chunk, len + 1, sm);
         }
     }
-    // the W_o input: this head's DH / 32 Q8_0 blocks
-    __syncthreads();
-    chunk[j] = acc;
-    __syncthreads();
-    if (j < DH / 8) {
-        float v[8];
+    // the weighted sum: value rows [slot][DH] of KV head g, channels c0 .. c0+63
+    const float* vh = a.v_cache + int64_t(g) * a.slots * DH + c0;
+    constexpr int LOADS = kPvChunk * 16 / 256;  // float4s per lane: 8
+    float4 v[LOADS];
+    auto fetch = [&](int base) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = chunk[8 * j + k];
-        uint16_t dh;
-        int8_t* qs = static_cast<int8_t*>(a.act_out);
-        float* qd = reinterpret_cast<float*>(qs + int64_t(a.Hq) * DH);
-        reinterpret_cast<int2*>(qs + int64_t(h) * DH)[j] = quantize8_in_quad(v, &dh);
-        if ((j & 3) == 0) qd[int64_t(h) * (DH / 32) + (j >> 2)] = half_bits_to_f32(dh);
+        for (int k = 0; k < LOADS; ++k) {
+            const int e = tid + 256 * k, key = e >> 4, c4 = e & 15;
+            v[k] = base + key < n ? reinterpret_cast<const float4*>(vh + int64_t(sp.slot(base + key)) * DH)[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    fetch(0);
+    float acc = 0.f;
+    int buf = 0;
+    for (int base = 0; base < n; base += kPvChunk) {
+#pragma unroll
+        for (int k = 0; k < LOADS; ++k) {
+            const int e = tid + 256 * k;
+            reinterpret_cast<float4*>(&vb[buf][0][0])[e] = v[k];
+        }
+        if (tid < kPvChunk && base + tid < n) al[buf][tid] = exp_f32(sc[base + tid] - mx) / total;
+        __syncthreads();
+        if (base + kPvChunk < n) fetch(base + kPvChunk);
+        if (tid < 64) {
+            const int len = min(kPvChunk, n - base);
+            for (int k = 0; k < len; ++k) acc += al[buf][k] * vb[buf][k][tid];
+        }
+        buf ^= 1;
     }
+    if (tid >= 64) return;
+    // Q8_0 of the 32-channel block this lane is in
+    float amax = fabsf(acc);
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    const float d = amax / 127.f;
+    const float id = d != 0.f ? 1.f / d : 0.f;
+    int8_t* qs = static_cast<int8_t*>(a.act_out);
+    float* qd = reinterpret_cast<float*>(qs + int64_t(a.Hq) * DH);
+    const int64_t idx = int64_t(h) * DH + c0 + tid;
+    qs[idx] = int8_t(int(roundf(acc * id)));
+    if ((tid & 31) == 0) qd[idx >> 5] = half_bits_to_f32(fp32_to_fp16_ref(d));
 }
 
 void launch_gemma_attention(const GemmaAttnArgs& a, hipStream_t s) {
     const unsigned prep = unsigned(a.Hq + (a.append ? 2 * a.Hkv : 0));
+    const int64_t vis = a.window > 0 ? std::min<int64_t>(a.window, a.slots) : a.max_ctx;
+    const unsigned tiles = unsigned(std::min<int64_t>(128, (vis + kGsTile - 1) / kGsTile));
+    const int group = a.Hq / a.Hkv;
     if (a.Dh == 256) {
         hipLaunchKernelGGL(gemma_attn_prep_kernel<256>, dim3(prep), dim3(256), 0, s, a);
-        hipLaunchKernelGGL(gemma_attn_kernel<256>, dim3(unsigned(a.Hq)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(gemma_scores_kernel<256>, dim3(unsigned(a.Hkv), tiles), dim3(256), size_t(kGsTile * 257 + group * 256) * 4, s, a);
+        hipLaunchKernelGGL(gemma_softmax_pv_kernel<256>, dim3(unsigned(a.Hq), 256 / 64), dim3(256), 0, s, a);
     } else {
         hipLaunchKernelGGL(gemma_attn_prep_kernel<512>, dim3(prep), dim3(512), 0, s, a);
-        hipLaunchKernelGGL(gemma_attn_kernel<512>, dim3(unsigned(a.Hq)), dim3(512), 0, s, a);
+        hipLaunchKernelGGL(gemma_scores_kernel<512>, dim3(unsigned(a.Hkv), tiles), dim3(256), size_t(kGsTile * 513 + group * 512) * 4, s, a);
+        hipLaunchKernelGGL(gemma_softmax_pv_kernel<512>, dim3(unsigned(a.Hq), 512 / 64), dim3(256), 0, s, a);
     }
 }
 
@@ -335,26 +424,25 @@ void launch_gemma_post_norm(const float* a, const float* gamma, const float* res
 // act = Q8_0 of gelu(gate[i]) * mul[i]: the GELU-gated MLP's down input
 // (GatedMLP, components.hpp:294-299: g = gelu(gate(x)); g *= up(x)) and the
 // PLE branch input (gemma4.hpp:100-101: hadamard(gelu(gate(h)), ple)).
-// A lane per 8 values (N % 32 == 0).
+// A lane per value (tanh's chain is long: every lane runs one); the 32 lanes
+// of a Q8_0 block share its amax (N % 32 == 0).
 __global__ __launch_bounds__(256) void gemma_gelu_mul_quant_kernel(const float* __restrict__ gate, const float* __restrict__ mul, int8_t* __restrict__ qs,
                                                                    float* __restrict__ qd, int64_t N) {
-    const int64_t lane = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (lane >= N / 8) return;  // whole quads
-    const float4 g0 = reinterpret_cast<const float4*>(gate)[2 * lane], g1 = reinterpret_cast<const float4*>(gate)[2 * lane + 1];
-    const float4 m0 = reinterpret_cast<const float4*>(mul)[2 * lane], m1 = reinterpret_cast<const float4*>(mul)[2 * lane + 1];
-    const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-    const float m[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
-    float v[8];
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= N) return;  // whole 32-lane blocks
+    const float v = gelu_tanh_f32(gate[i]) * mul[i];
+    float amax = fabsf(v);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = gelu_tanh_f32(g[k]) * m[k];
-    uint16_t dh;
-    reinterpret_cast<int2*>(qs)[lane] = quantize8_in_quad(v, &dh);
-    if ((lane & 3) == 0) qd[lane >> 2] = half_bits_to_f32(dh);
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    const float d = amax / 127.f;
+    const float id = d != 0.f ? 1.f / d : 0.f;
+    qs[i] = int8_t(int(roundf(v * id)));
+    if ((i & 31) == 0) qd[i >> 5] = half_bits_to_f32(fp32_to_fp16_ref(d));
 }
 
 void launch_gemma_gelu_mul_quant(const float* gate, const float* mul, void* act, int64_t N, hipStream_t s) {
     int8_t* qs = static_cast<int8_t*>(act);
-    hipLaunchKernelGGL(gemma_gelu_mul_quant_kernel, dim3(unsigned((N / 8 + 255) / 256)), dim3(256), 0, s, gate, mul, qs, reinterpret_cast<float*>(qs + N), N);
+    hipLaunchKernelGGL(gemma_gelu_mul_quant_kernel, dim3(unsigned((N + 255) / 256)), dim3(256), 0, s, gate, mul, qs, reinterpret_cast<float*>(qs + N), N);
 }
 
 // ---- the logit soft-cap ---------------------------------------------------------------

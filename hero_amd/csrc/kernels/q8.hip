@@ -17,8 +17,10 @@
 // sums and the per-block terms are computed in parallel; the final fp32 sum
 // is a sequential chain per row, so y is bit-identical to the reference.
 #include "hero/device.hpp"
+#include "hero/errors.hpp"
 #include "hero/kernels.hpp"
 #include "hero/seqsum.hpp"
+#include "hero_kernels.h"
 
 namespace hero {
 
@@ -102,10 +104,18 @@ void launch_pack_q8(const void* gguf_blocks, void* packed, int64_t N_total, int6
 // ---------------------------------------------------------------------------
 constexpr int kStreamRB = 8;  // rows per sub-batch
 
-template <int LG, int D, int EPI, int XM, int IL>
-__global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, GemvInput in, float* __restrict__ y, const float* __restrict__ resid, int N, int Npad, int TR) {
-    constexpr int K = 4096 * LG, nb = K / 32, ts = nb + 4;  // ts: padded term row (conflict-free 16-byte reads)
+// KC = K / 16 lanes carry a row's 16-byte chunks; the workgroup is KC rounded
+// up to whole waves, the lanes past KC issuing the same loads at out-of-range
+// offsets (zeros) and storing nothing.
+template <int KC>
+constexpr int stream_threads() { return (KC + 63) / 64 * 64; }
+
+template <int KC, int D, int EPI, int XM, int IL>
+__global__ __launch_bounds__(stream_threads<KC>()) void gemv_q8_stream_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, GemvInput in, float* __restrict__ y, const float* __restrict__ resid, int N, int Npad, int TR) {
+    constexpr int K = 16 * KC, nb = K / 32, ts = nb + 4;  // ts: padded term row (conflict-free 16-byte reads)
     constexpr int CPL = 1;  // K-chunks per lane
+    static_assert(KC % 2 == 0, "whole Q8_0 blocks");
+    static_assert(XM == kInAct || KC % 256 == 0, "the fused inputs take whole 256-lane groups");
     // row ranges in whole units: 8-row groups, or for the SwiGLU epilogue
     // 64-row groups of [32 gate rows | 32 up rows]
     constexpr int UR = EPI == kEpiSwigluQuant ? 64 : 8;
@@ -122,6 +132,7 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
     const int nsub = IL ? (U - int(blockIdx.x) + G - 1) / G : (rows + kStreamRB - 1) / kStreamRB;
     auto grp = [&](int j) { return IL ? int(blockIdx.x) + j * G : r_begin / kStreamRB + j; };  // 8-row group of sub-batch j
     const bool even = (tid & 1) == 0;
+    const bool on = tid < KC;  // the lane carries a chunk
     // the workgroup's rows (rows * K bytes) and their scale groups (nsub groups
     // of nb blocks x 8 fp16; r_begin is a multiple of 8); IL: the whole matrix
     const __amdgpu_buffer_rsrc_t bw = buffer_of(wq + int64_t(r_begin) * K, uint32_t(rows) * uint32_t(K));
@@ -141,11 +152,11 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int m = 0; m < CPL; ++m)  // the group's 8 scales of block tid / 2
-            sdst[m] = load_b128(bd, even && live ? (gj * uint32_t(nb) + uint32_t(tid >> 1)) * 16u : kOOB);
+            sdst[m] = load_b128(bd, even && live && on ? (gj * uint32_t(nb) + uint32_t(tid >> 1)) * 16u : kOOB);
 #pragma unroll
         for (int r = 0; r < kStreamRB; ++r)
 #pragma unroll
-            for (int m = 0; m < CPL; ++m) dst[r][m] = load_b128(bw, live ? (row0 + uint32_t(r)) * uint32_t(K) + uint32_t(tid) * 16u : kOOB);
+            for (int m = 0; m < CPL; ++m) dst[r][m] = load_b128(bw, live && on ? (row0 + uint32_t(r)) * uint32_t(K) + uint32_t(tid) * 16u : kOOB);
         __builtin_amdgcn_sched_barrier(0);
     };
     // The lane's x chunk tid as Q8_0, and the residual of the first
@@ -159,12 +170,12 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
     if constexpr (XM == kInAct) {
 #pragma unroll
         for (int m = 0; m < CPL; ++m) {
-            const int c = tid;
+            const int c = on ? tid : 0;
             xv[m] = reinterpret_cast<const int4*>(in.xq)[c];
             dx[m] = in.xd[c >> 1];
         }
     } else if constexpr (XM == kInRmsNorm) {
-        static_assert(LG == 1, "RMSNorm input needs K == 4096");
+        static_assert(KC == 256, "RMSNorm input needs K == 4096");
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const float4 a = reinterpret_cast<const float4*>(in.x)[4 * tid + k];
@@ -173,7 +184,7 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
             gr[4 * k] = g.x, gr[4 * k + 1] = g.y, gr[4 * k + 2] = g.z, gr[4 * k + 3] = g.w;
         }
     } else if constexpr (XM == kInHeadGate) {
-        static_assert(LG == 1, "head-gate input needs K == 4096");
+        static_assert(KC == 256, "head-gate input needs K == 4096");
         // elements 16 tid .. +15: head tid / 8, columns 16 (tid % 8) .. +15
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -293,7 +304,7 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
                 for (int m = 0; m < CPL; ++m) {
                     int v = dot16_i8(ring[s][r][m], xv[m], 0);
                     v += pair_swap_i32(v);  // the block's other 16 bytes (exact)
-                    if (even && r < rvalid) {
+                    if (even && on && r < rvalid) {
                         const int4 sc = sring[s][m];
                         const uint32_t two = uint32_t(pair == 0 ? sc.x : pair == 1 ? sc.y : pair == 2 ? sc.z : sc.w);
                         const uint16_t h = uint16_t((r & 1) ? (two >> 16) : (two & 0xFFFFu));
@@ -309,9 +320,12 @@ __global__ __launch_bounds__(256 * LG) void gemv_q8_stream_kernel(const int8_t* 
                 if (tid < prow) {
                     const float4* t = reinterpret_cast<const float4*>(terms + tid * ts);
                     float acc = 0.f;
+                    // four float4s of terms per step; past the row's nb / 4 the
+                    // terms are zeros (acc + 0 == acc: acc is never -0)
+                    static_assert(nb % 4 == 0, "K a multiple of 128");
                     float4 q[4];
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) q[u] = t[u];
+                    for (int u = 0; u < 4; ++u) q[u] = u < nb / 4 ? t[u] : make_float4(0.f, 0.f, 0.f, 0.f);
                     for (int b4 = 0; b4 < nb / 4; b4 += 4) {
                         float4 nq[4];
 #pragma unroll
@@ -448,37 +462,42 @@ int device_cus() {
 
 namespace {
 
-// K = 4096 outside the SwiGLU epilogue: interleaved 8-row groups (the grid
-// reads one contiguous stretch of the matrix at a time: 0.3-2.7 us less per
-// launch at the decode shapes); K = 8192, 12288 keep contiguous ranges
-template <int LG, int D, int XM>
+// Interleaved 8-row groups (the grid reads one contiguous stretch of the
+// matrix at a time: 0.3-2.7 us less per launch at K = 4096) except for the
+// SwiGLU epilogue and K = 8192, 12288, which keep contiguous ranges
+template <int KC, int D, int XM>
 void stream_dispatch(int epi, const int8_t* wq, const uint16_t* wd, const GemvInput& in, float* y, const float* resid, int N, int Npad, int G, int TR, size_t smem, hipStream_t s) {
-    const dim3 block(256 * LG);
-    constexpr int IL = LG == 1;
+    const dim3 block(stream_threads<KC>());
+    constexpr int IL = KC == 256 || KC % 256 != 0;
     if (epi == kEpiResidual)
-        hipLaunchKernelGGL((gemv_q8_stream_kernel<LG, D, kEpiResidual, XM, IL>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
-    else if constexpr (LG == 1)
+        hipLaunchKernelGGL((gemv_q8_stream_kernel<KC, D, kEpiResidual, XM, IL>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
+    else if constexpr (KC == 256)
         if (epi == kEpiSwigluQuant)
-            hipLaunchKernelGGL((gemv_q8_stream_kernel<LG, D, kEpiSwigluQuant, XM, 0>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
+            hipLaunchKernelGGL((gemv_q8_stream_kernel<KC, D, kEpiSwigluQuant, XM, 0>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
         else
-            hipLaunchKernelGGL((gemv_q8_stream_kernel<LG, D, kEpiStore, XM, IL>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
+            hipLaunchKernelGGL((gemv_q8_stream_kernel<KC, D, kEpiStore, XM, IL>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
     else
-        hipLaunchKernelGGL((gemv_q8_stream_kernel<LG, D, kEpiStore, XM, 0>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
+        hipLaunchKernelGGL((gemv_q8_stream_kernel<KC, D, kEpiStore, XM, IL>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
 }
 
-template <int LG, int D>
+template <int KC, int D>
 void stream_dispatch_in(int epi, const int8_t* wq, const uint16_t* wd, const GemvInput& in, float* y, const float* resid, int N, int Npad, int G, int TR, size_t smem, hipStream_t s) {
-    if (in.mode == kInSwiglu)
-        stream_dispatch<LG, D, kInSwiglu>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
-    else if constexpr (LG == 1)
+    if constexpr (KC % 256 == 0) {
+        if (in.mode == kInSwiglu) {
+            stream_dispatch<KC, D, kInSwiglu>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
+            return;
+        }
+    }
+    if constexpr (KC == 256) {
         if (in.mode == kInRmsNorm)
-            stream_dispatch<LG, D, kInRmsNorm>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
+            stream_dispatch<KC, D, kInRmsNorm>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
         else if (in.mode == kInHeadGate)
-            stream_dispatch<LG, D, kInHeadGate>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
+            stream_dispatch<KC, D, kInHeadGate>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
         else
-            stream_dispatch<LG, D, kInAct>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
-    else
-        stream_dispatch<LG, D, kInAct>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
+            stream_dispatch<KC, D, kInAct>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
+    } else {
+        stream_dispatch<KC, D, kInAct>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
+    }
 }
 
 template <int IPT>
@@ -492,7 +511,16 @@ void gemv_dispatch_epi(int epi, const int8_t* wq, const uint16_t* wd, const int8
 
 }  // namespace
 
+// the row lengths with a streaming instantiation: K = 4096, 8192, 12288 (every
+// input form) and the other decode widths of the Qwen and Gemma models (the
+// plain quantized input)
 bool gemv_streams(int64_t K) { return K % 4096 == 0 && K / 4096 <= 3; }
+bool gemv_streams_act(int64_t K) {
+    switch (K) {
+        case 256: case 1024: case 2048: case 2560: case 2816: case 4096: case 8192: case 10240: case 12288: return true;
+        default: return false;
+    }
+}
 
 int gemv_stream_grid(int64_t N, int epi) {
     const int64_t unit = epi == kEpiSwigluQuant ? 64 : 8;
@@ -534,19 +562,26 @@ void launch_gemv_q8_in(const void* packed, const GemvInput& in, float* y, const 
     const int64_t TR = epi == kEpiSwigluQuant ? 64 : std::min<int64_t>({64, rows_per, (65536 / ((nb + 4) * 4)) / 8 * 8});
     size_t smem = size_t(TR) * (nb + 4) * 4;
     if (in.mode == kInRmsNorm || in.mode == kInHeadGate) smem = std::max(smem, size_t(K) * 4);  // the squares
-    switch (K / 4096) {
-        // a ring of two 8-row sub-batches: deeper rings only add padding
-        // sub-batches where a workgroup has few rows
-        case 1: stream_dispatch_in<1, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
-        case 2: stream_dispatch_in<2, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
-        default: stream_dispatch_in<3, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+    // a ring of two 8-row sub-batches: deeper rings only add padding
+    // sub-batches where a workgroup has few rows
+    switch (K) {
+        case 256: stream_dispatch_in<16, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+        case 1024: stream_dispatch_in<64, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+        case 2048: stream_dispatch_in<128, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+        case 2560: stream_dispatch_in<160, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+        case 2816: stream_dispatch_in<176, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+        case 4096: stream_dispatch_in<256, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+        case 8192: stream_dispatch_in<512, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+        case 10240: stream_dispatch_in<640, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+        case 12288: stream_dispatch_in<768, 2>(epi, wq, wd, in, y, resid, int(N), Npad, G, int(TR), smem, s); break;
+        default: throw Error(HERO_EINVAL, "streaming GEMV: no instantiation for K = " + std::to_string(K));
     }
 }
 
 void launch_gemv_q8(const void* packed, const void* act, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s) {
     const int8_t* xq = static_cast<const int8_t*>(act);
     const float* xd = reinterpret_cast<const float*>(xq + K);
-    if (gemv_streams(K)) {
+    if (gemv_streams_act(K)) {
         GemvInput in{};
         in.mode = kInAct;
         in.xq = xq;

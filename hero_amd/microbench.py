@@ -23,6 +23,10 @@ gdn    the fused delta-net layer body (conv + SiLU, L2 norms, gates, the delta
        128 x 128: one decode step at B in {1, 8, 32} from a state warmed by 64
        steps, and the prefill of 4096 tokens: the bit-exact token-serial scan
        and the chunked (WY) form with chunks of 64.
+gemma4 the Gemma 4 E4B decode step (seeded synthetic 7.9 GB Q8_0 model): a
+       --gemma4-ctx-token prompt, then 32 greedy passes replayed as one
+       hipGraph each; ms per pass and the weight bytes a pass reads (every
+       layer and the tied head, one per-layer-table row) per second.
 attn   gated GQA decode (32 q / 8 kv heads of 128) at context {1k, 8k, 32k} x
        B {1, 16}: full causal (scale 1/sqrt(128)) and a 1024 sliding window
        (scale 1), over the fp32 cache (the reference's precision, bit-exact
@@ -559,9 +563,39 @@ def bench_attn(lib, replays: int = 20, contexts=ATTN_CTX, batches=ATTN_BATCH, ca
     return rows
 
 
+def bench_gemma4(lib, ctx: int = 600, passes: int = 32):
+    import time
+
+    import numpy as np
+
+    from .gemma4 import GEMMA4_E4B, Gemma4Model, synthetic_gemma4_image
+
+    shape = GEMMA4_E4B
+    image = synthetic_gemma4_image(shape, seed=4242)
+    model = Gemma4Model.open_image(image)
+    del image
+    d = model.dims
+    pl = d.per_layer_input * d.layers
+    table = lambda n, k: n * k + (n + 7) // 8 * 8 * (k // 32) * 2  # noqa: E731  packed Q8_0 bytes
+    step_bytes = d.device_bytes - table(d.vocab, pl) + pl * 17 // 16
+    prompt = np.random.default_rng(4242).integers(0, d.vocab, ctx).astype(np.int32)
+    state = model.new_state(ctx + passes + 1)
+    t = time.perf_counter()
+    first = model.forward(state, prompt, want_logits=False)
+    prompt_s = time.perf_counter() - t
+    model.decode_greedy(state, first, passes)
+    sec = model.last_decode_seconds()
+    ms = sec * 1e3 / passes
+    gbs = step_bytes / (sec / passes) / 1e9
+    print(f"gemma4 e4b decode at context {ctx}: {ms:.3f} ms/pass, {1e3 / ms:.1f} tok/s, {gbs:.0f} GB/s of weights", file=sys.stderr)
+    model.close()
+    return [{"suite": "gemma4", "model": "gemma4-e4b (synthetic Q8_0)", "context": ctx, "passes": passes, "prompt_s (token by token)": prompt_s,
+             "ms_per_pass": ms, "tok_s": 1e3 / ms, "weight_MB_per_pass": step_bytes / 1e6, "weight_GBps": gbs, "frac_8TBps": gbs / 8000.0}]
+
+
 def _markdown(rows) -> str:
     out = []
-    for suite in ("hbm", "mall", "gemv", "kquant", "gdn", "attn"):
+    for suite in ("hbm", "mall", "gemv", "kquant", "gdn", "attn", "gemma4"):
         rs = [r for r in rows if r["suite"] == suite]
         if not rs:
             continue
@@ -590,6 +624,7 @@ def main(argv=None) -> int:
     ap.add_argument("--attn-batch", default=",".join(map(str, ATTN_BATCH)), help="batches of the attn suite")
     ap.add_argument("--attn-cache", default=",".join(ATTN_CACHES), help="caches of the attn suite: fp32, fp16 (paged), q8 (paged)")
     ap.add_argument("--attn-variant", default=",".join(ATTN_VARIANTS), help="variants of the attn suite: full, swa1024")
+    ap.add_argument("--gemma4-ctx", type=int, default=600, help="prompt tokens before the gemma4 suite's decode passes")
     ap.add_argument("--direct", type=int, default=0, help="run each case this many times as plain launches instead of graph replays")
     ap.add_argument("--calibrate", action="store_true",
                     help="first copy 512 MiB device to device three times: the known-size dispatches hero_amd.traffic calibrates "
@@ -626,6 +661,8 @@ def main(argv=None) -> int:
     if "attn" in suites:
         rows += bench_attn(lib, contexts=[int(v) for v in args.attn_ctx.split(",")], batches=[int(v) for v in args.attn_batch.split(",")],
                            caches_run=args.attn_cache.split(","), variants=args.attn_variant.split(","))
+    if "gemma4" in suites:
+        rows += bench_gemma4(lib, ctx=args.gemma4_ctx)
     md = _markdown(rows)
     if args.out:
         with open(args.out, "w") as f:

@@ -64,6 +64,16 @@ _sigs = {
     "oracle_model_forward_ids": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "oracle_argmax": (c_int32, [c_void_p, c_size_t]),
     "oracle_model_greedy": (c_int, [c_void_p, c_void_p, c_size_t, c_size_t, c_void_p, c_void_p, POINTER(c_double), POINTER(c_double)]),
+    "oracle_gemma4_open": (c_void_p, [c_char_p]),
+    "oracle_gemma4_open_image": (c_void_p, [c_void_p, c_size_t]),
+    "oracle_gemma4_close": (None, [c_void_p]),
+    "oracle_gemma4_dims": (None, [c_void_p, c_void_p]),
+    "oracle_gemma4_reset": (None, [c_void_p]),
+    "oracle_gemma4_tokens": (c_size_t, [c_void_p]),
+    "oracle_gemma4_kv_source": (c_size_t, [c_void_p, c_size_t]),
+    "oracle_gemma4_embed": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "oracle_gemma4_forward": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "oracle_gemma_math": (None, [c_void_p, c_void_p, c_size_t, c_float]),
 }
 
 
@@ -399,3 +409,72 @@ class Model:
         if lib.oracle_model_greedy(self._h, _p(prompt), len(prompt), steps, _p(ids), _p(logits), ctypes.byref(pf), ctypes.byref(dc)) != 0:
             raise RuntimeError(lib.oracle_last_error().decode())
         return ids, logits, pf.value, dc.value
+
+
+def gemma_math(x, cap: float = 30.0):
+    """(gelu_pytorch_tanh(x), cap * tanh(x / cap)) with glibc's tanhf"""
+    x = _f32(x)
+    out = np.empty(2 * x.size, np.float32)
+    lib.oracle_gemma_math(_p(x), _p(out), x.size, cap)
+    return out[0::2].copy(), out[1::2].copy()
+
+
+class Gemma4:
+    """The oracle's Gemma 4 text model (E4B schema) over a GGUF file or an
+    in-memory image; forward runs the reference's batched form."""
+
+    def __init__(self, path: str | None = None, image: np.ndarray | None = None):
+        if path is not None:
+            self._h = lib.oracle_gemma4_open(path.encode())
+        else:
+            self._image = image
+            self._h = lib.oracle_gemma4_open_image(_p(image), image.nbytes)
+        if not self._h:
+            raise RuntimeError(lib.oracle_last_error().decode())
+        dims = np.zeros(6, np.uint64)
+        lib.oracle_gemma4_dims(self._h, _p(dims))
+        self.V, self.D, self.L, self.window, self.shared, self.P = (int(v) for v in dims)
+
+    def close(self):
+        if self._h:
+            lib.oracle_gemma4_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self):
+        lib.oracle_gemma4_reset(self._h)
+
+    def tokens(self) -> int:
+        return int(lib.oracle_gemma4_tokens(self._h))
+
+    def kv_source(self, layer: int) -> int:
+        return int(lib.oracle_gemma4_kv_source(self._h, layer))
+
+    def embed(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.empty((len(ids), self.D), np.float32)
+        if lib.oracle_gemma4_embed(self._h, _p(ids), len(ids), _p(out)) != 0:
+            raise RuntimeError(lib.oracle_last_error().decode())
+        return out
+
+    def forward(self, ids):
+        """soft-capped logits of the last of the T ids"""
+        ids = np.ascontiguousarray(ids, np.int32)
+        logits = np.empty(self.V, np.float32)
+        if lib.oracle_gemma4_forward(self._h, _p(ids), len(ids), _p(logits)) != 0:
+            raise RuntimeError(lib.oracle_last_error().decode())
+        return logits
+
+    def greedy(self, prompt, steps: int):
+        """prefill (batched) + `steps` single-token passes: (ids[steps+1], last logits)"""
+        logits = self.forward(prompt)
+        ids = [int(np.argmax(logits))]
+        for _ in range(steps):
+            logits = self.forward([ids[-1]])
+            ids.append(int(np.argmax(logits)))
+        return np.array(ids, np.int32), logits

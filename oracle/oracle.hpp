@@ -238,4 +238,55 @@ void forward(const Model& m, State& s, const float* rows, size_t T, float* logit
 // Logits::argmax: ties go to the lowest id (logits.hpp:61-66)
 int32_t argmax(const float* logits, size_t n);
 
+// ---- Gemma 4 text, E4B schema (gemma4.hpp:19-482, gemma4_loader.hpp:31-130) ----
+// Dimensions from the GGUF; the schedule is the reference's: layer l attends
+// over the whole context when l % 6 == 5, over a sliding window otherwise; the
+// last `shared` layers read the caches of the last earlier layer of their kind.
+struct Gemma4Config {
+    size_t V = 0, D = 0, L = 0, CTX = 0, FF = 0;
+    size_t Hq = 0, Hkv = 0, Dl = 0, Df = 0, P = 0;
+    size_t window = 0, shared = 0, local_rot = 0, full_rot = 0;
+    double local_base = 0, full_base = 0;
+    float eps = 0, softcap = 0;
+    bool full(size_t l) const { return l % 6 == 5; }                    // gemma4.hpp:37
+    bool shares_kv(size_t l) const { return l >= L - shared; }          // gemma4.hpp:38
+    size_t head_dim(size_t l) const { return full(l) ? Df : Dl; }
+    size_t kv_source(size_t l) const;                                   // gemma4.hpp:41-47, 370-373
+};
+
+struct Gemma4Layer {
+    std::vector<float> attn_norm, q_norm, k_norm, post_attn_norm, ffn_norm, post_ffn_norm, post_norm;
+    Linear wq, wk, wv, wo, gate, up, down, pgate, proj;
+    float out_scale = 1.f;  // layer_output_scale (gemma4_loader.hpp:56-63: 1 when absent)
+};
+
+struct Gemma4Model {
+    Gemma4Config c;
+    Linear embedding;  // [V rows of D], also the tied LM head
+    Linear ple_table;  // [V rows of P*L]
+    Linear ple_proj;   // [P*L rows of D]
+    std::vector<float> ple_norm, final_norm;
+    std::vector<Gemma4Layer> layers;
+    std::vector<float> inv_local, inv_full;
+};
+
+struct Gemma4State {
+    size_t tokens = 0;
+    // per layer that owns K/V: rows [tokens][Hkv*dh] (the window layers' rings
+    // hold the same rows; visibility is the window rule)
+    std::vector<std::vector<float>> keys, values;
+    void reset(const Gemma4Config& c);
+};
+
+// gelu_pytorch_tanh (components.hpp:73-81)
+float gelu_tanh(float v);
+// cap * tanh(v / cap) (gemma4.hpp:79)
+float gemma_softcap(float v, float cap);
+// Gemma4E4BModel::embed (gemma4.hpp:415-419): dequant_row * sqrt(D)
+void gemma4_embed(const Gemma4Model& m, const int32_t* ids, size_t n, float* out);
+// Gemma4E4BModel::forward (gemma4.hpp:424-445) over T token ids at
+// state.tokens: the batched form (every layer over all T rows); writes the
+// soft-capped logits [V] of the last row. Throws on context exhaustion.
+void gemma4_forward(const Gemma4Model& m, Gemma4State& s, const int32_t* ids, size_t T, float* logits);
+
 }  // namespace oracle

@@ -32,6 +32,11 @@ struct Session {
     Model model;
     State state;
 };
+struct Gemma4Session {
+    Gguf gguf;
+    Gemma4Model model;
+    Gemma4State state;
+};
 }  // namespace
 
 extern "C" {
@@ -247,6 +252,55 @@ int oracle_model_greedy(void* h, const int32_t* prompt, size_t n_prompt, size_t 
         if (prefill_seconds) *prefill_seconds = std::chrono::duration<double>(t1 - t0).count();
         if (decode_seconds) *decode_seconds = std::chrono::duration<double>(t2 - t1).count();
     });
+}
+
+// ---- Gemma 4 (oracle_gemma4.cpp) ----
+void* oracle_gemma4_open(const char* path) {
+    Gemma4Session* out = nullptr;
+    guarded([&] {
+        auto sess = std::make_unique<Gemma4Session>();
+        sess->gguf.open(path);
+        sess->model = load_gemma4(sess->gguf);
+        sess->state.reset(sess->model.c);
+        out = sess.release();
+    });
+    return out;
+}
+void* oracle_gemma4_open_image(const void* image, size_t size) {
+    Gemma4Session* out = nullptr;
+    guarded([&] {
+        auto sess = std::make_unique<Gemma4Session>();
+        sess->gguf.parse(static_cast<const uint8_t*>(image), size);
+        sess->model = load_gemma4(sess->gguf);
+        sess->state.reset(sess->model.c);
+        out = sess.release();
+    });
+    return out;
+}
+void oracle_gemma4_close(void* h) { delete static_cast<Gemma4Session*>(h); }
+// V, D, L, window, shared, P
+void oracle_gemma4_dims(void* h, size_t* out) {
+    const Gemma4Config& c = static_cast<Gemma4Session*>(h)->model.c;
+    out[0] = c.V, out[1] = c.D, out[2] = c.L, out[3] = c.window, out[4] = c.shared, out[5] = c.P;
+}
+void oracle_gemma4_reset(void* h) {
+    Gemma4Session* s = static_cast<Gemma4Session*>(h);
+    s->state.reset(s->model.c);
+}
+size_t oracle_gemma4_tokens(void* h) { return static_cast<Gemma4Session*>(h)->state.tokens; }
+size_t oracle_gemma4_kv_source(void* h, size_t layer) { return static_cast<Gemma4Session*>(h)->model.c.kv_source(layer); }
+int oracle_gemma4_embed(void* h, const int32_t* ids, size_t n, float* out) {
+    return guarded([&] { gemma4_embed(static_cast<Gemma4Session*>(h)->model, ids, n, out); });
+}
+int oracle_gemma4_forward(void* h, const int32_t* ids, size_t T, float* logits) {
+    Gemma4Session* s = static_cast<Gemma4Session*>(h);
+    return guarded([&] { gemma4_forward(s->model, s->state, ids, T, logits); });
+}
+void oracle_gemma_math(const float* x, float* out, size_t n, float cap) {
+    for (size_t i = 0; i < n; ++i) {
+        out[2 * i] = gelu_tanh(x[i]);
+        out[2 * i + 1] = gemma_softcap(x[i], cap);
+    }
 }
 
 }  // extern "C"

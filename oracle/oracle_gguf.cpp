@@ -1,4 +1,4 @@
-// oracle_gguf.cpp -- GGUF v3 reader and Qwen 3.5 loader for the oracle.
+// oracle_gguf.cpp -- GGUF v3 reader, Qwen 3.5 and Gemma 4 loaders for the oracle.
 // TEST INFRASTRUCTURE ONLY. Restates nm/src/gguf.cpp:130-230 (header,
 // metadata, tensor table, aligned data start, per-tensor bounds checks) and
 // nm/src/qwen35_loader.hpp:30-155 (schema validation, ssm_a sign
@@ -271,6 +271,78 @@ Model load_qwen35(const Gguf& g) {
             L.wv = load_linear(g, blk(l, "attn_v.weight"), c.D, c.Hkv * c.head_dim);
             L.wo = load_linear(g, blk(l, "attn_output.weight"), c.Hq * c.head_dim, c.D);
         }
+        m.layers.push_back(std::move(L));
+    }
+    return m;
+}
+
+// validate_e4b_text_metadata (gemma4_loader.hpp:31-52) with the dimensions
+// read from the metadata, then load_e4b_text (:105-130). Layers that reuse
+// K/V load no K/V tensors (:95-103).
+Gemma4Model load_gemma4(const Gguf& g) {
+    expect(g.str("general.architecture") == "gemma4", "general.architecture is not 'gemma4'");
+    Gemma4Config c;
+    c.L = size_t(g.num("gemma4.block_count"));
+    c.D = size_t(g.num("gemma4.embedding_length"));
+    c.FF = size_t(g.num("gemma4.feed_forward_length"));
+    c.Hq = size_t(g.num("gemma4.attention.head_count"));
+    c.Hkv = size_t(g.num("gemma4.attention.head_count_kv"));
+    c.Df = size_t(g.num("gemma4.attention.key_length"));
+    expect(size_t(g.num("gemma4.attention.value_length")) == c.Df, "attention.value_length != key_length");
+    c.Dl = size_t(g.num("gemma4.attention.key_length_swa"));
+    expect(size_t(g.num("gemma4.attention.value_length_swa")) == c.Dl, "attention.value_length_swa != key_length_swa");
+    c.window = size_t(g.num("gemma4.attention.sliding_window"));
+    c.shared = size_t(g.num("gemma4.attention.shared_kv_layers"));
+    c.P = size_t(g.num("gemma4.embedding_length_per_layer_input"));
+    c.eps = float(g.num("gemma4.attention.layer_norm_rms_epsilon"));
+    c.softcap = float(g.num("gemma4.final_logit_softcapping"));
+    c.CTX = g.has("gemma4.context_length") ? size_t(g.num("gemma4.context_length")) : 131072;
+    // gemma4.hpp:396-397: local heads rotate every plane (base 1e4), full
+    // heads their first quarter (base 1e6)
+    c.local_base = g.has("gemma4.rope.freq_base_swa") ? double(float(g.num("gemma4.rope.freq_base_swa"))) : 1e4;
+    c.full_base = g.has("gemma4.rope.freq_base") ? double(float(g.num("gemma4.rope.freq_base"))) : 1e6;
+    c.local_rot = g.has("gemma4.rope.dimension_count_swa") ? size_t(g.num("gemma4.rope.dimension_count_swa")) : c.Dl;
+    c.full_rot = g.has("gemma4.rope.dimension_count") ? size_t(g.num("gemma4.rope.dimension_count")) : c.Df / 4;
+    expect(c.Hkv != 0 && c.Hq % c.Hkv == 0, "query heads must be a multiple of K/V heads");
+    expect(c.L >= 1 && c.shared < c.L && c.window > 0 && c.P > 0, "block_count / shared_kv_layers / sliding_window / per-layer width out of range");
+    expect(c.local_rot <= c.Dl && c.full_rot <= c.Df, "rope dimension counts out of range");
+    const Gguf::Tensor& emb = g.require("token_embd.weight");
+    expect(emb.dims.size() == 2 && emb.dims[0] == c.D, "token_embd.weight has the wrong shape");
+    c.V = size_t(emb.dims[1]);
+    for (size_t l = 0; l < c.L; ++l) (void)c.kv_source(l);
+
+    Gemma4Model m;
+    m.c = c;
+    const size_t PL = c.P * c.L;
+    m.embedding = load_linear(g, "token_embd.weight", c.D, c.V);
+    m.ple_table = load_linear(g, "per_layer_token_embd.weight", PL, c.V);
+    m.ple_proj = load_linear(g, "per_layer_model_proj.weight", c.D, PL);
+    m.ple_norm = load_vector(g, "per_layer_proj_norm.weight", c.P);
+    m.final_norm = load_vector(g, "output_norm.weight", c.D);
+    m.inv_local = rope_inv_freq(c.Dl, c.local_base, c.local_rot);
+    m.inv_full = rope_inv_freq(c.Df, c.full_base, c.full_rot);
+    for (size_t l = 0; l < c.L; ++l) {
+        Gemma4Layer L;
+        const size_t dh = c.head_dim(l);
+        L.attn_norm = load_vector(g, blk(l, "attn_norm.weight"), c.D);
+        L.wq = load_linear(g, blk(l, "attn_q.weight"), c.D, c.Hq * dh);
+        L.q_norm = load_vector(g, blk(l, "attn_q_norm.weight"), dh);
+        if (!c.shares_kv(l)) {
+            L.wk = load_linear(g, blk(l, "attn_k.weight"), c.D, c.Hkv * dh);
+            L.k_norm = load_vector(g, blk(l, "attn_k_norm.weight"), dh);
+            L.wv = load_linear(g, blk(l, "attn_v.weight"), c.D, c.Hkv * dh);
+        }
+        L.wo = load_linear(g, blk(l, "attn_output.weight"), c.Hq * dh, c.D);
+        L.post_attn_norm = load_vector(g, blk(l, "post_attention_norm.weight"), c.D);
+        L.ffn_norm = load_vector(g, blk(l, "ffn_norm.weight"), c.D);
+        L.gate = load_linear(g, blk(l, "ffn_gate.weight"), c.D, c.FF);
+        L.up = load_linear(g, blk(l, "ffn_up.weight"), c.D, c.FF);
+        L.down = load_linear(g, blk(l, "ffn_down.weight"), c.FF, c.D);
+        L.post_ffn_norm = load_vector(g, blk(l, "post_ffw_norm.weight"), c.D);
+        L.pgate = load_linear(g, blk(l, "inp_gate.weight"), c.D, c.P);
+        L.proj = load_linear(g, blk(l, "proj.weight"), c.P, c.D);
+        L.post_norm = load_vector(g, blk(l, "post_norm.weight"), c.D);
+        if (g.find(blk(l, "layer_output_scale.weight"))) L.out_scale = load_vector(g, blk(l, "layer_output_scale.weight"), 1)[0];
         m.layers.push_back(std::move(L));
     }
     return m;

@@ -55,5 +55,7 @@ private:
 };
 
 Model load_qwen35(const Gguf& g);
+// gemma4_loader::load_e4b_text (gemma4_loader.hpp:31-52, 105-130)
+Gemma4Model load_gemma4(const Gguf& g);
 
 }  // namespace oracle

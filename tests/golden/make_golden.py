@@ -32,8 +32,9 @@ so it runs in the build container only). This script:
      to the E4B configuration, so the model is full size: a seeded synthetic
      7.9 GB Q8_0 GGUF), a 600-token prompt (past the 512-position window, so
      the rings wrap and the K/V-sharing layers read the window) and 32 greedy
-     passes -> gemma4_e4b_model.npz (ids, top-5, the first 8192 logits of
-     the prefill and last passes) and the sha256 of both full logit vectors;
+     passes, and a 16-token prompt with 4 passes (short_*) -> gemma4_e4b_model.npz
+     (ids, top-5, the first 8192 logits of the prefill and last passes) and
+     the sha256 of every full logit vector;
   7. `dh256`: the attention geometry of the reference's Qwen 3.5 4B / 9B
      configs (256-wide heads, a quarter rotating, RoPE base 1e7, Hk 4 over
      Hv 8, untied head) at tiny width -> tiny_dh256_model.npz.
@@ -405,9 +406,15 @@ GEMMA4_STEPS = 32
 GEMMA4_HEAD = 8192  # logits kept in full per vector (the rest by sha256)
 
 
+GEMMA4_SHORT_PROMPT = 16
+GEMMA4_SHORT_STEPS = 4
+
+
 def make_gemma4(tmp: str) -> dict:
     """Gemma 4 E4B (full size: the reference's Gemma classes take no other
-    shape), 600-token prompt, 32 greedy passes; a few minutes of reference CPU time"""
+    shape): a 600-token prompt and 32 greedy passes, and a short run (16
+    tokens, 4 passes) cheap enough to pin the oracle's restatement; a few
+    minutes of reference CPU time"""
     from hero_amd.gemma4 import GEMMA4_E4B, write_synthetic_gemma4
 
     shm = "/dev/shm" if os.path.isdir("/dev/shm") else tmp
@@ -418,23 +425,27 @@ def make_gemma4(tmp: str) -> dict:
         for chunk in iter(lambda: f.read(1 << 24), b""):
             h.update(chunk)
     digest = lambda a: hashlib.sha256(np.ascontiguousarray(a, np.float32).tobytes()).hexdigest()  # noqa: E731
-    prompt = np.random.default_rng(GEMMA4_SEED).integers(0, GEMMA4_E4B.vocab, GEMMA4_PROMPT).astype(np.int32)
-    prompt.tofile(os.path.join(tmp, "gemma4_prompt.i32"))
-    outdir = os.path.join(tmp, "gemma4_out")
-    os.makedirs(outdir, exist_ok=True)
+    runs = {"": (GEMMA4_SEED, GEMMA4_PROMPT, GEMMA4_STEPS), "short_": (GEMMA4_SEED + 1, GEMMA4_SHORT_PROMPT, GEMMA4_SHORT_STEPS)}
+    out, entry = {}, {"seed": GEMMA4_SEED, "gguf_sha256": h.hexdigest(), "gguf_bytes": os.path.getsize(gguf)}
     try:
-        subprocess.run([HARNESS, "model", "gemma4_e4b", gguf, os.path.join(tmp, "gemma4_prompt.i32"), str(GEMMA4_STEPS), outdir], check=True)
-        size = os.path.getsize(gguf)
+        for tag, (seed, plen, steps) in runs.items():
+            prompt = np.random.default_rng(seed).integers(0, GEMMA4_E4B.vocab, plen).astype(np.int32)
+            prompt.tofile(os.path.join(tmp, f"gemma4_{tag}prompt.i32"))
+            outdir = os.path.join(tmp, f"gemma4_{tag}out")
+            os.makedirs(outdir, exist_ok=True)
+            subprocess.run([HARNESS, "model", "gemma4_e4b", gguf, os.path.join(tmp, f"gemma4_{tag}prompt.i32"), str(steps), outdir], check=True)
+            rd = lambda n, dt: np.fromfile(os.path.join(outdir, n), dtype=dt)  # noqa: E731
+            prefill, last = rd("logits_prefill.f32", np.float32), rd("logits_last.f32", np.float32)
+            out.update({f"{tag}prompt": prompt, f"{tag}ids": rd("ids.i32", np.int32), f"{tag}top5_ids": rd("top5_ids.i32", np.int32).reshape(-1, 5),
+                        f"{tag}top5_logits": rd("top5_logits.f32", np.float32).reshape(-1, 5), f"{tag}prefill_head": prefill[:GEMMA4_HEAD],
+                        f"{tag}last_head": last[:GEMMA4_HEAD]})
+            entry.update({f"{tag}prompt_seed": seed, f"{tag}prompt_len": plen, f"{tag}decode_steps": steps,
+                          f"{tag}reference_times": open(os.path.join(outdir, "times.txt")).read(),
+                          f"{tag}logits_prefill_sha256": digest(prefill), f"{tag}logits_last_sha256": digest(last)})
     finally:
         os.remove(gguf)
-    rd = lambda n, dt: np.fromfile(os.path.join(outdir, n), dtype=dt)  # noqa: E731
-    prefill, last = rd("logits_prefill.f32", np.float32), rd("logits_last.f32", np.float32)
-    np.savez_compressed(os.path.join(HERE, "gemma4_e4b_model.npz"), prompt=prompt, ids=rd("ids.i32", np.int32),
-                        top5_ids=rd("top5_ids.i32", np.int32).reshape(-1, 5), top5_logits=rd("top5_logits.f32", np.float32).reshape(-1, 5),
-                        prefill_head=prefill[:GEMMA4_HEAD], last_head=last[:GEMMA4_HEAD])
-    return {"seed": GEMMA4_SEED, "prompt_len": GEMMA4_PROMPT, "decode_steps": GEMMA4_STEPS, "gguf_sha256": h.hexdigest(),
-            "gguf_bytes": size, "reference_times": open(os.path.join(outdir, "times.txt")).read(),
-            "logits_prefill_sha256": digest(prefill), "logits_last_sha256": digest(last)}
+    np.savez_compressed(os.path.join(HERE, "gemma4_e4b_model.npz"), **out)
+    return entry
 
 
 PARTS = {"kernels": make_kernels, "tiny": make_tiny, "window": make_window, "variant": make_variant, "kmix": make_kmix,

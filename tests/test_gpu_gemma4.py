@@ -77,21 +77,27 @@ def golden():
 
 
 @pytest.fixture(scope="module")
-def model(golden):
-    import torch
+def image(golden):
+    from hero_amd.gemma4 import GEMMA4_E4B, synthetic_gemma4_image
 
-    from hero_amd.gemma4 import GEMMA4_E4B, Gemma4Model, synthetic_gemma4_image
-
-    assert torch.cuda.is_available()
     g, _ = golden
     t = time.perf_counter()
-    image = synthetic_gemma4_image(GEMMA4_E4B, seed=g["seed"])
-    sha = hashlib.sha256(memoryview(image)).hexdigest()
-    say(f"[gemma4] synthetic E4B GGUF image {image.nbytes / 1e9:.2f} GB in {time.perf_counter() - t:.1f} s")
+    img = synthetic_gemma4_image(GEMMA4_E4B, seed=g["seed"])
+    sha = hashlib.sha256(memoryview(img)).hexdigest()
+    say(f"[gemma4] synthetic E4B GGUF image {img.nbytes / 1e9:.2f} GB in {time.perf_counter() - t:.1f} s")
     assert sha == g["gguf_sha256"], "synthetic Gemma 4 model bytes differ from the reference run's"
+    return img
+
+
+@pytest.fixture(scope="module")
+def model(image):
+    import torch
+
+    from hero_amd.gemma4 import Gemma4Model
+
+    assert torch.cuda.is_available()
     t = time.perf_counter()
     m = Gemma4Model.open_image(image)
-    del image
     say(f"[gemma4] loaded in {time.perf_counter() - t:.1f} s, {m.dims.device_bytes / 1e9:.2f} GB of weights")
     yield m
     m.close()
@@ -116,3 +122,32 @@ def test_gemma4_e4b_matches_reference(model, golden):
     assert np.array_equal(last.values[:head], gold["last_head"])
     assert digest(last.values) == g["logits_last_sha256"], "last-pass logits differ from the reference's"
     assert state.tokens() == len(prompt) + g["decode_steps"]
+
+
+def test_gemma4_e4b_short_run_gpu_and_oracle_match_reference(model, image, golden):
+    """The 16-token prompt and 4 greedy passes of the golden (short_*): the GPU
+    and the oracle's restatement (batched prefill, as the reference runs it)
+    both give the reference's logits bit for bit."""
+    import oracle
+
+    g, gold = golden
+    prompt, ids = gold["short_prompt"], [int(i) for i in gold["short_ids"]]
+    state = model.new_state(64)
+    logits = model.forward(state, prompt)
+    assert digest(logits.values) == g["short_logits_prefill_sha256"]
+    out, last = model.decode_greedy(state, ids[0], g["short_decode_steps"], want_logits=True)
+    assert [int(i) for i in out] == ids[1:]
+    assert digest(last.values) == g["short_logits_last_sha256"]
+
+    t = time.perf_counter()
+    ref = oracle.Gemma4(image=image)
+    pre = ref.forward(prompt)
+    assert np.array_equal(pre[:len(gold["short_prefill_head"])], gold["short_prefill_head"])
+    assert digest(pre) == g["short_logits_prefill_sha256"], "the oracle's prefill logits differ from the reference's"
+    got = [int(np.argmax(pre))]
+    for _ in range(g["short_decode_steps"]):
+        lg = ref.forward([got[-1]])
+        got.append(int(np.argmax(lg)))
+    assert got == ids and digest(lg) == g["short_logits_last_sha256"], "the oracle's decode differs from the reference's"
+    say(f"[gemma4] oracle short run in {time.perf_counter() - t:.1f} s")
+    ref.close()

@@ -28,6 +28,9 @@ __device__ __forceinline__ float sigmoid_f32(float x) { return 1.f / (1.f + exp_
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.f + exp_f32(-x)); }
 // nm/src/recurrent.hpp:35
 __device__ __forceinline__ float softplus_f32(float x) { return x > 20.f ? x : log1p_f32(exp_f32(x)); }
+// gelu_pytorch_tanh (nm/src/components.hpp:73-81):
+// 0.5 v (1 + tanh(0.7978845608 (v + 0.044715 v^3))), left to right
+__device__ __forceinline__ float gelu_tanh_f32(float v) { return 0.5f * v * (1.f + tanhf_glibc(0.7978845608f * (v + 0.044715f * v * v * v))); }
 
 // 0, in a vector register the compiler cannot see through: added to an
 // address, it keeps a load of a wave-uniform value a per-lane vector load

@@ -12,10 +12,12 @@
 
 namespace hero {
 
-// GEMV epilogues: y = Wx; y = r + Wx; and, for a [gate|up] matrix packed in
+// GEMV epilogues: y = Wx; y = r + Wx; for a [gate|up] matrix packed in
 // alternating 32-row chunks (K = 4096, N % 64 == 0), y <- the quantized
-// activation of silu(gate) * up ([N/2] int8 + [N/64] fp32 scales)
-enum : int { kEpiStore = 0, kEpiResidual = 1, kEpiSwigluQuant = 2 };
+// activation of silu(gate) * up ([N/2] int8 + [N/64] fp32 scales); and
+// (streaming GEMV, quantized input) y = gelu(Wx) on the rows below
+// GemvInput::act_rows, Wx past them
+enum : int { kEpiStore = 0, kEpiResidual = 1, kEpiSwigluQuant = 2, kEpiGelu = 3 };
 
 // packed Q8_0 weight: [N][K] int8, then the fp16 scales by 8-row group,
 // [Npad/8][K/32][8] with Npad = N rounded up to 8 (rows past N unused): the
@@ -55,9 +57,10 @@ void launch_sample_full(const float* logits, int64_t V, int top_k, float temp, f
 void launch_quantize_act(const float* x, void* act, int64_t M, int64_t K, hipStream_t s);
 void launch_pack_q8(const void* gguf_blocks, void* packed, int64_t N_total, int64_t K, int64_t row0, int64_t rows, hipStream_t s, int64_t interleave = 0);
 void launch_gemv_q8(const void* packed, const void* act, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s);
-// The streaming GEMV (K a multiple of 4096, at most 12288) with its input
-// formed in the prologue from one of three sources.
-enum : int { kInAct = 0, kInRmsNorm = 1, kInSwiglu = 2, kInHeadGate = 3 };
+// The streaming GEMV with its input formed in the prologue from one of five
+// sources (kInRmsNorm and kInHeadGate at K == 4096, kInSwiglu at K a multiple
+// of 4096, kInAct and kInMul at every K of gemv_streams_act).
+enum : int { kInAct = 0, kInRmsNorm = 1, kInSwiglu = 2, kInHeadGate = 3, kInMul = 4 };
 struct GemvInput {
     int mode;
     const int8_t* xq;        // kInAct: quantized activation [K] + fp32 scales [K/32]
@@ -65,10 +68,15 @@ struct GemvInput {
     const float* x;          // kInRmsNorm: residual row [K] (K == 4096), RMSNorm weight, eps
     const float* gamma;      // kInHeadGate: raw delta-net outputs [K] (K == 4096) in x, the
     float eps;               //   head norm's weight [128] in gamma, eps, and the gates silu(z) [K] in z
-    const float* gate_up;    // kInSwiglu: [gate K | up K]
+    const float* gate_up;    // kInSwiglu: [gate K | up K]; kInMul: a [K]
     const float* z;
+    const float* up;         // kInMul: b [K]; the input is Q8_0(a * b)
+    int act_rows;            // kEpiGelu: rows [0, act_rows) take the GELU
 };
 bool gemv_streams(int64_t K);
+// the row lengths the streaming GEMV takes with the plain quantized input (and
+// the GELU input): 256, 1024, 2048, 2560, 2816, 4096, 8192, 10240, 12288
+bool gemv_streams_act(int64_t K);
 // workgroups of the streaming GEMV's launch for N rows under epilogue epi
 int gemv_stream_grid(int64_t N, int epi);
 // what another kernel's workgroups read ahead of the streaming GEMV over a

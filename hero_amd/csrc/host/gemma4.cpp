@@ -12,13 +12,15 @@
 //   gemma_attention             norms, RoPE, append, softmax(q.k) v, Q8_0 of the W_o input
 //   gemv(w_o)                   a
 //   gemma_post_norm             h = x + post_attn_norm(a); act = Q8_0(ffn_norm(h))
-//   gemv(w_gate_up)             gate | up
-//   gemma_gelu_mul_quant        act = Q8_0(gelu(gate) * up)
-//   gemv(w_down)                a
+//   gemv(w_gate_up)             gelu(gate) | up
+//   gemv(w_down)                a, over Q8_0(gelu(gate) * up)
 //   gemma_post_norm             h2 = h + post_ffw_norm(a); act = Q8_0(h2)
-//   gemv(w_pgate)               pg
-//   gemma_gelu_mul_quant        act = Q8_0(gelu(pg) * ple[l])         (gemma4.hpp:100-105)
-//   gemv(w_proj)                a
+//   gemv(w_pgate)               gelu(pg)
+//   gemv(w_proj)                a, over Q8_0(gelu(pg) * ple[l])       (gemma4.hpp:100-105)
+// The GELU is applied to each gate row in the producing GEMV's epilogue (once
+// per value) and the product formed and quantized in the consuming GEMV's
+// prologue; at row lengths without a streaming GEMV a gemma_gelu_mul_quant
+// does both between two plain GEMVs.
 //   gemma_post_norm             x = (h2 + post_norm(a)) * layer_output_scale; act = Q8_0(next norm(x))
 // then the tied LM head over act (the final norm's output), the soft-cap and
 // the argmax (gemma4.hpp:440-444).
@@ -284,6 +286,34 @@ void Gemma4Model::State::reset() {
 }
 
 // ---- the step ------------------------------------------------------------------------
+namespace {
+// GELU gate, then a projection over it: g[G] = W_g x (its first `gated` rows
+// through the GELU when `fused`), then y[N] = W Q8_0(gelu(g[0..K)) * up[0..K))
+// (K = `gated`). fused: both row lengths stream, the GELU is in the first
+// GEMV's epilogue and the product in the second's prologue.
+bool gelu_fusable(int64_t Kx, int64_t K) { return gemv_streams_act(Kx) && gemv_streams_act(K); }
+void gelu_gated_pair(const DeviceBuffer& wg, const DeviceBuffer& act_in, float* g, int64_t G, int64_t Kx, const float* up, const DeviceBuffer& w, const DeviceBuffer& act_mid,
+                     float* y, int64_t N, int64_t K, hipStream_t s) {
+    if (gelu_fusable(Kx, K)) {
+        GemvInput in{};
+        in.mode = kInAct;
+        in.xq = act_in.get<int8_t>();
+        in.xd = reinterpret_cast<const float*>(act_in.get<int8_t>() + Kx);
+        in.act_rows = int(K);
+        launch_gemv_q8_in(wg.get(), in, g, nullptr, G, Kx, kEpiGelu, s);
+        GemvInput pin{};
+        pin.mode = kInMul;
+        pin.gate_up = g;
+        pin.up = up;
+        launch_gemv_q8_in(w.get(), pin, y, nullptr, N, K, kEpiStore, s);
+    } else {
+        launch_gemv_q8(wg.get(), act_in.get(), g, nullptr, G, Kx, kEpiStore, s);
+        launch_gemma_gelu_mul_quant(g, up, act_mid.get(), K, s);
+        launch_gemv_q8(w.get(), act_mid.get(), y, nullptr, N, K, kEpiStore, s);
+    }
+}
+}  // namespace
+
 void Gemma4Model::enqueue_step(State& st) const {
     const Gemma4Config& c = c_;
     hipStream_t s = stream_;
@@ -323,13 +353,9 @@ void Gemma4Model::enqueue_step(State& st) const {
         launch_gemma_attention(a, s);
         launch_gemv_q8(L.w_o.get(), st.act_o_.get(), st.a_.get<float>(), nullptr, c.D, QW, kEpiStore, s);
         launch_gemma_post_norm(st.a_.get<float>(), L.post_attn_norm.get<float>(), x, 1.f, c.eps, st.h_.get<float>(), L.ffn_norm.get<float>(), st.act_.get(), c.D, s);
-        launch_gemv_q8(L.w_gate_up.get(), st.act_.get(), st.gu_.get<float>(), nullptr, 2 * c.FF, c.D, kEpiStore, s);
-        launch_gemma_gelu_mul_quant(st.gu_.get<float>(), st.gu_.get<float>() + c.FF, st.act_ff_.get(), c.FF, s);
-        launch_gemv_q8(L.w_down.get(), st.act_ff_.get(), st.a_.get<float>(), nullptr, c.D, c.FF, kEpiStore, s);
+        gelu_gated_pair(L.w_gate_up, st.act_, st.gu_.get<float>(), 2 * c.FF, c.D, st.gu_.get<float>() + c.FF, L.w_down, st.act_ff_, st.a_.get<float>(), c.D, c.FF, s);
         launch_gemma_post_norm(st.a_.get<float>(), L.post_ffn_norm.get<float>(), st.h_.get<float>(), 1.f, c.eps, st.h2_.get<float>(), nullptr, st.act_.get(), c.D, s);
-        launch_gemv_q8(L.w_pgate.get(), st.act_.get(), st.pg_.get<float>(), nullptr, c.P, c.D, kEpiStore, s);
-        launch_gemma_gelu_mul_quant(st.pg_.get<float>(), st.ple_.get<float>() + l * c.P, st.act_p_.get(), c.P, s);
-        launch_gemv_q8(L.w_proj.get(), st.act_p_.get(), st.a_.get<float>(), nullptr, c.D, c.P, kEpiStore, s);
+        gelu_gated_pair(L.w_pgate, st.act_, st.pg_.get<float>(), c.P, c.D, st.ple_.get<float>() + l * c.P, L.w_proj, st.act_p_, st.a_.get<float>(), c.D, c.P, s);
         const float* next = l + 1 < c.L ? layers_[size_t(l + 1)].attn_norm.get<float>() : final_norm_.get<float>();
         launch_gemma_post_norm(st.a_.get<float>(), L.post_norm.get<float>(), st.h2_.get<float>(), L.out_scale, c.eps, x, next, st.act_.get(), c.D, s);
     }

@@ -14,12 +14,6 @@
 
 namespace hero {
 
-// gelu_pytorch_tanh (nm/src/components.hpp:73-81):
-// 0.5 v (1 + tanh(0.7978845608 (v + 0.044715 v^3))), left to right
-__device__ __forceinline__ float gelu_tanh_f32(float v) {
-    return 0.5f * v * (1.f + tanhf_glibc(0.7978845608f * (v + 0.044715f * v * v * v)));
-}
-
 // ---- embedding and per-layer inputs -----------------------------------------------
 // x = dequant_row(id) * embed_scale (Gemma4E4BModel::embed, nm/src/gemma4.hpp:415-419),
 // its Q8_0 quantization (the PLE projection's input), and the token part of

@@ -115,7 +115,7 @@ __global__ __launch_bounds__(stream_threads<KC>()) void gemv_q8_stream_kernel(co
     constexpr int K = 16 * KC, nb = K / 32, ts = nb + 4;  // ts: padded term row (conflict-free 16-byte reads)
     constexpr int CPL = 1;  // K-chunks per lane
     static_assert(KC % 2 == 0, "whole Q8_0 blocks");
-    static_assert(XM == kInAct || KC % 256 == 0, "the fused inputs take whole 256-lane groups");
+    static_assert(XM == kInAct || XM == kInMul || KC % 256 == 0, "the fused inputs take whole 256-lane groups");
     // row ranges in whole units: 8-row groups, or for the SwiGLU epilogue
     // 64-row groups of [32 gate rows | 32 up rows]
     constexpr int UR = EPI == kEpiSwigluQuant ? 64 : 8;
@@ -166,7 +166,7 @@ __global__ __launch_bounds__(stream_threads<KC>()) void gemv_q8_stream_kernel(co
     int4 xv[CPL];
     float dx[CPL];
     float xr[16], gr[16], zr[16];               // kInRmsNorm / kInHeadGate: the lane's 16 inputs, weights (and gates)
-    float4 gv[CPL][4], uv[CPL][4];              // kInSwiglu: the lane's gate and up values
+    float4 gv[CPL][4], uv[CPL][4];              // kInSwiglu / kInMul: the lane's two factors
     if constexpr (XM == kInAct) {
 #pragma unroll
         for (int m = 0; m < CPL; ++m) {
@@ -196,13 +196,14 @@ __global__ __launch_bounds__(stream_threads<KC>()) void gemv_q8_stream_kernel(co
             gr[4 * k] = g.x, gr[4 * k + 1] = g.y, gr[4 * k + 2] = g.z, gr[4 * k + 3] = g.w;
         }
     } else {
+        const float* up = XM == kInSwiglu ? in.gate_up + K : in.up;
 #pragma unroll
         for (int m = 0; m < CPL; ++m) {
-            const int c = tid;
+            const int c = on ? tid : 0;  // lanes past KC: chunk 0 (their products are never stored)
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 gv[m][k] = reinterpret_cast<const float4*>(in.gate_up)[4 * c + k];
-                uv[m][k] = reinterpret_cast<const float4*>(in.gate_up + K)[4 * c + k];
+                uv[m][k] = reinterpret_cast<const float4*>(up)[4 * c + k];
             }
         }
     }
@@ -269,17 +270,21 @@ __global__ __launch_bounds__(stream_threads<KC>()) void gemv_q8_stream_kernel(co
         uint16_t dh;
         xv[0] = quantize16_in_pair(v, &dh);
         dx[0] = half_bits_to_f32(dh);
-    } else if constexpr (XM == kInSwiglu) {
+    } else if constexpr (XM == kInSwiglu || XM == kInMul) {
         // SwiGLU (nm/src/components.hpp:300-304): silu(gate) * up over the row
-        // [gate K | up K], then quantize_row_q8_0
+        // [gate K | up K]; or a * b, Gemma's gelu(gate) * up with the GELU
+        // already applied by the GEMV that produced the gate (the GELU-gated
+        // FFN, nm/src/components.hpp:294-304, and the per-layer input gate,
+        // nm/src/gemma4.hpp:100-105); then quantize_row_q8_0
+        auto act = [](float g) { if constexpr (XM == kInSwiglu) return silu_f32(g); else return g; };
 #pragma unroll
         for (int m = 0; m < CPL; ++m) {
             float v[16];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const float4 g = gv[m][k], u = uv[m][k];
-                v[4 * k] = silu_f32(g.x) * u.x, v[4 * k + 1] = silu_f32(g.y) * u.y;
-                v[4 * k + 2] = silu_f32(g.z) * u.z, v[4 * k + 3] = silu_f32(g.w) * u.w;
+                v[4 * k] = act(g.x) * u.x, v[4 * k + 1] = act(g.y) * u.y;
+                v[4 * k + 2] = act(g.z) * u.z, v[4 * k + 3] = act(g.w) * u.w;
             }
             uint16_t dh;
             xv[m] = quantize16_in_pair(v, &dh);
@@ -347,6 +352,8 @@ __global__ __launch_bounds__(stream_threads<KC>()) void gemv_q8_stream_kernel(co
                         y[o] = rnext + acc;  // h = x + m (nm/src/qwen35.hpp:321)
                     else if constexpr (EPI == kEpiStore)
                         y[o] = acc;
+                    else if constexpr (EPI == kEpiGelu)
+                        y[o] = o < in.act_rows ? gelu_tanh_f32(acc) : acc;  // Gemma's GELU gates (nm/src/components.hpp:294-304)
                     else {
                         // rows chain_row0 .. +63 are 32 gate rows then the 32 up rows of
                         // the same FF indices: g = silu(gate) * up
@@ -469,6 +476,13 @@ template <int KC, int D, int XM>
 void stream_dispatch(int epi, const int8_t* wq, const uint16_t* wd, const GemvInput& in, float* y, const float* resid, int N, int Npad, int G, int TR, size_t smem, hipStream_t s) {
     const dim3 block(stream_threads<KC>());
     constexpr int IL = KC == 256 || KC % 256 != 0;
+    if constexpr (XM == kInAct) {
+        if (epi == kEpiGelu) {
+            hipLaunchKernelGGL((gemv_q8_stream_kernel<KC, D, kEpiGelu, XM, IL>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
+            return;
+        }
+    }
+    if (epi == kEpiGelu) throw Error(HERO_EINVAL, "streaming GEMV: the GELU epilogue takes the quantized input");
     if (epi == kEpiResidual)
         hipLaunchKernelGGL((gemv_q8_stream_kernel<KC, D, kEpiResidual, XM, IL>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
     else if constexpr (KC == 256)
@@ -482,6 +496,12 @@ void stream_dispatch(int epi, const int8_t* wq, const uint16_t* wd, const GemvIn
 
 template <int KC, int D>
 void stream_dispatch_in(int epi, const int8_t* wq, const uint16_t* wd, const GemvInput& in, float* y, const float* resid, int N, int Npad, int G, int TR, size_t smem, hipStream_t s) {
+    if (in.mode == kInMul) {  // Gemma's FFN and per-layer input projections: stored rows only
+        if (epi != kEpiStore) throw Error(HERO_EINVAL, "streaming GEMV: the product input takes the plain store epilogue");
+        constexpr int IL = KC == 256 || KC % 256 != 0;
+        hipLaunchKernelGGL((gemv_q8_stream_kernel<KC, D, kEpiStore, kInMul, IL>), dim3(unsigned(G)), dim3(stream_threads<KC>()), smem, s, wq, wd, in, y, resid, N, Npad, TR);
+        return;
+    }
     if constexpr (KC % 256 == 0) {
         if (in.mode == kInSwiglu) {
             stream_dispatch<KC, D, kInSwiglu>(epi, wq, wd, in, y, resid, N, Npad, G, TR, smem, s);
@@ -579,6 +599,7 @@ void launch_gemv_q8_in(const void* packed, const GemvInput& in, float* y, const 
 }
 
 void launch_gemv_q8(const void* packed, const void* act, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s) {
+    if (epi == kEpiGelu) throw Error(HERO_EINVAL, "GEMV: the GELU epilogue takes its row count through launch_gemv_q8_in");
     const int8_t* xq = static_cast<const int8_t*>(act);
     const float* xd = reinterpret_cast<const float*>(xq + K);
     if (gemv_streams_act(K)) {

@@ -1109,12 +1109,12 @@ __global__ __launch_bounds__(64) void gemm_q8_skinny_wave_kernel(const int8_t* _
 // scales into shared memory once, then each wave walks its own range of
 // 16-row weight groups exactly as gemm_q8_skinny_wave_kernel does, but reads
 // only the weights and their scales from memory: 5 load instructions per
-// 4 KB of weights instead of 11. The weight ring is issued before the copy,
-// so its first loads are in flight while the activations arrive from L2.
+// 4 KB of weights instead of 11. The copy's loads are issued first and the
+// weight ring right after them, so both are in flight at once.
 constexpr int kSklMaxK = 4096;
 constexpr int kSklRowPad = 16;  // activation row stride K + 16: 16 lanes' 16-byte reads hit distinct banks
 constexpr int kSklDxPad = 4;    // activation scale row stride nb + 4 (likewise)
-constexpr int kSklRing = 2;     // rounds in flight per wave (16 waves per CU)
+constexpr int kSklRing = 2;     // rounds in flight per wave (deeper rings measured slower)
 
 size_t skl_shared_bytes(int nw, int K) {
     const int nb = K / 32;
@@ -1122,7 +1122,7 @@ size_t skl_shared_bytes(int nw, int K) {
 }
 
 template <int EPI, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) void gemm_q8_skinny_lds_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 4 ? 2 : 4))) void gemm_q8_skinny_lds_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {
     extern __shared__ __align__(16) uint8_t skl_smem[];
     const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, q = lane >> 4, c = lane & 15;
     const int nb = K >> 5, rounds = nb / kSkwRound;
@@ -1157,20 +1157,40 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
         const bool drow = on && c < kSkwRound && g * 16 + 8 * (q >> 1) < N;
         L.d = __builtin_amdgcn_raw_buffer_load_b128(bd, drow ? uint32_t(scale_index(g * 16 + 8 * (q >> 1), b0 + c, nb)) * 2u : kOOB, 0, 0);
     };
+    // The activation rows and scales (rows >= M read as zeros) are loaded into
+    // registers first and the weight ring after them: loads retire in order,
+    // so the copy, on which the first MFMA waits, does not wait for the ring
+    // (M = 16: 24576 x 4096 29.9 -> 28.3 us, 10240 x 4096 24.3 -> 21.5 us).
+    constexpr int XP = (16 * kSklMaxK / 16 + 64 * NW - 1) / (64 * NW);  // 16-byte pieces per lane
+    constexpr int DP = (16 * kSklMaxK / 32 + 64 * NW - 1) / (64 * NW);  // scales per lane
+    const int cpr = K / 16;  // 16-byte pieces per row
+    v4b_t xv[XP];
+    float dv[DP];
+#pragma unroll
+    for (int u = 0; u < XP; ++u) {
+        const int p = tid + u * 64 * NW, row = p / cpr, col = 16 * (p % cpr);
+        xv[u] = __builtin_amdgcn_raw_buffer_load_b128(bx, p < 16 * cpr && row < M ? uint32_t(row) * uint32_t(K) + uint32_t(col) : kOOB, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < DP; ++u) {
+        const int e = tid + u * 64 * NW, row = e / nb, b = e % nb;
+        dv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bxd, e < 16 * nb && row < M ? uint32_t(row * nb + b) * 4u : kOOB, 0, 0));
+    }
+    __builtin_amdgcn_sched_barrier(0);
     Ring ring[kSklRing];
 #pragma unroll
     for (int k = 0; k < kSklRing; ++k) load(k, ring[k]);
-
-    // the activation rows and scales (rows >= M read as zeros)
-    const int cpr = K / 16;  // 16-byte pieces per row
-    for (int p = tid; p < 16 * cpr; p += 64 * NW) {
-        const int row = p / cpr, col = 16 * (p % cpr);
-        const v4b_t v = __builtin_amdgcn_raw_buffer_load_b128(bx, row < M ? uint32_t(row) * uint32_t(K) + uint32_t(col) : kOOB, 0, 0);
-        *reinterpret_cast<v4b_t*>(xs + row * rowb + col) = v;
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<kSklRing * (kSkwPairs + 1)>();  // the copy's loads have landed
+#pragma unroll
+    for (int u = 0; u < XP; ++u) {
+        const int p = tid + u * 64 * NW, row = p / cpr, col = 16 * (p % cpr);
+        if (p < 16 * cpr) *reinterpret_cast<v4b_t*>(xs + row * rowb + col) = xv[u];
     }
-    for (int e = tid; e < 16 * nb; e += 64 * NW) {
-        const int row = e / nb, b = e % nb;
-        dxs[row * dxrow + b] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bxd, row < M ? uint32_t(row * nb + b) * 4u : kOOB, 0, 0));
+#pragma unroll
+    for (int u = 0; u < DP; ++u) {
+        const int e = tid + u * 64 * NW, row = e / nb, b = e % nb;
+        if (e < 16 * nb) dxs[row * dxrow + b] = dv[u];
     }
     __syncthreads();
 
@@ -1246,7 +1266,7 @@ void gemm_dispatch(int epi, const int8_t* wq, const uint16_t* wd, const int8_t* 
 int gemm_q8_plan(int64_t M, int64_t N, int64_t K) {
     const int64_t groups = (N + 15) / 16;
     if (M <= 16 && groups >= 2 * device_cus() && K % (32 * kSkwRound) == 0 && K <= kSkwMaxK && N * K < (int64_t(1) << 31))
-        return kGemmPlanSkinnyWave;
+        return K <= kSklMaxK ? kGemmPlanSkinnyLds : kGemmPlanSkinnyWave;
     if (M <= 16 && K % 256 == 0 && K <= kSkMaxK && N * K < (int64_t(1) << 31)) return kGemmPlanSkinnyShared;
     // the tallest tile that still gives every CU two workgroups (the fp32
     // term work per CU is the same; more workgroups hide more latency)
@@ -1273,24 +1293,33 @@ void launch_gemm_q8(const void* packed, const void* act, float* y, const float* 
         return unsigned(std::min<int64_t>(int64_t(per_cu) * device_cus(), groups));
     };
     switch (gemm_q8_plan(M, N, K)) {
-    case kGemmPlanSkinnyWave:
-        // tall: a wave per group range, every chain in registers; for the
-        // tallest (8 or more groups per CU, the LM head) at K <= 4096 the
-        // activations in shared memory, eight waves per workgroup (152 us
-        // instead of 205 us for 151936 x 4096; with fewer groups per CU the
-        // workgroup's activation copy costs more than it saves)
-        if (K <= kSklMaxK && groups >= 8 * device_cus()) {
-            auto run = [&](auto kernel) {
-                const size_t smem = skl_shared_bytes(8, int(K));
-                const unsigned grid = unsigned(std::max<int64_t>(1, std::min<int64_t>(grid_for(kernel, 64 * 8, smem), groups / 8)));
-                hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * 8), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
+    case kGemmPlanSkinnyLds: {
+        // tall at K <= 4096: the activations in shared memory, read from L2
+        // once per workgroup instead of once per wave (at the same rows every
+        // round those reads keep the L2 busy on a few channels), each wave a
+        // range of at least one group, and as many waves per workgroup as
+        // gives about one group per wave: 4 below 3 groups per CU, 6 below 8,
+        // 8 above (M = 16: 24576 x 4096 35 -> 27 us, 16448 x 4096 30-34 ->
+        // 21 us, 10240 x 4096 18.5 -> 17 us, the LM head 205 -> 152 us)
+        {
+            const int64_t cus = device_cus();
+            auto run = [&](auto kernel, int nw) {
+                const size_t smem = skl_shared_bytes(nw, int(K));
+                const unsigned grid = unsigned(std::max<int64_t>(1, std::min<int64_t>(grid_for(kernel, 64 * nw, smem), (groups + nw - 1) / nw)));
+                hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * nw), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
             };
-            if (epi == kEpiResidual)
-                run(gemm_q8_skinny_lds_kernel<kEpiResidual, 8>);
+            const bool r = epi == kEpiResidual;
+            if (groups >= 8 * cus)
+                r ? run(gemm_q8_skinny_lds_kernel<kEpiResidual, 8>, 8) : run(gemm_q8_skinny_lds_kernel<kEpiStore, 8>, 8);
+            else if (groups >= 3 * cus)
+                r ? run(gemm_q8_skinny_lds_kernel<kEpiResidual, 6>, 6) : run(gemm_q8_skinny_lds_kernel<kEpiStore, 6>, 6);
             else
-                run(gemm_q8_skinny_lds_kernel<kEpiStore, 8>);
-            break;
+                r ? run(gemm_q8_skinny_lds_kernel<kEpiResidual, 4>, 4) : run(gemm_q8_skinny_lds_kernel<kEpiStore, 4>, 4);
         }
+        break;
+    }
+    case kGemmPlanSkinnyWave:
+        // tall at K > 4096: a wave per group range, every chain in registers
         if (epi == kEpiResidual)
             hipLaunchKernelGGL(gemm_q8_skinny_wave_kernel<kEpiResidual>, dim3(grid_for(gemm_q8_skinny_wave_kernel<kEpiResidual>, 64, 0)), dim3(64), 0, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
         else

@@ -1209,12 +1209,15 @@ struct PgRaw {  // one lane's 32 channels of a row as stored
     uint16_t d;  // Q8: the block scale
 };
 
-template <bool Q8>
+// G > 0: the query heads per KV head, known at compile time (the loops over
+// the group's heads then carry no per-head conditions); G = 0: read from the
+// arguments
+template <bool Q8, int G>
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnPagedArgs p) {
     const AttnDecodeArgs& a = p.a;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int g = blockIdx.x, sp = blockIdx.y, b = blockIdx.z;
-    const int Gs = a.Hq / a.Hkv;
+    const int Gs = G > 0 ? G : a.Hq / a.Hkv;
     const int pos = a.positions[b];
     if (pos < 0 || pos >= p.max_pages * p.page_size) return;
     const int first = visible_first(pos, a.window);
@@ -1419,7 +1422,7 @@ size_t attn_split_ring_smem(int Gs, int split) {
     return size_t(rg_slots<DH>()) * rg_slot<DH>() + size_t(Gs) * DH * 4 + size_t(Gs) * (split / kPgTile + 1) * kPgTile * 4;
 }
 
-template <int DH>
+template <int DH, int G>  // G as in attn_split_kernel
 __global__ __launch_bounds__(256) void attn_split_ring_kernel(AttnPagedArgs p) {
     constexpr int kSlots = rg_slots<DH>(), kSlot = rg_slot<DH>();
     constexpr int kLoads = kSlot / (256 * 16);  // 16-byte loads per lane per block
@@ -1429,7 +1432,7 @@ __global__ __launch_bounds__(256) void attn_split_ring_kernel(AttnPagedArgs p) {
     const AttnDecodeArgs& a = p.a;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int g = blockIdx.x, sp = blockIdx.y, b = blockIdx.z;
-    const int Gs = a.Hq / a.Hkv;
+    const int Gs = G > 0 ? G : a.Hq / a.Hkv;
     const int pos = a.positions[b];
     if (pos < 0 || pos >= p.max_pages * p.page_size) return;
     const int first = visible_first(pos, a.window);
@@ -1697,6 +1700,34 @@ __global__ __launch_bounds__(DH * kCombineGroups) void attn_combine_kernel(AttnP
     if ((c & 31) == 0) qd[(int64_t(b) * width + idx) >> 5] = half_bits_to_f32(fp32_to_fp16_ref(d));
 }
 
+namespace {
+// the split kernels for the group size: compiled for 1, 2, 4 and 8 query
+// heads per KV head (4: Qwen 3.5 and its tests), read at run time otherwise
+template <int DH>
+void split_ring_group(const AttnPagedArgs& p, int Gs, hipStream_t s) {
+    const dim3 grid(unsigned(p.a.Hkv), unsigned(p.nsplit), unsigned(p.a.B));
+    const size_t smem = attn_split_ring_smem<DH>(Gs, p.split);
+    switch (Gs) {
+        case 1: hipLaunchKernelGGL((attn_split_ring_kernel<DH, 1>), grid, dim3(256), smem, s, p); break;
+        case 2: hipLaunchKernelGGL((attn_split_ring_kernel<DH, 2>), grid, dim3(256), smem, s, p); break;
+        case 4: hipLaunchKernelGGL((attn_split_ring_kernel<DH, 4>), grid, dim3(256), smem, s, p); break;
+        case 8: hipLaunchKernelGGL((attn_split_ring_kernel<DH, 8>), grid, dim3(256), smem, s, p); break;
+        default: hipLaunchKernelGGL((attn_split_ring_kernel<DH, 0>), grid, dim3(256), smem, s, p); break;
+    }
+}
+template <bool Q8>
+void split_group(const AttnPagedArgs& p, int Gs, size_t smem, hipStream_t s) {
+    const dim3 grid(unsigned(p.a.Hkv), unsigned(p.nsplit), unsigned(p.a.B));
+    switch (Gs) {
+        case 1: hipLaunchKernelGGL((attn_split_kernel<Q8, 1>), grid, dim3(256), smem, s, p); break;
+        case 2: hipLaunchKernelGGL((attn_split_kernel<Q8, 2>), grid, dim3(256), smem, s, p); break;
+        case 4: hipLaunchKernelGGL((attn_split_kernel<Q8, 4>), grid, dim3(256), smem, s, p); break;
+        case 8: hipLaunchKernelGGL((attn_split_kernel<Q8, 8>), grid, dim3(256), smem, s, p); break;
+        default: hipLaunchKernelGGL((attn_split_kernel<Q8, 0>), grid, dim3(256), smem, s, p); break;
+    }
+}
+}  // namespace
+
 void attn_paged_plan(int64_t max_ctx, int window, int B, int Hkv, int* split, int* nsplit) {
     const int64_t vis = window > 0 ? std::min<int64_t>(max_ctx, window) : max_ctx;
     // about two workgroups per CU over all rows and KV heads
@@ -1714,7 +1745,7 @@ void launch_attn_paged(const AttnPagedArgs& p, hipStream_t s) {
     const int Gs = a.Hq / a.Hkv;
     if (a.Dh == 256) {  // fp16 pages of 64 positions (the host checks): the page-streaming form for any B
         hipLaunchKernelGGL(attn_paged_prep_kernel<256>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(256), 0, s, p);
-        hipLaunchKernelGGL(attn_split_ring_kernel<256>, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), attn_split_ring_smem<256>(Gs, p.split), s, p);
+        split_ring_group<256>(p, Gs, s);
         hipLaunchKernelGGL(attn_combine_kernel<256>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(256 * kCombineGroups), 0, s, p);
         return;
     }
@@ -1725,11 +1756,11 @@ void launch_attn_paged(const AttnPagedArgs& p, hipStream_t s) {
     // loads in flight, and the per-key form, with more workgroups per CU,
     // streams faster (32k context, 16 sequences: 536 vs 727 us)
     if (!p.q8 && p.page_size == kPgTile && a.B <= 2)
-        hipLaunchKernelGGL(attn_split_ring_kernel<kAttnDim>, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), attn_split_ring_smem<kAttnDim>(Gs, p.split), s, p);
+        split_ring_group<kAttnDim>(p, Gs, s);
     else if (p.q8)
-        hipLaunchKernelGGL(attn_split_kernel<true>, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), smem, s, p);
+        split_group<true>(p, Gs, smem, s);
     else
-        hipLaunchKernelGGL(attn_split_kernel<false>, dim3(unsigned(a.Hkv), unsigned(p.nsplit), unsigned(a.B)), dim3(256), smem, s, p);
+        split_group<false>(p, Gs, smem, s);
     hipLaunchKernelGGL(attn_combine_kernel<kAttnDim>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(kAttnDim * kCombineGroups), 0, s, p);
 }
 

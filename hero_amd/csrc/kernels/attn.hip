@@ -1649,29 +1649,60 @@ __global__ __launch_bounds__(DH * kCombineGroups) void attn_combine_kernel(AttnP
     const float* w = p.work + (int64_t(b) * a.Hq + h) * p.nsplit * rec;
     __shared__ float red[DH * kCombineGroups / 64];
     __shared__ float part[kCombineGroups][2][DH];
-    float mloc = -INFINITY;
-    for (int s = tid; s < p.nsplit; s += DH * kCombineGroups) mloc = fmaxf(mloc, w[s * rec]);
-    for (int off = 32; off > 0; off >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, off));
-    if ((tid & 63) == 0) red[tid >> 6] = mloc;
-    __syncthreads();
-    float m = red[0];
-    for (int i = 1; i < DH * kCombineGroups / 64; ++i) m = fmaxf(m, red[i]);
     float l = 0.f, o = 0.f;
-    for (int base = sg; base < p.nsplit; base += kCombineGroups * kCombinePass) {
+    if (p.nsplit <= kCombineGroups * kCombinePass) {
+        // one pass: the lane's records all loaded at once, the maximum over
+        // every split taken from them (a wave's lanes share a split group; the
+        // waves together hold every group)
         float mv[kCombinePass], lv[kCombinePass], ov[kCombinePass];
 #pragma unroll
         for (int u = 0; u < kCombinePass; ++u) {
-            const int s = min(base + u * kCombineGroups, p.nsplit - 1);
+            const int s = min(sg + u * kCombineGroups, p.nsplit - 1);
             mv[u] = w[s * rec];
             lv[u] = w[s * rec + 1];
             ov[u] = w[s * rec + 2 + c];
         }
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < kCombinePass; ++u)
+            if (sg + u * kCombineGroups < p.nsplit) mloc = fmaxf(mloc, mv[u]);
+        for (int off = 32; off > 0; off >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, off));
+        if ((tid & 63) == 0) red[tid >> 6] = mloc;
+        __syncthreads();
+        float m = red[0];
+        for (int i = 1; i < DH * kCombineGroups / 64; ++i) m = fmaxf(m, red[i]);
 #pragma unroll
         for (int u = 0; u < kCombinePass; ++u) {
-            if (base + u * kCombineGroups < p.nsplit && mv[u] != -INFINITY) {
+            if (sg + u * kCombineGroups < p.nsplit && mv[u] != -INFINITY) {
                 const float f = exp_f32(mv[u] - m);
                 l += lv[u] * f;
                 o += ov[u] * f;
+            }
+        }
+    } else {  // more splits: the maximum first, then passes of kCombinePass
+        float mloc = -INFINITY;
+        for (int s = tid; s < p.nsplit; s += DH * kCombineGroups) mloc = fmaxf(mloc, w[s * rec]);
+        for (int off = 32; off > 0; off >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, off));
+        if ((tid & 63) == 0) red[tid >> 6] = mloc;
+        __syncthreads();
+        float m = red[0];
+        for (int i = 1; i < DH * kCombineGroups / 64; ++i) m = fmaxf(m, red[i]);
+        for (int base = sg; base < p.nsplit; base += kCombineGroups * kCombinePass) {
+            float mv[kCombinePass], lv[kCombinePass], ov[kCombinePass];
+#pragma unroll
+            for (int u = 0; u < kCombinePass; ++u) {
+                const int s = min(base + u * kCombineGroups, p.nsplit - 1);
+                mv[u] = w[s * rec];
+                lv[u] = w[s * rec + 1];
+                ov[u] = w[s * rec + 2 + c];
+            }
+#pragma unroll
+            for (int u = 0; u < kCombinePass; ++u) {
+                if (base + u * kCombineGroups < p.nsplit && mv[u] != -INFINITY) {
+                    const float f = exp_f32(mv[u] - m);
+                    l += lv[u] * f;
+                    o += ov[u] * f;
+                }
             }
         }
     }

@@ -1122,7 +1122,7 @@ size_t skl_shared_bytes(int nw, int K) {
 }
 
 template <int EPI, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 4 ? 2 : 4))) void gemm_q8_skinny_lds_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) void gemm_q8_skinny_lds_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {
     extern __shared__ __align__(16) uint8_t skl_smem[];
     const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, q = lane >> 4, c = lane & 15;
     const int nb = K >> 5, rounds = nb / kSkwRound;
@@ -1266,7 +1266,7 @@ void gemm_dispatch(int epi, const int8_t* wq, const uint16_t* wd, const int8_t* 
 int gemm_q8_plan(int64_t M, int64_t N, int64_t K) {
     const int64_t groups = (N + 15) / 16;
     if (M <= 16 && groups >= 2 * device_cus() && K % (32 * kSkwRound) == 0 && K <= kSkwMaxK && N * K < (int64_t(1) << 31))
-        return K <= kSklMaxK ? kGemmPlanSkinnyLds : kGemmPlanSkinnyWave;
+        return K <= kSklMaxK && groups >= 4 * device_cus() ? kGemmPlanSkinnyLds : kGemmPlanSkinnyWave;
     if (M <= 16 && K % 256 == 0 && K <= kSkMaxK && N * K < (int64_t(1) << 31)) return kGemmPlanSkinnyShared;
     // the tallest tile that still gives every CU two workgroups (the fp32
     // term work per CU is the same; more workgroups hide more latency)
@@ -1294,32 +1294,30 @@ void launch_gemm_q8(const void* packed, const void* act, float* y, const float* 
     };
     switch (gemm_q8_plan(M, N, K)) {
     case kGemmPlanSkinnyLds: {
-        // tall at K <= 4096: the activations in shared memory, read from L2
-        // once per workgroup instead of once per wave (at the same rows every
-        // round those reads keep the L2 busy on a few channels), each wave a
-        // range of at least one group, and as many waves per workgroup as
-        // gives about one group per wave: 4 below 3 groups per CU, 6 below 8,
-        // 8 above (M = 16: 24576 x 4096 35 -> 27 us, 16448 x 4096 30-34 ->
-        // 21 us, 10240 x 4096 18.5 -> 17 us, the LM head 205 -> 152 us)
-        {
-            const int64_t cus = device_cus();
-            auto run = [&](auto kernel, int nw) {
-                const size_t smem = skl_shared_bytes(nw, int(K));
-                const unsigned grid = unsigned(std::max<int64_t>(1, std::min<int64_t>(grid_for(kernel, 64 * nw, smem), (groups + nw - 1) / nw)));
-                hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * nw), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
-            };
-            const bool r = epi == kEpiResidual;
-            if (groups >= 8 * cus)
-                r ? run(gemm_q8_skinny_lds_kernel<kEpiResidual, 8>, 8) : run(gemm_q8_skinny_lds_kernel<kEpiStore, 8>, 8);
-            else if (groups >= 3 * cus)
-                r ? run(gemm_q8_skinny_lds_kernel<kEpiResidual, 6>, 6) : run(gemm_q8_skinny_lds_kernel<kEpiStore, 6>, 6);
-            else
-                r ? run(gemm_q8_skinny_lds_kernel<kEpiResidual, 4>, 4) : run(gemm_q8_skinny_lds_kernel<kEpiStore, 4>, 4);
-        }
+        // tall at K <= 4096 with 4 or more groups per CU: the activations in
+        // shared memory, read from L2 once per workgroup instead of once per
+        // wave (at the same rows every round those reads keep the L2 busy on
+        // a few channels), each wave a range of at least one group, 6 waves per
+        // workgroup below 8 groups per CU and 8 above (M = 16: 24576 x 4096
+        // 35 -> 27 us, 16448 x 4096 30-34 -> 21 us, the LM head 205 -> 152 us).
+        // With fewer groups per CU the copy costs more than it saves (12288 x
+        // 4096: 22 us against 17-19; 10240 x 4096: 19.8 against 19.0).
+        const int64_t cus = device_cus();
+        auto run = [&](auto kernel, int nw) {
+            const size_t smem = skl_shared_bytes(nw, int(K));
+            const unsigned grid = unsigned(std::max<int64_t>(1, std::min<int64_t>(grid_for(kernel, 64 * nw, smem), (groups + nw - 1) / nw)));
+            hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * nw), smem, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
+        };
+        const bool r = epi == kEpiResidual;
+        if (groups >= 8 * cus)
+            r ? run(gemm_q8_skinny_lds_kernel<kEpiResidual, 8>, 8) : run(gemm_q8_skinny_lds_kernel<kEpiStore, 8>, 8);
+        else
+            r ? run(gemm_q8_skinny_lds_kernel<kEpiResidual, 6>, 6) : run(gemm_q8_skinny_lds_kernel<kEpiStore, 6>, 6);
         break;
     }
     case kGemmPlanSkinnyWave:
-        // tall at K > 4096: a wave per group range, every chain in registers
+        // tall, below 4 groups per CU or at K > 4096: a wave per group range,
+        // every chain in registers
         if (epi == kEpiResidual)
             hipLaunchKernelGGL(gemm_q8_skinny_wave_kernel<kEpiResidual>, dim3(grid_for(gemm_q8_skinny_wave_kernel<kEpiResidual>, 64, 0)), dim3(64), 0, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
         else

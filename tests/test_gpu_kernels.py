@@ -170,9 +170,10 @@ def test_rmsnorm_gate_up_swiglu_matches_oracle_bytes(lib, ff):
                                    # the skinny path (M <= 16): ragged 16-row groups, a partial round
                                    # (768 = 24 blocks), fewer rows than one group, the largest K
                                    (2, 4100, 4096), (8, 33, 12288), (16, 1003, 768), (13, 12288, 4096), (3, 7, 256), (16, 40, 16384),
-                                   # its tall forms (at least two 16-row groups per CU): K = 12288 (a wave per
-                                   # range), and at K = 4096 the activations in shared memory with 4 (8200 rows,
-                                   # a ragged last group), 6 (16448, 24576) and 8 (40000) waves per workgroup
+                                   # its tall forms (at least two 16-row groups per CU): a wave per range (8200
+                                   # rows with a ragged last group, K = 12288), and from four groups per CU at
+                                   # K = 4096 the activations in shared memory with 6 (16448, 24576) and 8
+                                   # (40000) waves per workgroup
                                    (16, 8200, 4096), (7, 9000, 12288), (5, 16448, 4096), (16, 24576, 4096), (11, 40000, 4096)])
 def test_gemm_matches_oracle_bitwise(lib, m, n, k):
     """M-row GEMM on int8 MFMA: every element equals the reference's matmul

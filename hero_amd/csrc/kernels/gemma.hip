@@ -132,6 +132,18 @@ __device__ __forceinline__ float serial_sum_lds(const float* p, int n) {
     float s = 0.f;
     const float4* p4 = reinterpret_cast<const float4*>(p);
     int i = 0;
+    for (; i + 32 <= n; i += 32) {  // 32 values read before their adds (one latency per 32)
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = p4[i / 4 + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            s += v[u].x;
+            s += v[u].y;
+            s += v[u].z;
+            s += v[u].w;
+        }
+    }
     for (; i + 4 <= n; i += 4) {
         const float4 v = p4[i / 4];
         s += v.x;
@@ -259,7 +271,7 @@ __global__ __launch_bounds__(256) void gemma_softmax_pv_kernel(GemmaAttnArgs a) 
     __shared__ seqsum::Shared sm;
     __shared__ __align__(16) float chunk[seqsum::kMaxN];
     __shared__ __align__(16) float vb[2][kPvChunk][64];
-    __shared__ float al[2][kPvChunk];
+    __shared__ __align__(16) float al[2][kPvChunk];
     __shared__ float red[4];
     const int tid = threadIdx.x, h = blockIdx.x, c0 = blockIdx.y * 64;
     const int g = h / (a.Hq / a.Hkv);
@@ -315,8 +327,27 @@ __global__ __launch_bounds__(256) void gemma_softmax_pv_kernel(GemmaAttnArgs a) 
         __syncthreads();
         if (base + kPvChunk < n) fetch(base + kPvChunk);
         if (tid < 64) {
+            // reads 16 keys ahead of the chain (the weights as float4s), so the
+            // adds do not wait on shared-memory latency key by key; the same
+            // products, added in key order
             const int len = min(kPvChunk, n - base);
-            for (int k = 0; k < len; ++k) acc += al[buf][k] * vb[buf][k][tid];
+            int k0 = 0;
+            for (; k0 + 16 <= len; k0 += 16) {
+                float4 aw[4];
+                float vv[16];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) aw[u] = reinterpret_cast<const float4*>(&al[buf][k0])[u];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) vv[u] = vb[buf][k0 + u][tid];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    acc += aw[u].x * vv[4 * u];
+                    acc += aw[u].y * vv[4 * u + 1];
+                    acc += aw[u].z * vv[4 * u + 2];
+                    acc += aw[u].w * vv[4 * u + 3];
+                }
+            }
+            for (int k = k0; k < len; ++k) acc += al[buf][k] * vb[buf][k][tid];
         }
         buf ^= 1;
     }

@@ -278,19 +278,43 @@ __global__ __launch_bounds__(256) void gemma_softmax_pv_kernel(GemmaAttnArgs a) 
     const GemmaSpan sp = gemma_span(a);
     const int n = sp.n;
     const float* sc = a.scores + int64_t(h) * a.max_ctx;
-    // max, then the exponentials' sequential sum
+    // value rows [slot][DH] of KV head g, channels c0 .. c0+63: the first
+    // chunk's loads are issued before the softmax (they do not depend on it)
+    const float* vh = a.v_cache + int64_t(g) * a.slots * DH + c0;
+    constexpr int LOADS = kPvChunk * 16 / 256;  // float4s per lane: 8
+    float4 v[LOADS];
+    auto fetch = [&](int base) {
+#pragma unroll
+        for (int k = 0; k < LOADS; ++k) {
+            const int e = tid + 256 * k, key = e >> 4, c4 = e & 15;
+            v[k] = base + key < n ? reinterpret_cast<const float4*>(vh + int64_t(sp.slot(base + key)) * DH)[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    fetch(0);
+    constexpr int CH = seqsum::kMaxN - 256;
+    // short spans (n <= CH): the scores are read once into the chunk buffer,
+    // which then holds the exponentials, and the weights are formed from those
+    const bool short_span = n <= CH;
+    // max, then the exponentials' sequential sum (components.hpp:131-141)
     float mx = -INFINITY;
-    for (int t = tid; t < n; t += 256) mx = fmaxf(mx, sc[t]);
+    for (int t = tid; t < n; t += 256) {
+        const float st = sc[t];
+        if (short_span) chunk[1 + t] = st;
+        mx = fmaxf(mx, st);
+    }
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    constexpr int CH = seqsum::kMaxN - 256;
     float total = 0.f;
     for (int base = 0; base < n; base += CH) {
         const int len = min(n - base, CH);
-        __syncthreads();  // chunk free
-        for (int u = tid; u < len; u += 256) chunk[1 + u] = exp_f32(sc[base + u] - mx);
+        if (short_span) {
+            for (int u = tid; u < len; u += 256) chunk[1 + u] = exp_f32(chunk[1 + u] - mx);  // each lane its own entries
+        } else {
+            __syncthreads();  // chunk free
+            for (int u = tid; u < len; u += 256) chunk[1 + u] = exp_f32(sc[base + u] - mx);
+        }
         if (tid == 0) chunk[0] = total;
         __syncthreads();
         if (len < 1024) {  // a short chain: one lane
@@ -303,18 +327,7 @@ __global__ __launch_bounds__(256) void gemma_softmax_pv_kernel(GemmaAttnArgs a) 
             total = seqsum::sum_nonneg<256>(chunk, len + 1, sm);
         }
     }
-    // the weighted sum: value rows [slot][DH] of KV head g, channels c0 .. c0+63
-    const float* vh = a.v_cache + int64_t(g) * a.slots * DH + c0;
-    constexpr int LOADS = kPvChunk * 16 / 256;  // float4s per lane: 8
-    float4 v[LOADS];
-    auto fetch = [&](int base) {
-#pragma unroll
-        for (int k = 0; k < LOADS; ++k) {
-            const int e = tid + 256 * k, key = e >> 4, c4 = e & 15;
-            v[k] = base + key < n ? reinterpret_cast<const float4*>(vh + int64_t(sp.slot(base + key)) * DH)[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    };
-    fetch(0);
+    // the weighted sum (Vec::scaled_add, core.hpp:206-208): out += alpha * v
     float acc = 0.f;
     int buf = 0;
     for (int base = 0; base < n; base += kPvChunk) {
@@ -323,7 +336,7 @@ __global__ __launch_bounds__(256) void gemma_softmax_pv_kernel(GemmaAttnArgs a) 
             const int e = tid + 256 * k;
             reinterpret_cast<float4*>(&vb[buf][0][0])[e] = v[k];
         }
-        if (tid < kPvChunk && base + tid < n) al[buf][tid] = exp_f32(sc[base + tid] - mx) / total;
+        if (tid < kPvChunk && base + tid < n) al[buf][tid] = (short_span ? chunk[1 + base + tid] : exp_f32(sc[base + tid] - mx)) / total;
         __syncthreads();
         if (base + kPvChunk < n) fetch(base + kPvChunk);
         if (tid < 64) {

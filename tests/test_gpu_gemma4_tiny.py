@@ -43,6 +43,7 @@ def model(paths):
 def ref(paths):
     import oracle
 
+    oracle.set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
     r = oracle.Gemma4(path=paths)
     yield r
     r.close()
@@ -52,7 +53,11 @@ def bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
-@pytest.mark.parametrize("prompt_len,steps,max_tokens", [(100, 20, 256), (30, 8, 40), (1, 70, 128)])
+# (1100, ...) and (3900, ...): the full-attention layers' softmax totals over
+# 1024 or more keys (the exact parallel sum) and over more keys than one
+# shared-memory chunk holds (3840: the scores re-read chunk by chunk)
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("prompt_len,steps,max_tokens", [(100, 20, 256), (30, 8, 40), (1, 70, 128), (1100, 4, 1200), (3900, 4, 4096)])
 def test_tiny_gemma4_matches_oracle(model, ref, prompt_len, steps, max_tokens):
     rng = np.random.default_rng(prompt_len)
     prompt = rng.integers(0, model.V, prompt_len).astype(np.int32)

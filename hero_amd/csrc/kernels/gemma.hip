@@ -412,11 +412,19 @@ __global__ __launch_bounds__(kPostThreads) void gemma_post_norm_kernel(const flo
     __shared__ __align__(16) float sq[seqsum::kMaxN];
     const int tid = threadIdx.x, i0 = tid * PT;
     const bool on = i0 < D;
-    float v[PT], s2[PT];
+    // every input read at entry (none depends on the sums): the weights and the
+    // residual arrive while the first sum runs
+    float v[PT], s2[PT], gm[PT], rs[PT], ng[PT];
+    auto load8 = [&](const float* p, float (&dst)[PT]) {
+        const float4 x0 = reinterpret_cast<const float4*>(p + i0)[0];
+        const float4 x1 = reinterpret_cast<const float4*>(p + i0)[1];
+        dst[0] = x0.x, dst[1] = x0.y, dst[2] = x0.z, dst[3] = x0.w, dst[4] = x1.x, dst[5] = x1.y, dst[6] = x1.z, dst[7] = x1.w;
+    };
     if (on) {
-        const float4 x0 = reinterpret_cast<const float4*>(a + i0)[0];
-        const float4 x1 = reinterpret_cast<const float4*>(a + i0)[1];
-        v[0] = x0.x, v[1] = x0.y, v[2] = x0.z, v[3] = x0.w, v[4] = x1.x, v[5] = x1.y, v[6] = x1.z, v[7] = x1.w;
+        load8(a, v);
+        load8(gamma, gm);
+        load8(res, rs);
+        if (next_gamma) load8(next_gamma, ng);
     } else {
 #pragma unroll
         for (int k = 0; k < PT; ++k) v[k] = 0.f;
@@ -428,7 +436,7 @@ __global__ __launch_bounds__(kPostThreads) void gemma_post_norm_kernel(const flo
     float o[PT];
     if (on) {
 #pragma unroll
-        for (int k = 0; k < PT; ++k) o[k] = (gamma[i0 + k] * v[k] * inv + res[i0 + k]) * scale;
+        for (int k = 0; k < PT; ++k) o[k] = (gm[k] * v[k] * inv + rs[k]) * scale;
         reinterpret_cast<float4*>(out + i0)[0] = make_float4(o[0], o[1], o[2], o[3]);
         reinterpret_cast<float4*>(out + i0)[1] = make_float4(o[4], o[5], o[6], o[7]);
     } else {
@@ -443,7 +451,7 @@ __global__ __launch_bounds__(kPostThreads) void gemma_post_norm_kernel(const flo
         const float inv2 = 1.f / sqrtf(s_2 / float(D) + eps);
         if (on) {
 #pragma unroll
-            for (int k = 0; k < PT; ++k) o[k] = next_gamma[i0 + k] * o[k] * inv2;
+            for (int k = 0; k < PT; ++k) o[k] = ng[k] * o[k] * inv2;
         }
     }
     if (!on) return;

@@ -378,6 +378,89 @@ __global__ __launch_bounds__(256) void gemma_softmax_pv_kernel(GemmaAttnArgs a) 
     if ((tid & 31) == 0) qd[idx >> 5] = half_bits_to_f32(fp32_to_fp16_ref(d));
 }
 
+// The same for a sliding-window layer (at most kShortMax visible keys): the
+// head's scores and the workgroup's whole value span (kShortMax rows x 64
+// channels, 128 KB) go straight into shared memory at entry (untracked
+// global_load_lds, each wave waiting for its own), so the value rows stream in
+// while the softmax runs; the weights are formed once, then the chain runs out
+// of shared memory. Same operations and order as gemma_softmax_pv_kernel.
+constexpr int kShortMax = 512;
+
+template <int DH>
+__global__ __launch_bounds__(256) void gemma_softmax_pv_short_kernel(GemmaAttnArgs a) {
+    __shared__ __align__(16) float vrows[kShortMax][64];
+    __shared__ __align__(16) float ex[kShortMax];        // the scores, as loaded
+    __shared__ __align__(16) float chunk[kShortMax + 4];  // [0] = 0, then the exponentials
+    __shared__ __align__(16) float al[kShortMax];         // the weights
+    __shared__ float red[4];
+    __shared__ float tot;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = blockIdx.x, c0 = blockIdx.y * 64;
+    const int g = h / (a.Hq / a.Hkv);
+    const GemmaSpan sp = gemma_span(a);
+    const int n = sp.n;  // 1 .. kShortMax (the host's condition)
+    const float* sc = a.scores + int64_t(h) * a.max_ctx;
+    const float* vh = a.v_cache + int64_t(g) * a.slots * DH + c0;
+    // wave w: scores [128 w, 128 w + 128) (two 64-lane pieces), then value
+    // rows 128 w .. 128 w + 127 (32 pieces of 4 rows); positions past n read
+    // position n - 1 (never used)
+#pragma unroll
+    for (int k = 0; k < 2; ++k) lds_dma_b32(sc + min(wave * 128 + k * 64 + lane, n - 1), lds_offset(ex + wave * 128 + k * 64));
+    for (int j = 0; j < 32; ++j) {
+        const int kb = 4 * (32 * wave + j), row = min(kb + (lane >> 4), n - 1);
+        lds_dma_b128(vh + int64_t(sp.slot(row)) * DH + 4 * (lane & 15), lds_offset(&vrows[kb][0]));
+    }
+    wait_vmcnt<32>();  // this wave's scores have landed
+    __syncthreads();
+    // max, then the exponentials' sequential sum (components.hpp:131-141)
+    float mx = -INFINITY;
+    for (int t = tid; t < n; t += 256) mx = fmaxf(mx, ex[t]);
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int u = tid; u < n; u += 256) chunk[1 + u] = exp_f32(ex[u] - mx);
+    if (tid == 0) chunk[0] = 0.f;
+    __syncthreads();
+    if (tid == 0) tot = serial_sum_lds(chunk, n + 1);
+    __syncthreads();
+    const float total = tot;
+    // the weights (zeros up to the next 16) for the chain's float4 reads
+    for (int u = tid; u < (n + 15) / 16 * 16; u += 256) al[u] = u < n ? chunk[1 + u] / total : 0.f;
+    wait_vmcnt<0>();  // this wave's value rows have landed
+    __syncthreads();
+    if (tid >= 64) return;
+    // the weighted sum (Vec::scaled_add, core.hpp:206-208), 16 keys read ahead
+    float acc = 0.f;
+    int k0 = 0;
+    for (; k0 + 16 <= n; k0 += 16) {
+        float4 aw[4];
+        float vv[16];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) aw[u] = reinterpret_cast<const float4*>(&al[k0])[u];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) vv[u] = vrows[k0 + u][tid];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            acc += aw[u].x * vv[4 * u];
+            acc += aw[u].y * vv[4 * u + 1];
+            acc += aw[u].z * vv[4 * u + 2];
+            acc += aw[u].w * vv[4 * u + 3];
+        }
+    }
+    for (int k = k0; k < n; ++k) acc += al[k] * vrows[k][tid];
+    // Q8_0 of the 32-channel block this lane is in
+    float amax = fabsf(acc);
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    const float d = amax / 127.f;
+    const float id = d != 0.f ? 1.f / d : 0.f;
+    int8_t* qs = static_cast<int8_t*>(a.act_out);
+    float* qd = reinterpret_cast<float*>(qs + int64_t(a.Hq) * DH);
+    const int64_t idx = int64_t(h) * DH + c0 + tid;
+    qs[idx] = int8_t(int(roundf(acc * id)));
+    if ((tid & 31) == 0) qd[idx >> 5] = half_bits_to_f32(fp32_to_fp16_ref(d));
+}
+
 void launch_gemma_attention(const GemmaAttnArgs& a, hipStream_t s) {
     const unsigned prep = unsigned(a.Hq + (a.append ? 2 * a.Hkv : 0));
     const int64_t vis = a.window > 0 ? std::min<int64_t>(a.window, a.slots) : a.max_ctx;
@@ -386,7 +469,10 @@ void launch_gemma_attention(const GemmaAttnArgs& a, hipStream_t s) {
     if (a.Dh == 256) {
         hipLaunchKernelGGL(gemma_attn_prep_kernel<256>, dim3(prep), dim3(256), 0, s, a);
         hipLaunchKernelGGL(gemma_scores_kernel<256>, dim3(unsigned(a.Hkv), tiles), dim3(256), size_t(kGsTile * 257 + group * 256) * 4, s, a);
-        hipLaunchKernelGGL(gemma_softmax_pv_kernel<256>, dim3(unsigned(a.Hq), 256 / 64), dim3(256), 0, s, a);
+        if (a.window > 0 && a.window <= kShortMax)
+            hipLaunchKernelGGL(gemma_softmax_pv_short_kernel<256>, dim3(unsigned(a.Hq), 256 / 64), dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL(gemma_softmax_pv_kernel<256>, dim3(unsigned(a.Hq), 256 / 64), dim3(256), 0, s, a);
     } else {
         hipLaunchKernelGGL(gemma_attn_prep_kernel<512>, dim3(prep), dim3(512), 0, s, a);
         hipLaunchKernelGGL(gemma_scores_kernel<512>, dim3(unsigned(a.Hkv), tiles), dim3(256), size_t(kGsTile * 513 + group * 512) * 4, s, a);

@@ -57,10 +57,11 @@ void launch_sample_full(const float* logits, int64_t V, int top_k, float temp, f
 void launch_quantize_act(const float* x, void* act, int64_t M, int64_t K, hipStream_t s);
 void launch_pack_q8(const void* gguf_blocks, void* packed, int64_t N_total, int64_t K, int64_t row0, int64_t rows, hipStream_t s, int64_t interleave = 0);
 void launch_gemv_q8(const void* packed, const void* act, float* y, const float* resid, int64_t N, int64_t K, int epi, hipStream_t s);
-// The streaming GEMV with its input formed in the prologue from one of five
+// The streaming GEMV with its input formed in the prologue from one of six
 // sources (kInRmsNorm and kInHeadGate at K == 4096, kInSwiglu at K a multiple
-// of 4096, kInAct and kInMul at every K of gemv_streams_act).
-enum : int { kInAct = 0, kInRmsNorm = 1, kInSwiglu = 2, kInHeadGate = 3, kInMul = 4 };
+// of 4096, kInAct and kInMul at every K of gemv_streams_act, kInPostNorm at
+// the K of gemv_post_norm_fusable).
+enum : int { kInAct = 0, kInRmsNorm = 1, kInSwiglu = 2, kInHeadGate = 3, kInMul = 4, kInPostNorm = 5 };
 struct GemvInput {
     int mode;
     const int8_t* xq;        // kInAct: quantized activation [K] + fp32 scales [K/32]
@@ -72,11 +73,22 @@ struct GemvInput {
     const float* z;
     const float* up;         // kInMul: b [K]; the input is Q8_0(a * b)
     int act_rows;            // kEpiGelu: rows [0, act_rows) take the GELU
+    // kInPostNorm: the end of a Gemma sub-block (launch_gemma_post_norm's
+    // arithmetic) formed by every workgroup: o = (RMSNorm(x) * gamma + res) *
+    // scale, written to out by workgroup 0; the input is Q8_0 of
+    // RMSNorm(o) * next_gamma, or of o when next_gamma is null. out must not
+    // alias x or res.
+    const float* res;
+    float scale;
+    float* out;
+    const float* next_gamma;
 };
 bool gemv_streams(int64_t K);
 // the row lengths the streaming GEMV takes with the plain quantized input (and
 // the GELU input): 256, 1024, 2048, 2560, 2816, 4096, 8192, 10240, 12288
 bool gemv_streams_act(int64_t K);
+// the row lengths the streaming GEMV takes with the post-norm input: 2560
+bool gemv_post_norm_fusable(int64_t K);
 // workgroups of the streaming GEMV's launch for N rows under epilogue epi
 int gemv_stream_grid(int64_t N, int epi);
 // what another kernel's workgroups read ahead of the streaming GEMV over a

@@ -17,11 +17,14 @@
 //   gemma_post_norm             h2 = h + post_ffw_norm(a); act = Q8_0(h2)
 //   gemv(w_pgate)               gelu(pg)
 //   gemv(w_proj)                a, over Q8_0(gelu(pg) * ple[l])       (gemma4.hpp:100-105)
+//   gemma_post_norm             x = (h2 + post_norm(a)) * layer_output_scale; act = Q8_0(next norm(x))
 // The GELU is applied to each gate row in the producing GEMV's epilogue (once
 // per value) and the product formed and quantized in the consuming GEMV's
 // prologue; at row lengths without a streaming GEMV a gemma_gelu_mul_quant
-// does both between two plain GEMVs.
-//   gemma_post_norm             x = (h2 + post_norm(a)) * layer_output_scale; act = Q8_0(next norm(x))
+// does both between two plain GEMVs. At d_model 2560 each post-norm runs in
+// the prologue of the GEMV that reads its act (w_gate_up, w_pgate, the next
+// layer's w_qkv): every workgroup forms the row itself and workgroup 0 writes
+// h, h2 or x; the last layer's stays a launch before the LM head.
 // then the tied LM head over act (the final norm's output), the soft-cap and
 // the argmax (gemma4.hpp:440-444).
 #include "hero/gemma4.hpp"
@@ -292,13 +295,57 @@ namespace {
 // (K = `gated`). fused: both row lengths stream, the GELU is in the first
 // GEMV's epilogue and the product in the second's prologue.
 bool gelu_fusable(int64_t Kx, int64_t K) { return gemv_streams_act(Kx) && gemv_streams_act(K); }
-void gelu_gated_pair(const DeviceBuffer& wg, const DeviceBuffer& act_in, float* g, int64_t G, int64_t Kx, const float* up, const DeviceBuffer& w, const DeviceBuffer& act_mid,
-                     float* y, int64_t N, int64_t K, hipStream_t s) {
+
+// the quantized row act [K] as a GEMV input
+GemvInput act_input(const DeviceBuffer& act, int64_t K) {
+    GemvInput in{};
+    in.mode = kInAct;
+    in.xq = act.get<int8_t>();
+    in.xd = reinterpret_cast<const float*>(act.get<int8_t>() + K);
+    return in;
+}
+
+// The end of a sub-block, out = (RMSNorm(a) * gamma + res) * scale, and the
+// next GEMV's input Q8_0(next_gamma ? RMSNorm(out) * next_gamma : out): formed
+// in that GEMV's prologue where its width allows, else by a post-norm launch
+// into act.
+struct SubBlockEnd {
+    const float* a;
+    const float* gamma;
+    const float* res;
+    float scale;
+    float* out;
+    const float* next_gamma;
+};
+GemvInput sub_block_end(const SubBlockEnd& e, float eps, const DeviceBuffer& act, int64_t D, hipStream_t s) {
+    if (!gemv_post_norm_fusable(D)) {
+        launch_gemma_post_norm(e.a, e.gamma, e.res, e.scale, eps, e.out, e.next_gamma, act.get(), D, s);
+        return act_input(act, D);
+    }
+    GemvInput in{};
+    in.mode = kInPostNorm;
+    in.x = e.a;
+    in.gamma = e.gamma;
+    in.res = e.res;
+    in.scale = e.scale;
+    in.out = e.out;
+    in.next_gamma = e.next_gamma;
+    in.eps = eps;
+    return in;
+}
+
+// y[N] = W over the input in (the quantized row act when in is kInAct)
+void gemv_in(const DeviceBuffer& w, const GemvInput& in, const DeviceBuffer& act, float* y, int64_t N, int64_t K, hipStream_t s) {
+    if (in.mode == kInAct)
+        launch_gemv_q8(w.get(), act.get(), y, nullptr, N, K, kEpiStore, s);
+    else
+        launch_gemv_q8_in(w.get(), in, y, nullptr, N, K, kEpiStore, s);
+}
+
+void gelu_gated_pair(const DeviceBuffer& wg, const GemvInput& in0, const DeviceBuffer& act_in, float* g, int64_t G, int64_t Kx, const float* up, const DeviceBuffer& w,
+                     const DeviceBuffer& act_mid, float* y, int64_t N, int64_t K, hipStream_t s) {
     if (gelu_fusable(Kx, K)) {
-        GemvInput in{};
-        in.mode = kInAct;
-        in.xq = act_in.get<int8_t>();
-        in.xd = reinterpret_cast<const float*>(act_in.get<int8_t>() + Kx);
+        GemvInput in = in0;
         in.act_rows = int(K);
         launch_gemv_q8_in(wg.get(), in, g, nullptr, G, Kx, kEpiGelu, s);
         GemvInput pin{};
@@ -307,7 +354,7 @@ void gelu_gated_pair(const DeviceBuffer& wg, const DeviceBuffer& act_in, float* 
         pin.up = up;
         launch_gemv_q8_in(w.get(), pin, y, nullptr, N, K, kEpiStore, s);
     } else {
-        launch_gemv_q8(wg.get(), act_in.get(), g, nullptr, G, Kx, kEpiStore, s);
+        gemv_in(wg, in0, act_in, g, G, Kx, s);
         launch_gemma_gelu_mul_quant(g, up, act_mid.get(), K, s);
         launch_gemv_q8(w.get(), act_mid.get(), y, nullptr, N, K, kEpiStore, s);
     }
@@ -325,10 +372,11 @@ void Gemma4Model::enqueue_step(State& st) const {
     launch_gemv_q8(ple_proj_.get(), st.act_.get(), st.ctx_.get<float>(), nullptr, PL, c.D, kEpiStore, s);
     launch_gemma_ple_inputs(st.ctx_.get<float>(), st.tok_.get<float>(), ple_norm_.get<float>(), c.eps, proj_scale_, comb_scale_, st.ple_.get<float>(), c.L, c.P, s);
     launch_rmsnorm_quant(x, layers_[0].attn_norm.get<float>(), c.eps, nullptr, st.act_.get(), 1, c.D, s);
+    GemvInput qkv_in = act_input(st.act_, c.D);  // after layer 0: the previous layer's end
     for (int64_t l = 0; l < c.L; ++l) {
         const Gemma4Layer& L = layers_[size_t(l)];
         const int64_t QW = c.Hq * L.dh, KW = c.Hkv * L.dh;
-        launch_gemv_q8(L.w_qkv.get(), st.act_.get(), st.proj_.get<float>(), nullptr, L.n_qkv, c.D, kEpiStore, s);
+        gemv_in(L.w_qkv, qkv_in, st.act_, st.proj_.get<float>(), L.n_qkv, c.D, s);
         GemmaAttnArgs a{};
         a.proj = st.proj_.get<float>();
         a.k_off = QW;
@@ -352,12 +400,16 @@ void Gemma4Model::enqueue_step(State& st) const {
         a.Dh = int(L.dh);
         launch_gemma_attention(a, s);
         launch_gemv_q8(L.w_o.get(), st.act_o_.get(), st.a_.get<float>(), nullptr, c.D, QW, kEpiStore, s);
-        launch_gemma_post_norm(st.a_.get<float>(), L.post_attn_norm.get<float>(), x, 1.f, c.eps, st.h_.get<float>(), L.ffn_norm.get<float>(), st.act_.get(), c.D, s);
-        gelu_gated_pair(L.w_gate_up, st.act_, st.gu_.get<float>(), 2 * c.FF, c.D, st.gu_.get<float>() + c.FF, L.w_down, st.act_ff_, st.a_.get<float>(), c.D, c.FF, s);
-        launch_gemma_post_norm(st.a_.get<float>(), L.post_ffn_norm.get<float>(), st.h_.get<float>(), 1.f, c.eps, st.h2_.get<float>(), nullptr, st.act_.get(), c.D, s);
-        gelu_gated_pair(L.w_pgate, st.act_, st.pg_.get<float>(), c.P, c.D, st.ple_.get<float>() + l * c.P, L.w_proj, st.act_p_, st.a_.get<float>(), c.D, c.P, s);
-        const float* next = l + 1 < c.L ? layers_[size_t(l + 1)].attn_norm.get<float>() : final_norm_.get<float>();
-        launch_gemma_post_norm(st.a_.get<float>(), L.post_norm.get<float>(), st.h2_.get<float>(), L.out_scale, c.eps, x, next, st.act_.get(), c.D, s);
+        // the sub-block ends: H = X + post_attn_norm(attn), H = H + post_ffn_norm(ffn),
+        // then the PLE branch and layer_output_scale (gemma4.hpp:102-104, 258-272)
+        const GemvInput ffn_in = sub_block_end({st.a_.get<float>(), L.post_attn_norm.get<float>(), x, 1.f, st.h_.get<float>(), L.ffn_norm.get<float>()}, c.eps, st.act_, c.D, s);
+        gelu_gated_pair(L.w_gate_up, ffn_in, st.act_, st.gu_.get<float>(), 2 * c.FF, c.D, st.gu_.get<float>() + c.FF, L.w_down, st.act_ff_, st.a_.get<float>(), c.D, c.FF, s);
+        const GemvInput ple_in = sub_block_end({st.a_.get<float>(), L.post_ffn_norm.get<float>(), st.h_.get<float>(), 1.f, st.h2_.get<float>(), nullptr}, c.eps, st.act_, c.D, s);
+        gelu_gated_pair(L.w_pgate, ple_in, st.act_, st.pg_.get<float>(), c.P, c.D, st.ple_.get<float>() + l * c.P, L.w_proj, st.act_p_, st.a_.get<float>(), c.D, c.P, s);
+        if (l + 1 < c.L)
+            qkv_in = sub_block_end({st.a_.get<float>(), L.post_norm.get<float>(), st.h2_.get<float>(), L.out_scale, x, layers_[size_t(l + 1)].attn_norm.get<float>()}, c.eps, st.act_, c.D, s);
+        else
+            launch_gemma_post_norm(st.a_.get<float>(), L.post_norm.get<float>(), st.h2_.get<float>(), L.out_scale, c.eps, x, final_norm_.get<float>(), st.act_.get(), c.D, s);
     }
     // tied head over the final norm's output, soft-cap, argmax into the step's id
     launch_gemv_q8(embedding_.get(), st.act_.get(), st.logits_.get<float>(), nullptr, c.V, c.D, kEpiStore, s);

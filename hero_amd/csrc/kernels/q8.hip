@@ -109,13 +109,16 @@ constexpr int kStreamRB = 8;  // rows per sub-batch
 // offsets (zeros) and storing nothing.
 template <int KC>
 constexpr int stream_threads() { return (KC + 63) / 64 * 64; }
+// the post-norm input runs its exact sums over 256 lanes (16 values each)
+template <int KC, int XM>
+constexpr int stream_block() { return XM == kInPostNorm ? 256 : stream_threads<KC>(); }
 
 template <int KC, int D, int EPI, int XM, int IL>
-__global__ __launch_bounds__(stream_threads<KC>()) void gemv_q8_stream_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, GemvInput in, float* __restrict__ y, const float* __restrict__ resid, int N, int Npad, int TR) {
+__global__ __launch_bounds__((stream_block<KC, XM>())) void gemv_q8_stream_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, GemvInput in, float* __restrict__ y, const float* __restrict__ resid, int N, int Npad, int TR) {
     constexpr int K = 16 * KC, nb = K / 32, ts = nb + 4;  // ts: padded term row (conflict-free 16-byte reads)
     constexpr int CPL = 1;  // K-chunks per lane
     static_assert(KC % 2 == 0, "whole Q8_0 blocks");
-    static_assert(XM == kInAct || XM == kInMul || KC % 256 == 0, "the fused inputs take whole 256-lane groups");
+    static_assert(XM == kInAct || XM == kInMul || (XM == kInPostNorm && KC <= 256) || KC % 256 == 0, "the fused inputs take whole 256-lane groups");
     // row ranges in whole units: 8-row groups, or for the SwiGLU epilogue
     // 64-row groups of [32 gate rows | 32 up rows]
     constexpr int UR = EPI == kEpiSwigluQuant ? 64 : 8;
@@ -165,7 +168,8 @@ __global__ __launch_bounds__(stream_threads<KC>()) void gemv_q8_stream_kernel(co
     // every weight in flight.
     int4 xv[CPL];
     float dx[CPL];
-    float xr[16], gr[16], zr[16];               // kInRmsNorm / kInHeadGate: the lane's 16 inputs, weights (and gates)
+    float xr[16], gr[16], zr[16];               // kInRmsNorm / kInHeadGate: the lane's 16 inputs, weights (and gates); kInPostNorm: zr the residual
+    float ng[16];                               // kInPostNorm: the next norm's weights
     float4 gv[CPL][4], uv[CPL][4];              // kInSwiglu / kInMul: the lane's two factors
     if constexpr (XM == kInAct) {
 #pragma unroll
@@ -195,6 +199,19 @@ __global__ __launch_bounds__(stream_threads<KC>()) void gemv_q8_stream_kernel(co
             zr[4 * k] = zz.x, zr[4 * k + 1] = zz.y, zr[4 * k + 2] = zz.z, zr[4 * k + 3] = zz.w;
             gr[4 * k] = g.x, gr[4 * k + 1] = g.y, gr[4 * k + 2] = g.z, gr[4 * k + 3] = g.w;
         }
+    } else if constexpr (XM == kInPostNorm) {
+        // lane t: elements 16t .. 16t+15 (zeros on the lanes past KC)
+        auto load16 = [&](const float* p, float (&dst)[16]) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 a = on ? reinterpret_cast<const float4*>(p)[4 * tid + k] : make_float4(0.f, 0.f, 0.f, 0.f);
+                dst[4 * k] = a.x, dst[4 * k + 1] = a.y, dst[4 * k + 2] = a.z, dst[4 * k + 3] = a.w;
+            }
+        };
+        load16(in.x, xr);
+        load16(in.gamma, gr);
+        load16(in.res, zr);
+        if (in.next_gamma) load16(in.next_gamma, ng);
     } else {
         const float* up = XM == kInSwiglu ? in.gate_up + K : in.up;
 #pragma unroll
@@ -269,6 +286,38 @@ __global__ __launch_bounds__(stream_threads<KC>()) void gemv_q8_stream_kernel(co
         for (int k = 0; k < 16; ++k) v[k] = (gr[k] * xr[k] * inv) * zr[k];  // zr: the gates silu(z)
         uint16_t dh;
         xv[0] = quantize16_in_pair(v, &dh);
+        dx[0] = half_bits_to_f32(dh);
+    } else if constexpr (XM == kInPostNorm) {
+        // launch_gemma_post_norm's arithmetic in every workgroup (the sub-block
+        // ends of GemmaE4BLayer::forward, nm/src/gemma4.hpp:258-272, and the
+        // per-layer input residual, :102-104): o = (RMSNorm(x) * gamma + res)
+        // * scale, then the next block's RMSNorm (components.hpp:176-181) and
+        // quantize_row_q8_0; both sums of squares are the exact sequential
+        // sums (hero/seqsum.hpp)
+        __shared__ seqsum::Shared sm;
+        float sq[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) sq[k] = xr[k] * xr[k];
+        const float s1 = seqsum::sum_nonneg_regs<256>(sq, terms, K, sm);
+        const float inv = 1.f / sqrtf(s1 / float(K) + in.eps);
+        float o[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) o[k] = (gr[k] * xr[k] * inv + zr[k]) * in.scale;
+        if (blockIdx.x == 0 && on) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) reinterpret_cast<float4*>(in.out)[4 * tid + k] = make_float4(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
+        }
+        if (in.next_gamma) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) sq[k] = o[k] * o[k];
+            __syncthreads();  // the first sum's readers of terms and sm are done
+            const float s2 = seqsum::sum_nonneg_regs<256>(sq, terms, K, sm);
+            const float inv2 = 1.f / sqrtf(s2 / float(K) + in.eps);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) o[k] = ng[k] * o[k] * inv2;
+        }
+        uint16_t dh;
+        xv[0] = quantize16_in_pair(o, &dh);
         dx[0] = half_bits_to_f32(dh);
     } else if constexpr (XM == kInSwiglu || XM == kInMul) {
         // SwiGLU (nm/src/components.hpp:300-304): silu(gate) * up over the row
@@ -496,6 +545,20 @@ void stream_dispatch(int epi, const int8_t* wq, const uint16_t* wd, const GemvIn
 
 template <int KC, int D>
 void stream_dispatch_in(int epi, const int8_t* wq, const uint16_t* wd, const GemvInput& in, float* y, const float* resid, int N, int Npad, int G, int TR, size_t smem, hipStream_t s) {
+    if (in.mode == kInPostNorm) {  // Gemma's sub-block ends: stored rows or GELU gates
+        if constexpr (KC == 160) {
+            constexpr int IL = 1;
+            const dim3 block(stream_block<KC, kInPostNorm>());
+            if (epi == kEpiGelu)
+                hipLaunchKernelGGL((gemv_q8_stream_kernel<KC, D, kEpiGelu, kInPostNorm, IL>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
+            else if (epi == kEpiStore)
+                hipLaunchKernelGGL((gemv_q8_stream_kernel<KC, D, kEpiStore, kInPostNorm, IL>), dim3(unsigned(G)), block, smem, s, wq, wd, in, y, resid, N, Npad, TR);
+            else
+                throw Error(HERO_EINVAL, "streaming GEMV: the post-norm input takes the store or GELU epilogue");
+            return;
+        }
+        throw Error(HERO_EINVAL, "streaming GEMV: no post-norm input at K = " + std::to_string(16 * KC));
+    }
     if (in.mode == kInMul) {  // Gemma's FFN and per-layer input projections: stored rows only
         if (epi != kEpiStore) throw Error(HERO_EINVAL, "streaming GEMV: the product input takes the plain store epilogue");
         constexpr int IL = KC == 256 || KC % 256 != 0;
@@ -541,6 +604,7 @@ bool gemv_streams_act(int64_t K) {
         default: return false;
     }
 }
+bool gemv_post_norm_fusable(int64_t K) { return K == 2560; }
 
 int gemv_stream_grid(int64_t N, int epi) {
     const int64_t unit = epi == kEpiSwigluQuant ? 64 : 8;
@@ -582,6 +646,7 @@ void launch_gemv_q8_in(const void* packed, const GemvInput& in, float* y, const 
     const int64_t TR = epi == kEpiSwigluQuant ? 64 : std::min<int64_t>({64, rows_per, (65536 / ((nb + 4) * 4)) / 8 * 8});
     size_t smem = size_t(TR) * (nb + 4) * 4;
     if (in.mode == kInRmsNorm || in.mode == kInHeadGate) smem = std::max(smem, size_t(K) * 4);  // the squares
+    if (in.mode == kInPostNorm) smem = std::max(smem, size_t(seqsum::kMaxN) * 4);  // the squares of the 256-lane sums
     // a ring of two 8-row sub-batches: deeper rings only add padding
     // sub-batches where a workgroup has few rows
     switch (K) {

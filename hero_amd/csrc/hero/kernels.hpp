@@ -104,7 +104,7 @@ void launch_gemv_q8_in(const void* packed, const GemvInput& in, float* y, const 
 void launch_gemm_q8(const void* packed, const void* act, float* y, const float* resid, int64_t M, int64_t N, int64_t K, int epi, hipStream_t s);
 // Which kernel launch_gemm_q8 runs for a shape: one of the two skinny forms
 // (M <= 16) or the tiled kernel's row-tile height BM (16, 32, 64, 128).
-enum : int { kGemmPlanSkinnyWave = 1, kGemmPlanSkinnyShared = 2, kGemmPlanSkinnyLds = 3 };
+enum : int { kGemmPlanSkinnyWave = 1, kGemmPlanSkinnyShared = 2, kGemmPlanSkinnyLds = 3, kGemmPlanSkinnyWave4 = 4 };
 int gemm_q8_plan(int64_t M, int64_t N, int64_t K);
 void launch_block_sums(const void* packed, const void* act, int32_t* out, int64_t N, int64_t K, hipStream_t s);
 

@@ -1056,6 +1056,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_q8_skinny_kernel(const int8_t* _
 // into terms float(sumi) * (d_w * d_x) and adds each to the chain of its
 // (n, m) output in block order (the reference's order): four independent
 // chains per lane, all in registers, and no barrier in the loop.
+// MG > 1 (M up to 16 MG): a workgroup of MG waves walks the same range, wave
+// w taking activation rows 16w .. 16w+15; the waves read the same weights at
+// about the same time, so HBM delivers each weight byte once and the other
+// waves' reads hit the caches.
 // ---------------------------------------------------------------------------
 constexpr int kSkwRound = 8;                    // blocks per round
 constexpr int kSkwPairs = kSkwRound / 2;         // 16-byte weight (and activation) loads per lane per round
@@ -1072,10 +1076,12 @@ struct SkwLoads {
 };
 
 
-template <int EPI>
-__global__ __launch_bounds__(64) void gemm_q8_skinny_wave_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {
-    __shared__ __align__(16) uint16_t dws[kSkwRing][2][kSkwRound][8];  // a round's weight scales: [8-row group][block][row]
-    const int lane = threadIdx.x, q = lane >> 4, c = lane & 15;
+template <int EPI, int MG>
+__global__ __launch_bounds__(64 * MG) void gemm_q8_skinny_wave_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {
+    __shared__ __align__(16) uint16_t dws_all[MG][kSkwRing][2][kSkwRound][8];  // per wave, a round's weight scales: [8-row group][block][row]
+    const int lane = threadIdx.x & 63, q = lane >> 4, c = lane & 15;
+    const int m = 16 * int(threadIdx.x >> 6) + c;  // the lane's activation row
+    auto& dws = dws_all[threadIdx.x >> 6];
     const int nb = K >> 5, rounds = nb / kSkwRound;
     const int groups = (N + 15) >> 4, G = gridDim.x;
     const int g_begin = int(int64_t(groups) * blockIdx.x / G), g_end = int(int64_t(groups) * (blockIdx.x + 1) / G);
@@ -1092,12 +1098,12 @@ __global__ __launch_bounds__(64) void gemm_q8_skinny_wave_kernel(const int8_t* _
         const int g = g_begin + step / rounds, r = step % rounds;
         const bool on = step < steps;
         const int n = g * 16 + c, b0 = r * kSkwRound;
-        const bool wrow = on && n < N, xrow = on && c < M;
+        const bool wrow = on && n < N, xrow = on && m < M;
 #pragma unroll
         for (int i = 0; i < kSkwPairs; ++i) {
             const uint32_t off = uint32_t(b0 + 2 * i) * 32u + 16u * uint32_t(q);
             L.w[i] = __builtin_amdgcn_raw_buffer_load_b128(bw, wrow ? uint32_t(n) * uint32_t(K) + off : kOOB, 0, 0);
-            L.x[i] = __builtin_amdgcn_raw_buffer_load_b128(bx, xrow ? uint32_t(c) * uint32_t(K) + off : kOOB, 0, 0);
+            L.x[i] = __builtin_amdgcn_raw_buffer_load_b128(bx, xrow ? uint32_t(m) * uint32_t(K) + off : kOOB, 0, 0);
         }
         // 8 rows x block b0 + c of 8-row group 2g + q / 2 (16 bytes; lanes q
         // and q ^ 1 read the same)
@@ -1105,14 +1111,14 @@ __global__ __launch_bounds__(64) void gemm_q8_skinny_wave_kernel(const int8_t* _
         L.d = __builtin_amdgcn_raw_buffer_load_b128(bd, drow ? uint32_t(scale_index(g * 16 + 8 * (q >> 1), b0 + c, nb)) * 2u : kOOB, 0, 0);
 #pragma unroll
         for (int i = 0; i < kSkwRound / 4; ++i)
-            L.dx[i] = __builtin_amdgcn_raw_buffer_load_b128(bxd, xrow ? (uint32_t(c) * uint32_t(nb) + uint32_t(b0 + 4 * i)) * 4u : kOOB, 0, 0);
+            L.dx[i] = __builtin_amdgcn_raw_buffer_load_b128(bxd, xrow ? (uint32_t(m) * uint32_t(nb) + uint32_t(b0 + 4 * i)) * 4u : kOOB, 0, 0);
     };
 
     SkwLoads ring[kSkwRing];
 #pragma unroll
     for (int k = 0; k < kSkwRing; ++k) load(k, ring[k]);
 
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // outputs (n = g*16 + 4q + r, m = c)
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // outputs (n = g*16 + 4q + r, m)
     for (int s0 = 0; s0 < steps_pad; s0 += kSkwRing) {
 #pragma unroll
         for (int k = 0; k < kSkwRing; ++k) {
@@ -1155,8 +1161,8 @@ __global__ __launch_bounds__(64) void gemm_q8_skinny_wave_kernel(const int8_t* _
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
                     const int n = g * 16 + 4 * q + rr;
-                    if (n < N && c < M) {
-                        const int64_t o = int64_t(c) * N + n;
+                    if (n < N && m < M) {
+                        const int64_t o = int64_t(m) * N + n;
                         if constexpr (EPI == kEpiResidual)
                             y[o] = resid[o] + acc[rr];  // h = x + m (nm/src/qwen35.hpp:321)
                         else
@@ -1333,6 +1339,13 @@ int gemm_q8_plan(int64_t M, int64_t N, int64_t K) {
     if (M <= 16 && groups >= 2 * device_cus() && K % (32 * kSkwRound) == 0 && K <= kSkwMaxK && N * K < (int64_t(1) << 31))
         return K <= kSklMaxK && groups >= 4 * device_cus() ? kGemmPlanSkinnyLds : kGemmPlanSkinnyWave;
     if (M <= 16 && K % 256 == 0 && K <= kSkMaxK && N * K < (int64_t(1) << 31)) return kGemmPlanSkinnyShared;
+    // 16 < M <= 64 with at most a group per CU, where the row tiles leave
+    // most CUs with one workgroup: the weights streamed once, every wave a
+    // 16-row activation group (M = 64: 4096 x 4096 27.6 -> 23.2 us, 12288 x
+    // 4096 77.6 -> 59.0 us). With more groups the waves' activation reads
+    // load the caches more than the tiles do (151936 rows: 706 us against
+    // 223; 12288 rows: 79 against 32).
+    if (M > 16 && M <= 64 && groups <= device_cus() && K % (32 * kSkwRound) == 0 && K <= kSkwMaxK && N * K < (int64_t(1) << 31)) return kGemmPlanSkinnyWave4;
     // the tallest tile that still gives every CU two workgroups (the fp32
     // term work per CU is the same; more workgroups hide more latency)
     const int64_t tiles_n = (N + kGemmBN - 1) / kGemmBN, want = 2 * device_cus();
@@ -1384,10 +1397,23 @@ void launch_gemm_q8(const void* packed, const void* act, float* y, const float* 
         // tall, below 4 groups per CU or at K > 4096: a wave per group range,
         // every chain in registers
         if (epi == kEpiResidual)
-            hipLaunchKernelGGL(gemm_q8_skinny_wave_kernel<kEpiResidual>, dim3(grid_for(gemm_q8_skinny_wave_kernel<kEpiResidual>, 64, 0)), dim3(64), 0, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
+            hipLaunchKernelGGL((gemm_q8_skinny_wave_kernel<kEpiResidual, 1>), dim3(grid_for(gemm_q8_skinny_wave_kernel<kEpiResidual, 1>, 64, 0)), dim3(64), 0, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
         else
-            hipLaunchKernelGGL(gemm_q8_skinny_wave_kernel<kEpiStore>, dim3(grid_for(gemm_q8_skinny_wave_kernel<kEpiStore>, 64, 0)), dim3(64), 0, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
+            hipLaunchKernelGGL((gemm_q8_skinny_wave_kernel<kEpiStore, 1>), dim3(grid_for(gemm_q8_skinny_wave_kernel<kEpiStore, 1>, 64, 0)), dim3(64), 0, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
         break;
+    case kGemmPlanSkinnyWave4: {
+        // 16 < M <= 64 at one group per CU or fewer: two or four waves per
+        // group range, one per 16 activation rows
+        auto run = [&](auto kernel, int mg) {
+            hipLaunchKernelGGL(kernel, dim3(grid_for(kernel, 64 * mg, 0)), dim3(64 * mg), 0, s, wq, wd, xq, xd, y, resid, int(M), int(N), Npad, int(K));
+        };
+        const bool r = epi == kEpiResidual;
+        if (M <= 32)
+            r ? run(gemm_q8_skinny_wave_kernel<kEpiResidual, 2>, 2) : run(gemm_q8_skinny_wave_kernel<kEpiStore, 2>, 2);
+        else
+            r ? run(gemm_q8_skinny_wave_kernel<kEpiResidual, 4>, 4) : run(gemm_q8_skinny_wave_kernel<kEpiStore, 4>, 4);
+        break;
+    }
     case kGemmPlanSkinnyShared: {
         // few groups: sixteen waves share each group's blocks
         constexpr int NW = 16;

@@ -96,8 +96,10 @@ int hero_q8_0_gemm(const void* packed, const void* act, float* y, const float* r
 /* Which kernel hero_q8_0_gemm runs for an (m, n, k) on the current device,
  * without running it: *kernel = 1 (skinny, one wave per range of 16-row
  * groups), 2 (skinny, sixteen waves sharing each group), 3 (skinny, waves
- * per range of 16-row groups with the activation rows in shared memory) or
- * the tiled kernel's rows per tile (16, 32, 64, 128). The choice depends on the
+ * per range of 16-row groups with the activation rows in shared memory), 4
+ * (skinny, two or four waves per range of 16-row groups, one per 16
+ * activation rows: 16 < m <= 64) or the tiled kernel's rows per tile (16, 32,
+ * 64, 128). The choice depends on the
  * device's compute-unit count. No counterpart in the reference (its matmul
  * has one form, nm/src/quant_i8.hpp:430-474); lets tests show that every
  * form was checked. */

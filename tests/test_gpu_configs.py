@@ -30,8 +30,8 @@ from gpu_util import act_to_blocks, bits, check, dev, empty, gdn_reference, host
 pytestmark = pytest.mark.gpu
 
 GEMM_SHAPES = [(4096, 4096), (4096, 12288), (4096, 151936), (12288, 4096)]  # (K, N)
-GEMM_ROWS = [1, 8, 24, 64, 512]
-PLAN_NAMES = {1: "skinny-wave", 2: "skinny-shared", 3: "skinny-lds", 16: "tile16", 32: "tile32", 64: "tile64", 128: "tile128"}
+GEMM_ROWS = [1, 8, 24, 64, 100, 512]
+PLAN_NAMES = {1: "skinny-wave", 2: "skinny-shared", 3: "skinny-lds", 4: "skinny-wave4", 16: "tile16", 32: "tile32", 64: "tile64", 128: "tile128"}
 
 
 def say(msg):

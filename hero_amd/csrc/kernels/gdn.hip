@@ -51,6 +51,35 @@ __device__ __forceinline__ float sum_squares_128(const float* v) {
     return ss;
 }
 
+// s = 0; s += p[i] for i = 0 .. 127, in order (128 floats in shared memory,
+// 16-byte aligned), read 32 at a time one chunk ahead of their adds
+__device__ __forceinline__ float seq_sum_128(const float* p) {
+    const float4* p4 = reinterpret_cast<const float4*>(p);
+    float4 a[8], b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = p4[i];
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        if (c < 3) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) b[i] = p4[8 * (c + 1) + i];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            s += a[i].x;
+            s += a[i].y;
+            s += a[i].z;
+            s += a[i].w;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[i] = b[i];
+    }
+    return s;
+}
+
 // Causal conv of one channel (nm/src/recurrent.hpp:75-106): sum = taps[W-1]*x,
 // then += taps[i] * (input at position p-(W-1)+i), oldest first.
 template <int W>
@@ -147,8 +176,9 @@ __device__ __forceinline__ void past_from_ring(const float (&ring)[W], int pos, 
     }
 }
 
-template <int W>
-__global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(GdnDecodeArgs a) {
+template <int W, int NT>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT == 256 ? 2 : 1))) void gdn_decode_kernel(GdnDecodeArgs a) {
+    constexpr int kGdnRows = kGdnDim * kGdnDim / NT;  // state rows per lane
     extern __shared__ __align__(16) float gdn_raw[];
     GdnDecodeShared& sh = *reinterpret_cast<GdnDecodeShared*>(gdn_raw);
     const int t = threadIdx.x, j = t % kGdnDim, i0 = (t / kGdnDim) * kGdnRows;
@@ -191,9 +221,14 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(GdnDecodeArgs a
         gamma = a.norm_gamma[j];
     }
     __builtin_amdgcn_sched_barrier(0);
+    // raw buffer accesses with the row in the scalar offset: one address
+    // register for all rows (64-bit addresses per row would hold 2 registers
+    // each until the store-back)
+    const __amdgpu_buffer_rsrc_t bS = buffer_of(S, uint32_t(kGdnState) * 4u);
+    const uint32_t soff = uint32_t(i0 * kGdnDim + j) * 4u;
     float col[kGdnRows];
 #pragma unroll
-    for (int r = 0; r < kGdnRows; ++r) col[r] = S[(i0 + r) * kGdnDim + j];
+    for (int r = 0; r < kGdnRows; ++r) col[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bS, soff, uint32_t(r * kGdnDim * 4), 0));
     __builtin_amdgcn_sched_barrier(0);
     if (t < 32) sh.etab[t] = etv;
     __syncthreads();  // the table
@@ -228,18 +263,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(GdnDecodeArgs a
     __syncthreads();
     // ---- L2 norms (nm/src/recurrent.hpp:40-48), sequential sums ----
     if (t == 0 || t == 64) {
-        const float4* s4 = reinterpret_cast<const float4*>(sh.sq[t == 0 ? 0 : 1]);
-        float4 x[kGdnDim / 4];
-#pragma unroll
-        for (int i = 0; i < kGdnDim / 4; ++i) x[i] = s4[i];
-        float ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < kGdnDim / 4; ++i) {
-            ss += x[i].x;
-            ss += x[i].y;
-            ss += x[i].z;
-            ss += x[i].w;
-        }
+        const float ss = seq_sum_128(sh.sq[t == 0 ? 0 : 1]);
         sh.scal[t == 0 ? 0 : 1] = 1.f / fmaxf(sqrtf(ss), 1e-6f);
     }
     __syncthreads();
@@ -251,42 +275,34 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(GdnDecodeArgs a
     __syncthreads();
 
     // ---- 2. decay and the prediction products (recurrent.hpp:146-177) ----
-    float kr[kGdnRows];
-#pragma unroll
-    for (int r = 0; r < kGdnRows; r += 4) {
-        const float4 k4 = *reinterpret_cast<const float4*>(sh.k + i0 + r);
-        kr[r] = k4.x, kr[r + 1] = k4.y, kr[r + 2] = k4.z, kr[r + 3] = k4.w;
-    }
     float* prow = &sh.prod[j][i0];
 #pragma unroll
     for (int r = 0; r < kGdnRows; r += 4) {
+        const float4 k4 = *reinterpret_cast<const float4*>(sh.k + i0 + r);
         col[r] = col[r] * decay, col[r + 1] = col[r + 1] * decay, col[r + 2] = col[r + 2] * decay, col[r + 3] = col[r + 3] * decay;
-        *reinterpret_cast<float4*>(prow + r) = make_float4(col[r] * kr[r], col[r + 1] * kr[r + 1], col[r + 2] * kr[r + 2], col[r + 3] * kr[r + 3]);
+        *reinterpret_cast<float4*>(prow + r) = make_float4(col[r] * k4.x, col[r + 1] * k4.y, col[r + 2] * k4.z, col[r + 3] * k4.w);
     }
     __syncthreads();
     if (owner) {  // pred_j = sum_i S[i][j] * k[i], in i order
-        const float4* p4 = reinterpret_cast<const float4*>(&sh.prod[j][0]);
-        float4 x[kGdnDim / 4];
-#pragma unroll
-        for (int i = 0; i < kGdnDim / 4; ++i) x[i] = p4[i];
-        float pred = 0.f;
-#pragma unroll
-        for (int i = 0; i < kGdnDim / 4; ++i) {
-            pred = pred + x[i].x;
-            pred = pred + x[i].y;
-            pred = pred + x[i].z;
-            pred = pred + x[i].w;
-        }
+        const float pred = seq_sum_128(&sh.prod[j][0]);
         sh.delta[j] = (v - pred) * beta;
     }
     __syncthreads();
 
     // ---- 3. the update, stored back, and the output products ----
     const float delta = sh.delta[j];
+    // k read again from shared memory (not kept in registers across the
+    // chain: the 64-row form would spill)
 #pragma unroll
-    for (int r = 0; r < kGdnRows; ++r) col[r] = col[r] + kr[r] * delta;
+    for (int r = 0; r < kGdnRows; r += 4) {
+        const float4 k4 = *reinterpret_cast<const float4*>(sh.k + i0 + r);
+        col[r] = col[r] + k4.x * delta;
+        col[r + 1] = col[r + 1] + k4.y * delta;
+        col[r + 2] = col[r + 2] + k4.z * delta;
+        col[r + 3] = col[r + 3] + k4.w * delta;
+    }
 #pragma unroll
-    for (int r = 0; r < kGdnRows; ++r) S[(i0 + r) * kGdnDim + j] = col[r];
+    for (int r = 0; r < kGdnRows; ++r) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, col[r]), bS, soff, uint32_t(r * kGdnDim * 4), 0);
 #pragma unroll
     for (int r = 0; r < kGdnRows; r += 4) {
         const float4 q4 = *reinterpret_cast<const float4*>(sh.q + i0 + r);
@@ -295,35 +311,14 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(GdnDecodeArgs a
     __syncthreads();
     float o = 0.f;
     if (owner) {  // o_j = sum_i S[i][j] * q[i], in i order
-        const float4* p4 = reinterpret_cast<const float4*>(&sh.prod[j][0]);
-        float4 x[kGdnDim / 4];
-#pragma unroll
-        for (int i = 0; i < kGdnDim / 4; ++i) x[i] = p4[i];
-#pragma unroll
-        for (int i = 0; i < kGdnDim / 4; ++i) {
-            o = o + x[i].x;
-            o = o + x[i].y;
-            o = o + x[i].z;
-            o = o + x[i].w;
-        }
+        o = seq_sum_128(&sh.prod[j][0]);
         sh.sq[0][j] = o * o;
     }
     __syncthreads();
 
     // ---- 4. per-head RMSNorm (components.hpp:176-181), SiLU(z) gate, quantize ----
     if (t == 0) {
-        const float4* s4 = reinterpret_cast<const float4*>(sh.sq[0]);
-        float4 x[kGdnDim / 4];
-#pragma unroll
-        for (int i = 0; i < kGdnDim / 4; ++i) x[i] = s4[i];
-        float ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < kGdnDim / 4; ++i) {
-            ss += x[i].x;
-            ss += x[i].y;
-            ss += x[i].z;
-            ss += x[i].w;
-        }
+        const float ss = seq_sum_128(sh.sq[0]);
         sh.scal[2] = 1.f / sqrtf(ss / float(kGdnDim) + a.eps);
     }
     __syncthreads();
@@ -1139,19 +1134,32 @@ __global__ __launch_bounds__(256) void gdn_hist_kernel(const float* __restrict__
     hist[int64_t((pos0 + t) % W) * CC + c] = proj[int64_t(t) * proj_stride + c];
 }
 
-void launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t s) {
+namespace {
+template <int NT>
+void gdn_decode_dispatch(const GdnDecodeArgs& a, hipStream_t s) {
     const dim3 grid(unsigned(a.Hv), unsigned(a.B));
     const size_t sm = sizeof(GdnDecodeShared);
     switch (a.W) {
-        case 1: hipLaunchKernelGGL(gdn_decode_kernel<1>, grid, dim3(kGdnThreads), sm, s, a); break;
-        case 2: hipLaunchKernelGGL(gdn_decode_kernel<2>, grid, dim3(kGdnThreads), sm, s, a); break;
-        case 3: hipLaunchKernelGGL(gdn_decode_kernel<3>, grid, dim3(kGdnThreads), sm, s, a); break;
-        case 4: hipLaunchKernelGGL(gdn_decode_kernel<4>, grid, dim3(kGdnThreads), sm, s, a); break;
-        case 5: hipLaunchKernelGGL(gdn_decode_kernel<5>, grid, dim3(kGdnThreads), sm, s, a); break;
-        case 6: hipLaunchKernelGGL(gdn_decode_kernel<6>, grid, dim3(kGdnThreads), sm, s, a); break;
-        case 7: hipLaunchKernelGGL(gdn_decode_kernel<7>, grid, dim3(kGdnThreads), sm, s, a); break;
-        default: hipLaunchKernelGGL(gdn_decode_kernel<8>, grid, dim3(kGdnThreads), sm, s, a); break;
+        case 1: hipLaunchKernelGGL((gdn_decode_kernel<1, NT>), grid, dim3(NT), sm, s, a); break;
+        case 2: hipLaunchKernelGGL((gdn_decode_kernel<2, NT>), grid, dim3(NT), sm, s, a); break;
+        case 3: hipLaunchKernelGGL((gdn_decode_kernel<3, NT>), grid, dim3(NT), sm, s, a); break;
+        case 4: hipLaunchKernelGGL((gdn_decode_kernel<4, NT>), grid, dim3(NT), sm, s, a); break;
+        case 5: hipLaunchKernelGGL((gdn_decode_kernel<5, NT>), grid, dim3(NT), sm, s, a); break;
+        case 6: hipLaunchKernelGGL((gdn_decode_kernel<6, NT>), grid, dim3(NT), sm, s, a); break;
+        case 7: hipLaunchKernelGGL((gdn_decode_kernel<7, NT>), grid, dim3(NT), sm, s, a); break;
+        default: hipLaunchKernelGGL((gdn_decode_kernel<8, NT>), grid, dim3(NT), sm, s, a); break;
     }
+}
+}  // namespace
+
+void launch_gdn_decode(const GdnDecodeArgs& a, hipStream_t s) {
+    // 512 lanes (32 state rows each) while every (sequence, head) gets a CU of
+    // its own; with more workgroups than CUs, 256 lanes (64 rows each), so
+    // that two fit per CU and every workgroup runs at once
+    if (int64_t(a.Hv) * a.B > device_cus())
+        gdn_decode_dispatch<256>(a, s);
+    else
+        gdn_decode_dispatch<kGdnThreads>(a, s);
 }
 
 void launch_gdn_decode_cols(const GdnDecodeArgs& a, float* o_raw, float* g_raw, hipStream_t s) {

@@ -66,9 +66,13 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_quant_regs_kernel(const 
     const int tid = threadIdx.x, i0 = tid * PT;
     const bool on = i0 < D;  // whole quads (D % 32 == 0)
     float v[PT], s2[PT];
+    // the weights are read at entry with the row (neither depends on the sum)
+    float4 ga = make_float4(0.f, 0.f, 0.f, 0.f), gb = ga;
     if (on) {
         const float4 a = reinterpret_cast<const float4*>(x + row * D + i0)[0];
         const float4 b = reinterpret_cast<const float4*>(x + row * D + i0)[1];
+        ga = reinterpret_cast<const float4*>(gamma + i0)[0];
+        gb = reinterpret_cast<const float4*>(gamma + i0)[1];
         v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
     } else {
 #pragma unroll
@@ -79,8 +83,6 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_quant_regs_kernel(const 
     const float s = seqsum::sum_nonneg_regs<kNormThreads>(s2, sq, D, sm);
     const float inv = 1.f / sqrtf(s / float(D) + eps);
     if (!on) return;
-    const float4 ga = reinterpret_cast<const float4*>(gamma + i0)[0];
-    const float4 gb = reinterpret_cast<const float4*>(gamma + i0)[1];
     float o[8] = {ga.x * v[0] * inv, ga.y * v[1] * inv, ga.z * v[2] * inv, ga.w * v[3] * inv, gb.x * v[4] * inv, gb.y * v[5] * inv, gb.z * v[6] * inv, gb.w * v[7] * inv};
     if (y) {
         reinterpret_cast<float4*>(y + row * D + i0)[0] = make_float4(o[0], o[1], o[2], o[3]);

@@ -254,6 +254,130 @@ __global__ __launch_bounds__(256) void gemma_scores_kernel(GemmaAttnArgs a) {
     }
 }
 
+// gemma_head's operations for one head by one wave: lane l holds the values
+// l + 64 m; buf is the wave's DH floats of shared memory (the squares, then
+// the normed values for the RoPE pairs). A wave's shared-memory accesses take
+// effect in order, so it needs no barrier.
+template <int DH>
+__device__ __forceinline__ void gemma_head_wave(const float* x, const float* gamma, float eps, const float* cs, float* buf, float* out) {
+    constexpr int PL = DH / 64;
+    const int lane = threadIdx.x & 63;
+    float v[PL];
+#pragma unroll
+    for (int m = 0; m < PL; ++m) v[m] = x[lane + 64 * m];
+#pragma unroll
+    for (int m = 0; m < PL; ++m) buf[lane + 64 * m] = v[m] * v[m];
+    float sc = 0.f;
+    if (lane == 0) sc = 1.f / sqrtf(serial_sum_lds(buf, DH) / float(DH) + eps);
+    sc = __shfl(sc, 0);
+    float n[PL];
+#pragma unroll
+    for (int m = 0; m < PL; ++m) n[m] = gamma ? gamma[lane + 64 * m] * v[m] * sc : v[m] * sc;
+    if (!cs) {
+#pragma unroll
+        for (int m = 0; m < PL; ++m) out[lane + 64 * m] = n[m];
+        return;
+    }
+#pragma unroll
+    for (int m = 0; m < PL; ++m) buf[lane + 64 * m] = n[m];
+    constexpr int half = DH / 2;
+#pragma unroll
+    for (int m = 0; m < PL; ++m) {
+        const int j = lane + 64 * m, i = j < half ? j : j - half;
+        const float c = cs[2 * i], sn = cs[2 * i + 1];
+        const float xx = buf[i], yy = buf[i + half];
+        out[j] = j < half ? xx * c - yy * sn : yy * c + xx * sn;
+    }
+}
+
+// The prep step folded into the scores: workgroup (KV head g, tile y) forms
+// its group's query heads itself (one wave per head, gemma_head's
+// operations) while its first tile's key rows land, and the workgroup whose
+// tiles include the new position also forms that position's key and value
+// (appending them to the caches) and puts the key into its tile in place of
+// the cached row. Then the scores exactly as gemma_scores_kernel.
+// Eight waves: every head's prep (the group's queries, and the new key and
+// value) runs at once, one wave each.
+constexpr int kPsThreads = 512, kPsWaves = kPsThreads / 64;
+template <int DH>
+constexpr size_t prep_scores_shared(int group) { return size_t(kGsTile * (DH + 1) + group * DH + DH + kPsWaves * DH) * 4; }
+
+template <int DH>
+__global__ __launch_bounds__(kPsThreads) void gemma_prep_scores_kernel(GemmaAttnArgs a) {
+    constexpr int KS = DH + 1;  // padded key row
+    extern __shared__ __align__(16) float kt[];  // [kGsTile][KS], q [group][DH], knew [DH], per-wave [kPsWaves][DH]
+    const int g = blockIdx.x, group = a.Hq / a.Hkv;
+    float* q = kt + kGsTile * KS;
+    float* knew = q + group * DH;
+    float* hb = knew + DH;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const GemmaSpan sp = gemma_span(a);
+    const int tiles = (sp.n + kGsTile - 1) / kGsTile;
+    if (int(blockIdx.y) >= tiles) return;  // no tile for this workgroup
+    const int pos = sp.first + sp.n - 1;
+    const int ptile = (sp.n - 1) / kGsTile, prow = (sp.n - 1) % kGsTile;  // the new position's tile and row
+    const bool has_pos = a.append && ptile % int(gridDim.y) == int(blockIdx.y);
+    const float* kh = a.k_cache + int64_t(g) * a.slots * DH;
+    constexpr int Q4 = DH / 4;                    // float4s per key row
+    constexpr int LOADS = kGsTile * Q4 / kPsThreads;  // per lane: 8 (DH 256) or 16 (DH 512)
+    float4 v[LOADS];
+    auto load_tile = [&](int tile) {
+        const int t0 = tile * kGsTile;
+#pragma unroll
+        for (int k = 0; k < LOADS; ++k) {
+            const int e = tid + kPsThreads * k, key = e / Q4, c4 = e % Q4;
+            v[k] = t0 + key < sp.n ? reinterpret_cast<const float4*>(kh + int64_t(sp.slot(t0 + key)) * DH)[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    int tile = blockIdx.y;
+    load_tile(tile);
+    // Q = rope(q_norm(WQ x)); with append, K = rope(k_norm(WK x)) and
+    // V = v_norm(WV x) of the position (GemmaE4BLayer::attention,
+    // nm/src/gemma4.hpp:205-208)
+    const float* cs = a.rope_cs + int64_t(pos) * DH;  // [DH/2][2]
+    const int64_t slot = a.window > 0 ? pos % a.slots : pos;
+    const int items = group + (has_pos ? 2 : 0);
+    for (int it = wave; it < items; it += kPsWaves) {
+        float* buf = hb + wave * DH;
+        if (it < group) {
+            gemma_head_wave<DH>(a.proj + int64_t(g * group + it) * DH, a.q_gamma, a.eps, cs, buf, q + it * DH);
+        } else if (it == group) {
+            gemma_head_wave<DH>(a.proj + a.k_off + int64_t(g) * DH, a.k_gamma, a.eps, cs, buf, knew);
+            float* kc = a.k_cache + (int64_t(g) * a.slots + slot) * DH;  // [Hkv][slots][DH]
+            for (int c = lane; c < DH; c += 64) kc[c] = knew[c];
+        } else {
+            gemma_head_wave<DH>(a.proj + a.v_off + int64_t(g) * DH, nullptr, a.eps, nullptr, buf, a.v_cache + (int64_t(g) * a.slots + slot) * DH);
+        }
+    }
+    while (true) {
+        const int t0 = tile * kGsTile;
+        __syncthreads();  // the previous tile's readers are done; the first time, the prep's results
+        const bool patch = has_pos && tile == ptile;
+#pragma unroll
+        for (int k = 0; k < LOADS; ++k) {
+            const int e = tid + kPsThreads * k, key = e / Q4, c4 = e % Q4;
+            const float4 x = patch && key == prow ? reinterpret_cast<const float4*>(knew)[c4] : v[k];
+            float* dst = kt + key * KS + 4 * c4;
+            dst[0] = x.x, dst[1] = x.y, dst[2] = x.z, dst[3] = x.w;
+        }
+        __syncthreads();
+        const int t = t0 + lane;
+        if (t < sp.n) {
+            const float* kr = kt + lane * KS;
+            for (int hh = wave; hh < group; hh += kPsWaves) {
+                const float* qh = q + hh * DH;
+                float dot = 0.f;
+#pragma unroll 16
+                for (int c = 0; c < DH; ++c) dot += qh[c] * kr[c];
+                a.scores[int64_t(g * group + hh) * a.max_ctx + t] = dot;
+            }
+        }
+        tile += gridDim.y;
+        if (tile >= tiles) break;
+        load_tile(tile);
+    }
+}
+
 // The softmax of head h's n scores (components.hpp:131-141: e_t = exp(s_t - max),
 // their sequential sum in chunks, each starting with the running total,
 // alpha_t = e_t / total) and the weighted sum of its value rows for 64
@@ -461,21 +585,31 @@ __global__ __launch_bounds__(256) void gemma_softmax_pv_short_kernel(GemmaAttnAr
     if ((tid & 31) == 0) qd[idx >> 5] = half_bits_to_f32(fp32_to_fp16_ref(d));
 }
 
+constexpr size_t kPrepScoresMaxShared = 160 * 1024;  // shared memory per CU
+
 void launch_gemma_attention(const GemmaAttnArgs& a, hipStream_t s) {
     const unsigned prep = unsigned(a.Hq + (a.append ? 2 * a.Hkv : 0));
     const int64_t vis = a.window > 0 ? std::min<int64_t>(a.window, a.slots) : a.max_ctx;
     const unsigned tiles = unsigned(std::min<int64_t>(128, (vis + kGsTile - 1) / kGsTile));
     const int group = a.Hq / a.Hkv;
     if (a.Dh == 256) {
-        hipLaunchKernelGGL(gemma_attn_prep_kernel<256>, dim3(prep), dim3(256), 0, s, a);
-        hipLaunchKernelGGL(gemma_scores_kernel<256>, dim3(unsigned(a.Hkv), tiles), dim3(256), size_t(kGsTile * 257 + group * 256) * 4, s, a);
+        if (prep_scores_shared<256>(group) <= kPrepScoresMaxShared) {
+            hipLaunchKernelGGL(gemma_prep_scores_kernel<256>, dim3(unsigned(a.Hkv), tiles), dim3(kPsThreads), prep_scores_shared<256>(group), s, a);
+        } else {
+            hipLaunchKernelGGL(gemma_attn_prep_kernel<256>, dim3(prep), dim3(256), 0, s, a);
+            hipLaunchKernelGGL(gemma_scores_kernel<256>, dim3(unsigned(a.Hkv), tiles), dim3(256), size_t(kGsTile * 257 + group * 256) * 4, s, a);
+        }
         if (a.window > 0 && a.window <= kShortMax)
             hipLaunchKernelGGL(gemma_softmax_pv_short_kernel<256>, dim3(unsigned(a.Hq), 256 / 64), dim3(256), 0, s, a);
         else
             hipLaunchKernelGGL(gemma_softmax_pv_kernel<256>, dim3(unsigned(a.Hq), 256 / 64), dim3(256), 0, s, a);
     } else {
-        hipLaunchKernelGGL(gemma_attn_prep_kernel<512>, dim3(prep), dim3(512), 0, s, a);
-        hipLaunchKernelGGL(gemma_scores_kernel<512>, dim3(unsigned(a.Hkv), tiles), dim3(256), size_t(kGsTile * 513 + group * 512) * 4, s, a);
+        if (prep_scores_shared<512>(group) <= kPrepScoresMaxShared) {
+            hipLaunchKernelGGL(gemma_prep_scores_kernel<512>, dim3(unsigned(a.Hkv), tiles), dim3(kPsThreads), prep_scores_shared<512>(group), s, a);
+        } else {
+            hipLaunchKernelGGL(gemma_attn_prep_kernel<512>, dim3(prep), dim3(512), 0, s, a);
+            hipLaunchKernelGGL(gemma_scores_kernel<512>, dim3(unsigned(a.Hkv), tiles), dim3(256), size_t(kGsTile * 513 + group * 512) * 4, s, a);
+        }
         hipLaunchKernelGGL(gemma_softmax_pv_kernel<512>, dim3(unsigned(a.Hq), 512 / 64), dim3(256), 0, s, a);
     }
 }

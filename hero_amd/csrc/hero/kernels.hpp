@@ -102,6 +102,11 @@ void launch_gemv_q8_in(const void* packed, const GemvInput& in, float* y, const 
 // Y[M][N] (+ R) = the M quantized activation rows (act_q8 layout, M rows)
 // times W^T, each element in the reference's block order; int8 MFMA.
 void launch_gemm_q8(const void* packed, const void* act, float* y, const float* resid, int64_t M, int64_t N, int64_t K, int epi, hipStream_t s);
+// The gate/up GEMM of rows interleaved as 64-row units [32 gate | 32 up] with
+// silu(gate) * up and its Q8_0 formed in the epilogue (out: the down
+// projection's act [M][N/2] + scales); false (nothing launched) where the
+// shape does not take the shared-memory skinny form
+bool launch_gemm_q8_swiglu(const void* packed, const void* act, void* out, int64_t M, int64_t N, int64_t K, hipStream_t s);
 // Which kernel launch_gemm_q8 runs for a shape: one of the two skinny forms
 // (M <= 16) or the tiled kernel's row-tile height BM (16, 32, 64, 128).
 enum : int { kGemmPlanSkinnyWave = 1, kGemmPlanSkinnyShared = 2, kGemmPlanSkinnyLds = 3, kGemmPlanSkinnyWave4 = 4 };

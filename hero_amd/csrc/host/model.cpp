@@ -1069,8 +1069,11 @@ void Qwen35Model::enqueue_batch_step(State& st) const {
         }
         launch_gemm_q8(L.w_out.get(), st.act_mix_.get(), h, x, B, c.D, k_mix, kEpiResidual, s);
         launch_rmsnorm_quant(h, L.channel_norm.get<float>(), c.eps, nullptr, st.act_d_.get(), B, c.D, s);
-        launch_gemm_q8(L.w_gate_up.get(), st.act_d_.get(), st.gate_up_.get<float>(), nullptr, B, 2 * c.FF, c.D, kEpiStore, s);
-        launch_swiglu_quant(st.gate_up_.get<float>(), st.act_ff_.get(), B, c.FF, s, ffn_fused_ ? 32 : 0);
+        // interleaved gate/up rows: SwiGLU and its quantization in the GEMM's epilogue
+        if (!ffn_fused_ || !launch_gemm_q8_swiglu(L.w_gate_up.get(), st.act_d_.get(), st.act_ff_.get(), B, 2 * c.FF, c.D, s)) {
+            launch_gemm_q8(L.w_gate_up.get(), st.act_d_.get(), st.gate_up_.get<float>(), nullptr, B, 2 * c.FF, c.D, kEpiStore, s);
+            launch_swiglu_quant(st.gate_up_.get<float>(), st.act_ff_.get(), B, c.FF, s, ffn_fused_ ? 32 : 0);
+        }
         launch_gemm_q8(L.w_down.get(), st.act_ff_.get(), x, h, B, c.D, c.FF, kEpiResidual, s);
     }
     launch_rmsnorm_quant(x, final_norm_.get<float>(), c.eps, nullptr, st.act_d_.get(), B, c.D, s);

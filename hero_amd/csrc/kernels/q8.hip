@@ -1187,13 +1187,23 @@ constexpr int kSklRowPad = 16;  // activation row stride K + 16: 16 lanes' 16-by
 constexpr int kSklDxPad = 4;    // activation scale row stride nb + 4 (likewise)
 constexpr int kSklRing = 2;     // rounds in flight per wave (deeper rings measured slower)
 
-size_t skl_shared_bytes(int nw, int K) {
+__host__ __device__ inline size_t skl_shared_bytes(int nw, int K) {
     const int nb = K / 32;
     return size_t(16) * size_t(K + kSklRowPad) + size_t(16) * size_t(nb + kSklDxPad) * 4 + size_t(nw) * kSklRing * 2 * kSkwRound * 8 * 2;
 }
 
+// EPI == kEpiSwigluQuant (NW = 8; rows interleaved as 64-row units [32 gate
+// | 32 up], N % 64 == 0): workgroup x owns units 2x and 2x + 1, wave w the
+// 16-row group w % 4 of unit 2x + w / 4; after the last round the four waves
+// of a unit exchange their chains through shared memory and the unit's first
+// wave forms silu(gate) * up (nm/src/components.hpp:300-304) and the Q8_0
+// blocks of the down projection's input (quantize_row_q8_0) into y, read as
+// int8 [M][N/2] then fp32 scales [M][N/64] -- the values swiglu_quant_kernel
+// forms from the stored gate and up rows.
 template <int EPI, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) void gemm_q8_skinny_lds_kernel(const int8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ xq, const float* __restrict__ xd, float* __restrict__ y, const float* __restrict__ resid, int M, int N, int Npad, int K) {
+    constexpr bool SW = EPI == kEpiSwigluQuant;
+    static_assert(!SW || NW == 8, "two 4-wave units per workgroup");
     extern __shared__ __align__(16) uint8_t skl_smem[];
     const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, q = lane >> 4, c = lane & 15;
     const int nb = K >> 5, rounds = nb / kSkwRound;
@@ -1203,7 +1213,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     uint16_t (*dws)[2][kSkwRound][8] = reinterpret_cast<uint16_t (*)[2][kSkwRound][8]>(dxs + 16 * dxrow) + wv * kSklRing;  // this wave's [ring][8-row group][block][row]
     const int groups = (N + 15) >> 4, G = gridDim.x;
     const int wg_begin = int(int64_t(groups) * blockIdx.x / G), wg_end = int(int64_t(groups) * (blockIdx.x + 1) / G);
-    const int g_begin = wg_begin + (wg_end - wg_begin) * wv / NW, g_end = wg_begin + (wg_end - wg_begin) * (wv + 1) / NW;
+    const int sw_unit = 2 * int(blockIdx.x) + wv / 4;  // SW: this wave's unit
+    const bool sw_live = sw_unit < groups / 4;
+    const int g_begin = SW ? 4 * sw_unit + (wv & 3) : wg_begin + (wg_end - wg_begin) * wv / NW;
+    const int g_end = SW ? (sw_live ? g_begin + 1 : g_begin) : wg_begin + (wg_end - wg_begin) * (wv + 1) / NW;
     const int steps = (g_end - g_begin) * rounds;
     const int steps_pad = (steps + kSklRing - 1) / kSklRing * kSklRing;
     const __amdgpu_buffer_rsrc_t bw = buffer_of(wq, uint32_t(N) * uint32_t(K));
@@ -1268,6 +1281,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     const int8_t* xrow = xs + c * rowb + 16 * q;
     const float* dxr = dxs + c * dxrow;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};  // outputs (n = g*16 + 4q + r, m = c)
+    float fin[4] = {0.f, 0.f, 0.f, 0.f};  // SW: the group's outputs
     for (int s0 = 0; s0 < steps_pad; s0 += kSklRing) {
 #pragma unroll
         for (int k = 0; k < kSklRing; ++k) {
@@ -1309,7 +1323,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
                     const int n = g * 16 + 4 * q + rr;
-                    if (n < N && c < M) {
+                    if constexpr (SW) {
+                        fin[rr] = acc[rr];
+                    } else if (n < N && c < M) {
                         const int64_t o = int64_t(c) * N + n;
                         if constexpr (EPI == kEpiResidual)
                             y[o] = resid[o] + acc[rr];
@@ -1318,6 +1334,38 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
                     }
                     acc[rr] = 0.f;
                 }
+            }
+        }
+    }
+    if constexpr (SW) {
+        // lane (q, c) of group j holds unit rows 16 j + 4 q + rr for activation
+        // row c: j = 0, 1 the gates of FF offsets 4q + rr and 16 + 4q + rr, j = 2,
+        // 3 the up values of the same offsets
+        float4* xg = reinterpret_cast<float4*>(skl_smem + skl_shared_bytes(NW, K));  // [NW][64]
+        xg[wv * 64 + lane] = make_float4(fin[0], fin[1], fin[2], fin[3]);
+        __syncthreads();
+        if ((wv & 3) == 0 && sw_live) {
+            const float4 g1 = xg[(wv + 1) * 64 + lane], u0 = xg[(wv + 2) * 64 + lane], u1 = xg[(wv + 3) * 64 + lane];
+            const float v[8] = {silu_f32(fin[0]) * u0.x, silu_f32(fin[1]) * u0.y, silu_f32(fin[2]) * u0.z, silu_f32(fin[3]) * u0.w,
+                                silu_f32(g1.x) * u1.x, silu_f32(g1.y) * u1.y, silu_f32(g1.z) * u1.z, silu_f32(g1.w) * u1.w};
+            // the 32-value block of (row c, unit) sits in lanes c, c + 16, c + 32, c + 48
+            float amax = 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
+            amax = fmaxf(amax, __shfl_xor(amax, 16));
+            amax = fmaxf(amax, __shfl_xor(amax, 32));
+            const float d = amax / 127.f;
+            const float id = d != 0.f ? 1.f / d : 0.f;
+            int packed[2] = {0, 0};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) packed[k / 4] |= (int(roundf(v[k] * id)) & 0xFF) << (8 * (k % 4));
+            if (c < M) {
+                const int FF = N / 2;
+                int8_t* qs = reinterpret_cast<int8_t*>(y);
+                int* row = reinterpret_cast<int*>(qs + int64_t(c) * FF + 32 * sw_unit);
+                row[q] = packed[0];      // offsets 4q .. 4q + 3
+                row[4 + q] = packed[1];  // offsets 16 + 4q .. 16 + 4q + 3
+                if (q == 0) reinterpret_cast<float*>(qs + int64_t(M) * FF)[int64_t(c) * (FF / 32) + sw_unit] = half_bits_to_f32(fp32_to_fp16_ref(d));
             }
         }
     }
@@ -1354,6 +1402,21 @@ int gemm_q8_plan(int64_t M, int64_t N, int64_t K) {
     if (M > 32 && grid_of(64) >= want) return 64;
     if (M > 16 && grid_of(32) >= want) return 32;
     return 16;
+}
+
+bool launch_gemm_q8_swiglu(const void* packed, const void* act, void* out, int64_t M, int64_t N, int64_t K, hipStream_t s) {
+    if (gemm_q8_plan(M, N, K) != kGemmPlanSkinnyLds || N % 64 != 0) return false;
+    const unsigned grid = unsigned((N / 64 + 1) / 2);
+    const size_t smem = skl_shared_bytes(8, int(K)) + 8 * 64 * 16;
+    auto kernel = gemm_q8_skinny_lds_kernel<kEpiSwigluQuant, 8>;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 512, smem) != hipSuccess || int64_t(per_cu) * device_cus() < grid) return false;
+    const int8_t* wq = static_cast<const int8_t*>(packed);
+    const uint16_t* wd = reinterpret_cast<const uint16_t*>(wq + N * K);
+    const int8_t* xq = static_cast<const int8_t*>(act);
+    const float* xd = reinterpret_cast<const float*>(xq + M * K);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(512), smem, s, wq, wd, xq, xd, static_cast<float*>(out), nullptr, int(M), int(N), int(packed_rows_pad(N)), int(K));
+    return true;
 }
 
 void launch_gemm_q8(const void* packed, const void* act, float* y, const float* resid, int64_t M, int64_t N, int64_t K, int epi, hipStream_t s) {

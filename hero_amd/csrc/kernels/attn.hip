@@ -280,6 +280,135 @@ __global__ __launch_bounds__(256) void attn_scores_tile_kernel(AttnDecodeArgs a)
     }
 }
 
+// The same for heads of 256 channels (the reference's Qwen 3.5 4B / 9B
+// attention): the [channel][key] tile is 64 KB, a wave's query (four values a
+// lane: channels lane + 64 m, so both of a lane's RoPE planes (i, i + 128) are
+// its own) stays in shared memory and is read four channels at a time, the
+// same for every lane.
+constexpr int kWideDim = 256;
+
+__global__ __launch_bounds__(256) void attn_scores_tile_wide_kernel(AttnDecodeArgs a) {
+    __shared__ __align__(16) float kt[kWideDim * kScTileKeys];  // [channel][key]
+    __shared__ __align__(16) float qb[kScoreHeads][kWideDim];    // per wave: squares, then its rotated query
+    __shared__ __align__(16) float kb[kWideDim];                 // the new key (workgroups holding its position)
+    const int b = blockIdx.z;
+    const int group = a.Hq / a.Hkv, nchunk = (group + kScoreHeads - 1) / kScoreHeads;
+    const int g = int(blockIdx.x) / nchunk, hq0 = g * group + (int(blockIdx.x) % nchunk) * kScoreHeads;
+    const int nh = min(kScoreHeads, g * group + group - hq0);
+    const int pos = a.positions[b];
+    if (pos < 0 || pos >= a.max_ctx) return;
+    const int first = visible_first(pos, a.window);
+    const int n = pos + 1 - first;
+    const int base0 = first & ~3;  // keys from base0 on, in tiles of 64
+    const int span = pos + 1 - base0;
+    if (int(blockIdx.y) * kScTileKeys >= span) return;
+    const int tid = int(threadIdx.x), wave = tid / 64, lane = tid % 64;
+    const int hh = __builtin_amdgcn_readfirstlane(min(wave, nh - 1));  // waves past nh repeat the last head (not stored)
+    const int64_t kv = cache_of(a, b) * a.Hkv + g;
+    const float* kh = a.k_cache + kv * kWideDim * a.max_ctx;
+    float* sc = a.scores + (int64_t(b) * a.Hq + hq0 + hh) * a.max_ctx;
+    const float* P = a.proj + int64_t(b) * a.proj_stride;
+    const float* cs = a.rope_cs + int64_t(pos) * kWideDim;  // [Dh/2][2]
+    const int pos_tile = (pos - base0) / kScTileKeys;
+    const bool has_pos = pos_tile % int(gridDim.y) == int(blockIdx.y);
+
+    // 4096 16-byte chunks: chunk p = channel p / 16, keys key0 + 4 (p % 16) ..;
+    // chunks past the cache's end read its last chunk (never stored)
+    auto issue_tile = [&](int key0) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int p = 256 * j + tid, c = p / 16;
+            const int k4 = min(key0 + 4 * (p % 16), int(a.max_ctx) - 4);
+            lds_dma_b128(kh + int64_t(c) * a.max_ctx + k4, lds_offset(kt + 4 * 256 * j + 4 * 64 * wave));
+        }
+    };
+    int t0 = int(blockIdx.y) * kScTileKeys;
+    issue_tile(base0 + t0);
+
+    // RMSNorm (the sequential 256-term sum of squares by lane 0) and RoPE of
+    // one head held as x[m] = channel lane + 64 m: norm_rope_head's operations
+    auto norm_rope4 = [&](float (&x)[4], const float* gamma, float* buf) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) buf[lane + 64 * m] = x[m] * x[m];
+        float scal = 0.f;
+        if (lane == 0) {
+            float ss = 0.f;
+            const float4* b4 = reinterpret_cast<const float4*>(buf);
+#pragma unroll
+            for (int i = 0; i < kWideDim / 4; ++i) {
+                const float4 v = b4[i];
+                ss += v.x;
+                ss += v.y;
+                ss += v.z;
+                ss += v.w;
+            }
+            scal = 1.f / sqrtf(ss / float(kWideDim) + a.eps);
+        }
+        scal = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(scal)));  // lane 0's value
+        float nn[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) nn[m] = gamma[lane + 64 * m] * x[m] * scal;
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {  // planes (i, i + 128), i = lane + 64 m
+            const int i = lane + 64 * m;
+            const float c = cs[2 * i], sn = cs[2 * i + 1];
+            x[m] = nn[m] * c - nn[m + 2] * sn;
+            x[m + 2] = nn[m + 2] * c + nn[m] * sn;
+        }
+    };
+
+    // ---- the prep step (nm/src/qwen35.hpp:343-362): the wave's query ----
+    {
+        float qx[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) qx[m] = P[int64_t(hq0 + hh) * 2 * kWideDim + lane + 64 * m];
+        norm_rope4(qx, a.q_gamma, qb[wave]);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) qb[wave][lane + 64 * m] = qx[m];
+    }
+    if (has_pos && wave == 0) {  // the new key (after the query: qb[0] then holds the query, kb the squares)
+        float kx[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) kx[m] = P[a.k_off + int64_t(g) * kWideDim + lane + 64 * m];
+        norm_rope4(kx, a.k_gamma, kb);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) kb[lane + 64 * m] = kx[m];
+        if (int(blockIdx.x) % nchunk == 0) {  // the cache, once per K/V head
+            float* vrow = a.v_cache + (cache_of(a, b) * a.max_ctx + pos) * (int64_t(a.Hkv) * kWideDim) + int64_t(g) * kWideDim;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                a.k_cache[(kv * kWideDim + lane + 64 * m) * a.max_ctx + pos] = kx[m];  // [B][Hkv][Dh][max_ctx]
+                vrow[lane + 64 * m] = P[a.v_off + int64_t(g) * kWideDim + lane + 64 * m];  // [B][max_ctx][Hkv*Dh]
+            }
+        }
+    }
+
+    const float4* q4 = reinterpret_cast<const float4*>(qb[wave]);
+    for (; t0 < span; t0 += int(gridDim.y) * kScTileKeys) {
+        const int key0 = base0 + t0;
+        if (t0 != int(blockIdx.y) * kScTileKeys) issue_tile(key0);
+        wait_vmcnt<0>();
+        __syncthreads();
+        if (has_pos && (pos - base0) / kScTileKeys * kScTileKeys == t0) {  // the new key into its column
+            kt[tid * kScTileKeys + (pos - key0)] = kb[tid];
+            __syncthreads();
+        }
+        // s_j = scale * dot(q, k_j), the dot a sequential 256-term sum (core.hpp:496-500)
+        float dot = 0.f;
+#pragma unroll 16
+        for (int c4 = 0; c4 < kWideDim / 4; ++c4) {
+            const float4 qv = q4[c4];
+            dot += qv.x * kt[(4 * c4) * kScTileKeys + lane];
+            dot += qv.y * kt[(4 * c4 + 1) * kScTileKeys + lane];
+            dot += qv.z * kt[(4 * c4 + 2) * kScTileKeys + lane];
+            dot += qv.w * kt[(4 * c4 + 3) * kScTileKeys + lane];
+        }
+        const int t = key0 + lane - first;  // index among the visible keys
+        if (wave < nh && t >= 0 && t < n) sc[t] = a.score_scale * dot;
+        __syncthreads();  // the tile is read before the next one lands
+    }
+}
+
 // ---- 3. softmax ------------------------------------------------------------------------------
 // max over the visible scores (order free), e_j = exp(s_j - max), the total as
 // the sequential sum over j computed exactly in parallel, alpha_j = e_j / total
@@ -1803,11 +1932,16 @@ namespace {
 void attn_decode_wide(const AttnDecodeArgs& a, unsigned chunks, unsigned tiles, hipStream_t s) {
     constexpr int DH = 256;
     const int group = a.Hq / a.Hkv;
-    hipLaunchKernelGGL(attn_prep_kernel<DH>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(DH), 0, s, a);
-    hipLaunchKernelGGL(attn_scores_kernel<DH>, dim3(chunks, tiles, unsigned(a.B)), dim3(256), 0, s, a);
+    const int64_t vis = a.window > 0 ? std::min<int64_t>(a.max_ctx, a.window) : a.max_ctx;
+    if (a.max_ctx % 4 == 0 && a.B <= 2 && !a.shared_cache) {  // few sequences: 64-key tiles, the prep folded in
+        hipLaunchKernelGGL(attn_scores_tile_wide_kernel, dim3(chunks, unsigned(std::min<int64_t>(kScTiles, (vis + 3 + kScTileKeys - 1) / kScTileKeys)), unsigned(a.B)),
+                           dim3(256), 0, s, a);
+    } else {
+        hipLaunchKernelGGL(attn_prep_kernel<DH>, dim3(unsigned(a.Hq), unsigned(a.B)), dim3(DH), 0, s, a);
+        hipLaunchKernelGGL(attn_scores_kernel<DH>, dim3(chunks, tiles, unsigned(a.B)), dim3(256), 0, s, a);
+    }
     // few sequences: the per-head pipeline (softmax and weighted sum in one
     // kernel, a workgroup per head and 32 channels) while it fits the CUs
-    const int64_t vis = a.window > 0 ? std::min<int64_t>(a.max_ctx, a.window) : a.max_ctx;
     if (!a.shared_cache && int64_t(a.B) * a.Hq * (DH / kPvCh) <= device_cus() && vis <= kSpvMaxN && a.max_ctx % 4 == 0) {
         hipLaunchKernelGGL(attn_softmax_pv_kernel<DH>, dim3(unsigned(a.Hq * (DH / kPvCh)), unsigned(a.B)), dim3(kSpvThreads), spv_shared_bytes(), s, a);
         return;

@@ -23,8 +23,8 @@
 // prologue; at row lengths without a streaming GEMV a gemma_gelu_mul_quant
 // does both between two plain GEMVs. At d_model 2560 each post-norm runs in
 // the prologue of the GEMV that reads its act (w_gate_up, w_pgate, the next
-// layer's w_qkv): every workgroup forms the row itself and workgroup 0 writes
-// h, h2 or x; the last layer's stays a launch before the LM head.
+// layer's w_qkv, after the last layer the LM head): every workgroup forms the
+// row itself and workgroup 0 writes h, h2 or x.
 // then the tied LM head over act (the final norm's output), the soft-cap and
 // the argmax (gemma4.hpp:440-444).
 #include "hero/gemma4.hpp"
@@ -406,13 +406,12 @@ void Gemma4Model::enqueue_step(State& st) const {
         gelu_gated_pair(L.w_gate_up, ffn_in, st.act_, st.gu_.get<float>(), 2 * c.FF, c.D, st.gu_.get<float>() + c.FF, L.w_down, st.act_ff_, st.a_.get<float>(), c.D, c.FF, s);
         const GemvInput ple_in = sub_block_end({st.a_.get<float>(), L.post_ffn_norm.get<float>(), st.h_.get<float>(), 1.f, st.h2_.get<float>(), nullptr}, c.eps, st.act_, c.D, s);
         gelu_gated_pair(L.w_pgate, ple_in, st.act_, st.pg_.get<float>(), c.P, c.D, st.ple_.get<float>() + l * c.P, L.w_proj, st.act_p_, st.a_.get<float>(), c.D, c.P, s);
-        if (l + 1 < c.L)
-            qkv_in = sub_block_end({st.a_.get<float>(), L.post_norm.get<float>(), st.h2_.get<float>(), L.out_scale, x, layers_[size_t(l + 1)].attn_norm.get<float>()}, c.eps, st.act_, c.D, s);
-        else
-            launch_gemma_post_norm(st.a_.get<float>(), L.post_norm.get<float>(), st.h2_.get<float>(), L.out_scale, c.eps, x, final_norm_.get<float>(), st.act_.get(), c.D, s);
+        // the next layer's attention norm, or after the last layer the final norm
+        const float* next = l + 1 < c.L ? layers_[size_t(l + 1)].attn_norm.get<float>() : final_norm_.get<float>();
+        qkv_in = sub_block_end({st.a_.get<float>(), L.post_norm.get<float>(), st.h2_.get<float>(), L.out_scale, x, next}, c.eps, st.act_, c.D, s);
     }
     // tied head over the final norm's output, soft-cap, argmax into the step's id
-    launch_gemv_q8(embedding_.get(), st.act_.get(), st.logits_.get<float>(), nullptr, c.V, c.D, kEpiStore, s);
+    gemv_in(embedding_, qkv_in, st.act_, st.logits_.get<float>(), c.V, c.D, s);
     launch_gemma_softcap(st.logits_.get<float>(), c.V, c.softcap, s);
     launch_argmax(st.logits_.get<float>(), 1, c.V, step + 1, st.argmax_scratch_.get<uint64_t>(), s);
     check_launch("gemma4 step");

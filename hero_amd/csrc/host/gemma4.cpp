@@ -18,6 +18,8 @@
 //   gemv(w_pgate)               gelu(pg)
 //   gemv(w_proj)                a, over Q8_0(gelu(pg) * ple[l])       (gemma4.hpp:100-105)
 //   gemma_post_norm             x = (h2 + post_norm(a)) * layer_output_scale; act = Q8_0(next norm(x))
+// then the tied LM head over act (the final norm's output), the soft-cap and
+// the argmax (gemma4.hpp:440-444).
 // The GELU is applied to each gate row in the producing GEMV's epilogue (once
 // per value) and the product formed and quantized in the consuming GEMV's
 // prologue; at row lengths without a streaming GEMV a gemma_gelu_mul_quant
@@ -25,8 +27,6 @@
 // the prologue of the GEMV that reads its act (w_gate_up, w_pgate, the next
 // layer's w_qkv, after the last layer the LM head): every workgroup forms the
 // row itself and workgroup 0 writes h, h2 or x.
-// then the tied LM head over act (the final norm's output), the soft-cap and
-// the argmax (gemma4.hpp:440-444).
 #include "hero/gemma4.hpp"
 
 #include <algorithm>

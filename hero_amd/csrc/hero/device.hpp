@@ -188,4 +188,22 @@ __device__ __forceinline__ int4 quantize16_in_pair(const float (&x)[16], uint16_
     return make_int4(packed[0], packed[1], packed[2], packed[3]);
 }
 
+// (query head, channel part) of workgroup x of a Hq x parts grid. Workgroups
+// go to the eight XCDs round robin by index; when the (K/V head, part) pairs
+// come in whole eights, the group's query heads of one part get indices equal
+// mod 8, so they run on one XCD and read their shared value rows through one
+// L2 (in index order they split over two, and the values were fetched from
+// HBM about twice).
+__device__ __forceinline__ void head_part_of(int x, int Hq, int Hkv, int parts, int& h, int& part) {
+    const int group = Hq / Hkv, pairs = Hkv * parts;
+    if (pairs % 8 == 0) {
+        const int r = x / 8, pp = 8 * (r / group) + x % 8;  // pair pp = K/V head * parts + part
+        part = pp % parts;
+        h = (pp / parts) * group + r % group;
+    } else {
+        h = x / parts;
+        part = x % parts;
+    }
+}
+
 }  // namespace hero

@@ -480,24 +480,6 @@ constexpr int kPvThreads = 320;                             // chain wave, two p
 constexpr int kPvVTile = kPvRows * kPvCh;                   // floats of V per tile
 constexpr int kPvVLoads = kPvVTile / 4 / 128;               // 16-byte V loads per loader lane per tile: 4
 static_assert(kPvVLoads == 4 && kPvRows == 64 && kPvCh * kPvRows / 4 / 4 == 128, "tile geometry");
-// (query head, channel part) of workgroup x of a Hq x parts grid. Workgroups
-// go to the eight XCDs round robin by index; when the (K/V head, part) pairs
-// come in whole eights, the group's query heads of one part get indices equal
-// mod 8, so they run on one XCD and read their shared value rows through one
-// L2 (in index order they split over two, and the values were fetched from
-// HBM about twice).
-__device__ __forceinline__ void head_part_of(int x, int Hq, int Hkv, int parts, int& h, int& part) {
-    const int group = Hq / Hkv, pairs = Hkv * parts;
-    if (pairs % 8 == 0) {
-        const int r = x / 8, pp = 8 * (r / group) + x % 8;  // pair pp = K/V head * parts + part
-        part = pp % parts;
-        h = (pp / parts) * group + r % group;
-    } else {
-        h = x / parts;
-        part = x % parts;
-    }
-}
-
 constexpr size_t pv_shared_bytes(int R) { return (size_t(R) * (kPvVTile + kPvRows) + size_t(2) * kPvCh * kPvStride) * 4; }
 
 template <int R>

@@ -397,7 +397,10 @@ __global__ __launch_bounds__(256) void gemma_softmax_pv_kernel(GemmaAttnArgs a) 
     __shared__ __align__(16) float vb[2][kPvChunk][64];
     __shared__ __align__(16) float al[2][kPvChunk];
     __shared__ float red[4];
-    const int tid = threadIdx.x, h = blockIdx.x, c0 = blockIdx.y * 64;
+    const int tid = threadIdx.x;
+    int h, part;
+    head_part_of(int(blockIdx.x), a.Hq, a.Hkv, DH / 64, h, part);
+    const int c0 = part * 64;
     const int g = h / (a.Hq / a.Hkv);
     const GemmaSpan sp = gemma_span(a);
     const int n = sp.n;
@@ -518,7 +521,10 @@ __global__ __launch_bounds__(256) void gemma_softmax_pv_short_kernel(GemmaAttnAr
     __shared__ __align__(16) float al[kShortMax];         // the weights
     __shared__ float red[4];
     __shared__ float tot;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = blockIdx.x, c0 = blockIdx.y * 64;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    int h, part;
+    head_part_of(int(blockIdx.x), a.Hq, a.Hkv, DH / 64, h, part);
+    const int c0 = part * 64;
     const int g = h / (a.Hq / a.Hkv);
     const GemmaSpan sp = gemma_span(a);
     const int n = sp.n;  // 1 .. kShortMax (the host's condition)
@@ -600,9 +606,9 @@ void launch_gemma_attention(const GemmaAttnArgs& a, hipStream_t s) {
             hipLaunchKernelGGL(gemma_scores_kernel<256>, dim3(unsigned(a.Hkv), tiles), dim3(256), size_t(kGsTile * 257 + group * 256) * 4, s, a);
         }
         if (a.window > 0 && a.window <= kShortMax)
-            hipLaunchKernelGGL(gemma_softmax_pv_short_kernel<256>, dim3(unsigned(a.Hq), 256 / 64), dim3(256), 0, s, a);
+            hipLaunchKernelGGL(gemma_softmax_pv_short_kernel<256>, dim3(unsigned(a.Hq * (256 / 64))), dim3(256), 0, s, a);
         else
-            hipLaunchKernelGGL(gemma_softmax_pv_kernel<256>, dim3(unsigned(a.Hq), 256 / 64), dim3(256), 0, s, a);
+            hipLaunchKernelGGL(gemma_softmax_pv_kernel<256>, dim3(unsigned(a.Hq * (256 / 64))), dim3(256), 0, s, a);
     } else {
         if (prep_scores_shared<512>(group) <= kPrepScoresMaxShared) {
             hipLaunchKernelGGL(gemma_prep_scores_kernel<512>, dim3(unsigned(a.Hkv), tiles), dim3(kPsThreads), prep_scores_shared<512>(group), s, a);
@@ -610,7 +616,7 @@ void launch_gemma_attention(const GemmaAttnArgs& a, hipStream_t s) {
             hipLaunchKernelGGL(gemma_attn_prep_kernel<512>, dim3(prep), dim3(512), 0, s, a);
             hipLaunchKernelGGL(gemma_scores_kernel<512>, dim3(unsigned(a.Hkv), tiles), dim3(256), size_t(kGsTile * 513 + group * 512) * 4, s, a);
         }
-        hipLaunchKernelGGL(gemma_softmax_pv_kernel<512>, dim3(unsigned(a.Hq), 512 / 64), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(gemma_softmax_pv_kernel<512>, dim3(unsigned(a.Hq * (512 / 64))), dim3(256), 0, s, a);
     }
 }
 

